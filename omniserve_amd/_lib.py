@@ -1,0 +1,95 @@
+"""ctypes binding of the gfx950 C ABI declared in include/omniserve_amd.h.
+
+The shared library is built in-tree by ``python -m omniserve_amd.build``.  There
+is no fallback: if it is missing or fails to load, every op raises.  torch is
+imported first so the library binds to the HIP runtime torch already loaded
+(both carry the soname libamdhip64.so.7) and can launch on torch's streams.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libomniserve_amd.so"
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_I64 = ctypes.c_int64
+_F = ctypes.c_float
+
+# name -> argtypes (restype is always c_int: 0 ok, <0 argument error, >0 hipError_t)
+SIGNATURES = {
+    "omni_rmsnorm": [_P, _P, _P, _I, _I, _F, _P],
+    "omni_add_rmsnorm": [_P, _P, _P, _P, _P, _I, _I, _F, _P],
+    "omni_add_rmsnorm_fp8": [_P, _P, _P, _P, _P, _P, _I, _I, _F, _P],
+    "omni_embed_rmsnorm": [_P, _P, _I, _I64, _P, _P, _P, _I, _I, _F, _P],
+    "omni_embedding": [_P, _P, _I, _I64, _P, _I, _I, _P],
+    "omni_silu_mul": [_P, _P, _I, _I, _P],
+    "omni_mrope_kv_write": [_P, _I, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I,
+                            _I, _I, _I, _I, _P],
+    "omni_decode_attention": [_P, _I, _P, _P, _I, _I, _P, _P, _I, _I, _P, _I, _I, _I, _I, _F, _I,
+                              _P, _P, _P],
+    "omni_prefill_attention": [_P, _I, _P, _P, _I, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _F,
+                               _P],
+    "omni_w4a16_gemm": [_P, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P],
+    "omni_f16_gemm": [_P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P],
+    "omni_lmhead_argmax_grid": [_I],
+    "omni_lmhead_argmax": [_P, _I, _P, _I, _I, _I, _P, _P, _P, _P, _P, _P],
+    "omni_gptq_repack": [_P, _P, _P, _P, _I, _I, _I, _P],
+    "omni_f16_pack": [_P, _P, _I, _I, _I, _P],
+    "omni_w4_dequant": [_P, _P, _P, _I, _I, _P],
+}
+
+ERRORS = {-1: "invalid argument", -2: "unsupported shape"}
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load (once) and return the HIP library; raises if it is not built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"omniserve_amd HIP library missing at {LIB_PATH}; build it with "
+                "`python -m omniserve_amd.build` (there is no CPU fallback)")
+        so = ctypes.CDLL(str(LIB_PATH))
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(so, name)
+            fn.argtypes = argtypes
+            fn.restype = _I
+        _lib = so
+    return _lib
+
+
+def call(name: str, *args) -> None:
+    """Invoke an entry point and raise on a non-zero return code."""
+    rc = getattr(lib(), name)(*args)
+    if rc != 0:
+        what = ERRORS.get(rc) or f"hipError_t {rc}"
+        raise RuntimeError(f"{name} failed: {what}")
+
+
+def ptr(t) -> int | None:
+    """Device pointer of a tensor (None -> NULL)."""
+    return None if t is None else t.data_ptr()
+
+
+def stream() -> int:
+    """Handle of torch's current HIP stream (captured streams included)."""
+    return torch.cuda.current_stream().cuda_stream
+
+
+def require_cuda(*tensors, dtype=None, contiguous=True) -> None:
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError("omniserve_amd ops run on the GPU only (got a CPU tensor)")
+        if dtype is not None and t.dtype != dtype:
+            raise TypeError(f"expected {dtype}, got {t.dtype}")
+        if contiguous and not t.is_contiguous():
+            raise ValueError("expected a contiguous tensor")

@@ -1,0 +1,555 @@
+// GQA split-K decode attention over the preallocated KV pool.
+//
+// Replaces the paged flash-decode call in omniserve/cache/kv_prealloc.py:272-290:
+// for every query token t (pool row slot[t]) and query head h the output is
+//   softmax(scale * q[t,h] . K[slot, 0:L, h div G]^T) . V[slot, 0:L, h div G]
+// with L = kv_len (keys [0, L) inclusive of the token written this step),
+// G = n_heads / n_kv_heads query heads per KV head (6 for Qwen2-VL-2B).
+//
+// Pool layout (kept from the reference): K, V = [pool_rows, max_len, n_kv, 128] fp16.
+//
+// Work split: one workgroup = (token, kv head, split group); its 4 waves each
+// stream a contiguous 32-token-aligned range of the context, so each K/V row
+// of a KV head is read from HBM exactly once for all G query heads sharing it.
+// Per 32-token block a wave does
+//   S^T[16 tok x 16 heads] = K[16 x 128] . Q^T     (4 MFMA 16x16x32 per 16 tokens,
+//                                                   K fed straight from global)
+//   online softmax in fp32 (exp2, running max/sum per head)
+//   O[16 heads x 128] += P[16 x 32] . V[32 x 128]  (8 MFMAs, V transposed via LDS)
+// Waves combine in LDS; split groups combine through a small fp32 workspace,
+// the last-arriving workgroup (device-scope counter, reset by that workgroup)
+// writing the fp16 output, so the kernel is graph-replayable with no memset.
+#include "common.h"
+
+#define ATT_HD 128
+#define ATT_BLK 32
+#define ATT_WAVES 4
+#define ATT_VSTRIDE 136   // LDS row stride (halfs) of the V tile: 16B-aligned, bank-spread
+#define ATT_MAXG 16       // query heads per KV head supported (MFMA N = 16)
+
+struct AttnArgs {
+  const half_t* q;
+  int q_stride;          // elements between tokens
+  const half_t* k_cache;
+  const half_t* v_cache;
+  int pool_rows, max_len, nkv, G;
+  const int64_t* slots;  // [T] or NULL (row t)
+  const int64_t* kv_len; // [T] (or indexed by slot when kv_by_slot)
+  int kv_by_slot;
+  int kv_add;            // kv = kv_len[...] + kv_add
+  half_t* out;           // [T, nkv*G, 128]
+  float* ws;             // [T, nkv, S, G, 128 + 2]   (S > 1)
+  int* counters;         // [T, nkv] zero-initialised, self-resetting (S > 1)
+  float scale_log2;
+  int T;
+  int S;                 // split groups per (token, kv head)
+};
+
+__device__ __forceinline__ int64_t clamp64(int64_t v, int64_t lo, int64_t hi) {
+  return v < lo ? lo : (v > hi ? hi : v);
+}
+
+__global__ __launch_bounds__(256, 2) void decode_attn_kernel(AttnArgs a) {
+  // The V tiles (used in the block loop) and the per-wave partial outputs
+  // (used after it) share one LDS buffer.
+  constexpr int kVsBytes = ATT_WAVES * ATT_BLK * ATT_VSTRIDE * 2;
+  constexpr int kOBytes = ATT_WAVES * ATT_MAXG * ATT_HD * 4;
+  __shared__ __attribute__((aligned(16))) char smem[kVsBytes > kOBytes ? kVsBytes : kOBytes];
+  __shared__ float ml_lds[ATT_WAVES][ATT_MAXG][2];
+  __shared__ int last_flag;
+  half_t (*vs_lds)[ATT_BLK * ATT_VSTRIDE] = (half_t (*)[ATT_BLK * ATT_VSTRIDE])smem;
+  float (*o_lds)[ATT_MAXG][ATT_HD] = (float (*)[ATT_MAXG][ATT_HD])smem;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int q16 = lane >> 4;     // lane group 0..3
+  const int c16 = lane & 15;     // column within MFMA tile
+  const int S = a.S;
+  const int sg = blockIdx.x % S;
+  const int g = (blockIdx.x / S) % a.nkv;
+  const int t = blockIdx.x / (S * a.nkv);
+  const int G = a.G;
+
+  const int64_t slot = a.slots ? a.slots[t] : t;
+  const bool slot_ok = slot >= 0 && slot < a.pool_rows;
+  int64_t L = slot_ok ? a.kv_len[a.kv_by_slot ? slot : t] + a.kv_add : 0;
+  L = clamp64(L, 0, a.max_len);
+
+  // Token range of this wave.
+  const int nsplit = S * ATT_WAVES;
+  int chunk = (int)((L + nsplit - 1) / nsplit);
+  chunk = (chunk + ATT_BLK - 1) / ATT_BLK * ATT_BLK;
+  const int wsplit = sg * ATT_WAVES + wave;
+  const int beg = (int)min((int64_t)wsplit * chunk, L);
+  const int end = (int)min((int64_t)(wsplit + 1) * chunk, L);
+
+  // Q fragments: B operand of S^T = K Q^T.  Lane holds head c16, dims 32ks + 8*q16 + e.
+  half8_t qf[4];
+  {
+    const bool hv = c16 < G;
+    const half_t* qp = a.q + (int64_t)t * a.q_stride + (int64_t)(g * G + (hv ? c16 : 0)) * ATT_HD;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      half8_t v = *(const half8_t*)(qp + ks * 32 + q16 * 8);
+      if (!hv) v = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
+      qf[ks] = v;
+    }
+  }
+
+  float m_run = -INFINITY;   // per head c16 (identical across q16 groups)
+  float l_run = 0.f;         // lane-partial sum, reduced at the end
+  f32x4 o_acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o_acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  const int64_t row_base = slot * (int64_t)a.max_len;
+  const half_t* kbase = a.k_cache + g * ATT_HD;
+  const half_t* vbase = a.v_cache + g * ATT_HD;
+  const int64_t tok_stride = (int64_t)a.nkv * ATT_HD;
+  half_t* vs = vs_lds[wave];
+
+  half8_t kf[2][4];
+  half8_t vr[8];
+  auto load_block = [&](int tb) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      int tok = tb + 16 * j + c16;
+      tok = tok < end ? tok : end - 1;
+      const half_t* kp = kbase + (row_base + tok) * tok_stride + q16 * 8;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) kf[j][ks] = *(const half8_t*)(kp + ks * 32);
+    }
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int c = lane + 64 * r;          // 512 chunks of 8 halfs = 32 tokens x 128 dims
+      int tok = tb + (c >> 4);
+      tok = tok < end ? tok : end - 1;
+      vr[r] = *(const half8_t*)(vbase + (row_base + tok) * tok_stride + (c & 15) * 8);
+    }
+  };
+
+  if (beg < end) load_block(beg);
+  for (int tb = beg; tb < end; tb += ATT_BLK) {
+    // Stage this block's V into LDS (row-major, padded), keep K in registers.
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int c = lane + 64 * r;
+      *(half8_t*)(vs + (c >> 4) * ATT_VSTRIDE + (c & 15) * 8) = vr[r];
+    }
+    half8_t kc[2][4];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) kc[j][ks] = kf[j][ks];
+    if (tb + ATT_BLK < end) load_block(tb + ATT_BLK);   // prefetch next block
+
+    // Scores: acc[j][i] = token tb + 16j + 4*q16 + i, head c16.
+    f32x4 sacc[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) acc = mfma16x16x32(kc[j][ks], qf[ks], acc);
+      sacc[j] = acc;
+    }
+    float sc[8];
+    float mblk = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int tok = tb + 16 * j + 4 * q16 + i;
+        const float s = tok < end ? sacc[j][i] * a.scale_log2 : -INFINITY;
+        sc[4 * j + i] = s;
+        mblk = fmaxf(mblk, s);
+      }
+    mblk = fmaxf(mblk, __shfl_xor(mblk, 16, 64));
+    mblk = fmaxf(mblk, __shfl_xor(mblk, 32, 64));
+    const float m_new = fmaxf(m_run, mblk);
+    const float alpha = exp2f(m_run - m_new);   // m_run = -inf -> 0
+    m_run = m_new;
+    half8_t pa;
+    float psum = 0.f;
+#pragma unroll
+    for (int s8 = 0; s8 < 8; ++s8) {
+      const float p = exp2f(sc[s8] - m_new);
+      psum += p;
+      pa[s8] = (half_t)p;
+    }
+    l_run = l_run * alpha + psum;
+
+    // Rescale O rows (heads 4*q16 + i) by their head's alpha.
+    float al[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * q16 + i, 64);
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o_acc[dt][i] *= al[i];
+
+    // P (A operand: head c16, slot s8 <-> token 16*(s8/4) + 4*q16 + s8%4) times V.
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      half8_t vb;
+#pragma unroll
+      for (int s8 = 0; s8 < 8; ++s8) {
+        const int tok = 16 * (s8 >> 2) + 4 * q16 + (s8 & 3);
+        vb[s8] = vs[tok * ATT_VSTRIDE + dt * 16 + c16];
+      }
+      o_acc[dt] = mfma16x16x32(pa, vb, o_acc[dt]);
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+
+  l_run += __shfl_xor(l_run, 16, 64);
+  l_run += __shfl_xor(l_run, 32, 64);
+  __syncthreads();   // every wave is done with its V tile before o_lds reuses the space
+
+  // Per-wave partials to LDS (heads < G only).
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int h = 4 * q16 + i;
+    if (h < G) {
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) o_lds[wave][h][dt * 16 + c16] = o_acc[dt][i];
+    }
+  }
+  if (lane < G) {
+    ml_lds[wave][lane][0] = m_run;
+    ml_lds[wave][lane][1] = l_run;
+  }
+  __syncthreads();
+
+  // Combine the 4 waves: thread -> (head, dim) pairs.
+  const int nout = G * ATT_HD;
+  const int T = a.T;
+  const int nh = a.nkv * G;
+  float* wsg = nullptr;
+  if (S > 1) wsg = a.ws + (((int64_t)t * a.nkv + g) * S + sg) * (int64_t)G * (ATT_HD + 2);
+  for (int idx = threadIdx.x; idx < nout; idx += 256) {
+    const int h = idx / ATT_HD;
+    const int d = idx % ATT_HD;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < ATT_WAVES; ++w) M = fmaxf(M, ml_lds[w][h][0]);
+    float lsum = 0.f, o = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < ATT_WAVES; ++w) {
+        const float f = exp2f(ml_lds[w][h][0] - M);
+        lsum += f * ml_lds[w][h][1];
+        o += f * o_lds[w][h][d];
+      }
+    }
+    if (S == 1) {
+      const float r = lsum > 0.f ? o / lsum : 0.f;
+      a.out[((int64_t)t * nh + g * G + h) * ATT_HD + d] = (half_t)r;
+    } else {
+      wsg[h * (ATT_HD + 2) + d] = o;
+      if (d == 0) {
+        wsg[h * (ATT_HD + 2) + ATT_HD] = M;
+        wsg[h * (ATT_HD + 2) + ATT_HD + 1] = lsum;
+      }
+    }
+  }
+  if (S == 1) return;
+
+  // Cross-workgroup combine: the last workgroup of (t, g) to arrive reduces.
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int* ctr = a.counters + (int64_t)t * a.nkv + g;
+    const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = prev == S - 1;
+    if (last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_flag = last;
+  }
+  __syncthreads();
+  if (!last_flag) return;
+  __threadfence();
+  const float* wsb = a.ws + ((int64_t)t * a.nkv + g) * S * (int64_t)G * (ATT_HD + 2);
+  for (int idx = threadIdx.x; idx < nout; idx += 256) {
+    const int h = idx / ATT_HD;
+    const int d = idx % ATT_HD;
+    float M = -INFINITY;
+    for (int s = 0; s < S; ++s)
+      M = fmaxf(M, __builtin_nontemporal_load(wsb + ((int64_t)s * G + h) * (ATT_HD + 2) + ATT_HD));
+    float lsum = 0.f, o = 0.f;
+    if (M != -INFINITY) {
+      for (int s = 0; s < S; ++s) {
+        const float* p = wsb + ((int64_t)s * G + h) * (ATT_HD + 2);
+        const float ms = __builtin_nontemporal_load(p + ATT_HD);
+        const float f = exp2f(ms - M);
+        lsum += f * __builtin_nontemporal_load(p + ATT_HD + 1);
+        o += f * __builtin_nontemporal_load(p + d);
+      }
+    }
+    const float r = lsum > 0.f ? o / lsum : 0.f;
+    a.out[((int64_t)t * nh + g * G + h) * ATT_HD + d] = (half_t)r;
+  }
+  (void)T;
+}
+
+// Decode / append attention over the pool.
+//   q          fp16, token t head h at q + t*q_stride + h*128
+//   k/v_cache  fp16 [pool_rows, max_len, n_kv, 128]
+//   slots      int64 [T] pool rows (NULL = row t)
+//   kv_len     int64; keys visible to token t = kv_len[kv_by_slot ? slot : t] + kv_add
+//   out        fp16 [T, n_heads, 128]
+//   splits     split groups per (token, kv head); > 1 needs workspace and counters:
+//   workspace  fp32, >= T * n_kv * splits * G * 130 floats
+//   counters   int32 [T * n_kv], zero before first use (the kernel leaves them zero)
+extern "C" int omni_decode_attention(const void* q, int q_stride, const void* k_cache,
+                                     const void* v_cache, int pool_rows, int max_len,
+                                     const int64_t* slots, const int64_t* kv_len, int kv_by_slot,
+                                     int kv_add, void* out, int T, int n_heads, int n_kv_heads,
+                                     int head_dim, float scale, int splits, float* workspace,
+                                     int* counters, void* stream) {
+  if (T < 0 || n_heads <= 0 || n_kv_heads <= 0 || pool_rows <= 0 || max_len <= 0) return OMNI_EINVAL;
+  if (head_dim != ATT_HD || n_heads % n_kv_heads) return OMNI_EUNSUPPORTED;
+  const int G = n_heads / n_kv_heads;
+  if (G > ATT_MAXG) return OMNI_EUNSUPPORTED;
+  if (splits < 1 || splits > 1024) return OMNI_EINVAL;
+  if (q_stride < n_heads * ATT_HD || (q_stride & 7)) return OMNI_EINVAL;
+  if (T == 0) return OMNI_OK;
+  if (!q || !k_cache || !v_cache || !kv_len || !out) return OMNI_EINVAL;
+  if (splits > 1 && (!workspace || !counters)) return OMNI_EINVAL;
+  AttnArgs a;
+  a.q = (const half_t*)q;
+  a.q_stride = q_stride;
+  a.k_cache = (const half_t*)k_cache;
+  a.v_cache = (const half_t*)v_cache;
+  a.pool_rows = pool_rows;
+  a.max_len = max_len;
+  a.nkv = n_kv_heads;
+  a.G = G;
+  a.slots = slots;
+  a.kv_len = kv_len;
+  a.kv_by_slot = kv_by_slot;
+  a.kv_add = kv_add;
+  a.out = (half_t*)out;
+  a.ws = workspace;
+  a.counters = counters;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.T = T;
+  a.S = splits;
+  const int64_t nblocks = (int64_t)splits * n_kv_heads * T;
+  if (nblocks > 0x7fffffff) return OMNI_EUNSUPPORTED;
+  hipLaunchKernelGGL(decode_attn_kernel, dim3((unsigned)nblocks), dim3(256), 0,
+                     (hipStream_t)stream, a);
+  OMNI_CHECK_LAUNCH();
+  return OMNI_OK;
+}
+
+// ===========================================================================
+// Packed (varlen) causal prefill / append attention over the pool.
+//
+// Replaces the varlen flash call of cache/kv_prealloc.py:181-203 (and, with
+// kv_len = start + i + 1, the append form of :149-174): each query token t of
+// a packed batch attends to keys [0, kv_len[t]) of its own pool row slot[t].
+// One wave owns a query block of up to 16 consecutive tokens of one segment
+// (same slot, increasing positions) for one query head; the MFMA structure is
+// the decode kernel's with "rows" = query tokens instead of query heads:
+//   S^T[16 keys x 16 queries] = K . Q^T;  O[16 queries x 128] += P . V.
+// Query rows past the block end replicate its last row (never all-masked).
+// ===========================================================================
+struct PrefillArgs {
+  const half_t* q;
+  int q_stride;
+  const half_t* k_cache;
+  const half_t* v_cache;
+  int pool_rows, max_len, nkv, G, nh;
+  const int64_t* slots;    // [T]
+  const int64_t* kv_len;   // [T]
+  const int* qblocks;      // [nqb][2] = (first token, count <= 16)
+  int nqb;
+  half_t* out;
+  int out_stride;
+  float scale_log2;
+};
+
+__global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
+  __shared__ __attribute__((aligned(16))) half_t vs_lds[ATT_WAVES][ATT_BLK * ATT_VSTRIDE];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int q16 = lane >> 4;
+  const int c16 = lane & 15;
+  const int item = blockIdx.x * ATT_WAVES + wave;
+  if (item >= a.nqb * a.nh) return;   // no workgroup barriers below
+  const int qb = item / a.nh;
+  const int h = item % a.nh;
+  const int g = h / a.G;
+  const int t0 = a.qblocks[2 * qb];
+  const int n = a.qblocks[2 * qb + 1];
+  const int64_t slot = a.slots[t0];
+  if (slot < 0 || slot >= a.pool_rows || n <= 0) return;
+
+  const int my_row = c16 < n ? c16 : n - 1;
+  int64_t lim64 = a.kv_len[t0 + my_row];
+  lim64 = clamp64(lim64, 1, a.max_len);
+  const int lim = (int)lim64;                 // keys visible to this lane's query row
+  int64_t end64 = clamp64(a.kv_len[t0 + n - 1], 1, a.max_len);
+  const int end = (int)end64;                 // key range of the block
+
+  half8_t qf[4];
+  {
+    const half_t* qp = a.q + (int64_t)(t0 + my_row) * a.q_stride + (int64_t)h * ATT_HD;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) qf[ks] = *(const half8_t*)(qp + ks * 32 + q16 * 8);
+  }
+
+  float m_run = -INFINITY;
+  float l_run = 0.f;
+  f32x4 o_acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o_acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  const int64_t row_base = slot * (int64_t)a.max_len;
+  const half_t* kbase = a.k_cache + g * ATT_HD;
+  const half_t* vbase = a.v_cache + g * ATT_HD;
+  const int64_t tok_stride = (int64_t)a.nkv * ATT_HD;
+  half_t* vs = vs_lds[wave];
+
+  half8_t kf[2][4];
+  half8_t vr[8];
+  auto load_block = [&](int tb) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      int tok = tb + 16 * j + c16;
+      tok = tok < end ? tok : end - 1;
+      const half_t* kp = kbase + (row_base + tok) * tok_stride + q16 * 8;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) kf[j][ks] = *(const half8_t*)(kp + ks * 32);
+    }
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int c = lane + 64 * r;
+      int tok = tb + (c >> 4);
+      tok = tok < end ? tok : end - 1;
+      vr[r] = *(const half8_t*)(vbase + (row_base + tok) * tok_stride + (c & 15) * 8);
+    }
+  };
+
+  load_block(0);
+  for (int tb = 0; tb < end; tb += ATT_BLK) {
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int c = lane + 64 * r;
+      *(half8_t*)(vs + (c >> 4) * ATT_VSTRIDE + (c & 15) * 8) = vr[r];
+    }
+    half8_t kc[2][4];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) kc[j][ks] = kf[j][ks];
+    if (tb + ATT_BLK < end) load_block(tb + ATT_BLK);
+
+    f32x4 sacc[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) acc = mfma16x16x32(kc[j][ks], qf[ks], acc);
+      sacc[j] = acc;
+    }
+    float sc[8];
+    float mblk = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = tb + 16 * j + 4 * q16 + i;
+        const float s = key < lim ? sacc[j][i] * a.scale_log2 : -INFINITY;
+        sc[4 * j + i] = s;
+        mblk = fmaxf(mblk, s);
+      }
+    mblk = fmaxf(mblk, __shfl_xor(mblk, 16, 64));
+    mblk = fmaxf(mblk, __shfl_xor(mblk, 32, 64));
+    const float m_new = fmaxf(m_run, mblk);    // finite: key 0 is visible to every row
+    const float alpha = exp2f(m_run - m_new);
+    m_run = m_new;
+    half8_t pa;
+    float psum = 0.f;
+#pragma unroll
+    for (int s8 = 0; s8 < 8; ++s8) {
+      const float p = exp2f(sc[s8] - m_new);
+      psum += p;
+      pa[s8] = (half_t)p;
+    }
+    l_run = l_run * alpha + psum;
+    float al[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * q16 + i, 64);
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o_acc[dt][i] *= al[i];
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      half8_t vb;
+#pragma unroll
+      for (int s8 = 0; s8 < 8; ++s8) {
+        const int tok = 16 * (s8 >> 2) + 4 * q16 + (s8 & 3);
+        vb[s8] = vs[tok * ATT_VSTRIDE + dt * 16 + c16];
+      }
+      o_acc[dt] = mfma16x16x32(pa, vb, o_acc[dt]);
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  l_run += __shfl_xor(l_run, 16, 64);
+  l_run += __shfl_xor(l_run, 32, 64);
+  float li[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) li[i] = __shfl(l_run, 4 * q16 + i, 64);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 4 * q16 + i;
+    if (r < n) {
+      half_t* op = a.out + (int64_t)(t0 + r) * a.out_stride + (int64_t)h * ATT_HD;
+      const float inv = 1.0f / li[i];
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) op[dt * 16 + c16] = (half_t)(o_acc[dt][i] * inv);
+    }
+  }
+}
+
+// Causal varlen attention for packed query tokens over the pool.
+//   qblocks int32 [nqb][2]: (first token, count <= 16); the tokens of a block share
+//   slots[t] and have increasing kv_len.  out fp16 rows of out_stride elements.
+extern "C" int omni_prefill_attention(const void* q, int q_stride, const void* k_cache,
+                                      const void* v_cache, int pool_rows, int max_len,
+                                      const int64_t* slots, const int64_t* kv_len,
+                                      const int* qblocks, int nqb, void* out, int out_stride,
+                                      int n_heads, int n_kv_heads, int head_dim, float scale,
+                                      void* stream) {
+  if (nqb < 0 || n_heads <= 0 || n_kv_heads <= 0 || pool_rows <= 0 || max_len <= 0) return OMNI_EINVAL;
+  if (head_dim != ATT_HD || n_heads % n_kv_heads) return OMNI_EUNSUPPORTED;
+  if (q_stride < n_heads * ATT_HD || (q_stride & 7) || out_stride < n_heads * ATT_HD) return OMNI_EINVAL;
+  if (nqb == 0) return OMNI_OK;
+  if (!q || !k_cache || !v_cache || !slots || !kv_len || !qblocks || !out) return OMNI_EINVAL;
+  PrefillArgs a;
+  a.q = (const half_t*)q;
+  a.q_stride = q_stride;
+  a.k_cache = (const half_t*)k_cache;
+  a.v_cache = (const half_t*)v_cache;
+  a.pool_rows = pool_rows;
+  a.max_len = max_len;
+  a.nkv = n_kv_heads;
+  a.G = n_heads / n_kv_heads;
+  a.nh = n_heads;
+  a.slots = slots;
+  a.kv_len = kv_len;
+  a.qblocks = qblocks;
+  a.nqb = nqb;
+  a.out = (half_t*)out;
+  a.out_stride = out_stride;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  const int64_t items = (int64_t)nqb * n_heads;
+  const int64_t grid = (items + ATT_WAVES - 1) / ATT_WAVES;
+  if (grid > 0x7fffffff) return OMNI_EUNSUPPORTED;
+  hipLaunchKernelGGL(prefill_attn_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, a);
+  OMNI_CHECK_LAUNCH();
+  return OMNI_OK;
+}

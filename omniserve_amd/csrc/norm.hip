@@ -1,0 +1,247 @@
+// Fused residual-add + RMSNorm family, SiLU-mul and the embedding gather.
+//
+// One 64-lane wavefront owns one row; a 256-thread workgroup carries four
+// rows.  Each lane holds 8 consecutive fp16 values per 512-element chunk, so a
+// 1536-wide Qwen2 row is three 16-byte loads per lane kept in registers between
+// the sum-of-squares and the scaling pass (one HBM read, one write).
+//
+// Numerics follow omniserve/kernels/fused_ops.py:
+//   rms_norm      (:21-29)  y = fp16(x * rstd * w), rstd = 1/sqrt(sum(x^2)/N + eps)
+//   add_rms_norm  (:43-57)  r = fp16(res + x) is stored, then normalised
+//   add_rms_fp8   (:74-91)  y32 = r*rstd*w; s = max(amax|y32|/448, 1e-12);
+//                           q = e4m3fn(y32 / s)
+//   silu_mul      (:111-119) out = fp16(silu(g) * u) in fp32
+#include "common.h"
+
+#define NORM_MAX_CHUNKS 16   // hidden <= 16 * 512 = 8192
+
+// Address of element (n, k) of an fp16 weight in the packed MFMA layout
+// [N/16][K/32][64 lanes][8]: lane = n%16 + 16*((k%32)/8), element k%8.
+__device__ __forceinline__ size_t packed16_offset(int64_t n, int k, int K) {
+  int64_t nt = n >> 4;
+  int ks = k >> 5;
+  int lane = (int)(n & 15) + 16 * ((k & 31) >> 3);
+  return ((((size_t)nt * (K >> 5) + ks) * 64 + lane) << 3) + (k & 7);
+}
+
+template <bool HAS_RES, bool GATHER, bool FP8OUT>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(
+    const half_t* x, const half_t* residual, const int64_t* __restrict__ ids,
+    const half_t* __restrict__ table, int table_packed, int64_t vocab,
+    const half_t* __restrict__ w, half_t* y, uint8_t* __restrict__ y8,
+    float* __restrict__ scale_out, half_t* res_out, int rows, int H, float eps) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nchunk = H >> 3;
+
+  int64_t tok = 0;
+  if (GATHER) {
+    tok = ids[row];
+    tok = tok < 0 ? 0 : (tok >= vocab ? vocab - 1 : tok);
+  }
+
+  half8_t r[NORM_MAX_CHUNKS];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NORM_MAX_CHUNKS; ++i) {
+    const int c = lane + 64 * i;
+    if (c < nchunk) {
+      half8_t v;
+      if (GATHER) {
+        size_t off = table_packed ? packed16_offset(tok, c * 8, H) : (size_t)tok * H + c * 8;
+        v = *(const half8_t*)(table + off);
+      } else {
+        v = *(const half8_t*)(x + (size_t)row * H + c * 8);
+      }
+      if (HAS_RES) {
+        half8_t rv = *(const half8_t*)(residual + (size_t)row * H + c * 8);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (half_t)((float)v[e] + (float)rv[e]);
+      }
+      r[i] = v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float f = (float)v[e];
+        ss += f * f;
+      }
+    }
+  }
+  ss = wave_sum(ss);
+  const float rstd = 1.0f / sqrtf(ss / (float)H + eps);
+
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < NORM_MAX_CHUNKS; ++i) {
+    const int c = lane + 64 * i;
+    if (c < nchunk) {
+      if (HAS_RES || GATHER) *(half8_t*)(res_out + (size_t)row * H + c * 8) = r[i];
+      half8_t wv = *(const half8_t*)(w + c * 8);
+      if (!FP8OUT) {
+        half8_t o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = (half_t)(((float)r[i][e] * rstd) * (float)wv[e]);
+        *(half8_t*)(y + (size_t)row * H + c * 8) = o;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(((float)r[i][e] * rstd) * (float)wv[e]));
+      }
+    }
+  }
+  if (FP8OUT) {
+    amax = wave_max(amax);
+    const float s = fmaxf(amax / 448.0f, 1e-12f);
+#pragma unroll
+    for (int i = 0; i < NORM_MAX_CHUNKS; ++i) {
+      const int c = lane + 64 * i;
+      if (c < nchunk) {
+        half8_t wv = *(const half8_t*)(w + c * 8);
+        uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          lo |= (uint32_t)f32_to_e4m3fn((((float)r[i][e] * rstd) * (float)wv[e]) / s) << (8 * e);
+          hi |= (uint32_t)f32_to_e4m3fn((((float)r[i][e + 4] * rstd) * (float)wv[e + 4]) / s) << (8 * e);
+        }
+        uint2 pk = {lo, hi};
+        *(uint2*)(y8 + (size_t)row * H + c * 8) = pk;
+      }
+    }
+    if (lane == 0) scale_out[row] = s;
+  }
+}
+
+static int check_norm_shape(int rows, int H) {
+  if (rows < 0 || H <= 0) return OMNI_EINVAL;
+  if ((H & 7) != 0 || H > NORM_MAX_CHUNKS * 512) return OMNI_EUNSUPPORTED;
+  return OMNI_OK;
+}
+
+extern "C" int omni_rmsnorm(const void* x, const void* weight, void* y, int rows, int hidden,
+                            float eps, void* stream) {
+  int rc = check_norm_shape(rows, hidden);
+  if (rc) return rc;
+  if (rows == 0) return OMNI_OK;
+  if (!x || !weight || !y) return OMNI_EINVAL;
+  hipLaunchKernelGGL((rmsnorm_kernel<false, false, false>), dim3(ceil_div(rows, 4)), dim3(256), 0,
+                     (hipStream_t)stream, (const half_t*)x, nullptr, nullptr, nullptr, 0, 0,
+                     (const half_t*)weight, (half_t*)y, nullptr, nullptr, nullptr, rows, hidden, eps);
+  OMNI_CHECK_LAUNCH();
+  return OMNI_OK;
+}
+
+extern "C" int omni_add_rmsnorm(const void* x, const void* residual, const void* weight, void* y,
+                                void* residual_out, int rows, int hidden, float eps, void* stream) {
+  int rc = check_norm_shape(rows, hidden);
+  if (rc) return rc;
+  if (rows == 0) return OMNI_OK;
+  if (!x || !residual || !weight || !y || !residual_out) return OMNI_EINVAL;
+  hipLaunchKernelGGL((rmsnorm_kernel<true, false, false>), dim3(ceil_div(rows, 4)), dim3(256), 0,
+                     (hipStream_t)stream, (const half_t*)x, (const half_t*)residual, nullptr, nullptr,
+                     0, 0, (const half_t*)weight, (half_t*)y, nullptr, nullptr,
+                     (half_t*)residual_out, rows, hidden, eps);
+  OMNI_CHECK_LAUNCH();
+  return OMNI_OK;
+}
+
+extern "C" int omni_add_rmsnorm_fp8(const void* x, const void* residual, const void* weight,
+                                    void* y_fp8, float* scale, void* residual_out, int rows,
+                                    int hidden, float eps, void* stream) {
+  int rc = check_norm_shape(rows, hidden);
+  if (rc) return rc;
+  if (rows == 0) return OMNI_OK;
+  if (!x || !residual || !weight || !y_fp8 || !scale || !residual_out) return OMNI_EINVAL;
+  hipLaunchKernelGGL((rmsnorm_kernel<true, false, true>), dim3(ceil_div(rows, 4)), dim3(256), 0,
+                     (hipStream_t)stream, (const half_t*)x, (const half_t*)residual, nullptr, nullptr,
+                     0, 0, (const half_t*)weight, nullptr, (uint8_t*)y_fp8, scale,
+                     (half_t*)residual_out, rows, hidden, eps);
+  OMNI_CHECK_LAUNCH();
+  return OMNI_OK;
+}
+
+extern "C" int omni_embed_rmsnorm(const int64_t* ids, const void* table, int table_packed,
+                                  int64_t vocab, const void* weight, void* y, void* residual_out,
+                                  int rows, int hidden, float eps, void* stream) {
+  int rc = check_norm_shape(rows, hidden);
+  if (rc) return rc;
+  if (rows == 0) return OMNI_OK;
+  if (!ids || !table || !weight || !y || !residual_out || vocab <= 0) return OMNI_EINVAL;
+  if (table_packed && ((hidden & 31) != 0 || (vocab & 15) != 0)) return OMNI_EUNSUPPORTED;
+  hipLaunchKernelGGL((rmsnorm_kernel<false, true, false>), dim3(ceil_div(rows, 4)), dim3(256), 0,
+                     (hipStream_t)stream, nullptr, nullptr, ids, (const half_t*)table, table_packed,
+                     vocab, (const half_t*)weight, (half_t*)y, nullptr, nullptr,
+                     (half_t*)residual_out, rows, hidden, eps);
+  OMNI_CHECK_LAUNCH();
+  return OMNI_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Embedding gather: out[t, :] = table[ids[t], :]   (models/qwen2_vl.py:93-94)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void embed_kernel(const int64_t* __restrict__ ids,
+                                                   const half_t* __restrict__ table, int packed,
+                                                   int64_t vocab, half_t* __restrict__ out,
+                                                   int rows, int H) {
+  const int nchunk = H >> 3;
+  const int64_t total = (int64_t)rows * nchunk;
+  for (int64_t i = blockIdx.x * 256LL + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int row = (int)(i / nchunk);
+    const int c = (int)(i % nchunk);
+    int64_t tok = ids[row];
+    tok = tok < 0 ? 0 : (tok >= vocab ? vocab - 1 : tok);
+    size_t off = packed ? packed16_offset(tok, c * 8, H) : (size_t)tok * H + c * 8;
+    *(half8_t*)(out + (size_t)row * H + c * 8) = *(const half8_t*)(table + off);
+  }
+}
+
+extern "C" int omni_embedding(const int64_t* ids, const void* table, int table_packed,
+                              int64_t vocab, void* out, int rows, int hidden, void* stream) {
+  if (rows < 0 || hidden <= 0 || vocab <= 0) return OMNI_EINVAL;
+  if ((hidden & 7) != 0) return OMNI_EUNSUPPORTED;
+  if (table_packed && ((hidden & 31) != 0 || (vocab & 15) != 0)) return OMNI_EUNSUPPORTED;
+  if (rows == 0) return OMNI_OK;
+  if (!ids || !table || !out) return OMNI_EINVAL;
+  int64_t work = (int64_t)rows * (hidden >> 3);
+  int grid = (int)((work + 255) / 256);
+  if (grid > 4096) grid = 4096;
+  hipLaunchKernelGGL(embed_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, ids,
+                     (const half_t*)table, table_packed, vocab, (half_t*)out, rows, hidden);
+  OMNI_CHECK_LAUNCH();
+  return OMNI_OK;
+}
+
+// ---------------------------------------------------------------------------
+// SiLU-mul: gate_up [rows, 2n] (gate first, up second) -> out [rows, n].
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float silu_f32(float g) { return g * (1.0f / (1.0f + __expf(-g))); }
+
+__global__ __launch_bounds__(256) void silu_mul_kernel(const half_t* __restrict__ gu,
+                                                      half_t* __restrict__ out, int rows, int n) {
+#pragma clang fp contract(off)
+  const int nchunk = n >> 3;
+  const int64_t total = (int64_t)rows * nchunk;
+  for (int64_t i = blockIdx.x * 256LL + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int row = (int)(i / nchunk);
+    const int c = (int)(i % nchunk);
+    half8_t g = *(const half8_t*)(gu + (size_t)row * 2 * n + c * 8);
+    half8_t u = *(const half8_t*)(gu + (size_t)row * 2 * n + n + c * 8);
+    half8_t o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = (half_t)(silu_f32((float)g[e]) * (float)u[e]);
+    *(half8_t*)(out + (size_t)row * n + c * 8) = o;
+  }
+}
+
+extern "C" int omni_silu_mul(const void* gate_up, void* out, int rows, int n, void* stream) {
+  if (rows < 0 || n <= 0) return OMNI_EINVAL;
+  if ((n & 7) != 0) return OMNI_EUNSUPPORTED;
+  if (rows == 0) return OMNI_OK;
+  if (!gate_up || !out) return OMNI_EINVAL;
+  int64_t work = (int64_t)rows * (n >> 3);
+  int grid = (int)((work + 255) / 256);
+  if (grid > 8192) grid = 8192;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream,
+                     (const half_t*)gate_up, (half_t*)out, rows, n);
+  OMNI_CHECK_LAUNCH();
+  return OMNI_OK;
+}

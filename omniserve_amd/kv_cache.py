@@ -1,0 +1,219 @@
+"""Preallocated batched KV pool with the reference's layout and cache-view protocol.
+
+Mirrors omniserve/cache/kv_prealloc.py:
+* ``PreallocatedKVCache`` (:20-115): per-layer ``k[l]``, ``v[l]`` of shape
+  ``[max_batch, max_len, n_kv, head_dim]`` fp16 (here views into one allocation
+  ``[n_layers, 2, max_batch, max_len, n_kv, head_dim]``), ``lengths`` int64 = valid
+  length = next write position per slot, slot ops (move/snapshot/restore/copy).
+* ``_CacheView.flash_decode`` (:272-290): write the new K/V at row*max_len + pos, then
+  attend over keys [0, pos] (inclusive); ``lengths`` advance after the last layer.
+* ``_PackedPrefillWriter.flash_prefill`` (:181-203): each packed segment's K/V goes to
+  ``pool[slot, :L]``; causal attention inside each segment; ``lengths[slot] = L``.
+
+Attention and the K/V writes run on the HIP kernels (omni_decode_attention,
+omni_mrope_kv_write, omni_prefill_attention); slot bookkeeping stays torch copies.
+"""
+
+from __future__ import annotations
+
+from typing import List, Sequence
+
+import torch
+
+from ._lib import call, ptr, require_cuda, stream
+
+MAX_DECODE_SPLITS = 64
+
+
+def decode_splits(n_tokens: int, n_kv: int, max_ctx: int) -> int:
+    """Split groups per (token, kv head) for omni_decode_attention: aim for >= ~512
+    workgroups (4 waves each) on the 256-CU MI355X, with >= 64 keys per wave."""
+    pairs = max(1, n_tokens * n_kv)
+    s = max(1, 512 // pairs)
+    s = min(s, max(1, max_ctx // 256), MAX_DECODE_SPLITS)
+    return s
+
+
+class PreallocatedKVCache:
+    def __init__(self, n_layers: int, max_batch: int, n_kv_heads: int, max_len: int,
+                 head_dim: int, device, dtype=torch.float16, n_heads: int | None = None):
+        if dtype != torch.float16:
+            raise ValueError("the KV pool is fp16")
+        self.n_layers = n_layers
+        self.max_batch = max_batch
+        self.max_len = max_len
+        self.n_kv_heads = n_kv_heads
+        self.head_dim = head_dim
+        self.n_heads = n_heads or 6 * n_kv_heads
+        self.device = torch.device(device)
+        self.storage = torch.zeros(n_layers, 2, max_batch, max_len, n_kv_heads, head_dim,
+                                   device=device, dtype=dtype)
+        self.k: List[torch.Tensor] = [self.storage[l, 0] for l in range(n_layers)]
+        self.v: List[torch.Tensor] = [self.storage[l, 1] for l in range(n_layers)]
+        self.lengths = torch.zeros(max_batch, dtype=torch.long, device=device)
+        self._active = 0
+        # split-K workspace of the decode attention (shared by all layers; launches on one
+        # stream are ordered) and its self-resetting counters.
+        G = self.n_heads // n_kv_heads
+        self._attn_ws = torch.empty(max_batch * n_kv_heads * MAX_DECODE_SPLITS * G * (head_dim + 2),
+                                    device=device, dtype=torch.float32)
+        self._attn_ctr = torch.zeros(max_batch * n_kv_heads, device=device, dtype=torch.int32)
+
+    # ---- slot operations (kv_prealloc.py:43-84) ------------------------------------
+    def set_slot_prefix(self, slot: int, legacy_kv, length: int) -> None:
+        for li, (k, v) in enumerate(legacy_kv):
+            self.k[li][slot, :length] = k[0].transpose(0, 1)
+            self.v[li][slot, :length] = v[0].transpose(0, 1)
+        self.lengths[slot] = length
+        self._active = max(self._active, slot + 1)
+
+    def move_slot(self, src: int, dst: int) -> None:
+        """Move a sequence's KV from slot src to dst (pool compaction on free).  Copies the
+        whole row in one strided copy across all layers and K/V."""
+        self.storage[:, :, dst].copy_(self.storage[:, :, src])
+        self.lengths[dst] = self.lengths[src]
+
+    def snapshot_slot(self, slot: int, length: int):
+        ks = [self.k[li][slot, :length].clone() for li in range(self.n_layers)]
+        vs = [self.v[li][slot, :length].clone() for li in range(self.n_layers)]
+        return ks, vs
+
+    def restore_slot(self, slot: int, snapshot, length: int) -> None:
+        ks, vs = snapshot
+        for li in range(self.n_layers):
+            self.k[li][slot, :length] = ks[li]
+            self.v[li][slot, :length] = vs[li]
+        self.lengths[slot] = length
+        self._active = max(self._active, slot + 1)
+
+    def copy_slot_kv(self, src: int, dst: int, length: int) -> None:
+        self.storage[:, :, dst, :length].copy_(self.storage[:, :, src, :length])
+        self.lengths[dst] = length
+        self._active = max(self._active, dst + 1)
+
+    # ---- views ---------------------------------------------------------------------
+    def view(self, n: int, rope_delta: torch.Tensor | None = None) -> "CacheView":
+        return CacheView(self, n, rope_delta)
+
+    def packed_prefill_cache(self, slots: Sequence[int], seg_lengths: Sequence[int]):
+        return PackedPrefillWriter(self, slots, seg_lengths)
+
+    # ---- kernel calls --------------------------------------------------------------
+    def attend(self, q: torch.Tensor, q_stride: int, layer_idx: int, kv_len: torch.Tensor,
+               kv_by_slot: bool, kv_add: int, out: torch.Tensor, n: int, scale: float,
+               slots: torch.Tensor | None = None, splits: int | None = None) -> torch.Tensor:
+        """omni_decode_attention over pool rows (slots or 0..n-1)."""
+        nh = out.shape[-2]
+        s = splits or decode_splits(n, self.n_kv_heads, self.max_len)
+        call("omni_decode_attention", ptr(q), q_stride, ptr(self.k[layer_idx]),
+             ptr(self.v[layer_idx]), self.max_batch, self.max_len, ptr(slots), ptr(kv_len),
+             int(kv_by_slot), kv_add, ptr(out), n, nh, self.n_kv_heads, self.head_dim,
+             float(scale), s, ptr(self._attn_ws), ptr(self._attn_ctr), stream())
+        return out
+
+
+class CacheView:
+    """Single-forward decode adapter over pool rows [0, n) (kv_prealloc.py:232-290).
+
+    Positions and write positions are read on the device from ``pool.lengths`` (and the
+    per-slot ``rope_delta``), so the same view serves eager and captured decode."""
+
+    def __init__(self, pool: PreallocatedKVCache, n: int, rope_delta: torch.Tensor | None):
+        self.pool = pool
+        self.n = n
+        self.rope_delta = rope_delta
+
+    def rope_and_write(self, qkv: torch.Tensor, layer_idx: int, cos_tab, sin_tab,
+                       mrope_section) -> None:
+        """Fused M-RoPE on q/k (in place in the qkv rows) + K/V write at lengths[row]."""
+        pool = self.pool
+        s0, s1, s2 = mrope_section
+        call("omni_mrope_kv_write", ptr(qkv), qkv.stride(0), None, ptr(pool.lengths),
+             ptr(self.rope_delta), ptr(cos_tab), ptr(sin_tab), cos_tab.shape[0],
+             ptr(pool.k[layer_idx]), ptr(pool.v[layer_idx]), None, None, pool.max_batch,
+             pool.max_len, self.n, pool.n_heads, pool.n_kv_heads, pool.head_dim, s0, s1, s2,
+             stream())
+
+    def attend_qkv(self, qkv: torch.Tensor, layer_idx: int, scale: float, out: torch.Tensor,
+                   splits: int | None = None) -> torch.Tensor:
+        """Attention for rows [0, n): keys [0, lengths[row]] (the token just written)."""
+        return self.pool.attend(qkv, qkv.stride(0), layer_idx, self.pool.lengths, True, 1, out,
+                                self.n, scale, splits=splits)
+
+    def flash_decode(self, q, key, value, layer_idx, scale):
+        """Reference protocol (kv_prealloc.py:272-290): q [n, nh, hd] (rotated), key/value
+        [n, nkv, hd]; writes K/V at lengths[row], attends, advances lengths on the last
+        layer."""
+        pool, n = self.pool, self.n
+        rows = torch.arange(n, device=q.device)
+        flat = rows * pool.max_len + pool.lengths[:n]
+        nkv, hd = pool.n_kv_heads, pool.head_dim
+        pool.k[layer_idx].view(-1, nkv, hd).index_copy_(0, flat, key.to(torch.float16))
+        pool.v[layer_idx].view(-1, nkv, hd).index_copy_(0, flat, value.to(torch.float16))
+        q = q.contiguous()
+        out = torch.empty_like(q)
+        pool.attend(q, q.shape[1] * q.shape[2], layer_idx, pool.lengths, True, 1, out, n, scale)
+        if layer_idx == pool.n_layers - 1:
+            pool.lengths[:n] += 1
+        return out
+
+
+class PackedPrefillWriter:
+    """Packed prefill adapter (kv_prealloc.py:177-215): segments of a packed batch go to
+    their own slots; attention is causal within each segment."""
+
+    def __init__(self, pool: PreallocatedKVCache, slots: Sequence[int],
+                 seg_lengths: Sequence[int]):
+        self.pool = pool
+        self.slots = list(slots)
+        self.seg = list(seg_lengths)
+        dev = pool.device
+        T = sum(self.seg)
+        slot_t, pos_t, cu = [], [], [0]
+        for s, L in zip(self.slots, self.seg):
+            slot_t += [s] * L
+            pos_t += list(range(L))
+            cu.append(cu[-1] + L)
+        self.T = T
+        self.token_slot = torch.tensor(slot_t, device=dev, dtype=torch.int64)
+        self.token_pos = torch.tensor(pos_t, device=dev, dtype=torch.int64)
+        self.kv_len = self.token_pos + 1          # causal: token i sees keys [0, i]
+        self.cu_seqlens = torch.tensor(cu, device=dev, dtype=torch.int32)
+        self.max_seg = max(self.seg) if self.seg else 0
+
+    def rope_and_write(self, qkv: torch.Tensor, layer_idx: int, positions: torch.Tensor,
+                       cos_tab, sin_tab, mrope_section) -> None:
+        pool = self.pool
+        s0, s1, s2 = mrope_section
+        call("omni_mrope_kv_write", ptr(qkv), qkv.stride(0), ptr(positions), None, None,
+             ptr(cos_tab), ptr(sin_tab), cos_tab.shape[0], ptr(pool.k[layer_idx]),
+             ptr(pool.v[layer_idx]), ptr(self.token_slot), ptr(self.token_pos), pool.max_batch,
+             pool.max_len, self.T, pool.n_heads, pool.n_kv_heads, pool.head_dim, s0, s1, s2,
+             stream())
+
+    def attend_qkv(self, qkv: torch.Tensor, layer_idx: int, scale: float,
+                   out: torch.Tensor) -> torch.Tensor:
+        from .attention import prefill_attention_pool
+        return prefill_attention_pool(self, qkv, layer_idx, scale, out)
+
+    def finish(self) -> None:
+        for s, L in zip(self.slots, self.seg):
+            self.pool.lengths[s] = L
+            self.pool._active = max(self.pool._active, s + 1)
+
+    def flash_prefill(self, q, k, v, layer_idx, scale):
+        """Reference protocol (kv_prealloc.py:181-203): q [T, nh, hd], k/v [T, nkv, hd]
+        (rotated).  Writes K/V to the slots, causal attention per segment."""
+        pool = self.pool
+        off = 0
+        for slot, L in zip(self.slots, self.seg):
+            pool.k[layer_idx][slot, :L] = k[off:off + L]
+            pool.v[layer_idx][slot, :L] = v[off:off + L]
+            off += L
+        q = q.contiguous()
+        out = torch.empty_like(q)
+        from .attention import prefill_attention_pool
+        prefill_attention_pool(self, q, layer_idx, scale, out, q_stride=q.shape[1] * q.shape[2])
+        if layer_idx == pool.n_layers - 1:
+            self.finish()
+        return out

@@ -1,0 +1,187 @@
+"""Qwen2 text decoder (Qwen2-VL-2B shape) driven by the gfx950 HIP kernels.
+
+Host mirror of omniserve/model/qwen2_llm.py: same config, same fused weight
+layouts (q|k|v with bias, gate|up), same residual threading (the add folded into
+the next RMSNorm, :145-157, final norm = add + norm, :186), M-RoPE with sections
+[16, 24, 24] (:59-72), tied lm_head (:167-168).
+
+Two entry points:
+* ``forward(inputs_embeds, position_ids, attn_mask, cache, logits_indices)`` - the
+  reference signature (:179-190), used for packed prefill (cache =
+  ``PackedPrefillWriter``) and eager decode (cache = ``CacheView``); returns logits.
+* ``decode_greedy(...)`` - the decode step on static buffers, ending in the fused
+  lm_head + argmax; allocation-free and host-sync-free, so the runner captures it
+  whole in a HIP graph.
+"""
+
+from __future__ import annotations
+
+from typing import Dict, List, Optional
+
+import torch
+from torch import nn
+
+from . import fused_ops as F
+from .linear import F16Linear, GPTQLinear, LMHeadArgmax
+from .synth import DecoderShape
+
+Qwen2Config = DecoderShape
+
+
+def rope_tables(cfg: Qwen2Config, max_pos: int, device):
+    """fp16 cos/sin [max_pos, head_dim/2] of p * inv_freq (qwen2_llm.py:169-177, 181):
+    inv_freq = 1/theta^(arange(0,hd,2)/hd) and p*inv_freq in fp32, cos/sin in fp32, cast to
+    fp16.  Built on the CPU once; the kernel reads the pair (d, d+64) from column d."""
+    inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, cfg.head_dim, 2).float() / cfg.head_dim))
+    freqs = torch.arange(max_pos)[:, None].float() * inv
+    return (freqs.cos().to(torch.float16).to(device).contiguous(),
+            freqs.sin().to(torch.float16).to(device).contiguous())
+
+
+class DecoderLayer(nn.Module):
+    def __init__(self, in_norm, post_norm, qkv_proj, o_proj, gate_up_proj, down_proj):
+        super().__init__()
+        self.register_buffer("in_norm", in_norm)
+        self.register_buffer("post_norm", post_norm)
+        self.qkv_proj = qkv_proj
+        self.o_proj = o_proj
+        self.gate_up_proj = gate_up_proj   # fused SiLU epilogue: [.., H] -> [.., I]
+        self.down_proj = down_proj
+
+
+class Qwen2LLM(nn.Module):
+    def __init__(self, cfg: Qwen2Config, embed: torch.Tensor, final_norm: torch.Tensor,
+                 layers: List[DecoderLayer], max_pos: int = 8192):
+        super().__init__()
+        self.cfg = cfg
+        self.lm_head = LMHeadArgmax(embed)         # packed tied table (also the embedding)
+        self.register_buffer("norm", final_norm)
+        self.layers = nn.ModuleList(layers)
+        cos, sin = rope_tables(cfg, max_pos, embed.device)
+        self.register_buffer("rope_cos", cos)
+        self.register_buffer("rope_sin", sin)
+        self.scale = cfg.head_dim ** -0.5
+        self._bufs: Dict[int, dict] = {}
+
+    # ------------------------------------------------------------------ builders
+    @classmethod
+    def from_fp16(cls, w: Dict, cfg: Qwen2Config, device, max_pos: int = 8192) -> "Qwen2LLM":
+        """fp16 weights in nn.Linear layout (see synth.fp16_decoder)."""
+        d = torch.device(device)
+        layers = []
+        for lw in w["layers"]:
+            layers.append(DecoderLayer(
+                lw["in_norm"].to(d), lw["post_norm"].to(d),
+                F16Linear(lw["qkv_w"].to(d), lw["qkv_b"].to(d)),
+                F16Linear(lw["o_w"].to(d)),
+                F16Linear(lw["gate_up_w"].to(d), fuse_silu=True),
+                F16Linear(lw["down_w"].to(d))))
+        return cls(cfg, w["embed"].to(d), w["norm"].to(d), layers, max_pos)
+
+    @classmethod
+    def from_gptq(cls, w: Dict, cfg: Qwen2Config, device, max_pos: int = 8192) -> "Qwen2LLM":
+        """GPTQ int4 decoder linears (AutoGPTQ layout, see synth.gptq_decoder), fp16
+        embedding / lm_head and norms (marlin_linear.py:114-143)."""
+        d = torch.device(device)
+        layers = []
+        for lw in w["layers"]:
+            layers.append(DecoderLayer(
+                lw["in_norm"].to(d), lw["post_norm"].to(d),
+                GPTQLinear(lw["qkv_q"].to(d), lw["qkv_s"].to(d), lw["qkv_b"].to(d)),
+                GPTQLinear(lw["o_q"].to(d), lw["o_s"].to(d)),
+                GPTQLinear(lw["gate_up_q"].to(d), lw["gate_up_s"].to(d), fuse_silu=True),
+                GPTQLinear(lw["down_q"].to(d), lw["down_s"].to(d))))
+        return cls(cfg, w["embed"].to(d), w["norm"].to(d), layers, max_pos)
+
+    # ------------------------------------------------------------------ embedding
+    def embed_tokens(self, ids: torch.Tensor) -> torch.Tensor:
+        """ids [...] int64 -> [..., H] fp16 (models/qwen2_vl.py:93-94), gathered from the
+        packed tied table."""
+        ids_c = ids.reshape(-1).contiguous()
+        out = torch.empty(ids_c.numel(), self.cfg.hidden_size, device=ids.device,
+                          dtype=torch.float16)
+        F.embedding_out(ids_c, self.lm_head.table_packed, True, out)
+        return out.reshape(*ids.shape, self.cfg.hidden_size)
+
+    # ------------------------------------------------------------------ reference forward
+    def forward(self, inputs_embeds, position_ids, attn_mask=None, cache=None,
+                logits_indices=None):
+        """inputs_embeds [B, L, H] fp16 with B*L packed tokens; position_ids [3, B, L].
+
+        ``cache`` must be a pool adapter (PackedPrefillWriter for prefill, CacheView for
+        decode); attn_mask is unused (causality / lengths come from the adapter)."""
+        cfg = self.cfg
+        B, L, H = inputs_embeds.shape
+        T = B * L
+        x = inputs_embeds.reshape(T, H).contiguous()
+        decode = not hasattr(cache, "token_slot")
+        pos = None if decode else position_ids.reshape(3, T).to(torch.int64).contiguous()
+        residual = None
+        for i, layer in enumerate(self.layers):
+            if residual is None:
+                residual = x
+                h = F.rms_norm(x, layer.in_norm, cfg.rms_norm_eps)
+            else:
+                h, residual = F.add_rms_norm(x, residual, layer.in_norm, cfg.rms_norm_eps)
+            qkv = layer.qkv_proj(h)
+            if decode:
+                cache.rope_and_write(qkv, i, self.rope_cos, self.rope_sin, cfg.mrope_section)
+            else:
+                cache.rope_and_write(qkv, i, pos, self.rope_cos, self.rope_sin,
+                                     cfg.mrope_section)
+            attn = torch.empty(T, cfg.num_heads, cfg.head_dim, device=x.device,
+                               dtype=torch.float16)
+            cache.attend_qkv(qkv, i, self.scale, attn)
+            o = layer.o_proj(attn.reshape(T, -1))
+            h, residual = F.add_rms_norm(o, residual, layer.post_norm, cfg.rms_norm_eps)
+            x = layer.down_proj(layer.gate_up_proj(h))
+        if decode:
+            cache.pool.lengths[:cache.n] += 1
+        else:
+            cache.finish()
+        if logits_indices is not None:
+            idx = torch.as_tensor(logits_indices, device=x.device, dtype=torch.long)
+            x, residual = x[idx].contiguous(), residual[idx].contiguous()
+        h, _ = F.add_rms_norm(x, residual, self.norm, cfg.rms_norm_eps)
+        logits = self.lm_head.logits(h)
+        return logits.reshape(1 if logits_indices is not None else B, -1, cfg.vocab_size)
+
+    # ------------------------------------------------------------------ decode fast path
+    def decode_buffers(self, n: int, device) -> dict:
+        """Static activation buffers for an n-row decode step (kept alive for graphs)."""
+        if n not in self._bufs:
+            cfg = self.cfg
+            H, I = cfg.hidden_size, cfg.intermediate_size
+            mk = lambda *s: torch.empty(*s, device=device, dtype=torch.float16)
+            self._bufs[n] = {
+                "h": mk(n, H), "res": mk(n, H), "x": mk(n, H), "o": mk(n, H),
+                "qkv": mk(n, cfg.qkv_out), "attn": mk(n, cfg.num_heads * cfg.head_dim),
+                "act": mk(n, I),
+            }
+        return self._bufs[n]
+
+    def decode_greedy(self, ids: torch.Tensor, view, ids_out: torch.Tensor,
+                      logits_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """One decode step for pool rows [0, n): ids [n] int64 (device) -> ids_out [n]
+        (greedy).  Reads positions from pool.lengths (+ rope delta), writes K/V, does not
+        advance lengths.  No allocation, no host sync."""
+        cfg = self.cfg
+        n = ids.shape[0]
+        b = self.decode_buffers(n, ids.device)
+        eps = cfg.rms_norm_eps
+        h, res, x = b["h"], b["res"], b["x"]
+        F.embed_rms_norm_out(ids, self.lm_head.table_packed, True, self.layers[0].in_norm, eps,
+                             h, res)
+        for i, layer in enumerate(self.layers):
+            if i > 0:
+                F.add_rms_norm_out(x, res, layer.in_norm, eps, h, res)
+            layer.qkv_proj.forward_out(h, b["qkv"])
+            view.rope_and_write(b["qkv"], i, self.rope_cos, self.rope_sin, cfg.mrope_section)
+            view.attend_qkv(b["qkv"], i, self.scale, b["attn"])
+            layer.o_proj.forward_out(b["attn"], b["o"])
+            F.add_rms_norm_out(b["o"], res, layer.post_norm, eps, h, res)
+            layer.gate_up_proj.forward_out(h, b["act"])
+            layer.down_proj.forward_out(b["act"], x)
+        F.add_rms_norm_out(x, res, self.norm, eps, h, res)
+        self.lm_head.argmax_out(h, ids_out, logits_out)
+        return ids_out

@@ -1,0 +1,331 @@
+"""Kernel-level parity of the HIP path against the CPU oracle (GPU tests).
+
+Each test feeds the same seeded fp16 inputs to the HIP kernel (through the C ABI
+via omniserve_amd's thin wrappers) and to oracle/qwen2_ref.py, and compares:
+bit-exact for integer/byte/index work and for the fp16-rounding-specified ops
+(M-RoPE, embedding gather, int4 dequant, KV writes), tolerance for reductions.
+"""
+
+import math
+
+import pytest
+import torch
+
+from oracle import qwen2_ref as ref
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(f"[gpu-test] {msg}", flush=True)
+
+
+def f16(shape, seed, std=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * std).to(torch.float16)
+
+
+# ----------------------------------------------------------------------------- norms
+@pytest.mark.parametrize("rows", [1, 5, 32, 257])
+def test_add_rmsnorm(gpu, rows):
+    from omniserve_amd import fused_ops as F
+    say(f"add_rmsnorm rows={rows}")
+    H = 1536
+    x, r = f16((rows, H), 1), f16((rows, H), 2)
+    w = (1.0 + 0.1 * f16((H,), 3).float()).to(torch.float16)
+    y, nr = F.add_rms_norm(x.to(gpu), r.to(gpu), w.to(gpu), 1e-6)
+    ey, er = ref.add_rms_norm(x.float(), r.float(), w.float(), 1e-6)
+    assert torch.equal(nr.cpu().float(), er)                 # residual add: exact fp16
+    d = (y.cpu().float() - ey).abs()
+    assert d.max().item() <= 2e-3 * max(1.0, ey.abs().max().item())
+    assert (d > 0).float().mean().item() < 0.02              # almost all bit-equal
+
+
+def test_rmsnorm_and_embed(gpu):
+    from omniserve_amd import fused_ops as F
+    say("rmsnorm / embedding gather (plain + packed) / embed_rmsnorm")
+    V, H = 4096, 1536
+    table = f16((V, H), 7, 0.02)
+    ids = torch.tensor([0, 5, 4095, 17, 1000], dtype=torch.int64)
+    w = torch.ones(H, dtype=torch.float16)
+    y = F.rms_norm(table[ids].to(gpu), w.to(gpu), 1e-6)
+    ey = ref.rms_norm(table[ids].float(), w.float(), 1e-6)
+    assert (y.cpu().float() - ey).abs().max().item() <= 2e-3 * ey.abs().max().item()
+
+    from omniserve_amd.linear import LMHeadArgmax
+    lm = LMHeadArgmax(table.to(gpu))
+    out = torch.empty(len(ids), H, device=gpu, dtype=torch.float16)
+    F.embedding_out(ids.to(gpu), lm.table_packed, True, out)
+    assert torch.equal(out.cpu(), table[ids])
+    out2 = torch.empty_like(out)
+    F.embedding_out(ids.to(gpu), table.to(gpu), False, out2)
+    assert torch.equal(out2.cpu(), table[ids])
+    h = torch.empty_like(out)
+    res = torch.empty_like(out)
+    F.embed_rms_norm_out(ids.to(gpu), lm.table_packed, True, w.to(gpu), 1e-6, h, res)
+    assert torch.equal(res.cpu(), table[ids])
+    assert torch.equal(h.cpu(), y.cpu())
+
+
+def test_add_rmsnorm_fp8(gpu):
+    from omniserve_amd import fused_ops as F
+    say("add_rmsnorm_fp8")
+    M, H = 64, 1536
+    x, r = f16((M, H), 11), f16((M, H), 12)
+    w = torch.ones(H, dtype=torch.float16)
+    q, s, nr = F.add_rms_norm_fp8(x.to(gpu), r.to(gpu), w.to(gpu), 1e-6)
+    eq, es, er = ref.add_rms_norm_fp8(x.float(), r.float(), w.float(), 1e-6)
+    assert torch.equal(nr.cpu().float(), er)
+    assert torch.allclose(s.cpu(), es, rtol=1e-5, atol=0)
+    qd, eqd = q.cpu().float(), eq.float()
+    mism = (q.cpu().view(torch.uint8) != eq.view(torch.uint8)).float().mean().item()
+    assert mism < 0.01
+    # any mismatch is one e4m3 step: relative difference <= 2^-3
+    assert ((qd - eqd).abs() <= 0.125 * eqd.abs() + 2.0 ** -9).all()
+
+
+def test_silu_mul(gpu):
+    from omniserve_amd import fused_ops as F
+    say("silu_mul")
+    gu = f16((7, 2 * 8960), 21, 2.0)
+    y = F.silu_mul(gu.to(gpu)).cpu().float()
+    ey = ref.silu_mul(gu.float())
+    d = (y - ey).abs()
+    assert d.max().item() <= 1e-3 * max(1.0, ey.abs().max().item())
+
+
+# ----------------------------------------------------------------------------- rope + kv
+@pytest.mark.parametrize("T", [1, 3, 32])
+def test_mrope_kv_write_decode(gpu, T):
+    """Decode form: positions = lengths[row] + rope_delta[row] on all three axes;
+    rotated K and raw V land at pool[row, lengths[row]].  Bit-exact vs the oracle."""
+    from omniserve_amd._lib import call, ptr, stream
+    from omniserve_amd.qwen2_llm import rope_tables
+    say(f"mrope_kv_write decode T={T}")
+    cfg = ref.Qwen2Config()
+    nh, nkv, hd = 12, 2, 128
+    P, ML = T + 1, 64
+    qkv = f16((T, (nh + 2 * nkv) * hd), 31)
+    lengths = torch.randint(0, 40, (P,), generator=torch.Generator().manual_seed(2))
+    delta = torch.randint(-5, 6, (P,), generator=torch.Generator().manual_seed(3))
+    cos, sin = rope_tables(cfg, 256, gpu)
+    kc = torch.zeros(P, ML, nkv, hd, dtype=torch.float16, device=gpu)
+    vc = torch.zeros_like(kc)
+    g = qkv.to(gpu)
+    lg, dg = lengths.to(gpu), delta.to(gpu)   # kept alive until the kernel has run
+    call("omni_mrope_kv_write", ptr(g), g.stride(0), None, ptr(lg), ptr(dg), ptr(cos),
+         ptr(sin), 256, ptr(kc), ptr(vc), None, None, P, ML, T, nh, nkv, hd, 16, 24, 24,
+         stream())
+    torch.cuda.synchronize()
+    pos = (lengths[:T] + delta[:T]).clamp(min=0)
+    c, s = ref.rope_cos_sin(pos.view(1, 1, T).expand(3, 1, T), cfg)
+    q = qkv[:, :nh * hd].float().view(T, nh, hd).transpose(0, 1).unsqueeze(0)
+    k = qkv[:, nh * hd:(nh + nkv) * hd].float().view(T, nkv, hd).transpose(0, 1).unsqueeze(0)
+    qr, kr = ref.apply_mrope(q, k, c, s, cfg.mrope_section)
+    out = g.cpu().float()
+    assert torch.equal(out[:, :nh * hd].view(T, nh, hd), qr[0].transpose(0, 1))
+    assert torch.equal(out[:, nh * hd:(nh + nkv) * hd].view(T, nkv, hd), kr[0].transpose(0, 1))
+    kcc, vcc = kc.cpu().float(), vc.cpu().float()
+    v = qkv[:, (nh + nkv) * hd:].float().view(T, nkv, hd)
+    for t in range(T):
+        assert torch.equal(kcc[t, lengths[t]], kr[0, :, t])
+        assert torch.equal(vcc[t, lengths[t]], v[t])
+    # nothing else written
+    assert (kcc != 0).sum().item() == (kr[0] != 0).sum().item()
+
+
+def test_mrope_3d_positions(gpu):
+    """Prefill form with distinct t/h/w position ids (image tokens): bit-exact."""
+    from omniserve_amd._lib import call, ptr, stream
+    from omniserve_amd.qwen2_llm import rope_tables
+    say("mrope 3-D positions")
+    cfg = ref.Qwen2Config()
+    nh, nkv, hd = 12, 2, 128
+    ids = [1] * 4 + [151655] * 16 + [2] * 3
+    pos, delta = ref.mrope_position_ids(ids, [(1, 8, 8)])
+    T = len(ids)
+    qkv = f16((T, (nh + 2 * nkv) * hd), 41)
+    cos, sin = rope_tables(cfg, 64, gpu)
+    g = qkv.to(gpu)
+    pg = pos.contiguous().to(gpu)
+    call("omni_mrope_kv_write", ptr(g), g.stride(0), ptr(pg), None, None, ptr(cos), ptr(sin),
+         64, None, None, None, None, 0, 0, T, nh, nkv, hd, 16, 24, 24, stream())
+    torch.cuda.synchronize()
+    c, s = ref.rope_cos_sin(pos.view(3, 1, T), cfg)
+    q = qkv[:, :nh * hd].float().view(T, nh, hd).transpose(0, 1).unsqueeze(0)
+    k = qkv[:, nh * hd:(nh + nkv) * hd].float().view(T, nkv, hd).transpose(0, 1).unsqueeze(0)
+    qr, kr = ref.apply_mrope(q, k, c, s, cfg.mrope_section)
+    out = g.cpu().float()
+    assert torch.equal(out[:, :nh * hd].view(T, nh, hd), qr[0].transpose(0, 1))
+    assert torch.equal(out[:, nh * hd:(nh + nkv) * hd].view(T, nkv, hd), kr[0].transpose(0, 1))
+
+
+# ----------------------------------------------------------------------------- attention
+@pytest.mark.parametrize("lengths,splits", [
+    ([1], 1), ([7], 1), ([33, 64, 100], 1), ([300, 5, 1000], 4), ([2048] * 4, 8),
+    ([1, 2, 3, 4095], 16),
+])
+def test_decode_attention(gpu, lengths, splits):
+    from omniserve_amd._lib import call, ptr, stream
+    say(f"decode_attention lengths={lengths} splits={splits}")
+    n = len(lengths)
+    nh, nkv, hd, ML = 12, 2, 128, 4096
+    P = n + 1
+    kp = f16((P, ML, nkv, hd), 51)
+    vp = f16((P, ML, nkv, hd), 52)
+    q = f16((n, nh * hd), 53)
+    L = torch.tensor(lengths, dtype=torch.int64)
+    out = torch.empty(n, nh, hd, device=gpu, dtype=torch.float16)
+    ws = torch.empty(n * nkv * splits * 6 * 130, device=gpu, dtype=torch.float32)
+    ctr = torch.zeros(n * nkv, device=gpu, dtype=torch.int32)
+    scale = hd ** -0.5
+    kg, vg, qg, Lg = kp.to(gpu), vp.to(gpu), q.to(gpu), L.to(gpu)
+    for rep in range(2):   # second launch checks the counters were reset
+        call("omni_decode_attention", ptr(qg), nh * hd, ptr(kg), ptr(vg), P, ML, None,
+             ptr(Lg), 0, 0, ptr(out), n, nh, nkv, hd, scale, splits, ptr(ws), ptr(ctr),
+             stream())
+        torch.cuda.synchronize()
+        e = ref.decode_attention(q.float().view(n, nh, hd), kp.float(), vp.float(),
+                                 torch.arange(n), L, scale)
+        d = (out.cpu().float() - e).abs().max().item()
+        assert d <= 4e-3, d
+    assert ctr.cpu().eq(0).all()
+
+
+@pytest.mark.parametrize("segs", [[1], [5, 16, 17], [256], [100, 37, 512]])
+def test_prefill_attention(gpu, segs):
+    from omniserve_amd.attention import query_blocks
+    from omniserve_amd._lib import call, ptr, stream
+    say(f"prefill_attention segs={segs}")
+    nh, nkv, hd, ML = 12, 2, 128, 1024
+    P = len(segs)
+    T = sum(segs)
+    q = f16((T, nh * hd), 61)
+    k = f16((T, nkv, hd), 62)
+    v = f16((T, nkv, hd), 63)
+    kp = torch.zeros(P, ML, nkv, hd, dtype=torch.float16)
+    vp = torch.zeros_like(kp)
+    slot, pos = [], []
+    off = 0
+    for s, Ls in enumerate(segs):
+        kp[s, :Ls] = k[off:off + Ls]
+        vp[s, :Ls] = v[off:off + Ls]
+        slot += [s] * Ls
+        pos += list(range(Ls))
+        off += Ls
+    slot_t = torch.tensor(slot, dtype=torch.int64, device=gpu)
+    kvl = torch.tensor(pos, dtype=torch.int64, device=gpu) + 1
+    qb = query_blocks(segs, gpu)
+    out = torch.empty(T, nh, hd, device=gpu, dtype=torch.float16)
+    qg, kg, vg = q.to(gpu), kp.to(gpu), vp.to(gpu)
+    call("omni_prefill_attention", ptr(qg), nh * hd, ptr(kg), ptr(vg), P, ML, ptr(slot_t),
+         ptr(kvl), ptr(qb), qb.shape[0], ptr(out), nh * hd, nh, nkv, hd, hd ** -0.5, stream())
+    torch.cuda.synchronize()
+    e = ref.prefill_attention(q.float().view(T, nh, hd), k.float(), v.float(), segs, hd ** -0.5)
+    d = (out.cpu().float() - e).abs().max().item()
+    assert d <= 4e-3, d
+
+
+# ----------------------------------------------------------------------------- linears
+def _gptq(K, N, seed):
+    from omniserve_amd.synth import gptq_random
+    return gptq_random(K, N, seed, "t")
+
+
+@pytest.mark.parametrize("K,N", [(1536, 2048), (8960, 1536), (1536, 256)])
+def test_w4_dequant_bit_exact(gpu, K, N):
+    from omniserve_amd.linear import GPTQLinear
+    say(f"int4 dequant K={K} N={N}")
+    qw, sc = _gptq(K, N, 71)
+    lin = GPTQLinear(qw.to(gpu), sc.to(gpu))
+    w = lin.dequantized().cpu().float()
+    e = ref.gptq_dequant(qw, sc)
+    assert torch.equal(w, e)
+
+
+@pytest.mark.parametrize("M", [1, 16, 32, 48, 64])
+@pytest.mark.parametrize("K,N,bias,silu", [
+    (1536, 2048, True, False), (1536, 1536, False, False), (8960, 1536, False, False),
+    (1536, 17920, False, True),
+])
+def test_w4a16_gemm(gpu, M, K, N, bias, silu):
+    from omniserve_amd.linear import GPTQLinear
+    say(f"w4a16 M={M} K={K} N={N} bias={bias} silu={silu}")
+    qw, sc = _gptq(K, N, 72 + K + N)
+    b = f16((N,), 73, 0.02) if bias else None
+    x = f16((M, K), 74)
+    lin = GPTQLinear(qw.to(gpu), sc.to(gpu), None if b is None else b.to(gpu), fuse_silu=silu)
+    y = lin(x.to(gpu)).cpu().float()
+    W = ref.gptq_dequant(qw, sc)
+    if silu:
+        e = ref.silu_mul(ref.linear(x.float(), W))
+    else:
+        e = ref.linear(x.float(), W, None if b is None else b.float(), bias_after_round=True)
+    d = (y - e).abs()
+    tol = 2e-3 * max(1.0, e.abs().max().item())
+    assert d.max().item() <= tol, (d.max().item(), tol)
+
+
+@pytest.mark.parametrize("M", [1, 16, 32])
+@pytest.mark.parametrize("K,N,bias,silu", [
+    (1536, 2048, True, False), (8960, 1536, False, False), (1536, 17920, False, True),
+])
+def test_f16_gemm(gpu, M, K, N, bias, silu):
+    from omniserve_amd.linear import F16Linear
+    say(f"f16 gemm M={M} K={K} N={N} bias={bias} silu={silu}")
+    w = f16((N, K), 81, 0.02)
+    b = f16((N,), 82, 0.02) if bias else None
+    x = f16((M, K), 83)
+    lin = F16Linear(w.to(gpu), None if b is None else b.to(gpu), fuse_silu=silu)
+    y = lin(x.to(gpu)).cpu().float()
+    if silu:
+        e = ref.silu_mul(ref.linear(x.float(), w.float().t()))
+    else:
+        e = ref.linear(x.float(), w.float().t(), None if b is None else b.float())
+    d = (y - e).abs()
+    tol = 2e-3 * max(1.0, e.abs().max().item())
+    assert d.max().item() <= tol, (d.max().item(), tol)
+
+
+@pytest.mark.parametrize("M", [1, 32])
+def test_lmhead_argmax(gpu, M):
+    from omniserve_amd.linear import LMHeadArgmax
+    say(f"lm_head argmax M={M}")
+    V, H = 151936, 1536
+    E = f16((V, H), 91, 0.02)
+    h = f16((M, H), 92)
+    lm = LMHeadArgmax(E.to(gpu))
+    ids = torch.empty(M, device=gpu, dtype=torch.int64)
+    logits = torch.empty(M, V, device=gpu, dtype=torch.float16)
+    for rep in range(2):
+        lm.argmax_out(h.to(gpu), ids, logits)
+        torch.cuda.synchronize()
+    e = ref.r16(h.float() @ E.float().t())
+    lg = logits.cpu().float()
+    d = (lg - e).abs().max().item()
+    assert d <= 2e-2, d
+    cos = torch.nn.functional.cosine_similarity(lg, e, dim=-1).min().item()
+    assert cos >= 0.9999
+    # the fused argmax is exactly torch.argmax of the kernel's own fp16 logits
+    assert torch.equal(ids.cpu(), logits.cpu().float().argmax(-1))
+    # and agrees with the oracle wherever the oracle's top-2 margin exceeds the tolerance
+    margin = ref.top2_margin(e)
+    ok = margin > 2 * d
+    assert torch.equal(ids.cpu()[ok], e.argmax(-1)[ok])
+
+
+def test_lmhead_argmax_ties(gpu):
+    """Equal fp16 logits at several columns: the lowest index wins (torch.argmax)."""
+    from omniserve_amd.linear import LMHeadArgmax
+    say("lm_head argmax ties")
+    V, H = 151936, 1536
+    E = torch.zeros(V, H, dtype=torch.float16)
+    for n in (70000, 3, 151935, 1000):
+        E[n, 0] = 1.0
+    h = torch.zeros(2, H, dtype=torch.float16)
+    h[:, 0] = 1.0
+    lm = LMHeadArgmax(E.to(gpu))
+    ids = torch.empty(2, device=gpu, dtype=torch.int64)
+    lm.argmax_out(h.to(gpu), ids)
+    torch.cuda.synchronize()
+    assert ids.cpu().tolist() == [3, 3]

@@ -1,0 +1,267 @@
+"""Decode-step benchmark of the Qwen2-VL-2B text decoder on one MI355X.
+
+Workload (the north-star configuration): W4A16 GPTQ
+decoder (all q/k/v/o/gate/up/down int4 symmetric, group 128, codes U{0..15},
+zero point 8, scales |N(0,0.02)|/7; fp16 embeddings / lm_head), batch 32, each
+sequence with a 2048-token context already in the KV pool [32(+1), 4096, 2, 128]
+fp16 (N(0,1) values), greedy decode, one new token per sequence per step.  Random
+seeded weights of the real architecture (no checkpoints offline).
+
+A step is one ``NativeQwenVLRunner.decode`` call (hipGraph replay of the whole
+28-layer step + lm_head/argmax, the H2D of token ids when needed, the D2H of the
+new ids).  ``value`` = 32 * steps / wall time of the timed steps.
+
+The JSON line also carries:
+* ``roofline`` for the dominant kernel (the split-K decode attention: ~63% of the
+  step's algorithmic bytes): algorithmic bytes per launch / its mean duration,
+  timed with HIP events on the stream it runs on, against 8 TB/s;
+* ``step_roofline``: algorithmic bytes per step / ms_per_step against 8 TB/s;
+* ``cpu_baseline``: the fp32 CPU restatement (oracle/) of the same step, timed on
+  this host on a bounded sample.
+
+Usage: python bench.py [--gpus 1] [--steps 128] [--warmup 3] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+PEAK_HBM = 8.0e12  # MI355X HBM3E, bytes/s
+
+H, I, NL, NH, NKV, HD, V = 1536, 8960, 28, 12, 2, 128, 151936
+LINEARS = [(H, (NH + 2 * NKV) * HD), (NH * HD, H), (H, 2 * I), (I, H)]   # (K, N)
+KV_TOKEN_BYTES = NL * 2 * NKV * HD * 2                                  # 28672 B / token
+
+
+def weight_bytes(quant: str) -> int:
+    """Algorithmic weight bytes per decode step (each weight read once)."""
+    if quant == "gptq":
+        lin = sum(K * N // 2 + (K // 128) * N * 2 for K, N in LINEARS)
+    else:
+        lin = sum(2 * K * N for K, N in LINEARS)
+    bias = 2 * LINEARS[0][1]
+    return NL * (lin + bias) + 2 * H * (2 * NL + 1) + 2 * V * H
+
+
+def step_bytes(quant: str, ctx_lens) -> int:
+    """Algorithmic HBM bytes of one decode step with the given pre-step context lengths:
+    weights once, attended KV rows once (incl. the new token), new KV rows written once,
+    embedding rows and ids.  Activations/logits are excluded (fusible)."""
+    B = len(ctx_lens)
+    kv_read = sum(int(L) + 1 for L in ctx_lens) * KV_TOKEN_BYTES
+    return weight_bytes(quant) + kv_read + B * KV_TOKEN_BYTES + B * H * 2 + B * 16
+
+
+def attn_launch_bytes(ctx_lens) -> int:
+    """Algorithmic bytes of one decode-attention launch (one layer): K and V rows
+    [0, L] of both KV heads, q in, output out."""
+    kv = sum(int(L) + 1 for L in ctx_lens) * 2 * NKV * HD * 2
+    return kv + 2 * len(ctx_lens) * NH * HD * 2
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def build_config3(device, batch: int = 32, ctx: int = 2048, max_len: int = 4096, seed: int = 0):
+    from omniserve_amd import synth
+    from omniserve_amd.request import Request, SamplingParams, Sequence
+    from omniserve_amd.runner import NativeQwenVLRunner
+
+    shape = synth.DecoderShape()
+    t0 = time.time()
+    w = synth.gptq_decoder(shape, seed=seed)
+    log(f"synthetic int4 weights generated in {time.time() - t0:.1f}s")
+    runner = NativeQwenVLRunner(max_running=batch, max_len=max_len, use_graph=True,
+                                quant="gptq", weights=w)
+    pool = runner.pool
+    g = torch.Generator(device=device)
+    g.manual_seed(seed + 1)
+    for l in range(NL):
+        for kv in (0, 1):
+            pool.storage[l, kv, :batch, :ctx].normal_(generator=g)
+    seqs = []
+    for b in range(batch):
+        ids = synth.random_ids(ctx, shape.vocab_size, seed, f"ctx{b}").tolist()
+        s = Sequence(Request(prompt=ids, sampling=SamplingParams(max_new_tokens=1 << 30)))
+        runner.tokenize(s)
+        s.request.sampling.stop_token_ids.clear()      # fixed-length decode
+        seqs.append(s)
+    runner.attach_prefilled(seqs, [ctx] * batch)
+    torch.cuda.synchronize()
+    log(f"config3 runner ready (pool {tuple(pool.storage.shape)})")
+    return runner, seqs, w, shape
+
+
+def time_kernel(fn, reps: int) -> float:
+    """Mean duration (s) of fn() over reps launches, HIP events on the current stream."""
+    st = torch.cuda.current_stream()
+    fn()
+    st.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(reps):
+        fn()
+    e1.record(st)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / 1e3 / reps
+
+
+def cpu_baseline(runner, seqs, w, shape, budget_s: float = 15.0) -> dict:
+    """fp32 CPU restatement (oracle) of the same decode step on this host's cores."""
+    from oracle import qwen2_ref as ref
+    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "16") or 16), 16)
+    torch.set_num_threads(threads)
+    t0 = time.time()
+    cfg = ref.Qwen2Config()
+    layers = [ref.LayerWeights(
+        in_norm=l["in_norm"].float(), post_norm=l["post_norm"].float(),
+        qkv_t=ref.gptq_dequant(l["qkv_q"], l["qkv_s"]), qkv_b=l["qkv_b"].float(),
+        o_t=ref.gptq_dequant(l["o_q"], l["o_s"]),
+        gate_up_t=ref.gptq_dequant(l["gate_up_q"], l["gate_up_s"]),
+        down_t=ref.gptq_dequant(l["down_q"], l["down_s"])) for l in w["layers"]]
+    orc = ref.Qwen2Ref(cfg, w["embed"].float(), w["norm"].float(), layers, True, f16=False)
+    B = len(seqs)
+    lengths = runner.pool.lengths[:B].cpu()
+    Lmax = int(lengths.max()) + 16
+    kp = [runner.pool.k[l][:B, :Lmax].float().cpu() for l in range(NL)]
+    vp = [runner.pool.v[l][:B, :Lmax].float().cpu() for l in range(NL)]
+    lengths = torch.cat([lengths, torch.zeros(1, dtype=torch.int64)])
+    log(f"cpu baseline: oracle built in {time.time() - t0:.1f}s, {threads} threads")
+    ids = [s.last_token_id() for s in seqs]
+    orc.decode_step(ids, kp, vp, lengths)          # warm-up
+    lengths[:B] += 1
+    n, t1 = 0, time.perf_counter()
+    while True:
+        orc.decode_step(ids, kp, vp, lengths)
+        lengths[:B] += 1
+        n += 1
+        el = time.perf_counter() - t1
+        if el >= budget_s or n >= 8:
+            break
+    per = el / n
+    return {"value": round(B / per, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "ms_per_step": round(per * 1e3, 1),
+            "sample": f"{n} decode steps (after 1 warm-up) of the same B={B}, ctx~{int(lengths[0])} "
+                      f"int4 config, all 28 layers, fp32 oracle (weights dequantised once)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--ctx", type=int, default=2048)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--kernel-reps", type=int, default=20)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(data-parallel sharding by sequence is a design note, not implemented)",
+              file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    runner, seqs, w, shape = build_config3(dev, args.batch, args.ctx)
+    B = len(seqs)
+
+    for _ in range(args.warmup):
+        runner.decode(seqs)
+    torch.cuda.synchronize()
+
+    ctx_before = runner.pool.lengths[:B].cpu().tolist()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record(st)
+    for _ in range(args.steps):
+        runner.decode(seqs)
+    e1.record(st)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    dev_ms = e0.elapsed_time(e1) / args.steps
+    ms = wall * 1e3 / args.steps
+    tok_s = B * args.steps / wall
+
+    # algorithmic bytes per step, averaged over the timed steps (contexts grow by 1/step)
+    avg_step_bytes = sum(step_bytes("gptq", [L + s for L in ctx_before])
+                         for s in range(args.steps)) / args.steps
+
+    # dominant kernel: decode attention of one layer at the current context
+    model = runner.adapter.model
+    bufs = model.decode_buffers(B, dev)
+    view = runner.pool.view(B, runner._rope_delta)
+    ctx_now = runner.pool.lengths[:B].cpu().tolist()
+    t_attn = time_kernel(lambda: view.attend_qkv(bufs["qkv"], 0, model.scale, bufs["attn"]),
+                         args.kernel_reps)
+    a_bytes = attn_launch_bytes([L - 1 for L in ctx_now])   # kv_len = lengths + 1 keys
+    achieved = a_bytes / t_attn
+    # second-largest stream: the gate_up W4A16 GEMM with the fused SiLU
+    lay = model.layers[0]
+    t_gu = time_kernel(lambda: lay.gate_up_proj.forward_out(bufs["h"], bufs["act"]),
+                       args.kernel_reps)
+    gu_bytes = H * 2 * I // 2 + (H // 128) * 2 * I * 2 + B * H * 2 + B * I * 2
+
+    out = {
+        "metric": "decode tok/s + ms/step, Qwen2-VL-2B LLM shape, B=1/32 int4; % HBM roofline",
+        "value": round(tok_s, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {
+            "workload": "Qwen2-VL-2B text decoder, W4A16 GPTQ int4 g128 (lm_head/embed fp16), "
+                        f"greedy decode B={B}, ctx {args.ctx} (pool [{B},{runner.pool.max_len},2,128] "
+                        "fp16, N(0,1) prefix), hipGraph step",
+            "batch": B, "context": args.ctx, "max_len": runner.pool.max_len,
+            "weights": "int4 codes U{0..15} zp 8, scales |N(0,0.02)|/7, seeded",
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm", "kernel": "decode_attn_kernel (split-K GQA decode attention, 1 layer)",
+            "achieved": round(achieved / 1e9, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM, 4), "traffic": None,
+            "launch_us": round(t_attn * 1e6, 2), "bytes_per_launch": a_bytes,
+        },
+        "step_roofline": {
+            "bytes_per_step": int(avg_step_bytes),
+            "achieved": round(avg_step_bytes / (ms / 1e3) / 1e9, 1), "unit": "GB/s",
+            "frac": round(avg_step_bytes / (ms / 1e3) / PEAK_HBM, 4),
+            "device_ms_per_step": round(dev_ms, 4),
+            "device_frac": round(avg_step_bytes / (dev_ms / 1e3) / PEAK_HBM, 4),
+        },
+        "kernels": {
+            "gate_up_w4a16_silu_us": round(t_gu * 1e6, 2),
+            "gate_up_GBps": round(gu_bytes / t_gu / 1e9, 1),
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        try:
+            out["cpu_baseline"] = cpu_baseline(runner, seqs, w, shape)
+        except Exception as e:  # report, never fail the GPU line on the CPU leg
+            out["cpu_baseline"] = {"error": repr(e)}
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -25,19 +25,24 @@ SIGNATURES = {
     "omni_rmsnorm": [_P, _P, _P, _I, _I, _F, _P],
     "omni_add_rmsnorm": [_P, _P, _P, _P, _P, _I, _I, _F, _P],
     "omni_add_rmsnorm_fp8": [_P, _P, _P, _P, _P, _P, _I, _I, _F, _P],
+    "omni_add_rmsnorm_partials": [_P, _I, _P, _P, _P, _P, _I, _I, _F, _P],
     "omni_embed_rmsnorm": [_P, _P, _I, _I64, _P, _P, _P, _I, _I, _F, _P],
     "omni_embedding": [_P, _P, _I, _I64, _P, _I, _I, _P],
     "omni_silu_mul": [_P, _P, _I, _I, _P],
     "omni_mrope_kv_write": [_P, _I, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I,
                             _I, _I, _I, _I, _P],
+    "omni_mrope_kv_write_partials": [_P, _I, _P, _I, _P, _I, _P, _P, _P, _P, _P, _I, _P, _P, _P,
+                                     _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P],
     "omni_decode_attention": [_P, _I, _P, _P, _I, _I, _P, _P, _I, _I, _P, _I, _I, _I, _I, _F, _I,
-                              _P, _P, _P],
+                              _I, _P, _P],
     "omni_prefill_attention": [_P, _I, _P, _P, _I, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _F,
                                _P],
-    "omni_w4a16_gemm": [_P, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P],
-    "omni_f16_gemm": [_P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P],
+    "omni_w4a16_gemm": [_P, _I, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I, _I, _P],
+    "omni_f16_gemm": [_P, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I, _P],
+    "omni_gemm_slices": [_I, _I],
     "omni_lmhead_argmax_grid": [_I],
-    "omni_lmhead_argmax": [_P, _I, _P, _I, _I, _I, _P, _P, _P, _P, _P, _P],
+    "omni_lmhead_candidates": [_P, _I, _P, _I, _I, _I, _P, _P, _P, _P],
+    "omni_argmax_finalize": [_P, _P, _I, _I, _P, _P, _P, _P],
     "omni_gptq_repack": [_P, _P, _P, _P, _I, _I, _I, _P],
     "omni_f16_pack": [_P, _P, _I, _I, _I, _P],
     "omni_w4_dequant": [_P, _P, _P, _I, _I, _P],

@@ -1,0 +1,97 @@
+"""Qwen2-VL adapter: model-specific pieces the generic runner delegates to.
+
+Mirrors the ``VLMAdapter`` interface (omniserve/models/base.py:24-74) as implemented
+by ``Qwen2VLAdapter`` (models/qwen2_vl.py:30-122) for the text decoder:
+embed_tokens (:93-94), prefill_positions (:100-106), decode_positions (:108-112),
+llm (:115-116), plus the shape attributes the KV pool needs.
+
+Weights: there are no checkpoints offline, so ``model_dir=None`` builds seeded
+synthetic weights of the real architecture (``synth``); ``weights=`` accepts an
+already generated dict (fp16 or GPTQ layout).  ``quant="gptq"`` selects the int4
+path (every decoder linear W4A16, embeddings / lm_head fp16, as
+kernels/marlin_linear.py:114-143).
+"""
+
+from __future__ import annotations
+
+from typing import List, Optional
+
+import torch
+
+from . import synth
+from .positions import IMAGE_TOKEN_ID, mrope_positions
+from .qwen2_llm import Qwen2LLM
+
+EOS_ID = 151645  # <|im_end|>
+
+
+class Qwen2VLAdapter:
+    def __init__(self, model_dir: Optional[str] = None, quant: Optional[str] = None,
+                 gptq_dir: Optional[str] = None, weights: Optional[dict] = None,
+                 shape: Optional[synth.DecoderShape] = None, seed: int = 0,
+                 num_layers: Optional[int] = None, device="cuda", max_pos: int = 8192):
+        if quant not in (None, "gptq"):
+            raise ValueError(f"unsupported quant {quant!r} (None or 'gptq')")
+        if model_dir is not None or gptq_dir is not None:
+            raise NotImplementedError("checkpoint loading is not part of this build; "
+                                      "pass weights= or use synthetic weights")
+        self.device = torch.device(device)
+        self.shape = shape or synth.DecoderShape()
+        if num_layers is not None:
+            self.shape.num_layers = num_layers
+        self.quant = quant
+        if weights is None:
+            gen = synth.gptq_decoder if quant == "gptq" else synth.fp16_decoder
+            weights = gen(self.shape, seed=seed)
+        build = Qwen2LLM.from_gptq if quant == "gptq" else Qwen2LLM.from_fp16
+        self._llm = build(weights, self.shape, self.device, max_pos=max_pos)
+        self.num_layers = len(weights["layers"])
+        self.num_kv_heads = self.shape.num_kv_heads
+        self.num_heads = self.shape.num_heads
+        self.head_dim = self.shape.head_dim
+        self.image_token_id = IMAGE_TOKEN_ID
+        self.eos_ids = {EOS_ID}
+
+    @property
+    def model(self) -> Qwen2LLM:
+        return self._llm
+
+    # ---- input side ---------------------------------------------------------------
+    def encode_prompt(self, prompt, grids=None) -> List[int]:
+        """Token ids of a prompt: a list of ids is taken as is; a string must be
+        whitespace-separated integer ids (there is no tokenizer offline)."""
+        if isinstance(prompt, str):
+            return [int(t) for t in prompt.split()]
+        return [int(t) for t in prompt]
+
+    def embed_tokens(self, input_ids: torch.Tensor) -> torch.Tensor:
+        return self._llm.embed_tokens(input_ids)
+
+    def vision_embed(self, images) -> torch.Tensor:
+        """Concatenated vision rows of the request's images (already ViT outputs)."""
+        rows = [im.embeds.to(self.device, torch.float16) for im in images]
+        return torch.cat(rows, 0)
+
+    # ---- positions (M-RoPE) -------------------------------------------------------
+    def prefill_positions(self, input_ids, grids):
+        L = len(input_ids)
+        if not grids:
+            pos = torch.arange(L, dtype=torch.int64).view(1, -1).expand(3, -1)
+            return pos, 0
+        return mrope_positions(input_ids, grids, self.image_token_id)
+
+    def decode_positions(self, write_pos: torch.Tensor, rope_deltas: torch.Tensor):
+        n = write_pos.shape[0]
+        pos = torch.empty(3, n, 1, device=write_pos.device, dtype=torch.long)
+        pos[:, :, 0] = (write_pos + rope_deltas).unsqueeze(0)
+        return pos
+
+    # ---- forward ------------------------------------------------------------------
+    def llm(self, embeds, positions, attn_mask, cache, logits_indices=None):
+        return self._llm(embeds, positions, attn_mask, cache, logits_indices=logits_indices)
+
+    def detokenize(self, token_ids) -> str:
+        return " ".join(str(int(t)) for t in token_ids)
+
+    def supports_quant(self, quant) -> bool:
+        return quant in (None, "gptq")

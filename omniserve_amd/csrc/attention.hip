@@ -1,31 +1,30 @@
-// GQA split-K decode attention over the preallocated KV pool.
+// GQA decode attention over the preallocated KV pool.
 //
 // Replaces the paged flash-decode call in omniserve/cache/kv_prealloc.py:272-290:
 // for every query token t (pool row slot[t]) and query head h the output is
 //   softmax(scale * q[t,h] . K[slot, 0:L, h div G]^T) . V[slot, 0:L, h div G]
-// with L = kv_len (keys [0, L) inclusive of the token written this step),
+// with L = kv_len (keys [0, L), inclusive of the token written this step),
 // G = n_heads / n_kv_heads query heads per KV head (6 for Qwen2-VL-2B).
 //
 // Pool layout (kept from the reference): K, V = [pool_rows, max_len, n_kv, 128] fp16.
 //
-// Work split: one workgroup = (token, kv head, split group); its 4 waves each
-// stream a contiguous 32-token-aligned range of the context, so each K/V row
-// of a KV head is read from HBM exactly once for all G query heads sharing it.
-// Per 32-token block a wave does
+// Work split: one workgroup per (token, kv head); its NWA waves (4, 8 or 16) each
+// stream a contiguous 32-token-aligned range of the context, so each K/V row of a
+// KV head is read from HBM exactly once for all G query heads sharing it, and the
+// waves' partial softmax states are merged in LDS.  Nothing crosses workgroups (no
+// device-scope fences).  Per 32-token block a wave does
 //   S^T[16 tok x 16 heads] = K[16 x 128] . Q^T     (4 MFMA 16x16x32 per 16 tokens,
 //                                                   K fed straight from global)
 //   online softmax in fp32 (exp2, running max/sum per head)
 //   O[16 heads x 128] += P[16 x 32] . V[32 x 128]  (8 MFMAs, V transposed via LDS)
-// Waves combine in LDS; split groups combine through a small fp32 workspace,
-// the last-arriving workgroup (device-scope counter, reset by that workgroup)
-// writing the fp16 output, so the kernel is graph-replayable with no memset.
+// while the next block's K and V loads are already in flight.
 #include "common.h"
 
 #define ATT_HD 128
 #define ATT_BLK 32
-#define ATT_WAVES 4
 #define ATT_VSTRIDE 136   // LDS row stride (halfs) of the V tile: 16B-aligned, bank-spread
 #define ATT_MAXG 16       // query heads per KV head supported (MFMA N = 16)
+#define ATT_WAVES 4       // waves per workgroup of the prefill kernel
 
 struct AttnArgs {
   const half_t* q;
@@ -38,34 +37,33 @@ struct AttnArgs {
   int kv_by_slot;
   int kv_add;            // kv = kv_len[...] + kv_add
   half_t* out;           // [T, nkv*G, 128]
-  float* ws;             // [T, nkv, S, G, 128 + 2]   (S > 1)
-  int* counters;         // [T, nkv] zero-initialised, self-resetting (S > 1)
+  float* part;           // S > 1: [T][nkv][S][G][128 + 2] fp32 (O unnormalised, m, l)
+  int S;                 // workgroups per (token, kv head)
   float scale_log2;
   int T;
-  int S;                 // split groups per (token, kv head)
 };
 
 __device__ __forceinline__ int64_t clamp64(int64_t v, int64_t lo, int64_t hi) {
   return v < lo ? lo : (v > hi ? hi : v);
 }
 
-__global__ __launch_bounds__(256, 2) void decode_attn_kernel(AttnArgs a) {
-  // The V tiles (used in the block loop) and the per-wave partial outputs
-  // (used after it) share one LDS buffer.
-  constexpr int kVsBytes = ATT_WAVES * ATT_BLK * ATT_VSTRIDE * 2;
-  constexpr int kOBytes = ATT_WAVES * ATT_MAXG * ATT_HD * 4;
+template <int NWA>
+__global__ __launch_bounds__(NWA * 64) void decode_attn_kernel(AttnArgs a) {
+  // The V tiles (used in the block loop) and the per-wave partial outputs (used
+  // after it) share one LDS buffer.
+  constexpr int kVsBytes = NWA * ATT_BLK * ATT_VSTRIDE * 2;
+  constexpr int kOBytes = NWA * 8 * ATT_HD * 4;
   __shared__ __attribute__((aligned(16))) char smem[kVsBytes > kOBytes ? kVsBytes : kOBytes];
-  __shared__ float ml_lds[ATT_WAVES][ATT_MAXG][2];
-  __shared__ int last_flag;
+  __shared__ float ml_lds[NWA][ATT_MAXG][2];
   half_t (*vs_lds)[ATT_BLK * ATT_VSTRIDE] = (half_t (*)[ATT_BLK * ATT_VSTRIDE])smem;
-  float (*o_lds)[ATT_MAXG][ATT_HD] = (float (*)[ATT_MAXG][ATT_HD])smem;
+  float (*o_lds)[8][ATT_HD] = (float (*)[8][ATT_HD])smem;   // heads < 8 are combined
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int q16 = lane >> 4;     // lane group 0..3
   const int c16 = lane & 15;     // column within MFMA tile
   const int S = a.S;
-  const int sg = blockIdx.x % S;
+  const int sp = blockIdx.x % S;
   const int g = (blockIdx.x / S) % a.nkv;
   const int t = blockIdx.x / (S * a.nkv);
   const int G = a.G;
@@ -75,11 +73,11 @@ __global__ __launch_bounds__(256, 2) void decode_attn_kernel(AttnArgs a) {
   int64_t L = slot_ok ? a.kv_len[a.kv_by_slot ? slot : t] + a.kv_add : 0;
   L = clamp64(L, 0, a.max_len);
 
-  // Token range of this wave.
-  const int nsplit = S * ATT_WAVES;
+  // Token range of this wave: the context is cut into S*NWA 32-aligned chunks.
+  const int nsplit = S * NWA;
   int chunk = (int)((L + nsplit - 1) / nsplit);
   chunk = (chunk + ATT_BLK - 1) / ATT_BLK * ATT_BLK;
-  const int wsplit = sg * ATT_WAVES + wave;
+  const int wsplit = sp * NWA + wave;
   const int beg = (int)min((int64_t)wsplit * chunk, L);
   const int end = (int)min((int64_t)(wsplit + 1) * chunk, L);
 
@@ -206,89 +204,80 @@ __global__ __launch_bounds__(256, 2) void decode_attn_kernel(AttnArgs a) {
   l_run += __shfl_xor(l_run, 32, 64);
   __syncthreads();   // every wave is done with its V tile before o_lds reuses the space
 
-  // Per-wave partials to LDS (heads < G only).
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int h = 4 * q16 + i;
-    if (h < G) {
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) o_lds[wave][h][dt * 16 + c16] = o_acc[dt][i];
-    }
-  }
+  // Merge the waves' softmax states: heads processed in groups of 8 (G <= 16).
+  const int nh = a.nkv * G;
   if (lane < G) {
     ml_lds[wave][lane][0] = m_run;
     ml_lds[wave][lane][1] = l_run;
   }
-  __syncthreads();
+  for (int hb = 0; hb < G; hb += 8) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int h = 4 * q16 + i - hb;
+      if (h >= 0 && h < 8 && h + hb < G) {
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) o_lds[wave][h][dt * 16 + c16] = o_acc[dt][i];
+      }
+    }
+    __syncthreads();
+    const int hn = min(8, G - hb);
+    for (int idx = threadIdx.x; idx < hn * ATT_HD; idx += NWA * 64) {
+      const int h = idx / ATT_HD;
+      const int d = idx % ATT_HD;
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < NWA; ++w) M = fmaxf(M, ml_lds[w][hb + h][0]);
+      float lsum = 0.f, o = 0.f;
+      if (M != -INFINITY) {
+#pragma unroll
+        for (int w = 0; w < NWA; ++w) {
+          const float f = exp2f(ml_lds[w][hb + h][0] - M);
+          lsum += f * ml_lds[w][hb + h][1];
+          o += f * o_lds[w][h][d];
+        }
+      }
+      if (S == 1) {
+        const float r = lsum > 0.f ? o / lsum : 0.f;
+        a.out[((int64_t)t * nh + g * G + hb + h) * ATT_HD + d] = (half_t)r;
+      } else {
+        float* pp = a.part + ((((int64_t)t * a.nkv + g) * S + sp) * G + hb + h) * (ATT_HD + 2);
+        pp[d] = o;
+        if (d == 0) {
+          pp[ATT_HD] = M;
+          pp[ATT_HD + 1] = lsum;
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
 
-  // Combine the 4 waves: thread -> (head, dim) pairs.
-  const int nout = G * ATT_HD;
-  const int T = a.T;
-  const int nh = a.nkv * G;
-  float* wsg = nullptr;
-  if (S > 1) wsg = a.ws + (((int64_t)t * a.nkv + g) * S + sg) * (int64_t)G * (ATT_HD + 2);
-  for (int idx = threadIdx.x; idx < nout; idx += 256) {
+// Merge of the S partial softmax states of each (token, kv head) written by
+// decode_attn_kernel (a separate launch: ordering comes from the kernel boundary).
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ part,
+                                                           half_t* __restrict__ out, int nkv,
+                                                           int G, int S) {
+  const int g = blockIdx.x % nkv;
+  const int t = blockIdx.x / nkv;
+  const int nh = nkv * G;
+  const float* base = part + ((int64_t)t * nkv + g) * S * G * (ATT_HD + 2);
+  for (int idx = threadIdx.x; idx < G * ATT_HD; idx += 256) {
     const int h = idx / ATT_HD;
     const int d = idx % ATT_HD;
     float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < ATT_WAVES; ++w) M = fmaxf(M, ml_lds[w][h][0]);
-    float lsum = 0.f, o = 0.f;
-    if (M != -INFINITY) {
-#pragma unroll
-      for (int w = 0; w < ATT_WAVES; ++w) {
-        const float f = exp2f(ml_lds[w][h][0] - M);
-        lsum += f * ml_lds[w][h][1];
-        o += f * o_lds[w][h][d];
-      }
-    }
-    if (S == 1) {
-      const float r = lsum > 0.f ? o / lsum : 0.f;
-      a.out[((int64_t)t * nh + g * G + h) * ATT_HD + d] = (half_t)r;
-    } else {
-      wsg[h * (ATT_HD + 2) + d] = o;
-      if (d == 0) {
-        wsg[h * (ATT_HD + 2) + ATT_HD] = M;
-        wsg[h * (ATT_HD + 2) + ATT_HD + 1] = lsum;
-      }
-    }
-  }
-  if (S == 1) return;
-
-  // Cross-workgroup combine: the last workgroup of (t, g) to arrive reduces.
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int* ctr = a.counters + (int64_t)t * a.nkv + g;
-    const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    const int last = prev == S - 1;
-    if (last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    last_flag = last;
-  }
-  __syncthreads();
-  if (!last_flag) return;
-  __threadfence();
-  const float* wsb = a.ws + ((int64_t)t * a.nkv + g) * S * (int64_t)G * (ATT_HD + 2);
-  for (int idx = threadIdx.x; idx < nout; idx += 256) {
-    const int h = idx / ATT_HD;
-    const int d = idx % ATT_HD;
-    float M = -INFINITY;
-    for (int s = 0; s < S; ++s)
-      M = fmaxf(M, __builtin_nontemporal_load(wsb + ((int64_t)s * G + h) * (ATT_HD + 2) + ATT_HD));
+    for (int s = 0; s < S; ++s) M = fmaxf(M, base[((int64_t)s * G + h) * (ATT_HD + 2) + ATT_HD]);
     float lsum = 0.f, o = 0.f;
     if (M != -INFINITY) {
       for (int s = 0; s < S; ++s) {
-        const float* p = wsb + ((int64_t)s * G + h) * (ATT_HD + 2);
-        const float ms = __builtin_nontemporal_load(p + ATT_HD);
-        const float f = exp2f(ms - M);
-        lsum += f * __builtin_nontemporal_load(p + ATT_HD + 1);
-        o += f * __builtin_nontemporal_load(p + d);
+        const float* pp = base + ((int64_t)s * G + h) * (ATT_HD + 2);
+        const float f = exp2f(pp[ATT_HD] - M);
+        lsum += f * pp[ATT_HD + 1];
+        o += f * pp[d];
       }
     }
     const float r = lsum > 0.f ? o / lsum : 0.f;
-    a.out[((int64_t)t * nh + g * G + h) * ATT_HD + d] = (half_t)r;
+    out[((int64_t)t * nh + g * G + h) * ATT_HD + d] = (half_t)r;
   }
-  (void)T;
 }
 
 // Decode / append attention over the pool.
@@ -297,24 +286,25 @@ __global__ __launch_bounds__(256, 2) void decode_attn_kernel(AttnArgs a) {
 //   slots      int64 [T] pool rows (NULL = row t)
 //   kv_len     int64; keys visible to token t = kv_len[kv_by_slot ? slot : t] + kv_add
 //   out        fp16 [T, n_heads, 128]
-//   splits     split groups per (token, kv head); > 1 needs workspace and counters:
-//   workspace  fp32, >= T * n_kv * splits * G * 130 floats
-//   counters   int32 [T * n_kv], zero before first use (the kernel leaves them zero)
+//   waves      waves per workgroup: 4, 8 or 16
+//   splits     workgroups per (token, kv head); > 1 writes partial states to
+//              workspace (fp32, >= T * n_kv * splits * G * 130) merged by a second launch
 extern "C" int omni_decode_attention(const void* q, int q_stride, const void* k_cache,
                                      const void* v_cache, int pool_rows, int max_len,
                                      const int64_t* slots, const int64_t* kv_len, int kv_by_slot,
                                      int kv_add, void* out, int T, int n_heads, int n_kv_heads,
-                                     int head_dim, float scale, int splits, float* workspace,
-                                     int* counters, void* stream) {
+                                     int head_dim, float scale, int waves, int splits,
+                                     float* workspace, void* stream) {
   if (T < 0 || n_heads <= 0 || n_kv_heads <= 0 || pool_rows <= 0 || max_len <= 0) return OMNI_EINVAL;
   if (head_dim != ATT_HD || n_heads % n_kv_heads) return OMNI_EUNSUPPORTED;
   const int G = n_heads / n_kv_heads;
   if (G > ATT_MAXG) return OMNI_EUNSUPPORTED;
-  if (splits < 1 || splits > 1024) return OMNI_EINVAL;
+  if (waves != 4 && waves != 8 && waves != 16) return OMNI_EINVAL;
+  if (splits < 1 || splits > 64) return OMNI_EINVAL;
   if (q_stride < n_heads * ATT_HD || (q_stride & 7)) return OMNI_EINVAL;
   if (T == 0) return OMNI_OK;
   if (!q || !k_cache || !v_cache || !kv_len || !out) return OMNI_EINVAL;
-  if (splits > 1 && (!workspace || !counters)) return OMNI_EINVAL;
+  if (splits > 1 && !workspace) return OMNI_EINVAL;
   AttnArgs a;
   a.q = (const half_t*)q;
   a.q_stride = q_stride;
@@ -329,16 +319,24 @@ extern "C" int omni_decode_attention(const void* q, int q_stride, const void* k_
   a.kv_by_slot = kv_by_slot;
   a.kv_add = kv_add;
   a.out = (half_t*)out;
-  a.ws = workspace;
-  a.counters = counters;
+  a.part = workspace;
+  a.S = splits;
   a.scale_log2 = scale * 1.4426950408889634f;
   a.T = T;
-  a.S = splits;
-  const int64_t nblocks = (int64_t)splits * n_kv_heads * T;
+  const int64_t nblocks = (int64_t)n_kv_heads * T * splits;
   if (nblocks > 0x7fffffff) return OMNI_EUNSUPPORTED;
-  hipLaunchKernelGGL(decode_attn_kernel, dim3((unsigned)nblocks), dim3(256), 0,
-                     (hipStream_t)stream, a);
+  hipStream_t st = (hipStream_t)stream;
+  switch (waves) {
+    case 4: hipLaunchKernelGGL(decode_attn_kernel<4>, dim3((unsigned)nblocks), dim3(256), 0, st, a); break;
+    case 8: hipLaunchKernelGGL(decode_attn_kernel<8>, dim3((unsigned)nblocks), dim3(512), 0, st, a); break;
+    default: hipLaunchKernelGGL(decode_attn_kernel<16>, dim3((unsigned)nblocks), dim3(1024), 0, st, a); break;
+  }
   OMNI_CHECK_LAUNCH();
+  if (splits > 1) {
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(n_kv_heads * T), dim3(256), 0, st, workspace,
+                       (half_t*)out, n_kv_heads, G, splits);
+    OMNI_CHECK_LAUNCH();
+  }
   return OMNI_OK;
 }
 

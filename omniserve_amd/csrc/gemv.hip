@@ -13,20 +13,29 @@
 //         bit 2e (e even) or 16+2(e-1) (e odd); scales sp fp16 [N/16][K/128][16].
 //   fp16  wp     [N/16][K/32][64 lanes][8]: lane l holds column 16*nt + l%16,
 //         k = 32*ks + 8*(l/16) + e.
-// In both, one 16-byte load per lane is exactly one MFMA 16x16x32 B operand set
-// (four of them for int4), a wavefront reads 1 KB contiguous per load, and the
-// int4 dequant is the magic-exponent trick on packed fp16 (no LUT, no shuffles).
+// One 16-byte load per lane is one MFMA 16x16x32 B operand set (four of them for
+// int4); a wavefront reads 1 KB contiguous per load; the int4 dequant is the
+// magic-exponent trick on packed fp16.
 //
-// Work split: a workgroup of NW waves owns NW*CPW column tiles of 16 and one
-// K-split; it stages x[:, k-split] in LDS once, each wave streams its tiles'
-// weights (prefetch depth PF k-groups) and runs MB*CPW MFMAs per 32-k step.
-// Split-K partials go to an fp32 workspace; the last workgroup of a column
-// group (device-scope counter it resets itself) sums them in split order, so
-// results are deterministic and the kernel is graph-replayable.
+// Work split (no cross-workgroup synchronisation anywhere: on this multi-XCD part a
+// device-scope fence costs an L2 write-back/invalidate per workgroup, far more than
+// the work it would order):
+//   * a workgroup owns CW*CPW column tiles of 16 and one K range (all of K, or one of
+//     KS slices); it has CW*KW waves: wave (cw, kw) streams its CPW tiles over the
+//     kw-th part of the range, issuing its first weight loads before x is staged;
+//   * x[:, range] is staged once per workgroup in LDS (loads batched, then stored);
+//   * the KW partial accumulators are summed in LDS (fixed order) and the epilogue
+//     runs once:
+//       STORE    fp16 out (+ bias)                                  KS == 1
+//       SILU     tiles (2p, 2p+1) = (gate, up) -> fp16 silu(g)*u    KS == 1
+//       PARTIAL  fp32 [KS][M][N] partial sums; the consumer kernel adds them in
+//                slice order (deterministic)
+//       ARGMAX   per-workgroup (max fp16 logit, lowest index) per row -> candidate
+//                arrays reduced by omni_argmax_finalize.
 #include "common.h"
 
 enum { W_INT4 = 0, W_FP16 = 1 };
-enum { EPI_STORE = 0, EPI_SILU = 1, EPI_ARGMAX = 2 };
+enum { EPI_STORE = 0, EPI_SILU = 1, EPI_PARTIAL = 2, EPI_ARGMAX = 3 };
 
 struct GemvArgs {
   const half_t* x;
@@ -37,13 +46,13 @@ struct GemvArgs {
   int bias_after_round;  // 1: fp16(fp16(acc) + b) (GPTQ path); 0: fp16(acc + b)
   half_t* out;
   int ldo;
+  float* partial;        // EPI_PARTIAL: [KS][M][N]
+  float* cand_val;       // EPI_ARGMAX: [gridDim][M]
+  int* cand_idx;
   int M, N, K;
-  int KS, KC;            // k splits, k per split (multiple of 128)
-  float* ws;             // [KS][M][N] fp32 partials (KS > 1)
-  int* counters;         // [column groups] (KS > 1) or [1] (argmax)
-  float* cand_val;       // [grid][M] (argmax)
-  int* cand_idx;         // [grid][M]
-  int64_t* ids_out;      // [M]
+  int KS;                // K slices across workgroups
+  int KC;                // K per slice (multiple of 128)
+  int xl;                // 1: x slice staged in LDS; 0: A fragments read from global
 };
 
 template <int WF>
@@ -85,43 +94,79 @@ __device__ __forceinline__ half_t finish_store(float v, const GemvArgs& a, int n
   return (half_t)v;
 }
 
-template <int WF, int MB, int EPI, int CPW, int NW, int PF>
-__global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
+// Dynamic LDS: the x tile [MB*16 rows][KC + 8 halfs], reused for the KW reduction.
+template <int WF, int MB, int EPI, int CPW, int CW, int KW, int PF>
+__global__ __launch_bounds__(CW * KW * 64) void gemv_kernel(GemvArgs a) {
 #pragma clang fp contract(off)
-  extern __shared__ __attribute__((aligned(16))) half_t xs[];
-  __shared__ float red_v[NW][MB * 16];
-  __shared__ int red_i[NW][MB * 16];
-  __shared__ int last_flag;
+  static_assert(EPI != EPI_ARGMAX || KW == 1, "argmax epilogue uses every wave of the workgroup");
+  constexpr int NW = CW * KW;
+  constexpr int NT_WG = CW * CPW;     // column tiles per workgroup
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  half_t* xs = (half_t*)smem;
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  const int cw = wave % CW;
+  const int kw = wave / CW;
   const int q16 = lane >> 4;
   const int c16 = lane & 15;
   const int NT = a.N >> 4;
-  constexpr int TPW = NW * CPW;  // column tiles per workgroup
-  const int ngroups = (NT + TPW - 1) / TPW;
+  const int ngroups = (NT + NT_WG - 1) / NT_WG;
   const int ng = blockIdx.x % ngroups;
   const int ksi = blockIdx.x / ngroups;
   const int k0 = ksi * a.KC;
-  const int kc = min(a.KC, a.K - k0);
+  const int kc = min(a.KC, a.K - k0);          // multiple of 128
   const int xstride = a.KC + 8;
+  const int ngk = kc >> 7;                      // k-groups in this slice
+  const int per = (ngk + KW - 1) / KW;          // k-groups per wave
+  const int g_beg = min(kw * per, ngk);
+  const int g_end = min(g_beg + per, ngk);
+  const int kg0 = (k0 >> 7) + g_beg;
+  const int myg = g_end - g_beg;
 
-  // Stage x[0:M, k0:k0+kc] (rows >= M zero) into LDS.
-  {
+  const int tile0 = ng * NT_WG + cw * CPW;
+  const bool active = tile0 < NT;
+
+  // 1. first weight loads in flight before x is staged
+  WFrag<WF> buf[PF][CPW];
+  if (active) {
+#pragma unroll
+    for (int p = 0; p < PF; ++p)
+      if (p < myg)
+#pragma unroll
+        for (int c = 0; c < CPW; ++c) load_frag<WF>(buf[p][c], a, tile0 + c, kg0 + p, lane);
+  }
+
+  // 2. stage x[0:M, k0:k0+kc] in LDS (rows >= M zero), 8 loads in flight per thread
+  if (a.xl) {
     const int cpr = kc >> 3;
     const int total = MB * 16 * cpr;
-    for (int i = threadIdx.x; i < total; i += NW * 64) {
-      const int r = i / cpr;
-      const int c = i - r * cpr;
-      half8_t v = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
-      if (r < a.M) v = *(const half8_t*)(a.x + (int64_t)r * a.ldx + k0 + c * 8);
-      *(half8_t*)(xs + r * xstride + c * 8) = v;
+    for (int base = threadIdx.x; base < total; base += 8 * NW * 64) {
+      half8_t v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int i = base + u * NW * 64;
+        v[u] = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
+        if (i < total) {
+          const int r = i / cpr;
+          const int c = i - r * cpr;
+          if (r < a.M) v[u] = *(const half8_t*)(a.x + (int64_t)r * a.ldx + k0 + c * 8);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int i = base + u * NW * 64;
+        if (i < total) {
+          const int r = i / cpr;
+          const int c = i - r * cpr;
+          *(half8_t*)(xs + r * xstride + c * 8) = v[u];
+        }
+      }
     }
   }
   __syncthreads();
 
-  const int tile0 = ng * TPW + wave * CPW;
-  const bool active = tile0 < NT;
+  // 3. stream weights, MFMA against x from LDS
   f32x4 acc[CPW][MB];
 #pragma unroll
   for (int c = 0; c < CPW; ++c)
@@ -129,32 +174,31 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
     for (int mb = 0; mb < MB; ++mb) acc[c][mb] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
   if (active) {
-    const int ngk = kc >> 7;
-    const int kg0 = k0 >> 7;
-    WFrag<WF> buf[PF][CPW];
-#pragma unroll
-    for (int p = 0; p < PF; ++p)
-      if (p < ngk)
-#pragma unroll
-        for (int c = 0; c < CPW; ++c) load_frag<WF>(buf[p][c], a, tile0 + c, kg0 + p, lane);
-
-    for (int base = 0; base < ngk; base += PF) {
+    for (int base = 0; base < myg; base += PF) {
 #pragma unroll
       for (int p = 0; p < PF; ++p) {
         const int i = base + p;
-        if (i < ngk) {
+        if (i < myg) {
           WFrag<WF> cur[CPW];
 #pragma unroll
           for (int c = 0; c < CPW; ++c) cur[c] = buf[p][c];
-          if (i + PF < ngk)
+          if (i + PF < myg)
 #pragma unroll
             for (int c = 0; c < CPW; ++c) load_frag<WF>(buf[p][c], a, tile0 + c, kg0 + i + PF, lane);
+          const int kl = (g_beg + i) * 128;     // k offset inside the staged slice
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             half8_t af[MB];
 #pragma unroll
-            for (int mb = 0; mb < MB; ++mb)
-              af[mb] = *(const half8_t*)(xs + (16 * mb + c16) * xstride + i * 128 + 32 * j + 8 * q16);
+            for (int mb = 0; mb < MB; ++mb) {
+              if (a.xl) {
+                af[mb] = *(const half8_t*)(xs + (16 * mb + c16) * xstride + kl + 32 * j + 8 * q16);
+              } else {
+                const int m = 16 * mb + c16;
+                af[mb] = m < a.M ? *(const half8_t*)(a.x + (int64_t)m * a.ldx + k0 + kl + 32 * j + 8 * q16)
+                                 : (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
+              }
+            }
 #pragma unroll
             for (int c = 0; c < CPW; ++c) {
               half8_t bf;
@@ -173,10 +217,36 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
     }
   }
 
-  // ------------------------------------------------------------ epilogues
+  // 4. sum the KW partial accumulators in LDS, in kw order
+  if constexpr (KW > 1) {
+    __syncthreads();                              // the x tile is no longer read
+    float* red = (float*)smem;                    // [KW-1][CW][CPW][MB][4][64]
+    if (kw > 0) {
+#pragma unroll
+      for (int c = 0; c < CPW; ++c)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            red[((((kw - 1) * CW + cw) * CPW + c) * MB + mb) * 256 + i * 64 + lane] = acc[c][mb][i];
+    }
+    __syncthreads();
+    if (kw > 0) return;                           // no workgroup barrier follows
+#pragma unroll
+    for (int k2 = 1; k2 < KW; ++k2)
+#pragma unroll
+      for (int c = 0; c < CPW; ++c)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            acc[c][mb][i] += red[((((k2 - 1) * CW + cw) * CPW + c) * MB + mb) * 256 + i * 64 + lane];
+  }
+  // Lane holds rows 16*mb + 4*q16 + i, column (tile0 + c)*16 + c16.
+
   if constexpr (EPI == EPI_ARGMAX) {
-    // logits = fp16(acc); greedy argmax on the fp16 values, lowest index wins ties
-    // (torch.argmax semantics).  Optional logits store.
+    __shared__ float red_v[CW][MB * 16];
+    __shared__ int red_i[CW][MB * 16];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -201,8 +271,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
           if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
         }
         if (c16 == 0) {
-          red_v[wave][m] = bv;
-          red_i[wave][m] = bi;
+          red_v[cw][m] = bv;
+          red_i[cw][m] = bi;
         }
       }
     __syncthreads();
@@ -211,7 +281,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
       float bv = red_v[0][m];
       int bi = red_i[0][m];
 #pragma unroll
-      for (int w = 1; w < NW; ++w) {
+      for (int w = 1; w < CW; ++w) {
         const float ov = red_v[w][m];
         const int oi = red_i[w][m];
         if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
@@ -219,126 +289,47 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
       a.cand_val[(int64_t)blockIdx.x * a.M + m] = bv;
       a.cand_idx[(int64_t)blockIdx.x * a.M + m] = bi;
     }
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      const int prev = __hip_atomic_fetch_add(a.counters, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-      const int last = prev == (int)gridDim.x - 1;
-      if (last) __hip_atomic_store(a.counters, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      last_flag = last;
-    }
-    __syncthreads();
-    if (!last_flag) return;
-    __threadfence();
-    // Final reduction over all workgroups: wave w handles rows w, w+NW, ...
-    for (int m = wave; m < a.M; m += NW) {
-      float bv = -INFINITY;
-      int bi = 0x7fffffff;
-      for (int b = lane; b < (int)gridDim.x; b += 64) {
-        const float ov = __builtin_nontemporal_load(a.cand_val + (int64_t)b * a.M + m);
-        const int oi = __builtin_nontemporal_load(a.cand_idx + (int64_t)b * a.M + m);
-        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-      }
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const float ov = __shfl_xor(bv, o, 64);
-        const int oi = __shfl_xor(bi, o, 64);
-        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-      }
-      if (lane == 0) a.ids_out[m] = bi;
-    }
     return;
   } else {
-    if (a.KS == 1) {
-      if (!active) return;
+    if (!active) return;
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
+    for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int m = 16 * mb + 4 * q16 + i;
-          if (m >= a.M) continue;
-          if constexpr (EPI == EPI_SILU) {
-            // tiles (2p, 2p+1) = (gate, up) columns 16p + c16 of the intermediate.
-            const int j = (tile0 >> 1) * 16 + c16;
-            const float g = (float)(half_t)acc[0][mb][i];
-            const float u = (float)(half_t)acc[1][mb][i];
-            a.out[(int64_t)m * a.ldo + j] = (half_t)(silu_ref(g) * u);
-          } else {
-#pragma unroll
-            for (int c = 0; c < CPW; ++c) {
-              const int n = (tile0 + c) * 16 + c16;
-              a.out[(int64_t)m * a.ldo + n] = finish_store(acc[c][mb][i], a, n);
-            }
-          }
-        }
-      return;
-    }
-    // Split-K: fp32 partials, then the last workgroup of this column group reduces.
-    if (active) {
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int m = 16 * mb + 4 * q16 + i;
-          if (m >= a.M) continue;
+      for (int i = 0; i < 4; ++i) {
+        const int m = 16 * mb + 4 * q16 + i;
+        if (m >= a.M) continue;
+        if constexpr (EPI == EPI_SILU) {
+          // tiles (2p, 2p+1) = (gate, up) columns 16p + c16 of the intermediate.
+          const int j = (tile0 >> 1) * 16 + c16;
+          const float g = (float)(half_t)acc[0][mb][i];
+          const float u = (float)(half_t)acc[1][mb][i];
+          a.out[(int64_t)m * a.ldo + j] = (half_t)(silu_ref(g) * u);
+        } else if constexpr (EPI == EPI_PARTIAL) {
 #pragma unroll
           for (int c = 0; c < CPW; ++c) {
             const int n = (tile0 + c) * 16 + c16;
-            a.ws[((int64_t)ksi * a.M + m) * a.N + n] = acc[c][mb][i];
+            a.partial[((int64_t)ksi * a.M + m) * a.N + n] = acc[c][mb][i];
+          }
+        } else {
+#pragma unroll
+          for (int c = 0; c < CPW; ++c) {
+            const int n = (tile0 + c) * 16 + c16;
+            a.out[(int64_t)m * a.ldo + n] = finish_store(acc[c][mb][i], a, n);
           }
         }
-    }
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      int* ctr = a.counters + ng;
-      const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-      const int last = prev == a.KS - 1;
-      if (last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      last_flag = last;
-    }
-    __syncthreads();
-    if (!last_flag) return;
-    __threadfence();
-    const int ncol_tiles = min(TPW, NT - ng * TPW);
-    if constexpr (EPI == EPI_SILU) {
-      const int npairs = ncol_tiles >> 1;
-      const int total = a.M * npairs * 16;
-      for (int idx = threadIdx.x; idx < total; idx += NW * 64) {
-        const int m = idx / (npairs * 16);
-        const int r = idx - m * npairs * 16;
-        const int pr = (ng * TPW >> 1) + (r >> 4);
-        const int cc = r & 15;
-        const int ng_ = pr * 32 + cc;       // gate column in packed (interleaved) order
-        const int nu_ = ng_ + 16;
-        float g = 0.f, u = 0.f;
-        for (int s = 0; s < a.KS; ++s) {
-          g += __builtin_nontemporal_load(a.ws + ((int64_t)s * a.M + m) * a.N + ng_);
-          u += __builtin_nontemporal_load(a.ws + ((int64_t)s * a.M + m) * a.N + nu_);
-        }
-        g = (float)(half_t)g;
-        u = (float)(half_t)u;
-        a.out[(int64_t)m * a.ldo + pr * 16 + cc] = (half_t)(silu_ref(g) * u);
       }
-    } else {
-      const int ncols = ncol_tiles * 16;
-      const int total = a.M * ncols;
-      for (int idx = threadIdx.x; idx < total; idx += NW * 64) {
-        const int m = idx / ncols;
-        const int n = ng * TPW * 16 + (idx - m * ncols);
-        float v = 0.f;
-        for (int s = 0; s < a.KS; ++s) v += __builtin_nontemporal_load(a.ws + ((int64_t)s * a.M + m) * a.N + n);
-        a.out[(int64_t)m * a.ldo + n] = finish_store(v, a, n);
-      }
-    }
   }
 }
 
 // ---------------------------------------------------------------------------
-// Host-side dispatch.
+// Host-side dispatch.  Presets (CPW, CW, KW):
+//   0: (1, 8, 2)  16 waves, 8 tiles = 128 columns per workgroup, K halved in-group
+//   1: (1, 8, 1)   8 waves, 8 tiles
+//   2: (1, 4, 4)  16 waves, 4 tiles, K in quarters
+//   3: (2, 4, 2)   8 waves, 8 tiles
+// SiLU (gate/up pairs, CPW = 2): 0: (2, 4, 4), 1: (2, 8, 1), 2: (2, 4, 2), 3: (2, 2, 4).
+// Argmax: (2, 8, 1) (16 tiles).
 // ---------------------------------------------------------------------------
-// Largest dynamic LDS a workgroup may request on the current device, leaving room
-// for the kernel's static arrays.
 static size_t max_dynamic_lds() {
   static int cached = -1;
   if (cached < 0) {
@@ -351,75 +342,82 @@ static size_t max_dynamic_lds() {
   return (size_t)cached > 4096 ? (size_t)cached - 4096 : 0;
 }
 
-template <int WF, int MB, int EPI, int CPW, int NW, int PF>
-static int launch_gemv(const GemvArgs& a, int grid, hipStream_t st) {
-  auto kern = gemv_kernel<WF, MB, EPI, CPW, NW, PF>;
-  const size_t lds = (size_t)MB * 16 * (a.KC + 8) * sizeof(half_t);
+template <int WF, int MB, int EPI, int CPW, int CW, int KW, int PF>
+static int launch_gemv(GemvArgs a, hipStream_t st) {
+  auto kern = gemv_kernel<WF, MB, EPI, CPW, CW, KW, PF>;
   const size_t lim = max_dynamic_lds();
+  const size_t xbytes = (size_t)MB * 16 * (a.KC + 8) * sizeof(half_t);
+  const size_t rbytes = (size_t)(KW > 1 ? KW - 1 : 0) * CW * CPW * MB * 256 * sizeof(float);
+  a.xl = xbytes <= lim;                         // else A fragments come from global/L2
+  const size_t lds = a.xl ? (xbytes > rbytes ? xbytes : rbytes) : rbytes;
   if (lds > lim) return OMNI_EUNSUPPORTED;
   static bool attr_set = false;
   if (!attr_set) {
     hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lim);
     attr_set = true;
   }
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(NW * 64), lds, st, a);
+  const int NT = a.N >> 4;
+  const int ngroups = (NT + CW * CPW - 1) / (CW * CPW);
+  const int grid = ngroups * a.KS;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(CW * KW * 64), lds, st, a);
   OMNI_CHECK_LAUNCH();
   return OMNI_OK;
 }
 
-template <int WF, int EPI, int CPW, int NW, int PF>
-static int dispatch_mb(const GemvArgs& a, int grid, hipStream_t st) {
-  const int mb = (a.M + 15) / 16;
-  switch (mb) {
-    case 1: return launch_gemv<WF, 1, EPI, CPW, NW, PF>(a, grid, st);
-    case 2: return launch_gemv<WF, 2, EPI, CPW, NW, PF>(a, grid, st);
-    case 3: return launch_gemv<WF, 3, EPI, CPW, NW, PF>(a, grid, st);
-    case 4: return launch_gemv<WF, 4, EPI, CPW, NW, PF>(a, grid, st);
+template <int WF, int EPI, int CPW, int CW, int KW, int PF>
+static int dispatch_mb(const GemvArgs& a, hipStream_t st) {
+  switch ((a.M + 15) / 16) {
+    case 1: return launch_gemv<WF, 1, EPI, CPW, CW, KW, PF>(a, st);
+    case 2: return launch_gemv<WF, 2, EPI, CPW, CW, KW, PF>(a, st);
+    case 3: return launch_gemv<WF, 3, EPI, CPW, CW, KW, PF>(a, st);
+    case 4: return launch_gemv<WF, 4, EPI, CPW, CW, KW, PF>(a, st);
     default: return OMNI_EUNSUPPORTED;
   }
 }
 
-// Tuning: (CPW, NW) per weight format / epilogue.
 template <int WF, int EPI>
-static int dispatch(const GemvArgs& a, int cpw, hipStream_t st) {
-  const int NT = a.N >> 4;
+static int dispatch_preset(const GemvArgs& a, int preset, hipStream_t st) {
+  constexpr int PF = WF == W_INT4 ? 4 : 2;
   if constexpr (EPI == EPI_SILU) {
-    constexpr int NW = 4;
-    const int ngroups = (NT + 2 * NW - 1) / (2 * NW);
-    const int grid = ngroups * a.KS;
-    if constexpr (WF == W_INT4) return dispatch_mb<WF, EPI, 2, NW, 4>(a, grid, st);
-    else return dispatch_mb<WF, EPI, 2, NW, 2>(a, grid, st);
-  } else {
-    constexpr int NW = 4;
-    if (cpw == 1) {
-      const int grid = ((NT + NW - 1) / NW) * a.KS;
-      if constexpr (WF == W_INT4) return dispatch_mb<WF, EPI, 1, NW, 4>(a, grid, st);
-      else return dispatch_mb<WF, EPI, 1, NW, 2>(a, grid, st);
+    switch (preset) {
+      case 1: return dispatch_mb<WF, EPI, 2, 8, 1, PF>(a, st);
+      case 2: return dispatch_mb<WF, EPI, 2, 4, 2, PF>(a, st);
+      case 3: return dispatch_mb<WF, EPI, 2, 2, 4, PF>(a, st);
+      default: return dispatch_mb<WF, EPI, 2, 4, 4, PF>(a, st);
     }
-    const int grid = ((NT + 2 * NW - 1) / (2 * NW)) * a.KS;
-    if constexpr (WF == W_INT4) return dispatch_mb<WF, EPI, 2, NW, 4>(a, grid, st);
-    else return dispatch_mb<WF, EPI, 2, NW, 2>(a, grid, st);
+  } else if constexpr (EPI == EPI_ARGMAX) {
+    return dispatch_mb<WF, EPI, 2, 8, 1, PF>(a, st);
+  } else {
+    switch (preset) {
+      case 0: return dispatch_mb<WF, EPI, 1, 8, 2, PF>(a, st);
+      case 1: return dispatch_mb<WF, EPI, 1, 8, 1, PF>(a, st);
+      case 2: return dispatch_mb<WF, EPI, 1, 4, 4, PF>(a, st);
+      case 3: return dispatch_mb<WF, EPI, 2, 4, 2, PF>(a, st);
+      default: return OMNI_EINVAL;
+    }
   }
 }
 
 static int gemv_common(int wf, const void* x, int ldx, const void* w, const void* scales,
-                       const void* bias, int bias_after_round, void* out, int ldo, int M, int N,
-                       int K, int epilogue, int ksplit, int cpw, float* ws, int* counters,
+                       const void* bias, int bias_after_round, void* out, int ldo,
+                       float* partial, int M, int N, int K, int epilogue, int ksplit, int preset,
                        void* stream) {
   if (M <= 0 || N <= 0 || K <= 0) return M == 0 ? OMNI_OK : OMNI_EINVAL;
   if (M > 64) return OMNI_EUNSUPPORTED;
   if ((N & 15) || (K & 127)) return OMNI_EUNSUPPORTED;
-  if (!x || !w || !out || (wf == W_INT4 && !scales)) return OMNI_EINVAL;
+  if (!x || !w || (wf == W_INT4 && !scales)) return OMNI_EINVAL;
   if (ldx < K || (ldx & 7)) return OMNI_EINVAL;
-  if (epilogue != EPI_STORE && epilogue != EPI_SILU) return OMNI_EINVAL;
-  if (epilogue == EPI_SILU && (N & 31)) return OMNI_EUNSUPPORTED;
-  if (ldo < (epilogue == EPI_SILU ? N / 2 : N)) return OMNI_EINVAL;
-  if (cpw != 1 && cpw != 2) return OMNI_EINVAL;
-  if (epilogue == EPI_SILU) cpw = 2;
-  if (cpw == 2 && (N & 31)) return OMNI_EUNSUPPORTED;  // tiles are taken in pairs
+  if (epilogue != EPI_STORE && epilogue != EPI_SILU && epilogue != EPI_PARTIAL) return OMNI_EINVAL;
+  if (epilogue == EPI_SILU && (N & 31)) return OMNI_EUNSUPPORTED;   // gate/up tile pairs
+  if (preset == 3 && (N & 31)) return OMNI_EUNSUPPORTED;            // 2 tiles per wave
   const int KG = K >> 7;
   if (ksplit < 1 || ksplit > KG) return OMNI_EINVAL;
-  if (ksplit > 1 && (!ws || !counters)) return OMNI_EINVAL;
+  if (epilogue == EPI_PARTIAL) {
+    if (!partial) return OMNI_EINVAL;
+  } else {
+    if (!out || ldo < (epilogue == EPI_SILU ? N / 2 : N)) return OMNI_EINVAL;
+    if (ksplit != 1) return OMNI_EINVAL;   // a split needs the PARTIAL epilogue
+  }
   GemvArgs a = {};
   a.x = (const half_t*)x;
   a.ldx = ldx;
@@ -429,51 +427,67 @@ static int gemv_common(int wf, const void* x, int ldx, const void* w, const void
   a.bias_after_round = bias_after_round;
   a.out = (half_t*)out;
   a.ldo = ldo;
+  a.partial = partial;
   a.M = M;
   a.N = N;
   a.K = K;
-  a.KS = ksplit;
   a.KC = ((KG + ksplit - 1) / ksplit) * 128;
-  a.KS = (K + a.KC - 1) / a.KC;  // effective splits after rounding the chunk
-  a.ws = ws;
-  a.counters = counters;
+  a.KS = (K + a.KC - 1) / a.KC;
   hipStream_t st = (hipStream_t)stream;
   if (wf == W_INT4) {
-    return epilogue == EPI_SILU ? dispatch<W_INT4, EPI_SILU>(a, cpw, st)
-                                : dispatch<W_INT4, EPI_STORE>(a, cpw, st);
+    switch (epilogue) {
+      case EPI_SILU: return dispatch_preset<W_INT4, EPI_SILU>(a, preset, st);
+      case EPI_PARTIAL: return dispatch_preset<W_INT4, EPI_PARTIAL>(a, preset, st);
+      default: return dispatch_preset<W_INT4, EPI_STORE>(a, preset, st);
+    }
   }
-  return epilogue == EPI_SILU ? dispatch<W_FP16, EPI_SILU>(a, cpw, st)
-                              : dispatch<W_FP16, EPI_STORE>(a, cpw, st);
+  switch (epilogue) {
+    case EPI_SILU: return dispatch_preset<W_FP16, EPI_SILU>(a, preset, st);
+    case EPI_PARTIAL: return dispatch_preset<W_FP16, EPI_PARTIAL>(a, preset, st);
+    default: return dispatch_preset<W_FP16, EPI_STORE>(a, preset, st);
+  }
+}
+
+// Number of K slices actually used for (K, ksplit) (slices are whole 128-groups).
+extern "C" int omni_gemm_slices(int K, int ksplit) {
+  const int KG = K >> 7;
+  if (KG <= 0 || ksplit < 1) return 0;
+  if (ksplit > KG) ksplit = KG;
+  const int kc = (KG + ksplit - 1) / ksplit;
+  return (KG + kc - 1) / kc;
 }
 
 extern "C" int omni_w4a16_gemm(const void* x, int ldx, const void* qweight_packed,
                                const void* scales_packed, const void* bias, int bias_after_round,
-                               void* out, int ldo, int M, int N, int K, int epilogue, int ksplit,
-                               int cols_per_wave, float* workspace, int* counters, void* stream) {
+                               void* out, int ldo, float* partial, int M, int N, int K,
+                               int epilogue, int ksplit, int preset, void* stream) {
   return gemv_common(W_INT4, x, ldx, qweight_packed, scales_packed, bias, bias_after_round, out,
-                     ldo, M, N, K, epilogue, ksplit, cols_per_wave, workspace, counters, stream);
+                     ldo, partial, M, N, K, epilogue, ksplit, preset, stream);
 }
 
 extern "C" int omni_f16_gemm(const void* x, int ldx, const void* weight_packed, const void* bias,
-                             void* out, int ldo, int M, int N, int K, int epilogue, int ksplit,
-                             int cols_per_wave, float* workspace, int* counters, void* stream) {
-  return gemv_common(W_FP16, x, ldx, weight_packed, nullptr, bias, 0, out, ldo, M, N, K, epilogue,
-                     ksplit, cols_per_wave, workspace, counters, stream);
+                             void* out, int ldo, float* partial, int M, int N, int K, int epilogue,
+                             int ksplit, int preset, void* stream) {
+  return gemv_common(W_FP16, x, ldx, weight_packed, nullptr, bias, 0, out, ldo, partial, M, N, K,
+                     epilogue, ksplit, preset, stream);
 }
 
-// Number of workgroups omni_lmhead_argmax launches (sizes its candidate buffers).
+// ---------------------------------------------------------------------------
+// lm_head + greedy argmax: the GEMM writes one (max, index) candidate per
+// workgroup and row; omni_argmax_finalize reduces them.
+// ---------------------------------------------------------------------------
 extern "C" int omni_lmhead_argmax_grid(int N) {
   const int NT = N >> 4;
-  return (NT + 7) / 8;
+  return (NT + 15) / 16;
 }
 
-extern "C" int omni_lmhead_argmax(const void* x, int ldx, const void* weight_packed, int M, int N,
-                                  int K, void* logits_out, int64_t* ids_out, float* cand_val,
-                                  int* cand_idx, int* counter, void* stream) {
+extern "C" int omni_lmhead_candidates(const void* x, int ldx, const void* weight_packed, int M,
+                                      int N, int K, void* logits_out, float* cand_val,
+                                      int* cand_idx, void* stream) {
   if (M <= 0 || N <= 0 || K <= 0) return M == 0 ? OMNI_OK : OMNI_EINVAL;
   if (M > 64) return OMNI_EUNSUPPORTED;
   if ((N & 31) || (K & 127)) return OMNI_EUNSUPPORTED;
-  if (!x || !weight_packed || !ids_out || !cand_val || !cand_idx || !counter) return OMNI_EINVAL;
+  if (!x || !weight_packed || !cand_val || !cand_idx) return OMNI_EINVAL;
   if (ldx < K || (ldx & 7)) return OMNI_EINVAL;
   GemvArgs a = {};
   a.x = (const half_t*)x;
@@ -486,12 +500,56 @@ extern "C" int omni_lmhead_argmax(const void* x, int ldx, const void* weight_pac
   a.K = K;
   a.KS = 1;
   a.KC = K;
-  a.counters = counter;
   a.cand_val = cand_val;
   a.cand_idx = cand_idx;
-  a.ids_out = ids_out;
-  const int grid = omni_lmhead_argmax_grid(N);
-  return dispatch_mb<W_FP16, EPI_ARGMAX, 2, 4, 2>(a, grid, (hipStream_t)stream);
+  return dispatch_preset<W_FP16, EPI_ARGMAX>(a, 0, (hipStream_t)stream);
+}
+
+// ids_out[m] = index of the max candidate (lowest index on ties).  Decode-step
+// bookkeeping folded in: next_ids[m] = ids_out[m] and lengths[m] += 1 when given.
+__global__ __launch_bounds__(256) void argmax_finalize_kernel(
+    const float* __restrict__ cv, const int* __restrict__ ci, int nblk, int M,
+    int64_t* __restrict__ ids_out, int64_t* __restrict__ next_ids, int64_t* __restrict__ lengths) {
+  const int m = blockIdx.x;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int b = threadIdx.x; b < nblk; b += 256) {
+    const float ov = cv[(int64_t)b * M + m];
+    const int oi = ci[(int64_t)b * M + m];
+    if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+  }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float ov = __shfl_xor(bv, o, 64);
+    const int oi = __shfl_xor(bi, o, 64);
+    if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+  }
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  if ((threadIdx.x & 63) == 0) {
+    sv[threadIdx.x >> 6] = bv;
+    si[threadIdx.x >> 6] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 4; ++w)
+      if (sv[w] > bv || (sv[w] == bv && si[w] < bi)) { bv = sv[w]; bi = si[w]; }
+    ids_out[m] = bi;
+    if (next_ids) next_ids[m] = bi;
+    if (lengths) lengths[m] += 1;
+  }
+}
+
+extern "C" int omni_argmax_finalize(const float* cand_val, const int* cand_idx, int nblk, int M,
+                                    int64_t* ids_out, int64_t* next_ids, int64_t* lengths,
+                                    void* stream) {
+  if (M < 0 || nblk <= 0) return OMNI_EINVAL;
+  if (M == 0) return OMNI_OK;
+  if (!cand_val || !cand_idx || !ids_out) return OMNI_EINVAL;
+  hipLaunchKernelGGL(argmax_finalize_kernel, dim3(M), dim3(256), 0, (hipStream_t)stream, cand_val,
+                     cand_idx, nblk, M, ids_out, next_ids, lengths);
+  OMNI_CHECK_LAUNCH();
+  return OMNI_OK;
 }
 
 // ---------------------------------------------------------------------------

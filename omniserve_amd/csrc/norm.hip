@@ -24,12 +24,15 @@ __device__ __forceinline__ size_t packed16_offset(int64_t n, int k, int K) {
   return ((((size_t)nt * (K >> 5) + ks) * 64 + lane) << 3) + (k & 7);
 }
 
-template <bool HAS_RES, bool GATHER, bool FP8OUT>
+// PARTS: x is the fp32 split-K partial sums [nparts][rows][H] of the producing
+// linear, summed in slice order and rounded to fp16 (= that linear's fp16 output).
+template <bool HAS_RES, bool GATHER, bool FP8OUT, bool PARTS = false>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(
     const half_t* x, const half_t* residual, const int64_t* __restrict__ ids,
     const half_t* __restrict__ table, int table_packed, int64_t vocab,
     const half_t* __restrict__ w, half_t* y, uint8_t* __restrict__ y8,
-    float* __restrict__ scale_out, half_t* res_out, int rows, int H, float eps) {
+    float* __restrict__ scale_out, half_t* res_out, int rows, int H, float eps,
+    const float* __restrict__ parts = nullptr, int nparts = 0) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -52,6 +55,16 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(
       if (GATHER) {
         size_t off = table_packed ? packed16_offset(tok, c * 8, H) : (size_t)tok * H + c * 8;
         v = *(const half8_t*)(table + off);
+      } else if (PARTS) {
+        float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int p = 0; p < nparts; ++p) {
+          const float4* pp = (const float4*)(parts + ((size_t)p * rows + row) * H + c * 8);
+          const float4 lo = pp[0], hi = pp[1];
+          sum[0] += lo.x; sum[1] += lo.y; sum[2] += lo.z; sum[3] += lo.w;
+          sum[4] += hi.x; sum[5] += hi.y; sum[6] += hi.z; sum[7] += hi.w;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (half_t)sum[e];
       } else {
         v = *(const half8_t*)(x + (size_t)row * H + c * 8);
       }
@@ -111,6 +124,60 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(
   }
 }
 
+// Decode-size add+RMSNorm: one workgroup per row, one 8-element chunk per thread
+// (H/8 threads, rounded up to whole waves), so every load of the row - including all
+// split-K partials - is in flight at once.  x is fp16, or (PARTS) the fp32 partial sums
+// [nparts][rows][H] added in slice order and rounded to fp16.
+template <bool PARTS>
+__global__ __launch_bounds__(1024) void rownorm_kernel(const half_t* x, const float* __restrict__ parts,
+                                                       int nparts, const half_t* residual,
+                                                       const half_t* __restrict__ w, half_t* y,
+                                                       half_t* res_out, int rows, int H, float eps) {
+#pragma clang fp contract(off)
+  __shared__ float wsum[16];
+  const int row = blockIdx.x;
+  const int c = threadIdx.x;
+  const int nchunk = H >> 3;
+  const bool live = c < nchunk;
+  half8_t v = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
+  if (live) {
+    if (PARTS) {
+      float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int p = 0; p < nparts; ++p) {
+        const float4* pp = (const float4*)(parts + ((size_t)p * rows + row) * H + c * 8);
+        const float4 lo = pp[0], hi = pp[1];
+        sum[0] += lo.x; sum[1] += lo.y; sum[2] += lo.z; sum[3] += lo.w;
+        sum[4] += hi.x; sum[5] += hi.y; sum[6] += hi.z; sum[7] += hi.w;
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (half_t)sum[e];
+    } else {
+      v = *(const half8_t*)(x + (size_t)row * H + c * 8);
+    }
+    const half8_t rv = *(const half8_t*)(residual + (size_t)row * H + c * 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (half_t)((float)v[e] + (float)rv[e]);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += (float)v[e] * (float)v[e];
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+  const int nw = (blockDim.x + 63) >> 6;
+  for (int i = 0; i < nw; ++i) tot += wsum[i];
+  const float rstd = 1.0f / sqrtf(tot / (float)H + eps);
+  if (live) {
+    *(half8_t*)(res_out + (size_t)row * H + c * 8) = v;
+    const half8_t wv = *(const half8_t*)(w + c * 8);
+    half8_t o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = (half_t)(((float)v[e] * rstd) * (float)wv[e]);
+    *(half8_t*)(y + (size_t)row * H + c * 8) = o;
+  }
+}
+
 static int check_norm_shape(int rows, int H) {
   if (rows < 0 || H <= 0) return OMNI_EINVAL;
   if ((H & 7) != 0 || H > NORM_MAX_CHUNKS * 512) return OMNI_EUNSUPPORTED;
@@ -136,10 +203,32 @@ extern "C" int omni_add_rmsnorm(const void* x, const void* residual, const void*
   if (rc) return rc;
   if (rows == 0) return OMNI_OK;
   if (!x || !residual || !weight || !y || !residual_out) return OMNI_EINVAL;
-  hipLaunchKernelGGL((rmsnorm_kernel<true, false, false>), dim3(ceil_div(rows, 4)), dim3(256), 0,
-                     (hipStream_t)stream, (const half_t*)x, (const half_t*)residual, nullptr, nullptr,
-                     0, 0, (const half_t*)weight, (half_t*)y, nullptr, nullptr,
-                     (half_t*)residual_out, rows, hidden, eps);
+  if (rows <= 256) {
+    const int threads = ceil_div(hidden >> 3, 64) * 64;
+    hipLaunchKernelGGL(rownorm_kernel<false>, dim3(rows), dim3(threads), 0, (hipStream_t)stream,
+                       (const half_t*)x, nullptr, 0, (const half_t*)residual,
+                       (const half_t*)weight, (half_t*)y, (half_t*)residual_out, rows, hidden, eps);
+  } else {
+    hipLaunchKernelGGL((rmsnorm_kernel<true, false, false>), dim3(ceil_div(rows, 4)), dim3(256), 0,
+                       (hipStream_t)stream, (const half_t*)x, (const half_t*)residual, nullptr,
+                       nullptr, 0, 0, (const half_t*)weight, (half_t*)y, nullptr, nullptr,
+                       (half_t*)residual_out, rows, hidden, eps);
+  }
+  OMNI_CHECK_LAUNCH();
+  return OMNI_OK;
+}
+
+extern "C" int omni_add_rmsnorm_partials(const float* partials, int nparts, const void* residual,
+                                         const void* weight, void* y, void* residual_out, int rows,
+                                         int hidden, float eps, void* stream) {
+  int rc = check_norm_shape(rows, hidden);
+  if (rc) return rc;
+  if (rows == 0) return OMNI_OK;
+  if (!partials || nparts <= 0 || !residual || !weight || !y || !residual_out) return OMNI_EINVAL;
+  const int threads = ceil_div(hidden >> 3, 64) * 64;
+  hipLaunchKernelGGL(rownorm_kernel<true>, dim3(rows), dim3(threads), 0, (hipStream_t)stream,
+                     nullptr, partials, nparts, (const half_t*)residual, (const half_t*)weight,
+                     (half_t*)y, (half_t*)residual_out, rows, hidden, eps);
   OMNI_CHECK_LAUNCH();
   return OMNI_OK;
 }

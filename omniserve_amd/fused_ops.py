@@ -47,6 +47,16 @@ def add_rms_norm(x, residual, weight, eps):
                             torch.empty_like(residual))
 
 
+def add_rms_norm_partials_out(partials, nparts: int, residual, weight, eps, out, res_out):
+    """add_rms_norm where x is fp16(sum of nparts fp32 split-K partials [S, M, H])."""
+    require_cuda(partials, dtype=torch.float32)
+    require_cuda(residual, weight, out, res_out, dtype=torch.float16)
+    m, n = _rows(residual)
+    call("omni_add_rmsnorm_partials", ptr(partials), nparts, ptr(residual), ptr(weight), ptr(out),
+         ptr(res_out), m, n, float(eps), stream())
+    return out, res_out
+
+
 def add_rms_norm_fp8(x, residual, weight, eps):
     """add_rms_norm with the normed output quantised to e4m3fn per row.
 

@@ -22,16 +22,20 @@ import torch
 
 from ._lib import call, ptr, require_cuda, stream
 
-MAX_DECODE_SPLITS = 64
+MAX_ATTN_SPLITS = 16
 
 
-def decode_splits(n_tokens: int, n_kv: int, max_ctx: int) -> int:
-    """Split groups per (token, kv head) for omni_decode_attention: aim for >= ~512
-    workgroups (4 waves each) on the 256-CU MI355X, with >= 64 keys per wave."""
-    pairs = max(1, n_tokens * n_kv)
-    s = max(1, 512 // pairs)
-    s = min(s, max(1, max_ctx // 256), MAX_DECODE_SPLITS)
-    return s
+def decode_plan(n_tokens: int, n_kv: int, ctx: int) -> tuple:
+    """(waves per workgroup, workgroups per (token, kv head)) for omni_decode_attention,
+    from the pool capacity ``ctx``: enough workgroups to reach the 256 CUs when contexts
+    can be long (measured best at 64 groups x 2k context: 8 waves x 3 workgroups); a
+    single workgroup (no partial-state merge launch) when the context is short."""
+    groups = max(1, n_tokens * n_kv)
+    if ctx <= 128:
+        return 4, 1
+    waves = 8 if groups >= 32 else 4
+    splits = max(1, min(MAX_ATTN_SPLITS, 192 // groups, ctx // 128))
+    return waves, splits
 
 
 class PreallocatedKVCache:
@@ -52,12 +56,12 @@ class PreallocatedKVCache:
         self.v: List[torch.Tensor] = [self.storage[l, 1] for l in range(n_layers)]
         self.lengths = torch.zeros(max_batch, dtype=torch.long, device=device)
         self._active = 0
-        # split-K workspace of the decode attention (shared by all layers; launches on one
-        # stream are ordered) and its self-resetting counters.
+        # partial softmax states of split decode attention (shared by all layers: launches
+        # on one stream are ordered)
         G = self.n_heads // n_kv_heads
-        self._attn_ws = torch.empty(max_batch * n_kv_heads * MAX_DECODE_SPLITS * G * (head_dim + 2),
+        self._attn_ws = torch.empty(max_batch * n_kv_heads * MAX_ATTN_SPLITS * G * (head_dim + 2),
                                     device=device, dtype=torch.float32)
-        self._attn_ctr = torch.zeros(max_batch * n_kv_heads, device=device, dtype=torch.int32)
+        self.attn_plan = None      # (waves, splits) override; None = decode_plan()
 
     # ---- slot operations (kv_prealloc.py:43-84) ------------------------------------
     def set_slot_prefix(self, slot: int, legacy_kv, length: int) -> None:
@@ -101,14 +105,18 @@ class PreallocatedKVCache:
     # ---- kernel calls --------------------------------------------------------------
     def attend(self, q: torch.Tensor, q_stride: int, layer_idx: int, kv_len: torch.Tensor,
                kv_by_slot: bool, kv_add: int, out: torch.Tensor, n: int, scale: float,
-               slots: torch.Tensor | None = None, splits: int | None = None) -> torch.Tensor:
+               slots: torch.Tensor | None = None, plan: tuple | None = None) -> torch.Tensor:
         """omni_decode_attention over pool rows (slots or 0..n-1)."""
-        nh = out.shape[-2]
-        s = splits or decode_splits(n, self.n_kv_heads, self.max_len)
+        nh = self.n_heads
+        if out.numel() < n * nh * self.head_dim:
+            raise ValueError("attention output buffer too small")
+        w, s = plan or self.attn_plan or decode_plan(n, self.n_kv_heads, self.max_len)
+        if n > self.max_batch or s > MAX_ATTN_SPLITS:
+            raise ValueError("attention plan exceeds the pool workspace")
         call("omni_decode_attention", ptr(q), q_stride, ptr(self.k[layer_idx]),
              ptr(self.v[layer_idx]), self.max_batch, self.max_len, ptr(slots), ptr(kv_len),
              int(kv_by_slot), kv_add, ptr(out), n, nh, self.n_kv_heads, self.head_dim,
-             float(scale), s, ptr(self._attn_ws), ptr(self._attn_ctr), stream())
+             float(scale), w, s, ptr(self._attn_ws), stream())
         return out
 
 
@@ -124,21 +132,32 @@ class CacheView:
         self.rope_delta = rope_delta
 
     def rope_and_write(self, qkv: torch.Tensor, layer_idx: int, cos_tab, sin_tab,
-                       mrope_section) -> None:
-        """Fused M-RoPE on q/k (in place in the qkv rows) + K/V write at lengths[row]."""
+                       mrope_section, parts=None) -> None:
+        """Fused M-RoPE on q/k (in place in the qkv rows) + K/V write at lengths[row].
+
+        ``parts = (partials fp32 [S, n, qkv], S, bias, bias_after_round)``: the qkv rows
+        are first formed from the qkv projection's split-K partials (+ bias)."""
         pool = self.pool
         s0, s1, s2 = mrope_section
-        call("omni_mrope_kv_write", ptr(qkv), qkv.stride(0), None, ptr(pool.lengths),
-             ptr(self.rope_delta), ptr(cos_tab), ptr(sin_tab), cos_tab.shape[0],
-             ptr(pool.k[layer_idx]), ptr(pool.v[layer_idx]), None, None, pool.max_batch,
-             pool.max_len, self.n, pool.n_heads, pool.n_kv_heads, pool.head_dim, s0, s1, s2,
-             stream())
+        if parts is None:
+            call("omni_mrope_kv_write", ptr(qkv), qkv.stride(0), None, ptr(pool.lengths),
+                 ptr(self.rope_delta), ptr(cos_tab), ptr(sin_tab), cos_tab.shape[0],
+                 ptr(pool.k[layer_idx]), ptr(pool.v[layer_idx]), None, None, pool.max_batch,
+                 pool.max_len, self.n, pool.n_heads, pool.n_kv_heads, pool.head_dim, s0, s1, s2,
+                 stream())
+            return
+        pbuf, S, bias, bar = parts
+        call("omni_mrope_kv_write_partials", ptr(qkv), qkv.stride(0), ptr(pbuf), S, ptr(bias),
+             int(bar), None, ptr(pool.lengths), ptr(self.rope_delta), ptr(cos_tab), ptr(sin_tab),
+             cos_tab.shape[0], ptr(pool.k[layer_idx]), ptr(pool.v[layer_idx]), None, None,
+             pool.max_batch, pool.max_len, self.n, pool.n_heads, pool.n_kv_heads, pool.head_dim,
+             s0, s1, s2, stream())
 
     def attend_qkv(self, qkv: torch.Tensor, layer_idx: int, scale: float, out: torch.Tensor,
-                   splits: int | None = None) -> torch.Tensor:
+                   plan: tuple | None = None) -> torch.Tensor:
         """Attention for rows [0, n): keys [0, lengths[row]] (the token just written)."""
         return self.pool.attend(qkv, qkv.stride(0), layer_idx, self.pool.lengths, True, 1, out,
-                                self.n, scale, splits=splits)
+                                self.n, scale, plan=plan)
 
     def flash_decode(self, q, key, value, layer_idx, scale):
         """Reference protocol (kv_prealloc.py:272-290): q [n, nh, hd] (rotated), key/value

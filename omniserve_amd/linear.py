@@ -9,53 +9,113 @@ an ``nn.Module`` with ``forward(x[..., K] fp16) -> [..., N] fp16`` installed by
                      (kernels/marlin_linear.py:83-96); repacked once into this library's
                      own MFMA layout.  Bias is added after the fp16 GEMM output (:59-62).
 * ``F16Linear``    - fp16 ``nn.Linear`` replacement using the packed fp16 layout.
+* ``LMHeadArgmax`` - tied lm_head + greedy argmax.
 
-Both run the skinny MFMA kernel (omni_w4a16_gemm / omni_f16_gemm), in blocks of at
-most 64 activation rows.  ``fuse_silu=True`` (the gate_up projection) interleaves the
-gate and up column tiles and emits silu(gate) * up directly: [.., 2I] -> [.., I].
+All run the skinny MFMA kernel (omni_w4a16_gemm / omni_f16_gemm) in blocks of at most
+64 activation rows.  ``fuse_silu=True`` (the gate_up projection) interleaves the gate
+and up column tiles and emits silu(gate) * up directly: [.., 2I] -> [.., I].
+``forward_partial`` writes fp32 split-K partial sums instead of fp16 output, for a
+consumer kernel (the next add+RMSNorm) that adds them in slice order.
+
+Launch plans (workgroup shape preset, K split) come from ``PLANS`` keyed by the
+weight format and shape; the decode step of the 2B decoder uses the entries below.
 """
 
 from __future__ import annotations
 
-import math
+from typing import Dict, Tuple
 
 import torch
 from torch import nn
 
 from ._lib import call, lib, ptr, require_cuda, stream
 
-EPI_STORE, EPI_SILU = 0, 1
+EPI_STORE, EPI_SILU, EPI_PARTIAL = 0, 1, 2
 MAX_SKINNY_M = 64
 
-
-def _ksplit(K: int, N: int, M: int) -> int:
-    """Split-K factor for the skinny kernel: enough workgroups to cover the 256 CUs
-    while keeping each wave's weight stream >= ~6 KB and the LDS tile <= 64 KB."""
-    KG = K // 128
-    mb = (M + 15) // 16
-    # LDS: mb*16 rows x (KC + 8) halfs
-    max_groups_lds = max(1, ((64 * 1024) // (mb * 16 * 2) - 8) // 128)
-    ngroups = max(1, N // 128)
-    ks = 1
-    while ngroups * ks < 256 and ks * 2 <= KG and KG // (ks * 2) >= 3:
-        ks *= 2
-    while math.ceil(KG / ks) > max_groups_lds:
-        ks += 1
-    return min(ks, KG)
-
-
-class _SkinnyBuffers:
-    """Per-module split-K workspace and self-resetting counters (graph-safe)."""
-
-    def __init__(self, N: int, K: int, device):
-        self.N, self.K = N, K
-        ks_max = K // 128
-        self.ws = torch.empty(ks_max * MAX_SKINNY_M * N, device=device, dtype=torch.float32)
-        self.counters = torch.zeros(max(1, N // 16), device=device, dtype=torch.int32)
+# (weight format, K, N) -> (store preset, partial preset, partial ksplit); measured on
+# MI355X at M = 32 (graph-replayed launches).  Presets (tiles per wave, column waves,
+# in-group K split): 0 = (1, 8, 2), 1 = (1, 8, 1), 2 = (1, 4, 4), 3 = (2, 4, 2);
+# SiLU: 0 = (2, 4, 4), 1 = (2, 8, 1), 2 = (2, 4, 2), 3 = (2, 2, 4).
+PLANS: Dict[Tuple[str, int, int], Tuple[int, int, int]] = {
+    ("int4", 1536, 2048): (2, 2, 7),
+    ("int4", 1536, 1536): (2, 2, 10),
+    ("int4", 8960, 1536): (2, 2, 10),
+    ("int4", 1536, 17920): (0, 2, 1),     # SiLU-fused gate_up: preset 0 = (2, 4, 4)
+    ("fp16", 1536, 2048): (2, 2, 7),
+    ("fp16", 1536, 1536): (2, 2, 10),
+    ("fp16", 8960, 1536): (2, 2, 10),
+    ("fp16", 1536, 17920): (0, 2, 1),
+}
 
 
-class GPTQLinear(nn.Module):
+def _plan(fmt: str, K: int, N: int) -> Tuple[int, int, int]:
+    if (fmt, K, N) in PLANS:
+        return PLANS[(fmt, K, N)]
+    ks = max(1, min(K // 128, (K // 128 + 6) // 7))
+    return (2, 1, ks)
+
+
+class _Skinny(nn.Module):
+    """Shared launch logic of the packed-weight linears."""
+
+    fmt = "fp16"
+
+    def _init_plan(self):
+        self.store_preset, self.partial_preset, self.partial_ksplit = _plan(self.fmt, self.K, self.N)
+
+    @property
+    def out_features(self) -> int:
+        return self.N // 2 if self.fuse_silu else self.N
+
+    def partial_slices(self, ksplit: int | None = None) -> int:
+        return lib().omni_gemm_slices(self.K, ksplit or self.partial_ksplit)
+
+    def _call(self, x2d, out, partial, epilogue, ksplit, preset):
+        raise NotImplementedError
+
+    def forward_out(self, x2d: torch.Tensor, out: torch.Tensor, preset: int | None = None):
+        """fp16 output (SiLU-fused for gate_up) into out; any number of rows."""
+        M = x2d.shape[0]
+        if M > MAX_SKINNY_M:
+            for s in range(0, M, MAX_SKINNY_M):
+                e = min(M, s + MAX_SKINNY_M)
+                self.forward_out(x2d[s:e], out[s:e], preset)
+            return out
+        epi = EPI_SILU if self.fuse_silu else EPI_STORE
+        self._call(x2d, out, None, epi, 1, self.store_preset if preset is None else preset)
+        return out
+
+    def forward_partial(self, x2d: torch.Tensor, partial: torch.Tensor,
+                        ksplit: int | None = None, preset: int | None = None) -> int:
+        """fp32 split-K partial sums [S][M][N] (no bias) into partial; returns S."""
+        if self.fuse_silu:
+            raise ValueError("the SiLU-fused projection has no partial form")
+        M = x2d.shape[0]
+        if M > MAX_SKINNY_M:
+            raise ValueError(f"partial sums support up to {MAX_SKINNY_M} rows")
+        ks = ksplit or self.partial_ksplit
+        S = self.partial_slices(ks)
+        if partial.numel() < S * M * self.N or partial.dtype != torch.float32:
+            raise ValueError("partial buffer too small or not fp32")
+        self._call(x2d, None, partial, EPI_PARTIAL, ks,
+                   self.partial_preset if preset is None else preset)
+        return S
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        x2d = x.reshape(-1, self.K)
+        if not x2d.is_contiguous():
+            x2d = x2d.contiguous()
+        require_cuda(x2d, dtype=torch.float16)
+        out = torch.empty(x2d.shape[0], self.out_features, device=x.device, dtype=torch.float16)
+        self.forward_out(x2d, out)
+        return out.reshape(*x.shape[:-1], self.out_features)
+
+
+class GPTQLinear(_Skinny):
     """W4A16 GPTQ linear: y = fp16(x . dequant(W)) (+ bias, added after rounding)."""
+
+    fmt = "int4"
 
     def __init__(self, qweight: torch.Tensor, scales: torch.Tensor, bias=None,
                  group_size: int = 128, fuse_silu: bool = False):
@@ -75,37 +135,16 @@ class GPTQLinear(nn.Module):
                                                           device=dev, dtype=torch.int32))
         self.register_buffer("scales_packed", torch.empty(N // 16, K // 128, 16,
                                                          device=dev, dtype=torch.float16))
-        call("omni_gptq_repack", ptr(qweight), ptr(scales), ptr(self.qweight_packed),
-             ptr(self.scales_packed), K, N, int(fuse_silu), stream())
+        call("omni_gptq_repack", ptr(qweight.contiguous()), ptr(scales.contiguous()),
+             ptr(self.qweight_packed), ptr(self.scales_packed), K, N, int(fuse_silu), stream())
         self.bias = None if bias is None else bias.to(device=dev, dtype=torch.float16).contiguous()
-        self._buf = _SkinnyBuffers(N, K, dev)
+        self._init_plan()
 
-    @property
-    def out_features(self) -> int:
-        return self.N // 2 if self.fuse_silu else self.N
-
-    def forward_out(self, x2d: torch.Tensor, out: torch.Tensor, ksplit: int | None = None):
-        M = x2d.shape[0]
-        if M > MAX_SKINNY_M:
-            for s in range(0, M, MAX_SKINNY_M):
-                e = min(M, s + MAX_SKINNY_M)
-                self.forward_out(x2d[s:e], out[s:e], ksplit)
-            return out
-        ks = ksplit or _ksplit(self.K, self.N, M)
+    def _call(self, x2d, out, partial, epilogue, ksplit, preset):
         call("omni_w4a16_gemm", ptr(x2d), x2d.stride(0), ptr(self.qweight_packed),
-             ptr(self.scales_packed), ptr(self.bias), 1, ptr(out), out.stride(0), M, self.N,
-             self.K, EPI_SILU if self.fuse_silu else EPI_STORE, ks, 2, ptr(self._buf.ws),
-             ptr(self._buf.counters), stream())
-        return out
-
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        x2d = x.reshape(-1, self.K)
-        if not x2d.is_contiguous():
-            x2d = x2d.contiguous()
-        require_cuda(x2d, dtype=torch.float16)
-        out = torch.empty(x2d.shape[0], self.out_features, device=x.device, dtype=torch.float16)
-        self.forward_out(x2d, out)
-        return out.reshape(*x.shape[:-1], self.out_features)
+             ptr(self.scales_packed), ptr(self.bias), 1, ptr(out),
+             0 if out is None else out.stride(0), ptr(partial), x2d.shape[0], self.N, self.K,
+             epilogue, ksplit, preset, stream())
 
     def dequantized(self) -> torch.Tensor:
         """W^T [K, N] fp16 as the kernels see it (columns in packed order)."""
@@ -115,8 +154,10 @@ class GPTQLinear(nn.Module):
         return w
 
 
-class F16Linear(nn.Module):
+class F16Linear(_Skinny):
     """fp16 linear over the packed MFMA layout: y = fp16(x . W^T + b)."""
+
+    fmt = "fp16"
 
     def __init__(self, weight: torch.Tensor, bias=None, fuse_silu: bool = False):
         super().__init__()
@@ -130,44 +171,24 @@ class F16Linear(nn.Module):
         call("omni_f16_pack", ptr(weight.contiguous()), ptr(self.weight_packed), K, N,
              int(fuse_silu), stream())
         self.bias = None if bias is None else bias.to(device=dev, dtype=torch.float16).contiguous()
-        self._buf = _SkinnyBuffers(N, K, dev)
+        self._init_plan()
 
     @classmethod
     def from_linear(cls, linear: nn.Linear, fuse_silu: bool = False) -> "F16Linear":
         return cls(linear.weight.data, linear.bias, fuse_silu=fuse_silu)
 
-    @property
-    def out_features(self) -> int:
-        return self.N // 2 if self.fuse_silu else self.N
-
-    def forward_out(self, x2d: torch.Tensor, out: torch.Tensor, ksplit: int | None = None):
-        M = x2d.shape[0]
-        if M > MAX_SKINNY_M:
-            for s in range(0, M, MAX_SKINNY_M):
-                e = min(M, s + MAX_SKINNY_M)
-                self.forward_out(x2d[s:e], out[s:e], ksplit)
-            return out
-        ks = ksplit or _ksplit(self.K, self.N, M)
+    def _call(self, x2d, out, partial, epilogue, ksplit, preset):
         call("omni_f16_gemm", ptr(x2d), x2d.stride(0), ptr(self.weight_packed), ptr(self.bias),
-             ptr(out), out.stride(0), M, self.N, self.K,
-             EPI_SILU if self.fuse_silu else EPI_STORE, ks, 2, ptr(self._buf.ws),
-             ptr(self._buf.counters), stream())
-        return out
-
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        x2d = x.reshape(-1, self.K)
-        if not x2d.is_contiguous():
-            x2d = x2d.contiguous()
-        require_cuda(x2d, dtype=torch.float16)
-        out = torch.empty(x2d.shape[0], self.out_features, device=x.device, dtype=torch.float16)
-        self.forward_out(x2d, out)
-        return out.reshape(*x.shape[:-1], self.out_features)
+             ptr(out), 0 if out is None else out.stride(0), ptr(partial), x2d.shape[0], self.N,
+             self.K, epilogue, ksplit, preset, stream())
 
 
 class LMHeadArgmax(nn.Module):
     """Tied lm_head (qwen2_llm.py:167-168, 190) fused with greedy argmax
     (runners/multimodal.py:307-308): ids = argmax_n fp16(h . E[n]), lowest index on ties.
-    The embedding table is stored once, packed; the token gather reads the packed form."""
+    The embedding table is stored once, packed; the token gather reads the packed form.
+    Two launches: the GEMM writes per-workgroup (max, index) candidates, a small kernel
+    reduces them (and can advance the decode-step bookkeeping)."""
 
     def __init__(self, embed: torch.Tensor):
         super().__init__()
@@ -178,24 +199,27 @@ class LMHeadArgmax(nn.Module):
         self.register_buffer("table_packed", torch.empty(V // 16, H // 32, 64, 8, device=dev,
                                                         dtype=torch.float16))
         call("omni_f16_pack", ptr(embed.contiguous()), ptr(self.table_packed), H, V, 0, stream())
-        grid = lib().omni_lmhead_argmax_grid(V)
-        self._cand_val = torch.empty(grid * MAX_SKINNY_M, device=dev, dtype=torch.float32)
-        self._cand_idx = torch.empty(grid * MAX_SKINNY_M, device=dev, dtype=torch.int32)
-        self._counter = torch.zeros(1, device=dev, dtype=torch.int32)
+        self.grid = lib().omni_lmhead_argmax_grid(V)
+        self._cand_val = torch.empty(self.grid * MAX_SKINNY_M, device=dev, dtype=torch.float32)
+        self._cand_idx = torch.empty(self.grid * MAX_SKINNY_M, device=dev, dtype=torch.int32)
 
-    def argmax_out(self, h2d: torch.Tensor, ids_out: torch.Tensor, logits_out=None):
+    def argmax_out(self, h2d: torch.Tensor, ids_out: torch.Tensor, logits_out=None,
+                   next_ids: torch.Tensor | None = None, lengths: torch.Tensor | None = None):
+        """ids_out[m] = greedy token of row m; optionally also next_ids[m] = ids_out[m] and
+        lengths[m] += 1 (rows < M) in the same finalize launch."""
         M = h2d.shape[0]
         if M > MAX_SKINNY_M:
             raise ValueError(f"lm_head argmax supports up to {MAX_SKINNY_M} rows per call")
         require_cuda(h2d, dtype=torch.float16)
         require_cuda(ids_out, dtype=torch.int64)
-        call("omni_lmhead_argmax", ptr(h2d), h2d.stride(0), ptr(self.table_packed), M, self.V,
-             self.H, ptr(logits_out), ptr(ids_out), ptr(self._cand_val), ptr(self._cand_idx),
-             ptr(self._counter), stream())
+        call("omni_lmhead_candidates", ptr(h2d), h2d.stride(0), ptr(self.table_packed), M,
+             self.V, self.H, ptr(logits_out), ptr(self._cand_val), ptr(self._cand_idx), stream())
+        call("omni_argmax_finalize", ptr(self._cand_val), ptr(self._cand_idx), self.grid, M,
+             ptr(ids_out), ptr(next_ids), ptr(lengths), stream())
         return ids_out
 
     def logits(self, h2d: torch.Tensor) -> torch.Tensor:
-        """fp16 logits [M, V] (and the argmax computed alongside, discarded)."""
+        """fp16 logits [M, V] (the fused argmax runs alongside and is discarded)."""
         out = torch.empty(h2d.shape[0], self.V, device=h2d.device, dtype=torch.float16)
         ids = torch.empty(h2d.shape[0], device=h2d.device, dtype=torch.int64)
         for s in range(0, h2d.shape[0], MAX_SKINNY_M):

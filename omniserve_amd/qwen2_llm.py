@@ -153,35 +153,52 @@ class Qwen2LLM(nn.Module):
             cfg = self.cfg
             H, I = cfg.hidden_size, cfg.intermediate_size
             mk = lambda *s: torch.empty(*s, device=device, dtype=torch.float16)
+            f32 = lambda *s: torch.empty(*s, device=device, dtype=torch.float32)
+            Sd = max(l.down_proj.partial_slices() for l in self.layers)
+            So = max(l.o_proj.partial_slices() for l in self.layers)
+            Sq = max(l.qkv_proj.partial_slices() for l in self.layers)
             self._bufs[n] = {
-                "h": mk(n, H), "res": mk(n, H), "x": mk(n, H), "o": mk(n, H),
+                "h": mk(n, H), "res": mk(n, H),
                 "qkv": mk(n, cfg.qkv_out), "attn": mk(n, cfg.num_heads * cfg.head_dim),
                 "act": mk(n, I),
+                "dpart": f32(Sd, n, H), "opart": f32(So, n, H), "qpart": f32(Sq, n, cfg.qkv_out),
             }
         return self._bufs[n]
 
     def decode_greedy(self, ids: torch.Tensor, view, ids_out: torch.Tensor,
-                      logits_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                      logits_out: Optional[torch.Tensor] = None,
+                      next_ids: Optional[torch.Tensor] = None,
+                      lengths: Optional[torch.Tensor] = None) -> torch.Tensor:
         """One decode step for pool rows [0, n): ids [n] int64 (device) -> ids_out [n]
-        (greedy).  Reads positions from pool.lengths (+ rope delta), writes K/V, does not
-        advance lengths.  No allocation, no host sync."""
+        (greedy).  Reads positions from pool.lengths (+ rope delta) and writes K/V there.
+        With ``lengths`` the final launch also advances lengths[:n] by one and with
+        ``next_ids`` copies the new ids there.  No allocation, no host sync.
+
+        Per layer (8 launches, 9 with split attention): add+RMSNorm over the previous
+        down projection's fp32 split-K partials -> qkv (partials) -> qkv bias + M-RoPE +
+        KV write -> attention -> o_proj (partials) -> add+RMSNorm over them ->
+        gate_up + SiLU -> down (partials).  Partial sums cross a kernel boundary, never
+        a device-scope fence."""
         cfg = self.cfg
         n = ids.shape[0]
         b = self.decode_buffers(n, ids.device)
         eps = cfg.rms_norm_eps
-        h, res, x = b["h"], b["res"], b["x"]
+        h, res = b["h"], b["res"]
         F.embed_rms_norm_out(ids, self.lm_head.table_packed, True, self.layers[0].in_norm, eps,
                              h, res)
+        S = 0
         for i, layer in enumerate(self.layers):
             if i > 0:
-                F.add_rms_norm_out(x, res, layer.in_norm, eps, h, res)
-            layer.qkv_proj.forward_out(h, b["qkv"])
-            view.rope_and_write(b["qkv"], i, self.rope_cos, self.rope_sin, cfg.mrope_section)
+                F.add_rms_norm_partials_out(b["dpart"], S, res, layer.in_norm, eps, h, res)
+            qp = layer.qkv_proj
+            Sq = qp.forward_partial(h, b["qpart"])
+            view.rope_and_write(b["qkv"], i, self.rope_cos, self.rope_sin, cfg.mrope_section,
+                                parts=(b["qpart"], Sq, qp.bias, qp.fmt == "int4"))
             view.attend_qkv(b["qkv"], i, self.scale, b["attn"])
-            layer.o_proj.forward_out(b["attn"], b["o"])
-            F.add_rms_norm_out(b["o"], res, layer.post_norm, eps, h, res)
+            So = layer.o_proj.forward_partial(b["attn"], b["opart"])
+            F.add_rms_norm_partials_out(b["opart"], So, res, layer.post_norm, eps, h, res)
             layer.gate_up_proj.forward_out(h, b["act"])
-            layer.down_proj.forward_out(b["act"], x)
-        F.add_rms_norm_out(x, res, self.norm, eps, h, res)
-        self.lm_head.argmax_out(h, ids_out, logits_out)
+            S = layer.down_proj.forward_partial(b["act"], b["dpart"])
+        F.add_rms_norm_partials_out(b["dpart"], S, res, self.norm, eps, h, res)
+        self.lm_head.argmax_out(h, ids_out, logits_out, next_ids, lengths)
         return ids_out

@@ -1,0 +1,328 @@
+"""Model runners: the drop-in boundary the engine/scheduler call every iteration.
+
+``ModelRunner`` (omniserve/runners/base.py:26-57) is the abstract interface;
+``StubRunner`` (:60-91) the no-GPU control-plane double; ``MultimodalRunner``
+(runners/multimodal.py:19-379) the model-agnostic runner over the preallocated KV
+pool; ``NativeQwenVLRunner`` (runners/qwen_vl_native.py:14-20) keeps the
+reference's entry-point name and constructor signature.
+
+Decode (multimodal.py:286-357): sequences sorted by slot must occupy slots [0, n);
+one step advances each by one token.  With ``use_graph=True`` the whole step -
+embedding gather + 28 layers + final norm + lm_head/argmax + length advance - is one
+HIP-graph replay per batch size (captured lazily, static buffers kept alive).  The
+host does at most one small H2D (token ids, only when the batch composition
+changed) and one D2H (the new ids) per step.
+"""
+
+from __future__ import annotations
+
+import abc
+from typing import Dict, List
+
+import torch
+
+from .kv_cache import PreallocatedKVCache
+from .request import Sequence
+
+
+class ModelRunner(abc.ABC):
+    @abc.abstractmethod
+    def tokenize(self, seq: Sequence) -> None:
+        """Fill seq.prompt_token_ids from the request prompt."""
+
+    @abc.abstractmethod
+    def prefill(self, seqs: List[Sequence]) -> None:
+        """Prefill each sequence's prompt; append the first generated token."""
+
+    @abc.abstractmethod
+    def decode(self, seqs: List[Sequence]) -> None:
+        """Advance every running sequence by exactly one token."""
+
+    def chunk_prefill(self, seq: Sequence) -> None:
+        raise NotImplementedError("this runner does not support chunked prefill")
+
+    def mixed_step(self, chunk_seq: Sequence, decode_seqs: List[Sequence]) -> None:
+        self.chunk_prefill(chunk_seq)
+        self.decode(decode_seqs)
+
+    @abc.abstractmethod
+    def detokenize(self, seq: Sequence, new_token_ids: List[int]) -> str:
+        """Render new token ids as text for streaming."""
+
+    def free(self, seq: Sequence) -> None:
+        """Release a finished sequence's resources (default: nothing)."""
+
+
+class StubRunner(ModelRunner):
+    """Deterministic no-GPU runner for exercising a scheduler/engine."""
+
+    def __init__(self, reply: str = "ok " * 8):
+        self._reply_tokens = reply.split()
+
+    def tokenize(self, seq: Sequence) -> None:
+        p = seq.request.prompt
+        n = len(p.split()) if isinstance(p, str) else len(p)
+        seq.prompt_token_ids = list(range(max(1, n)))
+
+    def prefill(self, seqs: List[Sequence]) -> None:
+        for seq in seqs:
+            seq.kv_handle = {"len": seq.num_prompt_tokens}
+            seq.append_token(0)
+            seq.maybe_finish()
+
+    def decode(self, seqs: List[Sequence]) -> None:
+        for seq in seqs:
+            seq.append_token(seq.num_output_tokens)
+            seq.kv_handle["len"] += 1
+            seq.maybe_finish()
+
+    def detokenize(self, seq: Sequence, new_token_ids: List[int]) -> str:
+        return " ".join(self._reply_tokens[t % len(self._reply_tokens)] for t in new_token_ids) + " "
+
+
+class MultimodalRunner(ModelRunner):
+    def __init__(self, adapter, max_running: int = 32, max_len: int = 1024, prefix_cache=None,
+                 use_graph: bool = False):
+        if prefix_cache is not None:
+            raise NotImplementedError("prefix caching is not part of this build")
+        self.adapter = adapter
+        self.device = adapter.device
+        self.max_running = max_running
+        self.image_token_id = adapter.image_token_id
+        self.eos_ids = adapter.eos_ids
+        self._use_graph = use_graph
+        self._reserve_slot = max_running       # kept for layout parity (multimodal.py:32-37)
+        self._pool = PreallocatedKVCache(
+            n_layers=adapter.num_layers, max_batch=max_running + 1,
+            n_kv_heads=adapter.num_kv_heads, max_len=max_len, head_dim=adapter.head_dim,
+            device=self.device, dtype=torch.float16, n_heads=adapter.num_heads)
+        self._rope_delta = torch.zeros(max_running + 1, dtype=torch.int64, device=self.device)
+        self._slot_seq: List[Sequence] = []
+        self._kv_len: List[int] = []          # host mirror of pool.lengths for active slots
+        self._graphs: Dict[int, tuple] = {}
+        self._eager: Dict[int, dict] = {}
+        self._dev_ids_for = None              # batch whose next ids already sit on device
+        self._pinned_ids = torch.zeros(max_running + 1, dtype=torch.int64).pin_memory()
+
+    @property
+    def pool(self) -> PreallocatedKVCache:
+        return self._pool
+
+    # ---- ModelRunner interface -----------------------------------------------------
+    def tokenize(self, seq: Sequence) -> None:
+        if not seq.prompt_token_ids:
+            seq.prompt_token_ids = self.adapter.encode_prompt(seq.request.prompt)
+        sp = seq.request.sampling
+        for e in self.eos_ids:
+            if e not in sp.stop_token_ids:
+                sp.stop_token_ids.append(e)
+
+    @torch.inference_mode()
+    def prefill(self, seqs: List[Sequence]) -> None:
+        """Packed prefill, compute branch (multimodal.py:116-144): every prompt in one
+        forward, causal within its segment, K/V written to its slot, logits only at
+        segment ends."""
+        if not seqs:
+            return
+        base = len(self._slot_seq)
+        if base + len(seqs) > self.max_running:
+            raise RuntimeError(f"KV pool full: {base} running + {len(seqs)} new > "
+                               f"{self.max_running}")
+        dev = self.device
+        embeds, positions, seg_lens, deltas = [], [], [], []
+        for seq in seqs:
+            if not seq.prompt_token_ids:
+                self.tokenize(seq)
+            ids = seq.prompt_token_ids
+            L = len(ids)
+            if L == 0 or L >= self._pool.max_len:
+                raise ValueError(f"prompt length {L} outside [1, max_len={self._pool.max_len})")
+            ids_t = torch.tensor(ids, dtype=torch.int64, device=dev)
+            emb = self.adapter.embed_tokens(ids_t)
+            images = seq.request.images
+            grids = [im.grid for im in images] if images else None
+            if images:
+                mask = ids_t == self.image_token_id
+                vis = self.adapter.vision_embed(images)
+                if int(mask.sum()) != vis.shape[0]:
+                    raise ValueError("image token count does not match the vision rows")
+                emb[mask] = vis
+            pos, delta = self.adapter.prefill_positions(ids, grids)
+            embeds.append(emb)
+            positions.append(pos.to(dev))
+            seg_lens.append(L)
+            deltas.append(delta)
+        slots = [base + i for i in range(len(seqs))]
+        packed = torch.cat(embeds, 0).unsqueeze(0)
+        pos = torch.cat(positions, dim=1).unsqueeze(1)            # [3, 1, T]
+        last = torch.tensor(seg_lens).cumsum(0) - 1
+        cache = self._pool.packed_prefill_cache(slots, seg_lens)
+        logits = self.adapter.llm(packed, pos, None, cache, logits_indices=last.tolist())[0]
+        toks = self._sample_rows(logits, seqs)
+        for i, seq in enumerate(seqs):
+            slot = slots[i]
+            self._rope_delta[slot] = deltas[i]
+            self._slot_seq.append(seq)
+            self._kv_len.append(seg_lens[i])
+            seq.kv_handle = {"slot": slot, "rope_delta": deltas[i]}
+            seq.append_token(toks[i])
+            seq.maybe_finish()
+        self._dev_ids_for = None
+
+    def attach_prefilled(self, seqs: List[Sequence], lengths: List[int],
+                         rope_deltas: List[int] | None = None) -> List[int]:
+        """Seat sequences whose KV prefix the caller already wrote into the pool (the
+        set_slot_prefix contract, cache/kv_prealloc.py:43-49): each takes the next slot
+        with lengths[slot] = L and decodes from there.  Returns the slots."""
+        base = len(self._slot_seq)
+        if base + len(seqs) > self.max_running:
+            raise RuntimeError("KV pool full")
+        slots = []
+        for i, (seq, L) in enumerate(zip(seqs, lengths)):
+            if not 0 < L < self._pool.max_len:
+                raise ValueError(f"length {L} outside (0, max_len)")
+            slot = base + i
+            d = 0 if rope_deltas is None else int(rope_deltas[i])
+            self._pool.lengths[slot] = L
+            self._rope_delta[slot] = d
+            self._slot_seq.append(seq)
+            self._kv_len.append(int(L))
+            seq.kv_handle = {"slot": slot, "rope_delta": d}
+            slots.append(slot)
+        self._dev_ids_for = None
+        return slots
+
+    def decode(self, seqs: List[Sequence]) -> None:
+        seqs = sorted(seqs, key=lambda s: s.kv_handle["slot"])
+        n = len(seqs)
+        if n == 0:
+            return
+        if [s.kv_handle["slot"] for s in seqs] != list(range(n)):
+            raise AssertionError("decode expects the running sequences in slots [0, n)")
+        for b in range(n):
+            if self._kv_len[b] >= self._pool.max_len:
+                raise RuntimeError(f"sequence in slot {b} reached max_len={self._pool.max_len}")
+        greedy = all(s.request.sampling.greedy for s in seqs)
+        if self._use_graph and greedy:
+            self._decode_graph(seqs, n)
+        else:
+            with torch.inference_mode():
+                self._decode_eager(seqs, n, greedy)
+
+    # ---- decode paths ----------------------------------------------------------------
+    def _load_ids(self, seqs, n, dst: torch.Tensor) -> None:
+        key = tuple(id(s) for s in seqs)
+        if self._dev_ids_for == key:
+            return                      # dst already holds the last step's outputs
+        for b, s in enumerate(seqs):
+            self._pinned_ids[b] = s.last_token_id()
+        dst.copy_(self._pinned_ids[:n], non_blocking=True)
+
+    def _decode_eager(self, seqs, n, greedy: bool):
+        model = self.adapter.model
+        if n not in self._eager:
+            self._eager[n] = {
+                "ids": torch.zeros(n, dtype=torch.int64, device=self.device),
+                "out": torch.zeros(n, dtype=torch.int64, device=self.device),
+                "logits": torch.empty(n, model.cfg.vocab_size, device=self.device,
+                                      dtype=torch.float16),
+            }
+        b = self._eager[n]
+        self._dev_ids_for = None
+        self._load_ids(seqs, n, b["ids"])
+        view = self._pool.view(n, self._rope_delta)
+        model.decode_greedy(b["ids"], view, b["out"], None if greedy else b["logits"],
+                            lengths=self._pool.lengths)
+        if greedy:
+            self._emit(seqs, b["out"].tolist())
+        else:
+            self._emit(seqs, self._sample_rows(b["logits"], seqs))
+
+    def _capture_graph(self, n):
+        model = self.adapter.model
+        bufs = {"ids": torch.zeros(n, dtype=torch.int64, device=self.device),
+                "out": torch.zeros(n, dtype=torch.int64, device=self.device)}
+        view = self._pool.view(n, self._rope_delta)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):   # warm-up: writes K/V at the (not yet valid) next position only
+                model.decode_greedy(bufs["ids"], view, bufs["out"])
+        torch.cuda.current_stream().wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            # the final launch advances lengths[:n] and leaves the new ids in bufs["ids"]
+            # as the next step's input
+            model.decode_greedy(bufs["ids"], view, bufs["out"], next_ids=bufs["ids"],
+                                lengths=self._pool.lengths)
+        # the view and buffers are referenced by the graph: keep them alive with it
+        self._graphs[n] = (g, bufs, view)
+
+    def _decode_graph(self, seqs, n):
+        if n not in self._graphs:
+            self._capture_graph(n)
+        g, bufs, _view = self._graphs[n]
+        self._load_ids(seqs, n, bufs["ids"])
+        g.replay()
+        toks = bufs["out"].tolist()
+        self._emit(seqs, toks)
+        self._dev_ids_for = tuple(id(s) for s in seqs) if all(
+            s.last_token_id() == t for s, t in zip(seqs, toks)) else None
+
+    def _emit(self, seqs, toks):
+        for b, seq in enumerate(seqs):
+            self._kv_len[b] += 1
+            seq.append_token(int(toks[b]))
+            seq.maybe_finish()
+
+    def _sample_rows(self, logits: torch.Tensor, seqs) -> List[int]:
+        """Greedy = argmax of the fp16 logits (multimodal.py:374-377); else temperature
+        sampling."""
+        out = []
+        greedy_rows = logits.float().argmax(-1).tolist()
+        for i, seq in enumerate(seqs):
+            sp = seq.request.sampling
+            if sp.greedy:
+                out.append(int(greedy_rows[i]))
+            else:
+                probs = torch.softmax(logits[i].float() / sp.temperature, dim=-1)
+                out.append(int(torch.multinomial(probs, 1).item()))
+        return out
+
+    # ---- release ----------------------------------------------------------------------
+    def free(self, seq: Sequence) -> None:
+        """Swap-compact the pool (multimodal.py:359-369): the last slot's sequence moves
+        into the freed slot; only its valid KV prefix is copied."""
+        h = seq.kv_handle or {}
+        slot = h.get("slot")
+        if slot is None:
+            return
+        last = len(self._slot_seq) - 1
+        if slot != last:
+            L = self._kv_len[last]
+            self._pool.copy_slot_kv(last, slot, L)
+            self._rope_delta[slot] = self._rope_delta[last]
+            moved = self._slot_seq[last]
+            moved.kv_handle["slot"] = slot
+            self._slot_seq[slot] = moved
+            self._kv_len[slot] = L
+        self._slot_seq.pop()
+        self._kv_len.pop()
+        self._dev_ids_for = None
+
+    def detokenize(self, seq: Sequence, new_token_ids: List[int]) -> str:
+        return self.adapter.detokenize(new_token_ids)
+
+
+class NativeQwenVLRunner(MultimodalRunner):
+    """Entry point with the reference's constructor (runners/qwen_vl_native.py:14-20).
+    Extra keyword arguments go to the adapter (weights=, seed=, num_layers=, ...)."""
+
+    def __init__(self, model_dir: str = None, max_running: int = 32, max_len: int = 1024,
+                 prefix_cache=None, quant: str = None, gptq_dir: str = None,
+                 use_graph: bool = False, **adapter_kwargs):
+        from .adapter import Qwen2VLAdapter
+        adapter = Qwen2VLAdapter(model_dir=model_dir, quant=quant, gptq_dir=gptq_dir,
+                                 max_pos=max(8192, 2 * max_len), **adapter_kwargs)
+        super().__init__(adapter, max_running=max_running, max_len=max_len,
+                         prefix_cache=prefix_cache, use_graph=use_graph)

@@ -161,13 +161,13 @@ def test_mrope_3d_positions(gpu):
 
 
 # ----------------------------------------------------------------------------- attention
-@pytest.mark.parametrize("lengths,splits", [
-    ([1], 1), ([7], 1), ([33, 64, 100], 1), ([300, 5, 1000], 4), ([2048] * 4, 8),
-    ([1, 2, 3, 4095], 16),
+@pytest.mark.parametrize("lengths,waves,splits", [
+    ([1], 4, 1), ([7], 4, 3), ([33, 64, 100], 4, 1), ([300, 5, 1000], 8, 4), ([2048] * 4, 16, 2),
+    ([1, 2, 3, 4095], 4, 16), ([31, 32, 33, 65], 16, 1), ([2049] * 3, 4, 8),
 ])
-def test_decode_attention(gpu, lengths, splits):
+def test_decode_attention(gpu, lengths, waves, splits):
     from omniserve_amd._lib import call, ptr, stream
-    say(f"decode_attention lengths={lengths} splits={splits}")
+    say(f"decode_attention lengths={lengths} waves={waves} splits={splits}")
     n = len(lengths)
     nh, nkv, hd, ML = 12, 2, 128, 4096
     P = n + 1
@@ -176,20 +176,16 @@ def test_decode_attention(gpu, lengths, splits):
     q = f16((n, nh * hd), 53)
     L = torch.tensor(lengths, dtype=torch.int64)
     out = torch.empty(n, nh, hd, device=gpu, dtype=torch.float16)
-    ws = torch.empty(n * nkv * splits * 6 * 130, device=gpu, dtype=torch.float32)
-    ctr = torch.zeros(n * nkv, device=gpu, dtype=torch.int32)
     scale = hd ** -0.5
     kg, vg, qg, Lg = kp.to(gpu), vp.to(gpu), q.to(gpu), L.to(gpu)
-    for rep in range(2):   # second launch checks the counters were reset
-        call("omni_decode_attention", ptr(qg), nh * hd, ptr(kg), ptr(vg), P, ML, None,
-             ptr(Lg), 0, 0, ptr(out), n, nh, nkv, hd, scale, splits, ptr(ws), ptr(ctr),
-             stream())
-        torch.cuda.synchronize()
-        e = ref.decode_attention(q.float().view(n, nh, hd), kp.float(), vp.float(),
-                                 torch.arange(n), L, scale)
-        d = (out.cpu().float() - e).abs().max().item()
-        assert d <= 4e-3, d
-    assert ctr.cpu().eq(0).all()
+    ws = torch.empty(n * nkv * splits * 6 * 130, device=gpu, dtype=torch.float32)
+    call("omni_decode_attention", ptr(qg), nh * hd, ptr(kg), ptr(vg), P, ML, None, ptr(Lg), 0, 0,
+         ptr(out), n, nh, nkv, hd, scale, waves, splits, ptr(ws), stream())
+    torch.cuda.synchronize()
+    e = ref.decode_attention(q.float().view(n, nh, hd), kp.float(), vp.float(),
+                             torch.arange(n), L, scale)
+    d = (out.cpu().float() - e).abs().max().item()
+    assert d <= 4e-3, d
 
 
 @pytest.mark.parametrize("segs", [[1], [5, 16, 17], [256], [100, 37, 512]])
@@ -255,15 +251,29 @@ def test_w4a16_gemm(gpu, M, K, N, bias, silu):
     b = f16((N,), 73, 0.02) if bias else None
     x = f16((M, K), 74)
     lin = GPTQLinear(qw.to(gpu), sc.to(gpu), None if b is None else b.to(gpu), fuse_silu=silu)
-    y = lin(x.to(gpu)).cpu().float()
     W = ref.gptq_dequant(qw, sc)
     if silu:
         e = ref.silu_mul(ref.linear(x.float(), W))
     else:
         e = ref.linear(x.float(), W, None if b is None else b.float(), bias_after_round=True)
-    d = (y - e).abs()
     tol = 2e-3 * max(1.0, e.abs().max().item())
-    assert d.max().item() <= tol, (d.max().item(), tol)
+    xg = x.to(gpu)
+    presets = [None] if silu else [0, 1, 2, 3]
+    for pr in presets:
+        out = torch.empty(M, lin.out_features, device=gpu, dtype=torch.float16)
+        lin.forward_out(xg, out, preset=pr)
+        d = (out.cpu().float() - e).abs().max().item()
+        assert d <= tol, (pr, d, tol)
+    if not silu:
+        # split-K partial sums (fp32, no bias): their slice-ordered sum is the GEMM
+        e32 = x.float() @ W
+        for ks in (2, 5):
+            for pr in (0, 1):
+                part = torch.empty(ks * M * N, device=gpu, dtype=torch.float32)
+                S = lin.forward_partial(xg, part, ks, pr)
+                got = part[:S * M * N].view(S, M, N).sum(0).cpu()
+                d = (got - e32).abs().max().item()
+                assert d <= 1e-3 * max(1.0, e32.abs().max().item()), (ks, pr, d)
 
 
 @pytest.mark.parametrize("M", [1, 16, 32])
@@ -285,6 +295,28 @@ def test_f16_gemm(gpu, M, K, N, bias, silu):
     d = (y - e).abs()
     tol = 2e-3 * max(1.0, e.abs().max().item())
     assert d.max().item() <= tol, (d.max().item(), tol)
+
+
+def test_add_rmsnorm_partials(gpu):
+    """x = fp16(sum of split-K partials in slice order), then add + RMSNorm."""
+    from omniserve_amd import fused_ops as F
+    say("add_rmsnorm over split-K partials")
+    S, M, H = 7, 32, 1536
+    g = torch.Generator().manual_seed(101)
+    parts = torch.randn(S, M, H, generator=g) * 0.3
+    r = f16((M, H), 102)
+    w = torch.ones(H, dtype=torch.float16)
+    pg, rg, wg = parts.to(gpu), r.to(gpu), w.to(gpu)
+    y = torch.empty(M, H, device=gpu, dtype=torch.float16)
+    nr = torch.empty_like(y)
+    F.add_rms_norm_partials_out(pg, S, rg, wg, 1e-6, y, nr)
+    torch.cuda.synchronize()
+    x16 = ref.r16(parts.sum(0))
+    ey, er = ref.add_rms_norm(x16, r.float(), w.float(), 1e-6)
+    # the slice-ordered fp32 sum can differ from torch's sum order by an ulp before the
+    # fp16 rounding: residuals agree to one fp16 ulp
+    assert (nr.cpu().float() - er).abs().max().item() <= 2e-3 * er.abs().max().item()
+    assert (y.cpu().float() - ey).abs().max().item() <= 2e-3 * ey.abs().max().item()
 
 
 @pytest.mark.parametrize("M", [1, 32])
@@ -329,3 +361,50 @@ def test_lmhead_argmax_ties(gpu):
     lm.argmax_out(h.to(gpu), ids)
     torch.cuda.synchronize()
     assert ids.cpu().tolist() == [3, 3]
+
+
+@pytest.mark.parametrize("bias_after_round", [0, 1])
+def test_mrope_from_partials(gpu, bias_after_round):
+    """qkv rows formed from split-K partials (+ bias) then rotated: bit-equal to forming
+    the fp16 rows on the host the same way and running the plain kernel."""
+    from omniserve_amd._lib import call, ptr, stream
+    from omniserve_amd.qwen2_llm import rope_tables
+    say(f"mrope from partials bias_after_round={bias_after_round}")
+    cfg = ref.Qwen2Config()
+    nh, nkv, hd = 12, 2, 128
+    T, S, P, ML = 5, 7, 6, 64
+    W = (nh + 2 * nkv) * hd
+    g = torch.Generator().manual_seed(111)
+    parts = torch.randn(S, T, W, generator=g) * 0.2
+    bias = f16((W,), 112, 0.02)
+    lengths = torch.randint(0, 40, (P,), generator=torch.Generator().manual_seed(113))
+    acc = torch.zeros(T, W)
+    for s_ in range(S):          # slice order, as the kernel adds them
+        acc = acc + parts[s_]
+    if bias_after_round:
+        rows = (acc.half().float() + bias.float()).half()
+    else:
+        rows = (acc + bias.float()).half()
+    cos, sin = rope_tables(cfg, 128, gpu)
+    outs = []
+    for mode in ("partials", "plain"):
+        kc = torch.zeros(P, ML, nkv, hd, dtype=torch.float16, device=gpu)
+        vc = torch.zeros_like(kc)
+        lg = lengths.to(gpu)
+        if mode == "partials":
+            q = torch.zeros(T, W, dtype=torch.float16, device=gpu)
+            pg, bg = parts.to(gpu), bias.to(gpu)
+            call("omni_mrope_kv_write_partials", ptr(q), W, ptr(pg), S, ptr(bg), bias_after_round,
+                 None, ptr(lg), None, ptr(cos), ptr(sin), 128, ptr(kc), ptr(vc), None, None, P,
+                 ML, T, nh, nkv, hd, 16, 24, 24, stream())
+        else:
+            q = rows.to(gpu)
+            call("omni_mrope_kv_write", ptr(q), W, None, ptr(lg), None, ptr(cos), ptr(sin), 128,
+                 ptr(kc), ptr(vc), None, None, P, ML, T, nh, nkv, hd, 16, 24, 24, stream())
+        torch.cuda.synchronize()
+        outs.append((q.cpu(), kc.cpu(), vc.cpu()))
+    # sums can differ from the host's in the last fp32 ulp -> allow 1 fp16 ulp
+    for a, b in zip(outs[0], outs[1]):
+        d = (a.float() - b.float()).abs()
+        assert d.max().item() <= 2e-3 * max(1.0, b.float().abs().max().item())
+        assert (d > 0).float().mean().item() < 0.01

@@ -1,0 +1,266 @@
+"""End-to-end parity of the decode step / runner on the GPU against the CPU oracle.
+
+Bar: fp16 logits within max-abs 2e-2 and cosine >= 0.9999
+of the oracle's fp16-faithful restatement; greedy ids equal to the oracle's argmax
+wherever the oracle's top-1/top-2 margin exceeds the measured logit error; int4
+dequantised weights bit-exact (test_gpu_kernels.py).  Free-running greedy
+continuations are compared token by token up to the first near-tie of the oracle.
+"""
+
+import pytest
+import torch
+
+from oracle import qwen2_ref as ref
+from tests.helpers import check_ids, compare_logits, oracle_from_fp16, oracle_from_gptq
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(f"[gpu-test] {msg}", flush=True)
+
+
+def _fill_pool(pool, lengths, seed):
+    """Random N(0,1) fp16 K/V prefix up to each row's length; returns fp32 CPU copies."""
+    g = torch.Generator().manual_seed(seed)
+    kp, vp = [], []
+    for l in range(pool.n_layers):
+        k = torch.zeros(pool.max_batch, pool.max_len, pool.n_kv_heads, pool.head_dim,
+                        dtype=torch.float16)
+        v = torch.zeros_like(k)
+        for b, L in enumerate(lengths):
+            k[b, :L] = torch.randn(L, pool.n_kv_heads, pool.head_dim, generator=g).half()
+            v[b, :L] = torch.randn(L, pool.n_kv_heads, pool.head_dim, generator=g).half()
+        pool.k[l].copy_(k)
+        pool.v[l].copy_(v)
+        kp.append(k.float())
+        vp.append(v.float())
+    for b, L in enumerate(lengths):
+        pool.lengths[b] = L
+    return kp, vp
+
+
+def _decode_once(gpu, quant, n_layers, lengths, seed):
+    from omniserve_amd import synth
+    from omniserve_amd.kv_cache import PreallocatedKVCache
+    from omniserve_amd.qwen2_llm import Qwen2LLM
+    shape = synth.DecoderShape()
+    if quant == "gptq":
+        w = synth.gptq_decoder(shape, seed=seed, num_layers=n_layers)
+        model = Qwen2LLM.from_gptq(w, shape, gpu, max_pos=1024)
+        orc = oracle_from_gptq(w, shape)
+    else:
+        w = synth.fp16_decoder(shape, seed=seed, num_layers=n_layers)
+        model = Qwen2LLM.from_fp16(w, shape, gpu, max_pos=1024)
+        orc = oracle_from_fp16(w, shape)
+    n = len(lengths)
+    pool = PreallocatedKVCache(n_layers, n + 1, 2, 512, 128, gpu, n_heads=12)
+    kp, vp = _fill_pool(pool, lengths, seed + 7)
+    delta = torch.zeros(n + 1, dtype=torch.int64)
+    delta[:n] = torch.arange(n) % 5 - 2
+    ids = synth.random_ids(n, shape.vocab_size, seed, "ids")
+    dg, ig = delta.to(gpu), ids.to(gpu)
+    out = torch.empty(n, dtype=torch.int64, device=gpu)
+    logits = torch.empty(n, shape.vocab_size, dtype=torch.float16, device=gpu)
+    model.decode_greedy(ig, pool.view(n, dg), out, logits)
+    torch.cuda.synchronize()
+    lens = torch.tensor(lengths + [0], dtype=torch.int64)
+    exp = orc.decode_step(ids.tolist(), kp, vp, lens, delta)
+    err, cos = compare_logits(logits, exp)
+    decisive = check_ids(out, exp, err)
+    assert torch.equal(out.cpu(), logits.float().cpu().argmax(-1))
+    # the K/V rows written this step match the oracle's (fp16 outputs of qkv GEMM + rope),
+    # to the same accumulated-fp16 tolerance as the logits, relative to the row magnitude
+    for l in (0, n_layers - 1):
+        for b, L in enumerate(lengths):
+            for got_row, exp_row in ((pool.k[l][b, L], kp[l][b, L]), (pool.v[l][b, L], vp[l][b, L])):
+                d = (got_row.float().cpu() - exp_row).abs().max().item()
+                assert d <= 1e-2 * max(1.0, exp_row.abs().max().item()), (l, b, d)
+    say(f"  max-abs {err:.2e} cos {cos:.6f} decisive rows {decisive}/{n}")
+
+
+@pytest.mark.parametrize("lengths", [[37], [37, 100, 5], [255] * 16])
+def test_decode_step_fp16(gpu, lengths):
+    say(f"decode step fp16 4 layers lengths={lengths[:4]}.. n={len(lengths)}")
+    _decode_once(gpu, None, 4, lengths, 3)
+
+
+@pytest.mark.parametrize("n", [1, 8, 32])
+def test_decode_step_gptq(gpu, n):
+    say(f"decode step gptq 4 layers n={n}")
+    lengths = [(37 * (b + 1)) % 400 + 1 for b in range(n)]
+    _decode_once(gpu, "gptq", 4, lengths, 4)
+
+
+def _greedy_oracle(orc, prompts, steps, max_len):
+    """Free-running greedy generation with the oracle: packed prefill then decode."""
+    cfg = orc.cfg
+    P = len(prompts)
+    kp = [torch.zeros(P + 1, max_len, cfg.num_kv_heads, cfg.head_dim) for _ in orc.layers]
+    vp = [torch.zeros_like(k) for k in kp]
+    lengths = torch.zeros(P + 1, dtype=torch.int64)
+    emb = torch.cat([orc.embed[torch.tensor(p)] for p in prompts], 0)
+    pos = torch.cat([torch.arange(len(p)).view(1, -1).expand(3, -1) for p in prompts], 1)
+    logits = orc.prefill(emb, pos, [len(p) for p in prompts], list(range(P)), kp, vp, lengths)
+    toks = [[t] for t in ref.greedy(logits)]
+    margins = [[m] for m in ref.top2_margin(logits).tolist()]
+    for _ in range(steps):
+        lg = orc.decode_step([t[-1] for t in toks], kp, vp, lengths)
+        lengths[:P] += 1
+        for b, (t, m) in enumerate(zip(ref.greedy(lg), ref.top2_margin(lg).tolist())):
+            toks[b].append(t)
+            margins[b].append(m)
+    return toks, margins
+
+
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_runner_greedy_matches_oracle(gpu, use_graph):
+    """NativeQwenVLRunner prefill + decode (eager and hipGraph) vs oracle greedy."""
+    from omniserve_amd import synth
+    from omniserve_amd.request import Request, SamplingParams, Sequence
+    from omniserve_amd.runner import NativeQwenVLRunner
+    say(f"runner greedy fp16 3 layers use_graph={use_graph}")
+    shape = synth.DecoderShape()
+    w = synth.fp16_decoder(shape, seed=5, num_layers=3)
+    prompts = [synth.random_ids(40, shape.vocab_size, 5, "p0").tolist(),
+               synth.random_ids(17, shape.vocab_size, 5, "p1").tolist()]
+    steps = 6
+    runner = NativeQwenVLRunner(max_running=4, max_len=256, use_graph=use_graph, weights=w)
+    seqs = [Sequence(Request(prompt=p, sampling=SamplingParams(max_new_tokens=steps + 1)))
+            for p in prompts]
+    for s in seqs:
+        runner.tokenize(s)
+    runner.prefill(seqs)
+    for _ in range(steps):
+        runner.decode(seqs)
+    got = [s.output_token_ids for s in seqs]
+    exp, margins = _greedy_oracle(oracle_from_fp16(w, shape), prompts, steps, 256)
+    for b in range(len(prompts)):
+        for i, (g, e, m) in enumerate(zip(got[b], exp[b], margins[b])):
+            if m < 0.05:      # oracle near-tie: later tokens may legitimately diverge
+                break
+            assert g == e, f"seq {b} token {i}: got {g} want {e} (margin {m:.3f})"
+
+
+def test_graph_equals_eager_with_compaction(gpu):
+    """hipGraph replay and eager decode give identical tokens, including after a
+    sequence finishes and the pool is compacted (free -> move last slot)."""
+    from omniserve_amd import synth
+    from omniserve_amd.request import Request, SamplingParams, Sequence, Status
+    from omniserve_amd.runner import NativeQwenVLRunner
+    say("graph vs eager with compaction (gptq, 2 layers)")
+    shape = synth.DecoderShape()
+    w = synth.gptq_decoder(shape, seed=6, num_layers=2)
+    prompts = [synth.random_ids(L, shape.vocab_size, 6, f"q{L}").tolist() for L in (9, 30, 21)]
+    budgets = [2, 7, 5]
+    streams = []
+    for use_graph in (False, True):
+        r = NativeQwenVLRunner(max_running=4, max_len=128, use_graph=use_graph, weights=w,
+                               quant="gptq")
+        seqs = [Sequence(Request(prompt=p, sampling=SamplingParams(max_new_tokens=m)))
+                for p, m in zip(prompts, budgets)]
+        for s in seqs:
+            r.tokenize(s)
+        r.prefill(seqs)
+        running = [s for s in seqs if s.status != Status.FINISHED]
+        while running:
+            r.decode(running)
+            for s in list(running):
+                if s.status == Status.FINISHED:
+                    r.free(s)
+                    running.remove(s)
+        streams.append([s.output_token_ids for s in seqs])
+    assert streams[0] == streams[1]
+    assert [len(t) for t in streams[0]] == budgets
+
+
+def test_multimodal_prefill_positions_and_logits(gpu):
+    """Packed prefill of image+text prompts: M-RoPE ids equal the oracle's; logits at the
+    segment ends and the pool contents match the oracle."""
+    from omniserve_amd import synth
+    from omniserve_amd.kv_cache import PreallocatedKVCache
+    from omniserve_amd.positions import IMAGE_TOKEN_ID, mrope_positions
+    from omniserve_amd.qwen2_llm import Qwen2LLM
+    say("multimodal packed prefill (gptq, 2 layers)")
+    shape = synth.DecoderShape()
+    w = synth.gptq_decoder(shape, seed=8, num_layers=2)
+    model = Qwen2LLM.from_gptq(w, shape, gpu, max_pos=1024)
+    orc = oracle_from_gptq(w, shape)
+    segs, pos_all, emb_all = [], [], []
+    for s in range(2):
+        text_a = synth.random_ids(8 + s, shape.vocab_size, 8, f"a{s}").tolist()
+        text_b = synth.random_ids(6, shape.vocab_size, 8, f"b{s}").tolist()
+        ids = text_a + [IMAGE_TOKEN_ID] * 16 + text_b          # grid (1, 8, 8) -> 16 rows
+        vis = synth.randn16((16, shape.hidden_size), 1.0, 8, f"vis{s}")
+        pos, delta = mrope_positions(ids, [(1, 8, 8)])
+        epos, edelta = ref.mrope_position_ids(ids, [(1, 8, 8)])
+        assert torch.equal(pos, epos) and delta == edelta
+        emb = w["embed"][torch.tensor(ids)].clone()
+        emb[torch.tensor(ids) == IMAGE_TOKEN_ID] = vis
+        segs.append(len(ids))
+        pos_all.append(pos)
+        emb_all.append(emb)
+    emb = torch.cat(emb_all, 0)
+    pos = torch.cat(pos_all, 1)
+    pool = PreallocatedKVCache(2, 3, 2, 128, 128, gpu, n_heads=12)
+    cache = pool.packed_prefill_cache([0, 1], segs)
+    last = (torch.tensor(segs).cumsum(0) - 1).tolist()
+    eg, pg = emb.to(gpu).unsqueeze(0), pos.to(gpu).unsqueeze(1)
+    logits = model(eg, pg, None, cache, logits_indices=last)[0]
+    torch.cuda.synchronize()
+    kp = [torch.zeros(3, 128, 2, 128) for _ in range(2)]
+    vp = [torch.zeros(3, 128, 2, 128) for _ in range(2)]
+    lens = torch.zeros(3, dtype=torch.int64)
+    exp = orc.prefill(emb.float(), pos, segs, [0, 1], kp, vp, lens)
+    err, cos = compare_logits(logits, exp)
+    check_ids(logits.float().cpu().argmax(-1), exp, err)
+    assert pool.lengths.cpu()[:2].tolist() == segs
+    for l in range(2):
+        for s, L in enumerate(segs):
+            assert (pool.k[l][s, :L].float().cpu() - kp[l][s, :L]).abs().max().item() <= 2e-2
+            assert (pool.v[l][s, :L].float().cpu() - vp[l][s, :L]).abs().max().item() <= 2e-2
+    say(f"  max-abs {err:.2e} cos {cos:.6f}")
+
+
+@pytest.mark.slow
+def test_full_depth_decode_fp16(gpu):
+    """All 28 layers at the real width: one decode step, B=2, contexts 300 and 400.
+
+    Tolerance at full depth: with random N(0,0.02) weights the fp16 storage roundings
+    alone move the logits ~0.02 from the exact result after 28 layers (the oracle's
+    fp16-faithful mode vs its fp32 mode measures this on the same inputs), and two fp16
+    implementations that round attention probabilities differently (this kernel and the
+    reference's flash path round P to fp16; the SDPA-form oracle does not) differ by the
+    same order.  So the bar is: cosine >= 0.9999 against both oracle modes, and the GPU's
+    distance from the exact fp32 result within max(2e-2, 1.25 x the fp16 oracle's own
+    distance from it); argmax equal on decisive rows."""
+    from omniserve_amd import synth
+    from omniserve_amd.kv_cache import PreallocatedKVCache
+    from omniserve_amd.qwen2_llm import Qwen2LLM
+    say("full-depth (28 layers) fp16 decode step")
+    shape = synth.DecoderShape()
+    w = synth.fp16_decoder(shape, seed=9, num_layers=28)
+    lengths = [300, 400]
+    n = 2
+    pool = PreallocatedKVCache(28, 3, 2, 512, 128, gpu, n_heads=12)
+    kp, vp = _fill_pool(pool, lengths, 16)
+    model = Qwen2LLM.from_fp16(w, shape, gpu, max_pos=1024)
+    ids = synth.random_ids(n, shape.vocab_size, 9, "ids")
+    ig = ids.to(gpu)
+    out = torch.empty(n, dtype=torch.int64, device=gpu)
+    logits = torch.empty(n, shape.vocab_size, dtype=torch.float16, device=gpu)
+    model.decode_greedy(ig, pool.view(n, None), out, logits)
+    torch.cuda.synchronize()
+    lens = torch.tensor(lengths + [0])
+    e16 = oracle_from_fp16(w, shape, f16=True).decode_step(
+        ids.tolist(), [k.clone() for k in kp], [v.clone() for v in vp], lens.clone())
+    e32 = oracle_from_fp16(w, shape, f16=False).decode_step(ids.tolist(), kp, vp, lens.clone())
+    got = logits.float().cpu()
+    noise = (e16 - e32).abs().max().item()
+    d32 = (got - e32).abs().max().item()
+    d16 = (got - e16).abs().max().item()
+    cos = lambda a, b: torch.nn.functional.cosine_similarity(a, b, dim=-1).min().item()
+    say(f"  gpu-f16oracle {d16:.4f} gpu-f32oracle {d32:.4f} f16oracle-f32oracle {noise:.4f}")
+    assert cos(got, e16) >= 0.9999 and cos(got, e32) >= 0.9999
+    assert d32 <= max(2e-2, 1.25 * noise), (d32, noise)
+    check_ids(out, e32, max(d32, d16))

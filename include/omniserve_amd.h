@@ -1,0 +1,181 @@
+/*
+ * omniserve_amd: C ABI of the MI355X (gfx950) kernels behind the Qwen2-VL text-decoder
+ * token loop.  Every entry point takes device pointers, sizes and a hipStream_t (as
+ * void*), allocates nothing, never synchronises, and returns
+ *     0   success
+ *    -1   invalid argument (OMNI_EINVAL)
+ *    -2   shape outside what the kernel supports (OMNI_EUNSUPPORTED)
+ *   >0    hipError_t of the launch.
+ * All calls are capturable in a HIP graph.  Calls on one stream that share a
+ * workspace must not overlap (they are stream-ordered when issued on one stream).
+ *
+ * Reference paths below are relative to the omniserve repository.
+ */
+#ifndef OMNISERVE_AMD_H
+#define OMNISERVE_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- norms / elementwise */
+
+/* rms_norm (kernels/fused_ops.py:32-39): y = fp16(x * rsqrt(mean(x^2) + eps) * w).
+ * x, y: fp16 [rows, hidden]; weight fp16 [hidden]; hidden % 8 == 0, <= 8192. */
+int omni_rmsnorm(const void* x, const void* weight, void* y, int rows, int hidden, float eps,
+                 void* stream);
+
+/* add_rms_norm (kernels/fused_ops.py:60-70): residual_out = fp16(residual + x),
+ * y = rms_norm(residual_out).  residual_out may alias residual, y may alias x. */
+int omni_add_rmsnorm(const void* x, const void* residual, const void* weight, void* y,
+                     void* residual_out, int rows, int hidden, float eps, void* stream);
+
+/* add_rms_norm with x = fp16(sum over nparts of fp32 partials [nparts][rows][hidden],
+ * added in slice order): consumes the split-K output of omni_w4a16_gemm/omni_f16_gemm
+ * (EPI_PARTIAL) of the reference's o_proj / down_proj (model/qwen2_llm.py:99, 134)
+ * followed by the next add_rms_norm (qwen2_llm.py:151, 153, 186). */
+int omni_add_rmsnorm_partials(const float* partials, int nparts, const void* residual,
+                              const void* weight, void* y, void* residual_out, int rows,
+                              int hidden, float eps, void* stream);
+
+/* add_rms_norm_fp8 (kernels/fused_ops.py:94-107): as add_rmsnorm, the normed row
+ * quantised to e4m3fn with s = max(amax/448, 1e-12): y_fp8 = e4m3(y32 / s), scale[row] = s. */
+int omni_add_rmsnorm_fp8(const void* x, const void* residual, const void* weight, void* y_fp8,
+                         float* scale, void* residual_out, int rows, int hidden, float eps,
+                         void* stream);
+
+/* Layer-0 input of a decode step (models/qwen2_vl.py:93-94 + qwen2_llm.py:148-150):
+ * residual_out = table[ids], y = rms_norm(residual_out).  table fp16 [vocab, hidden], or
+ * the packed lm_head layout when table_packed (see omni_f16_pack). */
+int omni_embed_rmsnorm(const int64_t* ids, const void* table, int table_packed, int64_t vocab,
+                       const void* weight, void* y, void* residual_out, int rows, int hidden,
+                       float eps, void* stream);
+
+/* embed_tokens (models/qwen2_vl.py:93-94): out[t] = table[ids[t]] (ids clamped to range). */
+int omni_embedding(const int64_t* ids, const void* table, int table_packed, int64_t vocab,
+                   void* out, int rows, int hidden, void* stream);
+
+/* silu_mul (kernels/fused_ops.py:122-130): gate_up fp16 [rows, 2n] (gate first) ->
+ * out fp16 [rows, n] = silu(g) * u in fp32. */
+int omni_silu_mul(const void* gate_up, void* out, int rows, int n, void* stream);
+
+/* ---------------------------------------------------------------- rope + KV pool */
+
+/* apply_mrope (model/qwen2_llm.py:59-72) in place on the q and k heads of qkv rows
+ * [T, qkv_stride] fp16 (q | k | v), fused with _CacheView._write_kv
+ * (cache/kv_prealloc.py:253-261): rotated K and raw V of token t go to
+ * k/v_cache[slot, wpos] ([pool_rows, max_len, n_kv, 128] fp16).
+ *   positions  int64 [3, T] (t/h/w), or NULL: base_pos[slot] + rope_delta[slot] on all
+ *              axes (decode, models/qwen2_vl.py:108-112)
+ *   write_pos  int64 [T], or NULL: base_pos[slot];  slots int64 [T] or NULL (= t)
+ *   cos/sin    fp16 [max_pos, 64] of p * inv_freq (qwen2_llm.py:169-177, 181)
+ *   k_cache/v_cache NULL: rotate only.  Sections (sec0, sec1, sec2) = [16, 24, 24]. */
+int omni_mrope_kv_write(void* qkv, int qkv_stride, const int64_t* positions,
+                        const int64_t* base_pos, const int64_t* rope_delta, const void* cos_tab,
+                        const void* sin_tab, int max_pos, void* k_cache, void* v_cache,
+                        const int64_t* slots, const int64_t* write_pos, int pool_rows, int max_len,
+                        int T, int n_heads, int n_kv_heads, int head_dim, int sec0, int sec1,
+                        int sec2, void* stream);
+
+/* omni_mrope_kv_write with the qkv rows formed from the qkv projection's fp32 split-K
+ * partials [nparts][T][qkv_stride] plus bias (qwen2_llm.py:88: qkv_proj with bias;
+ * bias_after_round = 1 adds it after the fp16 rounding as the GPTQ path does,
+ * kernels/marlin_linear.py:59-62); the rows are written to qkv. */
+int omni_mrope_kv_write_partials(void* qkv, int qkv_stride, const float* partials, int nparts,
+                                 const void* bias, int bias_after_round, const int64_t* positions,
+                                 const int64_t* base_pos, const int64_t* rope_delta,
+                                 const void* cos_tab, const void* sin_tab, int max_pos,
+                                 void* k_cache, void* v_cache, const int64_t* slots,
+                                 const int64_t* write_pos, int pool_rows, int max_len, int T,
+                                 int n_heads, int n_kv_heads, int head_dim, int sec0, int sec1,
+                                 int sec2, void* stream);
+
+/* ---------------------------------------------------------------- attention */
+
+/* _CacheView.flash_decode (cache/kv_prealloc.py:272-290): GQA decode attention over the
+ * pool.  Token t (pool row slots[t], or t) attends to keys [0, L), L = kv_len[kv_by_slot ?
+ * slot : t] + kv_add; out fp16 [T, n_heads, 128].  waves in {4, 8, 16} per workgroup;
+ * splits workgroups per (token, kv head) (1..64): splits > 1 writes partial softmax
+ * states to workspace (fp32, >= T * n_kv * splits * (n_heads/n_kv) * 130) and merges them
+ * in a second launch. */
+int omni_decode_attention(const void* q, int q_stride, const void* k_cache, const void* v_cache,
+                          int pool_rows, int max_len, const int64_t* slots, const int64_t* kv_len,
+                          int kv_by_slot, int kv_add, void* out, int T, int n_heads,
+                          int n_kv_heads, int head_dim, float scale, int waves, int splits,
+                          float* workspace, void* stream);
+
+/* _PackedPrefillWriter.flash_prefill (cache/kv_prealloc.py:181-203) and the append form
+ * of :149-174: token t attends causally to keys [0, kv_len[t]) of pool row slots[t].
+ * qblocks int32 [nqb][2] = (first token, count <= 16) of consecutive tokens of one
+ * segment.  out fp16 rows of out_stride elements. */
+int omni_prefill_attention(const void* q, int q_stride, const void* k_cache, const void* v_cache,
+                           int pool_rows, int max_len, const int64_t* slots, const int64_t* kv_len,
+                           const int* qblocks, int nqb, void* out, int out_stride, int n_heads,
+                           int n_kv_heads, int head_dim, float scale, void* stream);
+
+/* ---------------------------------------------------------------- linears */
+
+/* Epilogues of the skinny GEMMs. */
+#define OMNI_EPI_STORE 0   /* fp16 out (+ bias) */
+#define OMNI_EPI_SILU 1    /* gate_up: fp16 silu(gate) * up, out [M, N/2] (interleave_halves pack) */
+#define OMNI_EPI_PARTIAL 2 /* fp32 split-K partial sums [slices][M][N], no bias */
+
+/* GPTQMarlinLinear.forward (kernels/marlin_linear.py:54-62, 83-96): y = fp16(x . W), W =
+ * fp16((q - 8) * s), bias added after the fp16 rounding when bias_after_round.  x fp16
+ * [M <= 64, K] (row stride ldx); weights from omni_gptq_repack.  ksplit > 1 only with
+ * OMNI_EPI_PARTIAL (slices = omni_gemm_slices(K, ksplit)).  preset selects the
+ * workgroup shape (0..3). */
+int omni_w4a16_gemm(const void* x, int ldx, const void* qweight_packed, const void* scales_packed,
+                    const void* bias, int bias_after_round, void* out, int ldo, float* partial,
+                    int M, int N, int K, int epilogue, int ksplit, int preset, void* stream);
+
+/* fp16 nn.Linear (model/qwen2_llm.py:82-83, 120-121): y = fp16(x . W^T + b), weights from
+ * omni_f16_pack.  Same epilogues / split rules as omni_w4a16_gemm. */
+int omni_f16_gemm(const void* x, int ldx, const void* weight_packed, const void* bias, void* out,
+                  int ldo, float* partial, int M, int N, int K, int epilogue, int ksplit,
+                  int preset, void* stream);
+
+/* Number of K slices (whole 128-groups) a split of ksplit gives for K. */
+int omni_gemm_slices(int K, int ksplit);
+
+/* load_gptq_llm / gptq_marlin_repack (kernels/marlin_linear.py:94-95, 114-143): AutoGPTQ
+ * qweight int32 [K/8, N] + scales fp16 [K/128, N] -> this library's packed int4 layout
+ * (qweight_packed int32 [N/16][K/128][64][4], scales_packed fp16 [N/16][K/128][16]).
+ * interleave_halves: column tiles of the two halves of N interleaved (fused gate|up,
+ * marlin_linear.py:130-139) for OMNI_EPI_SILU. */
+int omni_gptq_repack(const int32_t* qweight, const void* scales, int32_t* qweight_packed,
+                     void* scales_packed, int K, int N, int interleave_halves, void* stream);
+
+/* fp16 weight [N, K] (nn.Linear layout) -> packed [N/16][K/32][64][8]. */
+int omni_f16_pack(const void* weight, void* weight_packed, int K, int N, int interleave_halves,
+                  void* stream);
+
+/* Packed int4 -> dense W^T [K, N] fp16 with W = fp16((q - 8) * s): the reference's
+ * dequantised weight (verification / load-time use). */
+int omni_w4_dequant(const int32_t* qweight_packed, const void* scales_packed, void* w, int K,
+                    int N, void* stream);
+
+/* ---------------------------------------------------------------- lm_head + greedy */
+
+/* Workgroups (= candidate rows per token) of omni_lmhead_candidates for vocab N. */
+int omni_lmhead_argmax_grid(int N);
+
+/* Tied lm_head (model/qwen2_llm.py:167-168, 190) with the greedy argmax of
+ * runners/multimodal.py:306-310: per workgroup and row the max fp16 logit and its lowest
+ * index go to cand_val/cand_idx ([grid][M]); logits_out fp16 [M, N] optional. */
+int omni_lmhead_candidates(const void* x, int ldx, const void* weight_packed, int M, int N, int K,
+                           void* logits_out, float* cand_val, int* cand_idx, void* stream);
+
+/* ids_out[m] = argmax over the candidates (lowest index on ties, torch.argmax semantics);
+ * optionally next_ids[m] = ids_out[m] and lengths[m] += 1 (the decode step's
+ * bookkeeping, runners/multimodal.py:355-356). */
+int omni_argmax_finalize(const float* cand_val, const int* cand_idx, int nblk, int M,
+                         int64_t* ids_out, int64_t* next_ids, int64_t* lengths, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OMNISERVE_AMD_H */

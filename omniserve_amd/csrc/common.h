@@ -7,6 +7,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "omniserve_amd.h"
+
 #define OMNI_WAVE 64
 
 typedef _Float16 half_t;

@@ -1,0 +1,82 @@
+"""The C-ABI library: loads without a GPU, exports exactly what include/omniserve_amd.h
+declares, the ctypes table matches the header's parameter counts, and argument
+validation rejects bad shapes before any HIP call (safe to exercise on the CPU)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "omniserve_amd.h"
+
+
+def header_decls():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    decls = {}
+    for m in re.finditer(r"\bint\s+(omni_\w+)\s*\(([^)]*)\)\s*;", text, flags=re.S):
+        params = [p.strip() for p in m.group(2).split(",") if p.strip()]
+        decls[m.group(1)] = params
+    return decls
+
+
+@pytest.fixture(scope="module")
+def so():
+    from omniserve_amd._lib import LIB_PATH
+    if not LIB_PATH.exists():
+        pytest.fail("HIP library not built: run python -m omniserve_amd.build")
+    return ctypes.CDLL(str(LIB_PATH))
+
+
+def test_header_declares_entry_points():
+    decls = header_decls()
+    assert len(decls) >= 20
+    assert "omni_decode_attention" in decls and "omni_w4a16_gemm" in decls
+
+
+def test_library_exports_every_declared_symbol(so):
+    for name in header_decls():
+        assert hasattr(so, name), f"{name} declared in the header but not exported"
+
+
+def test_ctypes_table_matches_header():
+    from omniserve_amd._lib import SIGNATURES
+    decls = header_decls()
+    assert set(SIGNATURES) == set(decls)
+    for name, params in decls.items():
+        assert len(SIGNATURES[name]) == len(params), name
+
+
+def test_bad_arguments_rejected_before_launch(so):
+    from omniserve_amd._lib import lib
+    L = lib()
+    # unsupported hidden size / negative rows
+    assert L.omni_rmsnorm(None, None, None, 4, 7, 1e-6, None) == -2
+    assert L.omni_rmsnorm(None, None, None, -1, 1536, 1e-6, None) == -1
+    # null pointers with real work
+    assert L.omni_add_rmsnorm(None, None, None, None, None, 4, 1536, 1e-6, None) == -1
+    # attention: bad waves / head_dim / splits
+    assert L.omni_decode_attention(None, 1536, None, None, 1, 16, None, None, 0, 0, None, 1, 12,
+                                   2, 128, 0.1, 3, 1, None, None) == -1
+    assert L.omni_decode_attention(None, 1536, None, None, 1, 16, None, None, 0, 0, None, 1, 12,
+                                   2, 64, 0.1, 4, 1, None, None) == -2
+    assert L.omni_decode_attention(None, 1536, None, None, 1, 16, None, None, 0, 0, None, 1, 12,
+                                   2, 128, 0.1, 4, 0, None, None) == -1
+    # skinny GEMM: too many rows, K not a multiple of 128, split without partial epilogue
+    assert L.omni_w4a16_gemm(None, 1536, None, None, None, 1, None, 2048, None, 65, 2048, 1536,
+                             0, 1, 2, None) == -2
+    assert L.omni_w4a16_gemm(None, 1536, None, None, None, 1, None, 2048, None, 32, 2048, 1500,
+                             0, 1, 2, None) == -2
+    fake = ctypes.c_void_p(16)   # never dereferenced: validation fails first
+    assert L.omni_f16_gemm(fake, 1536, fake, None, fake, 2048, None, 32, 2048, 1536, 0, 4, 2,
+                           None) == -1
+    # rope: head_dim / sections
+    assert L.omni_mrope_kv_write(None, 2048, None, None, None, None, None, 16, None, None, None,
+                                 None, 1, 16, 1, 12, 2, 64, 16, 24, 24, None) == -2
+    assert L.omni_mrope_kv_write(None, 2048, None, None, None, None, None, 16, None, None, None,
+                                 None, 1, 16, 1, 12, 2, 128, 16, 24, 20, None) == -2
+    # zero-size work is a no-op success
+    assert L.omni_silu_mul(None, None, 0, 8960, None) == 0
+    assert L.omni_gemm_slices(8960, 10) == 10 and L.omni_gemm_slices(1536, 7) == 6

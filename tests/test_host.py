@@ -1,0 +1,210 @@
+"""Host-side logic on the CPU: packed weight layouts (emulated in numpy and checked against
+the oracle's dequantisation), the device fp32->e4m3fn conversion (compiled for the host and
+compared with torch on every representable neighbourhood), launch plans, query blocks,
+the caller-side Sequence contract and a StubRunner engine loop, and bench byte counts."""
+
+import os
+import shutil
+import subprocess
+import tempfile
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import qwen2_ref as ref
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+# ----------------------------------------------------------------------------- layouts
+def emulate_gptq_repack_dequant(qweight: np.ndarray, scales: np.ndarray) -> np.ndarray:
+    """numpy restatement of the packed int4 layout + dequant8 -> W^T [K, N] fp16.
+
+    packed word (tile nt, group kg, lane l, j): column 16*nt + l%16, k = 128*kg + 32*j +
+    8*(l//16) + e; code e at bit 2e (e even) / 16 + 2(e-1) (e odd); dequant: the fp16 of
+    ((w >> 4r) & 0x000F000F) | 0x64006400 minus 1032 times the group scale."""
+    K8, N = qweight.shape
+    K = K8 * 8
+    W = np.zeros((K, N), dtype=np.float16)
+    src = qweight.astype(np.int64) & 0xFFFFFFFF
+    for nt in range(N // 16):
+        for kg in range(K // 128):
+            for lane in range(64):
+                n = nt * 16 + lane % 16
+                for j in range(4):
+                    kb = kg * 128 + 32 * j + 8 * (lane // 16)
+                    s_word = int(src[kb // 8, n])
+                    word = 0
+                    for e in range(8):
+                        code = (s_word >> (4 * e)) & 0xF
+                        bit = 16 + 2 * (e - 1) if e & 1 else 2 * e
+                        word |= code << bit
+                    s = np.float16(scales[kg, n])
+                    for r in range(4):
+                        t = ((word >> (4 * r)) & 0x000F000F) | 0x64006400
+                        lo = np.array([t & 0xFFFF], dtype=np.uint16).view(np.float16)[0]
+                        hi = np.array([t >> 16], dtype=np.uint16).view(np.float16)[0]
+                        for e_, h in ((2 * r, lo), (2 * r + 1, hi)):
+                            v = np.float16(np.float16(h - np.float16(1032)) * s)
+                            W[kb + e_, n] = v
+    return W
+
+
+def test_packed_int4_layout_reproduces_reference_dequant():
+    from omniserve_amd.synth import gptq_random
+    K, N = 256, 32
+    qw, sc = gptq_random(K, N, 5, "layout")
+    W = emulate_gptq_repack_dequant(qw.numpy(), sc.numpy())
+    assert np.array_equal(W.astype(np.float32), ref.gptq_dequant(qw, sc).numpy())
+
+
+def test_packed_fp16_offset_formula():
+    """Element (n, k) of the packed fp16 table (gather in norm.hip) sits at
+    (((n//16)*(K//32) + k//32)*64 + n%16 + 16*((k%32)//8))*8 + k%8 = where f16_pack puts it."""
+    N, K = 32, 64
+    w = np.arange(N * K).reshape(N, K)
+    packed = np.zeros(N * K, dtype=np.int64)
+    for nt in range(N // 16):
+        for ks in range(K // 32):
+            for lane in range(64):
+                n = nt * 16 + lane % 16
+                k = ks * 32 + 8 * (lane // 16)
+                base = ((nt * (K // 32) + ks) * 64 + lane) * 8
+                packed[base:base + 8] = w[n, k:k + 8]
+    for n in (0, 5, 17, 31):
+        for k in (0, 7, 8, 31, 32, 63):
+            off = (((n // 16) * (K // 32) + k // 32) * 64 + n % 16 + 16 * ((k % 32) // 8)) * 8 + k % 8
+            assert packed[off] == w[n, k]
+
+
+# ----------------------------------------------------------------------------- e4m3fn
+E4M3_SRC = r"""
+#include "common.h"
+#include <cstdio>
+#include <cstring>
+int main(int argc, char** argv) {
+  FILE* fi = fopen(argv[1], "rb"); FILE* fo = fopen(argv[2], "wb");
+  float f;
+  while (fread(&f, 4, 1, fi) == 1) { unsigned char c = f32_to_e4m3fn(f); fwrite(&c, 1, 1, fo); }
+  fclose(fi); fclose(fo); return 0;
+}
+"""
+
+
+@pytest.mark.skipif(shutil.which("hipcc") is None and not os.path.exists("/opt/rocm/bin/hipcc"),
+                    reason="hipcc not available")
+def test_device_e4m3_conversion_matches_torch():
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    with tempfile.TemporaryDirectory() as d:
+        src = Path(d) / "e4m3.cpp"
+        src.write_text(E4M3_SRC)
+        exe = Path(d) / "e4m3"
+        r = subprocess.run([hipcc, "--offload-arch=gfx950", "-O1",
+                            f"-I{ROOT / 'omniserve_amd/csrc'}", f"-I{ROOT / 'include'}", str(src),
+                            "-o", str(exe)], capture_output=True, text=True)
+        if r.returncode != 0:
+            pytest.skip(f"host build failed: {r.stderr[:300]}")
+        # every e4m3 value, the midpoints between neighbours (ties), and random values
+        codes = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float()
+        finite = codes[torch.isfinite(codes)].unique().sort().values
+        mids = (finite[1:] + finite[:-1]) / 2
+        g = torch.Generator().manual_seed(3)
+        rnd = torch.randn(20000, generator=g) * torch.exp(torch.randn(20000, generator=g) * 3)
+        vals = torch.cat([finite, mids, mids.nextafter(torch.tensor(1e9)),
+                          mids.nextafter(torch.tensor(-1e9)), rnd.clamp(-460, 460),
+                          torch.tensor([0.0, -0.0, 2.0 ** -10, 2.0 ** -9 * 0.5, 447.9, 448.0,
+                                        463.9, -463.9])])
+        fi, fo = Path(d) / "in.bin", Path(d) / "out.bin"
+        fi.write_bytes(vals.numpy().astype(np.float32).tobytes())
+        subprocess.run([str(exe), str(fi), str(fo)], check=True)
+        got = np.frombuffer(fo.read_bytes(), dtype=np.uint8)
+        want = vals.to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+        assert np.array_equal(got, want), np.nonzero(got != want)[0][:10]
+
+
+# ----------------------------------------------------------------------------- plans / blocks
+def test_query_blocks_cover_segments():
+    from omniserve_amd.attention import query_blocks
+    qb = query_blocks([5, 16, 17, 1], "cpu").tolist()
+    assert qb == [[0, 5], [5, 16], [21, 16], [37, 1], [38, 1]]
+
+
+def test_decode_plan_and_split_counts():
+    from omniserve_amd.kv_cache import MAX_ATTN_SPLITS, decode_plan
+    for n in (1, 8, 16, 32, 64):
+        for ctx in (64, 256, 1024, 4096):
+            w, s = decode_plan(n, 2, ctx)
+            assert w in (4, 8, 16) and 1 <= s <= MAX_ATTN_SPLITS
+    assert decode_plan(32, 2, 4096)[1] == 3
+    from omniserve_amd._lib import lib
+    assert lib().omni_gemm_slices(8960, 10) == 10
+    assert lib().omni_gemm_slices(1536, 10) == 6
+
+
+# ----------------------------------------------------------------------------- control plane
+def test_sequence_finish_rules():
+    from omniserve_amd.request import Request, SamplingParams, Sequence, Status
+    s = Sequence(Request(prompt=[1, 2], sampling=SamplingParams(max_new_tokens=3,
+                                                                stop_token_ids=[9])))
+    s.prompt_token_ids = [1, 2]
+    assert s.last_token_id() == 2
+    s.append_token(5)
+    assert not s.maybe_finish() and s.last_token_id() == 5
+    s.append_token(9)
+    assert s.maybe_finish() and s.status == Status.FINISHED
+    t = Sequence(Request(prompt=[1], sampling=SamplingParams(max_new_tokens=2)))
+    t.append_token(1)
+    t.append_token(2)
+    assert t.maybe_finish()
+
+
+def test_stub_runner_engine_loop():
+    """The reference's control-plane double (runners/base.py:60-91) driven like
+    LLMEngine.step: prefill new sequences, decode running ones, retire finished."""
+    from omniserve_amd.request import Request, SamplingParams, Sequence, Status
+    from omniserve_amd.runner import StubRunner
+    r = StubRunner("a b c")
+    seqs = [Sequence(Request(prompt="x y z", sampling=SamplingParams(max_new_tokens=n)))
+            for n in (1, 3, 5)]
+    for s in seqs:
+        r.tokenize(s)
+    r.prefill(seqs)
+    running = [s for s in seqs if s.status != Status.FINISHED]
+    steps = 0
+    while running:
+        r.decode(running)
+        running = [s for s in running if s.status != Status.FINISHED]
+        steps += 1
+    assert [s.output_token_ids for s in seqs] == [[0], [0, 1, 2], [0, 1, 2, 3, 4]]
+    assert steps == 4
+    assert r.detokenize(seqs[1], [0, 1, 2]) == "a b c "
+
+
+def test_synth_is_deterministic():
+    from omniserve_amd import synth
+    a = synth.gptq_random(256, 32, 7, "x")
+    b = synth.gptq_random(256, 32, 7, "x")
+    c = synth.gptq_random(256, 32, 7, "y")
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    assert not torch.equal(a[0], c[0])
+    codes = ref.gptq_unpack(a[0])
+    assert codes.min() >= 0 and codes.max() <= 15
+    assert (a[1] > 0).all()
+
+
+# ----------------------------------------------------------------------------- bench bytes
+def test_bench_byte_accounting_matches_published_floor():
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("bench", ROOT / "bench.py")
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    w4 = bench.weight_bytes("gptq")
+    assert abs(w4 / 1e9 - 1.143) < 0.005
+    w16 = bench.weight_bytes("fp16")
+    assert abs(w16 / 1e9 - 3.087) < 0.005
+    # config 3 averaged over its 128 steps (mean attended context ~2112): ~3.08 GB per step
+    assert abs(bench.step_bytes("gptq", [2111] * 32) / 1e9 - 3.08) < 0.01
+    # one attention launch: 32 x 2049 keys x (K+V) x 2 heads x 128 x 2 B + q/out
+    assert bench.attn_launch_bytes([2048] * 32) == 32 * 2049 * 1024 + 2 * 32 * 12 * 128 * 2

@@ -1,0 +1,305 @@
+"""Pins the CPU oracle (oracle/qwen2_ref.py) without trusting its own formulas.
+
+The reference ships no golden vectors, fixtures or known-answer tests for this path
+(its checks compare against HF weights on a CUDA GPU), so each oracle function is
+pinned by something independent of how it is written:
+
+  rms_norm / add_rms_norm   float64 numpy closed form; residual rounding = numpy fp16 add
+  add_rms_norm_fp8          scale closed form; dequantised codes within one e4m3 step;
+                            the row maximum maps to exactly +-448
+  silu_mul                  float64 numpy closed form
+  apply_mrope (t = h = w)   textbook RoPE as a complex rotation of (x_d, x_{d+64})
+  apply_mrope (3-D)         each section follows only its own axis (dims [0,16)+[64,80) ->
+                            t, [16,40)+[80,104) -> h, [40,64)+[104,128) -> w)
+  mrope_position_ids        text-only = arange / delta 0; BASELINE config-5 closed form
+                            (image t=64, h=w=64+0..15, text resumes at 80, delta -240);
+                            two images; product implementation equal
+  gptq pack/dequant         bit-level brute force with Python ints; round trip
+  decode_attention          float64 brute-force softmax loops
+  prefill_attention         brute force; last token of a segment == decode over it
+  fp8 linear                torch._scaled_mm (library GEMM) on the same fp8 operands
+  decode_step / prefill     append consistency: prefill(p[:L]) + decode(p[L]) gives the
+                            logits prefill(p[:L+1]) gives at its last position
+  greedy                    lowest index wins ties
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import qwen2_ref as ref
+
+
+def rnd(shape, seed, std=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g) * std
+
+
+# ----------------------------------------------------------------------------- norms
+def test_rms_norm_closed_form():
+    x = rnd((5, 64), 1).half().float()
+    w = (1 + 0.1 * rnd((64,), 2)).half().float()
+    y = ref.rms_norm(x, w, 1e-6, f16=False)
+    xn = x.double().numpy()
+    e = xn / np.sqrt((xn ** 2).mean(-1, keepdims=True) + 1e-6) * w.double().numpy()
+    assert np.abs(y.numpy() - e).max() < 1e-5
+
+
+def test_add_rms_norm_residual_is_fp16_sum():
+    x = rnd((4, 96), 3).half()
+    r = rnd((4, 96), 4).half()
+    _, nr = ref.add_rms_norm(x.float(), r.float(), torch.ones(96), 1e-6)
+    e = (x.numpy().astype(np.float16) + r.numpy().astype(np.float16)).astype(np.float32)
+    assert np.array_equal(nr.numpy(), e)
+
+
+def test_add_rms_norm_fp8():
+    x = rnd((6, 128), 5).half().float()
+    r = rnd((6, 128), 6).half().float()
+    q, s, nr = ref.add_rms_norm_fp8(x, r, torch.ones(128), 1e-6)
+    y = ref.rms_norm(nr, torch.ones(128), 1e-6, f16=False)
+    assert torch.allclose(s.view(-1), y.abs().amax(-1) / 448.0, rtol=1e-6)
+    deq = q.float() * s
+    assert ((deq - y).abs() <= 2.0 ** -4 * y.abs() + s * 2.0 ** -9).all()
+    assert (q.float().abs().amax(-1) == 448.0).all()
+
+
+def test_silu_mul_closed_form():
+    gu = rnd((3, 20), 7, 3.0)
+    y = ref.silu_mul(gu, f16=False).numpy()
+    g, u = gu[:, :10].double().numpy(), gu[:, 10:].double().numpy()
+    assert np.abs(y - g / (1 + np.exp(-g)) * u).max() < 1e-5
+
+
+# ----------------------------------------------------------------------------- rope
+def test_mrope_equals_textbook_rope_when_axes_agree():
+    cfg = ref.Qwen2Config()
+    T, nh = 7, 3
+    pos = torch.tensor([0, 1, 5, 100, 1023, 4000, 77])
+    q = rnd((1, nh, T, 128), 8)
+    k = rnd((1, 1, T, 128), 9)
+    cos, sin = ref.rope_cos_sin(pos.view(1, 1, T).expand(3, 1, T), cfg, f16=False)
+    qr, kr = ref.apply_mrope(q, k, cos, sin, cfg.mrope_section, f16=False)
+    inv = 1.0 / (1e6 ** (np.arange(0, 128, 2) / 128.0))
+    for x, xr in ((q, qr), (k, kr)):
+        xn = x.double().numpy()
+        z = xn[..., :64] + 1j * xn[..., 64:]
+        ang = pos.double().numpy()[:, None] * inv[None, :]
+        rot = z * np.exp(1j * ang)[None, None]
+        e = np.concatenate([rot.real, rot.imag], -1)
+        assert np.abs(xr.double().numpy() - e).max() < 2e-3   # fp32 angle rounding at p~4000
+
+
+def test_mrope_sections_follow_their_axis():
+    cfg = ref.Qwen2Config()
+    q = rnd((1, 1, 1, 128), 10)
+    k = rnd((1, 1, 1, 128), 11)
+    base = torch.tensor([10, 10, 10]).view(3, 1, 1)
+    c0, s0 = ref.rope_cos_sin(base, cfg, f16=False)
+    q0, _ = ref.apply_mrope(q, k, c0, s0, cfg.mrope_section, f16=False)
+    spans = {0: list(range(0, 16)) + list(range(64, 80)),
+             1: list(range(16, 40)) + list(range(80, 104)),
+             2: list(range(40, 64)) + list(range(104, 128))}
+    for axis in range(3):
+        p = base.clone()
+        p[axis] = 37
+        c, s = ref.rope_cos_sin(p, cfg, f16=False)
+        q1, _ = ref.apply_mrope(q, k, c, s, cfg.mrope_section, f16=False)
+        changed = set((q1 != q0).view(-1).nonzero().view(-1).tolist())
+        assert changed == set(spans[axis]), axis
+
+
+def test_mrope_positions_text_only():
+    pos, d = ref.mrope_position_ids(list(range(10)), [])
+    assert torch.equal(pos, torch.arange(10).view(1, -1).expand(3, -1)) and d == 0
+
+
+def test_mrope_positions_config5_closed_form():
+    ids = [5] * 64 + [151655] * 256 + [6] * 192
+    pos, d = ref.mrope_position_ids(ids, [(1, 32, 32)])
+    assert torch.equal(pos[:, :64], torch.arange(64).view(1, -1).expand(3, -1))
+    img = pos[:, 64:320]
+    assert (img[0] == 64).all()
+    assert torch.equal(img[1], 64 + torch.arange(16).repeat_interleave(16))
+    assert torch.equal(img[2], 64 + torch.arange(16).repeat(16))
+    assert torch.equal(pos[:, 320:], (80 + torch.arange(192)).view(1, -1).expand(3, -1))
+    assert d == 272 - 512 == -240
+
+
+def test_mrope_positions_two_images_and_product_agree():
+    from omniserve_amd.positions import mrope_positions
+    ids = [1, 2] + [151655] * 4 + [3] + [151655] * 9 + [4, 5]
+    grids = [(1, 4, 4), (1, 6, 6)]
+    pos, d = ref.mrope_position_ids(ids, grids)
+    # image 1 at positions 2..3, text at 4, image 2 at 5..7, text at 8, 9
+    assert pos[:, 6].tolist() == [4, 4, 4]
+    assert pos[:, 7:16].max().item() == 7
+    assert pos[:, 16:].tolist() == [[8, 9]] * 3 and d == 10 - 18
+    p2, d2 = mrope_positions(ids, grids)
+    assert torch.equal(pos, p2) and d == d2
+
+
+# ----------------------------------------------------------------------------- int4
+def test_gptq_pack_dequant_bit_level():
+    K, N = 256, 3
+    g = torch.Generator().manual_seed(12)
+    codes = torch.randint(0, 16, (K, N), generator=g)
+    qw = ref.gptq_pack(codes)
+    assert torch.equal(ref.gptq_unpack(qw), codes)
+    scales = (rnd((K // 128, N), 13).abs() * 0.003).half()
+    W = ref.gptq_dequant(qw, scales)
+    for k in (0, 1, 7, 8, 127, 128, 255):
+        for n in range(N):
+            word = int(qw[k // 8, n]) & 0xFFFFFFFF
+            q = (word >> (4 * (k % 8))) & 0xF
+            s = float(scales[k // 128, n])
+            e = float(np.float16(np.float32((q - 8)) * np.float32(s)))
+            assert float(W[k, n]) == e
+
+
+# ----------------------------------------------------------------------------- attention
+def _brute_attention(q, K, V, scale):
+    s = [sum(q[d] * K[j][d] for d in range(len(q))) * scale for j in range(len(K))]
+    m = max(s)
+    p = [math.exp(x - m) for x in s]
+    z = sum(p)
+    return [sum(p[j] * V[j][d] for j in range(len(K))) / z for d in range(len(V[0]))]
+
+
+def test_decode_attention_brute_force():
+    n, nh, nkv, hd, ML = 2, 4, 2, 8, 16
+    q = rnd((n, nh, hd), 14)
+    kp = rnd((3, ML, nkv, hd), 15)
+    vp = rnd((3, ML, nkv, hd), 16)
+    rows, L = torch.tensor([2, 0]), torch.tensor([5, 11])
+    out = ref.decode_attention(q, kp, vp, rows, L, 0.3, f16=False)
+    for b in range(n):
+        for h in range(nh):
+            g = h // (nh // nkv)
+            e = _brute_attention(q[b, h].tolist(), kp[rows[b], :L[b], g].tolist(),
+                                 vp[rows[b], :L[b], g].tolist(), 0.3)
+            assert np.allclose(out[b, h].numpy(), e, atol=1e-5)
+
+
+def test_prefill_attention_causal_and_consistent_with_decode():
+    nh, nkv, hd = 4, 2, 8
+    segs = [5, 3]
+    T = sum(segs)
+    q, k, v = rnd((T, nh, hd), 17), rnd((T, nkv, hd), 18), rnd((T, nkv, hd), 19)
+    out = ref.prefill_attention(q, k, v, segs, 0.25, f16=False)
+    # token 3 of segment 0 sees keys 0..3 only
+    for h in range(nh):
+        g = h // 2
+        e = _brute_attention(q[3, h].tolist(), k[:4, g].tolist(), v[:4, g].tolist(), 0.25)
+        assert np.allclose(out[3, h].numpy(), e, atol=1e-5)
+    # last token of segment 1 == decode attention over segment 1
+    kp = torch.zeros(1, 8, nkv, hd)
+    vp = torch.zeros(1, 8, nkv, hd)
+    kp[0, :3], vp[0, :3] = k[5:], v[5:]
+    d = ref.decode_attention(q[7:8], kp, vp, torch.tensor([0]), torch.tensor([3]), 0.25, f16=False)
+    assert torch.allclose(out[7], d[0], atol=1e-6)
+
+
+# ----------------------------------------------------------------------------- fp8
+def test_fp8_linear_matches_scaled_mm():
+    x = rnd((16, 64), 20).half().float()
+    w = rnd((32, 64), 21, 0.02).half().float()
+    wq, sw = ref.fp8_weight_rowwise(w)
+    xq, sa = ref.quant_fp8(x)
+    y = ref.fp8_linear_rowwise(xq, sa, wq, sw, out_f16=False)
+    # the library fp8 GEMM (per-tensor unit scales, fp32 out) on the same e4m3 operands,
+    # then the row / column scales and the bf16 rounding of the reference's epilogue
+    one = torch.tensor(1.0)
+    try:
+        acc = torch._scaled_mm(xq, wq.t(), scale_a=one, scale_b=one, out_dtype=torch.float32)
+    except (RuntimeError, NotImplementedError) as err:
+        pytest.skip(f"CPU _scaled_mm unavailable: {err}")
+    e = (acc * sa.view(-1, 1) * sw.view(1, -1)).to(torch.bfloat16).float()
+    assert torch.allclose(y, e, atol=0, rtol=2 ** -7)
+    # scales follow the closed forms
+    assert torch.allclose(sw, w.abs().amax(1) / 448.0)
+    assert torch.allclose(sa.view(-1), x.abs().amax(1) / 448.0)
+
+
+# ----------------------------------------------------------------------------- model
+def _tiny(f16=False, seed=22):
+    cfg = ref.Qwen2Config(hidden_size=256, num_layers=2, num_heads=2, num_kv_heads=1,
+                          head_dim=128, intermediate_size=384, vocab_size=500)
+    H, I = cfg.hidden_size, cfg.intermediate_size
+    qkv = (cfg.num_heads + 2 * cfg.num_kv_heads) * cfg.head_dim
+    layers = [ref.LayerWeights(
+        in_norm=torch.ones(H), post_norm=torch.ones(H),
+        qkv_t=rnd((H, qkv), seed + 10 * i, 0.05), qkv_b=rnd((qkv,), seed + 10 * i + 1, 0.05),
+        o_t=rnd((cfg.num_heads * cfg.head_dim, H), seed + 10 * i + 2, 0.05),
+        gate_up_t=rnd((H, 2 * I), seed + 10 * i + 3, 0.05),
+        down_t=rnd((I, H), seed + 10 * i + 4, 0.05)) for i in range(cfg.num_layers)]
+    return ref.Qwen2Ref(cfg, rnd((cfg.vocab_size, H), seed + 99, 0.05), torch.ones(H), layers,
+                        False, f16)
+
+
+def test_decode_after_prefill_equals_longer_prefill():
+    orc = _tiny()
+    cfg = orc.cfg
+    prompt = torch.randint(0, cfg.vocab_size, (13,), generator=torch.Generator().manual_seed(23))
+    L = 12
+
+    def pool():
+        return ([torch.zeros(2, 32, 1, 128) for _ in range(2)],
+                [torch.zeros(2, 32, 1, 128) for _ in range(2)], torch.zeros(2, dtype=torch.int64))
+
+    kp, vp, lens = pool()
+    orc.prefill(orc.embed[prompt[:L]], torch.arange(L).view(1, -1).expand(3, -1), [L], [0], kp, vp,
+                lens)
+    assert lens[0] == L
+    dec = orc.decode_step([int(prompt[L])], kp, vp, lens)
+    kp2, vp2, lens2 = pool()
+    full = orc.prefill(orc.embed[prompt], torch.arange(L + 1).view(1, -1).expand(3, -1), [L + 1],
+                       [0], kp2, vp2, lens2)
+    assert torch.allclose(dec, full, atol=1e-4)
+    # and the pools agree on the first L+1 positions
+    for l in range(2):
+        assert torch.allclose(kp[l][0, :L + 1], kp2[l][0, :L + 1], atol=1e-5)
+
+
+def test_packed_prefill_equals_separate_prefills():
+    orc = _tiny()
+    g = torch.Generator().manual_seed(24)
+    p1 = torch.randint(0, 500, (7,), generator=g)
+    p2 = torch.randint(0, 500, (4,), generator=g)
+
+    def run(prompts, slots):
+        kp = [torch.zeros(3, 16, 1, 128) for _ in range(2)]
+        vp = [torch.zeros(3, 16, 1, 128) for _ in range(2)]
+        lens = torch.zeros(3, dtype=torch.int64)
+        emb = torch.cat([orc.embed[p] for p in prompts])
+        pos = torch.cat([torch.arange(len(p)).view(1, -1).expand(3, -1) for p in prompts], 1)
+        return orc.prefill(emb, pos, [len(p) for p in prompts], slots, kp, vp, lens)
+
+    both = run([p1, p2], [0, 1])
+    assert torch.allclose(both[0], run([p1], [0])[0], atol=1e-5)
+    assert torch.allclose(both[1], run([p2], [1])[0], atol=1e-5)
+
+
+def test_greedy_lowest_index_on_ties():
+    lg = torch.tensor([[1.0, 3.0, 3.0, 2.0], [5.0, 5.0, 5.0, 5.0]])
+    assert ref.greedy(lg) == [1, 0]
+
+
+def test_golden_fixture_reproduced():
+    """The committed fixture (tests/golden/make_golden.py) is what the oracle computes."""
+    import json
+    import os
+    import sys
+    gdir = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+    sys.path.insert(0, gdir)
+    import make_golden
+    want = json.load(open(os.path.join(gdir, "decode_fp16_2layer.json")))
+    got = make_golden.generate()
+    assert got["prompts"] == want["prompts"]
+    for g, w in zip(got["steps"], want["steps"]):
+        for b in range(2):
+            if w["margin"][b] > 1e-3:
+                assert g["tokens"][b] == w["tokens"][b]
+        assert np.allclose(g["top5_logits"], w["top5_logits"], atol=1e-3)

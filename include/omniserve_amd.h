@@ -106,6 +106,20 @@ int omni_decode_attention(const void* q, int q_stride, const void* k_cache, cons
                           int n_kv_heads, int head_dim, float scale, int waves, int splits,
                           float* workspace, void* stream);
 
+/* The decode step's attention fused with its producer (model/qwen2_llm.py:88-99 for one
+ * decode token): q and the new k / v are formed from the qkv projection's fp32 split-K
+ * partials [nparts <= 16][T][(n_heads + 2 n_kv) * 128] plus qkv_bias (bias_after_round:
+ * GPTQ order), M-RoPE'd at lengths[slot] + rope_delta[slot], the new K/V row is stored at
+ * pool[slot, lengths[slot]] (cache/kv_prealloc.py:253-261) and token t attends to keys
+ * [0, lengths[slot]] (:272-290).  slots NULL = row t.  lengths are not advanced. */
+int omni_decode_attention_fused(const float* qkv_partials, int nparts, const void* qkv_bias,
+                                int bias_after_round, const void* cos_tab, const void* sin_tab,
+                                int max_pos, const int64_t* rope_delta, int sec0, int sec1,
+                                int sec2, void* k_cache, void* v_cache, int pool_rows, int max_len,
+                                const int64_t* slots, const int64_t* lengths, void* out, int T,
+                                int n_heads, int n_kv_heads, int head_dim, float scale, int waves,
+                                int splits, float* workspace, void* stream);
+
 /* _PackedPrefillWriter.flash_prefill (cache/kv_prealloc.py:181-203) and the append form
  * of :149-174: token t attends causally to keys [0, kv_len[t]) of pool row slots[t].
  * qblocks int32 [nqb][2] = (first token, count <= 16) of consecutive tokens of one

@@ -41,7 +41,50 @@ struct AttnArgs {
   int S;                 // workgroups per (token, kv head)
   float scale_log2;
   int T;
+  // Fused decode prologue (qparts != NULL): q, and the new token's k / v, are formed
+  // from the qkv projection's fp32 split-K partials [nq][T][(nh + 2 nkv) * 128] (+ bias),
+  // M-RoPE'd at position kv_len[slot] + rope_delta[slot] (the token is written at
+  // kv_len[slot], kv_add must be 1), and the new K/V row is written to the pool.
+  const float* qparts;
+  int nq;
+  const half_t* qbias;
+  int bias_after_round;
+  const half_t* cos_tab;
+  const half_t* sin_tab;
+  int max_pos;
+  const int64_t* rope_delta;
+  int s0, s1;
 };
+
+#define ATT_MAXPARTS 16
+
+// fp16 of the sum of nq fp32 partials (slice order) for 8 consecutive columns, + bias
+// with the producing linear's rounding (GPTQ: after the fp16 rounding).
+__device__ __forceinline__ half8_t sum_parts8(const float* __restrict__ parts, int nq, int64_t rs,
+                                              int64_t ps, const half_t* bias, int bar, int col) {
+#pragma clang fp contract(off)
+  float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int p = 0; p < ATT_MAXPARTS; ++p) {
+    if (p < nq) {
+      const float4* pp = (const float4*)(parts + p * ps + rs + col);
+      const float4 lo = pp[0], hi = pp[1];
+      sum[0] += lo.x; sum[1] += lo.y; sum[2] += lo.z; sum[3] += lo.w;
+      sum[4] += hi.x; sum[5] += hi.y; sum[6] += hi.z; sum[7] += hi.w;
+    }
+  }
+  half8_t v;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    if (bias) {
+      const float b = (float)bias[col + e];
+      v[e] = bar ? (half_t)((float)(half_t)sum[e] + b) : (half_t)(sum[e] + b);
+    } else {
+      v[e] = (half_t)sum[e];
+    }
+  }
+  return v;
+}
 
 __device__ __forceinline__ int64_t clamp64(int64_t v, int64_t lo, int64_t hi) {
   return v < lo ? lo : (v > hi ? hi : v);
@@ -55,6 +98,8 @@ __global__ __launch_bounds__(NWA * 64) void decode_attn_kernel(AttnArgs a) {
   constexpr int kOBytes = NWA * 8 * ATT_HD * 4;
   __shared__ __attribute__((aligned(16))) char smem[kVsBytes > kOBytes ? kVsBytes : kOBytes];
   __shared__ float ml_lds[NWA][ATT_MAXG][2];
+  __shared__ __attribute__((aligned(16))) half_t q_lds[ATT_MAXG][ATT_HD];   // fused prologue
+  __shared__ __attribute__((aligned(16))) half_t kv_new[2][ATT_HD];
   half_t (*vs_lds)[ATT_BLK * ATT_VSTRIDE] = (half_t (*)[ATT_BLK * ATT_VSTRIDE])smem;
   float (*o_lds)[8][ATT_HD] = (float (*)[8][ATT_HD])smem;   // heads < 8 are combined
 
@@ -70,8 +115,8 @@ __global__ __launch_bounds__(NWA * 64) void decode_attn_kernel(AttnArgs a) {
 
   const int64_t slot = a.slots ? a.slots[t] : t;
   const bool slot_ok = slot >= 0 && slot < a.pool_rows;
-  int64_t L = slot_ok ? a.kv_len[a.kv_by_slot ? slot : t] + a.kv_add : 0;
-  L = clamp64(L, 0, a.max_len);
+  const int64_t L_raw = slot_ok ? a.kv_len[a.kv_by_slot ? slot : t] + a.kv_add : 0;
+  const int64_t L = clamp64(L_raw, 0, a.max_len);
 
   // Token range of this wave: the context is cut into S*NWA 32-aligned chunks.
   const int nsplit = S * NWA;
@@ -80,19 +125,10 @@ __global__ __launch_bounds__(NWA * 64) void decode_attn_kernel(AttnArgs a) {
   const int wsplit = sp * NWA + wave;
   const int beg = (int)min((int64_t)wsplit * chunk, L);
   const int end = (int)min((int64_t)(wsplit + 1) * chunk, L);
-
-  // Q fragments: B operand of S^T = K Q^T.  Lane holds head c16, dims 32ks + 8*q16 + e.
-  half8_t qf[4];
-  {
-    const bool hv = c16 < G;
-    const half_t* qp = a.q + (int64_t)t * a.q_stride + (int64_t)(g * G + (hv ? c16 : 0)) * ATT_HD;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      half8_t v = *(const half8_t*)(qp + ks * 32 + q16 * 8);
-      if (!hv) v = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
-      qf[ks] = v;
-    }
-  }
+  const bool fused = a.qparts != nullptr;
+  // fused decode: the token written this step sits at index L - 1 (= kv_len[slot]); a row
+  // already at capacity (kv_len >= max_len) writes nothing and attends to the pool as is.
+  const int newtok = fused && L_raw == L ? (int)L - 1 : -1;
 
   float m_run = -INFINITY;   // per head c16 (identical across q16 groups)
   float l_run = 0.f;         // lane-partial sum, reduced at the end
@@ -126,8 +162,83 @@ __global__ __launch_bounds__(NWA * 64) void decode_attn_kernel(AttnArgs a) {
     }
   };
 
-  if (beg < end) load_block(beg);
+  if (beg < end) load_block(beg);          // first K/V block in flight during the prologue
+
+  if (fused) {
+    // qkv row of token t from the projection's partials: q heads g*G .. g*G+G-1 rotated
+    // into q_lds; the new k (rotated) and v of kv head g into kv_new.
+#pragma clang fp contract(off)
+    const int nh = a.nkv * G;
+    const int W = (nh + 2 * a.nkv) * ATT_HD;
+    const int64_t ps = (int64_t)a.T * W;
+    const int64_t rs = (int64_t)t * W;
+    int64_t pos = (slot_ok ? a.kv_len[slot] : 0) + (a.rope_delta && slot_ok ? a.rope_delta[slot] : 0);
+    pos = clamp64(pos, 0, a.max_pos - 1);
+    const int nitems = G * 8 + 8 + 16;
+    for (int it = threadIdx.x; it < nitems; it += NWA * 64) {
+      if (it < G * 8 + 8) {
+        const bool isq = it < G * 8;
+        const int c = isq ? (it & 7) : it - G * 8;
+        const int col = isq ? (g * G + (it >> 3)) * ATT_HD : (nh + g) * ATT_HD;
+        const int d0 = c * 8;
+        const int axis = d0 < a.s0 ? 0 : (d0 < a.s0 + a.s1 ? 1 : 2);
+        (void)axis;   // decode positions are equal on the three axes
+        const half8_t x1 = sum_parts8(a.qparts, a.nq, rs, ps, a.qbias, a.bias_after_round, col + d0);
+        const half8_t x2 = sum_parts8(a.qparts, a.nq, rs, ps, a.qbias, a.bias_after_round, col + d0 + 64);
+        const half8_t cs = *(const half8_t*)(a.cos_tab + pos * 64 + d0);
+        const half8_t sn = *(const half8_t*)(a.sin_tab + pos * 64 + d0);
+        const half8_t y1 = x1 * cs + (-x2) * sn;   // fp16 ops, one rounding each (no fma)
+        const half8_t y2 = x2 * cs + x1 * sn;
+        half_t* dst = isq ? q_lds[it >> 3] : kv_new[0];
+        *(half8_t*)(dst + d0) = y1;
+        *(half8_t*)(dst + d0 + 64) = y2;
+      } else {
+        const int c = it - G * 8 - 8;
+        *(half8_t*)(kv_new[1] + c * 8) =
+            sum_parts8(a.qparts, a.nq, rs, ps, a.qbias, a.bias_after_round, (nh + a.nkv + g) * ATT_HD + c * 8);
+      }
+    }
+    __syncthreads();
+    // the workgroup whose range holds the new token stores its K/V row in the pool
+    const int owner = newtok >= 0 && chunk > 0 ? newtok / chunk / NWA : -1;
+    if (owner == sp && newtok < a.max_len && threadIdx.x < 32) {
+      const int kvsel = threadIdx.x >> 4;
+      const int c = threadIdx.x & 15;
+      half_t* dst = const_cast<half_t*>(kvsel ? a.v_cache : a.k_cache) + (row_base + newtok) * tok_stride + g * ATT_HD + c * 8;
+      *(half8_t*)dst = *(const half8_t*)(kv_new[kvsel] + c * 8);
+    }
+  }
+
+  // Q fragments: B operand of S^T = K Q^T.  Lane holds head c16, dims 32ks + 8*q16 + e.
+  half8_t qf[4];
+  {
+    const bool hv = c16 < G;
+    const half_t* qp = fused ? q_lds[hv ? c16 : 0]
+                             : a.q + (int64_t)t * a.q_stride + (int64_t)(g * G + (hv ? c16 : 0)) * ATT_HD;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      half8_t v = *(const half8_t*)(qp + ks * 32 + q16 * 8);
+      if (!hv) v = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
+      qf[ks] = v;
+    }
+  }
+
   for (int tb = beg; tb < end; tb += ATT_BLK) {
+    // The new token's K/V come from the prologue, not from the pool row being written.
+    // Rows past the range were loaded from row end - 1 (= newtok in the last range), so
+    // they are compared by that clamped index: masked rows never carry stale pool data.
+    if (newtok >= tb && newtok < tb + ATT_BLK) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        if (min(tb + 16 * j + c16, end - 1) == newtok)
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) kf[j][ks] = *(const half8_t*)(kv_new[0] + ks * 32 + q16 * 8);
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const int c = lane + 64 * r;
+        if (min(tb + (c >> 4), end - 1) == newtok) vr[r] = *(const half8_t*)(kv_new[1] + (c & 15) * 8);
+      }
+    }
     // Stage this block's V into LDS (row-major, padded), keep K in registers.
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
@@ -280,6 +391,9 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
   }
 }
 
+static int launch_decode_attn(const AttnArgs& a, int n_kv_heads, int T, int G, int waves,
+                              int splits, float* workspace, hipStream_t st);
+
 // Decode / append attention over the pool.
 //   q          fp16, token t head h at q + t*q_stride + h*128
 //   k/v_cache  fp16 [pool_rows, max_len, n_kv, 128]
@@ -323,9 +437,21 @@ extern "C" int omni_decode_attention(const void* q, int q_stride, const void* k_
   a.S = splits;
   a.scale_log2 = scale * 1.4426950408889634f;
   a.T = T;
+  a.qparts = nullptr;
+  a.nq = 0;
+  a.qbias = nullptr;
+  a.bias_after_round = 0;
+  a.cos_tab = a.sin_tab = nullptr;
+  a.max_pos = 0;
+  a.rope_delta = nullptr;
+  a.s0 = a.s1 = 0;
+  return launch_decode_attn(a, n_kv_heads, T, G, waves, splits, workspace, (hipStream_t)stream);
+}
+
+static int launch_decode_attn(const AttnArgs& a, int n_kv_heads, int T, int G, int waves,
+                              int splits, float* workspace, hipStream_t st) {
   const int64_t nblocks = (int64_t)n_kv_heads * T * splits;
   if (nblocks > 0x7fffffff) return OMNI_EUNSUPPORTED;
-  hipStream_t st = (hipStream_t)stream;
   switch (waves) {
     case 4: hipLaunchKernelGGL(decode_attn_kernel<4>, dim3((unsigned)nblocks), dim3(256), 0, st, a); break;
     case 8: hipLaunchKernelGGL(decode_attn_kernel<8>, dim3((unsigned)nblocks), dim3(512), 0, st, a); break;
@@ -334,10 +460,67 @@ extern "C" int omni_decode_attention(const void* q, int q_stride, const void* k_
   OMNI_CHECK_LAUNCH();
   if (splits > 1) {
     hipLaunchKernelGGL(attn_combine_kernel, dim3(n_kv_heads * T), dim3(256), 0, st, workspace,
-                       (half_t*)out, n_kv_heads, G, splits);
+                       a.out, n_kv_heads, G, splits);
     OMNI_CHECK_LAUNCH();
   }
   return OMNI_OK;
+}
+
+// Decode step attention fused with its producer's epilogue: q and the new token's k / v
+// are formed from the qkv projection's fp32 split-K partials [nparts][T][(nh+2nkv)*128]
+// plus bias (bias_after_round: GPTQ rounding order), M-RoPE'd at position
+// lengths[slot] + rope_delta[slot] with the fp16 cos/sin tables, the new K/V row is
+// stored at pool[slot, lengths[slot]], and token t attends to keys [0, lengths[slot]].
+// Replaces omni_mrope_kv_write + omni_decode_attention for a decode step (lengths are
+// not advanced).
+extern "C" int omni_decode_attention_fused(
+    const float* qkv_partials, int nparts, const void* qkv_bias, int bias_after_round,
+    const void* cos_tab, const void* sin_tab, int max_pos, const int64_t* rope_delta, int sec0,
+    int sec1, int sec2, void* k_cache, void* v_cache, int pool_rows, int max_len,
+    const int64_t* slots, const int64_t* lengths, void* out, int T, int n_heads, int n_kv_heads,
+    int head_dim, float scale, int waves, int splits, float* workspace, void* stream) {
+  if (T < 0 || n_heads <= 0 || n_kv_heads <= 0 || pool_rows <= 0 || max_len <= 0 || max_pos <= 0)
+    return OMNI_EINVAL;
+  if (head_dim != ATT_HD || n_heads % n_kv_heads) return OMNI_EUNSUPPORTED;
+  if (sec0 + sec1 + sec2 != ATT_HD / 2 || (sec0 & 7) || (sec1 & 7) || (sec2 & 7)) return OMNI_EUNSUPPORTED;
+  const int G = n_heads / n_kv_heads;
+  if (G > ATT_MAXG) return OMNI_EUNSUPPORTED;
+  if (nparts < 1 || nparts > ATT_MAXPARTS) return OMNI_EUNSUPPORTED;
+  if (waves != 4 && waves != 8 && waves != 16) return OMNI_EINVAL;
+  if (splits < 1 || splits > 64) return OMNI_EINVAL;
+  if (T == 0) return OMNI_OK;
+  if (!qkv_partials || !cos_tab || !sin_tab || !k_cache || !v_cache || !lengths || !out)
+    return OMNI_EINVAL;
+  if (splits > 1 && !workspace) return OMNI_EINVAL;
+  AttnArgs a;
+  a.q = nullptr;
+  a.q_stride = 0;
+  a.k_cache = (const half_t*)k_cache;
+  a.v_cache = (const half_t*)v_cache;
+  a.pool_rows = pool_rows;
+  a.max_len = max_len;
+  a.nkv = n_kv_heads;
+  a.G = G;
+  a.slots = slots;
+  a.kv_len = lengths;
+  a.kv_by_slot = 1;
+  a.kv_add = 1;
+  a.out = (half_t*)out;
+  a.part = workspace;
+  a.S = splits;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.T = T;
+  a.qparts = qkv_partials;
+  a.nq = nparts;
+  a.qbias = (const half_t*)qkv_bias;
+  a.bias_after_round = bias_after_round;
+  a.cos_tab = (const half_t*)cos_tab;
+  a.sin_tab = (const half_t*)sin_tab;
+  a.max_pos = max_pos;
+  a.rope_delta = rope_delta;
+  a.s0 = sec0;
+  a.s1 = sec1;
+  return launch_decode_attn(a, n_kv_heads, T, G, waves, splits, workspace, (hipStream_t)stream);
 }
 
 // ===========================================================================

@@ -159,6 +159,22 @@ class CacheView:
         return self.pool.attend(qkv, qkv.stride(0), layer_idx, self.pool.lengths, True, 1, out,
                                 self.n, scale, plan=plan)
 
+    def attend_fused(self, qparts, nparts: int, bias, bias_after_round: bool, layer_idx: int,
+                     scale: float, cos_tab, sin_tab, mrope_section, out,
+                     plan: tuple | None = None) -> torch.Tensor:
+        """Decode attention fused with its producer's epilogue: q / new k, v from the qkv
+        projection's fp32 split-K partials (+ bias), M-RoPE at lengths[row] + rope_delta,
+        new K/V row stored at lengths[row], attention over keys [0, lengths[row]]."""
+        pool, n = self.pool, self.n
+        w, s = plan or pool.attn_plan or decode_plan(n, pool.n_kv_heads, pool.max_len)
+        s0, s1, s2 = mrope_section
+        call("omni_decode_attention_fused", ptr(qparts), nparts, ptr(bias), int(bias_after_round),
+             ptr(cos_tab), ptr(sin_tab), cos_tab.shape[0], ptr(self.rope_delta), s0, s1, s2,
+             ptr(pool.k[layer_idx]), ptr(pool.v[layer_idx]), pool.max_batch, pool.max_len, None,
+             ptr(pool.lengths), ptr(out), n, pool.n_heads, pool.n_kv_heads, pool.head_dim,
+             float(scale), w, s, ptr(pool._attn_ws), stream())
+        return out
+
     def flash_decode(self, q, key, value, layer_idx, scale):
         """Reference protocol (kv_prealloc.py:272-290): q [n, nh, hd] (rotated), key/value
         [n, nkv, hd]; writes K/V at lengths[row], attends, advances lengths on the last

@@ -408,3 +408,48 @@ def test_mrope_from_partials(gpu, bias_after_round):
         d = (a.float() - b.float()).abs()
         assert d.max().item() <= 2e-3 * max(1.0, b.float().abs().max().item())
         assert (d > 0).float().mean().item() < 0.01
+
+
+@pytest.mark.parametrize("bias_after_round,splits,lengths", [
+    (1, 3, [2047, 31, 0, 500]), (0, 1, [64, 7]), (1, 8, [4000, 1000]),
+])
+def test_decode_attention_fused_equals_unfused(gpu, bias_after_round, splits, lengths):
+    """Fused prologue (qkv partials + bias + M-RoPE + KV write) + attention gives exactly
+    what the separate M-RoPE-from-partials and attention launches give."""
+    from omniserve_amd._lib import call, ptr, stream
+    from omniserve_amd.qwen2_llm import rope_tables
+    say(f"fused decode attention bar={bias_after_round} splits={splits} lengths={lengths}")
+    cfg = ref.Qwen2Config()
+    nh, nkv, hd, ML = 12, 2, 128, 4096
+    n = len(lengths)
+    P = n + 1
+    W = (nh + 2 * nkv) * hd
+    S = 6
+    g = torch.Generator().manual_seed(120)
+    parts = (torch.randn(S, n, W, generator=g) * 0.3).to(gpu)
+    bias = f16((W,), 121, 0.02).to(gpu)
+    delta = torch.tensor([0, 3, -2, 1, 0][:P], dtype=torch.int64).to(gpu)
+    kp0 = f16((P, ML, nkv, hd), 122)
+    vp0 = f16((P, ML, nkv, hd), 123)
+    lens = torch.tensor(lengths + [0], dtype=torch.int64).to(gpu)
+    cos, sin = rope_tables(cfg, 8192, gpu)
+    outs = []
+    for mode in ("fused", "separate"):
+        kc, vc = kp0.to(gpu), vp0.to(gpu)
+        out = torch.empty(n, nh, hd, device=gpu, dtype=torch.float16)
+        ws = torch.empty(n * nkv * splits * 6 * 130, device=gpu, dtype=torch.float32)
+        if mode == "fused":
+            call("omni_decode_attention_fused", ptr(parts), S, ptr(bias), bias_after_round,
+                 ptr(cos), ptr(sin), 8192, ptr(delta), 16, 24, 24, ptr(kc), ptr(vc), P, ML, None,
+                 ptr(lens), ptr(out), n, nh, nkv, hd, hd ** -0.5, 8, splits, ptr(ws), stream())
+        else:
+            qkv = torch.empty(n, W, device=gpu, dtype=torch.float16)
+            call("omni_mrope_kv_write_partials", ptr(qkv), W, ptr(parts), S, ptr(bias),
+                 bias_after_round, None, ptr(lens), ptr(delta), ptr(cos), ptr(sin), 8192, ptr(kc),
+                 ptr(vc), None, None, P, ML, n, nh, nkv, hd, 16, 24, 24, stream())
+            call("omni_decode_attention", ptr(qkv), W, ptr(kc), ptr(vc), P, ML, None, ptr(lens),
+                 1, 1, ptr(out), n, nh, nkv, hd, hd ** -0.5, 8, splits, ptr(ws), stream())
+        torch.cuda.synchronize()
+        outs.append((out.cpu(), kc.cpu(), vc.cpu()))
+    for a, b in zip(outs[0], outs[1]):
+        assert torch.equal(a, b)

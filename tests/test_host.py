@@ -206,5 +206,7 @@ def test_bench_byte_accounting_matches_published_floor():
     assert abs(w16 / 1e9 - 3.087) < 0.005
     # config 3 averaged over its 128 steps (mean attended context ~2112): ~3.08 GB per step
     assert abs(bench.step_bytes("gptq", [2111] * 32) / 1e9 - 3.08) < 0.01
-    # one attention launch: 32 x 2049 keys x (K+V) x 2 heads x 128 x 2 B + q/out
-    assert bench.attn_launch_bytes([2048] * 32) == 32 * 2049 * 1024 + 2 * 32 * 12 * 128 * 2
+    # one fused attention launch: 32 x 2048 keys read + 32 new rows written, (K+V) x 2 heads
+    # x 128 x 2 B, the qkv rows + bias in, the output out
+    assert bench.attn_launch_bytes([2048] * 32) == (32 * 2049 * 1024 + 33 * 2048 * 2
+                                                    + 32 * 12 * 128 * 2)

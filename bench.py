@@ -116,37 +116,42 @@ def time_kernel(fn, reps: int) -> float:
     return e0.elapsed_time(e1) / 1e3 / reps
 
 
-def attention_in_step(runner, B: int, steps: int) -> tuple[float, int]:
-    """Mean duration (s) of the decode-attention launches inside eager decode steps: the
-    same 28-layer step as the timed graph (so caches hold what the step leaves there),
-    with a HIP event pair around each attention launch on the stream it runs on."""
-    from omniserve_amd.kv_cache import CacheView
+def attention_launch_time(runner, B: int, reps: int) -> tuple[float, int]:
+    """Mean duration (s) of one decode-attention launch at the current context: the 28
+    layers' launches (each over its own layer's K/V, so nothing is served from cache)
+    captured in a HIP graph and replayed ``reps`` times between HIP events on the stream
+    the kernels run on."""
     model = runner.adapter.model
+    cfg = model.cfg
     dev = runner.pool.storage.device
     view = runner.pool.view(B, runner._rope_delta)
-    ids = torch.randint(0, V, (B,), device=dev)
-    out_ids = torch.empty(B, dtype=torch.int64, device=dev)
-    events = []
-    orig = CacheView.attend_fused
+    bufs = model.decode_buffers(B, dev)
+    Sq = model.layers[0].qkv_proj.forward_partial(bufs["h"], bufs["qpart"])
 
-    def timed(self, *a, **k):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        r = orig(self, *a, **k)
-        e1.record()
-        events.append((e0, e1))
-        return r
+    def launches():
+        for i, layer in enumerate(model.layers):
+            view.attend_fused(bufs["qpart"], Sq, layer.qkv_proj.bias, layer.qkv_proj.fmt == "int4",
+                              i, model.scale, model.rope_cos, model.rope_sin, cfg.mrope_section)
 
-    model.decode_greedy(ids, view, out_ids)     # warm-up (lengths are not advanced)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        launches()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        launches()
+    g.replay()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    CacheView.attend_fused = timed
-    try:
-        for _ in range(steps):
-            model.decode_greedy(ids, view, out_ids)
-    finally:
-        CacheView.attend_fused = orig
+    e0.record(st)
+    for _ in range(reps):
+        g.replay()
+    e1.record(st)
     torch.cuda.synchronize()
-    return sum(a.elapsed_time(b) for a, b in events) / 1e3 / len(events), len(events)
+    n = reps * len(model.layers)
+    return e0.elapsed_time(e1) / 1e3 / n, n
 
 
 def cpu_baseline(runner, seqs, w, shape, budget_s: float = 15.0) -> dict:
@@ -197,8 +202,8 @@ def main():
     ap.add_argument("--ctx", type=int, default=2048)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--kernel-reps", type=int, default=20)
-    ap.add_argument("--kernel-steps", type=int, default=4,
-                    help="eager steps whose attention launches are timed for the roofline")
+    ap.add_argument("--kernel-steps", type=int, default=10,
+                    help="replays of the 28-launch attention graph timed for the roofline")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -234,6 +239,17 @@ def main():
     ms = wall * 1e3 / args.steps
     tok_s = B * args.steps / wall
 
+    # device time of the step alone: the captured graph replayed back to back (no D2H,
+    # no host bookkeeping between steps)
+    g = runner._graphs[B][0]
+    r0, r1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    r0.record(st)
+    for _ in range(8):
+        g.replay()
+    r1.record(st)
+    torch.cuda.synchronize()
+    replay_ms = r0.elapsed_time(r1) / 8
+
     # algorithmic bytes per step, averaged over the timed steps (contexts grow by 1/step)
     avg_step_bytes = sum(step_bytes("gptq", [L + s for L in ctx_before])
                          for s in range(args.steps)) / args.steps
@@ -242,7 +258,7 @@ def main():
     model = runner.adapter.model
     bufs = model.decode_buffers(B, dev)
     ctx_now = runner.pool.lengths[:B].cpu().tolist()
-    t_attn, n_attn = attention_in_step(runner, B, args.kernel_steps)
+    t_attn, n_attn = attention_launch_time(runner, B, args.kernel_steps)
     a_bytes = attn_launch_bytes(ctx_now)
     achieved = a_bytes / t_attn
     # second-largest stream: the gate_up W4A16 GEMM with the fused SiLU
@@ -274,8 +290,8 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode_attn_kernel (fused qkv-partials + M-RoPE + KV write + split-K GQA "
-                      "decode attention), mean over 28 layers x kernel_steps eager steps",
+            "kernel": "decode_attn_kernel (qkv partials + bias + M-RoPE + KV write + split GQA "
+                      "decode attention, states out), graph of the 28 layers' launches",
             "achieved": round(achieved / 1e9, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM, 4), "traffic": None,
             "launch_us": round(t_attn * 1e6, 2), "launches": n_attn, "bytes_per_launch": a_bytes,
@@ -286,6 +302,7 @@ def main():
             "frac": round(avg_step_bytes / (ms / 1e3) / PEAK_HBM, 4),
             "device_ms_per_step": round(dev_ms, 4),
             "device_frac": round(avg_step_bytes / (dev_ms / 1e3) / PEAK_HBM, 4),
+            "graph_replay_ms": round(replay_ms, 4),
         },
         "kernels": {
             "gate_up_w4a16_silu_us": round(t_gu * 1e6, 2),

@@ -98,7 +98,7 @@ int omni_mrope_kv_write_partials(void* qkv, int qkv_stride, const float* partial
  * pool.  Token t (pool row slots[t], or t) attends to keys [0, L), L = kv_len[kv_by_slot ?
  * slot : t] + kv_add; out fp16 [T, n_heads, 128].  waves in {4, 8, 16} per workgroup;
  * splits workgroups per (token, kv head) (1..64): splits > 1 writes partial softmax
- * states to workspace (fp32, >= T * n_kv * splits * (n_heads/n_kv) * 130) and merges them
+ * states to workspace (fp32, >= T * n_kv * splits * (n_heads/n_kv) * 132) and merges them
  * in a second launch. */
 int omni_decode_attention(const void* q, int q_stride, const void* k_cache, const void* v_cache,
                           int pool_rows, int max_len, const int64_t* slots, const int64_t* kv_len,
@@ -111,14 +111,17 @@ int omni_decode_attention(const void* q, int q_stride, const void* k_cache, cons
  * partials [nparts <= 16][T][(n_heads + 2 n_kv) * 128] plus qkv_bias (bias_after_round:
  * GPTQ order), M-RoPE'd at lengths[slot] + rope_delta[slot], the new K/V row is stored at
  * pool[slot, lengths[slot]] (cache/kv_prealloc.py:253-261) and token t attends to keys
- * [0, lengths[slot]] (:272-290).  slots NULL = row t.  lengths are not advanced. */
+ * [0, lengths[slot]] (:272-290).  slots NULL = row t.  lengths are not advanced.
+ * n_heads / n_kv_heads <= 8.  merge = 1: out fp16 [T, n_heads, 128] (a merge launch
+ * follows when splits > 1); merge = 0: the split states stay in workspace (>= T * n_kv *
+ * splits * G * 132 fp32) for omni_*_gemm_attn and out is not written. */
 int omni_decode_attention_fused(const float* qkv_partials, int nparts, const void* qkv_bias,
                                 int bias_after_round, const void* cos_tab, const void* sin_tab,
                                 int max_pos, const int64_t* rope_delta, int sec0, int sec1,
                                 int sec2, void* k_cache, void* v_cache, int pool_rows, int max_len,
                                 const int64_t* slots, const int64_t* lengths, void* out, int T,
                                 int n_heads, int n_kv_heads, int head_dim, float scale, int waves,
-                                int splits, float* workspace, void* stream);
+                                int splits, float* workspace, int merge, void* stream);
 
 /* _PackedPrefillWriter.flash_prefill (cache/kv_prealloc.py:181-203) and the append form
  * of :149-174: token t attends causally to keys [0, kv_len[t]) of pool row slots[t].
@@ -150,6 +153,20 @@ int omni_w4a16_gemm(const void* x, int ldx, const void* qweight_packed, const vo
 int omni_f16_gemm(const void* x, int ldx, const void* weight_packed, const void* bias, void* out,
                   int ldo, float* partial, int M, int N, int K, int epilogue, int ksplit,
                   int preset, void* stream);
+
+/* o_proj fed by the decode attention (model/qwen2_llm.py:98-99: o_proj(attn_out)) without
+ * the attention's merge launch: x[m, h*128 + d] is the merge of the attn_splits split
+ * states [M][n_kv_heads][attn_splits][group][132] fp32 that omni_decode_attention_fused
+ * left in its workspace (merge = 0), computed while x is staged (bit-identical to merging
+ * first).  K = n_kv_heads * group * 128; epilogue OMNI_EPI_STORE or OMNI_EPI_PARTIAL. */
+int omni_w4a16_gemm_attn(const float* attn_states, int attn_splits, int n_kv_heads, int group,
+                         const void* qweight_packed, const void* scales_packed, const void* bias,
+                         int bias_after_round, void* out, int ldo, float* partial, int M, int N,
+                         int K, int epilogue, int ksplit, int preset, void* stream);
+int omni_f16_gemm_attn(const float* attn_states, int attn_splits, int n_kv_heads, int group,
+                       const void* weight_packed, const void* bias, void* out, int ldo,
+                       float* partial, int M, int N, int K, int epilogue, int ksplit, int preset,
+                       void* stream);
 
 /* Number of K slices (whole 128-groups) a split of ksplit gives for K. */
 int omni_gemm_slices(int K, int ksplit);

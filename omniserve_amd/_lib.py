@@ -36,7 +36,10 @@ SIGNATURES = {
     "omni_decode_attention": [_P, _I, _P, _P, _I, _I, _P, _P, _I, _I, _P, _I, _I, _I, _I, _F, _I,
                               _I, _P, _P],
     "omni_decode_attention_fused": [_P, _I, _P, _I, _P, _P, _I, _P, _I, _I, _I, _P, _P, _I, _I,
-                                    _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _P, _P],
+                                    _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _P, _I, _P],
+    "omni_w4a16_gemm_attn": [_P, _I, _I, _I, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I, _I,
+                             _P],
+    "omni_f16_gemm_attn": [_P, _I, _I, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I, _P],
     "omni_prefill_attention": [_P, _I, _P, _P, _I, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _F,
                                _P],
     "omni_w4a16_gemm": [_P, _I, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I, _I, _P],

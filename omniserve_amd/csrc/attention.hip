@@ -17,13 +17,15 @@
 //                                                   K fed straight from global)
 //   online softmax in fp32 (exp2, running max/sum per head)
 //   O[16 heads x 128] += P[16 x 32] . V[32 x 128]  (8 MFMAs, V transposed via LDS)
-// while the next block's K and V loads are already in flight.
+// while the next block's K and V loads are already in flight (streamed with
+// non-temporal loads: each pool row is read once per step).
 #include "common.h"
 
 #define ATT_HD 128
 #define ATT_BLK 32
 #define ATT_VSTRIDE 136   // LDS row stride (halfs) of the V tile: 16B-aligned, bank-spread
 #define ATT_MAXG 16       // query heads per KV head supported (MFMA N = 16)
+#define ATT_FUSED_MAXG 8  // ... by the fused decode prologue
 #define ATT_WAVES 4       // waves per workgroup of the prefill kernel
 
 struct AttnArgs {
@@ -37,8 +39,9 @@ struct AttnArgs {
   int kv_by_slot;
   int kv_add;            // kv = kv_len[...] + kv_add
   half_t* out;           // [T, nkv*G, 128]
-  float* part;           // S > 1: [T][nkv][S][G][128 + 2] fp32 (O unnormalised, m, l)
+  float* part;           // parts_out: [T][nkv][S][G][ATT_REC] fp32 split states
   int S;                 // workgroups per (token, kv head)
+  int parts_out;         // 1: states to part (S > 1, or left for the consumer); 0: fp16 out
   float scale_log2;
   int T;
   // Fused decode prologue (qparts != NULL): q, and the new token's k / v, are formed
@@ -58,50 +61,28 @@ struct AttnArgs {
 
 #define ATT_MAXPARTS 16
 
-// fp16 of the sum of nq fp32 partials (slice order) for 8 consecutive columns, + bias
-// with the producing linear's rounding (GPTQ: after the fp16 rounding).
-__device__ __forceinline__ half8_t sum_parts8(const float* __restrict__ parts, int nq, int64_t rs,
-                                              int64_t ps, const half_t* bias, int bar, int col) {
-#pragma clang fp contract(off)
-  float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int p = 0; p < ATT_MAXPARTS; ++p) {
-    if (p < nq) {
-      const float4* pp = (const float4*)(parts + p * ps + rs + col);
-      const float4 lo = pp[0], hi = pp[1];
-      sum[0] += lo.x; sum[1] += lo.y; sum[2] += lo.z; sum[3] += lo.w;
-      sum[4] += hi.x; sum[5] += hi.y; sum[6] += hi.z; sum[7] += hi.w;
-    }
-  }
-  half8_t v;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    if (bias) {
-      const float b = (float)bias[col + e];
-      v[e] = bar ? (half_t)((float)(half_t)sum[e] + b) : (half_t)(sum[e] + b);
-    } else {
-      v[e] = (half_t)sum[e];
-    }
-  }
-  return v;
-}
-
 __device__ __forceinline__ int64_t clamp64(int64_t v, int64_t lo, int64_t hi) {
   return v < lo ? lo : (v > hi ? hi : v);
 }
 
 template <int NWA>
-__global__ __launch_bounds__(NWA * 64) void decode_attn_kernel(AttnArgs a) {
-  // The V tiles (used in the block loop) and the per-wave partial outputs (used
-  // after it) share one LDS buffer.
+__global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_kernel(AttnArgs a) {
+  constexpr int NT = NWA * 64;
+  // The V tiles (block loop), the fused prologue's pre-rotation rows (before it) and
+  // the per-wave partial outputs (after it) share one LDS buffer.
   constexpr int kVsBytes = NWA * ATT_BLK * ATT_VSTRIDE * 2;
   constexpr int kOBytes = NWA * 8 * ATT_HD * 4;
-  __shared__ __attribute__((aligned(16))) char smem[kVsBytes > kOBytes ? kVsBytes : kOBytes];
+  constexpr int kRawBytes = (ATT_FUSED_MAXG + 2) * ATT_HD * 2;
+  constexpr int kSmem = kVsBytes > kOBytes ? (kVsBytes > kRawBytes ? kVsBytes : kRawBytes)
+                                           : (kOBytes > kRawBytes ? kOBytes : kRawBytes);
+  __shared__ __attribute__((aligned(16))) char smem[kSmem];
   __shared__ float ml_lds[NWA][ATT_MAXG][2];
-  __shared__ __attribute__((aligned(16))) half_t q_lds[ATT_MAXG][ATT_HD];   // fused prologue
+  __shared__ __attribute__((aligned(16))) half_t q_lds[ATT_FUSED_MAXG][ATT_HD];   // fused prologue
   __shared__ __attribute__((aligned(16))) half_t kv_new[2][ATT_HD];
+  __shared__ __attribute__((aligned(16))) half_t cs_lds[2][ATT_HD / 2];
   half_t (*vs_lds)[ATT_BLK * ATT_VSTRIDE] = (half_t (*)[ATT_BLK * ATT_VSTRIDE])smem;
   float (*o_lds)[8][ATT_HD] = (float (*)[8][ATT_HD])smem;   // heads < 8 are combined
+  half_t* raw = (half_t*)smem;   // fused: [G + 2][128] q heads | k | v before M-RoPE
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -112,99 +93,156 @@ __global__ __launch_bounds__(NWA * 64) void decode_attn_kernel(AttnArgs a) {
   const int g = (blockIdx.x / S) % a.nkv;
   const int t = blockIdx.x / (S * a.nkv);
   const int G = a.G;
+  const int nh = a.nkv * G;
+  const bool fused = a.qparts != nullptr;
 
+  // 1. Fused prologue loads that do not depend on the context length: this token's
+  //    q heads g*G .. g*G+G-1, k and v of kv head g as fp32 split-K partials (up to 8
+  //    slices in flight per element pair; more slices are added in a second pass).
+  constexpr int PI = ((ATT_FUSED_MAXG + 2) * ATT_HD / 2 + NT - 1) / NT;
+  float2 pv[PI][8];
+  const int nel2 = (G + 2) * (ATT_HD / 2);
+  const int W = (nh + 2 * a.nkv) * ATT_HD;
+  const int64_t ps = (int64_t)a.T * W;
+  auto gathered_col = [&](int e) {       // element e of the gathered row -> qkv column
+    const int hh = e / ATT_HD;
+    const int d = e % ATT_HD;
+    const int head = hh < G ? g * G + hh : (hh == G ? nh + g : nh + a.nkv + g);
+    return head * ATT_HD + d;
+  };
+  if (fused) {
+    const float* rowp = a.qparts + (int64_t)t * W;
+#pragma unroll
+    for (int j = 0; j < PI; ++j) {
+      const int i = threadIdx.x + j * NT;
+      if (i < nel2) {
+        const float* src = rowp + gathered_col(2 * i);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (u < a.nq) pv[j][u] = *(const float2*)(src + u * ps);
+          else pv[j][u] = make_float2(0.f, 0.f);
+        }
+      }
+    }
+  }
+
+  // 2. Context length, this workgroup's key range, the rotary row.
   const int64_t slot = a.slots ? a.slots[t] : t;
   const bool slot_ok = slot >= 0 && slot < a.pool_rows;
   const int64_t L_raw = slot_ok ? a.kv_len[a.kv_by_slot ? slot : t] + a.kv_add : 0;
   const int64_t L = clamp64(L_raw, 0, a.max_len);
-
-  // Token range of this wave: the context is cut into S*NWA 32-aligned chunks.
-  const int nsplit = S * NWA;
-  int chunk = (int)((L + nsplit - 1) / nsplit);
-  chunk = (chunk + ATT_BLK - 1) / ATT_BLK * ATT_BLK;
-  const int wsplit = sp * NWA + wave;
-  const int beg = (int)min((int64_t)wsplit * chunk, L);
-  const int end = (int)min((int64_t)(wsplit + 1) * chunk, L);
-  const bool fused = a.qparts != nullptr;
   // fused decode: the token written this step sits at index L - 1 (= kv_len[slot]); a row
   // already at capacity (kv_len >= max_len) writes nothing and attends to the pool as is.
   const int newtok = fused && L_raw == L ? (int)L - 1 : -1;
 
-  float m_run = -INFINITY;   // per head c16 (identical across q16 groups)
-  float l_run = 0.f;         // lane-partial sum, reduced at the end
-  f32x4 o_acc[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) o_acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  // The context's 32-token blocks are dealt out evenly to the S*NWA waves of the
+  // (token, kv head): wave w gets blocks [w*nblk/nw, (w+1)*nblk/nw).
+  const int nblk = (int)((L + ATT_BLK - 1) / ATT_BLK);
+  const int nw = S * NWA;
+  const int wsplit = sp * NWA + wave;
+  const int beg = (int)min((int64_t)((int64_t)wsplit * nblk / nw) * ATT_BLK, L);
+  const int end = (int)min((int64_t)((int64_t)(wsplit + 1) * nblk / nw) * ATT_BLK, L);
+  const int wg_b0 = (int)((int64_t)sp * NWA * nblk / nw);
+  const int wg_b1 = (int)((int64_t)(sp + 1) * NWA * nblk / nw);
 
+  half8_t csv = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
+  if (fused && threadIdx.x < 16) {         // cos (threads 0-7) / sin (8-15) row at pos
+    int64_t pos = (slot_ok ? a.kv_len[slot] : 0) + (a.rope_delta && slot_ok ? a.rope_delta[slot] : 0);
+    pos = clamp64(pos, 0, a.max_pos - 1);
+    const half_t* tab = threadIdx.x < 8 ? a.cos_tab : a.sin_tab;
+    csv = *(const half8_t*)(tab + pos * (ATT_HD / 2) + (threadIdx.x & 7) * 8);
+  }
+
+  // 3. The first two K/V blocks of this wave go in flight.
   const int64_t row_base = slot * (int64_t)a.max_len;
   const half_t* kbase = a.k_cache + g * ATT_HD;
   const half_t* vbase = a.v_cache + g * ATT_HD;
   const int64_t tok_stride = (int64_t)a.nkv * ATT_HD;
   half_t* vs = vs_lds[wave];
 
-  half8_t kf[2][4];
-  half8_t vr[8];
-  auto load_block = [&](int tb) {
+  auto load_block = [&](half8_t (&kf)[2][4], half8_t (&vr)[8], int tb) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       int tok = tb + 16 * j + c16;
       tok = tok < end ? tok : end - 1;
       const half_t* kp = kbase + (row_base + tok) * tok_stride + q16 * 8;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) kf[j][ks] = *(const half8_t*)(kp + ks * 32);
+      for (int ks = 0; ks < 4; ++ks) kf[j][ks] = __builtin_nontemporal_load((const half8_t*)(kp + ks * 32));
     }
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
       const int c = lane + 64 * r;          // 512 chunks of 8 halfs = 32 tokens x 128 dims
       int tok = tb + (c >> 4);
       tok = tok < end ? tok : end - 1;
-      vr[r] = *(const half8_t*)(vbase + (row_base + tok) * tok_stride + (c & 15) * 8);
+      vr[r] = __builtin_nontemporal_load((const half8_t*)(vbase + (row_base + tok) * tok_stride + (c & 15) * 8));
     }
   };
-
-  if (beg < end) load_block(beg);          // first K/V block in flight during the prologue
+  half8_t kf0[2][4], vr0[8], kf1[2][4], vr1[8];
+  if (beg < end) load_block(kf0, vr0, beg);
+  if (beg + ATT_BLK < end) load_block(kf1, vr1, beg + ATT_BLK);
 
   if (fused) {
-    // qkv row of token t from the projection's partials: q heads g*G .. g*G+G-1 rotated
-    // into q_lds; the new k (rotated) and v of kv head g into kv_new.
+    // 4. Partial sums (slice order, as the unfused path) + bias -> fp16 rows in LDS.
 #pragma clang fp contract(off)
-    const int nh = a.nkv * G;
-    const int W = (nh + 2 * a.nkv) * ATT_HD;
-    const int64_t ps = (int64_t)a.T * W;
-    const int64_t rs = (int64_t)t * W;
-    int64_t pos = (slot_ok ? a.kv_len[slot] : 0) + (a.rope_delta && slot_ok ? a.rope_delta[slot] : 0);
-    pos = clamp64(pos, 0, a.max_pos - 1);
-    const int nitems = G * 8 + 8 + 16;
-    for (int it = threadIdx.x; it < nitems; it += NWA * 64) {
-      if (it < G * 8 + 8) {
-        const bool isq = it < G * 8;
-        const int c = isq ? (it & 7) : it - G * 8;
-        const int col = isq ? (g * G + (it >> 3)) * ATT_HD : (nh + g) * ATT_HD;
-        const int d0 = c * 8;
-        const int axis = d0 < a.s0 ? 0 : (d0 < a.s0 + a.s1 ? 1 : 2);
-        (void)axis;   // decode positions are equal on the three axes
-        const half8_t x1 = sum_parts8(a.qparts, a.nq, rs, ps, a.qbias, a.bias_after_round, col + d0);
-        const half8_t x2 = sum_parts8(a.qparts, a.nq, rs, ps, a.qbias, a.bias_after_round, col + d0 + 64);
-        const half8_t cs = *(const half8_t*)(a.cos_tab + pos * 64 + d0);
-        const half8_t sn = *(const half8_t*)(a.sin_tab + pos * 64 + d0);
-        const half8_t y1 = x1 * cs + (-x2) * sn;   // fp16 ops, one rounding each (no fma)
-        const half8_t y2 = x2 * cs + x1 * sn;
-        half_t* dst = isq ? q_lds[it >> 3] : kv_new[0];
-        *(half8_t*)(dst + d0) = y1;
-        *(half8_t*)(dst + d0 + 64) = y2;
+    const float* rowp = a.qparts + (int64_t)t * W;
+#pragma unroll
+    for (int j = 0; j < PI; ++j) {
+      const int i = threadIdx.x + j * NT;
+      if (i < nel2) {
+        const int col = gathered_col(2 * i);
+        float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const bool on = u < a.nq;
+          s0 += on ? pv[j][u].x : 0.f;
+          s1 += on ? pv[j][u].y : 0.f;
+        }
+        for (int p = 8; p < a.nq; ++p) {
+          const float2 v = *(const float2*)(rowp + col + p * ps);
+          s0 += v.x;
+          s1 += v.y;
+        }
+        half_t h0 = (half_t)s0, h1 = (half_t)s1;
+        if (a.qbias) {
+          const float b0 = (float)a.qbias[col], b1 = (float)a.qbias[col + 1];
+          h0 = a.bias_after_round ? (half_t)((float)h0 + b0) : (half_t)(s0 + b0);
+          h1 = a.bias_after_round ? (half_t)((float)h1 + b1) : (half_t)(s1 + b1);
+        }
+        raw[2 * i] = h0;
+        raw[2 * i + 1] = h1;
+      }
+    }
+    if (threadIdx.x < 16) *(half8_t*)(&cs_lds[threadIdx.x >> 3][(threadIdx.x & 7) * 8]) = csv;
+    __syncthreads();
+    // 5. M-RoPE (decode: one position on all three axes) in fp16 ops, one rounding
+    //    each and no contraction: y1 = x1*c + (-x2)*s, y2 = x2*c + x1*s.
+    for (int i = threadIdx.x; i < (G + 1) * 64 + 64; i += NT) {
+      if (i < (G + 1) * 64) {
+        const int hh = i >> 6;
+        const int d = i & 63;
+        const half_t x1 = raw[hh * ATT_HD + d];
+        const half_t x2 = raw[hh * ATT_HD + d + 64];
+        const half_t c = cs_lds[0][d];
+        const half_t s = cs_lds[1][d];
+        const half_t y1 = x1 * c + (-x2) * s;
+        const half_t y2 = x2 * c + x1 * s;
+        half_t* dst = hh < G ? q_lds[hh] : kv_new[0];
+        dst[d] = y1;
+        dst[d + 64] = y2;
       } else {
-        const int c = it - G * 8 - 8;
-        *(half8_t*)(kv_new[1] + c * 8) =
-            sum_parts8(a.qparts, a.nq, rs, ps, a.qbias, a.bias_after_round, (nh + a.nkv + g) * ATT_HD + c * 8);
+        const int j = i - (G + 1) * 64;
+        kv_new[1][2 * j] = raw[(G + 1) * ATT_HD + 2 * j];
+        kv_new[1][2 * j + 1] = raw[(G + 1) * ATT_HD + 2 * j + 1];
       }
     }
     __syncthreads();
-    // the workgroup whose range holds the new token stores its K/V row in the pool
-    const int owner = newtok >= 0 && chunk > 0 ? newtok / chunk / NWA : -1;
-    if (owner == sp && newtok < a.max_len && threadIdx.x < 32) {
+    // 6. The workgroup whose blocks hold the new token stores its K/V row in the pool.
+    const int nb = newtok >> 5;
+    if (newtok >= 0 && nb >= wg_b0 && nb < wg_b1 && threadIdx.x < 32) {
       const int kvsel = threadIdx.x >> 4;
       const int c = threadIdx.x & 15;
-      half_t* dst = const_cast<half_t*>(kvsel ? a.v_cache : a.k_cache) + (row_base + newtok) * tok_stride + g * ATT_HD + c * 8;
+      half_t* dst = const_cast<half_t*>(kvsel ? a.v_cache : a.k_cache) +
+                    (row_base + newtok) * tok_stride + g * ATT_HD + c * 8;
       *(half8_t*)dst = *(const half8_t*)(kv_new[kvsel] + c * 8);
     }
   }
@@ -223,7 +261,15 @@ __global__ __launch_bounds__(NWA * 64) void decode_attn_kernel(AttnArgs a) {
     }
   }
 
-  for (int tb = beg; tb < end; tb += ATT_BLK) {
+  float m_run = -INFINITY;   // per head c16 (identical across q16 groups)
+  float l_run = 0.f;         // lane-partial sum, reduced at the end
+  f32x4 o_acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o_acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  // One 32-token block: its K/V sit in (kf, vr); once they are consumed the same
+  // registers are refilled with the block two ahead.
+  auto process = [&](half8_t (&kf)[2][4], half8_t (&vr)[8], int tb) {
     // The new token's K/V come from the prologue, not from the pool row being written.
     // Rows past the range were loaded from row end - 1 (= newtok in the last range), so
     // they are compared by that clamped index: masked rows never carry stale pool data.
@@ -239,28 +285,24 @@ __global__ __launch_bounds__(NWA * 64) void decode_attn_kernel(AttnArgs a) {
         if (min(tb + (c >> 4), end - 1) == newtok) vr[r] = *(const half8_t*)(kv_new[1] + (c & 15) * 8);
       }
     }
-    // Stage this block's V into LDS (row-major, padded), keep K in registers.
+    // Stage this block's V into LDS (row-major, padded).
+    __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
       const int c = lane + 64 * r;
       *(half8_t*)(vs + (c >> 4) * ATT_VSTRIDE + (c & 15) * 8) = vr[r];
     }
-    half8_t kc[2][4];
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) kc[j][ks] = kf[j][ks];
-    if (tb + ATT_BLK < end) load_block(tb + ATT_BLK);   // prefetch next block
-
     // Scores: acc[j][i] = token tb + 16j + 4*q16 + i, head c16.
     f32x4 sacc[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) acc = mfma16x16x32(kc[j][ks], qf[ks], acc);
+      for (int ks = 0; ks < 4; ++ks) acc = mfma16x16x32(kf[j][ks], qf[ks], acc);
       sacc[j] = acc;
     }
+    if (tb + 2 * ATT_BLK < end) load_block(kf, vr, tb + 2 * ATT_BLK);   // refill
+
     float sc[8];
     float mblk = -INFINITY;
 #pragma unroll
@@ -309,6 +351,11 @@ __global__ __launch_bounds__(NWA * 64) void decode_attn_kernel(AttnArgs a) {
       o_acc[dt] = mfma16x16x32(pa, vb, o_acc[dt]);
     }
     __builtin_amdgcn_wave_barrier();
+  };
+
+  for (int tb = beg; tb < end; tb += 2 * ATT_BLK) {
+    process(kf0, vr0, tb);
+    if (tb + ATT_BLK < end) process(kf1, vr1, tb + ATT_BLK);
   }
 
   l_run += __shfl_xor(l_run, 16, 64);
@@ -316,7 +363,6 @@ __global__ __launch_bounds__(NWA * 64) void decode_attn_kernel(AttnArgs a) {
   __syncthreads();   // every wave is done with its V tile before o_lds reuses the space
 
   // Merge the waves' softmax states: heads processed in groups of 8 (G <= 16).
-  const int nh = a.nkv * G;
   if (lane < G) {
     ml_lds[wave][lane][0] = m_run;
     ml_lds[wave][lane][1] = l_run;
@@ -347,11 +393,11 @@ __global__ __launch_bounds__(NWA * 64) void decode_attn_kernel(AttnArgs a) {
           o += f * o_lds[w][h][d];
         }
       }
-      if (S == 1) {
+      if (!a.parts_out) {
         const float r = lsum > 0.f ? o / lsum : 0.f;
         a.out[((int64_t)t * nh + g * G + hb + h) * ATT_HD + d] = (half_t)r;
       } else {
-        float* pp = a.part + ((((int64_t)t * a.nkv + g) * S + sp) * G + hb + h) * (ATT_HD + 2);
+        float* pp = a.part + ((((int64_t)t * a.nkv + g) * S + sp) * G + hb + h) * ATT_REC;
         pp[d] = o;
         if (d == 0) {
           pp[ATT_HD] = M;
@@ -371,28 +417,17 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
   const int g = blockIdx.x % nkv;
   const int t = blockIdx.x / nkv;
   const int nh = nkv * G;
-  const float* base = part + ((int64_t)t * nkv + g) * S * G * (ATT_HD + 2);
-  for (int idx = threadIdx.x; idx < G * ATT_HD; idx += 256) {
-    const int h = idx / ATT_HD;
-    const int d = idx % ATT_HD;
-    float M = -INFINITY;
-    for (int s = 0; s < S; ++s) M = fmaxf(M, base[((int64_t)s * G + h) * (ATT_HD + 2) + ATT_HD]);
-    float lsum = 0.f, o = 0.f;
-    if (M != -INFINITY) {
-      for (int s = 0; s < S; ++s) {
-        const float* pp = base + ((int64_t)s * G + h) * (ATT_HD + 2);
-        const float f = exp2f(pp[ATT_HD] - M);
-        lsum += f * pp[ATT_HD + 1];
-        o += f * pp[d];
-      }
-    }
-    const float r = lsum > 0.f ? o / lsum : 0.f;
-    out[((int64_t)t * nh + g * G + h) * ATT_HD + d] = (half_t)r;
+  const float* base = part + ((int64_t)t * nkv + g) * S * G * ATT_REC;
+  for (int idx = threadIdx.x; idx < G * (ATT_HD / 8); idx += blockDim.x) {
+    const int h = idx / (ATT_HD / 8);
+    const int d0 = (idx % (ATT_HD / 8)) * 8;
+    *(half8_t*)(out + ((int64_t)t * nh + g * G + h) * ATT_HD + d0) =
+        attn_merge8(base + (int64_t)h * ATT_REC, (int64_t)G * ATT_REC, S, d0);
   }
 }
 
-static int launch_decode_attn(const AttnArgs& a, int n_kv_heads, int T, int G, int waves,
-                              int splits, float* workspace, hipStream_t st);
+static int launch_decode_attn(AttnArgs a, int n_kv_heads, int T, int G, int waves, int splits,
+                              int merge, float* workspace, hipStream_t st);
 
 // Decode / append attention over the pool.
 //   q          fp16, token t head h at q + t*q_stride + h*128
@@ -402,7 +437,7 @@ static int launch_decode_attn(const AttnArgs& a, int n_kv_heads, int T, int G, i
 //   out        fp16 [T, n_heads, 128]
 //   waves      waves per workgroup: 4, 8 or 16
 //   splits     workgroups per (token, kv head); > 1 writes partial states to
-//              workspace (fp32, >= T * n_kv * splits * G * 130) merged by a second launch
+//              workspace (fp32, >= T * n_kv * splits * G * 132) merged by a second launch
 extern "C" int omni_decode_attention(const void* q, int q_stride, const void* k_cache,
                                      const void* v_cache, int pool_rows, int max_len,
                                      const int64_t* slots, const int64_t* kv_len, int kv_by_slot,
@@ -445,11 +480,12 @@ extern "C" int omni_decode_attention(const void* q, int q_stride, const void* k_
   a.max_pos = 0;
   a.rope_delta = nullptr;
   a.s0 = a.s1 = 0;
-  return launch_decode_attn(a, n_kv_heads, T, G, waves, splits, workspace, (hipStream_t)stream);
+  return launch_decode_attn(a, n_kv_heads, T, G, waves, splits, 1, workspace, (hipStream_t)stream);
 }
 
-static int launch_decode_attn(const AttnArgs& a, int n_kv_heads, int T, int G, int waves,
-                              int splits, float* workspace, hipStream_t st) {
+static int launch_decode_attn(AttnArgs a, int n_kv_heads, int T, int G, int waves, int splits,
+                              int merge, float* workspace, hipStream_t st) {
+  a.parts_out = splits > 1 || !merge;
   const int64_t nblocks = (int64_t)n_kv_heads * T * splits;
   if (nblocks > 0x7fffffff) return OMNI_EUNSUPPORTED;
   switch (waves) {
@@ -458,9 +494,9 @@ static int launch_decode_attn(const AttnArgs& a, int n_kv_heads, int T, int G, i
     default: hipLaunchKernelGGL(decode_attn_kernel<16>, dim3((unsigned)nblocks), dim3(1024), 0, st, a); break;
   }
   OMNI_CHECK_LAUNCH();
-  if (splits > 1) {
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(n_kv_heads * T), dim3(256), 0, st, workspace,
-                       a.out, n_kv_heads, G, splits);
+  if (splits > 1 && merge) {
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(n_kv_heads * T), dim3(G * ATT_HD / 8 > 128 ? 256 : 128),
+                       0, st, workspace, a.out, n_kv_heads, G, splits);
     OMNI_CHECK_LAUNCH();
   }
   return OMNI_OK;
@@ -472,26 +508,27 @@ static int launch_decode_attn(const AttnArgs& a, int n_kv_heads, int T, int G, i
 // lengths[slot] + rope_delta[slot] with the fp16 cos/sin tables, the new K/V row is
 // stored at pool[slot, lengths[slot]], and token t attends to keys [0, lengths[slot]].
 // Replaces omni_mrope_kv_write + omni_decode_attention for a decode step (lengths are
-// not advanced).
+// not advanced).  merge = 0 leaves the split states in workspace (out unused) for the
+// o_proj GEMM that merges them while staging its input (omni_*_gemm_attn).
 extern "C" int omni_decode_attention_fused(
     const float* qkv_partials, int nparts, const void* qkv_bias, int bias_after_round,
     const void* cos_tab, const void* sin_tab, int max_pos, const int64_t* rope_delta, int sec0,
     int sec1, int sec2, void* k_cache, void* v_cache, int pool_rows, int max_len,
     const int64_t* slots, const int64_t* lengths, void* out, int T, int n_heads, int n_kv_heads,
-    int head_dim, float scale, int waves, int splits, float* workspace, void* stream) {
+    int head_dim, float scale, int waves, int splits, float* workspace, int merge, void* stream) {
   if (T < 0 || n_heads <= 0 || n_kv_heads <= 0 || pool_rows <= 0 || max_len <= 0 || max_pos <= 0)
     return OMNI_EINVAL;
   if (head_dim != ATT_HD || n_heads % n_kv_heads) return OMNI_EUNSUPPORTED;
   if (sec0 + sec1 + sec2 != ATT_HD / 2 || (sec0 & 7) || (sec1 & 7) || (sec2 & 7)) return OMNI_EUNSUPPORTED;
   const int G = n_heads / n_kv_heads;
-  if (G > ATT_MAXG) return OMNI_EUNSUPPORTED;
+  if (G > ATT_FUSED_MAXG) return OMNI_EUNSUPPORTED;
   if (nparts < 1 || nparts > ATT_MAXPARTS) return OMNI_EUNSUPPORTED;
   if (waves != 4 && waves != 8 && waves != 16) return OMNI_EINVAL;
   if (splits < 1 || splits > 64) return OMNI_EINVAL;
   if (T == 0) return OMNI_OK;
-  if (!qkv_partials || !cos_tab || !sin_tab || !k_cache || !v_cache || !lengths || !out)
-    return OMNI_EINVAL;
-  if (splits > 1 && !workspace) return OMNI_EINVAL;
+  if (!qkv_partials || !cos_tab || !sin_tab || !k_cache || !v_cache || !lengths) return OMNI_EINVAL;
+  if (merge ? !out : false) return OMNI_EINVAL;
+  if ((splits > 1 || !merge) && !workspace) return OMNI_EINVAL;
   AttnArgs a;
   a.q = nullptr;
   a.q_stride = 0;
@@ -520,7 +557,8 @@ extern "C" int omni_decode_attention_fused(
   a.rope_delta = rope_delta;
   a.s0 = sec0;
   a.s1 = sec1;
-  return launch_decode_attn(a, n_kv_heads, T, G, waves, splits, workspace, (hipStream_t)stream);
+  return launch_decode_attn(a, n_kv_heads, T, G, waves, splits, merge, workspace,
+                            (hipStream_t)stream);
 }
 
 // ===========================================================================

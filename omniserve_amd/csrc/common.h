@@ -99,24 +99,130 @@ __host__ __device__ __forceinline__ float e4m3fn_to_f32(uint8_t v) {
 // ---------------------------------------------------------------------------
 // int4 (uint4b8) dequant: one 32-bit word carries eight 4-bit codes for eight
 // consecutive k of one output column.  The repacked layout stores code e at
-// bit 2e (e even) or 16 + 2(e-1) (e odd), so the magic-exponent extraction
-//   ((w >> 4r) & 0x000F000F) | 0x64006400   ==  (1024 + q_{2r}, 1024 + q_{2r+1})
-// yields the codes in natural k order.  (1024 + q) - 1032 = q - 8 is exact in
-// fp16; the multiply by the fp16 group scale rounds once (RNE), which is the
-// reference's definition W = fp16((q - 8) * s).
+// bit 2e (e even) or 16 + 2(e-1) (e odd), so with u = w >> 8 the four fp16 pairs are
+//   (w & 0x000F000F) | 0x64006400  ==  (1024 + q0, 1024 + q1)   (mantissa LSB = 1)
+//   (w & 0x00F000F0) | 0x54005400  ==  (  64 + q2,   64 + q3)   (bits 4-7, ulp 1/16)
+//   (u & 0x000F000F) | 0x64006400  ==  (1024 + q4, 1024 + q5)
+//   (u & 0x00F000F0) | 0x54005400  ==  (  64 + q6,   64 + q7)
+// in natural k order; subtracting 1032 / 72 gives q - 8 exactly in fp16, and the
+// multiply by the fp16 group scale rounds once (RNE): the reference's definition
+// W = fp16((q - 8) * s).  One shift, four v_and_or_b32, four packed subtracts and four
+// packed multiplies per eight weights.
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t and_or_b32(uint32_t x, uint32_t mask, uint32_t bits) {
+  // (x & mask) | bits in one VALU op; mask from an SGPR, bits from a VGPR (the VOP3
+  // encoding takes one scalar operand and no 32-bit literal).
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(mask), "v"(bits));
+  return r;
+}
+
 __device__ __forceinline__ half8_t dequant8(uint32_t w, half2_t s2) {
-  const half2_t bias = {(half_t)1032.0f, (half_t)1032.0f};
+  const half2_t b_lo = {(half_t)1032.0f, (half_t)1032.0f};
+  const half2_t b_hi = {(half_t)72.0f, (half_t)72.0f};
+  const uint32_t u = w >> 8;
+  half2_t h[4];
+  h[0] = (__builtin_bit_cast(half2_t, and_or_b32(w, 0x000F000Fu, 0x64006400u)) - b_lo) * s2;
+  h[1] = (__builtin_bit_cast(half2_t, and_or_b32(w, 0x00F000F0u, 0x54005400u)) - b_hi) * s2;
+  h[2] = (__builtin_bit_cast(half2_t, and_or_b32(u, 0x000F000Fu, 0x64006400u)) - b_lo) * s2;
+  h[3] = (__builtin_bit_cast(half2_t, and_or_b32(u, 0x00F000F0u, 0x54005400u)) - b_hi) * s2;
   half8_t out;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    uint32_t t = ((w >> (4 * r)) & 0x000F000Fu) | 0x64006400u;
-    half2_t h = __builtin_bit_cast(half2_t, t);
-    h = (h - bias) * s2;
-    out[2 * r] = h[0];
-    out[2 * r + 1] = h[1];
+    out[2 * r] = h[r][0];
+    out[2 * r + 1] = h[r][1];
   }
   return out;
+}
+
+// sum[e] += base[p * stride + e] for p = 0 .. n-1 in ascending order (e = 0..7, fp32 split-K
+// slices).  Loads go out in batches of BATCH before the first add of the batch, so n
+// slices cost ceil(n/BATCH) memory round trips, not n; a slot past n adds +0.0f (sum is
+// never -0.0f).
+template <int BATCH = 8>
+__device__ __forceinline__ void sum_slices8(const float* __restrict__ base, int64_t stride, int n,
+                                            float sum[8]) {
+#pragma clang fp contract(off)
+  for (int b = 0; b < n; b += BATCH) {
+    float4 lo[BATCH], hi[BATCH];
+#pragma unroll
+    for (int u = 0; u < BATCH; ++u) {
+      if (b + u < n) {          // uniform: no load is issued for a missing slice
+        const float4* pp = (const float4*)(base + (int64_t)(b + u) * stride);
+        lo[u] = pp[0];
+        hi[u] = pp[1];
+      } else {
+        lo[u] = hi[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < BATCH; ++u) {
+      const bool on = b + u < n;
+      sum[0] += on ? lo[u].x : 0.f; sum[1] += on ? lo[u].y : 0.f;
+      sum[2] += on ? lo[u].z : 0.f; sum[3] += on ? lo[u].w : 0.f;
+      sum[4] += on ? hi[u].x : 0.f; sum[5] += on ? hi[u].y : 0.f;
+      sum[6] += on ? hi[u].z : 0.f; sum[7] += on ? hi[u].w : 0.f;
+    }
+  }
+}
+
+// Split decode-attention state of one (token, kv head, query head): o[128] (unnormalised,
+// relative to m), m (running max of the base-2 scaled scores), l (sum of exp2(s - m)),
+// two pad floats; records are 16-byte aligned.
+#define ATT_REC 132
+
+// Merge of S split states for dims d0..d0+7: the record of split s sits at
+// rec0 + s * sstride floats.  Splits are merged 8 at a time (every load of a batch in
+// flight before its first use); for S <= 8 this is M = max m_s, l = sum f_s l_s,
+// o = sum f_s o_s (f_s = exp2(m_s - M), split order, fused multiply-adds), fp16(o / l).
+__device__ __forceinline__ half8_t attn_merge8(const float* __restrict__ rec0, int64_t sstride,
+                                               int S, int d0) {
+#pragma clang fp contract(off)
+  float M = -INFINITY, lsum = 0.f;
+  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int b = 0; b < S; b += 8) {
+    float mm[8], ll[8];
+    float4 oa[8], ob[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (b + u < S) {          // uniform: no load is issued for a missing split
+        const float* p = rec0 + (int64_t)(b + u) * sstride;
+        const float2 ml = *(const float2*)(p + 128);
+        mm[u] = ml.x;
+        ll[u] = ml.y;
+        oa[u] = *(const float4*)(p + d0);
+        ob[u] = *(const float4*)(p + d0 + 4);
+      } else {
+        mm[u] = -INFINITY;
+        ll[u] = 0.f;
+        oa[u] = ob[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+    float mb = M;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) mb = fmaxf(mb, mm[u]);
+    if (mb == -INFINITY) continue;
+    const float sc = exp2f(M - mb);            // M = -inf -> 0
+    lsum *= sc;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] *= sc;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (b + u < S) {
+        const float f = exp2f(mm[u] - mb);
+        lsum = fmaf(f, ll[u], lsum);
+        o[0] = fmaf(f, oa[u].x, o[0]); o[1] = fmaf(f, oa[u].y, o[1]);
+        o[2] = fmaf(f, oa[u].z, o[2]); o[3] = fmaf(f, oa[u].w, o[3]);
+        o[4] = fmaf(f, ob[u].x, o[4]); o[5] = fmaf(f, ob[u].y, o[5]);
+        o[6] = fmaf(f, ob[u].z, o[6]); o[7] = fmaf(f, ob[u].w, o[7]);
+      }
+    }
+    M = mb;
+  }
+  half8_t r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = (half_t)(lsum > 0.f ? o[e] / lsum : 0.f);
+  return r;
 }
 
 __device__ __forceinline__ f32x4 mfma16x16x32(half8_t a, half8_t b, f32x4 c) {

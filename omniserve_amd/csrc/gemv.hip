@@ -53,6 +53,10 @@ struct GemvArgs {
   int KS;                // K slices across workgroups
   int KC;                // K per slice (multiple of 128)
   int xl;                // 1: x slice staged in LDS; 0: A fragments read from global
+  // x from split decode-attention states (XS == 1): x[m, h*128 + d] = merge over the aS
+  // splits of the states [M][a_nkv][aS][aG][ATT_REC] of head h (kv head h / aG).
+  const float* apart;
+  int aS, a_nkv, aG;
 };
 
 template <int WF>
@@ -95,7 +99,7 @@ __device__ __forceinline__ half_t finish_store(float v, const GemvArgs& a, int n
 }
 
 // Dynamic LDS: the x tile [MB*16 rows][KC + 8 halfs], reused for the KW reduction.
-template <int WF, int MB, int EPI, int CPW, int CW, int KW, int PF>
+template <int WF, int MB, int EPI, int CPW, int CW, int KW, int PF, int XS = 0>
 __global__ __launch_bounds__(CW * KW * 64) void gemv_kernel(GemvArgs a) {
 #pragma clang fp contract(off)
   static_assert(EPI != EPI_ARGMAX || KW == 1, "argmax epilogue uses every wave of the workgroup");
@@ -138,7 +142,25 @@ __global__ __launch_bounds__(CW * KW * 64) void gemv_kernel(GemvArgs a) {
   }
 
   // 2. stage x[0:M, k0:k0+kc] in LDS (rows >= M zero), 8 loads in flight per thread
-  if (a.xl) {
+  if constexpr (XS == 1) {
+    // merged attention output, one 8-dim chunk per thread and pass
+    const int cpr = kc >> 3;
+    const int total = MB * 16 * cpr;
+    const int64_t sstride = (int64_t)a.aG * ATT_REC;
+    for (int i = threadIdx.x; i < total; i += NW * 64) {
+      const int r = i / cpr;
+      const int c = i - r * cpr;
+      half8_t v = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
+      if (r < a.M) {
+        const int k = k0 + c * 8;
+        const int head = k >> 7;
+        const int gk = head / a.aG;
+        const float* rec0 = a.apart + ((((int64_t)r * a.a_nkv + gk) * a.aS) * a.aG + head % a.aG) * ATT_REC;
+        v = attn_merge8(rec0, sstride, a.aS, k & 127);
+      }
+      *(half8_t*)(xs + r * xstride + c * 8) = v;
+    }
+  } else if (a.xl) {
     const int cpr = kc >> 3;
     const int total = MB * 16 * cpr;
     for (int base = threadIdx.x; base < total; base += 8 * NW * 64) {
@@ -327,7 +349,8 @@ __global__ __launch_bounds__(CW * KW * 64) void gemv_kernel(GemvArgs a) {
 //   1: (1, 8, 1)   8 waves, 8 tiles
 //   2: (1, 4, 4)  16 waves, 4 tiles, K in quarters
 //   3: (2, 4, 2)   8 waves, 8 tiles
-// SiLU (gate/up pairs, CPW = 2): 0: (2, 4, 4), 1: (2, 8, 1), 2: (2, 4, 2), 3: (2, 2, 4).
+// SiLU (gate/up pairs, CPW = 2): 0: (2, 4, 4), 1: (2, 8, 1), 2: (2, 4, 2), 3: (2, 2, 4),
+//   4: (2, 3, 4) (6 tiles: 187 workgroups for the 2B decoder's gate_up), 5: (2, 2, 8).
 // Argmax: (2, 8, 1) (16 tiles).
 // ---------------------------------------------------------------------------
 static size_t max_dynamic_lds() {
@@ -342,18 +365,19 @@ static size_t max_dynamic_lds() {
   return (size_t)cached > 4096 ? (size_t)cached - 4096 : 0;
 }
 
-template <int WF, int MB, int EPI, int CPW, int CW, int KW, int PF>
+template <int WF, int MB, int EPI, int CPW, int CW, int KW, int PF, int XS>
 static int launch_gemv(GemvArgs a, hipStream_t st) {
-  auto kern = gemv_kernel<WF, MB, EPI, CPW, CW, KW, PF>;
+  auto kern = gemv_kernel<WF, MB, EPI, CPW, CW, KW, PF, XS>;
   const size_t lim = max_dynamic_lds();
   const size_t xbytes = (size_t)MB * 16 * (a.KC + 8) * sizeof(half_t);
   const size_t rbytes = (size_t)(KW > 1 ? KW - 1 : 0) * CW * CPW * MB * 256 * sizeof(float);
   a.xl = xbytes <= lim;                         // else A fragments come from global/L2
+  if (XS == 1 && !a.xl) return OMNI_EUNSUPPORTED;   // merged input is staged in LDS only
   const size_t lds = a.xl ? (xbytes > rbytes ? xbytes : rbytes) : rbytes;
   if (lds > lim) return OMNI_EUNSUPPORTED;
   static bool attr_set = false;
   if (!attr_set) {
-    hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lim);
+    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lim);
     attr_set = true;
   }
   const int NT = a.N >> 4;
@@ -364,18 +388,18 @@ static int launch_gemv(GemvArgs a, hipStream_t st) {
   return OMNI_OK;
 }
 
-template <int WF, int EPI, int CPW, int CW, int KW, int PF>
+template <int WF, int EPI, int CPW, int CW, int KW, int PF, int XS = 0>
 static int dispatch_mb(const GemvArgs& a, hipStream_t st) {
   switch ((a.M + 15) / 16) {
-    case 1: return launch_gemv<WF, 1, EPI, CPW, CW, KW, PF>(a, st);
-    case 2: return launch_gemv<WF, 2, EPI, CPW, CW, KW, PF>(a, st);
-    case 3: return launch_gemv<WF, 3, EPI, CPW, CW, KW, PF>(a, st);
-    case 4: return launch_gemv<WF, 4, EPI, CPW, CW, KW, PF>(a, st);
+    case 1: return launch_gemv<WF, 1, EPI, CPW, CW, KW, PF, XS>(a, st);
+    case 2: return launch_gemv<WF, 2, EPI, CPW, CW, KW, PF, XS>(a, st);
+    case 3: return launch_gemv<WF, 3, EPI, CPW, CW, KW, PF, XS>(a, st);
+    case 4: return launch_gemv<WF, 4, EPI, CPW, CW, KW, PF, XS>(a, st);
     default: return OMNI_EUNSUPPORTED;
   }
 }
 
-template <int WF, int EPI>
+template <int WF, int EPI, int XS = 0>
 static int dispatch_preset(const GemvArgs& a, int preset, hipStream_t st) {
   constexpr int PF = WF == W_INT4 ? 4 : 2;
   if constexpr (EPI == EPI_SILU) {
@@ -383,30 +407,44 @@ static int dispatch_preset(const GemvArgs& a, int preset, hipStream_t st) {
       case 1: return dispatch_mb<WF, EPI, 2, 8, 1, PF>(a, st);
       case 2: return dispatch_mb<WF, EPI, 2, 4, 2, PF>(a, st);
       case 3: return dispatch_mb<WF, EPI, 2, 2, 4, PF>(a, st);
+      case 4: return dispatch_mb<WF, EPI, 2, 3, 4, PF>(a, st);
+      case 5: return dispatch_mb<WF, EPI, 2, 2, 8, PF>(a, st);
       default: return dispatch_mb<WF, EPI, 2, 4, 4, PF>(a, st);
     }
   } else if constexpr (EPI == EPI_ARGMAX) {
     return dispatch_mb<WF, EPI, 2, 8, 1, PF>(a, st);
   } else {
     switch (preset) {
-      case 0: return dispatch_mb<WF, EPI, 1, 8, 2, PF>(a, st);
-      case 1: return dispatch_mb<WF, EPI, 1, 8, 1, PF>(a, st);
-      case 2: return dispatch_mb<WF, EPI, 1, 4, 4, PF>(a, st);
-      case 3: return dispatch_mb<WF, EPI, 2, 4, 2, PF>(a, st);
+      case 0: return dispatch_mb<WF, EPI, 1, 8, 2, PF, XS>(a, st);
+      case 1: return dispatch_mb<WF, EPI, 1, 8, 1, PF, XS>(a, st);
+      case 2: return dispatch_mb<WF, EPI, 1, 4, 4, PF, XS>(a, st);
+      case 3: return dispatch_mb<WF, EPI, 2, 4, 2, PF, XS>(a, st);
       default: return OMNI_EINVAL;
     }
   }
 }
 
+struct AttnIn {            // x from split decode-attention states (omni_*_gemm_attn)
+  const float* part;
+  int S, nkv, G;
+};
+
 static int gemv_common(int wf, const void* x, int ldx, const void* w, const void* scales,
                        const void* bias, int bias_after_round, void* out, int ldo,
                        float* partial, int M, int N, int K, int epilogue, int ksplit, int preset,
-                       void* stream) {
+                       void* stream, const AttnIn* ain = nullptr) {
   if (M <= 0 || N <= 0 || K <= 0) return M == 0 ? OMNI_OK : OMNI_EINVAL;
   if (M > 64) return OMNI_EUNSUPPORTED;
   if ((N & 15) || (K & 127)) return OMNI_EUNSUPPORTED;
-  if (!x || !w || (wf == W_INT4 && !scales)) return OMNI_EINVAL;
-  if (ldx < K || (ldx & 7)) return OMNI_EINVAL;
+  if (!w || (wf == W_INT4 && !scales)) return OMNI_EINVAL;
+  if (ain) {
+    if (!ain->part || ain->S < 1 || ain->S > 64 || ain->nkv < 1 || ain->G < 1) return OMNI_EINVAL;
+    if (K != ain->nkv * ain->G * 128) return OMNI_EINVAL;
+    if (epilogue == EPI_SILU) return OMNI_EINVAL;
+  } else {
+    if (!x) return OMNI_EINVAL;
+    if (ldx < K || (ldx & 7)) return OMNI_EINVAL;
+  }
   if (epilogue != EPI_STORE && epilogue != EPI_SILU && epilogue != EPI_PARTIAL) return OMNI_EINVAL;
   if (epilogue == EPI_SILU && (N & 31)) return OMNI_EUNSUPPORTED;   // gate/up tile pairs
   if (preset == 3 && (N & 31)) return OMNI_EUNSUPPORTED;            // 2 tiles per wave
@@ -434,6 +472,17 @@ static int gemv_common(int wf, const void* x, int ldx, const void* w, const void
   a.KC = ((KG + ksplit - 1) / ksplit) * 128;
   a.KS = (K + a.KC - 1) / a.KC;
   hipStream_t st = (hipStream_t)stream;
+  if (ain) {
+    a.apart = ain->part;
+    a.aS = ain->S;
+    a.a_nkv = ain->nkv;
+    a.aG = ain->G;
+    if (wf == W_INT4)
+      return epilogue == EPI_PARTIAL ? dispatch_preset<W_INT4, EPI_PARTIAL, 1>(a, preset, st)
+                                     : dispatch_preset<W_INT4, EPI_STORE, 1>(a, preset, st);
+    return epilogue == EPI_PARTIAL ? dispatch_preset<W_FP16, EPI_PARTIAL, 1>(a, preset, st)
+                                   : dispatch_preset<W_FP16, EPI_STORE, 1>(a, preset, st);
+  }
   if (wf == W_INT4) {
     switch (epilogue) {
       case EPI_SILU: return dispatch_preset<W_INT4, EPI_SILU>(a, preset, st);
@@ -463,6 +512,26 @@ extern "C" int omni_w4a16_gemm(const void* x, int ldx, const void* qweight_packe
                                int epilogue, int ksplit, int preset, void* stream) {
   return gemv_common(W_INT4, x, ldx, qweight_packed, scales_packed, bias, bias_after_round, out,
                      ldo, partial, M, N, K, epilogue, ksplit, preset, stream);
+}
+
+extern "C" int omni_w4a16_gemm_attn(const float* attn_states, int attn_splits, int n_kv_heads,
+                                    int group, const void* qweight_packed,
+                                    const void* scales_packed, const void* bias,
+                                    int bias_after_round, void* out, int ldo, float* partial, int M,
+                                    int N, int K, int epilogue, int ksplit, int preset,
+                                    void* stream) {
+  const AttnIn ain = {attn_states, attn_splits, n_kv_heads, group};
+  return gemv_common(W_INT4, nullptr, 0, qweight_packed, scales_packed, bias, bias_after_round, out,
+                     ldo, partial, M, N, K, epilogue, ksplit, preset, stream, &ain);
+}
+
+extern "C" int omni_f16_gemm_attn(const float* attn_states, int attn_splits, int n_kv_heads,
+                                  int group, const void* weight_packed, const void* bias, void* out,
+                                  int ldo, float* partial, int M, int N, int K, int epilogue,
+                                  int ksplit, int preset, void* stream) {
+  const AttnIn ain = {attn_states, attn_splits, n_kv_heads, group};
+  return gemv_common(W_FP16, nullptr, 0, weight_packed, nullptr, bias, 0, out, ldo, partial, M, N,
+                     K, epilogue, ksplit, preset, stream, &ain);
 }
 
 extern "C" int omni_f16_gemm(const void* x, int ldx, const void* weight_packed, const void* bias,

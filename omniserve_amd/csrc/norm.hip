@@ -141,20 +141,15 @@ __global__ __launch_bounds__(1024) void rownorm_kernel(const half_t* x, const fl
   const bool live = c < nchunk;
   half8_t v = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
   if (live) {
+    const half8_t rv = *(const half8_t*)(residual + (size_t)row * H + c * 8);
     if (PARTS) {
       float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      for (int p = 0; p < nparts; ++p) {
-        const float4* pp = (const float4*)(parts + ((size_t)p * rows + row) * H + c * 8);
-        const float4 lo = pp[0], hi = pp[1];
-        sum[0] += lo.x; sum[1] += lo.y; sum[2] += lo.z; sum[3] += lo.w;
-        sum[4] += hi.x; sum[5] += hi.y; sum[6] += hi.z; sum[7] += hi.w;
-      }
+      sum_slices8<16>(parts + (size_t)row * H + c * 8, (int64_t)rows * H, nparts, sum);
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[e] = (half_t)sum[e];
     } else {
       v = *(const half8_t*)(x + (size_t)row * H + c * 8);
     }
-    const half8_t rv = *(const half8_t*)(residual + (size_t)row * H + c * 8);
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = (half_t)((float)v[e] + (float)rv[e]);
   }

@@ -32,12 +32,7 @@ __device__ __forceinline__ half8_t qkv_chunk(const half_t* row, const QkvParts& 
 #pragma clang fp contract(off)
   if (!qp.parts) return *(const half8_t*)(row + col);
   float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int p = 0; p < qp.nparts; ++p) {
-    const float4* pp = (const float4*)(qp.parts + ((int64_t)p * T + t) * stride + col);
-    const float4 lo = pp[0], hi = pp[1];
-    sum[0] += lo.x; sum[1] += lo.y; sum[2] += lo.z; sum[3] += lo.w;
-    sum[4] += hi.x; sum[5] += hi.y; sum[6] += hi.z; sum[7] += hi.w;
-  }
+  sum_slices8(qp.parts + (int64_t)t * stride + col, (int64_t)T * stride, qp.nparts, sum);
   half8_t v;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {

@@ -27,14 +27,14 @@ MAX_ATTN_SPLITS = 16
 
 def decode_plan(n_tokens: int, n_kv: int, ctx: int) -> tuple:
     """(waves per workgroup, workgroups per (token, kv head)) for omni_decode_attention,
-    from the pool capacity ``ctx``: enough workgroups to reach the 256 CUs when contexts
-    can be long (measured best at 64 groups x 2k context: 8 waves x 3 workgroups); a
-    single workgroup (no partial-state merge launch) when the context is short."""
+    from the pool capacity ``ctx``: one workgroup per CU (256) when contexts can be long,
+    so that every wave's first two K/V blocks are in flight at once; a single workgroup
+    (no partial-state merge launch) when the context is short."""
     groups = max(1, n_tokens * n_kv)
     if ctx <= 128:
         return 4, 1
     waves = 8 if groups >= 32 else 4
-    splits = max(1, min(MAX_ATTN_SPLITS, 192 // groups, ctx // 128))
+    splits = max(1, min(MAX_ATTN_SPLITS, 256 // groups, ctx // 128))
     return waves, splits
 
 
@@ -59,7 +59,7 @@ class PreallocatedKVCache:
         # partial softmax states of split decode attention (shared by all layers: launches
         # on one stream are ordered)
         G = self.n_heads // n_kv_heads
-        self._attn_ws = torch.empty(max_batch * n_kv_heads * MAX_ATTN_SPLITS * G * (head_dim + 2),
+        self._attn_ws = torch.empty(max_batch * n_kv_heads * MAX_ATTN_SPLITS * G * (head_dim + 4),
                                     device=device, dtype=torch.float32)
         self.attn_plan = None      # (waves, splits) override; None = decode_plan()
 
@@ -160,11 +160,15 @@ class CacheView:
                                 self.n, scale, plan=plan)
 
     def attend_fused(self, qparts, nparts: int, bias, bias_after_round: bool, layer_idx: int,
-                     scale: float, cos_tab, sin_tab, mrope_section, out,
-                     plan: tuple | None = None) -> torch.Tensor:
+                     scale: float, cos_tab, sin_tab, mrope_section, out=None,
+                     plan: tuple | None = None):
         """Decode attention fused with its producer's epilogue: q / new k, v from the qkv
         projection's fp32 split-K partials (+ bias), M-RoPE at lengths[row] + rope_delta,
-        new K/V row stored at lengths[row], attention over keys [0, lengths[row]]."""
+        new K/V row stored at lengths[row], attention over keys [0, lengths[row]].
+
+        With ``out`` the merged fp16 output goes there and is returned; without it the
+        split softmax states stay in the pool's workspace and (states, splits) is returned
+        for the o_proj that merges them (forward_partial_attn)."""
         pool, n = self.pool, self.n
         w, s = plan or pool.attn_plan or decode_plan(n, pool.n_kv_heads, pool.max_len)
         s0, s1, s2 = mrope_section
@@ -172,8 +176,8 @@ class CacheView:
              ptr(cos_tab), ptr(sin_tab), cos_tab.shape[0], ptr(self.rope_delta), s0, s1, s2,
              ptr(pool.k[layer_idx]), ptr(pool.v[layer_idx]), pool.max_batch, pool.max_len, None,
              ptr(pool.lengths), ptr(out), n, pool.n_heads, pool.n_kv_heads, pool.head_dim,
-             float(scale), w, s, ptr(pool._attn_ws), stream())
-        return out
+             float(scale), w, s, ptr(pool._attn_ws), int(out is not None), stream())
+        return out if out is not None else (pool._attn_ws, s)
 
     def flash_decode(self, q, key, value, layer_idx, scale):
         """Reference protocol (kv_prealloc.py:272-290): q [n, nh, hd] (rotated), key/value

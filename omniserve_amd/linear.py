@@ -39,13 +39,13 @@ MAX_SKINNY_M = 64
 # SiLU: 0 = (2, 4, 4), 1 = (2, 8, 1), 2 = (2, 4, 2), 3 = (2, 2, 4).
 PLANS: Dict[Tuple[str, int, int], Tuple[int, int, int]] = {
     ("int4", 1536, 2048): (2, 2, 7),
-    ("int4", 1536, 1536): (2, 2, 10),
+    ("int4", 1536, 1536): (2, 1, 12),     # o_proj: one head per K slice (attention merge)
     ("int4", 8960, 1536): (2, 2, 10),
-    ("int4", 1536, 17920): (0, 2, 1),     # SiLU-fused gate_up: preset 0 = (2, 4, 4)
+    ("int4", 1536, 17920): (4, 2, 1),     # SiLU-fused gate_up: preset 4 = (2, 3, 4)
     ("fp16", 1536, 2048): (2, 2, 7),
-    ("fp16", 1536, 1536): (2, 2, 10),
+    ("fp16", 1536, 1536): (2, 1, 12),
     ("fp16", 8960, 1536): (2, 2, 10),
-    ("fp16", 1536, 17920): (0, 2, 1),
+    ("fp16", 1536, 17920): (4, 2, 1),
 }
 
 
@@ -102,6 +102,28 @@ class _Skinny(nn.Module):
                    self.partial_preset if preset is None else preset)
         return S
 
+    def forward_partial_attn(self, states: torch.Tensor, splits: int, n_kv: int, group: int,
+                             M: int, partial: torch.Tensor, ksplit: int | None = None,
+                             preset: int | None = None) -> int:
+        """forward_partial with x = the merge of the decode attention's split states
+        [M][n_kv][splits][group][132] (omni_decode_attention_fused, merge = 0)."""
+        if self.fuse_silu:
+            raise ValueError("the SiLU-fused projection has no partial form")
+        if M > MAX_SKINNY_M:
+            raise ValueError(f"partial sums support up to {MAX_SKINNY_M} rows")
+        ks = ksplit or self.partial_ksplit
+        S = self.partial_slices(ks)
+        if partial.numel() < S * M * self.N or partial.dtype != torch.float32:
+            raise ValueError("partial buffer too small or not fp32")
+        if states.dtype != torch.float32 or states.numel() < M * n_kv * splits * group * 132:
+            raise ValueError("attention state buffer too small or not fp32")
+        self._call_attn(states, splits, n_kv, group, M, partial, EPI_PARTIAL, ks,
+                        self.partial_preset if preset is None else preset)
+        return S
+
+    def _call_attn(self, states, splits, n_kv, group, M, partial, epilogue, ksplit, preset):
+        raise NotImplementedError
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         x2d = x.reshape(-1, self.K)
         if not x2d.is_contiguous():
@@ -146,6 +168,11 @@ class GPTQLinear(_Skinny):
              0 if out is None else out.stride(0), ptr(partial), x2d.shape[0], self.N, self.K,
              epilogue, ksplit, preset, stream())
 
+    def _call_attn(self, states, splits, n_kv, group, M, partial, epilogue, ksplit, preset):
+        call("omni_w4a16_gemm_attn", ptr(states), splits, n_kv, group, ptr(self.qweight_packed),
+             ptr(self.scales_packed), ptr(self.bias), 1, None, 0, ptr(partial), M, self.N,
+             self.K, epilogue, ksplit, preset, stream())
+
     def dequantized(self) -> torch.Tensor:
         """W^T [K, N] fp16 as the kernels see it (columns in packed order)."""
         w = torch.empty(self.K, self.N, device=self.qweight_packed.device, dtype=torch.float16)
@@ -181,6 +208,11 @@ class F16Linear(_Skinny):
         call("omni_f16_gemm", ptr(x2d), x2d.stride(0), ptr(self.weight_packed), ptr(self.bias),
              ptr(out), 0 if out is None else out.stride(0), ptr(partial), x2d.shape[0], self.N,
              self.K, epilogue, ksplit, preset, stream())
+
+    def _call_attn(self, states, splits, n_kv, group, M, partial, epilogue, ksplit, preset):
+        call("omni_f16_gemm_attn", ptr(states), splits, n_kv, group, ptr(self.weight_packed),
+             ptr(self.bias), None, 0, ptr(partial), M, self.N, self.K, epilogue, ksplit, preset,
+             stream())
 
 
 class LMHeadArgmax(nn.Module):

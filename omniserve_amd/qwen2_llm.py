@@ -174,11 +174,12 @@ class Qwen2LLM(nn.Module):
         With ``lengths`` the final launch also advances lengths[:n] by one and with
         ``next_ids`` copies the new ids there.  No allocation, no host sync.
 
-        Per layer (7 launches, 8 with split attention): add+RMSNorm over the previous
-        down projection's fp32 split-K partials -> qkv (partials) -> attention with the
-        qkv bias + M-RoPE + KV-pool write in its prologue -> o_proj (partials) ->
-        add+RMSNorm over them -> gate_up + SiLU -> down (partials).  Partial sums cross a
-        kernel boundary, never a device-scope fence."""
+        Per layer (7 launches): add+RMSNorm over the previous down projection's fp32
+        split-K partials -> qkv (partials) -> attention with the qkv bias + M-RoPE +
+        KV-pool write in its prologue, split softmax states out -> o_proj merging those
+        states while it stages its input (partials) -> add+RMSNorm over them -> gate_up +
+        SiLU -> down (partials).  Partial results cross a kernel boundary, never a
+        device-scope fence."""
         cfg = self.cfg
         n = ids.shape[0]
         b = self.decode_buffers(n, ids.device)
@@ -192,9 +193,11 @@ class Qwen2LLM(nn.Module):
                 F.add_rms_norm_partials_out(b["dpart"], S, res, layer.in_norm, eps, h, res)
             qp = layer.qkv_proj
             Sq = qp.forward_partial(h, b["qpart"])
-            view.attend_fused(b["qpart"], Sq, qp.bias, qp.fmt == "int4", i, self.scale,
-                              self.rope_cos, self.rope_sin, cfg.mrope_section, b["attn"])
-            So = layer.o_proj.forward_partial(b["attn"], b["opart"])
+            states, Sa = view.attend_fused(b["qpart"], Sq, qp.bias, qp.fmt == "int4", i,
+                                           self.scale, self.rope_cos, self.rope_sin,
+                                           cfg.mrope_section)
+            So = layer.o_proj.forward_partial_attn(states, Sa, cfg.num_kv_heads,
+                                                   cfg.num_heads // cfg.num_kv_heads, n, b["opart"])
             F.add_rms_norm_partials_out(b["opart"], So, res, layer.post_norm, eps, h, res)
             layer.gate_up_proj.forward_out(h, b["act"])
             S = layer.down_proj.forward_partial(b["act"], b["dpart"])

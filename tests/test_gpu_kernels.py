@@ -178,7 +178,7 @@ def test_decode_attention(gpu, lengths, waves, splits):
     out = torch.empty(n, nh, hd, device=gpu, dtype=torch.float16)
     scale = hd ** -0.5
     kg, vg, qg, Lg = kp.to(gpu), vp.to(gpu), q.to(gpu), L.to(gpu)
-    ws = torch.empty(n * nkv * splits * 6 * 130, device=gpu, dtype=torch.float32)
+    ws = torch.empty(n * nkv * splits * 6 * 132, device=gpu, dtype=torch.float32)
     call("omni_decode_attention", ptr(qg), nh * hd, ptr(kg), ptr(vg), P, ML, None, ptr(Lg), 0, 0,
          ptr(out), n, nh, nkv, hd, scale, waves, splits, ptr(ws), stream())
     torch.cuda.synchronize()
@@ -437,11 +437,11 @@ def test_decode_attention_fused_equals_unfused(gpu, bias_after_round, splits, le
     for mode in ("fused", "separate"):
         kc, vc = kp0.to(gpu), vp0.to(gpu)
         out = torch.empty(n, nh, hd, device=gpu, dtype=torch.float16)
-        ws = torch.empty(n * nkv * splits * 6 * 130, device=gpu, dtype=torch.float32)
+        ws = torch.empty(n * nkv * splits * 6 * 132, device=gpu, dtype=torch.float32)
         if mode == "fused":
             call("omni_decode_attention_fused", ptr(parts), S, ptr(bias), bias_after_round,
                  ptr(cos), ptr(sin), 8192, ptr(delta), 16, 24, 24, ptr(kc), ptr(vc), P, ML, None,
-                 ptr(lens), ptr(out), n, nh, nkv, hd, hd ** -0.5, 8, splits, ptr(ws), stream())
+                 ptr(lens), ptr(out), n, nh, nkv, hd, hd ** -0.5, 8, splits, ptr(ws), 1, stream())
         else:
             qkv = torch.empty(n, W, device=gpu, dtype=torch.float16)
             call("omni_mrope_kv_write_partials", ptr(qkv), W, ptr(parts), S, ptr(bias),
@@ -453,3 +453,50 @@ def test_decode_attention_fused_equals_unfused(gpu, bias_after_round, splits, le
         outs.append((out.cpu(), kc.cpu(), vc.cpu()))
     for a, b in zip(outs[0], outs[1]):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("fmt,splits", [("int4", 4), ("int4", 1), ("fp16", 3), ("int4", 11)])
+def test_oproj_merges_attention_states(gpu, fmt, splits):
+    """o_proj reading the decode attention's split states (merge in its input staging)
+    gives exactly merge launch + o_proj on the merged fp16 output."""
+    from omniserve_amd._lib import call, ptr, stream
+    from omniserve_amd.linear import F16Linear, GPTQLinear
+    from omniserve_amd.qwen2_llm import rope_tables
+    from omniserve_amd.synth import gptq_random
+    say(f"o_proj from attention states fmt={fmt} splits={splits}")
+    cfg = ref.Qwen2Config()
+    nh, nkv, hd, ML, H = 12, 2, 128, 4096, 1536
+    lengths = [2047, 31, 0, 500, 1300, 7, 64, 129] * 4
+    n = len(lengths)
+    P = n + 1
+    W = (nh + 2 * nkv) * hd
+    g = torch.Generator().manual_seed(130)
+    parts = (torch.randn(6, n, W, generator=g) * 0.3).to(gpu)
+    bias = f16((W,), 131, 0.02).to(gpu)
+    delta = torch.zeros(P, dtype=torch.int64).to(gpu)
+    kc = f16((P, ML, nkv, hd), 132).to(gpu)
+    vc = f16((P, ML, nkv, hd), 133).to(gpu)
+    lens = torch.tensor(lengths + [0], dtype=torch.int64).to(gpu)
+    cos, sin = rope_tables(cfg, 8192, gpu)
+    if fmt == "int4":
+        qw, sc = gptq_random(H, H, 134, "oproj")
+        lin = GPTQLinear(qw.to(gpu), sc.to(gpu))
+    else:
+        lin = F16Linear(f16((H, H), 135, 0.02).to(gpu))
+    ws = torch.empty(n * nkv * splits * 6 * 132, device=gpu, dtype=torch.float32)
+    out = torch.empty(n, nh, hd, device=gpu, dtype=torch.float16)
+    S_o = lin.partial_slices()
+    pa = torch.empty(S_o * n * H, device=gpu, dtype=torch.float32)
+    pb = torch.empty_like(pa)
+
+    def attn(merge):
+        call("omni_decode_attention_fused", ptr(parts), 6, ptr(bias), 1, ptr(cos), ptr(sin), 8192,
+             ptr(delta), 16, 24, 24, ptr(kc), ptr(vc), P, ML, None, ptr(lens),
+             ptr(out) if merge else None, n, nh, nkv, hd, hd ** -0.5, 8, splits, ptr(ws), merge,
+             stream())
+    attn(0)
+    lin.forward_partial_attn(ws, splits, nkv, nh // nkv, n, pa)
+    attn(1)                       # same K/V row rewritten with the same values
+    lin.forward_partial(out, pb)
+    torch.cuda.synchronize()
+    assert torch.equal(pa, pb)

@@ -137,7 +137,7 @@ def test_decode_plan_and_split_counts():
         for ctx in (64, 256, 1024, 4096):
             w, s = decode_plan(n, 2, ctx)
             assert w in (4, 8, 16) and 1 <= s <= MAX_ATTN_SPLITS
-    assert decode_plan(32, 2, 4096)[1] == 3
+    assert decode_plan(32, 2, 4096) == (8, 4)
     from omniserve_amd._lib import lib
     assert lib().omni_gemm_slices(8960, 10) == 10
     assert lib().omni_gemm_slices(1536, 10) == 6

@@ -175,54 +175,75 @@ __device__ __forceinline__ void sum_slices8(const float* __restrict__ base, int6
 // rec0 + s * sstride floats.  Splits are merged 8 at a time (every load of a batch in
 // flight before its first use); for S <= 8 this is M = max m_s, l = sum f_s l_s,
 // o = sum f_s o_s (f_s = exp2(m_s - M), split order, fused multiply-adds), fp16(o / l).
-__device__ __forceinline__ half8_t attn_merge8(const float* __restrict__ rec0, int64_t sstride,
-                                               int S, int d0) {
-#pragma clang fp contract(off)
+struct Merge8Loads {
+  float mm[8], ll[8];
+  float4 oa[8], ob[8];
+};
+struct Merge8State {
   float M = -INFINITY, lsum = 0.f;
   float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int b = 0; b < S; b += 8) {
-    float mm[8], ll[8];
-    float4 oa[8], ob[8];
+};
+
+// Issue the loads of splits b .. min(b + 8, S) - 1.
+__device__ __forceinline__ void attn_merge8_issue(Merge8Loads& L, const float* __restrict__ rec0,
+                                                  int64_t sstride, int b, int S, int d0) {
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      if (b + u < S) {          // uniform: no load is issued for a missing split
-        const float* p = rec0 + (int64_t)(b + u) * sstride;
-        const float2 ml = *(const float2*)(p + 128);
-        mm[u] = ml.x;
-        ll[u] = ml.y;
-        oa[u] = *(const float4*)(p + d0);
-        ob[u] = *(const float4*)(p + d0 + 4);
-      } else {
-        mm[u] = -INFINITY;
-        ll[u] = 0.f;
-        oa[u] = ob[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-      }
+  for (int u = 0; u < 8; ++u) {
+    if (b + u < S) {          // uniform: no load is issued for a missing split
+      const float* p = rec0 + (int64_t)(b + u) * sstride;
+      const float2 ml = *(const float2*)(p + 128);
+      L.mm[u] = ml.x;
+      L.ll[u] = ml.y;
+      L.oa[u] = *(const float4*)(p + d0);
+      L.ob[u] = *(const float4*)(p + d0 + 4);
+    } else {
+      L.mm[u] = -INFINITY;
+      L.ll[u] = 0.f;
+      L.oa[u] = L.ob[u] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    float mb = M;
-#pragma unroll
-    for (int u = 0; u < 8; ++u) mb = fmaxf(mb, mm[u]);
-    if (mb == -INFINITY) continue;
-    const float sc = exp2f(M - mb);            // M = -inf -> 0
-    lsum *= sc;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] *= sc;
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      if (b + u < S) {
-        const float f = exp2f(mm[u] - mb);
-        lsum = fmaf(f, ll[u], lsum);
-        o[0] = fmaf(f, oa[u].x, o[0]); o[1] = fmaf(f, oa[u].y, o[1]);
-        o[2] = fmaf(f, oa[u].z, o[2]); o[3] = fmaf(f, oa[u].w, o[3]);
-        o[4] = fmaf(f, ob[u].x, o[4]); o[5] = fmaf(f, ob[u].y, o[5]);
-        o[6] = fmaf(f, ob[u].z, o[6]); o[7] = fmaf(f, ob[u].w, o[7]);
-      }
-    }
-    M = mb;
   }
+}
+
+__device__ __forceinline__ void attn_merge8_batch(Merge8State& st, const Merge8Loads& L, int nvalid) {
+#pragma clang fp contract(off)
+  float mb = st.M;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) mb = fmaxf(mb, L.mm[u]);
+  if (mb == -INFINITY) return;
+  const float sc = exp2f(st.M - mb);          // M = -inf -> 0
+  st.lsum *= sc;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) st.o[e] *= sc;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    if (u < nvalid) {
+      const float f = exp2f(L.mm[u] - mb);
+      st.lsum = fmaf(f, L.ll[u], st.lsum);
+      st.o[0] = fmaf(f, L.oa[u].x, st.o[0]); st.o[1] = fmaf(f, L.oa[u].y, st.o[1]);
+      st.o[2] = fmaf(f, L.oa[u].z, st.o[2]); st.o[3] = fmaf(f, L.oa[u].w, st.o[3]);
+      st.o[4] = fmaf(f, L.ob[u].x, st.o[4]); st.o[5] = fmaf(f, L.ob[u].y, st.o[5]);
+      st.o[6] = fmaf(f, L.ob[u].z, st.o[6]); st.o[7] = fmaf(f, L.ob[u].w, st.o[7]);
+    }
+  }
+  st.M = mb;
+}
+
+__device__ __forceinline__ half8_t attn_merge8_result(const Merge8State& st) {
   half8_t r;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) r[e] = (half_t)(lsum > 0.f ? o[e] / lsum : 0.f);
+  for (int e = 0; e < 8; ++e) r[e] = (half_t)(st.lsum > 0.f ? st.o[e] / st.lsum : 0.f);
   return r;
+}
+
+__device__ __forceinline__ half8_t attn_merge8(const float* __restrict__ rec0, int64_t sstride,
+                                               int S, int d0) {
+  Merge8State st;
+  for (int b = 0; b < S; b += 8) {
+    Merge8Loads L;
+    attn_merge8_issue(L, rec0, sstride, b, S, d0);
+    attn_merge8_batch(st, L, S - b);
+  }
+  return attn_merge8_result(st);
 }
 
 __device__ __forceinline__ f32x4 mfma16x16x32(half8_t a, half8_t b, f32x4 c) {

@@ -34,6 +34,8 @@
 //                arrays reduced by omni_argmax_finalize.
 #include "common.h"
 
+#include <type_traits>
+
 enum { W_INT4 = 0, W_FP16 = 1 };
 enum { EPI_STORE = 0, EPI_SILU = 1, EPI_PARTIAL = 2, EPI_ARGMAX = 3 };
 
@@ -71,20 +73,34 @@ struct WFrag<W_FP16> {
   half8_t h[4];
 };
 
+// Per-wave weight stream of one column tile: fragments of consecutive k-groups.
 template <int WF>
-__device__ __forceinline__ void load_frag(WFrag<WF>& f, const GemvArgs& a, int nt, int kg, int lane) {
-  if constexpr (WF == W_INT4) {
-    const int KG = a.K >> 7;
-    const int64_t blk = (int64_t)nt * KG + kg;
-    f.q = __builtin_nontemporal_load((const u32x4*)a.w + blk * 64 + lane);
-    f.s = a.scales[blk * 16 + (lane & 15)];
-  } else {
-    const int KS32 = a.K >> 5;
-    const half8_t* wp = (const half8_t*)a.w + ((int64_t)nt * KS32 + kg * 4) * 64 + lane;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) f.h[j] = __builtin_nontemporal_load(wp + j * 64);
+struct WStream;
+template <>
+struct WStream<W_INT4> {
+  const u32x4* q;      // group g at q + 64 g
+  const half_t* s;     // group g at s + 16 g
+  __device__ void init(const GemvArgs& a, int nt, int kg0, int lane) {
+    const int64_t blk = (int64_t)nt * (a.K >> 7) + kg0;
+    q = (const u32x4*)a.w + blk * 64 + lane;
+    s = a.scales + blk * 16 + (lane & 15);
   }
-}
+  __device__ __forceinline__ void load(WFrag<W_INT4>& f, int g) const {
+    f.q = __builtin_nontemporal_load(q + g * 64);
+    f.s = s[g * 16];
+  }
+};
+template <>
+struct WStream<W_FP16> {
+  const half8_t* h;    // group g, sub-block j at h + (4 g + j) * 64
+  __device__ void init(const GemvArgs& a, int nt, int kg0, int lane) {
+    h = (const half8_t*)a.w + ((int64_t)nt * (a.K >> 5) + kg0 * 4) * 64 + lane;
+  }
+  __device__ __forceinline__ void load(WFrag<W_FP16>& f, int g) const {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f.h[j] = __builtin_nontemporal_load(h + (4 * g + j) * 64);
+  }
+};
 
 __device__ __forceinline__ float silu_ref(float g) { return g * (1.0f / (1.0f + __expf(-g))); }
 
@@ -131,59 +147,122 @@ __global__ __launch_bounds__(CW * KW * 64) void gemv_kernel(GemvArgs a) {
   const int tile0 = ng * NT_WG + cw * CPW;
   const bool active = tile0 < NT;
 
-  // 1. first weight loads in flight before x is staged
-  WFrag<WF> buf[PF][CPW];
-  if (active) {
-#pragma unroll
-    for (int p = 0; p < PF; ++p)
-      if (p < myg)
-#pragma unroll
-        for (int c = 0; c < CPW; ++c) load_frag<WF>(buf[p][c], a, tile0 + c, kg0 + p, lane);
-  }
+  // x chunk (row r, 8-column chunk c) of the staged slice for flat index i = r*cpr + c:
+  // the thread's first index is threadIdx.x and it advances by a whole workgroup each
+  // step, so (r, c) is stepped instead of divided (one division per thread).
+  const int cpr = kc >> 3;
+  const int xtotal = MB * 16 * cpr;
+  constexpr int NTH = NW * 64;
+  const int step_r = NTH / cpr;
+  const int step_c = NTH - step_r * cpr;
+  int xr = threadIdx.x / cpr;
+  int xc = threadIdx.x - xr * cpr;
+  auto xstep = [&]() {
+    xc += step_c;
+    xr += step_r;
+    if (xc >= cpr) {
+      xc -= cpr;
+      ++xr;
+    }
+  };
 
-  // 2. stage x[0:M, k0:k0+kc] in LDS (rows >= M zero), 8 loads in flight per thread
+  // 1. The first batch of x loads goes out before the weight loads: x is small and
+  //    cache-resident, and loads retire in issue order, so staging it never waits on
+  //    the weight stream.  The code is branch-free (clamped addresses, selects at the
+  //    store) so that the compiler's wait counts stay exact; a chunk past the slice is
+  //    marked with the row-0 pad offset (KC) and not stored.
+  half8_t xv[8];
+  int xo[8];
+  bool xlive[8];
+  const bool x_single = XS == 1 ? (xtotal <= NTH && a.aS <= 8) : true;
+  Merge8Loads ml;
+  int m_rec = a.KC;                             // XS: LDS offset of this thread's chunk
+  bool m_live = false;
   if constexpr (XS == 1) {
-    // merged attention output, one 8-dim chunk per thread and pass
-    const int cpr = kc >> 3;
-    const int total = MB * 16 * cpr;
-    const int64_t sstride = (int64_t)a.aG * ATT_REC;
-    for (int i = threadIdx.x; i < total; i += NW * 64) {
-      const int r = i / cpr;
-      const int c = i - r * cpr;
-      half8_t v = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
-      if (r < a.M) {
-        const int k = k0 + c * 8;
-        const int head = k >> 7;
-        const int gk = head / a.aG;
-        const float* rec0 = a.apart + ((((int64_t)r * a.a_nkv + gk) * a.aS) * a.aG + head % a.aG) * ATT_REC;
-        v = attn_merge8(rec0, sstride, a.aS, k & 127);
-      }
-      *(half8_t*)(xs + r * xstride + c * 8) = v;
+    if (x_single) {
+      const bool ok = (int)threadIdx.x < xtotal;
+      m_live = ok && xr < a.M;
+      m_rec = ok ? xr * xstride + xc * 8 : a.KC;
+      const int rr = m_live ? xr : 0;
+      const int k = k0 + (ok ? xc : 0) * 8;
+      const int head = k >> 7;
+      const float* rec0 = a.apart + ((((int64_t)rr * a.a_nkv + head / a.aG) * a.aS) * a.aG +
+                                     head % a.aG) * ATT_REC;
+      attn_merge8_issue(ml, rec0, (int64_t)a.aG * ATT_REC, 0, a.aS, k & 127);
     }
   } else if (a.xl) {
-    const int cpr = kc >> 3;
-    const int total = MB * 16 * cpr;
-    for (int base = threadIdx.x; base < total; base += 8 * NW * 64) {
-      half8_t v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const bool ok = (int)threadIdx.x + u * NTH < xtotal;
+      xlive[u] = ok && xr < a.M;
+      const int rr = xlive[u] ? xr : 0;
+      const int cc = ok ? xc : 0;
+      xv[u] = *(const half8_t*)(a.x + (int64_t)rr * a.ldx + k0 + cc * 8);
+      xo[u] = ok ? xr * xstride + xc * 8 : a.KC;
+      xstep();
+    }
+  }
+
+  // 2. weight loads: PF groups of every tile in flight.  Issued unconditionally (tiles
+  //    and groups past the end re-read the last valid one) so the wait counts of the
+  //    code below are exact instead of assuming the worst case.
+  WStream<WF> ws[CPW];
+  WFrag<WF> buf[PF][CPW];
+  {
+    // a wave without groups re-reads the slice's first group (loaded by wave kw = 0,
+    // so it is served from cache, not HBM)
+    const int gmax = myg > 0 ? myg - 1 : 0;
+    const int kgb = myg > 0 ? kg0 : (k0 >> 7);
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) ws[c].init(a, min(tile0 + c, NT - 1), kgb, lane);
+#pragma unroll
+    for (int p = 0; p < PF; ++p)
+#pragma unroll
+      for (int c = 0; c < CPW; ++c) ws[c].load(buf[p][c], min(p, gmax));
+  }
+
+  // 3. finish staging x[0:M, k0:k0+kc] in LDS (rows >= M zero)
+  const half8_t zero8 = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
+  if constexpr (XS == 1) {
+    if (x_single) {
+      Merge8State st;
+      attn_merge8_batch(st, ml, a.aS);
+      if (m_rec != a.KC) *(half8_t*)(xs + m_rec) = m_live ? attn_merge8_result(st) : zero8;
+    } else {
+      const int64_t sstride = (int64_t)a.aG * ATT_REC;
+      for (int i = threadIdx.x; i < xtotal; i += NTH) {
+        half8_t v = zero8;
+        if (xr < a.M) {
+          const int k = k0 + xc * 8;
+          const int head = k >> 7;
+          const float* rec0 = a.apart + ((((int64_t)xr * a.a_nkv + head / a.aG) * a.aS) * a.aG +
+                                         head % a.aG) * ATT_REC;
+          v = attn_merge8(rec0, sstride, a.aS, k & 127);
+        }
+        *(half8_t*)(xs + xr * xstride + xc * 8) = v;
+        xstep();
+      }
+    }
+  } else if (a.xl) {
+    // (a chunk past the slice stores nothing: many lanes writing one pad address would
+    // serialise on its LDS bank)
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (xo[u] != a.KC) *(half8_t*)(xs + xo[u]) = xlive[u] ? xv[u] : zero8;
+    for (int base = threadIdx.x + 8 * NTH; base < xtotal; base += 8 * NTH) {
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const int i = base + u * NW * 64;
-        v[u] = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
-        if (i < total) {
-          const int r = i / cpr;
-          const int c = i - r * cpr;
-          if (r < a.M) v[u] = *(const half8_t*)(a.x + (int64_t)r * a.ldx + k0 + c * 8);
-        }
+        const bool ok = base + u * NTH < xtotal;
+        xlive[u] = ok && xr < a.M;
+        const int rr = xlive[u] ? xr : 0;
+        const int cc = ok ? xc : 0;
+        xv[u] = *(const half8_t*)(a.x + (int64_t)rr * a.ldx + k0 + cc * 8);
+        xo[u] = ok ? xr * xstride + xc * 8 : a.KC;
+        xstep();
       }
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int i = base + u * NW * 64;
-        if (i < total) {
-          const int r = i / cpr;
-          const int c = i - r * cpr;
-          *(half8_t*)(xs + r * xstride + c * 8) = v[u];
-        }
-      }
+      for (int u = 0; u < 8; ++u)
+        if (xo[u] != a.KC) *(half8_t*)(xs + xo[u]) = xlive[u] ? xv[u] : zero8;
     }
   }
   __syncthreads();
@@ -195,48 +274,58 @@ __global__ __launch_bounds__(CW * KW * 64) void gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[c][mb] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-  if (active) {
-    for (int base = 0; base < myg; base += PF) {
+  // The A-fragment source is chosen once, outside the loop: a runtime branch inside it
+  // makes the compiler wait for every outstanding weight load at each fragment read.
+  auto stream_weights = [&](auto xl_const) {
+    constexpr bool XL = decltype(xl_const)::value;
+    auto group = [&](WFrag<WF>(&fr)[CPW], int i) {
+      const int kl = (g_beg + i) * 128;           // k offset inside the staged slice
 #pragma unroll
-      for (int p = 0; p < PF; ++p) {
-        const int i = base + p;
-        if (i < myg) {
-          WFrag<WF> cur[CPW];
+      for (int j = 0; j < 4; ++j) {
+        half8_t af[MB];
 #pragma unroll
-          for (int c = 0; c < CPW; ++c) cur[c] = buf[p][c];
-          if (i + PF < myg)
-#pragma unroll
-            for (int c = 0; c < CPW; ++c) load_frag<WF>(buf[p][c], a, tile0 + c, kg0 + i + PF, lane);
-          const int kl = (g_beg + i) * 128;     // k offset inside the staged slice
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            half8_t af[MB];
-#pragma unroll
-            for (int mb = 0; mb < MB; ++mb) {
-              if (a.xl) {
-                af[mb] = *(const half8_t*)(xs + (16 * mb + c16) * xstride + kl + 32 * j + 8 * q16);
-              } else {
-                const int m = 16 * mb + c16;
-                af[mb] = m < a.M ? *(const half8_t*)(a.x + (int64_t)m * a.ldx + k0 + kl + 32 * j + 8 * q16)
-                                 : (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
-              }
-            }
-#pragma unroll
-            for (int c = 0; c < CPW; ++c) {
-              half8_t bf;
-              if constexpr (WF == W_INT4) {
-                const half2_t s2 = {cur[c].s, cur[c].s};
-                bf = dequant8(cur[c].q[j], s2);
-              } else {
-                bf = cur[c].h[j];
-              }
-#pragma unroll
-              for (int mb = 0; mb < MB; ++mb) acc[c][mb] = mfma16x16x32(af[mb], bf, acc[c][mb]);
-            }
+        for (int mb = 0; mb < MB; ++mb) {
+          if constexpr (XL) {
+            af[mb] = *(const half8_t*)(xs + (16 * mb + c16) * xstride + kl + 32 * j + 8 * q16);
+          } else {
+            const int m = 16 * mb + c16;
+            af[mb] = m < a.M ? *(const half8_t*)(a.x + (int64_t)m * a.ldx + k0 + kl + 32 * j + 8 * q16)
+                             : (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
           }
         }
+#pragma unroll
+        for (int c = 0; c < CPW; ++c) {
+          half8_t bf;
+          if constexpr (WF == W_INT4) {
+            const half2_t s2 = {fr[c].s, fr[c].s};
+            bf = dequant8(fr[c].q[j], s2);
+          } else {
+            bf = fr[c].h[j];
+          }
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb) acc[c][mb] = mfma16x16x32(af[mb], bf, acc[c][mb]);
+        }
       }
+    };
+    // The prefetched groups are consumed in straight-line code (a loop carrying the
+    // fragment registers would copy them at entry, waiting for every load first).
+#pragma unroll
+    for (int p = 0; p < PF; ++p)
+      if (p < myg) group(buf[p], p);
+    // Groups beyond the prefetch depth (long K per wave): load a batch, then use it.
+    for (int base = PF; base < myg; base += PF) {
+#pragma unroll
+      for (int p = 0; p < PF; ++p)
+#pragma unroll
+        for (int c = 0; c < CPW; ++c) ws[c].load(buf[p][c], min(base + p, myg - 1));
+#pragma unroll
+      for (int p = 0; p < PF; ++p)
+        if (base + p < myg) group(buf[p], base + p);
     }
+  };
+  if (active) {
+    if (XS == 1 || a.xl) stream_weights(std::true_type{});
+    else stream_weights(std::false_type{});
   }
 
   // 4. sum the KW partial accumulators in LDS, in kw order
@@ -401,7 +490,7 @@ static int dispatch_mb(const GemvArgs& a, hipStream_t st) {
 
 template <int WF, int EPI, int XS = 0>
 static int dispatch_preset(const GemvArgs& a, int preset, hipStream_t st) {
-  constexpr int PF = WF == W_INT4 ? 4 : 2;
+  constexpr int PF = 4;
   if constexpr (EPI == EPI_SILU) {
     switch (preset) {
       case 1: return dispatch_mb<WF, EPI, 2, 8, 1, PF>(a, st);

@@ -38,13 +38,13 @@ MAX_SKINNY_M = 64
 # in-group K split): 0 = (1, 8, 2), 1 = (1, 8, 1), 2 = (1, 4, 4), 3 = (2, 4, 2);
 # SiLU: 0 = (2, 4, 4), 1 = (2, 8, 1), 2 = (2, 4, 2), 3 = (2, 2, 4).
 PLANS: Dict[Tuple[str, int, int], Tuple[int, int, int]] = {
-    ("int4", 1536, 2048): (2, 2, 7),
+    ("int4", 1536, 2048): (2, 1, 7),
     ("int4", 1536, 1536): (2, 1, 12),     # o_proj: one head per K slice (attention merge)
-    ("int4", 8960, 1536): (2, 2, 10),
+    ("int4", 8960, 1536): (2, 1, 14),
     ("int4", 1536, 17920): (4, 2, 1),     # SiLU-fused gate_up: preset 4 = (2, 3, 4)
-    ("fp16", 1536, 2048): (2, 2, 7),
+    ("fp16", 1536, 2048): (2, 1, 7),
     ("fp16", 1536, 1536): (2, 1, 12),
-    ("fp16", 8960, 1536): (2, 2, 10),
+    ("fp16", 8960, 1536): (2, 1, 14),
     ("fp16", 1536, 17920): (4, 2, 1),
 }
 

@@ -154,6 +154,44 @@ def attention_launch_time(runner, B: int, reps: int) -> tuple[float, int]:
     return e0.elapsed_time(e1) / 1e3 / n, n
 
 
+def pmc_probe(runner, seqs, B: int) -> None:
+    """Kernel launches for byte-counter runs: one decode attention per layer (eager, so
+    every dispatch is its own counter record) and a plain device copy of 256 MiB, whose
+    counters calibrate FETCH_SIZE / WRITE_SIZE against known bytes."""
+    model = runner.adapter.model
+    cfg = model.cfg
+    dev = runner.pool.storage.device
+    runner.decode(seqs)                       # graph captured and one step taken
+    torch.cuda.synchronize()
+    view = runner.pool.view(B, runner._rope_delta)
+    bufs = model.decode_buffers(B, dev)
+    Sq = model.layers[0].qkv_proj.forward_partial(bufs["h"], bufs["qpart"])
+    for i, layer in enumerate(model.layers):
+        view.attend_fused(bufs["qpart"], Sq, layer.qkv_proj.bias, layer.qkv_proj.fmt == "int4",
+                          i, model.scale, model.rope_cos, model.rope_sin, cfg.mrope_section)
+    torch.cuda.synchronize()
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"pmc probe: {len(model.layers)} attention launches at ctx "
+        f"{int(runner.pool.lengths[0])}, one 256 MiB copy")
+
+
+def traffic_from_profiles(kernel: str):
+    """HBM bytes per launch of ``kernel`` measured with rocprofv3 byte counters and
+    calibrated against a plain copy (profiles/traffic.json, written from the runs its
+    "commands" field lists), or None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+        k = t["kernels"][kernel]
+        return int(k["fetch_bytes"] + k["write_bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def cpu_baseline(runner, seqs, w, shape, budget_s: float = 15.0) -> dict:
     """fp32 CPU restatement (oracle) of the same decode step on this host's cores."""
     from oracle import qwen2_ref as ref
@@ -204,6 +242,10 @@ def main():
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--kernel-steps", type=int, default=10,
                     help="replays of the 28-launch attention graph timed for the roofline")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="for rocprofv3 --pmc: one eager launch of the decode attention per "
+                         "layer at the bench context, then a plain 256 MiB device copy (the "
+                         "byte-counter calibration); prints no JSON line")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -219,6 +261,9 @@ def main():
 
     runner, seqs, w, shape = build_config3(dev, args.batch, args.ctx)
     B = len(seqs)
+    if args.pmc_probe:
+        pmc_probe(runner, seqs, B)
+        return
 
     for _ in range(args.warmup):
         runner.decode(seqs)
@@ -293,7 +338,8 @@ def main():
             "kernel": "decode_attn_kernel (qkv partials + bias + M-RoPE + KV write + split GQA "
                       "decode attention, states out), graph of the 28 layers' launches",
             "achieved": round(achieved / 1e9, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-            "frac": round(achieved / PEAK_HBM, 4), "traffic": None,
+            "frac": round(achieved / PEAK_HBM, 4),
+            "traffic": traffic_from_profiles("decode_attn_kernel"),
             "launch_us": round(t_attn * 1e6, 2), "launches": n_attn, "bytes_per_launch": a_bytes,
         },
         "step_roofline": {

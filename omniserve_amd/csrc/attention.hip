@@ -89,9 +89,12 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
   const int q16 = lane >> 4;     // lane group 0..3
   const int c16 = lane & 15;     // column within MFMA tile
   const int S = a.S;
-  const int sp = blockIdx.x % S;
-  const int g = (blockIdx.x / S) % a.nkv;
-  const int t = blockIdx.x / (S * a.nkv);
+  // The S workgroups of one (token, kv head) are neighbours in XCD-aware order, so they
+  // share an L2 and the token's qkv partials are fetched from HBM once, not S times.
+  const int blk = xcd_logical_block(blockIdx.x, gridDim.x);
+  const int sp = blk % S;
+  const int g = (blk / S) % a.nkv;
+  const int t = blk / (S * a.nkv);
   const int G = a.G;
   const int nh = a.nkv * G;
   const bool fused = a.qparts != nullptr;

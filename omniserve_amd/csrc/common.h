@@ -135,6 +135,17 @@ __device__ __forceinline__ half8_t dequant8(uint32_t w, half2_t s2) {
   return out;
 }
 
+// XCD-aware workgroup numbering.  The dispatcher places workgroup b on XCD b % 8
+// (round robin over the 8 XCDs, each with its own L2).  This maps b to a logical index
+// such that every XCD receives one contiguous range of logical indices, so neighbouring
+// logical workgroups (which share inputs) share an L2.  A bijection on [0, n) for any n;
+// if the placement were different only locality, never correctness, would change.
+__device__ __forceinline__ int xcd_logical_block(int b, int n) {
+  const int q = n >> 3, r = n & 7;
+  const int x = b & 7, local = b >> 3;
+  return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + local;
+}
+
 // sum[e] += base[p * stride + e] for p = 0 .. n-1 in ascending order (e = 0..7, fp32 split-K
 // slices).  Loads go out in batches of BATCH before the first add of the batch, so n
 // slices cost ceil(n/BATCH) memory round trips, not n; a slot past n adds +0.0f (sum is

@@ -132,8 +132,10 @@ __global__ __launch_bounds__(CW * KW * 64) void gemv_kernel(GemvArgs a) {
   const int c16 = lane & 15;
   const int NT = a.N >> 4;
   const int ngroups = (NT + NT_WG - 1) / NT_WG;
-  const int ng = blockIdx.x % ngroups;
-  const int ksi = blockIdx.x / ngroups;
+  // XCD-aware order: the workgroups of one K slice (same x, different columns) share an L2
+  const int blk = xcd_logical_block(blockIdx.x, gridDim.x);
+  const int ng = blk % ngroups;
+  const int ksi = blk / ngroups;
   const int k0 = ksi * a.KC;
   const int kc = min(a.KC, a.K - k0);          // multiple of 128
   const int xstride = a.KC + 8;

@@ -188,6 +188,24 @@ int omni_f16_pack(const void* weight, void* weight_packed, int K, int N, int int
 int omni_w4_dequant(const int32_t* qweight_packed, const void* scales_packed, void* w, int K,
                     int N, void* stream);
 
+/* ---------------------------------------------------------------- fp8 (W8A8) */
+
+/* Row-wise e4m3fn quantisation: scale[r] = amax_k |x[r, k]| / 448 (max(., clamp_min) when
+ * clamp_min > 0), q[r, k] = e4m3(x[r, k] / scale[r]).  Activations: quant_fp8
+ * (kernels/fp8_linear.py:45-63, no clamp); weights at load: FP8Linear's sw / Wq
+ * (fp8_linear.py:83-86).  x fp16 [rows, K] (row stride ldx), q [rows, K] bytes. */
+int omni_fp8_quant_rows(const void* x, int ldx, void* q, float* scale, int rows, int K,
+                        float clamp_min, void* stream);
+
+/* FP8Linear.forward / forward_prequant (kernels/fp8_linear.py:99-126):
+ * y[m, n] = bf16((sum_k xq[m,k] wq[n,k]) * sa[m] * sw[n]) (fp32 accumulation, as
+ * torch._scaled_mm with out_dtype bf16); out_bf16 = 1 stores that bf16 value, else it is
+ * cast to fp16 and the fp16 bias (if any) added in fp16.  xq [M, K], wq [N, K] e4m3fn;
+ * out [M, ldo]; N % 128 == 0, K % 128 == 0. */
+int omni_fp8_gemm(const void* xq, const float* sa, const void* wq, const float* sw,
+                  const void* bias, void* out, int ldo, int M, int N, int K, int out_bf16,
+                  void* stream);
+
 /* ---------------------------------------------------------------- lm_head + greedy */
 
 /* Workgroups (= candidate rows per token) of omni_lmhead_candidates for vocab N. */

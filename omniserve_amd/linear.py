@@ -215,6 +215,72 @@ class F16Linear(_Skinny):
              stream())
 
 
+class FP8Linear(nn.Module):
+    """W8A8 e4m3fn linear with row-wise scales, FP8Linear's API (kernels/fp8_linear.py:66-126).
+
+    Weights are quantised on the device at construction: sw[n] = amax|W[n, :]|/448,
+    Wq = e4m3(W / sw).  ``forward(x)`` quantises x per token (quant_fp8, :45-63) and runs
+    the fp8 MFMA GEMM; the result is bf16((xq . Wq^T) * sa * sw) cast to fp16, plus the
+    bias.  ``forward_prequant(xq, scale)`` takes already-quantised rows (the output of
+    add_rms_norm_fp8) and returns the bf16 product, as the reference does (:99-108)."""
+
+    fmt = "fp8"
+
+    def __init__(self, weight: torch.Tensor, bias=None):
+        super().__init__()
+        N, K = weight.shape
+        require_cuda(weight, dtype=torch.float16)
+        if N % 128 or K % 128:
+            raise ValueError(f"FP8Linear needs N, K multiples of 128 (got {N}, {K})")
+        dev = weight.device
+        self.K, self.N = K, N
+        w = weight.contiguous()
+        self.register_buffer("weight_fp8", torch.empty(N, K, device=dev, dtype=torch.uint8))
+        self.register_buffer("weight_scale", torch.empty(N, device=dev, dtype=torch.float32))
+        call("omni_fp8_quant_rows", ptr(w), K, ptr(self.weight_fp8), ptr(self.weight_scale), N, K,
+             0.0, stream())
+        self.bias = None if bias is None else bias.to(device=dev, dtype=torch.float16).contiguous()
+
+    @property
+    def out_features(self) -> int:
+        return self.N
+
+    def quantize_input(self, x2d: torch.Tensor):
+        """quant_fp8: (xq e4m3 bytes [M, K], scale fp32 [M, 1])."""
+        M = x2d.shape[0]
+        xq = torch.empty(M, self.K, device=x2d.device, dtype=torch.uint8)
+        sa = torch.empty(M, 1, device=x2d.device, dtype=torch.float32)
+        call("omni_fp8_quant_rows", ptr(x2d), x2d.stride(0), ptr(xq), ptr(sa), M, self.K, 0.0,
+             stream())
+        return xq, sa
+
+    def gemm_out(self, xq: torch.Tensor, sa: torch.Tensor, out: torch.Tensor, bf16: bool):
+        M = xq.shape[0]
+        call("omni_fp8_gemm", ptr(xq), ptr(sa), ptr(self.weight_fp8), ptr(self.weight_scale),
+             None if bf16 else ptr(self.bias), ptr(out), out.stride(0), M, self.N, self.K,
+             int(bf16), stream())
+        return out
+
+    def forward_prequant(self, xq: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+        xq2 = xq.reshape(-1, self.K)
+        if xq2.dtype == torch.float8_e4m3fn:
+            xq2 = xq2.view(torch.uint8)
+        xq2 = xq2.contiguous()
+        out = torch.empty(xq2.shape[0], self.N, device=xq.device, dtype=torch.bfloat16)
+        self.gemm_out(xq2, scale.reshape(-1).contiguous().float(), out, True)
+        return out.reshape(*xq.shape[:-1], self.N)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        x2d = x.reshape(-1, self.K)
+        if not x2d.is_contiguous():
+            x2d = x2d.contiguous()
+        require_cuda(x2d, dtype=torch.float16)
+        xq, sa = self.quantize_input(x2d)
+        out = torch.empty(x2d.shape[0], self.N, device=x.device, dtype=torch.float16)
+        self.gemm_out(xq, sa, out, False)
+        return out.reshape(*x.shape[:-1], self.N)
+
+
 class LMHeadArgmax(nn.Module):
     """Tied lm_head (qwen2_llm.py:167-168, 190) fused with greedy argmax
     (runners/multimodal.py:307-308): ids = argmax_n fp16(h . E[n]), lowest index on ties.

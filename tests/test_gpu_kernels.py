@@ -500,3 +500,80 @@ def test_oproj_merges_attention_states(gpu, fmt, splits):
     lin.forward_partial(out, pb)
     torch.cuda.synchronize()
     assert torch.equal(pa, pb)
+
+
+# ----------------------------------------------------------------------------- fp8 W8A8
+def test_fp8_quant_rows_bit_exact(gpu):
+    """quant_fp8 (fp8_linear.py:45-63): per-row amax/448 scale and e4m3 codes, bit-exact."""
+    from omniserve_amd._lib import call, ptr, stream
+    say("fp8 row quantisation")
+    M, K = 37, 1536
+    x = f16((M, K), 140, 1.5)
+    x[3] = 0.5                                    # constant row
+    xg = x.to(gpu)
+    q = torch.empty(M, K, device=gpu, dtype=torch.uint8)
+    s = torch.empty(M, device=gpu, dtype=torch.float32)
+    call("omni_fp8_quant_rows", ptr(xg), K, ptr(q), ptr(s), M, K, 0.0, stream())
+    torch.cuda.synchronize()
+    eq, es = ref.quant_fp8(x.float())
+    assert torch.equal(s.cpu(), es.view(-1))
+    assert torch.equal(q.cpu(), eq.view(torch.uint8))
+
+
+def fp8_abs_product(xq, sa, wq, sw):
+    """|xq| . |wq|^T * sa * sw: the scale of the terms each output sums."""
+    return (xq.float().abs() @ wq.float().abs().t()) * sa.view(-1, 1) * sw.view(1, -1)
+
+
+@pytest.mark.parametrize("M,N,K,bias", [(1, 256, 1536, False), (100, 2048, 1536, True),
+                                        (256, 1536, 8960, False), (130, 384, 256, True)])
+def test_fp8_linear_matches_oracle(gpu, M, N, K, bias):
+    """FP8Linear.forward: bf16((xq.Wq^T)*sa*sw) -> fp16 (+bias) against the oracle on the
+    same quantised operands.  The fp8 MFMA sums groups of products with fewer bits than
+    fp32 (an on-device probe loses 1 next to +-448^2 inside one group, as fp8 tensor-core
+    GEMMs elsewhere do), so the bound is one bf16 step of the result plus 2^-14 of the
+    summed term magnitudes; nearly all outputs are still identical."""
+    from omniserve_amd.linear import FP8Linear
+    say(f"fp8 linear M={M} N={N} K={K} bias={bias}")
+    W = f16((N, K), 141, 0.02)
+    b = f16((N,), 142, 0.02) if bias else None
+    x = f16((M, K), 143)
+    lin = FP8Linear(W.to(gpu), None if b is None else b.to(gpu))
+    y = lin(x.to(gpu))
+    torch.cuda.synchronize()
+    wq, sw = ref.fp8_weight_rowwise(W.float())
+    assert torch.equal(lin.weight_fp8.cpu(), wq.view(torch.uint8))
+    assert torch.equal(lin.weight_scale.cpu(), sw)
+    xq, sa = ref.quant_fp8(x.float())
+    e = ref.fp8_linear_rowwise(xq, sa, wq, sw, None if b is None else b.float())
+    e0 = ref.fp8_linear_rowwise(xq, sa, wq, sw, None)          # before the bias
+    yc = y.cpu().float()
+    d = (yc - e).abs()
+    # one bf16 step of the pre-bias value (<= 2^-7 relative), the fp16 bias rounding, and
+    # the MFMA's reduced intermediate precision on the summed term magnitudes
+    tol = e0.abs() * 2.0 ** -7 + e.abs() * 2.0 ** -10 + fp8_abs_product(xq, sa, wq, sw) * 2.0 ** -14
+    assert (d <= tol + 1e-6).all(), (d - tol).max().item()
+    assert (d == 0).float().mean().item() > 0.95
+
+
+def test_fp8_prequant_chain(gpu):
+    """add_rms_norm_fp8 -> FP8Linear.forward_prequant (the reference MLP's fp8 route,
+    qwen2_llm.py:130-134) returns the bf16 product of the norm-quantised rows."""
+    from omniserve_amd import fused_ops as F
+    from omniserve_amd.linear import FP8Linear
+    say("fp8 prequant chain")
+    M, H, N = 64, 1536, 1024
+    x, r = f16((M, H), 144), f16((M, H), 145)
+    w = (1 + 0.1 * torch.randn(H, generator=torch.Generator().manual_seed(146))).half()
+    W = f16((N, H), 147, 0.02)
+    lin = FP8Linear(W.to(gpu))
+    q, s, nr = F.add_rms_norm_fp8(x.to(gpu), r.to(gpu), w.to(gpu), 1e-6)
+    y = lin.forward_prequant(q, s)
+    torch.cuda.synchronize()
+    assert y.dtype == torch.bfloat16
+    wq, sw = ref.fp8_weight_rowwise(W.float())
+    qc = q.cpu().view(torch.float8_e4m3fn)
+    e = ref.fp8_linear_rowwise(qc, s.cpu(), wq, sw, out_f16=False)
+    d = (y.cpu().float() - e).abs()
+    tol = e.abs() * 2.0 ** -7 + fp8_abs_product(qc, s.cpu(), wq, sw) * 2.0 ** -14
+    assert (d <= tol + 1e-6).all(), (d - tol).max().item()

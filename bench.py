@@ -73,9 +73,9 @@ def log(msg):
 
 
 def build_config3(device, batch: int = 32, ctx: int = 2048, max_len: int = 4096, seed: int = 0):
-    from omniserve_amd import synth
-    from omniserve_amd.request import Request, SamplingParams, Sequence
-    from omniserve_amd.runner import NativeQwenVLRunner
+    from omniserver_amd import synth
+    from omniserver_amd.request import Request, SamplingParams, Sequence
+    from omniserver_amd.runner import NativeQwenVLRunner
 
     shape = synth.DecoderShape()
     t0 = time.time()

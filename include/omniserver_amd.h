@@ -1,5 +1,5 @@
 /*
- * omniserve_amd: C ABI of the MI355X (gfx950) kernels behind the Qwen2-VL text-decoder
+ * omniserver_amd: C ABI of the MI355X (gfx950) kernels behind the Qwen2-VL text-decoder
  * token loop.  Every entry point takes device pointers, sizes and a hipStream_t (as
  * void*), allocates nothing, never synchronises, and returns
  *     0   success
@@ -11,8 +11,8 @@
  *
  * Reference paths below are relative to the omniserve repository.
  */
-#ifndef OMNISERVE_AMD_H
-#define OMNISERVE_AMD_H
+#ifndef OMNISERVER_AMD_H
+#define OMNISERVER_AMD_H
 
 #include <stdint.h>
 
@@ -227,4 +227,4 @@ int omni_argmax_finalize(const float* cand_val, const int* cand_idx, int nblk, i
 }
 #endif
 
-#endif /* OMNISERVE_AMD_H */
+#endif /* OMNISERVER_AMD_H */

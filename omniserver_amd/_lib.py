@@ -1,6 +1,6 @@
-"""ctypes binding of the gfx950 C ABI declared in include/omniserve_amd.h.
+"""ctypes binding of the gfx950 C ABI declared in include/omniserver_amd.h.
 
-The shared library is built in-tree by ``python -m omniserve_amd.build``.  There
+The shared library is built in-tree by ``python -m omniserver_amd.build``.  There
 is no fallback: if it is missing or fails to load, every op raises.  torch is
 imported first so the library binds to the HIP runtime torch already loaded
 (both carry the soname libamdhip64.so.7) and can launch on torch's streams.
@@ -13,7 +13,7 @@ from pathlib import Path
 
 import torch
 
-LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libomniserve_amd.so"
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libomniserver_amd.so"
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -66,8 +66,8 @@ def lib() -> ctypes.CDLL:
     if _lib is None:
         if not LIB_PATH.exists():
             raise RuntimeError(
-                f"omniserve_amd HIP library missing at {LIB_PATH}; build it with "
-                "`python -m omniserve_amd.build` (there is no CPU fallback)")
+                f"omniserver_amd HIP library missing at {LIB_PATH}; build it with "
+                "`python -m omniserver_amd.build` (there is no CPU fallback)")
         so = ctypes.CDLL(str(LIB_PATH))
         for name, argtypes in SIGNATURES.items():
             fn = getattr(so, name)
@@ -100,7 +100,7 @@ def require_cuda(*tensors, dtype=None, contiguous=True) -> None:
         if t is None:
             continue
         if not t.is_cuda:
-            raise RuntimeError("omniserve_amd ops run on the GPU only (got a CPU tensor)")
+            raise RuntimeError("omniserver_amd ops run on the GPU only (got a CPU tensor)")
         if dtype is not None and t.dtype != dtype:
             raise TypeError(f"expected {dtype}, got {t.dtype}")
         if contiguous and not t.is_contiguous():

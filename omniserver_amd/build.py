@@ -1,8 +1,8 @@
-"""Build recipe for the gfx950 HIP library behind the omniserve_amd C ABI.
+"""Build recipe for the gfx950 HIP library behind the omniserver_amd C ABI.
 
 Every ``csrc/*.hip`` file is compiled with hipcc for gfx950 only and linked
-into ``omniserve_amd/_lib/libomniserve_amd.so`` (in-tree, so it travels with
-the repository snapshot to the GPU box).  Run ``python -m omniserve_amd.build``.
+into ``omniserver_amd/_lib/libomniserver_amd.so`` (in-tree, so it travels with
+the repository snapshot to the GPU box).  Run ``python -m omniserver_amd.build``.
 """
 
 from __future__ import annotations
@@ -17,7 +17,7 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 OUT_DIR = PKG / "_lib"
-LIB_NAME = "libomniserve_amd.so"
+LIB_NAME = "libomniserver_amd.so"
 INCLUDE = PKG.parent / "include"
 
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")

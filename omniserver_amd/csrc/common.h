@@ -1,4 +1,4 @@
-// Shared device helpers for the omniserve_amd gfx950 kernels.
+// Shared device helpers for the omniserver_amd gfx950 kernels.
 //
 // Everything here is written for CDNA4 (gfx950): 64-lane wavefronts, MFMA
 // 16x16x32 f16 tiles, 160 KB of LDS per CU.  No other target is supported.
@@ -7,7 +7,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "omniserve_amd.h"
+#include "omniserver_amd.h"
 
 #define OMNI_WAVE 64
 

@@ -1,6 +1,6 @@
 """CPU oracle: an fp32 restatement of omniserve's Qwen2-VL text-decoder token loop.
 
-TEST INFRASTRUCTURE ONLY.  Nothing under ``omniserve_amd/`` imports this
+TEST INFRASTRUCTURE ONLY.  Nothing under ``omniserver_amd/`` imports this
 module; only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
 ``cpu_baseline`` leg use it, as the checker (and as the reported CPU baseline),
 never as the path that is measured or shipped.

@@ -18,6 +18,6 @@ def gpu():
     import torch
     if not torch.cuda.is_available():
         pytest.skip("no GPU visible")
-    from omniserve_amd._lib import lib
+    from omniserver_amd._lib import lib
     lib()  # fails loudly when the HIP library is not built
     return torch.device("cuda:0")

@@ -1,5 +1,5 @@
 """Writes tests/golden/decode_fp16_2layer.json: greedy decode of a 2-layer, full-width
-Qwen2-VL text decoder (seeded synthetic fp16 weights, omniserve_amd.synth seed 11) by the
+Qwen2-VL text decoder (seeded synthetic fp16 weights, omniserver_amd.synth seed 11) by the
 CPU oracle in its fp16-faithful mode.  The reference publishes no vectors for this path,
 so this fixture pins the oracle against regressions and lets GPU tests compare against
 stored values.  Run: python tests/golden/make_golden.py"""
@@ -14,7 +14,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)
 sys.path.insert(0, ROOT)
 
 from oracle import qwen2_ref as ref  # noqa: E402
-from omniserve_amd import synth  # noqa: E402
+from omniserver_amd import synth  # noqa: E402
 from tests.helpers import oracle_from_fp16  # noqa: E402
 
 SEED, LAYERS, PROMPT_LEN, STEPS = 11, 2, 24, 4

@@ -1,4 +1,4 @@
-"""The C-ABI library: loads without a GPU, exports exactly what include/omniserve_amd.h
+"""The C-ABI library: loads without a GPU, exports exactly what include/omniserver_amd.h
 declares, the ctypes table matches the header's parameter counts, and argument
 validation rejects bad shapes before any HIP call (safe to exercise on the CPU)."""
 
@@ -9,7 +9,7 @@ from pathlib import Path
 import pytest
 
 ROOT = Path(__file__).resolve().parent.parent
-HEADER = ROOT / "include" / "omniserve_amd.h"
+HEADER = ROOT / "include" / "omniserver_amd.h"
 
 
 def header_decls():
@@ -24,9 +24,9 @@ def header_decls():
 
 @pytest.fixture(scope="module")
 def so():
-    from omniserve_amd._lib import LIB_PATH
+    from omniserver_amd._lib import LIB_PATH
     if not LIB_PATH.exists():
-        pytest.fail("HIP library not built: run python -m omniserve_amd.build")
+        pytest.fail("HIP library not built: run python -m omniserver_amd.build")
     return ctypes.CDLL(str(LIB_PATH))
 
 
@@ -42,7 +42,7 @@ def test_library_exports_every_declared_symbol(so):
 
 
 def test_ctypes_table_matches_header():
-    from omniserve_amd._lib import SIGNATURES
+    from omniserver_amd._lib import SIGNATURES
     decls = header_decls()
     assert set(SIGNATURES) == set(decls)
     for name, params in decls.items():
@@ -50,7 +50,7 @@ def test_ctypes_table_matches_header():
 
 
 def test_bad_arguments_rejected_before_launch(so):
-    from omniserve_amd._lib import lib
+    from omniserver_amd._lib import lib
     L = lib()
     # unsupported hidden size / negative rows
     assert L.omni_rmsnorm(None, None, None, 4, 7, 1e-6, None) == -2

@@ -1,7 +1,7 @@
 """Kernel-level parity of the HIP path against the CPU oracle (GPU tests).
 
 Each test feeds the same seeded fp16 inputs to the HIP kernel (through the C ABI
-via omniserve_amd's thin wrappers) and to oracle/qwen2_ref.py, and compares:
+via omniserver_amd's thin wrappers) and to oracle/qwen2_ref.py, and compares:
 bit-exact for integer/byte/index work and for the fp16-rounding-specified ops
 (M-RoPE, embedding gather, int4 dequant, KV writes), tolerance for reductions.
 """
@@ -28,7 +28,7 @@ def f16(shape, seed, std=1.0):
 # ----------------------------------------------------------------------------- norms
 @pytest.mark.parametrize("rows", [1, 5, 32, 257])
 def test_add_rmsnorm(gpu, rows):
-    from omniserve_amd import fused_ops as F
+    from omniserver_amd import fused_ops as F
     say(f"add_rmsnorm rows={rows}")
     H = 1536
     x, r = f16((rows, H), 1), f16((rows, H), 2)
@@ -42,7 +42,7 @@ def test_add_rmsnorm(gpu, rows):
 
 
 def test_rmsnorm_and_embed(gpu):
-    from omniserve_amd import fused_ops as F
+    from omniserver_amd import fused_ops as F
     say("rmsnorm / embedding gather (plain + packed) / embed_rmsnorm")
     V, H = 4096, 1536
     table = f16((V, H), 7, 0.02)
@@ -52,7 +52,7 @@ def test_rmsnorm_and_embed(gpu):
     ey = ref.rms_norm(table[ids].float(), w.float(), 1e-6)
     assert (y.cpu().float() - ey).abs().max().item() <= 2e-3 * ey.abs().max().item()
 
-    from omniserve_amd.linear import LMHeadArgmax
+    from omniserver_amd.linear import LMHeadArgmax
     lm = LMHeadArgmax(table.to(gpu))
     out = torch.empty(len(ids), H, device=gpu, dtype=torch.float16)
     F.embedding_out(ids.to(gpu), lm.table_packed, True, out)
@@ -68,7 +68,7 @@ def test_rmsnorm_and_embed(gpu):
 
 
 def test_add_rmsnorm_fp8(gpu):
-    from omniserve_amd import fused_ops as F
+    from omniserver_amd import fused_ops as F
     say("add_rmsnorm_fp8")
     M, H = 64, 1536
     x, r = f16((M, H), 11), f16((M, H), 12)
@@ -85,7 +85,7 @@ def test_add_rmsnorm_fp8(gpu):
 
 
 def test_silu_mul(gpu):
-    from omniserve_amd import fused_ops as F
+    from omniserver_amd import fused_ops as F
     say("silu_mul")
     gu = f16((7, 2 * 8960), 21, 2.0)
     y = F.silu_mul(gu.to(gpu)).cpu().float()
@@ -99,8 +99,8 @@ def test_silu_mul(gpu):
 def test_mrope_kv_write_decode(gpu, T):
     """Decode form: positions = lengths[row] + rope_delta[row] on all three axes;
     rotated K and raw V land at pool[row, lengths[row]].  Bit-exact vs the oracle."""
-    from omniserve_amd._lib import call, ptr, stream
-    from omniserve_amd.qwen2_llm import rope_tables
+    from omniserver_amd._lib import call, ptr, stream
+    from omniserver_amd.qwen2_llm import rope_tables
     say(f"mrope_kv_write decode T={T}")
     cfg = ref.Qwen2Config()
     nh, nkv, hd = 12, 2, 128
@@ -136,8 +136,8 @@ def test_mrope_kv_write_decode(gpu, T):
 
 def test_mrope_3d_positions(gpu):
     """Prefill form with distinct t/h/w position ids (image tokens): bit-exact."""
-    from omniserve_amd._lib import call, ptr, stream
-    from omniserve_amd.qwen2_llm import rope_tables
+    from omniserver_amd._lib import call, ptr, stream
+    from omniserver_amd.qwen2_llm import rope_tables
     say("mrope 3-D positions")
     cfg = ref.Qwen2Config()
     nh, nkv, hd = 12, 2, 128
@@ -166,7 +166,7 @@ def test_mrope_3d_positions(gpu):
     ([1, 2, 3, 4095], 4, 16), ([31, 32, 33, 65], 16, 1), ([2049] * 3, 4, 8),
 ])
 def test_decode_attention(gpu, lengths, waves, splits):
-    from omniserve_amd._lib import call, ptr, stream
+    from omniserver_amd._lib import call, ptr, stream
     say(f"decode_attention lengths={lengths} waves={waves} splits={splits}")
     n = len(lengths)
     nh, nkv, hd, ML = 12, 2, 128, 4096
@@ -190,8 +190,8 @@ def test_decode_attention(gpu, lengths, waves, splits):
 
 @pytest.mark.parametrize("segs", [[1], [5, 16, 17], [256], [100, 37, 512]])
 def test_prefill_attention(gpu, segs):
-    from omniserve_amd.attention import query_blocks
-    from omniserve_amd._lib import call, ptr, stream
+    from omniserver_amd.attention import query_blocks
+    from omniserver_amd._lib import call, ptr, stream
     say(f"prefill_attention segs={segs}")
     nh, nkv, hd, ML = 12, 2, 128, 1024
     P = len(segs)
@@ -224,13 +224,13 @@ def test_prefill_attention(gpu, segs):
 
 # ----------------------------------------------------------------------------- linears
 def _gptq(K, N, seed):
-    from omniserve_amd.synth import gptq_random
+    from omniserver_amd.synth import gptq_random
     return gptq_random(K, N, seed, "t")
 
 
 @pytest.mark.parametrize("K,N", [(1536, 2048), (8960, 1536), (1536, 256)])
 def test_w4_dequant_bit_exact(gpu, K, N):
-    from omniserve_amd.linear import GPTQLinear
+    from omniserver_amd.linear import GPTQLinear
     say(f"int4 dequant K={K} N={N}")
     qw, sc = _gptq(K, N, 71)
     lin = GPTQLinear(qw.to(gpu), sc.to(gpu))
@@ -245,7 +245,7 @@ def test_w4_dequant_bit_exact(gpu, K, N):
     (1536, 17920, False, True),
 ])
 def test_w4a16_gemm(gpu, M, K, N, bias, silu):
-    from omniserve_amd.linear import GPTQLinear
+    from omniserver_amd.linear import GPTQLinear
     say(f"w4a16 M={M} K={K} N={N} bias={bias} silu={silu}")
     qw, sc = _gptq(K, N, 72 + K + N)
     b = f16((N,), 73, 0.02) if bias else None
@@ -281,7 +281,7 @@ def test_w4a16_gemm(gpu, M, K, N, bias, silu):
     (1536, 2048, True, False), (8960, 1536, False, False), (1536, 17920, False, True),
 ])
 def test_f16_gemm(gpu, M, K, N, bias, silu):
-    from omniserve_amd.linear import F16Linear
+    from omniserver_amd.linear import F16Linear
     say(f"f16 gemm M={M} K={K} N={N} bias={bias} silu={silu}")
     w = f16((N, K), 81, 0.02)
     b = f16((N,), 82, 0.02) if bias else None
@@ -299,7 +299,7 @@ def test_f16_gemm(gpu, M, K, N, bias, silu):
 
 def test_add_rmsnorm_partials(gpu):
     """x = fp16(sum of split-K partials in slice order), then add + RMSNorm."""
-    from omniserve_amd import fused_ops as F
+    from omniserver_amd import fused_ops as F
     say("add_rmsnorm over split-K partials")
     S, M, H = 7, 32, 1536
     g = torch.Generator().manual_seed(101)
@@ -321,7 +321,7 @@ def test_add_rmsnorm_partials(gpu):
 
 @pytest.mark.parametrize("M", [1, 32])
 def test_lmhead_argmax(gpu, M):
-    from omniserve_amd.linear import LMHeadArgmax
+    from omniserver_amd.linear import LMHeadArgmax
     say(f"lm_head argmax M={M}")
     V, H = 151936, 1536
     E = f16((V, H), 91, 0.02)
@@ -348,7 +348,7 @@ def test_lmhead_argmax(gpu, M):
 
 def test_lmhead_argmax_ties(gpu):
     """Equal fp16 logits at several columns: the lowest index wins (torch.argmax)."""
-    from omniserve_amd.linear import LMHeadArgmax
+    from omniserver_amd.linear import LMHeadArgmax
     say("lm_head argmax ties")
     V, H = 151936, 1536
     E = torch.zeros(V, H, dtype=torch.float16)
@@ -367,8 +367,8 @@ def test_lmhead_argmax_ties(gpu):
 def test_mrope_from_partials(gpu, bias_after_round):
     """qkv rows formed from split-K partials (+ bias) then rotated: bit-equal to forming
     the fp16 rows on the host the same way and running the plain kernel."""
-    from omniserve_amd._lib import call, ptr, stream
-    from omniserve_amd.qwen2_llm import rope_tables
+    from omniserver_amd._lib import call, ptr, stream
+    from omniserver_amd.qwen2_llm import rope_tables
     say(f"mrope from partials bias_after_round={bias_after_round}")
     cfg = ref.Qwen2Config()
     nh, nkv, hd = 12, 2, 128
@@ -416,8 +416,8 @@ def test_mrope_from_partials(gpu, bias_after_round):
 def test_decode_attention_fused_equals_unfused(gpu, bias_after_round, splits, lengths):
     """Fused prologue (qkv partials + bias + M-RoPE + KV write) + attention gives exactly
     what the separate M-RoPE-from-partials and attention launches give."""
-    from omniserve_amd._lib import call, ptr, stream
-    from omniserve_amd.qwen2_llm import rope_tables
+    from omniserver_amd._lib import call, ptr, stream
+    from omniserver_amd.qwen2_llm import rope_tables
     say(f"fused decode attention bar={bias_after_round} splits={splits} lengths={lengths}")
     cfg = ref.Qwen2Config()
     nh, nkv, hd, ML = 12, 2, 128, 4096
@@ -459,10 +459,10 @@ def test_decode_attention_fused_equals_unfused(gpu, bias_after_round, splits, le
 def test_oproj_merges_attention_states(gpu, fmt, splits):
     """o_proj reading the decode attention's split states (merge in its input staging)
     gives exactly merge launch + o_proj on the merged fp16 output."""
-    from omniserve_amd._lib import call, ptr, stream
-    from omniserve_amd.linear import F16Linear, GPTQLinear
-    from omniserve_amd.qwen2_llm import rope_tables
-    from omniserve_amd.synth import gptq_random
+    from omniserver_amd._lib import call, ptr, stream
+    from omniserver_amd.linear import F16Linear, GPTQLinear
+    from omniserver_amd.qwen2_llm import rope_tables
+    from omniserver_amd.synth import gptq_random
     say(f"o_proj from attention states fmt={fmt} splits={splits}")
     cfg = ref.Qwen2Config()
     nh, nkv, hd, ML, H = 12, 2, 128, 4096, 1536
@@ -505,7 +505,7 @@ def test_oproj_merges_attention_states(gpu, fmt, splits):
 # ----------------------------------------------------------------------------- fp8 W8A8
 def test_fp8_quant_rows_bit_exact(gpu):
     """quant_fp8 (fp8_linear.py:45-63): per-row amax/448 scale and e4m3 codes, bit-exact."""
-    from omniserve_amd._lib import call, ptr, stream
+    from omniserver_amd._lib import call, ptr, stream
     say("fp8 row quantisation")
     M, K = 37, 1536
     x = f16((M, K), 140, 1.5)
@@ -533,7 +533,7 @@ def test_fp8_linear_matches_oracle(gpu, M, N, K, bias):
     fp32 (an on-device probe loses 1 next to +-448^2 inside one group, as fp8 tensor-core
     GEMMs elsewhere do), so the bound is one bf16 step of the result plus 2^-14 of the
     summed term magnitudes; nearly all outputs are still identical."""
-    from omniserve_amd.linear import FP8Linear
+    from omniserver_amd.linear import FP8Linear
     say(f"fp8 linear M={M} N={N} K={K} bias={bias}")
     W = f16((N, K), 141, 0.02)
     b = f16((N,), 142, 0.02) if bias else None
@@ -559,8 +559,8 @@ def test_fp8_linear_matches_oracle(gpu, M, N, K, bias):
 def test_fp8_prequant_chain(gpu):
     """add_rms_norm_fp8 -> FP8Linear.forward_prequant (the reference MLP's fp8 route,
     qwen2_llm.py:130-134) returns the bf16 product of the norm-quantised rows."""
-    from omniserve_amd import fused_ops as F
-    from omniserve_amd.linear import FP8Linear
+    from omniserver_amd import fused_ops as F
+    from omniserver_amd.linear import FP8Linear
     say("fp8 prequant chain")
     M, H, N = 64, 1536, 1024
     x, r = f16((M, H), 144), f16((M, H), 145)

@@ -41,9 +41,9 @@ def _fill_pool(pool, lengths, seed):
 
 
 def _decode_once(gpu, quant, n_layers, lengths, seed):
-    from omniserve_amd import synth
-    from omniserve_amd.kv_cache import PreallocatedKVCache
-    from omniserve_amd.qwen2_llm import Qwen2LLM
+    from omniserver_amd import synth
+    from omniserver_amd.kv_cache import PreallocatedKVCache
+    from omniserver_amd.qwen2_llm import Qwen2LLM
     shape = synth.DecoderShape()
     if quant == "gptq":
         w = synth.gptq_decoder(shape, seed=seed, num_layers=n_layers)
@@ -116,9 +116,9 @@ def _greedy_oracle(orc, prompts, steps, max_len):
 @pytest.mark.parametrize("use_graph", [False, True])
 def test_runner_greedy_matches_oracle(gpu, use_graph):
     """NativeQwenVLRunner prefill + decode (eager and hipGraph) vs oracle greedy."""
-    from omniserve_amd import synth
-    from omniserve_amd.request import Request, SamplingParams, Sequence
-    from omniserve_amd.runner import NativeQwenVLRunner
+    from omniserver_amd import synth
+    from omniserver_amd.request import Request, SamplingParams, Sequence
+    from omniserver_amd.runner import NativeQwenVLRunner
     say(f"runner greedy fp16 3 layers use_graph={use_graph}")
     shape = synth.DecoderShape()
     w = synth.fp16_decoder(shape, seed=5, num_layers=3)
@@ -145,9 +145,9 @@ def test_runner_greedy_matches_oracle(gpu, use_graph):
 def test_graph_equals_eager_with_compaction(gpu):
     """hipGraph replay and eager decode give identical tokens, including after a
     sequence finishes and the pool is compacted (free -> move last slot)."""
-    from omniserve_amd import synth
-    from omniserve_amd.request import Request, SamplingParams, Sequence, Status
-    from omniserve_amd.runner import NativeQwenVLRunner
+    from omniserver_amd import synth
+    from omniserver_amd.request import Request, SamplingParams, Sequence, Status
+    from omniserver_amd.runner import NativeQwenVLRunner
     say("graph vs eager with compaction (gptq, 2 layers)")
     shape = synth.DecoderShape()
     w = synth.gptq_decoder(shape, seed=6, num_layers=2)
@@ -177,10 +177,10 @@ def test_graph_equals_eager_with_compaction(gpu):
 def test_multimodal_prefill_positions_and_logits(gpu):
     """Packed prefill of image+text prompts: M-RoPE ids equal the oracle's; logits at the
     segment ends and the pool contents match the oracle."""
-    from omniserve_amd import synth
-    from omniserve_amd.kv_cache import PreallocatedKVCache
-    from omniserve_amd.positions import IMAGE_TOKEN_ID, mrope_positions
-    from omniserve_amd.qwen2_llm import Qwen2LLM
+    from omniserver_amd import synth
+    from omniserver_amd.kv_cache import PreallocatedKVCache
+    from omniserver_amd.positions import IMAGE_TOKEN_ID, mrope_positions
+    from omniserver_amd.qwen2_llm import Qwen2LLM
     say("multimodal packed prefill (gptq, 2 layers)")
     shape = synth.DecoderShape()
     w = synth.gptq_decoder(shape, seed=8, num_layers=2)
@@ -234,9 +234,9 @@ def test_full_depth_decode_fp16(gpu):
     same order.  So the bar is: cosine >= 0.9999 against both oracle modes, and the GPU's
     distance from the exact fp32 result within max(2e-2, 1.25 x the fp16 oracle's own
     distance from it); argmax equal on decisive rows."""
-    from omniserve_amd import synth
-    from omniserve_amd.kv_cache import PreallocatedKVCache
-    from omniserve_amd.qwen2_llm import Qwen2LLM
+    from omniserver_amd import synth
+    from omniserver_amd.kv_cache import PreallocatedKVCache
+    from omniserver_amd.qwen2_llm import Qwen2LLM
     say("full-depth (28 layers) fp16 decode step")
     shape = synth.DecoderShape()
     w = synth.fp16_decoder(shape, seed=9, num_layers=28)
@@ -270,9 +270,9 @@ def test_runner_matches_golden_fixture(gpu):
     """hipGraph runner greedy tokens vs the committed oracle fixture (2 layers, full width)."""
     import json
     import os
-    from omniserve_amd import synth
-    from omniserve_amd.request import Request, SamplingParams, Sequence
-    from omniserve_amd.runner import NativeQwenVLRunner
+    from omniserver_amd import synth
+    from omniserver_amd.request import Request, SamplingParams, Sequence
+    from omniserver_amd.runner import NativeQwenVLRunner
     say("runner vs golden fixture")
     gdir = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
     gold = json.load(open(os.path.join(gdir, "decode_fp16_2layer.json")))

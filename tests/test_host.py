@@ -53,7 +53,7 @@ def emulate_gptq_repack_dequant(qweight: np.ndarray, scales: np.ndarray) -> np.n
 
 
 def test_packed_int4_layout_reproduces_reference_dequant():
-    from omniserve_amd.synth import gptq_random
+    from omniserver_amd.synth import gptq_random
     K, N = 256, 32
     qw, sc = gptq_random(K, N, 5, "layout")
     W = emulate_gptq_repack_dequant(qw.numpy(), sc.numpy())
@@ -102,7 +102,7 @@ def test_device_e4m3_conversion_matches_torch():
         src.write_text(E4M3_SRC)
         exe = Path(d) / "e4m3"
         r = subprocess.run([hipcc, "--offload-arch=gfx950", "-O1",
-                            f"-I{ROOT / 'omniserve_amd/csrc'}", f"-I{ROOT / 'include'}", str(src),
+                            f"-I{ROOT / 'omniserver_amd/csrc'}", f"-I{ROOT / 'include'}", str(src),
                             "-o", str(exe)], capture_output=True, text=True)
         if r.returncode != 0:
             pytest.skip(f"host build failed: {r.stderr[:300]}")
@@ -126,26 +126,26 @@ def test_device_e4m3_conversion_matches_torch():
 
 # ----------------------------------------------------------------------------- plans / blocks
 def test_query_blocks_cover_segments():
-    from omniserve_amd.attention import query_blocks
+    from omniserver_amd.attention import query_blocks
     qb = query_blocks([5, 16, 17, 1], "cpu").tolist()
     assert qb == [[0, 5], [5, 16], [21, 16], [37, 1], [38, 1]]
 
 
 def test_decode_plan_and_split_counts():
-    from omniserve_amd.kv_cache import MAX_ATTN_SPLITS, decode_plan
+    from omniserver_amd.kv_cache import MAX_ATTN_SPLITS, decode_plan
     for n in (1, 8, 16, 32, 64):
         for ctx in (64, 256, 1024, 4096):
             w, s = decode_plan(n, 2, ctx)
             assert w in (4, 8, 16) and 1 <= s <= MAX_ATTN_SPLITS
     assert decode_plan(32, 2, 4096) == (8, 4)
-    from omniserve_amd._lib import lib
+    from omniserver_amd._lib import lib
     assert lib().omni_gemm_slices(8960, 10) == 10
     assert lib().omni_gemm_slices(1536, 10) == 6
 
 
 # ----------------------------------------------------------------------------- control plane
 def test_sequence_finish_rules():
-    from omniserve_amd.request import Request, SamplingParams, Sequence, Status
+    from omniserver_amd.request import Request, SamplingParams, Sequence, Status
     s = Sequence(Request(prompt=[1, 2], sampling=SamplingParams(max_new_tokens=3,
                                                                 stop_token_ids=[9])))
     s.prompt_token_ids = [1, 2]
@@ -163,8 +163,8 @@ def test_sequence_finish_rules():
 def test_stub_runner_engine_loop():
     """The reference's control-plane double (runners/base.py:60-91) driven like
     LLMEngine.step: prefill new sequences, decode running ones, retire finished."""
-    from omniserve_amd.request import Request, SamplingParams, Sequence, Status
-    from omniserve_amd.runner import StubRunner
+    from omniserver_amd.request import Request, SamplingParams, Sequence, Status
+    from omniserver_amd.runner import StubRunner
     r = StubRunner("a b c")
     seqs = [Sequence(Request(prompt="x y z", sampling=SamplingParams(max_new_tokens=n)))
             for n in (1, 3, 5)]
@@ -183,7 +183,7 @@ def test_stub_runner_engine_loop():
 
 
 def test_synth_is_deterministic():
-    from omniserve_amd import synth
+    from omniserver_amd import synth
     a = synth.gptq_random(256, 32, 7, "x")
     b = synth.gptq_random(256, 32, 7, "x")
     c = synth.gptq_random(256, 32, 7, "y")

@@ -129,7 +129,7 @@ def test_mrope_positions_config5_closed_form():
 
 
 def test_mrope_positions_two_images_and_product_agree():
-    from omniserve_amd.positions import mrope_positions
+    from omniserver_amd.positions import mrope_positions
     ids = [1, 2] + [151655] * 4 + [3] + [151655] * 9 + [4, 5]
     grids = [(1, 4, 4), (1, 6, 6)]
     pos, d = ref.mrope_position_ids(ids, grids)

@@ -59,13 +59,15 @@ struct AttnArgs {
   int s0, s1;
 };
 
-#define ATT_MAXPARTS 16
+#define ATT_MAXPARTS 8   // qkv partial slices the fused prologue sums (one batch of loads)
 
 __device__ __forceinline__ int64_t clamp64(int64_t v, int64_t lo, int64_t hi) {
   return v < lo ? lo : (v > hi ? hi : v);
 }
 
-template <int NWA>
+// FUSED: q and the new token's k / v come from the qkv partials (a.qparts != NULL); the
+// two forms are separate instantiations so that neither carries the other's wait states.
+template <int NWA, bool FUSED>
 __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_kernel(AttnArgs a) {
   constexpr int NT = NWA * 64;
   // The V tiles (block loop), the fused prologue's pre-rotation rows (before it) and
@@ -97,13 +99,23 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
   const int t = blk / (S * a.nkv);
   const int G = a.G;
   const int nh = a.nkv * G;
-  const bool fused = a.qparts != nullptr;
+  constexpr bool fused = FUSED;
 
-  // 1. Fused prologue loads that do not depend on the context length: this token's
-  //    q heads g*G .. g*G+G-1, k and v of kv head g as fp32 split-K partials (up to 8
-  //    slices in flight per element pair; more slices are added in a second pass).
+  // 1. Loads that do not depend on the context length, all issued before any is used (a
+  //    load placed after a store or a use would cost the prologue another memory round
+  //    trip): the context length and rope delta of this token's pool row and, for the
+  //    fused prologue, q heads g*G .. g*G+G-1 and k, v of kv head g as fp32 split-K partials
+  //    (at most ATT_MAXPARTS slices, all in flight at once) and their bias.  Optional operands are read through a valid stand-in address and
+  //    replaced by zero, so no load sits behind a branch.
+  const int64_t slot = a.slots ? a.slots[t] : t;
+  const bool slot_ok = slot >= 0 && slot < a.pool_rows;
+  const int64_t srow = slot_ok ? slot : 0;
+  const int64_t kv_raw = a.kv_len[a.kv_by_slot ? srow : t];
+  const int64_t* dptr = a.rope_delta ? a.rope_delta : a.kv_len;
+  const int64_t delta_raw = fused ? dptr[srow] : 0;
   constexpr int PI = ((ATT_FUSED_MAXG + 2) * ATT_HD / 2 + NT - 1) / NT;
   float2 pv[PI][8];
+  half2_t bias2[PI];
   const int nel2 = (G + 2) * (ATT_HD / 2);
   const int W = (nh + 2 * a.nkv) * ATT_HD;
   const int64_t ps = (int64_t)a.T * W;
@@ -115,24 +127,25 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
   };
   if (fused) {
     const float* rowp = a.qparts + (int64_t)t * W;
+    const half_t* bptr = a.qbias ? a.qbias : (const half_t*)a.qparts;
 #pragma unroll
     for (int j = 0; j < PI; ++j) {
+      // an element past the gathered row re-reads this thread's first one and is not used;
+      // a slot past nq re-reads the last slice and is not added
       const int i = threadIdx.x + j * NT;
-      if (i < nel2) {
-        const float* src = rowp + gathered_col(2 * i);
+      const int col = gathered_col(2 * (i < nel2 ? i : (int)threadIdx.x % nel2));
+      const float* src = rowp + col;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          if (u < a.nq) pv[j][u] = *(const float2*)(src + u * ps);
-          else pv[j][u] = make_float2(0.f, 0.f);
-        }
+      for (int u = 0; u < 8; ++u) {
+        const int uu = u < a.nq ? u : a.nq - 1;
+        pv[j][u] = *(const float2*)(src + uu * ps);
       }
+      bias2[j] = *(const half2_t*)(bptr + col);
     }
   }
 
   // 2. Context length, this workgroup's key range, the rotary row.
-  const int64_t slot = a.slots ? a.slots[t] : t;
-  const bool slot_ok = slot >= 0 && slot < a.pool_rows;
-  const int64_t L_raw = slot_ok ? a.kv_len[a.kv_by_slot ? slot : t] + a.kv_add : 0;
+  const int64_t L_raw = slot_ok ? kv_raw + a.kv_add : 0;
   const int64_t L = clamp64(L_raw, 0, a.max_len);
   // fused decode: the token written this step sits at index L - 1 (= kv_len[slot]); a row
   // already at capacity (kv_len >= max_len) writes nothing and attends to the pool as is.
@@ -150,14 +163,15 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
 
   half8_t csv = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
   if (fused && threadIdx.x < 16) {         // cos (threads 0-7) / sin (8-15) row at pos
-    int64_t pos = (slot_ok ? a.kv_len[slot] : 0) + (a.rope_delta && slot_ok ? a.rope_delta[slot] : 0);
+    int64_t pos = slot_ok ? kv_raw + (a.rope_delta ? delta_raw : 0) : 0;
     pos = clamp64(pos, 0, a.max_pos - 1);
     const half_t* tab = threadIdx.x < 8 ? a.cos_tab : a.sin_tab;
     csv = *(const half8_t*)(tab + pos * (ATT_HD / 2) + (threadIdx.x & 7) * 8);
   }
 
-  // 3. The first two K/V blocks of this wave go in flight.
-  const int64_t row_base = slot * (int64_t)a.max_len;
+  // 3. The first two K/V blocks of this wave (issued below).
+  const int64_t row_base = (slot_ok ? slot : 0) * (int64_t)a.max_len;
+  const int tok_hi = end > 0 ? end - 1 : 0;    // loads past the range re-read this row
   const half_t* kbase = a.k_cache + g * ATT_HD;
   const half_t* vbase = a.v_cache + g * ATT_HD;
   const int64_t tok_stride = (int64_t)a.nkv * ATT_HD;
@@ -167,7 +181,7 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       int tok = tb + 16 * j + c16;
-      tok = tok < end ? tok : end - 1;
+      tok = tok < tok_hi ? tok : tok_hi;
       const half_t* kp = kbase + (row_base + tok) * tok_stride + q16 * 8;
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) kf[j][ks] = __builtin_nontemporal_load((const half8_t*)(kp + ks * 32));
@@ -176,13 +190,23 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
     for (int r = 0; r < 8; ++r) {
       const int c = lane + 64 * r;          // 512 chunks of 8 halfs = 32 tokens x 128 dims
       int tok = tb + (c >> 4);
-      tok = tok < end ? tok : end - 1;
+      tok = tok < tok_hi ? tok : tok_hi;
       vr[r] = __builtin_nontemporal_load((const half8_t*)(vbase + (row_base + tok) * tok_stride + (c & 15) * 8));
     }
   };
   half8_t kf0[2][4], vr0[8], kf1[2][4], vr1[8];
-  if (beg < end) load_block(kf0, vr0, beg);
-  if (beg + ATT_BLK < end) load_block(kf1, vr1, beg + ATT_BLK);
+  // Both first blocks are loaded unconditionally (a wave with fewer re-reads its last row,
+  // from cache): with branches around them the compiler drains the first block's loads
+  // before issuing the second's.
+  auto issue_first_blocks = [&]() {
+    load_block(kf0, vr0, beg);
+    load_block(kf1, vr1, beg + ATT_BLK);
+  };
+  // Without the fused prologue the stream starts at once.  With it, the K/V stream starts
+  // once the prologue's loads (the qkv partials and bias, cache-resident) have returned:
+  // issued behind the whole grid's K/V requests they would wait for nearly all of the
+  // context to arrive.  The rest of the prologue (LDS, M-RoPE) overlaps the stream.
+  if (!fused) issue_first_blocks();
 
   if (fused) {
     // 4. Partial sums (slice order, as the unfused path) + bias -> fp16 rows in LDS.
@@ -200,14 +224,9 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
           s0 += on ? pv[j][u].x : 0.f;
           s1 += on ? pv[j][u].y : 0.f;
         }
-        for (int p = 8; p < a.nq; ++p) {
-          const float2 v = *(const float2*)(rowp + col + p * ps);
-          s0 += v.x;
-          s1 += v.y;
-        }
         half_t h0 = (half_t)s0, h1 = (half_t)s1;
         if (a.qbias) {
-          const float b0 = (float)a.qbias[col], b1 = (float)a.qbias[col + 1];
+          const float b0 = (float)bias2[j][0], b1 = (float)bias2[j][1];
           h0 = a.bias_after_round ? (half_t)((float)h0 + b0) : (half_t)(s0 + b0);
           h1 = a.bias_after_round ? (half_t)((float)h1 + b1) : (half_t)(s1 + b1);
         }
@@ -216,7 +235,8 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
       }
     }
     if (threadIdx.x < 16) *(half8_t*)(&cs_lds[threadIdx.x >> 3][(threadIdx.x & 7) * 8]) = csv;
-    __syncthreads();
+    issue_first_blocks();   // every prologue load has been consumed above
+    lds_barrier();
     // 5. M-RoPE (decode: one position on all three axes) in fp16 ops, one rounding
     //    each and no contraction: y1 = x1*c + (-x2)*s, y2 = x2*c + x1*s.
     for (int i = threadIdx.x; i < (G + 1) * 64 + 64; i += NT) {
@@ -238,7 +258,7 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
         kv_new[1][2 * j + 1] = raw[(G + 1) * ATT_HD + 2 * j + 1];
       }
     }
-    __syncthreads();
+    lds_barrier();
     // 6. The workgroup whose blocks hold the new token stores its K/V row in the pool.
     const int nb = newtok >> 5;
     if (newtok >= 0 && nb >= wg_b0 && nb < wg_b1 && threadIdx.x < 32) {
@@ -491,10 +511,14 @@ static int launch_decode_attn(AttnArgs a, int n_kv_heads, int T, int G, int wave
   a.parts_out = splits > 1 || !merge;
   const int64_t nblocks = (int64_t)n_kv_heads * T * splits;
   if (nblocks > 0x7fffffff) return OMNI_EUNSUPPORTED;
-  switch (waves) {
-    case 4: hipLaunchKernelGGL(decode_attn_kernel<4>, dim3((unsigned)nblocks), dim3(256), 0, st, a); break;
-    case 8: hipLaunchKernelGGL(decode_attn_kernel<8>, dim3((unsigned)nblocks), dim3(512), 0, st, a); break;
-    default: hipLaunchKernelGGL(decode_attn_kernel<16>, dim3((unsigned)nblocks), dim3(1024), 0, st, a); break;
+  const bool fused = a.qparts != nullptr;
+  switch (waves * 2 + (fused ? 1 : 0)) {
+    case 8: hipLaunchKernelGGL((decode_attn_kernel<4, false>), dim3((unsigned)nblocks), dim3(256), 0, st, a); break;
+    case 9: hipLaunchKernelGGL((decode_attn_kernel<4, true>), dim3((unsigned)nblocks), dim3(256), 0, st, a); break;
+    case 16: hipLaunchKernelGGL((decode_attn_kernel<8, false>), dim3((unsigned)nblocks), dim3(512), 0, st, a); break;
+    case 17: hipLaunchKernelGGL((decode_attn_kernel<8, true>), dim3((unsigned)nblocks), dim3(512), 0, st, a); break;
+    case 32: hipLaunchKernelGGL((decode_attn_kernel<16, false>), dim3((unsigned)nblocks), dim3(1024), 0, st, a); break;
+    default: hipLaunchKernelGGL((decode_attn_kernel<16, true>), dim3((unsigned)nblocks), dim3(1024), 0, st, a); break;
   }
   OMNI_CHECK_LAUNCH();
   if (splits > 1 && merge) {

@@ -257,6 +257,15 @@ __device__ __forceinline__ half8_t attn_merge8(const float* __restrict__ rec0, i
   return attn_merge8_result(st);
 }
 
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS operations
+// (lgkmcnt(0)) and not for its outstanding global loads, so a stream of global loads issued
+// before it stays in flight across the barrier (__syncthreads would first drain them: its
+// workgroup-scope fence waits for vmcnt(0)).  Use only where no global memory written by
+// another wave of the workgroup is read after the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 __device__ __forceinline__ f32x4 mfma16x16x32(half8_t a, half8_t b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }

@@ -115,7 +115,10 @@ __device__ __forceinline__ half_t finish_store(float v, const GemvArgs& a, int n
 }
 
 // Dynamic LDS: the x tile [MB*16 rows][KC + 8 halfs], reused for the KW reduction.
-template <int WF, int MB, int EPI, int CPW, int CW, int KW, int PF, int XS = 0>
+// XF = 1: x is staged in LDS before any weight is requested (for a projection whose
+// workgroups stage a large x, so that x does not queue behind the grid's weight stream);
+// XF = 0: the weight stream is issued first and staging overlaps it.
+template <int WF, int MB, int EPI, int CPW, int CW, int KW, int PF, int XS = 0, int XF = 0>
 __global__ __launch_bounds__(CW * KW * 64) void gemv_kernel(GemvArgs a) {
 #pragma clang fp contract(off)
   static_assert(EPI != EPI_ARGMAX || KW == 1, "argmax epilogue uses every wave of the workgroup");
@@ -210,7 +213,7 @@ __global__ __launch_bounds__(CW * KW * 64) void gemv_kernel(GemvArgs a) {
   //    code below are exact instead of assuming the worst case.
   WStream<WF> ws[CPW];
   WFrag<WF> buf[PF][CPW];
-  {
+  auto issue_weights = [&]() {
     // a wave without groups re-reads the slice's first group (loaded by wave kw = 0,
     // so it is served from cache, not HBM)
     const int gmax = myg > 0 ? myg - 1 : 0;
@@ -221,53 +224,63 @@ __global__ __launch_bounds__(CW * KW * 64) void gemv_kernel(GemvArgs a) {
     for (int p = 0; p < PF; ++p)
 #pragma unroll
       for (int c = 0; c < CPW; ++c) ws[c].load(buf[p][c], min(p, gmax));
-  }
+  };
+  if constexpr (!XF) issue_weights();
 
   // 3. finish staging x[0:M, k0:k0+kc] in LDS (rows >= M zero)
   const half8_t zero8 = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
-  if constexpr (XS == 1) {
-    if (x_single) {
-      Merge8State st;
-      attn_merge8_batch(st, ml, a.aS);
-      if (m_rec != a.KC) *(half8_t*)(xs + m_rec) = m_live ? attn_merge8_result(st) : zero8;
-    } else {
-      const int64_t sstride = (int64_t)a.aG * ATT_REC;
-      for (int i = threadIdx.x; i < xtotal; i += NTH) {
-        half8_t v = zero8;
-        if (xr < a.M) {
-          const int k = k0 + xc * 8;
-          const int head = k >> 7;
-          const float* rec0 = a.apart + ((((int64_t)xr * a.a_nkv + head / a.aG) * a.aS) * a.aG +
-                                         head % a.aG) * ATT_REC;
-          v = attn_merge8(rec0, sstride, a.aS, k & 127);
+  auto stage_x = [&]() {
+    if constexpr (XS == 1) {
+      if (x_single) {
+        Merge8State st;
+        attn_merge8_batch(st, ml, a.aS);
+        if (m_rec != a.KC) *(half8_t*)(xs + m_rec) = m_live ? attn_merge8_result(st) : zero8;
+      } else {
+        const int64_t sstride = (int64_t)a.aG * ATT_REC;
+        for (int i = threadIdx.x; i < xtotal; i += NTH) {
+          half8_t v = zero8;
+          if (xr < a.M) {
+            const int k = k0 + xc * 8;
+            const int head = k >> 7;
+            const float* rec0 = a.apart + ((((int64_t)xr * a.a_nkv + head / a.aG) * a.aS) * a.aG +
+                                           head % a.aG) * ATT_REC;
+            v = attn_merge8(rec0, sstride, a.aS, k & 127);
+          }
+          *(half8_t*)(xs + xr * xstride + xc * 8) = v;
+          xstep();
         }
-        *(half8_t*)(xs + xr * xstride + xc * 8) = v;
-        xstep();
       }
-    }
-  } else if (a.xl) {
-    // (a chunk past the slice stores nothing: many lanes writing one pad address would
-    // serialise on its LDS bank)
-#pragma unroll
-    for (int u = 0; u < 8; ++u)
-      if (xo[u] != a.KC) *(half8_t*)(xs + xo[u]) = xlive[u] ? xv[u] : zero8;
-    for (int base = threadIdx.x + 8 * NTH; base < xtotal; base += 8 * NTH) {
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const bool ok = base + u * NTH < xtotal;
-        xlive[u] = ok && xr < a.M;
-        const int rr = xlive[u] ? xr : 0;
-        const int cc = ok ? xc : 0;
-        xv[u] = *(const half8_t*)(a.x + (int64_t)rr * a.ldx + k0 + cc * 8);
-        xo[u] = ok ? xr * xstride + xc * 8 : a.KC;
-        xstep();
-      }
+    } else if (a.xl) {
+      // (a chunk past the slice stores nothing: many lanes writing one pad address would
+      // serialise on its LDS bank)
 #pragma unroll
       for (int u = 0; u < 8; ++u)
         if (xo[u] != a.KC) *(half8_t*)(xs + xo[u]) = xlive[u] ? xv[u] : zero8;
+      for (int base = threadIdx.x + 8 * NTH; base < xtotal; base += 8 * NTH) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const bool ok = base + u * NTH < xtotal;
+          xlive[u] = ok && xr < a.M;
+          const int rr = xlive[u] ? xr : 0;
+          const int cc = ok ? xc : 0;
+          xv[u] = *(const half8_t*)(a.x + (int64_t)rr * a.ldx + k0 + cc * 8);
+          xo[u] = ok ? xr * xstride + xc * 8 : a.KC;
+          xstep();
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (xo[u] != a.KC) *(half8_t*)(xs + xo[u]) = xlive[u] ? xv[u] : zero8;
+      }
     }
+  };
+  if constexpr (XF) {
+    stage_x();
+    __syncthreads();
+    issue_weights();
+  } else {
+    stage_x();
+    lds_barrier();   // the weight stream stays in flight across the barrier
   }
-  __syncthreads();
 
   // 3. stream weights, MFMA against x from LDS
   f32x4 acc[CPW][MB];
@@ -333,15 +346,13 @@ __global__ __launch_bounds__(CW * KW * 64) void gemv_kernel(GemvArgs a) {
   // 4. sum the KW partial accumulators in LDS, in kw order
   if constexpr (KW > 1) {
     __syncthreads();                              // the x tile is no longer read
-    float* red = (float*)smem;                    // [KW-1][CW][CPW][MB][4][64]
+    f32x4* red = (f32x4*)smem;                    // [KW-1][CW][CPW][MB][64 lanes] x 4
     if (kw > 0) {
 #pragma unroll
       for (int c = 0; c < CPW; ++c)
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            red[((((kw - 1) * CW + cw) * CPW + c) * MB + mb) * 256 + i * 64 + lane] = acc[c][mb][i];
+          red[((((kw - 1) * CW + cw) * CPW + c) * MB + mb) * 64 + lane] = acc[c][mb];
     }
     __syncthreads();
     if (kw > 0) return;                           // no workgroup barrier follows
@@ -351,9 +362,7 @@ __global__ __launch_bounds__(CW * KW * 64) void gemv_kernel(GemvArgs a) {
       for (int c = 0; c < CPW; ++c)
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            acc[c][mb][i] += red[((((k2 - 1) * CW + cw) * CPW + c) * MB + mb) * 256 + i * 64 + lane];
+          acc[c][mb] += red[((((k2 - 1) * CW + cw) * CPW + c) * MB + mb) * 64 + lane];
   }
   // Lane holds rows 16*mb + 4*q16 + i, column (tile0 + c)*16 + c16.
 
@@ -441,7 +450,8 @@ __global__ __launch_bounds__(CW * KW * 64) void gemv_kernel(GemvArgs a) {
 //   2: (1, 4, 4)  16 waves, 4 tiles, K in quarters
 //   3: (2, 4, 2)   8 waves, 8 tiles
 // SiLU (gate/up pairs, CPW = 2): 0: (2, 4, 4), 1: (2, 8, 1), 2: (2, 4, 2), 3: (2, 2, 4),
-//   4: (2, 3, 4) (6 tiles: 187 workgroups for the 2B decoder's gate_up), 5: (2, 2, 8).
+//   4: (2, 3, 4) (6 tiles: 187 workgroups for the 2B decoder's gate_up), 5: (2, 2, 8);
+//   6, 7, 8, 9: (2, 3, 4), (2, 2, 4), (2, 4, 4), (2, 8, 1) with x staged first (XF).
 // Argmax: (2, 8, 1) (16 tiles).
 // ---------------------------------------------------------------------------
 static size_t max_dynamic_lds() {
@@ -456,9 +466,9 @@ static size_t max_dynamic_lds() {
   return (size_t)cached > 4096 ? (size_t)cached - 4096 : 0;
 }
 
-template <int WF, int MB, int EPI, int CPW, int CW, int KW, int PF, int XS>
+template <int WF, int MB, int EPI, int CPW, int CW, int KW, int PF, int XS, int XF>
 static int launch_gemv(GemvArgs a, hipStream_t st) {
-  auto kern = gemv_kernel<WF, MB, EPI, CPW, CW, KW, PF, XS>;
+  auto kern = gemv_kernel<WF, MB, EPI, CPW, CW, KW, PF, XS, XF>;
   const size_t lim = max_dynamic_lds();
   const size_t xbytes = (size_t)MB * 16 * (a.KC + 8) * sizeof(half_t);
   const size_t rbytes = (size_t)(KW > 1 ? KW - 1 : 0) * CW * CPW * MB * 256 * sizeof(float);
@@ -479,13 +489,13 @@ static int launch_gemv(GemvArgs a, hipStream_t st) {
   return OMNI_OK;
 }
 
-template <int WF, int EPI, int CPW, int CW, int KW, int PF, int XS = 0>
+template <int WF, int EPI, int CPW, int CW, int KW, int PF, int XS = 0, int XF = 0>
 static int dispatch_mb(const GemvArgs& a, hipStream_t st) {
   switch ((a.M + 15) / 16) {
-    case 1: return launch_gemv<WF, 1, EPI, CPW, CW, KW, PF, XS>(a, st);
-    case 2: return launch_gemv<WF, 2, EPI, CPW, CW, KW, PF, XS>(a, st);
-    case 3: return launch_gemv<WF, 3, EPI, CPW, CW, KW, PF, XS>(a, st);
-    case 4: return launch_gemv<WF, 4, EPI, CPW, CW, KW, PF, XS>(a, st);
+    case 1: return launch_gemv<WF, 1, EPI, CPW, CW, KW, PF, XS, XF>(a, st);
+    case 2: return launch_gemv<WF, 2, EPI, CPW, CW, KW, PF, XS, XF>(a, st);
+    case 3: return launch_gemv<WF, 3, EPI, CPW, CW, KW, PF, XS, XF>(a, st);
+    case 4: return launch_gemv<WF, 4, EPI, CPW, CW, KW, PF, XS, XF>(a, st);
     default: return OMNI_EUNSUPPORTED;
   }
 }
@@ -500,6 +510,11 @@ static int dispatch_preset(const GemvArgs& a, int preset, hipStream_t st) {
       case 3: return dispatch_mb<WF, EPI, 2, 2, 4, PF>(a, st);
       case 4: return dispatch_mb<WF, EPI, 2, 3, 4, PF>(a, st);
       case 5: return dispatch_mb<WF, EPI, 2, 2, 8, PF>(a, st);
+      // x staged before the weights are requested (XF)
+      case 6: return dispatch_mb<WF, EPI, 2, 3, 4, PF, 0, 1>(a, st);
+      case 7: return dispatch_mb<WF, EPI, 2, 2, 4, PF, 0, 1>(a, st);
+      case 8: return dispatch_mb<WF, EPI, 2, 4, 4, PF, 0, 1>(a, st);
+      case 9: return dispatch_mb<WF, EPI, 2, 8, 1, PF, 0, 1>(a, st);
       default: return dispatch_mb<WF, EPI, 2, 4, 4, PF>(a, st);
     }
   } else if constexpr (EPI == EPI_ARGMAX) {

@@ -36,16 +36,19 @@ MAX_SKINNY_M = 64
 # (weight format, K, N) -> (store preset, partial preset, partial ksplit); measured on
 # MI355X at M = 32 (graph-replayed launches).  Presets (tiles per wave, column waves,
 # in-group K split): 0 = (1, 8, 2), 1 = (1, 8, 1), 2 = (1, 4, 4), 3 = (2, 4, 2);
-# SiLU: 0 = (2, 4, 4), 1 = (2, 8, 1), 2 = (2, 4, 2), 3 = (2, 2, 4).
+# SiLU: 0 = (2, 4, 4), 1 = (2, 8, 1), 2 = (2, 4, 2), 3 = (2, 2, 4), 4 = (2, 3, 4), 5 = (2, 2, 8);
+# 6-9 = (2, 3, 4), (2, 2, 4), (2, 4, 4), (2, 8, 1) with x staged in LDS before the weight
+# stream is requested (the SiLU projection stages all of K, which otherwise queues behind
+# the grid's weight loads).
 PLANS: Dict[Tuple[str, int, int], Tuple[int, int, int]] = {
     ("int4", 1536, 2048): (2, 1, 7),
     ("int4", 1536, 1536): (2, 1, 12),     # o_proj: one head per K slice (attention merge)
     ("int4", 8960, 1536): (2, 1, 14),
-    ("int4", 1536, 17920): (4, 2, 1),     # SiLU-fused gate_up: preset 4 = (2, 3, 4)
+    ("int4", 1536, 17920): (6, 2, 1),     # SiLU-fused gate_up: preset 6 = (2, 3, 4), x first
     ("fp16", 1536, 2048): (2, 1, 7),
     ("fp16", 1536, 1536): (2, 1, 12),
     ("fp16", 8960, 1536): (2, 1, 14),
-    ("fp16", 1536, 17920): (4, 2, 1),
+    ("fp16", 1536, 17920): (6, 2, 1),
 }
 
 

@@ -258,12 +258,17 @@ def test_w4a16_gemm(gpu, M, K, N, bias, silu):
         e = ref.linear(x.float(), W, None if b is None else b.float(), bias_after_round=True)
     tol = 2e-3 * max(1.0, e.abs().max().item())
     xg = x.to(gpu)
-    presets = [None] if silu else [0, 1, 2, 3]
+    presets = [None, 1, 4, 6, 7, 9] if silu else [0, 1, 2, 3]
+    outs = {}
     for pr in presets:
         out = torch.empty(M, lin.out_features, device=gpu, dtype=torch.float16)
         lin.forward_out(xg, out, preset=pr)
+        outs[pr] = out.cpu()
         d = (out.cpu().float() - e).abs().max().item()
         assert d <= tol, (pr, d, tol)
+    if silu:
+        # x staged before (6, 7, 9) or after (4, 3, 1) the weights are requested: same sums
+        assert torch.equal(outs[4], outs[6]) and torch.equal(outs[1], outs[9])
     if not silu:
         # split-K partial sums (fp32, no bias): their slice-ordered sum is the GEMM
         e32 = x.float() @ W

@@ -16,10 +16,12 @@ The JSON line also carries:
   step's algorithmic bytes): algorithmic bytes per launch / its mean duration,
   timed with HIP events on the stream it runs on, against 8 TB/s;
 * ``step_roofline``: algorithmic bytes per step / ms_per_step against 8 TB/s;
+* ``fp8_gemm``: BASELINE configs[3], the FP8 W8A8 linears of one decoder layer at
+  M = 8192 (achieved dense TFLOP/s against the 5.0 PFLOP/s fp8 MFMA peak);
 * ``cpu_baseline``: the fp32 CPU restatement (oracle/) of the same step, timed on
   this host on a bounded sample.
 
-Usage: python bench.py [--gpus 1] [--steps 128] [--warmup 3] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps 128] [--warmup 3] [--no-cpu] [--no-fp8]
 """
 
 from __future__ import annotations
@@ -33,6 +35,7 @@ import time
 import torch
 
 PEAK_HBM = 8.0e12  # MI355X HBM3E, bytes/s
+PEAK_FP8 = 5.0e15  # MI355X dense fp8 MFMA, FLOP/s
 
 H, I, NL, NH, NKV, HD, V = 1536, 8960, 28, 12, 2, 128, 151936
 LINEARS = [(H, (NH + 2 * NKV) * HD), (NH * HD, H), (H, 2 * I), (I, H)]   # (K, N)
@@ -192,6 +195,36 @@ def traffic_from_profiles(kernel: str):
         return None
 
 
+def fp8_layer_gemms(device, M: int = 8192, reps: int = 10) -> dict:
+    """the FP8 e4m3fn W8A8 linears of one decoder layer on a packed
+    8 x 1024-token prefill (M = 8192): QKV 1536->2048, O 1536->1536, gate/up 1536->17920,
+    down 8960->1536.  Weights N(0, 0.02) quantised per output channel, activations N(0, 1)
+    quantised per token; the timed region is the fp8 MFMA GEMM (fp32 accumulate, bf16 ->
+    fp16 epilogue) with inputs resident in HBM.  Achieved dense TFLOP/s against the MI355X
+    fp8 peak (5.0 PFLOP/s)."""
+    from omniserver_amd.linear import FP8Linear
+    shapes = [("qkv", 1536, 2048), ("o", 1536, 1536), ("gate_up", 1536, 17920),
+              ("down", 8960, 1536)]
+    g = torch.Generator(device=device)
+    g.manual_seed(4)
+    per, tot_s, tot_f = {}, 0.0, 0.0
+    for name, K, N in shapes:
+        lin = FP8Linear((torch.randn(N, K, device=device, generator=g) * 0.02).half())
+        x = torch.randn(M, K, device=device, generator=g).half()
+        xq, sa = lin.quantize_input(x)
+        out = torch.empty(M, N, device=device, dtype=torch.float16)
+        t = time_kernel(lambda: lin.gemm_out(xq, sa, out, False), reps)
+        fl = 2.0 * M * N * K
+        per[name] = {"us": round(t * 1e6, 1), "tflops": round(fl / t / 1e12, 1)}
+        tot_s += t
+        tot_f += fl
+        del lin, x, xq, sa, out
+    return {"workload": f"one layer's W8A8 linears at M={M}", "gflop": round(tot_f / 1e9, 1),
+            "us": round(tot_s * 1e6, 1), "achieved": round(tot_f / tot_s / 1e12, 1),
+            "peak": PEAK_FP8 / 1e12, "unit": "TFLOP/s", "frac": round(tot_f / tot_s / PEAK_FP8, 4),
+            "per_shape": per}
+
+
 def cpu_baseline(runner, seqs, w, shape, budget_s: float = 15.0) -> dict:
     """fp32 CPU restatement (oracle) of the same decode step on this host's cores."""
     from oracle import qwen2_ref as ref
@@ -239,6 +272,8 @@ def main():
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--ctx", type=int, default=2048)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-fp8", action="store_true",
+                    help="skip the FP8 W8A8 GEMM leg (BASELINE configs[3])")
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--kernel-steps", type=int, default=10,
                     help="replays of the 28-launch attention graph timed for the roofline")
@@ -354,8 +389,14 @@ def main():
             "gate_up_w4a16_silu_us": round(t_gu * 1e6, 2),
             "gate_up_GBps": round(gu_bytes / t_gu / 1e9, 1),
         },
+        "fp8_gemm": None,
         "cpu_baseline": None,
     }
+    if not args.no_fp8:
+        try:
+            out["fp8_gemm"] = fp8_layer_gemms(dev)
+        except Exception as e:  # report, never fail the decode line on this leg
+            out["fp8_gemm"] = {"error": repr(e)}
     if not args.no_cpu:
         try:
             out["cpu_baseline"] = cpu_baseline(runner, seqs, w, shape)

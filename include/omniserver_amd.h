@@ -141,9 +141,11 @@ int omni_prefill_attention(const void* q, int q_stride, const void* k_cache, con
 
 /* GPTQMarlinLinear.forward (kernels/marlin_linear.py:54-62, 83-96): y = fp16(x . W), W =
  * fp16((q - 8) * s), bias added after the fp16 rounding when bias_after_round.  x fp16
- * [M <= 64, K] (row stride ldx); weights from omni_gptq_repack.  ksplit > 1 only with
- * OMNI_EPI_PARTIAL (slices = omni_gemm_slices(K, ksplit)).  preset selects the
- * workgroup shape (0..3). */
+ * [M, K] (row stride ldx); weights from omni_gptq_repack.  M <= 64 runs the skinny
+ * weight-streaming kernel: ksplit > 1 only with OMNI_EPI_PARTIAL (slices =
+ * omni_gemm_slices(K, ksplit)), preset selects the workgroup shape (0..3; SiLU 0..9).
+ * M > 64 (prefill) runs the tiled MFMA GEMM: OMNI_EPI_STORE / OMNI_EPI_SILU only, ksplit 1,
+ * preset ignored. */
 int omni_w4a16_gemm(const void* x, int ldx, const void* qweight_packed, const void* scales_packed,
                     const void* bias, int bias_after_round, void* out, int ldo, float* partial,
                     int M, int N, int K, int epilogue, int ksplit, int preset, void* stream);

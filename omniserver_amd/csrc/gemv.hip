@@ -530,6 +530,157 @@ static int dispatch_preset(const GemvArgs& a, int preset, hipStream_t st) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Tiled GEMM for many activation rows (prefill: M = packed prompt tokens), same packed
+// weight layouts and epilogues (STORE: fp16(acc) + bias, SILU: gate/up tile pairs) as
+// the skinny kernel above.
+//
+// One workgroup (4 waves, 2 x 2) owns a 128 (m) x 128 (n) output tile; wave (wm, wn) owns
+// rows 64 wm .. +63 and column tiles 4 wn .. +3 of it (4 x 4 MFMA 16x16x32 accumulators).
+// K advances one 128-group at a time: the x tile [128 x 128] fp16 is staged in LDS
+// (double buffered, loaded one group ahead into registers), the weight fragments are
+// read straight from the packed layout into registers (one 16-byte load per lane and
+// column tile for int4, four for fp16), also one group ahead.  Each staged x fragment
+// feeds 4 MFMAs and each weight fragment 4, per 32-k step.
+// ---------------------------------------------------------------------------
+#define GT_BM 128
+#define GT_BN 128
+#define GT_XSTRIDE 136     // LDS halfs per staged x row (128 + 8 pad)
+
+template <int WF, int EPI>
+__global__ __launch_bounds__(256, 1) void gemm_tile_kernel(GemvArgs a) {
+#pragma clang fp contract(off)
+  __shared__ __attribute__((aligned(16))) half_t xs[2][GT_BM * GT_XSTRIDE];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int q16 = lane >> 4, c16 = lane & 15;
+  const int NT = a.N >> 4;
+  const int tiles_n = (a.N + GT_BN - 1) / GT_BN;
+  // XCD-aware order: consecutive logical tiles share an x row block and sit on one XCD
+  const int blk = xcd_logical_block(blockIdx.x, gridDim.x);
+  const int tn = blk % tiles_n, tm = blk / tiles_n;
+  const int m0 = tm * GT_BM;
+  const int nt0 = tn * (GT_BN / 16) + wn * 4;   // this wave's first column tile
+  const int KG = a.K >> 7;
+
+  // x staging: thread t moves 16-byte chunks t + 256 u (u < 8) of the 128 x 128 tile:
+  // row (t + 256u) / 16, chunk t % 16.  Rows past M re-read row M - 1 (never stored).
+  const int xc = tid & 15;
+  const half_t* xsrc[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int r = (tid >> 4) + 16 * u;
+    xsrc[u] = a.x + (int64_t)min(m0 + r, a.M - 1) * a.ldx + xc * 8;
+  }
+  half8_t xr[8];
+  auto load_x = [&](int g) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) xr[u] = *(const half8_t*)(xsrc[u] + g * 128);
+  };
+  auto store_x = [&](int b) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) *(half8_t*)(&xs[b][((tid >> 4) + 16 * u) * GT_XSTRIDE + xc * 8]) = xr[u];
+  };
+
+  WStream<WF> ws[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) ws[c].init(a, min(nt0 + c, NT - 1), 0, lane);
+  WFrag<WF> wb[2][4];
+  auto load_w = [&](WFrag<WF>(&f)[4], int g) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) ws[c].load(f[c], g);
+  };
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[i][c] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](const half_t* xb, const WFrag<WF>(&f)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      half8_t af[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        af[i] = *(const half8_t*)(xb + (64 * wm + 16 * i + c16) * GT_XSTRIDE + 32 * j + 8 * q16);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        half8_t bf;
+        if constexpr (WF == W_INT4) {
+          const half2_t s2 = {f[c].s, f[c].s};
+          bf = dequant8(f[c].q[j], s2);
+        } else {
+          bf = f[c].h[j];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i][c] = mfma16x16x32(af[i], bf, acc[i][c]);
+      }
+    }
+  };
+
+  // Software pipeline over the K groups: group g + 1's x and weights are in flight while
+  // group g is multiplied.  Group g is staged in xs[g & 1]; the barrier at the top of an
+  // iteration also guarantees every wave finished reading that buffer two groups ago.
+  load_x(0);
+  load_w(wb[0], 0);
+  for (int g = 0; g < KG; g += 2) {
+    store_x(0);
+    __syncthreads();
+    if (g + 1 < KG) {
+      load_x(g + 1);
+      load_w(wb[1], g + 1);
+    }
+    compute(xs[0], wb[0]);
+    if (g + 1 >= KG) break;
+    store_x(1);
+    __syncthreads();
+    if (g + 2 < KG) {
+      load_x(g + 2);
+      load_w(wb[0], g + 2);
+    }
+    compute(xs[1], wb[1]);
+  }
+
+  // Epilogue.  Lane holds rows m0 + 64 wm + 16 i + 4 q16 + r, column (nt0 + c) * 16 + c16.
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = m0 + 64 * wm + 16 * i + 4 * q16 + r;
+      if (m >= a.M) continue;
+      if constexpr (EPI == EPI_SILU) {
+        // column tiles (2p, 2p+1) = (gate, up) of intermediate columns 16p .. 16p + 15
+#pragma unroll
+        for (int c = 0; c < 4; c += 2) {
+          if (nt0 + c + 1 >= NT) continue;
+          const int j = ((nt0 + c) >> 1) * 16 + c16;
+          const float gv = (float)(half_t)acc[i][c][r];
+          const float uv = (float)(half_t)acc[i][c + 1][r];
+          a.out[(int64_t)m * a.ldo + j] = (half_t)(silu_ref(gv) * uv);
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          if (nt0 + c >= NT) continue;
+          const int n = (nt0 + c) * 16 + c16;
+          a.out[(int64_t)m * a.ldo + n] = finish_store(acc[i][c][r], a, n);
+        }
+      }
+    }
+}
+
+template <int WF, int EPI>
+static int launch_gemm_tile(const GemvArgs& a, hipStream_t st) {
+  const int64_t tiles = (int64_t)((a.M + GT_BM - 1) / GT_BM) * ((a.N + GT_BN - 1) / GT_BN);
+  if (tiles > 0x7fffffff) return OMNI_EUNSUPPORTED;
+  hipLaunchKernelGGL((gemm_tile_kernel<WF, EPI>), dim3((unsigned)tiles), dim3(256), 0, st, a);
+  OMNI_CHECK_LAUNCH();
+  return OMNI_OK;
+}
+
 struct AttnIn {            // x from split decode-attention states (omni_*_gemm_attn)
   const float* part;
   int S, nkv, G;
@@ -540,7 +691,7 @@ static int gemv_common(int wf, const void* x, int ldx, const void* w, const void
                        float* partial, int M, int N, int K, int epilogue, int ksplit, int preset,
                        void* stream, const AttnIn* ain = nullptr) {
   if (M <= 0 || N <= 0 || K <= 0) return M == 0 ? OMNI_OK : OMNI_EINVAL;
-  if (M > 64) return OMNI_EUNSUPPORTED;
+  if (M > 64 && (ain || epilogue == EPI_PARTIAL)) return OMNI_EUNSUPPORTED;
   if ((N & 15) || (K & 127)) return OMNI_EUNSUPPORTED;
   if (!w || (wf == W_INT4 && !scales)) return OMNI_EINVAL;
   if (ain) {
@@ -578,6 +729,13 @@ static int gemv_common(int wf, const void* x, int ldx, const void* w, const void
   a.KC = ((KG + ksplit - 1) / ksplit) * 128;
   a.KS = (K + a.KC - 1) / a.KC;
   hipStream_t st = (hipStream_t)stream;
+  if (M > 64) {   // many rows (prefill): the tiled kernel, STORE / SILU epilogues
+    if (wf == W_INT4)
+      return epilogue == EPI_SILU ? launch_gemm_tile<W_INT4, EPI_SILU>(a, st)
+                                  : launch_gemm_tile<W_INT4, EPI_STORE>(a, st);
+    return epilogue == EPI_SILU ? launch_gemm_tile<W_FP16, EPI_SILU>(a, st)
+                                : launch_gemm_tile<W_FP16, EPI_STORE>(a, st);
+  }
   if (ain) {
     a.apart = ain->part;
     a.aS = ain->S;

@@ -11,8 +11,8 @@ an ``nn.Module`` with ``forward(x[..., K] fp16) -> [..., N] fp16`` installed by
 * ``F16Linear``    - fp16 ``nn.Linear`` replacement using the packed fp16 layout.
 * ``LMHeadArgmax`` - tied lm_head + greedy argmax.
 
-All run the skinny MFMA kernel (omni_w4a16_gemm / omni_f16_gemm) in blocks of at most
-64 activation rows.  ``fuse_silu=True`` (the gate_up projection) interleaves the gate
+All run omni_w4a16_gemm / omni_f16_gemm: the skinny weight-streaming kernel for up to
+64 activation rows (decode), the tiled MFMA GEMM beyond (prefill).  ``fuse_silu=True`` (the gate_up projection) interleaves the gate
 and up column tiles and emits silu(gate) * up directly: [.., 2I] -> [.., I].
 ``forward_partial`` writes fp32 split-K partial sums instead of fp16 output, for a
 consumer kernel (the next add+RMSNorm) that adds them in slice order.
@@ -78,13 +78,8 @@ class _Skinny(nn.Module):
         raise NotImplementedError
 
     def forward_out(self, x2d: torch.Tensor, out: torch.Tensor, preset: int | None = None):
-        """fp16 output (SiLU-fused for gate_up) into out; any number of rows."""
-        M = x2d.shape[0]
-        if M > MAX_SKINNY_M:
-            for s in range(0, M, MAX_SKINNY_M):
-                e = min(M, s + MAX_SKINNY_M)
-                self.forward_out(x2d[s:e], out[s:e], preset)
-            return out
+        """fp16 output (SiLU-fused for gate_up) into out; any number of rows (more than
+        MAX_SKINNY_M rows run the library's tiled MFMA GEMM, ``preset`` then unused)."""
         epi = EPI_SILU if self.fuse_silu else EPI_STORE
         self._call(x2d, out, None, epi, 1, self.store_preset if preset is None else preset)
         return out

@@ -281,6 +281,46 @@ def test_w4a16_gemm(gpu, M, K, N, bias, silu):
                 assert d <= 1e-3 * max(1.0, e32.abs().max().item()), (ks, pr, d)
 
 
+@pytest.mark.parametrize("fmt", ["int4", "fp16"])
+@pytest.mark.parametrize("M", [65, 300])
+@pytest.mark.parametrize("K,N,bias,silu", [
+    (1536, 2048, True, False), (8960, 1536, False, False), (1536, 17920, False, True),
+    (256, 48, True, False),
+])
+def test_tiled_gemm(gpu, fmt, M, K, N, bias, silu):
+    """Prefill-size linears (M > 64) run the tiled MFMA GEMM: within tolerance of the
+    oracle, and bit-equal to the skinny kernel run over 64-row blocks with one wave per
+    K range (the same k order: groups ascending, 32-k steps ascending)."""
+    from omniserver_amd.linear import F16Linear, GPTQLinear
+    say(f"tiled gemm fmt={fmt} M={M} K={K} N={N} bias={bias} silu={silu}")
+    b = f16((N,), 91, 0.02) if bias else None
+    x = f16((M, K), 92)
+    if fmt == "int4":
+        qw, sc = _gptq(K, N, 93 + K + N)
+        W = ref.gptq_dequant(qw, sc)
+        lin = GPTQLinear(qw.to(gpu), sc.to(gpu), None if b is None else b.to(gpu), fuse_silu=silu)
+    else:
+        wt = f16((N, K), 94, 0.02)
+        W = wt.float().t()
+        lin = F16Linear(wt.to(gpu), None if b is None else b.to(gpu), fuse_silu=silu)
+    if silu:
+        e = ref.silu_mul(ref.linear(x.float(), W))
+    else:
+        e = ref.linear(x.float(), W, None if b is None else b.float(),
+                       bias_after_round=fmt == "int4")
+    xg = x.to(gpu)
+    out = torch.empty(M, lin.out_features, device=gpu, dtype=torch.float16)
+    lin.forward_out(xg, out)
+    torch.cuda.synchronize()
+    d = (out.cpu().float() - e).abs().max().item()
+    assert d <= 2e-3 * max(1.0, e.abs().max().item()), d
+    blocks = torch.empty_like(out)
+    for s0 in range(0, M, 64):
+        s1 = min(M, s0 + 64)
+        lin.forward_out(xg[s0:s1], blocks[s0:s1], preset=1)
+    assert torch.equal(out.cpu(), blocks.cpu())
+
+
 @pytest.mark.parametrize("M", [1, 16, 32])
 @pytest.mark.parametrize("K,N,bias,silu", [
     (1536, 2048, True, False), (8960, 1536, False, False), (1536, 17920, False, True),

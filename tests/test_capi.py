@@ -64,9 +64,13 @@ def test_bad_arguments_rejected_before_launch(so):
                                    2, 64, 0.1, 4, 1, None, None) == -2
     assert L.omni_decode_attention(None, 1536, None, None, 1, 16, None, None, 0, 0, None, 1, 12,
                                    2, 128, 0.1, 4, 0, None, None) == -1
-    # skinny GEMM: too many rows, K not a multiple of 128, split without partial epilogue
+    # GEMM: split-K partials past the skinny kernel's 64 rows, K not a multiple of 128,
+    # split without partial epilogue; more rows with the STORE epilogue are the tiled GEMM
+    # (here rejected for its null pointers, not its size)
     assert L.omni_w4a16_gemm(None, 1536, None, None, None, 1, None, 2048, None, 65, 2048, 1536,
-                             0, 1, 2, None) == -2
+                             2, 1, 2, None) == -2
+    assert L.omni_w4a16_gemm(None, 1536, None, None, None, 1, None, 2048, None, 65, 2048, 1536,
+                             0, 1, 2, None) == -1
     assert L.omni_w4a16_gemm(None, 1536, None, None, None, 1, None, 2048, None, 32, 2048, 1500,
                              0, 1, 2, None) == -2
     fake = ctypes.c_void_p(16)   # never dereferenced: validation fails first

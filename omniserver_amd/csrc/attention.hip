@@ -23,7 +23,8 @@
 
 #define ATT_HD 128
 #define ATT_BLK 32
-#define ATT_VSTRIDE 136   // LDS row stride (halfs) of the V tile: 16B-aligned, bank-spread
+#define ATT_VSTRIDE 144   // LDS row stride (halfs) of the V tile: rows 8 banks apart, so the
+                          // 4 rows x 32 bytes of one 16-lane transpose read hit 32 distinct banks
 #define ATT_MAXG 16       // query heads per KV head supported (MFMA N = 16)
 #define ATT_FUSED_MAXG 8  // ... by the fused decode prologue
 #define ATT_WAVES 4       // waves per workgroup of the prefill kernel
@@ -73,7 +74,7 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
   // The V tiles (block loop), the fused prologue's pre-rotation rows (before it) and
   // the per-wave partial outputs (after it) share one LDS buffer.
   constexpr int kVsBytes = NWA * ATT_BLK * ATT_VSTRIDE * 2;
-  constexpr int kOBytes = NWA * 8 * ATT_HD * 4;
+  constexpr int kOBytes = NWA * ATT_MAXG * ATT_HD * 4;
   constexpr int kRawBytes = (ATT_FUSED_MAXG + 2) * ATT_HD * 2;
   constexpr int kSmem = kVsBytes > kOBytes ? (kVsBytes > kRawBytes ? kVsBytes : kRawBytes)
                                            : (kOBytes > kRawBytes ? kOBytes : kRawBytes);
@@ -83,7 +84,8 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
   __shared__ __attribute__((aligned(16))) half_t kv_new[2][ATT_HD];
   __shared__ __attribute__((aligned(16))) half_t cs_lds[2][ATT_HD / 2];
   half_t (*vs_lds)[ATT_BLK * ATT_VSTRIDE] = (half_t (*)[ATT_BLK * ATT_VSTRIDE])smem;
-  float (*o_lds)[8][ATT_HD] = (float (*)[8][ATT_HD])smem;   // heads < 8 are combined
+  // per-wave partial outputs for the merge: [wave][head][c16][dt] = O[head][16 dt + c16]
+  float (*o_lds)[ATT_MAXG][16][8] = (float (*)[ATT_MAXG][16][8])smem;
   half_t* raw = (half_t*)smem;   // fused: [G + 2][128] q heads | k | v before M-RoPE
 
   const int lane = threadIdx.x & 63;
@@ -365,12 +367,7 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
-      half8_t vb;
-#pragma unroll
-      for (int s8 = 0; s8 < 8; ++s8) {
-        const int tok = 16 * (s8 >> 2) + 4 * q16 + (s8 & 3);
-        vb[s8] = vs[tok * ATT_VSTRIDE + dt * 16 + c16];
-      }
+      const half8_t vb = lds_read_b_tr16(vs + dt * 16, ATT_VSTRIDE, q16, c16);
       o_acc[dt] = mfma16x16x32(pa, vb, o_acc[dt]);
     }
     __builtin_amdgcn_wave_barrier();
@@ -385,50 +382,59 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
   l_run += __shfl_xor(l_run, 32, 64);
   __syncthreads();   // every wave is done with its V tile before o_lds reuses the space
 
-  // Merge the waves' softmax states: heads processed in groups of 8 (G <= 16).
+  // Merge the waves' softmax states.  Lane (q16, c16) holds O[head 4 q16 + i][16 dt + c16];
+  // it stores them as 32 contiguous bytes per head, so that thread (h, c) of the merge
+  // reads the 8 dims 16 dt + c of every wave with two 16-byte LDS reads.
   if (lane < G) {
     ml_lds[wave][lane][0] = m_run;
     ml_lds[wave][lane][1] = l_run;
   }
-  for (int hb = 0; hb < G; hb += 8) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int h = 4 * q16 + i - hb;
-      if (h >= 0 && h < 8 && h + hb < G) {
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) o_lds[wave][h][dt * 16 + c16] = o_acc[dt][i];
-      }
+  for (int i = 0; i < 4; ++i) {
+    const int h = 4 * q16 + i;
+    if (h < G) {
+      f32x4 lo = {o_acc[0][i], o_acc[1][i], o_acc[2][i], o_acc[3][i]};
+      f32x4 hi = {o_acc[4][i], o_acc[5][i], o_acc[6][i], o_acc[7][i]};
+      *(f32x4*)&o_lds[wave][h][c16][0] = lo;
+      *(f32x4*)&o_lds[wave][h][c16][4] = hi;
     }
-    __syncthreads();
-    const int hn = min(8, G - hb);
-    for (int idx = threadIdx.x; idx < hn * ATT_HD; idx += NWA * 64) {
-      const int h = idx / ATT_HD;
-      const int d = idx % ATT_HD;
-      float M = -INFINITY;
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < G * 16) {
+    const int h = threadIdx.x >> 4;
+    const int c = threadIdx.x & 15;
+    float M = -INFINITY;
 #pragma unroll
-      for (int w = 0; w < NWA; ++w) M = fmaxf(M, ml_lds[w][hb + h][0]);
-      float lsum = 0.f, o = 0.f;
-      if (M != -INFINITY) {
+    for (int w = 0; w < NWA; ++w) M = fmaxf(M, ml_lds[w][h][0]);
+    float lsum = 0.f;
+    float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (M != -INFINITY) {
 #pragma unroll
-        for (int w = 0; w < NWA; ++w) {
-          const float f = exp2f(ml_lds[w][hb + h][0] - M);
-          lsum += f * ml_lds[w][hb + h][1];
-          o += f * o_lds[w][h][d];
-        }
-      }
-      if (!a.parts_out) {
-        const float r = lsum > 0.f ? o / lsum : 0.f;
-        a.out[((int64_t)t * nh + g * G + hb + h) * ATT_HD + d] = (half_t)r;
-      } else {
-        float* pp = a.part + ((((int64_t)t * a.nkv + g) * S + sp) * G + hb + h) * ATT_REC;
-        pp[d] = o;
-        if (d == 0) {
-          pp[ATT_HD] = M;
-          pp[ATT_HD + 1] = lsum;
+      for (int w = 0; w < NWA; ++w) {
+        const float f = exp2f(ml_lds[w][h][0] - M);
+        lsum += f * ml_lds[w][h][1];
+        const f32x4 lo = *(const f32x4*)&o_lds[w][h][c][0];
+        const f32x4 hi = *(const f32x4*)&o_lds[w][h][c][4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          o[e] += f * lo[e];
+          o[4 + e] += f * hi[e];
         }
       }
     }
-    __syncthreads();
+    if (!a.parts_out) {
+      half_t* op = a.out + ((int64_t)t * nh + g * G + h) * ATT_HD + c;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) op[16 * dt] = (half_t)(lsum > 0.f ? o[dt] / lsum : 0.f);
+    } else {
+      float* pp = a.part + ((((int64_t)t * a.nkv + g) * S + sp) * G + h) * ATT_REC;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) pp[16 * dt + c] = o[dt];
+      if (c == 0) {
+        pp[ATT_HD] = M;
+        pp[ATT_HD + 1] = lsum;
+      }
+    }
   }
 }
 
@@ -734,12 +740,7 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
-      half8_t vb;
-#pragma unroll
-      for (int s8 = 0; s8 < 8; ++s8) {
-        const int tok = 16 * (s8 >> 2) + 4 * q16 + (s8 & 3);
-        vb[s8] = vs[tok * ATT_VSTRIDE + dt * 16 + c16];
-      }
+      const half8_t vb = lds_read_b_tr16(vs + dt * 16, ATT_VSTRIDE, q16, c16);
       o_acc[dt] = mfma16x16x32(pa, vb, o_acc[dt]);
     }
     __builtin_amdgcn_wave_barrier();

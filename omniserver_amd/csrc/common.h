@@ -266,6 +266,24 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// MFMA 16x16x32 B operand of 32 k (rows of a row-major fp16 tile in LDS) x 16 n (columns),
+// read transposed with two ds_read_b64_tr_b16.  The transpose read works per group of 16
+// lanes: if lane i of a group addresses the 4 halves M[i][0..3], lane j receives
+// (M[4k + j/4][j%4], k = 0..3).  Lane (q16, c16) needs rows rows(q16) + 0..3 of column
+// c16 for its first four k and rows 16 + rows(q16) + 0..3 for the next four, so lane i of
+// group q16 addresses row 4 q16 + i/4, columns 4 (i%4) .. +3 (then 16 rows further).
+// tile: the 16-column block's first element in row 0; stride: halfs per LDS row (a
+// multiple of 4).  Lane slot s of the result holds row 16 (s/4) + 4 q16 + s%4, column c16.
+__device__ __forceinline__ half8_t lds_read_b_tr16(const half_t* tile, int stride, int q16, int c16) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  const half_t* p0 = tile + (4 * q16 + (c16 >> 2)) * stride + 4 * (c16 & 3);
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p0);
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p0 + 16 * stride));
+  const half4_t l = __builtin_bit_cast(half4_t, lo), h = __builtin_bit_cast(half4_t, hi);
+  return (half8_t){l[0], l[1], l[2], l[3], h[0], h[1], h[2], h[3]};
+}
+
 __device__ __forceinline__ f32x4 mfma16x16x32(half8_t a, half8_t b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }

@@ -146,6 +146,19 @@ __device__ __forceinline__ int xcd_logical_block(int b, int n) {
   return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + local;
 }
 
+// Grouped tile order for GEMMs: logical tile L -> (tm, tn) walking groups of GM tile rows
+// column by column, so that a run of consecutive logical tiles (the ones one XCD holds at a
+// time under xcd_logical_block) covers a GM x (run / GM) block and shares both operands
+// in that XCD's L2.  A bijection on [0, tiles_m * tiles_n).
+__device__ __forceinline__ void grouped_tile(int L, int tiles_m, int tiles_n, int GM, int& tm, int& tn) {
+  const int per_group = GM * tiles_n;
+  const int grp = L / per_group;
+  const int idx = L - grp * per_group;
+  const int rows = min(GM, tiles_m - grp * GM);
+  tm = grp * GM + idx % rows;
+  tn = idx / rows;
+}
+
 // sum[e] += base[p * stride + e] for p = 0 .. n-1 in ascending order (e = 0..7, fp32 split-K
 // slices).  Loads go out in batches of BATCH before the first add of the batch, so n
 // slices cost ceil(n/BATCH) memory round trips, not n; a slot past n adds +0.0f (sum is

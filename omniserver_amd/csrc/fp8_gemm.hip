@@ -160,6 +160,284 @@ __global__ __launch_bounds__(256, 2) void fp8_gemm_kernel(Fp8GemmArgs a) {
   }
 }
 
+// Pipelined, persistent form of the same GEMM (the default for K >= 4 steps).  A grid of at most one
+// workgroup per CU walks its tiles round by round (round r, slot b: logical tile r * grid
+// + b, slots XCD-grouped as above, logical tiles in grouped order so the 32 tiles an XCD
+// holds at once form a 4 x 8 block), and the K loop runs straight across tile boundaries,
+// so the next tile's first operand tiles are in flight while the current one finishes
+// and writes its outputs.
+// Operand tiles go global -> LDS directly (global_load_lds_dwordx4: lane i of a load
+// writes bytes 16 i .. 16 i + 15 past the instruction's LDS base), F8_NS stages deep: the
+// loads for step s + F8_NS - 1 are in flight while step s is multiplied.  LDS rows are
+// 128 bytes (one K step of one row); 16-byte chunk c of row r is stored in slot
+// c ^ (r & 7), so the 16 rows an operand read touches spread over the banks.  A stage is
+// waited for with vmcnt (each thread's own loads: every stage issues 5 per thread, the
+// operands and a share of the tile's row / column scales, and wave 0 a sixth with the
+// biases, so waiting for all but the 5 (F8_NS - 3) newest stages' loads covers a stage)
+// plus a barrier (everyone's).  A step's operands are read into registers before that
+// barrier, so its slot is refilled right after it, while the step's MFMAs run.
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+#define F8_NS 4
+#define F8_GM 4                        // tile rows per group of the tile order (grouped_tile)
+#define F8_ROWB 128                    // LDS bytes per staged row
+#define F8_TILEB (F8_BT * F8_ROWB)     // one operand tile of one stage
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
+
+// bf16 bits of f, round to nearest even, NaN kept quiet; branch-free.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, f);
+  const uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  return (u & 0x7fffffffu) > 0x7f800000u ? ((u >> 16) | 0x0040u) : r;
+}
+
+// One tile's load sources: per-lane x row pointers (rows clamped below M) for the four
+// row groups, the w row pointer of group 0 (groups u are 32 u rows further), the lane's
+// scale pointer and (wave 0) bias pointer.
+struct F8TileSrc {
+  const uint8_t* x[4];
+  const uint8_t* w;
+  const void* s;
+  const void* b;
+};
+
+__global__ __launch_bounds__(256, 1) void fp8_gemm_pipe_kernel(Fp8GemmArgs a) {
+#pragma clang fp contract(off)
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[F8_NS][2][F8_TILEB];   // [stage][x|w]
+  __shared__ __attribute__((aligned(16))) float scl[F8_NS][2 * F8_BT];         // [stage][sa|sw]
+  __shared__ __attribute__((aligned(16))) half_t bsl[F8_NS][512];              // [stage][bias]
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wave & 1;
+  const int wm = wave >> 1;
+  const int l16 = lane & 15;
+  const int g4 = lane >> 4;
+
+  const int tiles_n = a.N / F8_BT;
+  const int tiles_m = (a.M + F8_BT - 1) / F8_BT;
+  const int tiles = tiles_m * tiles_n;
+  const int G = gridDim.x;
+  const int slot = xcd_logical_block(blockIdx.x, G);
+  const int my_tiles = (tiles - slot + G - 1) / G;          // grid <= tiles: >= 1
+  const int nk = a.K / F8_BK;                               // >= F8_NS - 1 (host check)
+
+  // Load u (0..3) of this wave fills tile rows 32u + 8 wave .. +7: lane i -> row
+  // 32u + 8 wave + i/8, LDS slot i%8, which holds chunk (i%8) ^ (row & 7).  A fifth,
+  // 4-byte-per-lane load brings 64 of the tile's 256 scales: waves 0, 1 the token scales
+  // sa[m0 + 64 wave + lane], waves 2, 3 the channel scales sw[n0 + 64 (wave - 2) + lane].
+  const int lrow = 8 * wave + (lane >> 3);          // + 32u
+  const int lchunk = (lane & 7) ^ (lrow & 7);       // (32u + lrow) & 7 == lrow & 7
+  typedef __attribute__((address_space(3))) void lds_void;
+  typedef __attribute__((address_space(3))) uint8_t lds_u8;
+  const bool has_bias = a.bias != nullptr;
+  auto tile_src = [&](int r, int& m0, int& n0) {     // past the last tile: the last one again
+    int tm, tn;
+    grouped_tile(min(r, my_tiles - 1) * G + slot, tiles_m, tiles_n, F8_GM, tm, tn);
+    m0 = tm * F8_BT;
+    n0 = tn * F8_BT;
+    F8TileSrc t;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      t.x[u] = a.xq + (int64_t)min(m0 + 32 * u + lrow, a.M - 1) * a.K + lchunk * 16;
+    t.w = a.wq + (int64_t)(n0 + lrow) * a.K + lchunk * 16;
+    t.s = wave < 2 ? (const void*)(a.sa + min(m0 + 64 * wave + lane, a.M - 1))
+                   : (const void*)(a.sw + n0 + 64 * (wave - 2) + lane);
+    t.b = has_bias ? (const void*)(a.bias + n0 + 8 * min(lane, 15)) : t.s;
+    return t;
+  };
+  const int64_t wstep = (int64_t)32 * a.K;          // bytes between w row groups
+  auto issue = [&](const F8TileSrc& t, int ks, int st) {
+    const int k0 = ks * F8_BK;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      __builtin_amdgcn_global_load_lds((const void*)(t.x[u] + k0),
+                                       (lds_void*)((lds_u8*)&lds[st][0][(32 * u + 8 * wave) * F8_ROWB]), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(t.w + u * wstep + k0),
+                                       (lds_void*)((lds_u8*)&lds[st][1][(32 * u + 8 * wave) * F8_ROWB]), 16, 0, 0);
+    }
+    __builtin_amdgcn_global_load_lds(t.s, (lds_void*)((lds_u8*)&scl[st][64 * wave]), 4, 0, 0);
+    if (wave == 0 && has_bias)        // the tile's 128 fp16 biases (lanes 0-15; a sixth load,
+      __builtin_amdgcn_global_load_lds(t.b, (lds_void*)((lds_u8*)&bsl[st][0]), 16, 0, 0);   // wave 0 only)
+  };
+  // LDS reads of the staged tiles are inline asm with their own lgkmcnt wait: written as
+  // plain loads, the compiler makes each of them wait for every outstanding
+  // global->LDS load (vmcnt(0)), which are the later stages in flight; the stage read is
+  // complete by the vmcnt wait and barrier before it.
+  // Addresses of the 32 operand bytes (k = 32 g4 .. +31) of tile rows base + 16 i + l16.
+  auto operand_addrs = [&](int st, int o, int base, uint32_t (&ad)[8]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = base + 16 * i + l16;
+      const uint32_t row = (uint32_t)(uintptr_t)(lds_u8*)&lds[st][o][r * F8_ROWB];
+      ad[2 * i] = row + (((2 * g4) ^ (r & 7)) << 4);
+      ad[2 * i + 1] = row + (((2 * g4 + 1) ^ (r & 7)) << 4);
+    }
+  };
+  // Issue the 16 reads of stage st (w rows of this wave's n half, then x rows of its m
+  // half) without waiting for them.
+  auto read_issue = [&](int st, u32x4 (&v)[16]) {
+    uint32_t aw[8], ax[8];
+    operand_addrs(st, 1, 64 * wn, aw);
+    operand_addrs(st, 0, 64 * wm, ax);
+    asm volatile(
+        "ds_read_b128 %0, %16\n\tds_read_b128 %1, %17\n\tds_read_b128 %2, %18\n\t"
+        "ds_read_b128 %3, %19\n\tds_read_b128 %4, %20\n\tds_read_b128 %5, %21\n\t"
+        "ds_read_b128 %6, %22\n\tds_read_b128 %7, %23\n\tds_read_b128 %8, %24\n\t"
+        "ds_read_b128 %9, %25\n\tds_read_b128 %10, %26\n\tds_read_b128 %11, %27\n\t"
+        "ds_read_b128 %12, %28\n\tds_read_b128 %13, %29\n\tds_read_b128 %14, %30\n\t"
+        "ds_read_b128 %15, %31"
+        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
+          "=&v"(v[6]), "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11]),
+          "=&v"(v[12]), "=&v"(v[13]), "=&v"(v[14]), "=&v"(v[15])
+        : "v"(aw[0]), "v"(aw[1]), "v"(aw[2]), "v"(aw[3]), "v"(aw[4]), "v"(aw[5]), "v"(aw[6]),
+          "v"(aw[7]), "v"(ax[0]), "v"(ax[1]), "v"(ax[2]), "v"(ax[3]), "v"(ax[4]), "v"(ax[5]),
+          "v"(ax[6]), "v"(ax[7])
+        : "memory");
+  };
+  // Wait for reads issued by read_issue; the registers pass through the asm so that no
+  // use of them is scheduled before the wait.
+  auto read_wait = [&](u32x4 (&v)[16]) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
+                   "+v"(v[6]), "+v"(v[7]), "+v"(v[8]), "+v"(v[9]), "+v"(v[10]), "+v"(v[11]),
+                   "+v"(v[12]), "+v"(v[13]), "+v"(v[14]), "+v"(v[15])
+                 :
+                 : "memory");
+  };
+  auto frag = [](const u32x4& lo, const u32x4& hi) {
+    return (i32x8){(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+  };
+
+  // Tile scales and biases of a stage slot into registers (read before the slot is
+  // refilled).
+  float smv[4];
+  f32x4 snv[4];
+  u32x2 bv[4] = {};                  // 4 fp16 biases per n sub-tile (2 per word)
+  auto read_scales = [&](int st) {
+    typedef __attribute__((address_space(3))) float lds_f32;
+    typedef __attribute__((address_space(3))) half_t lds_f16;
+    uint32_t am[4], an[4], ab[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      am[j] = (uint32_t)(uintptr_t)(lds_f32*)&scl[st][64 * wm + 16 * j + l16];
+      an[j] = (uint32_t)(uintptr_t)(lds_f32*)&scl[st][F8_BT + 64 * wn + 16 * j + 4 * g4];
+      ab[j] = (uint32_t)(uintptr_t)(lds_f16*)&bsl[st][64 * wn + 16 * j + 4 * g4];
+    }
+    asm volatile(
+        "ds_read_b32 %0, %12\n\tds_read_b32 %1, %13\n\tds_read_b32 %2, %14\n\tds_read_b32 %3, %15\n\t"
+        "ds_read_b128 %4, %16\n\tds_read_b128 %5, %17\n\tds_read_b128 %6, %18\n\t"
+        "ds_read_b128 %7, %19\n\tds_read_b64 %8, %20\n\tds_read_b64 %9, %21\n\t"
+        "ds_read_b64 %10, %22\n\tds_read_b64 %11, %23\n\ts_waitcnt lgkmcnt(0)"
+        : "=&v"(smv[0]), "=&v"(smv[1]), "=&v"(smv[2]), "=&v"(smv[3]), "=&v"(snv[0]),
+          "=&v"(snv[1]), "=&v"(snv[2]), "=&v"(snv[3]), "=&v"(bv[0]), "=&v"(bv[1]), "=&v"(bv[2]),
+          "=&v"(bv[3])
+        : "v"(am[0]), "v"(am[1]), "v"(am[2]), "v"(am[3]), "v"(an[0]), "v"(an[1]), "v"(an[2]),
+          "v"(an[3]), "v"(ab[0]), "v"(ab[1]), "v"(ab[2]), "v"(ab[3])
+        : "memory");
+  };
+
+  // Steps sidx = 0, 1, ... walk the tiles' K steps back to back; step s sits in slot
+  // s % F8_NS.  F8_NS steps are in flight ahead of the one being read: after step s's
+  // operands are in registers and step s + 1 has landed everywhere (vmcnt + barrier),
+  // step s + F8_NS is loaded into slot s % F8_NS.
+  int m0c, n0c, m0n, n0n;
+  F8TileSrc cur = tile_src(0, m0c, n0c);
+  F8TileSrc nxt = tile_src(1, m0n, n0n);
+#pragma unroll
+  for (int s = 0; s < F8_NS; ++s) issue(cur, s, s);
+  wait_vmcnt<5 * (F8_NS - 1)>();
+  barrier_only();
+  int sidx = 0;
+  for (int r = 0; r < my_tiles; ++r) {
+    f32x4 acc[4][4];   // [n sub-tile][m sub-tile]
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int ks = 0; ks < nk; ++ks, ++sidx) {
+      const int st = sidx % F8_NS;
+      // step sidx's slot, landed everywhere (vmcnt + barrier at the end of the last step)
+      u32x4 ops[16];
+      read_issue(st, ops);
+      read_wait(ops);
+      if (ks == nk - 1) read_scales(st);
+      i32x8 wf[4], xf[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        wf[i] = frag(ops[2 * i], ops[2 * i + 1]);
+        xf[i] = frag(ops[8 + 2 * i], ops[8 + 2 * i + 1]);
+      }
+      // step sidx + 1 has landed for this thread, then for everyone; every wave has also
+      // read step sidx's slot, which is refilled with step sidx + F8_NS
+      wait_vmcnt<5 * (F8_NS - 2)>();
+      barrier_only();
+      {
+        const int iks = ks + F8_NS;
+        if (iks < nk) issue(cur, iks, st);
+        else issue(nxt, iks - nk, st);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf[i], xf[j], acc[i][j], 0, 0,
+                                                                        0, 127, 0, 127);
+    }
+    // Epilogue: lane holds n = n0 + 64wn + 16i + 4g4 + q of m = m0 + 64wm + 16j + l16.
+    const int m0 = m0c, n0 = n0c;
+    const uint32_t bias_mask = has_bias ? 0xffffffffu : 0u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int m = m0 + 64 * wm + 16 * j + l16;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int n = n0 + 64 * wn + 16 * i + 4 * g4;
+        uint32_t bits[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t b = f32_to_bf16_bits((acc[i][j][q] * smv[j]) * snv[i][q]);
+          // fp16 output: the bf16 value rounded to fp16, plus the bias (an fp16 add)
+          const half_t hb = (half_t)__builtin_bit_cast(float, b << 16);
+          const uint32_t bw = bv[i][q >> 1] & bias_mask;
+          const half_t bb = __builtin_bit_cast(half_t, (uint16_t)((q & 1) ? (bw >> 16) : (bw & 0xffffu)));
+          const half_t h = has_bias ? (half_t)((float)hb + (float)bb) : hb;
+          bits[q] = a.out_bf16 ? b : (uint32_t)__builtin_bit_cast(uint16_t, h);
+        }
+        if (m < a.M) {
+          uint2 pk;
+          pk.x = bits[0] | (bits[1] << 16);
+          pk.y = bits[2] | (bits[3] << 16);
+          *(uint2*)((uint16_t*)a.out + (int64_t)m * a.ldo + n) = pk;
+        }
+      }
+    }
+    // the next tile becomes current; its successor's sources are computed now
+    cur = nxt;
+    m0c = m0n;
+    n0c = n0n;
+    nxt = tile_src(r + 2, m0n, n0n);
+  }
+  wait_vmcnt<0>();                     // drain the clamped tail loads before exit
+}
+
+static int num_cus() {
+  static int n = 0;
+  if (n <= 0) {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+      v = 256;
+    n = v;
+  }
+  return n;
+}
+
 // Row-wise e4m3 quantisation: s[r] = amax_k |x[r, k]| / 448 (clamped below at clamp_min
 // when clamp_min > 0), q[r, k] = e4m3(x[r, k] / s[r]).  One workgroup per row.
 __global__ __launch_bounds__(256) void fp8_quant_rows_kernel(const half_t* __restrict__ x, int ldx,
@@ -205,6 +483,16 @@ extern "C" int omni_fp8_quant_rows(const void* x, int ldx, void* xq, float* scal
   return OMNI_OK;
 }
 
+// Kernel choice (the pipelined kernel unless OMNI_FP8_GEMM=simple is set at first use).
+static bool fp8_pipe_enabled() {
+  static int v = -1;
+  if (v < 0) {
+    const char* e = getenv("OMNI_FP8_GEMM");
+    v = (e && e[0] == 's') ? 0 : 1;
+  }
+  return v == 1;
+}
+
 extern "C" int omni_fp8_gemm(const void* xq, const float* sa, const void* wq, const float* sw,
                              const void* bias, void* out, int ldo, int M, int N, int K,
                              int out_bf16, void* stream) {
@@ -227,7 +515,12 @@ extern "C" int omni_fp8_gemm(const void* xq, const float* sa, const void* wq, co
   a.N = N;
   a.K = K;
   a.out_bf16 = out_bf16;
-  hipLaunchKernelGGL(fp8_gemm_kernel, dim3((unsigned)tiles), dim3(256), 0, (hipStream_t)stream, a);
+  if (fp8_pipe_enabled() && K / F8_BK >= F8_NS) {
+    const int grid = (int)(tiles < num_cus() ? tiles : num_cus());
+    hipLaunchKernelGGL(fp8_gemm_pipe_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, a);
+  } else {
+    hipLaunchKernelGGL(fp8_gemm_kernel, dim3((unsigned)tiles), dim3(256), 0, (hipStream_t)stream, a);
+  }
   OMNI_CHECK_LAUNCH();
   return OMNI_OK;
 }

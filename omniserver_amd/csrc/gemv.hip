@@ -558,9 +558,11 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(GemvArgs a) {
   const int q16 = lane >> 4, c16 = lane & 15;
   const int NT = a.N >> 4;
   const int tiles_n = (a.N + GT_BN - 1) / GT_BN;
-  // XCD-aware order: consecutive logical tiles share an x row block and sit on one XCD
-  const int blk = xcd_logical_block(blockIdx.x, gridDim.x);
-  const int tn = blk % tiles_n, tm = blk / tiles_n;
+  const int tiles_m = (a.M + GT_BM - 1) / GT_BM;
+  // XCD-aware, grouped order: the tiles one XCD holds at a time form a 4 x 8 block, so
+  // both operands are shared in its L2
+  int tm, tn;
+  grouped_tile(xcd_logical_block(blockIdx.x, gridDim.x), tiles_m, tiles_n, 4, tm, tn);
   const int m0 = tm * GT_BM;
   const int nt0 = tn * (GT_BN / 16) + wn * 4;   // this wave's first column tile
   const int KG = a.K >> 7;

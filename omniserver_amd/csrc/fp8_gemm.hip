@@ -20,6 +20,8 @@
 // applied in the epilogue.
 #include "common.h"
 
+#include <string.h>
+
 #define F8_BT 128          // tile rows (m) and columns (n) per workgroup
 #define F8_BK 128          // K per step (one MFMA)
 #define F8_STRIDE 144      // LDS bytes per staged row
@@ -167,18 +169,17 @@ __global__ __launch_bounds__(256, 2) void fp8_gemm_kernel(Fp8GemmArgs a) {
 // so the next tile's first operand tiles are in flight while the current one finishes
 // and writes its outputs.
 // Operand tiles go global -> LDS directly (global_load_lds_dwordx4: lane i of a load
-// writes bytes 16 i .. 16 i + 15 past the instruction's LDS base), F8_NS stages deep: the
-// loads for step s + F8_NS - 1 are in flight while step s is multiplied.  LDS rows are
+// writes bytes 16 i .. 16 i + 15 past the instruction's LDS base), NS stages deep.
+// WM waves along m, two along n, each wave owning a 64 x 64 block of the 64 WM x 128 tile.  LDS rows are
 // 128 bytes (one K step of one row); 16-byte chunk c of row r is stored in slot
 // c ^ (r & 7), so the 16 rows an operand read touches spread over the banks.  A stage is
-// waited for with vmcnt (each thread's own loads: every stage issues 5 per thread, the
-// operands and a share of the tile's row / column scales, and wave 0 a sixth with the
-// biases, so waiting for all but the 5 (F8_NS - 3) newest stages' loads covers a stage)
-// plus a barrier (everyone's).  A step's operands are read into registers before that
+// waited for with vmcnt (each thread's own loads: every stage issues at least OPS per
+// thread, the operands and, on most waves, a share of the tile's row / column scales or
+// the biases, so waiting for all but OPS loads per younger stage covers a stage) plus a
+// barrier (everyone's).  A step's operands are read into registers before that
 // barrier, so its slot is refilled right after it, while the step's MFMAs run.
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
-#define F8_NS 4
 #define F8_GM 4                        // tile rows per group of the tile order (grouped_tile)
 #define F8_ROWB 128                    // LDS bytes per staged row
 #define F8_TILEB (F8_BT * F8_ROWB)     // one operand tile of one stage
@@ -206,11 +207,20 @@ struct F8TileSrc {
   const void* b;
 };
 
-__global__ __launch_bounds__(256, 1) void fp8_gemm_pipe_kernel(Fp8GemmArgs a) {
+template <int WM, int NS>
+__global__ __launch_bounds__(128 * WM, 1) void fp8_gemm_pipe_kernel(Fp8GemmArgs a) {
 #pragma clang fp contract(off)
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[F8_NS][2][F8_TILEB];   // [stage][x|w]
-  __shared__ __attribute__((aligned(16))) float scl[F8_NS][2 * F8_BT];         // [stage][sa|sw]
-  __shared__ __attribute__((aligned(16))) half_t bsl[F8_NS][512];              // [stage][bias]
+  constexpr int BM = 64 * WM;                 // tile rows (tokens); 128 columns (channels)
+  constexpr int NWV = 2 * WM;                 // waves
+  constexpr int XLD = 4;                      // x loads per wave and stage
+  constexpr int WLD = 8 / WM;                 // w loads per wave and stage
+  constexpr int SCW = WM + 2;                 // waves loading scales (BM + 128 of them)
+  // fewest loads any thread issues per stage (the vmcnt unit of one stage)
+  constexpr int OPS = XLD + WLD + (SCW >= NWV ? 1 : 0);
+  __shared__ __attribute__((aligned(1024))) uint8_t xl[NS][BM * F8_ROWB];      // [stage] x tile
+  __shared__ __attribute__((aligned(1024))) uint8_t wl[NS][F8_BT * F8_ROWB];   // [stage] w tile
+  __shared__ __attribute__((aligned(16))) float scl[NS][BM + F8_BT];           // [stage][sa|sw]
+  __shared__ __attribute__((aligned(16))) half_t bsl[NS][512];                 // [stage][bias]
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -220,48 +230,50 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_pipe_kernel(Fp8GemmArgs a) {
   const int g4 = lane >> 4;
 
   const int tiles_n = a.N / F8_BT;
-  const int tiles_m = (a.M + F8_BT - 1) / F8_BT;
+  const int tiles_m = (a.M + BM - 1) / BM;
   const int tiles = tiles_m * tiles_n;
   const int G = gridDim.x;
   const int slot = xcd_logical_block(blockIdx.x, G);
   const int my_tiles = (tiles - slot + G - 1) / G;          // grid <= tiles: >= 1
-  const int nk = a.K / F8_BK;                               // >= F8_NS - 1 (host check)
+  const int nk = a.K / F8_BK;                               // >= NS (host check)
 
-  // Load u (0..3) of this wave fills tile rows 32u + 8 wave .. +7: lane i -> row
-  // 32u + 8 wave + i/8, LDS slot i%8, which holds chunk (i%8) ^ (row & 7).  A fifth,
-  // 4-byte-per-lane load brings 64 of the tile's 256 scales: waves 0, 1 the token scales
-  // sa[m0 + 64 wave + lane], waves 2, 3 the channel scales sw[n0 + 64 (wave - 2) + lane].
-  const int lrow = 8 * wave + (lane >> 3);          // + 32u
-  const int lchunk = (lane & 7) ^ (lrow & 7);       // (32u + lrow) & 7 == lrow & 7
+  // Load u of this wave fills tile rows 8 NWV u + 8 wave .. +7: lane i -> row
+  // 8 NWV u + 8 wave + i/8, LDS slot i%8, which holds chunk (i%8) ^ (row & 7).  One more
+  // 4-byte-per-lane load brings 64 of the tile's scales: waves 0 .. WM-1 the token scales
+  // sa[m0 + 64 wave + lane], waves WM, WM+1 the channel scales sw[n0 + 64 (wave - WM) + lane].
+  const int lrow = 8 * wave + (lane >> 3);          // + 8 NWV u
+  const int lchunk = (lane & 7) ^ (lrow & 7);       // (8 NWV u + lrow) & 7 == lrow & 7
   typedef __attribute__((address_space(3))) void lds_void;
   typedef __attribute__((address_space(3))) uint8_t lds_u8;
   const bool has_bias = a.bias != nullptr;
   auto tile_src = [&](int r, int& m0, int& n0) {     // past the last tile: the last one again
     int tm, tn;
     grouped_tile(min(r, my_tiles - 1) * G + slot, tiles_m, tiles_n, F8_GM, tm, tn);
-    m0 = tm * F8_BT;
+    m0 = tm * BM;
     n0 = tn * F8_BT;
     F8TileSrc t;
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-      t.x[u] = a.xq + (int64_t)min(m0 + 32 * u + lrow, a.M - 1) * a.K + lchunk * 16;
+    for (int u = 0; u < XLD; ++u)
+      t.x[u] = a.xq + (int64_t)min(m0 + 8 * NWV * u + lrow, a.M - 1) * a.K + lchunk * 16;
     t.w = a.wq + (int64_t)(n0 + lrow) * a.K + lchunk * 16;
-    t.s = wave < 2 ? (const void*)(a.sa + min(m0 + 64 * wave + lane, a.M - 1))
-                   : (const void*)(a.sw + n0 + 64 * (wave - 2) + lane);
+    t.s = wave < WM ? (const void*)(a.sa + min(m0 + 64 * wave + lane, a.M - 1))
+                    : (const void*)(a.sw + n0 + 64 * min(wave - WM, 1) + lane);
     t.b = has_bias ? (const void*)(a.bias + n0 + 8 * min(lane, 15)) : t.s;
     return t;
   };
-  const int64_t wstep = (int64_t)32 * a.K;          // bytes between w row groups
+  const int64_t wstep = (int64_t)8 * NWV * a.K;    // bytes between w row groups
   auto issue = [&](const F8TileSrc& t, int ks, int st) {
     const int k0 = ks * F8_BK;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < XLD; ++u)
       __builtin_amdgcn_global_load_lds((const void*)(t.x[u] + k0),
-                                       (lds_void*)((lds_u8*)&lds[st][0][(32 * u + 8 * wave) * F8_ROWB]), 16, 0, 0);
+                                       (lds_void*)((lds_u8*)&xl[st][(8 * NWV * u + 8 * wave) * F8_ROWB]), 16, 0, 0);
+#pragma unroll
+    for (int u = 0; u < WLD; ++u)
       __builtin_amdgcn_global_load_lds((const void*)(t.w + u * wstep + k0),
-                                       (lds_void*)((lds_u8*)&lds[st][1][(32 * u + 8 * wave) * F8_ROWB]), 16, 0, 0);
-    }
-    __builtin_amdgcn_global_load_lds(t.s, (lds_void*)((lds_u8*)&scl[st][64 * wave]), 4, 0, 0);
+                                       (lds_void*)((lds_u8*)&wl[st][(8 * NWV * u + 8 * wave) * F8_ROWB]), 16, 0, 0);
+    if (wave < SCW)
+      __builtin_amdgcn_global_load_lds(t.s, (lds_void*)((lds_u8*)&scl[st][64 * wave]), 4, 0, 0);
     if (wave == 0 && has_bias)        // the tile's 128 fp16 biases (lanes 0-15; a sixth load,
       __builtin_amdgcn_global_load_lds(t.b, (lds_void*)((lds_u8*)&bsl[st][0]), 16, 0, 0);   // wave 0 only)
   };
@@ -274,7 +286,7 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_pipe_kernel(Fp8GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = base + 16 * i + l16;
-      const uint32_t row = (uint32_t)(uintptr_t)(lds_u8*)&lds[st][o][r * F8_ROWB];
+      const uint32_t row = (uint32_t)(uintptr_t)(lds_u8*)(o ? &wl[st][r * F8_ROWB] : &xl[st][r * F8_ROWB]);
       ad[2 * i] = row + (((2 * g4) ^ (r & 7)) << 4);
       ad[2 * i + 1] = row + (((2 * g4 + 1) ^ (r & 7)) << 4);
     }
@@ -326,7 +338,7 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_pipe_kernel(Fp8GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       am[j] = (uint32_t)(uintptr_t)(lds_f32*)&scl[st][64 * wm + 16 * j + l16];
-      an[j] = (uint32_t)(uintptr_t)(lds_f32*)&scl[st][F8_BT + 64 * wn + 16 * j + 4 * g4];
+      an[j] = (uint32_t)(uintptr_t)(lds_f32*)&scl[st][BM + 64 * wn + 16 * j + 4 * g4];
       ab[j] = (uint32_t)(uintptr_t)(lds_f16*)&bsl[st][64 * wn + 16 * j + 4 * g4];
     }
     asm volatile(
@@ -343,15 +355,15 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_pipe_kernel(Fp8GemmArgs a) {
   };
 
   // Steps sidx = 0, 1, ... walk the tiles' K steps back to back; step s sits in slot
-  // s % F8_NS.  F8_NS steps are in flight ahead of the one being read: after step s's
-  // operands are in registers and step s + 1 has landed everywhere (vmcnt + barrier),
-  // step s + F8_NS is loaded into slot s % F8_NS.
+  // s % NS.  NS steps are in flight ahead of the one being read: after step s's operands
+  // are in registers and step s + 1 has landed everywhere (vmcnt + barrier), step s + NS
+  // is loaded into slot s % NS.
   int m0c, n0c, m0n, n0n;
   F8TileSrc cur = tile_src(0, m0c, n0c);
   F8TileSrc nxt = tile_src(1, m0n, n0n);
 #pragma unroll
-  for (int s = 0; s < F8_NS; ++s) issue(cur, s, s);
-  wait_vmcnt<5 * (F8_NS - 1)>();
+  for (int s = 0; s < NS; ++s) issue(cur, s, s);
+  wait_vmcnt<OPS * (NS - 1)>();
   barrier_only();
   int sidx = 0;
   for (int r = 0; r < my_tiles; ++r) {
@@ -361,7 +373,7 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_pipe_kernel(Fp8GemmArgs a) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
     for (int ks = 0; ks < nk; ++ks, ++sidx) {
-      const int st = sidx % F8_NS;
+      const int st = sidx % NS;
       // step sidx's slot, landed everywhere (vmcnt + barrier at the end of the last step)
       u32x4 ops[16];
       read_issue(st, ops);
@@ -374,11 +386,11 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_pipe_kernel(Fp8GemmArgs a) {
         xf[i] = frag(ops[8 + 2 * i], ops[8 + 2 * i + 1]);
       }
       // step sidx + 1 has landed for this thread, then for everyone; every wave has also
-      // read step sidx's slot, which is refilled with step sidx + F8_NS
-      wait_vmcnt<5 * (F8_NS - 2)>();
+      // read step sidx's slot, which is refilled with step sidx + NS
+      wait_vmcnt<OPS * (NS - 2)>();
       barrier_only();
       {
-        const int iks = ks + F8_NS;
+        const int iks = ks + NS;
         if (iks < nk) issue(cur, iks, st);
         else issue(nxt, iks - nk, st);
       }
@@ -483,14 +495,17 @@ extern "C" int omni_fp8_quant_rows(const void* x, int ldx, void* xq, float* scal
   return OMNI_OK;
 }
 
-// Kernel choice (the pipelined kernel unless OMNI_FP8_GEMM=simple is set at first use).
-static bool fp8_pipe_enabled() {
+// Kernel choice, read once from OMNI_FP8_GEMM: "simple" (0), "pipe4" (1: 4 waves, 128-row
+// tiles), "pipe8" (2: 8 waves, 256-row tiles; the default).
+static int fp8_variant() {
   static int v = -1;
   if (v < 0) {
     const char* e = getenv("OMNI_FP8_GEMM");
-    v = (e && e[0] == 's') ? 0 : 1;
+    v = 2;
+    if (e && e[0] == 's') v = 0;
+    else if (e && strcmp(e, "pipe4") == 0) v = 1;
   }
-  return v == 1;
+  return v;
 }
 
 extern "C" int omni_fp8_gemm(const void* xq, const float* sa, const void* wq, const float* sw,
@@ -515,9 +530,18 @@ extern "C" int omni_fp8_gemm(const void* xq, const float* sa, const void* wq, co
   a.N = N;
   a.K = K;
   a.out_bf16 = out_bf16;
-  if (fp8_pipe_enabled() && K / F8_BK >= F8_NS) {
-    const int grid = (int)(tiles < num_cus() ? tiles : num_cus());
-    hipLaunchKernelGGL(fp8_gemm_pipe_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, a);
+  const int variant = fp8_variant();
+  if (variant > 0 && K / F8_BK >= 4) {
+    if (variant == 2) {          // 8 waves, 256 x 128 tiles, 3 stages
+      const int64_t t8 = (int64_t)ceil_div(M, 256) * (N / F8_BT);
+      const int grid = (int)(t8 < num_cus() ? t8 : num_cus());
+      hipLaunchKernelGGL((fp8_gemm_pipe_kernel<4, 3>), dim3((unsigned)grid), dim3(512), 0,
+                         (hipStream_t)stream, a);
+    } else {                     // 4 waves, 128 x 128 tiles, 4 stages
+      const int grid = (int)(tiles < num_cus() ? tiles : num_cus());
+      hipLaunchKernelGGL((fp8_gemm_pipe_kernel<2, 4>), dim3((unsigned)grid), dim3(256), 0,
+                         (hipStream_t)stream, a);
+    }
   } else {
     hipLaunchKernelGGL(fp8_gemm_kernel, dim3((unsigned)tiles), dim3(256), 0, (hipStream_t)stream, a);
   }

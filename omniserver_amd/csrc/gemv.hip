@@ -811,9 +811,161 @@ extern "C" int omni_f16_gemm(const void* x, int ldx, const void* weight_packed, 
 // lm_head + greedy argmax: the GEMM writes one (max, index) candidate per
 // workgroup and row; omni_argmax_finalize reduces them.
 // ---------------------------------------------------------------------------
+// ---------------------------------------------------------------------------
+// lm_head + greedy-argmax candidates, persistent: one workgroup (8 waves) per CU stages
+// x [M <= 64, K] in LDS once, then its waves stream their share of the packed fp16 table
+// (column tiles t0 + wave, t0 + wave + 8, ... of the workgroup's contiguous tile range)
+// as one run of 4-group (512-k) batches, two batches in flight, so the stream does not
+// pause between tiles.  Per tile the accumulation order is the skinny kernel's (groups and
+// 32-k steps ascending); the logit is fp16(acc), compared as float, lowest index on ties.
+// ---------------------------------------------------------------------------
+static int num_cus_gemv() {
+  static int n = 0;
+  if (n <= 0) {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+      v = 256;
+    n = v;
+  }
+  return n;
+}
+
+template <int MB>
+__global__ __launch_bounds__(512, 1) void lmhead_kernel(GemvArgs a) {
+#pragma clang fp contract(off)
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  half_t* xs = (half_t*)smem;                  // [MB * 16][K + 8]
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int q16 = lane >> 4, c16 = lane & 15;
+  const int K = a.K;
+  const int xstride = K + 8;
+  // 1. x rows (zero past M) into LDS
+  {
+    const int cpr = K >> 3;
+    for (int i = threadIdx.x; i < MB * 16 * cpr; i += 512) {
+      const int r = i / cpr, c = i - r * cpr;
+      half8_t v = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
+      if (r < a.M) v = *(const half8_t*)(a.x + (int64_t)r * a.ldx + c * 8);
+      *(half8_t*)(xs + r * xstride + c * 8) = v;
+    }
+  }
+  __syncthreads();
+
+  const int NT = a.N >> 4;
+  const int KS32 = K >> 5;                     // 32-k steps per tile
+  const int BPT = K >> 9;                      // 512-k batches per tile (K % 512 == 0)
+  const int G = gridDim.x;
+  const int blk = xcd_logical_block(blockIdx.x, G);
+  const int t0 = (int)((int64_t)blk * NT / G), t1 = (int)((int64_t)(blk + 1) * NT / G);
+  const int ntw = t1 - t0 > wave ? (t1 - t0 - wave + 7) / 8 : 0;   // this wave's tiles
+  const int nb = ntw * BPT;
+  const half8_t* wp = (const half8_t*)a.w + lane;
+  auto load_batch = [&](half8_t (&buf)[16], int b) {
+    const int bc = min(b, max(nb - 1, 0));        // past the end: re-read the last batch
+    const int tile = min(t0 + wave + 8 * (bc / BPT), NT - 1);
+    const int s0 = (bc % BPT) * 16;               // first 32-k step of the batch
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+      buf[u] = __builtin_nontemporal_load(wp + ((int64_t)tile * KS32 + s0 + u) * 64);
+  };
+
+  float bv[MB][4];
+  int bi[MB][4];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      bv[mb][i] = -INFINITY;
+      bi[mb][i] = 0x7fffffff;
+    }
+  f32x4 acc[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) acc[mb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  auto use_batch = [&](const half8_t (&buf)[16], int b) {
+    const int kb = (b % BPT) * 512;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const half8_t af = *(const half8_t*)(xs + (16 * mb + c16) * xstride + kb + 32 * u + 8 * q16);
+        acc[mb] = mfma16x16x32(af, buf[u], acc[mb]);
+      }
+    }
+    if (b % BPT == BPT - 1) {                   // tile done: fp16 logits, running argmax
+      const int n = (t0 + wave + 8 * (b / BPT)) * 16 + c16;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = 16 * mb + 4 * q16 + i;
+          const half_t h = (half_t)acc[mb][i];
+          if (a.out && m < a.M) a.out[(int64_t)m * a.ldo + n] = h;
+          const float v = (float)h;
+          if (v > bv[mb][i]) {                  // columns ascend per lane: first max wins
+            bv[mb][i] = v;
+            bi[mb][i] = n;
+          }
+        }
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) acc[mb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    }
+  };
+
+  // 2. the stream: batches b (A) and b + 1 (B) in flight
+  half8_t ba[16], bb[16];
+  load_batch(ba, 0);
+  load_batch(bb, 1);
+  for (int b = 0; b < nb; b += 2) {
+    use_batch(ba, b);
+    load_batch(ba, b + 2);
+    if (b + 1 < nb) use_batch(bb, b + 1);
+    load_batch(bb, b + 3);
+  }
+
+  // 3. reduce: over the 16 columns of a lane group, then over the waves (LDS)
+  __shared__ float red_v[8][64];
+  __shared__ int red_i[8][64];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v = bv[mb][i];
+      int ix = bi[mb][i];
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) {
+        const float ov = __shfl_xor(v, o, 64);
+        const int oi = __shfl_xor(ix, o, 64);
+        if (ov > v || (ov == v && oi < ix)) { v = ov; ix = oi; }
+      }
+      if (c16 == 0) {
+        red_v[wave][16 * mb + 4 * q16 + i] = v;
+        red_i[wave][16 * mb + 4 * q16 + i] = ix;
+      }
+    }
+  __syncthreads();
+  if ((int)threadIdx.x < a.M) {
+    const int m = threadIdx.x;
+    float v = red_v[0][m];
+    int ix = red_i[0][m];
+#pragma unroll
+    for (int w = 1; w < 8; ++w) {
+      const float ov = red_v[w][m];
+      const int oi = red_i[w][m];
+      if (ov > v || (ov == v && oi < ix)) { v = ov; ix = oi; }
+    }
+    a.cand_val[(int64_t)blockIdx.x * a.M + m] = v;
+    a.cand_idx[(int64_t)blockIdx.x * a.M + m] = ix;
+  }
+}
+
+// Candidate slots per row written by omni_lmhead_candidates (= its grid size).
 extern "C" int omni_lmhead_argmax_grid(int N) {
   const int NT = N >> 4;
-  return (NT + 15) / 16;
+  const int cus = num_cus_gemv();
+  return NT < cus ? NT : cus;
 }
 
 extern "C" int omni_lmhead_candidates(const void* x, int ldx, const void* weight_packed, int M,
@@ -837,7 +989,32 @@ extern "C" int omni_lmhead_candidates(const void* x, int ldx, const void* weight
   a.KC = K;
   a.cand_val = cand_val;
   a.cand_idx = cand_idx;
-  return dispatch_preset<W_FP16, EPI_ARGMAX>(a, 0, (hipStream_t)stream);
+  if (K & 511) return OMNI_EUNSUPPORTED;          // 512-k batches
+  const size_t lds = (size_t)((M + 15) / 16) * 16 * (K + 8) * sizeof(half_t);
+  if (lds > max_dynamic_lds()) return OMNI_EUNSUPPORTED;
+  const int grid = omni_lmhead_argmax_grid(N);
+  hipStream_t st = (hipStream_t)stream;
+  switch ((M + 15) / 16) {
+#define OMNI_LMHEAD_CASE(MBV)                                                                   \
+    case MBV: {                                                                                  \
+      static bool attr = false;                                                                  \
+      if (!attr) {                                                                               \
+        (void)hipFuncSetAttribute((const void*)lmhead_kernel<MBV>,                               \
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)max_dynamic_lds()); \
+        attr = true;                                                                             \
+      }                                                                                          \
+      hipLaunchKernelGGL(lmhead_kernel<MBV>, dim3(grid), dim3(512), lds, st, a);                 \
+      break;                                                                                     \
+    }
+    OMNI_LMHEAD_CASE(1)
+    OMNI_LMHEAD_CASE(2)
+    OMNI_LMHEAD_CASE(3)
+    OMNI_LMHEAD_CASE(4)
+#undef OMNI_LMHEAD_CASE
+    default: return OMNI_EUNSUPPORTED;
+  }
+  OMNI_CHECK_LAUNCH();
+  return OMNI_OK;
 }
 
 // ids_out[m] = index of the max candidate (lowest index on ties).  Decode-step

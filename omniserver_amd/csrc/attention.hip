@@ -163,11 +163,15 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
   const int wg_b0 = (int)((int64_t)sp * NWA * nblk / nw);
   const int wg_b1 = (int)((int64_t)(sp + 1) * NWA * nblk / nw);
 
+  // cos (threads 0-7) / sin (8-15) row at pos.  Every thread issues the load (threads
+  // past 15 re-read a chunk and drop it): a load behind a thread-index branch leaves the
+  // compiler unsure whether it is outstanding, and it then waits for it (vmcnt(0)) before
+  // using any load issued earlier.
   half8_t csv = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
-  if (fused && threadIdx.x < 16) {         // cos (threads 0-7) / sin (8-15) row at pos
+  if (fused) {
     int64_t pos = slot_ok ? kv_raw + (a.rope_delta ? delta_raw : 0) : 0;
     pos = clamp64(pos, 0, a.max_pos - 1);
-    const half_t* tab = threadIdx.x < 8 ? a.cos_tab : a.sin_tab;
+    const half_t* tab = (threadIdx.x & 15) < 8 ? a.cos_tab : a.sin_tab;
     csv = *(const half8_t*)(tab + pos * (ATT_HD / 2) + (threadIdx.x & 7) * 8);
   }
 
@@ -236,8 +240,11 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
         raw[2 * i + 1] = h1;
       }
     }
+    // The K/V stream goes out as soon as the partials are consumed; the cos/sin row (a
+    // second round trip: its address needs the context length) was requested before it,
+    // so storing it below waits for that row only, not for the stream.
+    issue_first_blocks();
     if (threadIdx.x < 16) *(half8_t*)(&cs_lds[threadIdx.x >> 3][(threadIdx.x & 7) * 8]) = csv;
-    issue_first_blocks();   // every prologue load has been consumed above
     lds_barrier();
     // 5. M-RoPE (decode: one position on all three axes) in fp16 ops, one rounding
     //    each and no contraction: y1 = x1*c + (-x2)*s, y2 = x2*c + x1*s.

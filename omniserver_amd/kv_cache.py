@@ -9,6 +9,10 @@ Mirrors omniserve/cache/kv_prealloc.py:
   attend over keys [0, pos] (inclusive); ``lengths`` advance after the last layer.
 * ``_PackedPrefillWriter.flash_prefill`` (:181-203): each packed segment's K/V goes to
   ``pool[slot, :L]``; causal attention inside each segment; ``lengths[slot] = L``.
+* ``_ChunkedPrefillWriter`` / ``_MixedWriter`` (:118-174): the append form of the same
+  thing - segment s writes its ``new_len`` tokens at ``pool[slot, start:start+new_len]``
+  and its query i attends to keys ``[0, start+i]`` (cached prefix + the segment, causal);
+  ``lengths[slot] = start + new_len``.  A decode token is a segment of one.
 
 Attention and the K/V writes run on the HIP kernels (omni_decode_attention,
 omni_mrope_kv_write, omni_prefill_attention); slot bookkeeping stays torch copies.
@@ -101,6 +105,17 @@ class PreallocatedKVCache:
 
     def packed_prefill_cache(self, slots: Sequence[int], seg_lengths: Sequence[int]):
         return PackedPrefillWriter(self, slots, seg_lengths)
+
+    def chunked_prefill_cache(self, slot: int, start: int) -> "ChunkedPrefillWriter":
+        """One prefill chunk appended at pool[slot, start:start+L] (kv_prealloc.py:104-108);
+        L is the number of tokens the forward brings."""
+        return ChunkedPrefillWriter(self, slot, start)
+
+    def mixed_cache(self, slots: Sequence[int], new_lens: Sequence[int],
+                    starts: Sequence[int]) -> "PackedPrefillWriter":
+        """Decode tokens and a prefill chunk in one forward (kv_prealloc.py:110-116): segment
+        s appends new_lens[s] tokens to slot slots[s] at starts[s]."""
+        return PackedPrefillWriter(self, slots, new_lens, starts)
 
     # ---- kernel calls --------------------------------------------------------------
     def attend(self, q: torch.Tensor, q_stride: int, layer_idx: int, kv_len: torch.Tensor,
@@ -199,26 +214,51 @@ class CacheView:
 
 class PackedPrefillWriter:
     """Packed prefill adapter (kv_prealloc.py:177-215): segments of a packed batch go to
-    their own slots; attention is causal within each segment."""
+    their own slots; attention is causal within each segment.  With ``starts`` it is the
+    append (mixed batching) adapter of kv_prealloc.py:118-146: segment s writes its tokens
+    at pool[slot, start:start+L] and attends to the slot's cached prefix as well."""
 
     def __init__(self, pool: PreallocatedKVCache, slots: Sequence[int],
-                 seg_lengths: Sequence[int]):
+                 seg_lengths: Sequence[int] | None, starts: Sequence[int] | None = None):
         self.pool = pool
-        self.slots = list(slots)
-        self.seg = list(seg_lengths)
+        self.slots = [int(s) for s in slots]
+        self.starts = [0] * len(self.slots) if starts is None else [int(s) for s in starts]
+        if len(self.starts) != len(self.slots):
+            raise ValueError("one start per segment")
+        self.seg = None
+        if seg_lengths is not None:
+            self._build([int(L) for L in seg_lengths])
+
+    def _build(self, seg: List[int]) -> None:
+        pool = self.pool
+        if len(seg) != len(self.slots):
+            raise ValueError("one length per segment")
+        for slot, st, L in zip(self.slots, self.starts, seg):
+            if not 0 <= slot < pool.max_batch:
+                raise ValueError(f"slot {slot} outside the pool's {pool.max_batch} rows")
+            if L < 1 or st < 0 or st + L > pool.max_len:
+                raise ValueError(f"segment [{st}, {st + L}) outside [0, max_len={pool.max_len}]")
+        if len(set(self.slots)) != len(self.slots):
+            raise ValueError("a slot appears in two segments")
+        self.seg = seg
         dev = pool.device
-        T = sum(self.seg)
         slot_t, pos_t, cu = [], [], [0]
-        for s, L in zip(self.slots, self.seg):
+        for s, st, L in zip(self.slots, self.starts, seg):
             slot_t += [s] * L
-            pos_t += list(range(L))
+            pos_t += list(range(st, st + L))
             cu.append(cu[-1] + L)
-        self.T = T
+        self.T = cu[-1]
         self.token_slot = torch.tensor(slot_t, device=dev, dtype=torch.int64)
-        self.token_pos = torch.tensor(pos_t, device=dev, dtype=torch.int64)
-        self.kv_len = self.token_pos + 1          # causal: token i sees keys [0, i]
+        self.token_pos = torch.tensor(pos_t, device=dev, dtype=torch.int64)   # write positions
+        self.kv_len = self.token_pos + 1          # causal: token at position p sees keys [0, p]
         self.cu_seqlens = torch.tensor(cu, device=dev, dtype=torch.int32)
-        self.max_seg = max(self.seg) if self.seg else 0
+        self.max_seg = max(seg) if seg else 0
+
+    def bind(self, T: int) -> None:
+        """Number of tokens the forward brings (fixed at construction here)."""
+        if self.seg is None or self.T != T:
+            raise ValueError(f"the forward brings {T} tokens, the adapter was built for "
+                             f"{None if self.seg is None else self.T}")
 
     def rope_and_write(self, qkv: torch.Tensor, layer_idx: int, positions: torch.Tensor,
                        cos_tab, sin_tab, mrope_section) -> None:
@@ -236,18 +276,20 @@ class PackedPrefillWriter:
         return prefill_attention_pool(self, qkv, layer_idx, scale, out)
 
     def finish(self) -> None:
-        for s, L in zip(self.slots, self.seg):
-            self.pool.lengths[s] = L
+        for s, st, L in zip(self.slots, self.starts, self.seg):
+            self.pool.lengths[s] = st + L
             self.pool._active = max(self.pool._active, s + 1)
 
     def flash_prefill(self, q, k, v, layer_idx, scale):
-        """Reference protocol (kv_prealloc.py:181-203): q [T, nh, hd], k/v [T, nkv, hd]
-        (rotated).  Writes K/V to the slots, causal attention per segment."""
+        """Reference protocol (kv_prealloc.py:181-203, 121-146): q [T, nh, hd], k/v
+        [T, nkv, hd] (rotated).  Writes K/V to the slots at their starts, causal attention
+        per segment over the cached prefix + the segment; lengths on the last layer."""
         pool = self.pool
+        self.bind(q.shape[0])
         off = 0
-        for slot, L in zip(self.slots, self.seg):
-            pool.k[layer_idx][slot, :L] = k[off:off + L]
-            pool.v[layer_idx][slot, :L] = v[off:off + L]
+        for slot, st, L in zip(self.slots, self.starts, self.seg):
+            pool.k[layer_idx][slot, st:st + L] = k[off:off + L]
+            pool.v[layer_idx][slot, st:st + L] = v[off:off + L]
             off += L
         q = q.contiguous()
         out = torch.empty_like(q)
@@ -256,3 +298,17 @@ class PackedPrefillWriter:
         if layer_idx == pool.n_layers - 1:
             self.finish()
         return out
+
+
+class ChunkedPrefillWriter(PackedPrefillWriter):
+    """_ChunkedPrefillWriter (kv_prealloc.py:149-174): one chunk of a long prompt appended
+    at pool[slot, start:start+L]; its queries attend to pool[slot, 0:start+i] (the cached
+    prefix + the chunk, causal).  L is taken from the forward that uses it."""
+
+    def __init__(self, pool: PreallocatedKVCache, slot: int, start: int):
+        super().__init__(pool, [slot], None, [start])
+
+    def bind(self, T: int) -> None:
+        if self.seg is None:
+            self._build([int(T)])
+        super().bind(T)

@@ -108,12 +108,15 @@ class Qwen2LLM(nn.Module):
                 logits_indices=None):
         """inputs_embeds [B, L, H] fp16 with B*L packed tokens; position_ids [3, B, L].
 
-        ``cache`` must be a pool adapter (PackedPrefillWriter for prefill, CacheView for
-        decode); attn_mask is unused (causality / lengths come from the adapter)."""
+        ``cache`` must be a pool adapter (PackedPrefillWriter for packed / chunked / mixed
+        prefill, CacheView for decode); attn_mask is unused (causality / lengths come from
+        the adapter)."""
         cfg = self.cfg
         B, L, H = inputs_embeds.shape
         T = B * L
         x = inputs_embeds.reshape(T, H).contiguous()
+        if hasattr(cache, "bind"):              # prefill / append adapters: T tokens
+            cache.bind(T)
         decode = not hasattr(cache, "token_slot")
         pos = None if decode else position_ids.reshape(3, T).to(torch.int64).contiguous()
         residual = None

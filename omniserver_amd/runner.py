@@ -12,6 +12,12 @@ embedding gather + 28 layers + final norm + lm_head/argmax + length advance - is
 HIP-graph replay per batch size (captured lazily, static buffers kept alive).  The
 host does at most one small H2D (token ids, only when the batch composition
 changed) and one D2H (the new ids) per step.
+
+Chunked prefill and mixed batching (multimodal.py:200-284): a long text prompt is
+prefilled chunk by chunk into the reserve slot (pool row ``max_running``), each chunk
+attending to the chunks before it; ``mixed_step`` runs the running sequences' decode
+tokens and one chunk in a single forward.  After the last chunk the prompt's KV prefix
+is copied into the next decode slot.
 """
 
 from __future__ import annotations
@@ -103,6 +109,8 @@ class MultimodalRunner(ModelRunner):
         self._eager: Dict[int, dict] = {}
         self._dev_ids_for = None              # batch whose next ids already sit on device
         self._pinned_ids = torch.zeros(max_running + 1, dtype=torch.int64).pin_memory()
+        self._pinned_out = torch.zeros(max_running + 1, dtype=torch.int64).pin_memory()
+        self._out_ready = torch.cuda.Event() if torch.cuda.is_available() else None
 
     @property
     def pool(self) -> PreallocatedKVCache:
@@ -192,6 +200,95 @@ class MultimodalRunner(ModelRunner):
         self._dev_ids_for = None
         return slots
 
+    # ---- chunked prefill / mixed batching (multimodal.py:200-284) -------------------
+    def _chunk_bounds(self, seq: Sequence):
+        if not seq.prompt_token_ids:
+            self.tokenize(seq)
+        P = len(seq.prompt_token_ids)
+        start, L = seq.num_prefilled, seq.prefill_chunk
+        if P == 0 or P >= self._pool.max_len:
+            raise ValueError(f"prompt length {P} outside [1, max_len={self._pool.max_len})")
+        if L < 1 or start < 0 or start + L > P:
+            raise ValueError(f"chunk [{start}, {start + L}) outside the {P}-token prompt")
+        if start == 0:
+            # positions of the whole prompt once, sliced by later chunks (:212-216)
+            if seq.request.images:
+                raise AssertionError("chunked prefill supports text-only prompts (no images)")
+            pos_full, delta = self.adapter.prefill_positions(seq.prompt_token_ids, None)
+            seq.kv_handle = {"slot": self._reserve_slot, "rope_delta": int(delta),
+                             "pos_full": pos_full}
+        elif not seq.kv_handle or "pos_full" not in seq.kv_handle:
+            raise ValueError("a later chunk of a prompt whose first chunk was not run")
+        return start, L, start + L, P
+
+    def _seat_prefilled(self, seq: Sequence, length: int, logits_row: torch.Tensor) -> None:
+        """Last chunk done: move the reserve slot's KV into the decode region (valid prefix
+        only) and emit the first token (:229-235)."""
+        slot = len(self._slot_seq)
+        if slot >= self.max_running:
+            raise RuntimeError(f"KV pool full: {slot} running")
+        delta = seq.kv_handle["rope_delta"]
+        self._pool.copy_slot_kv(self._reserve_slot, slot, length)
+        self._rope_delta[slot] = delta
+        seq.kv_handle = {"slot": slot, "rope_delta": delta}
+        self._slot_seq.append(seq)
+        self._kv_len.append(length)
+        seq.append_token(self._sample_rows(logits_row, [seq])[0])
+        seq.maybe_finish()
+        self._dev_ids_for = None
+
+    def chunk_prefill(self, seq: Sequence) -> None:
+        """One chunk [num_prefilled, num_prefilled + prefill_chunk) of a long text prompt
+        (multimodal.py:200-235): appended to the reserve slot, attending to the chunks
+        before it; after the last chunk the sequence joins the decode slots and emits its
+        first token."""
+        with torch.inference_mode():
+            start, L, end, P = self._chunk_bounds(seq)
+            dev = self.device
+            ids = torch.tensor(seq.prompt_token_ids[start:end], dtype=torch.int64, device=dev)
+            emb = self.adapter.embed_tokens(ids).unsqueeze(0)                 # [1, L, H]
+            pos = seq.kv_handle["pos_full"][:, start:end].to(dev).unsqueeze(1)  # [3, 1, L]
+            cache = self._pool.chunked_prefill_cache(self._reserve_slot, start)
+            logits = self.adapter.llm(emb, pos, None, cache, logits_indices=[L - 1])[0]
+            seq.num_prefilled = end
+            if end == P:
+                self._seat_prefilled(seq, end, logits[0:1])
+
+    def mixed_step(self, chunk_seq: Sequence, decode_seqs: List[Sequence]) -> None:
+        """Mixed batching (multimodal.py:237-284): the running sequences' decode tokens and
+        one prefill chunk in a single forward - decode tokens first, the chunk after; each
+        segment appends to its own slot and attends to its own KV."""
+        with torch.inference_mode():
+            decode_seqs = sorted(decode_seqs, key=lambda s: s.kv_handle["slot"])
+            n = len(decode_seqs)
+            if [s.kv_handle["slot"] for s in decode_seqs] != list(range(n)):
+                raise AssertionError("mixed_step expects the running sequences in slots [0, n)")
+            for b in range(n):
+                if self._kv_len[b] >= self._pool.max_len:
+                    raise RuntimeError(f"sequence in slot {b} reached max_len={self._pool.max_len}")
+            start, L, end, P = self._chunk_bounds(chunk_seq)
+            dev = self.device
+            dec_len = [int(v) for v in self._kv_len[:n]]        # write positions = KV lengths
+            ids = [s.last_token_id() for s in decode_seqs] + chunk_seq.prompt_token_ids[start:end]
+            emb = self.adapter.embed_tokens(
+                torch.tensor(ids, dtype=torch.int64, device=dev)).unsqueeze(0)   # [1, n+L, H]
+            dec_pos = torch.tensor([dec_len[b] + int(s.kv_handle["rope_delta"])
+                                    for b, s in enumerate(decode_seqs)], dtype=torch.int64)
+            pos = torch.cat([dec_pos.view(1, n).expand(3, n),
+                             chunk_seq.kv_handle["pos_full"][:, start:end].to(torch.int64)], 1)
+            pos = pos.to(dev).unsqueeze(1)                                         # [3, 1, n+L]
+            cache = self._pool.mixed_cache(list(range(n)) + [self._reserve_slot],
+                                           [1] * n + [L], dec_len + [start])
+            final = end == P
+            idx = list(range(n)) + ([n + L - 1] if final else [])
+            logits = self.adapter.llm(emb, pos, None, cache, logits_indices=idx)[0]
+            self._dev_ids_for = None
+            if n:
+                self._emit(decode_seqs, self._sample_rows(logits[:n], decode_seqs))
+            chunk_seq.num_prefilled = end
+            if final:
+                self._seat_prefilled(chunk_seq, end, logits[n:n + 1])
+
     def decode(self, seqs: List[Sequence]) -> None:
         seqs = sorted(seqs, key=lambda s: s.kv_handle["slot"])
         n = len(seqs)
@@ -264,7 +361,12 @@ class MultimodalRunner(ModelRunner):
         g, bufs, _view = self._graphs[n]
         self._load_ids(seqs, n, bufs["ids"])
         g.replay()
-        toks = bufs["out"].tolist()
+        # the new ids come back through pinned memory (one DMA, then an event wait)
+        host = self._pinned_out[:n]
+        host.copy_(bufs["out"], non_blocking=True)
+        self._out_ready.record()
+        self._out_ready.synchronize()
+        toks = host.tolist()
         self._emit(seqs, toks)
         self._dev_ids_for = tuple(id(s) for s in seqs) if all(
             s.last_token_id() == t for s, t in zip(seqs, toks)) else None

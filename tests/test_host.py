@@ -131,6 +131,34 @@ def test_query_blocks_cover_segments():
     assert qb == [[0, 5], [5, 16], [21, 16], [37, 1], [38, 1]]
 
 
+def test_append_writer_metadata():
+    """Chunked / mixed adapters (kv_prealloc.py:104-174): per-token slot, write position
+    start+i and visible keys start+i+1; lengths = start+L after finish; bad segments raise."""
+    from omniserver_amd.kv_cache import PreallocatedKVCache
+    pool = PreallocatedKVCache(2, 4, 2, 64, 128, "cpu", n_heads=12)
+    w = pool.mixed_cache([0, 1, 3], [1, 1, 5], [10, 3, 20])
+    assert w.token_slot.tolist() == [0, 1, 3, 3, 3, 3, 3]
+    assert w.token_pos.tolist() == [10, 3, 20, 21, 22, 23, 24]
+    assert w.kv_len.tolist() == [11, 4, 21, 22, 23, 24, 25]
+    assert w.seg == [1, 1, 5] and w.T == 7
+    w.finish()
+    assert pool.lengths.tolist() == [11, 4, 0, 25]
+    c = pool.chunked_prefill_cache(3, 25)
+    assert c.seg is None
+    c.bind(6)
+    assert c.token_pos.tolist() == list(range(25, 31)) and c.kv_len.tolist() == list(range(26, 32))
+    with pytest.raises(ValueError):
+        c.bind(7)                                   # built for 6 tokens
+    with pytest.raises(ValueError):
+        pool.mixed_cache([0], [5], [60])            # past max_len
+    with pytest.raises(ValueError):
+        pool.mixed_cache([1, 1], [1, 2], [0, 5])    # one slot twice
+    with pytest.raises(ValueError):
+        pool.mixed_cache([4], [1], [0])             # slot outside the pool
+    packed = pool.packed_prefill_cache([0, 2], [3, 2])
+    assert packed.token_pos.tolist() == [0, 1, 2, 0, 1] and packed.kv_len.tolist() == [1, 2, 3, 1, 2]
+
+
 def test_decode_plan_and_split_counts():
     from omniserver_amd.kv_cache import MAX_ATTN_SPLITS, decode_plan
     for n in (1, 8, 16, 32, 64):

@@ -304,7 +304,10 @@ def main():
         runner.decode(seqs)
     torch.cuda.synchronize()
 
-    ctx_before = runner.pool.lengths[:B].cpu().tolist()
+    # the runner may hold the next step enqueued ahead (already run by the synchronize):
+    # the first timed step's contexts are the lengths before it
+    ahead = runner.steps_ahead()
+    ctx_before = [L - ahead for L in runner.pool.lengths[:B].cpu().tolist()]
     st = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -321,6 +324,7 @@ def main():
 
     # device time of the step alone: the captured graph replayed back to back (no D2H,
     # no host bookkeeping between steps)
+    runner.settle()
     g = runner._graphs[B][0]
     r0, r1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     r0.record(st)

@@ -11,7 +11,13 @@ one step advances each by one token.  With ``use_graph=True`` the whole step -
 embedding gather + 28 layers + final norm + lm_head/argmax + length advance - is one
 HIP-graph replay per batch size (captured lazily, static buffers kept alive).  The
 host does at most one small H2D (token ids, only when the batch composition
-changed) and one D2H (the new ids) per step.
+changed) and one D2H (the new ids) per step.  While the batch can go on unchanged
+(nobody has finished, every row has room) the next step's replay is enqueued before the
+current step is waited for - its input ids are the current step's outputs, left on the
+device by the graph - so the GPU never waits for the host's per-step bookkeeping.  Any
+other call on the runner (a different batch, prefill, free, chunked prefill) first takes
+that step back with ``settle()``: its length advance is undone and the K/V row it wrote
+lies past the valid length, to be overwritten.
 
 Chunked prefill and mixed batching (multimodal.py:200-284): a long text prompt is
 prefilled chunk by chunk into the reserve slot (pool row ``max_running``), each chunk
@@ -28,7 +34,7 @@ from typing import Dict, List
 import torch
 
 from .kv_cache import PreallocatedKVCache
-from .request import Sequence
+from .request import Sequence, Status
 
 
 class ModelRunner(abc.ABC):
@@ -109,8 +115,13 @@ class MultimodalRunner(ModelRunner):
         self._eager: Dict[int, dict] = {}
         self._dev_ids_for = None              # batch whose next ids already sit on device
         self._pinned_ids = torch.zeros(max_running + 1, dtype=torch.int64).pin_memory()
-        self._pinned_out = torch.zeros(max_running + 1, dtype=torch.int64).pin_memory()
-        self._out_ready = torch.cuda.Event() if torch.cuda.is_available() else None
+        # new ids come back through two pinned buffers (the step being collected and the
+        # one enqueued ahead of it), each with its event
+        self._pinned_out = [torch.zeros(max_running + 1, dtype=torch.int64).pin_memory()
+                            for _ in range(2)]
+        self._out_ready = [torch.cuda.Event() for _ in range(2)] if torch.cuda.is_available() else None
+        self._pin_next = 0
+        self._ahead = None                    # (batch key, n, buffer) of a step enqueued ahead
 
     @property
     def pool(self) -> PreallocatedKVCache:
@@ -125,6 +136,21 @@ class MultimodalRunner(ModelRunner):
             if e not in sp.stop_token_ids:
                 sp.stop_token_ids.append(e)
 
+    # ---- the decode step enqueued ahead --------------------------------------------
+    def steps_ahead(self) -> int:
+        """1 while a decode step for the last batch has been enqueued ahead of the caller."""
+        return 0 if self._ahead is None else 1
+
+    def settle(self) -> None:
+        """Take back a decode step enqueued ahead: undo its length advance and drop its
+        ids (its K/V rows sit at the first position past each valid length)."""
+        if self._ahead is None:
+            return
+        _, n, _ = self._ahead
+        self._ahead = None
+        self._pool.lengths[:n] -= 1
+        self._dev_ids_for = None
+
     @torch.inference_mode()
     def prefill(self, seqs: List[Sequence]) -> None:
         """Packed prefill, compute branch (multimodal.py:116-144): every prompt in one
@@ -132,6 +158,7 @@ class MultimodalRunner(ModelRunner):
         segment ends."""
         if not seqs:
             return
+        self.settle()
         base = len(self._slot_seq)
         if base + len(seqs) > self.max_running:
             raise RuntimeError(f"KV pool full: {base} running + {len(seqs)} new > "
@@ -182,6 +209,7 @@ class MultimodalRunner(ModelRunner):
         """Seat sequences whose KV prefix the caller already wrote into the pool (the
         set_slot_prefix contract, cache/kv_prealloc.py:43-49): each takes the next slot
         with lengths[slot] = L and decodes from there.  Returns the slots."""
+        self.settle()
         base = len(self._slot_seq)
         if base + len(seqs) > self.max_running:
             raise RuntimeError("KV pool full")
@@ -202,6 +230,7 @@ class MultimodalRunner(ModelRunner):
 
     # ---- chunked prefill / mixed batching (multimodal.py:200-284) -------------------
     def _chunk_bounds(self, seq: Sequence):
+        self.settle()
         if not seq.prompt_token_ids:
             self.tokenize(seq)
         P = len(seq.prompt_token_ids)
@@ -303,6 +332,7 @@ class MultimodalRunner(ModelRunner):
         if self._use_graph and greedy:
             self._decode_graph(seqs, n)
         else:
+            self.settle()
             with torch.inference_mode():
                 self._decode_eager(seqs, n, greedy)
 
@@ -355,21 +385,39 @@ class MultimodalRunner(ModelRunner):
         # the view and buffers are referenced by the graph: keep them alive with it
         self._graphs[n] = (g, bufs, view)
 
-    def _decode_graph(self, seqs, n):
-        if n not in self._graphs:
-            self._capture_graph(n)
+    def _launch(self, n: int) -> int:
+        """Replay the step graph for rows [0, n) (inputs: bufs["ids"]) and start the new
+        ids' copy to a pinned buffer; returns the buffer index."""
         g, bufs, _view = self._graphs[n]
-        self._load_ids(seqs, n, bufs["ids"])
         g.replay()
-        # the new ids come back through pinned memory (one DMA, then an event wait)
-        host = self._pinned_out[:n]
-        host.copy_(bufs["out"], non_blocking=True)
-        self._out_ready.record()
-        self._out_ready.synchronize()
-        toks = host.tolist()
+        i = self._pin_next
+        self._pin_next ^= 1
+        self._pinned_out[i][:n].copy_(bufs["out"], non_blocking=True)
+        self._out_ready[i].record()
+        return i
+
+    def _decode_graph(self, seqs, n):
+        key = tuple(id(s) for s in seqs)
+        if self._ahead is not None and self._ahead[0] == key:
+            cur = self._ahead[2]               # enqueued by the previous call
+            self._ahead = None
+        else:
+            self.settle()
+            if n not in self._graphs:
+                self._capture_graph(n)
+            self._load_ids(seqs, n, self._graphs[n][1]["ids"])
+            cur = self._launch(n)
+        # The next step goes out before this one is waited for, when the batch will decode
+        # again as is unless this step finishes someone (nobody has finished, every row has
+        # room): its inputs are this step's ids, which the graph leaves on the device.  If
+        # this step does finish a sequence, the caller's free() takes the next one back.
+        if (all(s.status not in (Status.FINISHED, Status.ABORTED) for s in seqs)
+                and all(self._kv_len[b] + 1 < self._pool.max_len for b in range(n))):
+            self._ahead = (key, n, self._launch(n))
+        self._out_ready[cur].synchronize()
+        toks = self._pinned_out[cur][:n].tolist()
         self._emit(seqs, toks)
-        self._dev_ids_for = tuple(id(s) for s in seqs) if all(
-            s.last_token_id() == t for s, t in zip(seqs, toks)) else None
+        self._dev_ids_for = key
 
     def _emit(self, seqs, toks):
         for b, seq in enumerate(seqs):
@@ -395,6 +443,7 @@ class MultimodalRunner(ModelRunner):
     def free(self, seq: Sequence) -> None:
         """Swap-compact the pool (multimodal.py:359-369): the last slot's sequence moves
         into the freed slot; only its valid KV prefix is copied."""
+        self.settle()
         h = seq.kv_handle or {}
         slot = h.get("slot")
         if slot is None:

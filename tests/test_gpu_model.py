@@ -174,6 +174,50 @@ def test_graph_equals_eager_with_compaction(gpu):
     assert [len(t) for t in streams[0]] == budgets
 
 
+def test_step_ahead_equals_eager(gpu):
+    """The graph runner enqueues the next decode step before returning when the batch will
+    decode again unchanged; a new prefill, a free or a different batch takes it back.  The
+    token streams equal the eager runner's through prefill-while-decoding and compaction,
+    and after settle() the device lengths equal the host's."""
+    from omniserver_amd import synth
+    from omniserver_amd.request import Request, SamplingParams, Sequence, Status
+    from omniserver_amd.runner import NativeQwenVLRunner
+    say("step enqueued ahead vs eager (gptq, 2 layers)")
+    shape = synth.DecoderShape()
+    w = synth.gptq_decoder(shape, seed=12, num_layers=2)
+    prompts = [synth.random_ids(L, shape.vocab_size, 12, f"s{L}").tolist() for L in (9, 30, 21)]
+    budgets = [6, 9, 4]
+    streams, aheads = [], []
+    for use_graph in (False, True):
+        r = NativeQwenVLRunner(max_running=4, max_len=128, use_graph=use_graph, weights=w,
+                               quant="gptq")
+        seqs = [Sequence(Request(prompt=p, sampling=SamplingParams(max_new_tokens=m)))
+                for p, m in zip(prompts, budgets)]
+        for s in seqs:
+            r.tokenize(s)
+        r.prefill(seqs[:2])
+        running = list(seqs[:2])
+        step = 0
+        while running:
+            r.decode(running)
+            aheads.append(r.steps_ahead())
+            step += 1
+            if step == 2:                      # a request arrives while two are decoding
+                r.prefill([seqs[2]])
+                running.append(seqs[2])
+            for s in list(running):
+                if s.status == Status.FINISHED:
+                    r.free(s)
+                    running.remove(s)
+        r.settle()
+        assert r.steps_ahead() == 0
+        assert r.pool.lengths[:len(r._kv_len)].cpu().tolist() == r._kv_len
+        streams.append([s.output_token_ids for s in seqs])
+    assert streams[0] == streams[1]
+    assert [len(t) for t in streams[0]] == budgets
+    assert any(aheads)                         # the graph runner did enqueue ahead
+
+
 def test_multimodal_prefill_positions_and_logits(gpu):
     """Packed prefill of image+text prompts: M-RoPE ids equal the oracle's; logits at the
     segment ends and the pool contents match the oracle."""

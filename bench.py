@@ -130,11 +130,13 @@ def attention_launch_time(runner, B: int, reps: int) -> tuple[float, int]:
     view = runner.pool.view(B, runner._rope_delta)
     bufs = model.decode_buffers(B, dev)
     Sq = model.layers[0].qkv_proj.forward_partial(bufs["h"], bufs["qpart"])
+    view.rope_rows(model.rope_cos, model.rope_sin, bufs["rope"])   # as the step's first launch
 
     def launches():
         for i, layer in enumerate(model.layers):
             view.attend_fused(bufs["qpart"], Sq, layer.qkv_proj.bias, layer.qkv_proj.fmt == "int4",
-                              i, model.scale, model.rope_cos, model.rope_sin, cfg.mrope_section)
+                              i, model.scale, model.rope_cos, model.rope_sin, cfg.mrope_section,
+                              rope_rows=bufs["rope"])
 
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -169,9 +171,11 @@ def pmc_probe(runner, seqs, B: int) -> None:
     view = runner.pool.view(B, runner._rope_delta)
     bufs = model.decode_buffers(B, dev)
     Sq = model.layers[0].qkv_proj.forward_partial(bufs["h"], bufs["qpart"])
+    view.rope_rows(model.rope_cos, model.rope_sin, bufs["rope"])
     for i, layer in enumerate(model.layers):
         view.attend_fused(bufs["qpart"], Sq, layer.qkv_proj.bias, layer.qkv_proj.fmt == "int4",
-                          i, model.scale, model.rope_cos, model.rope_sin, cfg.mrope_section)
+                          i, model.scale, model.rope_cos, model.rope_sin, cfg.mrope_section,
+                          rope_rows=bufs["rope"])
     torch.cuda.synchronize()
     src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)

@@ -53,6 +53,22 @@ int omni_embed_rmsnorm(const int64_t* ids, const void* table, int table_packed, 
                        const void* weight, void* y, void* residual_out, int rows, int hidden,
                        float eps, void* stream);
 
+/* omni_embed_rmsnorm that also writes the decode step's rotary rows (omni_rope_rows for
+ * rows 0..rows-1) in the same launch. */
+int omni_embed_rmsnorm_rope(const int64_t* ids, const void* table, int table_packed,
+                            int64_t vocab, const void* weight, void* y, void* residual_out,
+                            int rows, int hidden, float eps, const int64_t* lengths,
+                            const int64_t* rope_delta, const void* cos_tab, const void* sin_tab,
+                            int max_pos, void* rope_rows, void* stream);
+
+/* Rotary rows of T decode tokens (model/qwen2_llm.py:169-177, 181 at one position on all
+ * three M-RoPE axes): rope_rows fp16 [T][128] = cos | sin (fp16 tables [max_pos][64]) at
+ * p = lengths[r] + rope_delta[r] (clamped to the tables), r = slots[t] (NULL: t).  A decode
+ * step computes them once for all of its layers' omni_decode_attention_fused calls. */
+int omni_rope_rows(const int64_t* slots, const int64_t* lengths, const int64_t* rope_delta,
+                   const void* cos_tab, const void* sin_tab, int max_pos, int pool_rows, int T,
+                   void* rope_rows, void* stream);
+
 /* embed_tokens (models/qwen2_vl.py:93-94): out[t] = table[ids[t]] (ids clamped to range). */
 int omni_embedding(const int64_t* ids, const void* table, int table_packed, int64_t vocab,
                    void* out, int rows, int hidden, void* stream);
@@ -114,14 +130,17 @@ int omni_decode_attention(const void* q, int q_stride, const void* k_cache, cons
  * [0, lengths[slot]] (:272-290).  slots NULL = row t.  lengths are not advanced.
  * n_heads / n_kv_heads <= 8.  merge = 1: out fp16 [T, n_heads, 128] (a merge launch
  * follows when splits > 1); merge = 0: the split states stay in workspace (>= T * n_kv *
- * splits * G * 132 fp32) for omni_*_gemm_attn and out is not written. */
+ * splits * G * 132 fp32) for omni_*_gemm_attn and out is not written.  rope_rows (may be
+ * NULL): token t's rotary row from omni_rope_rows instead of a cos/sin table lookup at its
+ * position (cos_tab, sin_tab, max_pos, rope_delta are then unused). */
 int omni_decode_attention_fused(const float* qkv_partials, int nparts, const void* qkv_bias,
                                 int bias_after_round, const void* cos_tab, const void* sin_tab,
                                 int max_pos, const int64_t* rope_delta, int sec0, int sec1,
                                 int sec2, void* k_cache, void* v_cache, int pool_rows, int max_len,
                                 const int64_t* slots, const int64_t* lengths, void* out, int T,
                                 int n_heads, int n_kv_heads, int head_dim, float scale, int waves,
-                                int splits, float* workspace, int merge, void* stream);
+                                int splits, float* workspace, int merge, const void* rope_rows,
+                                void* stream);
 
 /* _PackedPrefillWriter.flash_prefill (cache/kv_prealloc.py:181-203) and the append form
  * of :149-174: token t attends causally to keys [0, kv_len[t]) of pool row slots[t].

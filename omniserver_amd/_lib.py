@@ -27,6 +27,9 @@ SIGNATURES = {
     "omni_add_rmsnorm_fp8": [_P, _P, _P, _P, _P, _P, _I, _I, _F, _P],
     "omni_add_rmsnorm_partials": [_P, _I, _P, _P, _P, _P, _I, _I, _F, _P],
     "omni_embed_rmsnorm": [_P, _P, _I, _I64, _P, _P, _P, _I, _I, _F, _P],
+    "omni_embed_rmsnorm_rope": [_P, _P, _I, _I64, _P, _P, _P, _I, _I, _F, _P, _P, _P, _P, _I,
+                                _P, _P],
+    "omni_rope_rows": [_P, _P, _P, _P, _P, _I, _I, _I, _P, _P],
     "omni_embedding": [_P, _P, _I, _I64, _P, _I, _I, _P],
     "omni_silu_mul": [_P, _P, _I, _I, _P],
     "omni_mrope_kv_write": [_P, _I, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I,
@@ -36,7 +39,7 @@ SIGNATURES = {
     "omni_decode_attention": [_P, _I, _P, _P, _I, _I, _P, _P, _I, _I, _P, _I, _I, _I, _I, _F, _I,
                               _I, _P, _P],
     "omni_decode_attention_fused": [_P, _I, _P, _I, _P, _P, _I, _P, _I, _I, _I, _P, _P, _I, _I,
-                                    _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _P, _I, _P],
+                                    _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _P, _I, _P, _P],
     "omni_fp8_quant_rows": [_P, _I, _P, _P, _I, _I, _F, _P],
     "omni_fp8_gemm": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
     "omni_w4a16_gemm_attn": [_P, _I, _I, _I, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I, _I,

@@ -58,6 +58,9 @@ struct AttnArgs {
   int max_pos;
   const int64_t* rope_delta;
   int s0, s1;
+  // Precomputed rotary rows [T][128] fp16: cos | sin of p * inv_freq at each token's
+  // position p (the same for every layer of a decode step, so written once per step).
+  const half_t* rope_rows;
 };
 
 #define ATT_MAXPARTS 8   // qkv partial slices the fused prologue sums (one batch of loads)
@@ -66,9 +69,12 @@ __device__ __forceinline__ int64_t clamp64(int64_t v, int64_t lo, int64_t hi) {
   return v < lo ? lo : (v > hi ? hi : v);
 }
 
-// FUSED: q and the new token's k / v come from the qkv partials (a.qparts != NULL); the
-// two forms are separate instantiations so that neither carries the other's wait states.
-template <int NWA, bool FUSED>
+// FUSED: q and the new token's k / v come from the qkv partials (a.qparts != NULL), with
+// the rotary row looked up in the cos/sin tables at the token's position (FUSED = 1) or
+// read from precomputed rows (FUSED = 2, requested with the partials, so that it is not a
+// second round trip behind the context length, queued behind the grid's K/V stream).  The
+// forms are separate instantiations so that none carries another's wait states.
+template <int NWA, int FUSED>
 __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_kernel(AttnArgs a) {
   constexpr int NT = NWA * 64;
   // The V tiles (block loop), the fused prologue's pre-rotation rows (before it) and
@@ -92,6 +98,17 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
   const int wave = threadIdx.x >> 6;
   const int q16 = lane >> 4;     // lane group 0..3
   const int c16 = lane & 15;     // column within MFMA tile
+  // Every argument the prologue's addresses need is read into registers in one batch
+  // first: scalar loads complete out of order, so a wait for any one of them waits for all,
+  // and an argument fetched after the context length would hold the prologue's global
+  // loads behind the length's round trip (each such chain is a memory round trip).
+  asm volatile("" ::"s"(a.S), "s"(a.nkv), "s"(a.G), "s"(a.T), "s"(a.nq), "s"(a.max_len),
+               "s"(a.pool_rows), "s"(a.kv_by_slot), "s"(a.kv_add), "s"(a.max_pos),
+               "s"(a.qparts), "s"(a.qbias), "s"(a.kv_len), "s"(a.slots), "s"(a.rope_delta),
+               "s"(a.cos_tab), "s"(a.sin_tab), "s"(a.k_cache), "s"(a.v_cache), "s"(gridDim.x),
+               "s"(a.bias_after_round), "s"(a.out), "s"(a.part), "s"(a.parts_out),
+               "s"(a.scale_log2), "s"(a.q), "s"(a.q_stride), "s"(a.s0), "s"(a.s1),
+               "s"(a.rope_rows));
   const int S = a.S;
   // The S workgroups of one (token, kv head) are neighbours in XCD-aware order, so they
   // share an L2 and the token's qkv partials are fetched from HBM once, not S times.
@@ -101,20 +118,15 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
   const int t = blk / (S * a.nkv);
   const int G = a.G;
   const int nh = a.nkv * G;
-  constexpr bool fused = FUSED;
+  constexpr bool fused = FUSED != 0;
 
   // 1. Loads that do not depend on the context length, all issued before any is used (a
   //    load placed after a store or a use would cost the prologue another memory round
-  //    trip): the context length and rope delta of this token's pool row and, for the
-  //    fused prologue, q heads g*G .. g*G+G-1 and k, v of kv head g as fp32 split-K partials
-  //    (at most ATT_MAXPARTS slices, all in flight at once) and their bias.  Optional operands are read through a valid stand-in address and
-  //    replaced by zero, so no load sits behind a branch.
-  const int64_t slot = a.slots ? a.slots[t] : t;
-  const bool slot_ok = slot >= 0 && slot < a.pool_rows;
-  const int64_t srow = slot_ok ? slot : 0;
-  const int64_t kv_raw = a.kv_len[a.kv_by_slot ? srow : t];
-  const int64_t* dptr = a.rope_delta ? a.rope_delta : a.kv_len;
-  const int64_t delta_raw = fused ? dptr[srow] : 0;
+  //    trip): for the fused prologue, q heads g*G .. g*G+G-1 and k, v of kv head g as fp32
+  //    split-K partials (at most ATT_MAXPARTS slices, all in flight at once) and their
+  //    bias, then the context length and rope delta of this token's pool row.  Optional
+  //    operands are read through a valid stand-in address and replaced by zero, so no
+  //    load sits behind a branch.
   constexpr int PI = ((ATT_FUSED_MAXG + 2) * ATT_HD / 2 + NT - 1) / NT;
   float2 pv[PI][8];
   half2_t bias2[PI];
@@ -145,6 +157,23 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
       bias2[j] = *(const half2_t*)(bptr + col);
     }
   }
+  // cos (threads 0-7) / sin (8-15) chunk of the token's rotary row.  Every thread issues
+  // the load (threads past 15 re-read a chunk and drop it): a load behind a thread-index
+  // branch leaves the compiler unsure whether it is outstanding, and it then waits for it
+  // (vmcnt(0)) before using any load issued earlier.
+  half8_t csv = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
+  if constexpr (FUSED == 2)
+    csv = *(const half8_t*)(a.rope_rows + (int64_t)t * ATT_HD + (threadIdx.x & 15) * 8);
+  // The context length and rope delta are requested after the partials (the barrier keeps
+  // the compiler from hoisting them, and the arithmetic on them, above those loads): the
+  // partials then go out at once instead of a round trip later.
+  asm volatile("" ::: "memory");
+  const int64_t slot = a.slots ? a.slots[t] : t;
+  const bool slot_ok = slot >= 0 && slot < a.pool_rows;
+  const int64_t srow = slot_ok ? slot : 0;
+  const int64_t kv_raw = a.kv_len[a.kv_by_slot ? srow : t];
+  const int64_t* dptr = a.rope_delta ? a.rope_delta : a.kv_len;
+  const int64_t delta_raw = FUSED == 1 ? dptr[srow] : 0;
 
   // 2. Context length, this workgroup's key range, the rotary row.
   const int64_t L_raw = slot_ok ? kv_raw + a.kv_add : 0;
@@ -163,12 +192,9 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
   const int wg_b0 = (int)((int64_t)sp * NWA * nblk / nw);
   const int wg_b1 = (int)((int64_t)(sp + 1) * NWA * nblk / nw);
 
-  // cos (threads 0-7) / sin (8-15) row at pos.  Every thread issues the load (threads
-  // past 15 re-read a chunk and drop it): a load behind a thread-index branch leaves the
-  // compiler unsure whether it is outstanding, and it then waits for it (vmcnt(0)) before
-  // using any load issued earlier.
-  half8_t csv = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
-  if (fused) {
+  // FUSED = 1: the rotary row from the tables at the token's position (a load that waits
+  // for the context length).
+  if constexpr (FUSED == 1) {
     int64_t pos = slot_ok ? kv_raw + (a.rope_delta ? delta_raw : 0) : 0;
     pos = clamp64(pos, 0, a.max_pos - 1);
     const half_t* tab = (threadIdx.x & 15) < 8 ? a.cos_tab : a.sin_tab;
@@ -208,10 +234,13 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
     load_block(kf0, vr0, beg);
     load_block(kf1, vr1, beg + ATT_BLK);
   };
-  // Without the fused prologue the stream starts at once.  With it, the K/V stream starts
-  // once the prologue's loads (the qkv partials and bias, cache-resident) have returned:
-  // issued behind the whole grid's K/V requests they would wait for nearly all of the
-  // context to arrive.  The rest of the prologue (LDS, M-RoPE) overlaps the stream.
+  // Without the fused prologue the stream starts at once.  With it, the first block goes
+  // out once the prologue's loads have returned (a load issued after the grid's K/V
+  // requests waits for nearly all of them) and the second once q is in registers: a wave
+  // issuing K/V loads stalls in issue while the CU has many requests outstanding, so
+  // prologue work placed after both blocks - even LDS-only work behind a barrier - would
+  // wait for most of the stream, while one block in flight during the rotary step keeps
+  // the stream going without holding that step back.
   if (!fused) issue_first_blocks();
 
   if (fused) {
@@ -240,10 +269,7 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
         raw[2 * i + 1] = h1;
       }
     }
-    // The K/V stream goes out as soon as the partials are consumed; the cos/sin row (a
-    // second round trip: its address needs the context length) was requested before it,
-    // so storing it below waits for that row only, not for the stream.
-    issue_first_blocks();
+    load_block(kf0, vr0, beg);
     if (threadIdx.x < 16) *(half8_t*)(&cs_lds[threadIdx.x >> 3][(threadIdx.x & 7) * 8]) = csv;
     lds_barrier();
     // 5. M-RoPE (decode: one position on all three axes) in fp16 ops, one rounding
@@ -292,6 +318,7 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
       qf[ks] = v;
     }
   }
+  if (fused) load_block(kf1, vr1, beg + ATT_BLK);
 
   float m_run = -INFINITY;   // per head c16 (identical across q16 groups)
   float l_run = 0.f;         // lane-partial sum, reduced at the end
@@ -516,6 +543,7 @@ extern "C" int omni_decode_attention(const void* q, int q_stride, const void* k_
   a.max_pos = 0;
   a.rope_delta = nullptr;
   a.s0 = a.s1 = 0;
+  a.rope_rows = nullptr;
   return launch_decode_attn(a, n_kv_heads, T, G, waves, splits, 1, workspace, (hipStream_t)stream);
 }
 
@@ -524,14 +552,18 @@ static int launch_decode_attn(AttnArgs a, int n_kv_heads, int T, int G, int wave
   a.parts_out = splits > 1 || !merge;
   const int64_t nblocks = (int64_t)n_kv_heads * T * splits;
   if (nblocks > 0x7fffffff) return OMNI_EUNSUPPORTED;
-  const bool fused = a.qparts != nullptr;
-  switch (waves * 2 + (fused ? 1 : 0)) {
-    case 8: hipLaunchKernelGGL((decode_attn_kernel<4, false>), dim3((unsigned)nblocks), dim3(256), 0, st, a); break;
-    case 9: hipLaunchKernelGGL((decode_attn_kernel<4, true>), dim3((unsigned)nblocks), dim3(256), 0, st, a); break;
-    case 16: hipLaunchKernelGGL((decode_attn_kernel<8, false>), dim3((unsigned)nblocks), dim3(512), 0, st, a); break;
-    case 17: hipLaunchKernelGGL((decode_attn_kernel<8, true>), dim3((unsigned)nblocks), dim3(512), 0, st, a); break;
-    case 32: hipLaunchKernelGGL((decode_attn_kernel<16, false>), dim3((unsigned)nblocks), dim3(1024), 0, st, a); break;
-    default: hipLaunchKernelGGL((decode_attn_kernel<16, true>), dim3((unsigned)nblocks), dim3(1024), 0, st, a); break;
+  const int form = a.qparts == nullptr ? 0 : (a.rope_rows ? 2 : 1);
+  const dim3 grid((unsigned)nblocks);
+  switch (waves * 4 + form) {
+    case 16: hipLaunchKernelGGL((decode_attn_kernel<4, 0>), grid, dim3(256), 0, st, a); break;
+    case 17: hipLaunchKernelGGL((decode_attn_kernel<4, 1>), grid, dim3(256), 0, st, a); break;
+    case 18: hipLaunchKernelGGL((decode_attn_kernel<4, 2>), grid, dim3(256), 0, st, a); break;
+    case 32: hipLaunchKernelGGL((decode_attn_kernel<8, 0>), grid, dim3(512), 0, st, a); break;
+    case 33: hipLaunchKernelGGL((decode_attn_kernel<8, 1>), grid, dim3(512), 0, st, a); break;
+    case 34: hipLaunchKernelGGL((decode_attn_kernel<8, 2>), grid, dim3(512), 0, st, a); break;
+    case 64: hipLaunchKernelGGL((decode_attn_kernel<16, 0>), grid, dim3(1024), 0, st, a); break;
+    case 65: hipLaunchKernelGGL((decode_attn_kernel<16, 1>), grid, dim3(1024), 0, st, a); break;
+    default: hipLaunchKernelGGL((decode_attn_kernel<16, 2>), grid, dim3(1024), 0, st, a); break;
   }
   OMNI_CHECK_LAUNCH();
   if (splits > 1 && merge) {
@@ -545,8 +577,10 @@ static int launch_decode_attn(AttnArgs a, int n_kv_heads, int T, int G, int wave
 // Decode step attention fused with its producer's epilogue: q and the new token's k / v
 // are formed from the qkv projection's fp32 split-K partials [nparts][T][(nh+2nkv)*128]
 // plus bias (bias_after_round: GPTQ rounding order), M-RoPE'd at position
-// lengths[slot] + rope_delta[slot] with the fp16 cos/sin tables, the new K/V row is
-// stored at pool[slot, lengths[slot]], and token t attends to keys [0, lengths[slot]].
+// lengths[slot] + rope_delta[slot] with the fp16 cos/sin tables - or, when rope_rows is
+// given, with that token's precomputed row rope_rows[t] = cos | sin at its position
+// (omni_rope_rows / omni_embed_rmsnorm_rope) - the new K/V row is stored at
+// pool[slot, lengths[slot]], and token t attends to keys [0, lengths[slot]].
 // Replaces omni_mrope_kv_write + omni_decode_attention for a decode step (lengths are
 // not advanced).  merge = 0 leaves the split states in workspace (out unused) for the
 // o_proj GEMM that merges them while staging its input (omni_*_gemm_attn).
@@ -555,9 +589,10 @@ extern "C" int omni_decode_attention_fused(
     const void* cos_tab, const void* sin_tab, int max_pos, const int64_t* rope_delta, int sec0,
     int sec1, int sec2, void* k_cache, void* v_cache, int pool_rows, int max_len,
     const int64_t* slots, const int64_t* lengths, void* out, int T, int n_heads, int n_kv_heads,
-    int head_dim, float scale, int waves, int splits, float* workspace, int merge, void* stream) {
-  if (T < 0 || n_heads <= 0 || n_kv_heads <= 0 || pool_rows <= 0 || max_len <= 0 || max_pos <= 0)
-    return OMNI_EINVAL;
+    int head_dim, float scale, int waves, int splits, float* workspace, int merge,
+    const void* rope_rows, void* stream) {
+  if (T < 0 || n_heads <= 0 || n_kv_heads <= 0 || pool_rows <= 0 || max_len <= 0) return OMNI_EINVAL;
+  if (!rope_rows && max_pos <= 0) return OMNI_EINVAL;
   if (head_dim != ATT_HD || n_heads % n_kv_heads) return OMNI_EUNSUPPORTED;
   if (sec0 + sec1 + sec2 != ATT_HD / 2 || (sec0 & 7) || (sec1 & 7) || (sec2 & 7)) return OMNI_EUNSUPPORTED;
   const int G = n_heads / n_kv_heads;
@@ -566,7 +601,8 @@ extern "C" int omni_decode_attention_fused(
   if (waves != 4 && waves != 8 && waves != 16) return OMNI_EINVAL;
   if (splits < 1 || splits > 64) return OMNI_EINVAL;
   if (T == 0) return OMNI_OK;
-  if (!qkv_partials || !cos_tab || !sin_tab || !k_cache || !v_cache || !lengths) return OMNI_EINVAL;
+  if (!qkv_partials || !k_cache || !v_cache || !lengths) return OMNI_EINVAL;
+  if (!rope_rows && (!cos_tab || !sin_tab)) return OMNI_EINVAL;
   if (merge ? !out : false) return OMNI_EINVAL;
   if ((splits > 1 || !merge) && !workspace) return OMNI_EINVAL;
   AttnArgs a;
@@ -597,6 +633,7 @@ extern "C" int omni_decode_attention_fused(
   a.rope_delta = rope_delta;
   a.s0 = sec0;
   a.s1 = sec1;
+  a.rope_rows = (const half_t*)rope_rows;
   return launch_decode_attn(a, n_kv_heads, T, G, waves, splits, merge, workspace,
                             (hipStream_t)stream);
 }

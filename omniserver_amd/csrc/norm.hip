@@ -24,15 +24,36 @@ __device__ __forceinline__ size_t packed16_offset(int64_t n, int k, int K) {
   return ((((size_t)nt * (K >> 5) + ks) * 64 + lane) << 3) + (k & 7);
 }
 
+// Rotary row of one decode token (lanes 0-15): row[0:64] = cos, row[64:128] = sin of
+// p * inv_freq, p = lengths[r] + rope_delta[r] clamped to the tables, read from the same
+// fp16 tables the attention would index (qwen2_llm.py:169-177; a decode token has one
+// position on all three M-RoPE axes).  A decode step writes these rows once for all of its
+// layers' attention launches.
+#define ROPE_HALF 64
+__device__ __forceinline__ void rope_row(int lane, int64_t r, const int64_t* __restrict__ len,
+                                         const int64_t* __restrict__ delta,
+                                         const half_t* __restrict__ cos_tab,
+                                         const half_t* __restrict__ sin_tab, int max_pos,
+                                         half_t* __restrict__ out_row) {
+  int64_t pos = len[r] + (delta ? delta[r] : 0);
+  pos = pos < 0 ? 0 : (pos >= max_pos ? max_pos - 1 : pos);
+  const half_t* tab = lane < 8 ? cos_tab : sin_tab;
+  *(half8_t*)(out_row + lane * 8) = *(const half8_t*)(tab + pos * ROPE_HALF + (lane & 7) * 8);
+}
+
 // PARTS: x is the fp32 split-K partial sums [nparts][rows][H] of the producing
 // linear, summed in slice order and rounded to fp16 (= that linear's fp16 output).
+// GATHER with rope_rows: the rows' rotary rows for the step are written as well.
 template <bool HAS_RES, bool GATHER, bool FP8OUT, bool PARTS = false>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(
     const half_t* x, const half_t* residual, const int64_t* __restrict__ ids,
     const half_t* __restrict__ table, int table_packed, int64_t vocab,
     const half_t* __restrict__ w, half_t* y, uint8_t* __restrict__ y8,
     float* __restrict__ scale_out, half_t* res_out, int rows, int H, float eps,
-    const float* __restrict__ parts = nullptr, int nparts = 0) {
+    const float* __restrict__ parts = nullptr, int nparts = 0,
+    const int64_t* __restrict__ rr_len = nullptr, const int64_t* __restrict__ rr_delta = nullptr,
+    const half_t* __restrict__ rr_cos = nullptr, const half_t* __restrict__ rr_sin = nullptr,
+    int rr_max = 0, half_t* __restrict__ rope_rows = nullptr) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -43,6 +64,8 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(
   if (GATHER) {
     tok = ids[row];
     tok = tok < 0 ? 0 : (tok >= vocab ? vocab - 1 : tok);
+    if (rope_rows && lane < 16)
+      rope_row(lane, row, rr_len, rr_delta, rr_cos, rr_sin, rr_max, rope_rows + (size_t)row * 2 * ROPE_HALF);
   }
 
   half8_t r[NORM_MAX_CHUNKS];
@@ -255,6 +278,57 @@ extern "C" int omni_embed_rmsnorm(const int64_t* ids, const void* table, int tab
                      (hipStream_t)stream, nullptr, nullptr, ids, (const half_t*)table, table_packed,
                      vocab, (const half_t*)weight, (half_t*)y, nullptr, nullptr,
                      (half_t*)residual_out, rows, hidden, eps);
+  OMNI_CHECK_LAUNCH();
+  return OMNI_OK;
+}
+
+// omni_embed_rmsnorm that also writes the step's rotary rows (see rope_row).
+extern "C" int omni_embed_rmsnorm_rope(const int64_t* ids, const void* table, int table_packed,
+                                       int64_t vocab, const void* weight, void* y,
+                                       void* residual_out, int rows, int hidden, float eps,
+                                       const int64_t* lengths, const int64_t* rope_delta,
+                                       const void* cos_tab, const void* sin_tab, int max_pos,
+                                       void* rope_rows, void* stream) {
+  int rc = check_norm_shape(rows, hidden);
+  if (rc) return rc;
+  if (rows == 0) return OMNI_OK;
+  if (!ids || !table || !weight || !y || !residual_out || vocab <= 0) return OMNI_EINVAL;
+  if (!lengths || !cos_tab || !sin_tab || !rope_rows || max_pos <= 0) return OMNI_EINVAL;
+  if (table_packed && ((hidden & 31) != 0 || (vocab & 15) != 0)) return OMNI_EUNSUPPORTED;
+  hipLaunchKernelGGL((rmsnorm_kernel<false, true, false>), dim3(ceil_div(rows, 4)), dim3(256), 0,
+                     (hipStream_t)stream, nullptr, nullptr, ids, (const half_t*)table, table_packed,
+                     vocab, (const half_t*)weight, (half_t*)y, nullptr, nullptr,
+                     (half_t*)residual_out, rows, hidden, eps, nullptr, 0, lengths, rope_delta,
+                     (const half_t*)cos_tab, (const half_t*)sin_tab, max_pos, (half_t*)rope_rows);
+  OMNI_CHECK_LAUNCH();
+  return OMNI_OK;
+}
+
+__global__ __launch_bounds__(64) void rope_rows_kernel(const int64_t* __restrict__ slots,
+                                                       const int64_t* __restrict__ lengths,
+                                                       const int64_t* __restrict__ delta,
+                                                       const half_t* __restrict__ cos_tab,
+                                                       const half_t* __restrict__ sin_tab,
+                                                       int max_pos, int pool_rows, int T,
+                                                       half_t* __restrict__ out) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 4);
+  if (t >= T) return;
+  int64_t r = slots ? slots[t] : t;
+  r = r < 0 ? 0 : (r >= pool_rows ? pool_rows - 1 : r);
+  rope_row(threadIdx.x & 15, r, lengths, delta, cos_tab, sin_tab, max_pos, out + (size_t)t * 2 * ROPE_HALF);
+}
+
+// Rotary rows [T][128] of T decode tokens (pool rows slots[t], or t) at their write
+// positions lengths[row] + rope_delta[row], for omni_decode_attention_fused.
+extern "C" int omni_rope_rows(const int64_t* slots, const int64_t* lengths,
+                              const int64_t* rope_delta, const void* cos_tab, const void* sin_tab,
+                              int max_pos, int pool_rows, int T, void* rope_rows, void* stream) {
+  if (T < 0 || max_pos <= 0 || pool_rows <= 0) return OMNI_EINVAL;
+  if (T == 0) return OMNI_OK;
+  if (!lengths || !cos_tab || !sin_tab || !rope_rows) return OMNI_EINVAL;
+  hipLaunchKernelGGL(rope_rows_kernel, dim3(ceil_div(T, 4)), dim3(64), 0, (hipStream_t)stream,
+                     slots, lengths, rope_delta, (const half_t*)cos_tab, (const half_t*)sin_tab,
+                     max_pos, pool_rows, T, (half_t*)rope_rows);
   OMNI_CHECK_LAUNCH();
   return OMNI_OK;
 }

@@ -108,3 +108,17 @@ def embed_rms_norm_out(ids, table, packed: bool, weight, eps, out, res_out):
     call("omni_embed_rmsnorm", ptr(ids), ptr(table), int(packed), vocab, ptr(weight), ptr(out),
          ptr(res_out), ids.numel(), hidden, float(eps), stream())
     return out, res_out
+
+
+def embed_rms_norm_rope_out(ids, table, packed: bool, weight, eps, out, res_out, lengths,
+                            rope_delta, cos_tab, sin_tab, rope_rows):
+    """embed_rms_norm_out that also writes the decode step's rotary rows [n, 128] (cos |
+    sin at lengths[row] + rope_delta[row]) in the same launch."""
+    require_cuda(ids, lengths, dtype=torch.int64)
+    require_cuda(table, weight, out, res_out, cos_tab, sin_tab, rope_rows, dtype=torch.float16)
+    hidden = out.shape[-1]
+    vocab = table.numel() // hidden
+    call("omni_embed_rmsnorm_rope", ptr(ids), ptr(table), int(packed), vocab, ptr(weight),
+         ptr(out), ptr(res_out), ids.numel(), hidden, float(eps), ptr(lengths), ptr(rope_delta),
+         ptr(cos_tab), ptr(sin_tab), cos_tab.shape[0], ptr(rope_rows), stream())
+    return out, res_out

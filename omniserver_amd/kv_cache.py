@@ -174,12 +174,21 @@ class CacheView:
         return self.pool.attend(qkv, qkv.stride(0), layer_idx, self.pool.lengths, True, 1, out,
                                 self.n, scale, plan=plan)
 
+    def rope_rows(self, cos_tab, sin_tab, out: torch.Tensor) -> torch.Tensor:
+        """out [n, 128] fp16 = cos | sin rows at each row's write position lengths[row] +
+        rope_delta[row] (one per decode step, for every layer's attend_fused)."""
+        pool = self.pool
+        call("omni_rope_rows", None, ptr(pool.lengths), ptr(self.rope_delta), ptr(cos_tab),
+             ptr(sin_tab), cos_tab.shape[0], pool.max_batch, self.n, ptr(out), stream())
+        return out
+
     def attend_fused(self, qparts, nparts: int, bias, bias_after_round: bool, layer_idx: int,
                      scale: float, cos_tab, sin_tab, mrope_section, out=None,
-                     plan: tuple | None = None):
+                     plan: tuple | None = None, rope_rows: torch.Tensor | None = None):
         """Decode attention fused with its producer's epilogue: q / new k, v from the qkv
-        projection's fp32 split-K partials (+ bias), M-RoPE at lengths[row] + rope_delta,
-        new K/V row stored at lengths[row], attention over keys [0, lengths[row]].
+        projection's fp32 split-K partials (+ bias), M-RoPE at lengths[row] + rope_delta
+        (from ``rope_rows`` when given, see rope_rows()), new K/V row stored at
+        lengths[row], attention over keys [0, lengths[row]].
 
         With ``out`` the merged fp16 output goes there and is returned; without it the
         split softmax states stay in the pool's workspace and (states, splits) is returned
@@ -191,7 +200,8 @@ class CacheView:
              ptr(cos_tab), ptr(sin_tab), cos_tab.shape[0], ptr(self.rope_delta), s0, s1, s2,
              ptr(pool.k[layer_idx]), ptr(pool.v[layer_idx]), pool.max_batch, pool.max_len, None,
              ptr(pool.lengths), ptr(out), n, pool.n_heads, pool.n_kv_heads, pool.head_dim,
-             float(scale), w, s, ptr(pool._attn_ws), int(out is not None), stream())
+             float(scale), w, s, ptr(pool._attn_ws), int(out is not None), ptr(rope_rows),
+             stream())
         return out if out is not None else (pool._attn_ws, s)
 
     def flash_decode(self, q, key, value, layer_idx, scale):

@@ -165,6 +165,7 @@ class Qwen2LLM(nn.Module):
                 "qkv": mk(n, cfg.qkv_out), "attn": mk(n, cfg.num_heads * cfg.head_dim),
                 "act": mk(n, I),
                 "dpart": f32(Sd, n, H), "opart": f32(So, n, H), "qpart": f32(Sq, n, cfg.qkv_out),
+                "rope": mk(n, cfg.head_dim),
             }
         return self._bufs[n]
 
@@ -188,8 +189,11 @@ class Qwen2LLM(nn.Module):
         b = self.decode_buffers(n, ids.device)
         eps = cfg.rms_norm_eps
         h, res = b["h"], b["res"]
-        F.embed_rms_norm_out(ids, self.lm_head.table_packed, True, self.layers[0].in_norm, eps,
-                             h, res)
+        # the step's rotary rows (one position per row, the same for every layer) come out
+        # of the first launch, so that no attention prologue looks them up
+        F.embed_rms_norm_rope_out(ids, self.lm_head.table_packed, True, self.layers[0].in_norm,
+                                  eps, h, res, view.pool.lengths, view.rope_delta, self.rope_cos,
+                                  self.rope_sin, b["rope"])
         S = 0
         for i, layer in enumerate(self.layers):
             if i > 0:
@@ -198,7 +202,7 @@ class Qwen2LLM(nn.Module):
             Sq = qp.forward_partial(h, b["qpart"])
             states, Sa = view.attend_fused(b["qpart"], Sq, qp.bias, qp.fmt == "int4", i,
                                            self.scale, self.rope_cos, self.rope_sin,
-                                           cfg.mrope_section)
+                                           cfg.mrope_section, rope_rows=b["rope"])
             So = layer.o_proj.forward_partial_attn(states, Sa, cfg.num_kv_heads,
                                                    cfg.num_heads // cfg.num_kv_heads, n, b["opart"])
             F.add_rms_norm_partials_out(b["opart"], So, res, layer.post_norm, eps, h, res)

@@ -49,6 +49,10 @@ def test_ctypes_table_matches_header():
         assert len(SIGNATURES[name]) == len(params), name
 
 
+def fake_ptr():
+    return ctypes.c_void_p(16)   # never dereferenced: validation fails first
+
+
 def test_bad_arguments_rejected_before_launch(so):
     from omniserver_amd._lib import lib
     L = lib()
@@ -64,6 +68,13 @@ def test_bad_arguments_rejected_before_launch(so):
                                    2, 64, 0.1, 4, 1, None, None) == -2
     assert L.omni_decode_attention(None, 1536, None, None, 1, 16, None, None, 0, 0, None, 1, 12,
                                    2, 128, 0.1, 4, 0, None, None) == -1
+    # rotary rows: negative count, missing tables; the fused attention without rows needs them
+    assert L.omni_rope_rows(None, None, None, None, None, 64, 4, -1, None, None) == -1
+    assert L.omni_rope_rows(None, fake_ptr(), None, None, None, 64, 4, 2, fake_ptr(), None) == -1
+    assert L.omni_decode_attention_fused(fake_ptr(), 6, None, 1, None, None, 64, None, 16, 24,
+                                         24, fake_ptr(), fake_ptr(), 4, 64, None, fake_ptr(),
+                                         fake_ptr(), 2, 12, 2, 128, 0.1, 8, 4, fake_ptr(), 1,
+                                         None, None) == -1
     # GEMM: split-K partials past the skinny kernel's 64 rows, K not a multiple of 128,
     # split without partial epilogue; more rows with the STORE epilogue are the tiled GEMM
     # (here rejected for its null pointers, not its size)

@@ -65,6 +65,19 @@ def test_rmsnorm_and_embed(gpu):
     F.embed_rms_norm_out(ids.to(gpu), lm.table_packed, True, w.to(gpu), 1e-6, h, res)
     assert torch.equal(res.cpu(), table[ids])
     assert torch.equal(h.cpu(), y.cpu())
+    # the decode step's first launch also writes each row's rotary row: the cos | sin table
+    # rows at lengths + delta (clamped), bit-equal to indexing the tables
+    from omniserver_amd.qwen2_llm import rope_tables
+    cos, sin = rope_tables(ref.Qwen2Config(), 512, gpu)
+    lens = torch.tensor([0, 37, 511, 600, 200], dtype=torch.int64)
+    delta = torch.tensor([0, -5, 3, 0, -300], dtype=torch.int64)
+    rows = torch.empty(len(ids), 128, device=gpu, dtype=torch.float16)
+    h2, res2 = torch.empty_like(out), torch.empty_like(out)
+    F.embed_rms_norm_rope_out(ids.to(gpu), lm.table_packed, True, w.to(gpu), 1e-6, h2, res2,
+                              lens.to(gpu), delta.to(gpu), cos, sin, rows)
+    assert torch.equal(h2.cpu(), h.cpu()) and torch.equal(res2.cpu(), res.cpu())
+    pos = (lens + delta).clamp(0, 511)
+    assert torch.equal(rows.cpu(), torch.cat([cos.cpu()[pos], sin.cpu()[pos]], 1))
 
 
 def test_add_rmsnorm_fp8(gpu):
@@ -478,15 +491,19 @@ def test_decode_attention_fused_equals_unfused(gpu, bias_after_round, splits, le
     vp0 = f16((P, ML, nkv, hd), 123)
     lens = torch.tensor(lengths + [0], dtype=torch.int64).to(gpu)
     cos, sin = rope_tables(cfg, 8192, gpu)
+    rows = torch.empty(n, hd, device=gpu, dtype=torch.float16)
+    call("omni_rope_rows", None, ptr(lens), ptr(delta), ptr(cos), ptr(sin), 8192, P, n, ptr(rows),
+         stream())
     outs = []
-    for mode in ("fused", "separate"):
+    for mode in ("fused", "fused-rows", "separate"):
         kc, vc = kp0.to(gpu), vp0.to(gpu)
         out = torch.empty(n, nh, hd, device=gpu, dtype=torch.float16)
         ws = torch.empty(n * nkv * splits * 6 * 132, device=gpu, dtype=torch.float32)
-        if mode == "fused":
+        if mode.startswith("fused"):
             call("omni_decode_attention_fused", ptr(parts), S, ptr(bias), bias_after_round,
                  ptr(cos), ptr(sin), 8192, ptr(delta), 16, 24, 24, ptr(kc), ptr(vc), P, ML, None,
-                 ptr(lens), ptr(out), n, nh, nkv, hd, hd ** -0.5, 8, splits, ptr(ws), 1, stream())
+                 ptr(lens), ptr(out), n, nh, nkv, hd, hd ** -0.5, 8, splits, ptr(ws), 1,
+                 ptr(rows) if mode == "fused-rows" else None, stream())
         else:
             qkv = torch.empty(n, W, device=gpu, dtype=torch.float16)
             call("omni_mrope_kv_write_partials", ptr(qkv), W, ptr(parts), S, ptr(bias),
@@ -496,8 +513,9 @@ def test_decode_attention_fused_equals_unfused(gpu, bias_after_round, splits, le
                  1, 1, ptr(out), n, nh, nkv, hd, hd ** -0.5, 8, splits, ptr(ws), stream())
         torch.cuda.synchronize()
         outs.append((out.cpu(), kc.cpu(), vc.cpu()))
-    for a, b in zip(outs[0], outs[1]):
-        assert torch.equal(a, b)
+    for other in outs[1:]:
+        for a, b in zip(outs[0], other):
+            assert torch.equal(a, b)
 
 
 @pytest.mark.parametrize("fmt,splits", [("int4", 4), ("int4", 1), ("fp16", 3), ("int4", 11)])
@@ -538,7 +556,7 @@ def test_oproj_merges_attention_states(gpu, fmt, splits):
         call("omni_decode_attention_fused", ptr(parts), 6, ptr(bias), 1, ptr(cos), ptr(sin), 8192,
              ptr(delta), 16, 24, 24, ptr(kc), ptr(vc), P, ML, None, ptr(lens),
              ptr(out) if merge else None, n, nh, nkv, hd, hd ** -0.5, 8, splits, ptr(ws), merge,
-             stream())
+             None, stream())
     attn(0)
     lin.forward_partial_attn(ws, splits, nkv, nh // nkv, n, pa)
     attn(1)                       # same K/V row rewritten with the same values

@@ -108,6 +108,17 @@ int omni_mrope_kv_write_partials(void* qkv, int qkv_stride, const float* partial
                                  int n_heads, int n_kv_heads, int head_dim, int sec0, int sec1,
                                  int sec2, void* stream);
 
+/* ---------------------------------------------------------------- KV-pool slots */
+
+/* PreallocatedKVCache.move_slot / copy_slot_kv (cache/kv_prealloc.py:51-57, 79-84): tokens
+ * [0, length) of pool row src copied to row dst in every layer's K and V in one launch,
+ * lengths[dst] = that length.  length < 0: lengths[src], read on the device (no host
+ * synchronisation; only the valid prefix is copied).  pool fp16 [n_layers][2][pool_rows]
+ * [max_len][row_halfs] (row_halfs = n_kv * head_dim, a multiple of 8); lengths int64
+ * [pool_rows], may be NULL when length >= 0. */
+int omni_kv_copy_slot(void* pool, int n_layers, int pool_rows, int max_len, int row_halfs,
+                      int src, int dst, int64_t length, int64_t* lengths, void* stream);
+
 /* ---------------------------------------------------------------- attention */
 
 /* _CacheView.flash_decode (cache/kv_prealloc.py:272-290): GQA decode attention over the

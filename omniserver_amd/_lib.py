@@ -30,6 +30,7 @@ SIGNATURES = {
     "omni_embed_rmsnorm_rope": [_P, _P, _I, _I64, _P, _P, _P, _I, _I, _F, _P, _P, _P, _P, _I,
                                 _P, _P],
     "omni_rope_rows": [_P, _P, _P, _P, _P, _I, _I, _I, _P, _P],
+    "omni_kv_copy_slot": [_P, _I, _I, _I, _I, _I, _I, _I64, _P, _P],
     "omni_embedding": [_P, _P, _I, _I64, _P, _I, _I, _P],
     "omni_silu_mul": [_P, _P, _I, _I, _P],
     "omni_mrope_kv_write": [_P, _I, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I,

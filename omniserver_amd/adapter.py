@@ -5,11 +5,13 @@ by ``Qwen2VLAdapter`` (models/qwen2_vl.py:30-122) for the text decoder:
 embed_tokens (:93-94), prefill_positions (:100-106), decode_positions (:108-112),
 llm (:115-116), plus the shape attributes the KV pool needs.
 
-Weights: there are no checkpoints offline, so ``model_dir=None`` builds seeded
-synthetic weights of the real architecture (``synth``); ``weights=`` accepts an
-already generated dict (fp16 or GPTQ layout).  ``quant="gptq"`` selects the int4
-path (every decoder linear W4A16, embeddings / lm_head fp16, as
-kernels/marlin_linear.py:114-143).
+Weights (models/qwen2_vl.py:31-61): ``quant="gptq"`` with ``gptq_dir`` reads the
+AutoGPTQ checkpoint's decoder tensors, ``quant=None`` with ``model_dir`` the fp16
+Hugging Face checkpoint's (``checkpoint``); without a directory (the reference would
+look in its default cache paths, which do not exist offline) seeded synthetic weights
+of the real architecture are built (``synth``); ``weights=`` accepts an already built
+dict (fp16 or GPTQ layout).  ``quant="gptq"`` selects the int4 path (every decoder
+linear W4A16, embeddings / lm_head fp16, as kernels/marlin_linear.py:114-143).
 """
 
 from __future__ import annotations
@@ -32,14 +34,23 @@ class Qwen2VLAdapter:
                  num_layers: Optional[int] = None, device="cuda", max_pos: int = 8192):
         if quant not in (None, "gptq"):
             raise ValueError(f"unsupported quant {quant!r} (None or 'gptq')")
-        if model_dir is not None or gptq_dir is not None:
-            raise NotImplementedError("checkpoint loading is not part of this build; "
-                                      "pass weights= or use synthetic weights")
         self.device = torch.device(device)
         self.shape = shape or synth.DecoderShape()
         if num_layers is not None:
             self.shape.num_layers = num_layers
         self.quant = quant
+        src = gptq_dir if quant == "gptq" else model_dir
+        if weights is None and src is not None:
+            from . import checkpoint
+            sd = checkpoint.read_safetensors(src)
+            weights = (checkpoint.gptq_decoder_from_state_dict(sd) if quant == "gptq"
+                       else checkpoint.fp16_decoder_from_state_dict(sd))
+            del sd
+            if weights["embed"].shape[1] != self.shape.hidden_size:
+                raise ValueError(f"checkpoint hidden size {weights['embed'].shape[1]} is not the "
+                                 f"Qwen2-VL-2B decoder's {self.shape.hidden_size}")
+            self.shape.num_layers = len(weights["layers"])
+            self.shape.vocab_size = weights["embed"].shape[0]
         if weights is None:
             gen = synth.gptq_decoder if quant == "gptq" else synth.fp16_decoder
             weights = gen(self.shape, seed=seed)

@@ -14,8 +14,9 @@ Mirrors omniserve/cache/kv_prealloc.py:
   and its query i attends to keys ``[0, start+i]`` (cached prefix + the segment, causal);
   ``lengths[slot] = start + new_len``.  A decode token is a segment of one.
 
-Attention and the K/V writes run on the HIP kernels (omni_decode_attention,
-omni_mrope_kv_write, omni_prefill_attention); slot bookkeeping stays torch copies.
+Attention, the K/V writes and the slot copies run on the HIP kernels
+(omni_decode_attention, omni_mrope_kv_write, omni_prefill_attention, omni_kv_copy_slot);
+snapshots for prefix reuse are torch clones.
 """
 
 from __future__ import annotations
@@ -75,11 +76,16 @@ class PreallocatedKVCache:
         self.lengths[slot] = length
         self._active = max(self._active, slot + 1)
 
+    def _copy_slot(self, src: int, dst: int, length: int) -> None:
+        call("omni_kv_copy_slot", ptr(self.storage), self.n_layers, self.max_batch, self.max_len,
+             self.n_kv_heads * self.head_dim, int(src), int(dst), int(length), ptr(self.lengths),
+             stream())
+
     def move_slot(self, src: int, dst: int) -> None:
-        """Move a sequence's KV from slot src to dst (pool compaction on free).  Copies the
-        whole row in one strided copy across all layers and K/V."""
-        self.storage[:, :, dst].copy_(self.storage[:, :, src])
-        self.lengths[dst] = self.lengths[src]
+        """Move a sequence's KV from slot src to dst (pool compaction on free): one launch
+        over every layer's K and V copying the valid prefix, lengths[src] read on the
+        device (no host synchronisation)."""
+        self._copy_slot(src, dst, -1)
 
     def snapshot_slot(self, slot: int, length: int):
         ks = [self.k[li][slot, :length].clone() for li in range(self.n_layers)]
@@ -95,8 +101,9 @@ class PreallocatedKVCache:
         self._active = max(self._active, slot + 1)
 
     def copy_slot_kv(self, src: int, dst: int, length: int) -> None:
-        self.storage[:, :, dst, :length].copy_(self.storage[:, :, src, :length])
-        self.lengths[dst] = length
+        if not 0 <= length <= self.max_len:
+            raise ValueError(f"length {length} outside [0, {self.max_len}]")
+        self._copy_slot(src, dst, length)
         self._active = max(self._active, dst + 1)
 
     # ---- views ---------------------------------------------------------------------

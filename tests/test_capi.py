@@ -75,6 +75,11 @@ def test_bad_arguments_rejected_before_launch(so):
                                          24, fake_ptr(), fake_ptr(), 4, 64, None, fake_ptr(),
                                          fake_ptr(), 2, 12, 2, 128, 0.1, 8, 4, fake_ptr(), 1,
                                          None, None) == -1
+    # slot copy: row out of range, row width not whole 16-byte chunks, device length without
+    # a lengths array
+    assert L.omni_kv_copy_slot(fake_ptr(), 2, 4, 64, 256, 0, 4, 3, None, None) == -1
+    assert L.omni_kv_copy_slot(fake_ptr(), 2, 4, 64, 250, 0, 1, 3, None, None) == -2
+    assert L.omni_kv_copy_slot(fake_ptr(), 2, 4, 64, 256, 0, 1, -1, None, None) == -1
     # GEMM: split-K partials past the skinny kernel's 64 rows, K not a multiple of 128,
     # split without partial epilogue; more rows with the STORE epilogue are the tiled GEMM
     # (here rejected for its null pointers, not its size)

@@ -565,6 +565,35 @@ def test_oproj_merges_attention_states(gpu, fmt, splits):
     assert torch.equal(pa, pb)
 
 
+@pytest.mark.parametrize("length", [-1, 0, 1, 63, 64, 65, 300, 512])
+def test_kv_copy_slot(gpu, length):
+    """move_slot / copy_slot_kv (kv_prealloc.py:51-57, 79-84): tokens [0, L) of row src copied
+    to row dst in every layer's K and V, bit-exact, nothing else written; lengths[dst] = L
+    (length -1: L = lengths[src] read on the device)."""
+    from omniserver_amd.kv_cache import PreallocatedKVCache
+    say(f"kv slot copy length={length}")
+    pool = PreallocatedKVCache(3, 5, 2, 512, 128, gpu, n_heads=12)
+    g = torch.Generator().manual_seed(150)
+    before = torch.randn(pool.storage.shape, generator=g).half()
+    pool.storage.copy_(before)
+    pool.lengths.copy_(torch.tensor([10, 300, 7, 0, 512]))
+    src, dst = 1, 3
+    if length < 0:
+        pool.move_slot(src, dst)
+        L = 300
+    else:
+        pool.copy_slot_kv(src, dst, length)
+        L = length
+    torch.cuda.synchronize()
+    exp = before.clone()
+    exp[:, :, dst, :L] = before[:, :, src, :L]
+    assert torch.equal(pool.storage.cpu(), exp)
+    assert pool.lengths.cpu().tolist() == [10, 300, 7, L, 512]
+    pool.copy_slot_kv(4, 4, 5)                      # same row: only the length changes
+    torch.cuda.synchronize()
+    assert torch.equal(pool.storage.cpu(), exp) and int(pool.lengths[4]) == 5
+
+
 # ----------------------------------------------------------------------------- fp8 W8A8
 def test_fp8_quant_rows_bit_exact(gpu):
     """quant_fp8 (fp8_linear.py:45-63): per-row amax/448 scale and e4m3 codes, bit-exact."""

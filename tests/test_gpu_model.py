@@ -347,6 +347,34 @@ def test_runner_chunked_prompt_matches_oracle(gpu, mode):
             assert g == e, f"seq {i} token {j}: got {g} want {e} (margin {m:.3f})"
 
 
+def test_runner_from_gptq_checkpoint(gpu, tmp_path):
+    """NativeQwenVLRunner(quant="gptq", gptq_dir=...) reads an AutoGPTQ safetensors
+    checkpoint (marlin_linear.py:114-143) and decodes exactly as the same weights given in
+    memory."""
+    from safetensors.torch import save_file
+    from omniserver_amd import checkpoint, synth
+    from omniserver_amd.request import Request, SamplingParams, Sequence
+    from omniserver_amd.runner import NativeQwenVLRunner
+    say("runner from a GPTQ checkpoint file (2 layers, vocab 4096)")
+    shape = synth.DecoderShape(vocab_size=4096)
+    w = synth.gptq_decoder(shape, seed=13, num_layers=2)
+    save_file(checkpoint.gptq_state_dict_from_decoder(w), str(tmp_path / "model.safetensors"))
+    prompts = [synth.random_ids(L, 4096, 13, f"c{L}").tolist() for L in (11, 26)]
+    streams = []
+    for kw in (dict(gptq_dir=str(tmp_path)), dict(weights=w, shape=shape)):
+        r = NativeQwenVLRunner(max_running=2, max_len=128, use_graph=True, quant="gptq", **kw)
+        assert r.adapter.num_layers == 2 and r.adapter.model.cfg.vocab_size == 4096
+        seqs = [Sequence(Request(prompt=p, sampling=SamplingParams(max_new_tokens=8)))
+                for p in prompts]
+        for s_ in seqs:
+            r.tokenize(s_)
+        r.prefill(seqs)
+        for _ in range(4):
+            r.decode(seqs)
+        streams.append([s_.output_token_ids for s_ in seqs])
+    assert streams[0] == streams[1]
+
+
 @pytest.mark.slow
 def test_full_depth_decode_fp16(gpu):
     """All 28 layers at the real width: one decode step, B=2, contexts 300 and 400.

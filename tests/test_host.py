@@ -159,6 +159,64 @@ def test_append_writer_metadata():
     assert packed.token_pos.tolist() == [0, 1, 2, 0, 1] and packed.kv_len.tolist() == [1, 2, 3, 1, 2]
 
 
+def _hf_fp16_state_dict(w, prefix="model."):
+    """fp16 weight dict -> Hugging Face Qwen2-VL key names (q/k/v, gate/up split)."""
+    nq, nkv = 12 * 128, 2 * 128
+    sd = {prefix + "embed_tokens.weight": w["embed"], prefix + "norm.weight": w["norm"]}
+    for i, l in enumerate(w["layers"]):
+        lp = f"{prefix}layers.{i}."
+        sd[lp + "input_layernorm.weight"] = l["in_norm"]
+        sd[lp + "post_attention_layernorm.weight"] = l["post_norm"]
+        for x, (a, b) in {"q": (0, nq), "k": (nq, nq + nkv), "v": (nq + nkv, nq + 2 * nkv)}.items():
+            sd[lp + f"self_attn.{x}_proj.weight"] = l["qkv_w"][a:b].contiguous()
+            sd[lp + f"self_attn.{x}_proj.bias"] = l["qkv_b"][a:b].contiguous()
+        sd[lp + "self_attn.o_proj.weight"] = l["o_w"]
+        I = l["gate_up_w"].shape[0] // 2
+        sd[lp + "mlp.gate_proj.weight"] = l["gate_up_w"][:I].contiguous()
+        sd[lp + "mlp.up_proj.weight"] = l["gate_up_w"][I:].contiguous()
+        sd[lp + "mlp.down_proj.weight"] = l["down_w"]
+    return sd
+
+
+def test_checkpoint_ingest(tmp_path):
+    """GPTQ and fp16 checkpoint ingest (marlin_linear.py:114-143, qwen2_llm.py:193-219): the
+    AutoGPTQ / Hugging Face tensors written to safetensors come back as the same fused
+    weight dicts; a missing tensor and an activation-order g_idx are rejected; qzeros and a
+    trivial g_idx are accepted; both state-dict prefixes load."""
+    from safetensors.torch import save_file
+    from omniserver_amd import checkpoint, synth
+    shape = synth.DecoderShape(vocab_size=512)
+    w = synth.gptq_decoder(shape, seed=3, num_layers=2)
+    sd = checkpoint.gptq_state_dict_from_decoder(w)
+    K = 1536
+    sd["model.layers.0.self_attn.q_proj.g_idx"] = torch.arange(K, dtype=torch.int32) // 128
+    sd["model.layers.0.self_attn.q_proj.qzeros"] = torch.full((K // 128, 192), 0x77777777,
+                                                              dtype=torch.int64).to(torch.int32)
+    sd["visual.blocks.0.attn.qkv.weight"] = torch.zeros(4, 4, dtype=torch.float16)   # ignored
+    save_file(sd, str(tmp_path / "model-00001-of-00001.safetensors"))
+    w2 = checkpoint.gptq_decoder_from_state_dict(checkpoint.read_safetensors(str(tmp_path)))
+    assert torch.equal(w2["embed"], w["embed"]) and torch.equal(w2["norm"], w["norm"])
+    for a, b in zip(w["layers"], w2["layers"]):
+        assert a.keys() == b.keys()
+        for k in a:
+            assert a[k].dtype == b[k].dtype and torch.equal(a[k], b[k]), k
+    bad = dict(sd)
+    del bad["model.layers.1.mlp.down_proj.scales"]
+    with pytest.raises(KeyError, match="down_proj.scales"):
+        checkpoint.gptq_decoder_from_state_dict(bad)
+    bad = dict(sd)
+    bad["model.layers.0.self_attn.q_proj.g_idx"] = torch.randperm(K).to(torch.int32) // 128
+    with pytest.raises(ValueError, match="desc_act"):
+        checkpoint.gptq_decoder_from_state_dict(bad)
+    f = synth.fp16_decoder(shape, seed=4, num_layers=2)
+    for prefix in ("model.", "model.language_model."):
+        f2 = checkpoint.fp16_decoder_from_state_dict(_hf_fp16_state_dict(f, prefix))
+        assert torch.equal(f2["embed"], f["embed"])
+        for a, b in zip(f["layers"], f2["layers"]):
+            for k in a:
+                assert torch.equal(a[k], b[k]), (prefix, k)
+
+
 def test_decode_plan_and_split_counts():
     from omniserver_amd.kv_cache import MAX_ATTN_SPLITS, decode_plan
     for n in (1, 8, 16, 32, 64):

@@ -161,8 +161,9 @@ __device__ __forceinline__ void grouped_tile(int L, int tiles_m, int tiles_n, in
 
 // sum[e] += base[p * stride + e] for p = 0 .. n-1 in ascending order (e = 0..7, fp32 split-K
 // slices).  Loads go out in batches of BATCH before the first add of the batch, so n
-// slices cost ceil(n/BATCH) memory round trips, not n; a slot past n adds +0.0f (sum is
-// never -0.0f).
+// slices cost ceil(n/BATCH) memory round trips, not n.  The batch is branch-free: a slot
+// past n re-reads slice n - 1 and adds +0.0f (sum is never -0.0f) - a load behind a
+// branch leaves the compiler unsure what is outstanding, and it then waits per slice.
 template <int BATCH = 8>
 __device__ __forceinline__ void sum_slices8(const float* __restrict__ base, int64_t stride, int n,
                                             float sum[8]) {
@@ -171,13 +172,10 @@ __device__ __forceinline__ void sum_slices8(const float* __restrict__ base, int6
     float4 lo[BATCH], hi[BATCH];
 #pragma unroll
     for (int u = 0; u < BATCH; ++u) {
-      if (b + u < n) {          // uniform: no load is issued for a missing slice
-        const float4* pp = (const float4*)(base + (int64_t)(b + u) * stride);
-        lo[u] = pp[0];
-        hi[u] = pp[1];
-      } else {
-        lo[u] = hi[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-      }
+      const int p = b + u < n ? b + u : n - 1;
+      const float4* pp = (const float4*)(base + (int64_t)p * stride);
+      lo[u] = pp[0];
+      hi[u] = pp[1];
     }
 #pragma unroll
     for (int u = 0; u < BATCH; ++u) {

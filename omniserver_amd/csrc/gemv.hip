@@ -127,6 +127,13 @@ __global__ __launch_bounds__(CW * KW * 64) void gemv_kernel(GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   half_t* xs = (half_t*)smem;
 
+  // Every kernel argument is read into registers in one batch first: scalar loads complete
+  // out of order, so a wait for any one of them waits for all, and an argument fetched
+  // after the first wait costs the launch another round trip before its loads go out.
+  asm volatile("" ::"s"(a.x), "s"(a.ldx), "s"(a.w), "s"(a.scales), "s"(a.bias),
+               "s"(a.bias_after_round), "s"(a.out), "s"(a.ldo), "s"(a.partial), "s"(a.M),
+               "s"(a.N), "s"(a.K), "s"(a.KS), "s"(a.KC), "s"(a.xl), "s"(a.apart), "s"(a.aS),
+               "s"(a.a_nkv), "s"(a.aG), "s"(gridDim.x));
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int cw = wave % CW;
@@ -173,9 +180,13 @@ __global__ __launch_bounds__(CW * KW * 64) void gemv_kernel(GemvArgs a) {
 
   // 1. The first batch of x loads goes out before the weight loads: x is small and
   //    cache-resident, and loads retire in issue order, so staging it never waits on
-  //    the weight stream.  The code is branch-free (clamped addresses, selects at the
-  //    store) so that the compiler's wait counts stay exact; a chunk past the slice is
-  //    marked with the row-0 pad offset (KC) and not stored.
+  //    the weight stream.  The code is branch-free (clamped addresses) so that the
+  //    compiler's wait counts stay exact; a chunk past the slice is marked with the
+  //    row-0 pad offset (KC) and not stored.  Rows past M stage row 0's values, stored
+  //    as loaded: their products are never stored (every epilogue skips rows >= M, and an
+  //    MFMA row depends only on its own A row), and a select on the loaded value would
+  //    let the compiler consume - wait for - each x load right after issuing it, ahead
+  //    of the weight loads.
   half8_t xv[8];
   int xo[8];
   bool xlive[8];
@@ -255,7 +266,7 @@ __global__ __launch_bounds__(CW * KW * 64) void gemv_kernel(GemvArgs a) {
       // serialise on its LDS bank)
 #pragma unroll
       for (int u = 0; u < 8; ++u)
-        if (xo[u] != a.KC) *(half8_t*)(xs + xo[u]) = xlive[u] ? xv[u] : zero8;
+        if (xo[u] != a.KC) *(half8_t*)(xs + xo[u]) = xv[u];
       for (int base = threadIdx.x + 8 * NTH; base < xtotal; base += 8 * NTH) {
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
@@ -269,7 +280,7 @@ __global__ __launch_bounds__(CW * KW * 64) void gemv_kernel(GemvArgs a) {
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u)
-          if (xo[u] != a.KC) *(half8_t*)(xs + xo[u]) = xlive[u] ? xv[u] : zero8;
+          if (xo[u] != a.KC) *(half8_t*)(xs + xo[u]) = xv[u];
       }
     }
   };
@@ -834,6 +845,9 @@ static int num_cus_gemv() {
 template <int MB>
 __global__ __launch_bounds__(512, 1) void lmhead_kernel(GemvArgs a) {
 #pragma clang fp contract(off)
+  // all arguments in one batch of scalar loads (a wait for one is a wait for all)
+  asm volatile("" ::"s"(a.x), "s"(a.ldx), "s"(a.w), "s"(a.M), "s"(a.N), "s"(a.K),
+               "s"(a.cand_val), "s"(a.cand_idx), "s"(gridDim.x));
   extern __shared__ __attribute__((aligned(16))) char smem[];
   half_t* xs = (half_t*)smem;                  // [MB * 16][K + 8]
   const int lane = threadIdx.x & 63;

@@ -55,6 +55,11 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(
     const half_t* __restrict__ rr_cos = nullptr, const half_t* __restrict__ rr_sin = nullptr,
     int rr_max = 0, half_t* __restrict__ rope_rows = nullptr) {
 #pragma clang fp contract(off)
+  // all arguments in one batch of scalar loads (a wait for one is a wait for all)
+  asm volatile("" ::"s"(x), "s"(residual), "s"(ids), "s"(table), "s"(table_packed), "s"(vocab),
+               "s"(w), "s"(y), "s"(y8), "s"(scale_out), "s"(res_out), "s"(rows), "s"(H), "s"(eps),
+               "s"(parts), "s"(nparts), "s"(rr_len), "s"(rr_delta), "s"(rr_cos), "s"(rr_sin),
+               "s"(rr_max), "s"(rope_rows));
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
@@ -151,12 +156,17 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(
 // (H/8 threads, rounded up to whole waves), so every load of the row - including all
 // split-K partials - is in flight at once.  x is fp16, or (PARTS) the fp32 partial sums
 // [nparts][rows][H] added in slice order and rounded to fp16.
-template <bool PARTS>
-__global__ __launch_bounds__(1024) void rownorm_kernel(const half_t* x, const float* __restrict__ parts,
+// MAXT: the workgroup size bound (256 covers H <= 2048 and leaves the registers for a
+// whole batch of 16 partial slices in flight; 1024 covers the largest H).
+template <bool PARTS, int MAXT>
+__global__ __launch_bounds__(MAXT) void rownorm_kernel(const half_t* x, const float* __restrict__ parts,
                                                        int nparts, const half_t* residual,
                                                        const half_t* __restrict__ w, half_t* y,
                                                        half_t* res_out, int rows, int H, float eps) {
 #pragma clang fp contract(off)
+  // all arguments in one batch of scalar loads (a wait for one is a wait for all)
+  asm volatile("" ::"s"(x), "s"(parts), "s"(nparts), "s"(residual), "s"(w), "s"(y), "s"(res_out),
+               "s"(rows), "s"(H), "s"(eps));
   __shared__ float wsum[16];
   const int row = blockIdx.x;
   const int c = threadIdx.x;
@@ -223,7 +233,8 @@ extern "C" int omni_add_rmsnorm(const void* x, const void* residual, const void*
   if (!x || !residual || !weight || !y || !residual_out) return OMNI_EINVAL;
   if (rows <= 256) {
     const int threads = ceil_div(hidden >> 3, 64) * 64;
-    hipLaunchKernelGGL(rownorm_kernel<false>, dim3(rows), dim3(threads), 0, (hipStream_t)stream,
+    auto kern = threads <= 256 ? rownorm_kernel<false, 256> : rownorm_kernel<false, 1024>;
+    hipLaunchKernelGGL(kern, dim3(rows), dim3(threads), 0, (hipStream_t)stream,
                        (const half_t*)x, nullptr, 0, (const half_t*)residual,
                        (const half_t*)weight, (half_t*)y, (half_t*)residual_out, rows, hidden, eps);
   } else {
@@ -244,7 +255,8 @@ extern "C" int omni_add_rmsnorm_partials(const float* partials, int nparts, cons
   if (rows == 0) return OMNI_OK;
   if (!partials || nparts <= 0 || !residual || !weight || !y || !residual_out) return OMNI_EINVAL;
   const int threads = ceil_div(hidden >> 3, 64) * 64;
-  hipLaunchKernelGGL(rownorm_kernel<true>, dim3(rows), dim3(threads), 0, (hipStream_t)stream,
+  auto kern = threads <= 256 ? rownorm_kernel<true, 256> : rownorm_kernel<true, 1024>;
+  hipLaunchKernelGGL(kern, dim3(rows), dim3(threads), 0, (hipStream_t)stream,
                      nullptr, partials, nparts, (const half_t*)residual, (const half_t*)weight,
                      (half_t*)y, (half_t*)residual_out, rows, hidden, eps);
   OMNI_CHECK_LAUNCH();

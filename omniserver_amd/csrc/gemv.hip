@@ -119,7 +119,7 @@ __device__ __forceinline__ half_t finish_store(float v, const GemvArgs& a, int n
 // workgroups stage a large x, so that x does not queue behind the grid's weight stream);
 // XF = 0: the weight stream is issued first and staging overlaps it.
 template <int WF, int MB, int EPI, int CPW, int CW, int KW, int PF, int XS = 0, int XF = 0>
-__global__ __launch_bounds__(CW * KW * 64) void gemv_kernel(GemvArgs a) {
+__global__ __launch_bounds__(CW * KW * 64, 1) void gemv_kernel(GemvArgs a) {
 #pragma clang fp contract(off)
   static_assert(EPI != EPI_ARGMAX || KW == 1, "argmax epilogue uses every wave of the workgroup");
   constexpr int NW = CW * KW;

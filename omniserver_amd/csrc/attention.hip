@@ -127,6 +127,18 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
   //    bias, then the context length and rope delta of this token's pool row.  Optional
   //    operands are read through a valid stand-in address and replaced by zero, so no
   //    load sits behind a branch.
+  // The context length first, as scalar loads: they are counted apart from the vector
+  // loads below, so the first K/V block can go out once the length is in, without waiting
+  // for the partials.
+  // (Read through the constant address space: this launch never writes them, and the
+  // compiler would otherwise use vector loads, as the kernel stores to global memory.)
+  typedef __attribute__((address_space(4))) const int64_t c_i64;
+  const int64_t slot = a.slots ? ((const c_i64*)a.slots)[t] : t;
+  const bool slot_ok = slot >= 0 && slot < a.pool_rows;
+  const int64_t srow = slot_ok ? slot : 0;
+  const int64_t kv_raw = ((const c_i64*)a.kv_len)[a.kv_by_slot ? srow : t];
+  const int64_t* dptr = a.rope_delta ? a.rope_delta : a.kv_len;
+  const int64_t delta_raw = FUSED == 1 ? ((const c_i64*)dptr)[srow] : 0;
   constexpr int PI = ((ATT_FUSED_MAXG + 2) * ATT_HD / 2 + NT - 1) / NT;
   float2 pv[PI][8];
   half2_t bias2[PI];
@@ -164,16 +176,6 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
   half8_t csv = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
   if constexpr (FUSED == 2)
     csv = *(const half8_t*)(a.rope_rows + (int64_t)t * ATT_HD + (threadIdx.x & 15) * 8);
-  // The context length and rope delta are requested after the partials (the barrier keeps
-  // the compiler from hoisting them, and the arithmetic on them, above those loads): the
-  // partials then go out at once instead of a round trip later.
-  asm volatile("" ::: "memory");
-  const int64_t slot = a.slots ? a.slots[t] : t;
-  const bool slot_ok = slot >= 0 && slot < a.pool_rows;
-  const int64_t srow = slot_ok ? slot : 0;
-  const int64_t kv_raw = a.kv_len[a.kv_by_slot ? srow : t];
-  const int64_t* dptr = a.rope_delta ? a.rope_delta : a.kv_len;
-  const int64_t delta_raw = FUSED == 1 ? dptr[srow] : 0;
 
   // 2. Context length, this workgroup's key range, the rotary row.
   const int64_t L_raw = slot_ok ? kv_raw + a.kv_add : 0;
@@ -235,13 +237,14 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
     load_block(kf1, vr1, beg + ATT_BLK);
   };
   // Without the fused prologue the stream starts at once.  With it, the first block goes
-  // out once the prologue's loads have returned (a load issued after the grid's K/V
-  // requests waits for nearly all of them) and the second once q is in registers: a wave
-  // issuing K/V loads stalls in issue while the CU has many requests outstanding, so
-  // prologue work placed after both blocks - even LDS-only work behind a barrier - would
-  // wait for most of the stream, while one block in flight during the rotary step keeps
-  // the stream going without holding that step back.
+  // out as soon as the context length is in (after the prologue's own loads, which a load
+  // issued behind the grid's K/V requests would wait for) and the second once q is in
+  // registers: a wave issuing K/V loads stalls in issue while the CU has many requests
+  // outstanding, so prologue work placed after both blocks - even LDS-only work behind a
+  // barrier - would wait for most of the stream, while one block in flight during the
+  // rotary step keeps the stream going without holding that step back.
   if (!fused) issue_first_blocks();
+  if (fused) load_block(kf0, vr0, beg);
 
   if (fused) {
     // 4. Partial sums (slice order, as the unfused path) + bias -> fp16 rows in LDS.
@@ -269,7 +272,6 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
         raw[2 * i + 1] = h1;
       }
     }
-    load_block(kf0, vr0, beg);
     if (threadIdx.x < 16) *(half8_t*)(&cs_lds[threadIdx.x >> 3][(threadIdx.x & 7) * 8]) = csv;
     lds_barrier();
     // 5. M-RoPE (decode: one position on all three axes) in fp16 ops, one rounding

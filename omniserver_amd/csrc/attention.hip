@@ -203,7 +203,7 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
     csv = *(const half8_t*)(tab + pos * (ATT_HD / 2) + (threadIdx.x & 7) * 8);
   }
 
-  // 3. The first two K/V blocks of this wave (issued below).
+  // 3. The K/V blocks of this wave (the first is issued below).
   const int64_t row_base = (slot_ok ? slot : 0) * (int64_t)a.max_len;
   const int tok_hi = end > 0 ? end - 1 : 0;    // loads past the range re-read this row
   const half_t* kbase = a.k_cache + g * ATT_HD;
@@ -228,23 +228,18 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
       vr[r] = __builtin_nontemporal_load((const half8_t*)(vbase + (row_base + tok) * tok_stride + (c & 15) * 8));
     }
   };
-  half8_t kf0[2][4], vr0[8], kf1[2][4], vr1[8];
-  // Both first blocks are loaded unconditionally (a wave with fewer re-reads its last row,
-  // from cache): with branches around them the compiler drains the first block's loads
-  // before issuing the second's.
-  auto issue_first_blocks = [&]() {
-    load_block(kf0, vr0, beg);
-    load_block(kf1, vr1, beg + ATT_BLK);
-  };
-  // Without the fused prologue the stream starts at once.  With it, the first block goes
-  // out as soon as the context length is in (after the prologue's own loads, which a load
-  // issued behind the grid's K/V requests would wait for) and the second once q is in
-  // registers: a wave issuing K/V loads stalls in issue while the CU has many requests
-  // outstanding, so prologue work placed after both blocks - even LDS-only work behind a
-  // barrier - would wait for most of the stream, while one block in flight during the
-  // rotary step keeps the stream going without holding that step back.
-  if (!fused) issue_first_blocks();
-  if (fused) load_block(kf0, vr0, beg);
+  // One 32-token block (16 KB of K and V) in flight per wave: the next block is requested
+  // once the current one's K and V have been consumed (V staged in LDS, scores done).
+  // Measured on a plain 67 MB stream, 8 waves per CU each keeping 8 / 16 / 32 KB in flight
+  // take 11.9 / 13.0 / 15.7 us: more requests outstanding per CU only lengthen the queues.
+  // The first block goes out as soon as the context length is in (after the prologue's own
+  // loads, which a load issued behind the grid's K/V requests would wait for); the wave's
+  // issue of it stalls while the CU has many requests outstanding, so nothing of the
+  // prologue waits behind a second block.  (A wave without blocks re-reads its clamped
+  // last row, from cache: with a branch around the load the compiler's wait counts would
+  // no longer be exact.)
+  half8_t kf0[2][4], vr0[8];
+  load_block(kf0, vr0, beg);
 
   if (fused) {
     // 4. Partial sums (slice order, as the unfused path) + bias -> fp16 rows in LDS.
@@ -320,7 +315,6 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
       qf[ks] = v;
     }
   }
-  if (fused) load_block(kf1, vr1, beg + ATT_BLK);
 
   float m_run = -INFINITY;   // per head c16 (identical across q16 groups)
   float l_run = 0.f;         // lane-partial sum, reduced at the end
@@ -329,7 +323,7 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
   for (int i = 0; i < 8; ++i) o_acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
   // One 32-token block: its K/V sit in (kf, vr); once they are consumed the same
-  // registers are refilled with the block two ahead.
+  // registers are refilled with the next block.
   auto process = [&](half8_t (&kf)[2][4], half8_t (&vr)[8], int tb) {
     // The new token's K/V come from the prologue, not from the pool row being written.
     // Rows past the range were loaded from row end - 1 (= newtok in the last range), so
@@ -362,7 +356,7 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
       for (int ks = 0; ks < 4; ++ks) acc = mfma16x16x32(kf[j][ks], qf[ks], acc);
       sacc[j] = acc;
     }
-    if (tb + 2 * ATT_BLK < end) load_block(kf, vr, tb + 2 * ATT_BLK);   // refill
+    if (tb + ATT_BLK < end) load_block(kf, vr, tb + ATT_BLK);   // the next block
 
     float sc[8];
     float mblk = -INFINITY;
@@ -409,10 +403,7 @@ __global__ __launch_bounds__(NWA * 64, NWA <= 8 ? 8 / NWA : 1) void decode_attn_
     __builtin_amdgcn_wave_barrier();
   };
 
-  for (int tb = beg; tb < end; tb += 2 * ATT_BLK) {
-    process(kf0, vr0, tb);
-    if (tb + ATT_BLK < end) process(kf1, vr1, tb + ATT_BLK);
-  }
+  for (int tb = beg; tb < end; tb += ATT_BLK) process(kf0, vr0, tb);
 
   l_run += __shfl_xor(l_run, 16, 64);
   l_run += __shfl_xor(l_run, 32, 64);

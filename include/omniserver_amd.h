@@ -220,6 +220,42 @@ int omni_f16_pack(const void* weight, void* weight_packed, int K, int N, int int
 int omni_w4_dequant(const int32_t* qweight_packed, const void* scales_packed, void* w, int K,
                     int N, void* stream);
 
+/* ---------------------------------------------------------------- vision tower */
+
+/* Epilogues of omni_f16_gemm_tiled beyond OMNI_EPI_STORE (h = fp16(x . W^T + bias)). */
+#define OMNI_EPI_QGELU 4   /* quick_gelu(h) = h * sigmoid(1.702 h), three fp16 roundings */
+#define OMNI_EPI_GELU 5    /* exact (erf) GELU of h */
+#define OMNI_EPI_RESID 6   /* fp16(res + h); res may alias out */
+
+/* The vision tower's nn.Linear layers at any M (model/qwen2_vit.py:41-44, 83, 88-89, and
+ * their use at :55, 64, 68, 121, 128): tiled MFMA GEMM over weights from omni_f16_pack with
+ * K a multiple of 128 (zero-padded past kx); x fp16 [M, kx] (row stride ldx, kx % 8 == 0);
+ * bias optional. */
+int omni_f16_gemm_tiled(const void* x, int ldx, int kx, const void* weight_packed,
+                        const void* bias, const void* res, int ldr, void* out, int ldo, int M,
+                        int N, int K, int epilogue, void* stream);
+
+/* nn.LayerNorm(N, eps) of M fp16 rows (model/qwen2_vit.py:39-40, 87): fp32 mean and biased
+ * variance, y = (x - mean) rsqrt(var + eps) w + b.  N % 8 == 0, N <= 2048; out may alias x. */
+int omni_layernorm(const void* x, int ldx, const void* weight, const void* bias, int M, int N,
+                   float eps, void* out, int ldo, void* stream);
+
+/* vision_rope (kernels/vision_rope.py:39-47, with the angles of model/qwen2_vit.py:96-116):
+ * in place on q heads [0, n_heads) and k heads [n_heads, 2 n_heads) of S qkv rows (row
+ * stride ld, head_dim % 16 == 0).  pos_hw int32 [S][2] patch (h, w); inv_freq fp32
+ * [head_dim / 4]; pair (d, d + head_dim/2) turns by pos_h inv_freq[d] (d < head_dim/4) or
+ * pos_w inv_freq[d - head_dim/4], fp32 math, fp16 out. */
+int omni_vision_rope(void* qkv, int ld, int S, int n_heads, int head_dim, const int* pos_hw,
+                     const float* inv_freq, void* stream);
+
+/* VisionBlock.attn's flash_attn_varlen_func(causal=False) (model/qwen2_vit.py:58-63):
+ * softmax(q k^T scale) v within each segment [cu[s], cu[s+1]) of the rotated qkv rows
+ * (q | k | v heads, head_dim 80).  tiles int32 [ntiles][2] = (first query, segment) in
+ * steps of 64 queries; out fp16 [S][ldo], head h at column 80 h. */
+int omni_vit_attention(const void* qkv, int ld, int S, int n_heads, int head_dim,
+                       const int* cu_seqlens, const int* tiles, int ntiles, void* out, int ldo,
+                       float scale, void* stream);
+
 /* ---------------------------------------------------------------- fp8 (W8A8) */
 
 /* Row-wise e4m3fn quantisation: scale[r] = amax_k |x[r, k]| / 448 (max(., clamp_min) when

@@ -37,7 +37,8 @@
 #include <type_traits>
 
 enum { W_INT4 = 0, W_FP16 = 1 };
-enum { EPI_STORE = 0, EPI_SILU = 1, EPI_PARTIAL = 2, EPI_ARGMAX = 3 };
+enum { EPI_STORE = 0, EPI_SILU = 1, EPI_PARTIAL = 2, EPI_ARGMAX = 3, EPI_QGELU = 4, EPI_GELU = 5,
+       EPI_RESID = 6 };
 
 struct GemvArgs {
   const half_t* x;
@@ -59,6 +60,10 @@ struct GemvArgs {
   // splits of the states [M][a_nkv][aS][aG][ATT_REC] of head h (kv head h / aG).
   const float* apart;
   int aS, a_nkv, aG;
+  // tiled kernel only: x columns [kx, K) read as zero (kx % 8 == 0); EPI_RESID adds res
+  int kx;
+  const half_t* res;
+  int ldr;
 };
 
 template <int WF>
@@ -103,6 +108,22 @@ struct WStream<W_FP16> {
 };
 
 __device__ __forceinline__ float silu_ref(float g) { return g * (1.0f / (1.0f + __expf(-g))); }
+
+// x * sigmoid(1.702 x) with the three fp16 roundings of the reference's elementwise ops
+// (model/qwen2_vit.py:18-19 on fp16 tensors: 1.702 x, sigmoid, product).
+__device__ __forceinline__ half_t quick_gelu_ref(half_t h) {
+#pragma clang fp contract(off)
+  const float t = (float)(half_t)((float)h * 1.702f);
+  const float sg = (float)(half_t)(1.0f / (1.0f + expf(-t)));
+  return (half_t)((float)h * sg);
+}
+
+// Exact (erf) GELU of an fp16 value, fp32 math, one rounding (F.gelu, model/qwen2_vit.py:128).
+__device__ __forceinline__ half_t gelu_erf_ref(half_t h) {
+#pragma clang fp contract(off)
+  const float x = (float)h;
+  return (half_t)(0.5f * x * (1.0f + erff(x * 0.70710678118654752f)));
+}
 
 __device__ __forceinline__ half_t finish_store(float v, const GemvArgs& a, int n) {
 #pragma clang fp contract(off)
@@ -580,21 +601,27 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(GemvArgs a) {
 
   // x staging: thread t moves 16-byte chunks t + 256 u (u < 8) of the 128 x 128 tile:
   // row (t + 256u) / 16, chunk t % 16.  Rows past M re-read row M - 1 (never stored).
+  // Columns past kx (a K padded to whole 128-groups) are loaded from column kx - 8, which
+  // is in bounds, and staged as zeros.
   const int xc = tid & 15;
   const half_t* xsrc[8];
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
     const int r = (tid >> 4) + 16 * u;
-    xsrc[u] = a.x + (int64_t)min(m0 + r, a.M - 1) * a.ldx + xc * 8;
+    xsrc[u] = a.x + (int64_t)min(m0 + r, a.M - 1) * a.ldx;
   }
   half8_t xr[8];
   auto load_x = [&](int g) {
+    const int col = min(g * 128 + xc * 8, a.kx - 8);
 #pragma unroll
-    for (int u = 0; u < 8; ++u) xr[u] = *(const half8_t*)(xsrc[u] + g * 128);
+    for (int u = 0; u < 8; ++u) xr[u] = *(const half8_t*)(xsrc[u] + col);
   };
-  auto store_x = [&](int b) {
+  auto store_x = [&](int b, int g) {
+    const bool live = g * 128 + xc * 8 < a.kx;
+    const half8_t z = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-    for (int u = 0; u < 8; ++u) *(half8_t*)(&xs[b][((tid >> 4) + 16 * u) * GT_XSTRIDE + xc * 8]) = xr[u];
+    for (int u = 0; u < 8; ++u)
+      *(half8_t*)(&xs[b][((tid >> 4) + 16 * u) * GT_XSTRIDE + xc * 8]) = live ? xr[u] : z;
   };
 
   WStream<WF> ws[4];
@@ -640,7 +667,7 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(GemvArgs a) {
   load_x(0);
   load_w(wb[0], 0);
   for (int g = 0; g < KG; g += 2) {
-    store_x(0);
+    store_x(0, g);
     __syncthreads();
     if (g + 1 < KG) {
       load_x(g + 1);
@@ -648,7 +675,7 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(GemvArgs a) {
     }
     compute(xs[0], wb[0]);
     if (g + 1 >= KG) break;
-    store_x(1);
+    store_x(1, g + 1);
     __syncthreads();
     if (g + 2 < KG) {
       load_x(g + 2);
@@ -679,7 +706,11 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(GemvArgs a) {
         for (int c = 0; c < 4; ++c) {
           if (nt0 + c >= NT) continue;
           const int n = (nt0 + c) * 16 + c16;
-          a.out[(int64_t)m * a.ldo + n] = finish_store(acc[i][c][r], a, n);
+          half_t h = finish_store(acc[i][c][r], a, n);
+          if constexpr (EPI == EPI_QGELU) h = quick_gelu_ref(h);
+          if constexpr (EPI == EPI_GELU) h = gelu_erf_ref(h);
+          if constexpr (EPI == EPI_RESID) h = (half_t)((float)a.res[(int64_t)m * a.ldr + n] + (float)h);
+          a.out[(int64_t)m * a.ldo + n] = h;
         }
       }
     }
@@ -741,6 +772,7 @@ static int gemv_common(int wf, const void* x, int ldx, const void* w, const void
   a.K = K;
   a.KC = ((KG + ksplit - 1) / ksplit) * 128;
   a.KS = (K + a.KC - 1) / a.KC;
+  a.kx = K;
   hipStream_t st = (hipStream_t)stream;
   if (M > 64) {   // many rows (prefill): the tiled kernel, STORE / SILU epilogues
     if (wf == W_INT4)
@@ -816,6 +848,50 @@ extern "C" int omni_f16_gemm(const void* x, int ldx, const void* weight_packed, 
                              int ksplit, int preset, void* stream) {
   return gemv_common(W_FP16, x, ldx, weight_packed, nullptr, bias, 0, out, ldo, partial, M, N, K,
                      epilogue, ksplit, preset, stream);
+}
+
+// Tiled fp16 GEMM at any M for the vision tower's linears (model/qwen2_vit.py:41-44, 83,
+// 88-89: nn.Linear in fp16, bias added before the single rounding):
+//   h = fp16(x[:, :kx] . W^T + bias), then per epilogue
+//   OMNI_EPI_STORE: h;  OMNI_EPI_QGELU: quick_gelu(h);  OMNI_EPI_GELU: gelu_erf(h);
+//   OMNI_EPI_RESID: fp16(res + h)  (res may alias out: each element is read, then written,
+//   by one thread).
+// W packed by omni_f16_pack with K a multiple of 128 (columns past kx zero-padded); x has
+// kx valid columns (kx % 8 == 0, row stride ldx).
+extern "C" int omni_f16_gemm_tiled(const void* x, int ldx, int kx, const void* weight_packed,
+                                   const void* bias, const void* res, int ldr, void* out,
+                                   int ldo, int M, int N, int K, int epilogue, void* stream) {
+  if (M < 0 || N <= 0 || K <= 0) return OMNI_EINVAL;
+  if (M == 0) return OMNI_OK;
+  if ((N & 15) || (K & 127)) return OMNI_EUNSUPPORTED;
+  if (kx <= 0 || kx > K || (kx & 7)) return OMNI_EINVAL;
+  if (!x || !weight_packed || !out) return OMNI_EINVAL;
+  if (ldx < kx || (ldx & 7) || ldo < N) return OMNI_EINVAL;
+  if (epilogue == EPI_RESID && (!res || ldr < N)) return OMNI_EINVAL;
+  GemvArgs a = {};
+  a.x = (const half_t*)x;
+  a.ldx = ldx;
+  a.kx = kx;
+  a.w = weight_packed;
+  a.bias = (const half_t*)bias;
+  a.bias_after_round = 0;
+  a.out = (half_t*)out;
+  a.ldo = ldo;
+  a.res = (const half_t*)res;
+  a.ldr = ldr;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.KC = K;
+  a.KS = 1;
+  hipStream_t st = (hipStream_t)stream;
+  switch (epilogue) {
+    case EPI_STORE: return launch_gemm_tile<W_FP16, EPI_STORE>(a, st);
+    case EPI_QGELU: return launch_gemm_tile<W_FP16, EPI_QGELU>(a, st);
+    case EPI_GELU: return launch_gemm_tile<W_FP16, EPI_GELU>(a, st);
+    case EPI_RESID: return launch_gemm_tile<W_FP16, EPI_RESID>(a, st);
+    default: return OMNI_EINVAL;
+  }
 }
 
 // ---------------------------------------------------------------------------

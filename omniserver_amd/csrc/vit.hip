@@ -1,0 +1,353 @@
+// Vision tower (Qwen2-VL ViT) kernels: LayerNorm, the 2-D vision rotary, and
+// non-causal segmented attention at head_dim 80.  The tower's linears run on the
+// tiled fp16 GEMM (gemv.hip, omni_f16_gemm_tiled) with its bias / QuickGELU / GELU /
+// residual epilogues.
+//
+// Replaces, per block of model/qwen2_vit.py:36-69: nn.LayerNorm (norm1 / norm2, and
+// the merger's ln_q at :128), the fused rotary of kernels/vision_rope.py:19-47, and
+// the varlen flash call at :58-63 (cu_seqlens separate the images; every patch of an
+// image attends to every patch of the same image).
+#include "common.h"
+
+// ---------------------------------------------------------------------------
+// LayerNorm over rows: y = (x - mean) * rsqrt(var + eps) * w + b, fp32 math, fp16 out
+// (biased variance, as nn.LayerNorm).  One wave per row; lane holds 16-byte chunks
+// lane + 64 u (u < 4), so N <= 2048.
+// ---------------------------------------------------------------------------
+#define LN_MAXCH 4
+
+__global__ __launch_bounds__(256) void layernorm_kernel(const half_t* __restrict__ x, int ldx,
+                                                        const half_t* __restrict__ w,
+                                                        const half_t* __restrict__ b, int M,
+                                                        int N, float eps, half_t* __restrict__ out,
+                                                        int ldo) {
+#pragma clang fp contract(off)
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const int lane = threadIdx.x & 63;
+  const int nc = N >> 3;
+  const half_t* xr = x + (int64_t)row * ldx;
+  float v[LN_MAXCH][8];
+  float s = 0.f;
+#pragma unroll
+  for (int u = 0; u < LN_MAXCH; ++u) {
+    const int c = lane + 64 * u;
+    half8_t h = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
+    if (c < nc) h = *(const half8_t*)(xr + c * 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      v[u][e] = (float)h[e];
+      s += v[u][e];
+    }
+  }
+  const float mean = wave_sum(s) / (float)N;
+  float q = 0.f;
+#pragma unroll
+  for (int u = 0; u < LN_MAXCH; ++u) {
+    if (lane + 64 * u < nc) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float d = v[u][e] - mean;
+        q += d * d;
+      }
+    }
+  }
+  const float var = wave_sum(q) / (float)N;
+  const float rstd = rsqrtf(var + eps);
+#pragma unroll
+  for (int u = 0; u < LN_MAXCH; ++u) {
+    const int c = lane + 64 * u;
+    if (c >= nc) continue;
+    const half8_t wv = *(const half8_t*)(w + c * 8);
+    const half8_t bv = *(const half8_t*)(b + c * 8);
+    half8_t y;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[e] = (half_t)((v[u][e] - mean) * rstd * (float)wv[e] + (float)bv[e]);
+    *(half8_t*)(out + (int64_t)row * ldo + c * 8) = y;
+  }
+}
+
+// LayerNorm of M rows of N (N % 8 == 0, N <= 2048); w, b fp16 [N]; out may alias x.
+extern "C" int omni_layernorm(const void* x, int ldx, const void* weight, const void* bias, int M,
+                              int N, float eps, void* out, int ldo, void* stream) {
+  if (M < 0 || N <= 0) return OMNI_EINVAL;
+  if (M == 0) return OMNI_OK;
+  if ((N & 7) || N > 64 * 8 * LN_MAXCH) return OMNI_EUNSUPPORTED;
+  if (!x || !weight || !bias || !out) return OMNI_EINVAL;
+  if (ldx < N || ldo < N || (ldx & 7) || (ldo & 7)) return OMNI_EINVAL;
+  hipLaunchKernelGGL(layernorm_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0,
+                     (hipStream_t)stream, (const half_t*)x, ldx, (const half_t*)weight,
+                     (const half_t*)bias, M, N, eps, (half_t*)out, ldo);
+  OMNI_CHECK_LAUNCH();
+  return OMNI_OK;
+}
+
+// ---------------------------------------------------------------------------
+// 2-D vision rotary, in place on the q and k heads of the qkv rows.
+// For head_dim D (half R = D / 2, quarter R / 2): pair (d, d + R), d < R, is rotated by
+//   angle_d = pos_h * inv_freq[d]        (d < R/2)
+//           = pos_w * inv_freq[d - R/2]  (R/2 <= d < R)
+// (model/qwen2_vit.py:96-116: freqs[pos_ids].flatten(1), emb = cat(rpe, rpe)), in fp32:
+//   y[d] = x[d] cos - x[d+R] sin,  y[d+R] = x[d+R] cos + x[d] sin
+// (kernels/vision_rope.py:19-24), rounded to fp16.  One thread per 8 consecutive d of one
+// (token, q|k, head).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void vision_rope_kernel(half_t* __restrict__ qkv, int ld, int S,
+                                                          int nh, int hd,
+                                                          const int* __restrict__ pos_hw,
+                                                          const float* __restrict__ inv_freq) {
+#pragma clang fp contract(off)
+  const int R = hd >> 1, Q = hd >> 2;
+  const int cpr = R >> 3;                                // chunks per rotated half
+  const int64_t total = (int64_t)S * 2 * nh * cpr;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  const int c = (int)(i % cpr);
+  const int64_t r = i / cpr;
+  const int head = (int)(r % (2 * nh));                  // q heads, then k heads
+  const int t = (int)(r / (2 * nh));
+  half_t* p = qkv + (int64_t)t * ld + head * hd + c * 8;
+  const half8_t x1 = *(const half8_t*)p;
+  const half8_t x2 = *(const half8_t*)(p + R);
+  const float ph = (float)pos_hw[2 * t], pw = (float)pos_hw[2 * t + 1];
+  half8_t y1, y2;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int d = c * 8 + e;
+    const float ang = d < Q ? ph * inv_freq[d] : pw * inv_freq[d - Q];
+    const float cs = cosf(ang), sn = sinf(ang);
+    const float a = (float)x1[e], b = (float)x2[e];
+    y1[e] = (half_t)(a * cs - b * sn);
+    y2[e] = (half_t)(b * cs + a * sn);
+  }
+  *(half8_t*)p = y1;
+  *(half8_t*)(p + R) = y2;
+}
+
+// Rotate q (heads [0, nh)) and k (heads [nh, 2 nh)) of S rows of qkv (row stride ld, head
+// dim hd, hd % 16 == 0) in place.  pos_hw int32 [S][2] = (h, w) patch position;
+// inv_freq fp32 [hd / 4].
+extern "C" int omni_vision_rope(void* qkv, int ld, int S, int n_heads, int head_dim,
+                                const int* pos_hw, const float* inv_freq, void* stream) {
+  if (S < 0 || n_heads <= 0 || head_dim <= 0) return OMNI_EINVAL;
+  if (S == 0) return OMNI_OK;
+  if (head_dim & 15) return OMNI_EUNSUPPORTED;
+  if (!qkv || !pos_hw || !inv_freq) return OMNI_EINVAL;
+  if (ld < 2 * n_heads * head_dim || (ld & 7)) return OMNI_EINVAL;
+  const int64_t total = (int64_t)S * 2 * n_heads * (head_dim / 16);
+  const int64_t grid = (total + 255) / 256;
+  if (grid > 0x7fffffff) return OMNI_EUNSUPPORTED;
+  hipLaunchKernelGGL(vision_rope_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream,
+                     (half_t*)qkv, ld, S, n_heads, head_dim, pos_hw, inv_freq);
+  OMNI_CHECK_LAUNCH();
+  return OMNI_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Segmented non-causal attention, head_dim 80 (model/qwen2_vit.py:48-64): for every head
+// and every query t of segment [cu[s], cu[s+1]), out[t] = softmax(q_t K^T * scale) V over
+// the keys of the same segment.
+//
+// One workgroup (4 waves) owns 64 consecutive queries of one segment and one head; each
+// wave 16 of them.  K and V tiles of 64 keys are staged in LDS once for the 4 waves
+// (double buffered, the next tile's loads in flight while the current one is used).  The
+// MFMA structure is the decode / prefill kernels': S^T[16 keys x 16 queries] = K . Q^T
+// (k = 96: dims 80..95 are zero in both operands), online softmax in fp32 (exp2),
+// O[16 queries x 80] += P . V with V read back through the transposing LDS reads.
+// The workgroups of one head are contiguous in the XCD-aware order, so that a head's K
+// and V are read into one XCD's L2.
+// ---------------------------------------------------------------------------
+#define VA_HD 80
+#define VA_KT 64       // keys per staged tile
+#define VA_KSTR 104    // LDS halfs per K row: 80 dims, 16 zeros (dims 80..95), 8 pad
+#define VA_VSTR 88     // LDS halfs per V row
+#define VA_CPR 10      // 16-byte chunks per 80-dim row
+#define VA_NLD 5       // tile chunks per thread: 2 * 64 * 10 / 256
+
+struct VitAttnArgs {
+  const half_t* qkv;   // rows [S][ld]: q heads | k heads | v heads, head_dim 80
+  int ld;
+  const int* cu;       // [nseg + 1]
+  const int* tiles;    // [ntiles][2] = (first query, segment)
+  int ntiles, nh, S;
+  half_t* out;         // [S][ldo], head h at column 80 h
+  int ldo;
+  float scale_log2;
+};
+
+__global__ __launch_bounds__(256, 2) void vit_attn_kernel(VitAttnArgs a) {
+#pragma clang fp contract(off)
+  __shared__ __attribute__((aligned(16))) half_t ks_lds[2][VA_KT * VA_KSTR];
+  __shared__ __attribute__((aligned(16))) half_t vs_lds[2][VA_KT * VA_VSTR];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int q16 = lane >> 4, c16 = lane & 15;
+  const int L = xcd_logical_block(blockIdx.x, gridDim.x);
+  const int h = L / a.ntiles, tile = L - h * a.ntiles;
+  const int q0 = a.tiles[2 * tile], seg = a.tiles[2 * tile + 1];
+  const int beg = max(a.cu[seg], 0), end = min(a.cu[seg + 1], a.S);
+  if (q0 < beg || q0 >= end) return;            // malformed table entry: nothing to do
+  const half8_t z8 = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
+
+  // the K tiles' dims 80..95 are zero for the whole kernel (tile stores never touch them)
+  for (int i = tid; i < 2 * VA_KT * 2; i += 256) {
+    const int bsel = i / (VA_KT * 2), rem = i - bsel * (VA_KT * 2);
+    *(half8_t*)(&ks_lds[bsel][(rem >> 1) * VA_KSTR + VA_HD + 8 * (rem & 1)]) = z8;
+  }
+
+  // this wave's query rows q0 + 16 wave + c16 (past the segment: its last row, not stored)
+  const int qrow = min(q0 + 16 * wave + c16, end - 1);
+  const half_t* qp = a.qkv + (int64_t)qrow * a.ld + h * VA_HD;
+  half8_t qf[3];
+  qf[0] = *(const half8_t*)(qp + 8 * q16);
+  qf[1] = *(const half8_t*)(qp + 32 + 8 * q16);
+  qf[2] = *(const half8_t*)(qp + 64 + 8 * (q16 & 1));
+  if (q16 >= 2) qf[2] = z8;                     // dims 80..95
+
+  // tile chunk u of this thread: index i = tid + 256 u; i < 640 is K (row i / 10, chunk
+  // i % 10), the rest V
+  int trow[VA_NLD], tsrc[VA_NLD], tdst[VA_NLD];
+  bool tv[VA_NLD];
+#pragma unroll
+  for (int u = 0; u < VA_NLD; ++u) {
+    const int i = tid + 256 * u;
+    tv[u] = i >= VA_KT * VA_CPR;
+    const int j = tv[u] ? i - VA_KT * VA_CPR : i;
+    trow[u] = j / VA_CPR;
+    const int ch = j - trow[u] * VA_CPR;
+    tsrc[u] = (tv[u] ? 2 : 1) * a.nh * VA_HD + h * VA_HD + ch * 8;
+    tdst[u] = tv[u] ? trow[u] * VA_VSTR + ch * 8 : trow[u] * VA_KSTR + ch * 8;
+  }
+  half8_t tr[VA_NLD];
+  auto load_tile = [&](int kb) {
+#pragma unroll
+    for (int u = 0; u < VA_NLD; ++u) {
+      const int tok = min(kb + trow[u], end - 1);
+      tr[u] = *(const half8_t*)(a.qkv + (int64_t)tok * a.ld + tsrc[u]);
+    }
+  };
+  auto store_tile = [&](int b) {
+#pragma unroll
+    for (int u = 0; u < VA_NLD; ++u) {
+      half_t* dst = tv[u] ? &vs_lds[b][tdst[u]] : &ks_lds[b][tdst[u]];
+      *(half8_t*)dst = tr[u];
+    }
+  };
+
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x4 o_acc[5];
+#pragma unroll
+  for (int i = 0; i < 5; ++i) o_acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  // Double buffer: tile n is staged in buffer n & 1; the barrier after staging tile n
+  // also means every wave has finished reading that buffer's previous tile (n - 2).
+  int b = 0;
+  load_tile(beg);
+  for (int kb = beg; kb < end; kb += VA_KT, b ^= 1) {
+    store_tile(b);
+    __syncthreads();
+    if (kb + VA_KT < end) load_tile(kb + VA_KT);
+    const half_t* kt = ks_lds[b];
+    const half_t* vt = vs_lds[b];
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) {             // 32-key halves of the tile
+      const int k0 = kb + 32 * hb;
+      if (k0 >= end) break;
+      f32x4 sacc[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 3; ++ks) {
+          const half8_t kf = *(const half8_t*)(kt + (32 * hb + 16 * j + c16) * VA_KSTR + 32 * ks + 8 * q16);
+          acc = mfma16x16x32(kf, qf[ks], acc);
+        }
+        sacc[j] = acc;
+      }
+      // lane holds scores of keys k0 + 16 j + 4 q16 + i for query c16
+      float sc[8];
+      float mblk = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = k0 + 16 * j + 4 * q16 + i;
+          const float s = key < end ? sacc[j][i] * a.scale_log2 : -INFINITY;
+          sc[4 * j + i] = s;
+          mblk = fmaxf(mblk, s);
+        }
+      mblk = fmaxf(mblk, __shfl_xor(mblk, 16, 64));
+      mblk = fmaxf(mblk, __shfl_xor(mblk, 32, 64));
+      const float m_new = fmaxf(m_run, mblk);      // finite: key k0 < end is visible
+      const float alpha = exp2f(m_run - m_new);
+      m_run = m_new;
+      half8_t pa;
+      float psum = 0.f;
+#pragma unroll
+      for (int s8 = 0; s8 < 8; ++s8) {
+        const float p = exp2f(sc[s8] - m_new);
+        psum += p;
+        pa[s8] = (half_t)p;
+      }
+      l_run = l_run * alpha + psum;
+      float al[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * q16 + i, 64);
+#pragma unroll
+      for (int dt = 0; dt < 5; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o_acc[dt][i] *= al[i];
+#pragma unroll
+      for (int dt = 0; dt < 5; ++dt) {
+        const half8_t vb = lds_read_b_tr16(vt + 32 * hb * VA_VSTR + dt * 16, VA_VSTR, q16, c16);
+        o_acc[dt] = mfma16x16x32(pa, vb, o_acc[dt]);
+      }
+    }
+  }
+  l_run += __shfl_xor(l_run, 16, 64);
+  l_run += __shfl_xor(l_run, 32, 64);
+  float li[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) li[i] = __shfl(l_run, 4 * q16 + i, 64);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = q0 + 16 * wave + 4 * q16 + i;
+    if (t < end && t < q0 + 64) {
+      half_t* op = a.out + (int64_t)t * a.ldo + h * VA_HD;
+      const float inv = 1.0f / li[i];
+#pragma unroll
+      for (int dt = 0; dt < 5; ++dt) op[dt * 16 + c16] = (half_t)(o_acc[dt][i] * inv);
+    }
+  }
+}
+
+// Non-causal attention within segments over the qkv rows (q | k | v heads, head_dim 80,
+// row stride ld), already rotated.  cu int32 [nseg + 1] (cu[0] = 0, increasing, cu[nseg]
+// = S); tiles int32 [ntiles][2] = (first query, segment) covering every segment in steps
+// of 64 queries; out fp16 [S][ldo] (head h at column 80 h).
+extern "C" int omni_vit_attention(const void* qkv, int ld, int S, int n_heads, int head_dim,
+                                  const int* cu_seqlens, const int* tiles, int ntiles, void* out,
+                                  int ldo, float scale, void* stream) {
+  if (S < 0 || n_heads <= 0 || ntiles < 0) return OMNI_EINVAL;
+  if (head_dim != VA_HD) return OMNI_EUNSUPPORTED;
+  if (S == 0 || ntiles == 0) return OMNI_OK;
+  if (!qkv || !cu_seqlens || !tiles || !out) return OMNI_EINVAL;
+  if (ld < 3 * n_heads * VA_HD || (ld & 7) || ldo < n_heads * VA_HD) return OMNI_EINVAL;
+  const int64_t grid = (int64_t)ntiles * n_heads;
+  if (grid > 0x7fffffff) return OMNI_EUNSUPPORTED;
+  VitAttnArgs a;
+  a.qkv = (const half_t*)qkv;
+  a.ld = ld;
+  a.cu = cu_seqlens;
+  a.tiles = tiles;
+  a.ntiles = ntiles;
+  a.nh = n_heads;
+  a.S = S;
+  a.out = (half_t*)out;
+  a.ldo = ldo;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  hipLaunchKernelGGL(vit_attn_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, a);
+  OMNI_CHECK_LAUNCH();
+  return OMNI_OK;
+}

@@ -131,3 +131,39 @@ def kv_prefix(n_layers: int, rows: int, max_len: int, nkv: int, hd: int, lengths
         L = int(lengths[b])
         t[b, :L] = torch.randn(L, nkv, hd, generator=g).to(torch.float16)
     return t
+
+
+def vision_tower(cfg=None, seed: int = 0, depth: int | None = None) -> Dict[str, torch.Tensor]:
+    """Seeded fp16 vision-tower weights under the Hugging Face ``visual.*`` key names
+    (the layout load_vit_from_state_dict reads): linear weights and biases N(0, 0.02),
+    LayerNorm gains 1 + N(0, 0.02) and biases N(0, 0.02)."""
+    from .vit import VisionConfig
+    cfg = cfg or VisionConfig()
+    D, I, M = cfg.embed_dim, cfg.mlp_dim, cfg.merged_dim
+    nb = cfg.depth if depth is None else depth
+    one = lambda n, name: (1.0 + randn16((n,), 0.02, seed, name).float()).to(torch.float16)
+    sd = {"visual.patch_embed.proj.weight": randn16(
+        (D, cfg.in_chans, cfg.temporal_patch_size, cfg.patch_size, cfg.patch_size), 0.02, seed, "pe")}
+    for i in range(nb):
+        p = f"visual.blocks.{i}."
+        for nm in ("norm1", "norm2"):
+            sd[p + nm + ".weight"] = one(D, f"{p}{nm}.w")
+            sd[p + nm + ".bias"] = randn16((D,), 0.02, seed, f"{p}{nm}.b")
+        for nm, (n, k) in {"attn.qkv": (3 * D, D), "attn.proj": (D, D), "mlp.fc1": (I, D),
+                           "mlp.fc2": (D, I)}.items():
+            sd[p + nm + ".weight"] = randn16((n, k), 0.02, seed, f"{p}{nm}.w")
+            sd[p + nm + ".bias"] = randn16((n,), 0.02, seed, f"{p}{nm}.b")
+    sd["visual.merger.ln_q.weight"] = one(D, "lnq.w")
+    sd["visual.merger.ln_q.bias"] = randn16((D,), 0.02, seed, "lnq.b")
+    sd["visual.merger.mlp.0.weight"] = randn16((M, M), 0.02, seed, "m0.w")
+    sd["visual.merger.mlp.0.bias"] = randn16((M,), 0.02, seed, "m0.b")
+    sd["visual.merger.mlp.2.weight"] = randn16((cfg.out_hidden, M), 0.02, seed, "m2.w")
+    sd["visual.merger.mlp.2.bias"] = randn16((cfg.out_hidden,), 0.02, seed, "m2.b")
+    return sd
+
+
+def pixel_patches(grids, patch_dim: int, seed: int, name: str = "px") -> torch.Tensor:
+    """N(0, 1) fp16 flattened patches [sum t*h*w, patch_dim] (normalised pixels) for the
+    given (t, h, w) grids."""
+    n = sum(t * h * w for t, h, w in grids)
+    return randn16((n, patch_dim), 1.0, seed, name)

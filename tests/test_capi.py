@@ -80,6 +80,17 @@ def test_bad_arguments_rejected_before_launch(so):
     assert L.omni_kv_copy_slot(fake_ptr(), 2, 4, 64, 256, 0, 4, 3, None, None) == -1
     assert L.omni_kv_copy_slot(fake_ptr(), 2, 4, 64, 250, 0, 1, 3, None, None) == -2
     assert L.omni_kv_copy_slot(fake_ptr(), 2, 4, 64, 256, 0, 1, -1, None, None) == -1
+    # vision tower: LayerNorm width past 2048, rotary head_dim not a multiple of 16,
+    # attention head_dim other than 80, tiled GEMM kx past K / residual without res
+    assert L.omni_layernorm(fake_ptr(), 2056, fake_ptr(), fake_ptr(), 4, 2056, 1e-6, fake_ptr(),
+                            2056, None) == -2
+    assert L.omni_vision_rope(fake_ptr(), 3840, 4, 16, 72, fake_ptr(), fake_ptr(), None) == -2
+    assert L.omni_vit_attention(fake_ptr(), 3840, 4, 16, 64, fake_ptr(), fake_ptr(), 1,
+                                fake_ptr(), 1280, 0.1, None) == -2
+    assert L.omni_f16_gemm_tiled(fake_ptr(), 1280, 1288, fake_ptr(), None, None, 0, fake_ptr(),
+                                 1280, 4, 1280, 1280, 0, None) == -1
+    assert L.omni_f16_gemm_tiled(fake_ptr(), 1280, 1280, fake_ptr(), None, None, 0, fake_ptr(),
+                                 1280, 4, 1280, 1280, 6, None) == -1
     # GEMM: split-K partials past the skinny kernel's 64 rows, K not a multiple of 128,
     # split without partial epilogue; more rows with the STORE epilogue are the tiled GEMM
     # (here rejected for its null pointers, not its size)

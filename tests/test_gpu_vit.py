@@ -1,0 +1,157 @@
+"""Vision tower on the GPU against the CPU oracle (oracle/qwen2_vit_ref.py).
+
+Kernel by kernel (LayerNorm, 2-D rotary, segmented attention, the tiled GEMM's
+epilogues incl. the zero-padded K of the patch embedding), then the whole tower at
+reduced and at full depth.  Tolerances are stated per test: the kernels accumulate in
+fp32 in another order than the oracle, so an fp16 rounding may land one ulp apart, and
+the attention rounds its probabilities to fp16 for the MFMA (as flash attention does).
+"""
+
+import pytest
+import torch
+
+from oracle import qwen2_vit_ref as vref
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(f"[gpu-test] {msg}", flush=True)
+
+
+def f16(shape, seed, std=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * std).to(torch.float16)
+
+
+def rel_err(got, want):
+    got, want = got.float().cpu(), want.float().cpu()
+    return (got - want).abs().max().item() / max(want.abs().max().item(), 1e-6)
+
+
+@pytest.mark.parametrize("rows", [1, 7, 300])
+def test_layernorm(gpu, rows):
+    from omniserver_amd import vit
+    say(f"layernorm rows={rows}")
+    N = 1280
+    x = f16((rows, N), 1, 2.0)
+    w = (1 + 0.1 * f16((N,), 2).float()).half()
+    b = f16((N,), 3, 0.1)
+    out = torch.empty(rows, N, device=gpu, dtype=torch.float16)
+    vit.layer_norm_out(x.to(gpu), w.to(gpu), b.to(gpu), 1e-6, out)
+    want = vref.layer_norm(x.float(), w.float(), b.float(), 1e-6)
+    d = (out.cpu().float() - want).abs()
+    # one fp16 ulp of each value (fp32 sums in another order)
+    assert (d <= want.abs() * 2.0 ** -10 + 1e-3).all(), d.max().item()
+
+
+@pytest.mark.parametrize("grids", [[(1, 4, 6)], [(1, 8, 8), (2, 2, 2), (1, 6, 4)]])
+def test_vision_rope(gpu, grids):
+    from omniserver_amd import vit
+    say(f"vision_rope grids={grids}")
+    nh, hd = 16, 80
+    S = sum(t * h * w for t, h, w in grids)
+    qkv = f16((S, 3 * nh * hd), 4)
+    dev = qkv.to(gpu)
+    vit.vision_rope_(dev, nh, hd, vit.rot_pos_ids(grids, 2).to(gpu),
+                     vit.vision_inv_freq(hd, 10000.0).to(gpu))
+    got = dev.cpu().view(S, 3, nh, hd)
+    cos, sin = vref.rot_cos_sin(grids, hd)
+    x = qkv.float().view(S, 3, nh, hd)
+    eq, ek = vref.vision_rope(x[:, 0], x[:, 1], cos, sin)
+    for g, e in ((got[:, 0], eq), (got[:, 1], ek)):
+        d = (g.float() - e).abs()
+        assert (d <= e.abs() * 2.0 ** -10 + 2.0 ** -20).all(), d.max().item()
+    assert torch.equal(got[:, 2], qkv.view(S, 3, nh, hd)[:, 2])          # v untouched
+
+
+@pytest.mark.parametrize("lens", [[4], [64], [100], [4, 64, 37, 200], [1024], [16, 16, 16, 16]])
+def test_vit_attention(gpu, lens):
+    from omniserver_amd import vit
+    say(f"vit_attention segments={lens}")
+    nh, hd = 16, 80
+    cu = [0]
+    for n in lens:
+        cu.append(cu[-1] + n)
+    S = cu[-1]
+    qkv = f16((S, 3 * nh * hd), 5)
+    cu_t = torch.tensor(cu, dtype=torch.int32)
+    tiles = vit.query_tiles(cu_t)
+    out = torch.full((S, nh * hd), float("nan"), device=gpu, dtype=torch.float16)
+    vit.vit_attention_out(qkv.to(gpu), nh, hd, cu_t.to(gpu), tiles.to(gpu), hd ** -0.5, out)
+    x = qkv.float().view(S, 3, nh, hd)
+    want = vref.seg_attention(x[:, 0], x[:, 1], x[:, 2], cu, hd ** -0.5).reshape(S, nh * hd)
+    got = out.cpu().float()
+    assert not torch.isnan(got).any()
+    assert (got - want).abs().max().item() <= 4e-3
+
+
+# (M, N, K, epilogue, bias): the tower's shapes (patch embed K = 1176 padded to 1280)
+GEMM_CASES = [(300, 1280, 1176, 0, False), (300, 3840, 1280, 0, True), (257, 5120, 1280, 4, True),
+              (64, 1280, 5120, 6, True), (75, 5120, 5120, 5, True), (75, 1536, 5120, 0, True),
+              (5, 1280, 1280, 6, True)]
+
+
+@pytest.mark.parametrize("M,N,K,epi,has_bias", GEMM_CASES)
+def test_gemm_tiled_epilogues(gpu, M, N, K, epi, has_bias):
+    from omniserver_amd import vit
+    say(f"gemm_tiled M={M} N={N} K={K} epi={epi}")
+    x = f16((M, K), 6)
+    w = f16((N, K), 7, 0.02)
+    b = f16((N,), 8, 0.02) if has_bias else None
+    res = f16((M, N), 9)
+    lin = vit.TiledLinear(w, b, gpu)
+    out = res.to(gpu).clone() if epi == vit.EPI_RESID else torch.empty(M, N, device=gpu,
+                                                                        dtype=torch.float16)
+    lin.out(x.to(gpu), out, epi, res=out if epi == vit.EPI_RESID else None)
+    h = vref.linear(x.float(), w.float(), None if b is None else b.float())
+    if epi == vit.EPI_QGELU:
+        want = vref.quick_gelu(h)
+    elif epi == vit.EPI_GELU:
+        want = vref.gelu(h)
+    elif epi == vit.EPI_RESID:
+        want = vref.r16(res.float() + h)
+    else:
+        want = h
+    d = (out.cpu().float() - want).abs()
+    # the fp32 sum may round to the neighbouring fp16 value (and that ulp carries through
+    # the elementwise epilogue)
+    tol = 2.0 ** -9 * (want.abs() + h.abs()) + 1e-3 * want.abs().max().item()
+    assert (d <= tol).all(), d.max().item()
+
+
+def _tower(gpu, depth, seed):
+    from omniserver_amd import synth, vit
+    cfg = vit.VisionConfig(depth=depth)
+    sd = synth.vision_tower(cfg, seed=seed, depth=depth)
+    tower = vit.load_vit_from_state_dict(vit.Qwen2VIT(depth=depth, device=gpu), sd)
+    return cfg, sd, tower
+
+
+def test_vit_tower_two_blocks(gpu):
+    from omniserver_amd import synth
+    say("vit tower depth 2, three images")
+    cfg, sd, tower = _tower(gpu, 2, 11)
+    grids = [(1, 8, 8), (1, 4, 6), (2, 2, 4)]
+    pv = synth.pixel_patches(grids, cfg.patch_dim, 12)
+    got = tower(pv.to(gpu), grids).cpu().float()
+    want = vref.vit_forward(pv.float(), grids, sd)
+    assert got.shape == want.shape == (16 + 6 + 4, 1536)
+    cos = torch.nn.functional.cosine_similarity(got, want, dim=-1).min().item()
+    e = rel_err(got, want)
+    say(f"depth 2: max rel err {e:.2e}, min cos {cos:.6f}")
+    assert e <= 1e-2 and cos >= 0.9999
+
+
+def test_vit_tower_full_depth(gpu):
+    from omniserver_amd import synth
+    say("vit tower depth 32, 16x16 patches")
+    cfg, sd, tower = _tower(gpu, 32, 13)
+    grids = [(1, 16, 16)]
+    pv = synth.pixel_patches(grids, cfg.patch_dim, 14)
+    got = tower(pv.to(gpu), grids).cpu().float()
+    want = vref.vit_forward(pv.float(), grids, sd)
+    cos = torch.nn.functional.cosine_similarity(got, want, dim=-1).min().item()
+    e = rel_err(got, want)
+    say(f"depth 32: max rel err {e:.2e}, min cos {cos:.6f}")
+    assert e <= 3e-2 and cos >= 0.999

@@ -36,6 +36,7 @@ import torch
 
 PEAK_HBM = 8.0e12  # MI355X HBM3E, bytes/s
 PEAK_FP8 = 5.0e15  # MI355X dense fp8 MFMA, FLOP/s
+PEAK_FP16 = 2.5e15  # MI355X dense fp16 MFMA, FLOP/s
 
 H, I, NL, NH, NKV, HD, V = 1536, 8960, 28, 12, 2, 128, 151936
 LINEARS = [(H, (NH + 2 * NKV) * HD), (NH * HD, H), (H, 2 * I), (I, H)]   # (K, N)
@@ -229,6 +230,36 @@ def fp8_layer_gemms(device, M: int = 8192, reps: int = 10) -> dict:
             "per_shape": per}
 
 
+def vit_flops(grids, cfg) -> float:
+    """Dense FLOPs of one vision-tower forward (model/qwen2_vit.py:118-129): the patch
+    embedding (K = 1176), per block the four linears and the two attention products within
+    each frame, the merger's two linears."""
+    D, I, M = cfg.embed_dim, cfg.mlp_dim, cfg.merged_dim
+    S = sum(t * h * w for t, h, w in grids)
+    attn = sum(t * 4.0 * (h * w) ** 2 * D for t, h, w in grids)
+    block = 2.0 * S * D * (3 * D + D + 2 * I) + attn
+    merger = 2.0 * (S // 4) * M * (M + cfg.out_hidden)
+    return 2.0 * S * cfg.patch_dim * D + cfg.depth * block + merger
+
+
+def vit_tower(device, grid=(1, 32, 32), reps: int = 5) -> dict:
+    """The vision tower (all 32 blocks + merger, seeded synthetic fp16 weights) on one
+    448 x 448 image (32 x 32 patches -> 256 rows), pixels resident in HBM.  Achieved dense
+    TFLOP/s against the MI355X fp16 MFMA peak (2.5 PFLOP/s)."""
+    from omniserver_amd import synth
+    from omniserver_amd.vit import Qwen2VIT, VisionConfig, load_vit_from_state_dict
+    cfg = VisionConfig()
+    tower = load_vit_from_state_dict(Qwen2VIT(device=device), synth.vision_tower(cfg, seed=5))
+    pv = synth.pixel_patches([grid], cfg.patch_dim, 6).to(device)
+    t = time_kernel(lambda: tower(pv, [grid]), reps)
+    fl = vit_flops([grid], cfg)
+    return {"workload": f"vision tower, 32 blocks + merger, one image grid {list(grid)} "
+                        f"({grid[0] * grid[1] * grid[2]} patches)",
+            "gflop": round(fl / 1e9, 1), "ms": round(t * 1e3, 3),
+            "achieved": round(fl / t / 1e12, 1), "peak": PEAK_FP16 / 1e12, "unit": "TFLOP/s",
+            "frac": round(fl / t / PEAK_FP16, 4)}
+
+
 def cpu_baseline(runner, seqs, w, shape, budget_s: float = 15.0) -> dict:
     """fp32 CPU restatement (oracle) of the same decode step on this host's cores."""
     from oracle import qwen2_ref as ref
@@ -278,6 +309,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-fp8", action="store_true",
                     help="skip the FP8 W8A8 GEMM leg (BASELINE configs[3])")
+    ap.add_argument("--no-vit", action="store_true", help="skip the vision-tower leg")
+    ap.add_argument("--vit-only", action="store_true",
+                    help="time only the vision tower (one JSON object) and exit")
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--kernel-steps", type=int, default=10,
                     help="replays of the 28-launch attention graph timed for the roofline")
@@ -297,6 +331,9 @@ def main():
         sys.exit(2)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.vit_only:
+        print(json.dumps(vit_tower(dev)), flush=True)
+        return
 
     runner, seqs, w, shape = build_config3(dev, args.batch, args.ctx)
     B = len(seqs)
@@ -398,6 +435,7 @@ def main():
             "gate_up_GBps": round(gu_bytes / t_gu / 1e9, 1),
         },
         "fp8_gemm": None,
+        "vit": None,
         "cpu_baseline": None,
     }
     if not args.no_fp8:
@@ -405,6 +443,11 @@ def main():
             out["fp8_gemm"] = fp8_layer_gemms(dev)
         except Exception as e:  # report, never fail the decode line on this leg
             out["fp8_gemm"] = {"error": repr(e)}
+    if not args.no_vit:
+        try:
+            out["vit"] = vit_tower(dev)
+        except Exception as e:  # report, never fail the decode line on this leg
+            out["vit"] = {"error": repr(e)}
     if not args.no_cpu:
         try:
             out["cpu_baseline"] = cpu_baseline(runner, seqs, w, shape)

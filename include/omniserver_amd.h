@@ -235,6 +235,15 @@ int omni_f16_gemm_tiled(const void* x, int ldx, int kx, const void* weight_packe
                         const void* bias, const void* res, int ldr, void* out, int ldo, int M,
                         int N, int K, int epilogue, void* stream);
 
+/* The same linears on a multi-stage global -> LDS pipeline GEMM (persistent grid, 128- or
+ * 256-row x 128-column tiles): w fp16 [N, K] in nn.Linear layout (row stride K, no
+ * packing).  N % 128 == 0, K % 64 == 0, K >= 256; x, w 16-byte aligned, ldx % 8 == 0,
+ * ldo / ldr % 4 == 0.  Epilogues as omni_f16_gemm_tiled; tile_rows 128, 256 or 0 (chosen
+ * from the shape). */
+int omni_f16_gemm_pipe(const void* x, int ldx, const void* w, const void* bias, const void* res,
+                       int ldr, void* out, int ldo, int M, int N, int K, int epilogue,
+                       int tile_rows, void* stream);
+
 /* nn.LayerNorm(N, eps) of M fp16 rows (model/qwen2_vit.py:39-40, 87): fp32 mean and biased
  * variance, y = (x - mean) rsqrt(var + eps) w + b.  N % 8 == 0, N <= 2048; out may alias x. */
 int omni_layernorm(const void* x, int ldx, const void* weight, const void* bias, int M, int N,

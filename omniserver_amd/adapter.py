@@ -31,7 +31,8 @@ class Qwen2VLAdapter:
     def __init__(self, model_dir: Optional[str] = None, quant: Optional[str] = None,
                  gptq_dir: Optional[str] = None, weights: Optional[dict] = None,
                  shape: Optional[synth.DecoderShape] = None, seed: int = 0,
-                 num_layers: Optional[int] = None, device="cuda", max_pos: int = 8192):
+                 num_layers: Optional[int] = None, device="cuda", max_pos: int = 8192,
+                 vision=None):
         if quant not in (None, "gptq"):
             raise ValueError(f"unsupported quant {quant!r} (None or 'gptq')")
         self.device = torch.device(device)
@@ -40,11 +41,14 @@ class Qwen2VLAdapter:
             self.shape.num_layers = num_layers
         self.quant = quant
         src = gptq_dir if quant == "gptq" else model_dir
+        vision_sd = vision if isinstance(vision, dict) else None
         if weights is None and src is not None:
             from . import checkpoint
             sd = checkpoint.read_safetensors(src)
             weights = (checkpoint.gptq_decoder_from_state_dict(sd) if quant == "gptq"
                        else checkpoint.fp16_decoder_from_state_dict(sd))
+            if vision_sd is None:
+                vision_sd = checkpoint.vision_state_dict(sd)
             del sd
             if weights["embed"].shape[1] != self.shape.hidden_size:
                 raise ValueError(f"checkpoint hidden size {weights['embed'].shape[1]} is not the "
@@ -56,6 +60,19 @@ class Qwen2VLAdapter:
             weights = gen(self.shape, seed=seed)
         build = Qwen2LLM.from_gptq if quant == "gptq" else Qwen2LLM.from_fp16
         self._llm = build(weights, self.shape, self.device, max_pos=max_pos)
+        # vision tower (models/qwen2_vl.py:46-48): the checkpoint's visual.* tensors, a
+        # given state dict, or (vision=True / an int depth) seeded synthetic weights
+        self._vit = None
+        if vision_sd is None and vision is not None and vision is not False:
+            from .vit import VisionConfig
+            depth = None if vision is True else int(vision)
+            vision_sd = synth.vision_tower(VisionConfig(), seed=seed, depth=depth)
+        if vision_sd:
+            from .vit import Qwen2VIT, load_vit_from_state_dict
+            depth = sum(1 for k in vision_sd if k.startswith("visual.blocks.") and
+                        k.endswith(".norm1.weight"))
+            self._vit = load_vit_from_state_dict(Qwen2VIT(depth=depth, device=self.device),
+                                                 vision_sd)
         self.num_layers = len(weights["layers"])
         self.num_kv_heads = self.shape.num_kv_heads
         self.num_heads = self.shape.num_heads
@@ -78,9 +95,32 @@ class Qwen2VLAdapter:
     def embed_tokens(self, input_ids: torch.Tensor) -> torch.Tensor:
         return self._llm.embed_tokens(input_ids)
 
+    @property
+    def vision(self):
+        """The vision tower (None when the adapter was built without one)."""
+        return self._vit
+
     def vision_embed(self, images) -> torch.Tensor:
-        """Concatenated vision rows of the request's images (already ViT outputs)."""
-        rows = [im.embeds.to(self.device, torch.float16) for im in images]
+        """Concatenated vision rows of the request's images, in order
+        (models/qwen2_vl.py:96-97): ``PixelInput`` items go through the vision tower in one
+        call (their cu_seqlens keep the images apart), ``VisionInput`` rows are taken as
+        given."""
+        from .request import PixelInput
+        pix = [im for im in images if isinstance(im, PixelInput)]
+        enc = []
+        if pix:
+            if self._vit is None:
+                raise RuntimeError("pixel inputs need the vision tower: build the adapter from "
+                                   "a checkpoint with visual.* tensors, or with vision=True")
+            pv = torch.cat([torch.as_tensor(im.pixel_values).to(self.device, torch.float16)
+                            for im in pix], 0)
+            out = self._vit(pv, [im.grid for im in pix])
+            sizes = [im.grid[0] * im.grid[1] * im.grid[2] // 4 for im in pix]
+            enc = list(torch.split(out, sizes, 0))
+        rows = []
+        for im in images:
+            rows.append(enc.pop(0) if isinstance(im, PixelInput)
+                        else im.embeds.to(self.device, torch.float16))
         return torch.cat(rows, 0)
 
     # ---- positions (M-RoPE) -------------------------------------------------------

@@ -13,10 +13,10 @@ Two layouts, the same two the reference reads:
   same way (model/qwen2_llm.py:193-219), with either the raw ``model.`` prefix or the
   ``model.language_model.`` prefix of newer transformers state dicts.
 
-Files are read with ``safetensors`` (no code runs from the file).  Vision-tower
-tensors are ignored: this build takes vision rows as inputs.  The result is the
-weight dict the model builders take (``synth.gptq_decoder`` / ``synth.fp16_decoder``
-layout).
+Files are read with ``safetensors`` (no code runs from the file).  The decoder
+result is the weight dict the model builders take (``synth.gptq_decoder`` /
+``synth.fp16_decoder`` layout); ``vision_state_dict`` picks the vision tower's fp16
+tensors (kept fp16 in both layouts, as models/qwen2_vl.py:39-48 loads them).
 """
 
 from __future__ import annotations
@@ -125,6 +125,18 @@ def fp16_decoder_from_state_dict(sd: Dict[str, torch.Tensor]) -> Dict:
             "gate_up_w": f16(torch.cat([g("mlp.gate_proj.weight"), g("mlp.up_proj.weight")], 0)),
             "down_w": f16(g("mlp.down_proj.weight")),
         })
+    return out
+
+
+def vision_state_dict(sd: Dict[str, torch.Tensor]) -> Dict[str, torch.Tensor]:
+    """The vision tower's tensors under ``visual.*`` (either the raw ``visual.`` prefix or
+    the ``model.visual.`` prefix of newer transformers state dicts); {} when absent."""
+    out = {}
+    for k, v in sd.items():
+        if k.startswith("visual."):
+            out[k] = v
+        elif k.startswith("model.visual."):
+            out[k[len("model."):]] = v
     return out
 
 

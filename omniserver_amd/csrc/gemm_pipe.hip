@@ -1,0 +1,317 @@
+// fp16 GEMM with a multi-stage global -> LDS pipeline, for the vision tower's linears:
+//   out[m, n] = epi(fp16(sum_k x[m, k] w[n, k] + bias[n]))
+// x fp16 [M, K] (row stride ldx), w fp16 [N, K] (nn.Linear layout, row stride K), fp32
+// accumulation on v_mfma_f32_16x16x32_f16.  Epilogues: STORE, QGELU (x sigmoid(1.702 x)),
+// GELU (erf), RESID (fp16(res + h)).
+//
+// Persistent grid (one workgroup per CU at most) walking 64 WM x 128 output tiles in
+// grouped, XCD-aware order.  2 WM waves, each owning a 64 (m) x 64 (n) sub-tile: per K
+// step of 64 (128 bytes of every operand row) it issues 16 LDS operand reads and 32
+// MFMAs.  Operand rows go global -> LDS with global_load_lds (16 bytes per lane), NS
+// steps ahead, across tile boundaries (the last steps of a tile load the next tile's
+// first ones); the 16-byte chunks of a row are XOR-swizzled by row so that the 16 rows an
+// operand read touches spread over the banks.  A step is consumed once an exact per-thread
+// vmcnt and a barrier say it landed everywhere; its slot is refilled right after the
+// barrier, while the step's MFMAs run.
+#include "common.h"
+
+#define GP_BN 128        // tile columns (n)
+#define GP_BKH 64        // K (halfs) per pipeline step
+#define GP_ROWB 128      // LDS bytes per staged operand row (one step)
+#define GP_GM 4          // tile rows per group of the tile order
+
+enum { GP_STORE = 0, GP_QGELU = 4, GP_GELU = 5, GP_RESID = 6 };
+
+struct GemmPipeArgs {
+  const half_t* x;
+  int ldx;
+  const half_t* w;
+  int ldw;
+  const half_t* bias;    // [N] or NULL
+  const half_t* res;     // GP_RESID: [M, ldr]
+  int ldr;
+  half_t* out;
+  int ldo;
+  int M, N, K;
+};
+
+template <int N>
+__device__ __forceinline__ void gp_wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void gp_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+__device__ __forceinline__ half_t gp_quick_gelu(half_t h) {
+#pragma clang fp contract(off)
+  const float t = (float)(half_t)((float)h * 1.702f);
+  const float sg = (float)(half_t)(1.0f / (1.0f + expf(-t)));
+  return (half_t)((float)h * sg);
+}
+
+__device__ __forceinline__ half_t gp_gelu(half_t h) {
+#pragma clang fp contract(off)
+  const float x = (float)h;
+  return (half_t)(0.5f * x * (1.0f + erff(x * 0.70710678118654752f)));
+}
+
+struct GpTileSrc {
+  const half_t* x[4];
+  const half_t* w;
+  const half_t* b;
+};
+
+template <int WM, int NS, int EPI>
+__global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) {
+#pragma clang fp contract(off)
+  constexpr int BM = 64 * WM;
+  constexpr int NWV = 2 * WM;
+  constexpr int XLD = 4;                // x loads per wave and step (BM rows / 8 / NWV)
+  constexpr int WLD = 8 / WM;           // w loads per wave and step (128 rows / 8 / NWV)
+  constexpr int OPS = XLD + WLD;        // loads every thread issues per step (wave 0: + bias)
+  __shared__ __attribute__((aligned(1024))) uint8_t xl[NS][BM * GP_ROWB];
+  __shared__ __attribute__((aligned(1024))) uint8_t wl[NS][GP_BN * GP_ROWB];
+  // bias slot: 64 lanes x 16 bytes land per load (lanes 16-63 repeat lane 15's chunk)
+  __shared__ __attribute__((aligned(16))) half_t bsl[NS][512];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wave & 1;
+  const int wm = wave >> 1;
+  const int l16 = lane & 15;
+  const int g4 = lane >> 4;
+
+  const int tiles_n = a.N / GP_BN;
+  const int tiles_m = (a.M + BM - 1) / BM;
+  const int tiles = tiles_m * tiles_n;
+  const int G = gridDim.x;
+  const int slot = xcd_logical_block(blockIdx.x, G);
+  const int my_tiles = (tiles - slot + G - 1) / G;       // grid <= tiles: >= 1
+  const int nk = a.K / GP_BKH;                           // >= NS (host check)
+
+  // Load u of this wave fills tile rows 8 NWV u + 8 wave + lane / 8; lane i writes LDS
+  // slot i % 8 of its row, which holds the row's chunk (i % 8) ^ (row & 7).
+  const int lrow = 8 * wave + (lane >> 3);
+  const int lchunk = (lane & 7) ^ (lrow & 7);
+  typedef __attribute__((address_space(3))) void lds_void;
+  typedef __attribute__((address_space(3))) uint8_t lds_u8;
+  const bool has_bias = a.bias != nullptr;
+  auto tile_src = [&](int r, int& m0, int& n0) {     // past the last tile: the last one again
+    int tm, tn;
+    grouped_tile(min(r, my_tiles - 1) * G + slot, tiles_m, tiles_n, GP_GM, tm, tn);
+    m0 = tm * BM;
+    n0 = tn * GP_BN;
+    GpTileSrc t;
+#pragma unroll
+    for (int u = 0; u < XLD; ++u)
+      t.x[u] = a.x + (int64_t)min(m0 + 8 * NWV * u + lrow, a.M - 1) * a.ldx + lchunk * 8;
+    t.w = a.w + (int64_t)(n0 + lrow) * a.ldw + lchunk * 8;
+    t.b = has_bias ? a.bias + n0 + 8 * min(lane, 15) : a.w;
+    return t;
+  };
+  const int64_t wstep = (int64_t)8 * NWV * a.ldw;       // halfs between w row groups
+  auto issue = [&](const GpTileSrc& t, int ks, int st) {
+    const int k0 = ks * GP_BKH;
+#pragma unroll
+    for (int u = 0; u < XLD; ++u)
+      __builtin_amdgcn_global_load_lds((const void*)(t.x[u] + k0),
+                                       (lds_void*)((lds_u8*)&xl[st][(8 * NWV * u + 8 * wave) * GP_ROWB]), 16, 0, 0);
+#pragma unroll
+    for (int u = 0; u < WLD; ++u)
+      __builtin_amdgcn_global_load_lds((const void*)(t.w + u * wstep + k0),
+                                       (lds_void*)((lds_u8*)&wl[st][(8 * NWV * u + 8 * wave) * GP_ROWB]), 16, 0, 0);
+    if (wave == 0 && has_bias)        // the tile's 128 biases (lanes 0-15 carry them)
+      __builtin_amdgcn_global_load_lds((const void*)t.b, (lds_void*)((lds_u8*)&bsl[st][0]), 16, 0, 0);
+  };
+  // Operand reads are inline asm with their own lgkmcnt wait: as plain loads the compiler
+  // would make each wait for every outstanding global->LDS load (vmcnt(0)).  A step's
+  // slot is complete by the vmcnt wait and barrier before it is read.
+  // Addresses of the lane's 16 operand bytes (k = 8 g4 .. +7 of K sub-step t) of tile rows
+  // base + 16 i + l16: chunk 4 t + g4.
+  auto operand_addrs = [&](int st, int o, int base, uint32_t (&ad)[8]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = base + 16 * i + l16;
+      const uint32_t row = (uint32_t)(uintptr_t)(lds_u8*)(o ? &wl[st][r * GP_ROWB] : &xl[st][r * GP_ROWB]);
+      ad[2 * i] = row + ((g4 ^ (r & 7)) << 4);
+      ad[2 * i + 1] = row + (((4 + g4) ^ (r & 7)) << 4);
+    }
+  };
+  auto read_issue = [&](int st, u32x4 (&v)[16]) {
+    uint32_t aw[8], ax[8];
+    operand_addrs(st, 1, 64 * wn, aw);
+    operand_addrs(st, 0, 64 * wm, ax);
+    asm volatile(
+        "ds_read_b128 %0, %16\n\tds_read_b128 %1, %17\n\tds_read_b128 %2, %18\n\t"
+        "ds_read_b128 %3, %19\n\tds_read_b128 %4, %20\n\tds_read_b128 %5, %21\n\t"
+        "ds_read_b128 %6, %22\n\tds_read_b128 %7, %23\n\tds_read_b128 %8, %24\n\t"
+        "ds_read_b128 %9, %25\n\tds_read_b128 %10, %26\n\tds_read_b128 %11, %27\n\t"
+        "ds_read_b128 %12, %28\n\tds_read_b128 %13, %29\n\tds_read_b128 %14, %30\n\t"
+        "ds_read_b128 %15, %31"
+        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
+          "=&v"(v[6]), "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11]),
+          "=&v"(v[12]), "=&v"(v[13]), "=&v"(v[14]), "=&v"(v[15])
+        : "v"(aw[0]), "v"(aw[1]), "v"(aw[2]), "v"(aw[3]), "v"(aw[4]), "v"(aw[5]), "v"(aw[6]),
+          "v"(aw[7]), "v"(ax[0]), "v"(ax[1]), "v"(ax[2]), "v"(ax[3]), "v"(ax[4]), "v"(ax[5]),
+          "v"(ax[6]), "v"(ax[7])
+        : "memory");
+  };
+  auto read_wait = [&](u32x4 (&v)[16]) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
+                   "+v"(v[6]), "+v"(v[7]), "+v"(v[8]), "+v"(v[9]), "+v"(v[10]), "+v"(v[11]),
+                   "+v"(v[12]), "+v"(v[13]), "+v"(v[14]), "+v"(v[15])
+                 :
+                 : "memory");
+  };
+  // the tile's biases of this lane's columns (4 per n sub-tile), read at the tile's last step
+  uint2 bv[4] = {};
+  auto read_bias = [&](int st) {
+    typedef __attribute__((address_space(3))) half_t lds_f16;
+    uint32_t ab[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ab[i] = (uint32_t)(uintptr_t)(lds_f16*)&bsl[st][64 * wn + 16 * i + 4 * g4];
+    asm volatile(
+        "ds_read_b64 %0, %4\n\tds_read_b64 %1, %5\n\tds_read_b64 %2, %6\n\tds_read_b64 %3, %7\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(bv[0]), "=&v"(bv[1]), "=&v"(bv[2]), "=&v"(bv[3])
+        : "v"(ab[0]), "v"(ab[1]), "v"(ab[2]), "v"(ab[3])
+        : "memory");
+  };
+
+  int m0c, n0c, m0n, n0n;
+  GpTileSrc cur = tile_src(0, m0c, n0c);
+  GpTileSrc nxt = tile_src(1, m0n, n0n);
+#pragma unroll
+  for (int s = 0; s < NS; ++s) issue(cur, s, s);
+  gp_wait_vmcnt<OPS * (NS - 1)>();
+  gp_barrier();
+  int sidx = 0;
+  for (int r = 0; r < my_tiles; ++r) {
+    f32x4 acc[4][4];   // [n sub-tile][m sub-tile]
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int ks = 0; ks < nk; ++ks, ++sidx) {
+      const int st = sidx % NS;
+      u32x4 ops[16];
+      read_issue(st, ops);
+      read_wait(ops);
+      if (ks == nk - 1 && has_bias) read_bias(st);
+      // step sidx + 1 has landed for this thread, then for everyone; every wave has also
+      // read step sidx's slot, which is refilled with step sidx + NS
+      gp_wait_vmcnt<OPS * (NS - 2)>();
+      gp_barrier();
+      {
+        const int iks = ks + NS;
+        if (iks < nk) issue(cur, iks, st);
+        else issue(nxt, iks - nk, st);
+      }
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const half8_t wf = __builtin_bit_cast(half8_t, ops[2 * i + t]);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const half8_t xf = __builtin_bit_cast(half8_t, ops[8 + 2 * j + t]);
+            acc[i][j] = mfma16x16x32(wf, xf, acc[i][j]);
+          }
+        }
+    }
+    // Epilogue: lane holds n = n0 + 64 wn + 16 i + 4 g4 + q of m = m0 + 64 wm + 16 j + l16.
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int m = m0c + 64 * wm + 16 * j + l16;
+      if (m >= a.M) continue;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int n = n0c + 64 * wn + 16 * i + 4 * g4;
+        const half4_t bb = __builtin_bit_cast(half4_t, bv[i]);
+        half4_t rr = (half4_t){0, 0, 0, 0};
+        if constexpr (EPI == GP_RESID) rr = *(const half4_t*)(a.res + (int64_t)m * a.ldr + n);
+        half4_t o;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          half_t h = has_bias ? (half_t)(acc[i][j][q] + (float)bb[q]) : (half_t)acc[i][j][q];
+          if constexpr (EPI == GP_QGELU) h = gp_quick_gelu(h);
+          if constexpr (EPI == GP_GELU) h = gp_gelu(h);
+          if constexpr (EPI == GP_RESID) h = (half_t)((float)rr[q] + (float)h);
+          o[q] = h;
+        }
+        *(half4_t*)(a.out + (int64_t)m * a.ldo + n) = o;
+      }
+    }
+    cur = nxt;
+    m0c = m0n;
+    n0c = n0n;
+    nxt = tile_src(r + 2, m0n, n0n);
+  }
+  gp_wait_vmcnt<0>();                  // drain the clamped tail loads before exit
+}
+
+static int gp_num_cus() {
+  static int n = 0;
+  if (n <= 0) {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+      v = 256;
+    n = v;
+  }
+  return n;
+}
+
+template <int WM, int NS>
+static int gp_launch(const GemmPipeArgs& a, int epilogue, hipStream_t st) {
+  const int64_t tiles = (int64_t)ceil_div(a.M, 64 * WM) * (a.N / GP_BN);
+  if (tiles > 0x7fffffff) return OMNI_EUNSUPPORTED;
+  const int grid = (int)(tiles < gp_num_cus() ? tiles : gp_num_cus());
+  const dim3 blk(128 * WM);
+  switch (epilogue) {
+    case GP_STORE: hipLaunchKernelGGL((gemm_pipe_kernel<WM, NS, GP_STORE>), dim3(grid), blk, 0, st, a); break;
+    case GP_QGELU: hipLaunchKernelGGL((gemm_pipe_kernel<WM, NS, GP_QGELU>), dim3(grid), blk, 0, st, a); break;
+    case GP_GELU: hipLaunchKernelGGL((gemm_pipe_kernel<WM, NS, GP_GELU>), dim3(grid), blk, 0, st, a); break;
+    case GP_RESID: hipLaunchKernelGGL((gemm_pipe_kernel<WM, NS, GP_RESID>), dim3(grid), blk, 0, st, a); break;
+    default: return OMNI_EINVAL;
+  }
+  OMNI_CHECK_LAUNCH();
+  return OMNI_OK;
+}
+
+// out = epi(fp16(x . w^T + bias)) with w fp16 [N, K] in nn.Linear layout (row stride K).
+// N % 128 == 0, K % 64 == 0 and K >= 256; x, w 16-byte aligned with ldx % 8 == 0;
+// ldo, ldr % 4 == 0.  tile_rows 128 or 256 (0: chosen from the shape).
+extern "C" int omni_f16_gemm_pipe(const void* x, int ldx, const void* w, const void* bias,
+                                  const void* res, int ldr, void* out, int ldo, int M, int N,
+                                  int K, int epilogue, int tile_rows, void* stream) {
+  if (M < 0 || N <= 0 || K <= 0) return OMNI_EINVAL;
+  if ((N % GP_BN) || (K % GP_BKH) || K < 4 * GP_BKH) return OMNI_EUNSUPPORTED;
+  if (M == 0) return OMNI_OK;
+  if (!x || !w || !out) return OMNI_EINVAL;
+  if (ldx < K || (ldx & 7) || ldo < N || (ldo & 3)) return OMNI_EINVAL;
+  if (((uintptr_t)x & 15) || ((uintptr_t)w & 15) || ((uintptr_t)out & 7)) return OMNI_EINVAL;
+  if (epilogue == GP_RESID && (!res || ldr < N || (ldr & 3) || ((uintptr_t)res & 7))) return OMNI_EINVAL;
+  if (bias && ((uintptr_t)bias & 15)) return OMNI_EINVAL;
+  if (tile_rows != 0 && tile_rows != 128 && tile_rows != 256) return OMNI_EINVAL;
+  GemmPipeArgs a;
+  a.x = (const half_t*)x;
+  a.ldx = ldx;
+  a.w = (const half_t*)w;
+  a.ldw = K;
+  a.bias = (const half_t*)bias;
+  a.res = (const half_t*)res;
+  a.ldr = ldr;
+  a.out = (half_t*)out;
+  a.ldo = ldo;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  if (tile_rows == 0) {
+    // 256-row tiles when they still give every CU a tile
+    const int64_t t256 = (int64_t)ceil_div(M, 256) * (N / GP_BN);
+    tile_rows = t256 >= gp_num_cus() ? 256 : 128;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  return tile_rows == 256 ? gp_launch<4, 3>(a, epilogue, st) : gp_launch<2, 4>(a, epilogue, st);
+}

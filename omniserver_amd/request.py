@@ -2,9 +2,10 @@
 
 Same fields and behaviour as omniserve/request.py (Status :21-25, SamplingParams
 :28-37, Request :40-47, Sequence :50-115), so a scheduler/engine written against
-the reference drives this runner unchanged.  ``Request.images`` may hold
-``VisionInput`` items (precomputed vision-embedding rows + their grid): this build
-has no ViT, the rows are what the reference's ViT would emit.
+the reference drives this runner unchanged.  ``Request.images`` holds, per image,
+either ``PixelInput`` (the image processor's flattened patches + grid, encoded by the
+adapter's vision tower, as models/qwen2_vl.py:76-97 does) or ``VisionInput``
+(precomputed vision rows + grid: the tower's output, supplied by the caller).
 """
 
 from __future__ import annotations
@@ -42,6 +43,15 @@ class VisionInput:
     """Vision-embedding rows [n_tokens, hidden] fp16 for one image and its patch grid
     (t, h, w) before the 2x2 merge, as the reference's ViT + merger would produce."""
     embeds: object
+    grid: Tuple[int, int, int]
+
+
+@dataclass
+class PixelInput:
+    """One image as the vision tower takes it: normalised pixel patches fp16
+    [t*h*w, 3*2*14*14] in merge-window order (the reference's preprocess_image output,
+    model/preprocess.py) and the patch grid (t, h, w); it becomes t*h*w/4 rows."""
+    pixel_values: object
     grid: Tuple[int, int, int]
 
 

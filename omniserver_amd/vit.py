@@ -140,30 +140,50 @@ def vit_attention_out(qkv: torch.Tensor, n_heads: int, head_dim: int, cu: torch.
     return out
 
 
-class TiledLinear:
-    """fp16 nn.Linear (weight [N, K], optional bias [N]) packed for the tiled GEMM; K is
-    zero-padded to whole 128-column groups (the patch embedding's K = 1176)."""
+class VisionLinear:
+    """fp16 nn.Linear (weight [N, K], optional bias [N]) on one of two GEMMs:
+    ``pipe`` (omni_f16_gemm_pipe: weights in nn.Linear layout, a multi-stage LDS pipeline;
+    N % 128 == 0, K % 64 == 0, K >= 256 - every linear of the blocks and the merger) or
+    ``tiled`` (omni_f16_gemm_tiled: weights packed with K zero-padded to whole 128-column
+    groups - the patch embedding's K = 1176)."""
 
-    def __init__(self, weight: torch.Tensor, bias: torch.Tensor | None, device):
+    def __init__(self, weight: torch.Tensor, bias: torch.Tensor | None, device,
+                 path: str | None = None):
         N, K = weight.shape
-        Kp = -(-K // 128) * 128
-        w = weight.to(device=device, dtype=torch.float16)
-        if Kp != K:
-            w = torch.nn.functional.pad(w, (0, Kp - K))
-        w = w.contiguous()
-        self.packed = torch.empty_like(w)
-        call("omni_f16_pack", ptr(w), ptr(self.packed), Kp, N, 0, stream())
+        if path is None:
+            path = "pipe" if N % 128 == 0 and K % 64 == 0 and K >= 256 else "tiled"
+        if path not in ("pipe", "tiled"):
+            raise ValueError(f"unknown GEMM path {path!r}")
+        self.path = path
+        w = weight.to(device=device, dtype=torch.float16).contiguous()
         self.bias = None if bias is None else bias.to(device=device, dtype=torch.float16).contiguous()
-        self.N, self.K, self.Kp = N, K, Kp
+        self.N, self.K = N, K
+        if path == "pipe":
+            self.w, self.Kp = w, K
+        else:
+            Kp = -(-K // 128) * 128
+            if Kp != K:
+                w = torch.nn.functional.pad(w, (0, Kp - K)).contiguous()
+            self.w = torch.empty_like(w)
+            call("omni_f16_pack", ptr(w), ptr(self.w), Kp, N, 0, stream())
+            self.Kp = Kp
 
     def out(self, x: torch.Tensor, out: torch.Tensor, epilogue: int = EPI_STORE,
-            res: torch.Tensor | None = None) -> torch.Tensor:
-        require_cuda(x, out, res, dtype=torch.float16)
+            res: torch.Tensor | None = None, tile_rows: int = 0) -> torch.Tensor:
+        require_cuda(x, out, res, dtype=torch.float16, contiguous=False)
         if x.shape[1] != self.K:
             raise ValueError(f"input has {x.shape[1]} columns, the linear takes {self.K}")
-        call("omni_f16_gemm_tiled", ptr(x), x.stride(0), self.K, ptr(self.packed), ptr(self.bias),
-             ptr(res), 0 if res is None else res.stride(0), ptr(out), out.stride(0), x.shape[0],
-             self.N, self.Kp, epilogue, stream())
+        if x.stride(1) != 1 or out.stride(1) != 1 or (res is not None and res.stride(1) != 1):
+            raise ValueError("rows must be contiguous")
+        ldr = 0 if res is None else res.stride(0)
+        if self.path == "pipe":
+            call("omni_f16_gemm_pipe", ptr(x), x.stride(0), ptr(self.w), ptr(self.bias), ptr(res),
+                 ldr, ptr(out), out.stride(0), x.shape[0], self.N, self.K, epilogue, tile_rows,
+                 stream())
+        else:
+            call("omni_f16_gemm_tiled", ptr(x), x.stride(0), self.K, ptr(self.w), ptr(self.bias),
+                 ptr(res), ldr, ptr(out), out.stride(0), x.shape[0], self.N, self.Kp, epilogue,
+                 stream())
         return out
 
 
@@ -172,7 +192,7 @@ class _Block:
         f16 = lambda k: sd[p + k].to(device=device, dtype=torch.float16).contiguous()
         self.n1w, self.n1b = f16("norm1.weight"), f16("norm1.bias")
         self.n2w, self.n2b = f16("norm2.weight"), f16("norm2.bias")
-        lin = lambda k: TiledLinear(sd[p + k + ".weight"], sd[p + k + ".bias"], device)
+        lin = lambda k: VisionLinear(sd[p + k + ".weight"], sd[p + k + ".bias"], device)
         self.qkv, self.proj = lin("attn.qkv"), lin("attn.proj")
         self.fc1, self.fc2 = lin("mlp.fc1"), lin("mlp.fc2")
 
@@ -251,10 +271,10 @@ def load_vit_from_state_dict(vit: Qwen2VIT, sd: Dict[str, torch.Tensor]) -> Qwen
     pe = g("patch_embed.proj.weight").reshape(cfg.embed_dim, -1)
     if pe.shape[1] != cfg.patch_dim:
         raise ValueError(f"patch kernel has {pe.shape[1]} inputs, expected {cfg.patch_dim}")
-    vit.patch_embed = TiledLinear(pe, None, dev)
+    vit.patch_embed = VisionLinear(pe, None, dev)
     vit.blocks = [_Block(sd, f"visual.blocks.{i}.", dev) for i in range(depth)]
     f16 = lambda k: g(k).to(device=dev, dtype=torch.float16).contiguous()
     vit.lnq_w, vit.lnq_b = f16("merger.ln_q.weight"), f16("merger.ln_q.bias")
-    vit.merger_fc1 = TiledLinear(g("merger.mlp.0.weight"), g("merger.mlp.0.bias"), dev)
-    vit.merger_fc2 = TiledLinear(g("merger.mlp.2.weight"), g("merger.mlp.2.bias"), dev)
+    vit.merger_fc1 = VisionLinear(g("merger.mlp.0.weight"), g("merger.mlp.0.bias"), dev)
+    vit.merger_fc2 = VisionLinear(g("merger.mlp.2.weight"), g("merger.mlp.2.bias"), dev)
     return vit

@@ -89,21 +89,26 @@ def test_vit_attention(gpu, lens):
 # (M, N, K, epilogue, bias): the tower's shapes (patch embed K = 1176 padded to 1280)
 GEMM_CASES = [(300, 1280, 1176, 0, False), (300, 3840, 1280, 0, True), (257, 5120, 1280, 4, True),
               (64, 1280, 5120, 6, True), (75, 5120, 5120, 5, True), (75, 1536, 5120, 0, True),
-              (5, 1280, 1280, 6, True)]
+              (5, 1280, 1280, 6, True), (1, 3840, 1280, 0, True), (1024, 1280, 5120, 6, True)]
+# (path, tile_rows): the pipelined GEMM at both tile heights, the packed tiled GEMM
+PATHS = [("pipe", 128), ("pipe", 256), ("tiled", 0)]
 
 
+@pytest.mark.parametrize("path,tile_rows", PATHS)
 @pytest.mark.parametrize("M,N,K,epi,has_bias", GEMM_CASES)
-def test_gemm_tiled_epilogues(gpu, M, N, K, epi, has_bias):
+def test_gemm_epilogues(gpu, M, N, K, epi, has_bias, path, tile_rows):
     from omniserver_amd import vit
-    say(f"gemm_tiled M={M} N={N} K={K} epi={epi}")
+    if path == "pipe" and K % 64:
+        pytest.skip("the pipelined GEMM takes K % 64 == 0 (the patch embedding uses the tiled one)")
+    say(f"gemm {path}/{tile_rows} M={M} N={N} K={K} epi={epi}")
     x = f16((M, K), 6)
     w = f16((N, K), 7, 0.02)
     b = f16((N,), 8, 0.02) if has_bias else None
     res = f16((M, N), 9)
-    lin = vit.TiledLinear(w, b, gpu)
+    lin = vit.VisionLinear(w, b, gpu, path=path)
     out = res.to(gpu).clone() if epi == vit.EPI_RESID else torch.empty(M, N, device=gpu,
                                                                         dtype=torch.float16)
-    lin.out(x.to(gpu), out, epi, res=out if epi == vit.EPI_RESID else None)
+    lin.out(x.to(gpu), out, epi, res=out if epi == vit.EPI_RESID else None, tile_rows=tile_rows)
     h = vref.linear(x.float(), w.float(), None if b is None else b.float())
     if epi == vit.EPI_QGELU:
         want = vref.quick_gelu(h)
@@ -155,3 +160,76 @@ def test_vit_tower_full_depth(gpu):
     e = rel_err(got, want)
     say(f"depth 32: max rel err {e:.2e}, min cos {cos:.6f}")
     assert e <= 3e-2 and cos >= 0.999
+
+
+def test_runner_pixel_inputs_match_oracle(gpu):
+    """Image+text requests given as pixel patches (PixelInput) go through the adapter's
+    vision tower (models/qwen2_vl.py:96-97, runners/multimodal.py:124-126): the greedy
+    streams equal those of the same requests given the tower's rows as VisionInput, and the
+    packed prefill's logits with the tower's rows equal the oracle's with the vision
+    oracle's rows (splice at the image tokens, M-RoPE positions)."""
+    from tests.helpers import check_ids, compare_logits, oracle_from_gptq
+    from omniserver_amd import synth
+    from omniserver_amd.kv_cache import PreallocatedKVCache
+    from omniserver_amd.positions import IMAGE_TOKEN_ID
+    from omniserver_amd.request import PixelInput, Request, SamplingParams, Sequence, VisionInput
+    from omniserver_amd.runner import NativeQwenVLRunner
+    from omniserver_amd.vit import VisionConfig
+    from oracle import qwen2_ref as ref
+    say("runner with pixel inputs (vision depth 2, gptq decoder 2 layers)")
+    shape = synth.DecoderShape()
+    w = synth.gptq_decoder(shape, seed=21, num_layers=2)
+    vsd = synth.vision_tower(VisionConfig(), seed=22, depth=2)
+    grids = [(1, 8, 8), (1, 4, 6)]
+    prompts, pixels = [], []
+    for s, g in enumerate(grids):
+        n_img = g[0] * g[1] * g[2] // 4
+        prompts.append(synth.random_ids(7 + s, shape.vocab_size, 21, f"a{s}").tolist()
+                       + [IMAGE_TOKEN_ID] * n_img
+                       + synth.random_ids(5, shape.vocab_size, 21, f"b{s}").tolist())
+        pixels.append(synth.pixel_patches([g], VisionConfig().patch_dim, 23 + s))
+
+    def run(images_of):
+        r = NativeQwenVLRunner(max_running=2, max_len=128, use_graph=True, quant="gptq",
+                               weights=w, vision=vsd)
+        seqs = [Sequence(Request(prompt=p, images=images_of(r, i),
+                                 sampling=SamplingParams(max_new_tokens=16)))
+                for i, p in enumerate(prompts)]
+        r.prefill(seqs)
+        for _ in range(5):
+            r.decode(seqs)
+        return r, [s.output_token_ids for s in seqs]
+
+    runner, pix = run(lambda r, i: [PixelInput(pixels[i].to(gpu), grids[i])])
+    _, rows = run(lambda r, i: [VisionInput(r.adapter.vision(pixels[i].to(gpu), [grids[i]]),
+                                            grids[i])])
+    assert pix == rows and all(len(t) == 6 for t in pix)
+
+    # packed prefill logits of both prompts: tower rows (GPU) vs vision-oracle rows (CPU)
+    from oracle import qwen2_vit_ref as vr
+    ad = runner.adapter
+    emb_g, emb_o, pos_all, segs = [], [], [], []
+    for p, g, pv in zip(prompts, grids, pixels):
+        ids = torch.tensor(p)
+        mask = ids == IMAGE_TOKEN_ID
+        eg = ad.embed_tokens(ids.to(gpu))
+        eg[mask.to(gpu)] = ad.vision_embed([PixelInput(pv.to(gpu), g)])
+        eo = w["embed"][ids].float()
+        eo[mask] = vr.vit_forward(pv.float(), [g], vsd)
+        pos, _ = ad.prefill_positions(p, [g])
+        emb_g.append(eg)
+        emb_o.append(eo)
+        pos_all.append(pos)
+        segs.append(len(p))
+    pos = torch.cat(pos_all, 1)
+    pool = PreallocatedKVCache(2, 3, 2, 128, 128, gpu, n_heads=12)
+    last = (torch.tensor(segs).cumsum(0) - 1).tolist()
+    logits = ad.llm(torch.cat(emb_g).unsqueeze(0), pos.to(gpu).unsqueeze(1), None,
+                    pool.packed_prefill_cache([0, 1], segs), logits_indices=last)[0]
+    kp = [torch.zeros(3, 128, 2, 128) for _ in range(2)]
+    vp = [torch.zeros(3, 128, 2, 128) for _ in range(2)]
+    exp = oracle_from_gptq(w, shape).prefill(torch.cat(emb_o), pos, segs, [0, 1], kp, vp,
+                                             torch.zeros(3, dtype=torch.int64))
+    err, cos = compare_logits(logits, exp)
+    check_ids(torch.tensor([t[0] for t in pix]), exp, err)
+    say(f"  prefill logits vs oracle: max-abs {err:.2e} cos {cos:.6f}")

@@ -239,10 +239,15 @@ int omni_f16_gemm_tiled(const void* x, int ldx, int kx, const void* weight_packe
  * 256-row x 128-column tiles): w fp16 [N, K] in nn.Linear layout (row stride K, no
  * packing).  N % 128 == 0, K % 64 == 0, K >= 256; x, w 16-byte aligned, ldx % 8 == 0,
  * ldo / ldr % 4 == 0.  Epilogues as omni_f16_gemm_tiled; tile_rows 128, 256 or 0 (chosen
- * from the shape). */
+ * from the shape).  ksplit K slices (0: omni_f16_gemm_pipe_splits), each >= 256 of K;
+ * ksplit > 1 writes fp32 partial sums to workspace (ksplit * M * N floats, 16-byte
+ * aligned) and finishes the epilogue in a second launch (slices summed in order). */
 int omni_f16_gemm_pipe(const void* x, int ldx, const void* w, const void* bias, const void* res,
                        int ldr, void* out, int ldo, int M, int N, int K, int epilogue,
-                       int tile_rows, void* stream);
+                       int tile_rows, int ksplit, float* workspace, void* stream);
+
+/* The K slices omni_f16_gemm_pipe uses for ksplit = 0 (tile_rows as there). */
+int omni_f16_gemm_pipe_splits(int M, int N, int K, int tile_rows);
 
 /* nn.LayerNorm(N, eps) of M fp16 rows (model/qwen2_vit.py:39-40, 87): fp32 mean and biased
  * variance, y = (x - mean) rsqrt(var + eps) w + b.  N % 8 == 0, N <= 2048; out may alias x. */

@@ -33,6 +33,8 @@ struct GemmPipeArgs {
   half_t* out;
   int ldo;
   int M, N, K;
+  int KS;                // K slices; > 1: fp32 partial sums to part, finished by a second kernel
+  float* part;           // [KS][M][N]
 };
 
 template <int N>
@@ -54,10 +56,14 @@ __device__ __forceinline__ half_t gp_gelu(half_t h) {
   return (half_t)(0.5f * x * (1.0f + erff(x * 0.70710678118654752f)));
 }
 
+// One work item (output tile x K slice): per-lane operand row pointers (at the slice's
+// first k; rows clamped below M) for the four x row groups and w row group 0, the bias
+// pointer, and the slice's K steps.
 struct GpTileSrc {
   const half_t* x[4];
   const half_t* w;
   const half_t* b;
+  int kc;
 };
 
 template <int WM, int NS, int EPI>
@@ -83,10 +89,11 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
   const int tiles_n = a.N / GP_BN;
   const int tiles_m = (a.M + BM - 1) / BM;
   const int tiles = tiles_m * tiles_n;
+  const int items = tiles * a.KS;                        // slice-major: item = s tiles + tile
   const int G = gridDim.x;
   const int slot = xcd_logical_block(blockIdx.x, G);
-  const int my_tiles = (tiles - slot + G - 1) / G;       // grid <= tiles: >= 1
-  const int nk = a.K / GP_BKH;                           // >= NS (host check)
+  const int my_items = (items - slot + G - 1) / G;       // grid <= items: >= 1
+  const int nk = a.K / GP_BKH;                           // every slice has >= NS steps (host check)
 
   // Load u of this wave fills tile rows 8 NWV u + 8 wave + lane / 8; lane i writes LDS
   // slot i % 8 of its row, which holds the row's chunk (i % 8) ^ (row & 7).
@@ -95,16 +102,20 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
   typedef __attribute__((address_space(3))) void lds_void;
   typedef __attribute__((address_space(3))) uint8_t lds_u8;
   const bool has_bias = a.bias != nullptr;
-  auto tile_src = [&](int r, int& m0, int& n0) {     // past the last tile: the last one again
+  auto tile_src = [&](int r, int& m0, int& n0, int& sl) {   // past the last item: the last one again
+    const int it = min(r, my_items - 1) * G + slot;
+    sl = it / tiles;
     int tm, tn;
-    grouped_tile(min(r, my_tiles - 1) * G + slot, tiles_m, tiles_n, GP_GM, tm, tn);
+    grouped_tile(it - sl * tiles, tiles_m, tiles_n, GP_GM, tm, tn);
     m0 = tm * BM;
     n0 = tn * GP_BN;
+    const int kb = sl * nk / a.KS;
     GpTileSrc t;
+    t.kc = (sl + 1) * nk / a.KS - kb;
 #pragma unroll
     for (int u = 0; u < XLD; ++u)
-      t.x[u] = a.x + (int64_t)min(m0 + 8 * NWV * u + lrow, a.M - 1) * a.ldx + lchunk * 8;
-    t.w = a.w + (int64_t)(n0 + lrow) * a.ldw + lchunk * 8;
+      t.x[u] = a.x + (int64_t)min(m0 + 8 * NWV * u + lrow, a.M - 1) * a.ldx + kb * GP_BKH + lchunk * 8;
+    t.w = a.w + (int64_t)(n0 + lrow) * a.ldw + kb * GP_BKH + lchunk * 8;
     t.b = has_bias ? a.bias + n0 + 8 * min(lane, 15) : a.w;
     return t;
   };
@@ -178,34 +189,35 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
         : "memory");
   };
 
-  int m0c, n0c, m0n, n0n;
-  GpTileSrc cur = tile_src(0, m0c, n0c);
-  GpTileSrc nxt = tile_src(1, m0n, n0n);
+  int m0c, n0c, m0n, n0n, slc, sln;
+  GpTileSrc cur = tile_src(0, m0c, n0c, slc);
+  GpTileSrc nxt = tile_src(1, m0n, n0n, sln);
 #pragma unroll
   for (int s = 0; s < NS; ++s) issue(cur, s, s);
   gp_wait_vmcnt<OPS * (NS - 1)>();
   gp_barrier();
   int sidx = 0;
-  for (int r = 0; r < my_tiles; ++r) {
+  for (int r = 0; r < my_items; ++r) {
+    const int kc = cur.kc;
     f32x4 acc[4][4];   // [n sub-tile][m sub-tile]
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    for (int ks = 0; ks < nk; ++ks, ++sidx) {
+    for (int ks = 0; ks < kc; ++ks, ++sidx) {
       const int st = sidx % NS;
       u32x4 ops[16];
       read_issue(st, ops);
       read_wait(ops);
-      if (ks == nk - 1 && has_bias) read_bias(st);
+      if (ks == kc - 1 && has_bias) read_bias(st);
       // step sidx + 1 has landed for this thread, then for everyone; every wave has also
       // read step sidx's slot, which is refilled with step sidx + NS
       gp_wait_vmcnt<OPS * (NS - 2)>();
       gp_barrier();
       {
         const int iks = ks + NS;
-        if (iks < nk) issue(cur, iks, st);
-        else issue(nxt, iks - nk, st);
+        if (iks < kc) issue(cur, iks, st);
+        else issue(nxt, iks - kc, st);
       }
 #pragma unroll
       for (int t = 0; t < 2; ++t)
@@ -224,6 +236,14 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
     for (int j = 0; j < 4; ++j) {
       const int m = m0c + 64 * wm + 16 * j + l16;
       if (m >= a.M) continue;
+      if (a.KS > 1) {                    // the slice's fp32 partial sums
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int n = n0c + 64 * wn + 16 * i + 4 * g4;
+          *(f32x4*)(a.part + ((int64_t)slc * a.M + m) * a.N + n) = acc[i][j];
+        }
+        continue;
+      }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int n = n0c + 64 * wn + 16 * i + 4 * g4;
@@ -245,7 +265,8 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
     cur = nxt;
     m0c = m0n;
     n0c = n0n;
-    nxt = tile_src(r + 2, m0n, n0n);
+    slc = sln;
+    nxt = tile_src(r + 2, m0n, n0n, sln);
   }
   gp_wait_vmcnt<0>();                  // drain the clamped tail loads before exit
 }
@@ -262,12 +283,57 @@ static int gp_num_cus() {
   return n;
 }
 
+// Split-K finish: out = epi(fp16(sum_s part[s] + bias)), slices summed in order; one
+// thread per 4 consecutive columns.
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_pipe_finish_kernel(GemmPipeArgs a) {
+#pragma clang fp contract(off)
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int nq = a.N >> 2;
+  if (i >= (int64_t)a.M * nq) return;
+  const int m = (int)(i / nq), n = (int)(i - (int64_t)m * nq) * 4;
+  f32x4 v = *(const f32x4*)(a.part + (int64_t)m * a.N + n);
+  for (int s = 1; s < a.KS; ++s) {
+    const f32x4 p = *(const f32x4*)(a.part + ((int64_t)s * a.M + m) * a.N + n);
+    v = (f32x4){v[0] + p[0], v[1] + p[1], v[2] + p[2], v[3] + p[3]};
+  }
+  half4_t bb = (half4_t){0, 0, 0, 0};
+  if (a.bias) bb = *(const half4_t*)(a.bias + n);
+  half4_t rr = (half4_t){0, 0, 0, 0};
+  if constexpr (EPI == GP_RESID) rr = *(const half4_t*)(a.res + (int64_t)m * a.ldr + n);
+  half4_t o;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    half_t h = a.bias ? (half_t)(v[q] + (float)bb[q]) : (half_t)v[q];
+    if constexpr (EPI == GP_QGELU) h = gp_quick_gelu(h);
+    if constexpr (EPI == GP_GELU) h = gp_gelu(h);
+    if constexpr (EPI == GP_RESID) h = (half_t)((float)rr[q] + (float)h);
+    o[q] = h;
+  }
+  *(half4_t*)(a.out + (int64_t)m * a.ldo + n) = o;
+}
+
 template <int WM, int NS>
 static int gp_launch(const GemmPipeArgs& a, int epilogue, hipStream_t st) {
-  const int64_t tiles = (int64_t)ceil_div(a.M, 64 * WM) * (a.N / GP_BN);
-  if (tiles > 0x7fffffff) return OMNI_EUNSUPPORTED;
-  const int grid = (int)(tiles < gp_num_cus() ? tiles : gp_num_cus());
+  const int64_t items = (int64_t)ceil_div(a.M, 64 * WM) * (a.N / GP_BN) * a.KS;
+  if (items > 0x7fffffff) return OMNI_EUNSUPPORTED;
+  const int grid = (int)(items < gp_num_cus() ? items : gp_num_cus());
   const dim3 blk(128 * WM);
+  if (a.KS > 1) {                    // partial sums, then the finish kernel's epilogue
+    hipLaunchKernelGGL((gemm_pipe_kernel<WM, NS, GP_STORE>), dim3(grid), blk, 0, st, a);
+    OMNI_CHECK_LAUNCH();
+    const int64_t nthr = (int64_t)a.M * (a.N / 4);
+    const dim3 fg((unsigned)((nthr + 255) / 256));
+    switch (epilogue) {
+      case GP_STORE: hipLaunchKernelGGL((gemm_pipe_finish_kernel<GP_STORE>), fg, dim3(256), 0, st, a); break;
+      case GP_QGELU: hipLaunchKernelGGL((gemm_pipe_finish_kernel<GP_QGELU>), fg, dim3(256), 0, st, a); break;
+      case GP_GELU: hipLaunchKernelGGL((gemm_pipe_finish_kernel<GP_GELU>), fg, dim3(256), 0, st, a); break;
+      case GP_RESID: hipLaunchKernelGGL((gemm_pipe_finish_kernel<GP_RESID>), fg, dim3(256), 0, st, a); break;
+      default: return OMNI_EINVAL;
+    }
+    OMNI_CHECK_LAUNCH();
+    return OMNI_OK;
+  }
   switch (epilogue) {
     case GP_STORE: hipLaunchKernelGGL((gemm_pipe_kernel<WM, NS, GP_STORE>), dim3(grid), blk, 0, st, a); break;
     case GP_QGELU: hipLaunchKernelGGL((gemm_pipe_kernel<WM, NS, GP_QGELU>), dim3(grid), blk, 0, st, a); break;
@@ -279,21 +345,48 @@ static int gp_launch(const GemmPipeArgs& a, int epilogue, hipStream_t st) {
   return OMNI_OK;
 }
 
+static int gp_tile_rows(int M, int N) {
+  // 256-row tiles when they still give every CU a tile
+  const int64_t t256 = (int64_t)ceil_div(M, 256) * (N / GP_BN);
+  return t256 >= gp_num_cus() ? 256 : 128;
+}
+
+// K slices for (M, N, K) at the given tile height (0: chosen): more slices while the
+// tiles alone leave over a quarter of the CUs idle and every slice keeps >= 8 K steps.
+extern "C" int omni_f16_gemm_pipe_splits(int M, int N, int K, int tile_rows) {
+  if (M <= 0 || N <= 0 || K <= 0 || (N % GP_BN) || (K % GP_BKH)) return 1;
+  if (tile_rows == 0) tile_rows = gp_tile_rows(M, N);
+  const int64_t tiles = (int64_t)ceil_div(M, tile_rows) * (N / GP_BN);
+  const int nk = K / GP_BKH;
+  int ks = 1;
+  while (ks < 8 && tiles * ks * 4 < 3 * (int64_t)gp_num_cus() && nk / (ks + 1) >= 8) ++ks;
+  return ks;
+}
+
 // out = epi(fp16(x . w^T + bias)) with w fp16 [N, K] in nn.Linear layout (row stride K).
 // N % 128 == 0, K % 64 == 0 and K >= 256; x, w 16-byte aligned with ldx % 8 == 0;
-// ldo, ldr % 4 == 0.  tile_rows 128 or 256 (0: chosen from the shape).
+// ldo, ldr % 4 == 0.  tile_rows 128 or 256 (0: chosen from the shape).  ksplit K slices
+// (0: omni_f16_gemm_pipe_splits; each slice >= 4 K steps of 64); ksplit > 1 needs an fp32
+// workspace of ksplit * M * N floats (16-byte aligned).
 extern "C" int omni_f16_gemm_pipe(const void* x, int ldx, const void* w, const void* bias,
                                   const void* res, int ldr, void* out, int ldo, int M, int N,
-                                  int K, int epilogue, int tile_rows, void* stream) {
-  if (M < 0 || N <= 0 || K <= 0) return OMNI_EINVAL;
+                                  int K, int epilogue, int tile_rows, int ksplit,
+                                  float* workspace, void* stream) {
+  if (M < 0 || N <= 0 || K <= 0 || ksplit < 0) return OMNI_EINVAL;
   if ((N % GP_BN) || (K % GP_BKH) || K < 4 * GP_BKH) return OMNI_EUNSUPPORTED;
   if (M == 0) return OMNI_OK;
   if (!x || !w || !out) return OMNI_EINVAL;
   if (ldx < K || (ldx & 7) || ldo < N || (ldo & 3)) return OMNI_EINVAL;
   if (((uintptr_t)x & 15) || ((uintptr_t)w & 15) || ((uintptr_t)out & 7)) return OMNI_EINVAL;
   if (epilogue == GP_RESID && (!res || ldr < N || (ldr & 3) || ((uintptr_t)res & 7))) return OMNI_EINVAL;
+  if (epilogue != GP_STORE && epilogue != GP_QGELU && epilogue != GP_GELU && epilogue != GP_RESID)
+    return OMNI_EINVAL;
   if (bias && ((uintptr_t)bias & 15)) return OMNI_EINVAL;
   if (tile_rows != 0 && tile_rows != 128 && tile_rows != 256) return OMNI_EINVAL;
+  if (tile_rows == 0) tile_rows = gp_tile_rows(M, N);
+  if (ksplit == 0) ksplit = omni_f16_gemm_pipe_splits(M, N, K, tile_rows);
+  if (K / GP_BKH / ksplit < 4) return OMNI_EUNSUPPORTED;       // every slice >= NS steps
+  if (ksplit > 1 && (!workspace || ((uintptr_t)workspace & 15))) return OMNI_EINVAL;
   GemmPipeArgs a;
   a.x = (const half_t*)x;
   a.ldx = ldx;
@@ -307,11 +400,8 @@ extern "C" int omni_f16_gemm_pipe(const void* x, int ldx, const void* w, const v
   a.M = M;
   a.N = N;
   a.K = K;
-  if (tile_rows == 0) {
-    // 256-row tiles when they still give every CU a tile
-    const int64_t t256 = (int64_t)ceil_div(M, 256) * (N / GP_BN);
-    tile_rows = t256 >= gp_num_cus() ? 256 : 128;
-  }
+  a.KS = ksplit;
+  a.part = workspace;
   hipStream_t st = (hipStream_t)stream;
   return tile_rows == 256 ? gp_launch<4, 3>(a, epilogue, st) : gp_launch<2, 4>(a, epilogue, st);
 }

@@ -21,7 +21,7 @@ from typing import Dict, List, Sequence, Tuple
 
 import torch
 
-from ._lib import call, ptr, require_cuda, stream
+from ._lib import call, lib, ptr, require_cuda, stream
 
 EPI_STORE, EPI_QGELU, EPI_GELU, EPI_RESID = 0, 4, 5, 6
 _QT = 64     # queries per attention workgroup (the kernel's tile)
@@ -155,6 +155,7 @@ class VisionLinear:
         if path not in ("pipe", "tiled"):
             raise ValueError(f"unknown GEMM path {path!r}")
         self.path = path
+        self._ws = None
         w = weight.to(device=device, dtype=torch.float16).contiguous()
         self.bias = None if bias is None else bias.to(device=device, dtype=torch.float16).contiguous()
         self.N, self.K = N, K
@@ -169,7 +170,8 @@ class VisionLinear:
             self.Kp = Kp
 
     def out(self, x: torch.Tensor, out: torch.Tensor, epilogue: int = EPI_STORE,
-            res: torch.Tensor | None = None, tile_rows: int = 0) -> torch.Tensor:
+            res: torch.Tensor | None = None, tile_rows: int = 0,
+            ksplit: int = 0) -> torch.Tensor:
         require_cuda(x, out, res, dtype=torch.float16, contiguous=False)
         if x.shape[1] != self.K:
             raise ValueError(f"input has {x.shape[1]} columns, the linear takes {self.K}")
@@ -177,9 +179,17 @@ class VisionLinear:
             raise ValueError("rows must be contiguous")
         ldr = 0 if res is None else res.stride(0)
         if self.path == "pipe":
+            M = x.shape[0]
+            ks = ksplit or lib().omni_f16_gemm_pipe_splits(M, self.N, self.K, tile_rows)
+            ws = None
+            if ks > 1:      # fp32 partial sums of the K slices
+                need = ks * M * self.N
+                if self._ws is None or self._ws.numel() < need:
+                    self._ws = torch.empty(need, device=x.device, dtype=torch.float32)
+                ws = self._ws
             call("omni_f16_gemm_pipe", ptr(x), x.stride(0), ptr(self.w), ptr(self.bias), ptr(res),
-                 ldr, ptr(out), out.stride(0), x.shape[0], self.N, self.K, epilogue, tile_rows,
-                 stream())
+                 ldr, ptr(out), out.stride(0), M, self.N, self.K, epilogue, tile_rows, ks,
+                 ptr(ws), stream())
         else:
             call("omni_f16_gemm_tiled", ptr(x), x.stride(0), self.K, ptr(self.w), ptr(self.bias),
                  ptr(res), ldr, ptr(out), out.stride(0), x.shape[0], self.N, self.Kp, epilogue,

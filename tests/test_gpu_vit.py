@@ -90,17 +90,20 @@ def test_vit_attention(gpu, lens):
 GEMM_CASES = [(300, 1280, 1176, 0, False), (300, 3840, 1280, 0, True), (257, 5120, 1280, 4, True),
               (64, 1280, 5120, 6, True), (75, 5120, 5120, 5, True), (75, 1536, 5120, 0, True),
               (5, 1280, 1280, 6, True), (1, 3840, 1280, 0, True), (1024, 1280, 5120, 6, True)]
-# (path, tile_rows): the pipelined GEMM at both tile heights, the packed tiled GEMM
-PATHS = [("pipe", 128), ("pipe", 256), ("tiled", 0)]
+# (path, tile_rows, ksplit): the pipelined GEMM at both tile heights, without and with
+# K slices (0 = its own choice), the packed tiled GEMM
+PATHS = [("pipe", 128, 1), ("pipe", 256, 1), ("pipe", 128, 0), ("pipe", 256, 3), ("tiled", 0, 0)]
 
 
-@pytest.mark.parametrize("path,tile_rows", PATHS)
+@pytest.mark.parametrize("path,tile_rows,ksplit", PATHS)
 @pytest.mark.parametrize("M,N,K,epi,has_bias", GEMM_CASES)
-def test_gemm_epilogues(gpu, M, N, K, epi, has_bias, path, tile_rows):
+def test_gemm_epilogues(gpu, M, N, K, epi, has_bias, path, tile_rows, ksplit):
     from omniserver_amd import vit
     if path == "pipe" and K % 64:
         pytest.skip("the pipelined GEMM takes K % 64 == 0 (the patch embedding uses the tiled one)")
-    say(f"gemm {path}/{tile_rows} M={M} N={N} K={K} epi={epi}")
+    if path == "pipe" and K // 64 // max(ksplit, 1) < 4:
+        pytest.skip("slices below 4 K steps")
+    say(f"gemm {path}/{tile_rows}/ks{ksplit} M={M} N={N} K={K} epi={epi}")
     x = f16((M, K), 6)
     w = f16((N, K), 7, 0.02)
     b = f16((N,), 8, 0.02) if has_bias else None
@@ -108,7 +111,8 @@ def test_gemm_epilogues(gpu, M, N, K, epi, has_bias, path, tile_rows):
     lin = vit.VisionLinear(w, b, gpu, path=path)
     out = res.to(gpu).clone() if epi == vit.EPI_RESID else torch.empty(M, N, device=gpu,
                                                                         dtype=torch.float16)
-    lin.out(x.to(gpu), out, epi, res=out if epi == vit.EPI_RESID else None, tile_rows=tile_rows)
+    lin.out(x.to(gpu), out, epi, res=out if epi == vit.EPI_RESID else None, tile_rows=tile_rows,
+            ksplit=ksplit)
     h = vref.linear(x.float(), w.float(), None if b is None else b.float())
     if epi == vit.EPI_QGELU:
         want = vref.quick_gelu(h)

@@ -76,15 +76,17 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def build_config3(device, batch: int = 32, ctx: int = 2048, max_len: int = 4096, seed: int = 0):
+def build_config3(device, batch: int = 32, ctx: int = 2048, max_len: int = 4096, seed: int = 0,
+                  w=None):
     from omniserver_amd import synth
     from omniserver_amd.request import Request, SamplingParams, Sequence
     from omniserver_amd.runner import NativeQwenVLRunner
 
     shape = synth.DecoderShape()
-    t0 = time.time()
-    w = synth.gptq_decoder(shape, seed=seed)
-    log(f"synthetic int4 weights generated in {time.time() - t0:.1f}s")
+    if w is None:
+        t0 = time.time()
+        w = synth.gptq_decoder(shape, seed=seed)
+        log(f"synthetic int4 weights generated in {time.time() - t0:.1f}s")
     runner = NativeQwenVLRunner(max_running=batch, max_len=max_len, use_graph=True,
                                 quant="gptq", weights=w)
     pool = runner.pool
@@ -230,6 +232,40 @@ def fp8_layer_gemms(device, M: int = 8192, reps: int = 10) -> dict:
             "per_shape": per}
 
 
+def decode_b1(device, w, ctx: int = 2048, steps: int = 64) -> dict:
+    """The metric's B = 1 case: the same int4 decoder and weights, one sequence at a 2048-token
+    context (pool [1, 4096, 2, 128] fp16), greedy hipGraph steps; algorithmic bytes per step
+    (weights once + the sequence's KV) against the 8 TB/s HBM peak."""
+    runner, seqs, _, _ = build_config3(device, 1, ctx, w=w)
+    for _ in range(3):
+        runner.decode(seqs)
+    torch.cuda.synchronize()
+    ahead = runner.steps_ahead()
+    ctx0 = int(runner.pool.lengths[0]) - ahead
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        runner.decode(seqs)
+    torch.cuda.synchronize()
+    per = (time.perf_counter() - t0) / steps
+    runner.settle()
+    g = runner._graphs[1][0]
+    st = torch.cuda.current_stream()
+    r0, r1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    r0.record(st)
+    for _ in range(16):
+        g.replay()
+    r1.record(st)
+    torch.cuda.synchronize()
+    nbytes = sum(step_bytes("gptq", [ctx0 + s]) for s in range(steps)) / steps
+    out = {"workload": f"int4 decode B=1, ctx {ctx}", "ms_per_step": round(per * 1e3, 4),
+           "tok_per_s": round(1.0 / per, 1), "graph_replay_ms": round(r0.elapsed_time(r1) / 16, 4),
+           "bytes_per_step": int(nbytes), "achieved_GBps": round(nbytes / per / 1e9, 1),
+           "frac": round(nbytes / per / PEAK_HBM, 4)}
+    del runner, seqs
+    torch.cuda.empty_cache()
+    return out
+
+
 def vit_flops(grids, cfg) -> float:
     """Dense FLOPs of one vision-tower forward (model/qwen2_vit.py:118-129): the patch
     embedding (K = 1176), per block the four linears and the two attention products within
@@ -310,6 +346,7 @@ def main():
     ap.add_argument("--no-fp8", action="store_true",
                     help="skip the FP8 W8A8 GEMM leg (BASELINE configs[3])")
     ap.add_argument("--no-vit", action="store_true", help="skip the vision-tower leg")
+    ap.add_argument("--no-b1", action="store_true", help="skip the B = 1 decode leg")
     ap.add_argument("--vit-only", action="store_true",
                     help="time only the vision tower (one JSON object) and exit")
     ap.add_argument("--kernel-reps", type=int, default=20)
@@ -434,10 +471,16 @@ def main():
             "gate_up_w4a16_silu_us": round(t_gu * 1e6, 2),
             "gate_up_GBps": round(gu_bytes / t_gu / 1e9, 1),
         },
+        "b1": None,
         "fp8_gemm": None,
         "vit": None,
         "cpu_baseline": None,
     }
+    if not args.no_b1:
+        try:
+            out["b1"] = decode_b1(dev, w, args.ctx)
+        except Exception as e:  # report, never fail the decode line on this leg
+            out["b1"] = {"error": repr(e)}
     if not args.no_fp8:
         try:
             out["fp8_gemm"] = fp8_layer_gemms(dev)

@@ -266,6 +266,129 @@ def decode_b1(device, w, ctx: int = 2048, steps: int = 64) -> dict:
     return out
 
 
+def _timed_decode(runner, seqs, steps: int, warmup: int = 3):
+    """(wall ms per step, graph replay ms, pre-step contexts) of `steps` greedy decode steps."""
+    for _ in range(warmup):
+        runner.decode(seqs)
+    torch.cuda.synchronize()
+    B = len(seqs)
+    ahead = runner.steps_ahead()
+    ctx0 = [L - ahead for L in runner.pool.lengths[:B].cpu().tolist()]
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        runner.decode(seqs)
+    torch.cuda.synchronize()
+    per = (time.perf_counter() - t0) / steps
+    runner.settle()
+    g = runner._graphs[B][0]
+    st = torch.cuda.current_stream()
+    r0, r1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    r0.record(st)
+    for _ in range(8):
+        g.replay()
+    r1.record(st)
+    torch.cuda.synchronize()
+    return per * 1e3, r0.elapsed_time(r1) / 8, ctx0
+
+
+def _decode_line(quant, per_ms, replay_ms, ctx0, steps):
+    B = len(ctx0)
+    nbytes = sum(step_bytes(quant, [L + s for L in ctx0]) for s in range(steps)) / steps
+    return {"ms_per_step": round(per_ms, 4), "tok_per_s": round(B / per_ms * 1e3, 1),
+            "graph_replay_ms": round(replay_ms, 4), "bytes_per_step": int(nbytes),
+            "frac": round(nbytes / (per_ms / 1e3) / PEAK_HBM, 4)}
+
+
+def baseline_configs(device, w_int4) -> dict:
+    """BASELINE configs[0], [1] and [4] end to end with their own shapes (configs[2] is the
+    headline line, configs[3] the fp8_gemm object): seeded synthetic weights, hipGraph
+    decode, decode rates against the HBM peak, the packed prefill against the fp16 MFMA
+    peak."""
+    from omniserver_amd import synth
+    from omniserver_amd.positions import IMAGE_TOKEN_ID
+    from omniserver_amd.request import Request, SamplingParams, Sequence, VisionInput
+    from omniserver_amd.runner import NativeQwenVLRunner
+    shape = synth.DecoderShape()
+    mk = lambda ids, **kw: Sequence(Request(prompt=ids, sampling=SamplingParams(max_new_tokens=1 << 30), **kw))
+    out = {}
+    t0 = time.time()
+    w16 = synth.fp16_decoder(shape, seed=1)
+    log(f"synthetic fp16 weights generated in {time.time() - t0:.1f}s")
+
+    # configs[0]: fp16, batch 1, 256-token prompt, 32 new tokens
+    r = NativeQwenVLRunner(max_running=1, max_len=1024, use_graph=True, weights=w16)
+    seqs = [mk(synth.random_ids(256, shape.vocab_size, 1, "c1").tolist())]
+    r.prefill(seqs)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    r.free(seqs[0])
+    seqs = [mk(synth.random_ids(256, shape.vocab_size, 1, "c1").tolist())]
+    r.prefill(seqs)
+    torch.cuda.synchronize()
+    pre_ms = (time.perf_counter() - t1) * 1e3
+    per, rep, ctx0 = _timed_decode(r, seqs, 32)
+    out["config1"] = {"workload": "fp16 decoder, B=1, 256-token prompt, 32 greedy steps",
+                      "prefill_ms": round(pre_ms, 3), **_decode_line("fp16", per, rep, ctx0, 32)}
+    del r, seqs
+
+    # configs[1]: fp16, batch 16, contexts U[512, 2048], pool [16, 4096], 64 steps
+    B = 16
+    lens = synth.context_lengths(B, 512, 2048, 2).tolist()
+    r = NativeQwenVLRunner(max_running=B, max_len=4096, use_graph=True, weights=w16)
+    g = torch.Generator(device=device)
+    g.manual_seed(3)
+    for l in range(NL):
+        for kv in (0, 1):
+            for b, L in enumerate(lens):
+                r.pool.storage[l, kv, b, :L].normal_(generator=g)
+    seqs = [mk(synth.random_ids(4, shape.vocab_size, 2, f"c2.{b}").tolist()) for b in range(B)]
+    for s_ in seqs:
+        r.tokenize(s_)
+    r.attach_prefilled(seqs, lens)
+    per, rep, ctx0 = _timed_decode(r, seqs, 64)
+    out["config2"] = {"workload": "fp16 decoder, B=16, contexts U[512, 2048], 64 greedy steps",
+                      **_decode_line("fp16", per, rep, ctx0, 64)}
+    del r, seqs, w16
+    torch.cuda.empty_cache()
+
+    # configs[4]: int4, 8 x [64 text, 256 vision rows (grid 1 x 32 x 32), 192 text] packed
+    # prefill (T = 4096, block-diagonal causal), then 128 greedy steps at B = 8
+    B = 8
+    r = NativeQwenVLRunner(max_running=B, max_len=4096, use_graph=True, quant="gptq", weights=w_int4)
+    def mm_seqs():
+        ss = []
+        for b in range(B):
+            ids = (synth.random_ids(64, shape.vocab_size, 5, f"c5a.{b}").tolist() + [IMAGE_TOKEN_ID] * 256
+                   + synth.random_ids(192, shape.vocab_size, 5, f"c5b.{b}").tolist())
+            rows = synth.randn16((256, shape.hidden_size), 1.0, 5, f"c5v.{b}").to(device)
+            ss.append(mk(ids, images=[VisionInput(rows, (1, 32, 32))]))
+        return ss
+    seqs = mm_seqs()
+    r.prefill(seqs)                        # warm-up (first use of the prefill kernels)
+    torch.cuda.synchronize()
+    for s_ in seqs:
+        r.free(s_)
+    seqs = mm_seqs()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    r.prefill(seqs)
+    torch.cuda.synchronize()
+    pre = time.perf_counter() - t1
+    T = 512 * B
+    lin = sum(2.0 * T * K * N for K, N in LINEARS) * NL
+    att = NL * B * 4.0 * (512 * 513 / 2) * NH * HD
+    per, rep, ctx0 = _timed_decode(r, seqs, 128)
+    out["config5"] = {"workload": "int4 decoder, 8 x 512-token image+text prompts: packed prefill "
+                                  "(T = 4096), then 128 greedy steps at B = 8",
+                      "prefill_ms": round(pre * 1e3, 3), "prefill_tok_per_s": round(T / pre, 1),
+                      "prefill_tflops": round((lin + att) / pre / 1e12, 1),
+                      "prefill_frac_fp16_peak": round((lin + att) / pre / PEAK_FP16, 4),
+                      **_decode_line("gptq", per, rep, ctx0, 128)}
+    del r, seqs
+    torch.cuda.empty_cache()
+    return out
+
+
 def vit_flops(grids, cfg) -> float:
     """Dense FLOPs of one vision-tower forward (model/qwen2_vit.py:118-129): the patch
     embedding (K = 1176), per block the four linears and the two attention products within
@@ -347,6 +470,8 @@ def main():
                     help="skip the FP8 W8A8 GEMM leg (BASELINE configs[3])")
     ap.add_argument("--no-vit", action="store_true", help="skip the vision-tower leg")
     ap.add_argument("--no-b1", action="store_true", help="skip the B = 1 decode leg")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip BASELINE configs[0], [1], [4] (fp16 B=1 / B=16, multimodal)")
     ap.add_argument("--vit-only", action="store_true",
                     help="time only the vision tower (one JSON object) and exit")
     ap.add_argument("--kernel-reps", type=int, default=20)
@@ -472,6 +597,7 @@ def main():
             "gate_up_GBps": round(gu_bytes / t_gu / 1e9, 1),
         },
         "b1": None,
+        "baseline_configs": None,
         "fp8_gemm": None,
         "vit": None,
         "cpu_baseline": None,
@@ -481,6 +607,11 @@ def main():
             out["b1"] = decode_b1(dev, w, args.ctx)
         except Exception as e:  # report, never fail the decode line on this leg
             out["b1"] = {"error": repr(e)}
+    if not args.no_configs:
+        try:
+            out["baseline_configs"] = baseline_configs(dev, w)
+        except Exception as e:  # report, never fail the decode line on this leg
+            out["baseline_configs"] = {"error": repr(e)}
     if not args.no_fp8:
         try:
             out["fp8_gemm"] = fp8_layer_gemms(dev)

@@ -16,7 +16,7 @@ The JSON line also carries:
   step's algorithmic bytes): algorithmic bytes per launch / its mean duration,
   timed with HIP events on the stream it runs on, against 8 TB/s;
 * ``step_roofline``: algorithmic bytes per step / ms_per_step against 8 TB/s;
-* ``fp8_gemm``: BASELINE configs[3], the FP8 W8A8 linears of one decoder layer at
+* ``fp8_gemm``: BASELINE.json configs[3], the FP8 W8A8 linears of one decoder layer at
   M = 8192 (achieved dense TFLOP/s against the 5.0 PFLOP/s fp8 MFMA peak);
 * ``cpu_baseline``: the fp32 CPU restatement (oracle/) of the same step, timed on
   this host on a bounded sample.
@@ -203,7 +203,7 @@ def traffic_from_profiles(kernel: str):
 
 
 def fp8_layer_gemms(device, M: int = 8192, reps: int = 10) -> dict:
-    """BASELINE configs[3]: the FP8 e4m3fn W8A8 linears of one decoder layer on a packed
+    """BASELINE.json configs[3]: the FP8 e4m3fn W8A8 linears of one decoder layer on a packed
     8 x 1024-token prefill (M = 8192): QKV 1536->2048, O 1536->1536, gate/up 1536->17920,
     down 8960->1536.  Weights N(0, 0.02) quantised per output channel, activations N(0, 1)
     quantised per token; the timed region is the fp8 MFMA GEMM (fp32 accumulate, bf16 ->
@@ -300,7 +300,7 @@ def _decode_line(quant, per_ms, replay_ms, ctx0, steps):
 
 
 def baseline_configs(device, w_int4) -> dict:
-    """BASELINE configs[0], [1] and [4] end to end with their own shapes (configs[2] is the
+    """BASELINE.json configs[0], [1] and [4] end to end with their own shapes (configs[2] is the
     headline line, configs[3] the fp8_gemm object): seeded synthetic weights, hipGraph
     decode, decode rates against the HBM peak, the packed prefill against the fp16 MFMA
     peak."""
@@ -467,11 +467,11 @@ def main():
     ap.add_argument("--ctx", type=int, default=2048)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-fp8", action="store_true",
-                    help="skip the FP8 W8A8 GEMM leg (BASELINE configs[3])")
+                    help="skip the FP8 W8A8 GEMM leg (BASELINE.json configs[3])")
     ap.add_argument("--no-vit", action="store_true", help="skip the vision-tower leg")
     ap.add_argument("--no-b1", action="store_true", help="skip the B = 1 decode leg")
     ap.add_argument("--no-configs", action="store_true",
-                    help="skip BASELINE configs[0], [1], [4] (fp16 B=1 / B=16, multimodal)")
+                    help="skip BASELINE.json configs[0], [1], [4] (fp16 B=1 / B=16, multimodal)")
     ap.add_argument("--vit-only", action="store_true",
                     help="time only the vision tower (one JSON object) and exit")
     ap.add_argument("--kernel-reps", type=int, default=20)

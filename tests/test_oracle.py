@@ -11,7 +11,7 @@ pinned by something independent of how it is written:
   apply_mrope (t = h = w)   textbook RoPE as a complex rotation of (x_d, x_{d+64})
   apply_mrope (3-D)         each section follows only its own axis (dims [0,16)+[64,80) ->
                             t, [16,40)+[80,104) -> h, [40,64)+[104,128) -> w)
-  mrope_position_ids        text-only = arange / delta 0; BASELINE config-5 closed form
+  mrope_position_ids        text-only = arange / delta 0; BASELINE.json config-5 closed form
                             (image t=64, h=w=64+0..15, text resumes at 80, delta -240);
                             two images; product implementation equal
   gptq pack/dequant         bit-level brute force with Python ints; round trip

@@ -16,12 +16,17 @@ The JSON line also carries:
   step's algorithmic bytes): algorithmic bytes per launch / its mean duration,
   timed with HIP events on the stream it runs on, against 8 TB/s;
 * ``step_roofline``: algorithmic bytes per step / ms_per_step against 8 TB/s;
+* ``b1``: the metric's B = 1 case (same int4 weights, one sequence at ctx 2048);
+* ``baseline_configs``: BASELINE.json configs[0], [1], [4] with their own shapes (fp16
+  B = 1 prefill + decode, fp16 B = 16 decode, multimodal packed prefill + B = 8 decode);
 * ``fp8_gemm``: BASELINE.json configs[3], the FP8 W8A8 linears of one decoder layer at
   M = 8192 (achieved dense TFLOP/s against the 5.0 PFLOP/s fp8 MFMA peak);
+* ``vit``: the vision tower on one 448 x 448 image (TFLOP/s against the fp16 peak);
 * ``cpu_baseline``: the fp32 CPU restatement (oracle/) of the same step, timed on
   this host on a bounded sample.
 
 Usage: python bench.py [--gpus 1] [--steps 128] [--warmup 3] [--no-cpu] [--no-fp8]
+       [--no-vit] [--no-b1] [--no-configs] [--vit-only] [--pmc-probe]
 """
 
 from __future__ import annotations

@@ -438,6 +438,192 @@ __global__ __launch_bounds__(128 * WM, 1) void fp8_gemm_pipe_kernel(Fp8GemmArgs 
   wait_vmcnt<0>();                     // drain the clamped tail loads before exit
 }
 
+// Large-tile form: 256 x 256 output tiles, 4 waves (one per SIMD) each owning a 128 (m) x
+// 128 (n) block, so every operand byte staged through LDS feeds twice the MFMA work of the
+// 64 x 64 blocks above (a 256 x 128 tile re-reads its operand rows from L2 for every
+// 128 columns; this one for every 256).  Per K step a wave issues 32 operand reads (32 bytes
+// per lane of 8 w and 8 x row groups) and 64 MFMAs; two stages of 64 KB each are in LDS
+// (the next step's operands land while this step's MFMAs run).  Same staging (direct
+// global->LDS loads, XOR-swizzled 128-byte rows), tile order and epilogue as the kernel
+// above.
+#define F8B_T 256
+
+template <int NS>
+__global__ __launch_bounds__(256, 1) void fp8_gemm_big_kernel(Fp8GemmArgs a) {
+#pragma clang fp contract(off)
+  constexpr int XLD = 8;                      // x loads per wave and stage (256 rows / 8 / 4)
+  constexpr int WLD = 8;                      // w loads per wave and stage
+  constexpr int OPS = XLD + WLD;              // loads every thread issues per stage
+  __shared__ __attribute__((aligned(1024))) uint8_t xl[NS][F8B_T * F8_ROWB];
+  __shared__ __attribute__((aligned(1024))) uint8_t wl[NS][F8B_T * F8_ROWB];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wave & 1;
+  const int wm = wave >> 1;
+  const int l16 = lane & 15;
+  const int g4 = lane >> 4;
+
+  const int tiles_n = a.N / F8B_T;
+  const int tiles_m = (a.M + F8B_T - 1) / F8B_T;
+  const int tiles = tiles_m * tiles_n;
+  const int G = gridDim.x;
+  const int slot = xcd_logical_block(blockIdx.x, G);
+  const int my_tiles = (tiles - slot + G - 1) / G;          // grid <= tiles: >= 1
+  const int nk = a.K / F8_BK;                               // >= NS (host check)
+
+  // Load u of this wave fills tile rows 32 u + 8 wave + lane / 8 (LDS slot lane % 8 holds
+  // the row's chunk (lane % 8) ^ (row & 7)).  M % 256 == 0 (host check): no row clamping,
+  // so one x pointer per tile serves every load.
+  const int lrow = 8 * wave + (lane >> 3);
+  const int lchunk = (lane & 7) ^ (lrow & 7);
+  typedef __attribute__((address_space(3))) void lds_void;
+  typedef __attribute__((address_space(3))) uint8_t lds_u8;
+  const bool has_bias = a.bias != nullptr;
+  struct Src {
+    const uint8_t* x;
+    const uint8_t* w;
+  };
+  auto tile_src = [&](int r, int& m0, int& n0) {
+    int tm, tn;
+    grouped_tile(min(r, my_tiles - 1) * G + slot, tiles_m, tiles_n, F8_GM, tm, tn);
+    m0 = tm * F8B_T;
+    n0 = tn * F8B_T;
+    Src t;
+    t.x = a.xq + (int64_t)(m0 + lrow) * a.K + lchunk * 16;
+    t.w = a.wq + (int64_t)(n0 + lrow) * a.K + lchunk * 16;
+    return t;
+  };
+  const int64_t rstep = (int64_t)32 * a.K;          // bytes between row groups
+  auto issue = [&](const Src& t, int ks, int st) {
+    const int k0 = ks * F8_BK;
+#pragma unroll
+    for (int u = 0; u < XLD; ++u)
+      __builtin_amdgcn_global_load_lds((const void*)(t.x + u * rstep + k0),
+                                       (lds_void*)((lds_u8*)&xl[st][(32 * u + 8 * wave) * F8_ROWB]), 16, 0, 0);
+#pragma unroll
+    for (int u = 0; u < WLD; ++u)
+      __builtin_amdgcn_global_load_lds((const void*)(t.w + u * rstep + k0),
+                                       (lds_void*)((lds_u8*)&wl[st][(32 * u + 8 * wave) * F8_ROWB]), 16, 0, 0);
+  };
+  // Operand reads in inline asm with their own lgkmcnt wait (as in the kernel above).
+  auto addrs = [&](int st, int o, int base, uint32_t (&ad)[16]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = base + 16 * i + l16;
+      const uint32_t row = (uint32_t)(uintptr_t)(lds_u8*)(o ? &wl[st][r * F8_ROWB] : &xl[st][r * F8_ROWB]);
+      ad[2 * i] = row + (((2 * g4) ^ (r & 7)) << 4);
+      ad[2 * i + 1] = row + (((2 * g4 + 1) ^ (r & 7)) << 4);
+    }
+  };
+  auto read16 = [&](const uint32_t (&ad)[16], u32x4* v) {
+    asm volatile(
+        "ds_read_b128 %0, %16\n\tds_read_b128 %1, %17\n\tds_read_b128 %2, %18\n\t"
+        "ds_read_b128 %3, %19\n\tds_read_b128 %4, %20\n\tds_read_b128 %5, %21\n\t"
+        "ds_read_b128 %6, %22\n\tds_read_b128 %7, %23\n\tds_read_b128 %8, %24\n\t"
+        "ds_read_b128 %9, %25\n\tds_read_b128 %10, %26\n\tds_read_b128 %11, %27\n\t"
+        "ds_read_b128 %12, %28\n\tds_read_b128 %13, %29\n\tds_read_b128 %14, %30\n\t"
+        "ds_read_b128 %15, %31"
+        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
+          "=&v"(v[6]), "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11]),
+          "=&v"(v[12]), "=&v"(v[13]), "=&v"(v[14]), "=&v"(v[15])
+        : "v"(ad[0]), "v"(ad[1]), "v"(ad[2]), "v"(ad[3]), "v"(ad[4]), "v"(ad[5]), "v"(ad[6]),
+          "v"(ad[7]), "v"(ad[8]), "v"(ad[9]), "v"(ad[10]), "v"(ad[11]), "v"(ad[12]), "v"(ad[13]),
+          "v"(ad[14]), "v"(ad[15])
+        : "memory");
+  };
+  auto wait16 = [&](u32x4* v) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
+                   "+v"(v[6]), "+v"(v[7]), "+v"(v[8]), "+v"(v[9]), "+v"(v[10]), "+v"(v[11]),
+                   "+v"(v[12]), "+v"(v[13]), "+v"(v[14]), "+v"(v[15])
+                 :
+                 : "memory");
+  };
+  auto frag = [](const u32x4& lo, const u32x4& hi) {
+    return (i32x8){(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+  };
+
+  int m0c, n0c, m0n, n0n;
+  Src cur = tile_src(0, m0c, n0c);
+  Src nxt = tile_src(1, m0n, n0n);
+#pragma unroll
+  for (int s = 0; s < NS; ++s) issue(cur, s, s);
+  wait_vmcnt<OPS * (NS - 1)>();
+  barrier_only();
+  int sidx = 0;
+  for (int r = 0; r < my_tiles; ++r) {
+    f32x4 acc[8][8];   // [n sub-tile][m sub-tile]
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int ks = 0; ks < nk; ++ks, ++sidx) {
+      const int st = sidx % NS;
+      u32x4 wo[16], xo[16];
+      {
+        uint32_t aw[16], ax[16];
+        addrs(st, 1, 128 * wn, aw);
+        addrs(st, 0, 128 * wm, ax);
+        read16(aw, wo);
+        read16(ax, xo);
+        wait16(wo);
+        wait16(xo);
+      }
+      // step sidx + 1 has landed for this thread, then for everyone; every wave has read
+      // step sidx's slot, which is refilled with step sidx + NS
+      wait_vmcnt<OPS * (NS - 2)>();
+      barrier_only();
+      {
+        const int iks = ks + NS;
+        if (iks < nk) issue(cur, iks, st);
+        else issue(nxt, iks - nk, st);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const i32x8 wf = frag(wo[2 * i], wo[2 * i + 1]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              wf, frag(xo[2 * j], xo[2 * j + 1]), acc[i][j], 0, 0, 0, 127, 0, 127);
+      }
+    }
+    // Epilogue: lane holds n = n0 + 128 wn + 16 i + 4 g4 + q of m = m0 + 128 wm + 16 j + l16;
+    // the row / column scales and biases come straight from global memory (L2-resident).
+    float smv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) smv[j] = a.sa[m0c + 128 * wm + 16 * j + l16];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int n = n0c + 128 * wn + 16 * i + 4 * g4;
+      const f32x4 sn = *(const f32x4*)(a.sw + n);
+      half4_t bb = (half4_t){0, 0, 0, 0};
+      if (has_bias) bb = *(const half4_t*)(a.bias + n);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int m = m0c + 128 * wm + 16 * j + l16;
+        uint32_t bits[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t b = f32_to_bf16_bits((acc[i][j][q] * smv[j]) * sn[q]);
+          const half_t hb = (half_t)__builtin_bit_cast(float, b << 16);
+          const half_t h = has_bias ? (half_t)((float)hb + (float)bb[q]) : hb;
+          bits[q] = a.out_bf16 ? b : (uint32_t)__builtin_bit_cast(uint16_t, h);
+        }
+        uint2 pk;
+        pk.x = bits[0] | (bits[1] << 16);
+        pk.y = bits[2] | (bits[3] << 16);
+        *(uint2*)((uint16_t*)a.out + (int64_t)m * a.ldo + n) = pk;
+      }
+    }
+    cur = nxt;
+    m0c = m0n;
+    n0c = n0n;
+    nxt = tile_src(r + 2, m0n, n0n);
+  }
+  wait_vmcnt<0>();                     // drain the clamped tail loads before exit
+}
+
 static int num_cus() {
   static int n = 0;
   if (n <= 0) {
@@ -496,7 +682,10 @@ extern "C" int omni_fp8_quant_rows(const void* x, int ldx, void* xq, float* scal
 }
 
 // Kernel choice, read once from OMNI_FP8_GEMM: "simple" (0), "pipe4" (1: 4 waves, 128-row
-// tiles), "pipe8" (2: 8 waves, 256-row tiles; the default).
+// tiles), "pipe8" (2: 8 waves, 256-row tiles; the default), "big" (3: 256 x 256 tiles for
+// every shape it takes).  By default the 256 x 256 tiles serve the long-K shapes (K >= 4096,
+// M and N multiples of 256: the down projection, 8 % faster there; with K = 1536 they were
+// 3-9 % slower than the 256 x 128 tiles, measured on MI355X at M = 8192, outputs bit-equal).
 static int fp8_variant() {
   static int v = -1;
   if (v < 0) {
@@ -504,6 +693,7 @@ static int fp8_variant() {
     v = 2;
     if (e && e[0] == 's') v = 0;
     else if (e && strcmp(e, "pipe4") == 0) v = 1;
+    else if (e && strcmp(e, "big") == 0) v = 3;
   }
   return v;
 }
@@ -531,7 +721,13 @@ extern "C" int omni_fp8_gemm(const void* xq, const float* sa, const void* wq, co
   a.K = K;
   a.out_bf16 = out_bf16;
   const int variant = fp8_variant();
-  if (variant > 0 && K / F8_BK >= 4) {
+  const bool big_ok = K / F8_BK >= 2 && (N % F8B_T) == 0 && (M % F8B_T) == 0;
+  if (big_ok && (variant == 3 || (variant == 2 && K >= 4096))) {   // 256 x 256 tiles
+    const int64_t tb = (int64_t)ceil_div(M, F8B_T) * (N / F8B_T);
+    const int grid = (int)(tb < num_cus() ? tb : num_cus());
+    hipLaunchKernelGGL((fp8_gemm_big_kernel<2>), dim3((unsigned)grid), dim3(256), 0,
+                       (hipStream_t)stream, a);
+  } else if (variant > 0 && K / F8_BK >= 4) {
     if (variant == 2) {          // 8 waves, 256 x 128 tiles, 3 stages
       const int64_t t8 = (int64_t)ceil_div(M, 256) * (N / F8_BT);
       const int grid = (int)(t8 < num_cus() ? t8 : num_cus());

@@ -618,7 +618,8 @@ def fp8_abs_product(xq, sa, wq, sw):
 
 
 @pytest.mark.parametrize("M,N,K,bias", [(1, 256, 1536, False), (100, 2048, 1536, True),
-                                        (256, 1536, 8960, False), (130, 384, 256, True)])
+                                        (256, 1536, 8960, False), (130, 384, 256, True),
+                                        (512, 1280, 4096, True)])
 def test_fp8_linear_matches_oracle(gpu, M, N, K, bias):
     """FP8Linear.forward: bf16((xq.Wq^T)*sa*sw) -> fp16 (+bias) against the oracle on the
     same quantised operands.  The fp8 MFMA sums groups of products with fewer bits than

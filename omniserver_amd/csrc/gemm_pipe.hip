@@ -346,21 +346,38 @@ static int gp_launch(const GemmPipeArgs& a, int epilogue, hipStream_t st) {
 }
 
 static int gp_tile_rows(int M, int N) {
-  // 256-row tiles when they still give every CU a tile
+  // 256-row tiles (8 waves) when they take fewer rounds of the persistent grid than 128-row
+  // tiles (e.g. M = 1024, N = 5120: 160 tiles in one round against 320 in two, 31 against
+  // 41 us); at equal rounds the 128-row tiles spread the work over more CUs
+  const int64_t cus = gp_num_cus();
+  const int64_t t128 = (int64_t)ceil_div(M, 128) * (N / GP_BN);
   const int64_t t256 = (int64_t)ceil_div(M, 256) * (N / GP_BN);
-  return t256 >= gp_num_cus() ? 256 : 128;
+  return (t256 + cus - 1) / cus < (t128 + cus - 1) / cus ? 256 : 128;
 }
 
-// K slices for (M, N, K) at the given tile height (0: chosen): more slices while the
-// tiles alone leave over a quarter of the CUs idle and every slice keeps >= 8 K steps.
+// K slices for (M, N, K) at the given tile height (0: chosen): the count (1-4, each slice
+// >= 8 K steps) that minimises rounds of the persistent grid x K steps per slice, with two
+// steps charged for the finish launch of a split (ties: fewer slices); none when the tiles
+// alone fill the grid.  Measured on MI355X
+// at the vision tower's shapes: fc2 (80 tiles, 80 steps) 56 -> 31 us with 3 slices; fc1 at
+// 256-row tiles stays whole (2 slices would take two rounds).
 extern "C" int omni_f16_gemm_pipe_splits(int M, int N, int K, int tile_rows) {
   if (M <= 0 || N <= 0 || K <= 0 || (N % GP_BN) || (K % GP_BKH)) return 1;
   if (tile_rows == 0) tile_rows = gp_tile_rows(M, N);
+  const int64_t cus = gp_num_cus();
   const int64_t tiles = (int64_t)ceil_div(M, tile_rows) * (N / GP_BN);
   const int nk = K / GP_BKH;
-  int ks = 1;
-  while (ks < 8 && tiles * ks * 4 < 3 * (int64_t)gp_num_cus() && nk / (ks + 1) >= 8) ++ks;
-  return ks;
+  int best = 1;
+  int64_t best_cost = ((tiles + cus - 1) / cus) * nk;
+  if (tiles >= cus) return 1;        // the grid is full: slices would only add partial traffic
+  for (int ks = 2; ks <= 4 && nk / ks >= 8; ++ks) {
+    const int64_t cost = ((tiles * ks + cus - 1) / cus) * ((nk + ks - 1) / ks) + 2;
+    if (cost < best_cost) {
+      best = ks;
+      best_cost = cost;
+    }
+  }
+  return best;
 }
 
 // out = epi(fp16(x . w^T + bias)) with w fp16 [N, K] in nn.Linear layout (row stride K).

@@ -38,7 +38,7 @@ def decode_plan(n_tokens: int, n_kv: int, ctx: int) -> tuple:
     groups = max(1, n_tokens * n_kv)
     if ctx <= 128:
         return 4, 1
-    waves = 8 if groups >= 32 else 4
+    waves = 8 if groups >= 16 else 4     # B = 8 (16 groups): (8, 16) 1.3 % faster than (4, 16)
     splits = max(1, min(MAX_ATTN_SPLITS, 256 // groups, ctx // 128))
     return waves, splits
 

@@ -45,11 +45,11 @@ PLANS: Dict[Tuple[str, int, int], Tuple[int, int, int]] = {
     ("int4", 1536, 1536): (2, 1, 12),     # o_proj: one head per K slice (attention merge)
     ("int4", 8960, 1536): (2, 1, 14),
     ("int4", 1536, 17920): (6, 2, 1),     # SiLU-fused gate_up: preset 6 = (2, 3, 4), x first
+    # fp16 (two weight groups in flight per tile): swept at B = 1, 16 and 32
     ("fp16", 1536, 2048): (2, 1, 7),
     ("fp16", 1536, 1536): (2, 1, 12),
-    ("fp16", 8960, 1536): (2, 1, 14),
-    ("fp16", 1536, 17920): (2, 2, 1),     # fp16 gate_up: preset 2 = (2, 4, 2); 20-23 % faster
-                                          # steps than preset 6 at B = 1, 16, 32
+    ("fp16", 8960, 1536): (2, 3, 20),     # down: preset 3 = (2, 4, 2) x 20 K slices
+    ("fp16", 1536, 17920): (4, 2, 1),     # gate_up: SiLU preset 4 = (2, 3, 4)
 }
 
 

@@ -172,20 +172,24 @@ __global__ __launch_bounds__(MAXT) void rownorm_kernel(const half_t* x, const fl
   const int c = threadIdx.x;
   const int nchunk = H >> 3;
   const bool live = c < nchunk;
-  half8_t v = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
-  if (live) {
-    const half8_t rv = *(const half8_t*)(residual + (size_t)row * H + c * 8);
-    if (PARTS) {
-      float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      sum_slices8<16>(parts + (size_t)row * H + c * 8, (int64_t)rows * H, nparts, sum);
+  // Every load is issued up front, branch-free: threads past the row re-read its last chunk
+  // (their values are dropped), and the gains are fetched with the inputs rather than after
+  // the reduction's barrier (which would cost another memory round trip).
+  const int cc = live ? c : nchunk - 1;
+  const half8_t rv = *(const half8_t*)(residual + (size_t)row * H + cc * 8);
+  const half8_t wv = *(const half8_t*)(w + cc * 8);
+  half8_t v;
+  if (PARTS) {
+    float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    sum_slices8<16>(parts + (size_t)row * H + cc * 8, (int64_t)rows * H, nparts, sum);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = (half_t)sum[e];
-    } else {
-      v = *(const half8_t*)(x + (size_t)row * H + c * 8);
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = (half_t)((float)v[e] + (float)rv[e]);
+    for (int e = 0; e < 8; ++e) v[e] = (half_t)sum[e];
+  } else {
+    v = *(const half8_t*)(x + (size_t)row * H + cc * 8);
   }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = (half_t)((float)v[e] + (float)rv[e]);
+  if (!live) v = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
   float ss = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) ss += (float)v[e] * (float)v[e];
@@ -198,7 +202,6 @@ __global__ __launch_bounds__(MAXT) void rownorm_kernel(const half_t* x, const fl
   const float rstd = 1.0f / sqrtf(tot / (float)H + eps);
   if (live) {
     *(half8_t*)(res_out + (size_t)row * H + c * 8) = v;
-    const half8_t wv = *(const half8_t*)(w + c * 8);
     half8_t o;
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = (half_t)(((float)v[e] * rstd) * (float)wv[e]);

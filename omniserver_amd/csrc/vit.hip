@@ -175,13 +175,21 @@ struct VitAttnArgs {
   float scale_log2;
 };
 
-__global__ __launch_bounds__(256, 2) void vit_attn_kernel(VitAttnArgs a) {
+// KH key halves: with KH = 2 the workgroup has 8 waves; waves 4 h .. 4 h + 3 take the
+// queries of waves 0 .. 3 against the h-th half of the segment's key tiles (each half with
+// its own double-buffered tiles), and the two halves' softmax states are merged through
+// LDS at the end - twice the waves per CU on the same queries.
+template <int KH>
+__global__ __launch_bounds__(256 * KH, 1) void vit_attn_kernel(VitAttnArgs a) {
 #pragma clang fp contract(off)
-  __shared__ __attribute__((aligned(16))) half_t ks_lds[2][VA_KT * VA_KSTR];
-  __shared__ __attribute__((aligned(16))) half_t vs_lds[2][VA_KT * VA_VSTR];
+  __shared__ __attribute__((aligned(16))) half_t ks_lds[KH][2][VA_KT * VA_KSTR];
+  __shared__ __attribute__((aligned(16))) half_t vs_lds[KH][2][VA_KT * VA_VSTR];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  const int kh = wave >> 2;                     // key half
+  const int qw = wave & 3;                      // query block of 16
+  const int ht = tid & 255;                     // thread index within the half
   const int q16 = lane >> 4, c16 = lane & 15;
   const int L = xcd_logical_block(blockIdx.x, gridDim.x);
   const int h = L / a.ntiles, tile = L - h * a.ntiles;
@@ -189,15 +197,22 @@ __global__ __launch_bounds__(256, 2) void vit_attn_kernel(VitAttnArgs a) {
   const int beg = max(a.cu[seg], 0), end = min(a.cu[seg + 1], a.S);
   if (q0 < beg || q0 >= end) return;            // malformed table entry: nothing to do
   const half8_t z8 = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
+  // this half's key range, in whole tiles: half 0 takes the first ceil(n/2) tiles
+  const int ntile = (end - beg + VA_KT - 1) / VA_KT;
+  const int nt0 = (ntile + KH - 1) / KH;
+  const int kbeg = beg + (kh == 0 ? 0 : nt0 * VA_KT);
+  const int kend = kh == 0 && KH > 1 ? min(end, beg + nt0 * VA_KT) : end;
+  const int my_nt = kend > kbeg ? (kend - kbeg + VA_KT - 1) / VA_KT : 0;
 
   // the K tiles' dims 80..95 are zero for the whole kernel (tile stores never touch them)
-  for (int i = tid; i < 2 * VA_KT * 2; i += 256) {
-    const int bsel = i / (VA_KT * 2), rem = i - bsel * (VA_KT * 2);
-    *(half8_t*)(&ks_lds[bsel][(rem >> 1) * VA_KSTR + VA_HD + 8 * (rem & 1)]) = z8;
+  for (int i = tid; i < KH * 2 * VA_KT * 2; i += 256 * KH) {
+    const int hb_ = i / (2 * VA_KT * 2), r1 = i - hb_ * (2 * VA_KT * 2);
+    const int bsel = r1 / (VA_KT * 2), rem = r1 - bsel * (VA_KT * 2);
+    *(half8_t*)(&ks_lds[hb_][bsel][(rem >> 1) * VA_KSTR + VA_HD + 8 * (rem & 1)]) = z8;
   }
 
-  // this wave's query rows q0 + 16 wave + c16 (past the segment: its last row, not stored)
-  const int qrow = min(q0 + 16 * wave + c16, end - 1);
+  // this wave's query rows q0 + 16 qw + c16 (past the segment: its last row, not stored)
+  const int qrow = min(q0 + 16 * qw + c16, end - 1);
   const half_t* qp = a.qkv + (int64_t)qrow * a.ld + h * VA_HD;
   half8_t qf[3];
   qf[0] = *(const half8_t*)(qp + 8 * q16);
@@ -205,13 +220,13 @@ __global__ __launch_bounds__(256, 2) void vit_attn_kernel(VitAttnArgs a) {
   qf[2] = *(const half8_t*)(qp + 64 + 8 * (q16 & 1));
   if (q16 >= 2) qf[2] = z8;                     // dims 80..95
 
-  // tile chunk u of this thread: index i = tid + 256 u; i < 640 is K (row i / 10, chunk
+  // tile chunk u of this thread: index i = ht + 256 u; i < 640 is K (row i / 10, chunk
   // i % 10), the rest V
   int trow[VA_NLD], tsrc[VA_NLD], tdst[VA_NLD];
   bool tv[VA_NLD];
 #pragma unroll
   for (int u = 0; u < VA_NLD; ++u) {
-    const int i = tid + 256 * u;
+    const int i = ht + 256 * u;
     tv[u] = i >= VA_KT * VA_CPR;
     const int j = tv[u] ? i - VA_KT * VA_CPR : i;
     trow[u] = j / VA_CPR;
@@ -220,17 +235,18 @@ __global__ __launch_bounds__(256, 2) void vit_attn_kernel(VitAttnArgs a) {
     tdst[u] = tv[u] ? trow[u] * VA_VSTR + ch * 8 : trow[u] * VA_KSTR + ch * 8;
   }
   half8_t tr[VA_NLD];
+  const int tok_hi = max(kend, kbeg + 1) - 1;   // a half without tiles re-reads one row
   auto load_tile = [&](int kb) {
 #pragma unroll
     for (int u = 0; u < VA_NLD; ++u) {
-      const int tok = min(kb + trow[u], end - 1);
+      const int tok = min(min(kb + trow[u], tok_hi), a.S - 1);
       tr[u] = *(const half8_t*)(a.qkv + (int64_t)tok * a.ld + tsrc[u]);
     }
   };
   auto store_tile = [&](int b) {
 #pragma unroll
     for (int u = 0; u < VA_NLD; ++u) {
-      half_t* dst = tv[u] ? &vs_lds[b][tdst[u]] : &ks_lds[b][tdst[u]];
+      half_t* dst = tv[u] ? &vs_lds[kh][b][tdst[u]] : &ks_lds[kh][b][tdst[u]];
       *(half8_t*)dst = tr[u];
     }
   };
@@ -240,20 +256,24 @@ __global__ __launch_bounds__(256, 2) void vit_attn_kernel(VitAttnArgs a) {
 #pragma unroll
   for (int i = 0; i < 5; ++i) o_acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-  // Double buffer: tile n is staged in buffer n & 1; the barrier after staging tile n
-  // also means every wave has finished reading that buffer's previous tile (n - 2).
+  // Double buffer per half: tile n is staged in buffer n & 1; the barrier after staging
+  // tile n also means every wave has finished reading that buffer's previous tile (n - 2).
+  // Both halves run the larger half's tile count so that every wave meets every barrier.
+  const int nt_all = nt0;                       // the first half is never the smaller
   int b = 0;
-  load_tile(beg);
-  for (int kb = beg; kb < end; kb += VA_KT, b ^= 1) {
+  load_tile(kbeg);
+  for (int it = 0; it < nt_all; ++it, b ^= 1) {
+    const int kb = kbeg + it * VA_KT;
     store_tile(b);
     __syncthreads();
-    if (kb + VA_KT < end) load_tile(kb + VA_KT);
-    const half_t* kt = ks_lds[b];
-    const half_t* vt = vs_lds[b];
+    if (it + 1 < my_nt) load_tile(kb + VA_KT);
+    if (it >= my_nt) continue;                  // this half is done (barriers still met)
+    const half_t* kt = ks_lds[kh][b];
+    const half_t* vt = vs_lds[kh][b];
 #pragma unroll
     for (int hb = 0; hb < 2; ++hb) {             // 32-key halves of the tile
       const int k0 = kb + 32 * hb;
-      if (k0 >= end) break;
+      if (k0 >= kend) break;
       f32x4 sacc[2];
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
@@ -273,13 +293,13 @@ __global__ __launch_bounds__(256, 2) void vit_attn_kernel(VitAttnArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int key = k0 + 16 * j + 4 * q16 + i;
-          const float s = key < end ? sacc[j][i] * a.scale_log2 : -INFINITY;
+          const float s = key < kend ? sacc[j][i] * a.scale_log2 : -INFINITY;
           sc[4 * j + i] = s;
           mblk = fmaxf(mblk, s);
         }
       mblk = fmaxf(mblk, __shfl_xor(mblk, 16, 64));
       mblk = fmaxf(mblk, __shfl_xor(mblk, 32, 64));
-      const float m_new = fmaxf(m_run, mblk);      // finite: key k0 < end is visible
+      const float m_new = fmaxf(m_run, mblk);      // finite: key k0 < kend is visible
       const float alpha = exp2f(m_run - m_new);
       m_run = m_new;
       half8_t pa;
@@ -307,12 +327,45 @@ __global__ __launch_bounds__(256, 2) void vit_attn_kernel(VitAttnArgs a) {
   }
   l_run += __shfl_xor(l_run, 16, 64);
   l_run += __shfl_xor(l_run, 32, 64);
-  float li[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) li[i] = __shfl(l_run, 4 * q16 + i, 64);
+  // per query row 4 q16 + i of this lane: the half's running max and sum
+  float mi[4], li[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int t = q0 + 16 * wave + 4 * q16 + i;
+    mi[i] = __shfl(m_run, 4 * q16 + i, 64);
+    li[i] = __shfl(l_run, 4 * q16 + i, 64);
+  }
+  if constexpr (KH == 2) {
+    // merge: the second half hands its (max, sum, O) to the first through LDS (the tile
+    // buffers are free once every wave is past the loop)
+    __syncthreads();
+    float* xch = (float*)&ks_lds[0][0][0];      // [4 query waves][64 lanes][4 m + 4 l + 20 O]
+    float* my = xch + (qw * 64 + lane) * 28;
+    if (kh == 1) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        my[i] = mi[i];
+        my[4 + i] = li[i];
+      }
+#pragma unroll
+      for (int dt = 0; dt < 5; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) my[8 + 4 * dt + i] = o_acc[dt][i];
+    }
+    __syncthreads();
+    if (kh == 1) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float m1 = my[i], l1 = my[4 + i];
+      const float m = fmaxf(mi[i], m1);         // finite: the first half is never empty
+      const float f0 = exp2f(mi[i] - m), f1 = exp2f(m1 - m);   // m1 = -inf -> 0
+      li[i] = li[i] * f0 + l1 * f1;
+#pragma unroll
+      for (int dt = 0; dt < 5; ++dt) o_acc[dt][i] = o_acc[dt][i] * f0 + my[8 + 4 * dt + i] * f1;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = q0 + 16 * qw + 4 * q16 + i;
     if (t < end && t < q0 + 64) {
       half_t* op = a.out + (int64_t)t * a.ldo + h * VA_HD;
       const float inv = 1.0f / li[i];
@@ -347,7 +400,7 @@ extern "C" int omni_vit_attention(const void* qkv, int ld, int S, int n_heads, i
   a.out = (half_t*)out;
   a.ldo = ldo;
   a.scale_log2 = scale * 1.4426950408889634f;
-  hipLaunchKernelGGL(vit_attn_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, a);
+  hipLaunchKernelGGL(vit_attn_kernel<2>, dim3((unsigned)grid), dim3(512), 0, (hipStream_t)stream, a);
   OMNI_CHECK_LAUNCH();
   return OMNI_OK;
 }

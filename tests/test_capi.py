@@ -91,6 +91,14 @@ def test_bad_arguments_rejected_before_launch(so):
                                  1280, 4, 1280, 1280, 0, None) == -1
     assert L.omni_f16_gemm_tiled(fake_ptr(), 1280, 1280, fake_ptr(), None, None, 0, fake_ptr(),
                                  1280, 4, 1280, 1280, 6, None) == -1
+    # pipelined fp16 GEMM: K not a multiple of 64, slices below 4 K steps, split without
+    # a workspace
+    assert L.omni_f16_gemm_pipe(fake_ptr(), 1288, fake_ptr(), None, None, 0, fake_ptr(), 1280,
+                                4, 1280, 1288, 0, 0, 1, None, None) == -2
+    assert L.omni_f16_gemm_pipe(fake_ptr(), 1280, fake_ptr(), None, None, 0, fake_ptr(), 1280,
+                                4, 1280, 1280, 0, 128, 8, None, None) == -2
+    assert L.omni_f16_gemm_pipe(fake_ptr(), 1280, fake_ptr(), None, None, 0, fake_ptr(), 1280,
+                                4, 1280, 1280, 0, 128, 2, None, None) == -1
     # GEMM: split-K partials past the skinny kernel's 64 rows, K not a multiple of 128,
     # split without partial epilogue; more rows with the STORE epilogue are the tiled GEMM
     # (here rejected for its null pointers, not its size)
@@ -111,3 +119,20 @@ def test_bad_arguments_rejected_before_launch(so):
     # zero-size work is a no-op success
     assert L.omni_silu_mul(None, None, 0, 8960, None) == 0
     assert L.omni_gemm_slices(8960, 10) == 10 and L.omni_gemm_slices(1536, 7) == 6
+
+
+def test_pipe_gemm_launch_choices(so):
+    """The pipelined GEMM's host-side choice of K slices (no GPU needed: without a device the
+    library assumes 256 CUs, the MI355X count).  The vision tower's shapes at 1024 patches:
+    the qkv and fc1 tiles fill the grid (no split), proj / fc2 / the merger's linears leave
+    CUs idle and are split; a full grid (M = 8192) is never split."""
+    from omniserver_amd._lib import lib
+    f = lib().omni_f16_gemm_pipe_splits
+    assert f(1024, 3840, 1280, 0) == 1
+    assert f(1024, 5120, 1280, 0) == 1
+    assert f(1024, 1280, 1280, 0) == 2
+    assert f(1024, 1280, 5120, 0) == 3
+    assert f(256, 5120, 5120, 0) == 3
+    assert f(256, 1536, 5120, 0) == 4
+    assert f(8192, 1280, 5120, 0) == 1
+    assert f(8192, 1280, 100, 0) == 1            # K % 64 != 0: never split

@@ -174,8 +174,10 @@ int omni_prefill_attention(const void* q, int q_stride, const void* k_cache, con
  * [M, K] (row stride ldx); weights from omni_gptq_repack.  M <= 64 runs the skinny
  * weight-streaming kernel: ksplit > 1 only with OMNI_EPI_PARTIAL (slices =
  * omni_gemm_slices(K, ksplit)), preset selects the workgroup shape (0..3; SiLU 0..9).
- * M > 64 (prefill) runs the tiled MFMA GEMM: OMNI_EPI_STORE / OMNI_EPI_SILU only, ksplit 1,
- * preset ignored. */
+ * M > 64 (prefill) runs the tiled MFMA GEMM: OMNI_EPI_STORE / OMNI_EPI_SILU, preset ignored;
+ * with OMNI_EPI_STORE, ksplit > 1 splits K over omni_gemm_slices(K, ksplit) slices whose
+ * fp32 sums go to partial ([slices][M][N], 16-byte aligned) before a second launch adds
+ * them in order and stores out (+ bias). */
 int omni_w4a16_gemm(const void* x, int ldx, const void* qweight_packed, const void* scales_packed,
                     const void* bias, int bias_after_round, void* out, int ldo, float* partial,
                     int M, int N, int K, int epilogue, int ksplit, int preset, void* stream);

@@ -595,11 +595,15 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(GemvArgs a) {
   const int tiles_m = (a.M + GT_BM - 1) / GT_BM;
   // XCD-aware, grouped order: the tiles one XCD holds at a time form a 4 x 8 block, so
   // both operands are shared in its L2
+  // with K slices (EPI_PARTIAL, KS > 1) logical block L is slice L % KS of tile L / KS
+  const int Lb = xcd_logical_block(blockIdx.x, gridDim.x);
+  const int ksl = Lb % a.KS;
   int tm, tn;
-  grouped_tile(xcd_logical_block(blockIdx.x, gridDim.x), tiles_m, tiles_n, 4, tm, tn);
+  grouped_tile(Lb / a.KS, tiles_m, tiles_n, 4, tm, tn);
   const int m0 = tm * GT_BM;
   const int nt0 = tn * (GT_BN / 16) + wn * 4;   // this wave's first column tile
-  const int KG = a.K >> 7;
+  const int g0 = ksl * (a.KC >> 7);              // the slice's first 128-group
+  const int KG = min(a.K >> 7, g0 + (a.KC >> 7)); // one past its last
 
   // x staging: thread t moves 16-byte chunks t + 256 u (u < 8) of the 128 x 128 tile:
   // row (t + 256u) / 16, chunk t % 16.  Rows past M re-read row M - 1 (never stored).
@@ -628,7 +632,7 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(GemvArgs a) {
 
   WStream<WF> ws[4];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) ws[c].init(a, min(nt0 + c, NT - 1), 0, lane);
+  for (int c = 0; c < 4; ++c) ws[c].init(a, min(nt0 + c, NT - 1), 0, lane);   // group g at g
   WFrag<WF> wb[2][4];
   auto load_w = [&](WFrag<WF>(&f)[4], int g) {
 #pragma unroll
@@ -666,9 +670,9 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(GemvArgs a) {
   // Software pipeline over the K groups: group g + 1's x and weights are in flight while
   // group g is multiplied.  Group g is staged in xs[g & 1]; the barrier at the top of an
   // iteration also guarantees every wave finished reading that buffer two groups ago.
-  load_x(0);
-  load_w(wb[0], 0);
-  for (int g = 0; g < KG; g += 2) {
+  load_x(g0);
+  load_w(wb[0], g0);
+  for (int g = g0; g < KG; g += 2) {
     store_x(0, g);
     __syncthreads();
     if (g + 1 < KG) {
@@ -703,6 +707,13 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(GemvArgs a) {
           const float uv = (float)(half_t)acc[i][c + 1][r];
           a.out[(int64_t)m * a.ldo + j] = (half_t)(silu_ref(gv) * uv);
         }
+      } else if constexpr (EPI == EPI_PARTIAL) {
+        // the slice's fp32 sums, [slice][M][N]
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          if (nt0 + c >= NT) continue;
+          a.partial[((int64_t)ksl * a.M + m) * a.N + (nt0 + c) * 16 + c16] = acc[i][c][r];
+        }
       } else {
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
@@ -720,9 +731,40 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(GemvArgs a) {
 
 template <int WF, int EPI>
 static int launch_gemm_tile(const GemvArgs& a, hipStream_t st) {
-  const int64_t tiles = (int64_t)((a.M + GT_BM - 1) / GT_BM) * ((a.N + GT_BN - 1) / GT_BN);
+  const int64_t tiles = (int64_t)((a.M + GT_BM - 1) / GT_BM) * ((a.N + GT_BN - 1) / GT_BN) * a.KS;
   if (tiles > 0x7fffffff) return OMNI_EUNSUPPORTED;
   hipLaunchKernelGGL((gemm_tile_kernel<WF, EPI>), dim3((unsigned)tiles), dim3(256), 0, st, a);
+  OMNI_CHECK_LAUNCH();
+  return OMNI_OK;
+}
+
+// Split-K finish of the tiled GEMM's STORE epilogue: out = finish_store(sum of the KS fp32
+// slices in slice order, bias), one thread per 4 consecutive columns.
+__global__ __launch_bounds__(256) void tile_finish_kernel(GemvArgs a) {
+#pragma clang fp contract(off)
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int nq = a.N >> 2;
+  if (i >= (int64_t)a.M * nq) return;
+  const int m = (int)(i / nq), n = (int)(i - (int64_t)m * nq) * 4;
+  f32x4 v = *(const f32x4*)(a.partial + (int64_t)m * a.N + n);
+  for (int s = 1; s < a.KS; ++s) {
+    const f32x4 p = *(const f32x4*)(a.partial + ((int64_t)s * a.M + m) * a.N + n);
+    v = (f32x4){v[0] + p[0], v[1] + p[1], v[2] + p[2], v[3] + p[3]};
+  }
+  half4_t o;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) o[q] = finish_store(v[q], a, n + q);
+  *(half4_t*)(a.out + (int64_t)m * a.ldo + n) = o;
+}
+
+// The tiled GEMM's STORE epilogue over a.KS K slices: fp32 partials into a.partial, then
+// the finish launch.
+template <int WF>
+static int launch_gemm_tile_split(const GemvArgs& a, hipStream_t st) {
+  int rc = launch_gemm_tile<WF, EPI_PARTIAL>(a, st);
+  if (rc != OMNI_OK) return rc;
+  const int64_t nthr = (int64_t)a.M * (a.N / 4);
+  hipLaunchKernelGGL(tile_finish_kernel, dim3((unsigned)((nthr + 255) / 256)), dim3(256), 0, st, a);
   OMNI_CHECK_LAUNCH();
   return OMNI_OK;
 }
@@ -753,11 +795,16 @@ static int gemv_common(int wf, const void* x, int ldx, const void* w, const void
   if (preset == 3 && (N & 31)) return OMNI_EUNSUPPORTED;            // 2 tiles per wave
   const int KG = K >> 7;
   if (ksplit < 1 || ksplit > KG) return OMNI_EINVAL;
+  // M > 64 with the STORE epilogue may be split along K too: partial is then the fp32
+  // workspace of the slices ([slices][M][N]) and a finish launch stores the sums
+  const bool tile_split = M > 64 && epilogue == EPI_STORE && ksplit > 1;
   if (epilogue == EPI_PARTIAL) {
     if (!partial) return OMNI_EINVAL;
   } else {
     if (!out || ldo < (epilogue == EPI_SILU ? N / 2 : N)) return OMNI_EINVAL;
-    if (ksplit != 1) return OMNI_EINVAL;   // a split needs the PARTIAL epilogue
+    if (ksplit != 1 && !tile_split) return OMNI_EINVAL;   // a split needs partial sums
+    if (tile_split && (!partial || ((uintptr_t)partial & 15) || (ldo & 3) || ((uintptr_t)out & 7)))
+      return OMNI_EINVAL;
   }
   GemvArgs a = {};
   a.x = (const half_t*)x;
@@ -777,6 +824,10 @@ static int gemv_common(int wf, const void* x, int ldx, const void* w, const void
   a.kx = K;
   hipStream_t st = (hipStream_t)stream;
   if (M > 64) {   // many rows (prefill): the tiled kernel, STORE / SILU epilogues
+    if (tile_split)
+      return wf == W_INT4 ? launch_gemm_tile_split<W_INT4>(a, st) : launch_gemm_tile_split<W_FP16>(a, st);
+    a.KS = 1;
+    a.KC = K;
     if (wf == W_INT4)
       return epilogue == EPI_SILU ? launch_gemm_tile<W_INT4, EPI_SILU>(a, st)
                                   : launch_gemm_tile<W_INT4, EPI_STORE>(a, st);

@@ -78,10 +78,32 @@ class _Skinny(nn.Module):
     def _call(self, x2d, out, partial, epilogue, ksplit, preset):
         raise NotImplementedError
 
-    def forward_out(self, x2d: torch.Tensor, out: torch.Tensor, preset: int | None = None):
+    def tile_ksplit(self, M: int) -> int:
+        """K split of the tiled GEMM (more than MAX_SKINNY_M rows, STORE epilogue): when its
+        128 x 128 tiles would leave over half of the 256 CUs idle (e.g. a 256-token prompt's
+        down projection: 24 tiles over K = 8960), the K groups are dealt to up to 8 slices of
+        at least 4 groups each, summed by a finish launch."""
+        if self.fuse_silu or M <= MAX_SKINNY_M:
+            return 1
+        tiles = -(-M // 128) * -(-self.N // 128)
+        KG = self.K // 128
+        if tiles >= 128 or KG < 8:
+            return 1
+        return max(1, min(8, KG // 4, 256 // tiles))
+
+    def forward_out(self, x2d: torch.Tensor, out: torch.Tensor, preset: int | None = None,
+                    ksplit: int | None = None):
         """fp16 output (SiLU-fused for gate_up) into out; any number of rows (more than
-        MAX_SKINNY_M rows run the library's tiled MFMA GEMM, ``preset`` then unused)."""
+        MAX_SKINNY_M rows run the library's tiled MFMA GEMM, ``preset`` then unused, split
+        along K as tile_ksplit says unless ``ksplit`` is given)."""
         epi = EPI_SILU if self.fuse_silu else EPI_STORE
+        M = x2d.shape[0]
+        ks = self.tile_ksplit(M) if ksplit is None else ksplit
+        if M > MAX_SKINNY_M and epi == EPI_STORE and ks > 1:
+            ws = torch.empty(self.partial_slices(ks) * M * self.N, device=x2d.device,
+                             dtype=torch.float32)
+            self._call(x2d, out, ws, epi, ks, 0)
+            return out
         self._call(x2d, out, None, epi, 1, self.store_preset if preset is None else preset)
         return out
 

@@ -323,7 +323,7 @@ def test_tiled_gemm(gpu, fmt, M, K, N, bias, silu):
                        bias_after_round=fmt == "int4")
     xg = x.to(gpu)
     out = torch.empty(M, lin.out_features, device=gpu, dtype=torch.float16)
-    lin.forward_out(xg, out)
+    lin.forward_out(xg, out, ksplit=1)
     torch.cuda.synchronize()
     d = (out.cpu().float() - e).abs().max().item()
     assert d <= 2e-3 * max(1.0, e.abs().max().item()), d
@@ -332,6 +332,23 @@ def test_tiled_gemm(gpu, fmt, M, K, N, bias, silu):
         s1 = min(M, s0 + 64)
         lin.forward_out(xg[s0:s1], blocks[s0:s1], preset=1)
     assert torch.equal(out.cpu(), blocks.cpu())
+    # split along K (the default for few tiles; 2 slices forced): the slices' fp32 sums add in
+    # another order, so an fp16 result may sit one step from the unsplit one
+    # (and the bias, added after that rounding for int4, can leave a result far smaller
+    # than the sum it was rounded at)
+    # (and where the sum nearly cancels, the fp32 accumulation error of the summed term
+    # magnitudes dominates)
+    if not silu and K >= 1024:
+        e_nb = ref.linear(x.float(), W).abs()
+        absprod = x.float().abs() @ W.abs()
+        for ks in (None, 2):
+            sp = torch.empty_like(out)
+            lin.forward_out(xg, sp, ksplit=ks)
+            torch.cuda.synchronize()
+            ds = (sp.cpu().float() - out.cpu().float()).abs()
+            mag = torch.maximum(torch.maximum(out.cpu().float().abs(), sp.cpu().float().abs()), e_nb)
+            assert (ds <= mag * 2.0 ** -9 + absprod * 2.0 ** -20).all(), ds.max().item()
+            assert (sp.cpu().float() - e).abs().max().item() <= 2e-3 * max(1.0, e.abs().max().item())
 
 
 @pytest.mark.parametrize("M", [1, 16, 32])

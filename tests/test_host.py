@@ -296,3 +296,16 @@ def test_bench_byte_accounting_matches_published_floor():
     # x 128 x 2 B, the qkv rows + bias in, the output out
     assert bench.attn_launch_bytes([2048] * 32) == (32 * 2049 * 1024 + 33 * 2048 * 2
                                                     + 32 * 12 * 128 * 2)
+
+
+def test_vision_state_dict_prefixes():
+    """The vision tower's tensors are taken under either checkpoint prefix (``visual.`` or
+    the newer ``model.visual.``) and come back under ``visual.``; decoder keys are left out."""
+    import torch
+    from omniserver_amd.checkpoint import vision_state_dict
+    t = torch.zeros(2)
+    sd = {"visual.blocks.0.norm1.weight": t, "model.visual.merger.ln_q.weight": t,
+          "model.layers.0.input_layernorm.weight": t, "model.embed_tokens.weight": t}
+    out = vision_state_dict(sd)
+    assert set(out) == {"visual.blocks.0.norm1.weight", "visual.merger.ln_q.weight"}
+    assert vision_state_dict({"model.norm.weight": t}) == {}

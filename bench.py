@@ -310,7 +310,7 @@ def baseline_configs(device, w_int4) -> dict:
     decode, decode rates against the HBM peak, the packed prefill against the fp16 MFMA
     peak."""
     from omniserver_amd import synth
-    from omniserver_amd.positions import IMAGE_TOKEN_ID
+    from omniserver_amd.positions import IMAGE_TOKEN_ID, VISION_START_TOKEN_ID
     from omniserver_amd.request import Request, SamplingParams, Sequence, VisionInput
     from omniserver_amd.runner import NativeQwenVLRunner
     shape = synth.DecoderShape()
@@ -363,7 +363,9 @@ def baseline_configs(device, w_int4) -> dict:
     def mm_seqs():
         ss = []
         for b in range(B):
-            ids = (synth.random_ids(64, shape.vocab_size, 5, f"c5a.{b}").tolist() + [IMAGE_TOKEN_ID] * 256
+            # 63 text tokens + <|vision_start|>, 256 image rows at index 64, 192 text tokens
+            ids = (synth.random_ids(63, shape.vocab_size, 5, f"c5a.{b}").tolist()
+                   + [VISION_START_TOKEN_ID] + [IMAGE_TOKEN_ID] * 256
                    + synth.random_ids(192, shape.vocab_size, 5, f"c5b.{b}").tolist())
             rows = synth.randn16((256, shape.hidden_size), 1.0, 5, f"c5v.{b}").to(device)
             ss.append(mk(ids, images=[VisionInput(rows, (1, 32, 32))]))

@@ -21,20 +21,28 @@ SPATIAL_MERGE_SIZE = 2
 
 def mrope_positions(input_ids: Sequence[int], grids: Sequence[Tuple[int, int, int]],
                     image_token_id: int = IMAGE_TOKEN_ID,
+                    vision_start_id: int = VISION_START_TOKEN_ID,
                     merge: int = SPATIAL_MERGE_SIZE) -> Tuple[torch.Tensor, int]:
+    """(pos [3, L] int64, rope_delta) of one prompt.  As in positions.py:27-30 the number of
+    images is the number of vision-start tokens directly followed by an image token; image i
+    is the run at the first image token at or after the current index (:35) and takes
+    grids[i]; every piece starts at the previous piece's max + 1."""
     ids = np.asarray(input_ids, dtype=np.int64)
     L = ids.shape[0]
     pos = np.empty((3, L), dtype=np.int64)
-    st = 0          # next token index
-    nxt = 0         # next position value
+    vs = np.flatnonzero(ids[:-1] == vision_start_id) if L > 1 else np.empty(0, np.int64)
+    n_images = int((ids[vs + 1] == image_token_id).sum()) if vs.size else 0
+    if n_images > len(grids):
+        raise ValueError(f"{n_images} images in the prompt, {len(grids)} grids given")
     img_at = np.flatnonzero(ids == image_token_id)
-    for (t, h, w) in grids:
-        later = img_at[img_at >= st]
-        if later.size == 0:
-            raise ValueError("more image grids than image token runs")
-        ed = int(later[0])
+    st = 0          # next token index
+    nxt = 0         # next position value (previous piece's max + 1)
+    for (t, h, w) in list(grids)[:n_images]:
+        ed = int(img_at[np.searchsorted(img_at, st)])
         gh, gw = h // merge, w // merge
         n_img = t * gh * gw
+        if ed + n_img > L:
+            raise ValueError("image grid longer than the prompt's image run")
         text_len = ed - st
         pos[:, st:ed] = np.arange(text_len) + nxt
         base = nxt + text_len

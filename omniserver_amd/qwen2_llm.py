@@ -30,9 +30,12 @@ Qwen2Config = DecoderShape
 
 def rope_tables(cfg: Qwen2Config, max_pos: int, device):
     """fp16 cos/sin [max_pos, head_dim/2] of p * inv_freq (qwen2_llm.py:169-177, 181):
-    inv_freq = 1/theta^(arange(0,hd,2)/hd) and p*inv_freq in fp32, cos/sin in fp32, cast to
-    fp16.  Built on the CPU once; the kernel reads the pair (d, d+64) from column d."""
+    inv_freq = 1/theta^(arange(0,hd,2)/hd) in fp32, held in fp16 as the deployed module
+    holds its buffer (``Qwen2LLM(cfg).half()``, models/qwen2_vl.py:50, casts it), then
+    p*inv_freq in fp32, cos/sin in fp32, cast to fp16.  Built on the CPU once; the kernel
+    reads the pair (d, d+64) from column d."""
     inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, cfg.head_dim, 2).float() / cfg.head_dim))
+    inv = inv.to(torch.float16).float()
     freqs = torch.arange(max_pos)[:, None].float() * inv
     return (freqs.cos().to(torch.float16).to(device).contiguous(),
             freqs.sin().to(torch.float16).to(device).contiguous())

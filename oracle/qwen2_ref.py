@@ -81,24 +81,30 @@ def silu_mul(gate_up, f16=True):
 
 
 # --------------------------------------------------------------------------- rope
-def inv_freq(cfg: Qwen2Config) -> torch.Tensor:
-    """model/qwen2_llm.py:169: 1 / theta^(arange(0, hd, 2)/hd), fp32."""
-    return 1.0 / (cfg.rope_theta ** (torch.arange(0, cfg.head_dim, 2).float() / cfg.head_dim))
+def inv_freq(cfg: Qwen2Config, f16_buffer: bool = True) -> torch.Tensor:
+    """model/qwen2_llm.py:169: 1 / theta^(arange(0, hd, 2)/hd) computed in fp32 and
+    registered as a buffer (:170).  The deployed model is ``Qwen2LLM(cfg).half()``
+    (models/qwen2_vl.py:50), which casts that buffer to fp16 like every floating tensor of
+    the module, so the frequencies the reference uses are the fp16 roundings
+    (``f16_buffer``; False = the buffer of a module left in fp32)."""
+    inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, cfg.head_dim, 2).float() / cfg.head_dim))
+    return r16(inv, f16_buffer)
 
 
-def rope_cos_sin(position_ids: torch.Tensor, cfg: Qwen2Config, f16=True):
-    """model/qwen2_llm.py:172-177 (+ the fp16 cast at :181).
+def rope_cos_sin(position_ids: torch.Tensor, cfg: Qwen2Config, f16=True, f16_buffer=True):
+    """model/qwen2_llm.py:172-177 (+ the fp16 cast at :181): freqs = pos.float() * inv in
+    fp32 (the fp16 buffer promotes to fp32), cos / sin in fp32, cast to fp16.
 
     position_ids [3, B, L] int -> cos, sin [3, B, L, head_dim]."""
-    freqs = position_ids[..., None].float() * inv_freq(cfg)
+    freqs = position_ids[..., None].float() * inv_freq(cfg, f16_buffer)
     emb = torch.cat([freqs, freqs], dim=-1)
     return r16(emb.cos(), f16), r16(emb.sin(), f16)
 
 
-def rope_table(max_pos: int, cfg: Qwen2Config):
+def rope_table(max_pos: int, cfg: Qwen2Config, f16_buffer: bool = True):
     """cos/sin of p * inv_freq for p in [0, max_pos), fp16-rounded, [max_pos, hd/2]:
     the same values rope_cos_sin produces for any position id (first half of emb)."""
-    freqs = torch.arange(max_pos)[:, None].float() * inv_freq(cfg)
+    freqs = torch.arange(max_pos)[:, None].float() * inv_freq(cfg, f16_buffer)
     return r16(freqs.cos()), r16(freqs.sin())
 
 
@@ -124,32 +130,38 @@ def apply_mrope(q, k, cos, sin, mrope_section, f16=True):
 
 
 def mrope_position_ids(input_ids: Sequence[int], grids: Sequence[Sequence[int]],
-                       image_token_id: int = 151655, merge: int = 2):
-    """model/positions.py:17-58 for one sequence: text tokens get sequential positions on
-    all three axes; an image run of t*(h/merge)*(w/merge) tokens gets its grid (t, h, w)
-    position offset by the preceding text; text after an image resumes at max + 1.
+                       image_token_id: int = 151655, vision_start_id: int = 151652,
+                       merge: int = 2):
+    """model/positions.py:17-58 for one sequence.  The number of images is the number of
+    vision-start tokens directly followed by an image token (:27-30); image i is the run
+    that starts at the first image token at or after the current token index (:35), whether
+    or not a vision-start precedes it, and takes grids[i].  Text tokens get sequential
+    positions on all three axes, starting at the previous piece's max + 1 (:39, :51); an
+    image run of t*(h/merge)*(w/merge) tokens gets its grid (t, h, w) coordinates offset
+    by the text before it and that start (:42-49).
 
     Returns (pos [3, L] int64, delta = max + 1 - L)."""
     ids = list(input_ids)
     L = len(ids)
+    n_images = sum(1 for i in range(L - 1)
+                   if ids[i] == vision_start_id and ids[i + 1] == image_token_id)
     pieces: List[np.ndarray] = []
     st = 0
-    nxt = 0  # next start position
-    for t, h, w in grids:
+    for img in range(n_images):
+        t, h, w = grids[img]
         ed = ids.index(image_token_id, st)
         gh, gw = h // merge, w // merge
         text_len = ed - st
-        pieces.append(np.tile(np.arange(text_len) + nxt, (3, 1)))
-        base = nxt + text_len
+        start = int(pieces[-1].max()) + 1 if pieces else 0
+        pieces.append(np.tile(np.arange(text_len) + start, (3, 1)))
         ti = np.repeat(np.arange(t), gh * gw)
         hi = np.tile(np.repeat(np.arange(gh), gw), t)
         wi = np.tile(np.arange(gw), t * gh)
-        img = np.stack([ti, hi, wi]) + base
-        pieces.append(img)
-        nxt = int(img.max()) + 1
+        pieces.append(np.stack([ti, hi, wi]) + text_len + start)
         st = ed + t * gh * gw
     if st < L:
-        pieces.append(np.tile(np.arange(L - st) + nxt, (3, 1)))
+        start = int(pieces[-1].max()) + 1 if pieces else 0
+        pieces.append(np.tile(np.arange(L - st) + start, (3, 1)))
     pos = np.concatenate(pieces, axis=1).astype(np.int64)
     return torch.from_numpy(pos), int(pos.max()) + 1 - L
 
@@ -194,6 +206,18 @@ def quant_fp8(x: torch.Tensor):
     """kernels/fp8_linear.py:45-63: per-token s = amax/448 (no clamp), q = e4m3(x / s)."""
     s = x.abs().amax(-1, keepdim=True) / 448.0
     return (x / s).to(E4M3), s
+
+
+def rbf16(x: torch.Tensor) -> torch.Tensor:
+    """Round fp32 values to bf16 and back."""
+    return x.to(torch.bfloat16).to(torch.float32)
+
+
+def fp8_linear_prequant(xq, sa, wq, sw, bias=None):
+    """FP8Linear.forward_prequant (kernels/fp8_linear.py:99-108): the bf16 product of
+    _scaled_mm, plus bias.to(bf16) added in bf16.  Returns fp32 holding bf16 values."""
+    y = rbf16((xq.float() @ wq.float().t()) * sa.view(-1, 1) * sw.view(1, -1))
+    return y if bias is None else rbf16(y + rbf16(bias.float()))
 
 
 def fp8_linear_rowwise(xq, sa, wq, sw, bias=None, out_f16=True):

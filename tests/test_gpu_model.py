@@ -223,7 +223,7 @@ def test_multimodal_prefill_positions_and_logits(gpu):
     segment ends and the pool contents match the oracle."""
     from omniserver_amd import synth
     from omniserver_amd.kv_cache import PreallocatedKVCache
-    from omniserver_amd.positions import IMAGE_TOKEN_ID, mrope_positions
+    from omniserver_amd.positions import IMAGE_TOKEN_ID, VISION_START_TOKEN_ID, mrope_positions
     from omniserver_amd.qwen2_llm import Qwen2LLM
     say("multimodal packed prefill (gptq, 2 layers)")
     shape = synth.DecoderShape()
@@ -234,7 +234,8 @@ def test_multimodal_prefill_positions_and_logits(gpu):
     for s in range(2):
         text_a = synth.random_ids(8 + s, shape.vocab_size, 8, f"a{s}").tolist()
         text_b = synth.random_ids(6, shape.vocab_size, 8, f"b{s}").tolist()
-        ids = text_a + [IMAGE_TOKEN_ID] * 16 + text_b          # grid (1, 8, 8) -> 16 rows
+        # <|vision_start|> then 16 image rows (grid (1, 8, 8)), then text
+        ids = text_a + [VISION_START_TOKEN_ID] + [IMAGE_TOKEN_ID] * 16 + text_b
         vis = synth.randn16((16, shape.hidden_size), 1.0, 8, f"vis{s}")
         pos, delta = mrope_positions(ids, [(1, 8, 8)])
         epos, edelta = ref.mrope_position_ids(ids, [(1, 8, 8)])

@@ -175,7 +175,7 @@ def test_runner_pixel_inputs_match_oracle(gpu):
     from tests.helpers import check_ids, compare_logits, oracle_from_gptq
     from omniserver_amd import synth
     from omniserver_amd.kv_cache import PreallocatedKVCache
-    from omniserver_amd.positions import IMAGE_TOKEN_ID
+    from omniserver_amd.positions import IMAGE_TOKEN_ID, VISION_START_TOKEN_ID
     from omniserver_amd.request import PixelInput, Request, SamplingParams, Sequence, VisionInput
     from omniserver_amd.runner import NativeQwenVLRunner
     from omniserver_amd.vit import VisionConfig
@@ -189,7 +189,7 @@ def test_runner_pixel_inputs_match_oracle(gpu):
     for s, g in enumerate(grids):
         n_img = g[0] * g[1] * g[2] // 4
         prompts.append(synth.random_ids(7 + s, shape.vocab_size, 21, f"a{s}").tolist()
-                       + [IMAGE_TOKEN_ID] * n_img
+                       + [VISION_START_TOKEN_ID] + [IMAGE_TOKEN_ID] * n_img
                        + synth.random_ids(5, shape.vocab_size, 21, f"b{s}").tolist())
         pixels.append(synth.pixel_patches([g], VisionConfig().patch_dim, 23 + s))
 

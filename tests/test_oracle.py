@@ -8,7 +8,8 @@ pinned by something independent of how it is written:
   add_rms_norm_fp8          scale closed form; dequantised codes within one e4m3 step;
                             the row maximum maps to exactly +-448
   silu_mul                  float64 numpy closed form
-  apply_mrope (t = h = w)   textbook RoPE as a complex rotation of (x_d, x_{d+64})
+  apply_mrope (t = h = w)   textbook RoPE as a complex rotation of (x_d, x_{d+64}) by
+                            p * fp16(1/theta^(2d/128)) (the .half() module's buffer)
   apply_mrope (3-D)         each section follows only its own axis (dims [0,16)+[64,80) ->
                             t, [16,40)+[80,104) -> h, [40,64)+[104,128) -> w)
   mrope_position_ids        text-only = arange / delta 0; BASELINE.json config-5 closed form
@@ -18,6 +19,9 @@ pinned by something independent of how it is written:
   decode_attention          float64 brute-force softmax loops
   prefill_attention         brute force; last token of a segment == decode over it
   fp8 linear                torch._scaled_mm (library GEMM) on the same fp8 operands
+  rounding points           torch fp16 / bf16 CPU ops evaluating the reference's expressions:
+                            the GPTQ bias add (marlin_linear.py:62), forward_prequant's bias
+                            (fp8_linear.py:106-107), apply_mrope (qwen2_llm.py:64-72)
   decode_step / prefill     append consistency: prefill(p[:L]) + decode(p[L]) gives the
                             logits prefill(p[:L+1]) gives at its last position
   greedy                    lowest index wins ties
@@ -82,7 +86,8 @@ def test_mrope_equals_textbook_rope_when_axes_agree():
     k = rnd((1, 1, T, 128), 9)
     cos, sin = ref.rope_cos_sin(pos.view(1, 1, T).expand(3, 1, T), cfg, f16=False)
     qr, kr = ref.apply_mrope(q, k, cos, sin, cfg.mrope_section, f16=False)
-    inv = 1.0 / (1e6 ** (np.arange(0, 128, 2) / 128.0))
+    # the deployed module's inverse frequencies: the fp16 rounding of 1/theta^(2j/128)
+    inv = (1.0 / (1e6 ** (np.arange(0, 128, 2) / 128.0))).astype(np.float16).astype(np.float64)
     for x, xr in ((q, qr), (k, kr)):
         xn = x.double().numpy()
         z = xn[..., :64] + 1j * xn[..., 64:]
@@ -117,7 +122,9 @@ def test_mrope_positions_text_only():
 
 
 def test_mrope_positions_config5_closed_form():
-    ids = [5] * 64 + [151655] * 256 + [6] * 192
+    # 63 text tokens, <|vision_start|>, 256 image tokens, 192 text tokens (the vision-start
+    # token is the 64th text token: positions.py:27-30 counts an image only after one)
+    ids = [5] * 63 + [151652] + [151655] * 256 + [6] * 192
     pos, d = ref.mrope_position_ids(ids, [(1, 32, 32)])
     assert torch.equal(pos[:, :64], torch.arange(64).view(1, -1).expand(3, -1))
     img = pos[:, 64:320]
@@ -130,15 +137,25 @@ def test_mrope_positions_config5_closed_form():
 
 def test_mrope_positions_two_images_and_product_agree():
     from omniserver_amd.positions import mrope_positions
-    ids = [1, 2] + [151655] * 4 + [3] + [151655] * 9 + [4, 5]
+    S, I = 151652, 151655
+    ids = [1, S] + [I] * 4 + [S] + [I] * 9 + [4, 5]
     grids = [(1, 4, 4), (1, 6, 6)]
     pos, d = ref.mrope_position_ids(ids, grids)
-    # image 1 at positions 2..3, text at 4, image 2 at 5..7, text at 8, 9
+    # image 1 at positions 2..3, vision-start at 4, image 2 at 5..7, text at 8, 9
     assert pos[:, 6].tolist() == [4, 4, 4]
     assert pos[:, 7:16].max().item() == 7
     assert pos[:, 16:].tolist() == [[8, 9]] * 3 and d == 10 - 18
     p2, d2 = mrope_positions(ids, grids)
     assert torch.equal(pos, p2) and d == d2
+
+
+def test_mrope_positions_image_without_vision_start_is_text():
+    """positions.py:27-30 counts images by vision-start tokens followed by an image token:
+    a prompt whose image run has none gets 1-D text positions."""
+    from omniserver_amd.positions import mrope_positions
+    ids = [1, 2] + [151655] * 4 + [3]
+    for pos, d in (ref.mrope_position_ids(ids, [(1, 4, 4)]), mrope_positions(ids, [(1, 4, 4)])):
+        assert torch.equal(pos, torch.arange(7).view(1, -1).expand(3, -1)) and d == 0
 
 
 # ----------------------------------------------------------------------------- int4
@@ -221,6 +238,50 @@ def test_fp8_linear_matches_scaled_mm():
     # scales follow the closed forms
     assert torch.allclose(sw, w.abs().amax(1) / 448.0)
     assert torch.allclose(sa.view(-1), x.abs().amax(1) / 448.0)
+
+
+# ----------------------------------------------------------------------------- rounding points
+def test_gptq_bias_added_after_the_fp16_output():
+    """_MarlinBase.forward returns ``out + self.bias`` on the fp16 GEMM output
+    (marlin_linear.py:59-62): two roundings, evaluated here by torch's fp16 add."""
+    x = rnd((9, 256), 30).half().float()
+    w = rnd((256, 64), 31, 0.05).half().float()
+    b = rnd((64,), 32, 0.5).half()
+    y = ref.linear(x, w, b.float(), bias_after_round=True)
+    want = (x @ w).half() + b
+    assert torch.equal(y, want.float())
+    # and it is a different rounding from the fp16 nn.Linear's single one on some outputs
+    assert not torch.equal(y, ref.linear(x, w, b.float(), bias_after_round=False))
+
+
+def test_fp8_prequant_bias_in_bf16():
+    """forward_prequant adds bias.to(bf16) to the bf16 _scaled_mm output (fp8_linear.py:106-107)."""
+    x = rnd((8, 128), 33).half().float()
+    w = rnd((64, 128), 34, 0.02).half().float()
+    b = rnd((64,), 35, 0.3).half()
+    wq, sw = ref.fp8_weight_rowwise(w)
+    xq, sa = ref.quant_fp8(x)
+    y = ref.fp8_linear_prequant(xq, sa, wq, sw, b.float())
+    prod = ((xq.float() @ wq.float().t()) * sa * sw.view(1, -1)).to(torch.bfloat16)
+    assert torch.equal(y, (prod + b.to(torch.bfloat16)).float())
+
+
+def test_apply_mrope_fp16_expression():
+    """apply_mrope's ``(q * cos) + (rotate_half(q) * sin)`` on fp16 tensors
+    (qwen2_llm.py:64-72, cos/sin cast to fp16 at :181) evaluated by torch's fp16 ops."""
+    cfg = ref.Qwen2Config()
+    q = rnd((1, 3, 5, 128), 36).half()
+    k = rnd((1, 2, 5, 128), 37).half()
+    pos = torch.tensor([[[0, 9, 300, 2047, 4095]], [[0, 8, 301, 2000, 4000]],
+                        [[0, 7, 302, 1999, 4001]]])
+    cos, sin = ref.rope_cos_sin(pos, cfg)
+    qr, kr = ref.apply_mrope(q.float(), k.float(), cos, sin, cfg.mrope_section)
+    sec = cfg.mrope_section * 2
+    c16 = torch.cat([m[i % 3] for i, m in enumerate(cos.half().split(sec, -1))], -1).unsqueeze(1)
+    s16 = torch.cat([m[i % 3] for i, m in enumerate(sin.half().split(sec, -1))], -1).unsqueeze(1)
+    rot = lambda x: torch.cat((-x[..., 64:], x[..., :64]), -1)
+    assert torch.equal(qr, ((q * c16) + (rot(q) * s16)).float())
+    assert torch.equal(kr, ((k * c16) + (rot(k) * s16)).float())
 
 
 # ----------------------------------------------------------------------------- model

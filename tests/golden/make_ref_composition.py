@@ -151,6 +151,7 @@ def run(dtype, M, KV, positions_fn, decode_positions):
 
 
 def main():
+    sys.dont_write_bytecode = True       # nothing is written under the reference tree
     sys.path.insert(0, REF)
     import omniserve.kernels.fused_ops as FO
     import omniserve.model.qwen2_llm as M

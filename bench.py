@@ -23,7 +23,11 @@ The JSON line also carries:
   M = 8192 (achieved dense TFLOP/s against the 5.0 PFLOP/s fp8 MFMA peak);
 * ``vit``: the vision tower on one 448 x 448 image (TFLOP/s against the fp16 peak);
 * ``cpu_baseline``: the fp32 CPU restatement (oracle/) of the same step, timed on
-  this host on a bounded sample.
+  this host on a bounded sample with torch using every host core (os.cpu_count()),
+  the CPU model name alongside.
+
+``roofline`` is one kernel's fraction (``scope``: "kernel"); the whole step's
+fraction, the one the >= 60 % target is stated for, is ``step_roofline.frac``.
 
 Usage: python bench.py [--gpus 1] [--steps 128] [--warmup 3] [--no-cpu] [--no-fp8]
        [--no-vit] [--no-b1] [--no-configs] [--vit-only] [--pmc-probe]
@@ -426,10 +430,22 @@ def vit_tower(device, grid=(1, 32, 32), reps: int = 5) -> dict:
             "frac": round(fl / t / PEAK_FP16, 4)}
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (what lscpu prints as 'Model name')."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(runner, seqs, w, shape, budget_s: float = 12.0, max_steps: int = 20) -> dict:
     """fp32 CPU restatement (oracle) of the same decode step on this host's cores."""
     from oracle import qwen2_ref as ref
-    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "16") or 16), 16)
+    threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
     t0 = time.time()
     cfg = ref.Qwen2Config()
@@ -460,6 +476,7 @@ def cpu_baseline(runner, seqs, w, shape, budget_s: float = 12.0, max_steps: int 
             break
     per = el / n
     return {"value": round(B / per, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(), "torch_threads": torch.get_num_threads(),
             "ms_per_step": round(per * 1e3, 1),
             "sample": f"{n} decode steps (after 1 warm-up) of the same B={B}, ctx~{int(lengths[0])} "
                       f"int4 config, all 28 layers, fp32 oracle (weights dequantised once)"}
@@ -583,6 +600,7 @@ def main():
             "parallelism": "single GPU",
         },
         "roofline": {
+            "scope": "kernel (the step's fraction is step_roofline.frac)",
             "bound": "hbm",
             "kernel": "decode_attn_kernel (qkv partials + bias + M-RoPE + KV write + split GQA "
                       "decode attention, states out), graph of the 28 layers' launches",

@@ -283,12 +283,20 @@ int omni_fp8_quant_rows(const void* x, int ldx, void* q, float* scale, int rows,
 
 /* FP8Linear.forward / forward_prequant (kernels/fp8_linear.py:99-126):
  * y[m, n] = bf16((sum_k xq[m,k] wq[n,k]) * sa[m] * sw[n]) (fp32 accumulation, as
- * torch._scaled_mm with out_dtype bf16); out_bf16 = 1 stores that bf16 value, else it is
- * cast to fp16 and the fp16 bias (if any) added in fp16.  xq [M, K], wq [N, K] e4m3fn;
+ * torch._scaled_mm with out_dtype bf16); out_bf16 = 1 stores that bf16 value plus
+ * bf16(bias) added in bf16 (forward_prequant, :99-108), else it is cast to fp16 and the
+ * fp16 bias (if any) added in fp16 (:115-124).  xq [M, K], wq [N, K] e4m3fn;
  * out [M, ldo]; N % 128 == 0, K % 128 == 0. */
 int omni_fp8_gemm(const void* xq, const float* sa, const void* wq, const float* sw,
                   const void* bias, void* out, int ldo, int M, int N, int K, int out_bf16,
                   void* stream);
+
+/* The kernel omni_fp8_gemm runs for a shape (no reference counterpart: it tells a caller
+ * or a test which form covers the shape): 0 one 128 x 128 tile per workgroup (K < 512),
+ * 1 the pipelined persistent 256 x 128 tiles, 2 the 256 x 256 tiles (K >= 4096, M and N
+ * multiples of 256); *grid (may be NULL) = its workgroups.  Returns -1 for a shape
+ * omni_fp8_gemm rejects. */
+int omni_fp8_gemm_plan(int M, int N, int K, int* grid);
 
 /* ---------------------------------------------------------------- lm_head + greedy */
 

@@ -43,6 +43,7 @@ SIGNATURES = {
                                     _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _P, _I, _P, _P],
     "omni_fp8_quant_rows": [_P, _I, _P, _P, _I, _I, _F, _P],
     "omni_fp8_gemm": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
+    "omni_fp8_gemm_plan": [_I, _I, _I, ctypes.POINTER(_I)],
     "omni_w4a16_gemm_attn": [_P, _I, _I, _I, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I, _I,
                              _P],
     "omni_f16_gemm_attn": [_P, _I, _I, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I, _P],

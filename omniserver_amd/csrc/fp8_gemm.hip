@@ -35,6 +35,13 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
   return (uint16_t)(u >> 16);
 }
 
+// The bf16 value nearest f (RNE, NaN kept quiet), as a float; branch-free.
+__device__ __forceinline__ float bf16_value(float f) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, f);
+  const uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u;
+  return __builtin_bit_cast(float, (u & 0x7fffffffu) > 0x7f800000u ? ((u & 0xffff0000u) | 0x00400000u) : r);
+}
+
 struct Fp8GemmArgs {
   const uint8_t* xq;     // [M, K] e4m3
   const float* sa;       // [M]
@@ -147,7 +154,10 @@ __global__ __launch_bounds__(256, 2) void fp8_gemm_kernel(Fp8GemmArgs a) {
       for (int r = 0; r < 4; ++r) {
         const uint16_t b = f32_to_bf16_rne((acc[i][j][r] * sm) * sv[r]);
         if (a.out_bf16) {
-          bits[r] = b;
+          // forward_prequant's bias: out + bias.to(bf16), a bf16 add
+          bits[r] = a.bias ? f32_to_bf16_rne(__builtin_bit_cast(float, (uint32_t)b << 16) +
+                                             bf16_value((float)a.bias[n + r]))
+                           : b;
         } else {
           half_t h = (half_t)__builtin_bit_cast(float, (uint32_t)b << 16);
           if (a.bias) h = (half_t)((float)h + (float)a.bias[n + r]);
@@ -419,7 +429,11 @@ __global__ __launch_bounds__(128 * WM, 1) void fp8_gemm_pipe_kernel(Fp8GemmArgs 
           const uint32_t bw = bv[i][q >> 1] & bias_mask;
           const half_t bb = __builtin_bit_cast(half_t, (uint16_t)((q & 1) ? (bw >> 16) : (bw & 0xffffu)));
           const half_t h = has_bias ? (half_t)((float)hb + (float)bb) : hb;
-          bits[q] = a.out_bf16 ? b : (uint32_t)__builtin_bit_cast(uint16_t, h);
+          // bf16 output (forward_prequant): + bias.to(bf16) as a bf16 add
+          const uint32_t bo =
+              has_bias ? f32_to_bf16_bits(__builtin_bit_cast(float, b << 16) + bf16_value((float)bb))
+                       : b;
+          bits[q] = a.out_bf16 ? bo : (uint32_t)__builtin_bit_cast(uint16_t, h);
         }
         if (m < a.M) {
           uint2 pk;
@@ -444,9 +458,49 @@ __global__ __launch_bounds__(128 * WM, 1) void fp8_gemm_pipe_kernel(Fp8GemmArgs 
 // 128 columns; this one for every 256).  Per K step a wave issues 32 operand reads (32 bytes
 // per lane of 8 w and 8 x row groups) and 64 MFMAs; two stages of 64 KB each are in LDS
 // (the next step's operands land while this step's MFMAs run).  Same staging (direct
-// global->LDS loads, XOR-swizzled 128-byte rows), tile order and epilogue as the kernel
-// above.
+// global->LDS loads, XOR-swizzled 128-byte rows) and tile order as the kernel above, but
+// one tile per workgroup (the long-K shapes it serves have at most a grid's worth of
+// tiles: config 4's down projection 192), which keeps no cross-tile state live beside the
+// 256 accumulators.
 #define F8B_T 256
+
+// Output bits of one product value v = acc * sa * sw: bf16(v), then either that bf16 plus
+// bf16(bias) as a bf16 add (out_bf16: forward_prequant, out + bias.to(bf16)) or the bf16
+// rounded to fp16 plus the fp16 bias as an fp16 add (forward).  A zero bias is the identity
+// in both (x + 0 rounds to x).
+template <bool OUT_BF16>
+__device__ __forceinline__ uint32_t fp8_out_bits(float v, half_t bias) {
+  const uint32_t b = f32_to_bf16_bits(v);
+  const float bf = __builtin_bit_cast(float, b << 16);
+  if (OUT_BF16) return f32_to_bf16_bits(bf + bf16_value((float)bias));
+  return (uint32_t)__builtin_bit_cast(uint16_t, (half_t)((float)(half_t)bf + (float)bias));
+}
+
+// The 256 x 256 kernel's epilogue for one wave's 128 x 128 block: acc[i][j][q] is column
+// 16 i + q of row 16 j of the block (relative to the lane's ob / sap / sw / bias).
+template <bool OUT_BF16>
+__device__ __forceinline__ void fp8_big_epilogue(const f32x4 (&acc)[8][8], uint16_t* ob, int ldo,
+                                                 const float* sap, const float* sw,
+                                                 const half_t* bias) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const f32x4 sn = *(const f32x4*)(sw + 16 * i);
+    half4_t bb = (half4_t){0, 0, 0, 0};
+    if (bias) bb = *(const half4_t*)(bias + 16 * i);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float sm = sap[16 * j];
+      uint32_t bits[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) bits[q] = fp8_out_bits<OUT_BF16>((acc[i][j][q] * sm) * sn[q], bb[q]);
+      uint2 pk;
+      pk.x = bits[0] | (bits[1] << 16);
+      pk.y = bits[2] | (bits[3] << 16);
+      *(uint2*)(ob + (16 * j * ldo + 16 * i)) = pk;
+    }
+  }
+}
 
 template <int NS>
 __global__ __launch_bounds__(256, 1) void fp8_gemm_big_kernel(Fp8GemmArgs a) {
@@ -464,13 +518,13 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_big_kernel(Fp8GemmArgs a) {
   const int l16 = lane & 15;
   const int g4 = lane >> 4;
 
+  // One tile per workgroup (grid = tiles), in grouped order, XCD-contiguous.
   const int tiles_n = a.N / F8B_T;
-  const int tiles_m = (a.M + F8B_T - 1) / F8B_T;
-  const int tiles = tiles_m * tiles_n;
-  const int G = gridDim.x;
-  const int slot = xcd_logical_block(blockIdx.x, G);
-  const int my_tiles = (tiles - slot + G - 1) / G;          // grid <= tiles: >= 1
+  const int tiles_m = a.M / F8B_T;
   const int nk = a.K / F8_BK;                               // >= NS (host check)
+  int tm, tn;
+  grouped_tile(xcd_logical_block(blockIdx.x, gridDim.x), tiles_m, tiles_n, F8_GM, tm, tn);
+  const int m0 = tm * F8B_T, n0 = tn * F8B_T;
 
   // Load u of this wave fills tile rows 32 u + 8 wave + lane / 8 (LDS slot lane % 8 holds
   // the row's chunk (lane % 8) ^ (row & 7)).  M % 256 == 0 (host check): no row clamping,
@@ -480,56 +534,49 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_big_kernel(Fp8GemmArgs a) {
   typedef __attribute__((address_space(3))) void lds_void;
   typedef __attribute__((address_space(3))) uint8_t lds_u8;
   const bool has_bias = a.bias != nullptr;
-  struct Src {
-    const uint8_t* x;
-    const uint8_t* w;
-  };
-  auto tile_src = [&](int r, int& m0, int& n0) {
-    int tm, tn;
-    grouped_tile(min(r, my_tiles - 1) * G + slot, tiles_m, tiles_n, F8_GM, tm, tn);
-    m0 = tm * F8B_T;
-    n0 = tn * F8B_T;
-    Src t;
-    t.x = a.xq + (int64_t)(m0 + lrow) * a.K + lchunk * 16;
-    t.w = a.wq + (int64_t)(n0 + lrow) * a.K + lchunk * 16;
-    return t;
-  };
-  const int64_t rstep = (int64_t)32 * a.K;          // bytes between row groups
-  auto issue = [&](const Src& t, int ks, int st) {
-    const int k0 = ks * F8_BK;
+  // The tile's sources are wave-uniform row bases (scalar registers); the lane's own part,
+  // row lrow and chunk lchunk, is one 32-bit offset shared by x and w (row offsets stay
+  // below 2^31: 256 rows of K <= 2^23 bytes).
+  const uint8_t* const xs = a.xq + (int64_t)m0 * a.K;
+  const uint8_t* const ws = a.wq + (int64_t)n0 * a.K;
+  const uint32_t loff = (uint32_t)lrow * (uint32_t)a.K + (uint32_t)lchunk * 16u;
+  const uint32_t rstep = 32u * (uint32_t)a.K;       // bytes between row groups
+  auto issue = [&](int ks, int st) {
+    const uint32_t k0 = loff + (uint32_t)ks * F8_BK;
 #pragma unroll
     for (int u = 0; u < XLD; ++u)
-      __builtin_amdgcn_global_load_lds((const void*)(t.x + u * rstep + k0),
+      __builtin_amdgcn_global_load_lds((const void*)(xs + (k0 + u * rstep)),
                                        (lds_void*)((lds_u8*)&xl[st][(32 * u + 8 * wave) * F8_ROWB]), 16, 0, 0);
 #pragma unroll
     for (int u = 0; u < WLD; ++u)
-      __builtin_amdgcn_global_load_lds((const void*)(t.w + u * rstep + k0),
+      __builtin_amdgcn_global_load_lds((const void*)(ws + (k0 + u * rstep)),
                                        (lds_void*)((lds_u8*)&wl[st][(32 * u + 8 * wave) * F8_ROWB]), 16, 0, 0);
   };
-  // Operand reads in inline asm with their own lgkmcnt wait (as in the kernel above).
-  auto addrs = [&](int st, int o, int base, uint32_t (&ad)[16]) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int r = base + 16 * i + l16;
-      const uint32_t row = (uint32_t)(uintptr_t)(lds_u8*)(o ? &wl[st][r * F8_ROWB] : &xl[st][r * F8_ROWB]);
-      ad[2 * i] = row + (((2 * g4) ^ (r & 7)) << 4);
-      ad[2 * i + 1] = row + (((2 * g4 + 1) ^ (r & 7)) << 4);
-    }
+  // Operand reads in inline asm with their own lgkmcnt wait (as in the kernel above).  Row
+  // r = base + 16 i + l16 of a wave's block keeps its 16-byte chunk c in slot c ^ (r & 7) =
+  // c ^ (l16 & 7) (base and 16 i are multiples of 8), so the 8 row groups of one chunk are
+  // one address plus immediate offsets of 16 rows (2 KB) each: two address registers per
+  // operand and step.
+  auto addrs = [&](int st, int o, int base, uint32_t& a0, uint32_t& a1) {
+    const int r = base + l16;
+    const uint32_t row = (uint32_t)(uintptr_t)(lds_u8*)(o ? &wl[st][r * F8_ROWB] : &xl[st][r * F8_ROWB]);
+    a0 = row + (((2 * g4) ^ (l16 & 7)) << 4);
+    a1 = row + (((2 * g4 + 1) ^ (l16 & 7)) << 4);
   };
-  auto read16 = [&](const uint32_t (&ad)[16], u32x4* v) {
+  auto read16 = [&](uint32_t a0, uint32_t a1, u32x4* v) {
     asm volatile(
-        "ds_read_b128 %0, %16\n\tds_read_b128 %1, %17\n\tds_read_b128 %2, %18\n\t"
-        "ds_read_b128 %3, %19\n\tds_read_b128 %4, %20\n\tds_read_b128 %5, %21\n\t"
-        "ds_read_b128 %6, %22\n\tds_read_b128 %7, %23\n\tds_read_b128 %8, %24\n\t"
-        "ds_read_b128 %9, %25\n\tds_read_b128 %10, %26\n\tds_read_b128 %11, %27\n\t"
-        "ds_read_b128 %12, %28\n\tds_read_b128 %13, %29\n\tds_read_b128 %14, %30\n\t"
-        "ds_read_b128 %15, %31"
+        "ds_read_b128 %0, %16\n\tds_read_b128 %1, %17\n\t"
+        "ds_read_b128 %2, %16 offset:2048\n\tds_read_b128 %3, %17 offset:2048\n\t"
+        "ds_read_b128 %4, %16 offset:4096\n\tds_read_b128 %5, %17 offset:4096\n\t"
+        "ds_read_b128 %6, %16 offset:6144\n\tds_read_b128 %7, %17 offset:6144\n\t"
+        "ds_read_b128 %8, %16 offset:8192\n\tds_read_b128 %9, %17 offset:8192\n\t"
+        "ds_read_b128 %10, %16 offset:10240\n\tds_read_b128 %11, %17 offset:10240\n\t"
+        "ds_read_b128 %12, %16 offset:12288\n\tds_read_b128 %13, %17 offset:12288\n\t"
+        "ds_read_b128 %14, %16 offset:14336\n\tds_read_b128 %15, %17 offset:14336"
         : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
           "=&v"(v[6]), "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11]),
           "=&v"(v[12]), "=&v"(v[13]), "=&v"(v[14]), "=&v"(v[15])
-        : "v"(ad[0]), "v"(ad[1]), "v"(ad[2]), "v"(ad[3]), "v"(ad[4]), "v"(ad[5]), "v"(ad[6]),
-          "v"(ad[7]), "v"(ad[8]), "v"(ad[9]), "v"(ad[10]), "v"(ad[11]), "v"(ad[12]), "v"(ad[13]),
-          "v"(ad[14]), "v"(ad[15])
+        : "v"(a0), "v"(a1)
         : "memory");
   };
   auto wait16 = [&](u32x4* v) {
@@ -544,41 +591,33 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_big_kernel(Fp8GemmArgs a) {
     return (i32x8){(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
   };
 
-  int m0c, n0c, m0n, n0n;
-  Src cur = tile_src(0, m0c, n0c);
-  Src nxt = tile_src(1, m0n, n0n);
 #pragma unroll
-  for (int s = 0; s < NS; ++s) issue(cur, s, s);
+  for (int s = 0; s < NS; ++s) issue(s, s);
   wait_vmcnt<OPS * (NS - 1)>();
   barrier_only();
-  int sidx = 0;
-  for (int r = 0; r < my_tiles; ++r) {
+  {
     f32x4 acc[8][8];   // [n sub-tile][m sub-tile]
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    for (int ks = 0; ks < nk; ++ks, ++sidx) {
-      const int st = sidx % NS;
+    for (int ks = 0; ks < nk; ++ks) {
+      const int st = ks % NS;
       u32x4 wo[16], xo[16];
       {
-        uint32_t aw[16], ax[16];
-        addrs(st, 1, 128 * wn, aw);
-        addrs(st, 0, 128 * wm, ax);
-        read16(aw, wo);
-        read16(ax, xo);
+        uint32_t aw0, aw1, ax0, ax1;
+        addrs(st, 1, 128 * wn, aw0, aw1);
+        addrs(st, 0, 128 * wm, ax0, ax1);
+        read16(aw0, aw1, wo);
+        read16(ax0, ax1, xo);
         wait16(wo);
         wait16(xo);
       }
-      // step sidx + 1 has landed for this thread, then for everyone; every wave has read
-      // step sidx's slot, which is refilled with step sidx + NS
+      // step ks + 1 has landed for this thread, then for everyone; every wave has read
+      // step ks's slot, which is refilled with step ks + NS
       wait_vmcnt<OPS * (NS - 2)>();
       barrier_only();
-      {
-        const int iks = ks + NS;
-        if (iks < nk) issue(cur, iks, st);
-        else issue(nxt, iks - nk, st);
-      }
+      if (ks + NS < nk) issue(ks + NS, st);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const i32x8 wf = frag(wo[2 * i], wo[2 * i + 1]);
@@ -590,38 +629,14 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_big_kernel(Fp8GemmArgs a) {
     }
     // Epilogue: lane holds n = n0 + 128 wn + 16 i + 4 g4 + q of m = m0 + 128 wm + 16 j + l16;
     // the row / column scales and biases come straight from global memory (L2-resident).
-    float smv[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) smv[j] = a.sa[m0c + 128 * wm + 16 * j + l16];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int n = n0c + 128 * wn + 16 * i + 4 * g4;
-      const f32x4 sn = *(const f32x4*)(a.sw + n);
-      half4_t bb = (half4_t){0, 0, 0, 0};
-      if (has_bias) bb = *(const half4_t*)(a.bias + n);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int m = m0c + 128 * wm + 16 * j + l16;
-        uint32_t bits[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint32_t b = f32_to_bf16_bits((acc[i][j][q] * smv[j]) * sn[q]);
-          const half_t hb = (half_t)__builtin_bit_cast(float, b << 16);
-          const half_t h = has_bias ? (half_t)((float)hb + (float)bb[q]) : hb;
-          bits[q] = a.out_bf16 ? b : (uint32_t)__builtin_bit_cast(uint16_t, h);
-        }
-        uint2 pk;
-        pk.x = bits[0] | (bits[1] << 16);
-        pk.y = bits[2] | (bits[3] << 16);
-        *(uint2*)((uint16_t*)a.out + (int64_t)m * a.ldo + n) = pk;
-      }
-    }
-    cur = nxt;
-    m0c = m0n;
-    n0c = n0n;
-    nxt = tile_src(r + 2, m0n, n0n);
+    // One base pointer per tile and 32-bit offsets inside it (256 rows of ldo halves).
+    const int mb = m0 + 128 * wm + l16;
+    const int nb = n0 + 128 * wn + 4 * g4;
+    uint16_t* const ob = (uint16_t*)a.out + (int64_t)mb * a.ldo + nb;
+    const float* const sap = a.sa + mb;
+    if (a.out_bf16) fp8_big_epilogue<true>(acc, ob, a.ldo, sap, a.sw + nb, has_bias ? a.bias + nb : nullptr);
+    else fp8_big_epilogue<false>(acc, ob, a.ldo, sap, a.sw + nb, has_bias ? a.bias + nb : nullptr);
   }
-  wait_vmcnt<0>();                     // drain the clamped tail loads before exit
 }
 
 static int num_cus() {
@@ -681,21 +696,30 @@ extern "C" int omni_fp8_quant_rows(const void* x, int ldx, void* xq, float* scal
   return OMNI_OK;
 }
 
-// Kernel choice, read once from OMNI_FP8_GEMM: "simple" (0), "pipe4" (1: 4 waves, 128-row
-// tiles), "pipe8" (2: 8 waves, 256-row tiles; the default), "big" (3: 256 x 256 tiles for
-// every shape it takes).  By default the 256 x 256 tiles serve the long-K shapes (K >= 4096,
-// M and N multiples of 256: the down projection, 8 % faster there; with K = 1536 they were
-// 3-9 % slower than the 256 x 128 tiles, measured on MI355X at M = 8192, outputs bit-equal).
-static int fp8_variant() {
-  static int v = -1;
-  if (v < 0) {
-    const char* e = getenv("OMNI_FP8_GEMM");
-    v = 2;
-    if (e && e[0] == 's') v = 0;
-    else if (e && strcmp(e, "pipe4") == 0) v = 1;
-    else if (e && strcmp(e, "big") == 0) v = 3;
+// Kernel choice by shape: the 256 x 256 tiles serve the long-K shapes (K >= 4096, M and N
+// multiples of 256: the down projection, 8 % faster there; with K = 1536 they were 3-9 %
+// slower than the 256 x 128 tiles, measured on MI355X at M = 8192, outputs bit-equal); the
+// 8-wave pipelined 256 x 128 form every other shape with at least 4 K steps; the
+// double-buffered one-tile-per-workgroup kernel the rest (K < 512).
+static bool fp8_big_tiles(int M, int N, int K) {
+  return K >= 4096 && (N % F8B_T) == 0 && (M % F8B_T) == 0;
+}
+
+// Which kernel omni_fp8_gemm runs for a shape: 0 one tile per workgroup, 1 the pipelined
+// 256 x 128 tiles, 2 the 256 x 256 tiles; and the persistent grid it launches.
+extern "C" int omni_fp8_gemm_plan(int M, int N, int K, int* grid) {
+  if (M <= 0 || N <= 0 || K <= 0 || (N % F8_BT) || (K % F8_BK)) return OMNI_EINVAL;
+  int kind, g;
+  if (fp8_big_tiles(M, N, K)) {
+    kind = 2, g = (M / F8B_T) * (N / F8B_T);
+  } else if (K / F8_BK >= 4) {
+    const int64_t t8 = (int64_t)ceil_div(M, 256) * (N / F8_BT);
+    kind = 1, g = (int)(t8 < num_cus() ? t8 : num_cus());
+  } else {
+    kind = 0, g = ceil_div(M, F8_BT) * (N / F8_BT);
   }
-  return v;
+  if (grid) *grid = g;
+  return kind;
 }
 
 extern "C" int omni_fp8_gemm(const void* xq, const float* sa, const void* wq, const float* sw,
@@ -720,24 +744,15 @@ extern "C" int omni_fp8_gemm(const void* xq, const float* sa, const void* wq, co
   a.N = N;
   a.K = K;
   a.out_bf16 = out_bf16;
-  const int variant = fp8_variant();
-  const bool big_ok = K / F8_BK >= 2 && (N % F8B_T) == 0 && (M % F8B_T) == 0;
-  if (big_ok && (variant == 3 || (variant == 2 && K >= 4096))) {   // 256 x 256 tiles
-    const int64_t tb = (int64_t)ceil_div(M, F8B_T) * (N / F8B_T);
-    const int grid = (int)(tb < num_cus() ? tb : num_cus());
+  if (fp8_big_tiles(M, N, K)) {                   // 256 x 256 tiles, one per workgroup
+    const int grid = (M / F8B_T) * (N / F8B_T);
     hipLaunchKernelGGL((fp8_gemm_big_kernel<2>), dim3((unsigned)grid), dim3(256), 0,
                        (hipStream_t)stream, a);
-  } else if (variant > 0 && K / F8_BK >= 4) {
-    if (variant == 2) {          // 8 waves, 256 x 128 tiles, 3 stages
-      const int64_t t8 = (int64_t)ceil_div(M, 256) * (N / F8_BT);
-      const int grid = (int)(t8 < num_cus() ? t8 : num_cus());
-      hipLaunchKernelGGL((fp8_gemm_pipe_kernel<4, 3>), dim3((unsigned)grid), dim3(512), 0,
-                         (hipStream_t)stream, a);
-    } else {                     // 4 waves, 128 x 128 tiles, 4 stages
-      const int grid = (int)(tiles < num_cus() ? tiles : num_cus());
-      hipLaunchKernelGGL((fp8_gemm_pipe_kernel<2, 4>), dim3((unsigned)grid), dim3(256), 0,
-                         (hipStream_t)stream, a);
-    }
+  } else if (K / F8_BK >= 4) {                    // 8 waves, 256 x 128 tiles, 3 stages
+    const int64_t t8 = (int64_t)ceil_div(M, 256) * (N / F8_BT);
+    const int grid = (int)(t8 < num_cus() ? t8 : num_cus());
+    hipLaunchKernelGGL((fp8_gemm_pipe_kernel<4, 3>), dim3((unsigned)grid), dim3(512), 0,
+                       (hipStream_t)stream, a);
   } else {
     hipLaunchKernelGGL(fp8_gemm_kernel, dim3((unsigned)tiles), dim3(256), 0, (hipStream_t)stream, a);
   }

@@ -276,10 +276,11 @@ class FP8Linear(nn.Module):
         return xq, sa
 
     def gemm_out(self, xq: torch.Tensor, sa: torch.Tensor, out: torch.Tensor, bf16: bool):
+        """bf16: the bf16 product plus bias.to(bf16) in bf16 (forward_prequant, :99-108);
+        else the bf16 product cast to fp16 plus the fp16 bias (forward, :115-124)."""
         M = xq.shape[0]
         call("omni_fp8_gemm", ptr(xq), ptr(sa), ptr(self.weight_fp8), ptr(self.weight_scale),
-             None if bf16 else ptr(self.bias), ptr(out), out.stride(0), M, self.N, self.K,
-             int(bf16), stream())
+             ptr(self.bias), ptr(out), out.stride(0), M, self.N, self.K, int(bf16), stream())
         return out
 
     def forward_prequant(self, xq: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:

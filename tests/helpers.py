@@ -57,3 +57,57 @@ def check_ids(ids, exp_logits: torch.Tensor, err: float):
     bad = (ids != want) & ok
     assert not bad.any(), f"argmax mismatch on decisive rows {bad.nonzero().flatten().tolist()}"
     return int(ok.sum())
+
+
+def oracle_stream_logits(orc: ref.Qwen2Ref, prompt, stream, max_len: int) -> torch.Tensor:
+    """Teacher-forced oracle: the logits before each token of ``stream`` when the oracle is
+    fed ``prompt`` and then the stream's own tokens (runners/multimodal.py:116-144 prefill,
+    then :296-313 one decode step per token).  Row i decides token i.  Following the GPU's
+    tokens, every step stays comparable past a near-tie (where the two may pick different
+    tokens) instead of ending the comparison there."""
+    cfg = orc.cfg
+    kp = [torch.zeros(2, max_len, cfg.num_kv_heads, cfg.head_dim) for _ in orc.layers]
+    vp = [torch.zeros_like(k) for k in kp]
+    lengths = torch.zeros(2, dtype=torch.int64)
+    L = len(prompt)
+    emb = orc.embed[torch.tensor(prompt)]
+    pos = torch.arange(L).view(1, -1).expand(3, -1)
+    rows = [orc.prefill(emb, pos, [L], [0], kp, vp, lengths)[0]]
+    for t in stream[:-1]:
+        rows.append(orc.decode_step([int(t)], kp, vp, lengths)[0])
+        lengths[0] += 1
+    return torch.stack(rows)
+
+
+def check_stream(stream, oracle_rows: torch.Tensor, cut: float, min_compared: int,
+                 label: str = "") -> int:
+    """Every token whose oracle top-1/top-2 margin exceeds ``cut`` (twice the measured
+    logit error) must be the oracle's argmax; returns how many were compared, which must
+    be at least ``min_compared``."""
+    margin = ref.top2_margin(oracle_rows)
+    want = oracle_rows.argmax(-1)
+    compared = 0
+    for i, g in enumerate(stream):
+        if margin[i] > cut:
+            compared += 1
+            assert int(g) == int(want[i]), (
+                f"{label} token {i}: got {g} want {int(want[i])} (margin {margin[i]:.4f} > {cut:.4f})")
+    print(f"[gpu-test] {label}: {compared}/{len(stream)} tokens compared "
+          f"(oracle margin > {cut:.4f})", flush=True)
+    assert compared >= min_compared, (label, compared, min_compared)
+    return compared
+
+
+def record_sampled_logits(runner):
+    """Wrap the runner's _sample_rows so a test sees the fp16 logits it samples from
+    (prefill segment ends, the last chunk of a chunked prompt): returns the list they are
+    appended to."""
+    seen = []
+    orig = runner._sample_rows
+
+    def wrapped(logits, seqs):
+        seen.append(logits.float().cpu().clone())
+        return orig(logits, seqs)
+
+    runner._sample_rows = wrapped
+    return seen

@@ -3,15 +3,18 @@
 Bar: fp16 logits within max-abs 2e-2 and cosine >= 0.9999
 of the oracle's fp16-faithful restatement; greedy ids equal to the oracle's argmax
 wherever the oracle's top-1/top-2 margin exceeds the measured logit error; int4
-dequantised weights bit-exact (test_gpu_kernels.py).  Free-running greedy
-continuations are compared token by token up to the first near-tie of the oracle.
+dequantised weights bit-exact (test_gpu_kernels.py).  Greedy streams are compared token
+by token against the oracle fed the same tokens (teacher forcing), on every token whose
+oracle margin exceeds twice the logit error measured in the same test; each test prints
+and bounds below how many tokens it compared.
 """
 
 import pytest
 import torch
 
 from oracle import qwen2_ref as ref
-from tests.helpers import check_ids, compare_logits, oracle_from_fp16, oracle_from_gptq
+from tests.helpers import (check_ids, check_stream, compare_logits, oracle_from_fp16,
+                           oracle_from_gptq, oracle_stream_logits, record_sampled_logits)
 
 pytestmark = pytest.mark.gpu
 
@@ -92,27 +95,6 @@ def test_decode_step_gptq(gpu, n):
     _decode_once(gpu, "gptq", 4, lengths, 4)
 
 
-def _greedy_oracle(orc, prompts, steps, max_len):
-    """Free-running greedy generation with the oracle: packed prefill then decode."""
-    cfg = orc.cfg
-    P = len(prompts)
-    kp = [torch.zeros(P + 1, max_len, cfg.num_kv_heads, cfg.head_dim) for _ in orc.layers]
-    vp = [torch.zeros_like(k) for k in kp]
-    lengths = torch.zeros(P + 1, dtype=torch.int64)
-    emb = torch.cat([orc.embed[torch.tensor(p)] for p in prompts], 0)
-    pos = torch.cat([torch.arange(len(p)).view(1, -1).expand(3, -1) for p in prompts], 1)
-    logits = orc.prefill(emb, pos, [len(p) for p in prompts], list(range(P)), kp, vp, lengths)
-    toks = [[t] for t in ref.greedy(logits)]
-    margins = [[m] for m in ref.top2_margin(logits).tolist()]
-    for _ in range(steps):
-        lg = orc.decode_step([t[-1] for t in toks], kp, vp, lengths)
-        lengths[:P] += 1
-        for b, (t, m) in enumerate(zip(ref.greedy(lg), ref.top2_margin(lg).tolist())):
-            toks[b].append(t)
-            margins[b].append(m)
-    return toks, margins
-
-
 @pytest.mark.parametrize("use_graph", [False, True])
 def test_runner_greedy_matches_oracle(gpu, use_graph):
     """NativeQwenVLRunner prefill + decode (eager and hipGraph) vs oracle greedy."""
@@ -126,6 +108,7 @@ def test_runner_greedy_matches_oracle(gpu, use_graph):
                synth.random_ids(17, shape.vocab_size, 5, "p1").tolist()]
     steps = 6
     runner = NativeQwenVLRunner(max_running=4, max_len=256, use_graph=use_graph, weights=w)
+    seen = record_sampled_logits(runner)
     seqs = [Sequence(Request(prompt=p, sampling=SamplingParams(max_new_tokens=steps + 1)))
             for p in prompts]
     for s in seqs:
@@ -133,13 +116,12 @@ def test_runner_greedy_matches_oracle(gpu, use_graph):
     runner.prefill(seqs)
     for _ in range(steps):
         runner.decode(seqs)
-    got = [s.output_token_ids for s in seqs]
-    exp, margins = _greedy_oracle(oracle_from_fp16(w, shape), prompts, steps, 256)
-    for b in range(len(prompts)):
-        for i, (g, e, m) in enumerate(zip(got[b], exp[b], margins[b])):
-            if m < 0.05:      # oracle near-tie: later tokens may legitimately diverge
-                break
-            assert g == e, f"seq {b} token {i}: got {g} want {e} (margin {m:.3f})"
+    orc = oracle_from_fp16(w, shape)
+    rows = [oracle_stream_logits(orc, p, s.output_token_ids, 256) for p, s in zip(prompts, seqs)]
+    err, _ = compare_logits(seen[0], torch.stack([r[0] for r in rows]))
+    total = sum(check_stream(s.output_token_ids, r, 2 * err + 1e-3, 0, f"seq {b}")
+                for b, (s, r) in enumerate(zip(seqs, rows)))
+    assert total >= len(prompts) * (steps + 1) // 2, total
 
 
 def test_graph_equals_eager_with_compaction(gpu):
@@ -322,6 +304,7 @@ def test_runner_chunked_prompt_matches_oracle(gpu, mode):
     w = synth.fp16_decoder(shape, seed=11, num_layers=3)
     prompts = [synth.random_ids(L, shape.vocab_size, 11, f"m{L}").tolist() for L in (20, 33, 150)]
     runner = NativeQwenVLRunner(max_running=4, max_len=256, use_graph=True, weights=w)
+    seen = record_sampled_logits(runner)
     seqs = [Sequence(Request(prompt=p, sampling=SamplingParams(max_new_tokens=16)))
             for p in prompts]
     for s in seqs:
@@ -340,12 +323,14 @@ def test_runner_chunked_prompt_matches_oracle(gpu, mode):
     for _ in range(3):
         runner.decode(seqs)
     assert [len(s.output_token_ids) for s in seqs] == [7, 7, 4]
-    exp, margins = _greedy_oracle(oracle_from_fp16(w, shape), prompts, 6, 256)
-    for i, s in enumerate(seqs):
-        for j, (g, e, m) in enumerate(zip(s.output_token_ids, exp[i], margins[i])):
-            if m < 0.05:      # oracle near-tie: later tokens may legitimately diverge
-                break
-            assert g == e, f"seq {i} token {j}: got {g} want {e} (margin {m:.3f})"
+    orc = oracle_from_fp16(w, shape)
+    rows = [oracle_stream_logits(orc, p, s.output_token_ids, 256) for p, s in zip(prompts, seqs)]
+    # logits the runner sampled the first tokens from: a and b's prefill, c's last chunk
+    err, _ = compare_logits(torch.cat([seen[0], seen[-1]]),
+                            torch.stack([rows[0][0], rows[1][0], rows[2][0]]))
+    total = sum(check_stream(s.output_token_ids, r, 2 * err + 1e-3, 0, f"{mode} seq {i}")
+                for i, (s, r) in enumerate(zip(seqs, rows)))
+    assert total >= 9, total
 
 
 def test_runner_from_gptq_checkpoint(gpu, tmp_path):
@@ -416,6 +401,7 @@ def test_full_depth_decode_fp16(gpu):
     cos = lambda a, b: torch.nn.functional.cosine_similarity(a, b, dim=-1).min().item()
     say(f"  gpu-f16oracle {d16:.4f} gpu-f32oracle {d32:.4f} f16oracle-f32oracle {noise:.4f}")
     assert cos(got, e16) >= 0.9999 and cos(got, e32) >= 0.9999
+    assert d16 <= 2e-2, d16                       # the north-star bar, fp16-faithful oracle
     assert d32 <= max(2e-2, 1.25 * noise), (d32, noise)
     check_ids(out, e32, max(d32, d16))
 
@@ -440,8 +426,15 @@ def test_runner_matches_golden_fixture(gpu):
     runner.prefill(seqs)
     for _ in range(len(gold["steps"]) - 1):
         runner.decode(seqs)
-    for i, st in enumerate(gold["steps"]):
-        for b in range(2):
-            if st["margin"][b] < 0.02:
-                return                     # past a near-tie the continuations may differ
+    # the fixture is the oracle's free-running stream: a sequence is compared up to its first
+    # token whose margin is within the 2e-2 logit bar (errors at this depth measure ~5e-3),
+    # after which the two streams may follow different, equally valid tokens
+    compared = 0
+    for b in range(2):
+        for i, st in enumerate(gold["steps"]):
+            if st["margin"][b] < 2e-2:
+                break
             assert seqs[b].output_token_ids[i] == st["tokens"][b], (i, b)
+            compared += 1
+    say(f"  {compared}/{2 * len(gold['steps'])} fixture tokens compared")
+    assert compared >= 8

@@ -315,6 +315,20 @@ int omni_lmhead_candidates(const void* x, int ldx, const void* weight_packed, in
 int omni_argmax_finalize(const float* cand_val, const int* cand_idx, int nblk, int M,
                          int64_t* ids_out, int64_t* next_ids, int64_t* lengths, void* stream);
 
+/* ---------------------------------------------------------------- allocation-free */
+
+/* No counterpart in the reference: omni_lmhead_candidates followed by omni_argmax_finalize
+ * in one call that allocates nothing and takes no workspace, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid it).  The candidates live in a device array the library holds once per GPU
+ * for the whole process (256 KiB: up to 32768 workgroup x row slots); shapes that would
+ * need more return OMNI_EUNSUPPORTED, as do M > 64 and N % 32 != 0.  Nothing has to start
+ * at zero; calls that overlap on one GPU (different streams) share the array and race.
+ * ids_out / logits_out / next_ids / lengths as in the two calls it stands for. */
+int omni_lmhead_argmax_noalloc(const void* x, int ldx, const void* weight_packed, int M, int N,
+                               int K, void* logits_out, int64_t* ids_out, int64_t* next_ids,
+                               int64_t* lengths, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -61,6 +61,7 @@ SIGNATURES = {
     "omni_lmhead_argmax_grid": [_I],
     "omni_lmhead_candidates": [_P, _I, _P, _I, _I, _I, _P, _P, _P, _P],
     "omni_argmax_finalize": [_P, _P, _I, _I, _P, _P, _P, _P],
+    "omni_lmhead_argmax_noalloc": [_P, _I, _P, _I, _I, _I, _P, _P, _P, _P, _P],
     "omni_gptq_repack": [_P, _P, _P, _P, _I, _I, _I, _P],
     "omni_f16_pack": [_P, _P, _I, _I, _I, _P],
     "omni_w4_dequant": [_P, _P, _P, _I, _I, _P],

@@ -34,6 +34,7 @@
 //                arrays reduced by omni_argmax_finalize.
 #include "common.h"
 
+#include <mutex>
 #include <type_traits>
 
 enum { W_INT4 = 0, W_FP16 = 1 };
@@ -1205,6 +1206,56 @@ extern "C" int omni_argmax_finalize(const float* cand_val, const int* cand_idx, 
                      cand_idx, nblk, M, ids_out, next_ids, lengths);
   OMNI_CHECK_LAUNCH();
   return OMNI_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free lm_head + greedy argmax, for callers that cannot allocate device memory
+// (code under HIP graph capture, tight serving loops).  The per-workgroup candidates live
+// in `scratch`, a file-scope device array every GPU holds once for the whole process:
+// NOALLOC_SLOTS (grid x rows) fp32 values, then as many int32 indices (256 KiB).  Every slot
+// a call reads, the same call's candidates launch wrote first, so nothing is cleared.
+// Calls that overlap on one GPU (two streams) share the array and race.
+// ---------------------------------------------------------------------------
+#define NOALLOC_SLOTS (512 * 64)
+#define NOALLOC_MAX_DEVICES 64
+
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SLOTS * 8];
+
+// This GPU's address of `scratch` (host code passes that, never the array's name), looked
+// up once per device with the device current; NULL if the lookup fails.
+static void* noalloc_scratch(int dev) {
+  static std::mutex mu;
+  static void* ptrs[NOALLOC_MAX_DEVICES] = {};
+  if (dev < 0 || dev >= NOALLOC_MAX_DEVICES) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+    ptrs[dev] = p;
+  }
+  return ptrs[dev];
+}
+
+extern "C" int omni_lmhead_argmax_noalloc(const void* x, int ldx, const void* weight_packed,
+                                          int M, int N, int K, void* logits_out, int64_t* ids_out,
+                                          int64_t* next_ids, int64_t* lengths, void* stream) {
+  if (M < 0 || N <= 0 || K <= 0) return OMNI_EINVAL;
+  if (M == 0) return OMNI_OK;
+  if (!x || !weight_packed || !ids_out) return OMNI_EINVAL;
+  if (M > 64 || (N & 31)) return OMNI_EUNSUPPORTED;
+  const int grid = omni_lmhead_argmax_grid(N);
+  if ((int64_t)grid * M > NOALLOC_SLOTS) return OMNI_EUNSUPPORTED;   // beyond the array
+  int dev = 0;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  unsigned char* base = (unsigned char*)noalloc_scratch(dev);
+  if (!base) return OMNI_EUNSUPPORTED;
+  float* cand_val = (float*)base;
+  int* cand_idx = (int*)(base + (size_t)NOALLOC_SLOTS * sizeof(float));
+  const int rc = omni_lmhead_candidates(x, ldx, weight_packed, M, N, K, logits_out, cand_val,
+                                        cand_idx, stream);
+  if (rc != OMNI_OK) return rc;
+  return omni_argmax_finalize(cand_val, cand_idx, grid, M, ids_out, next_ids, lengths, stream);
 }
 
 // ---------------------------------------------------------------------------

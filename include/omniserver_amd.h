@@ -77,6 +77,10 @@ int omni_embedding(const int64_t* ids, const void* table, int table_packed, int6
  * out fp16 [rows, n] = silu(g) * u in fp32. */
 int omni_silu_mul(const void* gate_up, void* out, int rows, int n, void* stream);
 
+/* silu_mul on bf16 gate_up (the reference's FP8 MLP route: gate_up.forward_prequant returns
+ * bf16, model/qwen2_llm.py:127-131): out bf16 [rows, n], fp32 math, bf16 stores (RNE). */
+int omni_silu_mul_bf16(const void* gate_up, void* out, int rows, int n, void* stream);
+
 /* ---------------------------------------------------------------- rope + KV pool */
 
 /* apply_mrope (model/qwen2_llm.py:59-72) in place on the q and k heads of qkv rows
@@ -123,15 +127,16 @@ int omni_kv_copy_slot(void* pool, int n_layers, int pool_rows, int max_len, int 
 
 /* _CacheView.flash_decode (cache/kv_prealloc.py:272-290): GQA decode attention over the
  * pool.  Token t (pool row slots[t], or t) attends to keys [0, L), L = kv_len[kv_by_slot ?
- * slot : t] + kv_add; out fp16 [T, n_heads, 128].  waves in {4, 8, 16} per workgroup;
+ * slot : t] + kv_add; out fp16 [T, n_heads, 128].  waves in {4, 8} per workgroup;
  * splits workgroups per (token, kv head) (1..64): splits > 1 writes partial softmax
- * states to workspace (fp32, >= T * n_kv * splits * (n_heads/n_kv) * 132) and merges them
- * in a second launch. */
+ * states to workspace (fp32, workspace_floats of capacity; a call that needs more than
+ * T * n_kv * splits * (n_heads/n_kv) * 132 is rejected with -1) and merges them in a
+ * second launch. */
 int omni_decode_attention(const void* q, int q_stride, const void* k_cache, const void* v_cache,
                           int pool_rows, int max_len, const int64_t* slots, const int64_t* kv_len,
                           int kv_by_slot, int kv_add, void* out, int T, int n_heads,
                           int n_kv_heads, int head_dim, float scale, int waves, int splits,
-                          float* workspace, void* stream);
+                          float* workspace, int64_t workspace_floats, void* stream);
 
 /* The decode step's attention fused with its producer (model/qwen2_llm.py:88-99 for one
  * decode token): q and the new k / v are formed from the qkv projection's fp32 split-K
@@ -140,8 +145,9 @@ int omni_decode_attention(const void* q, int q_stride, const void* k_cache, cons
  * pool[slot, lengths[slot]] (cache/kv_prealloc.py:253-261) and token t attends to keys
  * [0, lengths[slot]] (:272-290).  slots NULL = row t.  lengths are not advanced.
  * n_heads / n_kv_heads <= 8.  merge = 1: out fp16 [T, n_heads, 128] (a merge launch
- * follows when splits > 1); merge = 0: the split states stay in workspace (>= T * n_kv *
- * splits * G * 132 fp32) for omni_*_gemm_attn and out is not written.  rope_rows (may be
+ * follows when splits > 1); merge = 0: the split states stay in workspace (T * n_kv *
+ * splits * G * 132 fp32, within workspace_floats or the call is rejected) for
+ * omni_*_gemm_attn and out is not written.  waves in {4, 8}.  rope_rows (may be
  * NULL): token t's rotary row from omni_rope_rows instead of a cos/sin table lookup at its
  * position (cos_tab, sin_tab, max_pos, rope_delta are then unused). */
 int omni_decode_attention_fused(const float* qkv_partials, int nparts, const void* qkv_bias,
@@ -150,8 +156,8 @@ int omni_decode_attention_fused(const float* qkv_partials, int nparts, const voi
                                 int sec2, void* k_cache, void* v_cache, int pool_rows, int max_len,
                                 const int64_t* slots, const int64_t* lengths, void* out, int T,
                                 int n_heads, int n_kv_heads, int head_dim, float scale, int waves,
-                                int splits, float* workspace, int merge, const void* rope_rows,
-                                void* stream);
+                                int splits, float* workspace, int64_t workspace_floats, int merge,
+                                const void* rope_rows, void* stream);
 
 /* _PackedPrefillWriter.flash_prefill (cache/kv_prealloc.py:181-203) and the append form
  * of :149-174: token t attends causally to keys [0, kv_len[t]) of pool row slots[t].
@@ -281,6 +287,11 @@ int omni_vit_attention(const void* qkv, int ld, int S, int n_heads, int head_dim
 int omni_fp8_quant_rows(const void* x, int ldx, void* q, float* scale, int rows, int K,
                         float clamp_min, void* stream);
 
+/* omni_fp8_quant_rows on bf16 rows: quant_fp8 of the bf16 silu_mul output that an FP8
+ * down_proj takes directly (model/qwen2_llm.py:132-134, kernels/fp8_linear.py:45-63). */
+int omni_fp8_quant_rows_bf16(const void* x, int ldx, void* q, float* scale, int rows, int K,
+                             float clamp_min, void* stream);
+
 /* FP8Linear.forward / forward_prequant (kernels/fp8_linear.py:99-126):
  * y[m, n] = bf16((sum_k xq[m,k] wq[n,k]) * sa[m] * sw[n]) (fp32 accumulation, as
  * torch._scaled_mm with out_dtype bf16); out_bf16 = 1 stores that bf16 value plus
@@ -303,6 +314,10 @@ int omni_fp8_gemm_plan(int M, int N, int K, int* grid);
 /* Workgroups (= candidate rows per token) of omni_lmhead_candidates for vocab N. */
 int omni_lmhead_argmax_grid(int N);
 
+/* Rows M one omni_lmhead_candidates call takes at hidden size K (x is staged in LDS:
+ * 48 at K = 1536); callers split larger batches (helper, no reference counterpart). */
+int omni_lmhead_max_rows(int K);
+
 /* Tied lm_head (model/qwen2_llm.py:167-168, 190) with the greedy argmax of
  * runners/multimodal.py:306-310: per workgroup and row the max fp16 logit and its lowest
  * index go to cand_val/cand_idx ([grid][M]); logits_out fp16 [M, N] optional. */
@@ -322,7 +337,7 @@ int omni_argmax_finalize(const float* cand_val, const int* cand_idx, int nblk, i
  * allocate device memory (code under HIP graph capture, tight serving loops, harnesses
  * that forbid it).  The candidates live in a device array the library holds once per GPU
  * for the whole process (256 KiB: up to 32768 workgroup x row slots); shapes that would
- * need more return OMNI_EUNSUPPORTED, as do M > 64 and N % 32 != 0.  Nothing has to start
+ * need more return OMNI_EUNSUPPORTED, as do M > omni_lmhead_max_rows(K) and N % 32 != 0.  Nothing has to start
  * at zero; calls that overlap on one GPU (different streams) share the array and race.
  * ids_out / logits_out / next_ids / lengths as in the two calls it stands for. */
 int omni_lmhead_argmax_noalloc(const void* x, int ldx, const void* weight_packed, int M, int N,

@@ -33,15 +33,17 @@ SIGNATURES = {
     "omni_kv_copy_slot": [_P, _I, _I, _I, _I, _I, _I, _I64, _P, _P],
     "omni_embedding": [_P, _P, _I, _I64, _P, _I, _I, _P],
     "omni_silu_mul": [_P, _P, _I, _I, _P],
+    "omni_silu_mul_bf16": [_P, _P, _I, _I, _P],
     "omni_mrope_kv_write": [_P, _I, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I,
                             _I, _I, _I, _I, _P],
     "omni_mrope_kv_write_partials": [_P, _I, _P, _I, _P, _I, _P, _P, _P, _P, _P, _I, _P, _P, _P,
                                      _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P],
     "omni_decode_attention": [_P, _I, _P, _P, _I, _I, _P, _P, _I, _I, _P, _I, _I, _I, _I, _F, _I,
-                              _I, _P, _P],
+                              _I, _P, _I64, _P],
     "omni_decode_attention_fused": [_P, _I, _P, _I, _P, _P, _I, _P, _I, _I, _I, _P, _P, _I, _I,
-                                    _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _P, _I, _P, _P],
+                                    _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _P, _I64, _I, _P, _P],
     "omni_fp8_quant_rows": [_P, _I, _P, _P, _I, _I, _F, _P],
+    "omni_fp8_quant_rows_bf16": [_P, _I, _P, _P, _I, _I, _F, _P],
     "omni_fp8_gemm": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
     "omni_fp8_gemm_plan": [_I, _I, _I, ctypes.POINTER(_I)],
     "omni_w4a16_gemm_attn": [_P, _I, _I, _I, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I, _I,
@@ -59,6 +61,7 @@ SIGNATURES = {
     "omni_vit_attention": [_P, _I, _I, _I, _I, _P, _P, _I, _P, _I, _F, _P],
     "omni_gemm_slices": [_I, _I],
     "omni_lmhead_argmax_grid": [_I],
+    "omni_lmhead_max_rows": [_I],
     "omni_lmhead_candidates": [_P, _I, _P, _I, _I, _I, _P, _P, _P, _P],
     "omni_argmax_finalize": [_P, _P, _I, _I, _P, _P, _P, _P],
     "omni_lmhead_argmax_noalloc": [_P, _I, _P, _I, _I, _I, _P, _P, _P, _P, _P],

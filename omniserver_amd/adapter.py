@@ -11,7 +11,10 @@ Hugging Face checkpoint's (``checkpoint``); without a directory (the reference w
 look in its default cache paths, which do not exist offline) seeded synthetic weights
 of the real architecture are built (``synth``); ``weights=`` accepts an already built
 dict (fp16 or GPTQ layout).  ``quant="gptq"`` selects the int4 path (every decoder
-linear W4A16, embeddings / lm_head fp16, as kernels/marlin_linear.py:114-143).
+linear W4A16, embeddings / lm_head fp16, as kernels/marlin_linear.py:114-143);
+``"marlin"`` quantises the fp16 MLP linears to int4 by rounding (no calibration) and
+``"mixed"`` applies the default per-op plan (gate_up and down FP8 W8A8, attention
+projections fp16), as models/qwen2_vl.py:56-64 do.
 """
 
 from __future__ import annotations
@@ -33,8 +36,8 @@ class Qwen2VLAdapter:
                  shape: Optional[synth.DecoderShape] = None, seed: int = 0,
                  num_layers: Optional[int] = None, device="cuda", max_pos: int = 8192,
                  vision=None):
-        if quant not in (None, "gptq"):
-            raise ValueError(f"unsupported quant {quant!r} (None or 'gptq')")
+        if not self.supports_quant(quant):
+            raise ValueError(f"unsupported quant {quant!r} (None, 'marlin', 'gptq' or 'mixed')")
         self.device = torch.device(device)
         self.shape = shape or synth.DecoderShape()
         if num_layers is not None:
@@ -60,6 +63,13 @@ class Qwen2VLAdapter:
             weights = gen(self.shape, seed=seed)
         build = Qwen2LLM.from_gptq if quant == "gptq" else Qwen2LLM.from_fp16
         self._llm = build(weights, self.shape, self.device, max_pos=max_pos)
+        # models/qwen2_vl.py:56-64: RTN int4 MLP, or the per-op mixed-precision plan
+        if quant == "marlin":
+            from .mixed_precision import quantize_llm_marlin
+            quantize_llm_marlin(self._llm, scope="mlp")
+        elif quant == "mixed":
+            from .mixed_precision import apply_mixed
+            apply_mixed(self._llm)
         # vision tower (models/qwen2_vl.py:46-48): the checkpoint's visual.* tensors, a
         # given state dict, or (vision=True / an int depth) seeded synthetic weights
         self._vit = None
@@ -144,5 +154,6 @@ class Qwen2VLAdapter:
     def detokenize(self, token_ids) -> str:
         return " ".join(str(int(t)) for t in token_ids)
 
-    def supports_quant(self, quant) -> bool:
-        return quant in (None, "gptq")
+    @staticmethod
+    def supports_quant(quant) -> bool:
+        return quant in (None, "marlin", "gptq", "mixed")

@@ -491,25 +491,32 @@ static int launch_decode_attn(AttnArgs a, int n_kv_heads, int T, int G, int wave
 //   slots      int64 [T] pool rows (NULL = row t)
 //   kv_len     int64; keys visible to token t = kv_len[kv_by_slot ? slot : t] + kv_add
 //   out        fp16 [T, n_heads, 128]
-//   waves      waves per workgroup: 4, 8 or 16
+//   waves      waves per workgroup: 4 or 8
 //   splits     workgroups per (token, kv head); > 1 writes partial states to
-//              workspace (fp32, >= T * n_kv * splits * G * 132) merged by a second launch
+//              workspace (fp32, workspace_floats >= T * n_kv * splits * G * 132, else
+//              the call is rejected) merged by a second launch
+// fp32 workspace of the split states: [T][n_kv][splits][G][132].
+static int64_t attn_workspace_floats(int T, int n_kv, int splits, int G) {
+  return (int64_t)T * n_kv * splits * G * ATT_REC;
+}
+
 extern "C" int omni_decode_attention(const void* q, int q_stride, const void* k_cache,
                                      const void* v_cache, int pool_rows, int max_len,
                                      const int64_t* slots, const int64_t* kv_len, int kv_by_slot,
                                      int kv_add, void* out, int T, int n_heads, int n_kv_heads,
                                      int head_dim, float scale, int waves, int splits,
-                                     float* workspace, void* stream) {
+                                     float* workspace, int64_t workspace_floats, void* stream) {
   if (T < 0 || n_heads <= 0 || n_kv_heads <= 0 || pool_rows <= 0 || max_len <= 0) return OMNI_EINVAL;
   if (head_dim != ATT_HD || n_heads % n_kv_heads) return OMNI_EUNSUPPORTED;
   const int G = n_heads / n_kv_heads;
   if (G > ATT_MAXG) return OMNI_EUNSUPPORTED;
-  if (waves != 4 && waves != 8 && waves != 16) return OMNI_EINVAL;
+  if (waves != 4 && waves != 8) return OMNI_EINVAL;
   if (splits < 1 || splits > 64) return OMNI_EINVAL;
   if (q_stride < n_heads * ATT_HD || (q_stride & 7)) return OMNI_EINVAL;
   if (T == 0) return OMNI_OK;
   if (!q || !k_cache || !v_cache || !kv_len || !out) return OMNI_EINVAL;
-  if (splits > 1 && !workspace) return OMNI_EINVAL;
+  if (splits > 1 && (!workspace || workspace_floats < attn_workspace_floats(T, n_kv_heads, splits, G)))
+    return OMNI_EINVAL;
   AttnArgs a;
   a.q = (const half_t*)q;
   a.q_stride = q_stride;
@@ -554,9 +561,7 @@ static int launch_decode_attn(AttnArgs a, int n_kv_heads, int T, int G, int wave
     case 32: hipLaunchKernelGGL((decode_attn_kernel<8, 0>), grid, dim3(512), 0, st, a); break;
     case 33: hipLaunchKernelGGL((decode_attn_kernel<8, 1>), grid, dim3(512), 0, st, a); break;
     case 34: hipLaunchKernelGGL((decode_attn_kernel<8, 2>), grid, dim3(512), 0, st, a); break;
-    case 64: hipLaunchKernelGGL((decode_attn_kernel<16, 0>), grid, dim3(1024), 0, st, a); break;
-    case 65: hipLaunchKernelGGL((decode_attn_kernel<16, 1>), grid, dim3(1024), 0, st, a); break;
-    default: hipLaunchKernelGGL((decode_attn_kernel<16, 2>), grid, dim3(1024), 0, st, a); break;
+    default: return OMNI_EINVAL;
   }
   OMNI_CHECK_LAUNCH();
   if (splits > 1 && merge) {
@@ -582,8 +587,8 @@ extern "C" int omni_decode_attention_fused(
     const void* cos_tab, const void* sin_tab, int max_pos, const int64_t* rope_delta, int sec0,
     int sec1, int sec2, void* k_cache, void* v_cache, int pool_rows, int max_len,
     const int64_t* slots, const int64_t* lengths, void* out, int T, int n_heads, int n_kv_heads,
-    int head_dim, float scale, int waves, int splits, float* workspace, int merge,
-    const void* rope_rows, void* stream) {
+    int head_dim, float scale, int waves, int splits, float* workspace, int64_t workspace_floats,
+    int merge, const void* rope_rows, void* stream) {
   if (T < 0 || n_heads <= 0 || n_kv_heads <= 0 || pool_rows <= 0 || max_len <= 0) return OMNI_EINVAL;
   if (!rope_rows && max_pos <= 0) return OMNI_EINVAL;
   if (head_dim != ATT_HD || n_heads % n_kv_heads) return OMNI_EUNSUPPORTED;
@@ -591,13 +596,15 @@ extern "C" int omni_decode_attention_fused(
   const int G = n_heads / n_kv_heads;
   if (G > ATT_FUSED_MAXG) return OMNI_EUNSUPPORTED;
   if (nparts < 1 || nparts > ATT_MAXPARTS) return OMNI_EUNSUPPORTED;
-  if (waves != 4 && waves != 8 && waves != 16) return OMNI_EINVAL;
+  if (waves != 4 && waves != 8) return OMNI_EINVAL;
   if (splits < 1 || splits > 64) return OMNI_EINVAL;
   if (T == 0) return OMNI_OK;
   if (!qkv_partials || !k_cache || !v_cache || !lengths) return OMNI_EINVAL;
   if (!rope_rows && (!cos_tab || !sin_tab)) return OMNI_EINVAL;
   if (merge ? !out : false) return OMNI_EINVAL;
-  if ((splits > 1 || !merge) && !workspace) return OMNI_EINVAL;
+  if ((splits > 1 || !merge) &&
+      (!workspace || workspace_floats < attn_workspace_floats(T, n_kv_heads, splits, G)))
+    return OMNI_EINVAL;
   AttnArgs a;
   a.q = nullptr;
   a.q_stride = 0;

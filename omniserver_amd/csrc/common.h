@@ -191,6 +191,23 @@ __device__ __forceinline__ void sum_slices8(const float* __restrict__ base, int6
 // Split decode-attention state of one (token, kv head, query head): o[128] (unnormalised,
 // relative to m), m (running max of the base-2 scaled scores), l (sum of exp2(s - m)),
 // two pad floats; records are 16-byte aligned.
+// 16-bit storage that is fp16 or (BF16) bfloat16, read and written through fp32; bf16
+// stores round to nearest even and keep NaN quiet.
+typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+template <bool BF16>
+__device__ __forceinline__ float ld16f(unsigned short v) {
+  return BF16 ? __builtin_bit_cast(float, (uint32_t)v << 16) : (float)__builtin_bit_cast(half_t, v);
+}
+template <bool BF16>
+__device__ __forceinline__ unsigned short st16f(float f) {
+  if (BF16) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, f);
+    const uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+    return (unsigned short)((u & 0x7fffffffu) > 0x7f800000u ? ((u >> 16) | 0x0040u) : r);
+  }
+  return __builtin_bit_cast(unsigned short, (half_t)f);
+}
+
 #define ATT_REC 132
 
 // Merge of S split states for dims d0..d0+7: the record of split s sits at

@@ -653,18 +653,19 @@ static int num_cus() {
 
 // Row-wise e4m3 quantisation: s[r] = amax_k |x[r, k]| / 448 (clamped below at clamp_min
 // when clamp_min > 0), q[r, k] = e4m3(x[r, k] / s[r]).  One workgroup per row.
-__global__ __launch_bounds__(256) void fp8_quant_rows_kernel(const half_t* __restrict__ x, int ldx,
-                                                             uint8_t* __restrict__ q,
+template <bool BF16>
+__global__ __launch_bounds__(256) void fp8_quant_rows_kernel(const unsigned short* __restrict__ x,
+                                                             int ldx, uint8_t* __restrict__ q,
                                                              float* __restrict__ s, int K,
                                                              float clamp_min) {
   __shared__ float red[4];
   const int row = blockIdx.x;
-  const half_t* xr = x + (int64_t)row * ldx;
+  const unsigned short* xr = x + (int64_t)row * ldx;
   float amax = 0.f;
   for (int k = threadIdx.x * 8; k < K; k += 256 * 8) {
-    const half8_t v = *(const half8_t*)(xr + k);
+    const u16x8 v = *(const u16x8*)(xr + k);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf((float)v[e]));
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(ld16f<BF16>(v[e])));
   }
   amax = wave_max(amax);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
@@ -674,26 +675,37 @@ __global__ __launch_bounds__(256) void fp8_quant_rows_kernel(const half_t* __res
   if (clamp_min > 0.f) sc = fmaxf(sc, clamp_min);
   if (threadIdx.x == 0) s[row] = sc;
   for (int k = threadIdx.x * 8; k < K; k += 256 * 8) {
-    const half8_t v = *(const half8_t*)(xr + k);
+    const u16x8 v = *(const u16x8*)(xr + k);
     uint32_t lo = 0, hi = 0;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) lo |= (uint32_t)f32_to_e4m3fn((float)v[e] / sc) << (8 * e);
+    for (int e = 0; e < 4; ++e) lo |= (uint32_t)f32_to_e4m3fn(ld16f<BF16>(v[e]) / sc) << (8 * e);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) hi |= (uint32_t)f32_to_e4m3fn((float)v[4 + e] / sc) << (8 * e);
+    for (int e = 0; e < 4; ++e) hi |= (uint32_t)f32_to_e4m3fn(ld16f<BF16>(v[4 + e]) / sc) << (8 * e);
     *(uint2*)(q + (int64_t)row * K + k) = make_uint2(lo, hi);
   }
 }
 
-extern "C" int omni_fp8_quant_rows(const void* x, int ldx, void* xq, float* scale, int rows, int K,
-                                   float clamp_min, void* stream) {
+static int fp8_quant_rows_launch(const void* x, int ldx, void* xq, float* scale, int rows, int K,
+                                 float clamp_min, bool bf16, void* stream) {
   if (rows < 0 || K <= 0) return OMNI_EINVAL;
   if ((K & 7) || ldx < K || (ldx & 7)) return OMNI_EUNSUPPORTED;
   if (rows == 0) return OMNI_OK;
   if (!x || !xq || !scale) return OMNI_EINVAL;
-  hipLaunchKernelGGL(fp8_quant_rows_kernel, dim3(rows), dim3(256), 0, (hipStream_t)stream,
-                     (const half_t*)x, ldx, (uint8_t*)xq, scale, K, clamp_min);
+  auto kern = bf16 ? fp8_quant_rows_kernel<true> : fp8_quant_rows_kernel<false>;
+  hipLaunchKernelGGL(kern, dim3(rows), dim3(256), 0, (hipStream_t)stream,
+                     (const unsigned short*)x, ldx, (uint8_t*)xq, scale, K, clamp_min);
   OMNI_CHECK_LAUNCH();
   return OMNI_OK;
+}
+
+extern "C" int omni_fp8_quant_rows(const void* x, int ldx, void* xq, float* scale, int rows, int K,
+                                   float clamp_min, void* stream) {
+  return fp8_quant_rows_launch(x, ldx, xq, scale, rows, K, clamp_min, false, stream);
+}
+
+extern "C" int omni_fp8_quant_rows_bf16(const void* x, int ldx, void* xq, float* scale, int rows,
+                                        int K, float clamp_min, void* stream) {
+  return fp8_quant_rows_launch(x, ldx, xq, scale, rows, K, clamp_min, true, stream);
 }
 
 // Kernel choice by shape: the 256 x 256 tiles serve the long-K shapes (K >= 4096, M and N

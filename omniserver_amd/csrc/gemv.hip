@@ -538,22 +538,25 @@ static int dispatch_preset(const GemvArgs& a, int preset, hipStream_t st) {
   // weight groups in flight per column tile: 4 for int4 (16 bytes per lane and group), 2 for
   // fp16 (64 bytes; 4 kept twice the bytes in flight and measured 12 % slower fp16 steps)
   constexpr int PF = WF == W_FP16 ? 2 : 4;
+  // Presets whose register demand at 64 rows exceeds a wave's share (8-wave K splits of
+  // two tiles per wave, and every form with the merged attention input but preset 1) are
+  // not built: they spilled without being faster at the shapes they were swept on.
   if constexpr (EPI == EPI_SILU) {
     switch (preset) {
       case 1: return dispatch_mb<WF, EPI, 2, 8, 1, PF>(a, st);
       case 2: return dispatch_mb<WF, EPI, 2, 4, 2, PF>(a, st);
       case 3: return dispatch_mb<WF, EPI, 2, 2, 4, PF>(a, st);
       case 4: return dispatch_mb<WF, EPI, 2, 3, 4, PF>(a, st);
-      case 5: return dispatch_mb<WF, EPI, 2, 2, 8, PF>(a, st);
       // x staged before the weights are requested (XF)
       case 6: return dispatch_mb<WF, EPI, 2, 3, 4, PF, 0, 1>(a, st);
       case 7: return dispatch_mb<WF, EPI, 2, 2, 4, PF, 0, 1>(a, st);
-      case 8: return dispatch_mb<WF, EPI, 2, 4, 4, PF, 0, 1>(a, st);
       case 9: return dispatch_mb<WF, EPI, 2, 8, 1, PF, 0, 1>(a, st);
-      default: return dispatch_mb<WF, EPI, 2, 4, 4, PF>(a, st);
+      default: return OMNI_EINVAL;
     }
   } else if constexpr (EPI == EPI_ARGMAX) {
     return dispatch_mb<WF, EPI, 2, 8, 1, PF>(a, st);
+  } else if constexpr (XS == 1) {
+    return preset == 1 ? dispatch_mb<WF, EPI, 1, 8, 1, PF, XS>(a, st) : OMNI_EINVAL;
   } else {
     switch (preset) {
       case 0: return dispatch_mb<WF, EPI, 1, 8, 2, PF, XS>(a, st);
@@ -997,21 +1000,24 @@ __global__ __launch_bounds__(512, 1) void lmhead_kernel(GemvArgs a) {
   }
   __syncthreads();
 
+  // 32-k steps per batch: 16 (512 k); 8 at 64 rows, where two 16-step batches in flight
+  // beside the 4 row blocks' accumulators and running maxima exceed a wave's registers
+  constexpr int NBU = MB >= 4 ? 8 : 16;
   const int NT = a.N >> 4;
   const int KS32 = K >> 5;                     // 32-k steps per tile
-  const int BPT = K >> 9;                      // 512-k batches per tile (K % 512 == 0)
+  const int BPT = K / (32 * NBU);              // batches per tile (K % 512 == 0)
   const int G = gridDim.x;
   const int blk = xcd_logical_block(blockIdx.x, G);
   const int t0 = (int)((int64_t)blk * NT / G), t1 = (int)((int64_t)(blk + 1) * NT / G);
   const int ntw = t1 - t0 > wave ? (t1 - t0 - wave + 7) / 8 : 0;   // this wave's tiles
   const int nb = ntw * BPT;
   const half8_t* wp = (const half8_t*)a.w + lane;
-  auto load_batch = [&](half8_t (&buf)[16], int b) {
+  auto load_batch = [&](half8_t (&buf)[NBU], int b) {
     const int bc = min(b, max(nb - 1, 0));        // past the end: re-read the last batch
     const int tile = min(t0 + wave + 8 * (bc / BPT), NT - 1);
-    const int s0 = (bc % BPT) * 16;               // first 32-k step of the batch
+    const int s0 = (bc % BPT) * NBU;              // first 32-k step of the batch
 #pragma unroll
-    for (int u = 0; u < 16; ++u)
+    for (int u = 0; u < NBU; ++u)
       buf[u] = __builtin_nontemporal_load(wp + ((int64_t)tile * KS32 + s0 + u) * 64);
   };
 
@@ -1028,10 +1034,10 @@ __global__ __launch_bounds__(512, 1) void lmhead_kernel(GemvArgs a) {
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) acc[mb] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-  auto use_batch = [&](const half8_t (&buf)[16], int b) {
-    const int kb = (b % BPT) * 512;
+  auto use_batch = [&](const half8_t (&buf)[NBU], int b) {
+    const int kb = (b % BPT) * (32 * NBU);
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
+    for (int u = 0; u < NBU; ++u) {
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
         const half8_t af = *(const half8_t*)(xs + (16 * mb + c16) * xstride + kb + 32 * u + 8 * q16);
@@ -1059,7 +1065,7 @@ __global__ __launch_bounds__(512, 1) void lmhead_kernel(GemvArgs a) {
   };
 
   // 2. the stream: batches b (A) and b + 1 (B) in flight
-  half8_t ba[16], bb[16];
+  half8_t ba[NBU], bb[NBU];
   load_batch(ba, 0);
   load_batch(bb, 1);
   for (int b = 0; b < nb; b += 2) {
@@ -1103,6 +1109,15 @@ __global__ __launch_bounds__(512, 1) void lmhead_kernel(GemvArgs a) {
     a.cand_val[(int64_t)blockIdx.x * a.M + m] = v;
     a.cand_idx[(int64_t)blockIdx.x * a.M + m] = ix;
   }
+}
+
+// Rows one omni_lmhead_candidates call takes for hidden size K: x is staged in LDS as
+// whole 16-row blocks of K + 8 halves, at most 64 rows (48 at K = 1536 in 160 KiB).
+extern "C" int omni_lmhead_max_rows(int K) {
+  if (K <= 0) return 0;
+  const size_t per16 = (size_t)16 * (K + 8) * sizeof(half_t);
+  const int blocks = (int)(max_dynamic_lds() / per16);
+  return (blocks > 4 ? 4 : blocks) * 16;
 }
 
 // Candidate slots per row written by omni_lmhead_candidates (= its grid size).

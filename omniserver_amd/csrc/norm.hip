@@ -181,7 +181,9 @@ __global__ __launch_bounds__(MAXT) void rownorm_kernel(const half_t* x, const fl
   half8_t v;
   if (PARTS) {
     float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    sum_slices8<16>(parts + (size_t)row * H + cc * 8, (int64_t)rows * H, nparts, sum);
+    // 16 slices in flight per batch at 256 threads; 8 at 1024 (a quarter of the registers)
+    sum_slices8<MAXT <= 256 ? 16 : 8>(parts + (size_t)row * H + cc * 8, (int64_t)rows * H, nparts,
+                                       sum);
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = (half_t)sum[e];
   } else {
@@ -388,24 +390,28 @@ extern "C" int omni_embedding(const int64_t* ids, const void* table, int table_p
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float silu_f32(float g) { return g * (1.0f / (1.0f + __expf(-g))); }
 
-__global__ __launch_bounds__(256) void silu_mul_kernel(const half_t* __restrict__ gu,
-                                                      half_t* __restrict__ out, int rows, int n) {
+// fp16 (or, BF16, bf16 as the reference's FP8 route feeds it, qwen2_llm.py:130-131) in and out.
+template <bool BF16>
+__global__ __launch_bounds__(256) void silu_mul_kernel(const unsigned short* __restrict__ gu,
+                                                      unsigned short* __restrict__ out, int rows,
+                                                      int n) {
 #pragma clang fp contract(off)
   const int nchunk = n >> 3;
   const int64_t total = (int64_t)rows * nchunk;
   for (int64_t i = blockIdx.x * 256LL + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
     const int row = (int)(i / nchunk);
     const int c = (int)(i % nchunk);
-    half8_t g = *(const half8_t*)(gu + (size_t)row * 2 * n + c * 8);
-    half8_t u = *(const half8_t*)(gu + (size_t)row * 2 * n + n + c * 8);
-    half8_t o;
+    const u16x8 g = *(const u16x8*)(gu + (size_t)row * 2 * n + c * 8);
+    const u16x8 u = *(const u16x8*)(gu + (size_t)row * 2 * n + n + c * 8);
+    u16x8 o;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = (half_t)(silu_f32((float)g[e]) * (float)u[e]);
-    *(half8_t*)(out + (size_t)row * n + c * 8) = o;
+    for (int e = 0; e < 8; ++e) o[e] = st16f<BF16>(silu_f32(ld16f<BF16>(g[e])) * ld16f<BF16>(u[e]));
+    *(u16x8*)(out + (size_t)row * n + c * 8) = o;
   }
 }
 
-extern "C" int omni_silu_mul(const void* gate_up, void* out, int rows, int n, void* stream) {
+static int silu_mul_launch(const void* gate_up, void* out, int rows, int n, bool bf16,
+                           void* stream) {
   if (rows < 0 || n <= 0) return OMNI_EINVAL;
   if ((n & 7) != 0) return OMNI_EUNSUPPORTED;
   if (rows == 0) return OMNI_OK;
@@ -413,8 +419,17 @@ extern "C" int omni_silu_mul(const void* gate_up, void* out, int rows, int n, vo
   int64_t work = (int64_t)rows * (n >> 3);
   int grid = (int)((work + 255) / 256);
   if (grid > 8192) grid = 8192;
-  hipLaunchKernelGGL(silu_mul_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream,
-                     (const half_t*)gate_up, (half_t*)out, rows, n);
+  auto kern = bf16 ? silu_mul_kernel<true> : silu_mul_kernel<false>;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, (hipStream_t)stream,
+                     (const unsigned short*)gate_up, (unsigned short*)out, rows, n);
   OMNI_CHECK_LAUNCH();
   return OMNI_OK;
+}
+
+extern "C" int omni_silu_mul(const void* gate_up, void* out, int rows, int n, void* stream) {
+  return silu_mul_launch(gate_up, out, rows, n, false, stream);
+}
+
+extern "C" int omni_silu_mul_bf16(const void* gate_up, void* out, int rows, int n, void* stream) {
+  return silu_mul_launch(gate_up, out, rows, n, true, stream);
 }

@@ -74,9 +74,13 @@ def add_rms_norm_fp8(x, residual, weight, eps):
 
 
 def silu_mul_out(gate_up, out):
-    require_cuda(gate_up, out, dtype=torch.float16)
+    """fp16 in/out, or bf16 in/out (the fp8 MLP route's gate_up.forward_prequant output)."""
+    require_cuda(gate_up, out)
+    if gate_up.dtype != out.dtype or gate_up.dtype not in (torch.float16, torch.bfloat16):
+        raise TypeError(f"silu_mul takes fp16 or bf16 (got {gate_up.dtype} -> {out.dtype})")
     m, n2 = _rows(gate_up)
-    call("omni_silu_mul", ptr(gate_up), ptr(out), m, n2 // 2, stream())
+    fn = "omni_silu_mul_bf16" if gate_up.dtype == torch.bfloat16 else "omni_silu_mul"
+    call(fn, ptr(gate_up), ptr(out), m, n2 // 2, stream())
     return out
 
 

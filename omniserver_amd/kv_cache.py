@@ -110,6 +110,21 @@ class PreallocatedKVCache:
     def view(self, n: int, rope_delta: torch.Tensor | None = None) -> "CacheView":
         return CacheView(self, n, rope_delta)
 
+    def view_graph(self, n: int, write_pos: torch.Tensor, flat: torch.Tensor | None = None,
+                   seqused: torch.Tensor | None = None,
+                   rope_delta: torch.Tensor | None = None) -> "CacheView":
+        """Static view for a captured step (kv_prealloc.py:90-92): write positions come
+        from the caller's buffer ``write_pos`` [n] (int64, updated outside the graph) and
+        lengths are not advanced.  ``flat`` / ``seqused`` (the reference's precomputed
+        row * max_len + pos and pos + 1) are accepted and unused: the kernels derive both
+        from write_pos."""
+        return CacheView(self, n, rope_delta, write_pos=write_pos)
+
+    def prefill_cache(self, slot: int) -> "ChunkedPrefillWriter":
+        """One sequence's prefill into ``slot`` (kv_prealloc.py:94-97): its forward's tokens
+        go to pool[slot, :L], lengths[slot] = L."""
+        return ChunkedPrefillWriter(self, slot, 0)
+
     def packed_prefill_cache(self, slots: Sequence[int], seg_lengths: Sequence[int]):
         return PackedPrefillWriter(self, slots, seg_lengths)
 
@@ -132,26 +147,82 @@ class PreallocatedKVCache:
         nh = self.n_heads
         if out.numel() < n * nh * self.head_dim:
             raise ValueError("attention output buffer too small")
-        w, s = plan or self.attn_plan or decode_plan(n, self.n_kv_heads, self.max_len)
-        if n > self.max_batch or s > MAX_ATTN_SPLITS:
-            raise ValueError("attention plan exceeds the pool workspace")
+        w, s = self.checked_plan(n, plan)
         call("omni_decode_attention", ptr(q), q_stride, ptr(self.k[layer_idx]),
              ptr(self.v[layer_idx]), self.max_batch, self.max_len, ptr(slots), ptr(kv_len),
              int(kv_by_slot), kv_add, ptr(out), n, nh, self.n_kv_heads, self.head_dim,
-             float(scale), w, s, ptr(self._attn_ws), stream())
+             float(scale), w, s, ptr(self._attn_ws), self._attn_ws.numel(), stream())
         return out
+
+    def checked_plan(self, n: int, plan: tuple | None = None) -> tuple:
+        """(waves, splits) for n tokens: the given plan, the pool's override or decode_plan(),
+        refused when its split states would not fit the pool's workspace (the library also
+        checks the capacity it is given)."""
+        w, s = plan or self.attn_plan or decode_plan(n, self.n_kv_heads, self.max_len)
+        if n > self.max_batch or not 1 <= s <= MAX_ATTN_SPLITS or w not in (4, 8):
+            raise ValueError(f"attention plan (waves {w}, splits {s}) for {n} tokens exceeds "
+                             f"the pool workspace ({self.max_batch} rows, {MAX_ATTN_SPLITS} splits)")
+        return w, s
 
 
 class CacheView:
     """Single-forward decode adapter over pool rows [0, n) (kv_prealloc.py:232-290).
 
-    Positions and write positions are read on the device from ``pool.lengths`` (and the
-    per-slot ``rope_delta``), so the same view serves eager and captured decode."""
+    Write positions are read on the device from ``pool.lengths`` (eager: advanced by one
+    after the step, ``finish``) or, for a view made by ``view_graph``, from the caller's
+    ``write_pos`` buffer (never advanced here); positions add the per-slot ``rope_delta``.
+    Besides this build's fused protocol it has the reference's ``flash_decode`` and
+    ``update`` (the SDPA route, :263-270) and the transformers-cache queries."""
 
-    def __init__(self, pool: PreallocatedKVCache, n: int, rope_delta: torch.Tensor | None):
+    def __init__(self, pool: PreallocatedKVCache, n: int, rope_delta: torch.Tensor | None,
+                 write_pos: torch.Tensor | None = None):
         self.pool = pool
         self.n = n
         self.rope_delta = rope_delta
+        self._graph = write_pos is not None
+        if self._graph and (write_pos.dtype != torch.int64 or write_pos.numel() < n):
+            raise ValueError("write_pos must hold n int64 positions")
+        self.kv_pos = write_pos if self._graph else pool.lengths
+        self._snap = None                 # (write positions, window) for update()
+
+    def finish(self) -> None:
+        """After the step's last layer: eager views advance lengths[:n] by one (the graph
+        runner advances them outside the graph)."""
+        if not self._graph:
+            self.pool.lengths[:self.n] += 1
+
+    # ---- the reference's SDPA route and cache queries (kv_prealloc.py:240-300) -------
+    def _window(self):
+        if self._snap is None:
+            wp = self.kv_pos[:self.n].clone()
+            ret = self.pool.max_len if self._graph else int(wp.max().item()) + 1
+            self._snap = (wp, ret)
+        return self._snap
+
+    def update(self, key, value, layer_idx, cache_kwargs=None):
+        """key/value [n, n_kv, 1, hd] (rotated): written at each row's write position; on
+        the last layer (eager) lengths[:n] = write position + 1.  Returns the valid K/V
+        window [n, n_kv, L, hd] for SDPA (L = max write position + 1, or max_len)."""
+        pool, n = self.pool, self.n
+        wp, ret = self._window()
+        rows = torch.arange(n, device=wp.device)
+        flat = rows * pool.max_len + wp
+        nkv, hd = pool.n_kv_heads, pool.head_dim
+        pool.k[layer_idx].view(-1, nkv, hd).index_copy_(0, flat, key[:, :, 0, :].to(torch.float16))
+        pool.v[layer_idx].view(-1, nkv, hd).index_copy_(0, flat, value[:, :, 0, :].to(torch.float16))
+        if layer_idx == pool.n_layers - 1 and not self._graph:
+            pool.lengths[:n] = wp + 1
+        return (pool.k[layer_idx][:n, :ret].transpose(1, 2),
+                pool.v[layer_idx][:n, :ret].transpose(1, 2))
+
+    def get_seq_length(self, layer_idx: int = 0) -> int:
+        return self._window()[1] - 1
+
+    def get_mask_sizes(self, cache_position, layer_idx: int = 0):
+        return self._window()[1], 0
+
+    def get_max_cache_shape(self):
+        return self.pool.max_len
 
     def rope_and_write(self, qkv: torch.Tensor, layer_idx: int, cos_tab, sin_tab,
                        mrope_section, parts=None) -> None:
@@ -162,7 +233,7 @@ class CacheView:
         pool = self.pool
         s0, s1, s2 = mrope_section
         if parts is None:
-            call("omni_mrope_kv_write", ptr(qkv), qkv.stride(0), None, ptr(pool.lengths),
+            call("omni_mrope_kv_write", ptr(qkv), qkv.stride(0), None, ptr(self.kv_pos),
                  ptr(self.rope_delta), ptr(cos_tab), ptr(sin_tab), cos_tab.shape[0],
                  ptr(pool.k[layer_idx]), ptr(pool.v[layer_idx]), None, None, pool.max_batch,
                  pool.max_len, self.n, pool.n_heads, pool.n_kv_heads, pool.head_dim, s0, s1, s2,
@@ -170,22 +241,22 @@ class CacheView:
             return
         pbuf, S, bias, bar = parts
         call("omni_mrope_kv_write_partials", ptr(qkv), qkv.stride(0), ptr(pbuf), S, ptr(bias),
-             int(bar), None, ptr(pool.lengths), ptr(self.rope_delta), ptr(cos_tab), ptr(sin_tab),
+             int(bar), None, ptr(self.kv_pos), ptr(self.rope_delta), ptr(cos_tab), ptr(sin_tab),
              cos_tab.shape[0], ptr(pool.k[layer_idx]), ptr(pool.v[layer_idx]), None, None,
              pool.max_batch, pool.max_len, self.n, pool.n_heads, pool.n_kv_heads, pool.head_dim,
              s0, s1, s2, stream())
 
     def attend_qkv(self, qkv: torch.Tensor, layer_idx: int, scale: float, out: torch.Tensor,
                    plan: tuple | None = None) -> torch.Tensor:
-        """Attention for rows [0, n): keys [0, lengths[row]] (the token just written)."""
-        return self.pool.attend(qkv, qkv.stride(0), layer_idx, self.pool.lengths, True, 1, out,
+        """Attention for rows [0, n): keys [0, write position] (the token just written)."""
+        return self.pool.attend(qkv, qkv.stride(0), layer_idx, self.kv_pos, True, 1, out,
                                 self.n, scale, plan=plan)
 
     def rope_rows(self, cos_tab, sin_tab, out: torch.Tensor) -> torch.Tensor:
         """out [n, 128] fp16 = cos | sin rows at each row's write position lengths[row] +
         rope_delta[row] (one per decode step, for every layer's attend_fused)."""
         pool = self.pool
-        call("omni_rope_rows", None, ptr(pool.lengths), ptr(self.rope_delta), ptr(cos_tab),
+        call("omni_rope_rows", None, ptr(self.kv_pos), ptr(self.rope_delta), ptr(cos_tab),
              ptr(sin_tab), cos_tab.shape[0], pool.max_batch, self.n, ptr(out), stream())
         return out
 
@@ -201,14 +272,14 @@ class CacheView:
         split softmax states stay in the pool's workspace and (states, splits) is returned
         for the o_proj that merges them (forward_partial_attn)."""
         pool, n = self.pool, self.n
-        w, s = plan or pool.attn_plan or decode_plan(n, pool.n_kv_heads, pool.max_len)
+        w, s = pool.checked_plan(n, plan)
         s0, s1, s2 = mrope_section
         call("omni_decode_attention_fused", ptr(qparts), nparts, ptr(bias), int(bias_after_round),
              ptr(cos_tab), ptr(sin_tab), cos_tab.shape[0], ptr(self.rope_delta), s0, s1, s2,
              ptr(pool.k[layer_idx]), ptr(pool.v[layer_idx]), pool.max_batch, pool.max_len, None,
-             ptr(pool.lengths), ptr(out), n, pool.n_heads, pool.n_kv_heads, pool.head_dim,
-             float(scale), w, s, ptr(pool._attn_ws), int(out is not None), ptr(rope_rows),
-             stream())
+             ptr(self.kv_pos), ptr(out), n, pool.n_heads, pool.n_kv_heads, pool.head_dim,
+             float(scale), w, s, ptr(pool._attn_ws), pool._attn_ws.numel(), int(out is not None),
+             ptr(rope_rows), stream())
         return out if out is not None else (pool._attn_ws, s)
 
     def flash_decode(self, q, key, value, layer_idx, scale):
@@ -217,15 +288,15 @@ class CacheView:
         layer."""
         pool, n = self.pool, self.n
         rows = torch.arange(n, device=q.device)
-        flat = rows * pool.max_len + pool.lengths[:n]
+        flat = rows * pool.max_len + self.kv_pos[:n]
         nkv, hd = pool.n_kv_heads, pool.head_dim
         pool.k[layer_idx].view(-1, nkv, hd).index_copy_(0, flat, key.to(torch.float16))
         pool.v[layer_idx].view(-1, nkv, hd).index_copy_(0, flat, value.to(torch.float16))
         q = q.contiguous()
         out = torch.empty_like(q)
-        pool.attend(q, q.shape[1] * q.shape[2], layer_idx, pool.lengths, True, 1, out, n, scale)
+        pool.attend(q, q.shape[1] * q.shape[2], layer_idx, self.kv_pos, True, 1, out, n, scale)
         if layer_idx == pool.n_layers - 1:
-            pool.lengths[:n] += 1
+            self.finish()
         return out
 
 
@@ -296,6 +367,22 @@ class PackedPrefillWriter:
         for s, st, L in zip(self.slots, self.starts, self.seg):
             self.pool.lengths[s] = st + L
             self.pool._active = max(self.pool._active, s + 1)
+
+    def update(self, k, v, layer_idx, cache_kwargs=None):
+        """The reference's SDPA route (kv_prealloc.py:205-215, 222-229): k, v [1, n_kv, T, hd]
+        (rotated) of the packed tokens, each segment's rows written to its slot at its start;
+        lengths set on the last layer.  Returns k, v unchanged (the caller attends over the
+        packed tokens with its own mask)."""
+        pool = self.pool
+        self.bind(k.shape[2])
+        off = 0
+        for slot, st, L in zip(self.slots, self.starts, self.seg):
+            pool.k[layer_idx][slot, st:st + L] = k[0, :, off:off + L].transpose(0, 1)
+            pool.v[layer_idx][slot, st:st + L] = v[0, :, off:off + L].transpose(0, 1)
+            off += L
+        if layer_idx == pool.n_layers - 1:
+            self.finish()
+        return k, v
 
     def flash_prefill(self, q, k, v, layer_idx, scale):
         """Reference protocol (kv_prealloc.py:181-203, 121-146): q [T, nh, hd], k/v

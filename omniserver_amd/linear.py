@@ -60,6 +60,31 @@ def _plan(fmt: str, K: int, N: int) -> Tuple[int, int, int]:
     return (2, 1, ks)
 
 
+def rtn_int4(weight: torch.Tensor, group_size: int = 128):
+    """Round-to-nearest symmetric int4 (uint4b8) of an fp16 weight [N, K], the quantiser
+    the reference's MarlinInt4Linear calls (vLLM's quantize_weights for uint4b8, group
+    ``group_size`` along K): per group and output column, in fp16,
+    s = max(|max_k w| / 7, |min_k w| / 8), q = clamp(round(w / s), -8, 7) + 8.  Returns
+    the AutoGPTQ tensors (qweight int32 [K/8, N], k % 8 at bits 4 (k % 8); scales fp16
+    [K/group, N]) that GPTQLinear takes; the kernels then compute with fp16((q - 8) s).
+    Load-time tensor work on the weight's device."""
+    N, K = weight.shape
+    if K % group_size or K % 8:
+        raise ValueError(f"K = {K} is not a multiple of the group size {group_size}")
+    w = weight.t().contiguous().to(torch.float16).view(K // group_size, group_size, N)
+    mx = w.amax(1, keepdim=True)
+    mn = w.amin(1, keepdim=True)
+    s = torch.maximum((mx / 7.0).abs(), (mn / -8.0).abs())
+    # an all-zero group has s = 0: its codes are 8 (value 0) rather than 0/0
+    q = torch.round(w / torch.where(s == 0, torch.ones_like(s), s)).to(torch.int32)
+    q = torch.clamp(q, -8, 7) + 8                                         # [K/g, g, N]
+    q = q.view(K // 8, 8, N)
+    shifts = (torch.arange(8, device=q.device, dtype=torch.int32) * 4).view(1, 8, 1)
+    qweight = (q << shifts).sum(1, dtype=torch.int64).to(torch.int64)
+    qweight = torch.where(qweight >= 2 ** 31, qweight - 2 ** 32, qweight).to(torch.int32)
+    return qweight.contiguous(), s.view(K // group_size, N).contiguous()
+
+
 class _Skinny(nn.Module):
     """Shared launch logic of the packed-weight linears."""
 
@@ -194,6 +219,18 @@ class GPTQLinear(_Skinny):
              ptr(self.scales_packed), ptr(self.bias), 1, None, 0, ptr(partial), M, self.N,
              self.K, epilogue, ksplit, preset, stream())
 
+    @classmethod
+    def from_linear_rtn(cls, linear, group_size: int = 128, fuse_silu: bool | None = None):
+        """Round-to-nearest int4 of an fp16 linear with no calibration, the reference's
+        MarlinInt4Linear (kernels/marlin_linear.py:65-80: vLLM marlin_quantize, uint4b8,
+        symmetric, group 128 along K): see rtn_int4.  ``linear`` is an nn.Linear-like module
+        (weight [N, K], bias) or an F16Linear (unpacked; its gate|up fusion kept)."""
+        if fuse_silu is None:
+            fuse_silu = bool(getattr(linear, "fuse_silu", False))
+        w = linear.dense_weight() if hasattr(linear, "dense_weight") else linear.weight.data
+        qweight, scales = rtn_int4(w.to(torch.float16), group_size)
+        return cls(qweight, scales, getattr(linear, "bias", None), group_size, fuse_silu)
+
     def dequantized(self) -> torch.Tensor:
         """W^T [K, N] fp16 as the kernels see it (columns in packed order)."""
         w = torch.empty(self.K, self.N, device=self.qweight_packed.device, dtype=torch.float16)
@@ -224,6 +261,17 @@ class F16Linear(_Skinny):
     @classmethod
     def from_linear(cls, linear: nn.Linear, fuse_silu: bool = False) -> "F16Linear":
         return cls(linear.weight.data, linear.bias, fuse_silu=fuse_silu)
+
+    def dense_weight(self) -> torch.Tensor:
+        """The nn.Linear weight [N, K] fp16 back from the packed layout (element (t, s, l, e)
+        of tile t is W[16 t' + l % 16, 32 s + 8 (l // 16) + e], t' the tile before the
+        gate|up interleave), for building other linear kinds from this one."""
+        NT, KS = self.N // 16, self.K // 32
+        w = self.weight_packed.view(NT, KS, 4, 16, 8).permute(0, 3, 1, 2, 4)
+        w = w.reshape(NT, 16, self.K)
+        if self.fuse_silu:
+            w = torch.cat([w[0::2], w[1::2]], 0)
+        return w.reshape(self.N, self.K).contiguous()
 
     def _call(self, x2d, out, partial, epilogue, ksplit, preset):
         call("omni_f16_gemm", ptr(x2d), x2d.stride(0), ptr(self.weight_packed), ptr(self.bias),
@@ -262,17 +310,25 @@ class FP8Linear(nn.Module):
              0.0, stream())
         self.bias = None if bias is None else bias.to(device=dev, dtype=torch.float16).contiguous()
 
+    @classmethod
+    def from_linear(cls, linear) -> "FP8Linear":
+        """From an fp16 linear (fp8_linear.py:93-97, rowwise): an nn.Linear-like module
+        (weight [N, K], bias) or an F16Linear (unpacked)."""
+        w = linear.dense_weight() if hasattr(linear, "dense_weight") else linear.weight.data
+        return cls(w.to(torch.float16), getattr(linear, "bias", None))
+
     @property
     def out_features(self) -> int:
         return self.N
 
     def quantize_input(self, x2d: torch.Tensor):
-        """quant_fp8: (xq e4m3 bytes [M, K], scale fp32 [M, 1])."""
+        """quant_fp8 (fp8_linear.py:45-63) of fp16 or bf16 rows: (xq e4m3 bytes [M, K],
+        scale fp32 [M, 1])."""
         M = x2d.shape[0]
         xq = torch.empty(M, self.K, device=x2d.device, dtype=torch.uint8)
         sa = torch.empty(M, 1, device=x2d.device, dtype=torch.float32)
-        call("omni_fp8_quant_rows", ptr(x2d), x2d.stride(0), ptr(xq), ptr(sa), M, self.K, 0.0,
-             stream())
+        fn = "omni_fp8_quant_rows_bf16" if x2d.dtype == torch.bfloat16 else "omni_fp8_quant_rows"
+        call(fn, ptr(x2d), x2d.stride(0), ptr(xq), ptr(sa), M, self.K, 0.0, stream())
         return xq, sa
 
     def gemm_out(self, xq: torch.Tensor, sa: torch.Tensor, out: torch.Tensor, bf16: bool):
@@ -293,10 +349,14 @@ class FP8Linear(nn.Module):
         return out.reshape(*xq.shape[:-1], self.N)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        """fp16 or bf16 x (the bf16 silu_mul output of the fp8 MLP route, qwen2_llm.py:132-134)
+        -> fp16."""
         x2d = x.reshape(-1, self.K)
         if not x2d.is_contiguous():
             x2d = x2d.contiguous()
-        require_cuda(x2d, dtype=torch.float16)
+        require_cuda(x2d)
+        if x2d.dtype not in (torch.float16, torch.bfloat16):
+            raise TypeError(f"expected fp16 or bf16 activations, got {x2d.dtype}")
         xq, sa = self.quantize_input(x2d)
         out = torch.empty(x2d.shape[0], self.N, device=x.device, dtype=torch.float16)
         self.gemm_out(xq, sa, out, False)
@@ -320,6 +380,7 @@ class LMHeadArgmax(nn.Module):
                                                         dtype=torch.float16))
         call("omni_f16_pack", ptr(embed.contiguous()), ptr(self.table_packed), H, V, 0, stream())
         self.grid = lib().omni_lmhead_argmax_grid(V)
+        self.max_rows = lib().omni_lmhead_max_rows(H)     # rows per candidates launch
         self._cand_val = torch.empty(self.grid * MAX_SKINNY_M, device=dev, dtype=torch.float32)
         self._cand_idx = torch.empty(self.grid * MAX_SKINNY_M, device=dev, dtype=torch.int32)
 
@@ -332,10 +393,16 @@ class LMHeadArgmax(nn.Module):
             raise ValueError(f"lm_head argmax supports up to {MAX_SKINNY_M} rows per call")
         require_cuda(h2d, dtype=torch.float16)
         require_cuda(ids_out, dtype=torch.int64)
-        call("omni_lmhead_candidates", ptr(h2d), h2d.stride(0), ptr(self.table_packed), M,
-             self.V, self.H, ptr(logits_out), ptr(self._cand_val), ptr(self._cand_idx), stream())
-        call("omni_argmax_finalize", ptr(self._cand_val), ptr(self._cand_idx), self.grid, M,
-             ptr(ids_out), ptr(next_ids), ptr(lengths), stream())
+        # one candidates + finalize pair per block of rows the kernel stages at once
+        rows = lambda t, s, e: None if t is None else t[s:e]
+        for s in range(0, M, self.max_rows):
+            e = min(M, s + self.max_rows)
+            call("omni_lmhead_candidates", ptr(h2d[s:e]), h2d.stride(0), ptr(self.table_packed),
+                 e - s, self.V, self.H, ptr(rows(logits_out, s, e)), ptr(self._cand_val),
+                 ptr(self._cand_idx), stream())
+            call("omni_argmax_finalize", ptr(self._cand_val), ptr(self._cand_idx), self.grid,
+                 e - s, ptr(ids_out[s:e]), ptr(rows(next_ids, s, e)), ptr(rows(lengths, s, e)),
+                 stream())
         return ids_out
 
     def logits(self, h2d: torch.Tensor) -> torch.Tensor:

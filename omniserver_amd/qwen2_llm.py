@@ -22,7 +22,7 @@ import torch
 from torch import nn
 
 from . import fused_ops as F
-from .linear import F16Linear, GPTQLinear, LMHeadArgmax
+from .linear import F16Linear, GPTQLinear, LMHeadArgmax, _Skinny
 from .synth import DecoderShape
 
 Qwen2Config = DecoderShape
@@ -41,15 +41,90 @@ def rope_tables(cfg: Qwen2Config, max_pos: int, device):
             freqs.sin().to(torch.float16).to(device).contiguous())
 
 
-class DecoderLayer(nn.Module):
-    def __init__(self, in_norm, post_norm, qkv_proj, o_proj, gate_up_proj, down_proj):
+class RMSNorm(nn.Module):
+    """model/qwen2_llm.py:40-56: rms_norm without a residual, add_rms_norm with one, and -
+    with ``fp8_out`` set (kernels/mixed_precision.py fuse_norm_fp8) - add_rms_norm_fp8,
+    returning ((e4m3 rows, per-row scale), new residual) for an FP8 gate_up."""
+
+    def __init__(self, weight: torch.Tensor, eps: float):
         super().__init__()
-        self.register_buffer("in_norm", in_norm)
-        self.register_buffer("post_norm", post_norm)
+        self.register_buffer("weight", weight)
+        self.eps = eps
+        self.fp8_out = False
+
+    def forward(self, x, residual=None):
+        if self.fp8_out and residual is not None:
+            fq, scale, nres = F.add_rms_norm_fp8(x, residual, self.weight, self.eps)
+            return (fq, scale), nres
+        if residual is None:
+            return F.rms_norm(x, self.weight, self.eps)
+        return F.add_rms_norm(x, residual, self.weight, self.eps)
+
+
+class Attention(nn.Module):
+    """The projections of model/qwen2_llm.py:75-84 (attention itself runs in the cache
+    adapters): ``qkv_proj`` q|k|v with bias, ``o_proj``; any module with forward(x fp16)
+    may be installed on them (kernels/mixed_precision.py:21-50)."""
+
+    def __init__(self, qkv_proj: nn.Module, o_proj: nn.Module):
+        super().__init__()
         self.qkv_proj = qkv_proj
         self.o_proj = o_proj
-        self.gate_up_proj = gate_up_proj   # fused SiLU epilogue: [.., H] -> [.., I]
+
+
+class MLP(nn.Module):
+    """model/qwen2_llm.py:115-134.  gate_up -> silu_mul -> down, where
+    * a gate_up module built with the SiLU epilogue (``fuse_silu``) already emits
+      silu(gate) * up;
+    * an (e4m3 rows, scale) input from an fp8_out norm goes to gate_up.forward_prequant,
+      whose bf16 product silu_mul keeps in bf16;
+    * a non-fp16 activation reaches down_proj as is when down_proj can quantise it itself
+      (it has forward_prequant), else cast to fp16."""
+
+    def __init__(self, gate_up_proj: nn.Module, down_proj: nn.Module):
+        super().__init__()
+        self.gate_up_proj = gate_up_proj
         self.down_proj = down_proj
+
+    def forward(self, x):
+        if isinstance(x, tuple):
+            xq, scale = x
+            gu = self.gate_up_proj.forward_prequant(xq, scale)
+        else:
+            gu = self.gate_up_proj(x)
+        out = gu if getattr(self.gate_up_proj, "fuse_silu", False) else F.silu_mul(gu)
+        if out.dtype != torch.float16 and not hasattr(self.down_proj, "forward_prequant"):
+            out = out.to(torch.float16)
+        return self.down_proj(out)
+
+
+class DecoderLayer(nn.Module):
+    """model/qwen2_llm.py:137-157: input_layernorm, self_attn, post_attention_layernorm,
+    mlp (the reference's module names, so linears can be replaced by setattr).  The fused
+    decode step reads the same modules through the short aliases below."""
+
+    def __init__(self, in_norm, post_norm, qkv_proj, o_proj, gate_up_proj, down_proj,
+                 eps: float = 1e-6):
+        super().__init__()
+        self.input_layernorm = RMSNorm(in_norm, eps)
+        self.self_attn = Attention(qkv_proj, o_proj)
+        self.post_attention_layernorm = RMSNorm(post_norm, eps)
+        self.mlp = MLP(gate_up_proj, down_proj)
+
+    in_norm = property(lambda self: self.input_layernorm.weight)
+    post_norm = property(lambda self: self.post_attention_layernorm.weight)
+    qkv_proj = property(lambda self: self.self_attn.qkv_proj)
+    o_proj = property(lambda self: self.self_attn.o_proj)
+    gate_up_proj = property(lambda self: self.mlp.gate_up_proj)
+    down_proj = property(lambda self: self.mlp.down_proj)
+
+    def fused_decode_ready(self) -> bool:
+        """The fused decode step needs this library's packed linears (split-K partial
+        outputs, the attention-merging o_proj, the SiLU-fused gate_up) and plain norms."""
+        lin = (self.qkv_proj, self.o_proj, self.down_proj)
+        return (all(isinstance(m, _Skinny) and not m.fuse_silu for m in lin)
+                and isinstance(self.gate_up_proj, _Skinny) and self.gate_up_proj.fuse_silu
+                and not self.post_attention_layernorm.fp8_out)
 
 
 class Qwen2LLM(nn.Module):
@@ -78,7 +153,7 @@ class Qwen2LLM(nn.Module):
                 F16Linear(lw["qkv_w"].to(d), lw["qkv_b"].to(d)),
                 F16Linear(lw["o_w"].to(d)),
                 F16Linear(lw["gate_up_w"].to(d), fuse_silu=True),
-                F16Linear(lw["down_w"].to(d))))
+                F16Linear(lw["down_w"].to(d)), cfg.rms_norm_eps))
         return cls(cfg, w["embed"].to(d), w["norm"].to(d), layers, max_pos)
 
     @classmethod
@@ -93,8 +168,13 @@ class Qwen2LLM(nn.Module):
                 GPTQLinear(lw["qkv_q"].to(d), lw["qkv_s"].to(d), lw["qkv_b"].to(d)),
                 GPTQLinear(lw["o_q"].to(d), lw["o_s"].to(d)),
                 GPTQLinear(lw["gate_up_q"].to(d), lw["gate_up_s"].to(d), fuse_silu=True),
-                GPTQLinear(lw["down_q"].to(d), lw["down_s"].to(d))))
+                GPTQLinear(lw["down_q"].to(d), lw["down_s"].to(d)), cfg.rms_norm_eps))
         return cls(cfg, w["embed"].to(d), w["norm"].to(d), layers, max_pos)
+
+    def fused_decode_ready(self) -> bool:
+        """Whether decode_greedy can run this model (every layer on the packed linears);
+        otherwise decoding goes through forward()."""
+        return all(layer.fused_decode_ready() for layer in self.layers)
 
     # ------------------------------------------------------------------ embedding
     def embed_tokens(self, ids: torch.Tensor) -> torch.Tensor:
@@ -126,10 +206,10 @@ class Qwen2LLM(nn.Module):
         for i, layer in enumerate(self.layers):
             if residual is None:
                 residual = x
-                h = F.rms_norm(x, layer.in_norm, cfg.rms_norm_eps)
+                h = layer.input_layernorm(x)
             else:
-                h, residual = F.add_rms_norm(x, residual, layer.in_norm, cfg.rms_norm_eps)
-            qkv = layer.qkv_proj(h)
+                h, residual = layer.input_layernorm(x, residual)
+            qkv = layer.self_attn.qkv_proj(h)
             if decode:
                 cache.rope_and_write(qkv, i, self.rope_cos, self.rope_sin, cfg.mrope_section)
             else:
@@ -138,13 +218,10 @@ class Qwen2LLM(nn.Module):
             attn = torch.empty(T, cfg.num_heads, cfg.head_dim, device=x.device,
                                dtype=torch.float16)
             cache.attend_qkv(qkv, i, self.scale, attn)
-            o = layer.o_proj(attn.reshape(T, -1))
-            h, residual = F.add_rms_norm(o, residual, layer.post_norm, cfg.rms_norm_eps)
-            x = layer.down_proj(layer.gate_up_proj(h))
-        if decode:
-            cache.pool.lengths[:cache.n] += 1
-        else:
-            cache.finish()
+            o = layer.self_attn.o_proj(attn.reshape(T, -1))
+            h, residual = layer.post_attention_layernorm(o, residual)
+            x = layer.mlp(h)
+        cache.finish()
         if logits_indices is not None:
             idx = torch.as_tensor(logits_indices, device=x.device, dtype=torch.long)
             x, residual = x[idx].contiguous(), residual[idx].contiguous()
@@ -177,7 +254,8 @@ class Qwen2LLM(nn.Module):
                       next_ids: Optional[torch.Tensor] = None,
                       lengths: Optional[torch.Tensor] = None) -> torch.Tensor:
         """One decode step for pool rows [0, n): ids [n] int64 (device) -> ids_out [n]
-        (greedy).  Reads positions from pool.lengths (+ rope delta) and writes K/V there.
+        (greedy).  Reads write positions from the view (pool.lengths, or a view_graph
+        view's write_pos buffer) plus the rope delta, and writes K/V there.
         With ``lengths`` the final launch also advances lengths[:n] by one and with
         ``next_ids`` copies the new ids there.  No allocation, no host sync.
 
@@ -188,6 +266,9 @@ class Qwen2LLM(nn.Module):
         SiLU -> down (partials).  Partial results cross a kernel boundary, never a
         device-scope fence."""
         cfg = self.cfg
+        if not self.fused_decode_ready():
+            raise RuntimeError("decode_greedy runs the packed int4 / fp16 linears only; decode "
+                               "a model with other linears (FP8, fp8_out norms) through forward()")
         n = ids.shape[0]
         b = self.decode_buffers(n, ids.device)
         eps = cfg.rms_norm_eps
@@ -195,7 +276,7 @@ class Qwen2LLM(nn.Module):
         # the step's rotary rows (one position per row, the same for every layer) come out
         # of the first launch, so that no attention prologue looks them up
         F.embed_rms_norm_rope_out(ids, self.lm_head.table_packed, True, self.layers[0].in_norm,
-                                  eps, h, res, view.pool.lengths, view.rope_delta, self.rope_cos,
+                                  eps, h, res, view.kv_pos, view.rope_delta, self.rope_cos,
                                   self.rope_sin, b["rope"])
         S = 0
         for i, layer in enumerate(self.layers):

@@ -329,12 +329,16 @@ class MultimodalRunner(ModelRunner):
             if self._kv_len[b] >= self._pool.max_len:
                 raise RuntimeError(f"sequence in slot {b} reached max_len={self._pool.max_len}")
         greedy = all(s.request.sampling.greedy for s in seqs)
-        if self._use_graph and greedy:
+        fused = self.adapter.model.fused_decode_ready()
+        if self._use_graph and greedy and fused:
             self._decode_graph(seqs, n)
         else:
             self.settle()
             with torch.inference_mode():
-                self._decode_eager(seqs, n, greedy)
+                if fused:
+                    self._decode_eager(seqs, n, greedy)
+                else:
+                    self._decode_forward(seqs, n)
 
     # ---- decode paths ----------------------------------------------------------------
     def _load_ids(self, seqs, n, dst: torch.Tensor) -> None:
@@ -364,6 +368,20 @@ class MultimodalRunner(ModelRunner):
             self._emit(seqs, b["out"].tolist())
         else:
             self._emit(seqs, self._sample_rows(b["logits"], seqs))
+
+    def _decode_forward(self, seqs, n):
+        """Decode through the model's forward (multimodal.py:286-313, eager): for linears
+        the fused step cannot run (FP8 W8A8 modules, an fp8_out norm), the reference's
+        per-op route - one token per row appended at its length, logits, then sampling."""
+        model = self.adapter.model
+        self._dev_ids_for = None
+        ids = torch.tensor([s.last_token_id() for s in seqs], dtype=torch.int64,
+                           device=self.device)
+        emb = model.embed_tokens(ids).unsqueeze(1)                       # [n, 1, H]
+        view = self._pool.view(n, self._rope_delta)
+        pos = self.adapter.decode_positions(self._pool.lengths[:n], self._rope_delta[:n])
+        logits = self.adapter.llm(emb, pos, None, view)[:, -1, :]
+        self._emit(seqs, self._sample_rows(logits, seqs))
 
     def _capture_graph(self, n):
         model = self.adapter.model

@@ -194,6 +194,26 @@ def gptq_dequant(qweight: torch.Tensor, scales: torch.Tensor, group: int = 128) 
     return r16((q - 8.0) * s)
 
 
+def rtn_int4(weight: torch.Tensor, group: int = 128):
+    """Round-to-nearest int4 of an fp16 weight [N, K] as the reference's MarlinInt4Linear
+    gets it (kernels/marlin_linear.py:65-80 -> vLLM 0.12 marlin_quantize -> quantize_weights
+    for scalar type uint4b8, symmetric, group ``group`` along K; vLLM is not in this image,
+    so this restates its published algorithm): on fp16 values, per group and column,
+    s = max(|max w / 7|, |min w / -8|) (the type's largest / smallest unbiased code),
+    q = clamp(round(w / s), -8, 7) + 8 (round half to even), dequantised fp16((q - 8) s).
+    Returns (qweight [K/8, N] int32 AutoGPTQ packing, scales [K/group, N] fp16 values as
+    fp32).  An all-zero group (s = 0) gets code 8."""
+    N, K = weight.shape
+    w = weight.t().to(torch.float16).reshape(K // group, group, N)
+    mx = w.amax(1, keepdim=True)
+    mn = w.amin(1, keepdim=True)
+    s = torch.maximum((mx / 7.0).abs(), (mn / -8.0).abs())
+    safe = torch.where(s == 0, torch.ones_like(s), s)
+    codes = torch.clamp(torch.round(w / safe).to(torch.int32), -8, 7) + 8
+    qweight = gptq_pack(codes.reshape(K, N))
+    return qweight, s.reshape(K // group, N).float()
+
+
 # --------------------------------------------------------------------------- fp8
 def fp8_weight_rowwise(weight: torch.Tensor):
     """kernels/fp8_linear.py:83-86: sw[n] = amax_k |W[n, :]| / 448, Wq = e4m3(W / sw).
@@ -300,6 +320,13 @@ class LayerWeights:
     o_t: torch.Tensor
     gate_up_t: torch.Tensor
     down_t: torch.Tensor
+    # the FP8 MLP route (kernels/mixed_precision.py fuse_norm_fp8 + plan gate_up/down fp8):
+    # (Wq e4m3 [N, K], sw [N]) of the row-wise FP8 gate_up / down, or None for fp16
+    fp8_gate_up: Optional[tuple] = None
+    fp8_down: Optional[tuple] = None
+    # fuse_norm_fp8 (mixed_precision.py:53-75): the post-attention norm emits e4m3 rows
+    # for the FP8 gate_up's forward_prequant; False = FP8Linear.forward quantises itself
+    norm_fp8: bool = False
 
 
 class Qwen2Ref:
@@ -338,6 +365,38 @@ class Qwen2Ref:
         gu = linear(x, lw.gate_up_t, None, self.f16)
         return linear(silu_mul(gu, self.f16), lw.down_t, None, self.f16)
 
+    def _post_norm_mlp(self, o, residual, lw: LayerWeights):
+        """post_attention_layernorm + MLP (qwen2_llm.py:153-154, 123-134) with either linear
+        of the MLP optionally FP8 (FP8Linear, rowwise, fp8_linear.py:66-126):
+        * fused norm (norm_fp8, fuse_norm_fp8): add_rms_norm_fp8 quantises the normed rows
+          (fused_ops.py:74-91), gate_up.forward_prequant returns the bf16 product (:99-108),
+          silu_mul keeps bf16 (fused_ops.py:122-130 stores in its input dtype);
+        * otherwise the fp16 norm output, and an FP8 gate_up's forward quantises it per
+          token (quant_fp8, :45-63) and casts its bf16 product to fp16 (:115-118);
+        the down projection takes the activation as it comes: an FP8 one quantises it (bf16
+        or fp16), an fp16 one gets it cast to fp16 (qwen2_llm.py:132-133)."""
+        c = self.cfg
+        if lw.fp8_gate_up is not None and lw.norm_fp8:
+            xq, sa, residual = add_rms_norm_fp8(o, residual, lw.post_norm, c.rms_norm_eps)
+            gu = fp8_linear_prequant(xq, sa, *lw.fp8_gate_up)
+            n = gu.shape[-1] // 2
+            g, u = gu[..., :n], gu[..., n:]
+            act = rbf16(g * torch.sigmoid(g) * u)
+        else:
+            h, residual = add_rms_norm(o, residual, lw.post_norm, c.rms_norm_eps, self.f16)
+            if lw.fp8_gate_up is None:
+                if lw.fp8_down is None:
+                    return self._mlp(h, lw), residual
+                gu = linear(h, lw.gate_up_t, None, self.f16)
+            else:
+                xq, sa = quant_fp8(h)
+                gu = fp8_linear_rowwise(xq, sa, *lw.fp8_gate_up)
+            act = silu_mul(gu, self.f16)
+        if lw.fp8_down is None:
+            return linear(r16(act), lw.down_t, None, self.f16), residual
+        xq, sa = quant_fp8(act)
+        return fp8_linear_rowwise(xq, sa, *lw.fp8_down), residual
+
     def lm_head(self, h):
         return r16(h @ self.embed.t(), self.f16)
 
@@ -370,8 +429,7 @@ class Qwen2Ref:
             a = decode_attention(q, k_pool[i], v_pool[i], torch.arange(n), wpos + 1, scale,
                                  self.f16)
             o = linear(a.reshape(n, -1), lw.o_t, None, self.f16)
-            h, residual = add_rms_norm(o, residual, lw.post_norm, c.rms_norm_eps, self.f16)
-            x = self._mlp(h, lw)
+            x, residual = self._post_norm_mlp(o, residual, lw)
         h, _ = add_rms_norm(x, residual, self.final_norm, c.rms_norm_eps, self.f16)
         logits = self.lm_head(h)
         return (logits, h) if return_hidden else logits
@@ -400,8 +458,7 @@ class Qwen2Ref:
                 off += L
             a = prefill_attention(q, k, v, seg_lens, scale, self.f16)
             o = linear(a.reshape(a.shape[0], -1), lw.o_t, None, self.f16)
-            h, residual = add_rms_norm(o, residual, lw.post_norm, c.rms_norm_eps, self.f16)
-            x = self._mlp(h, lw)
+            x, residual = self._post_norm_mlp(o, residual, lw)
         last = torch.tensor(np.cumsum(seg_lens) - 1)
         h, _ = add_rms_norm(x[last], residual[last], self.final_norm, c.rms_norm_eps, self.f16)
         for slot, L in zip(slots, seg_lens):

@@ -111,3 +111,25 @@ def record_sampled_logits(runner):
 
     runner._sample_rows = wrapped
     return seen
+
+
+def oracle_with_plan(w, shape, plan: dict, f16=True, norm_fp8=False) -> ref.Qwen2Ref:
+    """The fp16 decoder's oracle with per-op precision applied as the reference's
+    mixed_precision / quantize_llm_marlin would: "fp8" MLP linears take the FP8 route
+    (row-wise e4m3 weights; with ``norm_fp8`` the post-attention norm quantises for the FP8
+    gate_up, fuse_norm_fp8), "marlin" linears use the RTN int4 dequantised weights."""
+    orc = oracle_from_fp16(w, shape, f16)
+    for lw, src in zip(orc.layers, w["layers"]):
+        lw.norm_fp8 = norm_fp8
+        for op, key, attr in (("gate_up", "gate_up_w", "gate_up_t"), ("down", "down_w", "down_t"),
+                              ("qkv", "qkv_w", "qkv_t"), ("o", "o_w", "o_t")):
+            prec = plan.get(op, "fp16")
+            if prec == "marlin":
+                setattr(lw, attr, ref.gptq_dequant(*ref.rtn_int4(src[key].float())))
+            elif prec == "fp8":
+                if op not in ("gate_up", "down"):
+                    raise ValueError("the oracle's FP8 route covers the MLP linears")
+                setattr(lw, "fp8_" + op, ref.fp8_weight_rowwise(src[key].float()))
+    if any(plan.get(op) == "marlin" for op in ("qkv", "o")):
+        orc.bias_after_round = True
+    return orc

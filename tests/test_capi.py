@@ -63,18 +63,29 @@ def test_bad_arguments_rejected_before_launch(so):
     assert L.omni_add_rmsnorm(None, None, None, None, None, 4, 1536, 1e-6, None) == -1
     # attention: bad waves / head_dim / splits
     assert L.omni_decode_attention(None, 1536, None, None, 1, 16, None, None, 0, 0, None, 1, 12,
-                                   2, 128, 0.1, 3, 1, None, None) == -1
+                                   2, 128, 0.1, 3, 1, None, 0, None) == -1
     assert L.omni_decode_attention(None, 1536, None, None, 1, 16, None, None, 0, 0, None, 1, 12,
-                                   2, 64, 0.1, 4, 1, None, None) == -2
+                                   2, 64, 0.1, 4, 1, None, 0, None) == -2
     assert L.omni_decode_attention(None, 1536, None, None, 1, 16, None, None, 0, 0, None, 1, 12,
-                                   2, 128, 0.1, 4, 0, None, None) == -1
+                                   2, 128, 0.1, 4, 0, None, 0, None) == -1
+    # 16 waves per workgroup are no longer built; a workspace below the split states' size
+    assert L.omni_decode_attention(fake_ptr(), 1536, fake_ptr(), fake_ptr(), 2, 16, None,
+                                   fake_ptr(), 0, 0, fake_ptr(), 1, 12, 2, 128, 0.1, 16, 1, None,
+                                   0, None) == -1
+    assert L.omni_decode_attention(fake_ptr(), 1536, fake_ptr(), fake_ptr(), 2, 16, None,
+                                   fake_ptr(), 0, 0, fake_ptr(), 1, 12, 2, 128, 0.1, 8, 4,
+                                   fake_ptr(), 1 * 2 * 4 * 6 * 132 - 1, None) == -1
     # rotary rows: negative count, missing tables; the fused attention without rows needs them
     assert L.omni_rope_rows(None, None, None, None, None, 64, 4, -1, None, None) == -1
     assert L.omni_rope_rows(None, fake_ptr(), None, None, None, 64, 4, 2, fake_ptr(), None) == -1
     assert L.omni_decode_attention_fused(fake_ptr(), 6, None, 1, None, None, 64, None, 16, 24,
                                          24, fake_ptr(), fake_ptr(), 4, 64, None, fake_ptr(),
-                                         fake_ptr(), 2, 12, 2, 128, 0.1, 8, 4, fake_ptr(), 1,
-                                         None, None) == -1
+                                         fake_ptr(), 2, 12, 2, 128, 0.1, 8, 4, fake_ptr(),
+                                         2 * 2 * 4 * 6 * 132, 1, None, None) == -1
+    assert L.omni_decode_attention_fused(fake_ptr(), 6, None, 1, None, None, 64, None, 16, 24,
+                                         24, fake_ptr(), fake_ptr(), 4, 64, None, fake_ptr(),
+                                         fake_ptr(), 2, 12, 2, 128, 0.1, 8, 4, fake_ptr(),
+                                         2 * 2 * 4 * 6 * 132 - 1, 1, fake_ptr(), None) == -1
     # slot copy: row out of range, row width not whole 16-byte chunks, device length without
     # a lengths array
     assert L.omni_kv_copy_slot(fake_ptr(), 2, 4, 64, 256, 0, 4, 3, None, None) == -1

@@ -175,8 +175,8 @@ def test_mrope_3d_positions(gpu):
 
 # ----------------------------------------------------------------------------- attention
 @pytest.mark.parametrize("lengths,waves,splits", [
-    ([1], 4, 1), ([7], 4, 3), ([33, 64, 100], 4, 1), ([300, 5, 1000], 8, 4), ([2048] * 4, 16, 2),
-    ([1, 2, 3, 4095], 4, 16), ([31, 32, 33, 65], 16, 1), ([2049] * 3, 4, 8),
+    ([1], 4, 1), ([7], 4, 3), ([33, 64, 100], 4, 1), ([300, 5, 1000], 8, 4), ([2048] * 4, 8, 2),
+    ([1, 2, 3, 4095], 4, 16), ([31, 32, 33, 65], 8, 1), ([2049] * 3, 4, 8),
 ])
 def test_decode_attention(gpu, lengths, waves, splits):
     from omniserver_amd._lib import call, ptr, stream
@@ -193,7 +193,7 @@ def test_decode_attention(gpu, lengths, waves, splits):
     kg, vg, qg, Lg = kp.to(gpu), vp.to(gpu), q.to(gpu), L.to(gpu)
     ws = torch.empty(n * nkv * splits * 6 * 132, device=gpu, dtype=torch.float32)
     call("omni_decode_attention", ptr(qg), nh * hd, ptr(kg), ptr(vg), P, ML, None, ptr(Lg), 0, 0,
-         ptr(out), n, nh, nkv, hd, scale, waves, splits, ptr(ws), stream())
+         ptr(out), n, nh, nkv, hd, scale, waves, splits, ptr(ws), ws.numel(), stream())
     torch.cuda.synchronize()
     e = ref.decode_attention(q.float().view(n, nh, hd), kp.float(), vp.float(),
                              torch.arange(n), L, scale)
@@ -372,11 +372,12 @@ def test_f16_gemm(gpu, M, K, N, bias, silu):
     assert d.max().item() <= tol, (d.max().item(), tol)
 
 
-def test_add_rmsnorm_partials(gpu):
-    """x = fp16(sum of split-K partials in slice order), then add + RMSNorm."""
+@pytest.mark.parametrize("S,M,H", [(7, 32, 1536), (20, 5, 1536), (11, 3, 4096)])
+def test_add_rmsnorm_partials(gpu, S, M, H):
+    """x = fp16(sum of split-K partials in slice order), then add + RMSNorm (H = 4096 runs
+    the 1024-thread form, 20 slices two batches of the 256-thread one)."""
     from omniserver_amd import fused_ops as F
-    say("add_rmsnorm over split-K partials")
-    S, M, H = 7, 32, 1536
+    say(f"add_rmsnorm over split-K partials S={S} M={M} H={H}")
     g = torch.Generator().manual_seed(101)
     parts = torch.randn(S, M, H, generator=g) * 0.3
     r = f16((M, H), 102)
@@ -394,7 +395,7 @@ def test_add_rmsnorm_partials(gpu):
     assert (y.cpu().float() - ey).abs().max().item() <= 2e-3 * ey.abs().max().item()
 
 
-@pytest.mark.parametrize("M", [1, 32])
+@pytest.mark.parametrize("M", [1, 32, 49, 64])
 def test_lmhead_argmax(gpu, M):
     from omniserver_amd.linear import LMHeadArgmax
     say(f"lm_head argmax M={M}")
@@ -519,15 +520,16 @@ def test_decode_attention_fused_equals_unfused(gpu, bias_after_round, splits, le
         if mode.startswith("fused"):
             call("omni_decode_attention_fused", ptr(parts), S, ptr(bias), bias_after_round,
                  ptr(cos), ptr(sin), 8192, ptr(delta), 16, 24, 24, ptr(kc), ptr(vc), P, ML, None,
-                 ptr(lens), ptr(out), n, nh, nkv, hd, hd ** -0.5, 8, splits, ptr(ws), 1,
-                 ptr(rows) if mode == "fused-rows" else None, stream())
+                 ptr(lens), ptr(out), n, nh, nkv, hd, hd ** -0.5, 8, splits, ptr(ws), ws.numel(),
+                 1, ptr(rows) if mode == "fused-rows" else None, stream())
         else:
             qkv = torch.empty(n, W, device=gpu, dtype=torch.float16)
             call("omni_mrope_kv_write_partials", ptr(qkv), W, ptr(parts), S, ptr(bias),
                  bias_after_round, None, ptr(lens), ptr(delta), ptr(cos), ptr(sin), 8192, ptr(kc),
                  ptr(vc), None, None, P, ML, n, nh, nkv, hd, 16, 24, 24, stream())
             call("omni_decode_attention", ptr(qkv), W, ptr(kc), ptr(vc), P, ML, None, ptr(lens),
-                 1, 1, ptr(out), n, nh, nkv, hd, hd ** -0.5, 8, splits, ptr(ws), stream())
+                 1, 1, ptr(out), n, nh, nkv, hd, hd ** -0.5, 8, splits, ptr(ws), ws.numel(),
+                 stream())
         torch.cuda.synchronize()
         outs.append((out.cpu(), kc.cpu(), vc.cpu()))
     for other in outs[1:]:
@@ -572,8 +574,8 @@ def test_oproj_merges_attention_states(gpu, fmt, splits):
     def attn(merge):
         call("omni_decode_attention_fused", ptr(parts), 6, ptr(bias), 1, ptr(cos), ptr(sin), 8192,
              ptr(delta), 16, 24, 24, ptr(kc), ptr(vc), P, ML, None, ptr(lens),
-             ptr(out) if merge else None, n, nh, nkv, hd, hd ** -0.5, 8, splits, ptr(ws), merge,
-             None, stream())
+             ptr(out) if merge else None, n, nh, nkv, hd, hd ** -0.5, 8, splits, ptr(ws),
+             ws.numel(), merge, None, stream())
     attn(0)
     lin.forward_partial_attn(ws, splits, nkv, nh // nkv, n, pa)
     attn(1)                       # same K/V row rewritten with the same values

@@ -88,7 +88,7 @@ def test_decode_step_fp16(gpu, lengths):
     _decode_once(gpu, None, 4, lengths, 3)
 
 
-@pytest.mark.parametrize("n", [1, 8, 32])
+@pytest.mark.parametrize("n", [1, 8, 32, 56])
 def test_decode_step_gptq(gpu, n):
     say(f"decode step gptq 4 layers n={n}")
     lengths = [(37 * (b + 1)) % 400 + 1 for b in range(n)]

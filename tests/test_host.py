@@ -309,3 +309,63 @@ def test_vision_state_dict_prefixes():
     out = vision_state_dict(sd)
     assert set(out) == {"visual.blocks.0.norm1.weight", "visual.merger.ln_q.weight"}
     assert vision_state_dict({"model.norm.weight": t}) == {}
+
+
+# ----------------------------------------------------------------------------- cache protocol
+def _cpu_pool(n_layers=2, rows=3, max_len=16):
+    from omniserver_amd.kv_cache import PreallocatedKVCache
+    return PreallocatedKVCache(n_layers, rows, 2, max_len, 8, "cpu", n_heads=12)
+
+
+def test_cache_view_update_matches_reference_semantics():
+    """_CacheView.update (kv_prealloc.py:263-270): the new key/value of each row goes to
+    its write position (the length when the view was made), the valid window
+    [:, :max(pos) + 1] comes back as [n, n_kv, L, hd], and lengths advance on the last
+    layer only; a view_graph view (:90-92) writes at the caller's positions and never
+    advances lengths."""
+    pool = _cpu_pool()
+    pool.lengths[:2] = torch.tensor([3, 5])
+    view = pool.view(2)
+    for layer in range(2):
+        key = torch.full((2, 2, 1, 8), float(layer + 1), dtype=torch.float16)
+        val = -key
+        k, v = view.update(key, val, layer)
+        assert k.shape == (2, 2, 6, 8) and v.shape == (2, 2, 6, 8)
+        assert torch.equal(pool.k[layer][0, 3], key[0, :, 0]) and torch.equal(pool.k[layer][1, 5], key[1, :, 0])
+        assert torch.equal(pool.v[layer][1, 5], val[1, :, 0])
+        assert torch.equal(k[1, :, 5], key[1, :, 0])
+        want = [3, 5] if layer == 0 else [4, 6]
+        assert pool.lengths[:2].tolist() == want
+    assert view.get_seq_length() == 5 and view.get_mask_sizes(None) == (6, 0)
+    assert view.get_max_cache_shape() == 16
+
+    wp = torch.tensor([7, 1], dtype=torch.int64)
+    g = pool.view_graph(2, wp, None, None)
+    k, _ = g.update(torch.ones(2, 2, 1, 8, dtype=torch.float16), torch.ones(2, 2, 1, 8,
+                    dtype=torch.float16), 1)
+    assert k.shape[2] == 16 and pool.lengths[:2].tolist() == [4, 6]
+    assert pool.k[1][0, 7].eq(1).all() and pool.k[1][1, 1].eq(1).all()
+    g.finish()
+    assert pool.lengths[:2].tolist() == [4, 6]
+    view.finish()
+    assert pool.lengths[:2].tolist() == [5, 7]
+
+
+def test_prefill_writers_update():
+    """_PackedPrefillWriter.update / _PrefillWriter.update (kv_prealloc.py:205-229): each
+    segment of the packed [1, n_kv, T, hd] keys lands in its slot; lengths on the last
+    layer; the keys come back unchanged."""
+    pool = _cpu_pool()
+    w = pool.packed_prefill_cache([2, 0], [3, 4])
+    k = torch.arange(7, dtype=torch.float16).view(1, 1, 7, 1).expand(1, 2, 7, 8).contiguous()
+    for layer in range(2):
+        rk, rv = w.update(k, -k, layer)
+        assert rk is k
+    assert pool.lengths.tolist() == [4, 0, 3]
+    assert pool.k[1][2, :3, 0, 0].tolist() == [0, 1, 2]
+    assert pool.k[1][0, :4, 1, 0].tolist() == [3, 4, 5, 6]
+    assert pool.v[0][0, 3, 0, 0].item() == -6
+    single = pool.prefill_cache(1)
+    for layer in range(2):
+        single.update(k[:, :, :5], k[:, :, :5], layer)
+    assert pool.lengths.tolist() == [4, 5, 3] and pool.k[0][1, :5, 0, 0].tolist() == [0, 1, 2, 3, 4]

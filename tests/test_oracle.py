@@ -364,3 +364,91 @@ def test_golden_fixture_reproduced():
             if w["margin"][b] > 1e-3:
                 assert g["tokens"][b] == w["tokens"][b]
         assert np.allclose(g["top5_logits"], w["top5_logits"], atol=1e-3)
+
+
+# ----------------------------------------------------------------------------- RTN int4
+def _rtn_brute(w16: np.ndarray, group: int):
+    """Python-scalar restatement of the RTN rule on fp16 values: per group and column the
+    scale max(|max/7|, |min/-8|) in fp16 arithmetic, the quotient w/s rounded to fp16 (the
+    reference divides fp16 tensors), then round half to even and clamp to [-8, 7]."""
+    K, N = w16.shape
+    codes = np.zeros((K, N), dtype=np.int64)
+    scales = np.zeros((K // group, N), dtype=np.float16)
+    for gi in range(K // group):
+        for n in range(N):
+            col = w16[gi * group:(gi + 1) * group, n]
+            mx, mn = col.max(), col.min()
+            s = max(abs(np.float16(mx / np.float16(7))), abs(np.float16(mn / np.float16(-8))))
+            scales[gi, n] = s
+            for i, v in enumerate(col):
+                q = 0 if s == 0 else round(float(np.float16(v / s)))
+                codes[gi * group + i, n] = min(max(q, -8), 7) + 8
+    return codes, scales
+
+
+def test_rtn_int4_brute_force_and_bounds():
+    """marlin_linear.py:65-80 (vLLM quantize_weights, uint4b8): the oracle's codes and
+    scales equal a scalar brute force; every dequantised weight is within s/2 of its fp16
+    value (plus the fp16 rounding of the product); the dominating extreme of each group
+    maps to code 15 (max/7 side) or 0 (min/-8 side); an all-zero group gives code 8."""
+    N, K, G = 6, 256, 128
+    w = (rnd((N, K), 40) * 0.02).half()
+    w[2, :128] = 0                                   # an all-zero group
+    qw, s = ref.rtn_int4(w.float(), G)
+    codes = ref.gptq_unpack(qw)
+    bc, bs = _rtn_brute(w.t().numpy().astype(np.float16), G)
+    assert np.array_equal(codes.numpy(), bc)
+    assert np.array_equal(s.numpy().astype(np.float16), bs)
+    deq = ref.gptq_dequant(qw, s.half(), G)                       # [K, N]
+    wt = w.t().float()
+    srep = s.repeat_interleave(G, 0)
+    assert ((deq - wt).abs() <= srep / 2 + wt.abs() * 2.0 ** -10 + 1e-8).all()
+    for gi in range(K // G):
+        for n in range(N):
+            col = wt[gi * G:(gi + 1) * G, n]
+            cc = codes[gi * G:(gi + 1) * G, n]
+            if col.abs().max() == 0:
+                assert (cc == 8).all()
+                continue
+            up = col.max().item() / 7 >= -col.min().item() / 8
+            assert cc[col.argmax()] == 15 if up else cc[col.argmin()] == 0
+
+
+# ----------------------------------------------------------------------------- fp8 MLP route
+def test_fp8_mlp_route_matches_reference_expressions():
+    """The oracle's FP8 MLP route (post-attention add_rms_norm_fp8 -> gate_up
+    forward_prequant -> bf16 silu_mul -> FP8 down) against the reference's MLP.forward
+    expressions evaluated with torch's own CPU ops: torch._scaled_mm on the e4m3 operands
+    (unit scales, the row / column scales applied to its fp32 result as the row-wise GEMM
+    does), F.silu on the bf16 gate/up, the bf16 activation re-quantised per row, the fp16
+    output cast of FP8Linear.forward (qwen2_llm.py:124-134, fp8_linear.py:45-63, 99-126)."""
+    M, H, I = 8, 128, 96
+    cfg = ref.Qwen2Config(hidden_size=H, num_layers=1, intermediate_size=I)
+    o = rnd((M, H), 41).half().float()
+    res = rnd((M, H), 42).half().float()
+    w_norm = (1 + 0.1 * rnd((H,), 43)).half().float()
+    Wgu = (rnd((2 * I, H), 44) * 0.05).half().float()
+    Wd = (rnd((H, I), 45) * 0.05).half().float()
+    gu_q, gu_s = ref.fp8_weight_rowwise(Wgu)
+    d_q, d_s = ref.fp8_weight_rowwise(Wd)
+    lw = ref.LayerWeights(in_norm=w_norm, post_norm=w_norm, qkv_t=None, qkv_b=None, o_t=None,
+                          gate_up_t=None, down_t=None, fp8_gate_up=(gu_q, gu_s),
+                          fp8_down=(d_q, d_s), norm_fp8=True)
+    orc = ref.Qwen2Ref(cfg, torch.zeros(4, H), w_norm, [lw])
+    y, nres = orc._post_norm_mlp(o, res, lw)
+
+    one = torch.ones((), dtype=torch.float32)
+    xq, sa, r = ref.add_rms_norm_fp8(o, res, w_norm, 1e-6)
+    assert torch.equal(nres, r)
+    mm = lambda a, b: torch._scaled_mm(a, b.t(), scale_a=one, scale_b=one, out_dtype=torch.float32)
+    gu = (mm(xq, gu_q) * sa * gu_s.view(1, -1)).to(torch.bfloat16)
+    g, u = gu[:, :I].float(), gu[:, I:].float()
+    act = (torch.nn.functional.silu(g) * u).to(torch.bfloat16).float()
+    s2 = act.abs().amax(-1, keepdim=True) / 448.0
+    aq = (act / s2).to(torch.float8_e4m3fn)
+    e = (mm(aq, d_q) * s2 * d_s.view(1, -1)).to(torch.bfloat16).to(torch.float16).float()
+    d = (y - e).abs()
+    # the two GEMMs may sum in different orders: nearly all outputs identical (they all are
+    # here), the rest within one bf16 step
+    assert (d == 0).float().mean() > 0.99
+    assert (d <= e.abs() * 2.0 ** -7 + 1e-6).all()

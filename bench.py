@@ -172,29 +172,55 @@ def attention_launch_time(runner, B: int, reps: int) -> tuple[float, int]:
 
 
 def pmc_probe(runner, seqs, B: int) -> None:
-    """Kernel launches for byte-counter runs: one decode attention per layer (eager, so
-    every dispatch is its own counter record) and a plain device copy of 256 MiB, whose
-    counters calibrate FETCH_SIZE / WRITE_SIZE against known bytes."""
+    """Kernel launches for rocprofv3 counter runs (--pmc), each its own dispatch record,
+    in this order (the summaries key dispatches by it):
+      1. one eager decode step of the config-3 model at B rows (embedding + layer-0 norm,
+         then per layer: qkv, attention, o_proj, add+RMSNorm, gate_up + SiLU, down,
+         add+RMSNorm; lm_head candidates, argmax) and then
+      2. the same step for one row (B = 1), both at the bench context (K/V written past
+         the valid lengths only, which are not advanced);
+      3. a plain 256 MiB device copy: the byte-counter calibration;
+      4. BASELINE.json configs[3]'s four FP8 linears at M = 8192 (qkv, o, gate_up, down);
+      5. layer 0's four int4 linears at M = 4096 (config 5's packed prefill: the tiled
+         MFMA GEMM, qkv and down over their split-K finish launches).
+    Prints no JSON line."""
+    from omniserver_amd.linear import FP8Linear
     model = runner.adapter.model
-    cfg = model.cfg
     dev = runner.pool.storage.device
     runner.decode(seqs)                       # graph captured and one step taken
+    runner.settle()
     torch.cuda.synchronize()
-    view = runner.pool.view(B, runner._rope_delta)
-    bufs = model.decode_buffers(B, dev)
-    Sq = model.layers[0].qkv_proj.forward_partial(bufs["h"], bufs["qpart"])
-    view.rope_rows(model.rope_cos, model.rope_sin, bufs["rope"])
-    for i, layer in enumerate(model.layers):
-        view.attend_fused(bufs["qpart"], Sq, layer.qkv_proj.bias, layer.qkv_proj.fmt == "int4",
-                          i, model.scale, model.rope_cos, model.rope_sin, cfg.mrope_section,
-                          rope_rows=bufs["rope"])
-    torch.cuda.synchronize()
+    for n in (B, 1):
+        ids = torch.tensor([s.last_token_id() for s in seqs[:n]], dtype=torch.int64, device=dev)
+        out = torch.empty(n, dtype=torch.int64, device=dev)
+        model.decode_greedy(ids, runner.pool.view(n, runner._rope_delta), out)
+        torch.cuda.synchronize()
     src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     dst.copy_(src)
     torch.cuda.synchronize()
-    log(f"pmc probe: {len(model.layers)} attention launches at ctx "
-        f"{int(runner.pool.lengths[0])}, one 256 MiB copy")
+    del src, dst
+    g = torch.Generator(device=dev)
+    g.manual_seed(4)
+    for K, N in LINEARS:
+        w = (torch.randn(N, K, generator=g, device=dev) * 0.02).half()
+        x = torch.randn(8192, K, generator=g, device=dev).half()
+        lin = FP8Linear(w)
+        xq, sa = lin.quantize_input(x)
+        y = torch.empty(8192, N, device=dev, dtype=torch.float16)
+        torch.cuda.synchronize()
+        lin.gemm_out(xq, sa, y, False)
+        torch.cuda.synchronize()
+        del w, x, lin, xq, y
+    lay = model.layers[0]
+    for lin in (lay.qkv_proj, lay.o_proj, lay.gate_up_proj, lay.down_proj):
+        x = torch.randn(4096, lin.K, generator=g, device=dev).half()
+        y = torch.empty(4096, lin.out_features, device=dev, dtype=torch.float16)
+        torch.cuda.synchronize()
+        lin.forward_out(x, y)
+        torch.cuda.synchronize()
+    log(f"pmc probe: eager decode steps at B={B} and 1 (ctx {int(runner.pool.lengths[0])}), "
+        f"one 256 MiB copy, 4 FP8 linears at M=8192, 4 int4 linears at M=4096")
 
 
 def traffic_from_profiles(kernel: str):
@@ -207,6 +233,19 @@ def traffic_from_profiles(kernel: str):
             t = json.load(f)
         k = t["kernels"][kernel]
         return int(k["fetch_bytes"] + k["write_bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def mfma_from_profiles(prefix: str) -> dict | None:
+    """MFMA busy % per linear from rocprofv3 counters (profiles/traffic.json "mfma", written
+    from the runs its "commands" list): {linear: busy %} for the GEMMs whose key starts with
+    ``prefix``, or None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            g = json.load(f)["mfma"]["gemms"]
+        return {k.split()[-1]: v["mfma_busy_pct"] for k, v in g.items() if k.startswith(prefix)}
     except (OSError, KeyError, ValueError):
         return None
 
@@ -238,7 +277,8 @@ def fp8_layer_gemms(device, M: int = 8192, reps: int = 10) -> dict:
     return {"workload": f"one layer's W8A8 linears at M={M}", "gflop": round(tot_f / 1e9, 1),
             "us": round(tot_s * 1e6, 1), "achieved": round(tot_f / tot_s / 1e12, 1),
             "peak": PEAK_FP8 / 1e12, "unit": "TFLOP/s", "frac": round(tot_f / tot_s / PEAK_FP8, 4),
-            "per_shape": per}
+            "per_shape": per,
+            "mfma_busy_pct_counters": mfma_from_profiles("fp8 W8A8 M=8192")}
 
 
 def decode_b1(device, w, ctx: int = 2048, steps: int = 64) -> dict:
@@ -394,6 +434,7 @@ def baseline_configs(device, w_int4) -> dict:
                       "prefill_ms": round(pre * 1e3, 3), "prefill_tok_per_s": round(T / pre, 1),
                       "prefill_tflops": round((lin + att) / pre / 1e12, 1),
                       "prefill_frac_fp16_peak": round((lin + att) / pre / PEAK_FP16, 4),
+                      "prefill_gemm_mfma_busy_pct_counters": mfma_from_profiles("int4 prefill M=4096"),
                       **_decode_line("gptq", per, rep, ctx0, 128)}
     del r, seqs
     torch.cuda.empty_cache()
@@ -502,9 +543,9 @@ def main():
     ap.add_argument("--kernel-steps", type=int, default=10,
                     help="replays of the 28-launch attention graph timed for the roofline")
     ap.add_argument("--pmc-probe", action="store_true",
-                    help="for rocprofv3 --pmc: one eager launch of the decode attention per "
-                         "layer at the bench context, then a plain 256 MiB device copy (the "
-                         "byte-counter calibration); prints no JSON line")
+                    help="for rocprofv3 --pmc: eager decode steps at B and 1, a plain 256 MiB "
+                         "device copy (the byte-counter calibration), the FP8 and int4 prefill "
+                         "linears (see pmc_probe); prints no JSON line")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:

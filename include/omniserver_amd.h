@@ -180,7 +180,8 @@ int omni_prefill_attention(const void* q, int q_stride, const void* k_cache, con
  * [M, K] (row stride ldx); weights from omni_gptq_repack.  M <= 64 runs the skinny
  * weight-streaming kernel: ksplit > 1 only with OMNI_EPI_PARTIAL (slices =
  * omni_gemm_slices(K, ksplit)), preset selects the workgroup shape (0..3; SiLU 0..9).
- * M > 64 (prefill) runs the tiled MFMA GEMM: OMNI_EPI_STORE / OMNI_EPI_SILU, preset ignored;
+ * M > 64 (prefill) runs an MFMA GEMM (omni_packed_gemm_pipe's pipeline where its shape and
+ * alignment rules hold, else a tiled kernel): OMNI_EPI_STORE / OMNI_EPI_SILU, preset ignored;
  * with OMNI_EPI_STORE, ksplit > 1 splits K over omni_gemm_slices(K, ksplit) slices whose
  * fp32 sums go to partial ([slices][M][N], 16-byte aligned) before a second launch adds
  * them in order and stores out (+ bias). */
@@ -256,6 +257,23 @@ int omni_f16_gemm_pipe(const void* x, int ldx, const void* w, const void* bias, 
 
 /* The K slices omni_f16_gemm_pipe uses for ksplit = 0 (tile_rows as there). */
 int omni_f16_gemm_pipe_splits(int M, int N, int K, int tile_rows);
+
+/* The decoder's linears at prefill sizes (GPTQMarlinLinear.forward,
+ * kernels/marlin_linear.py:54-62, 83-96, and the fp16 nn.Linear of model/qwen2.py's
+ * attention and MLP) on the pipeline of omni_f16_gemm_pipe, with this library's packed
+ * weights: fmt 0 int4 + scales from omni_gptq_repack (W = fp16((q - 8) s)), fmt 1 fp16
+ * from omni_f16_pack (scales_packed unused).  out = fp16(x . W^T) (+ bias, after the fp16
+ * rounding when bias_after_round); OMNI_EPI_SILU: gate|up packed with interleave_halves,
+ * out [M, N/2] = fp16(silu(g) u) of the fp16 g, u (no bias, ksplit 1).  N % 128 == 0,
+ * K % 128 == 0, K >= 256; x, w 16-byte and scales 4-byte aligned, ldx % 8 == 0,
+ * ldo % 4 == 0, out 8-byte aligned.  tile_rows 128, 256 or 0 (from the shape); ksplit K
+ * slices of whole 128-groups (0: omni_f16_gemm_pipe_splits; each slice >= 3 groups for
+ * int4 at 128 rows, else >= 2), ksplit > 1 with fp32 workspace (ksplit * M * N floats,
+ * 16-byte aligned) summed in order by a second launch. */
+int omni_packed_gemm_pipe(const void* x, int ldx, const void* w_packed, const void* scales_packed,
+                          int fmt, const void* bias, int bias_after_round, void* out, int ldo,
+                          int M, int N, int K, int epilogue, int tile_rows, int ksplit,
+                          float* workspace, void* stream);
 
 /* nn.LayerNorm(N, eps) of M fp16 rows (model/qwen2_vit.py:39-40, 87): fp32 mean and biased
  * variance, y = (x - mean) rsqrt(var + eps) w + b.  N % 8 == 0, N <= 2048; out may alias x. */

@@ -117,6 +117,17 @@ __device__ __forceinline__ uint32_t and_or_b32(uint32_t x, uint32_t mask, uint32
   return r;
 }
 
+// SwiGLU's silu(g) * u in fp32, from the fp16 (or bf16) roundings g, u of the projections.
+// The empty asm makes the product opaque: without it the backend may fold the last multiply
+// and the caller's fp16 rounding into one mixed-precision fma (one rounding instead of the
+// fp32 product's two), which changes near-tie results from kernel to kernel.
+__device__ __forceinline__ float silu_mul_f32(float g, float u) {
+#pragma clang fp contract(off)
+  float p = g * (1.0f / (1.0f + __expf(-g))) * u;
+  asm("" : "+v"(p));
+  return p;
+}
+
 __device__ __forceinline__ half8_t dequant8(uint32_t w, half2_t s2) {
   const half2_t b_lo = {(half_t)1032.0f, (half_t)1032.0f};
   const half2_t b_hi = {(half_t)72.0f, (half_t)72.0f};

@@ -1,8 +1,20 @@
-// fp16 GEMM with a multi-stage global -> LDS pipeline, for the vision tower's linears:
+// fp16 GEMM with a multi-stage global -> LDS pipeline, for the vision tower's linears and
+// the decoder's prefill linears:
 //   out[m, n] = epi(fp16(sum_k x[m, k] w[n, k] + bias[n]))
-// x fp16 [M, K] (row stride ldx), w fp16 [N, K] (nn.Linear layout, row stride K), fp32
-// accumulation on v_mfma_f32_16x16x32_f16.  Epilogues: STORE, QGELU (x sigmoid(1.702 x)),
-// GELU (erf), RESID (fp16(res + h)).
+// x fp16 [M, K] (row stride ldx); w one of
+//   GW_ROWS  fp16 [N, K] (nn.Linear layout, row stride K),
+//   GW_F16   this library's packed fp16 layout [N/16][K/32][64][8] (omni_f16_pack),
+//   GW_INT4  the packed int4 layout [N/16][K/128][64][4] + scales [N/16][K/128][16]
+//            (omni_gptq_repack), dequantised as fp16((q - 8) s);
+// fp32 accumulation on v_mfma_f32_16x16x32_f16.  Epilogues: STORE (bias added before or,
+// GPTQ order, after the fp16 rounding), QGELU (x sigmoid(1.702 x)), GELU (erf), RESID
+// (fp16(res + h)), SILU (packed weights with gate|up tiles interleaved: silu(g) * u).
+//
+// The packed layouts are MFMA operand blocks: 1 KB per (16 columns, 32 k) for fp16, per
+// (16 columns, 128 k) for int4 (lane l: column l % 16, k = 8 (l / 16) + e, one 4-byte
+// word per 32-k step), so a block is staged to LDS as one contiguous load and read back
+// by each lane at 16 l (fp16) or 4 l (int4: the step's two words land as two 256-byte
+// planes): no swizzle is needed for them.
 //
 // Persistent grid (one workgroup per CU at most) walking 64 WM x 128 output tiles in
 // grouped, XCD-aware order.  2 WM waves, each owning a 64 (m) x 64 (n) sub-tile: per K
@@ -20,13 +32,17 @@
 #define GP_ROWB 128      // LDS bytes per staged operand row (one step)
 #define GP_GM 4          // tile rows per group of the tile order
 
-enum { GP_STORE = 0, GP_QGELU = 4, GP_GELU = 5, GP_RESID = 6 };
+enum { GP_STORE = 0, GP_SILU = 1, GP_QGELU = 4, GP_GELU = 5, GP_RESID = 6 };
+enum { GW_ROWS = 0, GW_F16 = 1, GW_INT4 = 2 };
 
 struct GemmPipeArgs {
   const half_t* x;
   int ldx;
-  const half_t* w;
+  const half_t* w;       // GW_ROWS / GW_F16
   int ldw;
+  const uint32_t* wq;    // GW_INT4 codes
+  const half_t* wsc;     // GW_INT4 scales
+  int bias_after_round;  // 1: fp16(fp16(acc) + b) (GPTQ); 0: fp16(acc + b)
   const half_t* bias;    // [N] or NULL
   const half_t* res;     // GP_RESID: [M, ldr]
   int ldr;
@@ -50,6 +66,13 @@ __device__ __forceinline__ half_t gp_quick_gelu(half_t h) {
   return (half_t)((float)h * sg);
 }
 
+// fp16 of acc + bias in the linear's order (bias_after_round: added to the fp16 rounding)
+__device__ __forceinline__ half_t gp_bias(float acc, half_t b, bool has_bias, int bar) {
+#pragma clang fp contract(off)
+  if (!has_bias) return (half_t)acc;
+  return bar ? (half_t)((float)(half_t)acc + (float)b) : (half_t)(acc + (float)b);
+}
+
 __device__ __forceinline__ half_t gp_gelu(half_t h) {
 #pragma clang fp contract(off)
   const float x = (float)h;
@@ -61,23 +84,29 @@ __device__ __forceinline__ half_t gp_gelu(half_t h) {
 // pointer, and the slice's K steps.
 struct GpTileSrc {
   const half_t* x[4];
-  const half_t* w;
+  const half_t* w;       // GW_ROWS: the lane's row
+  const void* wp[4];     // GW_F16 / GW_INT4: the lane's block of each w load (step 0 / group 0)
+  const half_t* sp;      // GW_INT4: the lane's scale pair (group 0)
   const half_t* b;
+  int kb;                // the slice's first K step
   int kc;
 };
 
-template <int WM, int NS, int EPI>
+template <int WF, int WM, int NS, int EPI>
 __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) {
 #pragma clang fp contract(off)
   constexpr int BM = 64 * WM;
   constexpr int NWV = 2 * WM;
   constexpr int XLD = 4;                // x loads per wave and step (BM rows / 8 / NWV)
-  constexpr int WLD = 8 / WM;           // w loads per wave and step (128 rows / 8 / NWV)
-  constexpr int OPS = XLD + WLD;        // loads every thread issues per step (wave 0: + bias)
+  constexpr int WLD = 8 / WM;           // w loads per wave and step (16 per step / NWV)
+  constexpr int OPS = XLD + WLD;        // loads every thread issues per step (waves 0, 1: + 1)
+  constexpr int WB = WF == GW_INT4 ? 16 * 256 : GP_BN * GP_ROWB;   // w bytes per stage
   __shared__ __attribute__((aligned(1024))) uint8_t xl[NS][BM * GP_ROWB];
-  __shared__ __attribute__((aligned(1024))) uint8_t wl[NS][GP_BN * GP_ROWB];
+  __shared__ __attribute__((aligned(1024))) uint8_t wl[NS][WB];
   // bias slot: 64 lanes x 16 bytes land per load (lanes 16-63 repeat lane 15's chunk)
   __shared__ __attribute__((aligned(16))) half_t bsl[NS][512];
+  // GW_INT4 scale slot: the 8 tiles' 16 scales of the step's group
+  __shared__ __attribute__((aligned(16))) half_t ssl[NS][WF == GW_INT4 ? 128 : 2];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -109,14 +138,35 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
     grouped_tile(it - sl * tiles, tiles_m, tiles_n, GP_GM, tm, tn);
     m0 = tm * BM;
     n0 = tn * GP_BN;
-    const int kb = sl * nk / a.KS;
+    // int4 slices are whole 128-k groups (pairs of steps): a step's scales are its group's
+    const int kb = WF == GW_INT4 ? 2 * (sl * (nk / 2) / a.KS) : sl * nk / a.KS;
+    const int ke = WF == GW_INT4 ? 2 * ((sl + 1) * (nk / 2) / a.KS) : (sl + 1) * nk / a.KS;
     GpTileSrc t;
-    t.kc = (sl + 1) * nk / a.KS - kb;
+    t.kb = kb;
+    t.kc = ke - kb;
 #pragma unroll
     for (int u = 0; u < XLD; ++u)
       t.x[u] = a.x + (int64_t)min(m0 + 8 * NWV * u + lrow, a.M - 1) * a.ldx + kb * GP_BKH + lchunk * 8;
-    t.w = a.w + (int64_t)(n0 + lrow) * a.ldw + kb * GP_BKH + lchunk * 8;
-    t.b = has_bias ? a.bias + n0 + 8 * min(lane, 15) : a.w;
+    if constexpr (WF == GW_ROWS) {
+      t.w = a.w + (int64_t)(n0 + lrow) * a.ldw + kb * GP_BKH + lchunk * 8;
+    } else if constexpr (WF == GW_F16) {
+      // load u of this wave moves block b = NWV u + wave: column tile b / 2, 32-k block b % 2
+#pragma unroll
+      for (int u = 0; u < WLD; ++u) {
+        const int b = NWV * u + wave;
+        t.wp[u] = a.w + (((int64_t)(n0 / 16 + b / 2) * (a.K / 32) + 2 * kb + (b & 1)) * 64 + lane) * 8;
+      }
+    } else {
+      // load u moves word (step parity) b % 2 of column tile b / 2's block, 4 bytes a lane
+#pragma unroll
+      for (int u = 0; u < WLD; ++u) {
+        const int b = NWV * u + wave;
+        t.wp[u] = a.wq + ((int64_t)(n0 / 16 + b / 2) * (a.K / 128) * 64 + lane) * 4 + (b & 1);
+      }
+      // lane i: scales 2 (i % 8), +1 of column tile i / 8
+      t.sp = a.wsc + (int64_t)(n0 / 16 + lane / 8) * (a.K / 128) * 16 + 2 * (lane & 7);
+    }
+    t.b = has_bias ? a.bias + n0 + 8 * min(lane, 15) : a.x;
     return t;
   };
   const int64_t wstep = (int64_t)8 * NWV * a.ldw;       // halfs between w row groups
@@ -126,10 +176,27 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
     for (int u = 0; u < XLD; ++u)
       __builtin_amdgcn_global_load_lds((const void*)(t.x[u] + k0),
                                        (lds_void*)((lds_u8*)&xl[st][(8 * NWV * u + 8 * wave) * GP_ROWB]), 16, 0, 0);
+    if constexpr (WF == GW_ROWS) {
 #pragma unroll
-    for (int u = 0; u < WLD; ++u)
-      __builtin_amdgcn_global_load_lds((const void*)(t.w + u * wstep + k0),
-                                       (lds_void*)((lds_u8*)&wl[st][(8 * NWV * u + 8 * wave) * GP_ROWB]), 16, 0, 0);
+      for (int u = 0; u < WLD; ++u)
+        __builtin_amdgcn_global_load_lds((const void*)(t.w + u * wstep + k0),
+                                         (lds_void*)((lds_u8*)&wl[st][(8 * NWV * u + 8 * wave) * GP_ROWB]), 16, 0, 0);
+    } else if constexpr (WF == GW_F16) {
+#pragma unroll
+      for (int u = 0; u < WLD; ++u)     // two 1 KB blocks per tile and step
+        __builtin_amdgcn_global_load_lds((const void*)((const half_t*)t.wp[u] + ks * 1024),
+                                         (lds_void*)((lds_u8*)&wl[st][(NWV * u + wave) * 1024]), 16, 0, 0);
+    } else {
+      const int S = t.kb + ks;          // absolute step: group S / 2, words 2 (S % 2) + 0/1
+      const int64_t woff = (int64_t)(S >> 1) * 256 + 2 * (S & 1);
+#pragma unroll
+      for (int u = 0; u < WLD; ++u)
+        __builtin_amdgcn_global_load_lds((const void*)((const uint32_t*)t.wp[u] + woff),
+                                         (lds_void*)((lds_u8*)&wl[st][(NWV * u + wave) * 256]), 4, 0, 0);
+      if (wave == 1)                    // the 8 tiles' scales of the group
+        __builtin_amdgcn_global_load_lds((const void*)(t.sp + (int64_t)(S >> 1) * 16),
+                                         (lds_void*)((lds_u8*)&ssl[st][0]), 4, 0, 0);
+    }
     if (wave == 0 && has_bias)        // the tile's 128 biases (lanes 0-15 carry them)
       __builtin_amdgcn_global_load_lds((const void*)t.b, (lds_void*)((lds_u8*)&bsl[st][0]), 16, 0, 0);
   };
@@ -139,6 +206,16 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
   // Addresses of the lane's 16 operand bytes (k = 8 g4 .. +7 of K sub-step t) of tile rows
   // base + 16 i + l16: chunk 4 t + g4.
   auto operand_addrs = [&](int st, int o, int base, uint32_t (&ad)[8]) {
+    if (o && WF != GW_ROWS) {           // packed blocks: (tile 4 wn + i, step half t)
+      const uint32_t blk = (uint32_t)(uintptr_t)(lds_u8*)&wl[st][0];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          ad[2 * i + t] = blk + ((uint32_t)(2 * (4 * wn + i) + t) << (WF == GW_INT4 ? 8 : 10)) +
+                          (uint32_t)lane * (WF == GW_INT4 ? 4 : 16);
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = base + 16 * i + l16;
@@ -165,6 +242,48 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
           "v"(aw[7]), "v"(ax[0]), "v"(ax[1]), "v"(ax[2]), "v"(ax[3]), "v"(ax[4]), "v"(ax[5]),
           "v"(ax[6]), "v"(ax[7])
         : "memory");
+  };
+  // GW_INT4: the 8 x operands (b128), the 8 step words of the wave's 4 tiles (b32) and their
+  // 4 column scales (u16)
+  auto read_issue_q = [&](int st, u32x4 (&v)[16], uint32_t (&wd)[8], uint32_t (&sc)[4]) {
+    uint32_t aw[8], ax[8], as[4];
+    operand_addrs(st, 1, 64 * wn, aw);
+    operand_addrs(st, 0, 64 * wm, ax);
+    typedef __attribute__((address_space(3))) half_t lds_f16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) as[i] = (uint32_t)(uintptr_t)(lds_f16*)&ssl[st][16 * (4 * wn + i) + l16];
+    asm volatile(
+        "ds_read_b128 %0, %8\n\tds_read_b128 %1, %9\n\tds_read_b128 %2, %10\n\t"
+        "ds_read_b128 %3, %11\n\tds_read_b128 %4, %12\n\tds_read_b128 %5, %13\n\t"
+        "ds_read_b128 %6, %14\n\tds_read_b128 %7, %15"
+        : "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11]), "=&v"(v[12]), "=&v"(v[13]),
+          "=&v"(v[14]), "=&v"(v[15])
+        : "v"(ax[0]), "v"(ax[1]), "v"(ax[2]), "v"(ax[3]), "v"(ax[4]), "v"(ax[5]), "v"(ax[6]),
+          "v"(ax[7])
+        : "memory");
+    asm volatile(
+        "ds_read_b32 %0, %8\n\tds_read_b32 %1, %9\n\tds_read_b32 %2, %10\n\t"
+        "ds_read_b32 %3, %11\n\tds_read_b32 %4, %12\n\tds_read_b32 %5, %13\n\t"
+        "ds_read_b32 %6, %14\n\tds_read_b32 %7, %15"
+        : "=&v"(wd[0]), "=&v"(wd[1]), "=&v"(wd[2]), "=&v"(wd[3]), "=&v"(wd[4]), "=&v"(wd[5]),
+          "=&v"(wd[6]), "=&v"(wd[7])
+        : "v"(aw[0]), "v"(aw[1]), "v"(aw[2]), "v"(aw[3]), "v"(aw[4]), "v"(aw[5]), "v"(aw[6]),
+          "v"(aw[7])
+        : "memory");
+    asm volatile(
+        "ds_read_u16 %0, %4\n\tds_read_u16 %1, %5\n\tds_read_u16 %2, %6\n\tds_read_u16 %3, %7"
+        : "=&v"(sc[0]), "=&v"(sc[1]), "=&v"(sc[2]), "=&v"(sc[3])
+        : "v"(as[0]), "v"(as[1]), "v"(as[2]), "v"(as[3])
+        : "memory");
+  };
+  auto read_wait_q = [&](u32x4 (&v)[16], uint32_t (&wd)[8], uint32_t (&sc)[4]) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(v[8]), "+v"(v[9]), "+v"(v[10]), "+v"(v[11]), "+v"(v[12]), "+v"(v[13]),
+                   "+v"(v[14]), "+v"(v[15]), "+v"(wd[0]), "+v"(wd[1]), "+v"(wd[2]), "+v"(wd[3]),
+                   "+v"(wd[4]), "+v"(wd[5]), "+v"(wd[6]), "+v"(wd[7]), "+v"(sc[0]), "+v"(sc[1]),
+                   "+v"(sc[2]), "+v"(sc[3])
+                 :
+                 : "memory");
   };
   auto read_wait = [&](u32x4 (&v)[16]) {
     asm volatile("s_waitcnt lgkmcnt(0)"
@@ -207,8 +326,21 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
     for (int ks = 0; ks < kc; ++ks, ++sidx) {
       const int st = sidx % NS;
       u32x4 ops[16];
-      read_issue(st, ops);
-      read_wait(ops);
+      if constexpr (WF == GW_INT4) {
+        uint32_t wd[8], sc[4];
+        read_issue_q(st, ops, wd, sc);
+        read_wait_q(ops, wd, sc);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const half_t sv = __builtin_bit_cast(half_t, (uint16_t)sc[i]);
+          const half2_t s2 = {sv, sv};
+#pragma unroll
+          for (int t = 0; t < 2; ++t) ops[2 * i + t] = __builtin_bit_cast(u32x4, dequant8(wd[2 * i + t], s2));
+        }
+      } else {
+        read_issue(st, ops);
+        read_wait(ops);
+      }
       if (ks == kc - 1 && has_bias) read_bias(st);
       // step sidx + 1 has landed for this thread, then for everyone; every wave has also
       // read step sidx's slot, which is refilled with step sidx + NS
@@ -244,6 +376,20 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
         }
         continue;
       }
+      if constexpr (EPI == GP_SILU) {
+        // tiles (4 wn + i, 4 wn + i + 1), i even, are (gate, up) of intermediate columns
+        // 16 ((n0 + 64 wn) / 32 + i / 2) + 4 g4 + q
+#pragma unroll
+        for (int i = 0; i < 4; i += 2) {
+          const int n = (n0c + 64 * wn + 16 * i) / 2 + 4 * g4;
+          half4_t o;
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            o[q] = (half_t)silu_mul_f32((float)(half_t)acc[i][j][q], (float)(half_t)acc[i + 1][j][q]);
+          *(half4_t*)(a.out + (int64_t)m * a.ldo + n) = o;
+        }
+        continue;
+      }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int n = n0c + 64 * wn + 16 * i + 4 * g4;
@@ -253,7 +399,7 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
         half4_t o;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          half_t h = has_bias ? (half_t)(acc[i][j][q] + (float)bb[q]) : (half_t)acc[i][j][q];
+          half_t h = gp_bias(acc[i][j][q], bb[q], has_bias, a.bias_after_round);
           if constexpr (EPI == GP_QGELU) h = gp_quick_gelu(h);
           if constexpr (EPI == GP_GELU) h = gp_gelu(h);
           if constexpr (EPI == GP_RESID) h = (half_t)((float)rr[q] + (float)h);
@@ -304,7 +450,7 @@ __global__ __launch_bounds__(256) void gemm_pipe_finish_kernel(GemmPipeArgs a) {
   half4_t o;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    half_t h = a.bias ? (half_t)(v[q] + (float)bb[q]) : (half_t)v[q];
+    half_t h = gp_bias(v[q], bb[q], a.bias != nullptr, a.bias_after_round);
     if constexpr (EPI == GP_QGELU) h = gp_quick_gelu(h);
     if constexpr (EPI == GP_GELU) h = gp_gelu(h);
     if constexpr (EPI == GP_RESID) h = (half_t)((float)rr[q] + (float)h);
@@ -313,14 +459,15 @@ __global__ __launch_bounds__(256) void gemm_pipe_finish_kernel(GemmPipeArgs a) {
   *(half4_t*)(a.out + (int64_t)m * a.ldo + n) = o;
 }
 
-template <int WM, int NS>
+template <int WF, int WM, int NS>
 static int gp_launch(const GemmPipeArgs& a, int epilogue, hipStream_t st) {
   const int64_t items = (int64_t)ceil_div(a.M, 64 * WM) * (a.N / GP_BN) * a.KS;
   if (items > 0x7fffffff) return OMNI_EUNSUPPORTED;
   const int grid = (int)(items < gp_num_cus() ? items : gp_num_cus());
   const dim3 blk(128 * WM);
   if (a.KS > 1) {                    // partial sums, then the finish kernel's epilogue
-    hipLaunchKernelGGL((gemm_pipe_kernel<WM, NS, GP_STORE>), dim3(grid), blk, 0, st, a);
+    if (epilogue == GP_SILU) return OMNI_EINVAL;
+    hipLaunchKernelGGL((gemm_pipe_kernel<WF, WM, NS, GP_STORE>), dim3(grid), blk, 0, st, a);
     OMNI_CHECK_LAUNCH();
     const int64_t nthr = (int64_t)a.M * (a.N / 4);
     const dim3 fg((unsigned)((nthr + 255) / 256));
@@ -335,10 +482,14 @@ static int gp_launch(const GemmPipeArgs& a, int epilogue, hipStream_t st) {
     return OMNI_OK;
   }
   switch (epilogue) {
-    case GP_STORE: hipLaunchKernelGGL((gemm_pipe_kernel<WM, NS, GP_STORE>), dim3(grid), blk, 0, st, a); break;
-    case GP_QGELU: hipLaunchKernelGGL((gemm_pipe_kernel<WM, NS, GP_QGELU>), dim3(grid), blk, 0, st, a); break;
-    case GP_GELU: hipLaunchKernelGGL((gemm_pipe_kernel<WM, NS, GP_GELU>), dim3(grid), blk, 0, st, a); break;
-    case GP_RESID: hipLaunchKernelGGL((gemm_pipe_kernel<WM, NS, GP_RESID>), dim3(grid), blk, 0, st, a); break;
+    case GP_STORE: hipLaunchKernelGGL((gemm_pipe_kernel<WF, WM, NS, GP_STORE>), dim3(grid), blk, 0, st, a); break;
+    case GP_SILU:
+      if constexpr (WF == GW_ROWS) return OMNI_EINVAL;
+      else hipLaunchKernelGGL((gemm_pipe_kernel<WF, WM, NS, GP_SILU>), dim3(grid), blk, 0, st, a);
+      break;
+    case GP_QGELU: hipLaunchKernelGGL((gemm_pipe_kernel<WF, WM, NS, GP_QGELU>), dim3(grid), blk, 0, st, a); break;
+    case GP_GELU: hipLaunchKernelGGL((gemm_pipe_kernel<WF, WM, NS, GP_GELU>), dim3(grid), blk, 0, st, a); break;
+    case GP_RESID: hipLaunchKernelGGL((gemm_pipe_kernel<WF, WM, NS, GP_RESID>), dim3(grid), blk, 0, st, a); break;
     default: return OMNI_EINVAL;
   }
   OMNI_CHECK_LAUNCH();
@@ -419,6 +570,65 @@ extern "C" int omni_f16_gemm_pipe(const void* x, int ldx, const void* w, const v
   a.K = K;
   a.KS = ksplit;
   a.part = workspace;
+  a.wq = nullptr;
+  a.wsc = nullptr;
+  a.bias_after_round = 0;
   hipStream_t st = (hipStream_t)stream;
-  return tile_rows == 256 ? gp_launch<4, 3>(a, epilogue, st) : gp_launch<2, 4>(a, epilogue, st);
+  return tile_rows == 256 ? gp_launch<GW_ROWS, 4, 3>(a, epilogue, st)
+                          : gp_launch<GW_ROWS, 2, 4>(a, epilogue, st);
+}
+
+// The decoder's prefill linears on the same pipeline with this library's packed weights
+// (fmt 0: int4 from omni_gptq_repack with its scales, 1: fp16 from omni_f16_pack); see the
+// header for the arguments.  Stages per tile height: int4 6 (128 rows) / 4 (256 rows),
+// fp16 4 / 3 (the int4 operand tile is a quarter of the fp16 one).
+extern "C" int omni_packed_gemm_pipe(const void* x, int ldx, const void* w_packed,
+                                     const void* scales_packed, int fmt, const void* bias,
+                                     int bias_after_round, void* out, int ldo, int M, int N, int K,
+                                     int epilogue, int tile_rows, int ksplit, float* workspace,
+                                     void* stream) {
+  if (M < 0 || N <= 0 || K <= 0 || ksplit < 0) return OMNI_EINVAL;
+  if (fmt != 0 && fmt != 1) return OMNI_EINVAL;
+  if ((N % GP_BN) || (K % 128) || K < 4 * GP_BKH) return OMNI_EUNSUPPORTED;
+  if (M == 0) return OMNI_OK;
+  if (!x || !w_packed || !out || (fmt == 0 && !scales_packed)) return OMNI_EINVAL;
+  if (epilogue != GP_STORE && epilogue != GP_SILU) return OMNI_EINVAL;
+  const int n_out = epilogue == GP_SILU ? N / 2 : N;
+  if (ldx < K || (ldx & 7) || ldo < n_out || (ldo & 3)) return OMNI_EINVAL;
+  if (((uintptr_t)x & 15) || ((uintptr_t)w_packed & 15) || ((uintptr_t)out & 7)) return OMNI_EINVAL;
+  if (bias && ((uintptr_t)bias & 15)) return OMNI_EINVAL;
+  if (epilogue == GP_SILU && bias) return OMNI_EINVAL;
+  if (tile_rows != 0 && tile_rows != 128 && tile_rows != 256) return OMNI_EINVAL;
+  if (tile_rows == 0) tile_rows = gp_tile_rows(M, N);
+  if (fmt == 0 && ((uintptr_t)scales_packed & 3)) return OMNI_EINVAL;
+  if (ksplit == 0) ksplit = epilogue == GP_SILU ? 1 : omni_f16_gemm_pipe_splits(M, N, K, tile_rows);
+  if (epilogue == GP_SILU && ksplit != 1) return OMNI_EINVAL;
+  // every slice covers at least NS pipeline steps (slices are whole 128-groups of 2 steps)
+  const int ns = fmt == 0 ? (tile_rows == 256 ? 4 : 6) : (tile_rows == 256 ? 3 : 4);
+  if (2 * (K / 128 / ksplit) < ns) return OMNI_EUNSUPPORTED;
+  if (ksplit > 1 && (!workspace || ((uintptr_t)workspace & 15))) return OMNI_EINVAL;
+  GemmPipeArgs a;
+  a.x = (const half_t*)x;
+  a.ldx = ldx;
+  a.w = fmt == 1 ? (const half_t*)w_packed : nullptr;
+  a.ldw = K;
+  a.wq = fmt == 0 ? (const uint32_t*)w_packed : nullptr;
+  a.wsc = (const half_t*)scales_packed;
+  a.bias_after_round = bias_after_round;
+  a.bias = (const half_t*)bias;
+  a.res = nullptr;
+  a.ldr = 0;
+  a.out = (half_t*)out;
+  a.ldo = ldo;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.KS = ksplit;
+  a.part = workspace;
+  hipStream_t st = (hipStream_t)stream;
+  if (fmt == 0)
+    return tile_rows == 256 ? gp_launch<GW_INT4, 4, 4>(a, epilogue, st)
+                            : gp_launch<GW_INT4, 2, 6>(a, epilogue, st);
+  return tile_rows == 256 ? gp_launch<GW_F16, 4, 3>(a, epilogue, st)
+                          : gp_launch<GW_F16, 2, 4>(a, epilogue, st);
 }

@@ -108,7 +108,6 @@ struct WStream<W_FP16> {
   }
 };
 
-__device__ __forceinline__ float silu_ref(float g) { return g * (1.0f / (1.0f + __expf(-g))); }
 
 // x * sigmoid(1.702 x) with the three fp16 roundings of the reference's elementwise ops
 // (model/qwen2_vit.py:18-19 on fp16 tensors: 1.702 x, sigmoid, product).
@@ -458,7 +457,7 @@ __global__ __launch_bounds__(CW * KW * 64, 1) void gemv_kernel(GemvArgs a) {
           const int j = (tile0 >> 1) * 16 + c16;
           const float g = (float)(half_t)acc[0][mb][i];
           const float u = (float)(half_t)acc[1][mb][i];
-          a.out[(int64_t)m * a.ldo + j] = (half_t)(silu_ref(g) * u);
+          a.out[(int64_t)m * a.ldo + j] = (half_t)silu_mul_f32(g, u);
         } else if constexpr (EPI == EPI_PARTIAL) {
 #pragma unroll
           for (int c = 0; c < CPW; ++c) {
@@ -709,7 +708,7 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(GemvArgs a) {
           const int j = ((nt0 + c) >> 1) * 16 + c16;
           const float gv = (float)(half_t)acc[i][c][r];
           const float uv = (float)(half_t)acc[i][c + 1][r];
-          a.out[(int64_t)m * a.ldo + j] = (half_t)(silu_ref(gv) * uv);
+          a.out[(int64_t)m * a.ldo + j] = (half_t)silu_mul_f32(gv, uv);
         }
       } else if constexpr (EPI == EPI_PARTIAL) {
         // the slice's fp32 sums, [slice][M][N]
@@ -827,7 +826,19 @@ static int gemv_common(int wf, const void* x, int ldx, const void* w, const void
   a.KS = (K + a.KC - 1) / a.KC;
   a.kx = K;
   hipStream_t st = (hipStream_t)stream;
-  if (M > 64) {   // many rows (prefill): the tiled kernel, STORE / SILU epilogues
+  if (M > 64) {   // many rows (prefill): STORE / SILU epilogues
+    // the pipelined GEMM where its shape and alignment rules hold (every K slice at least
+    // 3 groups: its deepest pipeline is 6 steps of 64), else the tiled kernel
+    const int slices = tile_split ? omni_gemm_slices(K, ksplit) : 1;
+    const bool pipe = (N % 128) == 0 && K >= 256 && KG / slices >= 3 &&
+                      ((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0 &&
+                      ((uintptr_t)out & 7) == 0 && (ldo & 3) == 0 &&
+                      (!bias || ((uintptr_t)bias & 15) == 0) &&
+                      (wf != W_INT4 || ((uintptr_t)scales & 3) == 0);
+    if (pipe)
+      return omni_packed_gemm_pipe(x, ldx, w, scales, wf == W_INT4 ? 0 : 1, bias, bias_after_round,
+                                   out, ldo, M, N, K, epilogue, 0, slices,
+                                   tile_split ? partial : nullptr, stream);
     if (tile_split)
       return wf == W_INT4 ? launch_gemm_tile_split<W_INT4>(a, st) : launch_gemm_tile_split<W_FP16>(a, st);
     a.KS = 1;

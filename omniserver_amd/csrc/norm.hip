@@ -388,8 +388,6 @@ extern "C" int omni_embedding(const int64_t* ids, const void* table, int table_p
 // ---------------------------------------------------------------------------
 // SiLU-mul: gate_up [rows, 2n] (gate first, up second) -> out [rows, n].
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float silu_f32(float g) { return g * (1.0f / (1.0f + __expf(-g))); }
-
 // fp16 (or, BF16, bf16 as the reference's FP8 route feeds it, qwen2_llm.py:130-131) in and out.
 template <bool BF16>
 __global__ __launch_bounds__(256) void silu_mul_kernel(const unsigned short* __restrict__ gu,
@@ -405,7 +403,7 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const unsigned short* __r
     const u16x8 u = *(const u16x8*)(gu + (size_t)row * 2 * n + n + c * 8);
     u16x8 o;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = st16f<BF16>(silu_f32(ld16f<BF16>(g[e])) * ld16f<BF16>(u[e]));
+    for (int e = 0; e < 8; ++e) o[e] = st16f<BF16>(silu_mul_f32(ld16f<BF16>(g[e]), ld16f<BF16>(u[e])));
     *(u16x8*)(out + (size_t)row * n + c * 8) = o;
   }
 }

@@ -298,12 +298,14 @@ def test_w4a16_gemm(gpu, M, K, N, bias, silu):
 @pytest.mark.parametrize("M", [65, 300])
 @pytest.mark.parametrize("K,N,bias,silu", [
     (1536, 2048, True, False), (8960, 1536, False, False), (1536, 17920, False, True),
-    (256, 48, True, False),
+    # N % 128 != 0: the tiled kernel instead of the pipelined one
+    (256, 48, True, False), (1536, 2064, True, False), (1536, 17952, False, True),
 ])
 def test_tiled_gemm(gpu, fmt, M, K, N, bias, silu):
-    """Prefill-size linears (M > 64) run the tiled MFMA GEMM: within tolerance of the
-    oracle, and bit-equal to the skinny kernel run over 64-row blocks with one wave per
-    K range (the same k order: groups ascending, 32-k steps ascending)."""
+    """Prefill-size linears (M > 64) run an MFMA GEMM (the pipelined one for N % 128 == 0,
+    else the tiled one): within tolerance of the oracle, and bit-equal to the skinny kernel
+    run over 64-row blocks with one wave per K range (the same k order: groups ascending,
+    32-k steps ascending)."""
     from omniserver_amd.linear import F16Linear, GPTQLinear
     say(f"tiled gemm fmt={fmt} M={M} K={K} N={N} bias={bias} silu={silu}")
     b = f16((N,), 91, 0.02) if bias else None
@@ -349,6 +351,75 @@ def test_tiled_gemm(gpu, fmt, M, K, N, bias, silu):
             mag = torch.maximum(torch.maximum(out.cpu().float().abs(), sp.cpu().float().abs()), e_nb)
             assert (ds <= mag * 2.0 ** -9 + absprod * 2.0 ** -20).all(), ds.max().item()
             assert (sp.cpu().float() - e).abs().max().item() <= 2e-3 * max(1.0, e.abs().max().item())
+
+
+@pytest.mark.parametrize("fmt", ["int4", "fp16"])
+@pytest.mark.parametrize("M", [65, 300, 1000])
+@pytest.mark.parametrize("K,N,bias,silu", [
+    (1536, 2048, True, False), (8960, 1536, True, False), (1536, 17920, False, True),
+    (384, 256, False, False),
+])
+def test_packed_gemm_pipe(gpu, fmt, M, K, N, bias, silu):
+    """omni_packed_gemm_pipe through the C ABI at both tile heights and several K splits:
+    unsplit results equal at 128 and 256 rows (the same k order per output) and equal to
+    the skinny kernel over 64-row blocks; every form within tolerance of the oracle; split
+    results within a rounding step of the unsplit ones."""
+    from omniserver_amd._lib import call, ptr, stream
+    from omniserver_amd.linear import F16Linear, GPTQLinear
+    say(f"packed gemm pipe fmt={fmt} M={M} K={K} N={N} bias={bias} silu={silu}")
+    b = f16((N,), 95, 0.02) if bias else None
+    x = f16((M, K), 96)
+    if fmt == "int4":
+        qw, sc = _gptq(K, N, 97 + K + N)
+        W = ref.gptq_dequant(qw, sc)
+        lin = GPTQLinear(qw.to(gpu), sc.to(gpu), None if b is None else b.to(gpu), fuse_silu=silu)
+        wp, sp, code = lin.qweight_packed, lin.scales_packed, 0
+    else:
+        wt = f16((N, K), 98, 0.02)
+        W = wt.float().t()
+        lin = F16Linear(wt.to(gpu), None if b is None else b.to(gpu), fuse_silu=silu)
+        wp, sp, code = lin.weight_packed, None, 1
+    if silu:
+        e = ref.silu_mul(ref.linear(x.float(), W))
+    else:
+        e = ref.linear(x.float(), W, None if b is None else b.float(),
+                       bias_after_round=fmt == "int4")
+    tol = 2e-3 * max(1.0, e.abs().max().item())
+    xg = x.to(gpu)
+    bg = lin.bias
+    epi = 1 if silu else 0
+    nout = lin.out_features
+
+    def run(tile_rows, ksplit):
+        out = torch.full((M, nout), float("nan"), device=gpu, dtype=torch.float16)
+        ws = torch.empty(max(4, ksplit) * M * N, device=gpu, dtype=torch.float32)  # ksplit 0: <= 4
+        call("omni_packed_gemm_pipe", ptr(xg), K, ptr(wp), ptr(sp), code, ptr(bg),
+             int(fmt == "int4"), ptr(out), nout, M, N, K, epi, tile_rows, ksplit,
+             ptr(ws) if ksplit != 1 else None, stream())
+        torch.cuda.synchronize()
+        return out.cpu()
+
+    o128, o256 = run(128, 1), run(256, 1)
+    assert torch.equal(o128, o256)
+    assert (o128.float() - e).abs().max().item() <= tol
+    blocks = torch.empty(M, nout, device=gpu, dtype=torch.float16)
+    for s0 in range(0, M, 64):
+        s1 = min(M, s0 + 64)
+        lin.forward_out(xg[s0:s1], blocks[s0:s1], preset=1)
+    assert torch.equal(o128, blocks.cpu())
+    if silu:
+        return
+    e_nb = ref.linear(x.float(), W).abs()
+    absprod = x.float().abs() @ W.abs()
+    KG = K // 128
+    for tr, ks in ((128, 0), (128, 2), (256, KG // 3), (256, 0)):
+        if ks > 1 and 2 * (KG // ks) < (6 if fmt == "int4" and tr == 128 else 4):
+            continue
+        sp_out = run(tr, ks)
+        ds = (sp_out.float() - o128.float()).abs()
+        mag = torch.maximum(torch.maximum(o128.float().abs(), sp_out.float().abs()), e_nb)
+        assert (ds <= mag * 2.0 ** -9 + absprod * 2.0 ** -20).all(), (tr, ks, ds.max().item())
+        assert (sp_out.float() - e).abs().max().item() <= tol, (tr, ks)
 
 
 @pytest.mark.parametrize("M", [1, 16, 32])

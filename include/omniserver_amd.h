@@ -229,6 +229,13 @@ int omni_f16_pack(const void* weight, void* weight_packed, int K, int N, int int
 int omni_w4_dequant(const int32_t* qweight_packed, const void* scales_packed, void* w, int K,
                     int N, void* stream);
 
+/* Packed int4 -> packed fp16 (omni_f16_pack's layout, tile order kept, so gate|up stays
+ * interleaved), W = fp16((q - 8) * s) as the int4 kernels dequantise it: the GPTQ prefill
+ * linears at many rows (kernels/marlin_linear.py:54-62) then run the fp16 GEMM on the same
+ * values.  weight_packed 16-byte aligned, N * K halfs. */
+int omni_w4_unpack_f16(const int32_t* qweight_packed, const void* scales_packed,
+                       void* weight_packed, int K, int N, void* stream);
+
 /* ---------------------------------------------------------------- vision tower */
 
 /* Epilogues of omni_f16_gemm_tiled beyond OMNI_EPI_STORE (h = fp16(x . W^T + bias)). */
@@ -246,7 +253,7 @@ int omni_f16_gemm_tiled(const void* x, int ldx, int kx, const void* weight_packe
 
 /* The same linears on a multi-stage global -> LDS pipeline GEMM (persistent grid, 128- or
  * 256-row x 128-column tiles): w fp16 [N, K] in nn.Linear layout (row stride K, no
- * packing).  N % 128 == 0, K % 64 == 0, K >= 256; x, w 16-byte aligned, ldx % 8 == 0,
+ * packing).  N % 128 == 0, K % 128 == 0, K >= 256; x, w 16-byte aligned, ldx % 8 == 0,
  * ldo / ldr % 4 == 0.  Epilogues as omni_f16_gemm_tiled; tile_rows 128, 256 or 0 (chosen
  * from the shape).  ksplit K slices (0: omni_f16_gemm_pipe_splits), each >= 256 of K;
  * ksplit > 1 writes fp32 partial sums to workspace (ksplit * M * N floats, 16-byte

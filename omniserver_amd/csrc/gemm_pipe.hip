@@ -22,9 +22,11 @@
 // MFMAs.  Operand rows go global -> LDS with global_load_lds (16 bytes per lane), NS
 // steps ahead, across tile boundaries (the last steps of a tile load the next tile's
 // first ones); the 16-byte chunks of a row are XOR-swizzled by row so that the 16 rows an
-// operand read touches spread over the banks.  A step is consumed once an exact per-thread
-// vmcnt and a barrier say it landed everywhere; its slot is refilled right after the
-// barrier, while the step's MFMAs run.
+// operand read touches spread over the banks.  A step's slot is read once an exact
+// per-thread vmcnt and a barrier say it landed everywhere, and refilled after the next
+// barrier; the LDS reads of step s + 1 are issued before the MFMAs of step s (two register
+// sets), so the read latency hides behind the MFMAs instead of following the barrier that
+// every wave of the workgroup passes together.  K slices are whole 128-k groups.
 #include "common.h"
 
 #define GP_BN 128        // tile columns (n)
@@ -138,9 +140,10 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
     grouped_tile(it - sl * tiles, tiles_m, tiles_n, GP_GM, tm, tn);
     m0 = tm * BM;
     n0 = tn * GP_BN;
-    // int4 slices are whole 128-k groups (pairs of steps): a step's scales are its group's
-    const int kb = WF == GW_INT4 ? 2 * (sl * (nk / 2) / a.KS) : sl * nk / a.KS;
-    const int ke = WF == GW_INT4 ? 2 * ((sl + 1) * (nk / 2) / a.KS) : (sl + 1) * nk / a.KS;
+    // slices are whole 128-k groups (pairs of steps): the main loop takes two steps at a
+    // time, and an int4 step's scales are its group's
+    const int kb = 2 * (sl * (nk / 2) / a.KS);
+    const int ke = 2 * ((sl + 1) * (nk / 2) / a.KS);
     GpTileSrc t;
     t.kb = kb;
     t.kc = ke - kb;
@@ -203,77 +206,111 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
   // Operand reads are inline asm with their own lgkmcnt wait: as plain loads the compiler
   // would make each wait for every outstanding global->LDS load (vmcnt(0)).  A step's
   // slot is complete by the vmcnt wait and barrier before it is read.
-  // Addresses of the lane's 16 operand bytes (k = 8 g4 .. +7 of K sub-step t) of tile rows
-  // base + 16 i + l16: chunk 4 t + g4.
-  auto operand_addrs = [&](int st, int o, int base, uint32_t (&ad)[8]) {
-    if (o && WF != GW_ROWS) {           // packed blocks: (tile 4 wn + i, step half t)
-      const uint32_t blk = (uint32_t)(uintptr_t)(lds_u8*)&wl[st][0];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-          ad[2 * i + t] = blk + ((uint32_t)(2 * (4 * wn + i) + t) << (WF == GW_INT4 ? 8 : 10)) +
-                          (uint32_t)lane * (WF == GW_INT4 ? 4 : 16);
-      return;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = base + 16 * i + l16;
-      const uint32_t row = (uint32_t)(uintptr_t)(lds_u8*)(o ? &wl[st][r * GP_ROWB] : &xl[st][r * GP_ROWB]);
-      ad[2 * i] = row + ((g4 ^ (r & 7)) << 4);
-      ad[2 * i + 1] = row + (((4 + g4) ^ (r & 7)) << 4);
-    }
+  // LDS byte addresses of the lane's operand fragments, as bases plus the immediate
+  // offsets of the reads.  Row-major tiles (x, and GW_ROWS w): fragment (i, t) holds k =
+  // 32 t + 8 g4 .. +7 of tile row base + 16 i + l16, at chunk (4 t + g4) ^ (row & 7) of the
+  // row; 16 i leaves row & 7 = l16 & 7, so sub-tiles i sit 16 rows = 2 KB apart from one
+  // base per t.  Packed w: block (tile 4 wn + i, half t) at (2 (4 wn + i) + t) 1 KB (fp16)
+  // or 256 B (int4 planes), the lane's bytes at 16 lane or 4 lane.
+  auto row_bases = [&](const uint8_t* tile, int base, uint32_t (&b)[2]) {
+    const int r = base + l16;
+    const uint32_t row = (uint32_t)(uintptr_t)(lds_u8*)(tile + r * GP_ROWB);
+    b[0] = row + ((g4 ^ (r & 7)) << 4);
+    b[1] = row + (((4 + g4) ^ (r & 7)) << 4);
+  };
+  auto packed_base = [&](int st) -> uint32_t {
+    return (uint32_t)(uintptr_t)(lds_u8*)&wl[st][0] + (uint32_t)(8 * wn) * (WF == GW_INT4 ? 256u : 1024u) +
+           (uint32_t)lane * (WF == GW_INT4 ? 4u : 16u);
   };
   auto read_issue = [&](int st, u32x4 (&v)[16]) {
-    uint32_t aw[8], ax[8];
-    operand_addrs(st, 1, 64 * wn, aw);
-    operand_addrs(st, 0, 64 * wm, ax);
-    asm volatile(
-        "ds_read_b128 %0, %16\n\tds_read_b128 %1, %17\n\tds_read_b128 %2, %18\n\t"
-        "ds_read_b128 %3, %19\n\tds_read_b128 %4, %20\n\tds_read_b128 %5, %21\n\t"
-        "ds_read_b128 %6, %22\n\tds_read_b128 %7, %23\n\tds_read_b128 %8, %24\n\t"
-        "ds_read_b128 %9, %25\n\tds_read_b128 %10, %26\n\tds_read_b128 %11, %27\n\t"
-        "ds_read_b128 %12, %28\n\tds_read_b128 %13, %29\n\tds_read_b128 %14, %30\n\t"
-        "ds_read_b128 %15, %31"
-        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
-          "=&v"(v[6]), "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11]),
-          "=&v"(v[12]), "=&v"(v[13]), "=&v"(v[14]), "=&v"(v[15])
-        : "v"(aw[0]), "v"(aw[1]), "v"(aw[2]), "v"(aw[3]), "v"(aw[4]), "v"(aw[5]), "v"(aw[6]),
-          "v"(aw[7]), "v"(ax[0]), "v"(ax[1]), "v"(ax[2]), "v"(ax[3]), "v"(ax[4]), "v"(ax[5]),
-          "v"(ax[6]), "v"(ax[7])
-        : "memory");
+    uint32_t bx[2];
+    row_bases(&xl[st][0], 64 * wm, bx);
+    if constexpr (WF == GW_ROWS) {
+      uint32_t bw[2];
+      row_bases(&wl[st][0], 64 * wn, bw);
+      asm volatile(
+        "ds_read_b128 %0, %16 offset:0\n\t"
+        "ds_read_b128 %1, %17 offset:0\n\t"
+        "ds_read_b128 %2, %16 offset:2048\n\t"
+        "ds_read_b128 %3, %17 offset:2048\n\t"
+        "ds_read_b128 %4, %16 offset:4096\n\t"
+        "ds_read_b128 %5, %17 offset:4096\n\t"
+        "ds_read_b128 %6, %16 offset:6144\n\t"
+        "ds_read_b128 %7, %17 offset:6144\n\t"
+        "ds_read_b128 %8, %18 offset:0\n\t"
+        "ds_read_b128 %9, %19 offset:0\n\t"
+        "ds_read_b128 %10, %18 offset:2048\n\t"
+        "ds_read_b128 %11, %19 offset:2048\n\t"
+        "ds_read_b128 %12, %18 offset:4096\n\t"
+        "ds_read_b128 %13, %19 offset:4096\n\t"
+        "ds_read_b128 %14, %18 offset:6144\n\t"
+        "ds_read_b128 %15, %19 offset:6144"
+          : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]), "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11]), "=&v"(v[12]), "=&v"(v[13]), "=&v"(v[14]), "=&v"(v[15])
+          : "v"(bw[0]), "v"(bw[1]), "v"(bx[0]), "v"(bx[1])
+          : "memory");
+    } else {
+      const uint32_t bw = packed_base(st);
+      asm volatile(
+        "ds_read_b128 %0, %16 offset:0\n\t"
+        "ds_read_b128 %1, %16 offset:1024\n\t"
+        "ds_read_b128 %2, %16 offset:2048\n\t"
+        "ds_read_b128 %3, %16 offset:3072\n\t"
+        "ds_read_b128 %4, %16 offset:4096\n\t"
+        "ds_read_b128 %5, %16 offset:5120\n\t"
+        "ds_read_b128 %6, %16 offset:6144\n\t"
+        "ds_read_b128 %7, %16 offset:7168\n\t"
+        "ds_read_b128 %8, %17 offset:0\n\t"
+        "ds_read_b128 %9, %18 offset:0\n\t"
+        "ds_read_b128 %10, %17 offset:2048\n\t"
+        "ds_read_b128 %11, %18 offset:2048\n\t"
+        "ds_read_b128 %12, %17 offset:4096\n\t"
+        "ds_read_b128 %13, %18 offset:4096\n\t"
+        "ds_read_b128 %14, %17 offset:6144\n\t"
+        "ds_read_b128 %15, %18 offset:6144"
+          : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]), "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11]), "=&v"(v[12]), "=&v"(v[13]), "=&v"(v[14]), "=&v"(v[15])
+          : "v"(bw), "v"(bx[0]), "v"(bx[1])
+          : "memory");
+    }
   };
-  // GW_INT4: the 8 x operands (b128), the 8 step words of the wave's 4 tiles (b32) and their
-  // 4 column scales (u16)
+  // GW_INT4: the 8 x fragments (b128), the 8 step words of the wave's 4 tiles (b32) and
+  // their 4 column scales (u16)
   auto read_issue_q = [&](int st, u32x4 (&v)[16], uint32_t (&wd)[8], uint32_t (&sc)[4]) {
-    uint32_t aw[8], ax[8], as[4];
-    operand_addrs(st, 1, 64 * wn, aw);
-    operand_addrs(st, 0, 64 * wm, ax);
+    uint32_t bx[2];
+    row_bases(&xl[st][0], 64 * wm, bx);
+    const uint32_t bw = packed_base(st);
     typedef __attribute__((address_space(3))) half_t lds_f16;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) as[i] = (uint32_t)(uintptr_t)(lds_f16*)&ssl[st][16 * (4 * wn + i) + l16];
+    const uint32_t bs = (uint32_t)(uintptr_t)(lds_f16*)&ssl[st][64 * wn + l16];
     asm volatile(
-        "ds_read_b128 %0, %8\n\tds_read_b128 %1, %9\n\tds_read_b128 %2, %10\n\t"
-        "ds_read_b128 %3, %11\n\tds_read_b128 %4, %12\n\tds_read_b128 %5, %13\n\t"
-        "ds_read_b128 %6, %14\n\tds_read_b128 %7, %15"
-        : "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11]), "=&v"(v[12]), "=&v"(v[13]),
-          "=&v"(v[14]), "=&v"(v[15])
-        : "v"(ax[0]), "v"(ax[1]), "v"(ax[2]), "v"(ax[3]), "v"(ax[4]), "v"(ax[5]), "v"(ax[6]),
-          "v"(ax[7])
+        "ds_read_b128 %0, %8 offset:0\n\t"
+        "ds_read_b128 %1, %9 offset:0\n\t"
+        "ds_read_b128 %2, %8 offset:2048\n\t"
+        "ds_read_b128 %3, %9 offset:2048\n\t"
+        "ds_read_b128 %4, %8 offset:4096\n\t"
+        "ds_read_b128 %5, %9 offset:4096\n\t"
+        "ds_read_b128 %6, %8 offset:6144\n\t"
+        "ds_read_b128 %7, %9 offset:6144"
+        : "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11]), "=&v"(v[12]), "=&v"(v[13]), "=&v"(v[14]), "=&v"(v[15])
+        : "v"(bx[0]), "v"(bx[1])
         : "memory");
     asm volatile(
-        "ds_read_b32 %0, %8\n\tds_read_b32 %1, %9\n\tds_read_b32 %2, %10\n\t"
-        "ds_read_b32 %3, %11\n\tds_read_b32 %4, %12\n\tds_read_b32 %5, %13\n\t"
-        "ds_read_b32 %6, %14\n\tds_read_b32 %7, %15"
-        : "=&v"(wd[0]), "=&v"(wd[1]), "=&v"(wd[2]), "=&v"(wd[3]), "=&v"(wd[4]), "=&v"(wd[5]),
-          "=&v"(wd[6]), "=&v"(wd[7])
-        : "v"(aw[0]), "v"(aw[1]), "v"(aw[2]), "v"(aw[3]), "v"(aw[4]), "v"(aw[5]), "v"(aw[6]),
-          "v"(aw[7])
+        "ds_read_b32 %0, %8 offset:0\n\t"
+        "ds_read_b32 %1, %8 offset:256\n\t"
+        "ds_read_b32 %2, %8 offset:512\n\t"
+        "ds_read_b32 %3, %8 offset:768\n\t"
+        "ds_read_b32 %4, %8 offset:1024\n\t"
+        "ds_read_b32 %5, %8 offset:1280\n\t"
+        "ds_read_b32 %6, %8 offset:1536\n\t"
+        "ds_read_b32 %7, %8 offset:1792"
+        : "=&v"(wd[0]), "=&v"(wd[1]), "=&v"(wd[2]), "=&v"(wd[3]), "=&v"(wd[4]), "=&v"(wd[5]), "=&v"(wd[6]), "=&v"(wd[7])
+        : "v"(bw)
         : "memory");
     asm volatile(
-        "ds_read_u16 %0, %4\n\tds_read_u16 %1, %5\n\tds_read_u16 %2, %6\n\tds_read_u16 %3, %7"
+        "ds_read_u16 %0, %4 offset:0\n\t"
+        "ds_read_u16 %1, %4 offset:32\n\t"
+        "ds_read_u16 %2, %4 offset:64\n\t"
+        "ds_read_u16 %3, %4 offset:96"
         : "=&v"(sc[0]), "=&v"(sc[1]), "=&v"(sc[2]), "=&v"(sc[3])
-        : "v"(as[0]), "v"(as[1]), "v"(as[2]), "v"(as[3])
+        : "v"(bs)
         : "memory");
   };
   auto read_wait_q = [&](u32x4 (&v)[16], uint32_t (&wd)[8], uint32_t (&sc)[4]) {
@@ -315,6 +352,70 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
   for (int s = 0; s < NS; ++s) issue(cur, s, s);
   gp_wait_vmcnt<OPS * (NS - 1)>();
   gp_barrier();
+  // A step's operands: 16 fragments (w 0-7, x 8-15) and, GW_INT4, the raw words and scales
+  struct Ops {
+    u32x4 v[16];
+    uint32_t wd[8], sc[4];
+  };
+  auto rd_issue = [&](int st, Ops& o) {
+    if constexpr (WF == GW_INT4) read_issue_q(st, o.v, o.wd, o.sc);
+    else read_issue(st, o.v);
+  };
+  auto rd_wait = [&](Ops& o) {
+    if constexpr (WF == GW_INT4) {
+      read_wait_q(o.v, o.wd, o.sc);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const half_t sv = __builtin_bit_cast(half_t, (uint16_t)o.sc[i]);
+        const half2_t s2 = {sv, sv};
+#pragma unroll
+        for (int t = 0; t < 2; ++t) o.v[2 * i + t] = __builtin_bit_cast(u32x4, dequant8(o.wd[2 * i + t], s2));
+      }
+    } else {
+      read_wait(o.v);
+    }
+  };
+  auto mfmas = [&](const Ops& o, f32x4 (&acc)[4][4]) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const half8_t wf = __builtin_bit_cast(half8_t, o.v[2 * i + t]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const half8_t xf = __builtin_bit_cast(half8_t, o.v[8 + 2 * j + t]);
+          acc[i][j] = mfma16x16x32(wf, xf, acc[i][j]);
+        }
+      }
+  };
+  // One step: its operands (read into `now`) are complete; once step sidx + 1 has landed
+  // for this thread and then (barrier) for everyone - every wave has also finished reading
+  // this step's slot - the slot is refilled with step sidx + NS and the next step's operand
+  // reads go out into `later`, in flight while this step's MFMAs run.  Two register sets
+  // alternate over the steps: every K slice is an even number of steps, so the sets' roles
+  // are fixed at compile time within a two-step iteration, and the next tile's first step
+  // (read ahead during the last MFMAs of a tile) is always in set A.
+  auto step = [&](Ops& now, Ops& later, f32x4 (&acc)[4][4], int ks, int kc, int sidx, bool last) {
+    const int st = sidx % NS;
+    rd_wait(now);
+    if (last && has_bias) read_bias(st);
+    gp_wait_vmcnt<OPS * (NS - 2)>();
+    gp_barrier();
+    const int iks = ks + NS;
+    if (iks < kc) issue(cur, iks, st);
+    else issue(nxt, iks - kc, st);
+    rd_issue((sidx + 1) % NS, later);
+    // the MFMAs' operands pass through an (empty) volatile asm after the reads: volatile
+    // asm keeps its order, so the compiler cannot sink the reads below the MFMAs
+    asm volatile(""
+                 : "+v"(now.v[0]), "+v"(now.v[1]), "+v"(now.v[2]), "+v"(now.v[3]), "+v"(now.v[4]),
+                   "+v"(now.v[5]), "+v"(now.v[6]), "+v"(now.v[7]), "+v"(now.v[8]), "+v"(now.v[9]),
+                   "+v"(now.v[10]), "+v"(now.v[11]), "+v"(now.v[12]), "+v"(now.v[13]),
+                   "+v"(now.v[14]), "+v"(now.v[15]));
+    mfmas(now, acc);
+  };
+  Ops A, B;
+  rd_issue(0, A);
   int sidx = 0;
   for (int r = 0; r < my_items; ++r) {
     const int kc = cur.kc;
@@ -323,45 +424,9 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    for (int ks = 0; ks < kc; ++ks, ++sidx) {
-      const int st = sidx % NS;
-      u32x4 ops[16];
-      if constexpr (WF == GW_INT4) {
-        uint32_t wd[8], sc[4];
-        read_issue_q(st, ops, wd, sc);
-        read_wait_q(ops, wd, sc);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const half_t sv = __builtin_bit_cast(half_t, (uint16_t)sc[i]);
-          const half2_t s2 = {sv, sv};
-#pragma unroll
-          for (int t = 0; t < 2; ++t) ops[2 * i + t] = __builtin_bit_cast(u32x4, dequant8(wd[2 * i + t], s2));
-        }
-      } else {
-        read_issue(st, ops);
-        read_wait(ops);
-      }
-      if (ks == kc - 1 && has_bias) read_bias(st);
-      // step sidx + 1 has landed for this thread, then for everyone; every wave has also
-      // read step sidx's slot, which is refilled with step sidx + NS
-      gp_wait_vmcnt<OPS * (NS - 2)>();
-      gp_barrier();
-      {
-        const int iks = ks + NS;
-        if (iks < kc) issue(cur, iks, st);
-        else issue(nxt, iks - kc, st);
-      }
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const half8_t wf = __builtin_bit_cast(half8_t, ops[2 * i + t]);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const half8_t xf = __builtin_bit_cast(half8_t, ops[8 + 2 * j + t]);
-            acc[i][j] = mfma16x16x32(wf, xf, acc[i][j]);
-          }
-        }
+    for (int ks = 0; ks < kc; ks += 2, sidx += 2) {
+      step(A, B, acc, ks, kc, sidx, false);
+      step(B, A, acc, ks + 1, kc, sidx + 1, ks + 2 == kc);
     }
     // Epilogue: lane holds n = n0 + 64 wn + 16 i + 4 g4 + q of m = m0 + 64 wm + 16 j + l16.
 #pragma unroll
@@ -513,7 +578,7 @@ static int gp_tile_rows(int M, int N) {
 // at the vision tower's shapes: fc2 (80 tiles, 80 steps) 56 -> 31 us with 3 slices; fc1 at
 // 256-row tiles stays whole (2 slices would take two rounds).
 extern "C" int omni_f16_gemm_pipe_splits(int M, int N, int K, int tile_rows) {
-  if (M <= 0 || N <= 0 || K <= 0 || (N % GP_BN) || (K % GP_BKH)) return 1;
+  if (M <= 0 || N <= 0 || K <= 0 || (N % GP_BN) || (K % 128)) return 1;
   if (tile_rows == 0) tile_rows = gp_tile_rows(M, N);
   const int64_t cus = gp_num_cus();
   const int64_t tiles = (int64_t)ceil_div(M, tile_rows) * (N / GP_BN);
@@ -532,16 +597,16 @@ extern "C" int omni_f16_gemm_pipe_splits(int M, int N, int K, int tile_rows) {
 }
 
 // out = epi(fp16(x . w^T + bias)) with w fp16 [N, K] in nn.Linear layout (row stride K).
-// N % 128 == 0, K % 64 == 0 and K >= 256; x, w 16-byte aligned with ldx % 8 == 0;
+// N % 128 == 0, K % 128 == 0 and K >= 256; x, w 16-byte aligned with ldx % 8 == 0;
 // ldo, ldr % 4 == 0.  tile_rows 128 or 256 (0: chosen from the shape).  ksplit K slices
-// (0: omni_f16_gemm_pipe_splits; each slice >= 4 K steps of 64); ksplit > 1 needs an fp32
+// (0: omni_f16_gemm_pipe_splits; each slice >= 2 groups of 128); ksplit > 1 needs an fp32
 // workspace of ksplit * M * N floats (16-byte aligned).
 extern "C" int omni_f16_gemm_pipe(const void* x, int ldx, const void* w, const void* bias,
                                   const void* res, int ldr, void* out, int ldo, int M, int N,
                                   int K, int epilogue, int tile_rows, int ksplit,
                                   float* workspace, void* stream) {
   if (M < 0 || N <= 0 || K <= 0 || ksplit < 0) return OMNI_EINVAL;
-  if ((N % GP_BN) || (K % GP_BKH) || K < 4 * GP_BKH) return OMNI_EUNSUPPORTED;
+  if ((N % GP_BN) || (K % 128) || K < 4 * GP_BKH) return OMNI_EUNSUPPORTED;
   if (M == 0) return OMNI_OK;
   if (!x || !w || !out) return OMNI_EINVAL;
   if (ldx < K || (ldx & 7) || ldo < N || (ldo & 3)) return OMNI_EINVAL;
@@ -553,7 +618,7 @@ extern "C" int omni_f16_gemm_pipe(const void* x, int ldx, const void* w, const v
   if (tile_rows != 0 && tile_rows != 128 && tile_rows != 256) return OMNI_EINVAL;
   if (tile_rows == 0) tile_rows = gp_tile_rows(M, N);
   if (ksplit == 0) ksplit = omni_f16_gemm_pipe_splits(M, N, K, tile_rows);
-  if (K / GP_BKH / ksplit < 4) return OMNI_EUNSUPPORTED;       // every slice >= NS steps
+  if (2 * (K / 128 / ksplit) < 4) return OMNI_EUNSUPPORTED;    // every slice >= NS steps
   if (ksplit > 1 && (!workspace || ((uintptr_t)workspace & 15))) return OMNI_EINVAL;
   GemmPipeArgs a;
   a.x = (const half_t*)x;

@@ -12,7 +12,8 @@ an ``nn.Module`` with ``forward(x[..., K] fp16) -> [..., N] fp16`` installed by
 * ``LMHeadArgmax`` - tied lm_head + greedy argmax.
 
 All run omni_w4a16_gemm / omni_f16_gemm: the skinny weight-streaming kernel for up to
-64 activation rows (decode), the tiled MFMA GEMM beyond (prefill).  ``fuse_silu=True`` (the gate_up projection) interleaves the gate
+64 activation rows (decode), the pipelined MFMA GEMM beyond (prefill; GPTQ at 2048 rows and
+more unpacks its weights to fp16 first).  ``fuse_silu=True`` (the gate_up projection) interleaves the gate
 and up column tiles and emits silu(gate) * up directly: [.., 2I] -> [.., I].
 ``forward_partial`` writes fp32 split-K partial sums instead of fp16 output, for a
 consumer kernel (the next add+RMSNorm) that adds them in slice order.
@@ -83,6 +84,19 @@ def rtn_int4(weight: torch.Tensor, group_size: int = 128):
     qweight = (q << shifts).sum(1, dtype=torch.int64).to(torch.int64)
     qweight = torch.where(qweight >= 2 ** 31, qweight - 2 ** 32, qweight).to(torch.int32)
     return qweight.contiguous(), s.view(K // group_size, N).contiguous()
+
+
+_UNPACK: Dict[torch.device, torch.Tensor] = {}
+
+
+def _unpack_scratch(device: torch.device, halfs: int) -> torch.Tensor:
+    """The device's fp16 scratch for unpacked int4 weights (grown to the largest linear,
+    kept for the process; used by one linear at a time, in stream order)."""
+    buf = _UNPACK.get(device)
+    if buf is None or buf.numel() < halfs:
+        buf = torch.empty(halfs, device=device, dtype=torch.float16)
+        _UNPACK[device] = buf
+    return buf
 
 
 class _Skinny(nn.Module):
@@ -213,6 +227,32 @@ class GPTQLinear(_Skinny):
              ptr(self.scales_packed), ptr(self.bias), 1, ptr(out),
              0 if out is None else out.stride(0), ptr(partial), x2d.shape[0], self.N, self.K,
              epilogue, ksplit, preset, stream())
+
+    # From this many rows a prefill linear unpacks its int4 weights to fp16 once (into a
+    # scratch buffer shared by every linear on the device) and runs the fp16 pipelined GEMM
+    # on the same values: at M = 4096 the four linears of a 2B layer take 608 us with the
+    # dequantisation in the GEMM loop (redone by every wave that reads a tile) against 459 us
+    # in fp16 plus about 23 us of unpacking (MI355X).
+    UNPACK_ROWS = 2048
+
+    def forward_out(self, x2d: torch.Tensor, out: torch.Tensor, preset: int | None = None,
+                    ksplit: int | None = None):
+        M = x2d.shape[0]
+        if (M >= self.UNPACK_ROWS and ksplit is None and self.N % 128 == 0 and self.K >= 256
+                and x2d.data_ptr() % 16 == 0 and x2d.stride(0) % 8 == 0
+                and out.data_ptr() % 8 == 0 and out.stride(0) % 4 == 0):
+            w16 = _unpack_scratch(x2d.device, self.N * self.K)
+            call("omni_w4_unpack_f16", ptr(self.qweight_packed), ptr(self.scales_packed),
+                 ptr(w16), self.K, self.N, stream())
+            epi = EPI_SILU if self.fuse_silu else EPI_STORE
+            ks = 1 if self.fuse_silu else lib().omni_f16_gemm_pipe_splits(M, self.N, self.K, 0)
+            ws = (torch.empty(ks * M * self.N, device=x2d.device, dtype=torch.float32)
+                  if ks > 1 else None)
+            call("omni_packed_gemm_pipe", ptr(x2d), x2d.stride(0), ptr(w16), None, 1,
+                 ptr(self.bias), 1, ptr(out), out.stride(0), M, self.N, self.K, epi, 0, ks,
+                 ptr(ws), stream())
+            return out
+        return super().forward_out(x2d, out, preset, ksplit)
 
     def _call_attn(self, states, splits, n_kv, group, M, partial, epilogue, ksplit, preset):
         call("omni_w4a16_gemm_attn", ptr(states), splits, n_kv, group, ptr(self.qweight_packed),

@@ -143,7 +143,7 @@ def vit_attention_out(qkv: torch.Tensor, n_heads: int, head_dim: int, cu: torch.
 class VisionLinear:
     """fp16 nn.Linear (weight [N, K], optional bias [N]) on one of two GEMMs:
     ``pipe`` (omni_f16_gemm_pipe: weights in nn.Linear layout, a multi-stage LDS pipeline;
-    N % 128 == 0, K % 64 == 0, K >= 256 - every linear of the blocks and the merger) or
+    N % 128 == 0, K % 128 == 0, K >= 256 - every linear of the blocks and the merger) or
     ``tiled`` (omni_f16_gemm_tiled: weights packed with K zero-padded to whole 128-column
     groups - the patch embedding's K = 1176)."""
 
@@ -151,7 +151,7 @@ class VisionLinear:
                  path: str | None = None):
         N, K = weight.shape
         if path is None:
-            path = "pipe" if N % 128 == 0 and K % 64 == 0 and K >= 256 else "tiled"
+            path = "pipe" if N % 128 == 0 and K % 128 == 0 and K >= 256 else "tiled"
         if path not in ("pipe", "tiled"):
             raise ValueError(f"unknown GEMM path {path!r}")
         self.path = path

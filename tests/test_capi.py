@@ -146,4 +146,4 @@ def test_pipe_gemm_launch_choices(so):
     assert f(256, 5120, 5120, 0) == 3
     assert f(256, 1536, 5120, 0) == 4
     assert f(8192, 1280, 5120, 0) == 1
-    assert f(8192, 1280, 100, 0) == 1            # K % 64 != 0: never split
+    assert f(8192, 1280, 100, 0) == 1            # K % 128 != 0: never split

@@ -422,6 +422,48 @@ def test_packed_gemm_pipe(gpu, fmt, M, K, N, bias, silu):
         assert (sp_out.float() - e).abs().max().item() <= tol, (tr, ks)
 
 
+@pytest.mark.parametrize("K,N,bias,silu", [
+    (1536, 2048, True, False), (8960, 1536, False, False), (1536, 17920, False, True),
+])
+def test_gptq_prefill_unpacked(gpu, K, N, bias, silu):
+    """From GPTQLinear.UNPACK_ROWS rows the int4 weights are unpacked to packed fp16 and the
+    fp16 pipeline runs: omni_w4_unpack_f16 equals omni_f16_pack of the dequantised weight,
+    the output equals the int4 pipeline's at the same K split (same fp16 weights, same k
+    order), and it is within tolerance of the oracle."""
+    from omniserver_amd._lib import call, lib, ptr, stream
+    from omniserver_amd.linear import GPTQLinear
+    M = GPTQLinear.UNPACK_ROWS + 37
+    say(f"gptq prefill unpacked M={M} K={K} N={N} bias={bias} silu={silu}")
+    qw, sc = _gptq(K, N, 111 + K + N)
+    b = f16((N,), 112, 0.02) if bias else None
+    x = f16((M, K), 113)
+    lin = GPTQLinear(qw.to(gpu), sc.to(gpu), None if b is None else b.to(gpu), fuse_silu=silu)
+    unp = torch.empty(N * K, device=gpu, dtype=torch.float16)
+    call("omni_w4_unpack_f16", ptr(lin.qweight_packed), ptr(lin.scales_packed), ptr(unp), K, N,
+         stream())
+    ref_pack = torch.empty(N * K, device=gpu, dtype=torch.float16)
+    call("omni_f16_pack", ptr(lin.dequantized().t().contiguous()), ptr(ref_pack), K, N, 0, stream())
+    torch.cuda.synchronize()
+    assert torch.equal(unp.cpu(), ref_pack.cpu())
+    xg = x.to(gpu)
+    out = torch.empty(M, lin.out_features, device=gpu, dtype=torch.float16)
+    lin.forward_out(xg, out)
+    ks = 1 if silu else lib().omni_f16_gemm_pipe_splits(M, N, K, 0)
+    direct = torch.empty_like(out)
+    ws = torch.empty(ks * M * N, device=gpu, dtype=torch.float32)
+    call("omni_packed_gemm_pipe", ptr(xg), K, ptr(lin.qweight_packed), ptr(lin.scales_packed), 0,
+         ptr(lin.bias), 1, ptr(direct), lin.out_features, M, N, K, 1 if silu else 0, 0, ks,
+         ptr(ws) if ks > 1 else None, stream())
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), direct.cpu())
+    W = ref.gptq_dequant(qw, sc)
+    if silu:
+        e = ref.silu_mul(ref.linear(x.float(), W))
+    else:
+        e = ref.linear(x.float(), W, None if b is None else b.float(), bias_after_round=True)
+    assert (out.cpu().float() - e).abs().max().item() <= 2e-3 * max(1.0, e.abs().max().item())
+
+
 @pytest.mark.parametrize("M", [1, 16, 32])
 @pytest.mark.parametrize("K,N,bias,silu", [
     (1536, 2048, True, False), (8960, 1536, False, False), (1536, 17920, False, True),

@@ -9,7 +9,9 @@ reference's entry-point name and constructor signature.
 Decode (multimodal.py:286-357): sequences sorted by slot must occupy slots [0, n);
 one step advances each by one token.  With ``use_graph=True`` the whole step -
 embedding gather + 28 layers + final norm + lm_head/argmax + length advance - is one
-HIP-graph replay per batch size (captured lazily, static buffers kept alive).  The
+HIP-graph replay per batch size (captured lazily, static buffers kept alive; a batch with
+non-greedy rows replays a second graph that also writes the fp16 logits, from which the
+host samples, multimodal.py:306-313, 342-357).  The
 host does at most one small H2D (token ids, only when the batch composition
 changed) and one D2H (the new ids) per step.  While the batch can go on unchanged
 (nobody has finished, every row has room) the next step's replay is enqueued before the
@@ -112,6 +114,7 @@ class MultimodalRunner(ModelRunner):
         self._slot_seq: List[Sequence] = []
         self._kv_len: List[int] = []          # host mirror of pool.lengths for active slots
         self._graphs: Dict[int, tuple] = {}
+        self._graphs_sampled: Dict[int, tuple] = {}
         self._eager: Dict[int, dict] = {}
         self._dev_ids_for = None              # batch whose next ids already sit on device
         self._pinned_ids = torch.zeros(max_running + 1, dtype=torch.int64).pin_memory()
@@ -330,8 +333,11 @@ class MultimodalRunner(ModelRunner):
                 raise RuntimeError(f"sequence in slot {b} reached max_len={self._pool.max_len}")
         greedy = all(s.request.sampling.greedy for s in seqs)
         fused = self.adapter.model.fused_decode_ready()
-        if self._use_graph and greedy and fused:
-            self._decode_graph(seqs, n)
+        if self._use_graph and fused:
+            if greedy:
+                self._decode_graph(seqs, n)
+            else:
+                self._decode_graph_sampled(seqs, n)
         else:
             self.settle()
             with torch.inference_mode():
@@ -383,25 +389,45 @@ class MultimodalRunner(ModelRunner):
         logits = self.adapter.llm(emb, pos, None, view)[:, -1, :]
         self._emit(seqs, self._sample_rows(logits, seqs))
 
-    def _capture_graph(self, n):
+    def _capture_graph(self, n, sampled: bool = False):
+        """Capture the step for rows [0, n).  Greedy: the final launch advances lengths[:n]
+        and leaves the new ids in bufs["ids"] as the next step's input.  ``sampled``: the
+        step also writes the fp16 logits to bufs["logits"] (the host samples from them and
+        loads the next ids itself)."""
         model = self.adapter.model
         bufs = {"ids": torch.zeros(n, dtype=torch.int64, device=self.device),
                 "out": torch.zeros(n, dtype=torch.int64, device=self.device)}
+        if sampled:
+            bufs["logits"] = torch.empty(n, model.cfg.vocab_size, device=self.device,
+                                         dtype=torch.float16)
         view = self._pool.view(n, self._rope_delta)
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
             for _ in range(3):   # warm-up: writes K/V at the (not yet valid) next position only
-                model.decode_greedy(bufs["ids"], view, bufs["out"])
+                model.decode_greedy(bufs["ids"], view, bufs["out"], bufs.get("logits"))
         torch.cuda.current_stream().wait_stream(side)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            # the final launch advances lengths[:n] and leaves the new ids in bufs["ids"]
-            # as the next step's input
-            model.decode_greedy(bufs["ids"], view, bufs["out"], next_ids=bufs["ids"],
+            model.decode_greedy(bufs["ids"], view, bufs["out"], bufs.get("logits"),
+                                next_ids=None if sampled else bufs["ids"],
                                 lengths=self._pool.lengths)
         # the view and buffers are referenced by the graph: keep them alive with it
-        self._graphs[n] = (g, bufs, view)
+        (self._graphs_sampled if sampled else self._graphs)[n] = (g, bufs, view)
+
+    def _decode_graph_sampled(self, seqs, n):
+        """A batch with non-greedy rows in graph mode (multimodal.py:306-313, 342-357):
+        replay the step graph that also captures the logits, then sample every row from
+        them on the host side of the step (greedy rows take the argmax, as _sample_rows
+        does for the eager paths)."""
+        self.settle()
+        if n not in self._graphs_sampled:
+            self._capture_graph(n, sampled=True)
+        g, bufs, _view = self._graphs_sampled[n]
+        self._dev_ids_for = None               # the next ids come from the host
+        self._load_ids(seqs, n, bufs["ids"])
+        g.replay()
+        self._emit(seqs, self._sample_rows(bufs["logits"], seqs))
 
     def _launch(self, n: int) -> int:
         """Replay the step graph for rows [0, n) (inputs: bufs["ids"]) and start the new

@@ -156,6 +156,52 @@ def test_graph_equals_eager_with_compaction(gpu):
     assert [len(t) for t in streams[0]] == budgets
 
 
+def test_graph_sampling_equals_eager(gpu):
+    """A batch with temperature-sampled rows (and a greedy one) decodes in graph mode by
+    replaying the logits-capturing step graph and sampling on the host: with the same
+    random state before every step, the token streams equal the eager runner's (the same
+    kernels give the same logits); the greedy row equals its greedy-only stream."""
+    from omniserver_amd import synth
+    from omniserver_amd.request import Request, SamplingParams, Sequence, Status
+    from omniserver_amd.runner import NativeQwenVLRunner
+    say("graph sampling vs eager (gptq, 2 layers)")
+    shape = synth.DecoderShape()
+    w = synth.gptq_decoder(shape, seed=14, num_layers=2)
+    prompts = [synth.random_ids(L, shape.vocab_size, 14, f"t{L}").tolist() for L in (11, 25, 17)]
+    temps = [0.8, 0.0, 1.3]
+    budgets = [6, 8, 5]
+
+    def run(use_graph, temps):
+        r = NativeQwenVLRunner(max_running=4, max_len=128, use_graph=use_graph, weights=w,
+                               quant="gptq")
+        seqs = [Sequence(Request(prompt=p, sampling=SamplingParams(max_new_tokens=m,
+                                                                   temperature=t)))
+                for p, m, t in zip(prompts, budgets, temps)]
+        for s in seqs:
+            r.tokenize(s)
+        torch.manual_seed(999)
+        r.prefill(seqs)
+        running = [s for s in seqs if s.status != Status.FINISHED]
+        step = 0
+        while running:
+            torch.manual_seed(1000 + step)
+            r.decode(running)
+            step += 1
+            for s in list(running):
+                if s.status == Status.FINISHED:
+                    r.free(s)
+                    running.remove(s)
+        return r, [s.output_token_ids for s in seqs]
+
+    r_eager, eager = run(False, temps)
+    r_graph, graph = run(True, temps)
+    assert r_graph._graphs_sampled and not r_eager._graphs_sampled
+    assert graph == eager
+    assert [len(t) for t in graph] == budgets
+    _, greedy_only = run(True, [0.0, 0.0, 0.0])
+    assert graph[1] == greedy_only[1]
+
+
 def test_step_ahead_equals_eager(gpu):
     """The graph runner enqueues the next decode step before returning when the batch will
     decode again unchanged; a new prefill, a free or a different batch takes it back.  The

@@ -12,7 +12,7 @@
 * config 2: fp16 decoder, 28 layers, B = 16, contexts U[512, 2048] in a [17, 4096, 2, 128]
   pool: one decode step, checked as config 3.
 * config 5: 8 image + text prompts (64 text, 256 N(0,1) vision rows, 192 text) packed into
-  T = 4096 rows with 3-D M-RoPE positions, prefill (the tiled GEMMs at M = 4096 and the
+  T = 4096 rows with 3-D M-RoPE positions, prefill (the pipelined GEMMs at M = 4096 and the
   block-diagonal causal attention) then 8 greedy int4 decode steps at B = 8, on 2 layers
   so that the oracle's T = 4096 prefill takes seconds.
 

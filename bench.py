@@ -181,8 +181,9 @@ def pmc_probe(runner, seqs, B: int) -> None:
          the valid lengths only, which are not advanced);
       3. a plain 256 MiB device copy: the byte-counter calibration;
       4. BASELINE.json configs[3]'s four FP8 linears at M = 8192 (qkv, o, gate_up, down);
-      5. layer 0's four int4 linears at M = 4096 (config 5's packed prefill: the tiled
-         MFMA GEMM, qkv and down over their split-K finish launches).
+      5. layer 0's four int4 linears at M = 4096 (config 5's packed prefill: each unpacks
+         its weights to fp16, then the pipelined MFMA GEMM, with a split-K finish launch
+         where the tiles alone leave CUs idle).
     Prints no JSON line."""
     from omniserver_amd.linear import FP8Linear
     model = runner.adapter.model

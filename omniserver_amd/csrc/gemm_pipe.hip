@@ -572,9 +572,9 @@ static int gp_tile_rows(int M, int N) {
 }
 
 // K slices for (M, N, K) at the given tile height (0: chosen): the count (1-4, each slice
-// >= 8 K steps) that minimises rounds of the persistent grid x K steps per slice, with two
-// steps charged for the finish launch of a split (ties: fewer slices); none when the tiles
-// alone fill the grid.  Measured on MI355X
+// >= 8 K steps) that minimises rounds of the persistent grid x K steps per slice, with the
+// finish launch and the partial sums' traffic charged to a split (ties: fewer slices); none
+// when the tiles alone fill the grid.  Measured on MI355X
 // at the vision tower's shapes: fc2 (80 tiles, 80 steps) 56 -> 31 us with 3 slices; fc1 at
 // 256-row tiles stays whole (2 slices would take two rounds).
 extern "C" int omni_f16_gemm_pipe_splits(int M, int N, int K, int tile_rows) {
@@ -587,7 +587,11 @@ extern "C" int omni_f16_gemm_pipe_splits(int M, int N, int K, int tile_rows) {
   int64_t best_cost = ((tiles + cus - 1) / cus) * nk;
   if (tiles >= cus) return 1;        // the grid is full: slices would only add partial traffic
   for (int ks = 2; ks <= 4 && nk / ks >= 8; ++ks) {
-    const int64_t cost = ((tiles * ks + cus - 1) / cus) * ((nk + ks - 1) / ks) + 2;
+    // a split is charged two steps for its finish launch plus its fp32 partial traffic
+    // (ks M N floats written and read back: one step per 400 K elements, fitted to the
+    // 2B decoder's down projection at M = 4096, where 4 slices took 146 us against 140)
+    const int64_t cost = ((tiles * ks + cus - 1) / cus) * ((nk + ks - 1) / ks) + 2 +
+                         (int64_t)ks * M * N / 400000;
     if (cost < best_cost) {
       best = ks;
       best_cost = cost;

@@ -349,14 +349,94 @@ def _decode_line(quant, per_ms, replay_ms, ctx0, steps):
             "frac": round(nbytes / (per_ms / 1e3) / PEAK_HBM, 4)}
 
 
+def _prefill_ms(r, make_seqs, reps: int):
+    """Median wall time (ms) of ``reps`` prefills of make_seqs() on runner r, each into a
+    freshly freed pool after one warm-up prefill (first use of the prefill kernels);
+    returns (median ms, the last prefill's sequences)."""
+    seqs = make_seqs()
+    r.prefill(seqs)
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        for s_ in seqs:
+            r.free(s_)
+        seqs = make_seqs()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        r.prefill(seqs)
+        torch.cuda.synchronize()
+        ts.append((time.perf_counter() - t1) * 1e3)
+    return sorted(ts)[len(ts) // 2], seqs
+
+
+def _config1_runner(w16):
+    """configs[0]'s runner and prompt maker: fp16, batch 1, a 256-token prompt."""
+    from omniserver_amd import synth
+    from omniserver_amd.request import Request, SamplingParams, Sequence
+    from omniserver_amd.runner import NativeQwenVLRunner
+    shape = synth.DecoderShape()
+    r = NativeQwenVLRunner(max_running=1, max_len=1024, use_graph=True, weights=w16)
+    mk = lambda: [Sequence(Request(prompt=synth.random_ids(256, shape.vocab_size, 1, "c1").tolist(),
+                                   sampling=SamplingParams(max_new_tokens=1 << 30)))]
+    return r, mk
+
+
+def _config5_runner(device, w_int4, B: int = 8):
+    """configs[4]'s runner and prompt maker: int4, 8 x [63 text, <|vision_start|>, 256 vision
+    rows (grid 1 x 32 x 32), 192 text] packed into T = 4096 rows."""
+    from omniserver_amd import synth
+    from omniserver_amd.positions import IMAGE_TOKEN_ID, VISION_START_TOKEN_ID
+    from omniserver_amd.request import Request, SamplingParams, Sequence, VisionInput
+    from omniserver_amd.runner import NativeQwenVLRunner
+    shape = synth.DecoderShape()
+    r = NativeQwenVLRunner(max_running=B, max_len=4096, use_graph=True, quant="gptq", weights=w_int4)
+
+    def mk():
+        ss = []
+        for b in range(B):
+            ids = (synth.random_ids(63, shape.vocab_size, 5, f"c5a.{b}").tolist()
+                   + [VISION_START_TOKEN_ID] + [IMAGE_TOKEN_ID] * 256
+                   + synth.random_ids(192, shape.vocab_size, 5, f"c5b.{b}").tolist())
+            rows = synth.randn16((256, shape.hidden_size), 1.0, 5, f"c5v.{b}").to(device)
+            ss.append(Sequence(Request(prompt=ids, sampling=SamplingParams(max_new_tokens=1 << 30),
+                                       images=[VisionInput(rows, (1, 32, 32))])))
+        return ss
+    return r, mk
+
+
+def _prefill_flops(T: int, B: int, L: int) -> float:
+    """Dense FLOPs of a packed prefill of B segments of L tokens (T = B L): the four linears
+    per layer (2 T K N) and the causal attention (QK^T and PV over L (L + 1) / 2 pairs)."""
+    lin = sum(2.0 * T * K * N for K, N in LINEARS) * NL
+    att = NL * B * 4.0 * (L * (L + 1) / 2) * NH * HD
+    return lin + att
+
+
+def prefill_only(device) -> dict:
+    """configs[0]'s and configs[4]'s prefills alone (median of 5 / 3 after a warm-up), for
+    profiling the prefill path: ``python bench.py --prefill-only``."""
+    from omniserver_amd import synth
+    shape = synth.DecoderShape()
+    r, mk = _config1_runner(synth.fp16_decoder(shape, seed=1))
+    c1, _ = _prefill_ms(r, mk, 5)
+    del r
+    torch.cuda.empty_cache()
+    r, mk = _config5_runner(device, synth.gptq_decoder(shape, seed=0))
+    c5, _ = _prefill_ms(r, mk, 3)
+    fl = _prefill_flops(4096, 8, 512)
+    return {"metric": "prefill ms (BASELINE configs[0] and [4])", "config1_prefill_ms": round(c1, 3),
+            "config5_prefill_ms": round(c5, 3),
+            "config5_prefill_tflops": round(fl / (c5 * 1e-3) / 1e12, 1),
+            "config5_prefill_frac_fp16_peak": round(fl / (c5 * 1e-3) / PEAK_FP16, 4)}
+
+
 def baseline_configs(device, w_int4) -> dict:
     """BASELINE.json configs[0], [1] and [4] end to end with their own shapes (configs[2] is the
     headline line, configs[3] the fp8_gemm object): seeded synthetic weights, hipGraph
     decode, decode rates against the HBM peak, the packed prefill against the fp16 MFMA
     peak."""
     from omniserver_amd import synth
-    from omniserver_amd.positions import IMAGE_TOKEN_ID, VISION_START_TOKEN_ID
-    from omniserver_amd.request import Request, SamplingParams, Sequence, VisionInput
+    from omniserver_amd.request import Request, SamplingParams, Sequence
     from omniserver_amd.runner import NativeQwenVLRunner
     shape = synth.DecoderShape()
     mk = lambda ids, **kw: Sequence(Request(prompt=ids, sampling=SamplingParams(max_new_tokens=1 << 30), **kw))
@@ -365,17 +445,9 @@ def baseline_configs(device, w_int4) -> dict:
     w16 = synth.fp16_decoder(shape, seed=1)
     log(f"synthetic fp16 weights generated in {time.time() - t0:.1f}s")
 
-    # fp16, batch 1, 256-token prompt, 32 new tokens
-    r = NativeQwenVLRunner(max_running=1, max_len=1024, use_graph=True, weights=w16)
-    seqs = [mk(synth.random_ids(256, shape.vocab_size, 1, "c1").tolist())]
-    r.prefill(seqs)
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    r.free(seqs[0])
-    seqs = [mk(synth.random_ids(256, shape.vocab_size, 1, "c1").tolist())]
-    r.prefill(seqs)
-    torch.cuda.synchronize()
-    pre_ms = (time.perf_counter() - t1) * 1e3
+    # fp16, batch 1, 256-token prompt, 32 new tokens (prefill: median of 5)
+    r, mk1 = _config1_runner(w16)
+    pre_ms, seqs = _prefill_ms(r, mk1, 5)
     per, rep, ctx0 = _timed_decode(r, seqs, 32)
     out["config1"] = {"workload": "fp16 decoder, B=1, 256-token prompt, 32 greedy steps",
                       "prefill_ms": round(pre_ms, 3), **_decode_line("fp16", per, rep, ctx0, 32)}
@@ -402,39 +474,19 @@ def baseline_configs(device, w_int4) -> dict:
     torch.cuda.empty_cache()
 
     # int4, 8 x [64 text, 256 vision rows (grid 1 x 32 x 32), 192 text] packed
-    # prefill (T = 4096, block-diagonal causal), then 128 greedy steps at B = 8
+    # prefill (T = 4096, block-diagonal causal; median of 3), then 128 greedy steps at B = 8
     B = 8
-    r = NativeQwenVLRunner(max_running=B, max_len=4096, use_graph=True, quant="gptq", weights=w_int4)
-    def mm_seqs():
-        ss = []
-        for b in range(B):
-            # 63 text tokens + <|vision_start|>, 256 image rows at index 64, 192 text tokens
-            ids = (synth.random_ids(63, shape.vocab_size, 5, f"c5a.{b}").tolist()
-                   + [VISION_START_TOKEN_ID] + [IMAGE_TOKEN_ID] * 256
-                   + synth.random_ids(192, shape.vocab_size, 5, f"c5b.{b}").tolist())
-            rows = synth.randn16((256, shape.hidden_size), 1.0, 5, f"c5v.{b}").to(device)
-            ss.append(mk(ids, images=[VisionInput(rows, (1, 32, 32))]))
-        return ss
-    seqs = mm_seqs()
-    r.prefill(seqs)                        # warm-up (first use of the prefill kernels)
-    torch.cuda.synchronize()
-    for s_ in seqs:
-        r.free(s_)
-    seqs = mm_seqs()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    r.prefill(seqs)
-    torch.cuda.synchronize()
-    pre = time.perf_counter() - t1
+    r, mk5 = _config5_runner(device, w_int4, B)
+    pre_ms5, seqs = _prefill_ms(r, mk5, 3)
+    pre = pre_ms5 * 1e-3
     T = 512 * B
-    lin = sum(2.0 * T * K * N for K, N in LINEARS) * NL
-    att = NL * B * 4.0 * (512 * 513 / 2) * NH * HD
+    fl = _prefill_flops(T, B, 512)
     per, rep, ctx0 = _timed_decode(r, seqs, 128)
     out["config5"] = {"workload": "int4 decoder, 8 x 512-token image+text prompts: packed prefill "
                                   "(T = 4096), then 128 greedy steps at B = 8",
                       "prefill_ms": round(pre * 1e3, 3), "prefill_tok_per_s": round(T / pre, 1),
-                      "prefill_tflops": round((lin + att) / pre / 1e12, 1),
-                      "prefill_frac_fp16_peak": round((lin + att) / pre / PEAK_FP16, 4),
+                      "prefill_tflops": round(fl / pre / 1e12, 1),
+                      "prefill_frac_fp16_peak": round(fl / pre / PEAK_FP16, 4),
                       "prefill_gemm_mfma_busy_pct_counters": mfma_from_profiles("int4 prefill M=4096"),
                       **_decode_line("gptq", per, rep, ctx0, 128)}
     del r, seqs
@@ -538,6 +590,8 @@ def main():
     ap.add_argument("--no-b1", action="store_true", help="skip the B = 1 decode leg")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip BASELINE.json configs[0], [1], [4] (fp16 B=1 / B=16, multimodal)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="time only configs[0]'s and configs[4]'s prefills (one JSON object)")
     ap.add_argument("--vit-only", action="store_true",
                     help="time only the vision tower (one JSON object) and exit")
     ap.add_argument("--kernel-reps", type=int, default=20)
@@ -561,6 +615,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.vit_only:
         print(json.dumps(vit_tower(dev)), flush=True)
+        return
+    if args.prefill_only:
+        print(json.dumps(prefill_only(dev)), flush=True)
         return
 
     runner, seqs, w, shape = build_config3(dev, args.batch, args.ctx)

@@ -168,6 +168,16 @@ int omni_prefill_attention(const void* q, int q_stride, const void* k_cache, con
                            const int* qblocks, int nqb, void* out, int out_stride, int n_heads,
                            int n_kv_heads, int head_dim, float scale, void* stream);
 
+/* The same attention with query blocks of up to 32 tokens (qblocks counts <= 32): one
+ * workgroup per (block, KV head) loads each 32-key K/V tile once into LDS for all the
+ * group's query heads (n_heads / n_kv_heads <= 8); outputs equal omni_prefill_attention's
+ * bit for bit.  For long segments. */
+int omni_prefill_attention_gqa(const void* q, int q_stride, const void* k_cache,
+                               const void* v_cache, int pool_rows, int max_len,
+                               const int64_t* slots, const int64_t* kv_len, const int* qblocks,
+                               int nqb, void* out, int out_stride, int n_heads, int n_kv_heads,
+                               int head_dim, float scale, void* stream);
+
 /* ---------------------------------------------------------------- linears */
 
 /* Epilogues of the skinny GEMMs. */
@@ -232,7 +242,7 @@ int omni_w4_dequant(const int32_t* qweight_packed, const void* scales_packed, vo
 /* Packed int4 -> packed fp16 (omni_f16_pack's layout, tile order kept, so gate|up stays
  * interleaved), W = fp16((q - 8) * s) as the int4 kernels dequantise it: the GPTQ prefill
  * linears at many rows (kernels/marlin_linear.py:54-62) then run the fp16 GEMM on the same
- * values.  weight_packed 16-byte aligned, N * K halfs. */
+ * values.  qweight_packed and weight_packed 16-byte aligned; weight_packed holds N * K halfs. */
 int omni_w4_unpack_f16(const int32_t* qweight_packed, const void* scales_packed,
                        void* weight_packed, int K, int N, void* stream);
 

@@ -806,6 +806,197 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
   }
 }
 
+// The same attention for long segments: one workgroup (4 waves) per (block of up to 32
+// query tokens of one segment, KV head).  The block's keys go global -> registers -> LDS
+// one 32-key tile at a time (the next two tiles' loads in flight during the current tile's
+// MFMAs), and every wave reads them from LDS for its 16 query rows (wave & 1) and half of
+// the group's query heads (wave >> 1): each K/V byte crosses the L2 once per 32 queries and
+// G heads instead of once per 16 queries and head.  Per (query, head) the arithmetic is
+// prefill_attn_kernel's, tile for tile (a tile past a row's last key adds exactly nothing),
+// so the two kernels agree bit for bit.  K tiles are stored with their 16-byte chunks
+// XOR-swizzled by row (the A-operand reads of 16 rows then spread over the banks); V tiles
+// as the decode kernel stages them, for the transposed B-operand reads.
+template <int HPW>
+__global__ __launch_bounds__(256, 1) void prefill_attn_gqa_kernel(PrefillArgs a) {
+  __shared__ __attribute__((aligned(16))) half_t ks_lds[2][ATT_BLK * ATT_HD];
+  __shared__ __attribute__((aligned(16))) half_t vs_lds[2][ATT_BLK * ATT_VSTRIDE];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int q16 = lane >> 4;
+  const int c16 = lane & 15;
+  // longest blocks first: a segment's later blocks see more keys
+  const int item = (int)gridDim.x - 1 - (int)blockIdx.x;
+  const int qb = item / a.nkv;
+  const int g = item - qb * a.nkv;
+  const int t0 = a.qblocks[2 * qb];
+  const int n = a.qblocks[2 * qb + 1];
+  const int64_t slot = a.slots[t0];
+  if (slot < 0 || slot >= a.pool_rows || n <= 0) return;   // the whole workgroup
+  const int sub = wave & 1;                     // query rows 16 sub .. +15 of the block
+  const int h0 = (wave >> 1) * HPW;             // first of this wave's heads in the group
+  const bool rows_here = 16 * sub < n;
+  const int my_row = min(16 * sub + c16, n - 1);
+  const int lim = (int)clamp64(a.kv_len[t0 + my_row], 1, a.max_len);
+  const int end = (int)clamp64(a.kv_len[t0 + n - 1], 1, a.max_len);
+  const int ntiles = (end + ATT_BLK - 1) / ATT_BLK;
+
+  half8_t qf[HPW][4];
+#pragma unroll
+  for (int u = 0; u < HPW; ++u) {
+    const int h = g * a.G + min(h0 + u, a.G - 1);
+    const half_t* qp = a.q + (int64_t)(t0 + my_row) * a.q_stride + (int64_t)h * ATT_HD;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) qf[u][ks] = *(const half8_t*)(qp + ks * 32 + q16 * 8);
+  }
+  float m_run[HPW], l_run[HPW];
+  f32x4 o_acc[HPW][8];
+#pragma unroll
+  for (int u = 0; u < HPW; ++u) {
+    m_run[u] = -INFINITY;
+    l_run[u] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o_acc[u][i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  }
+
+  const int64_t row_base = slot * (int64_t)a.max_len;
+  const int64_t tok_stride = (int64_t)a.nkv * ATT_HD;
+  const half_t* kbase = a.k_cache + g * ATT_HD;
+  const half_t* vbase = a.v_cache + g * ATT_HD;
+  // thread tid moves 16-byte chunks c = tid and tid + 256 of the tile's K and of its V:
+  // row c / 16, chunk c % 16.  Two register sets hold the next two tiles' loads.
+  struct TileRegs {
+    half8_t k[2], v[2];
+  };
+  auto load_tile = [&](int tb, TileRegs& t) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int c = tid + 256 * u;
+      const int tok = min(tb + (c >> 4), end - 1);
+      const int64_t off = (row_base + tok) * tok_stride + (c & 15) * 8;
+      t.k[u] = *(const half8_t*)(kbase + off);
+      t.v[u] = *(const half8_t*)(vbase + off);
+    }
+  };
+  auto store_tile = [&](int buf, const TileRegs& t) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int c = tid + 256 * u;
+      const int r = c >> 4, ch = c & 15;
+      *(half8_t*)(&ks_lds[buf][r * ATT_HD + ((ch ^ (r & 15)) << 3)]) = t.k[u];
+      *(half8_t*)(&vs_lds[buf][r * ATT_VSTRIDE + ch * 8]) = t.v[u];
+    }
+  };
+  auto compute_tile = [&](int buf, int tb) {
+    if (rows_here) {
+      // K fragments (A operand of S^T = K Q^T): key 16 j + c16, dims 32 ks + 8 q16 .. +7
+      half8_t kc[2][4];
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+          kc[j][ks] = *(const half8_t*)(&ks_lds[buf][(16 * j + c16) * ATT_HD + (((4 * ks + q16) ^ c16) << 3)]);
+      half8_t vb[8];
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) vb[dt] = lds_read_b_tr16(&vs_lds[buf][dt * 16], ATT_VSTRIDE, q16, c16);
+#pragma unroll
+      for (int u = 0; u < HPW; ++u) {
+        if (h0 + u >= a.G) continue;
+        f32x4 sacc[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) acc = mfma16x16x32(kc[j][ks], qf[u][ks], acc);
+          sacc[j] = acc;
+        }
+        float sc[8];
+        float mblk = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int key = tb + 16 * j + 4 * q16 + i;
+            const float sv = key < lim ? sacc[j][i] * a.scale_log2 : -INFINITY;
+            sc[4 * j + i] = sv;
+            mblk = fmaxf(mblk, sv);
+          }
+        mblk = fmaxf(mblk, __shfl_xor(mblk, 16, 64));
+        mblk = fmaxf(mblk, __shfl_xor(mblk, 32, 64));
+        const float m_new = fmaxf(m_run[u], mblk);    // finite: key 0 is visible to every row
+        const float alpha = exp2f(m_run[u] - m_new);
+        m_run[u] = m_new;
+        half8_t pa;
+        float psum = 0.f;
+#pragma unroll
+        for (int s8 = 0; s8 < 8; ++s8) {
+          const float p = exp2f(sc[s8] - m_new);
+          psum += p;
+          pa[s8] = (half_t)p;
+        }
+        l_run[u] = l_run[u] * alpha + psum;
+        float al[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * q16 + i, 64);
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o_acc[u][dt][i] *= al[i];
+          o_acc[u][dt] = mfma16x16x32(pa, vb[dt], o_acc[u][dt]);
+        }
+      }
+    }
+  };
+
+  // Tile i sits in LDS buffer i % 2 while it is computed; during step i the registers hold
+  // tiles i + 1 (landed by now, stored into the other buffer after the step's MFMAs) and
+  // i + 2 (in flight), and the freed set takes tile i + 3's loads.  Steps go in pairs so
+  // that the two register sets keep fixed roles.
+  TileRegs ra, rb;
+  load_tile(0, ra);
+  store_tile(0, ra);
+  __syncthreads();
+  if (ntiles > 1) load_tile(ATT_BLK, rb);
+  if (ntiles > 2) load_tile(2 * ATT_BLK, ra);
+  for (int it = 0; it < ntiles; it += 2) {
+    compute_tile(0, it * ATT_BLK);
+    if (it + 1 < ntiles) {
+      store_tile(1, rb);                      // tile it + 1; buffer 1's last reader is done
+      if (it + 3 < ntiles) load_tile((it + 3) * ATT_BLK, rb);
+    }
+    lds_barrier();   // the stores are visible and every wave is done with this tile
+    if (it + 1 >= ntiles) break;
+    compute_tile(1, (it + 1) * ATT_BLK);
+    if (it + 2 < ntiles) {
+      store_tile(0, ra);                      // tile it + 2
+      if (it + 4 < ntiles) load_tile((it + 4) * ATT_BLK, ra);
+    }
+    lds_barrier();
+  }
+  if (!rows_here) return;
+#pragma unroll
+  for (int u = 0; u < HPW; ++u) {
+    if (h0 + u >= a.G) continue;
+    const int h = g * a.G + h0 + u;
+    float l = l_run[u];
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    float li[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) li[i] = __shfl(l, 4 * q16 + i, 64);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 16 * sub + 4 * q16 + i;
+      if (r < n) {
+        half_t* op = a.out + (int64_t)(t0 + r) * a.out_stride + (int64_t)h * ATT_HD;
+        const float inv = 1.0f / li[i];
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) op[dt * 16 + c16] = (half_t)(o_acc[u][dt][i] * inv);
+      }
+    }
+  }
+}
+
 // Causal varlen attention for packed query tokens over the pool.
 //   qblocks int32 [nqb][2]: (first token, count <= 16); the tokens of a block share
 //   slots[t] and have increasing kv_len.  out fp16 rows of out_stride elements.
@@ -841,6 +1032,50 @@ extern "C" int omni_prefill_attention(const void* q, int q_stride, const void* k
   const int64_t grid = (items + ATT_WAVES - 1) / ATT_WAVES;
   if (grid > 0x7fffffff) return OMNI_EUNSUPPORTED;
   hipLaunchKernelGGL(prefill_attn_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, a);
+  OMNI_CHECK_LAUNCH();
+  return OMNI_OK;
+}
+
+// The same attention with query blocks of up to 32 tokens (qblocks as above, count <= 32),
+// one workgroup per (block, KV head) sharing each K/V tile among the group's query heads
+// (prefill_attn_gqa_kernel; at most 8 query heads per KV head).  Outputs equal
+// omni_prefill_attention's bit for bit.
+extern "C" int omni_prefill_attention_gqa(const void* q, int q_stride, const void* k_cache,
+                                          const void* v_cache, int pool_rows, int max_len,
+                                          const int64_t* slots, const int64_t* kv_len,
+                                          const int* qblocks, int nqb, void* out, int out_stride,
+                                          int n_heads, int n_kv_heads, int head_dim, float scale,
+                                          void* stream) {
+  if (nqb < 0 || n_heads <= 0 || n_kv_heads <= 0 || pool_rows <= 0 || max_len <= 0) return OMNI_EINVAL;
+  if (head_dim != ATT_HD || n_heads % n_kv_heads || n_heads / n_kv_heads > 8) return OMNI_EUNSUPPORTED;
+  if (q_stride < n_heads * ATT_HD || (q_stride & 7) || out_stride < n_heads * ATT_HD) return OMNI_EINVAL;
+  if (nqb == 0) return OMNI_OK;
+  if (!q || !k_cache || !v_cache || !slots || !kv_len || !qblocks || !out) return OMNI_EINVAL;
+  PrefillArgs a;
+  a.q = (const half_t*)q;
+  a.q_stride = q_stride;
+  a.k_cache = (const half_t*)k_cache;
+  a.v_cache = (const half_t*)v_cache;
+  a.pool_rows = pool_rows;
+  a.max_len = max_len;
+  a.nkv = n_kv_heads;
+  a.G = n_heads / n_kv_heads;
+  a.nh = n_heads;
+  a.slots = slots;
+  a.kv_len = kv_len;
+  a.qblocks = qblocks;
+  a.nqb = nqb;
+  a.out = (half_t*)out;
+  a.out_stride = out_stride;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  const int64_t grid = (int64_t)nqb * n_kv_heads;
+  if (grid > 0x7fffffff) return OMNI_EUNSUPPORTED;
+  if (a.G <= 6)
+    hipLaunchKernelGGL((prefill_attn_gqa_kernel<3>), dim3((unsigned)grid), dim3(256), 0,
+                       (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL((prefill_attn_gqa_kernel<4>), dim3((unsigned)grid), dim3(256), 0,
+                       (hipStream_t)stream, a);
   OMNI_CHECK_LAUNCH();
   return OMNI_OK;
 }

@@ -1402,17 +1402,20 @@ __global__ void w4_dequant_kernel(const uint32_t* __restrict__ qp, const half_t*
 // interleave carries over): word j of (tile, group, lane) becomes the lane's 8 halfs of
 // 32-k block 4 group + j, fp16((q - 8) s) as every int4 kernel dequantises it.  For the
 // prefill linears at many rows, where the fp16 GEMM outruns the in-loop dequantisation.
-__global__ void w4_unpack_f16_kernel(const uint32_t* __restrict__ qp, const half_t* __restrict__ sp,
-                                     half_t* __restrict__ w, int K, int N) {
-  const int KG = K >> 7;
-  const int64_t total = (int64_t)(N >> 4) * KG * 256;
+__global__ __launch_bounds__(256) void w4_unpack_f16_kernel(const u32x4* __restrict__ qp,
+                                                            const half_t* __restrict__ sp,
+                                                            half8_t* __restrict__ w, int K, int N) {
+  // thread = (tile, group, lane): its 16 bytes of codes become 4 x 16 bytes, one in each of
+  // the group's four 32-k blocks (a wave reads 1 KB and writes four 1 KB runs)
+  const int64_t total = (int64_t)(N >> 4) * (K >> 7) * 64;
   for (int64_t idx = blockIdx.x * 256LL + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
-    const int j = (int)(idx & 3);
-    const int lane = (int)((idx >> 2) & 63);
-    const int64_t blk = idx >> 8;                 // nt * KG + kg
+    const int lane = (int)(idx & 63);
+    const int64_t blk = idx >> 6;                 // nt * KG + kg
+    const u32x4 q = __builtin_nontemporal_load(qp + idx);
     const half_t s = sp[blk * 16 + (lane & 15)];
     const half2_t s2 = {s, s};
-    *(half8_t*)(w + ((blk * 4 + j) * 64 + lane) * 8) = dequant8(qp[idx], s2);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[(blk * 4 + j) * 64 + lane] = dequant8(q[j], s2);
   }
 }
 
@@ -1420,14 +1423,15 @@ extern "C" int omni_w4_unpack_f16(const int32_t* qweight_packed, const void* sca
                                   void* weight_packed, int K, int N, void* stream) {
   if (K <= 0 || N <= 0) return OMNI_EINVAL;
   if ((K & 127) || (N & 15)) return OMNI_EUNSUPPORTED;
-  if (!qweight_packed || !scales_packed || !weight_packed || ((uintptr_t)weight_packed & 15))
+  if (!qweight_packed || !scales_packed || !weight_packed || ((uintptr_t)weight_packed & 15) ||
+      ((uintptr_t)qweight_packed & 15))
     return OMNI_EINVAL;
-  const int64_t total = (int64_t)(N >> 4) * (K >> 7) * 256;
+  const int64_t total = (int64_t)(N >> 4) * (K >> 7) * 64;
   int grid = (int)((total + 255) / 256);
   if (grid > 16384) grid = 16384;
   hipLaunchKernelGGL(w4_unpack_f16_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream,
-                     (const uint32_t*)qweight_packed, (const half_t*)scales_packed,
-                     (half_t*)weight_packed, K, N);
+                     (const u32x4*)qweight_packed, (const half_t*)scales_packed,
+                     (half8_t*)weight_packed, K, N);
   OMNI_CHECK_LAUNCH();
   return OMNI_OK;
 }

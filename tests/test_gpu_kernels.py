@@ -201,9 +201,12 @@ def test_decode_attention(gpu, lengths, waves, splits):
     assert d <= 4e-3, d
 
 
-@pytest.mark.parametrize("segs", [[1], [5, 16, 17], [256], [100, 37, 512]])
+@pytest.mark.parametrize("segs", [[1], [5, 16, 17], [256], [100, 37, 512], [33, 64, 511, 2]])
 def test_prefill_attention(gpu, segs):
-    from omniserver_amd.attention import query_blocks
+    """Both prefill attention kernels against the oracle, and equal to each other bit for bit
+    (query blocks of 16 / 32 tokens; the shared-tile kernel adds only fully masked tiles for
+    a block's first rows, which change nothing)."""
+    from omniserver_amd.attention import QBLOCK_GQA, query_blocks
     from omniserver_amd._lib import call, ptr, stream
     say(f"prefill_attention segs={segs}")
     nh, nkv, hd, ML = 12, 2, 128, 1024
@@ -229,10 +232,16 @@ def test_prefill_attention(gpu, segs):
     qg, kg, vg = q.to(gpu), kp.to(gpu), vp.to(gpu)
     call("omni_prefill_attention", ptr(qg), nh * hd, ptr(kg), ptr(vg), P, ML, ptr(slot_t),
          ptr(kvl), ptr(qb), qb.shape[0], ptr(out), nh * hd, nh, nkv, hd, hd ** -0.5, stream())
+    qb32 = query_blocks(segs, gpu, QBLOCK_GQA)
+    out32 = torch.full_like(out, float("nan"))
+    call("omni_prefill_attention_gqa", ptr(qg), nh * hd, ptr(kg), ptr(vg), P, ML, ptr(slot_t),
+         ptr(kvl), ptr(qb32), qb32.shape[0], ptr(out32), nh * hd, nh, nkv, hd, hd ** -0.5,
+         stream())
     torch.cuda.synchronize()
     e = ref.prefill_attention(q.float().view(T, nh, hd), k.float(), v.float(), segs, hd ** -0.5)
     d = (out.cpu().float() - e).abs().max().item()
     assert d <= 4e-3, d
+    assert torch.equal(out.cpu(), out32.cpu())
 
 
 # ----------------------------------------------------------------------------- linears

@@ -286,7 +286,9 @@ int omni_f16_gemm_pipe_splits(int M, int N, int K, int tile_rows);
  * ldo % 4 == 0, out 8-byte aligned.  tile_rows 128, 256 or 0 (from the shape); ksplit K
  * slices of whole 128-groups (0: omni_f16_gemm_pipe_splits; each slice >= 3 groups for
  * int4 at 128 rows, else >= 2), ksplit > 1 with fp32 workspace (ksplit * M * N floats,
- * 16-byte aligned) summed in order by a second launch. */
+ * 16-byte aligned) summed in order by a second launch.  OMNI_EPI_PARTIAL: the ksplit fp32
+ * slices [ksplit][M][N] only, into workspace (out and bias unused, NULL), for a consumer
+ * that sums them in order (omni_add_rmsnorm_partials, omni_mrope_kv_write_partials). */
 int omni_packed_gemm_pipe(const void* x, int ldx, const void* w_packed, const void* scales_packed,
                           int fmt, const void* bias, int bias_after_round, void* out, int ldo,
                           int M, int N, int K, int epilogue, int tile_rows, int ksplit,

@@ -34,7 +34,7 @@
 #define GP_ROWB 128      // LDS bytes per staged operand row (one step)
 #define GP_GM 4          // tile rows per group of the tile order
 
-enum { GP_STORE = 0, GP_SILU = 1, GP_QGELU = 4, GP_GELU = 5, GP_RESID = 6 };
+enum { GP_STORE = 0, GP_SILU = 1, GP_PARTIAL = 2, GP_QGELU = 4, GP_GELU = 5, GP_RESID = 6 };
 enum { GW_ROWS = 0, GW_F16 = 1, GW_INT4 = 2 };
 
 struct GemmPipeArgs {
@@ -433,7 +433,7 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
     for (int j = 0; j < 4; ++j) {
       const int m = m0c + 64 * wm + 16 * j + l16;
       if (m >= a.M) continue;
-      if (a.KS > 1) {                    // the slice's fp32 partial sums
+      if (a.KS > 1 || EPI == GP_PARTIAL) {   // the slice's fp32 partial sums
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int n = n0c + 64 * wn + 16 * i + 4 * g4;
@@ -530,6 +530,12 @@ static int gp_launch(const GemmPipeArgs& a, int epilogue, hipStream_t st) {
   if (items > 0x7fffffff) return OMNI_EUNSUPPORTED;
   const int grid = (int)(items < gp_num_cus() ? items : gp_num_cus());
   const dim3 blk(128 * WM);
+  if (epilogue == GP_PARTIAL) {      // the slices' partial sums only, for a consumer to add
+    if constexpr (WF == GW_ROWS) return OMNI_EINVAL;
+    else hipLaunchKernelGGL((gemm_pipe_kernel<WF, WM, NS, GP_PARTIAL>), dim3(grid), blk, 0, st, a);
+    OMNI_CHECK_LAUNCH();
+    return OMNI_OK;
+  }
   if (a.KS > 1) {                    // partial sums, then the finish kernel's epilogue
     if (epilogue == GP_SILU) return OMNI_EINVAL;
     hipLaunchKernelGGL((gemm_pipe_kernel<WF, WM, NS, GP_STORE>), dim3(grid), blk, 0, st, a);
@@ -660,13 +666,14 @@ extern "C" int omni_packed_gemm_pipe(const void* x, int ldx, const void* w_packe
   if (fmt != 0 && fmt != 1) return OMNI_EINVAL;
   if ((N % GP_BN) || (K % 128) || K < 4 * GP_BKH) return OMNI_EUNSUPPORTED;
   if (M == 0) return OMNI_OK;
-  if (!x || !w_packed || !out || (fmt == 0 && !scales_packed)) return OMNI_EINVAL;
-  if (epilogue != GP_STORE && epilogue != GP_SILU) return OMNI_EINVAL;
+  if (epilogue != GP_STORE && epilogue != GP_SILU && epilogue != GP_PARTIAL) return OMNI_EINVAL;
+  const bool part = epilogue == GP_PARTIAL;     // fp32 slices to workspace, no out, no bias
+  if (!x || !w_packed || (!part && !out) || (fmt == 0 && !scales_packed)) return OMNI_EINVAL;
   const int n_out = epilogue == GP_SILU ? N / 2 : N;
-  if (ldx < K || (ldx & 7) || ldo < n_out || (ldo & 3)) return OMNI_EINVAL;
+  if (ldx < K || (ldx & 7) || (!part && (ldo < n_out || (ldo & 3)))) return OMNI_EINVAL;
   if (((uintptr_t)x & 15) || ((uintptr_t)w_packed & 15) || ((uintptr_t)out & 7)) return OMNI_EINVAL;
   if (bias && ((uintptr_t)bias & 15)) return OMNI_EINVAL;
-  if (epilogue == GP_SILU && bias) return OMNI_EINVAL;
+  if ((epilogue == GP_SILU || part) && bias) return OMNI_EINVAL;
   if (tile_rows != 0 && tile_rows != 128 && tile_rows != 256) return OMNI_EINVAL;
   if (tile_rows == 0) tile_rows = gp_tile_rows(M, N);
   if (fmt == 0 && ((uintptr_t)scales_packed & 3)) return OMNI_EINVAL;
@@ -675,7 +682,7 @@ extern "C" int omni_packed_gemm_pipe(const void* x, int ldx, const void* w_packe
   // every slice covers at least NS pipeline steps (slices are whole 128-groups of 2 steps)
   const int ns = fmt == 0 ? (tile_rows == 256 ? 4 : 6) : (tile_rows == 256 ? 3 : 4);
   if (2 * (K / 128 / ksplit) < ns) return OMNI_EUNSUPPORTED;
-  if (ksplit > 1 && (!workspace || ((uintptr_t)workspace & 15))) return OMNI_EINVAL;
+  if ((ksplit > 1 || part) && (!workspace || ((uintptr_t)workspace & 15))) return OMNI_EINVAL;
   GemmPipeArgs a;
   a.x = (const half_t*)x;
   a.ldx = ldx;

@@ -349,9 +349,20 @@ class PackedPrefillWriter:
                              f"{None if self.seg is None else self.T}")
 
     def rope_and_write(self, qkv: torch.Tensor, layer_idx: int, positions: torch.Tensor,
-                       cos_tab, sin_tab, mrope_section) -> None:
+                       cos_tab, sin_tab, mrope_section, parts=None) -> None:
+        """M-RoPE on q/k (in place in the qkv rows) + K/V write of the packed tokens.
+        ``parts = (partials fp32 [S, T, qkv], S, bias, bias_after_round)``: the qkv rows are
+        first formed from the qkv projection's split-K partials (+ bias)."""
         pool = self.pool
         s0, s1, s2 = mrope_section
+        if parts is not None:
+            pbuf, S, bias, bar = parts
+            call("omni_mrope_kv_write_partials", ptr(qkv), qkv.stride(0), ptr(pbuf), S, ptr(bias),
+                 int(bar), ptr(positions), None, None, ptr(cos_tab), ptr(sin_tab),
+                 cos_tab.shape[0], ptr(pool.k[layer_idx]), ptr(pool.v[layer_idx]),
+                 ptr(self.token_slot), ptr(self.token_pos), pool.max_batch, pool.max_len, self.T,
+                 pool.n_heads, pool.n_kv_heads, pool.head_dim, s0, s1, s2, stream())
+            return
         call("omni_mrope_kv_write", ptr(qkv), qkv.stride(0), ptr(positions), None, None,
              ptr(cos_tab), ptr(sin_tab), cos_tab.shape[0], ptr(pool.k[layer_idx]),
              ptr(pool.v[layer_idx]), ptr(self.token_slot), ptr(self.token_pos), pool.max_batch,

@@ -148,12 +148,21 @@ class _Skinny(nn.Module):
 
     def forward_partial(self, x2d: torch.Tensor, partial: torch.Tensor,
                         ksplit: int | None = None, preset: int | None = None) -> int:
-        """fp32 split-K partial sums [S][M][N] (no bias) into partial; returns S."""
+        """fp32 split-K partial sums [S][M][N] (no bias) into partial; returns S.  More than
+        MAX_SKINNY_M rows run the pipelined GEMM's partial form (S = ksplit, default
+        tile_ksplit(M); N % 128 == 0)."""
         if self.fuse_silu:
             raise ValueError("the SiLU-fused projection has no partial form")
         M = x2d.shape[0]
         if M > MAX_SKINNY_M:
-            raise ValueError(f"partial sums support up to {MAX_SKINNY_M} rows")
+            # the slice count forward_out's split form uses, so that the sums agree with it
+            ks = lib().omni_gemm_slices(self.K, ksplit or self.tile_ksplit(M))
+            if partial.numel() < ks * M * self.N or partial.dtype != torch.float32:
+                raise ValueError("partial buffer too small or not fp32")
+            if self.N % 128 or x2d.stride(0) % 8:
+                raise ValueError("the prefill partial form takes N % 128 == 0, ldx % 8 == 0")
+            self._call_pipe_partial(x2d, partial, ks)
+            return ks
         ks = ksplit or self.partial_ksplit
         S = self.partial_slices(ks)
         if partial.numel() < S * M * self.N or partial.dtype != torch.float32:
@@ -182,6 +191,9 @@ class _Skinny(nn.Module):
         return S
 
     def _call_attn(self, states, splits, n_kv, group, M, partial, epilogue, ksplit, preset):
+        raise NotImplementedError
+
+    def _call_pipe_partial(self, x2d, partial, ksplit):
         raise NotImplementedError
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
@@ -254,6 +266,19 @@ class GPTQLinear(_Skinny):
             return out
         return super().forward_out(x2d, out, preset, ksplit)
 
+    def _call_pipe_partial(self, x2d, partial, ksplit):
+        M = x2d.shape[0]
+        if M >= self.UNPACK_ROWS:
+            w16 = _unpack_scratch(x2d.device, self.N * self.K)
+            call("omni_w4_unpack_f16", ptr(self.qweight_packed), ptr(self.scales_packed),
+                 ptr(w16), self.K, self.N, stream())
+            call("omni_packed_gemm_pipe", ptr(x2d), x2d.stride(0), ptr(w16), None, 1, None, 0,
+                 None, 0, M, self.N, self.K, EPI_PARTIAL, 0, ksplit, ptr(partial), stream())
+        else:
+            call("omni_packed_gemm_pipe", ptr(x2d), x2d.stride(0), ptr(self.qweight_packed),
+                 ptr(self.scales_packed), 0, None, 0, None, 0, M, self.N, self.K, EPI_PARTIAL, 0,
+                 ksplit, ptr(partial), stream())
+
     def _call_attn(self, states, splits, n_kv, group, M, partial, epilogue, ksplit, preset):
         call("omni_w4a16_gemm_attn", ptr(states), splits, n_kv, group, ptr(self.qweight_packed),
              ptr(self.scales_packed), ptr(self.bias), 1, None, 0, ptr(partial), M, self.N,
@@ -317,6 +342,11 @@ class F16Linear(_Skinny):
         call("omni_f16_gemm", ptr(x2d), x2d.stride(0), ptr(self.weight_packed), ptr(self.bias),
              ptr(out), 0 if out is None else out.stride(0), ptr(partial), x2d.shape[0], self.N,
              self.K, epilogue, ksplit, preset, stream())
+
+    def _call_pipe_partial(self, x2d, partial, ksplit):
+        call("omni_packed_gemm_pipe", ptr(x2d), x2d.stride(0), ptr(self.weight_packed), None, 1,
+             None, 0, None, 0, x2d.shape[0], self.N, self.K, EPI_PARTIAL, 0, ksplit, ptr(partial),
+             stream())
 
     def _call_attn(self, states, splits, n_kv, group, M, partial, epilogue, ksplit, preset):
         call("omni_f16_gemm_attn", ptr(states), splits, n_kv, group, ptr(self.weight_packed),

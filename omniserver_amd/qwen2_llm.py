@@ -140,6 +140,8 @@ class Qwen2LLM(nn.Module):
         self.register_buffer("rope_sin", sin)
         self.scale = cfg.head_dim ** -0.5
         self._bufs: Dict[int, dict] = {}
+        # prefill hands split-K partial sums to the next kernel where prefill_partials_ok
+        self.prefill_partials = True
 
     # ------------------------------------------------------------------ builders
     @classmethod
@@ -202,6 +204,8 @@ class Qwen2LLM(nn.Module):
             cache.bind(T)
         decode = not hasattr(cache, "token_slot")
         pos = None if decode else position_ids.reshape(3, T).to(torch.int64).contiguous()
+        if not decode and self.prefill_partials_ok(T):
+            return self._forward_partials(x, pos, cache, logits_indices, B)
         residual = None
         for i, layer in enumerate(self.layers):
             if residual is None:
@@ -226,6 +230,60 @@ class Qwen2LLM(nn.Module):
             idx = torch.as_tensor(logits_indices, device=x.device, dtype=torch.long)
             x, residual = x[idx].contiguous(), residual[idx].contiguous()
         h, _ = F.add_rms_norm(x, residual, self.norm, cfg.rms_norm_eps)
+        logits = self.lm_head.logits(h)
+        return logits.reshape(1 if logits_indices is not None else B, -1, cfg.vocab_size)
+
+    def prefill_partials_ok(self, T: int) -> bool:
+        """Whether forward runs a T-token prefill with qkv / o / down writing split-K
+        partial sums that the next kernel adds (the M-RoPE + KV write, the add+RMSNorms)
+        instead of finishing each projection in a launch of its own: the packed linears with
+        the SiLU-fused gate_up, more than 64 rows, and every such projection split at T."""
+        if not self.prefill_partials or T <= 64 or not self.fused_decode_ready():
+            return False
+        for layer in self.layers:
+            for lin in (layer.qkv_proj, layer.o_proj, layer.down_proj):
+                if lin.N % 128 or lin.tile_ksplit(T) < 2:
+                    return False
+        return True
+
+    def _forward_partials(self, x, pos, cache, logits_indices, B):
+        """forward's prefill with the projections' split-K partial sums handed to the next
+        kernel (prefill_partials_ok): the same roundings in the same order as the finished
+        projections, so the outputs are identical, with three launches per layer fewer."""
+        cfg = self.cfg
+        T, H = x.shape
+        eps = cfg.rms_norm_eps
+        dev = x.device
+        f32 = lambda n: torch.empty(n, device=dev, dtype=torch.float32)
+        l0 = self.layers[0]
+        qpart = f32(8 * T * l0.qkv_proj.N)
+        opart = f32(8 * T * l0.o_proj.N)
+        dpart = f32(8 * T * l0.down_proj.N)
+        residual = x.clone()
+        h = torch.empty(T, H, device=dev, dtype=torch.float16)
+        qkv = torch.empty(T, cfg.qkv_out, device=dev, dtype=torch.float16)
+        attn = torch.empty(T, cfg.num_heads, cfg.head_dim, device=dev, dtype=torch.float16)
+        act = torch.empty(T, cfg.intermediate_size, device=dev, dtype=torch.float16)
+        Sd = 0
+        for i, layer in enumerate(self.layers):
+            if i == 0:
+                h = layer.input_layernorm(x)
+            else:
+                F.add_rms_norm_partials_out(dpart, Sd, residual, layer.in_norm, eps, h, residual)
+            qp = layer.qkv_proj
+            Sq = qp.forward_partial(h, qpart)
+            cache.rope_and_write(qkv, i, pos, self.rope_cos, self.rope_sin, cfg.mrope_section,
+                                 parts=(qpart, Sq, qp.bias, qp.fmt == "int4"))
+            cache.attend_qkv(qkv, i, self.scale, attn)
+            So = layer.o_proj.forward_partial(attn.reshape(T, -1), opart)
+            F.add_rms_norm_partials_out(opart, So, residual, layer.post_norm, eps, h, residual)
+            layer.gate_up_proj.forward_out(h, act)
+            Sd = layer.down_proj.forward_partial(act, dpart)
+        cache.finish()
+        F.add_rms_norm_partials_out(dpart, Sd, residual, self.norm, eps, h, residual)
+        if logits_indices is not None:
+            idx = torch.as_tensor(logits_indices, device=dev, dtype=torch.long)
+            h = h[idx].contiguous()
         logits = self.lm_head.logits(h)
         return logits.reshape(1 if logits_indices is not None else B, -1, cfg.vocab_size)
 

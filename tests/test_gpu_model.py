@@ -156,6 +156,55 @@ def test_graph_equals_eager_with_compaction(gpu):
     assert [len(t) for t in streams[0]] == budgets
 
 
+@pytest.mark.parametrize("quant,segs", [(None, [256]), ("gptq", [100, 37, 100]), (None, [65]),
+                                        ("gptq", [100, 37, 200])])
+def test_prefill_partials_equal_finished(gpu, quant, segs):
+    """The packed prefill with qkv / o / down handing split-K partial sums to the next kernel
+    (prefill_partials_ok) gives the same logits and the same K/V pool rows, bit for bit, as
+    with every projection finished in its own launch - up to 256 tokens, where both routes
+    run the same add+RMSNorm kernel.  Past 256 rows the finished route's fp16 add+RMSNorm is
+    the many-row kernel, whose sum of squares adds in another order, so there the logits agree
+    within a few fp16 steps and layer 0's K/V rows (written before any such norm) exactly."""
+    from omniserver_amd import synth
+    from omniserver_amd.kv_cache import PreallocatedKVCache
+    from omniserver_amd.qwen2_llm import Qwen2LLM
+    say(f"prefill partials vs finished quant={quant} segs={segs}")
+    shape = synth.DecoderShape()
+    if quant == "gptq":
+        model = Qwen2LLM.from_gptq(synth.gptq_decoder(shape, seed=31, num_layers=3), shape, gpu,
+                                   max_pos=1024)
+    else:
+        model = Qwen2LLM.from_fp16(synth.fp16_decoder(shape, seed=31, num_layers=3), shape, gpu,
+                                   max_pos=1024)
+    T = sum(segs)
+    ids = synth.random_ids(T, shape.vocab_size, 31, "pp").to(gpu)
+    emb = model.embed_tokens(ids).unsqueeze(0)
+    pos = torch.cat([torch.arange(L) for L in segs]).view(1, 1, T).expand(3, 1, T).contiguous().to(gpu)
+    last = (torch.tensor(segs).cumsum(0) - 1).tolist()
+    outs = []
+    for flag in (False, True):
+        model.prefill_partials = flag
+        assert model.prefill_partials_ok(T) == (flag and T > 64)
+        pool = PreallocatedKVCache(n_layers=3, max_batch=len(segs) + 1,
+                                   n_kv_heads=shape.num_kv_heads, max_len=512,
+                                   head_dim=shape.head_dim, device=gpu, dtype=torch.float16,
+                                   n_heads=shape.num_heads)
+        cache = pool.packed_prefill_cache(list(range(len(segs))), segs)
+        logits = model(emb, pos, None, cache, logits_indices=last)
+        torch.cuda.synchronize()
+        outs.append((logits.cpu(), pool.storage.cpu(), pool.lengths.cpu()))
+    model.prefill_partials = True
+    assert torch.equal(outs[0][2], outs[1][2])
+    if T <= 256:
+        assert torch.equal(outs[0][0], outs[1][0])
+        assert torch.equal(outs[0][1], outs[1][1])
+    else:
+        d = (outs[0][0].float() - outs[1][0].float()).abs().max().item()
+        say(f"T={T}: logits max-abs difference {d:.2e}")
+        assert d <= 1e-2, d
+        assert torch.equal(outs[0][1][0], outs[1][1][0])
+
+
 def test_graph_sampling_equals_eager(gpu):
     """A batch with temperature-sampled rows (and a greedy one) decodes in graph mode by
     replaying the logits-capturing step graph and sampling on the host: with the same

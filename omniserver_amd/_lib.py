@@ -96,9 +96,15 @@ def lib() -> ctypes.CDLL:
     return _lib
 
 
+_FN: dict = {}
+
+
 def call(name: str, *args) -> None:
     """Invoke an entry point and raise on a non-zero return code."""
-    rc = getattr(lib(), name)(*args)
+    fn = _FN.get(name)
+    if fn is None:
+        fn = _FN[name] = getattr(lib(), name)
+    rc = fn(*args)
     if rc != 0:
         what = ERRORS.get(rc) or f"hipError_t {rc}"
         raise RuntimeError(f"{name} failed: {what}")
@@ -110,8 +116,9 @@ def ptr(t) -> int | None:
 
 
 def stream() -> int:
-    """Handle of torch's current HIP stream (captured streams included)."""
-    return torch.cuda.current_stream().cuda_stream
+    """Handle of torch's current HIP stream on the current device (captured streams
+    included), read without building a Stream object (a tenth of the host time)."""
+    return torch._C._cuda_getCurrentRawStream(torch._C._cuda_getDevice())
 
 
 def require_cuda(*tensors, dtype=None, contiguous=True) -> None:

@@ -155,8 +155,12 @@ class _Skinny(nn.Module):
             raise ValueError("the SiLU-fused projection has no partial form")
         M = x2d.shape[0]
         if M > MAX_SKINNY_M:
-            # the slice count forward_out's split form uses, so that the sums agree with it
-            ks = lib().omni_gemm_slices(self.K, ksplit or self.tile_ksplit(M))
+            # the slice count forward_out's split form uses (omni_gemm_slices: slices of
+            # whole 128-groups), so that the sums agree with it
+            KG = self.K // 128
+            ks = min(ksplit or self.tile_ksplit(M), KG)
+            kc = -(-KG // ks)
+            ks = -(-KG // kc)
             if partial.numel() < ks * M * self.N or partial.dtype != torch.float32:
                 raise ValueError("partial buffer too small or not fp32")
             if self.N % 128 or x2d.stride(0) % 8:

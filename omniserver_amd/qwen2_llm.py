@@ -240,11 +240,9 @@ class Qwen2LLM(nn.Module):
         the SiLU-fused gate_up, more than 64 rows, and every such projection split at T."""
         if not self.prefill_partials or T <= 64 or not self.fused_decode_ready():
             return False
-        for layer in self.layers:
-            for lin in (layer.qkv_proj, layer.o_proj, layer.down_proj):
-                if lin.N % 128 or lin.tile_ksplit(T) < 2:
-                    return False
-        return True
+        return all(lin.N % 128 == 0 and lin.tile_ksplit(T) >= 2
+                   for layer in self.layers
+                   for lin in (layer.qkv_proj, layer.o_proj, layer.down_proj))
 
     def _forward_partials(self, x, pos, cache, logits_indices, B):
         """forward's prefill with the projections' split-K partial sums handed to the next

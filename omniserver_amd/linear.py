@@ -244,38 +244,67 @@ class GPTQLinear(_Skinny):
              0 if out is None else out.stride(0), ptr(partial), x2d.shape[0], self.N, self.K,
              epilogue, ksplit, preset, stream())
 
-    # From this many rows a prefill linear unpacks its int4 weights to fp16 once (into a
-    # scratch buffer shared by every linear on the device) and runs the fp16 pipelined GEMM
-    # on the same values: at M = 4096 the four linears of a 2B layer take 608 us with the
-    # dequantisation in the GEMM loop (redone by every wave that reads a tile) against 459 us
-    # in fp16 plus about 23 us of unpacking (MI355X).
+    # Prefill linears run the fp16 pipelined GEMM on the fp16 values of their int4 weights
+    # (fp16((q - 8) s), the values the int4 kernels dequantise to, so the outputs are the
+    # same): at M = 4096 a 2B layer's four linears take 459 us in fp16 against 608 us with the
+    # dequantisation in the GEMM loop (redone by every wave that reads a tile), at M = 256
+    # 83 against 104 us (MI355X).  With keep_f16 the expansion (omni_w4_unpack_f16, K N fp16:
+    # 2.6 GB for the 2B decoder beside its 0.7 GB of int4, on a 288 GB part) is made at the
+    # first prefill of F16_ROWS rows or more and kept with the linear; decode (up to 64 rows)
+    # always streams the int4 words.  Without it, from UNPACK_ROWS rows the weights are
+    # unpacked into a per-device scratch on every call (~23 us per layer at 2B).  The copy is
+    # of the weights as they are at that first call: a linear whose packed weights are
+    # rewritten afterwards calls release_f16() first.
     UNPACK_ROWS = 2048
+    F16_ROWS = 256
+    keep_f16 = True
+
+    def release_f16(self) -> None:
+        """Drop the resident fp16 expansion (made again at the next large prefill)."""
+        self._w16 = None
+
+    def _prefill_f16(self, M: int) -> torch.Tensor | None:
+        """The packed fp16 weights the prefill GEMM runs on for M rows, or None (the int4
+        pipeline dequantises in its loop)."""
+        if self.N % 128 or self.K < 256:
+            return None
+        if self.keep_f16 and M >= self.F16_ROWS:
+            w16 = getattr(self, "_w16", None)
+            if w16 is None:
+                w16 = torch.empty(self.N * self.K, device=self.qweight_packed.device,
+                                  dtype=torch.float16)
+                call("omni_w4_unpack_f16", ptr(self.qweight_packed), ptr(self.scales_packed),
+                     ptr(w16), self.K, self.N, stream())
+                self._w16 = w16
+            return w16
+        if M >= self.UNPACK_ROWS:
+            w16 = _unpack_scratch(self.qweight_packed.device, self.N * self.K)
+            call("omni_w4_unpack_f16", ptr(self.qweight_packed), ptr(self.scales_packed),
+                 ptr(w16), self.K, self.N, stream())
+            return w16
+        return None
 
     def forward_out(self, x2d: torch.Tensor, out: torch.Tensor, preset: int | None = None,
                     ksplit: int | None = None):
         M = x2d.shape[0]
-        if (M >= self.UNPACK_ROWS and ksplit is None and self.N % 128 == 0 and self.K >= 256
-                and x2d.data_ptr() % 16 == 0 and x2d.stride(0) % 8 == 0
-                and out.data_ptr() % 8 == 0 and out.stride(0) % 4 == 0):
-            w16 = _unpack_scratch(x2d.device, self.N * self.K)
-            call("omni_w4_unpack_f16", ptr(self.qweight_packed), ptr(self.scales_packed),
-                 ptr(w16), self.K, self.N, stream())
-            epi = EPI_SILU if self.fuse_silu else EPI_STORE
-            ks = 1 if self.fuse_silu else lib().omni_f16_gemm_pipe_splits(M, self.N, self.K, 0)
-            ws = (torch.empty(ks * M * self.N, device=x2d.device, dtype=torch.float32)
-                  if ks > 1 else None)
-            call("omni_packed_gemm_pipe", ptr(x2d), x2d.stride(0), ptr(w16), None, 1,
-                 ptr(self.bias), 1, ptr(out), out.stride(0), M, self.N, self.K, epi, 0, ks,
-                 ptr(ws), stream())
-            return out
+        if (M > MAX_SKINNY_M and ksplit is None and x2d.data_ptr() % 16 == 0
+                and x2d.stride(0) % 8 == 0 and out.data_ptr() % 8 == 0 and out.stride(0) % 4 == 0):
+            w16 = self._prefill_f16(M)
+            if w16 is not None:
+                epi = EPI_SILU if self.fuse_silu else EPI_STORE
+                ks = 1 if self.fuse_silu else lib().omni_f16_gemm_pipe_splits(M, self.N, self.K, 0)
+                ws = (torch.empty(ks * M * self.N, device=x2d.device, dtype=torch.float32)
+                      if ks > 1 else None)
+                call("omni_packed_gemm_pipe", ptr(x2d), x2d.stride(0), ptr(w16), None, 1,
+                     ptr(self.bias), 1, ptr(out), out.stride(0), M, self.N, self.K, epi, 0, ks,
+                     ptr(ws), stream())
+                return out
         return super().forward_out(x2d, out, preset, ksplit)
 
     def _call_pipe_partial(self, x2d, partial, ksplit):
         M = x2d.shape[0]
-        if M >= self.UNPACK_ROWS:
-            w16 = _unpack_scratch(x2d.device, self.N * self.K)
-            call("omni_w4_unpack_f16", ptr(self.qweight_packed), ptr(self.scales_packed),
-                 ptr(w16), self.K, self.N, stream())
+        w16 = self._prefill_f16(M)
+        if w16 is not None:
             call("omni_packed_gemm_pipe", ptr(x2d), x2d.stride(0), ptr(w16), None, 1, None, 0,
                  None, 0, M, self.N, self.K, EPI_PARTIAL, 0, ksplit, ptr(partial), stream())
         else:

@@ -473,6 +473,58 @@ def test_gptq_prefill_unpacked(gpu, K, N, bias, silu):
     assert (out.cpu().float() - e).abs().max().item() <= 2e-3 * max(1.0, e.abs().max().item())
 
 
+@pytest.mark.parametrize("K,N,bias,silu", [(1536, 2048, True, False), (1536, 17920, False, True)])
+def test_gptq_prefill_resident_f16(gpu, K, N, bias, silu):
+    """From GPTQLinear.F16_ROWS rows a GPTQ linear runs on the fp16 expansion of its int4
+    weights, made at the first such call and kept: two calls (the second with fewer rows)
+    use one buffer and equal the int4 pipeline's outputs bit for bit (same fp16 values, same
+    k order), the partial-sum form equals the int4 partial form, and with keep_f16 off no
+    copy is made and the int4 pipeline runs."""
+    from omniserver_amd._lib import call, ptr, stream
+    from omniserver_amd.linear import EPI_PARTIAL, GPTQLinear
+    qw, sc = _gptq(K, N, 211 + K + N)
+    b = f16((N,), 212, 0.02) if bias else None
+    lin = GPTQLinear(qw.to(gpu), sc.to(gpu), None if b is None else b.to(gpu), fuse_silu=silu)
+
+    def int4_direct(xg, ks):
+        o = torch.empty(xg.shape[0], lin.out_features, device=gpu, dtype=torch.float16)
+        ws = torch.empty(max(1, ks) * xg.shape[0] * N, device=gpu, dtype=torch.float32)
+        call("omni_packed_gemm_pipe", ptr(xg), K, ptr(lin.qweight_packed), ptr(lin.scales_packed), 0,
+             ptr(lin.bias), 1, ptr(o), lin.out_features, xg.shape[0], N, K, 1 if silu else 0, 0, ks,
+             ptr(ws) if ks > 1 else None, stream())
+        return o
+
+    from omniserver_amd._lib import lib
+    bufs = []
+    for M in (GPTQLinear.F16_ROWS + 300, GPTQLinear.F16_ROWS + 7):
+        say(f"gptq resident fp16 M={M} K={K} N={N} bias={bias} silu={silu}")
+        xg = f16((M, K), 213 + M).to(gpu)
+        out = torch.empty(M, lin.out_features, device=gpu, dtype=torch.float16)
+        lin.forward_out(xg, out)
+        bufs.append(lin._w16.data_ptr())
+        ks = 1 if silu else lib().omni_f16_gemm_pipe_splits(M, N, K, 0)
+        direct = int4_direct(xg, ks)
+        torch.cuda.synchronize()
+        assert torch.equal(out.cpu(), direct.cpu()), M
+    assert bufs[0] == bufs[1]
+    if not silu:
+        M = GPTQLinear.F16_ROWS + 44
+        xg = f16((M, K), 214).to(gpu)
+        p16 = torch.empty(8 * M * N, device=gpu, dtype=torch.float32)
+        S = lin.forward_partial(xg, p16, ksplit=4)
+        p4 = torch.empty_like(p16)
+        call("omni_packed_gemm_pipe", ptr(xg), K, ptr(lin.qweight_packed), ptr(lin.scales_packed), 0,
+             None, 0, None, 0, M, N, K, EPI_PARTIAL, 0, S, ptr(p4), stream())
+        torch.cuda.synchronize()
+        assert torch.equal(p16[:S * M * N].cpu(), p4[:S * M * N].cpu())
+    lin.release_f16()
+    lin.keep_f16 = False
+    xg = f16((GPTQLinear.F16_ROWS + 5, K), 215).to(gpu)
+    out = torch.empty(xg.shape[0], lin.out_features, device=gpu, dtype=torch.float16)
+    lin.forward_out(xg, out)
+    assert lin._w16 is None
+
+
 @pytest.mark.parametrize("M", [1, 16, 32])
 @pytest.mark.parametrize("K,N,bias,silu", [
     (1536, 2048, True, False), (8960, 1536, False, False), (1536, 17920, False, True),

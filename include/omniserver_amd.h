@@ -219,6 +219,27 @@ int omni_f16_gemm_attn(const float* attn_states, int attn_splits, int n_kv_heads
                        float* partial, int M, int N, int K, int epilogue, int ksplit, int preset,
                        void* stream);
 
+/* DecoderLayer's add_rms_norm followed by the linear it feeds (model/qwen2_llm.py:145-157:
+ * input_layernorm -> qkv_proj, post_attention_layernorm -> gate_up_proj; the norm of
+ * kernels/fused_ops.py:60-70), for decode steps of a row or two: x = RMSNorm(h) * weight with
+ * h = fp16(fp16(sum of the fp32 split-K partials [nparts][M][K] in slice order) + residual),
+ * the previous projection's OMNI_EPI_PARTIAL output, formed by every workgroup in its input
+ * staging (x and h bit-identical to omni_add_rmsnorm_partials'), so that no norm launch sits
+ * between the two projections.  One workgroup writes h to residual_out, which must not
+ * alias residual.  M <= 16, K % 512 == 0, M * K / 8 <= the preset's threads (preset 1: 512;
+ * OMNI_EPI_SILU preset 1 or 4: 512 / 768); 16-byte aligned pointers.  The linear as
+ * omni_w4a16_gemm / omni_f16_gemm (OMNI_EPI_STORE, OMNI_EPI_SILU or OMNI_EPI_PARTIAL). */
+int omni_w4a16_gemm_addnorm(const float* partials, int nparts, const void* residual,
+                            const void* weight, float eps, void* residual_out,
+                            const void* qweight_packed, const void* scales_packed, const void* bias,
+                            int bias_after_round, void* out, int ldo, float* partial, int M, int N,
+                            int K, int epilogue, int ksplit, int preset, void* stream);
+int omni_f16_gemm_addnorm(const float* partials, int nparts, const void* residual,
+                          const void* weight, float eps, void* residual_out,
+                          const void* weight_packed, const void* bias, void* out, int ldo,
+                          float* partial, int M, int N, int K, int epilogue, int ksplit, int preset,
+                          void* stream);
+
 /* Number of K slices (whole 128-groups) a split of ksplit gives for K. */
 int omni_gemm_slices(int K, int ksplit);
 

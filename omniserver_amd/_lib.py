@@ -49,6 +49,10 @@ SIGNATURES = {
     "omni_w4a16_gemm_attn": [_P, _I, _I, _I, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I, _I,
                              _P],
     "omni_f16_gemm_attn": [_P, _I, _I, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I, _P],
+    "omni_w4a16_gemm_addnorm": [_P, _I, _P, _P, _F, _P, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I,
+                                _I, _I, _I, _P],
+    "omni_f16_gemm_addnorm": [_P, _I, _P, _P, _F, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I,
+                              _P],
     "omni_prefill_attention_gqa": [_P, _I, _P, _P, _I, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I,
                                    _F, _P],
     "omni_prefill_attention": [_P, _I, _P, _P, _I, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _F,

@@ -65,6 +65,16 @@ struct GemvArgs {
   int kx;
   const half_t* res;
   int ldr;
+  // x from an add+RMSNorm of the previous projection's split-K partials (XS == 2):
+  //   h[m, :] = fp16(fp16(sum of nparts fp32 slices [nnp][M][K], slice order) + nres[m, :]),
+  //   x[m, :] = fp16((h * rstd_m) * ngain), rstd_m = 1 / sqrt(sum(h^2) / K + neps),
+  // every workgroup forming its rows' statistics; logical block 0 writes h to nres_out.
+  const float* nparts;
+  int nnp;
+  const half_t* nres;
+  const half_t* ngain;
+  half_t* nres_out;
+  float neps;
 };
 
 template <int WF>
@@ -211,6 +221,15 @@ __global__ __launch_bounds__(CW * KW * 64, 1) void gemv_kernel(GemvArgs a) {
   half8_t xv[8];
   int xo[8];
   bool xlive[8];
+  // XS == 2: thread t holds chunk n_c of row n_r (t = n_r nch + n_c, whole waves per row);
+  // NB partial slices in flight per thread (8 where three waves share a SIMD's registers)
+  constexpr int NB = XS == 2 ? (NW > 8 ? 8 : 16) : 1;
+  const int n_nch = a.K >> 3;
+  const int n_r = XS == 2 ? (int)threadIdx.x / n_nch : 0;
+  const int n_c = XS == 2 ? (int)threadIdx.x - n_r * n_nch : 0;
+  const int n_rr = n_r < a.M ? n_r : 0;
+  float4 n_lo[NB], n_hi[NB];
+  half8_t n_rv, n_gv;
   const bool x_single = XS == 1 ? (xtotal <= NTH && a.aS <= 8) : true;
   Merge8Loads ml;
   int m_rec = a.KC;                             // XS: LDS offset of this thread's chunk
@@ -227,7 +246,19 @@ __global__ __launch_bounds__(CW * KW * 64, 1) void gemv_kernel(GemvArgs a) {
                                      head % a.aG) * ATT_REC;
       attn_merge8_issue(ml, rec0, (int64_t)a.aG * ATT_REC, 0, a.aS, k & 127);
     }
-  } else if (a.xl) {
+  } else if (XS == 2) {
+    // the rows' first NB partial slices, residual and gain, requested before the weights
+    // (loads retire in order: issued after them, the norm would wait for the whole stream)
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int p = u < a.nnp ? u : a.nnp - 1;
+      const float4* pp = (const float4*)(a.nparts + ((int64_t)p * a.M + n_rr) * a.K + n_c * 8);
+      n_lo[u] = pp[0];
+      n_hi[u] = pp[1];
+    }
+    n_rv = *(const half8_t*)(a.nres + (int64_t)n_rr * a.K + n_c * 8);
+    n_gv = *(const half8_t*)(a.ngain + n_c * 8);
+  } else if (XS == 0 && a.xl) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const bool ok = (int)threadIdx.x + u * NTH < xtotal;
@@ -257,7 +288,7 @@ __global__ __launch_bounds__(CW * KW * 64, 1) void gemv_kernel(GemvArgs a) {
 #pragma unroll
       for (int c = 0; c < CPW; ++c) ws[c].load(buf[p][c], min(p, gmax));
   };
-  if constexpr (!XF) issue_weights();
+  if constexpr (!XF || XS == 2) issue_weights();
 
   // 3. finish staging x[0:M, k0:k0+kc] in LDS (rows >= M zero)
   const half8_t zero8 = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
@@ -280,6 +311,58 @@ __global__ __launch_bounds__(CW * KW * 64, 1) void gemv_kernel(GemvArgs a) {
           }
           *(half8_t*)(xs + xr * xstride + xc * 8) = v;
           xstep();
+        }
+      }
+    } else if (XS == 2) {
+      // add+RMSNorm of the M rows, one 8-element chunk per thread (row r = t / nch, whole
+      // waves per row), in rownorm_kernel's order: the slices summed in order and rounded,
+      // the residual added and rounded, the squares summed per chunk, per wave, then over
+      // the row's waves in order.  The weights are already in flight: the sums wait for
+      // them (loads retire in order), which is at most one round trip.
+#pragma clang fp contract(off)
+      __shared__ float nws[16];
+      const int nch = n_nch;                    // multiple of 64 (host check)
+      const int r = n_r;
+      const int c = n_c;
+      const bool live = r < a.M;                // M nch <= threads (host check)
+      const int rr = n_rr;
+      float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int u = 0; u < NB; ++u) {            // slices 0 .. NB-1 (a slot past nnp adds +0)
+        const bool on = u < a.nnp;
+        sum[0] += on ? n_lo[u].x : 0.f; sum[1] += on ? n_lo[u].y : 0.f;
+        sum[2] += on ? n_lo[u].z : 0.f; sum[3] += on ? n_lo[u].w : 0.f;
+        sum[4] += on ? n_hi[u].x : 0.f; sum[5] += on ? n_hi[u].y : 0.f;
+        sum[6] += on ? n_hi[u].z : 0.f; sum[7] += on ? n_hi[u].w : 0.f;
+      }
+      if (a.nnp > NB)                           // the rest, in order (behind the weights)
+        sum_slices8<NB>(a.nparts + ((int64_t)NB * a.M + rr) * a.K + c * 8, (int64_t)a.M * a.K,
+                        a.nnp - NB, sum);
+      const half8_t rv = n_rv;
+      const half8_t gv = n_gv;
+      half8_t v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (half_t)sum[e];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (half_t)((float)v[e] + (float)rv[e]);
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += (float)v[e] * (float)v[e];
+      ss = wave_sum(ss);
+      if ((threadIdx.x & 63) == 0) nws[threadIdx.x >> 6] = ss;
+      lds_barrier();
+      const int w0 = (rr * nch) >> 6;
+      float tot = 0.f;
+      for (int i = 0; i < (nch >> 6); ++i) tot += nws[w0 + i];
+      const float rstd = 1.0f / sqrtf(tot / (float)a.K + a.neps);
+      if (live) {
+        if (blk == 0) *(half8_t*)(a.nres_out + (int64_t)r * a.K + c * 8) = v;
+        const int kk = c * 8 - k0;
+        if (kk >= 0 && kk < kc) {
+          half8_t o;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[e] = (half_t)(((float)v[e] * rstd) * (float)gv[e]);
+          *(half8_t*)(xs + r * xstride + kk) = o;
         }
       }
     } else if (a.xl) {
@@ -305,7 +388,7 @@ __global__ __launch_bounds__(CW * KW * 64, 1) void gemv_kernel(GemvArgs a) {
       }
     }
   };
-  if constexpr (XF) {
+  if constexpr (XF && XS != 2) {
     stage_x();
     __syncthreads();
     issue_weights();
@@ -371,7 +454,7 @@ __global__ __launch_bounds__(CW * KW * 64, 1) void gemv_kernel(GemvArgs a) {
     }
   };
   if (active) {
-    if (XS == 1 || a.xl) stream_weights(std::true_type{});
+    if (XS != 0 || a.xl) stream_weights(std::true_type{});
     else stream_weights(std::false_type{});
   }
 
@@ -505,7 +588,8 @@ static int launch_gemv(GemvArgs a, hipStream_t st) {
   const size_t xbytes = (size_t)MB * 16 * (a.KC + 8) * sizeof(half_t);
   const size_t rbytes = (size_t)(KW > 1 ? KW - 1 : 0) * CW * CPW * MB * 256 * sizeof(float);
   a.xl = xbytes <= lim;                         // else A fragments come from global/L2
-  if (XS == 1 && !a.xl) return OMNI_EUNSUPPORTED;   // merged input is staged in LDS only
+  if (XS != 0 && !a.xl) return OMNI_EUNSUPPORTED;   // merged / normalised input: LDS only
+  if (XS == 2 && a.M * (a.K >> 3) > CW * KW * 64) return OMNI_EUNSUPPORTED;   // a chunk a thread
   const size_t lds = a.xl ? (xbytes > rbytes ? xbytes : rbytes) : rbytes;
   if (lds > lim) return OMNI_EUNSUPPORTED;
   static bool attr_set = false;
@@ -540,7 +624,17 @@ static int dispatch_preset(const GemvArgs& a, int preset, hipStream_t st) {
   // Presets whose register demand at 64 rows exceeds a wave's share (8-wave K splits of
   // two tiles per wave, and every form with the merged attention input but preset 1) are
   // not built: they spilled without being faster at the shapes they were swept on.
-  if constexpr (EPI == EPI_SILU) {
+  if constexpr (XS == 2) {        // add+RMSNorm input: one row block, the decode plans' shapes
+    if constexpr (EPI == EPI_SILU) {
+      switch (preset) {
+        case 1: return launch_gemv<WF, 1, EPI, 2, 8, 1, PF, 2, 0>(a, st);
+        case 4: return launch_gemv<WF, 1, EPI, 2, 3, 4, PF, 2, 0>(a, st);
+        default: return OMNI_EINVAL;
+      }
+    } else {
+      return preset == 1 ? launch_gemv<WF, 1, EPI, 1, 8, 1, PF, 2, 0>(a, st) : OMNI_EINVAL;
+    }
+  } else if constexpr (EPI == EPI_SILU) {
     switch (preset) {
       case 1: return dispatch_mb<WF, EPI, 2, 8, 1, PF>(a, st);
       case 2: return dispatch_mb<WF, EPI, 2, 4, 2, PF>(a, st);
@@ -777,19 +871,37 @@ struct AttnIn {            // x from split decode-attention states (omni_*_gemm_
   int S, nkv, G;
 };
 
+struct NormIn {            // x from an add+RMSNorm of split-K partials (omni_*_gemm_addnorm)
+  const float* parts;
+  int nparts;
+  const void* res;
+  const void* gain;
+  float eps;
+  void* res_out;
+};
+
 static int gemv_common(int wf, const void* x, int ldx, const void* w, const void* scales,
                        const void* bias, int bias_after_round, void* out, int ldo,
                        float* partial, int M, int N, int K, int epilogue, int ksplit, int preset,
-                       void* stream, const AttnIn* ain = nullptr) {
+                       void* stream, const AttnIn* ain = nullptr, const NormIn* nin = nullptr) {
   if (M <= 0 || N <= 0 || K <= 0) return M == 0 ? OMNI_OK : OMNI_EINVAL;
   if (M > 64 && (ain || epilogue == EPI_PARTIAL)) return OMNI_EUNSUPPORTED;
+  if (nin) {
+    if (M > 16 || (K & 511)) return OMNI_EUNSUPPORTED;   // one row block; whole waves per row
+    if (!nin->parts || nin->nparts < 1 || nin->nparts > 64 || !nin->res || !nin->gain ||
+        !nin->res_out || ((uintptr_t)nin->parts & 15) || ((uintptr_t)nin->res & 15) ||
+        ((uintptr_t)nin->gain & 15) || ((uintptr_t)nin->res_out & 15))
+      return OMNI_EINVAL;
+    if (nin->res_out == nin->res) return OMNI_EINVAL;      // read by every workgroup
+    if (epilogue != EPI_SILU && epilogue != EPI_PARTIAL && epilogue != EPI_STORE) return OMNI_EINVAL;
+  }
   if ((N & 15) || (K & 127)) return OMNI_EUNSUPPORTED;
   if (!w || (wf == W_INT4 && !scales)) return OMNI_EINVAL;
   if (ain) {
     if (!ain->part || ain->S < 1 || ain->S > 64 || ain->nkv < 1 || ain->G < 1) return OMNI_EINVAL;
     if (K != ain->nkv * ain->G * 128) return OMNI_EINVAL;
     if (epilogue == EPI_SILU) return OMNI_EINVAL;
-  } else {
+  } else if (!nin) {
     if (!x) return OMNI_EINVAL;
     if (ldx < K || (ldx & 7)) return OMNI_EINVAL;
   }
@@ -848,6 +960,26 @@ static int gemv_common(int wf, const void* x, int ldx, const void* w, const void
                                   : launch_gemm_tile<W_INT4, EPI_STORE>(a, st);
     return epilogue == EPI_SILU ? launch_gemm_tile<W_FP16, EPI_SILU>(a, st)
                                 : launch_gemm_tile<W_FP16, EPI_STORE>(a, st);
+  }
+  if (nin) {
+    a.nparts = nin->parts;
+    a.nnp = nin->nparts;
+    a.nres = (const half_t*)nin->res;
+    a.ngain = (const half_t*)nin->gain;
+    a.nres_out = (half_t*)nin->res_out;
+    a.neps = nin->eps;
+    if (wf == W_INT4) {
+      switch (epilogue) {
+        case EPI_SILU: return dispatch_preset<W_INT4, EPI_SILU, 2>(a, preset, st);
+        case EPI_PARTIAL: return dispatch_preset<W_INT4, EPI_PARTIAL, 2>(a, preset, st);
+        default: return dispatch_preset<W_INT4, EPI_STORE, 2>(a, preset, st);
+      }
+    }
+    switch (epilogue) {
+      case EPI_SILU: return dispatch_preset<W_FP16, EPI_SILU, 2>(a, preset, st);
+      case EPI_PARTIAL: return dispatch_preset<W_FP16, EPI_PARTIAL, 2>(a, preset, st);
+      default: return dispatch_preset<W_FP16, EPI_STORE, 2>(a, preset, st);
+    }
   }
   if (ain) {
     a.apart = ain->part;
@@ -916,6 +1048,36 @@ extern "C" int omni_f16_gemm(const void* x, int ldx, const void* weight_packed, 
                              int ksplit, int preset, void* stream) {
   return gemv_common(W_FP16, x, ldx, weight_packed, nullptr, bias, 0, out, ldo, partial, M, N, K,
                      epilogue, ksplit, preset, stream);
+}
+
+// add_rms_norm followed by the linear it feeds (model/qwen2_llm.py:145-157: input_layernorm
+// -> qkv_proj, post_attention_layernorm -> gate_up_proj; kernels/fused_ops.py:60-70), for one
+// row block (M <= 16, K % 512 == 0, M K / 8 <= the preset's threads): the norm's input is the
+// previous projection's fp32 split-K partials [nparts][M][K] (omni_w4a16_gemm's
+// OMNI_EPI_PARTIAL, summed in slice order), the residual and gain as omni_add_rmsnorm_partials
+// takes them.  Every workgroup forms the rows' statistics; one writes the new residual to
+// residual_out, which must not alias residual (every workgroup reads it).  The linear's
+// output, epilogue (OMNI_EPI_STORE / OMNI_EPI_SILU / OMNI_EPI_PARTIAL), ksplit and preset (1;
+// SiLU 1 or 4) as omni_w4a16_gemm.  x and y are identical to omni_add_rmsnorm_partials'.
+extern "C" int omni_w4a16_gemm_addnorm(const float* partials, int nparts, const void* residual,
+                                       const void* weight, float eps, void* residual_out,
+                                       const void* qweight_packed, const void* scales_packed,
+                                       const void* bias, int bias_after_round, void* out, int ldo,
+                                       float* partial, int M, int N, int K, int epilogue,
+                                       int ksplit, int preset, void* stream) {
+  const NormIn nin = {partials, nparts, residual, weight, eps, residual_out};
+  return gemv_common(W_INT4, nullptr, 0, qweight_packed, scales_packed, bias, bias_after_round, out,
+                     ldo, partial, M, N, K, epilogue, ksplit, preset, stream, nullptr, &nin);
+}
+
+extern "C" int omni_f16_gemm_addnorm(const float* partials, int nparts, const void* residual,
+                                     const void* weight, float eps, void* residual_out,
+                                     const void* weight_packed, const void* bias, void* out,
+                                     int ldo, float* partial, int M, int N, int K, int epilogue,
+                                     int ksplit, int preset, void* stream) {
+  const NormIn nin = {partials, nparts, residual, weight, eps, residual_out};
+  return gemv_common(W_FP16, nullptr, 0, weight_packed, nullptr, bias, 0, out, ldo, partial, M, N,
+                     K, epilogue, ksplit, preset, stream, nullptr, &nin);
 }
 
 // Tiled fp16 GEMM at any M for the vision tower's linears (model/qwen2_vit.py:41-44, 83,

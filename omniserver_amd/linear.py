@@ -197,6 +197,44 @@ class _Skinny(nn.Module):
     def _call_attn(self, states, splits, n_kv, group, M, partial, epilogue, ksplit, preset):
         raise NotImplementedError
 
+    # workgroup shape of the add+RMSNorm-input form for a SiLU store preset (the same shape;
+    # staging the norm first is part of that form)
+    _ADDNORM_SILU_PRESET = {1: 1, 4: 4, 6: 4, 9: 1}
+
+    def forward_addnorm(self, parts: torch.Tensor, nparts: int, residual: torch.Tensor,
+                        gain: torch.Tensor, eps: float, residual_out: torch.Tensor,
+                        out: torch.Tensor | None = None,
+                        partial: torch.Tensor | None = None) -> int:
+        """This linear on add_rms_norm's output (fused_ops.py:60-70) whose input x is the fp16
+        sum of the fp32 split-K partials parts[:nparts] ([nparts][M][K], slice order): every
+        workgroup forms the M rows' norm itself, so no add+RMSNorm launch runs between the
+        producer and this linear, and residual_out (not residual) receives the new residual.
+        One row block whose rows fit the workgroup (M (K / 8) <= its threads: M <= 2 for the 2B
+        decoder's qkv).  SiLU-fused: out [M, N/2], returns 1; else the fp32 split-K partial
+        sums into partial (as forward_partial), returns their count."""
+        M = residual.shape[0]
+        if residual_out.data_ptr() == residual.data_ptr():
+            raise ValueError("residual_out must not alias residual (every workgroup reads it)")
+        if parts.dtype != torch.float32 or parts.numel() < nparts * M * self.K:
+            raise ValueError("partials too small or not fp32")
+        if self.fuse_silu:
+            if out is None:
+                raise ValueError("the SiLU-fused form needs out")
+            preset = self._ADDNORM_SILU_PRESET.get(self.store_preset, 4)
+            self._call_addnorm(parts, nparts, residual, gain, eps, residual_out, out, None,
+                               EPI_SILU, 1, preset)
+            return 1
+        S = self.partial_slices(self.partial_ksplit)
+        if partial is None or partial.numel() < S * M * self.N or partial.dtype != torch.float32:
+            raise ValueError("partial buffer too small or not fp32")
+        self._call_addnorm(parts, nparts, residual, gain, eps, residual_out, None, partial,
+                           EPI_PARTIAL, self.partial_ksplit, 1)
+        return S
+
+    def _call_addnorm(self, parts, nparts, residual, gain, eps, residual_out, out, partial,
+                      epilogue, ksplit, preset):
+        raise NotImplementedError
+
     def _call_pipe_partial(self, x2d, partial, ksplit):
         raise NotImplementedError
 
@@ -312,6 +350,13 @@ class GPTQLinear(_Skinny):
                  ptr(self.scales_packed), 0, None, 0, None, 0, M, self.N, self.K, EPI_PARTIAL, 0,
                  ksplit, ptr(partial), stream())
 
+    def _call_addnorm(self, parts, nparts, residual, gain, eps, residual_out, out, partial,
+                      epilogue, ksplit, preset):
+        call("omni_w4a16_gemm_addnorm", ptr(parts), nparts, ptr(residual), ptr(gain), float(eps),
+             ptr(residual_out), ptr(self.qweight_packed), ptr(self.scales_packed), ptr(self.bias),
+             1, ptr(out), 0 if out is None else out.stride(0), ptr(partial), residual.shape[0],
+             self.N, self.K, epilogue, ksplit, preset, stream())
+
     def _call_attn(self, states, splits, n_kv, group, M, partial, epilogue, ksplit, preset):
         call("omni_w4a16_gemm_attn", ptr(states), splits, n_kv, group, ptr(self.qweight_packed),
              ptr(self.scales_packed), ptr(self.bias), 1, None, 0, ptr(partial), M, self.N,
@@ -380,6 +425,13 @@ class F16Linear(_Skinny):
         call("omni_packed_gemm_pipe", ptr(x2d), x2d.stride(0), ptr(self.weight_packed), None, 1,
              None, 0, None, 0, x2d.shape[0], self.N, self.K, EPI_PARTIAL, 0, ksplit, ptr(partial),
              stream())
+
+    def _call_addnorm(self, parts, nparts, residual, gain, eps, residual_out, out, partial,
+                      epilogue, ksplit, preset):
+        call("omni_f16_gemm_addnorm", ptr(parts), nparts, ptr(residual), ptr(gain), float(eps),
+             ptr(residual_out), ptr(self.weight_packed), ptr(self.bias), ptr(out),
+             0 if out is None else out.stride(0), ptr(partial), residual.shape[0], self.N, self.K,
+             epilogue, ksplit, preset, stream())
 
     def _call_attn(self, states, splits, n_kv, group, M, partial, epilogue, ksplit, preset):
         call("omni_f16_gemm_attn", ptr(states), splits, n_kv, group, ptr(self.weight_packed),

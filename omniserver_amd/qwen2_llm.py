@@ -297,7 +297,7 @@ class Qwen2LLM(nn.Module):
             So = max(l.o_proj.partial_slices() for l in self.layers)
             Sq = max(l.qkv_proj.partial_slices() for l in self.layers)
             self._bufs[n] = {
-                "h": mk(n, H), "res": mk(n, H),
+                "h": mk(n, H), "res": mk(n, H), "res2": mk(n, H),
                 "qkv": mk(n, cfg.qkv_out), "attn": mk(n, cfg.num_heads * cfg.head_dim),
                 "act": mk(n, I),
                 "dpart": f32(Sd, n, H), "opart": f32(So, n, H), "qpart": f32(Sq, n, cfg.qkv_out),
@@ -320,7 +320,10 @@ class Qwen2LLM(nn.Module):
         KV-pool write in its prologue, split softmax states out -> o_proj merging those
         states while it stages its input (partials) -> add+RMSNorm over them -> gate_up +
         SiLU -> down (partials).  Partial results cross a kernel boundary, never a
-        device-scope fence."""
+        device-scope fence.  Up to ``decode_addnorm_rows`` rows (5 launches per layer): qkv
+        and gate_up form the add+RMSNorm over the partials in their own input staging (each
+        workgroup reads the rows' partials, a few tens of KB), with the residual alternating
+        between two buffers; the outputs are the same."""
         cfg = self.cfg
         if not self.fused_decode_ready():
             raise RuntimeError("decode_greedy runs the packed int4 / fp16 linears only; decode "
@@ -329,6 +332,8 @@ class Qwen2LLM(nn.Module):
         b = self.decode_buffers(n, ids.device)
         eps = cfg.rms_norm_eps
         h, res = b["h"], b["res"]
+        if n <= self.decode_addnorm_rows:
+            return self._decode_greedy_addnorm(ids, view, ids_out, logits_out, next_ids, lengths, b)
         # the step's rotary rows (one position per row, the same for every layer) come out
         # of the first launch, so that no attention prologue looks them up
         F.embed_rms_norm_rope_out(ids, self.lm_head.table_packed, True, self.layers[0].in_norm,
@@ -349,5 +354,53 @@ class Qwen2LLM(nn.Module):
             layer.gate_up_proj.forward_out(h, b["act"])
             S = layer.down_proj.forward_partial(b["act"], b["dpart"])
         F.add_rms_norm_partials_out(b["dpart"], S, res, self.norm, eps, h, res)
+        self.lm_head.argmax_out(h, ids_out, logits_out, next_ids, lengths)
+        return ids_out
+
+    # rows up to which decode_greedy forms the add+RMSNorms inside qkv / gate_up (each of
+    # their workgroups then reads the rows' fp32 partials: ~86 KB a row for down's 14 slices,
+    # which only pays off for a row or two; 0 disables).  The saving is far below the two
+    # launches' ~3.7 us each: the consumers' critical path takes the partials' round trip
+    # and the rows' reduction instead.
+    decode_addnorm_rows = 2
+    # o_proj's K slices in that chain (two heads each): few enough that gate_up requests all
+    # of them ahead of its weights (8 per thread in flight).  Graph-timed int4 steps, ctx
+    # 2048: B = 1 1.118 ms against 1.149 with the norm launches (12 slices: 1.160, 4: 1.125);
+    # B = 2 1.159 against 1.181.  Fewer down slices (what qkv reads) made down slower than the
+    # smaller read saved (7: 1.176, 5: 1.224 ms).
+    decode_addnorm_oslices = 6
+
+    def _decode_greedy_addnorm(self, ids, view, ids_out, logits_out, next_ids, lengths, b):
+        """decode_greedy's 5-launch layers (n <= decode_addnorm_rows): qkv (layers > 0) and
+        gate_up take the previous projection's partials, the residual and the norm gain,
+        and write the new residual to the other of res / res2."""
+        cfg = self.cfg
+        eps = cfg.rms_norm_eps
+        n = ids.shape[0]
+        h = b["h"]
+        cur, other = b["res"], b["res2"]
+        F.embed_rms_norm_rope_out(ids, self.lm_head.table_packed, True, self.layers[0].in_norm,
+                                  eps, h, cur, view.kv_pos, view.rope_delta, self.rope_cos,
+                                  self.rope_sin, b["rope"])
+        S = 0
+        for i, layer in enumerate(self.layers):
+            qp = layer.qkv_proj
+            if i > 0:
+                Sq = qp.forward_addnorm(b["dpart"], S, cur, layer.in_norm, eps, other,
+                                        partial=b["qpart"])
+                cur, other = other, cur
+            else:
+                Sq = qp.forward_partial(h, b["qpart"])
+            states, Sa = view.attend_fused(b["qpart"], Sq, qp.bias, qp.fmt == "int4", i,
+                                           self.scale, self.rope_cos, self.rope_sin,
+                                           cfg.mrope_section, rope_rows=b["rope"])
+            So = layer.o_proj.forward_partial_attn(states, Sa, cfg.num_kv_heads,
+                                                   cfg.num_heads // cfg.num_kv_heads, n, b["opart"],
+                                                   ksplit=self.decode_addnorm_oslices)
+            layer.gate_up_proj.forward_addnorm(b["opart"], So, cur, layer.post_norm, eps, other,
+                                               out=b["act"])
+            cur, other = other, cur
+            S = layer.down_proj.forward_partial(b["act"], b["dpart"])
+        F.add_rms_norm_partials_out(b["dpart"], S, cur, self.norm, eps, h, cur)
         self.lm_head.argmax_out(h, ids_out, logits_out, next_ids, lengths)
         return ids_out

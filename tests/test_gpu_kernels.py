@@ -569,6 +569,63 @@ def test_add_rmsnorm_partials(gpu, S, M, H):
     assert (y.cpu().float() - ey).abs().max().item() <= 2e-3 * ey.abs().max().item()
 
 
+@pytest.mark.parametrize("fmt", ["int4", "fp16"])
+@pytest.mark.parametrize("M", [1, 2])
+def test_gemm_addnorm(gpu, fmt, M):
+    """qkv / gate_up with the add+RMSNorm in their input staging (omni_*_gemm_addnorm) equal
+    add+RMSNorm over the partials followed by the linear, bit for bit: the new residual, the
+    qkv split-K partial sums and the gate_up SiLU output; residual_out must not alias the
+    residual, and rows past what the workgroup holds are refused."""
+    from omniserver_amd import fused_ops as F
+    from omniserver_amd.linear import F16Linear, GPTQLinear
+    H = 1536
+    g = torch.Generator().manual_seed(301 + M)
+    for nparts, (N, silu) in ((14, (2048, False)), (12, (17920, True))):
+        say(f"gemm_addnorm fmt={fmt} M={M} nparts={nparts} N={N} silu={silu}")
+        parts = (torch.randn(nparts, M, H, generator=g) * 0.3).to(gpu)
+        res = f16((M, H), 302 + nparts).to(gpu)
+        gain = (1.0 + 0.1 * f16((H,), 303)).to(gpu)
+        if fmt == "int4":
+            qw, sc = _gptq(H, N, 304 + N)
+            lin = GPTQLinear(qw.to(gpu), sc.to(gpu), f16((N,), 305, 0.02).to(gpu) if not silu else None,
+                             fuse_silu=silu)
+        else:
+            lin = F16Linear(f16((N, H), 306, 0.02).to(gpu), f16((N,), 305, 0.02).to(gpu) if not silu else None,
+                            fuse_silu=silu)
+        # reference: the norm launch, then the linear
+        y = torch.empty(M, H, device=gpu, dtype=torch.float16)
+        r1 = torch.empty_like(y)
+        F.add_rms_norm_partials_out(parts, nparts, res, gain, 1e-6, y, r1)
+        r2 = torch.full_like(y, float("nan"))
+        if silu:
+            o1 = torch.empty(M, N // 2, device=gpu, dtype=torch.float16)
+            lin.forward_out(y, o1)
+            o2 = torch.full_like(o1, float("nan"))
+            lin.forward_addnorm(parts, nparts, res, gain, 1e-6, r2, out=o2)
+        else:
+            S = lin.partial_slices()
+            o1 = torch.empty(S * M * N, device=gpu, dtype=torch.float32)
+            S1 = lin.forward_partial(y, o1)
+            o2 = torch.full_like(o1, float("nan"))
+            S2 = lin.forward_addnorm(parts, nparts, res, gain, 1e-6, r2, partial=o2)
+            assert S1 == S2 == S
+        torch.cuda.synchronize()
+        assert torch.equal(r1.cpu(), r2.cpu())
+        assert torch.equal(o1.cpu(), o2.cpu())
+        with pytest.raises(ValueError):
+            lin.forward_addnorm(parts, nparts, res, gain, 1e-6, res, out=o2, partial=o2)
+    if fmt == "int4":
+        big = 3 * 512 // (H // 8) + 1          # more rows than the 512-thread form holds
+        p3 = torch.zeros(14, big, H, device=gpu)
+        r3 = torch.zeros(big, H, device=gpu, dtype=torch.float16)
+        qw, sc = _gptq(H, 2048, 307)
+        lin = GPTQLinear(qw.to(gpu), sc.to(gpu))
+        with pytest.raises(RuntimeError):
+            lin.forward_addnorm(p3, 14, r3, torch.ones(H, device=gpu, dtype=torch.float16), 1e-6,
+                                torch.empty_like(r3),
+                                partial=torch.empty(8 * big * 2048, device=gpu))
+
+
 @pytest.mark.parametrize("M", [1, 32, 49, 64])
 def test_lmhead_argmax(gpu, M):
     from omniserver_amd.linear import LMHeadArgmax

@@ -95,6 +95,66 @@ def test_decode_step_gptq(gpu, n):
     _decode_once(gpu, "gptq", 4, lengths, 4)
 
 
+@pytest.mark.parametrize("quant", [None, "gptq"])
+@pytest.mark.parametrize("n", [1, 2])
+def test_decode_addnorm_chain_equals_norm_launches(gpu, quant, n):
+    """Up to decode_addnorm_rows rows the decode step forms each add+RMSNorm inside qkv /
+    gate_up (5 launches per layer); with o_proj split as in the 7-launch step (its default
+    there is 6 slices, so its fp32 sums add in another order) it gives the 7-launch step's
+    logits, ids, K/V rows and final residual bit for bit, eagerly and replayed from a
+    hipGraph.  The default slicing is checked against the oracle by the decode-step, runner
+    and smoke tests at one and two rows."""
+    from omniserver_amd import synth
+    from omniserver_amd.kv_cache import PreallocatedKVCache
+    from omniserver_amd.qwen2_llm import Qwen2LLM
+    say(f"addnorm decode chain vs norm launches quant={quant} n={n} (4 layers)")
+    shape = synth.DecoderShape()
+    if quant == "gptq":
+        model = Qwen2LLM.from_gptq(synth.gptq_decoder(shape, seed=21, num_layers=4), shape, gpu,
+                                   max_pos=1024)
+    else:
+        model = Qwen2LLM.from_fp16(synth.fp16_decoder(shape, seed=21, num_layers=4), shape, gpu,
+                                   max_pos=1024)
+    lengths = [300, 41][:n]
+    ids = synth.random_ids(n, shape.vocab_size, 22, "ids").to(gpu)
+    delta = torch.zeros(n + 1, dtype=torch.int64, device=gpu)
+    model.decode_addnorm_oslices = model.layers[0].o_proj.partial_ksplit
+    outs = {}
+    for rows in (0, 2):
+        model.decode_addnorm_rows = rows
+        pool = PreallocatedKVCache(4, n + 1, 2, 512, 128, gpu, n_heads=12)
+        _fill_pool(pool, lengths, 23)
+        out = torch.empty(n, dtype=torch.int64, device=gpu)
+        logits = torch.empty(n, shape.vocab_size, dtype=torch.float16, device=gpu)
+        model.decode_greedy(ids, pool.view(n, delta), out, logits)
+        torch.cuda.synchronize()
+        b = model.decode_buffers(n, gpu)
+        outs[rows] = (out.cpu(), logits.cpu(), pool.storage.cpu(), b["h"].cpu())
+    model.decode_addnorm_rows = 2
+    for a_, b_ in zip(outs[0], outs[2]):
+        assert torch.equal(a_, b_)
+    # graph replay of the 5-launch step
+    pool = PreallocatedKVCache(4, n + 1, 2, 512, 128, gpu, n_heads=12)
+    _fill_pool(pool, lengths, 23)
+    out = torch.empty(n, dtype=torch.int64, device=gpu)
+    logits = torch.empty(n, shape.vocab_size, dtype=torch.float16, device=gpu)
+    view = pool.view(n, delta)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        model.decode_greedy(ids, view, out, logits)       # warm-up (writes K/V at lengths)
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        model.decode_greedy(ids, view, out, logits)
+    for rep in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.cpu(), outs[2][0]) and torch.equal(logits.cpu(), outs[2][1]), rep
+    model.decode_addnorm_rows = type(model).decode_addnorm_rows
+    model.decode_addnorm_oslices = type(model).decode_addnorm_oslices
+
+
 @pytest.mark.parametrize("use_graph", [False, True])
 def test_runner_greedy_matches_oracle(gpu, use_graph):
     """NativeQwenVLRunner prefill + decode (eager and hipGraph) vs oracle greedy."""

@@ -1173,9 +1173,10 @@ __global__ __launch_bounds__(512, 1) void lmhead_kernel(GemvArgs a) {
   }
   __syncthreads();
 
-  // 32-k steps per batch: 16 (512 k); 8 at 64 rows, where two 16-step batches in flight
-  // beside the 4 row blocks' accumulators and running maxima exceed a wave's registers
-  constexpr int NBU = MB >= 4 ? 8 : 16;
+  // 32-k steps per batch: 4 (two batches = 8 KB in flight per wave; 16 / 32 KB measured
+  // 1-3 % slower: 78.4 / 82.0 / 80.6 us at 32 rows, 74.3 / 74.9 / 76.5 at one row); 8 at 64
+  // rows, as measured when that form was sized for its registers
+  constexpr int NBU = MB >= 4 ? 8 : 4;
   const int NT = a.N >> 4;
   const int KS32 = K >> 5;                     // 32-k steps per tile
   const int BPT = K / (32 * NBU);              // batches per tile (K % 512 == 0)

@@ -332,7 +332,7 @@ class Qwen2LLM(nn.Module):
         b = self.decode_buffers(n, ids.device)
         eps = cfg.rms_norm_eps
         h, res = b["h"], b["res"]
-        if n <= self.decode_addnorm_rows:
+        if self._addnorm_ok(n):
             return self._decode_greedy_addnorm(ids, view, ids_out, logits_out, next_ids, lengths, b)
         # the step's rotary rows (one position per row, the same for every layer) come out
         # of the first launch, so that no attention prologue looks them up
@@ -369,6 +369,13 @@ class Qwen2LLM(nn.Module):
     # B = 2 1.159 against 1.181.  Fewer down slices (what qkv reads) made down slower than the
     # smaller read saved (7: 1.176, 5: 1.224 ms).
     decode_addnorm_oslices = 6
+
+    def _addnorm_ok(self, n: int) -> bool:
+        """Whether an n-row decode step takes the 5-launch chain: n <= decode_addnorm_rows,
+        and the norms' rows fit the fused forms (a chunk of 8 per thread, whole waves per row:
+        hidden % 512 == 0, n hidden / 8 <= 512 threads)."""
+        H = self.cfg.hidden_size
+        return 0 < n <= self.decode_addnorm_rows and H % 512 == 0 and n * (H // 8) <= 512
 
     def _decode_greedy_addnorm(self, ids, view, ids_out, logits_out, next_ids, lengths, b):
         """decode_greedy's 5-launch layers (n <= decode_addnorm_rows): qkv (layers > 0) and

@@ -369,3 +369,19 @@ def test_prefill_writers_update():
     for layer in range(2):
         single.update(k[:, :, :5], k[:, :, :5], layer)
     assert pool.lengths.tolist() == [4, 5, 3] and pool.k[0][1, :5, 0, 0].tolist() == [0, 1, 2, 3, 4]
+
+
+def test_decode_addnorm_eligibility():
+    """The 5-launch decode chain is taken only for up to decode_addnorm_rows rows whose norms
+    fit the fused forms (hidden % 512 == 0, rows x hidden / 8 <= 512 threads)."""
+    from types import SimpleNamespace
+    from omniserver_amd.qwen2_llm import Qwen2LLM
+    m = SimpleNamespace(cfg=SimpleNamespace(hidden_size=1536), decode_addnorm_rows=2)
+    ok = lambda n: Qwen2LLM._addnorm_ok(m, n)
+    assert ok(1) and ok(2) and not ok(3) and not ok(0)
+    m.cfg.hidden_size = 1280                 # not whole waves per row
+    assert not ok(1)
+    m.cfg.hidden_size = 3072                 # 384 threads a row: one row only
+    assert ok(1) and not ok(2)
+    m.cfg.hidden_size, m.decode_addnorm_rows = 1536, 0
+    assert not ok(1)

@@ -168,6 +168,17 @@ int omni_prefill_attention(const void* q, int q_stride, const void* k_cache, con
                            const int* qblocks, int nqb, void* out, int out_stride, int n_heads,
                            int n_kv_heads, int head_dim, float scale, void* stream);
 
+/* The same attention (qblocks counts <= 16) with each (block, head) item's key tiles split
+ * over the four waves of a workgroup and the partial softmax states merged in LDS: for few
+ * items with many keys each (a prompt of a few hundred tokens, an appended chunk).  Agrees
+ * with omni_prefill_attention to the fp16 rounding of the probabilities (replaces the same
+ * cache/kv_prealloc.py:181-203 call). */
+int omni_prefill_attention_split(const void* q, int q_stride, const void* k_cache,
+                                 const void* v_cache, int pool_rows, int max_len,
+                                 const int64_t* slots, const int64_t* kv_len, const int* qblocks,
+                                 int nqb, void* out, int out_stride, int n_heads, int n_kv_heads,
+                                 int head_dim, float scale, void* stream);
+
 /* The same attention with query blocks of up to 32 tokens (qblocks counts <= 32): one
  * workgroup per (block, KV head) loads each 32-key K/V tile once into LDS for all the
  * group's query heads (n_heads / n_kv_heads <= 8); outputs equal omni_prefill_attention's

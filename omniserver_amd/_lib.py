@@ -57,6 +57,8 @@ SIGNATURES = {
                                    _F, _P],
     "omni_prefill_attention": [_P, _I, _P, _P, _I, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _F,
                                _P],
+    "omni_prefill_attention_split": [_P, _I, _P, _P, _I, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I,
+                                     _F, _P],
     "omni_w4a16_gemm": [_P, _I, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I, _I, _P],
     "omni_f16_gemm": [_P, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I, _P],
     "omni_f16_gemm_tiled": [_P, _I, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _P],

@@ -665,47 +665,27 @@ struct PrefillArgs {
   float scale_log2;
 };
 
-__global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) half_t vs_lds[ATT_WAVES][ATT_BLK * ATT_VSTRIDE];
+// One wave's part of a (query block, head) item: the online softmax over the 32-key tiles
+// [tlo, thi) of the block's key range [0, end) (tile t = keys 32 t .. 32 t + 31), for the
+// 16 query rows whose Q fragments qf hold (lane (q16, c16): row c16, dims 32 ks + 8 q16 ..
+// +7; lim = keys visible to row c16).  K fragments go global -> registers, the next tile's
+// loads in flight during the current tile's MFMAs; V goes through the wave's LDS tile vs
+// for the transposed B-operand reads.  On return: m_run = running max of row c16's scores
+// (log2 units; -inf while none of its keys has been seen), l_run = this lane's part of that
+// row's sum (keys 4 q16 .. +3 of every 16), o_acc = unnormalised output (row 4 q16 + i,
+// column 16 dt + c16).
+__device__ __forceinline__ void prefill_wave_tiles(const PrefillArgs& a, int64_t slot, int g,
+                                                   int end, int lim, int tlo, int thi,
+                                                   const half8_t (&qf)[4], half_t* vs,
+                                                   float& m_run, float& l_run,
+                                                   f32x4 (&o_acc)[8]) {
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
   const int q16 = lane >> 4;
   const int c16 = lane & 15;
-  const int item = blockIdx.x * ATT_WAVES + wave;
-  if (item >= a.nqb * a.nh) return;   // no workgroup barriers below
-  const int qb = item / a.nh;
-  const int h = item % a.nh;
-  const int g = h / a.G;
-  const int t0 = a.qblocks[2 * qb];
-  const int n = a.qblocks[2 * qb + 1];
-  const int64_t slot = a.slots[t0];
-  if (slot < 0 || slot >= a.pool_rows || n <= 0) return;
-
-  const int my_row = c16 < n ? c16 : n - 1;
-  int64_t lim64 = a.kv_len[t0 + my_row];
-  lim64 = clamp64(lim64, 1, a.max_len);
-  const int lim = (int)lim64;                 // keys visible to this lane's query row
-  int64_t end64 = clamp64(a.kv_len[t0 + n - 1], 1, a.max_len);
-  const int end = (int)end64;                 // key range of the block
-
-  half8_t qf[4];
-  {
-    const half_t* qp = a.q + (int64_t)(t0 + my_row) * a.q_stride + (int64_t)h * ATT_HD;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) qf[ks] = *(const half8_t*)(qp + ks * 32 + q16 * 8);
-  }
-
-  float m_run = -INFINITY;
-  float l_run = 0.f;
-  f32x4 o_acc[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) o_acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
-
   const int64_t row_base = slot * (int64_t)a.max_len;
   const half_t* kbase = a.k_cache + g * ATT_HD;
   const half_t* vbase = a.v_cache + g * ATT_HD;
   const int64_t tok_stride = (int64_t)a.nkv * ATT_HD;
-  half_t* vs = vs_lds[wave];
 
   half8_t kf[2][4];
   half8_t vr[8];
@@ -727,8 +707,10 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
     }
   };
 
-  load_block(0);
-  for (int tb = 0; tb < end; tb += ATT_BLK) {
+  if (tlo >= thi) return;
+  load_block(tlo * ATT_BLK);
+  for (int t = tlo; t < thi; ++t) {
+    const int tb = t * ATT_BLK;
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
       const int c = lane + 64 * r;
@@ -739,7 +721,7 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) kc[j][ks] = kf[j][ks];
-    if (tb + ATT_BLK < end) load_block(tb + ATT_BLK);
+    if (t + 1 < thi) load_block(tb + ATT_BLK);
 
     f32x4 sacc[2];
 #pragma unroll
@@ -762,14 +744,18 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
       }
     mblk = fmaxf(mblk, __shfl_xor(mblk, 16, 64));
     mblk = fmaxf(mblk, __shfl_xor(mblk, 32, 64));
-    const float m_new = fmaxf(m_run, mblk);    // finite: key 0 is visible to every row
-    const float alpha = exp2f(m_run - m_new);
+    const float m_new = fmaxf(m_run, mblk);
+    // -inf only for a row none of whose keys this wave has seen yet (a tile range that
+    // starts past the row's last key); exp2(-inf - -inf) would be NaN.  From tile 0 on,
+    // key 0 is visible to every row, so a range that starts there never needs it.
+    const float m_ref = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = exp2f(m_run - m_ref);
     m_run = m_new;
     half8_t pa;
     float psum = 0.f;
 #pragma unroll
     for (int s8 = 0; s8 < 8; ++s8) {
-      const float p = exp2f(sc[s8] - m_new);
+      const float p = exp2f(sc[s8] - m_ref);
       psum += p;
       pa[s8] = (half_t)p;
     }
@@ -789,6 +775,48 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
     }
     __builtin_amdgcn_wave_barrier();
   }
+}
+
+// The Q fragments of a wave's 16 query rows (row c16 of the lane; rows past the block's n
+// tokens replicate its last one).
+__device__ __forceinline__ void prefill_load_q(const PrefillArgs& a, int t0, int row, int h,
+                                               half8_t (&qf)[4]) {
+  const int q16 = (threadIdx.x & 63) >> 4;
+  const half_t* qp = a.q + (int64_t)(t0 + row) * a.q_stride + (int64_t)h * ATT_HD;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) qf[ks] = *(const half8_t*)(qp + ks * 32 + q16 * 8);
+}
+
+__global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
+  __shared__ __attribute__((aligned(16))) half_t vs_lds[ATT_WAVES][ATT_BLK * ATT_VSTRIDE];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int q16 = lane >> 4;
+  const int c16 = lane & 15;
+  const int item = blockIdx.x * ATT_WAVES + wave;
+  if (item >= a.nqb * a.nh) return;   // no workgroup barriers below
+  const int qb = item / a.nh;
+  const int h = item % a.nh;
+  const int g = h / a.G;
+  const int t0 = a.qblocks[2 * qb];
+  const int n = a.qblocks[2 * qb + 1];
+  const int64_t slot = a.slots[t0];
+  if (slot < 0 || slot >= a.pool_rows || n <= 0) return;
+
+  const int my_row = c16 < n ? c16 : n - 1;
+  const int lim = (int)clamp64(a.kv_len[t0 + my_row], 1, a.max_len);   // keys row c16 sees
+  const int end = (int)clamp64(a.kv_len[t0 + n - 1], 1, a.max_len);     // the block's keys
+
+  half8_t qf[4];
+  prefill_load_q(a, t0, my_row, h, qf);
+  float m_run = -INFINITY;
+  float l_run = 0.f;
+  f32x4 o_acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o_acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  prefill_wave_tiles(a, slot, g, end, lim, 0, ceil_div(end, ATT_BLK), qf, vs_lds[wave], m_run,
+                     l_run, o_acc);
+
   l_run += __shfl_xor(l_run, 16, 64);
   l_run += __shfl_xor(l_run, 32, 64);
   float li[4];
@@ -804,6 +832,94 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
       for (int dt = 0; dt < 8; ++dt) op[dt * 16 + c16] = (half_t)(o_acc[dt][i] * inv);
     }
   }
+}
+
+// The same attention with each (query block, head) item spread over the four waves of one
+// workgroup: wave w takes the w-th quarter of the item's key tiles (prefill_wave_tiles) and
+// the four softmax states are merged through LDS, each wave's sums and outputs scaled by
+// 2^(m_w - max_w m_w) and added in wave order.  For prompts of a few hundred tokens, where
+// one wave per item leaves most CUs idle and walks the longest block's tiles one after
+// another.  The scores are prefill_attn_kernel's; P is rounded to fp16 against a wave's own
+// running max, so the outputs agree with it to fp16 rounding, not bit for bit.
+__global__ __launch_bounds__(256, 2) void prefill_attn_split_kernel(PrefillArgs a) {
+  __shared__ __attribute__((aligned(16))) half_t vs_lds[ATT_WAVES][ATT_BLK * ATT_VSTRIDE];
+  // row stride ATT_HD + 4 floats: the 16-lane column runs of rows 4 apart fall on
+  // different banks (row r at bank offset 16 r mod 64)
+  __shared__ __attribute__((aligned(16))) float o_lds[ATT_WAVES][16][ATT_HD + 4];
+  __shared__ float m_lds[ATT_WAVES][16], l_lds[ATT_WAVES][16];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int q16 = lane >> 4;
+  const int c16 = lane & 15;
+  // the query heads of one KV head in one XCD's range: they read the same K/V rows
+  const int item = xcd_logical_block(blockIdx.x, gridDim.x);
+  const int qb = item / a.nh;
+  const int h = item % a.nh;
+  const int g = h / a.G;
+  const int t0 = a.qblocks[2 * qb];
+  const int n = a.qblocks[2 * qb + 1];
+  const int64_t slot = a.slots[t0];
+  if (slot < 0 || slot >= a.pool_rows || n <= 0) return;   // the whole workgroup
+
+  const int my_row = c16 < n ? c16 : n - 1;
+  const int lim = (int)clamp64(a.kv_len[t0 + my_row], 1, a.max_len);
+  const int end = (int)clamp64(a.kv_len[t0 + n - 1], 1, a.max_len);
+  const int ntiles = ceil_div(end, ATT_BLK);
+  // the waves' ranges partition [0, ntiles): the one holding tile 0 (key 0, visible to
+  // every row) gives every row a finite maximum
+  const int tlo = wave * ntiles / ATT_WAVES;
+  const int thi = (wave + 1) * ntiles / ATT_WAVES;
+
+  half8_t qf[4];
+  prefill_load_q(a, t0, my_row, h, qf);
+  float m_run = -INFINITY;
+  float l_run = 0.f;
+  f32x4 o_acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o_acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  prefill_wave_tiles(a, slot, g, end, lim, tlo, thi, qf, vs_lds[wave], m_run, l_run, o_acc);
+
+  l_run += __shfl_xor(l_run, 16, 64);
+  l_run += __shfl_xor(l_run, 32, 64);
+  if (q16 == 0) {
+    m_lds[wave][c16] = m_run;
+    l_lds[wave][c16] = l_run;
+  }
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o_lds[wave][4 * q16 + i][dt * 16 + c16] = o_acc[dt][i];
+  __syncthreads();
+
+  // wave w writes columns 32 w .. 32 w + 31 of the 16 rows: lane -> row lane / 4, 8 columns
+  const int r = lane >> 2;
+  const int col = 32 * wave + 8 * (lane & 3);
+  if (r >= n) return;
+  float mx = m_lds[0][r];
+#pragma unroll
+  for (int w = 1; w < ATT_WAVES; ++w) mx = fmaxf(mx, m_lds[w][r]);
+  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float l = 0.f;
+#pragma unroll
+  for (int w = 0; w < ATT_WAVES; ++w) {
+    const float sw = exp2f(m_lds[w][r] - mx);   // 0 for a wave that saw none of the row's keys
+    l += l_lds[w][r] * sw;
+    const float4 lo = *(const float4*)&o_lds[w][r][col];
+    const float4 hi = *(const float4*)&o_lds[w][r][col + 4];
+    o[0] += lo.x * sw;
+    o[1] += lo.y * sw;
+    o[2] += lo.z * sw;
+    o[3] += lo.w * sw;
+    o[4] += hi.x * sw;
+    o[5] += hi.y * sw;
+    o[6] += hi.z * sw;
+    o[7] += hi.w * sw;
+  }
+  const float inv = 1.0f / l;
+  half8_t ov;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ov[e] = (half_t)(o[e] * inv);
+  *(half8_t*)(a.out + (int64_t)(t0 + r) * a.out_stride + (int64_t)h * ATT_HD + col) = ov;
 }
 
 // The same attention for long segments: one workgroup (4 waves) per (block of up to 32
@@ -997,21 +1113,18 @@ __global__ __launch_bounds__(256, 1) void prefill_attn_gqa_kernel(PrefillArgs a)
   }
 }
 
-// Causal varlen attention for packed query tokens over the pool.
-//   qblocks int32 [nqb][2]: (first token, count <= 16); the tokens of a block share
-//   slots[t] and have increasing kv_len.  out fp16 rows of out_stride elements.
-extern "C" int omni_prefill_attention(const void* q, int q_stride, const void* k_cache,
-                                      const void* v_cache, int pool_rows, int max_len,
-                                      const int64_t* slots, const int64_t* kv_len,
-                                      const int* qblocks, int nqb, void* out, int out_stride,
-                                      int n_heads, int n_kv_heads, int head_dim, float scale,
-                                      void* stream) {
+// The arguments the prefill entry points share, checked: q [T, q_stride] fp16 (heads of
+// head_dim = 128), pool K/V [pool_rows, max_len, n_kv_heads, 128] fp16, qblocks int32
+// [nqb][2] = (first token, count), out fp16 rows of out_stride elements.
+static int prefill_args(PrefillArgs& a, const void* q, int q_stride, const void* k_cache,
+                        const void* v_cache, int pool_rows, int max_len, const int64_t* slots,
+                        const int64_t* kv_len, const int* qblocks, int nqb, void* out,
+                        int out_stride, int n_heads, int n_kv_heads, int head_dim, float scale) {
   if (nqb < 0 || n_heads <= 0 || n_kv_heads <= 0 || pool_rows <= 0 || max_len <= 0) return OMNI_EINVAL;
   if (head_dim != ATT_HD || n_heads % n_kv_heads) return OMNI_EUNSUPPORTED;
   if (q_stride < n_heads * ATT_HD || (q_stride & 7) || out_stride < n_heads * ATT_HD) return OMNI_EINVAL;
-  if (nqb == 0) return OMNI_OK;
-  if (!q || !k_cache || !v_cache || !slots || !kv_len || !qblocks || !out) return OMNI_EINVAL;
-  PrefillArgs a;
+  if (nqb > 0 && (!q || !k_cache || !v_cache || !slots || !kv_len || !qblocks || !out))
+    return OMNI_EINVAL;
   a.q = (const half_t*)q;
   a.q_stride = q_stride;
   a.k_cache = (const half_t*)k_cache;
@@ -1028,10 +1141,48 @@ extern "C" int omni_prefill_attention(const void* q, int q_stride, const void* k
   a.out = (half_t*)out;
   a.out_stride = out_stride;
   a.scale_log2 = scale * 1.4426950408889634f;
+  return OMNI_OK;
+}
+
+// Causal varlen attention for packed query tokens over the pool.
+//   qblocks int32 [nqb][2]: (first token, count <= 16); the tokens of a block share
+//   slots[t] and have increasing kv_len.  out fp16 rows of out_stride elements.
+extern "C" int omni_prefill_attention(const void* q, int q_stride, const void* k_cache,
+                                      const void* v_cache, int pool_rows, int max_len,
+                                      const int64_t* slots, const int64_t* kv_len,
+                                      const int* qblocks, int nqb, void* out, int out_stride,
+                                      int n_heads, int n_kv_heads, int head_dim, float scale,
+                                      void* stream) {
+  PrefillArgs a;
+  const int rc = prefill_args(a, q, q_stride, k_cache, v_cache, pool_rows, max_len, slots, kv_len,
+                              qblocks, nqb, out, out_stride, n_heads, n_kv_heads, head_dim, scale);
+  if (rc || nqb == 0) return rc;
   const int64_t items = (int64_t)nqb * n_heads;
   const int64_t grid = (items + ATT_WAVES - 1) / ATT_WAVES;
   if (grid > 0x7fffffff) return OMNI_EUNSUPPORTED;
   hipLaunchKernelGGL(prefill_attn_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, a);
+  OMNI_CHECK_LAUNCH();
+  return OMNI_OK;
+}
+
+// The same attention (qblocks as above, count <= 16) with each (block, head) item's keys
+// split over the four waves of a workgroup and the partial softmax states merged in LDS
+// (prefill_attn_split_kernel): for few items with many keys each.  Agrees with
+// omni_prefill_attention to the fp16 rounding of the probabilities.
+extern "C" int omni_prefill_attention_split(const void* q, int q_stride, const void* k_cache,
+                                            const void* v_cache, int pool_rows, int max_len,
+                                            const int64_t* slots, const int64_t* kv_len,
+                                            const int* qblocks, int nqb, void* out,
+                                            int out_stride, int n_heads, int n_kv_heads,
+                                            int head_dim, float scale, void* stream) {
+  PrefillArgs a;
+  const int rc = prefill_args(a, q, q_stride, k_cache, v_cache, pool_rows, max_len, slots, kv_len,
+                              qblocks, nqb, out, out_stride, n_heads, n_kv_heads, head_dim, scale);
+  if (rc || nqb == 0) return rc;
+  const int64_t grid = (int64_t)nqb * n_heads;
+  if (grid > 0x7fffffff) return OMNI_EUNSUPPORTED;
+  hipLaunchKernelGGL(prefill_attn_split_kernel, dim3((unsigned)grid), dim3(256), 0,
+                     (hipStream_t)stream, a);
   OMNI_CHECK_LAUNCH();
   return OMNI_OK;
 }
@@ -1046,28 +1197,12 @@ extern "C" int omni_prefill_attention_gqa(const void* q, int q_stride, const voi
                                           const int* qblocks, int nqb, void* out, int out_stride,
                                           int n_heads, int n_kv_heads, int head_dim, float scale,
                                           void* stream) {
-  if (nqb < 0 || n_heads <= 0 || n_kv_heads <= 0 || pool_rows <= 0 || max_len <= 0) return OMNI_EINVAL;
-  if (head_dim != ATT_HD || n_heads % n_kv_heads || n_heads / n_kv_heads > 8) return OMNI_EUNSUPPORTED;
-  if (q_stride < n_heads * ATT_HD || (q_stride & 7) || out_stride < n_heads * ATT_HD) return OMNI_EINVAL;
-  if (nqb == 0) return OMNI_OK;
-  if (!q || !k_cache || !v_cache || !slots || !kv_len || !qblocks || !out) return OMNI_EINVAL;
   PrefillArgs a;
-  a.q = (const half_t*)q;
-  a.q_stride = q_stride;
-  a.k_cache = (const half_t*)k_cache;
-  a.v_cache = (const half_t*)v_cache;
-  a.pool_rows = pool_rows;
-  a.max_len = max_len;
-  a.nkv = n_kv_heads;
-  a.G = n_heads / n_kv_heads;
-  a.nh = n_heads;
-  a.slots = slots;
-  a.kv_len = kv_len;
-  a.qblocks = qblocks;
-  a.nqb = nqb;
-  a.out = (half_t*)out;
-  a.out_stride = out_stride;
-  a.scale_log2 = scale * 1.4426950408889634f;
+  const int rc = prefill_args(a, q, q_stride, k_cache, v_cache, pool_rows, max_len, slots, kv_len,
+                              qblocks, nqb, out, out_stride, n_heads, n_kv_heads, head_dim, scale);
+  if (rc) return rc;
+  if (a.G > 8) return OMNI_EUNSUPPORTED;
+  if (nqb == 0) return OMNI_OK;
   const int64_t grid = (int64_t)nqb * n_kv_heads;
   if (grid > 0x7fffffff) return OMNI_EUNSUPPORTED;
   if (a.G <= 6)

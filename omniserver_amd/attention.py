@@ -26,6 +26,7 @@ from __future__ import annotations
 import torch
 
 from ._lib import call, ptr, stream
+from .hostio import to_device
 
 QBLOCK = 16
 QBLOCK_GQA = 32
@@ -50,7 +51,7 @@ def query_blocks(seg_lengths, device, block: int = QBLOCK) -> torch.Tensor:
         for s in range(0, L, block):
             blocks.append((off + s, min(block, L - s)))
         off += L
-    return torch.tensor(blocks, dtype=torch.int32, device=device).reshape(-1, 2)
+    return to_device(blocks, torch.int32, device).reshape(-1, 2)
 
 
 def prefill_attention_pool(writer, q: torch.Tensor, layer_idx: int, scale: float,

@@ -26,6 +26,7 @@ from typing import List, Sequence
 import torch
 
 from ._lib import call, ptr, require_cuda, stream
+from .hostio import to_device
 
 MAX_ATTN_SPLITS = 16
 
@@ -336,10 +337,17 @@ class PackedPrefillWriter:
             pos_t += list(range(st, st + L))
             cu.append(cu[-1] + L)
         self.T = cu[-1]
-        self.token_slot = torch.tensor(slot_t, device=dev, dtype=torch.int64)
-        self.token_pos = torch.tensor(pos_t, device=dev, dtype=torch.int64)   # write positions
+        # one staged upload (no host wait): token slots, write positions, then the slots and
+        # new lengths finish() stores
+        n = len(seg)
+        meta = to_device(slot_t + pos_t + self.slots + [st + L for st, L in zip(self.starts, seg)],
+                         torch.int64, dev)
+        self.token_slot = meta[:self.T]
+        self.token_pos = meta[self.T:2 * self.T]  # write positions
+        self._fin_slots = meta[2 * self.T:2 * self.T + n]
+        self._fin_lengths = meta[2 * self.T + n:]
         self.kv_len = self.token_pos + 1          # causal: token at position p sees keys [0, p]
-        self.cu_seqlens = torch.tensor(cu, device=dev, dtype=torch.int32)
+        self.cu_seqlens = to_device(cu, torch.int32, dev)
         self.max_seg = max(seg) if seg else 0
 
     def bind(self, T: int) -> None:
@@ -375,9 +383,11 @@ class PackedPrefillWriter:
         return prefill_attention_pool(self, qkv, layer_idx, scale, out)
 
     def finish(self) -> None:
-        for s, st, L in zip(self.slots, self.starts, self.seg):
-            self.pool.lengths[s] = st + L
-            self.pool._active = max(self.pool._active, s + 1)
+        # on the device from the uploaded values: a host scalar stored into the lengths
+        # would wait for the queue
+        if self.slots:
+            self.pool.lengths.index_copy_(0, self._fin_slots, self._fin_lengths)
+            self.pool._active = max(self.pool._active, max(self.slots) + 1)
 
     def update(self, k, v, layer_idx, cache_kwargs=None):
         """The reference's SDPA route (kv_prealloc.py:205-215, 222-229): k, v [1, n_kv, T, hd]

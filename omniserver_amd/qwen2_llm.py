@@ -22,6 +22,7 @@ import torch
 from torch import nn
 
 from . import fused_ops as F
+from .hostio import to_device
 from .linear import F16Linear, GPTQLinear, LMHeadArgmax, _Skinny
 from .synth import DecoderShape
 
@@ -227,7 +228,7 @@ class Qwen2LLM(nn.Module):
             x = layer.mlp(h)
         cache.finish()
         if logits_indices is not None:
-            idx = torch.as_tensor(logits_indices, device=x.device, dtype=torch.long)
+            idx = to_device(logits_indices, torch.long, x.device)
             x, residual = x[idx].contiguous(), residual[idx].contiguous()
         h, _ = F.add_rms_norm(x, residual, self.norm, cfg.rms_norm_eps)
         logits = self.lm_head.logits(h)
@@ -280,7 +281,7 @@ class Qwen2LLM(nn.Module):
         cache.finish()
         F.add_rms_norm_partials_out(dpart, Sd, residual, self.norm, eps, h, residual)
         if logits_indices is not None:
-            idx = torch.as_tensor(logits_indices, device=dev, dtype=torch.long)
+            idx = to_device(logits_indices, torch.long, dev)
             h = h[idx].contiguous()
         logits = self.lm_head.logits(h)
         return logits.reshape(1 if logits_indices is not None else B, -1, cfg.vocab_size)

@@ -35,6 +35,7 @@ from typing import Dict, List
 
 import torch
 
+from .hostio import to_device
 from .kv_cache import PreallocatedKVCache
 from .request import Sequence, Status
 
@@ -175,19 +176,20 @@ class MultimodalRunner(ModelRunner):
             L = len(ids)
             if L == 0 or L >= self._pool.max_len:
                 raise ValueError(f"prompt length {L} outside [1, max_len={self._pool.max_len})")
-            ids_t = torch.tensor(ids, dtype=torch.int64, device=dev)
-            emb = self.adapter.embed_tokens(ids_t)
+            emb = self.adapter.embed_tokens(to_device(ids, torch.int64, dev))
             images = seq.request.images
             grids = [im.grid for im in images] if images else None
             if images:
-                mask = ids_t == self.image_token_id
+                # the image rows located on the host: a mask on the device would make the
+                # host wait for the queue (its count, its nonzero rows)
+                rows = [i for i, t in enumerate(ids) if t == self.image_token_id]
                 vis = self.adapter.vision_embed(images)
-                if int(mask.sum()) != vis.shape[0]:
+                if len(rows) != vis.shape[0]:
                     raise ValueError("image token count does not match the vision rows")
-                emb[mask] = vis
+                emb.index_copy_(0, to_device(rows, torch.int64, dev), vis.to(emb.dtype))
             pos, delta = self.adapter.prefill_positions(ids, grids)
             embeds.append(emb)
-            positions.append(pos.to(dev))
+            positions.append(to_device(pos, torch.int64, dev))
             seg_lens.append(L)
             deltas.append(delta)
         slots = [base + i for i in range(len(seqs))]
@@ -277,9 +279,10 @@ class MultimodalRunner(ModelRunner):
         with torch.inference_mode():
             start, L, end, P = self._chunk_bounds(seq)
             dev = self.device
-            ids = torch.tensor(seq.prompt_token_ids[start:end], dtype=torch.int64, device=dev)
+            ids = to_device(seq.prompt_token_ids[start:end], torch.int64, dev)
             emb = self.adapter.embed_tokens(ids).unsqueeze(0)                 # [1, L, H]
-            pos = seq.kv_handle["pos_full"][:, start:end].to(dev).unsqueeze(1)  # [3, 1, L]
+            pos = to_device(seq.kv_handle["pos_full"][:, start:end], torch.int64,
+                            dev).unsqueeze(1)                                 # [3, 1, L]
             cache = self._pool.chunked_prefill_cache(self._reserve_slot, start)
             logits = self.adapter.llm(emb, pos, None, cache, logits_indices=[L - 1])[0]
             seq.num_prefilled = end
@@ -303,12 +306,12 @@ class MultimodalRunner(ModelRunner):
             dec_len = [int(v) for v in self._kv_len[:n]]        # write positions = KV lengths
             ids = [s.last_token_id() for s in decode_seqs] + chunk_seq.prompt_token_ids[start:end]
             emb = self.adapter.embed_tokens(
-                torch.tensor(ids, dtype=torch.int64, device=dev)).unsqueeze(0)   # [1, n+L, H]
+                to_device(ids, torch.int64, dev)).unsqueeze(0)                   # [1, n+L, H]
             dec_pos = torch.tensor([dec_len[b] + int(s.kv_handle["rope_delta"])
                                     for b, s in enumerate(decode_seqs)], dtype=torch.int64)
             pos = torch.cat([dec_pos.view(1, n).expand(3, n),
                              chunk_seq.kv_handle["pos_full"][:, start:end].to(torch.int64)], 1)
-            pos = pos.to(dev).unsqueeze(1)                                         # [3, 1, n+L]
+            pos = to_device(pos, torch.int64, dev).unsqueeze(1)                   # [3, 1, n+L]
             cache = self._pool.mixed_cache(list(range(n)) + [self._reserve_slot],
                                            [1] * n + [L], dec_len + [start])
             final = end == P
@@ -381,8 +384,7 @@ class MultimodalRunner(ModelRunner):
         per-op route - one token per row appended at its length, logits, then sampling."""
         model = self.adapter.model
         self._dev_ids_for = None
-        ids = torch.tensor([s.last_token_id() for s in seqs], dtype=torch.int64,
-                           device=self.device)
+        ids = to_device([s.last_token_id() for s in seqs], torch.int64, self.device)
         emb = model.embed_tokens(ids).unsqueeze(1)                       # [n, 1, H]
         view = self._pool.view(n, self._rope_delta)
         pos = self.adapter.decode_positions(self._pool.lengths[:n], self._rope_delta[:n])

@@ -22,6 +22,7 @@ from typing import Dict, List, Sequence, Tuple
 import torch
 
 from ._lib import call, lib, ptr, require_cuda, stream
+from .hostio import to_device
 
 EPI_STORE, EPI_QGELU, EPI_GELU, EPI_RESID = 0, 4, 5, 6
 _QT = 64     # queries per attention workgroup (the kernel's tile)
@@ -239,10 +240,10 @@ class Qwen2VIT:
             raise ValueError(f"pixel_values must be [{S}, {cfg.patch_dim}] for grids {grids}")
         pv = pixel_values.to(device=dev, dtype=torch.float16).contiguous()
         m2 = cfg.spatial_merge_size ** 2
-        pos = rot_pos_ids(grids, cfg.spatial_merge_size).to(dev)
+        pos = to_device(rot_pos_ids(grids, cfg.spatial_merge_size), torch.int32, dev)
         cu_h = cu_seqlens(grids)
-        tiles = query_tiles(cu_h).to(dev)
-        cu = cu_h.to(dev)
+        tiles = to_device(query_tiles(cu_h), torch.int32, dev)
+        cu = to_device(cu_h, torch.int32, dev)
         D, nh, hd = cfg.embed_dim, cfg.n_heads, cfg.head_dim
         mk = lambda *s: torch.empty(*s, device=dev, dtype=torch.float16)
         x, h, att = mk(S, D), mk(S, D), mk(S, D)

@@ -808,19 +808,22 @@ def test_decode_attention_fused_equals_unfused(gpu, bias_after_round, splits, le
             assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("fmt,splits", [("int4", 4), ("int4", 1), ("fp16", 3), ("int4", 11)])
-def test_oproj_merges_attention_states(gpu, fmt, splits):
+@pytest.mark.parametrize("fmt,splits,n,ksplit", [
+    ("int4", 4, 32, None), ("int4", 1, 32, None), ("fp16", 3, 32, None), ("int4", 11, 32, None),
+    # 9-16 splits for few rows: the merge's two batches requested by two threads
+    ("int4", 16, 1, 6), ("int4", 16, 2, 6), ("int4", 9, 8, None), ("fp16", 16, 8, None),
+    ("int4", 13, 3, 12)])
+def test_oproj_merges_attention_states(gpu, fmt, splits, n, ksplit):
     """o_proj reading the decode attention's split states (merge in its input staging)
     gives exactly merge launch + o_proj on the merged fp16 output."""
     from omniserver_amd._lib import call, ptr, stream
     from omniserver_amd.linear import F16Linear, GPTQLinear
     from omniserver_amd.qwen2_llm import rope_tables
     from omniserver_amd.synth import gptq_random
-    say(f"o_proj from attention states fmt={fmt} splits={splits}")
+    say(f"o_proj from attention states fmt={fmt} splits={splits} rows={n} ksplit={ksplit}")
     cfg = ref.Qwen2Config()
     nh, nkv, hd, ML, H = 12, 2, 128, 4096, 1536
-    lengths = [2047, 31, 0, 500, 1300, 7, 64, 129] * 4
-    n = len(lengths)
+    lengths = ([2047, 31, 0, 500, 1300, 7, 64, 129] * 4)[:n]
     P = n + 1
     W = (nh + 2 * nkv) * hd
     g = torch.Generator().manual_seed(130)
@@ -838,7 +841,7 @@ def test_oproj_merges_attention_states(gpu, fmt, splits):
         lin = F16Linear(f16((H, H), 135, 0.02).to(gpu))
     ws = torch.empty(n * nkv * splits * 6 * 132, device=gpu, dtype=torch.float32)
     out = torch.empty(n, nh, hd, device=gpu, dtype=torch.float16)
-    S_o = lin.partial_slices()
+    S_o = lin.partial_slices(ksplit)
     pa = torch.empty(S_o * n * H, device=gpu, dtype=torch.float32)
     pb = torch.empty_like(pa)
 
@@ -848,9 +851,9 @@ def test_oproj_merges_attention_states(gpu, fmt, splits):
              ptr(out) if merge else None, n, nh, nkv, hd, hd ** -0.5, 8, splits, ptr(ws),
              ws.numel(), merge, None, stream())
     attn(0)
-    lin.forward_partial_attn(ws, splits, nkv, nh // nkv, n, pa)
+    lin.forward_partial_attn(ws, splits, nkv, nh // nkv, n, pa, ksplit=ksplit)
     attn(1)                       # same K/V row rewritten with the same values
-    lin.forward_partial(out, pb)
+    lin.forward_partial(out, pb, ksplit=ksplit)
     torch.cuda.synchronize()
     assert torch.equal(pa, pb)
 

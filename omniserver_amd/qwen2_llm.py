@@ -29,6 +29,15 @@ from .synth import DecoderShape
 Qwen2Config = DecoderShape
 
 
+def _indices_on(indices, device) -> torch.Tensor:
+    """logits_indices as an int64 tensor on device: a tensor already there is used as is (no
+    host transfer, so a forward given one can be captured in a graph)."""
+    if isinstance(indices, torch.Tensor) and indices.device == torch.device(device) \
+            and indices.dtype == torch.long:
+        return indices
+    return to_device(indices, torch.long, device)
+
+
 def rope_tables(cfg: Qwen2Config, max_pos: int, device):
     """fp16 cos/sin [max_pos, head_dim/2] of p * inv_freq (qwen2_llm.py:169-177, 181):
     inv_freq = 1/theta^(arange(0,hd,2)/hd) in fp32, held in fp16 as the deployed module
@@ -228,7 +237,7 @@ class Qwen2LLM(nn.Module):
             x = layer.mlp(h)
         cache.finish()
         if logits_indices is not None:
-            idx = to_device(logits_indices, torch.long, x.device)
+            idx = _indices_on(logits_indices, x.device)
             x, residual = x[idx].contiguous(), residual[idx].contiguous()
         h, _ = F.add_rms_norm(x, residual, self.norm, cfg.rms_norm_eps)
         logits = self.lm_head.logits(h)
@@ -281,7 +290,7 @@ class Qwen2LLM(nn.Module):
         cache.finish()
         F.add_rms_norm_partials_out(dpart, Sd, residual, self.norm, eps, h, residual)
         if logits_indices is not None:
-            idx = to_device(logits_indices, torch.long, dev)
+            idx = _indices_on(logits_indices, dev)
             h = h[idx].contiguous()
         logits = self.lm_head.logits(h)
         return logits.reshape(1 if logits_indices is not None else B, -1, cfg.vocab_size)

@@ -115,6 +115,7 @@ class MultimodalRunner(ModelRunner):
         self._slot_seq: List[Sequence] = []
         self._kv_len: List[int] = []          # host mirror of pool.lengths for active slots
         self._graphs: Dict[int, tuple] = {}
+        self._prefill_graphs: Dict[tuple, dict] = {}
         self._graphs_sampled: Dict[int, tuple] = {}
         self._eager: Dict[int, dict] = {}
         self._dev_ids_for = None              # batch whose next ids already sit on device
@@ -195,9 +196,12 @@ class MultimodalRunner(ModelRunner):
         slots = [base + i for i in range(len(seqs))]
         packed = torch.cat(embeds, 0).unsqueeze(0)
         pos = torch.cat(positions, dim=1).unsqueeze(1)            # [3, 1, T]
-        last = torch.tensor(seg_lens).cumsum(0) - 1
-        cache = self._pool.packed_prefill_cache(slots, seg_lens)
-        logits = self.adapter.llm(packed, pos, None, cache, logits_indices=last.tolist())[0]
+        if self._use_graph and self.prefill_graph_layouts > 0:
+            logits = self._prefill_graphed(packed, pos, slots, seg_lens)
+        else:
+            last = torch.tensor(seg_lens).cumsum(0) - 1
+            cache = self._pool.packed_prefill_cache(slots, seg_lens)
+            logits = self.adapter.llm(packed, pos, None, cache, logits_indices=last.tolist())[0]
         toks = self._sample_rows(logits, seqs)
         for i, seq in enumerate(seqs):
             slot = slots[i]
@@ -208,6 +212,54 @@ class MultimodalRunner(ModelRunner):
             seq.append_token(toks[i])
             seq.maybe_finish()
         self._dev_ids_for = None
+
+    # Packed prefills run as HIP graphs keyed by their segment lengths (with use_graph): the
+    # first prefill of a layout runs eagerly on the layout's static input buffers and is then
+    # captured; a later prefill of the same layout copies its embeddings, positions and slots
+    # into those buffers and replays.  Token positions, query blocks and new lengths depend
+    # only on the layout; the slot of every token is rewritten on the device before a replay.
+    # Up to this many layouts are kept (least recently used dropped); 0 disables.
+    prefill_graph_layouts = 4
+
+    def _prefill_graphed(self, packed, pos, slots, seg_lens):
+        key = tuple(int(L) for L in seg_lens)
+        graphs = self._prefill_graphs
+        ent = graphs.pop(key, None)
+        dev = self.device
+        if ent is not None:
+            graphs[key] = ent                                     # most recently used last
+            ent["x"].copy_(packed)
+            ent["pos"].copy_(pos)
+            if ent["slots"] != slots:
+                writer = ent["writer"]
+                tok = [s for s, L in zip(slots, key) for _ in range(L)]
+                new = to_device(tok + list(slots), torch.int64, dev)
+                writer.token_slot.copy_(new[:len(tok)])
+                writer._fin_slots.copy_(new[len(tok):])
+                writer.slots = list(slots)
+                ent["slots"] = list(slots)
+            ent["graph"].replay()
+            self._pool._active = max(self._pool._active, max(slots) + 1)
+            return ent["out"]
+        # first prefill of this layout: run it on static buffers, then capture (outside
+        # inference mode, as the decode graphs are: a capture made inside it would leave the
+        # generator's graph state as inference tensors that later captures cannot update)
+        with torch.inference_mode(False):
+            last = torch.tensor(key).cumsum(0) - 1
+            ent = {"x": packed.clone(), "pos": pos.clone(), "slots": list(slots),
+                   "idx": to_device(last, torch.int64, dev),
+                   "writer": self._pool.packed_prefill_cache(slots, list(key))}
+            run = lambda: self.adapter.llm(ent["x"], ent["pos"], None, ent["writer"],
+                                           logits_indices=ent["idx"])[0]
+            logits = run().clone()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                ent["out"] = run()
+            ent["graph"] = g
+        graphs[key] = ent
+        while len(graphs) > self.prefill_graph_layouts:
+            graphs.pop(next(iter(graphs)))
+        return logits
 
     def attach_prefilled(self, seqs: List[Sequence], lengths: List[int],
                          rope_deltas: List[int] | None = None) -> List[int]:

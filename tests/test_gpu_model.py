@@ -593,3 +593,54 @@ def test_runner_matches_golden_fixture(gpu):
             compared += 1
     say(f"  {compared}/{2 * len(gold['steps'])} fixture tokens compared")
     assert compared >= 8
+
+
+def test_prefill_graph_equals_eager(gpu):
+    """Packed prefills replayed from HIP graphs keyed by their segment layout give the same
+    first tokens, pool rows and lengths as the eager forward: a layout's first prefill
+    (eager on static buffers, then captured), a replay at the same slots, a new layout, and
+    a replay at other slots than the capture's (after compaction)."""
+    from omniserver_amd import synth
+    from omniserver_amd.request import Request, SamplingParams, Sequence
+    from omniserver_amd.runner import NativeQwenVLRunner
+    say("prefill graphs vs eager (gptq, 2 layers)")
+    shape = synth.DecoderShape()
+    w = synth.gptq_decoder(shape, seed=16, num_layers=2)
+    runners = [NativeQwenVLRunner(max_running=4, max_len=256, use_graph=g, weights=w,
+                                  quant="gptq") for g in (False, True)]
+    runners[0].prefill_graph_layouts = 0
+    mk = lambda L, tag: Sequence(Request(prompt=synth.random_ids(L, shape.vocab_size, 16, tag).tolist(),
+                                         sampling=SamplingParams(max_new_tokens=64)))
+    seqs = [dict() for _ in runners]
+
+    def phase(name, new=(), free=()):
+        for r, ss in zip(runners, seqs):
+            for tag in free:
+                r.free(ss.pop(tag))
+            batch = [mk(L, tag) for tag, L in new]
+            for (tag, _), s in zip(new, batch):
+                ss[tag] = s
+            if batch:
+                r.prefill(batch)
+        for r in runners:
+            r.settle()               # a decode step enqueued ahead is taken back
+        torch.cuda.synchronize()
+        toks = [{t: s.output_token_ids for t, s in ss.items()} for ss in seqs]
+        assert toks[0] == toks[1], name
+        a, b = (r.pool for r in runners)
+        assert torch.equal(a.lengths.cpu(), b.lengths.cpu()), name
+        for slot, L in enumerate(a.lengths.cpu().tolist()[:len(seqs[0])]):   # valid rows
+            assert torch.equal(a.storage[:, :, slot, :L].view(torch.int16).cpu(),
+                               b.storage[:, :, slot, :L].view(torch.int16).cpu()), (name, slot)
+        slots = {t: s.kv_handle["slot"] for t, s in seqs[1].items()}
+        say(f"  {name}: equal (slots {slots})")
+
+    phase("first prefill of [100, 60]", new=[("a0", 100), ("a1", 60)])
+    phase("replay of [100, 60]", new=[("b0", 100), ("b1", 60)], free=["a0", "a1"])
+    phase("first prefill of [80]", new=[("c", 80)])
+    phase("replay of [80] at another slot", new=[("d", 80)], free=["b0", "b1"])
+    assert len(runners[1]._prefill_graphs) == 2
+    for _ in range(3):
+        for r, ss in zip(runners, seqs):
+            r.decode(list(ss.values()))
+    phase("decode after the replays")

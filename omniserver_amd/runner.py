@@ -169,7 +169,10 @@ class MultimodalRunner(ModelRunner):
             raise RuntimeError(f"KV pool full: {base} running + {len(seqs)} new > "
                                f"{self.max_running}")
         dev = self.device
-        embeds, positions, seg_lens, deltas = [], [], [], []
+        # the packed prompt's host-side inputs are gathered first and uploaded once each
+        # (ids, image row indices, positions): per-sequence uploads and launches would hold
+        # the GPU idle while the host issues them
+        all_ids, positions, seg_lens, deltas, img_rows, vis = [], [], [], [], [], []
         for seq in seqs:
             if not seq.prompt_token_ids:
                 self.tokenize(seq)
@@ -177,35 +180,39 @@ class MultimodalRunner(ModelRunner):
             L = len(ids)
             if L == 0 or L >= self._pool.max_len:
                 raise ValueError(f"prompt length {L} outside [1, max_len={self._pool.max_len})")
-            emb = self.adapter.embed_tokens(to_device(ids, torch.int64, dev))
             images = seq.request.images
             grids = [im.grid for im in images] if images else None
             if images:
                 # the image rows located on the host: a mask on the device would make the
                 # host wait for the queue (its count, its nonzero rows)
-                rows = [i for i, t in enumerate(ids) if t == self.image_token_id]
-                vis = self.adapter.vision_embed(images)
-                if len(rows) != vis.shape[0]:
+                off = len(all_ids)
+                rows = [off + i for i, t in enumerate(ids) if t == self.image_token_id]
+                v = self.adapter.vision_embed(images)
+                if len(rows) != v.shape[0]:
                     raise ValueError("image token count does not match the vision rows")
-                emb.index_copy_(0, to_device(rows, torch.int64, dev), vis.to(emb.dtype))
+                img_rows += rows
+                vis.append(v)
             pos, delta = self.adapter.prefill_positions(ids, grids)
-            embeds.append(emb)
-            positions.append(to_device(pos, torch.int64, dev))
+            all_ids += ids
+            positions.append(pos)
             seg_lens.append(L)
             deltas.append(delta)
         slots = [base + i for i in range(len(seqs))]
-        packed = torch.cat(embeds, 0).unsqueeze(0)
-        pos = torch.cat(positions, dim=1).unsqueeze(1)            # [3, 1, T]
+        emb = self.adapter.embed_tokens(to_device(all_ids, torch.int64, dev))
+        if img_rows:
+            emb.index_copy_(0, to_device(img_rows, torch.int64, dev), torch.cat(vis, 0).to(emb.dtype))
+        packed = emb.unsqueeze(0)
+        pos = to_device(torch.cat(positions, dim=1), torch.int64, dev).unsqueeze(1)   # [3, 1, T]
         if self._use_graph and self.prefill_graph_layouts > 0:
             logits = self._prefill_graphed(packed, pos, slots, seg_lens)
         else:
             last = torch.tensor(seg_lens).cumsum(0) - 1
             cache = self._pool.packed_prefill_cache(slots, seg_lens)
             logits = self.adapter.llm(packed, pos, None, cache, logits_indices=last.tolist())[0]
+        self._rope_delta[base:base + len(seqs)].copy_(to_device(deltas, torch.int64, dev))
         toks = self._sample_rows(logits, seqs)
         for i, seq in enumerate(seqs):
             slot = slots[i]
-            self._rope_delta[slot] = deltas[i]
             self._slot_seq.append(seq)
             self._kv_len.append(seg_lens[i])
             seq.kv_handle = {"slot": slot, "rope_delta": deltas[i]}
@@ -527,7 +534,7 @@ class MultimodalRunner(ModelRunner):
         """Greedy = argmax of the fp16 logits (multimodal.py:374-377); else temperature
         sampling."""
         out = []
-        greedy_rows = logits.float().argmax(-1).tolist()
+        greedy_rows = logits.argmax(-1).tolist()      # first maximum, as on the fp32 copy
         for i, seq in enumerate(seqs):
             sp = seq.request.sampling
             if sp.greedy:

@@ -228,6 +228,12 @@ class MultimodalRunner(ModelRunner):
     # Up to this many layouts are kept (least recently used dropped); 0 disables.
     prefill_graph_layouts = 4
 
+    def drop_prefill_graphs(self) -> None:
+        """Forget the captured prefill graphs.  They launch on the device addresses of the
+        weights they were captured with (including the GPTQ linears' resident fp16
+        expansions), so call this after rewriting or releasing weights."""
+        self._prefill_graphs.clear()
+
     def _prefill_graphed(self, packed, pos, slots, seg_lens):
         key = tuple(int(L) for L in seg_lens)
         graphs = self._prefill_graphs

@@ -609,8 +609,18 @@ def test_prefill_graph_equals_eager(gpu):
     runners = [NativeQwenVLRunner(max_running=4, max_len=256, use_graph=g, weights=w,
                                   quant="gptq") for g in (False, True)]
     runners[0].prefill_graph_layouts = 0
-    mk = lambda L, tag: Sequence(Request(prompt=synth.random_ids(L, shape.vocab_size, 16, tag).tolist(),
-                                         sampling=SamplingParams(max_new_tokens=64)))
+    from omniserver_amd.positions import IMAGE_TOKEN_ID, VISION_START_TOKEN_ID
+    from omniserver_amd.request import VisionInput
+
+    def mk(L, tag):
+        ids = synth.random_ids(L, shape.vocab_size, 16, tag).tolist()
+        images = None
+        if tag.startswith("img"):   # <|vision_start|> + 16 image rows (grid 1 x 8 x 8) inside
+            ids[10:27] = [VISION_START_TOKEN_ID] + [IMAGE_TOKEN_ID] * 16
+            rows = synth.randn16((16, shape.hidden_size), 1.0, 16, tag).to(gpu)
+            images = [VisionInput(rows, (1, 8, 8))]
+        return Sequence(Request(prompt=ids, sampling=SamplingParams(max_new_tokens=64),
+                                images=images))
     seqs = [dict() for _ in runners]
 
     def phase(name, new=(), free=()):
@@ -639,7 +649,11 @@ def test_prefill_graph_equals_eager(gpu):
     phase("replay of [100, 60]", new=[("b0", 100), ("b1", 60)], free=["a0", "a1"])
     phase("first prefill of [80]", new=[("c", 80)])
     phase("replay of [80] at another slot", new=[("d", 80)], free=["b0", "b1"])
-    assert len(runners[1]._prefill_graphs) == 2
+    phase("first prefill of image prompts [70, 50]", new=[("img0", 70), ("img1", 50)],
+          free=["c", "d"])
+    phase("replay of image prompts [70, 50]", new=[("img2", 70), ("img3", 50)],
+          free=["img0", "img1"])
+    assert len(runners[1]._prefill_graphs) == 3
     for _ in range(3):
         for r, ss in zip(runners, seqs):
             r.decode(list(ss.values()))

@@ -206,11 +206,11 @@ def pmc_probe(runner, seqs, B: int) -> None:
     for K, N in LINEARS:
         w = (torch.randn(N, K, generator=g, device=dev) * 0.02).half()
         x = torch.randn(8192, K, generator=g, device=dev).half()
-        lin = FP8Linear(w)
+        lin = FP8Linear(w, rowwise=True)
         xq, sa = lin.quantize_input(x)
         y = torch.empty(8192, N, device=dev, dtype=torch.float16)
         torch.cuda.synchronize()
-        lin.gemm_out(xq, sa, y, False)
+        lin.gemm_out(xq, sa, y, FP8Linear.OUT_F16_VIA_BF16)
         torch.cuda.synchronize()
         del w, x, lin, xq, y
     lay = model.layers[0]
@@ -265,11 +265,12 @@ def fp8_layer_gemms(device, M: int = 8192, reps: int = 10) -> dict:
     g.manual_seed(4)
     per, tot_s, tot_f = {}, 0.0, 0.0
     for name, K, N in shapes:
-        lin = FP8Linear((torch.randn(N, K, device=device, generator=g) * 0.02).half())
+        lin = FP8Linear((torch.randn(N, K, device=device, generator=g) * 0.02).half(),
+                        rowwise=True)
         x = torch.randn(M, K, device=device, generator=g).half()
         xq, sa = lin.quantize_input(x)
         out = torch.empty(M, N, device=device, dtype=torch.float16)
-        t = time_kernel(lambda: lin.gemm_out(xq, sa, out, False), reps)
+        t = time_kernel(lambda: lin.gemm_out(xq, sa, out, FP8Linear.OUT_F16_VIA_BF16), reps)
         fl = 2.0 * M * N * K
         per[name] = {"us": round(t * 1e6, 1), "tflops": round(fl / t / 1e12, 1)}
         tot_s += t

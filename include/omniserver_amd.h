@@ -361,14 +361,34 @@ int omni_fp8_quant_rows(const void* x, int ldx, void* q, float* scale, int rows,
 int omni_fp8_quant_rows_bf16(const void* x, int ldx, void* q, float* scale, int rows, int K,
                              float clamp_min, void* stream);
 
-/* FP8Linear.forward / forward_prequant (kernels/fp8_linear.py:99-126):
- * y[m, n] = bf16((sum_k xq[m,k] wq[n,k]) * sa[m] * sw[n]) (fp32 accumulation, as
- * torch._scaled_mm with out_dtype bf16); out_bf16 = 1 stores that bf16 value plus
- * bf16(bias) added in bf16 (forward_prequant, :99-108), else it is cast to fp16 and the
- * fp16 bias (if any) added in fp16 (:115-124).  xq [M, K], wq [N, K] e4m3fn;
- * out [M, ldo]; N % 128 == 0, K % 128 == 0. */
+/* FP8Linear's row-wise weight quantisation (kernels/fp8_linear.py:83-86) on the fp16 weight
+ * [N, K] (row stride ldw): scale[n] = fp16(amax_k |w[n, k]| / 448) (the reference divides
+ * the fp16 amax by 448 in fp16), wq[n, k] = e4m3(w[n, k] / scale[n]) (fp32 division, the
+ * [N, 1] scale promotes it). */
+int omni_fp8_quant_weight_rows(const void* w, int ldw, void* wq, float* scale, int N, int K,
+                               void* stream);
+
+/* Per-tensor e4m3 quantisation, FP8Linear's default form: _quant_fp8_pertensor's eager
+ * branch (kernels/fp8_linear.py:40-41) for activations and the weight quantisation of
+ * :87-89, both ops on the fp16 (bf16 = 1: bf16) tensor: s = R(amax |x| / 448),
+ * q = e4m3(R(x / s)), R the input's rounding.  s is written to scale[r] for every row (the
+ * [M] / [N] scale array omni_fp8_gemm takes).  work: omni_fp8_quant_tensor_work(rows)
+ * floats of scratch (one partial maximum per workgroup).  Two launches. */
+int omni_fp8_quant_tensor(const void* x, int ldx, void* q, float* scale, float* work,
+                          int rows, int K, int bf16, void* stream);
+int omni_fp8_quant_tensor_work(int rows);
+
+/* FP8Linear.forward / forward_prequant (kernels/fp8_linear.py:99-126): the product
+ * v[m, n] = (sum_k xq[m,k] wq[n,k]) * sa[m] * sw[n] (fp32 accumulation, as
+ * torch._scaled_mm) stored by out_mode:
+ *   0  bf16(v) cast to fp16, + fp16 bias in fp16 (row-wise forward, :115-118, 124-125);
+ *   1  bf16(v) + bf16(bias) added in bf16 (forward_prequant, :99-108);
+ *   2  fp16(v), + fp16 bias in fp16 (per-tensor forward: out_dtype fp16, :119-125; sa and
+ *      sw hold one value each, repeated).  This form runs the 256 x 128 kernel where
+ *      omni_fp8_gemm_plan names the 256 x 256 one (its epilogue has no room for it).
+ * xq [M, K], wq [N, K] e4m3fn; out [M, ldo]; N % 128 == 0, K % 128 == 0. */
 int omni_fp8_gemm(const void* xq, const float* sa, const void* wq, const float* sw,
-                  const void* bias, void* out, int ldo, int M, int N, int K, int out_bf16,
+                  const void* bias, void* out, int ldo, int M, int N, int K, int out_mode,
                   void* stream);
 
 /* The kernel omni_fp8_gemm runs for a shape (no reference counterpart: it tells a caller

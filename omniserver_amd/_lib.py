@@ -44,6 +44,9 @@ SIGNATURES = {
                                     _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _P, _I64, _I, _P, _P],
     "omni_fp8_quant_rows": [_P, _I, _P, _P, _I, _I, _F, _P],
     "omni_fp8_quant_rows_bf16": [_P, _I, _P, _P, _I, _I, _F, _P],
+    "omni_fp8_quant_weight_rows": [_P, _I, _P, _P, _I, _I, _P],
+    "omni_fp8_quant_tensor": [_P, _I, _P, _P, _P, _I, _I, _I, _P],
+    "omni_fp8_quant_tensor_work": [_I],
     "omni_fp8_gemm": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
     "omni_fp8_gemm_plan": [_I, _I, _I, ctypes.POINTER(_I)],
     "omni_w4a16_gemm_attn": [_P, _I, _I, _I, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I, _I,

@@ -7,6 +7,10 @@
 //   product   y[m, n] = bf16((sum_k xq[m,k] * Wq[n,k]) * sa[m] * sw[n])    (:115-118,
 //             torch._scaled_mm with fp32 accumulation and a bf16 result), then cast to
 //             fp16 by FP8Linear.forward (two roundings), plus bias in fp16.
+// and FP8Linear's default per-tensor form (:87-90, 119-125): one weight scale and one
+// activation scale (both fp16-rounded: ops on fp16 tensors), the product written as fp16
+// directly (_scaled_mm out_dtype fp16), bias added in fp16.  The GEMM takes the scales as
+// the same [M] / [N] arrays, filled with the one value.
 //
 // Kernel: one workgroup (4 waves) per 128 x 128 output tile, K consumed in steps of 128
 // through double-buffered LDS (each row padded to 144 bytes so the 16 rows one MFMA
@@ -51,7 +55,14 @@ struct Fp8GemmArgs {
   void* out;             // [M, ldo] fp16 (or bf16)
   int ldo;
   int M, N, K;
-  int out_bf16;          // 1: write the bf16 result (forward_prequant); 0: fp16 (+bias)
+  int out_mode;          // FP8_OUT_*: how the scaled product is stored (+ bias)
+};
+
+// Output forms of the scaled product v = acc * sa[m] * sw[n]:
+enum {
+  FP8_OUT_F16_VIA_BF16 = 0,   // fp16(bf16(v)) + fp16 bias (row-wise forward, :115-118)
+  FP8_OUT_BF16 = 1,           // bf16(v) + bf16(bias) as a bf16 add (forward_prequant)
+  FP8_OUT_F16 = 2,            // fp16(v) + fp16 bias (per-tensor forward, :122-125)
 };
 
 __global__ __launch_bounds__(256, 2) void fp8_gemm_kernel(Fp8GemmArgs a) {
@@ -152,14 +163,16 @@ __global__ __launch_bounds__(256, 2) void fp8_gemm_kernel(Fp8GemmArgs a) {
       uint16_t bits[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const uint16_t b = f32_to_bf16_rne((acc[i][j][r] * sm) * sv[r]);
-        if (a.out_bf16) {
+        const float v = (acc[i][j][r] * sm) * sv[r];
+        const uint16_t b = f32_to_bf16_rne(v);
+        if (a.out_mode == FP8_OUT_BF16) {
           // forward_prequant's bias: out + bias.to(bf16), a bf16 add
           bits[r] = a.bias ? f32_to_bf16_rne(__builtin_bit_cast(float, (uint32_t)b << 16) +
                                              bf16_value((float)a.bias[n + r]))
                            : b;
         } else {
-          half_t h = (half_t)__builtin_bit_cast(float, (uint32_t)b << 16);
+          half_t h = a.out_mode == FP8_OUT_F16 ? (half_t)v
+                                               : (half_t)__builtin_bit_cast(float, (uint32_t)b << 16);
           if (a.bias) h = (half_t)((float)h + (float)a.bias[n + r]);
           bits[r] = __builtin_bit_cast(uint16_t, h);
         }
@@ -414,6 +427,7 @@ __global__ __launch_bounds__(128 * WM, 1) void fp8_gemm_pipe_kernel(Fp8GemmArgs 
     // Epilogue: lane holds n = n0 + 64wn + 16i + 4g4 + q of m = m0 + 64wm + 16j + l16.
     const int m0 = m0c, n0 = n0c;
     const uint32_t bias_mask = has_bias ? 0xffffffffu : 0u;
+    const bool direct = a.out_mode == FP8_OUT_F16;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int m = m0 + 64 * wm + 16 * j + l16;
@@ -423,9 +437,11 @@ __global__ __launch_bounds__(128 * WM, 1) void fp8_gemm_pipe_kernel(Fp8GemmArgs 
         uint32_t bits[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const uint32_t b = f32_to_bf16_bits((acc[i][j][q] * smv[j]) * snv[i][q]);
-          // fp16 output: the bf16 value rounded to fp16, plus the bias (an fp16 add)
-          const half_t hb = (half_t)__builtin_bit_cast(float, b << 16);
+          const float v = (acc[i][j][q] * smv[j]) * snv[i][q];
+          const uint32_t b = f32_to_bf16_bits(v);
+          // fp16 output: the product (FP8_OUT_F16) or its bf16 value rounded to fp16, plus
+          // the bias (an fp16 add)
+          const half_t hb = (half_t)(direct ? v : __builtin_bit_cast(float, b << 16));
           const uint32_t bw = bv[i][q >> 1] & bias_mask;
           const half_t bb = __builtin_bit_cast(half_t, (uint16_t)((q & 1) ? (bw >> 16) : (bw & 0xffffu)));
           const half_t h = has_bias ? (half_t)((float)hb + (float)bb) : hb;
@@ -433,7 +449,7 @@ __global__ __launch_bounds__(128 * WM, 1) void fp8_gemm_pipe_kernel(Fp8GemmArgs 
           const uint32_t bo =
               has_bias ? f32_to_bf16_bits(__builtin_bit_cast(float, b << 16) + bf16_value((float)bb))
                        : b;
-          bits[q] = a.out_bf16 ? bo : (uint32_t)__builtin_bit_cast(uint16_t, h);
+          bits[q] = a.out_mode == FP8_OUT_BF16 ? bo : (uint32_t)__builtin_bit_cast(uint16_t, h);
         }
         if (m < a.M) {
           uint2 pk;
@@ -465,9 +481,12 @@ __global__ __launch_bounds__(128 * WM, 1) void fp8_gemm_pipe_kernel(Fp8GemmArgs 
 #define F8B_T 256
 
 // Output bits of one product value v = acc * sa * sw: bf16(v), then either that bf16 plus
-// bf16(bias) as a bf16 add (out_bf16: forward_prequant, out + bias.to(bf16)) or the bf16
-// rounded to fp16 plus the fp16 bias as an fp16 add (forward).  A zero bias is the identity
-// in both (x + 0 rounds to x).
+// bf16(bias) as a bf16 add (FP8_OUT_BF16: forward_prequant, out + bias.to(bf16)) or the
+// bf16 rounded to fp16 plus the fp16 bias as an fp16 add (FP8_OUT_F16_VIA_BF16: the
+// row-wise forward).  A zero bias is the identity in both (x + 0 rounds to x).  The
+// per-tensor form (FP8_OUT_F16) does not run here: a third epilogue form does not fit
+// beside this kernel's 256 accumulators without spilling, so omni_fp8_gemm sends it to
+// the 256 x 128 kernel.
 template <bool OUT_BF16>
 __device__ __forceinline__ uint32_t fp8_out_bits(float v, half_t bias) {
   const uint32_t b = f32_to_bf16_bits(v);
@@ -493,7 +512,8 @@ __device__ __forceinline__ void fp8_big_epilogue(const f32x4 (&acc)[8][8], uint1
       const float sm = sap[16 * j];
       uint32_t bits[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) bits[q] = fp8_out_bits<OUT_BF16>((acc[i][j][q] * sm) * sn[q], bb[q]);
+      for (int q = 0; q < 4; ++q)
+        bits[q] = fp8_out_bits<OUT_BF16>((acc[i][j][q] * sm) * sn[q], bb[q]);
       uint2 pk;
       pk.x = bits[0] | (bits[1] << 16);
       pk.y = bits[2] | (bits[3] << 16);
@@ -634,7 +654,8 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_big_kernel(Fp8GemmArgs a) {
     const int nb = n0 + 128 * wn + 4 * g4;
     uint16_t* const ob = (uint16_t*)a.out + (int64_t)mb * a.ldo + nb;
     const float* const sap = a.sa + mb;
-    if (a.out_bf16) fp8_big_epilogue<true>(acc, ob, a.ldo, sap, a.sw + nb, has_bias ? a.bias + nb : nullptr);
+    // (FP8_OUT_F16 never reaches this kernel: only 0 and 1 here)
+    if (a.out_mode) fp8_big_epilogue<true>(acc, ob, a.ldo, sap, a.sw + nb, has_bias ? a.bias + nb : nullptr);
     else fp8_big_epilogue<false>(acc, ob, a.ldo, sap, a.sw + nb, has_bias ? a.bias + nb : nullptr);
   }
 }
@@ -652,8 +673,10 @@ static int num_cus() {
 }
 
 // Row-wise e4m3 quantisation: s[r] = amax_k |x[r, k]| / 448 (clamped below at clamp_min
-// when clamp_min > 0), q[r, k] = e4m3(x[r, k] / s[r]).  One workgroup per row.
-template <bool BF16>
+// when clamp_min > 0; rounded to fp16 when S16: FP8Linear's row-wise weight scale, an op on
+// the fp16 weight), q[r, k] = e4m3(x[r, k] / s[r]) (one rounding: fp32 division).  One
+// workgroup per row.
+template <bool BF16, bool S16 = false>
 __global__ __launch_bounds__(256) void fp8_quant_rows_kernel(const unsigned short* __restrict__ x,
                                                              int ldx, uint8_t* __restrict__ q,
                                                              float* __restrict__ s, int K,
@@ -672,6 +695,7 @@ __global__ __launch_bounds__(256) void fp8_quant_rows_kernel(const unsigned shor
   __syncthreads();
   amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   float sc = amax / 448.0f;
+  if (S16) sc = (float)(half_t)sc;
   if (clamp_min > 0.f) sc = fmaxf(sc, clamp_min);
   if (threadIdx.x == 0) s[row] = sc;
   for (int k = threadIdx.x * 8; k < K; k += 256 * 8) {
@@ -686,12 +710,13 @@ __global__ __launch_bounds__(256) void fp8_quant_rows_kernel(const unsigned shor
 }
 
 static int fp8_quant_rows_launch(const void* x, int ldx, void* xq, float* scale, int rows, int K,
-                                 float clamp_min, bool bf16, void* stream) {
+                                 float clamp_min, bool bf16, void* stream, bool s16 = false) {
   if (rows < 0 || K <= 0) return OMNI_EINVAL;
   if ((K & 7) || ldx < K || (ldx & 7)) return OMNI_EUNSUPPORTED;
   if (rows == 0) return OMNI_OK;
   if (!x || !xq || !scale) return OMNI_EINVAL;
-  auto kern = bf16 ? fp8_quant_rows_kernel<true> : fp8_quant_rows_kernel<false>;
+  auto kern = s16 ? fp8_quant_rows_kernel<false, true>
+                  : bf16 ? fp8_quant_rows_kernel<true> : fp8_quant_rows_kernel<false>;
   hipLaunchKernelGGL(kern, dim3(rows), dim3(256), 0, (hipStream_t)stream,
                      (const unsigned short*)x, ldx, (uint8_t*)xq, scale, K, clamp_min);
   OMNI_CHECK_LAUNCH();
@@ -708,13 +733,113 @@ extern "C" int omni_fp8_quant_rows_bf16(const void* x, int ldx, void* xq, float*
   return fp8_quant_rows_launch(x, ldx, xq, scale, rows, K, clamp_min, true, stream);
 }
 
+extern "C" int omni_fp8_quant_weight_rows(const void* w, int ldw, void* wq, float* scale, int N,
+                                          int K, void* stream) {
+  return fp8_quant_rows_launch(w, ldw, wq, scale, N, K, 0.f, false, stream, true);
+}
+
+// Per-tensor e4m3 quantisation (FP8Linear's default form): s = R(amax |x| / 448) and
+// q = e4m3(R(x / s)), R the input's own rounding (fp16, or bf16 for bf16 input): the
+// reference forms both with ops on the fp16 / bf16 tensor (fp8_linear.py:40-41, 87-89).
+// Two launches, no atomics: fp8_amax_kernel writes one partial maximum per workgroup
+// (rows b, b + grid, ...), fp8_quant_tensor_kernel reduces the grid's partials in every
+// workgroup and quantises the same rows, writing s into scale[r] for each of them.
+#define FP8_AMAX_GRID 256
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void fp8_amax_kernel(const unsigned short* __restrict__ x,
+                                                       int ldx, int rows, int K,
+                                                       float* __restrict__ part) {
+  __shared__ float red[4];
+  float amax = 0.f;
+  for (int r = blockIdx.x; r < rows; r += gridDim.x) {
+    const unsigned short* xr = x + (int64_t)r * ldx;
+    for (int k = threadIdx.x * 8; k < K; k += 256 * 8) {
+      const u16x8 v = *(const u16x8*)(xr + k);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(ld16f<BF16>(v[e])));
+    }
+  }
+  amax = wave_max(amax);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  if (threadIdx.x == 0) part[blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+template <bool BF16>
+__device__ __forceinline__ float round_in(float v) {
+  return BF16 ? bf16_value(v) : (float)(half_t)v;
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void fp8_quant_tensor_kernel(const unsigned short* __restrict__ x,
+                                                               int ldx, int rows, int K,
+                                                               const float* __restrict__ part,
+                                                               uint8_t* __restrict__ q,
+                                                               float* __restrict__ s) {
+#pragma clang fp contract(off)
+  __shared__ float red[4];
+  float amax = 0.f;
+  for (int i = threadIdx.x; i < (int)gridDim.x; i += 256) amax = fmaxf(amax, part[i]);
+  amax = wave_max(amax);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float sc = round_in<BF16>(amax / 448.0f);
+  for (int r = blockIdx.x; r < rows; r += gridDim.x) {
+    const unsigned short* xr = x + (int64_t)r * ldx;
+    if (threadIdx.x == 0) s[r] = sc;
+    for (int k = threadIdx.x * 8; k < K; k += 256 * 8) {
+      const u16x8 v = *(const u16x8*)(xr + k);
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        lo |= (uint32_t)f32_to_e4m3fn(round_in<BF16>(ld16f<BF16>(v[e]) / sc)) << (8 * e);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        hi |= (uint32_t)f32_to_e4m3fn(round_in<BF16>(ld16f<BF16>(v[4 + e]) / sc)) << (8 * e);
+      *(uint2*)(q + (int64_t)r * K + k) = make_uint2(lo, hi);
+    }
+  }
+}
+
+extern "C" int omni_fp8_quant_tensor_work(int rows) {
+  return rows <= 0 ? 0 : (rows < FP8_AMAX_GRID ? rows : FP8_AMAX_GRID);
+}
+
+extern "C" int omni_fp8_quant_tensor(const void* x, int ldx, void* q, float* scale, float* work,
+                                     int rows, int K, int bf16, void* stream) {
+  if (rows < 0 || K <= 0) return OMNI_EINVAL;
+  if ((K & 7) || ldx < K || (ldx & 7)) return OMNI_EUNSUPPORTED;
+  if (rows == 0) return OMNI_OK;
+  if (!x || !q || !scale || !work) return OMNI_EINVAL;
+  const int grid = omni_fp8_quant_tensor_work(rows);
+  if (bf16) {
+    hipLaunchKernelGGL(fp8_amax_kernel<true>, dim3(grid), dim3(256), 0, (hipStream_t)stream,
+                       (const unsigned short*)x, ldx, rows, K, work);
+    OMNI_CHECK_LAUNCH();
+    hipLaunchKernelGGL(fp8_quant_tensor_kernel<true>, dim3(grid), dim3(256), 0,
+                       (hipStream_t)stream, (const unsigned short*)x, ldx, rows, K, work,
+                       (uint8_t*)q, scale);
+  } else {
+    hipLaunchKernelGGL(fp8_amax_kernel<false>, dim3(grid), dim3(256), 0, (hipStream_t)stream,
+                       (const unsigned short*)x, ldx, rows, K, work);
+    OMNI_CHECK_LAUNCH();
+    hipLaunchKernelGGL(fp8_quant_tensor_kernel<false>, dim3(grid), dim3(256), 0,
+                       (hipStream_t)stream, (const unsigned short*)x, ldx, rows, K, work,
+                       (uint8_t*)q, scale);
+  }
+  OMNI_CHECK_LAUNCH();
+  return OMNI_OK;
+}
+
 // Kernel choice by shape: the 256 x 256 tiles serve the long-K shapes (K >= 4096, M and N
 // multiples of 256: the down projection, 8 % faster there; with K = 1536 they were 3-9 %
 // slower than the 256 x 128 tiles, measured on MI355X at M = 8192, outputs bit-equal); the
 // 8-wave pipelined 256 x 128 form every other shape with at least 4 K steps; the
 // double-buffered one-tile-per-workgroup kernel the rest (K < 512).
-static bool fp8_big_tiles(int M, int N, int K) {
-  return K >= 4096 && (N % F8B_T) == 0 && (M % F8B_T) == 0;
+static bool fp8_big_tiles(int M, int N, int K, int out_mode = FP8_OUT_F16_VIA_BF16) {
+  return K >= 4096 && (N % F8B_T) == 0 && (M % F8B_T) == 0 && out_mode != FP8_OUT_F16;
 }
 
 // Which kernel omni_fp8_gemm runs for a shape: 0 one tile per workgroup, 1 the pipelined
@@ -736,10 +861,11 @@ extern "C" int omni_fp8_gemm_plan(int M, int N, int K, int* grid) {
 
 extern "C" int omni_fp8_gemm(const void* xq, const float* sa, const void* wq, const float* sw,
                              const void* bias, void* out, int ldo, int M, int N, int K,
-                             int out_bf16, void* stream) {
+                             int out_mode, void* stream) {
   if (M < 0 || N <= 0 || K <= 0) return OMNI_EINVAL;
   if ((N % F8_BT) || (K % F8_BK)) return OMNI_EUNSUPPORTED;
   if (ldo < N || (ldo & 3)) return OMNI_EINVAL;
+  if (out_mode < FP8_OUT_F16_VIA_BF16 || out_mode > FP8_OUT_F16) return OMNI_EINVAL;
   if (M == 0) return OMNI_OK;
   if (!xq || !sa || !wq || !sw || !out) return OMNI_EINVAL;
   const int64_t tiles = (int64_t)ceil_div(M, F8_BT) * (N / F8_BT);
@@ -755,8 +881,8 @@ extern "C" int omni_fp8_gemm(const void* xq, const float* sa, const void* wq, co
   a.M = M;
   a.N = N;
   a.K = K;
-  a.out_bf16 = out_bf16;
-  if (fp8_big_tiles(M, N, K)) {                   // 256 x 256 tiles, one per workgroup
+  a.out_mode = out_mode;
+  if (fp8_big_tiles(M, N, K, out_mode)) {         // 256 x 256 tiles, one per workgroup
     const int grid = (M / F8B_T) * (N / F8B_T);
     hipLaunchKernelGGL((fp8_gemm_big_kernel<2>), dim3((unsigned)grid), dim3(256), 0,
                        (hipStream_t)stream, a);

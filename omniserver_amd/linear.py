@@ -440,17 +440,27 @@ class F16Linear(_Skinny):
 
 
 class FP8Linear(nn.Module):
-    """W8A8 e4m3fn linear with row-wise scales, FP8Linear's API (kernels/fp8_linear.py:66-126).
+    """W8A8 e4m3fn linear, FP8Linear's API (kernels/fp8_linear.py:66-126), in both of its
+    forms:
 
-    Weights are quantised on the device at construction: sw[n] = amax|W[n, :]|/448,
-    Wq = e4m3(W / sw).  ``forward(x)`` quantises x per token (quant_fp8, :45-63) and runs
-    the fp8 MFMA GEMM; the result is bf16((xq . Wq^T) * sa * sw) cast to fp16, plus the
-    bias.  ``forward_prequant(xq, scale)`` takes already-quantised rows (the output of
-    add_rms_norm_fp8) and returns the bf16 product, as the reference does (:99-108)."""
+    * per-tensor (``rowwise=False``, the reference's default and what apply_mixed builds):
+      one weight scale sw = fp16(amax |W| / 448), Wq = e4m3(fp16(W / sw)) (:87-90); the
+      forward quantises x with one dynamic scale, sa = fp16(amax |x| / 448),
+      xq = e4m3(fp16(x / sa)) (_quant_fp8_pertensor's eager branch, :40-41; bf16 input:
+      the same in bf16) and writes the fp16 product directly, plus the fp16 bias
+      (:119-125);
+    * row-wise (``rowwise=True``, fuse_norm_fp8's gate_up): sw[n] = fp16(amax_k |W[n, :]| /
+      448), Wq = e4m3(W / sw) (:83-86, an fp32 division); the forward quantises x per
+      token (quant_fp8, :45-63) and returns bf16((xq . Wq^T) * sa * sw) cast to fp16 plus
+      the bias (:115-118, 124-125); ``forward_prequant(xq, scale)`` takes rows already
+      quantised by add_rms_norm_fp8 and returns the bf16 product (:99-108).
+
+    Weights are quantised on the device at construction.  The scales are stored as an [N]
+    array either way (per-tensor: the one value repeated), the form the GEMM reads."""
 
     fmt = "fp8"
 
-    def __init__(self, weight: torch.Tensor, bias=None):
+    def __init__(self, weight: torch.Tensor, bias=None, rowwise: bool = False):
         super().__init__()
         N, K = weight.shape
         require_cuda(weight, dtype=torch.float16)
@@ -458,54 +468,87 @@ class FP8Linear(nn.Module):
             raise ValueError(f"FP8Linear needs N, K multiples of 128 (got {N}, {K})")
         dev = weight.device
         self.K, self.N = K, N
+        self.rowwise = bool(rowwise)
         w = weight.contiguous()
         self.register_buffer("weight_fp8", torch.empty(N, K, device=dev, dtype=torch.uint8))
         self.register_buffer("weight_scale", torch.empty(N, device=dev, dtype=torch.float32))
-        call("omni_fp8_quant_rows", ptr(w), K, ptr(self.weight_fp8), ptr(self.weight_scale), N, K,
-             0.0, stream())
+        if self.rowwise:
+            call("omni_fp8_quant_weight_rows", ptr(w), K, ptr(self.weight_fp8),
+                 ptr(self.weight_scale), N, K, stream())
+        else:
+            work = torch.empty(lib().omni_fp8_quant_tensor_work(N), device=dev,
+                               dtype=torch.float32)
+            call("omni_fp8_quant_tensor", ptr(w), K, ptr(self.weight_fp8), ptr(self.weight_scale),
+                 ptr(work), N, K, 0, stream())
         self.bias = None if bias is None else bias.to(device=dev, dtype=torch.float16).contiguous()
 
     @classmethod
-    def from_linear(cls, linear) -> "FP8Linear":
-        """From an fp16 linear (fp8_linear.py:93-97, rowwise): an nn.Linear-like module
-        (weight [N, K], bias) or an F16Linear (unpacked)."""
+    def from_linear(cls, linear, rowwise: bool = False) -> "FP8Linear":
+        """From an fp16 linear (fp8_linear.py:93-97): an nn.Linear-like module (weight
+        [N, K], bias) or an F16Linear (unpacked)."""
         w = linear.dense_weight() if hasattr(linear, "dense_weight") else linear.weight.data
-        return cls(w.to(torch.float16), getattr(linear, "bias", None))
+        return cls(w.to(torch.float16), getattr(linear, "bias", None), rowwise=rowwise)
 
     @property
     def out_features(self) -> int:
         return self.N
 
+    @property
+    def wq(self) -> torch.Tensor:
+        """The e4m3 weight codes [N, K] (the reference's ``wq`` buffer)."""
+        return self.weight_fp8.view(torch.float8_e4m3fn)
+
+    @property
+    def wscale(self) -> torch.Tensor:
+        """The reference's ``wscale``: [1, N] row-wise, a 0-dim scalar per-tensor."""
+        return self.weight_scale.view(1, -1) if self.rowwise else self.weight_scale[0]
+
     def quantize_input(self, x2d: torch.Tensor):
-        """quant_fp8 (fp8_linear.py:45-63) of fp16 or bf16 rows: (xq e4m3 bytes [M, K],
-        scale fp32 [M, 1])."""
+        """The forward's activation quantisation of fp16 or bf16 rows: (xq e4m3 bytes
+        [M, K], scale fp32 [M, 1]) - per token (quant_fp8, fp8_linear.py:45-63) for the
+        row-wise form, one value repeated for the per-tensor form (:40-41)."""
         M = x2d.shape[0]
         xq = torch.empty(M, self.K, device=x2d.device, dtype=torch.uint8)
         sa = torch.empty(M, 1, device=x2d.device, dtype=torch.float32)
-        fn = "omni_fp8_quant_rows_bf16" if x2d.dtype == torch.bfloat16 else "omni_fp8_quant_rows"
-        call(fn, ptr(x2d), x2d.stride(0), ptr(xq), ptr(sa), M, self.K, 0.0, stream())
+        bf16 = x2d.dtype == torch.bfloat16
+        if self.rowwise:
+            fn = "omni_fp8_quant_rows_bf16" if bf16 else "omni_fp8_quant_rows"
+            call(fn, ptr(x2d), x2d.stride(0), ptr(xq), ptr(sa), M, self.K, 0.0, stream())
+        else:
+            work = torch.empty(lib().omni_fp8_quant_tensor_work(M), device=x2d.device,
+                               dtype=torch.float32)
+            call("omni_fp8_quant_tensor", ptr(x2d), x2d.stride(0), ptr(xq), ptr(sa), ptr(work),
+                 M, self.K, int(bf16), stream())
         return xq, sa
 
-    def gemm_out(self, xq: torch.Tensor, sa: torch.Tensor, out: torch.Tensor, bf16: bool):
-        """bf16: the bf16 product plus bias.to(bf16) in bf16 (forward_prequant, :99-108);
-        else the bf16 product cast to fp16 plus the fp16 bias (forward, :115-124)."""
+    # omni_fp8_gemm's output forms
+    OUT_F16_VIA_BF16, OUT_BF16, OUT_F16 = 0, 1, 2
+
+    def gemm_out(self, xq: torch.Tensor, sa: torch.Tensor, out: torch.Tensor, mode: int):
+        """The scaled product into ``out`` in form ``mode``: OUT_BF16 the bf16 product plus
+        bias.to(bf16) in bf16 (forward_prequant, :99-108); OUT_F16_VIA_BF16 the bf16
+        product cast to fp16 plus the fp16 bias (row-wise forward, :115-118); OUT_F16 the
+        fp16 product plus the fp16 bias (per-tensor forward, :119-125)."""
         M = xq.shape[0]
         call("omni_fp8_gemm", ptr(xq), ptr(sa), ptr(self.weight_fp8), ptr(self.weight_scale),
-             ptr(self.bias), ptr(out), out.stride(0), M, self.N, self.K, int(bf16), stream())
+             ptr(self.bias), ptr(out), out.stride(0), M, self.N, self.K, int(mode), stream())
         return out
 
     def forward_prequant(self, xq: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+        if not self.rowwise:
+            raise ValueError("forward_prequant needs the row-wise form (fp8_linear.py:99-103: "
+                             "per-token activation scales with per-channel weight scales)")
         xq2 = xq.reshape(-1, self.K)
         if xq2.dtype == torch.float8_e4m3fn:
             xq2 = xq2.view(torch.uint8)
         xq2 = xq2.contiguous()
         out = torch.empty(xq2.shape[0], self.N, device=xq.device, dtype=torch.bfloat16)
-        self.gemm_out(xq2, scale.reshape(-1).contiguous().float(), out, True)
+        self.gemm_out(xq2, scale.reshape(-1).contiguous().float(), out, self.OUT_BF16)
         return out.reshape(*xq.shape[:-1], self.N)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        """fp16 or bf16 x (the bf16 silu_mul output of the fp8 MLP route, qwen2_llm.py:132-134)
-        -> fp16."""
+        """fp16 or bf16 x (the bf16 silu_mul output of the fused FP8 MLP route,
+        qwen2_llm.py:132-134) -> fp16."""
         x2d = x.reshape(-1, self.K)
         if not x2d.is_contiguous():
             x2d = x2d.contiguous()
@@ -514,7 +557,7 @@ class FP8Linear(nn.Module):
             raise TypeError(f"expected fp16 or bf16 activations, got {x2d.dtype}")
         xq, sa = self.quantize_input(x2d)
         out = torch.empty(x2d.shape[0], self.N, device=x.device, dtype=torch.float16)
-        self.gemm_out(xq, sa, out, False)
+        self.gemm_out(xq, sa, out, self.OUT_F16_VIA_BF16 if self.rowwise else self.OUT_F16)
         return out.reshape(*x.shape[:-1], self.N)
 
 

@@ -6,13 +6,16 @@ Operators are replaced by ``setattr`` on the reference's module paths
 ``Qwen2LLM.from_fp16`` model holds (F16Linear unpacks its weight for the conversion):
 
 * ``"fp16"`` keeps the module;
-* ``"fp8"``  FP8Linear (W8A8 e4m3, row-wise weight scale, dynamic per-token activation
-  scale, kernels/fp8_linear.py:66-126);
+* ``"fp8"``  FP8Linear in its default per-tensor form (W8A8 e4m3, one weight scale, one
+  dynamic activation scale, fp16 product; kernels/fp8_linear.py:66-126 via
+  FP8Linear.from_linear, mixed_precision.py:39-41);
 * ``"marlin"`` round-to-nearest int4 (uint4b8, group 128) as GPTQLinear, the reference's
   MarlinInt4Linear (marlin_linear.py:65-80).
 
 ``fuse_norm_fp8`` folds gate_up's activation quantisation into the post-attention norm
-(mixed_precision.py:53-75): gate_up becomes FP8 and the norm emits (e4m3, scale).
+(mixed_precision.py:53-73): gate_up becomes row-wise FP8 and the norm emits (e4m3 rows,
+per-token scale); a gate_up that is already per-tensor FP8 is refused, as the reference
+refuses it.
 Hadamard rotations ("+h") and the M-adaptive "fp8a" linear are not part of this build.
 """
 
@@ -41,7 +44,7 @@ def _replace(layer, op: str, prec: str) -> int:
     if prec == "fp8":
         if isinstance(lin, FP8Linear):       # already FP8 (e.g. by fuse_norm_fp8)
             return 0
-        new = FP8Linear.from_linear(lin)
+        new = FP8Linear.from_linear(lin)     # per-tensor, FP8Linear's default
     elif prec == "marlin":
         if isinstance(lin, GPTQLinear):
             return 0
@@ -66,11 +69,21 @@ def apply_mixed(model, plan: dict | None = None) -> dict:
 
 def fuse_norm_fp8(model) -> int:
     """gate_up as row-wise FP8 fed straight by the post-attention norm's per-token e4m3
-    output (mixed_precision.py:53-75); returns the number of layers fused."""
+    output (mixed_precision.py:53-73), called on the fp16 model; returns the number of
+    layers fused.  Raises ValueError, as the reference does (:69-70), for a gate_up that
+    is already per-tensor FP8, and for one that is neither fp16 nor row-wise FP8 (int4)."""
     n = 0
     for layer in model.layers:
-        if not isinstance(layer.mlp.gate_up_proj, FP8Linear):
-            layer.mlp.gate_up_proj = FP8Linear.from_linear(layer.mlp.gate_up_proj)
+        gu = layer.mlp.gate_up_proj
+        if isinstance(gu, FP8Linear):
+            if not gu.rowwise:
+                raise ValueError("gate_up is already per-tensor FP8; the fused norm needs a "
+                                 "row-wise gate_up: call fuse_norm_fp8 before quantising")
+        elif isinstance(gu, GPTQLinear):
+            raise ValueError("fuse_norm_fp8 needs an fp16 (or row-wise FP8) gate_up, "
+                             "not an int4 one")
+        else:
+            layer.mlp.gate_up_proj = FP8Linear.from_linear(gu, rowwise=True)
         layer.post_attention_layernorm.fp8_out = True
         n += 1
     return n

@@ -216,10 +216,21 @@ def rtn_int4(weight: torch.Tensor, group: int = 128):
 
 # --------------------------------------------------------------------------- fp8
 def fp8_weight_rowwise(weight: torch.Tensor):
-    """kernels/fp8_linear.py:83-86: sw[n] = amax_k |W[n, :]| / 448, Wq = e4m3(W / sw).
+    """kernels/fp8_linear.py:83-86 on the fp16 weight of the reference's ``.half()``
+    model: ``weight.abs().amax(1) / 448.0`` is an fp16 tensor op, so sw[n] =
+    fp16(amax_k |W[n, :]| / 448) (stored as fp32); ``weight / wscale`` with the [N, 1]
+    fp32 scale promotes to fp32, so Wq = e4m3(W / sw) rounds once.
     weight [N, K] (fp16 values) -> (wq e4m3 [N, K], sw [N] fp32)."""
-    sw = (weight.abs().amax(1, keepdim=True) / 448.0).float()
+    sw = r16(weight.abs().amax(1, keepdim=True) / 448.0)
     return (weight / sw).to(E4M3), sw.view(-1)
+
+
+def fp8_weight_pertensor(weight: torch.Tensor):
+    """kernels/fp8_linear.py:87-90 (FP8Linear's default form) on the fp16 weight:
+    sw = fp16(amax |W| / 448); ``weight / wscale`` with the 0-dim scale stays fp16, so
+    Wq = e4m3(fp16(W / sw)) (two roundings).  -> (wq e4m3 [N, K], sw 0-dim fp32)."""
+    sw = r16(weight.abs().max() / 448.0)
+    return r16(weight / sw).to(E4M3), sw
 
 
 def quant_fp8(x: torch.Tensor):
@@ -231,6 +242,36 @@ def quant_fp8(x: torch.Tensor):
 def rbf16(x: torch.Tensor) -> torch.Tensor:
     """Round fp32 values to bf16 and back."""
     return x.to(torch.bfloat16).to(torch.float32)
+
+
+def quant_fp8_pertensor(x: torch.Tensor, bf16: bool = False):
+    """_quant_fp8_pertensor's eager branch (kernels/fp8_linear.py:40-41, the one that runs
+    without vLLM) on an fp16 tensor (bf16=True: the bf16 silu_mul output): sa =
+    dtype(amax / 448) and q = e4m3(dtype(x / sa)), every op in the input's dtype.
+    -> (q e4m3 [M, K], sa 0-dim fp32)."""
+    rd = rbf16 if bf16 else r16
+    sa = rd(x.abs().max() / 448.0)
+    return rd(x / sa).to(E4M3), sa
+
+
+def fp8_linear_pertensor(xq, sa, wq, sw, bias=None):
+    """FP8Linear.forward, per-tensor (kernels/fp8_linear.py:119-125): _scaled_mm with
+    scalar scales and out_dtype fp16 = fp16((sum_k xq wq) * sa * sw) (fp32 accumulation,
+    scaled in that order as torch's _scaled_mm does), then ``out + bias`` in fp16."""
+    y = r16((xq.float() @ wq.float().t()) * sa * sw)
+    return y if bias is None else r16(y + bias)
+
+
+def fp8_linear(x, w, bf16_in: bool = False):
+    """An FP8Linear's forward on fp16 (or bf16) activations x, for w = (wq, sw) of either
+    form: per-tensor (0-dim sw, fp16 out) or row-wise (quant_fp8 per token, bf16 product
+    cast to fp16).  Returns fp32 holding fp16 values."""
+    wq, sw = w
+    if sw.dim() == 0:
+        xq, sa = quant_fp8_pertensor(x, bf16_in)
+        return fp8_linear_pertensor(xq, sa, wq, sw)
+    xq, sa = quant_fp8(x)
+    return fp8_linear_rowwise(xq, sa, wq, sw)
 
 
 def fp8_linear_prequant(xq, sa, wq, sw, bias=None):
@@ -320,8 +361,9 @@ class LayerWeights:
     o_t: torch.Tensor
     gate_up_t: torch.Tensor
     down_t: torch.Tensor
-    # the FP8 MLP route (kernels/mixed_precision.py fuse_norm_fp8 + plan gate_up/down fp8):
-    # (Wq e4m3 [N, K], sw [N]) of the row-wise FP8 gate_up / down, or None for fp16
+    # the FP8 MLP route (kernels/mixed_precision.py apply_mixed / fuse_norm_fp8):
+    # (Wq e4m3 [N, K], sw) of an FP8 gate_up / down - sw [N] row-wise, 0-dim per-tensor
+    # (FP8Linear's default, what apply_mixed builds) - or None for fp16
     fp8_gate_up: Optional[tuple] = None
     fp8_down: Optional[tuple] = None
     # fuse_norm_fp8 (mixed_precision.py:53-75): the post-attention norm emits e4m3 rows
@@ -367,21 +409,26 @@ class Qwen2Ref:
 
     def _post_norm_mlp(self, o, residual, lw: LayerWeights):
         """post_attention_layernorm + MLP (qwen2_llm.py:153-154, 123-134) with either linear
-        of the MLP optionally FP8 (FP8Linear, rowwise, fp8_linear.py:66-126):
-        * fused norm (norm_fp8, fuse_norm_fp8): add_rms_norm_fp8 quantises the normed rows
-          (fused_ops.py:74-91), gate_up.forward_prequant returns the bf16 product (:99-108),
-          silu_mul keeps bf16 (fused_ops.py:122-130 stores in its input dtype);
-        * otherwise the fp16 norm output, and an FP8 gate_up's forward quantises it per
-          token (quant_fp8, :45-63) and casts its bf16 product to fp16 (:115-118);
+        of the MLP optionally FP8 (FP8Linear, fp8_linear.py:66-126, per-tensor or row-wise):
+        * fused norm (norm_fp8, fuse_norm_fp8, which makes gate_up row-wise):
+          add_rms_norm_fp8 quantises the normed rows (fused_ops.py:74-91),
+          gate_up.forward_prequant returns the bf16 product (:99-108), silu_mul keeps bf16
+          (fused_ops.py:122-130 stores in its input dtype);
+        * otherwise the fp16 norm output goes to gate_up's forward (fp8_linear);
         the down projection takes the activation as it comes: an FP8 one quantises it (bf16
-        or fp16), an fp16 one gets it cast to fp16 (qwen2_llm.py:132-133)."""
+        or fp16, qwen2_llm.py:132-134), an fp16 one gets it cast to fp16 (:132-133)."""
         c = self.cfg
+        bf16_act = False
         if lw.fp8_gate_up is not None and lw.norm_fp8:
+            if lw.fp8_gate_up[1].dim() == 0:
+                raise ValueError("the fused norm feeds a row-wise FP8 gate_up only "
+                                 "(mixed_precision.py:69-70)")
             xq, sa, residual = add_rms_norm_fp8(o, residual, lw.post_norm, c.rms_norm_eps)
             gu = fp8_linear_prequant(xq, sa, *lw.fp8_gate_up)
             n = gu.shape[-1] // 2
             g, u = gu[..., :n], gu[..., n:]
             act = rbf16(g * torch.sigmoid(g) * u)
+            bf16_act = True
         else:
             h, residual = add_rms_norm(o, residual, lw.post_norm, c.rms_norm_eps, self.f16)
             if lw.fp8_gate_up is None:
@@ -389,13 +436,11 @@ class Qwen2Ref:
                     return self._mlp(h, lw), residual
                 gu = linear(h, lw.gate_up_t, None, self.f16)
             else:
-                xq, sa = quant_fp8(h)
-                gu = fp8_linear_rowwise(xq, sa, *lw.fp8_gate_up)
+                gu = fp8_linear(h, lw.fp8_gate_up)
             act = silu_mul(gu, self.f16)
         if lw.fp8_down is None:
             return linear(r16(act), lw.down_t, None, self.f16), residual
-        xq, sa = quant_fp8(act)
-        return fp8_linear_rowwise(xq, sa, *lw.fp8_down), residual
+        return fp8_linear(act, lw.fp8_down, bf16_act), residual
 
     def lm_head(self, h):
         return r16(h @ self.embed.t(), self.f16)

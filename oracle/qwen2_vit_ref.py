@@ -15,7 +15,11 @@ torch's float64 library routines, QuickGELU against its closed form with the
 roundings placed by hand, the rotary against complex multiplication and its
 invariants, the patch positions against a per-patch loop of the window order, the
 segmented attention against per-image float64 softmax attention and the
-block-diagonal mask form, and the whole tower against its own fp64 evaluation.
+block-diagonal mask form; the composition (stage order, residuals, merger) against the
+reference's own Qwen2VIT.forward run on the CPU (tests/golden/ref_vit.npz), stage by
+stage and end to end.  vLLM's varlen flash attention (the reference's attention core) is
+not in this image: the oracle's exact softmax stands in for it, so its rounding inside
+the attention stays unpinned.
 """
 
 from __future__ import annotations

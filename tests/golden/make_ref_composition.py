@@ -51,6 +51,15 @@ def _torch_fused_ops(FO):
     FO.rms_norm, FO.add_rms_norm, FO.silu_mul = rms_norm, add_rms_norm, silu_mul
 
 
+def _tap_value(t):
+    """A tapped tensor as a 2-D numpy array: float32 values (e4m3 codes as their float
+    values); an (e4m3 rows, scale) tuple as the codes' values followed by the scale column."""
+    if isinstance(t, tuple):
+        q, s = t
+        return np.concatenate([_tap_value(q), _tap_value(s)], axis=1)
+    return t.reshape(-1, t.shape[-1]).float().numpy().copy()
+
+
 class _UpdateOnly:
     """The decode view with only the transformers-cache ``update`` visible."""
 
@@ -81,13 +90,30 @@ def _hf_state_dict(w):
     return sd
 
 
-def run(dtype, M, KV, positions_fn, decode_positions):
+def default_taps(model, tap):
+    """Layer 0's o_proj input (attention output) and output, MLP input / output and
+    down_proj input (SiLU-mul output)."""
+    lay0 = model.layers[0]
+    lay0.self_attn.o_proj.register_forward_hook(tap("attn", "in"))
+    lay0.self_attn.o_proj.register_forward_hook(tap("o", "out"))
+    lay0.mlp.register_forward_hook(tap("mlp_in", "in"))
+    lay0.mlp.register_forward_hook(tap("mlp_out", "out"))
+    lay0.mlp.down_proj.register_forward_hook(tap("act", "in"))
+
+
+def run(dtype, M, KV, positions_fn, decode_positions, prepare=None, register_taps=default_taps):
+    """The case's prompts and decode steps through the reference's forward.  ``prepare``
+    (if given) rewrites the loaded fp16 model before it runs (e.g. an FP8 plan);
+    ``register_taps(model, tap)`` installs the forward hooks whose values are kept for the
+    first prompt's prefill and the first decode step."""
     cfg = M.Qwen2Config(hidden_size=C.HIDDEN, num_layers=C.LAYERS, num_heads=C.HEADS,
                         num_kv_heads=C.KV_HEADS, head_dim=C.HEAD_DIM,
                         intermediate_size=C.INTER, vocab_size=C.VOCAB, rms_norm_eps=C.EPS,
                         rope_theta=C.THETA, mrope_section=list(C.SECTIONS))
     model = M.Qwen2LLM(cfg).half()               # models/qwen2_vl.py:50
     M.load_from_hf(model, _hf_state_dict(C.weights()))
+    if prepare is not None:
+        prepare(model)
     model.eval()
     pool = KV(C.LAYERS, 3, C.KV_HEADS, C.MAX_LEN, C.HEAD_DIM, "cpu", dtype)
     out = {}
@@ -99,15 +125,12 @@ def run(dtype, M, KV, positions_fn, decode_positions):
         def hook(mod, inp, res):
             if tap_on["tag"] is not None:
                 t = inp[0] if which == "in" else res
-                taps[f"{tap_on['tag']}_{name}"] = t.reshape(-1, t.shape[-1]).float().numpy().copy()
+                taps[f"{tap_on['tag']}_{name}"] = _tap_value(t)
         return hook
 
-    lay0 = model.layers[0]
-    lay0.self_attn.o_proj.register_forward_hook(tap("attn", "in"))
-    lay0.self_attn.o_proj.register_forward_hook(tap("o", "out"))
-    lay0.mlp.register_forward_hook(tap("mlp_in", "in"))
-    lay0.mlp.register_forward_hook(tap("mlp_out", "out"))
-    lay0.mlp.down_proj.register_forward_hook(tap("act", "in"))
+    tap.record = lambda name, t: (taps.__setitem__(f"{tap_on['tag']}_{name}", _tap_value(t))
+                                  if tap_on["tag"] is not None else None)
+    register_taps(model, tap)
     prefill, deltas = [], []
     with torch.no_grad():
         for slot, (ids, img, grids) in enumerate(C.prompts()):

@@ -115,9 +115,10 @@ def record_sampled_logits(runner):
 
 def oracle_with_plan(w, shape, plan: dict, f16=True, norm_fp8=False) -> ref.Qwen2Ref:
     """The fp16 decoder's oracle with per-op precision applied as the reference's
-    mixed_precision / quantize_llm_marlin would: "fp8" MLP linears take the FP8 route
-    (row-wise e4m3 weights; with ``norm_fp8`` the post-attention norm quantises for the FP8
-    gate_up, fuse_norm_fp8), "marlin" linears use the RTN int4 dequantised weights."""
+    mixed_precision / quantize_llm_marlin would: "fp8" MLP linears take the FP8 route as
+    apply_mixed builds them (per-tensor e4m3 weights, FP8Linear's default; with
+    ``norm_fp8`` the gate_up is row-wise and fed by the post-attention norm's e4m3 rows,
+    fuse_norm_fp8), "marlin" linears use the RTN int4 dequantised weights."""
     orc = oracle_from_fp16(w, shape, f16)
     for lw, src in zip(orc.layers, w["layers"]):
         lw.norm_fp8 = norm_fp8
@@ -129,7 +130,9 @@ def oracle_with_plan(w, shape, plan: dict, f16=True, norm_fp8=False) -> ref.Qwen
             elif prec == "fp8":
                 if op not in ("gate_up", "down"):
                     raise ValueError("the oracle's FP8 route covers the MLP linears")
-                setattr(lw, "fp8_" + op, ref.fp8_weight_rowwise(src[key].float()))
+                rowwise = norm_fp8 and op == "gate_up"
+                quant = ref.fp8_weight_rowwise if rowwise else ref.fp8_weight_pertensor
+                setattr(lw, "fp8_" + op, quant(src[key].float()))
     if any(plan.get(op) == "marlin" for op in ("qkv", "o")):
         orc.bias_after_round = True
     return orc

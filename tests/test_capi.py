@@ -127,6 +127,17 @@ def test_bad_arguments_rejected_before_launch(so):
                                  None, 1, 16, 1, 12, 2, 64, 16, 24, 24, None) == -2
     assert L.omni_mrope_kv_write(None, 2048, None, None, None, None, None, 16, None, None, None,
                                  None, 1, 16, 1, 12, 2, 128, 16, 24, 20, None) == -2
+    # fp8: an output form past the three; per-tensor quantisation without its workspace or
+    # with K not whole 8-element chunks; the workspace is one float per workgroup (<= 256)
+    assert L.omni_fp8_gemm(fake_ptr(), fake_ptr(), fake_ptr(), fake_ptr(), None, fake_ptr(),
+                           256, 8, 256, 256, 3, None) == -1
+    assert L.omni_fp8_quant_tensor(fake_ptr(), 256, fake_ptr(), fake_ptr(), None, 8, 256, 0,
+                                   None) == -1
+    assert L.omni_fp8_quant_tensor(fake_ptr(), 260, fake_ptr(), fake_ptr(), fake_ptr(), 8, 250,
+                                   0, None) == -2
+    assert L.omni_fp8_quant_weight_rows(None, 256, None, None, -1, 256, None) == -1
+    assert [L.omni_fp8_quant_tensor_work(r) for r in (0, 1, 255, 256, 100000)] == [0, 1, 255,
+                                                                                  256, 256]
     # zero-size work is a no-op success
     assert L.omni_silu_mul(None, None, 0, 8960, None) == 0
     assert L.omni_gemm_slices(8960, 10) == 10 and L.omni_gemm_slices(1536, 7) == 6

@@ -75,7 +75,7 @@ def test_fp8_config4_linear(gpu, name, M, K, N, bias):
     W = f16((N, K), 400 + N % 97, 0.02)
     b = f16((N,), 401, 0.02) if bias else None
     x = f16((M, K), 402 + K % 89)
-    lin = FP8Linear(W.to(gpu), None if b is None else b.to(gpu))
+    lin = FP8Linear(W.to(gpu), None if b is None else b.to(gpu), rowwise=True)
     y = lin(x.to(gpu)).cpu()
     torch.cuda.synchronize()
     wq, sw = ref.fp8_weight_rowwise(W.float())
@@ -119,7 +119,7 @@ def test_fp8_prequant_bias_bf16(gpu):
     w = torch.ones(H, dtype=torch.float16)
     W = f16((N, H), 412, 0.02)
     b = f16((N,), 413, 0.05)
-    lin = FP8Linear(W.to(gpu), b.to(gpu))
+    lin = FP8Linear(W.to(gpu), b.to(gpu), rowwise=True)
     q, s, _ = F.add_rms_norm_fp8(x.to(gpu), r.to(gpu), w.to(gpu), 1e-6)
     y = lin.forward_prequant(q, s)
     torch.cuda.synchronize()

@@ -905,6 +905,48 @@ def test_fp8_quant_rows_bit_exact(gpu):
     assert torch.equal(q.cpu(), eq.view(torch.uint8))
 
 
+def test_fp8_quant_weight_rows_bit_exact(gpu):
+    """FP8Linear's row-wise weight form (fp8_linear.py:83-86): scale = fp16(amax / 448)
+    (an op on the fp16 weight), codes = e4m3(w / scale), bit-exact."""
+    from omniserver_amd._lib import call, ptr, stream
+    say("fp8 row-wise weight quantisation")
+    N, K = 300, 1536
+    w = f16((N, K), 148, 0.02)
+    w[7] = 0.25                                   # constant row
+    wg = w.to(gpu)
+    q = torch.empty(N, K, device=gpu, dtype=torch.uint8)
+    s = torch.empty(N, device=gpu, dtype=torch.float32)
+    call("omni_fp8_quant_weight_rows", ptr(wg), K, ptr(q), ptr(s), N, K, stream())
+    torch.cuda.synchronize()
+    eq, es = ref.fp8_weight_rowwise(w.float())
+    assert torch.equal(s.cpu(), es)
+    assert torch.equal(q.cpu(), eq.view(torch.uint8))
+
+
+@pytest.mark.parametrize("rows,K,bf16", [(1, 384, False), (37, 1536, False), (300, 1536, True),
+                                         (1000, 8960, False), (2000, 384, True)])
+def test_fp8_quant_tensor_bit_exact(gpu, rows, K, bf16):
+    """Per-tensor quantisation (_quant_fp8_pertensor's eager branch, fp8_linear.py:40-41;
+    the per-tensor weight form :87-89): one scale R(amax / 448) over the whole tensor (an
+    outlier placed in one row), codes e4m3(R(x / s)), R the input's rounding; bit-exact,
+    also past the 256 rows one workgroup of the amax pass covers."""
+    from omniserver_amd._lib import call, lib, ptr, stream
+    say(f"fp8 per-tensor quantisation rows={rows} K={K} bf16={bf16}")
+    x = f16((rows, K), 150 + rows % 17, 1.5)
+    x[rows // 2, K // 3] = -37.0
+    xt = x.to(torch.bfloat16) if bf16 else x
+    xg = xt.to(gpu)
+    q = torch.empty(rows, K, device=gpu, dtype=torch.uint8)
+    s = torch.empty(rows, device=gpu, dtype=torch.float32)
+    work = torch.empty(lib().omni_fp8_quant_tensor_work(rows), device=gpu, dtype=torch.float32)
+    call("omni_fp8_quant_tensor", ptr(xg), K, ptr(q), ptr(s), ptr(work), rows, K, int(bf16),
+         stream())
+    torch.cuda.synchronize()
+    eq, es = ref.quant_fp8_pertensor(xt.float(), bf16=bf16)
+    assert torch.equal(s.cpu(), es.expand(rows))
+    assert torch.equal(q.cpu(), eq.view(torch.uint8))
+
+
 def fp8_abs_product(xq, sa, wq, sw):
     """|xq| . |wq|^T * sa * sw: the scale of the terms each output sums."""
     return (xq.float().abs() @ wq.float().abs().t()) * sa.view(-1, 1) * sw.view(1, -1)
@@ -924,7 +966,7 @@ def test_fp8_linear_matches_oracle(gpu, M, N, K, bias):
     W = f16((N, K), 141, 0.02)
     b = f16((N,), 142, 0.02) if bias else None
     x = f16((M, K), 143)
-    lin = FP8Linear(W.to(gpu), None if b is None else b.to(gpu))
+    lin = FP8Linear(W.to(gpu), None if b is None else b.to(gpu), rowwise=True)
     y = lin(x.to(gpu))
     torch.cuda.synchronize()
     wq, sw = ref.fp8_weight_rowwise(W.float())
@@ -942,6 +984,84 @@ def test_fp8_linear_matches_oracle(gpu, M, N, K, bias):
     assert (d == 0).float().mean().item() > 0.95
 
 
+@pytest.mark.parametrize("M,N,K,bias,bf16", [(1, 256, 1536, False, False),
+                                              (100, 2048, 1536, True, False),
+                                              (256, 1536, 8960, False, True),
+                                              (512, 1280, 4096, True, False)])
+def test_fp8_linear_pertensor_matches_oracle(gpu, M, N, K, bias, bf16):
+    """FP8Linear's default per-tensor form (fp8_linear.py:87-90, 119-125): weight and
+    activation codes and scales bit-exact, the fp16 product (+ fp16 bias) within one fp16
+    step plus the MFMA's reduced intermediate precision (see test_fp8_linear_matches_oracle)."""
+    from omniserver_amd.linear import FP8Linear
+    say(f"fp8 per-tensor linear M={M} N={N} K={K} bias={bias} bf16 input={bf16}")
+    W = f16((N, K), 161, 0.02)
+    b = f16((N,), 162, 0.02) if bias else None
+    x = f16((M, K), 163)
+    xt = x.to(torch.bfloat16) if bf16 else x
+    lin = FP8Linear(W.to(gpu), None if b is None else b.to(gpu))
+    assert not lin.rowwise
+    xq_g, sa_g = lin.quantize_input(xt.to(gpu))
+    y = lin(xt.to(gpu))
+    torch.cuda.synchronize()
+    assert y.dtype == torch.float16
+    wq, sw = ref.fp8_weight_pertensor(W.float())
+    assert torch.equal(lin.weight_fp8.cpu(), wq.view(torch.uint8))
+    assert torch.equal(lin.weight_scale.cpu(), sw.expand(N))
+    assert torch.equal(lin.wscale.cpu(), sw)
+    xq, sa = ref.quant_fp8_pertensor(xt.float(), bf16=bf16)
+    assert torch.equal(xq_g.cpu(), xq.view(torch.uint8))
+    assert torch.equal(sa_g.cpu().view(-1), sa.expand(M))
+    e = ref.fp8_linear_pertensor(xq, sa, wq, sw, None if b is None else b.float())
+    e0 = ref.fp8_linear_pertensor(xq, sa, wq, sw, None)
+    d = (y.cpu().float() - e).abs()
+    tol = (e0.abs() + e.abs()) * 2.0 ** -10 + fp8_abs_product(xq, sa, wq, sw) * 2.0 ** -14
+    assert (d <= tol + 1e-6).all(), (d - tol).max().item()
+    # an fp16 result has 3 more bits than the bf16 of the row-wise form, so the MFMA's
+    # reduced intermediate precision shows as a last-bit difference more often (93 % of
+    # the outputs bit-equal measured at M = 1)
+    assert (d == 0).float().mean().item() > 0.85
+
+
+def test_fp8_linear_matches_reference_fixture(gpu):
+    """FP8Linear in both forms against the reference's own FP8Linear outputs
+    (tests/golden/ref_fp8_route.npz, written on the CPU by make_ref_vit_fp8.py): weight
+    codes and scales bit for bit; forward (fp16 and bf16 input, with and without bias) and
+    forward_prequant within the bounds of the oracle tests above."""
+    import os
+    import sys
+    import numpy as np
+    from omniserver_amd.linear import FP8Linear
+    golden = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+    sys.path.insert(0, golden)
+    import fp8_case as P
+    g = np.load(os.path.join(golden, "ref_fp8_route.npz"))
+    say("fp8 linear vs the reference's FP8Linear outputs")
+    w, b, x = P.linear_case()
+    W, B, X = w.half().to(gpu), b.half().to(gpu), x.half().to(gpu)
+    for tag, rowwise in (("pt", False), ("rw", True)):
+        lin = FP8Linear(W, B, rowwise=rowwise)
+        nb = FP8Linear(W, None, rowwise=rowwise)
+        assert np.array_equal(lin.weight_fp8.cpu().numpy(), g[f"{tag}_wq"])
+        assert np.array_equal(lin.wscale.cpu().reshape(-1).numpy(), g[f"{tag}_wscale"])
+        # one step of the stored product's rounding (fp16 per-tensor, bf16 row-wise), the
+        # bias rounding, and the MFMA's reduced intermediate precision (2^-10 of the
+        # largest output bounds 2^-14 of any output's summed term magnitudes here)
+        step = 2.0 ** -10 if tag == "pt" else 2.0 ** -7
+        for key, got in ((f"{tag}_out", lin(X)), (f"{tag}_out_nobias", nb(X)),
+                         (f"{tag}_out_bf16in", lin(X.bfloat16()))):
+            want = torch.tensor(g[key])
+            d = (got.cpu().float() - want).abs()
+            tol = want.abs() * (step + 2.0 ** -10) + 2.0 ** -10 * want.abs().max() + 1e-6
+            assert (d <= tol).all(), (key, (d - tol).max().item())
+            assert (d == 0).float().mean().item() > 0.9, key
+    rw = FP8Linear(W, B, rowwise=True)
+    xq = torch.tensor(g["rw_xq"]).to(gpu)
+    s = torch.tensor(g["rw_xscale"]).to(gpu)
+    got = rw.forward_prequant(xq, s).cpu().float()
+    want = torch.tensor(g["rw_prequant"])
+    assert (got - want).abs().max().item() <= 2.0 ** -6 * want.abs().max().item()
+
+
 def test_fp8_prequant_chain(gpu):
     """add_rms_norm_fp8 -> FP8Linear.forward_prequant (the reference MLP's fp8 route,
     qwen2_llm.py:130-134) returns the bf16 product of the norm-quantised rows."""
@@ -952,7 +1072,7 @@ def test_fp8_prequant_chain(gpu):
     x, r = f16((M, H), 144), f16((M, H), 145)
     w = (1 + 0.1 * torch.randn(H, generator=torch.Generator().manual_seed(146))).half()
     W = f16((N, H), 147, 0.02)
-    lin = FP8Linear(W.to(gpu))
+    lin = FP8Linear(W.to(gpu), rowwise=True)
     q, s, nr = F.add_rms_norm_fp8(x.to(gpu), r.to(gpu), w.to(gpu), 1e-6)
     y = lin.forward_prequant(q, s)
     torch.cuda.synchronize()

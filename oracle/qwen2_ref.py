@@ -308,10 +308,17 @@ def linear(x, w_t, bias=None, f16=True, bias_after_round=False):
 
 
 # --------------------------------------------------------------------------- attention
-def decode_attention(q, k_pool, v_pool, rows, kv_len, scale, f16=True):
+def decode_attention(q, k_pool, v_pool, rows, kv_len, scale, f16=True, p16=False):
     """cache/kv_prealloc.py:272-290 semantics in the SDPA + repeat_interleave form of
     model/qwen2_llm.py:105-113: per token b and head h,
     softmax(scale * q[b,h] . K[rows[b], 0:kv_len[b], h // G]^T) . V[...] (fp32 softmax).
+
+    ``p16`` places one more rounding where a flash kernel has it (the published
+    FlashAttention-2 algorithm, which vLLM's flash_attn_varlen_func follows: the
+    unnormalised probabilities exp(s - max) are cast to fp16 for the P.V product, their
+    sum stays fp32); the block-wise running maximum of a real kernel is not modelled (the
+    row's maximum is used), so this is one member of the family of roundings the
+    reference's flash path can produce, not its bits.
 
     q [n, nh, hd]; k_pool/v_pool [P, max_len, nkv, hd]; returns [n, nh, hd]."""
     n, nh, hd = q.shape
@@ -323,8 +330,12 @@ def decode_attention(q, k_pool, v_pool, rows, kv_len, scale, f16=True):
         k = k_pool[int(rows[b]), :L].transpose(0, 1).repeat_interleave(rep, 0)  # [nh, L, hd]
         v = v_pool[int(rows[b]), :L].transpose(0, 1).repeat_interleave(rep, 0)
         s = torch.einsum("hd,hld->hl", q[b], k) * scale
-        p = torch.softmax(s, dim=-1)
-        out[b] = torch.einsum("hl,hld->hd", p, v)
+        if p16:
+            e = torch.exp(s - s.max(-1, keepdim=True).values)
+            out[b] = torch.einsum("hl,hld->hd", r16(e), v) / e.sum(-1, keepdim=True)
+        else:
+            p = torch.softmax(s, dim=-1)
+            out[b] = torch.einsum("hl,hld->hd", p, v)
     return r16(out, f16)
 
 
@@ -379,13 +390,15 @@ class Qwen2Ref:
 
     def __init__(self, cfg: Qwen2Config, embed: torch.Tensor, final_norm: torch.Tensor,
                  layers: List[LayerWeights], gptq_bias_after_round: bool = False,
-                 f16: bool = True):
+                 f16: bool = True, attn_p16: bool = False):
         self.cfg = cfg
         self.embed = embed          # [V, H] (tied lm_head, qwen2_llm.py:167-168)
         self.final_norm = final_norm
         self.layers = layers
         self.bias_after_round = gptq_bias_after_round
         self.f16 = f16
+        # decode attention with the flash kernel's fp16 probabilities (decode_attention p16)
+        self.attn_p16 = attn_p16
 
     # -- pieces
     def _attn_in(self, x, lw: LayerWeights, pos3):
@@ -472,7 +485,7 @@ class Qwen2Ref:
                 k_pool[i][b, int(wpos[b])] = k[b]
                 v_pool[i][b, int(wpos[b])] = v[b]
             a = decode_attention(q, k_pool[i], v_pool[i], torch.arange(n), wpos + 1, scale,
-                                 self.f16)
+                                 self.f16, self.attn_p16)
             o = linear(a.reshape(n, -1), lw.o_t, None, self.f16)
             x, residual = self._post_norm_mlp(o, residual, lw)
         h, _ = add_rms_norm(x, residual, self.final_norm, c.rms_norm_eps, self.f16)

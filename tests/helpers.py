@@ -10,7 +10,7 @@ import torch
 from oracle import qwen2_ref as ref
 
 
-def oracle_from_fp16(w, shape, f16=True) -> ref.Qwen2Ref:
+def oracle_from_fp16(w, shape, f16=True, attn_p16=False) -> ref.Qwen2Ref:
     cfg = ref.Qwen2Config(hidden_size=shape.hidden_size, num_layers=len(w["layers"]),
                           num_heads=shape.num_heads, num_kv_heads=shape.num_kv_heads,
                           head_dim=shape.head_dim, intermediate_size=shape.intermediate_size,
@@ -20,7 +20,7 @@ def oracle_from_fp16(w, shape, f16=True) -> ref.Qwen2Ref:
         qkv_t=l["qkv_w"].float().t().contiguous(), qkv_b=l["qkv_b"].float(),
         o_t=l["o_w"].float().t().contiguous(), gate_up_t=l["gate_up_w"].float().t().contiguous(),
         down_t=l["down_w"].float().t().contiguous()) for l in w["layers"]]
-    return ref.Qwen2Ref(cfg, w["embed"].float(), w["norm"].float(), layers, False, f16)
+    return ref.Qwen2Ref(cfg, w["embed"].float(), w["norm"].float(), layers, False, f16, attn_p16)
 
 
 def oracle_from_gptq(w, shape, f16=True) -> ref.Qwen2Ref:

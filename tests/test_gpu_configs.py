@@ -1,16 +1,17 @@
 """BASELINE.json configs at their real sizes on the GPU, against the CPU oracle.
 
 * config 3 (the north star): W4A16 GPTQ decoder, all 28 layers, B = 32, 2048-token
-  contexts in a [33, 4096, 2, 128] pool: one decode step's logits against both oracle
-  modes (fp16-faithful and exact fp32), row by row (_full_depth_check: the 2e-2 bar
-  against the exact result wherever the reference's own fp16 rounding sequence meets it),
-  greedy ids equal on every row whose margin exceeds twice the measured error.
+  contexts in a [33, 4096, 2, 128] pool, through the runner the bench times: one eager
+  decode step's logits against the oracle, row by row (_full_depth_check: 2e-2 from the
+  fp16-faithful oracle, or the reference's own rounding family's spread on the rows where
+  that is wider), greedy ids equal on every row whose margin exceeds twice the measured
+  error; then 5 graph-replayed steps, every token checked teacher-forced.
 * config 1: fp16 decoder, 28 layers, B = 1, a 256-token prompt, prefill then 32 greedy
   steps through the hipGraph runner; every emitted token is checked against the oracle fed
   the same tokens (teacher forcing), wherever the oracle's margin exceeds twice the
   measured prefill logit error.
 * config 2: fp16 decoder, 28 layers, B = 16, contexts U[512, 2048] in a [17, 4096, 2, 128]
-  pool: one decode step, checked as config 3.
+  pool: one decode step, checked as config 3's eager step.
 * config 5: 8 image + text prompts (64 text, 256 N(0,1) vision rows, 192 text) packed into
   T = 4096 rows with 3-D M-RoPE positions, prefill (the pipelined GEMMs at M = 4096 and the
   block-diagonal causal attention) then 8 greedy int4 decode steps at B = 8, on 2 layers
@@ -54,36 +55,56 @@ def _fill_pool_device(pool, lengths, seed, gpu):
     return kp, vp
 
 
-def _full_depth_check(logits, out, e16, e32, label):
-    """Full-depth logits against both oracle modes.  The fp16-faithful oracle (the
-    reference's storage roundings, exact attention) is itself ``noise`` away from the exact
-    fp32 result: at 28 layers of fp16 weights ~2e-2 on every row, with int4 weights a few
-    1e-3 except on rows whose values sit near rounding boundaries.  The GPU's computation
-    order (fp32 accumulation order, attention probabilities rounded to fp16 as the
-    reference's flash path rounds them) is another sample of the same rounding noise, so it
-    can be as far from the fp16 oracle as both are from exact.  Bar: the GPU's distance from
-    the exact result within max(2e-2, 1.5 x the largest noise of the batch) on every row and
-    its median over rows within 1.25 x the oracle's median noise (+1e-3): it is no noisier
-    than the reference's own rounding sequence.  Cosine >= 0.9999 against both modes;
-    greedy ids equal the exact argmax where its margin exceeds twice the GPU's error.  The
-    distance from the fp16 oracle and the rows within 2e-2 of it are printed."""
+def _full_depth_check(logits, out, e16, e32, ep16, label):
+    """Full-depth logits against the fp16-faithful oracle, row by row.
+
+    The reference's path is a family of rounding sequences, not one: its fp16 storage
+    points are fixed, but its attention (vLLM flash) rounds the probabilities to fp16 for
+    the P.V product and sums in its own order.  Three members are evaluated here: ``e16``
+    (fp16 storage, exact softmax), ``ep16`` (the same with the probabilities rounded to
+    fp16 where a flash kernel rounds them) and ``e32`` (no fp16 rounding).  At 28 layers
+    any last-bit difference is amplified to ~2e-2 of the logits (on the CPU, rounding the
+    probabilities alone moves config 2's fp16 oracle by 0.0217 max-abs, median 0.019), so
+    a row's bar is 2e-2 or, where the family itself spreads wider on that row,
+    1.25 x that row's spread (the largest distance between two members): the GPU is held
+    to be as close to the fp16-faithful oracle as the reference's own roundings are to
+    each other.  Also: cosine >= 0.9999 against every member; the median row within
+    1.25 x the median spread + 1e-3; greedy ids equal the exact argmax wherever its margin
+    exceeds twice the GPU's error.  Rows needing the wider bar are printed."""
     g = logits.float().cpu()
-    d16 = (g - e16).abs().max(1).values
-    d32 = (g - e32).abs().max(1).values
-    noise = (e16 - e32).abs().max(1).values
+    row = lambda a, b: (a - b).abs().max(1).values
+    d16, d32, dp = row(g, e16), row(g, e32), row(g, ep16)
+    fam = torch.stack([row(e16, e32), row(ep16, e32), row(e16, ep16)]).max(0).values
     cos = lambda a, b: torch.nn.functional.cosine_similarity(a, b, dim=-1).min().item()
-    c16, c32 = cos(g, e16), cos(g, e32)
-    bar = max(2e-2, 1.5 * noise.max().item())
+    c16, c32, cp = cos(g, e16), cos(g, e32), cos(g, ep16)
+    bar = torch.clamp(1.25 * fam, min=2e-2)
     say(f"{label}: max-abs gpu-f16oracle {d16.max():.4f} (rows within 2e-2: "
-        f"{int((d16 <= 2e-2).sum())}/{len(d16)}), gpu-f32 {d32.max():.4f} (median "
-        f"{d32.median():.4f}), f16oracle-f32 {noise.max():.4f} (median {noise.median():.4f}); "
-        f"cos {c16:.6f} / {c32:.6f}")
-    assert c16 >= 0.9999 and c32 >= 0.9999, (c16, c32)
-    assert (d32 <= bar).all(), (d32.max().item(), bar)
-    assert d32.median() <= 1.25 * noise.median() + 1e-3, (d32.median(), noise.median())
+        f"{int((d16 <= 2e-2).sum())}/{len(d16)}), gpu-f16oracle(fp16 P) {dp.max():.4f}, "
+        f"gpu-f32 {d32.max():.4f} (median {d32.median():.4f}); reference-family spread "
+        f"max {fam.max():.4f} (median {fam.median():.4f}); cos {c16:.6f} / {cp:.6f} / {c32:.6f}")
+    for r in range(len(d16)):
+        if d16[r] > 2e-2:
+            say(f"{label}:   row {r}: gpu-f16oracle {d16[r]:.4f} > 2e-2, family spread "
+                f"{fam[r]:.4f} -> bar {bar[r]:.4f}")
+    assert min(c16, c32, cp) >= 0.9999, (c16, cp, c32)
+    assert (d16 <= bar).all(), [(r, d16[r].item(), bar[r].item()) for r in range(len(d16))
+                                if d16[r] > bar[r]]
+    assert d32.median() <= 1.25 * fam.median() + 1e-3, (d32.median(), fam.median())
     decisive = check_ids(out, e32, d32.max().item())
     say(f"{label}: greedy ids equal on {decisive}/{len(d16)} decisive rows")
     return decisive
+
+
+def _oracle_members(orc16, orc32, ids, kp, vp, lens):
+    """e16, e32, ep16 for one decode step, and the exact oracle's pools after it (kp / vp
+    are left holding the step's K/V rows as the fp16-faithful oracle writes them)."""
+    k32, v32 = [k.clone() for k in kp], [v.clone() for v in vp]
+    e32 = orc32.decode_step(ids, k32, v32, lens.clone())
+    orc16.attn_p16 = True
+    ep16 = orc16.decode_step(ids, [k.clone() for k in kp], [v.clone() for v in vp], lens.clone())
+    orc16.attn_p16 = False
+    e16 = orc16.decode_step(ids, kp, vp, lens.clone())
+    return e16, e32, ep16, (k32, v32)
 
 
 def _one_step(gpu, model, pool, orc, lengths, ids, label):
@@ -95,26 +116,43 @@ def _one_step(gpu, model, pool, orc, lengths, ids, label):
     return out, logits
 
 
-def test_config3_full_step(gpu):
+def test_config3_full_step_and_graph_stream(gpu):
+    """Config 3 through the runner the bench times (W4A16, 28 layers, B = 32, 2048-token
+    contexts, hipGraph step): one eager step's logits against the oracle family
+    (_full_depth_check), then 5 graph-replayed steps (runners/multimodal.py:306-313,
+    342-357), whose first tokens must equal the eager step's and whose every later token
+    is checked, teacher-forced, against the exact oracle wherever its margin exceeds twice
+    the measured error."""
     from omniserver_amd import synth
-    from omniserver_amd.kv_cache import PreallocatedKVCache
-    from omniserver_amd.qwen2_llm import Qwen2LLM
-    B, ctx = 32, 2048
-    say(f"config 3: int4, 28 layers, B={B}, ctx {ctx}, pool [{B + 1}, 4096, 2, 128]")
+    from omniserver_amd.request import Request, SamplingParams, Sequence
+    from omniserver_amd.runner import NativeQwenVLRunner
+    B, ctx, steps = 32, 2048, 5
+    say(f"config 3: int4, 28 layers, B={B}, ctx {ctx}, pool [{B + 1}, 4096, 2, 128]; "
+        f"1 eager + {steps} graph steps")
     shape = synth.DecoderShape()
     w = synth.gptq_decoder(shape, seed=0)
-    model = Qwen2LLM.from_gptq(w, shape, gpu, max_pos=8192)
-    pool = PreallocatedKVCache(28, B + 1, 2, 4096, 128, gpu, n_heads=12)
+    runner = NativeQwenVLRunner(max_running=B, max_len=4096, use_graph=True, quant="gptq",
+                                weights=w)
+    model, pool = runner.adapter.model, runner.pool
     lengths = [ctx] * B
     kp, vp = _fill_pool_device(pool, lengths, 31, gpu)
-    ids = synth.random_ids(B, shape.vocab_size, 0, "c3ids")
-    out, logits = _one_step(gpu, model, pool, None, lengths, ids, "config 3")
+    kp = [torch.cat([k, torch.zeros(B + 1, steps + 2, 2, 128)], 1) for k in kp]
+    vp = [torch.cat([v, torch.zeros(B + 1, steps + 2, 2, 128)], 1) for v in vp]
+    seqs = []
+    for b in range(B):
+        ids = synth.random_ids(8, shape.vocab_size, 0, f"c3p{b}").tolist()
+        sq = Sequence(Request(prompt=ids, sampling=SamplingParams(max_new_tokens=1 << 20)))
+        runner.tokenize(sq)
+        sq.request.sampling.stop_token_ids.clear()
+        seqs.append(sq)
+    runner.attach_prefilled(seqs, lengths)
+    ids0 = torch.tensor([sq.last_token_id() for sq in seqs], dtype=torch.int64)
+    out, logits = _one_step(gpu, model, pool, None, lengths, ids0, "config 3")
     lens = torch.tensor(lengths + [0])
-    e32 = oracle_from_gptq(w, shape, f16=False).decode_step(
-        ids.tolist(), [k.clone() for k in kp], [v.clone() for v in vp], lens.clone())
-    orc = oracle_from_gptq(w, shape, f16=True)
+    orc32 = oracle_from_gptq(w, shape, f16=False)
+    orc16 = oracle_from_gptq(w, shape, f16=True)
     del w
-    e16 = orc.decode_step(ids.tolist(), kp, vp, lens.clone())
+    e16, e32, ep16, (kp32, vp32) = _oracle_members(orc16, orc32, ids0.tolist(), kp, vp, lens)
     # the new K/V rows of the first layer (before any depth has accumulated) and the last
     dk0 = (pool.k[0][:B, ctx].float().cpu() - kp[0][:B, ctx]).abs().max().item()
     assert dk0 <= 2e-2, dk0
@@ -122,8 +160,32 @@ def test_config3_full_step(gpu):
         dk = (pool.k[l][:B, ctx].float().cpu() - kp[l][:B, ctx]).abs().max().item()
         dv = (pool.v[l][:B, ctx].float().cpu() - vp[l][:B, ctx]).abs().max().item()
         say(f"config 3: layer {l} new K/V rows max-abs {dk:.4f} / {dv:.4f}")
-    decisive = _full_depth_check(logits, out, e16, e32, "config 3")
+    decisive = _full_depth_check(logits, out, e16, e32, ep16, "config 3")
     assert decisive >= B // 2
+    err = (logits.float().cpu() - e32).abs().max().item()
+    del orc16, kp, vp
+
+    # the graph stream: the eager step above wrote the same K/V rows the first replay
+    # writes and left the lengths alone
+    for _ in range(steps):
+        runner.decode(seqs)
+    runner.settle()
+    stream = torch.tensor([sq.output_token_ids[:steps] for sq in seqs])      # [B, steps]
+    assert torch.equal(stream[:, 0], out.cpu()), "graph step 0 != eager step"
+    compared = int((ref.top2_margin(e32) > 2 * err + 1e-3).sum())
+    lens32 = lens.clone()
+    lens32[:B] += 1                     # kp32 / vp32 hold step 0's K/V rows already
+    for i in range(1, steps):
+        lg = orc32.decode_step(stream[:, i - 1].tolist(), kp32, vp32, lens32.clone())
+        lens32[:B] += 1
+        margin = ref.top2_margin(lg)
+        decisive = margin > 2 * err + 1e-3
+        bad = (lg.argmax(-1) != stream[:, i]) & decisive
+        assert not bad.any(), (i, bad.nonzero().flatten().tolist())
+        compared += int(decisive.sum())
+    say(f"config 3 graph stream: {compared}/{B * steps} tokens compared (exact-oracle margin "
+        f"> {2 * err + 1e-3:.4f}), all equal")
+    assert compared >= B * steps // 2, compared
 
 
 def test_config1_greedy_32_steps(gpu):
@@ -167,11 +229,11 @@ def test_config2_ragged_step(gpu):
     ids = synth.random_ids(B, shape.vocab_size, 2, "c2ids")
     out, logits = _one_step(gpu, model, pool, None, lengths, ids, "config 2")
     lens = torch.tensor(lengths + [0])
-    e32 = oracle_from_fp16(w, shape, f16=False).decode_step(
-        ids.tolist(), [k.clone() for k in kp], [v.clone() for v in vp], lens.clone())
-    e16 = oracle_from_fp16(w, shape, f16=True).decode_step(ids.tolist(), kp, vp, lens.clone())
+    e16, e32, ep16, _ = _oracle_members(oracle_from_fp16(w, shape, f16=True),
+                                        oracle_from_fp16(w, shape, f16=False), ids.tolist(),
+                                        kp, vp, lens)
     del w
-    decisive = _full_depth_check(logits, out, e16, e32, "config 2")
+    decisive = _full_depth_check(logits, out, e16, e32, ep16, "config 2")
     assert decisive >= B // 2
 
 

@@ -358,14 +358,14 @@ def _swap_kv(monkeypatch):
 def _remap_heads_attention():
     orig = ref.decode_attention
 
-    def bad(q, k_pool, v_pool, rows, kv_len, scale, f16=True):
+    def bad(q, k_pool, v_pool, rows, kv_len, scale, f16=True, p16=False):
         n, nh, hd = q.shape
         nkv = k_pool.shape[2]
         out = torch.empty(n, nh, hd)
         for h in range(nh):                       # head h reads kv head h % nkv
             g = h % nkv
             out[:, h:h + 1] = orig(q[:, h:h + 1], k_pool[:, :, g:g + 1], v_pool[:, :, g:g + 1],
-                                   rows, kv_len, scale, f16)
+                                   rows, kv_len, scale, f16, p16)
         return out
     return bad
 

@@ -1433,7 +1433,8 @@ extern "C" int omni_lmhead_argmax_noalloc(const void* x, int ldx, const void* we
   if (!x || !weight_packed || !ids_out) return OMNI_EINVAL;
   if (M > 64 || (N & 31)) return OMNI_EUNSUPPORTED;
   const int grid = omni_lmhead_argmax_grid(N);
-  if ((int64_t)grid * M > NOALLOC_SLOTS) return OMNI_EUNSUPPORTED;   // beyond the array
+  // beyond the array: only on a part with more than 512 CUs (one workgroup per CU)
+  if ((int64_t)grid * M > NOALLOC_SLOTS) return OMNI_EUNSUPPORTED;
   int dev = 0;
   const hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return (int)e;

@@ -292,13 +292,18 @@ class GPTQLinear(_Skinny):
     # always streams the int4 words.  Without it, from UNPACK_ROWS rows the weights are
     # unpacked into a per-device scratch on every call (~23 us per layer at 2B).  The copy is
     # of the weights as they are at that first call: a linear whose packed weights are
-    # rewritten afterwards calls release_f16() first.
+    # rewritten afterwards calls release_f16() (which also retires captured prefill graphs).
     UNPACK_ROWS = 2048
     F16_ROWS = 256
     keep_f16 = True
 
     def release_f16(self) -> None:
-        """Drop the resident fp16 expansion (made again at the next large prefill)."""
+        """Drop the resident fp16 expansion (made again at the next large prefill).  Graphs
+        captured over it would launch on freed memory: the release advances
+        ``weights_epoch()``, which graph owners compare before a replay."""
+        global _WEIGHTS_EPOCH
+        if getattr(self, "_w16", None) is not None:
+            _WEIGHTS_EPOCH += 1
         self._w16 = None
 
     def _prefill_f16(self, M: int) -> torch.Tensor | None:
@@ -437,6 +442,15 @@ class F16Linear(_Skinny):
         call("omni_f16_gemm_attn", ptr(states), splits, n_kv, group, ptr(self.weight_packed),
              ptr(self.bias), None, 0, ptr(partial), M, self.N, self.K, epilogue, ksplit, preset,
              stream())
+
+
+# Advanced whenever a linear frees device memory that a captured graph may launch on
+# (GPTQLinear.release_f16); the runner's prefill graphs are dropped when it moves.
+_WEIGHTS_EPOCH = 0
+
+
+def weights_epoch() -> int:
+    return _WEIGHTS_EPOCH
 
 
 class FP8Linear(nn.Module):

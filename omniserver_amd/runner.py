@@ -37,6 +37,7 @@ import torch
 
 from .hostio import to_device
 from .kv_cache import PreallocatedKVCache
+from .linear import weights_epoch
 from .request import Sequence, Status
 
 
@@ -116,6 +117,7 @@ class MultimodalRunner(ModelRunner):
         self._kv_len: List[int] = []          # host mirror of pool.lengths for active slots
         self._graphs: Dict[int, tuple] = {}
         self._prefill_graphs: Dict[tuple, dict] = {}
+        self._prefill_epoch = weights_epoch()
         self._graphs_sampled: Dict[int, tuple] = {}
         self._eager: Dict[int, dict] = {}
         self._dev_ids_for = None              # batch whose next ids already sit on device
@@ -230,13 +232,17 @@ class MultimodalRunner(ModelRunner):
 
     def drop_prefill_graphs(self) -> None:
         """Forget the captured prefill graphs.  They launch on the device addresses of the
-        weights they were captured with (including the GPTQ linears' resident fp16
-        expansions), so call this after rewriting or releasing weights."""
+        weights they were captured with, so call this after replacing weight tensors (a
+        GPTQ linear's release_f16 is noticed by itself: see _prefill_graphed)."""
         self._prefill_graphs.clear()
 
     def _prefill_graphed(self, packed, pos, slots, seg_lens):
         key = tuple(int(L) for L in seg_lens)
         graphs = self._prefill_graphs
+        epoch = weights_epoch()
+        if epoch != self._prefill_epoch:         # a resident fp16 expansion was released
+            graphs.clear()
+            self._prefill_epoch = epoch
         ent = graphs.pop(key, None)
         dev = self.device
         if ent is not None:

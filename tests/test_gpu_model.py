@@ -658,3 +658,25 @@ def test_prefill_graph_equals_eager(gpu):
         for r, ss in zip(runners, seqs):
             r.decode(list(ss.values()))
     phase("decode after the replays")
+    # 300 rows: the GPTQ linears' resident fp16 expansions are made and captured
+    phase("first prefill of [200, 100]", new=[("e0", 200), ("e1", 100)],
+          free=["img2", "img3"])
+    phase("replay of [200, 100]", new=[("f0", 200), ("f1", 100)], free=["e0", "e1"])
+    # the weights rewritten in place (layers 0 and 1 swap their linears' packed words) and
+    # the expansions released, as GPTQLinear's comment asks: the next prefill of the same
+    # layout must use the new weights, not replay a graph over the freed expansions
+    from omniserver_amd.linear import GPTQLinear
+    for r in runners:
+        l0, l1 = r.adapter.model.layers
+        for name in ("qkv_proj", "o_proj", "gate_up_proj", "down_proj"):
+            a, b = getattr(l0, name), getattr(l1, name)
+            assert isinstance(a, GPTQLinear) and a._w16 is not None
+            for buf in ("qweight_packed", "scales_packed"):
+                ta, tb = getattr(a, buf), getattr(b, buf)
+                tmp = ta.clone()
+                ta.copy_(tb)
+                tb.copy_(tmp)
+            a.release_f16()
+            b.release_f16()
+    phase("[200, 100] after the weights were rewritten", new=[("g0", 200), ("g1", 100)],
+          free=["f0", "f1"])

@@ -370,6 +370,43 @@ def _prefill_ms(r, make_seqs, reps: int):
     return sorted(ts)[len(ts) // 2], seqs
 
 
+def _prefill_eager_ms(r, make_seqs, reps: int):
+    """_prefill_ms with the runner's prefill graphs off: every prefill runs eagerly, as the
+    first prefill of a segment layout does (a serving engine rarely repeats a layout)."""
+    keep = r.prefill_graph_layouts
+    r.prefill_graph_layouts = 0
+    try:
+        ms, seqs = _prefill_ms(r, make_seqs, reps)
+    finally:
+        r.prefill_graph_layouts = keep
+    for s_ in seqs:
+        r.free(s_)
+    return ms
+
+
+def _f16_expansion(r) -> dict:
+    """The GPTQ linears' resident fp16 expansions the int4 prefill runs on: their bytes, and
+    the device time of making them all again (omni_w4_unpack_f16, CUDA events around the
+    launches into a scratch buffer), which the first large prefill pays once."""
+    from omniserver_amd._lib import call, ptr, stream
+    from omniserver_amd.linear import GPTQLinear
+    lins = [m for m in r.adapter.model.modules() if isinstance(m, GPTQLinear)]
+    nbytes = sum(2 * m.N * m.K for m in lins if getattr(m, "_w16", None) is not None)
+    buf = torch.empty(max(m.N * m.K for m in lins), device=r.device, dtype=torch.float16)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for m in lins:
+        call("omni_w4_unpack_f16", ptr(m.qweight_packed), ptr(m.scales_packed), ptr(buf), m.K,
+             m.N, stream())
+    e1.record()
+    torch.cuda.synchronize()
+    del buf
+    int4 = sum(m.qweight_packed.numel() * 4 + m.scales_packed.numel() * 2 for m in lins)
+    return {"prefill_f16_resident_bytes": int(nbytes), "int4_weight_bytes": int(int4),
+            "prefill_f16_unpack_ms": round(e0.elapsed_time(e1), 3)}
+
+
 def _config1_runner(w16):
     """configs[0]'s runner and prompt maker: fp16, batch 1, a 256-token prompt."""
     from omniserver_amd import synth
@@ -419,16 +456,20 @@ def prefill_only(device) -> dict:
     from omniserver_amd import synth
     shape = synth.DecoderShape()
     r, mk = _config1_runner(synth.fp16_decoder(shape, seed=1))
+    c1e = _prefill_eager_ms(r, mk, 5)
     c1, _ = _prefill_ms(r, mk, 5)
     del r
     torch.cuda.empty_cache()
     r, mk = _config5_runner(device, synth.gptq_decoder(shape, seed=0))
+    c5e = _prefill_eager_ms(r, mk, 3)
     c5, _ = _prefill_ms(r, mk, 3)
     fl = _prefill_flops(4096, 8, 512)
     return {"metric": "prefill ms (BASELINE configs[0] and [4])", "config1_prefill_ms": round(c1, 3),
-            "config5_prefill_ms": round(c5, 3),
+            "config1_prefill_eager_ms": round(c1e, 3),
+            "config5_prefill_ms": round(c5, 3), "config5_prefill_eager_ms": round(c5e, 3),
             "config5_prefill_tflops": round(fl / (c5 * 1e-3) / 1e12, 1),
-            "config5_prefill_frac_fp16_peak": round(fl / (c5 * 1e-3) / PEAK_FP16, 4)}
+            "config5_prefill_frac_fp16_peak": round(fl / (c5 * 1e-3) / PEAK_FP16, 4),
+            **_f16_expansion(r)}
 
 
 def baseline_configs(device, w_int4) -> dict:
@@ -448,10 +489,14 @@ def baseline_configs(device, w_int4) -> dict:
 
     # fp16, batch 1, 256-token prompt, 32 new tokens (prefill: median of 5)
     r, mk1 = _config1_runner(w16)
+    eager_ms = _prefill_eager_ms(r, mk1, 5)
     pre_ms, seqs = _prefill_ms(r, mk1, 5)
     per, rep, ctx0 = _timed_decode(r, seqs, 32)
     out["config1"] = {"workload": "fp16 decoder, B=1, 256-token prompt, 32 greedy steps",
-                      "prefill_ms": round(pre_ms, 3), **_decode_line("fp16", per, rep, ctx0, 32)}
+                      "prefill_ms": round(pre_ms, 3), "prefill_eager_ms": round(eager_ms, 3),
+                      "prefill_note": "prefill_ms: graph replay of a captured segment layout; "
+                                      "prefill_eager_ms: every prefill eager (a new layout)",
+                      **_decode_line("fp16", per, rep, ctx0, 32)}
     del r, seqs
 
     # fp16, batch 16, contexts U[512, 2048], pool [16, 4096], 64 steps
@@ -478,6 +523,7 @@ def baseline_configs(device, w_int4) -> dict:
     # prefill (T = 4096, block-diagonal causal; median of 3), then 128 greedy steps at B = 8
     B = 8
     r, mk5 = _config5_runner(device, w_int4, B)
+    eager5 = _prefill_eager_ms(r, mk5, 3)
     pre_ms5, seqs = _prefill_ms(r, mk5, 3)
     pre = pre_ms5 * 1e-3
     T = 512 * B
@@ -485,9 +531,17 @@ def baseline_configs(device, w_int4) -> dict:
     per, rep, ctx0 = _timed_decode(r, seqs, 128)
     out["config5"] = {"workload": "int4 decoder, 8 x 512-token image+text prompts: packed prefill "
                                   "(T = 4096), then 128 greedy steps at B = 8",
-                      "prefill_ms": round(pre * 1e3, 3), "prefill_tok_per_s": round(T / pre, 1),
+                      "prefill_ms": round(pre * 1e3, 3), "prefill_eager_ms": round(eager5, 3),
+                      "prefill_tok_per_s": round(T / pre, 1),
                       "prefill_tflops": round(fl / pre / 1e12, 1),
                       "prefill_frac_fp16_peak": round(fl / pre / PEAK_FP16, 4),
+                      "prefill_eager_frac_fp16_peak": round(fl / (eager5 * 1e-3) / PEAK_FP16, 4),
+                      "prefill_note": "the int4 linears' prefill GEMMs run on a resident fp16 "
+                                      "expansion of their weights, made at the first prefill of "
+                                      ">= 256 rows (prefill_f16_unpack_ms, outside the timed "
+                                      "prefills) and kept (prefill_f16_resident_bytes beside "
+                                      "int4_weight_bytes); decode streams the int4 words",
+                      **_f16_expansion(r),
                       "prefill_gemm_mfma_busy_pct_counters": mfma_from_profiles("int4 prefill M=4096"),
                       **_decode_line("gptq", per, rep, ctx0, 128)}
     del r, seqs

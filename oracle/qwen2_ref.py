@@ -339,9 +339,10 @@ def decode_attention(q, k_pool, v_pool, rows, kv_len, scale, f16=True, p16=False
     return r16(out, f16)
 
 
-def prefill_attention(q, k, v, seg_lens, scale, f16=True):
+def prefill_attention(q, k, v, seg_lens, scale, f16=True, p16=False):
     """cache/kv_prealloc.py:181-203: causal attention inside each packed segment.
-    q [T, nh, hd], k/v [T, nkv, hd] -> [T, nh, hd]."""
+    q [T, nh, hd], k/v [T, nkv, hd] -> [T, nh, hd].  ``p16``: the probabilities rounded to
+    fp16 for the P.V product as a flash kernel rounds them (see decode_attention)."""
     T, nh, hd = q.shape
     rep = nh // k.shape[1]
     out = torch.empty(T, nh, hd)
@@ -353,8 +354,12 @@ def prefill_attention(q, k, v, seg_lens, scale, f16=True):
         s = torch.einsum("hid,hjd->hij", qs, ks) * scale
         mask = torch.ones(L, L, dtype=torch.bool).tril()
         s = s.masked_fill(~mask, float("-inf"))
-        p = torch.softmax(s, dim=-1)
-        out[off:off + L] = torch.einsum("hij,hjd->hid", p, vs).transpose(0, 1)
+        if p16:
+            e = torch.exp(s - s.max(-1, keepdim=True).values)
+            o = torch.einsum("hij,hjd->hid", r16(e), vs) / e.sum(-1, keepdim=True)
+        else:
+            o = torch.einsum("hij,hjd->hid", torch.softmax(s, dim=-1), vs)
+        out[off:off + L] = o.transpose(0, 1)
         off += L
     return r16(out, f16)
 
@@ -397,7 +402,7 @@ class Qwen2Ref:
         self.layers = layers
         self.bias_after_round = gptq_bias_after_round
         self.f16 = f16
-        # decode attention with the flash kernel's fp16 probabilities (decode_attention p16)
+        # attention with the flash kernel's fp16 probabilities (decode_attention p16)
         self.attn_p16 = attn_p16
 
     # -- pieces
@@ -514,7 +519,7 @@ class Qwen2Ref:
                 k_pool[i][slot, :L] = k[off:off + L]
                 v_pool[i][slot, :L] = v[off:off + L]
                 off += L
-            a = prefill_attention(q, k, v, seg_lens, scale, self.f16)
+            a = prefill_attention(q, k, v, seg_lens, scale, self.f16, self.attn_p16)
             o = linear(a.reshape(a.shape[0], -1), lw.o_t, None, self.f16)
             x, residual = self._post_norm_mlp(o, residual, lw)
         last = torch.tensor(np.cumsum(seg_lens) - 1)

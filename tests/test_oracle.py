@@ -16,7 +16,8 @@ pinned by something independent of how it is written:
                             (image t=64, h=w=64+0..15, text resumes at 80, delta -240);
                             two images; product implementation equal
   gptq pack/dequant         bit-level brute force with Python ints; round trip
-  decode_attention          float64 brute-force softmax loops
+  decode_attention          float64 brute-force softmax loops; the fp16-probability option
+                            exact where every probability is a power of two
   prefill_attention         brute force; last token of a segment == decode over it
   fp8 linear                torch._scaled_mm (library GEMM) on the same fp8 operands;
                             both FP8Linear forms and the FP8 MLP routes against the
@@ -219,6 +220,46 @@ def test_prefill_attention_causal_and_consistent_with_decode():
     kp[0, :3], vp[0, :3] = k[5:], v[5:]
     d = ref.decode_attention(q[7:8], kp, vp, torch.tensor([0]), torch.tensor([3]), 0.25, f16=False)
     assert torch.allclose(out[7], d[0], atol=1e-6)
+
+
+def test_attention_fp16_probabilities_option():
+    """The flash-rounding option of both attentions (p16): where every unnormalised
+    probability exp(s - max) is a power of two (scores integer multiples of ln 2) the fp16
+    rounding is exact and the result equals the exact softmax; on generic scores it moves
+    each output by at most one fp16 rounding of each probability (relative 2^-11 of the
+    sum of |p v|)."""
+    L, hd = 9, 128
+    ln2 = math.log(2.0)
+    # q = e_0 * c, k_j = e_0 * (-j ln2 / c) / scale: scores s_j = -j ln 2
+    scale, c = 0.25, 2.0
+    q = torch.zeros(1, 1, hd)
+    q[0, 0, 0] = c
+    k = torch.zeros(1, L + 1, 1, hd)
+    for j in range(L):
+        k[0, j, 0, 0] = -j * ln2 / (c * scale)
+    v = rnd((1, L + 1, 1, hd), 60)
+    ex = ref.decode_attention(q, k, v, torch.tensor([0]), torch.tensor([L]), scale, f16=False)
+    p16 = ref.decode_attention(q, k, v, torch.tensor([0]), torch.tensor([L]), scale, f16=False,
+                               p16=True)
+    assert torch.allclose(ex, p16, rtol=1e-6, atol=1e-7)
+    # generic scores: within one fp16 rounding per probability
+    q2 = rnd((3, 4, hd), 61, 0.3)
+    k2 = rnd((3, 40, 2, hd), 62)
+    v2 = rnd((3, 40, 2, hd), 63)
+    lens = torch.tensor([40, 17, 1])
+    a = ref.decode_attention(q2, k2, v2, torch.arange(3), lens, 0.1, f16=False)
+    b = ref.decode_attention(q2, k2, v2, torch.arange(3), lens, 0.1, f16=False, p16=True)
+    bound = 2.0 ** -11 * 4.0         # |v| <~ 4: sum_j p_j |v_j| <= max |v|
+    assert (a - b).abs().max().item() <= bound and not torch.equal(a, b)
+    # the prefill form: the last query of a segment is the decode form over it
+    qs, ks, vs = rnd((6, 4, hd), 64, 0.3), rnd((6, 2, hd), 65), rnd((6, 2, hd), 66)
+    pf = ref.prefill_attention(qs, ks, vs, [6], 0.1, f16=False, p16=True)
+    kp = torch.zeros(1, 6, 2, hd)
+    vp = torch.zeros(1, 6, 2, hd)
+    kp[0], vp[0] = ks, vs
+    dc = ref.decode_attention(qs[5:6], kp, vp, torch.tensor([0]), torch.tensor([6]), 0.1,
+                              f16=False, p16=True)
+    assert torch.allclose(pf[5], dc[0], atol=1e-6)
 
 
 # ----------------------------------------------------------------------------- fp8

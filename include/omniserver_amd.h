@@ -189,6 +189,19 @@ int omni_prefill_attention_gqa(const void* q, int q_stride, const void* k_cache,
                                int nqb, void* out, int out_stride, int n_heads, int n_kv_heads,
                                int head_dim, float scale, void* stream);
 
+/* The omni_prefill_attention_gqa attention (qblocks counts <= 32, n_heads / n_kv_heads
+ * <= 6) with each workgroup's key tiles split between two groups of four waves, the second
+ * group's normalised output (rounded to fp16) and softmax state merged into the first's in
+ * LDS: the longest (last) blocks of a segment take half as many tile steps.  Agrees with
+ * omni_prefill_attention to that fp16 rounding (replaces the same
+ * cache/kv_prealloc.py:181-203 call); -2 for n_heads / n_kv_heads > 6. */
+int omni_prefill_attention_gqa_halves(const void* q, int q_stride, const void* k_cache,
+                                      const void* v_cache, int pool_rows, int max_len,
+                                      const int64_t* slots, const int64_t* kv_len,
+                                      const int* qblocks, int nqb, void* out, int out_stride,
+                                      int n_heads, int n_kv_heads, int head_dim, float scale,
+                                      void* stream);
+
 /* ---------------------------------------------------------------- linears */
 
 /* Epilogues of the skinny GEMMs. */

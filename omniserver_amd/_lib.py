@@ -58,6 +58,8 @@ SIGNATURES = {
                               _P],
     "omni_prefill_attention_gqa": [_P, _I, _P, _P, _I, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I,
                                    _F, _P],
+    "omni_prefill_attention_gqa_halves": [_P, _I, _P, _P, _I, _I, _P, _P, _P, _I, _P, _I, _I,
+                                          _I, _I, _F, _P],
     "omni_prefill_attention": [_P, _I, _P, _P, _I, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _F,
                                _P],
     "omni_prefill_attention_split": [_P, _I, _P, _P, _I, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I,

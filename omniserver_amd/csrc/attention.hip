@@ -932,13 +932,23 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_split_kernel(PrefillArgs 
 // so the two kernels agree bit for bit.  K tiles are stored with their 16-byte chunks
 // XOR-swizzled by row (the A-operand reads of 16 rows then spread over the banks); V tiles
 // as the decode kernel stages them, for the transposed B-operand reads.
-template <int HPW>
-__global__ __launch_bounds__(256, 1) void prefill_attn_gqa_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) half_t ks_lds[2][ATT_BLK * ATT_HD];
-  __shared__ __attribute__((aligned(16))) half_t vs_lds[2][ATT_BLK * ATT_VSTRIDE];
+// HALVES = 2: the block's key tiles are split between two groups of 4 waves (tiles
+// [0, ceil(n/2)) and the rest), each with its own LDS tiles, so the longest blocks' tile
+// loop is half as long and two waves share each SIMD; the second group hands its
+// normalised output (fp16) and softmax state through LDS to the first, which merges.
+// Tile 0 (key 0, visible to every row) is always in the first group.
+template <int HPW, int HALVES>
+__global__ __launch_bounds__(256 * HALVES, 1) void prefill_attn_gqa_kernel(PrefillArgs a) {
+  constexpr int KS_BYTES = HALVES * 2 * ATT_BLK * ATT_HD * 2;
+  constexpr int VS_BYTES = HALVES * 2 * ATT_BLK * ATT_VSTRIDE * 2;
+  __shared__ __attribute__((aligned(16))) char smem[KS_BYTES + VS_BYTES];
+  half_t (*ks_lds)[2][ATT_BLK * ATT_HD] = (half_t (*)[2][ATT_BLK * ATT_HD])smem;
+  half_t (*vs_lds)[2][ATT_BLK * ATT_VSTRIDE] = (half_t (*)[2][ATT_BLK * ATT_VSTRIDE])(smem + KS_BYTES);
   const int tid = threadIdx.x;
+  const int hf = HALVES > 1 ? tid >> 8 : 0;     // key-range group
+  const int ltid = tid & 255;                    // thread within the group
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = ltid >> 6;                    // wave within the group
   const int q16 = lane >> 4;
   const int c16 = lane & 15;
   // longest blocks first: a segment's later blocks see more keys
@@ -956,6 +966,11 @@ __global__ __launch_bounds__(256, 1) void prefill_attn_gqa_kernel(PrefillArgs a)
   const int lim = (int)clamp64(a.kv_len[t0 + my_row], 1, a.max_len);
   const int end = (int)clamp64(a.kv_len[t0 + n - 1], 1, a.max_len);
   const int ntiles = (end + ATT_BLK - 1) / ATT_BLK;
+  // this group's tiles [tbeg, tbeg + nt); both groups run `steps` loop steps (the same
+  // barriers), computing only their own tiles
+  const int steps = HALVES > 1 ? (ntiles + 1) / 2 : ntiles;
+  const int tbeg = hf == 0 ? 0 : steps;
+  const int nt = hf == 0 ? steps : ntiles - steps;
 
   half8_t qf[HPW][4];
 #pragma unroll
@@ -979,7 +994,7 @@ __global__ __launch_bounds__(256, 1) void prefill_attn_gqa_kernel(PrefillArgs a)
   const int64_t tok_stride = (int64_t)a.nkv * ATT_HD;
   const half_t* kbase = a.k_cache + g * ATT_HD;
   const half_t* vbase = a.v_cache + g * ATT_HD;
-  // thread tid moves 16-byte chunks c = tid and tid + 256 of the tile's K and of its V:
+  // thread ltid moves 16-byte chunks c = ltid and ltid + 256 of the tile's K and of its V:
   // row c / 16, chunk c % 16.  Two register sets hold the next two tiles' loads.
   struct TileRegs {
     half8_t k[2], v[2];
@@ -987,7 +1002,7 @@ __global__ __launch_bounds__(256, 1) void prefill_attn_gqa_kernel(PrefillArgs a)
   auto load_tile = [&](int tb, TileRegs& t) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const int c = tid + 256 * u;
+      const int c = ltid + 256 * u;
       const int tok = min(tb + (c >> 4), end - 1);
       const int64_t off = (row_base + tok) * tok_stride + (c & 15) * 8;
       t.k[u] = *(const half8_t*)(kbase + off);
@@ -997,24 +1012,96 @@ __global__ __launch_bounds__(256, 1) void prefill_attn_gqa_kernel(PrefillArgs a)
   auto store_tile = [&](int buf, const TileRegs& t) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const int c = tid + 256 * u;
+      const int c = ltid + 256 * u;
       const int r = c >> 4, ch = c & 15;
-      *(half8_t*)(&ks_lds[buf][r * ATT_HD + ((ch ^ (r & 15)) << 3)]) = t.k[u];
-      *(half8_t*)(&vs_lds[buf][r * ATT_VSTRIDE + ch * 8]) = t.v[u];
+      *(half8_t*)(&ks_lds[hf][buf][r * ATT_HD + ((ch ^ (r & 15)) << 3)]) = t.k[u];
+      *(half8_t*)(&vs_lds[hf][buf][r * ATT_VSTRIDE + ch * 8]) = t.v[u];
     }
   };
+  // One head's scores (S^T, keys along the lane quads) turned into fp16 probabilities
+  // (pa) and the factors that rescale its running output rows (al), with m_run / l_run
+  // updated.
+  auto softmax_tile = [&](int u, int tb, const f32x4 (&sacc)[2], half8_t& pa, float (&al)[4]) {
+    float sc[8];
+    float mblk = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = tb + 16 * j + 4 * q16 + i;
+        const float sv = key < lim ? sacc[j][i] * a.scale_log2 : -INFINITY;
+        sc[4 * j + i] = sv;
+        mblk = fmaxf(mblk, sv);
+      }
+    mblk = fmaxf(mblk, __shfl_xor(mblk, 16, 64));
+    mblk = fmaxf(mblk, __shfl_xor(mblk, 32, 64));
+    const float m_new = fmaxf(m_run[u], mblk);
+    // -inf only in the second key group, for a row none of whose keys it has seen yet
+    // (exp2(-inf - -inf) would be NaN); the first group starts at key 0
+    const float m_ref = HALVES > 1 && m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = exp2f(m_run[u] - m_ref);
+    m_run[u] = m_new;
+    float psum = 0.f;
+#pragma unroll
+    for (int s8 = 0; s8 < 8; ++s8) {
+      const float p = exp2f(sc[s8] - m_ref);
+      psum += p;
+      pa[s8] = (half_t)p;
+    }
+    l_run[u] = l_run[u] * alpha + psum;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * q16 + i, 64);
+  };
   auto compute_tile = [&](int buf, int tb) {
-    if (rows_here) {
+    if (!rows_here) return;
+    if constexpr (HALVES > 1) {
+      // Two waves share each SIMD here, so registers are tighter: every head's scores are
+      // formed one 16-key chunk of K fragments at a time, then V is read one 16-column
+      // strip at a time (the same arithmetic per element as below, in another order).
+      f32x4 sacc[HPW][2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        half8_t kc[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+          kc[ks] = *(const half8_t*)(&ks_lds[hf][buf][(16 * j + c16) * ATT_HD + (((4 * ks + q16) ^ c16) << 3)]);
+#pragma unroll
+        for (int u = 0; u < HPW; ++u) {
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) acc = mfma16x16x32(kc[ks], qf[u][ks], acc);
+          sacc[u][j] = acc;
+        }
+      }
+      half8_t pa[HPW];
+      float al[HPW][4];
+#pragma unroll
+      for (int u = 0; u < HPW; ++u)
+        if (h0 + u < a.G) softmax_tile(u, tb, sacc[u], pa[u], al[u]);
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const half8_t vb = lds_read_b_tr16(&vs_lds[hf][buf][dt * 16], ATT_VSTRIDE, q16, c16);
+#pragma unroll
+        for (int u = 0; u < HPW; ++u) {
+          if (h0 + u >= a.G) continue;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o_acc[u][dt][i] *= al[u][i];
+          o_acc[u][dt] = mfma16x16x32(pa[u], vb, o_acc[u][dt]);
+        }
+      }
+      return;
+    }
+    {
       // K fragments (A operand of S^T = K Q^T): key 16 j + c16, dims 32 ks + 8 q16 .. +7
       half8_t kc[2][4];
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
-          kc[j][ks] = *(const half8_t*)(&ks_lds[buf][(16 * j + c16) * ATT_HD + (((4 * ks + q16) ^ c16) << 3)]);
+          kc[j][ks] = *(const half8_t*)(&ks_lds[hf][buf][(16 * j + c16) * ATT_HD + (((4 * ks + q16) ^ c16) << 3)]);
       half8_t vb[8];
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) vb[dt] = lds_read_b_tr16(&vs_lds[buf][dt * 16], ATT_VSTRIDE, q16, c16);
+      for (int dt = 0; dt < 8; ++dt) vb[dt] = lds_read_b_tr16(&vs_lds[hf][buf][dt * 16], ATT_VSTRIDE, q16, c16);
 #pragma unroll
       for (int u = 0; u < HPW; ++u) {
         if (h0 + u >= a.G) continue;
@@ -1026,34 +1113,9 @@ __global__ __launch_bounds__(256, 1) void prefill_attn_gqa_kernel(PrefillArgs a)
           for (int ks = 0; ks < 4; ++ks) acc = mfma16x16x32(kc[j][ks], qf[u][ks], acc);
           sacc[j] = acc;
         }
-        float sc[8];
-        float mblk = -INFINITY;
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int key = tb + 16 * j + 4 * q16 + i;
-            const float sv = key < lim ? sacc[j][i] * a.scale_log2 : -INFINITY;
-            sc[4 * j + i] = sv;
-            mblk = fmaxf(mblk, sv);
-          }
-        mblk = fmaxf(mblk, __shfl_xor(mblk, 16, 64));
-        mblk = fmaxf(mblk, __shfl_xor(mblk, 32, 64));
-        const float m_new = fmaxf(m_run[u], mblk);    // finite: key 0 is visible to every row
-        const float alpha = exp2f(m_run[u] - m_new);
-        m_run[u] = m_new;
         half8_t pa;
-        float psum = 0.f;
-#pragma unroll
-        for (int s8 = 0; s8 < 8; ++s8) {
-          const float p = exp2f(sc[s8] - m_new);
-          psum += p;
-          pa[s8] = (half_t)p;
-        }
-        l_run[u] = l_run[u] * alpha + psum;
         float al[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * q16 + i, 64);
+        softmax_tile(u, tb, sacc, pa, al);
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
 #pragma unroll
@@ -1064,50 +1126,116 @@ __global__ __launch_bounds__(256, 1) void prefill_attn_gqa_kernel(PrefillArgs a)
     }
   };
 
-  // Tile i sits in LDS buffer i % 2 while it is computed; during step i the registers hold
-  // tiles i + 1 (landed by now, stored into the other buffer after the step's MFMAs) and
-  // i + 2 (in flight), and the freed set takes tile i + 3's loads.  Steps go in pairs so
-  // that the two register sets keep fixed roles.
+  // Tile i of the group sits in LDS buffer i % 2 while it is computed; during step i the
+  // registers hold tiles i + 1 (landed by now, stored into the other buffer after the
+  // step's MFMAs) and i + 2 (in flight), and the freed set takes tile i + 3's loads.  Steps
+  // go in pairs so that the two register sets keep fixed roles.
   TileRegs ra, rb;
-  load_tile(0, ra);
-  store_tile(0, ra);
+  if (nt > 0) {
+    load_tile(tbeg * ATT_BLK, ra);
+    store_tile(0, ra);
+  }
   __syncthreads();
-  if (ntiles > 1) load_tile(ATT_BLK, rb);
-  if (ntiles > 2) load_tile(2 * ATT_BLK, ra);
-  for (int it = 0; it < ntiles; it += 2) {
-    compute_tile(0, it * ATT_BLK);
-    if (it + 1 < ntiles) {
+  if (nt > 1) load_tile((tbeg + 1) * ATT_BLK, rb);
+  if (nt > 2) load_tile((tbeg + 2) * ATT_BLK, ra);
+  for (int it = 0; it < steps; it += 2) {
+    if (it < nt) compute_tile(0, (tbeg + it) * ATT_BLK);
+    if (it + 1 < nt) {
       store_tile(1, rb);                      // tile it + 1; buffer 1's last reader is done
-      if (it + 3 < ntiles) load_tile((it + 3) * ATT_BLK, rb);
+      if (it + 3 < nt) load_tile((tbeg + it + 3) * ATT_BLK, rb);
     }
     lds_barrier();   // the stores are visible and every wave is done with this tile
-    if (it + 1 >= ntiles) break;
-    compute_tile(1, (it + 1) * ATT_BLK);
-    if (it + 2 < ntiles) {
+    if (it + 1 >= steps) break;
+    if (it + 1 < nt) compute_tile(1, (tbeg + it + 1) * ATT_BLK);
+    if (it + 2 < nt) {
       store_tile(0, ra);                      // tile it + 2
-      if (it + 4 < ntiles) load_tile((it + 4) * ATT_BLK, ra);
+      if (it + 4 < nt) load_tile((tbeg + it + 4) * ATT_BLK, ra);
     }
     lds_barrier();
+  }
+
+  // The row sums (each lane holds keys 4 q16 .. +3 of every 16) reduced to row c16.
+  float lrow[HPW];
+#pragma unroll
+  for (int u = 0; u < HPW; ++u) {
+    float l = l_run[u];
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    lrow[u] = l;
+  }
+  // HALVES = 2: the second group's normalised output (fp16) and (max, sum) per row go
+  // through LDS (the tile buffers, free after the loop) to the first group's same wave.
+  float w1[HPW][4];      // second group's weight l1 2^(m1 - M) per output row (0: none)
+  float wd[HPW][4];      // the merged denominator per output row
+  float w0[HPW][4];      // first group's 2^(m0 - M)
+  half_t (*o1)[HPW][8][64][4] = (half_t (*)[HPW][8][64][4])smem;
+  float (*ml1)[HPW][16][2] = (float (*)[HPW][16][2])(smem + 4 * HPW * 8 * 64 * 4 * 2);
+  if constexpr (HALVES > 1) {
+    static_assert(4 * HPW * 8 * 64 * 4 * 2 + 4 * HPW * 16 * 2 * 4 <= KS_BYTES + VS_BYTES,
+                  "merge buffers exceed the tile buffers");
+    __syncthreads();                           // every tile read is done: the LDS is free
+    if (hf == 1 && rows_here) {
+#pragma unroll
+      for (int u = 0; u < HPW; ++u) {
+        float li[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) li[i] = __shfl(lrow[u], 4 * q16 + i, 64);
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+          half4_t hv;
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            hv[i] = (half_t)(li[i] > 0.f ? o_acc[u][dt][i] / li[i] : 0.f);
+          *(half4_t*)&o1[wave][u][dt][lane][0] = hv;
+        }
+        if (q16 == 0) {
+          ml1[wave][u][c16][0] = m_run[u];
+          ml1[wave][u][c16][1] = lrow[u];
+        }
+      }
+    }
+    __syncthreads();
+    if (hf == 1) return;                       // no barrier follows
+#pragma unroll
+    for (int u = 0; u < HPW; ++u) {
+      const float m1 = ml1[wave][u][c16][0], l1 = ml1[wave][u][c16][1];
+      const float M = fmaxf(m_run[u], m1);     // finite: key 0 is in the first group
+      const float a0 = exp2f(m_run[u] - M);
+      const float b1 = l1 > 0.f ? l1 * exp2f(m1 - M) : 0.f;
+      const float den = lrow[u] * a0 + b1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        w0[u][i] = __shfl(a0, 4 * q16 + i, 64);
+        w1[u][i] = __shfl(b1, 4 * q16 + i, 64);
+        wd[u][i] = __shfl(den, 4 * q16 + i, 64);
+      }
+    }
   }
   if (!rows_here) return;
 #pragma unroll
   for (int u = 0; u < HPW; ++u) {
     if (h0 + u >= a.G) continue;
     const int h = g * a.G + h0 + u;
-    float l = l_run[u];
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
     float li[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) li[i] = __shfl(l, 4 * q16 + i, 64);
+    for (int i = 0; i < 4; ++i) li[i] = __shfl(lrow[u], 4 * q16 + i, 64);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 16 * sub + 4 * q16 + i;
       if (r < n) {
         half_t* op = a.out + (int64_t)(t0 + r) * a.out_stride + (int64_t)h * ATT_HD;
-        const float inv = 1.0f / li[i];
+        if constexpr (HALVES > 1) {
+          const float inv = 1.0f / wd[u][i];
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) op[dt * 16 + c16] = (half_t)(o_acc[u][dt][i] * inv);
+          for (int dt = 0; dt < 8; ++dt) {
+            const float o1v = (float)o1[wave][u][dt][lane][i];
+            op[dt * 16 + c16] = (half_t)((o_acc[u][dt][i] * w0[u][i] + o1v * w1[u][i]) * inv);
+          }
+        } else {
+          const float inv = 1.0f / li[i];
+#pragma unroll
+          for (int dt = 0; dt < 8; ++dt) op[dt * 16 + c16] = (half_t)(o_acc[u][dt][i] * inv);
+        }
       }
     }
   }
@@ -1206,11 +1334,31 @@ extern "C" int omni_prefill_attention_gqa(const void* q, int q_stride, const voi
   const int64_t grid = (int64_t)nqb * n_kv_heads;
   if (grid > 0x7fffffff) return OMNI_EUNSUPPORTED;
   if (a.G <= 6)
-    hipLaunchKernelGGL((prefill_attn_gqa_kernel<3>), dim3((unsigned)grid), dim3(256), 0,
+    hipLaunchKernelGGL((prefill_attn_gqa_kernel<3, 1>), dim3((unsigned)grid), dim3(256), 0,
                        (hipStream_t)stream, a);
   else
-    hipLaunchKernelGGL((prefill_attn_gqa_kernel<4>), dim3((unsigned)grid), dim3(256), 0,
+    hipLaunchKernelGGL((prefill_attn_gqa_kernel<4, 1>), dim3((unsigned)grid), dim3(256), 0,
                        (hipStream_t)stream, a);
+  OMNI_CHECK_LAUNCH();
+  return OMNI_OK;
+}
+
+extern "C" int omni_prefill_attention_gqa_halves(const void* q, int q_stride, const void* k_cache,
+                                                 const void* v_cache, int pool_rows, int max_len,
+                                                 const int64_t* slots, const int64_t* kv_len,
+                                                 const int* qblocks, int nqb, void* out,
+                                                 int out_stride, int n_heads, int n_kv_heads,
+                                                 int head_dim, float scale, void* stream) {
+  PrefillArgs a;
+  const int rc = prefill_args(a, q, q_stride, k_cache, v_cache, pool_rows, max_len, slots, kv_len,
+                              qblocks, nqb, out, out_stride, n_heads, n_kv_heads, head_dim, scale);
+  if (rc) return rc;
+  if (a.G > 6) return OMNI_EUNSUPPORTED;
+  if (nqb == 0) return OMNI_OK;
+  const int64_t grid = (int64_t)nqb * n_kv_heads;
+  if (grid > 0x7fffffff) return OMNI_EUNSUPPORTED;
+  hipLaunchKernelGGL((prefill_attn_gqa_kernel<3, 2>), dim3((unsigned)grid), dim3(512), 0,
+                     (hipStream_t)stream, a);
   OMNI_CHECK_LAUNCH();
   return OMNI_OK;
 }

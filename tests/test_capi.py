@@ -138,6 +138,14 @@ def test_bad_arguments_rejected_before_launch(so):
     assert L.omni_fp8_quant_weight_rows(None, 256, None, None, -1, 256, None) == -1
     assert [L.omni_fp8_quant_tensor_work(r) for r in (0, 1, 255, 256, 100000)] == [0, 1, 255,
                                                                                   256, 256]
+    # prefill attention with the key tiles split between two wave groups: at most 6 query
+    # heads per KV head (28 / 4 is rejected, 12 / 2 with no blocks is a no-op)
+    assert L.omni_prefill_attention_gqa_halves(None, 28 * 128, None, None, 1, 16, None, None,
+                                               None, 0, None, 28 * 128, 28, 4, 128, 0.1,
+                                               None) == -2
+    assert L.omni_prefill_attention_gqa_halves(None, 12 * 128, None, None, 1, 16, None, None,
+                                               None, 0, None, 12 * 128, 12, 2, 128, 0.1,
+                                               None) == 0
     # zero-size work is a no-op success
     assert L.omni_silu_mul(None, None, 0, 8960, None) == 0
     assert L.omni_gemm_slices(8960, 10) == 10 and L.omni_gemm_slices(1536, 7) == 6

@@ -240,6 +240,10 @@ def test_prefill_attention(gpu, segs):
     outs = torch.full_like(out, float("nan"))
     call("omni_prefill_attention_split", ptr(qg), nh * hd, ptr(kg), ptr(vg), P, ML, ptr(slot_t),
          ptr(kvl), ptr(qb), qb.shape[0], ptr(outs), nh * hd, nh, nkv, hd, hd ** -0.5, stream())
+    outh = torch.full_like(out, float("nan"))
+    call("omni_prefill_attention_gqa_halves", ptr(qg), nh * hd, ptr(kg), ptr(vg), P, ML,
+         ptr(slot_t), ptr(kvl), ptr(qb32), qb32.shape[0], ptr(outh), nh * hd, nh, nkv, hd,
+         hd ** -0.5, stream())
     torch.cuda.synchronize()
     e = ref.prefill_attention(q.float().view(T, nh, hd), k.float(), v.float(), segs, hd ** -0.5)
     d = (out.cpu().float() - e).abs().max().item()
@@ -248,15 +252,20 @@ def test_prefill_attention(gpu, segs):
     # key tiles split over four waves: P rounded to fp16 against each wave's own maximum
     ds = (outs.cpu().float() - e).abs().max().item()
     assert ds <= 4e-3, ds
+    # key tiles split between two wave groups: the same, plus the second group's normalised
+    # output rounded to fp16 before the merge
+    dh = (outh.cpu().float() - e).abs().max().item()
+    assert dh <= 4e-3, dh
 
 
 @pytest.mark.parametrize("ctx,chunk", [((40, 300), (16, 7)), ((2048,), (256,)),
                                        ((97, 1023, 5), (33, 16, 5))])
 def test_prefill_attention_append(gpu, ctx, chunk):
     """The append form (a chunk of chunk[s] new tokens at the end of a context of ctx[s]
-    keys: token i of the chunk sees keys [0, ctx - chunk + i + 1)) for the per-wave and the
-    key-split kernels, against the oracle's per-token attention over the same pool rows."""
-    from omniserver_amd.attention import query_blocks
+    keys: token i of the chunk sees keys [0, ctx - chunk + i + 1)) for every prefill kernel
+    (16-token blocks for the per-head ones, 32 for the shared-tile ones), against the
+    oracle's per-token attention over the same pool rows."""
+    from omniserver_amd.attention import QBLOCK_GQA, query_blocks
     from omniserver_amd._lib import call, ptr, stream
     say(f"prefill_attention append ctx={ctx} chunk={chunk}")
     nh, nkv, hd, ML = 12, 2, 128, 2048
@@ -269,13 +278,16 @@ def test_prefill_attention_append(gpu, ctx, chunk):
     for s, (Lk, Lq) in enumerate(zip(ctx, chunk)):
         slot += [s] * Lq
         kvl += [Lk - Lq + i + 1 for i in range(Lq)]
-    qb = query_blocks(chunk, gpu)
+    qb16 = query_blocks(chunk, gpu)
     slot_t = torch.tensor(slot, dtype=torch.int64, device=gpu)
     kvl_t = torch.tensor(kvl, dtype=torch.int64, device=gpu)
     qg, kg, vg = q.to(gpu), kp.to(gpu), vp.to(gpu)
     e = ref.decode_attention(q.float().view(T, nh, hd), kp.float(), vp.float(),
                              torch.tensor(slot), torch.tensor(kvl), hd ** -0.5)
-    for fn in ("omni_prefill_attention", "omni_prefill_attention_split"):
+    qb32 = query_blocks(chunk, gpu, QBLOCK_GQA)
+    for fn in ("omni_prefill_attention", "omni_prefill_attention_split",
+               "omni_prefill_attention_gqa", "omni_prefill_attention_gqa_halves"):
+        qb = qb32 if "gqa" in fn else qb16
         out = torch.full((T, nh, hd), float("nan"), device=gpu, dtype=torch.float16)
         call(fn, ptr(qg), nh * hd, ptr(kg), ptr(vg), P, ML, ptr(slot_t), ptr(kvl_t), ptr(qb),
              qb.shape[0], ptr(out), nh * hd, nh, nkv, hd, hd ** -0.5, stream())

@@ -398,7 +398,7 @@ int omni_fp8_quant_tensor_work(int rows);
  *   1  bf16(v) + bf16(bias) added in bf16 (forward_prequant, :99-108);
  *   2  fp16(v), + fp16 bias in fp16 (per-tensor forward: out_dtype fp16, :119-125; sa and
  *      sw hold one value each, repeated).  This form runs the 256 x 128 kernel where
- *      omni_fp8_gemm_plan names the 256 x 256 one (its epilogue has no room for it).
+ *      omni_fp8_gemm_plan names a 256-row big-tile one (their epilogue has no room for it).
  * xq [M, K], wq [N, K] e4m3fn; out [M, ldo]; N % 128 == 0, K % 128 == 0. */
 int omni_fp8_gemm(const void* xq, const float* sa, const void* wq, const float* sw,
                   const void* bias, void* out, int ldo, int M, int N, int K, int out_mode,
@@ -406,8 +406,10 @@ int omni_fp8_gemm(const void* xq, const float* sa, const void* wq, const float* 
 
 /* The kernel omni_fp8_gemm runs for a shape (no reference counterpart: it tells a caller
  * or a test which form covers the shape): 0 one 128 x 128 tile per workgroup (K < 512),
- * 1 the pipelined persistent 256 x 128 tiles, 2 the 256 x 256 tiles (K >= 4096, M and N
- * multiples of 256); *grid (may be NULL) = its workgroups.  Returns -1 for a shape
+ * 1 the pipelined persistent 256 x 128 tiles, 2 the 256 x 256 tiles, 3 the 256 x 192 tiles
+ * (2 and 3: K >= 1024, M a multiple of 256, N of the width, where their tiles keep at least
+ * as many CU slots busy over the grid's rounds as the 256 x 128 ones, more for K < 4096:
+ * e.g. N = 1536 at M = 8192); *grid (may be NULL) = its workgroups.  Returns -1 for a shape
  * omni_fp8_gemm rejects. */
 int omni_fp8_gemm_plan(int M, int N, int K, int* grid);
 

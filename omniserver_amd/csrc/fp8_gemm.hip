@@ -477,7 +477,9 @@ __global__ __launch_bounds__(128 * WM, 1) void fp8_gemm_pipe_kernel(Fp8GemmArgs 
 // global->LDS loads, XOR-swizzled 128-byte rows) and tile order as the kernel above, but
 // one tile per workgroup (the long-K shapes it serves have at most a grid's worth of
 // tiles: config 4's down projection 192), which keeps no cross-tile state live beside the
-// 256 accumulators.
+// 256 accumulators.  NI = 6 narrows the tile to 256 x 192 (each wave 128 x 96, 12 w row
+// groups): N = 1536 then makes 8 column tiles, so M = 8192 gives 256 tiles, one per CU,
+// where the 256-column tiles leave a quarter of the CUs idle.
 #define F8B_T 256
 
 // Output bits of one product value v = acc * sa * sw: bf16(v), then either that bf16 plus
@@ -495,15 +497,15 @@ __device__ __forceinline__ uint32_t fp8_out_bits(float v, half_t bias) {
   return (uint32_t)__builtin_bit_cast(uint16_t, (half_t)((float)(half_t)bf + (float)bias));
 }
 
-// The 256 x 256 kernel's epilogue for one wave's 128 x 128 block: acc[i][j][q] is column
+// The 256 x 16·2·NI kernel's epilogue for one wave's 128 x 16 NI block: acc[i][j][q] is column
 // 16 i + q of row 16 j of the block (relative to the lane's ob / sap / sw / bias).
-template <bool OUT_BF16>
-__device__ __forceinline__ void fp8_big_epilogue(const f32x4 (&acc)[8][8], uint16_t* ob, int ldo,
+template <bool OUT_BF16, int NI>
+__device__ __forceinline__ void fp8_big_epilogue(const f32x4 (&acc)[NI][8], uint16_t* ob, int ldo,
                                                  const float* sap, const float* sw,
                                                  const half_t* bias) {
 #pragma clang fp contract(off)
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < NI; ++i) {
     const f32x4 sn = *(const f32x4*)(sw + 16 * i);
     half4_t bb = (half4_t){0, 0, 0, 0};
     if (bias) bb = *(const half4_t*)(bias + 16 * i);
@@ -522,14 +524,16 @@ __device__ __forceinline__ void fp8_big_epilogue(const f32x4 (&acc)[8][8], uint1
   }
 }
 
-template <int NS>
+template <int NS, int NI>
 __global__ __launch_bounds__(256, 1) void fp8_gemm_big_kernel(Fp8GemmArgs a) {
 #pragma clang fp contract(off)
+  constexpr int BN = 32 * NI;                 // tile columns: two waves of 16 NI
   constexpr int XLD = 8;                      // x loads per wave and stage (256 rows / 8 / 4)
-  constexpr int WLD = 8;                      // w loads per wave and stage
+  constexpr int WLD = NI;                     // w loads per wave and stage (BN rows / 8 / 4)
   constexpr int OPS = XLD + WLD;              // loads every thread issues per stage
+  static_assert(NI == 6 || NI == 8, "tile widths 192 and 256");
   __shared__ __attribute__((aligned(1024))) uint8_t xl[NS][F8B_T * F8_ROWB];
-  __shared__ __attribute__((aligned(1024))) uint8_t wl[NS][F8B_T * F8_ROWB];
+  __shared__ __attribute__((aligned(1024))) uint8_t wl[NS][BN * F8_ROWB];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -539,12 +543,12 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_big_kernel(Fp8GemmArgs a) {
   const int g4 = lane >> 4;
 
   // One tile per workgroup (grid = tiles), in grouped order, XCD-contiguous.
-  const int tiles_n = a.N / F8B_T;
+  const int tiles_n = a.N / BN;
   const int tiles_m = a.M / F8B_T;
   const int nk = a.K / F8_BK;                               // >= NS (host check)
   int tm, tn;
   grouped_tile(xcd_logical_block(blockIdx.x, gridDim.x), tiles_m, tiles_n, F8_GM, tm, tn);
-  const int m0 = tm * F8B_T, n0 = tn * F8B_T;
+  const int m0 = tm * F8B_T, n0 = tn * BN;
 
   // Load u of this wave fills tile rows 32 u + 8 wave + lane / 8 (LDS slot lane % 8 holds
   // the row's chunk (lane % 8) ^ (row & 7)).  M % 256 == 0 (host check): no row clamping,
@@ -599,6 +603,26 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_big_kernel(Fp8GemmArgs a) {
         : "v"(a0), "v"(a1)
         : "memory");
   };
+  auto read12 = [&](uint32_t a0, uint32_t a1, u32x4* v) {
+    asm volatile(
+        "ds_read_b128 %0, %12\n\tds_read_b128 %1, %13\n\t"
+        "ds_read_b128 %2, %12 offset:2048\n\tds_read_b128 %3, %13 offset:2048\n\t"
+        "ds_read_b128 %4, %12 offset:4096\n\tds_read_b128 %5, %13 offset:4096\n\t"
+        "ds_read_b128 %6, %12 offset:6144\n\tds_read_b128 %7, %13 offset:6144\n\t"
+        "ds_read_b128 %8, %12 offset:8192\n\tds_read_b128 %9, %13 offset:8192\n\t"
+        "ds_read_b128 %10, %12 offset:10240\n\tds_read_b128 %11, %13 offset:10240"
+        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
+          "=&v"(v[6]), "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11])
+        : "v"(a0), "v"(a1)
+        : "memory");
+  };
+  auto wait12 = [&](u32x4* v) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
+                   "+v"(v[6]), "+v"(v[7]), "+v"(v[8]), "+v"(v[9]), "+v"(v[10]), "+v"(v[11])
+                 :
+                 : "memory");
+  };
   auto wait16 = [&](u32x4* v) {
     asm volatile("s_waitcnt lgkmcnt(0)"
                  : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
@@ -616,21 +640,23 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_big_kernel(Fp8GemmArgs a) {
   wait_vmcnt<OPS * (NS - 1)>();
   barrier_only();
   {
-    f32x4 acc[8][8];   // [n sub-tile][m sub-tile]
+    f32x4 acc[NI][8];   // [n sub-tile][m sub-tile]
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < NI; ++i)
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
     for (int ks = 0; ks < nk; ++ks) {
       const int st = ks % NS;
-      u32x4 wo[16], xo[16];
+      u32x4 wo[2 * NI], xo[16];
       {
         uint32_t aw0, aw1, ax0, ax1;
-        addrs(st, 1, 128 * wn, aw0, aw1);
+        addrs(st, 1, 16 * NI * wn, aw0, aw1);
         addrs(st, 0, 128 * wm, ax0, ax1);
-        read16(aw0, aw1, wo);
+        if constexpr (NI == 8) read16(aw0, aw1, wo);
+        else read12(aw0, aw1, wo);
         read16(ax0, ax1, xo);
-        wait16(wo);
+        if constexpr (NI == 8) wait16(wo);
+        else wait12(wo);
         wait16(xo);
       }
       // step ks + 1 has landed for this thread, then for everyone; every wave has read
@@ -639,7 +665,7 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_big_kernel(Fp8GemmArgs a) {
       barrier_only();
       if (ks + NS < nk) issue(ks + NS, st);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < NI; ++i) {
         const i32x8 wf = frag(wo[2 * i], wo[2 * i + 1]);
 #pragma unroll
         for (int j = 0; j < 8; ++j)
@@ -651,12 +677,12 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_big_kernel(Fp8GemmArgs a) {
     // the row / column scales and biases come straight from global memory (L2-resident).
     // One base pointer per tile and 32-bit offsets inside it (256 rows of ldo halves).
     const int mb = m0 + 128 * wm + l16;
-    const int nb = n0 + 128 * wn + 4 * g4;
+    const int nb = n0 + 16 * NI * wn + 4 * g4;
     uint16_t* const ob = (uint16_t*)a.out + (int64_t)mb * a.ldo + nb;
     const float* const sap = a.sa + mb;
     // (FP8_OUT_F16 never reaches this kernel: only 0 and 1 here)
-    if (a.out_mode) fp8_big_epilogue<true>(acc, ob, a.ldo, sap, a.sw + nb, has_bias ? a.bias + nb : nullptr);
-    else fp8_big_epilogue<false>(acc, ob, a.ldo, sap, a.sw + nb, has_bias ? a.bias + nb : nullptr);
+    if (a.out_mode) fp8_big_epilogue<true, NI>(acc, ob, a.ldo, sap, a.sw + nb, has_bias ? a.bias + nb : nullptr);
+    else fp8_big_epilogue<false, NI>(acc, ob, a.ldo, sap, a.sw + nb, has_bias ? a.bias + nb : nullptr);
   }
 }
 
@@ -833,22 +859,41 @@ extern "C" int omni_fp8_quant_tensor(const void* x, int ldx, void* q, float* sca
   return OMNI_OK;
 }
 
-// Kernel choice by shape: the 256 x 256 tiles serve the long-K shapes (K >= 4096, M and N
-// multiples of 256: the down projection, 8 % faster there; with K = 1536 they were 3-9 %
-// slower than the 256 x 128 tiles, measured on MI355X at M = 8192, outputs bit-equal); the
-// 8-wave pipelined 256 x 128 form every other shape with at least 4 K steps; the
-// double-buffered one-tile-per-workgroup kernel the rest (K < 512).
-static bool fp8_big_tiles(int M, int N, int K, int out_mode = FP8_OUT_F16_VIA_BF16) {
-  return K >= 4096 && (N % F8B_T) == 0 && (M % F8B_T) == 0 && out_mode != FP8_OUT_F16;
+// Kernel choice by shape, from the share of CU slots a grid's tiles keep busy over its
+// rounds ("fill"; one tile per CU per round).  The 256-row big tiles (256 or 192 columns,
+// one per workgroup) run where their fill is at least the 8-wave pipelined 256 x 128
+// form's for K >= 4096 and above it for shorter K (the best-filling width, 256 on a tie);
+// the pipelined form every other shape with at least 4 K steps; the double-buffered
+// one-tile-per-workgroup kernel the rest (K < 512).  MI355X, M = 8192, us (pipelined /
+// 256 x 192 / 256 x 256; outputs bit-equal): K 8960 -> N 1536 172.8 / 129.5 / 153.3;
+// 1536 -> 1536 47.9 / 38.9 / 46.6; 1536 -> 2048 44.9 / - / 45.2; 1536 -> 17920 342.2 /
+// - / 396.3; at M = 4096 (the big tiles filling half or less of the grid) 8960 -> 1536
+// 78.9 / 117.8 / 145.4, 1536 -> 1536 24.2 / 34.1 / 41.8.  Returns the big tile's width
+// (0: not big).
+static int fp8_big_cols(int M, int N, int K, int out_mode = FP8_OUT_F16_VIA_BF16) {
+  if (K < 1024 || (M % F8B_T) || out_mode == FP8_OUT_F16) return 0;
+  const int64_t cus = num_cus();
+  auto fill = [&](int64_t t) { return (double)t / (double)(((t + cus - 1) / cus) * cus); };
+  const double fp = fill((int64_t)(M / 256) * (N / F8_BT));
+  int best = 0;
+  double fb = 0.0;
+  for (int bn : {256, 192}) {
+    if (N % bn) continue;
+    const double f = fill((int64_t)(M / F8B_T) * (N / bn));
+    if (f > fb) best = bn, fb = f;
+  }
+  if (!best) return 0;
+  return (K >= 4096 ? fb >= fp : fb > fp) ? best : 0;
 }
 
 // Which kernel omni_fp8_gemm runs for a shape: 0 one tile per workgroup, 1 the pipelined
-// 256 x 128 tiles, 2 the 256 x 256 tiles; and the persistent grid it launches.
+// 256 x 128 tiles, 2 the 256 x 256 tiles, 3 the 256 x 192 tiles; and the grid it launches.
 extern "C" int omni_fp8_gemm_plan(int M, int N, int K, int* grid) {
   if (M <= 0 || N <= 0 || K <= 0 || (N % F8_BT) || (K % F8_BK)) return OMNI_EINVAL;
   int kind, g;
-  if (fp8_big_tiles(M, N, K)) {
-    kind = 2, g = (M / F8B_T) * (N / F8B_T);
+  const int bc = fp8_big_cols(M, N, K);
+  if (bc) {
+    kind = bc == 256 ? 2 : 3, g = (M / F8B_T) * (N / bc);
   } else if (K / F8_BK >= 4) {
     const int64_t t8 = (int64_t)ceil_div(M, 256) * (N / F8_BT);
     kind = 1, g = (int)(t8 < num_cus() ? t8 : num_cus());
@@ -882,9 +927,14 @@ extern "C" int omni_fp8_gemm(const void* xq, const float* sa, const void* wq, co
   a.N = N;
   a.K = K;
   a.out_mode = out_mode;
-  if (fp8_big_tiles(M, N, K, out_mode)) {         // 256 x 256 tiles, one per workgroup
-    const int grid = (M / F8B_T) * (N / F8B_T);
-    hipLaunchKernelGGL((fp8_gemm_big_kernel<2>), dim3((unsigned)grid), dim3(256), 0,
+  const int bc = fp8_big_cols(M, N, K, out_mode);
+  if (bc == 256) {                                // 256 x 256 tiles, one per workgroup
+    const int grid = (M / F8B_T) * (N / 256);
+    hipLaunchKernelGGL((fp8_gemm_big_kernel<2, 8>), dim3((unsigned)grid), dim3(256), 0,
+                       (hipStream_t)stream, a);
+  } else if (bc == 192) {                         // 256 x 192 tiles, one per workgroup
+    const int grid = (M / F8B_T) * (N / 192);
+    hipLaunchKernelGGL((fp8_gemm_big_kernel<2, 6>), dim3((unsigned)grid), dim3(256), 0,
                        (hipStream_t)stream, a);
   } else if (K / F8_BK >= 4) {                    // 8 waves, 256 x 128 tiles, 3 stages
     const int64_t t8 = (int64_t)ceil_div(M, 256) * (N / F8_BT);

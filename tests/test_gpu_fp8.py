@@ -5,9 +5,11 @@ the oracle on the same quantised operands.
 Shapes (K -> N): QKV 1536 -> 2048 (with the q|k|v bias), O 1536 -> 1536, gate/up
 1536 -> 17920, down 8960 -> 1536; x ~ N(0, 1) fp16, W ~ N(0, 0.02) fp16 (config 4).  At
 M = 8192 every shape runs a persistent grid over many tile rounds (gate/up: 32 x 140
-tiles of 256 x 128 on 256 workgroups, 18 rounds), the down projection on the 256 x 256
-tiles; a ragged M puts a partial tile in the last round, and K < 512 takes the
-one-tile-per-workgroup kernel.  ``omni_fp8_gemm_plan`` names the kernel and grid each
+tiles of 256 x 128 on 256 workgroups, 18 rounds), O and the down projection on 256 x 192
+tiles (256 of them: one per CU); K = 4096 -> N = 2048 takes the 256 x 256 tiles, and the
+down shape at M = 4096 (big tiles would fill half the grid) the 256 x 128 pipeline; a
+ragged M puts a partial tile in the last round, and K < 512 takes the one-tile-per-workgroup
+kernel.  ``omni_fp8_gemm_plan`` names the kernel and grid each
 case runs, so the test states which path it covered.
 
 The oracle's product is computed for 8 rows of every 256-row block (one row in each of
@@ -23,7 +25,9 @@ from oracle import qwen2_ref as ref
 
 pytestmark = pytest.mark.gpu
 
-KIND = {0: "one tile per workgroup", 1: "pipelined 256x128 persistent", 2: "256x256 tiles"}
+KIND = {0: "one tile per workgroup", 1: "pipelined 256x128 persistent", 2: "256x256 tiles",
+        3: "256x192 tiles"}
+COLS = {0: 128, 1: 128, 2: 256, 3: 192}
 BLOCK_ROWS = (0, 17, 63, 98, 133, 228, 239, 255)    # within each 256-row block
 
 
@@ -59,6 +63,8 @@ CASES = [
     ("o", 8192, 1536, 1536, False),
     ("gate_up", 8192, 1536, 17920, False),
     ("down", 8192, 8960, 1536, False),
+    ("256-wide", 8192, 4096, 2048, True),
+    ("down half grid", 4096, 8960, 1536, False),
     ("gate_up ragged", 8192 + 100, 1536, 17920, False),
     ("down ragged", 2000, 8960, 1536, True),
     ("short K", 1000, 384, 2048, True),
@@ -69,7 +75,7 @@ CASES = [
 def test_fp8_config4_linear(gpu, name, M, K, N, bias):
     from omniserver_amd.linear import FP8Linear
     kind, grid = plan(M, N, K)
-    tiles = -(-M // (256 if kind else 128)) * (N // (256 if kind == 2 else 128))
+    tiles = -(-M // (256 if kind else 128)) * (N // COLS[kind])
     say(f"fp8 {name}: M={M} K={K} N={N} bias={bias} -> {KIND[kind]}, grid {grid}, "
         f"{tiles} tiles ({-(-tiles // grid)} rounds)")
     W = f16((N, K), 400 + N % 97, 0.02)

@@ -333,11 +333,21 @@ int omni_f16_gemm_pipe_splits(int M, int N, int K, int tile_rows);
  * int4 at 128 rows, else >= 2), ksplit > 1 with fp32 workspace (ksplit * M * N floats,
  * 16-byte aligned) summed in order by a second launch.  OMNI_EPI_PARTIAL: the ksplit fp32
  * slices [ksplit][M][N] only, into workspace (out and bias unused, NULL), for a consumer
- * that sums them in order (omni_add_rmsnorm_partials, omni_mrope_kv_write_partials). */
+ * that sums them in order (omni_add_rmsnorm_partials, omni_mrope_kv_write_partials).
+ * With tile_rows and ksplit both 0, fp16 weights and STORE / PARTIAL, N % 192 == 0 shapes
+ * whose 128 x 192 tiles take fewer grid rounds x tile outputs run those (same k order per
+ * output: results equal the 128 x 128 tiles' bit for bit). */
 int omni_packed_gemm_pipe(const void* x, int ldx, const void* w_packed, const void* scales_packed,
                           int fmt, const void* bias, int bias_after_round, void* out, int ldo,
                           int M, int N, int K, int epilogue, int tile_rows, int ksplit,
                           float* workspace, void* stream);
+
+/* The tiling omni_packed_gemm_pipe runs for a shape (no reference counterpart: it tells a
+ * caller or a test which form covers the shape): *rows x *cols tiles (128 / 256 x 128, or
+ * 128 x 192) and *ks K slices for the given tile_rows / ksplit (0: chosen); any output may
+ * be NULL.  -1 for a shape it rejects. */
+int omni_packed_gemm_pipe_plan(int M, int N, int K, int fmt, int epilogue, int tile_rows,
+                               int ksplit, int* rows, int* cols, int* ks);
 
 /* nn.LayerNorm(N, eps) of M fp16 rows (model/qwen2_vit.py:39-40, 87): fp32 mean and biased
  * variance, y = (x - mean) rsqrt(var + eps) w + b.  N % 8 == 0, N <= 2048; out may alias x. */
@@ -406,11 +416,12 @@ int omni_fp8_gemm(const void* xq, const float* sa, const void* wq, const float* 
 
 /* The kernel omni_fp8_gemm runs for a shape (no reference counterpart: it tells a caller
  * or a test which form covers the shape): 0 one 128 x 128 tile per workgroup (K < 512),
- * 1 the pipelined persistent 256 x 128 tiles, 2 the 256 x 256 tiles, 3 the 256 x 192 tiles
- * (2 and 3: K >= 1024, M a multiple of 256, N of the width, where their tiles keep at least
- * as many CU slots busy over the grid's rounds as the 256 x 128 ones, more for K < 4096:
- * e.g. N = 1536 at M = 8192); *grid (may be NULL) = its workgroups.  Returns -1 for a shape
- * omni_fp8_gemm rejects. */
+ * 1 the pipelined persistent 256 x 128 tiles, 2 the persistent 256 x 256 tiles, 3 the
+ * persistent 256 x 192 tiles (2 and 3: K >= 1024, M a multiple of 256, N of the width,
+ * where rounds of the grid times the tile's work come out below the 256 x 128 tiles', a big
+ * tile counted at 0.85 of its size: e.g. every config-4 shape at M = 8192, not N = 1536 at
+ * M = 4096); *grid (may be NULL) = its workgroups.  Returns -1 for a shape omni_fp8_gemm
+ * rejects. */
 int omni_fp8_gemm_plan(int M, int N, int K, int* grid);
 
 /* ---------------------------------------------------------------- lm_head + greedy */

@@ -474,12 +474,10 @@ __global__ __launch_bounds__(128 * WM, 1) void fp8_gemm_pipe_kernel(Fp8GemmArgs 
 // 128 columns; this one for every 256).  Per K step a wave issues 32 operand reads (32 bytes
 // per lane of 8 w and 8 x row groups) and 64 MFMAs; two stages of 64 KB each are in LDS
 // (the next step's operands land while this step's MFMAs run).  Same staging (direct
-// global->LDS loads, XOR-swizzled 128-byte rows) and tile order as the kernel above, but
-// one tile per workgroup (the long-K shapes it serves have at most a grid's worth of
-// tiles: config 4's down projection 192), which keeps no cross-tile state live beside the
-// 256 accumulators.  NI = 6 narrows the tile to 256 x 192 (each wave 128 x 96, 12 w row
-// groups): N = 1536 then makes 8 column tiles, so M = 8192 gives 256 tiles, one per CU,
-// where the 256-column tiles leave a quarter of the CUs idle.
+// global->LDS loads, XOR-swizzled 128-byte rows) and XCD-grouped tile order as the kernel
+// above.  NI = 6 narrows the tile to 256 x 192 (each wave 128 x 96, 12 w row groups): N =
+// 1536 then makes 8 column tiles, so M = 8192 gives 256 tiles, one per CU, where the
+// 256-column tiles leave a quarter of the CUs idle.
 #define F8B_T 256
 
 // Output bits of one product value v = acc * sa * sw: bf16(v), then either that bf16 plus
@@ -497,25 +495,32 @@ __device__ __forceinline__ uint32_t fp8_out_bits(float v, half_t bias) {
   return (uint32_t)__builtin_bit_cast(uint16_t, (half_t)((float)(half_t)bf + (float)bias));
 }
 
-// The 256 x 16·2·NI kernel's epilogue for one wave's 128 x 16 NI block: acc[i][j][q] is column
-// 16 i + q of row 16 j of the block (relative to the lane's ob / sap / sw / bias).
-template <bool OUT_BF16, int NI>
-__device__ __forceinline__ void fp8_big_epilogue(const f32x4 (&acc)[NI][8], uint16_t* ob, int ldo,
-                                                 const float* sap, const float* sw,
-                                                 const half_t* bias) {
+// Persistent form of the big tiles: a grid of at most one workgroup per CU walks its tiles
+// (round r, slot b: logical tile r * grid + b, in the same XCD-grouped order), and the K
+// loop runs straight across tile boundaries: the next tile's first two stages are loaded
+// during the current tile's last two steps, so no tile waits for its first operands.  The
+// tile's row / column scales and biases ride with its first stage into an LDS slot of their
+// own (two, by tile parity), which the epilogue reads with its own lgkmcnt wait: an epilogue
+// that read them from global memory would wait (vmcnt) for the next tile's stages in flight.
+template <bool OUT_BF16, int NI, typename ReadCol>
+__device__ __forceinline__ void fp8_bigp_epilogue(const f32x4 (&acc)[NI][8], uint16_t* ob, int ldo,
+                                                  const float (&sm)[8], ReadCol read_col,
+                                                  bool has_bias) {
 #pragma clang fp contract(off)
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
-    const f32x4 sn = *(const f32x4*)(sw + 16 * i);
+    f32x4 snv;
+    u32x2 bw;
+    read_col(i, snv, bw);       // column scales and biases of n sub-tile i
+    const f32x4 sn_i = snv;
     half4_t bb = (half4_t){0, 0, 0, 0};
-    if (bias) bb = *(const half4_t*)(bias + 16 * i);
+    if (has_bias) bb = __builtin_bit_cast(half4_t, bw);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float sm = sap[16 * j];
       uint32_t bits[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q)
-        bits[q] = fp8_out_bits<OUT_BF16>((acc[i][j][q] * sm) * sn[q], bb[q]);
+        bits[q] = fp8_out_bits<OUT_BF16>((acc[i][j][q] * sm[j]) * sn_i[q], bb[q]);
       uint2 pk;
       pk.x = bits[0] | (bits[1] << 16);
       pk.y = bits[2] | (bits[3] << 16);
@@ -524,16 +529,19 @@ __device__ __forceinline__ void fp8_big_epilogue(const f32x4 (&acc)[NI][8], uint
   }
 }
 
-template <int NS, int NI>
-__global__ __launch_bounds__(256, 1) void fp8_gemm_big_kernel(Fp8GemmArgs a) {
+template <int NI>
+__global__ __launch_bounds__(256, 1) void fp8_gemm_bigp_kernel(Fp8GemmArgs a) {
 #pragma clang fp contract(off)
+  constexpr int NS = 2;                       // stages (64 KB + 16 NI * 2 KB each)
   constexpr int BN = 32 * NI;                 // tile columns: two waves of 16 NI
   constexpr int XLD = 8;                      // x loads per wave and stage (256 rows / 8 / 4)
   constexpr int WLD = NI;                     // w loads per wave and stage (BN rows / 8 / 4)
-  constexpr int OPS = XLD + WLD;              // loads every thread issues per stage
+  constexpr int OPS = XLD + WLD;              // operand loads every thread issues per stage
   static_assert(NI == 6 || NI == 8, "tile widths 192 and 256");
   __shared__ __attribute__((aligned(1024))) uint8_t xl[NS][F8B_T * F8_ROWB];
   __shared__ __attribute__((aligned(1024))) uint8_t wl[NS][BN * F8_ROWB];
+  __shared__ __attribute__((aligned(16))) float scl[2][F8B_T + BN];    // [tile parity][sa | sw]
+  __shared__ __attribute__((aligned(16))) half_t bsl[2][512];          // [tile parity][bias]
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -542,30 +550,30 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_big_kernel(Fp8GemmArgs a) {
   const int l16 = lane & 15;
   const int g4 = lane >> 4;
 
-  // One tile per workgroup (grid = tiles), in grouped order, XCD-contiguous.
   const int tiles_n = a.N / BN;
   const int tiles_m = a.M / F8B_T;
+  const int tiles = tiles_m * tiles_n;
+  const int G = gridDim.x;
+  const int slot = xcd_logical_block(blockIdx.x, G);
+  const int my_tiles = (tiles - slot + G - 1) / G;          // grid <= tiles: >= 1
   const int nk = a.K / F8_BK;                               // >= NS (host check)
-  int tm, tn;
-  grouped_tile(xcd_logical_block(blockIdx.x, gridDim.x), tiles_m, tiles_n, F8_GM, tm, tn);
-  const int m0 = tm * F8B_T, n0 = tn * BN;
+  auto tile_at = [&](int r, int& m0, int& n0) {             // past the last tile: the last one
+    int tm, tn;
+    grouped_tile(min(r, my_tiles - 1) * G + slot, tiles_m, tiles_n, F8_GM, tm, tn);
+    m0 = tm * F8B_T;
+    n0 = tn * BN;
+  };
 
-  // Load u of this wave fills tile rows 32 u + 8 wave + lane / 8 (LDS slot lane % 8 holds
-  // the row's chunk (lane % 8) ^ (row & 7)).  M % 256 == 0 (host check): no row clamping,
-  // so one x pointer per tile serves every load.
   const int lrow = 8 * wave + (lane >> 3);
   const int lchunk = (lane & 7) ^ (lrow & 7);
   typedef __attribute__((address_space(3))) void lds_void;
   typedef __attribute__((address_space(3))) uint8_t lds_u8;
   const bool has_bias = a.bias != nullptr;
-  // The tile's sources are wave-uniform row bases (scalar registers); the lane's own part,
-  // row lrow and chunk lchunk, is one 32-bit offset shared by x and w (row offsets stay
-  // below 2^31: 256 rows of K <= 2^23 bytes).
-  const uint8_t* const xs = a.xq + (int64_t)m0 * a.K;
-  const uint8_t* const ws = a.wq + (int64_t)n0 * a.K;
   const uint32_t loff = (uint32_t)lrow * (uint32_t)a.K + (uint32_t)lchunk * 16u;
-  const uint32_t rstep = 32u * (uint32_t)a.K;       // bytes between row groups
-  auto issue = [&](int ks, int st) {
+  const uint32_t rstep = 32u * (uint32_t)a.K;
+  auto issue = [&](int m0, int n0, int ks, int st) {
+    const uint8_t* const xs = a.xq + (int64_t)m0 * a.K;
+    const uint8_t* const ws = a.wq + (int64_t)n0 * a.K;
     const uint32_t k0 = loff + (uint32_t)ks * F8_BK;
 #pragma unroll
     for (int u = 0; u < XLD; ++u)
@@ -576,11 +584,28 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_big_kernel(Fp8GemmArgs a) {
       __builtin_amdgcn_global_load_lds((const void*)(ws + (k0 + u * rstep)),
                                        (lds_void*)((lds_u8*)&wl[st][(32 * u + 8 * wave) * F8_ROWB]), 16, 0, 0);
   };
-  // Operand reads in inline asm with their own lgkmcnt wait (as in the kernel above).  Row
-  // r = base + 16 i + l16 of a wave's block keeps its 16-byte chunk c in slot c ^ (r & 7) =
-  // c ^ (l16 & 7) (base and 16 i are multiples of 8), so the 8 row groups of one chunk are
-  // one address plus immediate offsets of 16 rows (2 KB) each: two address registers per
-  // operand and step.
+  // the tile's 256 row scales (one per thread), BN column scales (waves < BN / 64) and BN
+  // biases (wave 0, 16 bytes a lane; lanes past BN / 8 repeat the last chunk)
+  // (wave-uniform bases plus 32-bit lane offsets from a lane index passed through an empty
+  // asm, so that the compiler cannot hoist 64-bit lane addresses out of the loops and keep
+  // them live beside the accumulators)
+  auto issue_scales = [&](int m0, int n0, int p) {
+    uint32_t ln = (uint32_t)lane;
+    asm volatile("" : "+v"(ln));
+    const uint8_t* const sab = (const uint8_t*)(a.sa + m0 + 64 * wave);
+    __builtin_amdgcn_global_load_lds((const void*)(sab + 4u * ln),
+                                     (lds_void*)((lds_u8*)&scl[p][64 * wave]), 4, 0, 0);
+    if (wave < BN / 64) {
+      const uint8_t* const swb = (const uint8_t*)(a.sw + n0 + 64 * wave);
+      __builtin_amdgcn_global_load_lds((const void*)(swb + 4u * ln),
+                                       (lds_void*)((lds_u8*)&scl[p][F8B_T + 64 * wave]), 4, 0, 0);
+    }
+    if (wave == 0 && has_bias) {
+      const uint8_t* const bb = (const uint8_t*)(a.bias + n0);
+      __builtin_amdgcn_global_load_lds((const void*)(bb + 16u * min(ln, (uint32_t)(BN / 8 - 1))),
+                                       (lds_void*)((lds_u8*)&bsl[p][0]), 16, 0, 0);
+    }
+  };
   auto addrs = [&](int st, int o, int base, uint32_t& a0, uint32_t& a1) {
     const int r = base + l16;
     const uint32_t row = (uint32_t)(uintptr_t)(lds_u8*)(o ? &wl[st][r * F8_ROWB] : &xl[st][r * F8_ROWB]);
@@ -616,13 +641,6 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_big_kernel(Fp8GemmArgs a) {
         : "v"(a0), "v"(a1)
         : "memory");
   };
-  auto wait12 = [&](u32x4* v) {
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
-                   "+v"(v[6]), "+v"(v[7]), "+v"(v[8]), "+v"(v[9]), "+v"(v[10]), "+v"(v[11])
-                 :
-                 : "memory");
-  };
   auto wait16 = [&](u32x4* v) {
     asm volatile("s_waitcnt lgkmcnt(0)"
                  : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
@@ -631,22 +649,66 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_big_kernel(Fp8GemmArgs a) {
                  :
                  : "memory");
   };
+  auto wait12 = [&](u32x4* v) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
+                   "+v"(v[6]), "+v"(v[7]), "+v"(v[8]), "+v"(v[9]), "+v"(v[10]), "+v"(v[11])
+                 :
+                 : "memory");
+  };
   auto frag = [](const u32x4& lo, const u32x4& hi) {
     return (i32x8){(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
   };
+  // The epilogue's scales and biases of tile parity p, each read with its own lgkmcnt
+  // wait: row scales of rows 128 wm + 16 j + l16 (64 bytes apart), then per n sub-tile i the
+  // column scales and biases of columns 16 NI wn + 16 i + 4 g4 .. +3.
+  typedef __attribute__((address_space(3))) float lds_f32;
+  typedef __attribute__((address_space(3))) half_t lds_f16;
+  auto read_row_scales = [&](int p, float (&sm)[8]) {
+    uint32_t ln = (uint32_t)lane;             // (not hoisted: see issue_scales)
+    asm volatile("" : "+v"(ln));
+    const uint32_t am = (uint32_t)(uintptr_t)(lds_f32*)&scl[p][128 * wm + (ln & 15u)];
+    asm volatile(
+        "ds_read_b32 %0, %8\n\tds_read_b32 %1, %8 offset:64\n\tds_read_b32 %2, %8 offset:128\n\t"
+        "ds_read_b32 %3, %8 offset:192\n\tds_read_b32 %4, %8 offset:256\n\tds_read_b32 %5, %8 offset:320\n\t"
+        "ds_read_b32 %6, %8 offset:384\n\tds_read_b32 %7, %8 offset:448\n\ts_waitcnt lgkmcnt(0)"
+        : "=&v"(sm[0]), "=&v"(sm[1]), "=&v"(sm[2]), "=&v"(sm[3]), "=&v"(sm[4]), "=&v"(sm[5]),
+          "=&v"(sm[6]), "=&v"(sm[7])
+        : "v"(am)
+        : "memory");
+  };
+  auto read_col = [&](int p, int i, f32x4& sn, u32x2& bw) {
+    uint32_t ln = (uint32_t)lane;             // (not hoisted: see issue_scales)
+    asm volatile("" : "+v"(ln));
+    const uint32_t c4 = 4u * (ln >> 4);
+    const uint32_t an = (uint32_t)(uintptr_t)(lds_f32*)&scl[p][F8B_T + 16 * NI * wn + 16 * i + c4];
+    const uint32_t ab = (uint32_t)(uintptr_t)(lds_f16*)&bsl[p][16 * NI * wn + 16 * i + c4];
+    asm volatile("ds_read_b128 %0, %2\n\tds_read_b64 %1, %3\n\ts_waitcnt lgkmcnt(0)"
+                 : "=&v"(sn), "=&v"(bw)
+                 : "v"(an), "v"(ab)
+                 : "memory");
+  };
 
-#pragma unroll
-  for (int s = 0; s < NS; ++s) issue(s, s);
-  wait_vmcnt<OPS * (NS - 1)>();
+  // Steps sidx = 0, 1, ... walk the tiles' K steps back to back in slots sidx % 2; after
+  // step s's operands are in registers and step s + 1 has landed everywhere (vmcnt 0 +
+  // barrier: with two stages nothing younger is in flight), step s + 2 goes into slot s % 2.
+  int m0c, n0c, m0n, n0n;
+  tile_at(0, m0c, n0c);
+  tile_at(1, m0n, n0n);
+  issue_scales(m0c, n0c, 0);
+  issue(m0c, n0c, 0, 0);
+  issue(m0c, n0c, 1, 1);
+  wait_vmcnt<OPS>();                          // the scales and stage 0 (issued first)
   barrier_only();
-  {
+  int sidx = 0;
+  for (int r = 0; r < my_tiles; ++r) {
     f32x4 acc[NI][8];   // [n sub-tile][m sub-tile]
 #pragma unroll
     for (int i = 0; i < NI; ++i)
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    for (int ks = 0; ks < nk; ++ks) {
-      const int st = ks % NS;
+    for (int ks = 0; ks < nk; ++ks, ++sidx) {
+      const int st = sidx & 1;
       u32x4 wo[2 * NI], xo[16];
       {
         uint32_t aw0, aw1, ax0, ax1;
@@ -659,11 +721,17 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_big_kernel(Fp8GemmArgs a) {
         else wait12(wo);
         wait16(xo);
       }
-      // step ks + 1 has landed for this thread, then for everyone; every wave has read
-      // step ks's slot, which is refilled with step ks + NS
-      wait_vmcnt<OPS * (NS - 2)>();
+      wait_vmcnt<0>();
       barrier_only();
-      if (ks + NS < nk) issue(ks + NS, st);
+      {
+        const int iks = ks + NS;
+        if (iks < nk) {
+          issue(m0c, n0c, iks, st);
+        } else {
+          if (iks == nk) issue_scales(m0n, n0n, (r + 1) & 1);
+          issue(m0n, n0n, iks - nk, st);
+        }
+      }
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
         const i32x8 wf = frag(wo[2 * i], wo[2 * i + 1]);
@@ -673,17 +741,22 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_big_kernel(Fp8GemmArgs a) {
               wf, frag(xo[2 * j], xo[2 * j + 1]), acc[i][j], 0, 0, 0, 127, 0, 127);
       }
     }
-    // Epilogue: lane holds n = n0 + 128 wn + 16 i + 4 g4 + q of m = m0 + 128 wm + 16 j + l16;
-    // the row / column scales and biases come straight from global memory (L2-resident).
-    // One base pointer per tile and 32-bit offsets inside it (256 rows of ldo halves).
-    const int mb = m0 + 128 * wm + l16;
-    const int nb = n0 + 16 * NI * wn + 4 * g4;
-    uint16_t* const ob = (uint16_t*)a.out + (int64_t)mb * a.ldo + nb;
-    const float* const sap = a.sa + mb;
-    // (FP8_OUT_F16 never reaches this kernel: only 0 and 1 here)
-    if (a.out_mode) fp8_big_epilogue<true, NI>(acc, ob, a.ldo, sap, a.sw + nb, has_bias ? a.bias + nb : nullptr);
-    else fp8_big_epilogue<false, NI>(acc, ob, a.ldo, sap, a.sw + nb, has_bias ? a.bias + nb : nullptr);
+    // Epilogue: lane holds n = n0 + 16 NI wn + 16 i + 4 g4 + q of m = m0 + 128 wm + 16 j + l16.
+    {
+      float sm[8];
+      read_row_scales(r & 1, sm);
+      uint32_t ln = (uint32_t)lane;           // (not hoisted: see issue_scales)
+      asm volatile("" : "+v"(ln));
+      uint16_t* const ob = (uint16_t*)a.out + (int64_t)(m0c + 128 * wm) * a.ldo + n0c + 16 * NI * wn +
+                           ((ln & 15u) * (uint32_t)a.ldo + 4u * (ln >> 4));
+      if (a.out_mode) fp8_bigp_epilogue<true, NI>(acc, ob, a.ldo, sm, [&](int i, f32x4& sn, u32x2& bw) { read_col(r & 1, i, sn, bw); }, has_bias);
+      else fp8_bigp_epilogue<false, NI>(acc, ob, a.ldo, sm, [&](int i, f32x4& sn, u32x2& bw) { read_col(r & 1, i, sn, bw); }, has_bias);
+    }
+    m0c = m0n;
+    n0c = n0n;
+    tile_at(r + 2, m0n, n0n);
   }
+  wait_vmcnt<0>();                             // drain the clamped tail loads before exit
 }
 
 static int num_cus() {
@@ -859,31 +932,29 @@ extern "C" int omni_fp8_quant_tensor(const void* x, int ldx, void* q, float* sca
   return OMNI_OK;
 }
 
-// Kernel choice by shape, from the share of CU slots a grid's tiles keep busy over its
-// rounds ("fill"; one tile per CU per round).  The 256-row big tiles (256 or 192 columns,
-// one per workgroup) run where their fill is at least the 8-wave pipelined 256 x 128
-// form's for K >= 4096 and above it for shorter K (the best-filling width, 256 on a tie);
-// the pipelined form every other shape with at least 4 K steps; the double-buffered
-// one-tile-per-workgroup kernel the rest (K < 512).  MI355X, M = 8192, us (pipelined /
-// 256 x 192 / 256 x 256; outputs bit-equal): K 8960 -> N 1536 172.8 / 129.5 / 153.3;
-// 1536 -> 1536 47.9 / 38.9 / 46.6; 1536 -> 2048 44.9 / - / 45.2; 1536 -> 17920 342.2 /
-// - / 396.3; at M = 4096 (the big tiles filling half or less of the grid) 8960 -> 1536
-// 78.9 / 117.8 / 145.4, 1536 -> 1536 24.2 / 34.1 / 41.8.  Returns the big tile's width
-// (0: not big).
+// Kernel choice by shape: the persistent big tiles (256 x 256 or 256 x 192) where a cost
+// model of rounds of the grid (one tile per CU per round) times a tile's work puts them
+// ahead of the 8-wave pipelined 256 x 128 tiles: a big tile costs 0.85 x its size in
+// 256 x 128 tiles (fitted on MI355X: the big tiles' operand bytes per MFMA are lower); the
+// pipelined form every other shape with at least 4 K steps; the double-buffered
+// one-tile-per-workgroup kernel the rest (K < 512).  MI355X, us (pipelined / persistent
+// 256 x 192 / persistent 256 x 256, outputs bit-equal), M = 8192: K 1536 -> N 17920 344.4 /
+// - / 302.3; 1536 -> 2048 45.1 / - / 35.6; 1536 -> 1536 43.0 / 28.0 / 33.7; 8960 -> 1536
+// 156.7 / 100.3 / 121.4; M = 4096: 1536 -> 17920 172.9 / - / 146.8; 8960 -> 1536 78.8 /
+// 95.6 / 119.0 (hipBLASLt's row-wise _scaled_mm on the same shapes 245.9, 29.9, 27.0,
+// 93.3, 113.3, 60.8).  Returns the big tile's width (0: not big).
 static int fp8_big_cols(int M, int N, int K, int out_mode = FP8_OUT_F16_VIA_BF16) {
   if (K < 1024 || (M % F8B_T) || out_mode == FP8_OUT_F16) return 0;
   const int64_t cus = num_cus();
-  auto fill = [&](int64_t t) { return (double)t / (double)(((t + cus - 1) / cus) * cus); };
-  const double fp = fill((int64_t)(M / 256) * (N / F8_BT));
-  int best = 0;
-  double fb = 0.0;
+  auto rounds = [&](int64_t t) { return (t + cus - 1) / cus; };
+  double best = (double)rounds((int64_t)(M / 256) * (N / F8_BT));   // pipelined tiles
+  int cols = 0;
   for (int bn : {256, 192}) {
     if (N % bn) continue;
-    const double f = fill((int64_t)(M / F8B_T) * (N / bn));
-    if (f > fb) best = bn, fb = f;
+    const double c = (double)rounds((int64_t)(M / F8B_T) * (N / bn)) * (bn / 128.0) * 0.85;
+    if (c < best) best = c, cols = bn;
   }
-  if (!best) return 0;
-  return (K >= 4096 ? fb >= fp : fb > fp) ? best : 0;
+  return cols;
 }
 
 // Which kernel omni_fp8_gemm runs for a shape: 0 one tile per workgroup, 1 the pipelined
@@ -893,7 +964,8 @@ extern "C" int omni_fp8_gemm_plan(int M, int N, int K, int* grid) {
   int kind, g;
   const int bc = fp8_big_cols(M, N, K);
   if (bc) {
-    kind = bc == 256 ? 2 : 3, g = (M / F8B_T) * (N / bc);
+    const int t = (M / F8B_T) * (N / bc);
+    kind = bc == 256 ? 2 : 3, g = t < num_cus() ? t : num_cus();
   } else if (K / F8_BK >= 4) {
     const int64_t t8 = (int64_t)ceil_div(M, 256) * (N / F8_BT);
     kind = 1, g = (int)(t8 < num_cus() ? t8 : num_cus());
@@ -928,14 +1000,13 @@ extern "C" int omni_fp8_gemm(const void* xq, const float* sa, const void* wq, co
   a.K = K;
   a.out_mode = out_mode;
   const int bc = fp8_big_cols(M, N, K, out_mode);
-  if (bc == 256) {                                // 256 x 256 tiles, one per workgroup
-    const int grid = (M / F8B_T) * (N / 256);
-    hipLaunchKernelGGL((fp8_gemm_big_kernel<2, 8>), dim3((unsigned)grid), dim3(256), 0,
-                       (hipStream_t)stream, a);
-  } else if (bc == 192) {                         // 256 x 192 tiles, one per workgroup
-    const int grid = (M / F8B_T) * (N / 192);
-    hipLaunchKernelGGL((fp8_gemm_big_kernel<2, 6>), dim3((unsigned)grid), dim3(256), 0,
-                       (hipStream_t)stream, a);
+  if (bc) {                                       // persistent 256 x bc tiles
+    const int bt = (M / F8B_T) * (N / bc);
+    const int grid = bt < num_cus() ? bt : num_cus();
+    if (bc == 256)
+      hipLaunchKernelGGL((fp8_gemm_bigp_kernel<8>), dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, a);
+    else
+      hipLaunchKernelGGL((fp8_gemm_bigp_kernel<6>), dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, a);
   } else if (K / F8_BK >= 4) {                    // 8 waves, 256 x 128 tiles, 3 stages
     const int64_t t8 = (int64_t)ceil_div(M, 256) * (N / F8_BT);
     const int grid = (int)(t8 < num_cus() ? t8 : num_cus());

@@ -87,22 +87,28 @@ __device__ __forceinline__ half_t gp_gelu(half_t h) {
 struct GpTileSrc {
   const half_t* x[4];
   const half_t* w;       // GW_ROWS: the lane's row
-  const void* wp[4];     // GW_F16 / GW_INT4: the lane's block of each w load (step 0 / group 0)
+  const void* wp[6];     // GW_F16 / GW_INT4: the lane's block of each w load (step 0 / group 0)
   const half_t* sp;      // GW_INT4: the lane's scale pair (group 0)
   const half_t* b;
   int kb;                // the slice's first K step
   int kc;
 };
 
-template <int WF, int WM, int NS, int EPI>
+// NI: n sub-tiles of 16 per wave (tile columns BN = 32 NI: 128, or 192 for the packed fp16
+// weights with the STORE / PARTIAL epilogues).
+template <int WF, int WM, int NS, int EPI, int NI = 4>
 __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) {
 #pragma clang fp contract(off)
+  static_assert(NI == 4 || (NI == 6 && WF == GW_F16 && (EPI == GP_STORE || EPI == GP_PARTIAL)),
+                "192-column tiles: packed fp16 weights, STORE / PARTIAL epilogues");
   constexpr int BM = 64 * WM;
+  constexpr int BN = 32 * NI;
   constexpr int NWV = 2 * WM;
+  constexpr int NV = 2 * NI + 8;        // operand fragments per step: w 2 NI, then x 8
   constexpr int XLD = 4;                // x loads per wave and step (BM rows / 8 / NWV)
-  constexpr int WLD = 8 / WM;           // w loads per wave and step (16 per step / NWV)
+  constexpr int WLD = 2 * NI / WM;      // w loads per wave and step (4 NI per step / NWV)
   constexpr int OPS = XLD + WLD;        // loads every thread issues per step (waves 0, 1: + 1)
-  constexpr int WB = WF == GW_INT4 ? 16 * 256 : GP_BN * GP_ROWB;   // w bytes per stage
+  constexpr int WB = WF == GW_INT4 ? 16 * 256 : BN * GP_ROWB;      // w bytes per stage
   __shared__ __attribute__((aligned(1024))) uint8_t xl[NS][BM * GP_ROWB];
   __shared__ __attribute__((aligned(1024))) uint8_t wl[NS][WB];
   // bias slot: 64 lanes x 16 bytes land per load (lanes 16-63 repeat lane 15's chunk)
@@ -117,7 +123,7 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
   const int l16 = lane & 15;
   const int g4 = lane >> 4;
 
-  const int tiles_n = a.N / GP_BN;
+  const int tiles_n = a.N / BN;
   const int tiles_m = (a.M + BM - 1) / BM;
   const int tiles = tiles_m * tiles_n;
   const int items = tiles * a.KS;                        // slice-major: item = s tiles + tile
@@ -139,7 +145,7 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
     int tm, tn;
     grouped_tile(it - sl * tiles, tiles_m, tiles_n, GP_GM, tm, tn);
     m0 = tm * BM;
-    n0 = tn * GP_BN;
+    n0 = tn * BN;
     // slices are whole 128-k groups (pairs of steps): the main loop takes two steps at a
     // time, and an int4 step's scales are its group's
     const int kb = 2 * (sl * (nk / 2) / a.KS);
@@ -169,7 +175,7 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
       // lane i: scales 2 (i % 8), +1 of column tile i / 8
       t.sp = a.wsc + (int64_t)(n0 / 16 + lane / 8) * (a.K / 128) * 16 + 2 * (lane & 7);
     }
-    t.b = has_bias ? a.bias + n0 + 8 * min(lane, 15) : a.x;
+    t.b = has_bias ? a.bias + n0 + 8 * min(lane, BN / 8 - 1) : a.x;
     return t;
   };
   const int64_t wstep = (int64_t)8 * NWV * a.ldw;       // halfs between w row groups
@@ -219,10 +225,10 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
     b[1] = row + (((4 + g4) ^ (r & 7)) << 4);
   };
   auto packed_base = [&](int st) -> uint32_t {
-    return (uint32_t)(uintptr_t)(lds_u8*)&wl[st][0] + (uint32_t)(8 * wn) * (WF == GW_INT4 ? 256u : 1024u) +
+    return (uint32_t)(uintptr_t)(lds_u8*)&wl[st][0] + (uint32_t)(2 * NI * wn) * (WF == GW_INT4 ? 256u : 1024u) +
            (uint32_t)lane * (WF == GW_INT4 ? 4u : 16u);
   };
-  auto read_issue = [&](int st, u32x4 (&v)[16]) {
+  auto read_issue = [&](int st, u32x4 (&v)[NV]) {
     uint32_t bx[2];
     row_bases(&xl[st][0], 64 * wm, bx);
     if constexpr (WF == GW_ROWS) {
@@ -248,7 +254,7 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
           : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]), "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11]), "=&v"(v[12]), "=&v"(v[13]), "=&v"(v[14]), "=&v"(v[15])
           : "v"(bw[0]), "v"(bw[1]), "v"(bx[0]), "v"(bx[1])
           : "memory");
-    } else {
+    } else if constexpr (NI == 4) {
       const uint32_t bw = packed_base(st);
       asm volatile(
         "ds_read_b128 %0, %16 offset:0\n\t"
@@ -270,11 +276,38 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
           : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]), "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11]), "=&v"(v[12]), "=&v"(v[13]), "=&v"(v[14]), "=&v"(v[15])
           : "v"(bw), "v"(bx[0]), "v"(bx[1])
           : "memory");
+    } else {
+      // 192-column tiles: the wave's 6 column tiles x 2 halves, then x
+      const uint32_t bw = packed_base(st);
+      asm volatile(
+        "ds_read_b128 %0, %20 offset:0\n\t"
+        "ds_read_b128 %1, %20 offset:1024\n\t"
+        "ds_read_b128 %2, %20 offset:2048\n\t"
+        "ds_read_b128 %3, %20 offset:3072\n\t"
+        "ds_read_b128 %4, %20 offset:4096\n\t"
+        "ds_read_b128 %5, %20 offset:5120\n\t"
+        "ds_read_b128 %6, %20 offset:6144\n\t"
+        "ds_read_b128 %7, %20 offset:7168\n\t"
+        "ds_read_b128 %8, %20 offset:8192\n\t"
+        "ds_read_b128 %9, %20 offset:9216\n\t"
+        "ds_read_b128 %10, %20 offset:10240\n\t"
+        "ds_read_b128 %11, %20 offset:11264\n\t"
+        "ds_read_b128 %12, %21 offset:0\n\t"
+        "ds_read_b128 %13, %22 offset:0\n\t"
+        "ds_read_b128 %14, %21 offset:2048\n\t"
+        "ds_read_b128 %15, %22 offset:2048\n\t"
+        "ds_read_b128 %16, %21 offset:4096\n\t"
+        "ds_read_b128 %17, %22 offset:4096\n\t"
+        "ds_read_b128 %18, %21 offset:6144\n\t"
+        "ds_read_b128 %19, %22 offset:6144"
+          : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]), "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11]), "=&v"(v[12]), "=&v"(v[13]), "=&v"(v[14]), "=&v"(v[15]), "=&v"(v[16]), "=&v"(v[17]), "=&v"(v[18]), "=&v"(v[19])
+          : "v"(bw), "v"(bx[0]), "v"(bx[1])
+          : "memory");
     }
   };
   // GW_INT4: the 8 x fragments (b128), the 8 step words of the wave's 4 tiles (b32) and
   // their 4 column scales (u16)
-  auto read_issue_q = [&](int st, u32x4 (&v)[16], uint32_t (&wd)[8], uint32_t (&sc)[4]) {
+  auto read_issue_q = [&](int st, u32x4 (&v)[NV], uint32_t (&wd)[8], uint32_t (&sc)[4]) {
     uint32_t bx[2];
     row_bases(&xl[st][0], 64 * wm, bx);
     const uint32_t bw = packed_base(st);
@@ -313,7 +346,7 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
         : "v"(bs)
         : "memory");
   };
-  auto read_wait_q = [&](u32x4 (&v)[16], uint32_t (&wd)[8], uint32_t (&sc)[4]) {
+  auto read_wait_q = [&](u32x4 (&v)[NV], uint32_t (&wd)[8], uint32_t (&sc)[4]) {
     asm volatile("s_waitcnt lgkmcnt(0)"
                  : "+v"(v[8]), "+v"(v[9]), "+v"(v[10]), "+v"(v[11]), "+v"(v[12]), "+v"(v[13]),
                    "+v"(v[14]), "+v"(v[15]), "+v"(wd[0]), "+v"(wd[1]), "+v"(wd[2]), "+v"(wd[3]),
@@ -322,27 +355,38 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
                  :
                  : "memory");
   };
-  auto read_wait = [&](u32x4 (&v)[16]) {
+  auto read_wait = [&](u32x4 (&v)[NV]) {
     asm volatile("s_waitcnt lgkmcnt(0)"
                  : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
                    "+v"(v[6]), "+v"(v[7]), "+v"(v[8]), "+v"(v[9]), "+v"(v[10]), "+v"(v[11]),
                    "+v"(v[12]), "+v"(v[13]), "+v"(v[14]), "+v"(v[15])
                  :
                  : "memory");
+    if constexpr (NV > 16) asm volatile("" : "+v"(v[16]), "+v"(v[17]), "+v"(v[18]), "+v"(v[19]));
   };
   // the tile's biases of this lane's columns (4 per n sub-tile), read at the tile's last step
-  uint2 bv[4] = {};
+  uint2 bv[NI] = {};
   auto read_bias = [&](int st) {
     typedef __attribute__((address_space(3))) half_t lds_f16;
-    uint32_t ab[4];
+    uint32_t ab[NI];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ab[i] = (uint32_t)(uintptr_t)(lds_f16*)&bsl[st][64 * wn + 16 * i + 4 * g4];
-    asm volatile(
-        "ds_read_b64 %0, %4\n\tds_read_b64 %1, %5\n\tds_read_b64 %2, %6\n\tds_read_b64 %3, %7\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(bv[0]), "=&v"(bv[1]), "=&v"(bv[2]), "=&v"(bv[3])
-        : "v"(ab[0]), "v"(ab[1]), "v"(ab[2]), "v"(ab[3])
-        : "memory");
+    for (int i = 0; i < NI; ++i) ab[i] = (uint32_t)(uintptr_t)(lds_f16*)&bsl[st][16 * NI * wn + 16 * i + 4 * g4];
+    if constexpr (NI == 4) {
+      asm volatile(
+          "ds_read_b64 %0, %4\n\tds_read_b64 %1, %5\n\tds_read_b64 %2, %6\n\tds_read_b64 %3, %7\n\t"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(bv[0]), "=&v"(bv[1]), "=&v"(bv[2]), "=&v"(bv[3])
+          : "v"(ab[0]), "v"(ab[1]), "v"(ab[2]), "v"(ab[3])
+          : "memory");
+    } else {
+      asm volatile(
+          "ds_read_b64 %0, %6\n\tds_read_b64 %1, %7\n\tds_read_b64 %2, %8\n\t"
+          "ds_read_b64 %3, %9\n\tds_read_b64 %4, %10\n\tds_read_b64 %5, %11\n\t"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(bv[0]), "=&v"(bv[1]), "=&v"(bv[2]), "=&v"(bv[3]), "=&v"(bv[4]), "=&v"(bv[5])
+          : "v"(ab[0]), "v"(ab[1]), "v"(ab[2]), "v"(ab[3]), "v"(ab[4]), "v"(ab[5])
+          : "memory");
+    }
   };
 
   int m0c, n0c, m0n, n0n, slc, sln;
@@ -352,9 +396,10 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
   for (int s = 0; s < NS; ++s) issue(cur, s, s);
   gp_wait_vmcnt<OPS * (NS - 1)>();
   gp_barrier();
-  // A step's operands: 16 fragments (w 0-7, x 8-15) and, GW_INT4, the raw words and scales
+  // A step's operands: NV fragments (w 0 .. 2 NI - 1, then x) and, GW_INT4, the raw words
+  // and scales
   struct Ops {
-    u32x4 v[16];
+    u32x4 v[NV];
     uint32_t wd[8], sc[4];
   };
   auto rd_issue = [&](int st, Ops& o) {
@@ -375,15 +420,15 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
       read_wait(o.v);
     }
   };
-  auto mfmas = [&](const Ops& o, f32x4 (&acc)[4][4]) {
+  auto mfmas = [&](const Ops& o, f32x4 (&acc)[NI][4]) {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < NI; ++i) {
         const half8_t wf = __builtin_bit_cast(half8_t, o.v[2 * i + t]);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const half8_t xf = __builtin_bit_cast(half8_t, o.v[8 + 2 * j + t]);
+          const half8_t xf = __builtin_bit_cast(half8_t, o.v[2 * NI + 2 * j + t]);
           acc[i][j] = mfma16x16x32(wf, xf, acc[i][j]);
         }
       }
@@ -395,7 +440,7 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
   // alternate over the steps: every K slice is an even number of steps, so the sets' roles
   // are fixed at compile time within a two-step iteration, and the next tile's first step
   // (read ahead during the last MFMAs of a tile) is always in set A.
-  auto step = [&](Ops& now, Ops& later, f32x4 (&acc)[4][4], int ks, int kc, int sidx, bool last) {
+  auto step = [&](Ops& now, Ops& later, f32x4 (&acc)[NI][4], int ks, int kc, int sidx, bool last) {
     const int st = sidx % NS;
     rd_wait(now);
     if (last && has_bias) read_bias(st);
@@ -412,6 +457,8 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
                    "+v"(now.v[5]), "+v"(now.v[6]), "+v"(now.v[7]), "+v"(now.v[8]), "+v"(now.v[9]),
                    "+v"(now.v[10]), "+v"(now.v[11]), "+v"(now.v[12]), "+v"(now.v[13]),
                    "+v"(now.v[14]), "+v"(now.v[15]));
+    if constexpr (NV > 16)
+      asm volatile("" : "+v"(now.v[16]), "+v"(now.v[17]), "+v"(now.v[18]), "+v"(now.v[19]));
     mfmas(now, acc);
   };
   Ops A, B;
@@ -419,24 +466,24 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
   int sidx = 0;
   for (int r = 0; r < my_items; ++r) {
     const int kc = cur.kc;
-    f32x4 acc[4][4];   // [n sub-tile][m sub-tile]
+    f32x4 acc[NI][4];   // [n sub-tile][m sub-tile]
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NI; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
     for (int ks = 0; ks < kc; ks += 2, sidx += 2) {
       step(A, B, acc, ks, kc, sidx, false);
       step(B, A, acc, ks + 1, kc, sidx + 1, ks + 2 == kc);
     }
-    // Epilogue: lane holds n = n0 + 64 wn + 16 i + 4 g4 + q of m = m0 + 64 wm + 16 j + l16.
+    // Epilogue: lane holds n = n0 + 16 NI wn + 16 i + 4 g4 + q of m = m0 + 64 wm + 16 j + l16.
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int m = m0c + 64 * wm + 16 * j + l16;
       if (m >= a.M) continue;
       if (a.KS > 1 || EPI == GP_PARTIAL) {   // the slice's fp32 partial sums
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int n = n0c + 64 * wn + 16 * i + 4 * g4;
+        for (int i = 0; i < NI; ++i) {
+          const int n = n0c + 16 * NI * wn + 16 * i + 4 * g4;
           *(f32x4*)(a.part + ((int64_t)slc * a.M + m) * a.N + n) = acc[i][j];
         }
         continue;
@@ -456,8 +503,8 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
         continue;
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int n = n0c + 64 * wn + 16 * i + 4 * g4;
+      for (int i = 0; i < NI; ++i) {
+        const int n = n0c + 16 * NI * wn + 16 * i + 4 * g4;
         const half4_t bb = __builtin_bit_cast(half4_t, bv[i]);
         half4_t rr = (half4_t){0, 0, 0, 0};
         if constexpr (EPI == GP_RESID) rr = *(const half4_t*)(a.res + (int64_t)m * a.ldr + n);
@@ -524,21 +571,21 @@ __global__ __launch_bounds__(256) void gemm_pipe_finish_kernel(GemmPipeArgs a) {
   *(half4_t*)(a.out + (int64_t)m * a.ldo + n) = o;
 }
 
-template <int WF, int WM, int NS>
+template <int WF, int WM, int NS, int NI = 4>
 static int gp_launch(const GemmPipeArgs& a, int epilogue, hipStream_t st) {
-  const int64_t items = (int64_t)ceil_div(a.M, 64 * WM) * (a.N / GP_BN) * a.KS;
+  const int64_t items = (int64_t)ceil_div(a.M, 64 * WM) * (a.N / (32 * NI)) * a.KS;
   if (items > 0x7fffffff) return OMNI_EUNSUPPORTED;
   const int grid = (int)(items < gp_num_cus() ? items : gp_num_cus());
   const dim3 blk(128 * WM);
   if (epilogue == GP_PARTIAL) {      // the slices' partial sums only, for a consumer to add
     if constexpr (WF == GW_ROWS) return OMNI_EINVAL;
-    else hipLaunchKernelGGL((gemm_pipe_kernel<WF, WM, NS, GP_PARTIAL>), dim3(grid), blk, 0, st, a);
+    else hipLaunchKernelGGL((gemm_pipe_kernel<WF, WM, NS, GP_PARTIAL, NI>), dim3(grid), blk, 0, st, a);
     OMNI_CHECK_LAUNCH();
     return OMNI_OK;
   }
   if (a.KS > 1) {                    // partial sums, then the finish kernel's epilogue
     if (epilogue == GP_SILU) return OMNI_EINVAL;
-    hipLaunchKernelGGL((gemm_pipe_kernel<WF, WM, NS, GP_STORE>), dim3(grid), blk, 0, st, a);
+    hipLaunchKernelGGL((gemm_pipe_kernel<WF, WM, NS, GP_STORE, NI>), dim3(grid), blk, 0, st, a);
     OMNI_CHECK_LAUNCH();
     const int64_t nthr = (int64_t)a.M * (a.N / 4);
     const dim3 fg((unsigned)((nthr + 255) / 256));
@@ -549,6 +596,12 @@ static int gp_launch(const GemmPipeArgs& a, int epilogue, hipStream_t st) {
       case GP_RESID: hipLaunchKernelGGL((gemm_pipe_finish_kernel<GP_RESID>), fg, dim3(256), 0, st, a); break;
       default: return OMNI_EINVAL;
     }
+    OMNI_CHECK_LAUNCH();
+    return OMNI_OK;
+  }
+  if constexpr (NI != 4) {            // the wide tiles store only
+    if (epilogue != GP_STORE) return OMNI_EINVAL;
+    hipLaunchKernelGGL((gemm_pipe_kernel<WF, WM, NS, GP_STORE, NI>), dim3(grid), blk, 0, st, a);
     OMNI_CHECK_LAUNCH();
     return OMNI_OK;
   }
@@ -565,6 +618,18 @@ static int gp_launch(const GemmPipeArgs& a, int epilogue, hipStream_t st) {
   }
   OMNI_CHECK_LAUNCH();
   return OMNI_OK;
+}
+
+// Whether the packed fp16 weights take 128 x 192 tiles (4 waves, 64 x 96 each, 3 stages)
+// instead of the tiles of tile_rows x 128: when the grid's rounds times a tile's outputs
+// come out smaller (config 5's N = 1536 projections at M = 4096: 256 tiles in one round
+// against 192 of 256 x 128, which leave a quarter of the CUs idle).
+static bool gp_wide_tiles(int M, int N, int tile_rows) {
+  if (N % 192) return false;
+  const int64_t cus = gp_num_cus();
+  const int64_t tn = (int64_t)ceil_div(M, tile_rows) * (N / GP_BN);
+  const int64_t tw = (int64_t)ceil_div(M, 128) * (N / 192);
+  return ((tw + cus - 1) / cus) * 128 * 192 < ((tn + cus - 1) / cus) * tile_rows * GP_BN;
 }
 
 static int gp_tile_rows(int M, int N) {
@@ -653,6 +718,35 @@ extern "C" int omni_f16_gemm_pipe(const void* x, int ldx, const void* w, const v
                           : gp_launch<GW_ROWS, 2, 4>(a, epilogue, st);
 }
 
+// omni_packed_gemm_pipe's tiling for a shape: tile rows and columns and K slices, from the
+// caller's tile_rows / ksplit (0: chosen).  128 x 192 tiles only where both were chosen.
+static void gp_packed_plan(int M, int N, int K, int fmt, int epilogue, int tile_rows, int ksplit,
+                           int& rows, int& cols, int& ks) {
+  rows = tile_rows ? tile_rows : gp_tile_rows(M, N);
+  ks = ksplit ? ksplit : (epilogue == GP_SILU ? 1 : omni_f16_gemm_pipe_splits(M, N, K, rows));
+  cols = GP_BN;
+  if (fmt == 1 && tile_rows == 0 && ks == 1 && (epilogue == GP_STORE || epilogue == GP_PARTIAL) &&
+      gp_wide_tiles(M, N, rows)) {
+    rows = 128;
+    cols = 192;
+  }
+}
+
+// The tiling omni_packed_gemm_pipe runs for a shape (no reference counterpart: it tells a
+// caller or a test which tile form covers the shape).
+extern "C" int omni_packed_gemm_pipe_plan(int M, int N, int K, int fmt, int epilogue,
+                                          int tile_rows, int ksplit, int* rows, int* cols,
+                                          int* ks) {
+  if (M <= 0 || N <= 0 || K <= 0 || (N % GP_BN) || (K % 128) || (fmt != 0 && fmt != 1)) return OMNI_EINVAL;
+  if (tile_rows != 0 && tile_rows != 128 && tile_rows != 256) return OMNI_EINVAL;
+  int r, c, k;
+  gp_packed_plan(M, N, K, fmt, epilogue, tile_rows, ksplit, r, c, k);
+  if (rows) *rows = r;
+  if (cols) *cols = c;
+  if (ks) *ks = k;
+  return OMNI_OK;
+}
+
 // The decoder's prefill linears on the same pipeline with this library's packed weights
 // (fmt 0: int4 from omni_gptq_repack with its scales, 1: fp16 from omni_f16_pack); see the
 // header for the arguments.  Stages per tile height: int4 6 (128 rows) / 4 (256 rows),
@@ -675,9 +769,9 @@ extern "C" int omni_packed_gemm_pipe(const void* x, int ldx, const void* w_packe
   if (bias && ((uintptr_t)bias & 15)) return OMNI_EINVAL;
   if ((epilogue == GP_SILU || part) && bias) return OMNI_EINVAL;
   if (tile_rows != 0 && tile_rows != 128 && tile_rows != 256) return OMNI_EINVAL;
-  if (tile_rows == 0) tile_rows = gp_tile_rows(M, N);
   if (fmt == 0 && ((uintptr_t)scales_packed & 3)) return OMNI_EINVAL;
-  if (ksplit == 0) ksplit = epilogue == GP_SILU ? 1 : omni_f16_gemm_pipe_splits(M, N, K, tile_rows);
+  int cols;
+  gp_packed_plan(M, N, K, fmt, epilogue, tile_rows, ksplit, tile_rows, cols, ksplit);
   if (epilogue == GP_SILU && ksplit != 1) return OMNI_EINVAL;
   // every slice covers at least NS pipeline steps (slices are whole 128-groups of 2 steps)
   const int ns = fmt == 0 ? (tile_rows == 256 ? 4 : 6) : (tile_rows == 256 ? 3 : 4);
@@ -705,6 +799,7 @@ extern "C" int omni_packed_gemm_pipe(const void* x, int ldx, const void* w_packe
   if (fmt == 0)
     return tile_rows == 256 ? gp_launch<GW_INT4, 4, 4>(a, epilogue, st)
                             : gp_launch<GW_INT4, 2, 6>(a, epilogue, st);
+  if (cols == 192) return gp_launch<GW_F16, 2, 3, 6>(a, epilogue, st);
   return tile_rows == 256 ? gp_launch<GW_F16, 4, 3>(a, epilogue, st)
                           : gp_launch<GW_F16, 2, 4>(a, epilogue, st);
 }

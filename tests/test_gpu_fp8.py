@@ -4,13 +4,12 @@ the oracle on the same quantised operands.
 
 Shapes (K -> N): QKV 1536 -> 2048 (with the q|k|v bias), O 1536 -> 1536, gate/up
 1536 -> 17920, down 8960 -> 1536; x ~ N(0, 1) fp16, W ~ N(0, 0.02) fp16 (config 4).  At
-M = 8192 every shape runs a persistent grid over many tile rounds (gate/up: 32 x 140
-tiles of 256 x 128 on 256 workgroups, 18 rounds), O and the down projection on 256 x 192
-tiles (256 of them: one per CU); K = 4096 -> N = 2048 takes the 256 x 256 tiles, and the
-down shape at M = 4096 (big tiles would fill half the grid) the 256 x 128 pipeline; a
-ragged M puts a partial tile in the last round, and K < 512 takes the one-tile-per-workgroup
-kernel.  ``omni_fp8_gemm_plan`` names the kernel and grid each
-case runs, so the test states which path it covered.
+M = 8192 every config-4 shape runs a persistent grid of 256-row big tiles (gate/up: 32 x 70
+tiles of 256 x 256 on 256 workgroups, 9 rounds; O and down 256 tiles of 256 x 192, one
+per CU); the 256 x 128 pipeline takes the down shape at M = 4096 (big tiles would fill half
+the grid) and a ragged M (a partial tile in the last round); K < 512 takes the
+one-tile-per-workgroup kernel.  ``omni_fp8_gemm_plan`` names the kernel and grid each case
+runs, so the test states which path it covered.
 
 The oracle's product is computed for 8 rows of every 256-row block (one row in each of
 the four 64-row wave bands, several 16-row sub-tiles and lane positions) and every column:
@@ -25,8 +24,8 @@ from oracle import qwen2_ref as ref
 
 pytestmark = pytest.mark.gpu
 
-KIND = {0: "one tile per workgroup", 1: "pipelined 256x128 persistent", 2: "256x256 tiles",
-        3: "256x192 tiles"}
+KIND = {0: "one tile per workgroup", 1: "pipelined 256x128 persistent",
+        2: "persistent 256x256 tiles", 3: "persistent 256x192 tiles"}
 COLS = {0: 128, 1: 128, 2: 256, 3: 192}
 BLOCK_ROWS = (0, 17, 63, 98, 133, 228, 239, 255)    # within each 256-row block
 

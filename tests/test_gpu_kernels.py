@@ -414,6 +414,52 @@ def test_tiled_gemm(gpu, fmt, M, K, N, bias, silu):
             assert (sp.cpu().float() - e).abs().max().item() <= 2e-3 * max(1.0, e.abs().max().item())
 
 
+def _packed_plan(M, N, K, fmt, epi):
+    import ctypes
+    from omniserver_amd._lib import lib
+    r, c, k = ctypes.c_int(0), ctypes.c_int(0), ctypes.c_int(0)
+    assert lib().omni_packed_gemm_pipe_plan(M, N, K, fmt, epi, 0, 0, ctypes.byref(r),
+                                            ctypes.byref(c), ctypes.byref(k)) == 0
+    return r.value, c.value, k.value
+
+
+@pytest.mark.parametrize("M,K,bias", [(4096, 1536, True), (4000, 8960, False)])
+def test_packed_gemm_pipe_wide_tiles(gpu, M, K, bias):
+    """The 128 x 192 tiles omni_packed_gemm_pipe picks for config 5's N = 1536 projections
+    (fp16 weights, one K slice; a ragged M puts a partial row tile in the round): STORE
+    and PARTIAL results equal the 256 x 128 tiles' bit for bit (same k order per output),
+    and 64 sampled rows (every row tile) are within tolerance of the oracle."""
+    from omniserver_amd._lib import call, ptr, stream
+    from omniserver_amd.linear import F16Linear
+    N = 1536
+    rows, cols, ks = _packed_plan(M, N, K, 1, 0)
+    say(f"packed gemm pipe wide tiles M={M} K={K} N={N} bias={bias}: {rows} x {cols}, {ks} slice")
+    assert (rows, cols, ks) == (128, 192, 1)
+    assert _packed_plan(M, N, K, 1, 2)[1] == 192
+    wt = f16((N, K), 99, 0.02)
+    b = f16((N,), 100, 0.02) if bias else None
+    x = f16((M, K), 101)
+    lin = F16Linear(wt.to(gpu), None if b is None else b.to(gpu))
+    xg = x.to(gpu)
+
+    def run(tile_rows, epi):
+        out = torch.full((M, N), float("nan"), device=gpu, dtype=torch.float16)
+        ws = torch.full((M * N,), float("nan"), device=gpu, dtype=torch.float32)
+        call("omni_packed_gemm_pipe", ptr(xg), K, ptr(lin.weight_packed), None, 1,
+             ptr(lin.bias) if epi == 0 else None, 0, ptr(out) if epi == 0 else None, N, M, N, K,
+             epi, tile_rows, 1, ptr(ws) if epi == 2 else None, stream())
+        torch.cuda.synchronize()
+        return out.cpu() if epi == 0 else ws.cpu()
+
+    wide, o256 = run(0, 0), run(256, 0)
+    assert torch.equal(wide, o256)
+    assert torch.equal(run(0, 2), run(256, 2))
+    rows_s = torch.tensor(sorted({64 * i + (37 * i) % 64 for i in range(M // 64)} | {M - 1}))
+    e = ref.linear(x[rows_s].float(), wt.float().t(), None if b is None else b.float())
+    tol = 2e-3 * max(1.0, e.abs().max().item())
+    assert (wide[rows_s].float() - e).abs().max().item() <= tol
+
+
 @pytest.mark.parametrize("fmt", ["int4", "fp16"])
 @pytest.mark.parametrize("M", [65, 300, 1000])
 @pytest.mark.parametrize("K,N,bias,silu", [

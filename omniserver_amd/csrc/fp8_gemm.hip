@@ -468,25 +468,26 @@ __global__ __launch_bounds__(128 * WM, 1) void fp8_gemm_pipe_kernel(Fp8GemmArgs 
   wait_vmcnt<0>();                     // drain the clamped tail loads before exit
 }
 
-// Large-tile form: 256 x 256 output tiles, 4 waves (one per SIMD) each owning a 128 (m) x
-// 128 (n) block, so every operand byte staged through LDS feeds twice the MFMA work of the
-// 64 x 64 blocks above (a 256 x 128 tile re-reads its operand rows from L2 for every
-// 128 columns; this one for every 256).  Per K step a wave issues 32 operand reads (32 bytes
-// per lane of 8 w and 8 x row groups) and 64 MFMAs; two stages of 64 KB each are in LDS
-// (the next step's operands land while this step's MFMAs run).  Same staging (direct
+// Large-tile form: 256 x 256 output tiles, 8 waves (two per SIMD: 2 along m x 4 along n)
+// each owning a 128 (m) x 64 (n) block, so every operand byte staged through LDS feeds twice
+// the MFMA work it feeds in the 256 x 128 tiles above (those re-read their operand rows from
+// L2 for every 128 columns; this one for every 256).  Per K step a wave issues 24 operand
+// reads (32 bytes per lane of 4 w and 8 x row groups) and 32 MFMAs; two stages of 64 KB each
+// are in LDS (the next step's operands land while this step's MFMAs run), and the second
+// wave on each SIMD keeps its matrix core busy while the first waits (on MI355X 6-11 %
+// faster than four waves of 128 x 128, outputs bit-equal).  Same staging (direct
 // global->LDS loads, XOR-swizzled 128-byte rows) and XCD-grouped tile order as the kernel
-// above.  NI = 6 narrows the tile to 256 x 192 (each wave 128 x 96, 12 w row groups): N =
-// 1536 then makes 8 column tiles, so M = 8192 gives 256 tiles, one per CU, where the
-// 256-column tiles leave a quarter of the CUs idle.
+// above.  NI = 6 narrows the tile to 256 x 192 (each wave 128 x 48): N = 1536 then makes 8
+// column tiles, so M = 8192 gives 256 tiles, one per CU, where the 256-column tiles leave a
+// quarter of the CUs idle.
 #define F8B_T 256
 
 // Output bits of one product value v = acc * sa * sw: bf16(v), then either that bf16 plus
 // bf16(bias) as a bf16 add (FP8_OUT_BF16: forward_prequant, out + bias.to(bf16)) or the
 // bf16 rounded to fp16 plus the fp16 bias as an fp16 add (FP8_OUT_F16_VIA_BF16: the
 // row-wise forward).  A zero bias is the identity in both (x + 0 rounds to x).  The
-// per-tensor form (FP8_OUT_F16) does not run here: a third epilogue form does not fit
-// beside this kernel's 256 accumulators without spilling, so omni_fp8_gemm sends it to
-// the 256 x 128 kernel.
+// per-tensor form (FP8_OUT_F16) does not run here (omni_fp8_gemm sends it to the 256 x 128
+// kernel, which has all three forms).
 template <bool OUT_BF16>
 __device__ __forceinline__ uint32_t fp8_out_bits(float v, half_t bias) {
   const uint32_t b = f32_to_bf16_bits(v);
@@ -502,13 +503,13 @@ __device__ __forceinline__ uint32_t fp8_out_bits(float v, half_t bias) {
 // tile's row / column scales and biases ride with its first stage into an LDS slot of their
 // own (two, by tile parity), which the epilogue reads with its own lgkmcnt wait: an epilogue
 // that read them from global memory would wait (vmcnt) for the next tile's stages in flight.
-template <bool OUT_BF16, int NI, typename ReadCol>
-__device__ __forceinline__ void fp8_bigp_epilogue(const f32x4 (&acc)[NI][8], uint16_t* ob, int ldo,
+template <bool OUT_BF16, int NIW, typename ReadCol>
+__device__ __forceinline__ void fp8_bigp_epilogue(const f32x4 (&acc)[NIW][8], uint16_t* ob, int ldo,
                                                   const float (&sm)[8], ReadCol read_col,
                                                   bool has_bias) {
 #pragma clang fp contract(off)
 #pragma unroll
-  for (int i = 0; i < NI; ++i) {
+  for (int i = 0; i < NIW; ++i) {
     f32x4 snv;
     u32x2 bw;
     read_col(i, snv, bw);       // column scales and biases of n sub-tile i
@@ -530,12 +531,13 @@ __device__ __forceinline__ void fp8_bigp_epilogue(const f32x4 (&acc)[NI][8], uin
 }
 
 template <int NI>
-__global__ __launch_bounds__(256, 1) void fp8_gemm_bigp_kernel(Fp8GemmArgs a) {
+__global__ __launch_bounds__(512, 1) void fp8_gemm_bigp_kernel(Fp8GemmArgs a) {
 #pragma clang fp contract(off)
   constexpr int NS = 2;                       // stages (64 KB + 16 NI * 2 KB each)
-  constexpr int BN = 32 * NI;                 // tile columns: two waves of 16 NI
-  constexpr int XLD = 8;                      // x loads per wave and stage (256 rows / 8 / 4)
-  constexpr int WLD = NI;                     // w loads per wave and stage (BN rows / 8 / 4)
+  constexpr int BN = 32 * NI;                 // tile columns: four waves of 8 NI
+  constexpr int XLD = 4;                      // x loads per wave and stage (256 rows / 8 / 8)
+  constexpr int WLD = NI / 2;                 // w loads per wave and stage (BN rows / 8 / 8)
+  constexpr int NIW = NI / 2;                 // n sub-tiles per wave (4 waves along n)
   constexpr int OPS = XLD + WLD;              // operand loads every thread issues per stage
   static_assert(NI == 6 || NI == 8, "tile widths 192 and 256");
   __shared__ __attribute__((aligned(1024))) uint8_t xl[NS][F8B_T * F8_ROWB];
@@ -545,8 +547,8 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_bigp_kernel(Fp8GemmArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wn = wave & 1;
-  const int wm = wave >> 1;
+  const int wn = wave & 3;
+  const int wm = wave >> 2;
   const int l16 = lane & 15;
   const int g4 = lane >> 4;
 
@@ -570,7 +572,7 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_bigp_kernel(Fp8GemmArgs a) {
   typedef __attribute__((address_space(3))) uint8_t lds_u8;
   const bool has_bias = a.bias != nullptr;
   const uint32_t loff = (uint32_t)lrow * (uint32_t)a.K + (uint32_t)lchunk * 16u;
-  const uint32_t rstep = 32u * (uint32_t)a.K;
+  const uint32_t rstep = 64u * (uint32_t)a.K;
   auto issue = [&](int m0, int n0, int ks, int st) {
     const uint8_t* const xs = a.xq + (int64_t)m0 * a.K;
     const uint8_t* const ws = a.wq + (int64_t)n0 * a.K;
@@ -578,11 +580,11 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_bigp_kernel(Fp8GemmArgs a) {
 #pragma unroll
     for (int u = 0; u < XLD; ++u)
       __builtin_amdgcn_global_load_lds((const void*)(xs + (k0 + u * rstep)),
-                                       (lds_void*)((lds_u8*)&xl[st][(32 * u + 8 * wave) * F8_ROWB]), 16, 0, 0);
+                                       (lds_void*)((lds_u8*)&xl[st][(64 * u + 8 * wave) * F8_ROWB]), 16, 0, 0);
 #pragma unroll
     for (int u = 0; u < WLD; ++u)
       __builtin_amdgcn_global_load_lds((const void*)(ws + (k0 + u * rstep)),
-                                       (lds_void*)((lds_u8*)&wl[st][(32 * u + 8 * wave) * F8_ROWB]), 16, 0, 0);
+                                       (lds_void*)((lds_u8*)&wl[st][(64 * u + 8 * wave) * F8_ROWB]), 16, 0, 0);
   };
   // the tile's 256 row scales (one per thread), BN column scales (waves < BN / 64) and BN
   // biases (wave 0, 16 bytes a lane; lanes past BN / 8 repeat the last chunk)
@@ -592,9 +594,11 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_bigp_kernel(Fp8GemmArgs a) {
   auto issue_scales = [&](int m0, int n0, int p) {
     uint32_t ln = (uint32_t)lane;
     asm volatile("" : "+v"(ln));
-    const uint8_t* const sab = (const uint8_t*)(a.sa + m0 + 64 * wave);
-    __builtin_amdgcn_global_load_lds((const void*)(sab + 4u * ln),
-                                     (lds_void*)((lds_u8*)&scl[p][64 * wave]), 4, 0, 0);
+    if (wave < 4) {
+      const uint8_t* const sab = (const uint8_t*)(a.sa + m0 + 64 * wave);
+      __builtin_amdgcn_global_load_lds((const void*)(sab + 4u * ln),
+                                       (lds_void*)((lds_u8*)&scl[p][64 * wave]), 4, 0, 0);
+    }
     if (wave < BN / 64) {
       const uint8_t* const swb = (const uint8_t*)(a.sw + n0 + 64 * wave);
       __builtin_amdgcn_global_load_lds((const void*)(swb + 4u * ln),
@@ -628,19 +632,6 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_bigp_kernel(Fp8GemmArgs a) {
         : "v"(a0), "v"(a1)
         : "memory");
   };
-  auto read12 = [&](uint32_t a0, uint32_t a1, u32x4* v) {
-    asm volatile(
-        "ds_read_b128 %0, %12\n\tds_read_b128 %1, %13\n\t"
-        "ds_read_b128 %2, %12 offset:2048\n\tds_read_b128 %3, %13 offset:2048\n\t"
-        "ds_read_b128 %4, %12 offset:4096\n\tds_read_b128 %5, %13 offset:4096\n\t"
-        "ds_read_b128 %6, %12 offset:6144\n\tds_read_b128 %7, %13 offset:6144\n\t"
-        "ds_read_b128 %8, %12 offset:8192\n\tds_read_b128 %9, %13 offset:8192\n\t"
-        "ds_read_b128 %10, %12 offset:10240\n\tds_read_b128 %11, %13 offset:10240"
-        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
-          "=&v"(v[6]), "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11])
-        : "v"(a0), "v"(a1)
-        : "memory");
-  };
   auto wait16 = [&](u32x4* v) {
     asm volatile("s_waitcnt lgkmcnt(0)"
                  : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
@@ -649,10 +640,36 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_bigp_kernel(Fp8GemmArgs a) {
                  :
                  : "memory");
   };
-  auto wait12 = [&](u32x4* v) {
+  auto read8 = [&](uint32_t a0, uint32_t a1, u32x4* v) {
+    asm volatile(
+        "ds_read_b128 %0, %8\n\tds_read_b128 %1, %9\n\t"
+        "ds_read_b128 %2, %8 offset:2048\n\tds_read_b128 %3, %9 offset:2048\n\t"
+        "ds_read_b128 %4, %8 offset:4096\n\tds_read_b128 %5, %9 offset:4096\n\t"
+        "ds_read_b128 %6, %8 offset:6144\n\tds_read_b128 %7, %9 offset:6144"
+        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
+          "=&v"(v[6]), "=&v"(v[7])
+        : "v"(a0), "v"(a1)
+        : "memory");
+  };
+  auto read6 = [&](uint32_t a0, uint32_t a1, u32x4* v) {
+    asm volatile(
+        "ds_read_b128 %0, %6\n\tds_read_b128 %1, %7\n\t"
+        "ds_read_b128 %2, %6 offset:2048\n\tds_read_b128 %3, %7 offset:2048\n\t"
+        "ds_read_b128 %4, %6 offset:4096\n\tds_read_b128 %5, %7 offset:4096"
+        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5])
+        : "v"(a0), "v"(a1)
+        : "memory");
+  };
+  auto wait8 = [&](u32x4* v) {
     asm volatile("s_waitcnt lgkmcnt(0)"
                  : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
-                   "+v"(v[6]), "+v"(v[7]), "+v"(v[8]), "+v"(v[9]), "+v"(v[10]), "+v"(v[11])
+                   "+v"(v[6]), "+v"(v[7])
+                 :
+                 : "memory");
+  };
+  auto wait6 = [&](u32x4* v) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5])
                  :
                  : "memory");
   };
@@ -681,8 +698,8 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_bigp_kernel(Fp8GemmArgs a) {
     uint32_t ln = (uint32_t)lane;             // (not hoisted: see issue_scales)
     asm volatile("" : "+v"(ln));
     const uint32_t c4 = 4u * (ln >> 4);
-    const uint32_t an = (uint32_t)(uintptr_t)(lds_f32*)&scl[p][F8B_T + 16 * NI * wn + 16 * i + c4];
-    const uint32_t ab = (uint32_t)(uintptr_t)(lds_f16*)&bsl[p][16 * NI * wn + 16 * i + c4];
+    const uint32_t an = (uint32_t)(uintptr_t)(lds_f32*)&scl[p][F8B_T + 16 * NIW * wn + 16 * i + c4];
+    const uint32_t ab = (uint32_t)(uintptr_t)(lds_f16*)&bsl[p][16 * NIW * wn + 16 * i + c4];
     asm volatile("ds_read_b128 %0, %2\n\tds_read_b64 %1, %3\n\ts_waitcnt lgkmcnt(0)"
                  : "=&v"(sn), "=&v"(bw)
                  : "v"(an), "v"(ab)
@@ -702,23 +719,23 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_bigp_kernel(Fp8GemmArgs a) {
   barrier_only();
   int sidx = 0;
   for (int r = 0; r < my_tiles; ++r) {
-    f32x4 acc[NI][8];   // [n sub-tile][m sub-tile]
+    f32x4 acc[NIW][8];   // [n sub-tile][m sub-tile]
 #pragma unroll
-    for (int i = 0; i < NI; ++i)
+    for (int i = 0; i < NIW; ++i)
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
     for (int ks = 0; ks < nk; ++ks, ++sidx) {
       const int st = sidx & 1;
-      u32x4 wo[2 * NI], xo[16];
+      u32x4 wo[2 * NIW], xo[16];
       {
         uint32_t aw0, aw1, ax0, ax1;
-        addrs(st, 1, 16 * NI * wn, aw0, aw1);
+        addrs(st, 1, 16 * NIW * wn, aw0, aw1);
         addrs(st, 0, 128 * wm, ax0, ax1);
-        if constexpr (NI == 8) read16(aw0, aw1, wo);
-        else read12(aw0, aw1, wo);
+        if constexpr (NIW == 4) read8(aw0, aw1, wo);
+        else read6(aw0, aw1, wo);
         read16(ax0, ax1, xo);
-        if constexpr (NI == 8) wait16(wo);
-        else wait12(wo);
+        if constexpr (NIW == 4) wait8(wo);
+        else wait6(wo);
         wait16(xo);
       }
       wait_vmcnt<0>();
@@ -733,7 +750,7 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_bigp_kernel(Fp8GemmArgs a) {
         }
       }
 #pragma unroll
-      for (int i = 0; i < NI; ++i) {
+      for (int i = 0; i < NIW; ++i) {
         const i32x8 wf = frag(wo[2 * i], wo[2 * i + 1]);
 #pragma unroll
         for (int j = 0; j < 8; ++j)
@@ -747,10 +764,10 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_bigp_kernel(Fp8GemmArgs a) {
       read_row_scales(r & 1, sm);
       uint32_t ln = (uint32_t)lane;           // (not hoisted: see issue_scales)
       asm volatile("" : "+v"(ln));
-      uint16_t* const ob = (uint16_t*)a.out + (int64_t)(m0c + 128 * wm) * a.ldo + n0c + 16 * NI * wn +
+      uint16_t* const ob = (uint16_t*)a.out + (int64_t)(m0c + 128 * wm) * a.ldo + n0c + 16 * NIW * wn +
                            ((ln & 15u) * (uint32_t)a.ldo + 4u * (ln >> 4));
-      if (a.out_mode) fp8_bigp_epilogue<true, NI>(acc, ob, a.ldo, sm, [&](int i, f32x4& sn, u32x2& bw) { read_col(r & 1, i, sn, bw); }, has_bias);
-      else fp8_bigp_epilogue<false, NI>(acc, ob, a.ldo, sm, [&](int i, f32x4& sn, u32x2& bw) { read_col(r & 1, i, sn, bw); }, has_bias);
+      if (a.out_mode) fp8_bigp_epilogue<true, NIW>(acc, ob, a.ldo, sm, [&](int i, f32x4& sn, u32x2& bw) { read_col(r & 1, i, sn, bw); }, has_bias);
+      else fp8_bigp_epilogue<false, NIW>(acc, ob, a.ldo, sm, [&](int i, f32x4& sn, u32x2& bw) { read_col(r & 1, i, sn, bw); }, has_bias);
     }
     m0c = m0n;
     n0c = n0n;
@@ -1004,9 +1021,9 @@ extern "C" int omni_fp8_gemm(const void* xq, const float* sa, const void* wq, co
     const int bt = (M / F8B_T) * (N / bc);
     const int grid = bt < num_cus() ? bt : num_cus();
     if (bc == 256)
-      hipLaunchKernelGGL((fp8_gemm_bigp_kernel<8>), dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, a);
+      hipLaunchKernelGGL((fp8_gemm_bigp_kernel<8>), dim3((unsigned)grid), dim3(512), 0, (hipStream_t)stream, a);
     else
-      hipLaunchKernelGGL((fp8_gemm_bigp_kernel<6>), dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, a);
+      hipLaunchKernelGGL((fp8_gemm_bigp_kernel<6>), dim3((unsigned)grid), dim3(512), 0, (hipStream_t)stream, a);
   } else if (K / F8_BK >= 4) {                    // 8 waves, 256 x 128 tiles, 3 stages
     const int64_t t8 = (int64_t)ceil_div(M, 256) * (N / F8_BT);
     const int grid = (int)(t8 < num_cus() ? t8 : num_cus());

@@ -334,20 +334,22 @@ int omni_f16_gemm_pipe_splits(int M, int N, int K, int tile_rows);
  * 16-byte aligned) summed in order by a second launch.  OMNI_EPI_PARTIAL: the ksplit fp32
  * slices [ksplit][M][N] only, into workspace (out and bias unused, NULL), for a consumer
  * that sums them in order (omni_add_rmsnorm_partials, omni_mrope_kv_write_partials).
- * With tile_rows and ksplit both 0, fp16 weights and STORE / PARTIAL, N % 192 == 0 shapes
- * whose 128 x 192 tiles take fewer grid rounds x tile outputs run those (same k order per
- * output: results equal the 128 x 128 tiles' bit for bit). */
+ * With tile_rows and ksplit both 0 and fp16 weights, shapes whose 128 x 192 tiles (STORE /
+ * PARTIAL, N % 192 == 0) or persistent 256 x 256 tiles (STORE without a bias / SILU, M and
+ * N % 256 == 0) take fewer grid rounds x tile work run those (omni_packed_gemm_pipe_plan;
+ * same k order per output: results equal the 128 x 128 tiles' bit for bit). */
 int omni_packed_gemm_pipe(const void* x, int ldx, const void* w_packed, const void* scales_packed,
                           int fmt, const void* bias, int bias_after_round, void* out, int ldo,
                           int M, int N, int K, int epilogue, int tile_rows, int ksplit,
                           float* workspace, void* stream);
 
 /* The tiling omni_packed_gemm_pipe runs for a shape (no reference counterpart: it tells a
- * caller or a test which form covers the shape): *rows x *cols tiles (128 / 256 x 128, or
- * 128 x 192) and *ks K slices for the given tile_rows / ksplit (0: chosen); any output may
- * be NULL.  -1 for a shape it rejects. */
-int omni_packed_gemm_pipe_plan(int M, int N, int K, int fmt, int epilogue, int tile_rows,
-                               int ksplit, int* rows, int* cols, int* ks);
+ * caller or a test which form covers the shape): *rows x *cols tiles (128 / 256 x 128,
+ * 128 x 192, or the persistent 256 x 256) and *ks K slices for the given epilogue, bias
+ * (has_bias != 0) and tile_rows / ksplit (0: chosen); any output may be NULL.  -1 for a
+ * shape it rejects. */
+int omni_packed_gemm_pipe_plan(int M, int N, int K, int fmt, int epilogue, int has_bias,
+                               int tile_rows, int ksplit, int* rows, int* cols, int* ks);
 
 /* nn.LayerNorm(N, eps) of M fp16 rows (model/qwen2_vit.py:39-40, 87): fp32 mean and biased
  * variance, y = (x - mean) rsqrt(var + eps) w + b.  N % 8 == 0, N <= 2048; out may alias x. */

@@ -70,7 +70,7 @@ SIGNATURES = {
     "omni_f16_gemm_pipe": [_P, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P],
     "omni_f16_gemm_pipe_splits": [_I, _I, _I, _I],
     "omni_packed_gemm_pipe": [_P, _I, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P],
-    "omni_packed_gemm_pipe_plan": [_I, _I, _I, _I, _I, _I, _I, ctypes.POINTER(_I),
+    "omni_packed_gemm_pipe_plan": [_I, _I, _I, _I, _I, _I, _I, _I, ctypes.POINTER(_I),
                                    ctypes.POINTER(_I), ctypes.POINTER(_I)],
     "omni_layernorm": [_P, _I, _P, _P, _I, _I, _F, _P, _I, _P],
     "omni_vision_rope": [_P, _I, _I, _I, _I, _P, _P, _P],

@@ -529,6 +529,196 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
   gp_wait_vmcnt<0>();                  // drain the clamped tail loads before exit
 }
 
+// Persistent 256 x 256 tiles for the packed fp16 weights (STORE without a bias and SILU
+// epilogues, M and N multiples of 256, one K slice): 8 waves (two per SIMD: 2 along m x 4
+// along n), each owning a 128 (m) x 64 (n) block, so every operand byte staged through LDS
+// feeds twice the MFMA work it feeds in the 256 x 128 tiles above; two 64 KB stages (x rows
+// XOR-swizzled as above, w as the packed 1 KB blocks, one global_load_lds per lane); a grid
+// of at most one workgroup per CU walks its tiles in the XCD-grouped order with the K loop
+// running across tile boundaries (the next tile's first two stages load during the current
+// tile's last two steps).  Per 64-k step a wave issues 24 operand reads and 64 MFMAs.
+// (Biased linears, e.g. qkv, stay on the kernel above: with the bias staging beside the
+// accumulators a four-wave form of this kernel spilled.)  Same k order per output as the
+// kernel above: results equal its bit for bit.  MI355X, us (256 x 128 or 128 x 192 / this,
+// interleaved, median of 7): M = 4096 gate_up + SiLU 240.1 / 222.6; M = 8192 gate_up 469.7 /
+// 397.5, down 238.6 / 200.2 (four waves of 128 x 128: 440.0 and 216.5).
+// The wave's lane index computed afresh (v_mbcnt in an asm block, which the compiler can
+// neither hoist nor merge with an earlier value): for addresses needed once per tile, so
+// that neither they nor the lane index stay live beside 256 accumulators.
+__device__ __forceinline__ uint32_t gp_lane_now() {
+  uint32_t l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
+template <int EPI>
+__global__ __launch_bounds__(512, 1) void gemm_bigp_f16_kernel(GemmPipeArgs a) {
+#pragma clang fp contract(off)
+  static_assert(EPI == GP_STORE || EPI == GP_SILU, "STORE and SILU epilogues");
+  constexpr int NS = 2;
+  constexpr int BT = 256;               // tile rows and columns
+  constexpr int XLD = 4;                // x loads per wave and stage (256 rows / 8 / 8)
+  constexpr int WLD = 4;                // w loads per wave and stage (32 blocks / 8)
+  constexpr int OPS = XLD + WLD;
+  __shared__ __attribute__((aligned(1024))) uint8_t xl[NS][BT * GP_ROWB];
+  __shared__ __attribute__((aligned(1024))) uint8_t wl[NS][BT * GP_ROWB];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wave & 3;              // 4 waves along n (64 columns each), 2 along m
+  const int wm = wave >> 2;
+  const int l16 = lane & 15;
+  const int g4 = lane >> 4;
+
+  const int tiles_n = a.N / BT;
+  const int tiles_m = a.M / BT;
+  const int tiles = tiles_m * tiles_n;
+  const int G = gridDim.x;
+  const int slot = xcd_logical_block(blockIdx.x, G);
+  const int my_tiles = (tiles - slot + G - 1) / G;          // grid <= tiles: >= 1
+  const int nk = a.K / GP_BKH;                              // >= NS (host check)
+  auto tile_at = [&](int r, int& m0, int& n0) {             // past the last tile: the last one
+    int tm, tn;
+    grouped_tile(min(r, my_tiles - 1) * G + slot, tiles_m, tiles_n, GP_GM, tm, tn);
+    m0 = tm * BT;
+    n0 = tn * BT;
+  };
+
+  typedef __attribute__((address_space(3))) void lds_void;
+  typedef __attribute__((address_space(3))) uint8_t lds_u8;
+  // Lane byte offsets from wave-uniform bases, recomputed at every issue from the lane index
+  // (hoisted, the sixteen loads' lane offsets would stay live through the loops): x row
+  // 32 u + lrow of the tile (lrow = 8 wave + lane / 8), its 16-byte chunk (lane % 8) ^ (lrow
+  // % 8) in LDS slot lane % 8; w block b = 4 u + wave of the step (column tile b / 2, 32-k
+  // half b % 2), 1 KB blocks, (K / 32) of them per column tile.
+  const uint32_t xstep = 64u * (uint32_t)a.ldx * 2u;
+  const uint32_t kblk = (uint32_t)(a.K / 32) * 1024u;       // bytes per packed column tile
+  auto issue = [&](int m0, int n0, int ks, int st) {
+    const uint8_t* const xs = (const uint8_t*)(a.x + (int64_t)m0 * a.ldx) + (uint32_t)ks * 128u;
+    const uint8_t* const ws = (const uint8_t*)(a.w + (int64_t)(n0 / 16) * (a.K / 32) * 512) +
+                              (uint32_t)ks * 2048u;
+    const uint32_t ln = gp_lane_now();
+    const uint32_t lrow = 8u * (uint32_t)wave + (ln >> 3);
+    const uint32_t xoff = lrow * (uint32_t)a.ldx * 2u + (((ln & 7u) ^ (lrow & 7u)) << 4);
+    const uint32_t lw = ln * 16u;
+#pragma unroll
+    for (int u = 0; u < XLD; ++u)
+      __builtin_amdgcn_global_load_lds((const void*)(xs + (xoff + u * xstep)),
+                                       (lds_void*)((lds_u8*)&xl[st][(64 * u + 8 * wave) * GP_ROWB]), 16, 0, 0);
+#pragma unroll
+    for (int u = 0; u < WLD; ++u) {
+      const int b = 8 * u + wave;
+      __builtin_amdgcn_global_load_lds(
+          (const void*)(ws + ((uint32_t)(b >> 1) * kblk + (uint32_t)(b & 1) * 1024u + lw)),
+          (lds_void*)((lds_u8*)&wl[st][b * 1024]), 16, 0, 0);
+    }
+  };
+  // Operand reads: x fragment (j, t) = k 32 t + 8 g4 .. +7 of row 128 wm + 16 j + l16, at
+  // chunk (4 t + g4) ^ (l16 & 7) of the row (16 j keeps row & 7 = l16 & 7): two bases (t)
+  // plus 2 KB per j; w fragment (i, t) = the lane's 16 bytes of block 2 (8 wn + i) + t.
+  auto read24 = [&](int st, u32x4 (&v)[24]) {
+    const int r = 128 * wm + l16;
+    const uint32_t row = (uint32_t)(uintptr_t)(lds_u8*)&xl[st][r * GP_ROWB];
+    const uint32_t bx0 = row + ((g4 ^ (l16 & 7)) << 4);
+    const uint32_t bx1 = row + (((4 + g4) ^ (l16 & 7)) << 4);
+    const uint32_t bw = (uint32_t)(uintptr_t)(lds_u8*)&wl[st][8 * wn * 1024] + (uint32_t)lane * 16u;
+    asm volatile(
+        "ds_read_b128 %0, %24\n\tds_read_b128 %1, %24 offset:1024\n\t"
+        "ds_read_b128 %2, %24 offset:2048\n\tds_read_b128 %3, %24 offset:3072\n\t"
+        "ds_read_b128 %4, %24 offset:4096\n\tds_read_b128 %5, %24 offset:5120\n\t"
+        "ds_read_b128 %6, %24 offset:6144\n\tds_read_b128 %7, %24 offset:7168\n\t"
+        "ds_read_b128 %8, %25\n\tds_read_b128 %9, %26\n\t"
+        "ds_read_b128 %10, %25 offset:2048\n\tds_read_b128 %11, %26 offset:2048\n\t"
+        "ds_read_b128 %12, %25 offset:4096\n\tds_read_b128 %13, %26 offset:4096\n\t"
+        "ds_read_b128 %14, %25 offset:6144\n\tds_read_b128 %15, %26 offset:6144\n\t"
+        "ds_read_b128 %16, %25 offset:8192\n\tds_read_b128 %17, %26 offset:8192\n\t"
+        "ds_read_b128 %18, %25 offset:10240\n\tds_read_b128 %19, %26 offset:10240\n\t"
+        "ds_read_b128 %20, %25 offset:12288\n\tds_read_b128 %21, %26 offset:12288\n\t"
+        "ds_read_b128 %22, %25 offset:14336\n\tds_read_b128 %23, %26 offset:14336\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
+          "=&v"(v[6]), "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11]),
+          "=&v"(v[12]), "=&v"(v[13]), "=&v"(v[14]), "=&v"(v[15]), "=&v"(v[16]), "=&v"(v[17]),
+          "=&v"(v[18]), "=&v"(v[19]), "=&v"(v[20]), "=&v"(v[21]), "=&v"(v[22]), "=&v"(v[23])
+        : "v"(bw), "v"(bx0), "v"(bx1)
+        : "memory");
+  };
+  int m0c, n0c, m0n, n0n;
+  tile_at(0, m0c, n0c);
+  tile_at(1, m0n, n0n);
+  issue(m0c, n0c, 0, 0);
+  issue(m0c, n0c, 1, 1);
+  gp_wait_vmcnt<OPS>();                 // stage 0
+  gp_barrier();
+  int sidx = 0;
+  for (int r = 0; r < my_tiles; ++r) {
+    f32x4 acc[4][8];   // [n sub-tile][m sub-tile]
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int ks = 0; ks < nk; ++ks, ++sidx) {
+      const int st = sidx & 1;
+      u32x4 v[24];
+      read24(st, v);
+      // step sidx + 1 has landed (nothing younger is in flight with two stages) for this
+      // thread, then for everyone; every wave has read this slot, refilled with sidx + 2
+      gp_wait_vmcnt<0>();
+      gp_barrier();
+      {
+        const int iks = ks + NS;
+        if (iks < nk) issue(m0c, n0c, iks, st);
+        else issue(m0n, n0n, iks - nk, st);
+      }
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const half8_t wf = __builtin_bit_cast(half8_t, v[2 * i + t]);
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            acc[i][j] = mfma16x16x32(wf, __builtin_bit_cast(half8_t, v[8 + 2 * j + t]), acc[i][j]);
+        }
+    }
+    // Epilogue: lane holds n = n0 + 128 wn + 16 i + 4 g4 + q of m = m0 + 128 wm + 16 j + l16.
+    {
+      const uint32_t ln = gp_lane_now();
+      const int64_t mrow = (int64_t)(m0c + 128 * wm) * a.ldo;
+      const uint32_t lo = (ln & 15u) * (uint32_t)a.ldo + 4u * (ln >> 4);
+      if constexpr (EPI == GP_SILU) {
+        // column tiles (i, i + 1), i even, are (gate, up) of intermediate columns
+        // (n0 + 128 wn + 16 i) / 2 + 4 g4 + q
+        half_t* const ob = a.out + mrow + (n0c + 64 * wn) / 2 + lo;
+#pragma unroll
+        for (int i = 0; i < 4; i += 2)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            half4_t o;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              o[q] = (half_t)silu_mul_f32((float)(half_t)acc[i][j][q], (float)(half_t)acc[i + 1][j][q]);
+            *(half4_t*)(ob + (16 * j * a.ldo + 8 * i)) = o;
+          }
+      } else {
+        half_t* const ob = a.out + mrow + n0c + 64 * wn + lo;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            half4_t o;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) o[q] = (half_t)acc[i][j][q];
+            *(half4_t*)(ob + (16 * j * a.ldo + 16 * i)) = o;
+          }
+      }
+    }
+    m0c = m0n;
+    n0c = n0n;
+    tile_at(r + 2, m0n, n0n);
+  }
+  gp_wait_vmcnt<0>();                   // drain the clamped tail loads before exit
+}
+
 static int gp_num_cus() {
   static int n = 0;
   if (n <= 0) {
@@ -620,16 +810,24 @@ static int gp_launch(const GemmPipeArgs& a, int epilogue, hipStream_t st) {
   return OMNI_OK;
 }
 
+// Relative costs of the packed fp16 weights' tile forms per 128 x 128 outputs (fitted on
+// MI355X with grid rounds x tile size): the 8-wave 256 x 128 / 4-wave 128 x 128 tiles 1, the
+// 4-wave 128 x 192 tiles 1.3 (config 5's down at M = 4096: 125.1 us for 256 of them against
+// 128.6 us for 192 of 256 x 128), the persistent 8-wave 256 x 256 tiles 0.85.
+#define GP_WIDE_COST 1.3
+#define GP_BIG_COST 0.85
+
 // Whether the packed fp16 weights take 128 x 192 tiles (4 waves, 64 x 96 each, 3 stages)
-// instead of the tiles of tile_rows x 128: when the grid's rounds times a tile's outputs
-// come out smaller (config 5's N = 1536 projections at M = 4096: 256 tiles in one round
-// against 192 of 256 x 128, which leave a quarter of the CUs idle).
+// instead of the tiles of tile_rows x 128: when the grid's rounds times a tile's cost come
+// out smaller (config 5's N = 1536 projections at M = 4096: 256 tiles in one round against
+// 192 of 256 x 128, which leave a quarter of the CUs idle).
 static bool gp_wide_tiles(int M, int N, int tile_rows) {
   if (N % 192) return false;
   const int64_t cus = gp_num_cus();
   const int64_t tn = (int64_t)ceil_div(M, tile_rows) * (N / GP_BN);
   const int64_t tw = (int64_t)ceil_div(M, 128) * (N / 192);
-  return ((tw + cus - 1) / cus) * 128 * 192 < ((tn + cus - 1) / cus) * tile_rows * GP_BN;
+  return (double)((tw + cus - 1) / cus) * 1.5 * GP_WIDE_COST <
+         (double)((tn + cus - 1) / cus) * (tile_rows / 128);
 }
 
 static int gp_tile_rows(int M, int N) {
@@ -719,28 +917,42 @@ extern "C" int omni_f16_gemm_pipe(const void* x, int ldx, const void* w, const v
 }
 
 // omni_packed_gemm_pipe's tiling for a shape: tile rows and columns and K slices, from the
-// caller's tile_rows / ksplit (0: chosen).  128 x 192 tiles only where both were chosen.
-static void gp_packed_plan(int M, int N, int K, int fmt, int epilogue, int tile_rows, int ksplit,
-                           int& rows, int& cols, int& ks) {
+// caller's tile_rows / ksplit (0: chosen).  128 x 192 and persistent 256 x 256 tiles only
+// where both were chosen; the 256 x 256 ones (fp16 weights, STORE without a bias / SILU, M
+// and N multiples of 256) where rounds of the grid times the tile's cost (per 128 x 128
+// outputs: GP_BIG_COST, against 1 or GP_WIDE_COST) come out below the other plan's.
+static void gp_packed_plan(int M, int N, int K, int fmt, int epilogue, bool has_bias, int tile_rows,
+                           int ksplit, int& rows, int& cols, int& ks) {
   rows = tile_rows ? tile_rows : gp_tile_rows(M, N);
   ks = ksplit ? ksplit : (epilogue == GP_SILU ? 1 : omni_f16_gemm_pipe_splits(M, N, K, rows));
   cols = GP_BN;
-  if (fmt == 1 && tile_rows == 0 && ks == 1 && (epilogue == GP_STORE || epilogue == GP_PARTIAL) &&
-      gp_wide_tiles(M, N, rows)) {
+  if (fmt != 1 || tile_rows != 0 || ks != 1) return;
+  if ((epilogue == GP_STORE || epilogue == GP_PARTIAL) && gp_wide_tiles(M, N, rows)) {
     rows = 128;
     cols = 192;
+  }
+  if (((epilogue == GP_STORE && !has_bias) || epilogue == GP_SILU) && M % 256 == 0 && N % 256 == 0) {
+    const int64_t cus = gp_num_cus();
+    auto rounds = [&](int64_t t) { return (double)((t + cus - 1) / cus); };
+    const double cur = rounds((int64_t)ceil_div(M, rows) * (N / cols)) * (rows * cols) / 16384.0 *
+                       (cols == 192 ? GP_WIDE_COST : 1.0);
+    const double big = rounds((int64_t)(M / 256) * (N / 256)) * 4.0 * GP_BIG_COST;
+    if (big < cur) {
+      rows = 256;
+      cols = 256;
+    }
   }
 }
 
 // The tiling omni_packed_gemm_pipe runs for a shape (no reference counterpart: it tells a
 // caller or a test which tile form covers the shape).
 extern "C" int omni_packed_gemm_pipe_plan(int M, int N, int K, int fmt, int epilogue,
-                                          int tile_rows, int ksplit, int* rows, int* cols,
-                                          int* ks) {
+                                          int has_bias, int tile_rows, int ksplit, int* rows,
+                                          int* cols, int* ks) {
   if (M <= 0 || N <= 0 || K <= 0 || (N % GP_BN) || (K % 128) || (fmt != 0 && fmt != 1)) return OMNI_EINVAL;
   if (tile_rows != 0 && tile_rows != 128 && tile_rows != 256) return OMNI_EINVAL;
   int r, c, k;
-  gp_packed_plan(M, N, K, fmt, epilogue, tile_rows, ksplit, r, c, k);
+  gp_packed_plan(M, N, K, fmt, epilogue, has_bias != 0, tile_rows, ksplit, r, c, k);
   if (rows) *rows = r;
   if (cols) *cols = c;
   if (ks) *ks = k;
@@ -771,7 +983,7 @@ extern "C" int omni_packed_gemm_pipe(const void* x, int ldx, const void* w_packe
   if (tile_rows != 0 && tile_rows != 128 && tile_rows != 256) return OMNI_EINVAL;
   if (fmt == 0 && ((uintptr_t)scales_packed & 3)) return OMNI_EINVAL;
   int cols;
-  gp_packed_plan(M, N, K, fmt, epilogue, tile_rows, ksplit, tile_rows, cols, ksplit);
+  gp_packed_plan(M, N, K, fmt, epilogue, bias != nullptr, tile_rows, ksplit, tile_rows, cols, ksplit);
   if (epilogue == GP_SILU && ksplit != 1) return OMNI_EINVAL;
   // every slice covers at least NS pipeline steps (slices are whole 128-groups of 2 steps)
   const int ns = fmt == 0 ? (tile_rows == 256 ? 4 : 6) : (tile_rows == 256 ? 3 : 4);
@@ -800,6 +1012,16 @@ extern "C" int omni_packed_gemm_pipe(const void* x, int ldx, const void* w_packe
     return tile_rows == 256 ? gp_launch<GW_INT4, 4, 4>(a, epilogue, st)
                             : gp_launch<GW_INT4, 2, 6>(a, epilogue, st);
   if (cols == 192) return gp_launch<GW_F16, 2, 3, 6>(a, epilogue, st);
+  if (cols == 256) {                     // persistent 256 x 256 tiles
+    const int64_t t = (int64_t)(M / 256) * (N / 256);
+    const int grid = (int)(t < gp_num_cus() ? t : gp_num_cus());
+    if (epilogue == GP_SILU)
+      hipLaunchKernelGGL((gemm_bigp_f16_kernel<GP_SILU>), dim3(grid), dim3(512), 0, st, a);
+    else
+      hipLaunchKernelGGL((gemm_bigp_f16_kernel<GP_STORE>), dim3(grid), dim3(512), 0, st, a);
+    OMNI_CHECK_LAUNCH();
+    return OMNI_OK;
+  }
   return tile_rows == 256 ? gp_launch<GW_F16, 4, 3>(a, epilogue, st)
                           : gp_launch<GW_F16, 2, 4>(a, epilogue, st);
 }

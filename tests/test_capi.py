@@ -147,8 +147,8 @@ def test_bad_arguments_rejected_before_launch(so):
                                                None, 0, None, 12 * 128, 12, 2, 128, 0.1,
                                                None) == 0
     # packed prefill GEMM plan: N not a multiple of 128, an unknown weight format
-    assert L.omni_packed_gemm_pipe_plan(4096, 1500, 1536, 1, 0, 0, 0, None, None, None) == -1
-    assert L.omni_packed_gemm_pipe_plan(4096, 1536, 1536, 2, 0, 0, 0, None, None, None) == -1
+    assert L.omni_packed_gemm_pipe_plan(4096, 1500, 1536, 1, 0, 0, 0, 0, None, None, None) == -1
+    assert L.omni_packed_gemm_pipe_plan(4096, 1536, 1536, 2, 0, 0, 0, 0, None, None, None) == -1
     # zero-size work is a no-op success
     assert L.omni_silu_mul(None, None, 0, 8960, None) == 0
     assert L.omni_gemm_slices(8960, 10) == 10 and L.omni_gemm_slices(1536, 7) == 6

@@ -414,11 +414,11 @@ def test_tiled_gemm(gpu, fmt, M, K, N, bias, silu):
             assert (sp.cpu().float() - e).abs().max().item() <= 2e-3 * max(1.0, e.abs().max().item())
 
 
-def _packed_plan(M, N, K, fmt, epi):
+def _packed_plan(M, N, K, fmt, epi, has_bias=0):
     import ctypes
     from omniserver_amd._lib import lib
     r, c, k = ctypes.c_int(0), ctypes.c_int(0), ctypes.c_int(0)
-    assert lib().omni_packed_gemm_pipe_plan(M, N, K, fmt, epi, 0, 0, ctypes.byref(r),
+    assert lib().omni_packed_gemm_pipe_plan(M, N, K, fmt, epi, has_bias, 0, 0, ctypes.byref(r),
                                             ctypes.byref(c), ctypes.byref(k)) == 0
     return r.value, c.value, k.value
 
@@ -432,7 +432,7 @@ def test_packed_gemm_pipe_wide_tiles(gpu, M, K, bias):
     from omniserver_amd._lib import call, ptr, stream
     from omniserver_amd.linear import F16Linear
     N = 1536
-    rows, cols, ks = _packed_plan(M, N, K, 1, 0)
+    rows, cols, ks = _packed_plan(M, N, K, 1, 0, int(bias))
     say(f"packed gemm pipe wide tiles M={M} K={K} N={N} bias={bias}: {rows} x {cols}, {ks} slice")
     assert (rows, cols, ks) == (128, 192, 1)
     assert _packed_plan(M, N, K, 1, 2)[1] == 192
@@ -458,6 +458,43 @@ def test_packed_gemm_pipe_wide_tiles(gpu, M, K, bias):
     e = ref.linear(x[rows_s].float(), wt.float().t(), None if b is None else b.float())
     tol = 2e-3 * max(1.0, e.abs().max().item())
     assert (wide[rows_s].float() - e).abs().max().item() <= tol
+
+
+@pytest.mark.parametrize("M,K,N,silu", [(4096, 1536, 17920, True), (8192, 1536, 2048, False)])
+def test_packed_gemm_pipe_big_tiles(gpu, M, K, N, silu):
+    """The persistent 256 x 256 tiles omni_packed_gemm_pipe picks for config 5's gate_up (SiLU)
+    at M = 4096 and for an unbiased STORE at M = 8192: equal to the 256 x 128 tiles' results
+    bit for bit (same k order per output), and 64 sampled rows (every row tile) within
+    tolerance of the oracle."""
+    from omniserver_amd._lib import call, ptr, stream
+    from omniserver_amd.linear import F16Linear
+    rows, cols, ks = _packed_plan(M, N, K, 1, 1 if silu else 0)
+    say(f"packed gemm pipe big tiles M={M} K={K} N={N} silu={silu}: {rows} x {cols}, {ks} slice")
+    assert (rows, cols, ks) == (256, 256, 1)
+    assert _packed_plan(M, N, K, 1, 0, 1)[1] != 256          # a bias keeps the pipelined tiles
+    wt = f16((N, K), 102, 0.02)
+    x = f16((M, K), 103)
+    lin = F16Linear(wt.to(gpu), fuse_silu=silu)
+    xg = x.to(gpu)
+    nout = N // 2 if silu else N
+
+    def run(tile_rows):
+        out = torch.full((M, nout), float("nan"), device=gpu, dtype=torch.float16)
+        call("omni_packed_gemm_pipe", ptr(xg), K, ptr(lin.weight_packed), None, 1, None, 0,
+             ptr(out), nout, M, N, K, 1 if silu else 0, tile_rows, 1, None, stream())
+        torch.cuda.synchronize()
+        return out.cpu()
+
+    big, o256 = run(0), run(256)
+    assert torch.equal(big, o256)
+    rows_s = torch.tensor(sorted({64 * i + (37 * i) % 64 for i in range(M // 64)} | {M - 1}))
+    rows_s = rows_s[:: max(1, len(rows_s) // 64)]
+    W = wt.float().t()
+    e = ref.linear(x[rows_s].float(), W)
+    if silu:
+        e = ref.silu_mul(e)
+    tol = 2e-3 * max(1.0, e.abs().max().item())
+    assert (big[rows_s].float() - e).abs().max().item() <= tol
 
 
 @pytest.mark.parametrize("fmt", ["int4", "fp16"])

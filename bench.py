@@ -358,10 +358,15 @@ def _decode_line(quant, per_ms, replay_ms, ctx0, steps):
 def _prefill_ms(r, make_seqs, reps: int):
     """Median wall time (ms) of ``reps`` prefills of make_seqs() on runner r, each into a
     freshly freed pool after one warm-up prefill (first use of the prefill kernels);
-    returns (median ms, the last prefill's sequences)."""
+    returns (median ms, the last prefill's sequences).  The wall time includes the
+    prefill's host-side input preparation, so the timing starts once the host's thread
+    pools, still spinning after the set-up's CPU work (synthetic weights, packing), have
+    gone idle: without the pause the same prefills measured 3.16 / 16.75 ms (configs 1 / 5)
+    right after a runner's set-up against 2.91 / 15.95 ms later in the same process."""
     seqs = make_seqs()
     r.prefill(seqs)
     torch.cuda.synchronize()
+    time.sleep(0.5)
     ts = []
     for _ in range(reps):
         for s_ in seqs:

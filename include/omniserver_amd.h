@@ -411,7 +411,8 @@ int omni_fp8_quant_tensor_work(int rows);
  *   2  fp16(v), + fp16 bias in fp16 (per-tensor forward: out_dtype fp16, :119-125; sa and
  *      sw hold one value each, repeated).  This form runs the 256 x 128 kernel where
  *      omni_fp8_gemm_plan names a 256-row big-tile one (their epilogue has no room for it).
- * xq [M, K], wq [N, K] e4m3fn; out [M, ldo]; N % 128 == 0, K % 128 == 0. */
+ * xq [M, K], wq [N, K] e4m3fn; out [M, ldo]; N % 128 == 0, K % 128 == 0; xq, wq and bias
+ * 16-byte aligned, sa / sw 4-byte, out 8-byte (else -1). */
 int omni_fp8_gemm(const void* xq, const float* sa, const void* wq, const float* sw,
                   const void* bias, void* out, int ldo, int M, int N, int K, int out_mode,
                   void* stream);

@@ -1002,6 +1002,11 @@ extern "C" int omni_fp8_gemm(const void* xq, const float* sa, const void* wq, co
   if (out_mode < FP8_OUT_F16_VIA_BF16 || out_mode > FP8_OUT_F16) return OMNI_EINVAL;
   if (M == 0) return OMNI_OK;
   if (!xq || !sa || !wq || !sw || !out) return OMNI_EINVAL;
+  // the kernels stage operand rows and biases with 16-byte global->LDS loads, scales with
+  // 4-byte ones, and store 8 bytes at a time
+  if (((uintptr_t)xq & 15) || ((uintptr_t)wq & 15) || ((uintptr_t)bias & 15) ||
+      ((uintptr_t)sa & 3) || ((uintptr_t)sw & 3) || ((uintptr_t)out & 7))
+    return OMNI_EINVAL;
   const int64_t tiles = (int64_t)ceil_div(M, F8_BT) * (N / F8_BT);
   if (tiles > 0x7fffffff) return OMNI_EUNSUPPORTED;
   Fp8GemmArgs a;

@@ -131,6 +131,11 @@ def test_bad_arguments_rejected_before_launch(so):
     # with K not whole 8-element chunks; the workspace is one float per workgroup (<= 256)
     assert L.omni_fp8_gemm(fake_ptr(), fake_ptr(), fake_ptr(), fake_ptr(), None, fake_ptr(),
                            256, 8, 256, 256, 3, None) == -1
+    # operands and bias staged with 16-byte loads: a misaligned pointer is rejected
+    assert L.omni_fp8_gemm(ctypes.c_void_p(16 + 8), fake_ptr(), fake_ptr(), fake_ptr(), None,
+                           fake_ptr(), 256, 8, 256, 256, 0, None) == -1
+    assert L.omni_fp8_gemm(fake_ptr(), fake_ptr(), fake_ptr(), fake_ptr(), ctypes.c_void_p(16 + 2),
+                           fake_ptr(), 256, 8, 256, 256, 0, None) == -1
     assert L.omni_fp8_quant_tensor(fake_ptr(), 256, fake_ptr(), fake_ptr(), None, 8, 256, 0,
                                    None) == -1
     assert L.omni_fp8_quant_tensor(fake_ptr(), 260, fake_ptr(), fake_ptr(), fake_ptr(), 8, 250,

@@ -529,19 +529,24 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
   gp_wait_vmcnt<0>();                  // drain the clamped tail loads before exit
 }
 
-// Persistent 256 x 256 tiles for the packed fp16 weights (STORE without a bias and SILU
-// epilogues, M and N multiples of 256, one K slice): 8 waves (two per SIMD: 2 along m x 4
-// along n), each owning a 128 (m) x 64 (n) block, so every operand byte staged through LDS
-// feeds twice the MFMA work it feeds in the 256 x 128 tiles above; two 64 KB stages (x rows
-// XOR-swizzled as above, w as the packed 1 KB blocks, one global_load_lds per lane); a grid
-// of at most one workgroup per CU walks its tiles in the XCD-grouped order with the K loop
-// running across tile boundaries (the next tile's first two stages load during the current
-// tile's last two steps).  Per 64-k step a wave issues 24 operand reads and 64 MFMAs.
-// (Biased linears, e.g. qkv, stay on the kernel above: with the bias staging beside the
+// Persistent 256 x 256 or 256 x 192 tiles for the packed fp16 weights (STORE without a
+// bias, SILU (256 columns) and PARTIAL epilogues, M a multiple of 256, N of the tile width):
+// 8 waves (two per SIMD: 2 along m x 4 along n), each owning a 128 (m) x 16 NIW (n) block,
+// so every operand byte staged through LDS feeds twice the MFMA work it feeds in the
+// 256 x 128 tiles above; two stages of 32 KB of x and 8 NIW KB of w (x rows XOR-swizzled as
+// above, w as the packed 1 KB blocks, one global_load_lds per lane); a grid of at most one
+// workgroup per CU walks its items (tile x K slice, slice-major, tiles in the XCD-grouped
+// order) with the K loop running across item boundaries (the next item's first two stages
+// load during the current one's last two steps).  Per 64-k step a wave issues 16 + 2 NIW
+// operand reads and 16 NIW MFMAs.  PARTIAL writes each K slice's fp32 sums to
+// part[slice][M][N] for the consumer to add in slice order (config 5's N = 1536 projections
+// at M = 4096: 128 tiles of 256 x 192 in two slices fill the 256 CUs once).  (Biased
+// linears, e.g. qkv, stay on the kernel above: with the bias staging beside the
 // accumulators a four-wave form of this kernel spilled.)  Same k order per output as the
-// kernel above: results equal its bit for bit.  MI355X, us (256 x 128 or 128 x 192 / this,
-// interleaved, median of 7): M = 4096 gate_up + SiLU 240.1 / 222.6; M = 8192 gate_up 469.7 /
-// 397.5, down 238.6 / 200.2 (four waves of 128 x 128: 440.0 and 216.5).
+// kernel above within a slice: one-slice results equal its bit for bit.  MI355X, us
+// (256 x 128 or 128 x 192 / this, interleaved, median of 7): M = 4096 gate_up + SiLU
+// 240.1 / 222.6; M = 8192 gate_up 469.7 / 397.5, down 238.6 / 200.2 (four waves of 128 x 128:
+// 440.0 and 216.5).
 // The wave's lane index computed afresh (v_mbcnt in an asm block, which the compiler can
 // neither hoist nor merge with an earlier value): for addresses needed once per tile, so
 // that neither they nor the lane index stay live beside 256 accumulators.
@@ -551,46 +556,60 @@ __device__ __forceinline__ uint32_t gp_lane_now() {
   return l;
 }
 
-template <int EPI>
+template <int EPI, int NIW>
 __global__ __launch_bounds__(512, 1) void gemm_bigp_f16_kernel(GemmPipeArgs a) {
 #pragma clang fp contract(off)
-  static_assert(EPI == GP_STORE || EPI == GP_SILU, "STORE and SILU epilogues");
+  static_assert(((EPI == GP_STORE || EPI == GP_PARTIAL) && (NIW == 3 || NIW == 4)) ||
+                    (EPI == GP_SILU && NIW == 4),
+                "STORE / PARTIAL at 192 or 256 columns, SILU at 256");
   constexpr int NS = 2;
-  constexpr int BT = 256;               // tile rows and columns
+  constexpr int BM = 256;               // tile rows
+  constexpr int BN = 64 * NIW;          // tile columns
   constexpr int XLD = 4;                // x loads per wave and stage (256 rows / 8 / 8)
-  constexpr int WLD = 4;                // w loads per wave and stage (32 blocks / 8)
-  constexpr int OPS = XLD + WLD;
-  __shared__ __attribute__((aligned(1024))) uint8_t xl[NS][BT * GP_ROWB];
-  __shared__ __attribute__((aligned(1024))) uint8_t wl[NS][BT * GP_ROWB];
+  constexpr int WLD = NIW;              // w loads per wave and stage (8 NIW blocks / 8)
+  constexpr int NV = 2 * NIW + 16;      // operand fragments per step: w 2 NIW, then x 16
+  __shared__ __attribute__((aligned(1024))) uint8_t xl[NS][BM * GP_ROWB];
+  __shared__ __attribute__((aligned(1024))) uint8_t wl[NS][BN * GP_ROWB];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wn = wave & 3;              // 4 waves along n (64 columns each), 2 along m
+  const int wn = wave & 3;              // 4 waves along n (16 NIW columns each), 2 along m
   const int wm = wave >> 2;
   const int l16 = lane & 15;
   const int g4 = lane >> 4;
 
-  const int tiles_n = a.N / BT;
-  const int tiles_m = a.M / BT;
+  const int tiles_n = a.N / BN;
+  const int tiles_m = a.M / BM;
   const int tiles = tiles_m * tiles_n;
+  const int items = tiles * a.KS;                           // slice-major: item = s tiles + tile
   const int G = gridDim.x;
   const int slot = xcd_logical_block(blockIdx.x, G);
-  const int my_tiles = (tiles - slot + G - 1) / G;          // grid <= tiles: >= 1
-  const int nk = a.K / GP_BKH;                              // >= NS (host check)
-  auto tile_at = [&](int r, int& m0, int& n0) {             // past the last tile: the last one
+  const int my_items = (items - slot + G - 1) / G;          // grid <= items: >= 1
+  const int nk = a.K / GP_BKH;                              // every slice >= NS steps (host check)
+  struct Item {
+    int m0, n0, sl, kb, kc;            // tile origin, K slice, its first step and step count
+  };
+  auto item_at = [&](int r) {                               // past the last item: the last one
+    Item t;
+    const int it = min(r, my_items - 1) * G + slot;
+    t.sl = it / tiles;
     int tm, tn;
-    grouped_tile(min(r, my_tiles - 1) * G + slot, tiles_m, tiles_n, GP_GM, tm, tn);
-    m0 = tm * BT;
-    n0 = tn * BT;
+    grouped_tile(it - t.sl * tiles, tiles_m, tiles_n, GP_GM, tm, tn);
+    t.m0 = tm * BM;
+    t.n0 = tn * BN;
+    // slices are whole 128-k groups (pairs of steps), as in the kernel above
+    t.kb = 2 * (t.sl * (nk / 2) / a.KS);
+    t.kc = 2 * ((t.sl + 1) * (nk / 2) / a.KS) - t.kb;
+    return t;
   };
 
   typedef __attribute__((address_space(3))) void lds_void;
   typedef __attribute__((address_space(3))) uint8_t lds_u8;
   // Lane byte offsets from wave-uniform bases, recomputed at every issue from the lane index
-  // (hoisted, the sixteen loads' lane offsets would stay live through the loops): x row
-  // 32 u + lrow of the tile (lrow = 8 wave + lane / 8), its 16-byte chunk (lane % 8) ^ (lrow
-  // % 8) in LDS slot lane % 8; w block b = 4 u + wave of the step (column tile b / 2, 32-k
-  // half b % 2), 1 KB blocks, (K / 32) of them per column tile.
+  // (hoisted, the loads' lane offsets would stay live through the loops): x row 64 u + lrow
+  // of the tile (lrow = 8 wave + lane / 8), its 16-byte chunk (lane % 8) ^ (lrow % 8) in LDS
+  // slot lane % 8; w block b = 8 u + wave of the step (column tile b / 2, 32-k half b % 2),
+  // 1 KB blocks, (K / 32) of them per column tile.  ks: the absolute K step.
   const uint32_t xstep = 64u * (uint32_t)a.ldx * 2u;
   const uint32_t kblk = (uint32_t)(a.K / 32) * 1024u;       // bytes per packed column tile
   auto issue = [&](int m0, int n0, int ks, int st) {
@@ -615,14 +634,14 @@ __global__ __launch_bounds__(512, 1) void gemm_bigp_f16_kernel(GemmPipeArgs a) {
   };
   // Operand reads: x fragment (j, t) = k 32 t + 8 g4 .. +7 of row 128 wm + 16 j + l16, at
   // chunk (4 t + g4) ^ (l16 & 7) of the row (16 j keeps row & 7 = l16 & 7): two bases (t)
-  // plus 2 KB per j; w fragment (i, t) = the lane's 16 bytes of block 2 (8 wn + i) + t.
-  auto read24 = [&](int st, u32x4 (&v)[24]) {
+  // plus 2 KB per j; w fragment (i, t) = the lane's 16 bytes of block 2 (NIW wn + i) + t.
+  auto read_ops = [&](int st, u32x4 (&v)[NV]) {
     const int r = 128 * wm + l16;
     const uint32_t row = (uint32_t)(uintptr_t)(lds_u8*)&xl[st][r * GP_ROWB];
     const uint32_t bx0 = row + ((g4 ^ (l16 & 7)) << 4);
     const uint32_t bx1 = row + (((4 + g4) ^ (l16 & 7)) << 4);
-    const uint32_t bw = (uint32_t)(uintptr_t)(lds_u8*)&wl[st][8 * wn * 1024] + (uint32_t)lane * 16u;
-    asm volatile(
+    const uint32_t bw = (uint32_t)(uintptr_t)(lds_u8*)&wl[st][2 * NIW * wn * 1024] + (uint32_t)lane * 16u;
+    if constexpr (NIW == 4) asm volatile(
         "ds_read_b128 %0, %24\n\tds_read_b128 %1, %24 offset:1024\n\t"
         "ds_read_b128 %2, %24 offset:2048\n\tds_read_b128 %3, %24 offset:3072\n\t"
         "ds_read_b128 %4, %24 offset:4096\n\tds_read_b128 %5, %24 offset:5120\n\t"
@@ -642,53 +661,78 @@ __global__ __launch_bounds__(512, 1) void gemm_bigp_f16_kernel(GemmPipeArgs a) {
           "=&v"(v[18]), "=&v"(v[19]), "=&v"(v[20]), "=&v"(v[21]), "=&v"(v[22]), "=&v"(v[23])
         : "v"(bw), "v"(bx0), "v"(bx1)
         : "memory");
+    else asm volatile(
+        "ds_read_b128 %0, %22\n\tds_read_b128 %1, %22 offset:1024\n\t"
+        "ds_read_b128 %2, %22 offset:2048\n\tds_read_b128 %3, %22 offset:3072\n\t"
+        "ds_read_b128 %4, %22 offset:4096\n\tds_read_b128 %5, %22 offset:5120\n\t"
+        "ds_read_b128 %6, %23\n\tds_read_b128 %7, %24\n\t"
+        "ds_read_b128 %8, %23 offset:2048\n\tds_read_b128 %9, %24 offset:2048\n\t"
+        "ds_read_b128 %10, %23 offset:4096\n\tds_read_b128 %11, %24 offset:4096\n\t"
+        "ds_read_b128 %12, %23 offset:6144\n\tds_read_b128 %13, %24 offset:6144\n\t"
+        "ds_read_b128 %14, %23 offset:8192\n\tds_read_b128 %15, %24 offset:8192\n\t"
+        "ds_read_b128 %16, %23 offset:10240\n\tds_read_b128 %17, %24 offset:10240\n\t"
+        "ds_read_b128 %18, %23 offset:12288\n\tds_read_b128 %19, %24 offset:12288\n\t"
+        "ds_read_b128 %20, %23 offset:14336\n\tds_read_b128 %21, %24 offset:14336\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
+          "=&v"(v[6]), "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11]),
+          "=&v"(v[12]), "=&v"(v[13]), "=&v"(v[14]), "=&v"(v[15]), "=&v"(v[16]), "=&v"(v[17]),
+          "=&v"(v[18]), "=&v"(v[19]), "=&v"(v[20]), "=&v"(v[21])
+        : "v"(bw), "v"(bx0), "v"(bx1)
+        : "memory");
   };
-  int m0c, n0c, m0n, n0n;
-  tile_at(0, m0c, n0c);
-  tile_at(1, m0n, n0n);
-  issue(m0c, n0c, 0, 0);
-  issue(m0c, n0c, 1, 1);
-  gp_wait_vmcnt<OPS>();                 // stage 0
+  Item cur = item_at(0), nxt = item_at(1);
+  issue(cur.m0, cur.n0, cur.kb, 0);
+  issue(cur.m0, cur.n0, cur.kb + 1, 1);
+  gp_wait_vmcnt<XLD + WLD>();           // stage 0
   gp_barrier();
   int sidx = 0;
-  for (int r = 0; r < my_tiles; ++r) {
-    f32x4 acc[4][8];   // [n sub-tile][m sub-tile]
+  for (int r = 0; r < my_items; ++r) {
+    f32x4 acc[NIW][8];   // [n sub-tile][m sub-tile]
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NIW; ++i)
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    for (int ks = 0; ks < nk; ++ks, ++sidx) {
+    for (int ks = 0; ks < cur.kc; ++ks, ++sidx) {
       const int st = sidx & 1;
-      u32x4 v[24];
-      read24(st, v);
+      u32x4 v[NV];
+      read_ops(st, v);
       // step sidx + 1 has landed (nothing younger is in flight with two stages) for this
       // thread, then for everyone; every wave has read this slot, refilled with sidx + 2
       gp_wait_vmcnt<0>();
       gp_barrier();
       {
         const int iks = ks + NS;
-        if (iks < nk) issue(m0c, n0c, iks, st);
-        else issue(m0n, n0n, iks - nk, st);
+        if (iks < cur.kc) issue(cur.m0, cur.n0, cur.kb + iks, st);
+        else issue(nxt.m0, nxt.n0, nxt.kb + iks - cur.kc, st);
       }
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < NIW; ++i) {
           const half8_t wf = __builtin_bit_cast(half8_t, v[2 * i + t]);
 #pragma unroll
           for (int j = 0; j < 8; ++j)
-            acc[i][j] = mfma16x16x32(wf, __builtin_bit_cast(half8_t, v[8 + 2 * j + t]), acc[i][j]);
+            acc[i][j] = mfma16x16x32(wf, __builtin_bit_cast(half8_t, v[2 * NIW + 2 * j + t]), acc[i][j]);
         }
     }
-    // Epilogue: lane holds n = n0 + 128 wn + 16 i + 4 g4 + q of m = m0 + 128 wm + 16 j + l16.
+    // Epilogue: lane holds n = n0 + 16 NIW wn + 16 i + 4 g4 + q of m = m0 + 128 wm + 16 j + l16.
     {
       const uint32_t ln = gp_lane_now();
-      const int64_t mrow = (int64_t)(m0c + 128 * wm) * a.ldo;
+      if constexpr (EPI == GP_PARTIAL) {
+        const uint32_t lp = (ln & 15u) * (uint32_t)a.N + 4u * (ln >> 4);
+        float* const pb = a.part + ((int64_t)cur.sl * a.M + cur.m0 + 128 * wm) * a.N + cur.n0 + 16 * NIW * wn + lp;
+#pragma unroll
+        for (int i = 0; i < NIW; ++i)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) *(f32x4*)(pb + ((int64_t)16 * j * a.N + 16 * i)) = acc[i][j];
+      }
+      const int64_t mrow = (int64_t)(cur.m0 + 128 * wm) * a.ldo;
       const uint32_t lo = (ln & 15u) * (uint32_t)a.ldo + 4u * (ln >> 4);
       if constexpr (EPI == GP_SILU) {
         // column tiles (i, i + 1), i even, are (gate, up) of intermediate columns
-        // (n0 + 128 wn + 16 i) / 2 + 4 g4 + q
-        half_t* const ob = a.out + mrow + (n0c + 64 * wn) / 2 + lo;
+        // (n0 + 64 wn + 16 i) / 2 + 4 g4 + q
+        half_t* const ob = a.out + mrow + (cur.n0 + 64 * wn) / 2 + lo;
 #pragma unroll
         for (int i = 0; i < 4; i += 2)
 #pragma unroll
@@ -699,10 +743,10 @@ __global__ __launch_bounds__(512, 1) void gemm_bigp_f16_kernel(GemmPipeArgs a) {
               o[q] = (half_t)silu_mul_f32((float)(half_t)acc[i][j][q], (float)(half_t)acc[i + 1][j][q]);
             *(half4_t*)(ob + (16 * j * a.ldo + 8 * i)) = o;
           }
-      } else {
-        half_t* const ob = a.out + mrow + n0c + 64 * wn + lo;
+      } else if constexpr (EPI == GP_STORE) {
+        half_t* const ob = a.out + mrow + cur.n0 + 16 * NIW * wn + lo;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < NIW; ++i)
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
             half4_t o;
@@ -712,9 +756,8 @@ __global__ __launch_bounds__(512, 1) void gemm_bigp_f16_kernel(GemmPipeArgs a) {
           }
       }
     }
-    m0c = m0n;
-    n0c = n0n;
-    tile_at(r + 2, m0n, n0n);
+    cur = nxt;
+    nxt = item_at(r + 2);
   }
   gp_wait_vmcnt<0>();                   // drain the clamped tail loads before exit
 }
@@ -816,6 +859,7 @@ static int gp_launch(const GemmPipeArgs& a, int epilogue, hipStream_t st) {
 // 128.6 us for 192 of 256 x 128), the persistent 8-wave 256 x 256 tiles 0.85.
 #define GP_WIDE_COST 1.3
 #define GP_BIG_COST 0.85
+#define GP_PART_ELEMS 400000.0   // fp32 partial sums written and read back per step of cost
 
 // Whether the packed fp16 weights take 128 x 192 tiles (4 waves, 64 x 96 each, 3 stages)
 // instead of the tiles of tile_rows x 128: when the grid's rounds times a tile's cost come
@@ -926,10 +970,38 @@ static void gp_packed_plan(int M, int N, int K, int fmt, int epilogue, bool has_
   rows = tile_rows ? tile_rows : gp_tile_rows(M, N);
   ks = ksplit ? ksplit : (epilogue == GP_SILU ? 1 : omni_f16_gemm_pipe_splits(M, N, K, rows));
   cols = GP_BN;
+  const bool free_split = ksplit == 0;
   if (fmt != 1 || tile_rows != 0 || ks != 1) return;
   if ((epilogue == GP_STORE || epilogue == GP_PARTIAL) && gp_wide_tiles(M, N, rows)) {
     rows = 128;
     cols = 192;
+  }
+  if (epilogue == GP_PARTIAL && free_split && M % 256 == 0) {
+    // fp32 slices are the output anyway: the persistent 256-row tiles (256 or 192 columns)
+    // in 1-4 K slices, where rounds of the grid x a slice's steps x the tile's cost per step
+    // (128 x 128 outputs: 1, or GP_WIDE_COST for 128 x 192, GP_BIG_COST for the persistent
+    // tiles) plus each extra slice's partial traffic (one step per GP_PART_ELEMS floats)
+    // come out below the plan above
+    const int64_t cus = gp_num_cus();
+    const int nk = K / GP_BKH;
+    auto rounds = [&](int64_t t) { return (double)((t + cus - 1) / cus); };
+    double best = rounds((int64_t)ceil_div(M, rows) * (N / cols)) * nk * (rows * cols) / 16384.0 *
+                  (cols == 192 ? GP_WIDE_COST : 1.0);
+    for (int c = 256; c >= 192; c -= 64) {
+      if (N % c) continue;
+      for (int k = 1; k <= 4 && K / 128 >= 2 * k; ++k) {
+        const double cost = rounds((int64_t)(M / 256) * (N / c) * k) * (2 * ((nk / 2 + k - 1) / k)) *
+                                (c / 64) * GP_BIG_COST +
+                            (double)(k - 1) * M * N / GP_PART_ELEMS;
+        if (cost < best) {
+          best = cost;
+          rows = 256;
+          cols = c;
+          ks = k;
+        }
+      }
+    }
+    return;
   }
   if (((epilogue == GP_STORE && !has_bias) || epilogue == GP_SILU) && M % 256 == 0 && N % 256 == 0) {
     const int64_t cus = gp_num_cus();
@@ -986,7 +1058,7 @@ extern "C" int omni_packed_gemm_pipe(const void* x, int ldx, const void* w_packe
   gp_packed_plan(M, N, K, fmt, epilogue, bias != nullptr, tile_rows, ksplit, tile_rows, cols, ksplit);
   if (epilogue == GP_SILU && ksplit != 1) return OMNI_EINVAL;
   // every slice covers at least NS pipeline steps (slices are whole 128-groups of 2 steps)
-  const int ns = fmt == 0 ? (tile_rows == 256 ? 4 : 6) : (tile_rows == 256 ? 3 : 4);
+  const int ns = fmt == 0 ? (tile_rows == 256 ? 4 : 6) : tile_rows == 256 ? (cols == GP_BN ? 3 : 2) : 4;
   if (2 * (K / 128 / ksplit) < ns) return OMNI_EUNSUPPORTED;
   if ((ksplit > 1 || part) && (!workspace || ((uintptr_t)workspace & 15))) return OMNI_EINVAL;
   GemmPipeArgs a;
@@ -1011,17 +1083,26 @@ extern "C" int omni_packed_gemm_pipe(const void* x, int ldx, const void* w_packe
   if (fmt == 0)
     return tile_rows == 256 ? gp_launch<GW_INT4, 4, 4>(a, epilogue, st)
                             : gp_launch<GW_INT4, 2, 6>(a, epilogue, st);
-  if (cols == 192) return gp_launch<GW_F16, 2, 3, 6>(a, epilogue, st);
-  if (cols == 256) {                     // persistent 256 x 256 tiles
-    const int64_t t = (int64_t)(M / 256) * (N / 256);
+  if (tile_rows == 256 && cols != GP_BN) {     // persistent 8-wave tiles of 256 x cols
+    if (M % 256 || N % cols || (cols == 192 && epilogue == GP_SILU) || (epilogue == GP_STORE && bias))
+      return OMNI_EINVAL;                      // (the plan picks them only where they hold)
+    const int64_t t = (int64_t)(M / 256) * (N / cols) * ksplit;
     const int grid = (int)(t < gp_num_cus() ? t : gp_num_cus());
+    const dim3 blk(512);
     if (epilogue == GP_SILU)
-      hipLaunchKernelGGL((gemm_bigp_f16_kernel<GP_SILU>), dim3(grid), dim3(512), 0, st, a);
+      hipLaunchKernelGGL((gemm_bigp_f16_kernel<GP_SILU, 4>), dim3(grid), blk, 0, st, a);
+    else if (epilogue == GP_PARTIAL && cols == 256)
+      hipLaunchKernelGGL((gemm_bigp_f16_kernel<GP_PARTIAL, 4>), dim3(grid), blk, 0, st, a);
+    else if (epilogue == GP_PARTIAL)
+      hipLaunchKernelGGL((gemm_bigp_f16_kernel<GP_PARTIAL, 3>), dim3(grid), blk, 0, st, a);
+    else if (cols == 256)
+      hipLaunchKernelGGL((gemm_bigp_f16_kernel<GP_STORE, 4>), dim3(grid), blk, 0, st, a);
     else
-      hipLaunchKernelGGL((gemm_bigp_f16_kernel<GP_STORE>), dim3(grid), dim3(512), 0, st, a);
+      hipLaunchKernelGGL((gemm_bigp_f16_kernel<GP_STORE, 3>), dim3(grid), blk, 0, st, a);
     OMNI_CHECK_LAUNCH();
     return OMNI_OK;
   }
+  if (cols == 192) return gp_launch<GW_F16, 2, 3, 6>(a, epilogue, st);
   return tile_rows == 256 ? gp_launch<GW_F16, 4, 3>(a, epilogue, st)
                           : gp_launch<GW_F16, 2, 4>(a, epilogue, st);
 }

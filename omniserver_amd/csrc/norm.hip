@@ -259,11 +259,18 @@ extern "C" int omni_add_rmsnorm_partials(const float* partials, int nparts, cons
   if (rc) return rc;
   if (rows == 0) return OMNI_OK;
   if (!partials || nparts <= 0 || !residual || !weight || !y || !residual_out) return OMNI_EINVAL;
-  const int threads = ceil_div(hidden >> 3, 64) * 64;
-  auto kern = threads <= 256 ? rownorm_kernel<true, 256> : rownorm_kernel<true, 1024>;
-  hipLaunchKernelGGL(kern, dim3(rows), dim3(threads), 0, (hipStream_t)stream,
-                     nullptr, partials, nparts, (const half_t*)residual, (const half_t*)weight,
-                     (half_t*)y, (half_t*)residual_out, rows, hidden, eps);
+  if (rows <= 256) {   // the same kernels (and reduction orders) as omni_add_rmsnorm
+    const int threads = ceil_div(hidden >> 3, 64) * 64;
+    auto kern = threads <= 256 ? rownorm_kernel<true, 256> : rownorm_kernel<true, 1024>;
+    hipLaunchKernelGGL(kern, dim3(rows), dim3(threads), 0, (hipStream_t)stream,
+                       nullptr, partials, nparts, (const half_t*)residual, (const half_t*)weight,
+                       (half_t*)y, (half_t*)residual_out, rows, hidden, eps);
+  } else {
+    hipLaunchKernelGGL((rmsnorm_kernel<true, false, false, true>), dim3(ceil_div(rows, 4)), dim3(256), 0,
+                       (hipStream_t)stream, nullptr, (const half_t*)residual, nullptr, nullptr, 0, 0,
+                       (const half_t*)weight, (half_t*)y, nullptr, nullptr, (half_t*)residual_out,
+                       rows, hidden, eps, partials, nparts);
+  }
   OMNI_CHECK_LAUNCH();
   return OMNI_OK;
 }

@@ -24,6 +24,7 @@ weight format and shape; the decode step of the 2B decoder uses the entries belo
 
 from __future__ import annotations
 
+import ctypes
 from typing import Dict, Tuple
 
 import torch
@@ -175,6 +176,41 @@ class _Skinny(nn.Module):
                    self.partial_preset if preset is None else preset)
         return S
 
+    def _prefill_fmt(self, M: int) -> int:
+        """Weight format the tiled GEMM runs on at M rows: 1 packed fp16, 0 packed int4."""
+        return 1
+
+    def partial_plan(self, M: int) -> int:
+        """K slices forward_partial_planned writes at M rows (more than MAX_SKINNY_M): the
+        tiled GEMM's own choice for fp32 partial output, which may be the persistent 256-row
+        tiles in several slices (the 2B decoder's down projection at M = 4096: 256 x 192 tiles
+        in 2 slices, one item per CU)."""
+        if M <= MAX_SKINNY_M or self.fuse_silu or self.N % 128 or self.K % 128:
+            return 1
+        key = (M, self._prefill_fmt(M))
+        plans = self.__dict__.setdefault("_partial_plans", {})
+        if key not in plans:
+            r, c, k = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+            call("omni_packed_gemm_pipe_plan", M, self.N, self.K, key[1], EPI_PARTIAL, 0, 0, 0,
+                 ctypes.byref(r), ctypes.byref(c), ctypes.byref(k))
+            plans[key] = k.value
+        return plans[key]
+
+    def forward_partial_planned(self, x2d: torch.Tensor, partial: torch.Tensor) -> int:
+        """fp32 partial sums [S][M][N] (no bias) into partial with S = partial_plan(M) K
+        slices of whole 128-groups; returns S."""
+        M = x2d.shape[0]
+        if self.fuse_silu or M <= MAX_SKINNY_M:
+            raise ValueError("the planned partial form takes more than MAX_SKINNY_M rows and "
+                             "no SiLU-fused projection")
+        if self.N % 128 or self.K % 128 or x2d.stride(0) % 8:
+            raise ValueError("the planned partial form takes N, K % 128 == 0, ldx % 8 == 0")
+        S = self.partial_plan(M)
+        if partial.numel() < S * M * self.N or partial.dtype != torch.float32:
+            raise ValueError("partial buffer too small or not fp32")
+        self._call_pipe_partial(x2d, partial, 0)
+        return S
+
     def forward_partial_attn(self, states: torch.Tensor, splits: int, n_kv: int, group: int,
                              M: int, partial: torch.Tensor, ksplit: int | None = None,
                              preset: int | None = None) -> int:
@@ -305,6 +341,11 @@ class GPTQLinear(_Skinny):
         if getattr(self, "_w16", None) is not None:
             _WEIGHTS_EPOCH += 1
         self._w16 = None
+
+    def _prefill_fmt(self, M: int) -> int:
+        if self.N % 128 or self.K < 256:
+            return 0
+        return 1 if (self.keep_f16 and M >= self.F16_ROWS) or M >= self.UNPACK_ROWS else 0
 
     def _prefill_f16(self, M: int) -> torch.Tensor | None:
         """The packed fp16 weights the prefill GEMM runs on for M rows, or None (the int4

@@ -216,6 +216,8 @@ class Qwen2LLM(nn.Module):
         pos = None if decode else position_ids.reshape(3, T).to(torch.int64).contiguous()
         if not decode and self.prefill_partials_ok(T):
             return self._forward_partials(x, pos, cache, logits_indices, B)
+        if not decode and self.prefill_down_partials_ok(T):
+            return self._forward_partials(x, pos, cache, logits_indices, B, down_only=True)
         residual = None
         for i, layer in enumerate(self.layers):
             if residual is None:
@@ -254,19 +256,40 @@ class Qwen2LLM(nn.Module):
                    for layer in self.layers
                    for lin in (layer.qkv_proj, layer.o_proj, layer.down_proj))
 
-    def _forward_partials(self, x, pos, cache, logits_indices, B):
+    def prefill_down_partials_ok(self, T: int) -> bool:
+        """Whether forward runs a T-token prefill with only the down projection writing
+        split-K partial sums for the next add+RMSNorm (qkv and o finished in their launches):
+        where the tiled GEMM's own plan for partial output splits every layer's down
+        projection over K (partial_plan >= 2; e.g. 4096 rows: 256 x 192 tiles in two slices
+        fill the CUs once, where the finished form's 128 x 192 tiles run below the persistent
+        tiles' rate), so the fp16 store and, for smaller T, a split's finish launch go."""
+        if not self.prefill_partials or T <= 64 or not self.fused_decode_ready():
+            return False
+        return all(layer.down_proj.N % 128 == 0 and layer.down_proj.partial_plan(T) >= 2
+                   for layer in self.layers)
+
+    def _forward_partials(self, x, pos, cache, logits_indices, B, down_only: bool = False):
         """forward's prefill with the projections' split-K partial sums handed to the next
         kernel (prefill_partials_ok): the same roundings in the same order as the finished
-        projections, so the outputs are identical, with three launches per layer fewer."""
+        projections, so the outputs are identical, with three launches per layer fewer.
+        down_only (prefill_down_partials_ok): qkv and o finished as in forward, the down
+        projection's partials in the tiled GEMM's planned slices summed by the next
+        add+RMSNorm (in slice order, then rounded to fp16 as the finished projection rounds
+        its fp32 sum: the same values up to the order of the fp32 additions)."""
         cfg = self.cfg
         T, H = x.shape
         eps = cfg.rms_norm_eps
         dev = x.device
         f32 = lambda n: torch.empty(n, device=dev, dtype=torch.float32)
         l0 = self.layers[0]
-        qpart = f32(8 * T * l0.qkv_proj.N)
-        opart = f32(8 * T * l0.o_proj.N)
-        dpart = f32(8 * T * l0.down_proj.N)
+        if down_only:
+            dparts = max(layer.down_proj.partial_plan(T) for layer in self.layers)
+            qpart = opart = None
+        else:
+            dparts = 8
+            qpart = f32(8 * T * l0.qkv_proj.N)
+            opart = f32(8 * T * l0.o_proj.N)
+        dpart = f32(dparts * T * l0.down_proj.N)
         residual = x.clone()
         h = torch.empty(T, H, device=dev, dtype=torch.float16)
         qkv = torch.empty(T, cfg.qkv_out, device=dev, dtype=torch.float16)
@@ -279,14 +302,25 @@ class Qwen2LLM(nn.Module):
             else:
                 F.add_rms_norm_partials_out(dpart, Sd, residual, layer.in_norm, eps, h, residual)
             qp = layer.qkv_proj
-            Sq = qp.forward_partial(h, qpart)
-            cache.rope_and_write(qkv, i, pos, self.rope_cos, self.rope_sin, cfg.mrope_section,
-                                 parts=(qpart, Sq, qp.bias, qp.fmt == "int4"))
+            if down_only:
+                qp.forward_out(h, qkv)
+                cache.rope_and_write(qkv, i, pos, self.rope_cos, self.rope_sin, cfg.mrope_section)
+            else:
+                Sq = qp.forward_partial(h, qpart)
+                cache.rope_and_write(qkv, i, pos, self.rope_cos, self.rope_sin, cfg.mrope_section,
+                                     parts=(qpart, Sq, qp.bias, qp.fmt == "int4"))
             cache.attend_qkv(qkv, i, self.scale, attn)
-            So = layer.o_proj.forward_partial(attn.reshape(T, -1), opart)
-            F.add_rms_norm_partials_out(opart, So, residual, layer.post_norm, eps, h, residual)
+            if down_only:
+                o = layer.o_proj(attn.reshape(T, -1))
+                F.add_rms_norm_out(o, residual, layer.post_norm, eps, h, residual)
+            else:
+                So = layer.o_proj.forward_partial(attn.reshape(T, -1), opart)
+                F.add_rms_norm_partials_out(opart, So, residual, layer.post_norm, eps, h, residual)
             layer.gate_up_proj.forward_out(h, act)
-            Sd = layer.down_proj.forward_partial(act, dpart)
+            if down_only:
+                Sd = layer.down_proj.forward_partial_planned(act, dpart)
+            else:
+                Sd = layer.down_proj.forward_partial(act, dpart)
         cache.finish()
         F.add_rms_norm_partials_out(dpart, Sd, residual, self.norm, eps, h, residual)
         if logits_indices is not None:

@@ -174,3 +174,30 @@ def test_pipe_gemm_launch_choices(so):
     assert f(256, 1536, 5120, 0) == 4
     assert f(8192, 1280, 5120, 0) == 1
     assert f(8192, 1280, 100, 0) == 1            # K % 128 != 0: never split
+
+
+def test_packed_partial_plan(so):
+    """The packed prefill GEMM's tiling for fp32 partial output with the K slices left to the
+    plan (no GPU needed: 256 CUs assumed): config 5's down projection at M = 4096 on the
+    persistent 256 x 192 tiles in 2 slices (128 tiles x 2 = one item per CU), a 2048-wide one
+    on 256 x 256 tiles in 2 slices; the o projection (K = 1536) as well (its extra slice's
+    traffic priced against the 128 x 192 tiles' cost); a caller's ksplit, int4 weights, or M
+    not a multiple of 256 keep the pipelined tiles; the STORE plan is unchanged."""
+    import ctypes
+    from omniserver_amd._lib import lib
+    L = lib()
+
+    def plan(M, N, K, fmt, epi, ksplit=0):
+        r, c, k = ctypes.c_int(0), ctypes.c_int(0), ctypes.c_int(0)
+        assert L.omni_packed_gemm_pipe_plan(M, N, K, fmt, epi, 0, 0, ksplit, ctypes.byref(r),
+                                            ctypes.byref(c), ctypes.byref(k)) == 0
+        return r.value, c.value, k.value
+
+    assert plan(4096, 1536, 8960, 1, 2) == (256, 192, 2)
+    assert plan(4096, 2048, 8960, 1, 2) == (256, 256, 2)
+    assert plan(4096, 1536, 1536, 1, 2) == (256, 192, 2)
+    assert plan(4096, 1536, 8960, 1, 2, ksplit=1) == (128, 192, 1)
+    assert plan(4096, 1536, 8960, 0, 2)[0:2] != (256, 192)
+    assert plan(4000, 1536, 8960, 1, 2)[0] != 256
+    assert plan(4096, 1536, 8960, 1, 0) == (128, 192, 1)
+    assert plan(1024, 1536, 8960, 1, 2) == (128, 128, 2)

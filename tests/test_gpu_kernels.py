@@ -497,6 +497,56 @@ def test_packed_gemm_pipe_big_tiles(gpu, M, K, N, silu):
     assert (big[rows_s].float() - e).abs().max().item() <= tol
 
 
+@pytest.mark.parametrize("M,K,N,form", [(4096, 8960, 1536, (256, 192, 2)),
+                                         (4096, 8960, 2048, (256, 256, 2))])
+def test_packed_gemm_pipe_big_partial(gpu, M, K, N, form):
+    """fp32 partial output with the K slices left to the plan (ksplit 0): the persistent
+    256-row tiles in two slices (config 5's down projection at M = 4096 on 256 x 192 tiles; a
+    2048-wide projection on 256 x 256).  Slice s holds the products over its whole 128-groups
+    [s G / S, (s + 1) G / S) of G = K / 128: each slice within fp32 tolerance of the oracle's
+    sums over that K range on sampled rows (every row tile), and fp16 of the slices' sum
+    within one fp16 step of the finished STORE output."""
+    from omniserver_amd._lib import call, ptr, stream
+    from omniserver_amd.linear import F16Linear
+    plan = _packed_plan(M, N, K, 1, 2)
+    say(f"packed gemm pipe big partial M={M} K={K} N={N}: plan {plan}")
+    assert plan == form
+    S = plan[2]
+    wt = f16((N, K), 112, 0.02)
+    x = f16((M, K), 113)
+    lin = F16Linear(wt.to(gpu))
+    xg = x.to(gpu)
+    assert lin.partial_plan(M) == S
+    part = torch.full((S * M * N,), float("nan"), device=gpu, dtype=torch.float32)
+    assert lin.forward_partial_planned(xg, part) == S
+    out = torch.full((M, N), float("nan"), device=gpu, dtype=torch.float16)
+    call("omni_packed_gemm_pipe", ptr(xg), K, ptr(lin.weight_packed), None, 1, None, 0,
+         ptr(out), N, M, N, K, 0, 0, 0, None, stream())
+    torch.cuda.synchronize()
+    P = part.view(S, M, N).cpu()
+    assert not torch.isnan(P).any()
+    rows_s = torch.tensor(sorted({64 * i + (29 * i) % 64 for i in range(M // 64)} | {M - 1}))
+    rows_s = rows_s[:: max(1, len(rows_s) // 64)]
+    G = K // 128
+    for s_ in range(S):
+        k0, k1 = 128 * (s_ * G // S), 128 * ((s_ + 1) * G // S)
+        e = x[rows_s, k0:k1].float() @ wt[:, k0:k1].float().t()
+        d = (P[s_][rows_s] - e).abs().max().item()
+        tol = 5e-4 * max(1.0, e.abs().max().item())
+        say(f"  slice {s_}: k [{k0}, {k1}) max|d| {d:.2e} (tol {tol:.1e})")
+        assert d <= tol
+    tot, mag = P[0].clone(), P[0].abs()
+    for s_ in range(1, S):
+        tot += P[s_]
+        mag += P[s_].abs()
+    o = out.cpu().float()
+    # one fp16 step of the output, plus the fp32 rounding of the slices' sums, which shows
+    # where slices of opposite sign nearly cancel (e.g. -0.4315 + 0.4319), and of the running
+    # sums over K (the finished output itself is 1.5e-6 from the oracle's at such a point)
+    ulp = torch.clamp(o.abs(), min=6.1e-5) * 2.0 ** -10
+    assert ((tot.half().float() - o).abs() <= ulp * 1.01 + 1e-5 * mag + 5e-6).all()
+
+
 @pytest.mark.parametrize("fmt", ["int4", "fp16"])
 @pytest.mark.parametrize("M", [65, 300, 1000])
 @pytest.mark.parametrize("K,N,bias,silu", [
@@ -681,10 +731,12 @@ def test_f16_gemm(gpu, M, K, N, bias, silu):
     assert d.max().item() <= tol, (d.max().item(), tol)
 
 
-@pytest.mark.parametrize("S,M,H", [(7, 32, 1536), (20, 5, 1536), (11, 3, 4096)])
+@pytest.mark.parametrize("S,M,H", [(7, 32, 1536), (20, 5, 1536), (11, 3, 4096), (2, 1000, 1536),
+                                   (3, 300, 4096)])
 def test_add_rmsnorm_partials(gpu, S, M, H):
     """x = fp16(sum of split-K partials in slice order), then add + RMSNorm (H = 4096 runs
-    the 1024-thread form, 20 slices two batches of the 256-thread one)."""
+    the 1024-thread form, 20 slices two batches of the 256-thread one; past 256 rows the
+    many-row kernel, bit-equal to omni_add_rmsnorm on the slice-ordered fp16 sum)."""
     from omniserver_amd import fused_ops as F
     say(f"add_rmsnorm over split-K partials S={S} M={M} H={H}")
     g = torch.Generator().manual_seed(101)
@@ -702,6 +754,14 @@ def test_add_rmsnorm_partials(gpu, S, M, H):
     # fp16 rounding: residuals agree to one fp16 ulp
     assert (nr.cpu().float() - er).abs().max().item() <= 2e-3 * er.abs().max().item()
     assert (y.cpu().float() - ey).abs().max().item() <= 2e-3 * ey.abs().max().item()
+    if M > 256:
+        xs = pg[0].clone()
+        for p in range(1, S):
+            xs = xs + pg[p]
+        y2, r2 = torch.empty_like(y), torch.empty_like(y)
+        F.add_rms_norm_out(xs.half(), rg, wg, 1e-6, y2, r2)
+        torch.cuda.synchronize()
+        assert torch.equal(y.cpu(), y2.cpu()) and torch.equal(nr.cpu(), r2.cpu())
 
 
 @pytest.mark.parametrize("fmt", ["int4", "fp16"])

@@ -265,6 +265,53 @@ def test_prefill_partials_equal_finished(gpu, quant, segs):
         assert torch.equal(outs[0][1][0], outs[1][1][0])
 
 
+@pytest.mark.parametrize("quant,segs", [(None, [512] * 8), ("gptq", [512] * 8), ("gptq", [600, 424])])
+def test_prefill_down_partials(gpu, quant, segs):
+    """Past the all-partials range (qkv / o unsplit at T), the packed prefill hands only the
+    down projection's split-K partial sums - the tiled GEMM's planned slices: 256 x 192 tiles
+    in two slices at T = 4096, 128 x 128 tiles in two at T = 1024 - to the next add+RMSNorm
+    (prefill_down_partials_ok).  Against every projection finished in its own launch: layer
+    0's K/V pool rows equal (written before any down projection), the logits within a few fp16
+    steps (the slices' fp32 sums add in another order than one pass over K)."""
+    from omniserver_amd import synth
+    from omniserver_amd.kv_cache import PreallocatedKVCache
+    from omniserver_amd.qwen2_llm import Qwen2LLM
+    say(f"prefill down partials quant={quant} segs={segs}")
+    shape = synth.DecoderShape()
+    if quant == "gptq":
+        model = Qwen2LLM.from_gptq(synth.gptq_decoder(shape, seed=37, num_layers=3), shape, gpu,
+                                   max_pos=1024)
+    else:
+        model = Qwen2LLM.from_fp16(synth.fp16_decoder(shape, seed=37, num_layers=3), shape, gpu,
+                                   max_pos=1024)
+    T = sum(segs)
+    ids = synth.random_ids(T, shape.vocab_size, 37, "dp").to(gpu)
+    emb = model.embed_tokens(ids).unsqueeze(0)
+    pos = torch.cat([torch.arange(L) for L in segs]).view(1, 1, T).expand(3, 1, T).contiguous().to(gpu)
+    last = (torch.tensor(segs).cumsum(0) - 1).tolist()
+    outs = []
+    for flag in (False, True):
+        model.prefill_partials = flag
+        assert not model.prefill_partials_ok(T)
+        assert model.prefill_down_partials_ok(T) == flag
+        pool = PreallocatedKVCache(n_layers=3, max_batch=len(segs) + 1,
+                                   n_kv_heads=shape.num_kv_heads, max_len=1024,
+                                   head_dim=shape.head_dim, device=gpu, dtype=torch.float16,
+                                   n_heads=shape.num_heads)
+        cache = pool.packed_prefill_cache(list(range(len(segs))), segs)
+        logits = model(emb, pos, None, cache, logits_indices=last)
+        torch.cuda.synchronize()
+        outs.append((logits.cpu(), pool.storage.cpu(), pool.lengths.cpu()))
+    model.prefill_partials = True
+    say(f"T={T}: down slices {model.layers[0].down_proj.partial_plan(T)}")
+    assert model.layers[0].down_proj.partial_plan(T) == 2
+    assert torch.equal(outs[0][2], outs[1][2])
+    assert torch.equal(outs[0][1][0], outs[1][1][0])
+    d = (outs[0][0].float() - outs[1][0].float()).abs().max().item()
+    say(f"T={T}: logits max-abs difference {d:.2e}")
+    assert d <= 1e-2, d
+
+
 def test_graph_sampling_equals_eager(gpu):
     """A batch with temperature-sampled rows (and a greedy one) decodes in graph mode by
     replaying the logits-capturing step graph and sampling on the host: with the same

@@ -53,6 +53,8 @@ struct GemmPipeArgs {
   int M, N, K;
   int KS;                // K slices; > 1: fp32 partial sums to part, finished by a second kernel
   float* part;           // [KS][M][N]
+  int n_big;             // persistent 256-column tiles: whole tiles below column n_big, 128-column
+                         // half tiles from there to N (one K slice); N elsewhere
 };
 
 template <int N>
@@ -578,25 +580,38 @@ __global__ __launch_bounds__(512, 1) void gemm_bigp_f16_kernel(GemmPipeArgs a) {
   const int l16 = lane & 15;
   const int g4 = lane >> 4;
 
-  const int tiles_n = a.N / BN;
+  const int tiles_n = a.n_big / BN;
   const int tiles_m = a.M / BM;
   const int tiles = tiles_m * tiles_n;
-  const int items = tiles * a.KS;                           // slice-major: item = s tiles + tile
+  const int items_big = tiles * a.KS;                       // slice-major: item = s tiles + tile
+  // the columns past n_big in 256 x (BN / 2) half tiles, after every whole tile: a grid whose
+  // whole tiles fill R rounds exactly then ends with at most half a tile per workgroup
+  const int tiles_hn = NIW == 4 ? (a.N - a.n_big) / (BN / 2) : 0;
+  const int items = items_big + tiles_m * tiles_hn;
   const int G = gridDim.x;
   const int slot = xcd_logical_block(blockIdx.x, G);
   const int my_items = (items - slot + G - 1) / G;          // grid <= items: >= 1
   const int nk = a.K / GP_BKH;                              // every slice >= NS steps (host check)
   struct Item {
     int m0, n0, sl, kb, kc;            // tile origin, K slice, its first step and step count
+    int half;                          // a 256 x (BN / 2) tile past n_big
   };
   auto item_at = [&](int r) {                               // past the last item: the last one
     Item t;
     const int it = min(r, my_items - 1) * G + slot;
-    t.sl = it / tiles;
     int tm, tn;
-    grouped_tile(it - t.sl * tiles, tiles_m, tiles_n, GP_GM, tm, tn);
+    if (it < items_big) {
+      t.sl = it / tiles;
+      grouped_tile(it - t.sl * tiles, tiles_m, tiles_n, GP_GM, tm, tn);
+      t.n0 = tn * BN;
+      t.half = 0;
+    } else {
+      t.sl = 0;
+      grouped_tile(it - items_big, tiles_m, tiles_hn, GP_GM, tm, tn);
+      t.n0 = a.n_big + tn * (BN / 2);
+      t.half = 1;
+    }
     t.m0 = tm * BM;
-    t.n0 = tn * BN;
     // slices are whole 128-k groups (pairs of steps), as in the kernel above
     t.kb = 2 * (t.sl * (nk / 2) / a.KS);
     t.kc = 2 * ((t.sl + 1) * (nk / 2) / a.KS) - t.kb;
@@ -612,7 +627,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bigp_f16_kernel(GemmPipeArgs a) {
   // 1 KB blocks, (K / 32) of them per column tile.  ks: the absolute K step.
   const uint32_t xstep = 64u * (uint32_t)a.ldx * 2u;
   const uint32_t kblk = (uint32_t)(a.K / 32) * 1024u;       // bytes per packed column tile
-  auto issue = [&](int m0, int n0, int ks, int st) {
+  auto issue = [&](int m0, int n0, int ks, int st, int half) {
     const uint8_t* const xs = (const uint8_t*)(a.x + (int64_t)m0 * a.ldx) + (uint32_t)ks * 128u;
     const uint8_t* const ws = (const uint8_t*)(a.w + (int64_t)(n0 / 16) * (a.K / 32) * 512) +
                               (uint32_t)ks * 2048u;
@@ -626,6 +641,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bigp_f16_kernel(GemmPipeArgs a) {
                                        (lds_void*)((lds_u8*)&xl[st][(64 * u + 8 * wave) * GP_ROWB]), 16, 0, 0);
 #pragma unroll
     for (int u = 0; u < WLD; ++u) {
+      if (half && 2 * u >= WLD) break;   // a half tile's 4 NIW blocks
       const int b = 8 * u + wave;
       __builtin_amdgcn_global_load_lds(
           (const void*)(ws + ((uint32_t)(b >> 1) * kblk + (uint32_t)(b & 1) * 1024u + lw)),
@@ -635,12 +651,37 @@ __global__ __launch_bounds__(512, 1) void gemm_bigp_f16_kernel(GemmPipeArgs a) {
   // Operand reads: x fragment (j, t) = k 32 t + 8 g4 .. +7 of row 128 wm + 16 j + l16, at
   // chunk (4 t + g4) ^ (l16 & 7) of the row (16 j keeps row & 7 = l16 & 7): two bases (t)
   // plus 2 KB per j; w fragment (i, t) = the lane's 16 bytes of block 2 (NIW wn + i) + t.
-  auto read_ops = [&](int st, u32x4 (&v)[NV]) {
+  auto read_ops = [&](int st, u32x4 (&v)[NV], int half) {
     const int r = 128 * wm + l16;
     const uint32_t row = (uint32_t)(uintptr_t)(lds_u8*)&xl[st][r * GP_ROWB];
     const uint32_t bx0 = row + ((g4 ^ (l16 & 7)) << 4);
     const uint32_t bx1 = row + (((4 + g4) ^ (l16 & 7)) << 4);
     const uint32_t bw = (uint32_t)(uintptr_t)(lds_u8*)&wl[st][2 * NIW * wn * 1024] + (uint32_t)lane * 16u;
+    if (NIW == 4 && half) {
+      // a half tile: the wave's 2 column tiles (blocks 4 wn .. 4 wn + 3) into v[0..3]; x as below
+      const uint32_t bh = (uint32_t)(uintptr_t)(lds_u8*)&wl[st][4 * wn * 1024] + (uint32_t)lane * 16u;
+      asm volatile(
+          "ds_read_b128 %0, %20\n\tds_read_b128 %1, %20 offset:1024\n\t"
+          "ds_read_b128 %2, %20 offset:2048\n\tds_read_b128 %3, %20 offset:3072\n\t"
+          "ds_read_b128 %4, %21\n\tds_read_b128 %5, %22\n\t"
+          "ds_read_b128 %6, %21 offset:2048\n\tds_read_b128 %7, %22 offset:2048\n\t"
+          "ds_read_b128 %8, %21 offset:4096\n\tds_read_b128 %9, %22 offset:4096\n\t"
+          "ds_read_b128 %10, %21 offset:6144\n\tds_read_b128 %11, %22 offset:6144\n\t"
+          "ds_read_b128 %12, %21 offset:8192\n\tds_read_b128 %13, %22 offset:8192\n\t"
+          "ds_read_b128 %14, %21 offset:10240\n\tds_read_b128 %15, %22 offset:10240\n\t"
+          "ds_read_b128 %16, %21 offset:12288\n\tds_read_b128 %17, %22 offset:12288\n\t"
+          "ds_read_b128 %18, %21 offset:14336\n\tds_read_b128 %19, %22 offset:14336\n\t"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[2 * NIW]),
+            "=&v"(v[2 * NIW + 1]), "=&v"(v[2 * NIW + 2]), "=&v"(v[2 * NIW + 3]), "=&v"(v[2 * NIW + 4]),
+            "=&v"(v[2 * NIW + 5]), "=&v"(v[2 * NIW + 6]), "=&v"(v[2 * NIW + 7]), "=&v"(v[2 * NIW + 8]),
+            "=&v"(v[2 * NIW + 9]), "=&v"(v[2 * NIW + 10]), "=&v"(v[2 * NIW + 11]),
+            "=&v"(v[2 * NIW + 12]), "=&v"(v[2 * NIW + 13]), "=&v"(v[2 * NIW + 14]),
+            "=&v"(v[2 * NIW + 15])
+          : "v"(bh), "v"(bx0), "v"(bx1)
+          : "memory");
+      return;
+    }
     if constexpr (NIW == 4) asm volatile(
         "ds_read_b128 %0, %24\n\tds_read_b128 %1, %24 offset:1024\n\t"
         "ds_read_b128 %2, %24 offset:2048\n\tds_read_b128 %3, %24 offset:3072\n\t"
@@ -682,8 +723,8 @@ __global__ __launch_bounds__(512, 1) void gemm_bigp_f16_kernel(GemmPipeArgs a) {
         : "memory");
   };
   Item cur = item_at(0), nxt = item_at(1);
-  issue(cur.m0, cur.n0, cur.kb, 0);
-  issue(cur.m0, cur.n0, cur.kb + 1, 1);
+  issue(cur.m0, cur.n0, cur.kb, 0, cur.half);
+  issue(cur.m0, cur.n0, cur.kb + 1, 1, cur.half);
   gp_wait_vmcnt<XLD + WLD>();           // stage 0
   gp_barrier();
   int sidx = 0;
@@ -696,20 +737,21 @@ __global__ __launch_bounds__(512, 1) void gemm_bigp_f16_kernel(GemmPipeArgs a) {
     for (int ks = 0; ks < cur.kc; ++ks, ++sidx) {
       const int st = sidx & 1;
       u32x4 v[NV];
-      read_ops(st, v);
+      read_ops(st, v, cur.half);
       // step sidx + 1 has landed (nothing younger is in flight with two stages) for this
       // thread, then for everyone; every wave has read this slot, refilled with sidx + 2
       gp_wait_vmcnt<0>();
       gp_barrier();
       {
         const int iks = ks + NS;
-        if (iks < cur.kc) issue(cur.m0, cur.n0, cur.kb + iks, st);
-        else issue(nxt.m0, nxt.n0, nxt.kb + iks - cur.kc, st);
+        if (iks < cur.kc) issue(cur.m0, cur.n0, cur.kb + iks, st, cur.half);
+        else issue(nxt.m0, nxt.n0, nxt.kb + iks - cur.kc, st, nxt.half);
       }
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int i = 0; i < NIW; ++i) {
+          if (cur.half && 2 * i >= NIW) break;   // a half tile's NIW / 2 column tiles
           const half8_t wf = __builtin_bit_cast(half8_t, v[2 * i + t]);
 #pragma unroll
           for (int j = 0; j < 8; ++j)
@@ -719,34 +761,42 @@ __global__ __launch_bounds__(512, 1) void gemm_bigp_f16_kernel(GemmPipeArgs a) {
     // Epilogue: lane holds n = n0 + 16 NIW wn + 16 i + 4 g4 + q of m = m0 + 128 wm + 16 j + l16.
     {
       const uint32_t ln = gp_lane_now();
+      // the wave's first column: 16 NIW wn of a whole tile, 8 NIW wn of a half tile
+      const int wc = cur.n0 + (cur.half ? 8 : 16) * NIW * wn;
+      const int ni = cur.half ? NIW / 2 : NIW;
       if constexpr (EPI == GP_PARTIAL) {
         const uint32_t lp = (ln & 15u) * (uint32_t)a.N + 4u * (ln >> 4);
-        float* const pb = a.part + ((int64_t)cur.sl * a.M + cur.m0 + 128 * wm) * a.N + cur.n0 + 16 * NIW * wn + lp;
+        float* const pb = a.part + ((int64_t)cur.sl * a.M + cur.m0 + 128 * wm) * a.N + wc + lp;
 #pragma unroll
-        for (int i = 0; i < NIW; ++i)
+        for (int i = 0; i < NIW; ++i) {
+          if (i >= ni) break;
 #pragma unroll
           for (int j = 0; j < 8; ++j) *(f32x4*)(pb + ((int64_t)16 * j * a.N + 16 * i)) = acc[i][j];
+        }
       }
       const int64_t mrow = (int64_t)(cur.m0 + 128 * wm) * a.ldo;
       const uint32_t lo = (ln & 15u) * (uint32_t)a.ldo + 4u * (ln >> 4);
       if constexpr (EPI == GP_SILU) {
         // column tiles (i, i + 1), i even, are (gate, up) of intermediate columns
-        // (n0 + 64 wn + 16 i) / 2 + 4 g4 + q
-        half_t* const ob = a.out + mrow + (cur.n0 + 64 * wn) / 2 + lo;
-#pragma unroll
-        for (int i = 0; i < 4; i += 2)
+        // (wc + 16 i) / 2 + 4 g4 + q
+        half_t* const ob = a.out + mrow + wc / 2 + lo;
+        auto pair = [&](f32x4 (&g)[8], f32x4 (&u)[8], int c) {
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
             half4_t o;
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-              o[q] = (half_t)silu_mul_f32((float)(half_t)acc[i][j][q], (float)(half_t)acc[i + 1][j][q]);
-            *(half4_t*)(ob + (16 * j * a.ldo + 8 * i)) = o;
+              o[q] = (half_t)silu_mul_f32((float)(half_t)g[j][q], (float)(half_t)u[j][q]);
+            *(half4_t*)(ob + (16 * j * a.ldo + c)) = o;
           }
+        };
+        pair(acc[0], acc[1], 0);
+        if (!cur.half) pair(acc[2], acc[3], 16);
       } else if constexpr (EPI == GP_STORE) {
-        half_t* const ob = a.out + mrow + cur.n0 + 16 * NIW * wn + lo;
+        half_t* const ob = a.out + mrow + wc + lo;
 #pragma unroll
-        for (int i = 0; i < NIW; ++i)
+        for (int i = 0; i < NIW; ++i) {
+          if (i >= ni) break;
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
             half4_t o;
@@ -754,6 +804,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bigp_f16_kernel(GemmPipeArgs a) {
             for (int q = 0; q < 4; ++q) o[q] = (half_t)acc[i][j][q];
             *(half4_t*)(ob + (16 * j * a.ldo + 16 * i)) = o;
           }
+        }
       }
     }
     cur = nxt;
@@ -853,6 +904,22 @@ static int gp_launch(const GemmPipeArgs& a, int epilogue, hipStream_t st) {
   return OMNI_OK;
 }
 
+// The persistent 256 x 256 tiles' column split (one K slice): where the whole tiles would
+// leave a last round partly idle, the columns past the returned one run as 256 x 128 half
+// tiles after R full rounds of whole tiles, at most one half tile per CU (config 5's gate_up
+// at M = 4096: 1120 tiles = 4 rounds of 256 + 96, so 1024 whole tiles over columns
+// [0, 16384) and 192 half tiles over the last 1536); N where no such split exists.
+static int gp_big_tail_cols(int M, int N) {
+  const int64_t cus = gp_num_cus();
+  const int64_t tm = M / 256, tn = N / 256;
+  const int64_t tiles = tm * tn;
+  const int64_t R = tiles / cus;
+  if (R == 0 || tiles % cus == 0 || (R * cus) % tm) return N;
+  const int64_t nb = R * cus / tm;                    // whole column tiles
+  if (2 * tm * (tn - nb) > cus) return N;
+  return (int)(nb * 256);
+}
+
 // Relative costs of the packed fp16 weights' tile forms per 128 x 128 outputs (fitted on
 // MI355X with grid rounds x tile size): the 8-wave 256 x 128 / 4-wave 128 x 128 tiles 1, the
 // 4-wave 128 x 192 tiles 1.3 (config 5's down at M = 4096: 125.1 us for 256 of them against
@@ -860,6 +927,7 @@ static int gp_launch(const GemmPipeArgs& a, int epilogue, hipStream_t st) {
 #define GP_WIDE_COST 1.3
 #define GP_BIG_COST 0.85
 #define GP_PART_ELEMS 400000.0   // fp32 partial sums written and read back per step of cost
+#define GP_TAIL_COST 0.65        // a round of 256 x 128 tail tiles, in rounds of 256 x 256 tiles
 
 // Whether the packed fp16 weights take 128 x 192 tiles (4 waves, 64 x 96 each, 3 stages)
 // instead of the tiles of tile_rows x 128: when the grid's rounds times a tile's cost come
@@ -952,6 +1020,7 @@ extern "C" int omni_f16_gemm_pipe(const void* x, int ldx, const void* w, const v
   a.K = K;
   a.KS = ksplit;
   a.part = workspace;
+  a.n_big = N;
   a.wq = nullptr;
   a.wsc = nullptr;
   a.bias_after_round = 0;
@@ -1008,7 +1077,11 @@ static void gp_packed_plan(int M, int N, int K, int fmt, int epilogue, bool has_
     auto rounds = [&](int64_t t) { return (double)((t + cus - 1) / cus); };
     const double cur = rounds((int64_t)ceil_div(M, rows) * (N / cols)) * (rows * cols) / 16384.0 *
                        (cols == 192 ? GP_WIDE_COST : 1.0);
-    const double big = rounds((int64_t)(M / 256) * (N / 256)) * 4.0 * GP_BIG_COST;
+    // a half-tile tail round (gp_big_tail_cols) measured at 0.65 of a whole one: M = 4096
+    // gate_up + SiLU 204.9 against 221.1 us with whole tiles only
+    const int64_t tb = (int64_t)(M / 256) * (N / 256);
+    const double big = (gp_big_tail_cols(M, N) < N ? (double)(tb / cus) + GP_TAIL_COST : rounds(tb)) *
+                       4.0 * GP_BIG_COST;
     if (big < cur) {
       rows = 256;
       cols = 256;
@@ -1079,6 +1152,7 @@ extern "C" int omni_packed_gemm_pipe(const void* x, int ldx, const void* w_packe
   a.K = K;
   a.KS = ksplit;
   a.part = workspace;
+  a.n_big = N;
   hipStream_t st = (hipStream_t)stream;
   if (fmt == 0)
     return tile_rows == 256 ? gp_launch<GW_INT4, 4, 4>(a, epilogue, st)
@@ -1086,7 +1160,11 @@ extern "C" int omni_packed_gemm_pipe(const void* x, int ldx, const void* w_packe
   if (tile_rows == 256 && cols != GP_BN) {     // persistent 8-wave tiles of 256 x cols
     if (M % 256 || N % cols || (cols == 192 && epilogue == GP_SILU) || (epilogue == GP_STORE && bias))
       return OMNI_EINVAL;                      // (the plan picks them only where they hold)
-    const int64_t t = (int64_t)(M / 256) * (N / cols) * ksplit;
+    int64_t t = (int64_t)(M / 256) * (N / cols) * ksplit;
+    if (cols == 256 && ksplit == 1) {
+      a.n_big = gp_big_tail_cols(M, N);
+      t = (int64_t)(M / 256) * (a.n_big / 256 + (N - a.n_big) / 128);
+    }
     const int grid = (int)(t < gp_num_cus() ? t : gp_num_cus());
     const dim3 blk(512);
     if (epilogue == GP_SILU)

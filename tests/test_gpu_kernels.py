@@ -460,12 +460,14 @@ def test_packed_gemm_pipe_wide_tiles(gpu, M, K, bias):
     assert (wide[rows_s].float() - e).abs().max().item() <= tol
 
 
-@pytest.mark.parametrize("M,K,N,silu", [(4096, 1536, 17920, True), (8192, 1536, 2048, False)])
+@pytest.mark.parametrize("M,K,N,silu", [(4096, 1536, 17920, True), (4096, 1536, 17920, False),
+                                        (8192, 1536, 2048, False)])
 def test_packed_gemm_pipe_big_tiles(gpu, M, K, N, silu):
     """The persistent 256 x 256 tiles omni_packed_gemm_pipe picks for config 5's gate_up (SiLU)
-    at M = 4096 and for an unbiased STORE at M = 8192: equal to the 256 x 128 tiles' results
-    bit for bit (same k order per output), and 64 sampled rows (every row tile) within
-    tolerance of the oracle."""
+    at M = 4096 (and an unbiased STORE at that shape): 1024 whole tiles over the first 16384
+    columns, the last 1536 in 256 x 128 half tiles; and an unbiased STORE at M = 8192 (whole
+    tiles only): equal to the 256 x 128 tiles' results bit for bit (same k order per output),
+    and 64 sampled rows (every row tile) within tolerance of the oracle."""
     from omniserver_amd._lib import call, ptr, stream
     from omniserver_amd.linear import F16Linear
     rows, cols, ks = _packed_plan(M, N, K, 1, 1 if silu else 0)

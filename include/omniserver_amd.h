@@ -417,6 +417,13 @@ int omni_fp8_gemm(const void* xq, const float* sa, const void* wq, const float* 
                   const void* bias, void* out, int ldo, int M, int N, int K, int out_mode,
                   void* stream);
 
+/* Self-check of the bf16 rounding the FP8 GEMM epilogues use (no reference counterpart: a
+ * test of this library's arithmetic): every one of the 2^32 float bit patterns through the
+ * device's packed bf16 conversion and through the integer round-to-nearest-even with quieted
+ * NaNs that the reference's bf16 outputs follow; adds the non-NaN mismatches to
+ * mismatches[0] and the NaN ones to mismatches[1] (device memory, zeroed by the caller). */
+int omni_bf16_rne_check(unsigned long long* mismatches, void* stream);
+
 /* The kernel omni_fp8_gemm runs for a shape (no reference counterpart: it tells a caller
  * or a test which form covers the shape): 0 one 128 x 128 tile per workgroup (K < 512),
  * 1 the pipelined persistent 256 x 128 tiles, 2 the persistent 256 x 256 tiles, 3 the

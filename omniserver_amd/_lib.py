@@ -85,6 +85,7 @@ SIGNATURES = {
     "omni_f16_pack": [_P, _P, _I, _I, _I, _P],
     "omni_w4_dequant": [_P, _P, _P, _I, _I, _P],
     "omni_w4_unpack_f16": [_P, _P, _P, _I, _I, _P],
+    "omni_bf16_rne_check": [_P, _P],
 }
 
 ERRORS = {-1: "invalid argument", -2: "unsupported shape"}

@@ -32,18 +32,31 @@
 
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 
-__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
-  uint32_t u = __builtin_bit_cast(uint32_t, f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);   // quiet NaN
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+typedef __bf16 bf16x2_hw __attribute__((ext_vector_type(2)));
+typedef float f32x2_hw __attribute__((ext_vector_type(2)));
+
+// The integer form of bf16 rounding: round to nearest even, NaNs quieted (sign and upper
+// payload kept).
+__device__ __forceinline__ uint32_t bf16_bits_int(uint32_t u) {
+  const uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  return (u & 0x7fffffffu) > 0x7f800000u ? ((u >> 16) | 0x0040u) : r;
 }
 
-// The bf16 value nearest f (RNE, NaN kept quiet), as a float; branch-free.
+// bf16 bits of (a, b), a in the low half: gfx950's v_cvt_pk_bf16_f32, one instruction per
+// pair, equal to bf16_bits_int on every one of the 2^32 float inputs
+// (omni_bf16_rne_check).
+__device__ __forceinline__ uint32_t bf16x2_bits(float a, float b) {
+  const f32x2_hw v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_hw));
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  return (uint16_t)(bf16x2_bits(f, 0.f) & 0xffffu);
+}
+
+// The bf16 value nearest f (RNE, NaN kept quiet), as a float.
 __device__ __forceinline__ float bf16_value(float f) {
-  const uint32_t u = __builtin_bit_cast(uint32_t, f);
-  const uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u;
-  return __builtin_bit_cast(float, (u & 0x7fffffffu) > 0x7f800000u ? ((u & 0xffff0000u) | 0x00400000u) : r);
+  return __builtin_bit_cast(float, bf16x2_bits(f, 0.f) << 16);
 }
 
 struct Fp8GemmArgs {
@@ -213,12 +226,8 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 __device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
 
-// bf16 bits of f, round to nearest even, NaN kept quiet; branch-free.
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  const uint32_t u = __builtin_bit_cast(uint32_t, f);
-  const uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-  return (u & 0x7fffffffu) > 0x7f800000u ? ((u >> 16) | 0x0040u) : r;
-}
+// bf16 bits of f, round to nearest even, NaN kept quiet.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) { return bf16x2_bits(f, 0.f) & 0xffffu; }
 
 // One tile's load sources: per-lane x row pointers (rows clamped below M) for the four
 // row groups, the w row pointer of group 0 (groups u are 32 u rows further), the lane's
@@ -496,6 +505,17 @@ __device__ __forceinline__ uint32_t fp8_out_bits(float v, half_t bias) {
   return (uint32_t)__builtin_bit_cast(uint16_t, (half_t)((float)(half_t)bf + (float)bias));
 }
 
+// fp8_out_bits of two adjacent outputs, packed (v0 low): one bf16 conversion per pair.
+template <bool OUT_BF16>
+__device__ __forceinline__ uint32_t fp8_out_bits2(float v0, float v1, half_t b0, half_t b1) {
+  const uint32_t p = bf16x2_bits(v0, v1);
+  const float f0 = __builtin_bit_cast(float, p << 16), f1 = __builtin_bit_cast(float, p & 0xffff0000u);
+  if (OUT_BF16) return bf16x2_bits(f0 + bf16_value((float)b0), f1 + bf16_value((float)b1));
+  const half_t h0 = (half_t)((float)(half_t)f0 + (float)b0);
+  const half_t h1 = (half_t)((float)(half_t)f1 + (float)b1);
+  return (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+}
+
 // Persistent form of the big tiles: a grid of at most one workgroup per CU walks its tiles
 // (round r, slot b: logical tile r * grid + b, in the same XCD-grouped order), and the K
 // loop runs straight across tile boundaries: the next tile's first two stages are loaded
@@ -518,13 +538,12 @@ __device__ __forceinline__ void fp8_bigp_epilogue(const f32x4 (&acc)[NIW][8], ui
     if (has_bias) bb = __builtin_bit_cast(half4_t, bw);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      uint32_t bits[4];
+      float v[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        bits[q] = fp8_out_bits<OUT_BF16>((acc[i][j][q] * sm[j]) * sn_i[q], bb[q]);
+      for (int q = 0; q < 4; ++q) v[q] = (acc[i][j][q] * sm[j]) * sn_i[q];
       uint2 pk;
-      pk.x = bits[0] | (bits[1] << 16);
-      pk.y = bits[2] | (bits[3] << 16);
+      pk.x = fp8_out_bits2<OUT_BF16>(v[0], v[1], bb[0], bb[1]);
+      pk.y = fp8_out_bits2<OUT_BF16>(v[2], v[3], bb[2], bb[3]);
       *(uint2*)(ob + (16 * j * ldo + 16 * i)) = pk;
     }
   }
@@ -1037,6 +1056,31 @@ extern "C" int omni_fp8_gemm(const void* xq, const float* sa, const void* wq, co
   } else {
     hipLaunchKernelGGL(fp8_gemm_kernel, dim3((unsigned)tiles), dim3(256), 0, (hipStream_t)stream, a);
   }
+  OMNI_CHECK_LAUNCH();
+  return OMNI_OK;
+}
+
+// Exhaustive device check of the bf16 rounding the FP8 epilogues use: every one of the 2^32
+// float bit patterns through bf16x2_bits (the hardware conversion) and bf16_bits_int (the
+// integer rounding); mismatches[0] counts non-NaN inputs that differ, mismatches[1] NaNs.
+__global__ __launch_bounds__(256) void bf16_rne_check_kernel(unsigned long long* mismatches) {
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;      // 2^24 threads, 256 patterns each
+  uint32_t bad = 0, badnan = 0;
+  for (uint32_t k = 0; k < 256; k += 2) {
+    const uint32_t u0 = (i << 8) | k, u1 = u0 | 1u;
+    const uint32_t hw = bf16x2_bits(__builtin_bit_cast(float, u0), __builtin_bit_cast(float, u1));
+    const bool n0 = (u0 & 0x7fffffffu) > 0x7f800000u, n1 = (u1 & 0x7fffffffu) > 0x7f800000u;
+    if ((hw & 0xffffu) != bf16_bits_int(u0)) ++(n0 ? badnan : bad);
+    if ((hw >> 16) != bf16_bits_int(u1)) ++(n1 ? badnan : bad);
+  }
+  if (bad) atomicAdd(&mismatches[0], (unsigned long long)bad);
+  if (badnan) atomicAdd(&mismatches[1], (unsigned long long)badnan);
+}
+
+extern "C" int omni_bf16_rne_check(unsigned long long* mismatches, void* stream) {
+  if (!mismatches || ((uintptr_t)mismatches & 7)) return OMNI_EINVAL;
+  hipLaunchKernelGGL(bf16_rne_check_kernel, dim3(1u << 16), dim3(256), 0, (hipStream_t)stream,
+                     mismatches);
   OMNI_CHECK_LAUNCH();
   return OMNI_OK;
 }

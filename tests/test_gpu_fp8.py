@@ -137,3 +137,15 @@ def test_fp8_prequant_bias_bf16(gpu):
     tol = (e0.abs() + e.abs()) * 2.0 ** -7 + abs_product(qc, s.cpu(), wq, sw) * 2.0 ** -14
     assert (d <= tol + 1e-6).all(), (d - tol).max().item()
     assert (d == 0).float().mean().item() > 0.95
+
+
+def test_bf16_rounding_exhaustive(gpu):
+    """The FP8 epilogues round to bf16 with the device's packed conversion: on every one of
+    the 2^32 float bit patterns it equals the integer round-to-nearest-even with quieted NaNs
+    (the rounding of the reference's bf16 outputs), NaN inputs included."""
+    from omniserver_amd._lib import call, ptr, stream
+    say("bf16 rounding: all 2^32 float inputs")
+    mism = torch.zeros(2, device=gpu, dtype=torch.int64)
+    call("omni_bf16_rne_check", ptr(mism), stream())
+    torch.cuda.synchronize()
+    assert mism.tolist() == [0, 0]

@@ -426,7 +426,9 @@ int omni_bf16_rne_check(unsigned long long* mismatches, void* stream);
 
 /* The kernel omni_fp8_gemm runs for a shape (no reference counterpart: it tells a caller
  * or a test which form covers the shape): 0 one 128 x 128 tile per workgroup (K < 512),
- * 1 the pipelined persistent 256 x 128 tiles, 2 the persistent 256 x 256 tiles, 3 the
+ * 1 the pipelined persistent 256 x 128 tiles, 2 the persistent 256 x 256 tiles (where whole
+ * tiles would leave the grid's last round partly idle, the columns past whole rounds as
+ * 256 x 192 tiles after them, at most one per CU: config 4's gate_up at M = 8192), 3 the
  * persistent 256 x 192 tiles (2 and 3: K >= 1024, M a multiple of 256, N of the width,
  * where rounds of the grid times the tile's work come out below the 256 x 128 tiles', a big
  * tile counted at 0.85 of its size: e.g. every config-4 shape at M = 8192, not N = 1536 at

@@ -69,6 +69,8 @@ struct Fp8GemmArgs {
   int ldo;
   int M, N, K;
   int out_mode;          // FP8_OUT_*: how the scaled product is stored (+ bias)
+  int n_big;             // persistent 256-column tiles: whole tiles below column n_big, 192-column
+                         // tiles from there to N; N elsewhere
 };
 
 // Output forms of the scaled product v = acc * sa[m] * sw[n]:
@@ -526,10 +528,11 @@ __device__ __forceinline__ uint32_t fp8_out_bits2(float v0, float v1, half_t b0,
 template <bool OUT_BF16, int NIW, typename ReadCol>
 __device__ __forceinline__ void fp8_bigp_epilogue(const f32x4 (&acc)[NIW][8], uint16_t* ob, int ldo,
                                                   const float (&sm)[8], ReadCol read_col,
-                                                  bool has_bias) {
+                                                  bool has_bias, int ni) {
 #pragma clang fp contract(off)
 #pragma unroll
   for (int i = 0; i < NIW; ++i) {
+    if (i >= ni) continue;      // (wave-uniform) a 192-column tail tile stores 3 of 4
     f32x4 snv;
     u32x2 bw;
     read_col(i, snv, bw);       // column scales and biases of n sub-tile i
@@ -549,7 +552,7 @@ __device__ __forceinline__ void fp8_bigp_epilogue(const f32x4 (&acc)[NIW][8], ui
   }
 }
 
-template <int NI>
+template <int NI, bool TAIL = false>
 __global__ __launch_bounds__(512, 1) void fp8_gemm_bigp_kernel(Fp8GemmArgs a) {
 #pragma clang fp contract(off)
   constexpr int NS = 2;                       // stages (64 KB + 16 NI * 2 KB each)
@@ -559,6 +562,7 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_bigp_kernel(Fp8GemmArgs a) {
   constexpr int NIW = NI / 2;                 // n sub-tiles per wave (4 waves along n)
   constexpr int OPS = XLD + WLD;              // operand loads every thread issues per stage
   static_assert(NI == 6 || NI == 8, "tile widths 192 and 256");
+  static_assert(!TAIL || NI == 8, "192-column tail tiles after 256-column ones");
   __shared__ __attribute__((aligned(1024))) uint8_t xl[NS][F8B_T * F8_ROWB];
   __shared__ __attribute__((aligned(1024))) uint8_t wl[NS][BN * F8_ROWB];
   __shared__ __attribute__((aligned(16))) float scl[2][F8B_T + BN];    // [tile parity][sa | sw]
@@ -571,18 +575,30 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_bigp_kernel(Fp8GemmArgs a) {
   const int l16 = lane & 15;
   const int g4 = lane >> 4;
 
-  const int tiles_n = a.N / BN;
+  const int tiles_n = a.n_big / BN;
   const int tiles_m = a.M / F8B_T;
   const int tiles = tiles_m * tiles_n;
+  // 256-column tiles: the columns past n_big as 256 x 192 tiles after every whole tile (a
+  // grid whose whole tiles fill R rounds exactly then ends with at most one such tile per CU)
+  const int tiles_tn = TAIL ? (a.N - a.n_big) / 192 : 0;
+  const int items = tiles + tiles_m * tiles_tn;
   const int G = gridDim.x;
   const int slot = xcd_logical_block(blockIdx.x, G);
-  const int my_tiles = (tiles - slot + G - 1) / G;          // grid <= tiles: >= 1
+  const int my_tiles = (items - slot + G - 1) / G;          // grid <= items: >= 1
   const int nk = a.K / F8_BK;                               // >= NS (host check)
-  auto tile_at = [&](int r, int& m0, int& n0) {             // past the last tile: the last one
+  auto tile_at = [&](int r, int& m0, int& n0, int& tl) {    // past the last tile: the last one
+    const int it = min(r, my_tiles - 1) * G + slot;
     int tm, tn;
-    grouped_tile(min(r, my_tiles - 1) * G + slot, tiles_m, tiles_n, F8_GM, tm, tn);
+    if (!TAIL || it < tiles) {
+      grouped_tile(it, tiles_m, tiles_n, F8_GM, tm, tn);
+      n0 = tn * BN;
+      tl = 0;
+    } else {
+      grouped_tile(it - tiles, tiles_m, tiles_tn, F8_GM, tm, tn);
+      n0 = a.n_big + tn * 192;
+      tl = 1;
+    }
     m0 = tm * F8B_T;
-    n0 = tn * BN;
   };
 
   const int lrow = 8 * wave + (lane >> 3);
@@ -592,7 +608,7 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_bigp_kernel(Fp8GemmArgs a) {
   const bool has_bias = a.bias != nullptr;
   const uint32_t loff = (uint32_t)lrow * (uint32_t)a.K + (uint32_t)lchunk * 16u;
   const uint32_t rstep = 64u * (uint32_t)a.K;
-  auto issue = [&](int m0, int n0, int ks, int st) {
+  auto issue = [&](int m0, int n0, int ks, int st, int tl) {
     const uint8_t* const xs = a.xq + (int64_t)m0 * a.K;
     const uint8_t* const ws = a.wq + (int64_t)n0 * a.K;
     const uint32_t k0 = loff + (uint32_t)ks * F8_BK;
@@ -601,31 +617,34 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_bigp_kernel(Fp8GemmArgs a) {
       __builtin_amdgcn_global_load_lds((const void*)(xs + (k0 + u * rstep)),
                                        (lds_void*)((lds_u8*)&xl[st][(64 * u + 8 * wave) * F8_ROWB]), 16, 0, 0);
 #pragma unroll
-    for (int u = 0; u < WLD; ++u)
+    for (int u = 0; u < WLD; ++u) {
+      if (TAIL && tl && u >= 3) break;  // a 192-column tile's 3 row groups of w
       __builtin_amdgcn_global_load_lds((const void*)(ws + (k0 + u * rstep)),
                                        (lds_void*)((lds_u8*)&wl[st][(64 * u + 8 * wave) * F8_ROWB]), 16, 0, 0);
+    }
   };
   // the tile's 256 row scales (one per thread), BN column scales (waves < BN / 64) and BN
   // biases (wave 0, 16 bytes a lane; lanes past BN / 8 repeat the last chunk)
   // (wave-uniform bases plus 32-bit lane offsets from a lane index passed through an empty
   // asm, so that the compiler cannot hoist 64-bit lane addresses out of the loops and keep
   // them live beside the accumulators)
-  auto issue_scales = [&](int m0, int n0, int p) {
+  auto issue_scales = [&](int m0, int n0, int p, int tl) {
     uint32_t ln = (uint32_t)lane;
     asm volatile("" : "+v"(ln));
+    const int bn = TAIL && tl ? 192 : BN;   // the tile's columns
     if (wave < 4) {
       const uint8_t* const sab = (const uint8_t*)(a.sa + m0 + 64 * wave);
       __builtin_amdgcn_global_load_lds((const void*)(sab + 4u * ln),
                                        (lds_void*)((lds_u8*)&scl[p][64 * wave]), 4, 0, 0);
     }
-    if (wave < BN / 64) {
+    if (wave < bn / 64) {
       const uint8_t* const swb = (const uint8_t*)(a.sw + n0 + 64 * wave);
       __builtin_amdgcn_global_load_lds((const void*)(swb + 4u * ln),
                                        (lds_void*)((lds_u8*)&scl[p][F8B_T + 64 * wave]), 4, 0, 0);
     }
     if (wave == 0 && has_bias) {
       const uint8_t* const bb = (const uint8_t*)(a.bias + n0);
-      __builtin_amdgcn_global_load_lds((const void*)(bb + 16u * min(ln, (uint32_t)(BN / 8 - 1))),
+      __builtin_amdgcn_global_load_lds((const void*)(bb + 16u * min(ln, (uint32_t)(bn / 8 - 1))),
                                        (lds_void*)((lds_u8*)&bsl[p][0]), 16, 0, 0);
     }
   };
@@ -713,12 +732,12 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_bigp_kernel(Fp8GemmArgs a) {
         : "v"(am)
         : "memory");
   };
-  auto read_col = [&](int p, int i, f32x4& sn, u32x2& bw) {
+  auto read_col = [&](int p, int cw, int i, f32x4& sn, u32x2& bw) {
     uint32_t ln = (uint32_t)lane;             // (not hoisted: see issue_scales)
     asm volatile("" : "+v"(ln));
     const uint32_t c4 = 4u * (ln >> 4);
-    const uint32_t an = (uint32_t)(uintptr_t)(lds_f32*)&scl[p][F8B_T + 16 * NIW * wn + 16 * i + c4];
-    const uint32_t ab = (uint32_t)(uintptr_t)(lds_f16*)&bsl[p][16 * NIW * wn + 16 * i + c4];
+    const uint32_t an = (uint32_t)(uintptr_t)(lds_f32*)&scl[p][F8B_T + cw + 16 * i + c4];
+    const uint32_t ab = (uint32_t)(uintptr_t)(lds_f16*)&bsl[p][cw + 16 * i + c4];
     asm volatile("ds_read_b128 %0, %2\n\tds_read_b64 %1, %3\n\ts_waitcnt lgkmcnt(0)"
                  : "=&v"(sn), "=&v"(bw)
                  : "v"(an), "v"(ab)
@@ -728,12 +747,12 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_bigp_kernel(Fp8GemmArgs a) {
   // Steps sidx = 0, 1, ... walk the tiles' K steps back to back in slots sidx % 2; after
   // step s's operands are in registers and step s + 1 has landed everywhere (vmcnt 0 +
   // barrier: with two stages nothing younger is in flight), step s + 2 goes into slot s % 2.
-  int m0c, n0c, m0n, n0n;
-  tile_at(0, m0c, n0c);
-  tile_at(1, m0n, n0n);
-  issue_scales(m0c, n0c, 0);
-  issue(m0c, n0c, 0, 0);
-  issue(m0c, n0c, 1, 1);
+  int m0c, n0c, m0n, n0n, tlc, tln;
+  tile_at(0, m0c, n0c, tlc);
+  tile_at(1, m0n, n0n, tln);
+  issue_scales(m0c, n0c, 0, tlc);
+  issue(m0c, n0c, 0, 0, tlc);
+  issue(m0c, n0c, 1, 1, tlc);
   wait_vmcnt<OPS>();                          // the scales and stage 0 (issued first)
   barrier_only();
   int sidx = 0;
@@ -748,7 +767,10 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_bigp_kernel(Fp8GemmArgs a) {
       u32x4 wo[2 * NIW], xo[16];
       {
         uint32_t aw0, aw1, ax0, ax1;
-        addrs(st, 1, 16 * NIW * wn, aw0, aw1);
+        // a 192-column tile (tlc): the wave's 3 n sub-tiles start at 48 wn; its fourth
+        // fragment reads the slot's next 16 rows (the next wave's, or rows 192-255 that this
+        // tile leaves unloaded) into accumulators the epilogue does not store
+        addrs(st, 1, (TAIL && tlc ? 48 : 16 * NIW) * wn, aw0, aw1);
         addrs(st, 0, 128 * wm, ax0, ax1);
         if constexpr (NIW == 4) read8(aw0, aw1, wo);
         else read6(aw0, aw1, wo);
@@ -762,10 +784,10 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_bigp_kernel(Fp8GemmArgs a) {
       {
         const int iks = ks + NS;
         if (iks < nk) {
-          issue(m0c, n0c, iks, st);
+          issue(m0c, n0c, iks, st, tlc);
         } else {
-          if (iks == nk) issue_scales(m0n, n0n, (r + 1) & 1);
-          issue(m0n, n0n, iks - nk, st);
+          if (iks == nk) issue_scales(m0n, n0n, (r + 1) & 1, tln);
+          issue(m0n, n0n, iks - nk, st, tln);
         }
       }
 #pragma unroll
@@ -783,14 +805,18 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_bigp_kernel(Fp8GemmArgs a) {
       read_row_scales(r & 1, sm);
       uint32_t ln = (uint32_t)lane;           // (not hoisted: see issue_scales)
       asm volatile("" : "+v"(ln));
-      uint16_t* const ob = (uint16_t*)a.out + (int64_t)(m0c + 128 * wm) * a.ldo + n0c + 16 * NIW * wn +
+      const int cw = (TAIL && tlc ? 48 : 16 * NIW) * wn;   // the wave's first column in the tile
+      uint16_t* const ob = (uint16_t*)a.out + (int64_t)(m0c + 128 * wm) * a.ldo + n0c + cw +
                            ((ln & 15u) * (uint32_t)a.ldo + 4u * (ln >> 4));
-      if (a.out_mode) fp8_bigp_epilogue<true, NIW>(acc, ob, a.ldo, sm, [&](int i, f32x4& sn, u32x2& bw) { read_col(r & 1, i, sn, bw); }, has_bias);
-      else fp8_bigp_epilogue<false, NIW>(acc, ob, a.ldo, sm, [&](int i, f32x4& sn, u32x2& bw) { read_col(r & 1, i, sn, bw); }, has_bias);
+      auto rc = [&](int i, f32x4& sn, u32x2& bw) { read_col(r & 1, cw, i, sn, bw); };
+      const int ni = TAIL && tlc ? 3 : NIW;           // n sub-tiles stored
+      if (a.out_mode) fp8_bigp_epilogue<true, NIW>(acc, ob, a.ldo, sm, rc, has_bias, ni);
+      else fp8_bigp_epilogue<false, NIW>(acc, ob, a.ldo, sm, rc, has_bias, ni);
     }
     m0c = m0n;
     n0c = n0n;
-    tile_at(r + 2, m0n, n0n);
+    tlc = tln;
+    tile_at(r + 2, m0n, n0n, tln);
   }
   wait_vmcnt<0>();                             // drain the clamped tail loads before exit
 }
@@ -979,6 +1005,24 @@ extern "C" int omni_fp8_quant_tensor(const void* x, int ldx, void* q, float* sca
 // 156.7 / 100.3 / 121.4; M = 4096: 1536 -> 17920 172.9 / - / 146.8; 8960 -> 1536 78.8 /
 // 95.6 / 119.0 (hipBLASLt's row-wise _scaled_mm on the same shapes 245.9, 29.9, 27.0,
 // 93.3, 113.3, 60.8).  Returns the big tile's width (0: not big).
+// The persistent 256 x 256 tiles' column split: where whole tiles would leave the last round
+// partly idle, the columns past the returned one run as 256 x 192 tiles after R full rounds
+// of whole tiles, at most one per CU (config 4's gate_up at M = 8192: 2240 tiles = 8 rounds
+// and 192 more, so 2048 whole tiles over columns [0, 16384) and 256 tiles of 192 columns over
+// the last 1536: every CU runs 8.75 tiles' work where 192 of them ran 9); N where no such
+// split exists.
+static int fp8_tail_cols(int M, int N) {
+  const int64_t cus = num_cus();
+  const int64_t tm = M / F8B_T, tn = N / 256;
+  const int64_t tiles = tm * tn;
+  const int64_t R = tiles / cus;
+  if (R == 0 || tiles % cus == 0 || (R * cus) % tm) return N;
+  const int64_t nb = R * cus / tm;                    // whole column tiles
+  const int64_t rest = (int64_t)N - nb * 256;
+  if (rest % 192 || tm * (rest / 192) > cus) return N;
+  return (int)(nb * 256);
+}
+
 static int fp8_big_cols(int M, int N, int K, int out_mode = FP8_OUT_F16_VIA_BF16) {
   if (K < 1024 || (M % F8B_T) || out_mode == FP8_OUT_F16) return 0;
   const int64_t cus = num_cus();
@@ -987,10 +1031,20 @@ static int fp8_big_cols(int M, int N, int K, int out_mode = FP8_OUT_F16_VIA_BF16
   int cols = 0;
   for (int bn : {256, 192}) {
     if (N % bn) continue;
-    const double c = (double)rounds((int64_t)(M / F8B_T) * (N / bn)) * (bn / 128.0) * 0.85;
+    const int64_t t = (int64_t)(M / F8B_T) * (N / bn);
+    // with a 192-column tail (fp8_tail_cols) the last round is 0.75 of a whole one
+    const double r = bn == 256 && fp8_tail_cols(M, N) < N ? (double)(t / cus) + 0.75 : (double)rounds(t);
+    const double c = r * (bn / 128.0) * 0.85;
     if (c < best) best = c, cols = bn;
   }
   return cols;
+}
+
+// Items of the persistent big kernel (whole tiles plus the 192-column tail tiles).
+static int64_t fp8_big_items(int M, int N, int bc) {
+  if (bc != 256) return (int64_t)(M / F8B_T) * (N / bc);
+  const int nb = fp8_tail_cols(M, N);
+  return (int64_t)(M / F8B_T) * (nb / 256 + (N - nb) / 192);
 }
 
 // Which kernel omni_fp8_gemm runs for a shape: 0 one tile per workgroup, 1 the pipelined
@@ -1000,8 +1054,8 @@ extern "C" int omni_fp8_gemm_plan(int M, int N, int K, int* grid) {
   int kind, g;
   const int bc = fp8_big_cols(M, N, K);
   if (bc) {
-    const int t = (M / F8B_T) * (N / bc);
-    kind = bc == 256 ? 2 : 3, g = t < num_cus() ? t : num_cus();
+    const int64_t t = fp8_big_items(M, N, bc);
+    kind = bc == 256 ? 2 : 3, g = (int)(t < num_cus() ? t : num_cus());
   } else if (K / F8_BK >= 4) {
     const int64_t t8 = (int64_t)ceil_div(M, 256) * (N / F8_BT);
     kind = 1, g = (int)(t8 < num_cus() ? t8 : num_cus());
@@ -1040,11 +1094,15 @@ extern "C" int omni_fp8_gemm(const void* xq, const float* sa, const void* wq, co
   a.N = N;
   a.K = K;
   a.out_mode = out_mode;
+  a.n_big = N;
   const int bc = fp8_big_cols(M, N, K, out_mode);
   if (bc) {                                       // persistent 256 x bc tiles
-    const int bt = (M / F8B_T) * (N / bc);
-    const int grid = bt < num_cus() ? bt : num_cus();
-    if (bc == 256)
+    if (bc == 256) a.n_big = fp8_tail_cols(M, N);
+    const int64_t bt = fp8_big_items(M, N, bc);
+    const int grid = (int)(bt < num_cus() ? bt : num_cus());
+    if (bc == 256 && a.n_big < N)
+      hipLaunchKernelGGL((fp8_gemm_bigp_kernel<8, true>), dim3((unsigned)grid), dim3(512), 0, (hipStream_t)stream, a);
+    else if (bc == 256)
       hipLaunchKernelGGL((fp8_gemm_bigp_kernel<8>), dim3((unsigned)grid), dim3(512), 0, (hipStream_t)stream, a);
     else
       hipLaunchKernelGGL((fp8_gemm_bigp_kernel<6>), dim3((unsigned)grid), dim3(512), 0, (hipStream_t)stream, a);

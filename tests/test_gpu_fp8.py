@@ -61,6 +61,7 @@ CASES = [
     ("qkv", 8192, 1536, 2048, True),
     ("o", 8192, 1536, 1536, False),
     ("gate_up", 8192, 1536, 17920, False),
+    ("gate_up biased", 8192, 1536, 17920, True),   # 192-column tail tiles with biases
     ("down", 8192, 8960, 1536, False),
     ("256-wide", 8192, 4096, 2048, True),
     ("down half grid", 4096, 8960, 1536, False),

@@ -183,8 +183,8 @@ def pmc_probe(runner, seqs, B: int) -> None:
       3. a plain 256 MiB device copy: the byte-counter calibration;
       4. BASELINE.json configs[3]'s four FP8 linears at M = 8192 (qkv, o, gate_up, down);
       5. layer 0's four int4 linears at M = 4096 (config 5's packed prefill: each unpacks
-         its weights to fp16, then the pipelined MFMA GEMM, with a split-K finish launch
-         where the tiles alone leave CUs idle).
+         its weights to fp16, then the pipelined MFMA GEMM; the down projection as the
+         prefill runs it at 4096 rows, fp32 partial sums in the GEMM's planned K slices).
     Prints no JSON line."""
     from omniserver_amd.linear import FP8Linear
     model = runner.adapter.model
@@ -217,9 +217,14 @@ def pmc_probe(runner, seqs, B: int) -> None:
     lay = model.layers[0]
     for lin in (lay.qkv_proj, lay.o_proj, lay.gate_up_proj, lay.down_proj):
         x = torch.randn(4096, lin.K, generator=g, device=dev).half()
-        y = torch.empty(4096, lin.out_features, device=dev, dtype=torch.float16)
         torch.cuda.synchronize()
-        lin.forward_out(x, y)
+        if lin is lay.down_proj and model.prefill_down_partials_ok(4096):
+            part = torch.empty(lin.partial_plan(4096) * 4096 * lin.N, device=dev,
+                               dtype=torch.float32)
+            lin.forward_partial_planned(x, part)
+        else:
+            y = torch.empty(4096, lin.out_features, device=dev, dtype=torch.float16)
+            lin.forward_out(x, y)
         torch.cuda.synchronize()
     log(f"pmc probe: eager decode steps at B={B} and 1 (ctx {int(runner.pool.lengths[0])}), "
         f"one 256 MiB copy, 4 FP8 linears at M=8192, 4 int4 linears at M=4096")

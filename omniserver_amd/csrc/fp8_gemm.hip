@@ -525,6 +525,10 @@ __device__ __forceinline__ uint32_t fp8_out_bits2(float v0, float v1, half_t b0,
 // tile's row / column scales and biases ride with its first stage into an LDS slot of their
 // own (two, by tile parity), which the epilogue reads with its own lgkmcnt wait: an epilogue
 // that read them from global memory would wait (vmcnt) for the next tile's stages in flight.
+// TAIL (256 columns): the columns past a.n_big run as 256 x 192 tiles after every whole tile
+// (fp8_tail_cols); such a tile loads 3 of the 4 row groups of w, reads its wave's 3 n
+// sub-tiles from 48 wn plus a fourth fragment from the slot's next 16 rows (unused), and
+// stores 3 of its 4 n sub-tiles, so both kinds share the loop's code and registers.
 template <bool OUT_BF16, int NIW, typename ReadCol>
 __device__ __forceinline__ void fp8_bigp_epilogue(const f32x4 (&acc)[NIW][8], uint16_t* ob, int ldo,
                                                   const float (&sm)[8], ReadCol read_col,

@@ -540,9 +540,12 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm_pipe_kernel(GemmPipeArgs a) 
 // workgroup per CU walks its items (tile x K slice, slice-major, tiles in the XCD-grouped
 // order) with the K loop running across item boundaries (the next item's first two stages
 // load during the current one's last two steps).  Per 64-k step a wave issues 16 + 2 NIW
-// operand reads and 16 NIW MFMAs.  PARTIAL writes each K slice's fp32 sums to
-// part[slice][M][N] for the consumer to add in slice order (config 5's N = 1536 projections
-// at M = 4096: 128 tiles of 256 x 192 in two slices fill the 256 CUs once).  (Biased
+// operand reads and 16 NIW MFMAs.  At 256 columns the columns past a.n_big run as 256 x 128
+// half tiles after every whole tile (gp_big_tail_cols: the last round of whole tiles would
+// leave CUs idle), read and stored by the same code for NIW / 2 column tiles per wave.
+// PARTIAL writes each K slice's fp32 sums to part[slice][M][N] for the consumer to add in
+// slice order (config 5's down projection at M = 4096: 128 tiles of 256 x 192 in two
+// slices fill the 256 CUs once).  (Biased
 // linears, e.g. qkv, stay on the kernel above: with the bias staging beside the
 // accumulators a four-wave form of this kernel spilled.)  Same k order per output as the
 // kernel above within a slice: one-slice results equal its bit for bit.  MI355X, us

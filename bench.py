@@ -360,28 +360,38 @@ def _decode_line(quant, per_ms, replay_ms, ctx0, steps):
             "frac": round(nbytes / (per_ms / 1e3) / PEAK_HBM, 4)}
 
 
-def _prefill_ms(r, make_seqs, reps: int):
+def _prefill_ms(r, make_seqs, reps: int, idle_s: float = 0.0):
     """Median wall time (ms) of ``reps`` prefills of make_seqs() on runner r, each into a
-    freshly freed pool after one warm-up prefill (first use of the prefill kernels);
-    returns (median ms, the last prefill's sequences).  The wall time includes the
-    prefill's host-side input preparation, so the timing starts once the host's thread
-    pools, still spinning after the set-up's CPU work (synthetic weights, packing), have
-    gone idle: without the pause the same prefills measured 3.16 / 16.75 ms (configs 1 / 5)
-    right after a runner's set-up against 2.91 / 15.95 ms later in the same process."""
+    freshly freed pool; returns (median ms, the last prefill's sequences).  The wall time
+    includes the prefill's host-side input preparation (tokens, image rows, M-RoPE positions,
+    the upload).  The requests themselves are made before the timed loop, as a serving
+    engine's queue holds them: their synthetic vision rows are host-side random draws that
+    would otherwise leave the GPU idle for tens of ms before every timed prefill, and MI355X
+    lowers its clocks within a few ms of idle (configs[4]'s graph replay after 0.5 / 1 / 5 /
+    20 ms of host idle: 12.4 / 12.45 / 13.5 / 14.1 ms).  Consecutive prefills are then
+    separated by the pool's frees alone, as in serving, where prefills run between decode
+    steps; ``idle_s`` > 0 instead times each prefill after that long idle (reported beside).
+    The loop starts once the host's thread pools, still spinning after the set-up's CPU work
+    (synthetic weights, packing), have gone idle, behind one untimed prefill (the first use of
+    the prefill kernels, or a layout's graph capture)."""
     seqs = make_seqs()
     r.prefill(seqs)
     torch.cuda.synchronize()
+    batches = [make_seqs() for _ in range(reps + 1)]
     time.sleep(0.5)
     ts = []
-    for _ in range(reps):
+    for i, nxt in enumerate(batches):
         for s_ in seqs:
             r.free(s_)
-        seqs = make_seqs()
+        seqs = nxt
         torch.cuda.synchronize()
+        if idle_s:
+            time.sleep(idle_s)
         t1 = time.perf_counter()
         r.prefill(seqs)
         torch.cuda.synchronize()
-        ts.append((time.perf_counter() - t1) * 1e3)
+        if i:
+            ts.append((time.perf_counter() - t1) * 1e3)
     return sorted(ts)[len(ts) // 2], seqs
 
 
@@ -539,6 +549,9 @@ def baseline_configs(device, w_int4) -> dict:
     B = 8
     r, mk5 = _config5_runner(device, w_int4, B)
     eager5 = _prefill_eager_ms(r, mk5, 3)
+    idle5, seqs = _prefill_ms(r, mk5, 3, idle_s=0.02)
+    for s_ in seqs:
+        r.free(s_)
     pre_ms5, seqs = _prefill_ms(r, mk5, 3)
     pre = pre_ms5 * 1e-3
     T = 512 * B
@@ -547,6 +560,7 @@ def baseline_configs(device, w_int4) -> dict:
     out["config5"] = {"workload": "int4 decoder, 8 x 512-token image+text prompts: packed prefill "
                                   "(T = 4096), then 128 greedy steps at B = 8",
                       "prefill_ms": round(pre * 1e3, 3), "prefill_eager_ms": round(eager5, 3),
+                      "prefill_after_idle_ms": round(idle5, 3),
                       "prefill_tok_per_s": round(T / pre, 1),
                       "prefill_tflops": round(fl / pre / 1e12, 1),
                       "prefill_frac_fp16_peak": round(fl / pre / PEAK_FP16, 4),
@@ -555,7 +569,9 @@ def baseline_configs(device, w_int4) -> dict:
                                       "expansion of their weights, made at the first prefill of "
                                       ">= 256 rows (prefill_f16_unpack_ms, outside the timed "
                                       "prefills) and kept (prefill_f16_resident_bytes beside "
-                                      "int4_weight_bytes); decode streams the int4 words",
+                                      "int4_weight_bytes); decode streams the int4 words; "
+                                      "prefill_after_idle_ms: each prefill after 20 ms of GPU "
+                                      "idle (the clocks drop within a few ms of idle)",
                       **_f16_expansion(r),
                       "prefill_gemm_mfma_busy_pct_counters": mfma_from_profiles("int4 prefill M=4096"),
                       **_decode_line("gptq", per, rep, ctx0, 128)}

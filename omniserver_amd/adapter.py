@@ -99,8 +99,8 @@ class Qwen2VLAdapter:
         """Token ids of a prompt: a list of ids is taken as is; a string must be
         whitespace-separated integer ids (there is no tokenizer offline)."""
         if isinstance(prompt, str):
-            return [int(t) for t in prompt.split()]
-        return [int(t) for t in prompt]
+            return list(map(int, prompt.split()))
+        return list(map(int, prompt))
 
     def embed_tokens(self, input_ids: torch.Tensor) -> torch.Tensor:
         return self._llm.embed_tokens(input_ids)

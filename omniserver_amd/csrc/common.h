@@ -121,9 +121,14 @@ __device__ __forceinline__ uint32_t and_or_b32(uint32_t x, uint32_t mask, uint32
 // The empty asm makes the product opaque: without it the backend may fold the last multiply
 // and the caller's fp16 rounding into one mixed-precision fma (one rounding instead of the
 // fp32 product's two), which changes near-tie results from kernel to kernel.
+// The sigmoid's reciprocal is the hardware v_rcp_f32 (1 ulp): the correctly rounded division
+// is 11 instructions of the 20 per output, and the GEMMs' SiLU epilogues are VALU-bound with
+// the matrix cores idle; 1 ulp of fp32 moves the fp16 output only at near ties.  Every SiLU
+// kernel (decode GEMVs, prefill GEMMs, the standalone SiLU-mul) uses this one helper, so
+// their outputs agree bit for bit.
 __device__ __forceinline__ float silu_mul_f32(float g, float u) {
 #pragma clang fp contract(off)
-  float p = g * (1.0f / (1.0f + __expf(-g))) * u;
+  float p = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
   asm("" : "+v"(p));
   return p;
 }

@@ -152,6 +152,109 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(
   }
 }
 
+// Many-row add+RMSNorm with every load of a row issued before any arithmetic: H = 512 * NC,
+// so each lane owns exactly NC 8-element chunks (no lane divergence, nothing for the compiler
+// to keep behind a branch), x fp16 (NP = 0) or NP fp32 split-K partial slices summed in slice
+// order.  rmsnorm_kernel's operations in its order (the same per-lane chunk sequence, the
+// same wave reduction), so the outputs are bit-identical to it; the residual, the inputs and
+// the gains are all in flight together where rmsnorm_kernel waits chunk by chunk and fetches
+// the gains after its reduction.  res_out may alias residual (each lane reads its chunks
+// before it writes them).
+template <int NC, int NP>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) void addnorm_rows_kernel(const half_t* x,
+                                                           const float* __restrict__ parts,
+                                                           const half_t* residual,
+                                                           const half_t* __restrict__ w, half_t* y,
+                                                           half_t* res_out, int rows, float eps) {
+#pragma clang fp contract(off)
+  asm volatile("" ::"s"(x), "s"(parts), "s"(residual), "s"(w), "s"(y), "s"(res_out), "s"(rows),
+               "s"(eps));
+  constexpr int H = NC * 512;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const size_t base = (size_t)row * H + lane * 8;
+  half8_t rv[NC], xv[NP == 0 ? NC : 1], wv[NC];
+  float4 pv[NP > 0 ? NP : 1][NC][2];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    if (NP == 0) {
+      xv[i] = *(const half8_t*)(x + base + 512 * i);
+    } else {
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        const float4* pp = (const float4*)(parts + (size_t)p * rows * H + base + 512 * i);
+        pv[p][i][0] = pp[0];
+        pv[p][i][1] = pp[1];
+      }
+    }
+    rv[i] = *(const half8_t*)(residual + base + 512 * i);
+  }
+#pragma unroll
+  for (int i = 0; i < NC; ++i) wv[i] = *(const half8_t*)(w + lane * 8 + 512 * i);
+
+  half8_t r[NC];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    half8_t v;
+    if (NP == 0) {
+      v = xv[i];
+    } else {
+      float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        sum[0] += pv[p][i][0].x; sum[1] += pv[p][i][0].y;
+        sum[2] += pv[p][i][0].z; sum[3] += pv[p][i][0].w;
+        sum[4] += pv[p][i][1].x; sum[5] += pv[p][i][1].y;
+        sum[6] += pv[p][i][1].z; sum[7] += pv[p][i][1].w;
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (half_t)sum[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (half_t)((float)v[e] + (float)rv[i][e]);
+    r[i] = v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float f = (float)v[e];
+      ss += f * f;
+    }
+  }
+  ss = wave_sum(ss);
+  const float rstd = 1.0f / sqrtf(ss / (float)H + eps);
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    *(half8_t*)(res_out + base + 512 * i) = r[i];
+    half8_t o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = (half_t)(((float)r[i][e] * rstd) * (float)wv[i][e]);
+    *(half8_t*)(y + base + 512 * i) = o;
+  }
+}
+
+// The addnorm_rows_kernel instance for (hidden, nparts), or nullptr (rmsnorm_kernel then).
+typedef void (*addnorm_rows_fn)(const half_t*, const float*, const half_t*, const half_t*,
+                                half_t*, half_t*, int, float);
+static addnorm_rows_fn addnorm_rows_for(int hidden, int nparts) {
+  if (hidden == 1536) {
+    switch (nparts) {
+      case 0: return addnorm_rows_kernel<3, 0>;
+      case 1: return addnorm_rows_kernel<3, 1>;
+      case 2: return addnorm_rows_kernel<3, 2>;
+      case 3: return addnorm_rows_kernel<3, 3>;
+      case 4: return addnorm_rows_kernel<3, 4>;
+    }
+  } else if (hidden == 3584) {
+    switch (nparts) {
+      case 0: return addnorm_rows_kernel<7, 0>;
+      case 1: return addnorm_rows_kernel<7, 1>;
+      case 2: return addnorm_rows_kernel<7, 2>;
+    }
+  }
+  return nullptr;
+}
+
 // Decode-size add+RMSNorm: one workgroup per row, one 8-element chunk per thread
 // (H/8 threads, rounded up to whole waves), so every load of the row - including all
 // split-K partials - is in flight at once.  x is fp16, or (PARTS) the fp32 partial sums
@@ -242,6 +345,10 @@ extern "C" int omni_add_rmsnorm(const void* x, const void* residual, const void*
     hipLaunchKernelGGL(kern, dim3(rows), dim3(threads), 0, (hipStream_t)stream,
                        (const half_t*)x, nullptr, 0, (const half_t*)residual,
                        (const half_t*)weight, (half_t*)y, (half_t*)residual_out, rows, hidden, eps);
+  } else if (addnorm_rows_fn kern = addnorm_rows_for(hidden, 0)) {
+    hipLaunchKernelGGL(kern, dim3(ceil_div(rows, 4)), dim3(256), 0, (hipStream_t)stream,
+                       (const half_t*)x, nullptr, (const half_t*)residual, (const half_t*)weight,
+                       (half_t*)y, (half_t*)residual_out, rows, eps);
   } else {
     hipLaunchKernelGGL((rmsnorm_kernel<true, false, false>), dim3(ceil_div(rows, 4)), dim3(256), 0,
                        (hipStream_t)stream, (const half_t*)x, (const half_t*)residual, nullptr,
@@ -265,6 +372,10 @@ extern "C" int omni_add_rmsnorm_partials(const float* partials, int nparts, cons
     hipLaunchKernelGGL(kern, dim3(rows), dim3(threads), 0, (hipStream_t)stream,
                        nullptr, partials, nparts, (const half_t*)residual, (const half_t*)weight,
                        (half_t*)y, (half_t*)residual_out, rows, hidden, eps);
+  } else if (addnorm_rows_fn kern = addnorm_rows_for(hidden, nparts)) {
+    hipLaunchKernelGGL(kern, dim3(ceil_div(rows, 4)), dim3(256), 0, (hipStream_t)stream,
+                       nullptr, partials, (const half_t*)residual, (const half_t*)weight,
+                       (half_t*)y, (half_t*)residual_out, rows, eps);
   } else {
     hipLaunchKernelGGL((rmsnorm_kernel<true, false, false, true>), dim3(ceil_div(rows, 4)), dim3(256), 0,
                        (hipStream_t)stream, nullptr, (const half_t*)residual, nullptr, nullptr, 0, 0,

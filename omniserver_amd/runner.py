@@ -33,6 +33,7 @@ from __future__ import annotations
 import abc
 from typing import Dict, List
 
+import numpy as np
 import torch
 
 from .hostio import to_device
@@ -171,15 +172,17 @@ class MultimodalRunner(ModelRunner):
             raise RuntimeError(f"KV pool full: {base} running + {len(seqs)} new > "
                                f"{self.max_running}")
         dev = self.device
-        # the packed prompt's host-side inputs are gathered first and uploaded once each
-        # (ids, image row indices, positions): per-sequence uploads and launches would hold
-        # the GPU idle while the host issues them
-        all_ids, positions, seg_lens, deltas, img_rows, vis = [], [], [], [], [], []
+        # The packed prompt's host-side inputs are gathered as numpy arrays and uploaded in
+        # one pinned copy (ids, image row indices, positions, rope deltas): the GPU is idle
+        # until the host has issued them, so per-token Python work and per-input uploads
+        # would add to every prefill's latency.
+        ids_l, pos_l, seg_lens, deltas, img_rows, vis = [], [], [], [], [], []
+        T = 0
         for seq in seqs:
             if not seq.prompt_token_ids:
                 self.tokenize(seq)
-            ids = seq.prompt_token_ids
-            L = len(ids)
+            ids = np.asarray(seq.prompt_token_ids, dtype=np.int64)
+            L = int(ids.shape[0])
             if L == 0 or L >= self._pool.max_len:
                 raise ValueError(f"prompt length {L} outside [1, max_len={self._pool.max_len})")
             images = seq.request.images
@@ -187,31 +190,35 @@ class MultimodalRunner(ModelRunner):
             if images:
                 # the image rows located on the host: a mask on the device would make the
                 # host wait for the queue (its count, its nonzero rows)
-                off = len(all_ids)
-                rows = [off + i for i, t in enumerate(ids) if t == self.image_token_id]
+                rows = np.flatnonzero(ids == self.image_token_id)
                 v = self.adapter.vision_embed(images)
-                if len(rows) != v.shape[0]:
+                if rows.shape[0] != v.shape[0]:
                     raise ValueError("image token count does not match the vision rows")
-                img_rows += rows
+                img_rows.append(rows + T)
                 vis.append(v)
             pos, delta = self.adapter.prefill_positions(ids, grids)
-            all_ids += ids
-            positions.append(pos)
+            ids_l.append(ids)
+            pos_l.append(pos.numpy() if isinstance(pos, torch.Tensor) else np.asarray(pos))
             seg_lens.append(L)
-            deltas.append(delta)
+            deltas.append(int(delta))
+            T += L
         slots = [base + i for i in range(len(seqs))]
-        emb = self.adapter.embed_tokens(to_device(all_ids, torch.int64, dev))
+        nr = sum(int(r.shape[0]) for r in img_rows)
+        host = np.concatenate(ids_l + img_rows + [np.concatenate(pos_l, axis=1).reshape(-1),
+                                                  np.asarray(deltas, dtype=np.int64)])
+        up = to_device(torch.from_numpy(host), torch.int64, dev)
+        emb = self.adapter.embed_tokens(up[:T])
         if img_rows:
-            emb.index_copy_(0, to_device(img_rows, torch.int64, dev), torch.cat(vis, 0).to(emb.dtype))
+            emb.index_copy_(0, up[T:T + nr], torch.cat(vis, 0).to(emb.dtype))
         packed = emb.unsqueeze(0)
-        pos = to_device(torch.cat(positions, dim=1), torch.int64, dev).unsqueeze(1)   # [3, 1, T]
+        pos = up[T + nr:T + nr + 3 * T].view(3, 1, T)                           # [3, 1, T]
         if self._use_graph and self.prefill_graph_layouts > 0:
             logits = self._prefill_graphed(packed, pos, slots, seg_lens)
         else:
             last = torch.tensor(seg_lens).cumsum(0) - 1
             cache = self._pool.packed_prefill_cache(slots, seg_lens)
             logits = self.adapter.llm(packed, pos, None, cache, logits_indices=last.tolist())[0]
-        self._rope_delta[base:base + len(seqs)].copy_(to_device(deltas, torch.int64, dev))
+        self._rope_delta[base:base + len(seqs)].copy_(up[T + nr + 3 * T:])
         toks = self._sample_rows(logits, seqs)
         for i, seq in enumerate(seqs):
             slot = slots[i]

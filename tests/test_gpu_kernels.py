@@ -766,6 +766,38 @@ def test_add_rmsnorm_partials(gpu, S, M, H):
         assert torch.equal(y.cpu(), y2.cpu()) and torch.equal(nr.cpu(), r2.cpu())
 
 
+@pytest.mark.parametrize("H,M", [(1536, 1001), (3584, 300)])
+def test_addnorm_rows_equals_generic(gpu, H, M):
+    """Past 256 rows at H = 1536 / 3584 the add+RMSNorm runs the load-batched many-row kernel
+    (x fp16, or 1-4 / 1-2 partial slices); any other slice count runs the generic many-row
+    kernel.  Padding the slices with zero slices up to 5 (x + 0 = x in fp32) sends the same
+    sums through the generic kernel: outputs and residuals equal bit for bit, with the
+    residual updated in place as the prefill does; a ragged last workgroup (M % 4 != 0)."""
+    from omniserver_amd import fused_ops as F
+    g = torch.Generator().manual_seed(111 + H)
+    gain = (1.0 + 0.1 * f16((H,), 112)).to(gpu)
+    res = f16((M, H), 113).to(gpu)
+    x = f16((M, H), 114).to(gpu)
+    nps = (0, 1, 2, 3, 4) if H == 1536 else (0, 1, 2)
+    for S in nps:
+        say(f"addnorm rows H={H} M={M} slices={S}")
+        if S == 0:
+            sl = [x.float()]
+        else:
+            sl = [(torch.randn(M, H, generator=g) * 0.3).to(gpu) for _ in range(S)]
+        y = torch.empty(M, H, device=gpu, dtype=torch.float16)
+        r_new = res.clone()
+        if S == 0:
+            F.add_rms_norm_out(x, r_new, gain, 1e-6, y, r_new)
+        else:
+            F.add_rms_norm_partials_out(torch.stack(sl), S, r_new, gain, 1e-6, y, r_new)
+        pad = torch.stack(sl + [torch.zeros(M, H, device=gpu)] * (5 - len(sl)))
+        y5, r5 = torch.empty_like(y), torch.empty_like(y)
+        F.add_rms_norm_partials_out(pad, 5, res, gain, 1e-6, y5, r5)
+        torch.cuda.synchronize()
+        assert torch.equal(r_new.cpu(), r5.cpu()) and torch.equal(y.cpu(), y5.cpu())
+
+
 @pytest.mark.parametrize("fmt", ["int4", "fp16"])
 @pytest.mark.parametrize("M", [1, 2])
 def test_gemm_addnorm(gpu, fmt, M):

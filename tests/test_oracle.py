@@ -152,6 +152,32 @@ def test_mrope_positions_two_images_and_product_agree():
     assert torch.equal(pos, p2) and d == d2
 
 
+def test_mrope_positions_random_layouts_agree():
+    """The product's positions (cached per-grid offsets, running maximum) equal the oracle's
+    on random layouts: 0-3 images of t = 1-2 frames and even h, w, text of any length
+    before, between and after (none too), a stray image token without a vision-start, and
+    prompts given as lists or int64 arrays."""
+    from omniserver_amd.positions import mrope_positions
+    S, I = 151652, 151655
+    g = np.random.default_rng(7)
+    for case in range(60):
+        ids, grids = [], []
+        for _ in range(int(g.integers(0, 4))):
+            ids += [int(x) for x in g.integers(0, 1000, int(g.integers(0, 6)))]
+            t, h, w = int(g.integers(1, 3)), 2 * int(g.integers(1, 5)), 2 * int(g.integers(1, 5))
+            ids += [S] + [I] * (t * (h // 2) * (w // 2))
+            grids.append((t, h, w))
+        ids += [int(x) for x in g.integers(0, 1000, int(g.integers(0, 6)))]
+        if case % 7 == 3:
+            ids += [I]                                   # no vision-start before it: text
+        if not ids:
+            ids = [1]
+        pos, d = ref.mrope_position_ids(ids, grids)
+        for arg in (ids, np.asarray(ids, dtype=np.int64)):
+            p2, d2 = mrope_positions(arg, grids)
+            assert torch.equal(pos, p2) and d == d2, case
+
+
 def test_mrope_positions_image_without_vision_start_is_text():
     """positions.py:27-30 counts images by vision-start tokens followed by an image token:
     a prompt whose image run has none gets 1-D text positions."""

@@ -336,8 +336,10 @@ int omni_f16_gemm_pipe_splits(int M, int N, int K, int tile_rows);
  * that sums them in order (omni_add_rmsnorm_partials, omni_mrope_kv_write_partials).
  * With tile_rows and ksplit both 0 and fp16 weights, shapes whose 128 x 192 tiles (STORE /
  * PARTIAL, N % 192 == 0) or persistent 256 x 256 tiles (STORE without a bias / SILU, M and
- * N % 256 == 0) take fewer grid rounds x tile work run those (omni_packed_gemm_pipe_plan;
- * same k order per output: results equal the 128 x 128 tiles' bit for bit). */
+ * N % 256 == 0) take fewer grid rounds x tile work run those, and the SILU epilogue at
+ * 129-256 rows runs 128 x 160 tiles (five gate|up pairs) where they fill the CUs in one
+ * round (omni_packed_gemm_pipe_plan; same k order per output: results equal the 128 x 128
+ * tiles' bit for bit). */
 int omni_packed_gemm_pipe(const void* x, int ldx, const void* w_packed, const void* scales_packed,
                           int fmt, const void* bias, int bias_after_round, void* out, int ldo,
                           int M, int N, int K, int epilogue, int tile_rows, int ksplit,
@@ -345,7 +347,7 @@ int omni_packed_gemm_pipe(const void* x, int ldx, const void* w_packed, const vo
 
 /* The tiling omni_packed_gemm_pipe runs for a shape (no reference counterpart: it tells a
  * caller or a test which form covers the shape): *rows x *cols tiles (128 / 256 x 128,
- * 128 x 192, or the persistent 256 x 256) and *ks K slices for the given epilogue, bias
+ * 128 x 192, 128 x 160, or the persistent 256 x 256) and *ks K slices for the given epilogue, bias
  * (has_bias != 0) and tile_rows / ksplit (0: chosen); any output may be NULL.  -1 for a
  * shape it rejects. */
 int omni_packed_gemm_pipe_plan(int M, int N, int K, int fmt, int epilogue, int has_bias,

@@ -816,6 +816,157 @@ __global__ __launch_bounds__(512, 1) void gemm_bigp_f16_kernel(GemmPipeArgs a) {
   gp_wait_vmcnt<0>();                   // drain the clamped tail loads before exit
 }
 
+// 128 x 160 tiles (five gate|up column pairs) for the SiLU-fused gate_up projection on the
+// packed fp16 weights at 129-256 rows, one tile per workgroup: config 1's 256-token prompt
+// (N = 17920) has 224 of them, one round on 256 CUs, where 256 x 128 tiles fill 140 CUs and
+// 128 x 128 tiles take two rounds.  A step stages 16 KB of x and 20 KB of w (36 KB per CU
+// against 48 KB for a 256 x 128 tile; at these sizes a step's time follows the bytes it
+// stages).  8 waves, two per SIMD: 4 along m (32 rows each) x 2 along n, the first n group
+// holding pairs 0-2 (column tiles 0-5) and the second pairs 3-4 (column tiles 6-9), so that
+// every SIMD holds one wave of each.  Per 64-k step a wave reads 4 x fragments and 12 or 8 w
+// fragments and issues 24 or 16 MFMAs; the K order of every output is the 256 x 128 tiles'
+// (steps ascending, each step's two 32-k halves in order), so the outputs equal theirs bit
+// for bit.  w blocks: 20 per step, three loads each for waves 0-3 and two for waves 4-7.
+template <int NS>
+__global__ __launch_bounds__(512, 1) void gemm_silu160_kernel(GemmPipeArgs a) {
+#pragma clang fp contract(off)
+  constexpr int BM = 128, BN = 160;
+  constexpr int NCT = BN / 16;          // column tiles (gate and up of 5 pairs)
+  constexpr int XLD = 2;                // x loads per wave and step (128 rows / 8 / 8)
+  __shared__ __attribute__((aligned(1024))) uint8_t xl[NS][BM * GP_ROWB];
+  __shared__ __attribute__((aligned(1024))) uint8_t wl[NS][2 * NCT * 1024];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 3;
+  const int wn = wave >> 2;             // 0: pairs 0-2, 1: pairs 3-4
+  const int l16 = lane & 15;
+  const int g4 = lane >> 4;
+  const int tiles_m = (a.M + BM - 1) / BM;
+  // tiles sharing a column range (the same weights) sit on the same XCD
+  const int t = xcd_logical_block(blockIdx.x, gridDim.x);
+  const int m0 = (t % tiles_m) * BM;
+  const int n0 = (t / tiles_m) * BN;
+  const int nk = a.K / GP_BKH;          // >= NS (host check)
+
+  typedef __attribute__((address_space(3))) void lds_void;
+  typedef __attribute__((address_space(3))) uint8_t lds_u8;
+  const int lrow = 8 * wave + (lane >> 3);
+  const int lchunk = (lane & 7) ^ (lrow & 7);
+  const half_t* xs[XLD];
+#pragma unroll
+  for (int u = 0; u < XLD; ++u)
+    xs[u] = a.x + (int64_t)min(m0 + 64 * u + lrow, a.M - 1) * a.ldx + lchunk * 8;
+  // w block b = 8 u + wave (u < 3 for waves 0-3, u < 2 for 4-7): column tile b / 2, 32-k half b % 2
+  const half_t* ws[3];
+#pragma unroll
+  for (int u = 0; u < 3; ++u) {
+    const int b = min(8 * u + wave, 2 * NCT - 1);
+    ws[u] = a.w + (((int64_t)(n0 / 16 + b / 2) * (a.K / 32) + (b & 1)) * 64 + lane) * 8;
+  }
+  auto issue = [&](int ks, int st) {
+#pragma unroll
+    for (int u = 0; u < XLD; ++u)
+      __builtin_amdgcn_global_load_lds((const void*)(xs[u] + ks * GP_BKH),
+                                       (lds_void*)((lds_u8*)&xl[st][(64 * u + 8 * wave) * GP_ROWB]), 16, 0, 0);
+#pragma unroll
+    for (int u = 0; u < 3; ++u) {
+      if (u == 2 && wave >= 4) break;
+      __builtin_amdgcn_global_load_lds((const void*)(ws[u] + ks * 1024),
+                                       (lds_void*)((lds_u8*)&wl[st][(8 * u + wave) * 1024]), 16, 0, 0);
+    }
+  };
+  // operands: w fragments (column tile c of the wave, half t) in v[2 c + t], x (row
+  // sub-tile j, half t) in v[12 + 2 j + t]
+  auto read_ops = [&](int st, u32x4 (&v)[16]) {
+    const int r = 32 * wm + l16;
+    const uint32_t row = (uint32_t)(uintptr_t)(lds_u8*)&xl[st][r * GP_ROWB];
+    const uint32_t bx0 = row + ((g4 ^ (l16 & 7)) << 4);
+    const uint32_t bx1 = row + (((4 + g4) ^ (l16 & 7)) << 4);
+    const uint32_t bw = (uint32_t)(uintptr_t)(lds_u8*)&wl[st][wn ? 12 * 1024 : 0] + (uint32_t)lane * 16u;
+    if (wn == 0)
+      asm volatile(
+          "ds_read_b128 %0, %16\n\tds_read_b128 %1, %16 offset:1024\n\t"
+          "ds_read_b128 %2, %16 offset:2048\n\tds_read_b128 %3, %16 offset:3072\n\t"
+          "ds_read_b128 %4, %16 offset:4096\n\tds_read_b128 %5, %16 offset:5120\n\t"
+          "ds_read_b128 %6, %16 offset:6144\n\tds_read_b128 %7, %16 offset:7168\n\t"
+          "ds_read_b128 %8, %16 offset:8192\n\tds_read_b128 %9, %16 offset:9216\n\t"
+          "ds_read_b128 %10, %16 offset:10240\n\tds_read_b128 %11, %16 offset:11264\n\t"
+          "ds_read_b128 %12, %17\n\tds_read_b128 %13, %18\n\t"
+          "ds_read_b128 %14, %17 offset:2048\n\tds_read_b128 %15, %18 offset:2048\n\t"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
+            "=&v"(v[6]), "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11]),
+            "=&v"(v[12]), "=&v"(v[13]), "=&v"(v[14]), "=&v"(v[15])
+          : "v"(bw), "v"(bx0), "v"(bx1)
+          : "memory");
+    else
+      asm volatile(
+          "ds_read_b128 %0, %12\n\tds_read_b128 %1, %12 offset:1024\n\t"
+          "ds_read_b128 %2, %12 offset:2048\n\tds_read_b128 %3, %12 offset:3072\n\t"
+          "ds_read_b128 %4, %12 offset:4096\n\tds_read_b128 %5, %12 offset:5120\n\t"
+          "ds_read_b128 %6, %12 offset:6144\n\tds_read_b128 %7, %12 offset:7168\n\t"
+          "ds_read_b128 %8, %13\n\tds_read_b128 %9, %14\n\t"
+          "ds_read_b128 %10, %13 offset:2048\n\tds_read_b128 %11, %14 offset:2048\n\t"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
+            "=&v"(v[6]), "=&v"(v[7]), "=&v"(v[12]), "=&v"(v[13]), "=&v"(v[14]), "=&v"(v[15])
+          : "v"(bw), "v"(bx0), "v"(bx1)
+          : "memory");
+  };
+  const int ncw = wn ? 4 : 6;           // the wave's column tiles
+  f32x4 acc[6][2];
+#pragma unroll
+  for (int c = 0; c < 6; ++c)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[c][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < NS; ++s) issue(s, s);
+  // a thread's loads per stage: 5 for waves 0-3, 4 for waves 4-7; stage 0 landed
+  if (wave < 4) gp_wait_vmcnt<5 * (NS - 1)>();
+  else gp_wait_vmcnt<4 * (NS - 1)>();
+  gp_barrier();
+  for (int ks = 0; ks < nk; ++ks) {
+    const int st = ks % NS;
+    u32x4 v[16];
+    read_ops(st, v);
+    // step ks + 1 has landed for this thread, then for everyone; every wave has read this
+    // slot, refilled with step ks + NS (past the end: the last step again, never read)
+    if (wave < 4) gp_wait_vmcnt<5 * (NS - 2)>();
+    else gp_wait_vmcnt<4 * (NS - 2)>();
+    gp_barrier();
+    issue(min(ks + NS, nk - 1), st);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int c = 0; c < 6; ++c) {
+        if (c >= ncw) break;
+        const half8_t wf = __builtin_bit_cast(half8_t, v[2 * c + h]);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[c][j] = mfma16x16x32(wf, __builtin_bit_cast(half8_t, v[12 + 2 * j + h]), acc[c][j]);
+      }
+  }
+  gp_wait_vmcnt<0>();                   // drain the clamped tail loads
+  // lane holds columns 16 c + 4 g4 + q of the wave's tiles, rows m0 + 32 wm + 16 j + l16;
+  // pair p of the wave (column tiles 2 p, 2 p + 1) is intermediate pair n0 / 32 + 3 wn + p
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int m = m0 + 32 * wm + 16 * j + l16;
+    if (m >= a.M) continue;
+    half_t* const ob = a.out + (int64_t)m * a.ldo + n0 / 2 + 48 * wn + 4 * g4;
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+      if (2 * p >= ncw) break;
+      half4_t o;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        o[q] = (half_t)silu_mul_f32((float)(half_t)acc[2 * p][j][q], (float)(half_t)acc[2 * p + 1][j][q]);
+      *(half4_t*)(ob + 16 * p) = o;
+    }
+  }
+}
+
 static int gp_num_cus() {
   static int n = 0;
   if (n <= 0) {
@@ -1044,6 +1195,14 @@ static void gp_packed_plan(int M, int N, int K, int fmt, int epilogue, bool has_
   cols = GP_BN;
   const bool free_split = ksplit == 0;
   if (fmt != 1 || tile_rows != 0 || ks != 1) return;
+  if (epilogue == GP_SILU && M > 128 && M <= 256 && N % 160 == 0 &&
+      2 * (int64_t)(N / 160) <= gp_num_cus()) {
+    // gemm_silu160_kernel: one round of 128 x 160 tiles where the 256 x 128 tiles (also one
+    // round) stage a third more bytes per step per CU
+    rows = 128;
+    cols = 160;
+    return;
+  }
   if ((epilogue == GP_STORE || epilogue == GP_PARTIAL) && gp_wide_tiles(M, N, rows)) {
     rows = 128;
     cols = 192;
@@ -1180,6 +1339,13 @@ extern "C" int omni_packed_gemm_pipe(const void* x, int ldx, const void* w_packe
       hipLaunchKernelGGL((gemm_bigp_f16_kernel<GP_STORE, 4>), dim3(grid), blk, 0, st, a);
     else
       hipLaunchKernelGGL((gemm_bigp_f16_kernel<GP_STORE, 3>), dim3(grid), blk, 0, st, a);
+    OMNI_CHECK_LAUNCH();
+    return OMNI_OK;
+  }
+  if (cols == 160) {                         // five gate|up pairs per tile, one tile per CU
+    if (epilogue != GP_SILU || M > 256 || N % 160) return OMNI_EINVAL;
+    const int grid = ceil_div(M, 128) * (N / 160);
+    hipLaunchKernelGGL((gemm_silu160_kernel<4>), dim3(grid), dim3(512), 0, st, a);
     OMNI_CHECK_LAUNCH();
     return OMNI_OK;
   }

@@ -201,3 +201,31 @@ def test_packed_partial_plan(so):
     assert plan(4000, 1536, 8960, 1, 2)[0] != 256
     assert plan(4096, 1536, 8960, 1, 0) == (128, 192, 1)
     assert plan(1024, 1536, 8960, 1, 2) == (128, 128, 2)
+
+
+def test_packed_silu160_plan(so):
+    """The SiLU-fused gate_up at 129-256 rows on packed fp16 weights takes 128 x 160 tiles
+    (five gate|up pairs) where they fill the 256 CUs in one round (config 1's 256-token
+    prompt: 224 tiles); 128 rows or fewer, more than 256, int4 weights, N not a multiple of
+    160, too many tiles for one round, a forced tile height or the STORE epilogue keep the
+    other tiles."""
+    import ctypes
+    from omniserver_amd._lib import lib
+    L = lib()
+
+    def plan(M, N, K, fmt, epi, tile_rows=0):
+        r, c, k = ctypes.c_int(0), ctypes.c_int(0), ctypes.c_int(0)
+        assert L.omni_packed_gemm_pipe_plan(M, N, K, fmt, epi, 0, tile_rows, 0, ctypes.byref(r),
+                                            ctypes.byref(c), ctypes.byref(k)) == 0
+        return r.value, c.value, k.value
+
+    assert plan(256, 17920, 1536, 1, 1) == (128, 160, 1)
+    assert plan(129, 17920, 1536, 1, 1) == (128, 160, 1)
+    assert plan(256, 1280, 512, 1, 1) == (128, 160, 1)
+    assert plan(128, 17920, 1536, 1, 1)[1] == 128
+    assert plan(257, 17920, 1536, 1, 1)[1] != 160
+    assert plan(256, 17920, 1536, 0, 1)[1] != 160
+    assert plan(256, 17920 + 128, 1536, 1, 1)[1] != 160
+    assert plan(256, 25600 + 640, 1536, 1, 1)[1] != 160     # 2 x 164 tiles > 256 CUs
+    assert plan(256, 17920, 1536, 1, 1, tile_rows=256) == (256, 128, 1)
+    assert plan(256, 17920, 1536, 1, 0)[1] != 160

@@ -423,6 +423,37 @@ def _packed_plan(M, N, K, fmt, epi, has_bias=0):
     return r.value, c.value, k.value
 
 
+@pytest.mark.parametrize("M,K,N", [(256, 1536, 17920), (200, 1536, 17920), (129, 512, 1280)])
+def test_packed_gemm_pipe_silu160(gpu, M, K, N):
+    """The SiLU-fused gate_up at 129-256 rows on 128 x 160 tiles (five gate|up pairs, one
+    tile per workgroup: config 1's 256-token gate_up), equal bit for bit to the forced
+    256 x 128 tiles (same K order per output), a ragged last row tile included, and sampled
+    rows within tolerance of the oracle."""
+    from omniserver_amd._lib import call, ptr, stream
+    from omniserver_amd.linear import F16Linear
+    assert _packed_plan(M, N, K, 1, 1) == (128, 160, 1)
+    say(f"packed gemm pipe silu160 M={M} K={K} N={N}")
+    wt = f16((N, K), 121, 0.02)
+    x = f16((M, K), 122)
+    lin = F16Linear(wt.to(gpu), fuse_silu=True)
+    xg = x.to(gpu)
+
+    def run(tile_rows):
+        out = torch.full((M, N // 2), float("nan"), device=gpu, dtype=torch.float16)
+        call("omni_packed_gemm_pipe", ptr(xg), K, ptr(lin.weight_packed), None, 1, None, 0,
+             ptr(out), N // 2, M, N, K, 1, tile_rows, 1, None, stream())
+        torch.cuda.synchronize()
+        return out.cpu()
+
+    narrow, wide = run(0), run(256)
+    assert not torch.isnan(narrow).any()
+    assert torch.equal(narrow, wide)
+    rows = torch.tensor(sorted({0, 31, 32, 77, 127, 128, M - 1}))
+    e = ref.silu_mul(ref.linear(x[rows].float(), wt.float().t()))
+    tol = 2e-3 * max(1.0, e.abs().max().item())
+    assert (narrow[rows].float() - e).abs().max().item() <= tol
+
+
 @pytest.mark.parametrize("M,K,bias", [(4096, 1536, True), (4000, 8960, False)])
 def test_packed_gemm_pipe_wide_tiles(gpu, M, K, bias):
     """The 128 x 192 tiles omni_packed_gemm_pipe picks for config 5's N = 1536 projections

@@ -353,10 +353,33 @@ int omni_packed_gemm_pipe(const void* x, int ldx, const void* w_packed, const vo
 int omni_packed_gemm_pipe_plan(int M, int N, int K, int fmt, int epilogue, int has_bias,
                                int tile_rows, int ksplit, int* rows, int* cols, int* ks);
 
+/* omni_f16_gemm_pipe on this library's packed fp16 weights (omni_f16_pack with no gate|up
+ * interleave): the same epilogues (OMNI_EPI_STORE / QGELU / GELU / RESID, the bias added
+ * before the fp16 rounding) plus OMNI_EPI_PARTIAL (each K slice's fp32 sums to
+ * workspace[slice][M][N]; no bias, out unused; omni_layernorm_partials adds them).  Tiling
+ * and K slices as omni_packed_gemm_pipe plans them (omni_packed_gemm_pipe_plan, fmt 1;
+ * ksplit > 0 fixes the slices).  The vision tower's linears (model/qwen2_vit.py:41-44, 83,
+ * 88-89, 123-129). */
+int omni_f16_gemm_pipe_packed(const void* x, int ldx, const void* w_packed, const void* bias,
+                              const void* res, int ldr, void* out, int ldo, int M, int N, int K,
+                              int epilogue, int tile_rows, int ksplit, float* workspace,
+                              void* stream);
+
 /* nn.LayerNorm(N, eps) of M fp16 rows (model/qwen2_vit.py:39-40, 87): fp32 mean and biased
  * variance, y = (x - mean) rsqrt(var + eps) w + b.  N % 8 == 0, N <= 2048; out may alias x. */
 int omni_layernorm(const void* x, int ldx, const void* weight, const void* bias, int M, int N,
                    float eps, void* out, int ldo, void* stream);
+
+/* A split-K linear's residual add followed by a LayerNorm (model/qwen2_vit.py:66-69: x = x +
+ * attn(...) then norm2(x); x = x + mlp(...) then the next norm1 or the merger's ln_q):
+ * residual_out = fp16(residual + fp16(sum of the fp32 slices [nparts][M][N] in slice order +
+ * lin_bias)) - what omni_f16_gemm_pipe's finish launch writes with OMNI_EPI_RESID - and
+ * out = LayerNorm(residual_out; weight, bias, eps) as omni_layernorm.  1 <= nparts <= 16;
+ * lin_bias may be NULL; residual_out may alias residual; pointers 16-byte aligned. */
+int omni_layernorm_partials(const float* partials, int nparts, const void* lin_bias,
+                            const void* residual, int ldr, void* residual_out, int ldro,
+                            const void* weight, const void* bias, int M, int N, float eps,
+                            void* out, int ldo, void* stream);
 
 /* vision_rope (kernels/vision_rope.py:39-47, with the angles of model/qwen2_vit.py:96-116):
  * in place on q heads [0, n_heads) and k heads [n_heads, 2 n_heads) of S qkv rows (row

@@ -73,6 +73,8 @@ SIGNATURES = {
     "omni_packed_gemm_pipe_plan": [_I, _I, _I, _I, _I, _I, _I, _I, ctypes.POINTER(_I),
                                    ctypes.POINTER(_I), ctypes.POINTER(_I)],
     "omni_layernorm": [_P, _I, _P, _P, _I, _I, _F, _P, _I, _P],
+    "omni_layernorm_partials": [_P, _I, _P, _P, _I, _P, _I, _P, _P, _I, _I, _F, _P, _I, _P],
+    "omni_f16_gemm_pipe_packed": [_P, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P],
     "omni_vision_rope": [_P, _I, _I, _I, _I, _P, _P, _P],
     "omni_vit_attention": [_P, _I, _I, _I, _I, _P, _P, _I, _P, _I, _F, _P],
     "omni_gemm_slices": [_I, _I],

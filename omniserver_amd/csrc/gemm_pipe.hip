@@ -1266,6 +1266,9 @@ extern "C" int omni_packed_gemm_pipe_plan(int M, int N, int K, int fmt, int epil
   return OMNI_OK;
 }
 
+static int gp_packed_f16_launch(GemmPipeArgs& a, int epilogue, int tile_rows, int cols,
+                                hipStream_t st);
+
 // The decoder's prefill linears on the same pipeline with this library's packed weights
 // (fmt 0: int4 from omni_gptq_repack with its scales, 1: fp16 from omni_f16_pack); see the
 // header for the arguments.  Stages per tile height: int4 6 (128 rows) / 4 (256 rows),
@@ -1319,8 +1322,19 @@ extern "C" int omni_packed_gemm_pipe(const void* x, int ldx, const void* w_packe
   if (fmt == 0)
     return tile_rows == 256 ? gp_launch<GW_INT4, 4, 4>(a, epilogue, st)
                             : gp_launch<GW_INT4, 2, 6>(a, epilogue, st);
+  return gp_packed_f16_launch(a, epilogue, tile_rows, cols, st);
+}
+
+// The packed fp16 weights' launch for a planned tiling (gp_packed_plan): a's fields set,
+// a.KS the plan's slices.
+static int gp_packed_f16_launch(GemmPipeArgs& a, int epilogue, int tile_rows, int cols,
+                                hipStream_t st) {
+  const int M = a.M, N = a.N;
+  const int ksplit = a.KS;
+  const bool bias = a.bias != nullptr;
   if (tile_rows == 256 && cols != GP_BN) {     // persistent 8-wave tiles of 256 x cols
-    if (M % 256 || N % cols || (cols == 192 && epilogue == GP_SILU) || (epilogue == GP_STORE && bias))
+    if (M % 256 || N % cols || (cols == 192 && epilogue == GP_SILU) || (epilogue == GP_STORE && bias) ||
+        (epilogue != GP_SILU && epilogue != GP_PARTIAL && epilogue != GP_STORE))
       return OMNI_EINVAL;                      // (the plan picks them only where they hold)
     int64_t t = (int64_t)(M / 256) * (N / cols) * ksplit;
     if (cols == 256 && ksplit == 1) {
@@ -1352,4 +1366,53 @@ extern "C" int omni_packed_gemm_pipe(const void* x, int ldx, const void* w_packe
   if (cols == 192) return gp_launch<GW_F16, 2, 3, 6>(a, epilogue, st);
   return tile_rows == 256 ? gp_launch<GW_F16, 4, 3>(a, epilogue, st)
                           : gp_launch<GW_F16, 2, 4>(a, epilogue, st);
+}
+
+// omni_f16_gemm_pipe on this library's packed fp16 weights (omni_f16_pack): every epilogue
+// of that entry (STORE, QGELU, GELU, RESID, each with the bias added before the rounding)
+// and OMNI_EPI_PARTIAL (the K slices' fp32 sums into workspace, no bias, no out); the tiling
+// as omni_packed_gemm_pipe plans it (omni_packed_gemm_pipe_plan with fmt 1).  For the vision
+// tower's linears (model/qwen2_vit.py:41-44, 83, 88-89, 123-129).
+extern "C" int omni_f16_gemm_pipe_packed(const void* x, int ldx, const void* w_packed,
+                                         const void* bias, const void* res, int ldr, void* out,
+                                         int ldo, int M, int N, int K, int epilogue, int tile_rows,
+                                         int ksplit, float* workspace, void* stream) {
+  if (M < 0 || N <= 0 || K <= 0 || ksplit < 0) return OMNI_EINVAL;
+  if ((N % GP_BN) || (K % 128) || K < 4 * GP_BKH) return OMNI_EUNSUPPORTED;
+  if (M == 0) return OMNI_OK;
+  if (epilogue != GP_STORE && epilogue != GP_QGELU && epilogue != GP_GELU && epilogue != GP_RESID &&
+      epilogue != GP_PARTIAL)
+    return OMNI_EINVAL;
+  const bool part = epilogue == GP_PARTIAL;
+  if (!x || !w_packed || (!part && !out)) return OMNI_EINVAL;
+  if (ldx < K || (ldx & 7) || (!part && (ldo < N || (ldo & 3)))) return OMNI_EINVAL;
+  if (((uintptr_t)x & 15) || ((uintptr_t)w_packed & 15) || ((uintptr_t)out & 7)) return OMNI_EINVAL;
+  if (bias && (part || ((uintptr_t)bias & 15))) return OMNI_EINVAL;
+  if (epilogue == GP_RESID && (!res || ldr < N || (ldr & 3) || ((uintptr_t)res & 7))) return OMNI_EINVAL;
+  if (tile_rows != 0 && tile_rows != 128 && tile_rows != 256) return OMNI_EINVAL;
+  int cols;
+  gp_packed_plan(M, N, K, 1, epilogue, bias != nullptr, tile_rows, ksplit, tile_rows, cols, ksplit);
+  const int ns = tile_rows == 256 ? (cols == GP_BN ? 3 : 2) : 4;
+  if (2 * (K / 128 / ksplit) < ns) return OMNI_EUNSUPPORTED;
+  if ((ksplit > 1 || part) && (!workspace || ((uintptr_t)workspace & 15))) return OMNI_EINVAL;
+  GemmPipeArgs a;
+  a.x = (const half_t*)x;
+  a.ldx = ldx;
+  a.w = (const half_t*)w_packed;
+  a.ldw = K;
+  a.wq = nullptr;
+  a.wsc = nullptr;
+  a.bias_after_round = 0;
+  a.bias = (const half_t*)bias;
+  a.res = (const half_t*)res;
+  a.ldr = ldr;
+  a.out = (half_t*)out;
+  a.ldo = ldo;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.KS = ksplit;
+  a.part = workspace;
+  a.n_big = N;
+  return gp_packed_f16_launch(a, epilogue, tile_rows, cols, (hipStream_t)stream);
 }

@@ -1,7 +1,8 @@
-// Vision tower (Qwen2-VL ViT) kernels: LayerNorm, the 2-D vision rotary, and
-// non-causal segmented attention at head_dim 80.  The tower's linears run on the
-// tiled fp16 GEMM (gemv.hip, omni_f16_gemm_tiled) with its bias / QuickGELU / GELU /
-// residual epilogues.
+// Vision tower (Qwen2-VL ViT) kernels: LayerNorm (also over a split-K linear's partial
+// sums, with its bias and residual add), the 2-D vision rotary, and non-causal segmented
+// attention at head_dim 80.  The tower's linears run on the pipelined fp16 GEMM over packed
+// weights (gemm_pipe.hip, omni_f16_gemm_pipe_packed: bias / QuickGELU / GELU / residual /
+// partial-sum epilogues) and the patch embedding on the tiled one (gemv.hip).
 //
 // Replaces, per block of model/qwen2_vit.py:36-69: nn.LayerNorm (norm1 / norm2, and
 // the merger's ln_q at :128), the fused rotary of kernels/vision_rope.py:19-47, and
@@ -16,11 +17,20 @@
 // ---------------------------------------------------------------------------
 #define LN_MAXCH 4
 
-__global__ __launch_bounds__(256) void layernorm_kernel(const half_t* __restrict__ x, int ldx,
+// PARTS: x is formed first, as a split-K linear's finish with the residual epilogue would
+// form it (gemm_pipe_finish_kernel, GP_RESID): h = fp16(sum of the nparts fp32 slices
+// [nparts][M][N] in slice order (+ bias, before the rounding)), x = fp16(res + h), with the
+// residual rows read from x (row stride ldx) and x written to x_out (which may alias them:
+// each lane reads its chunks before it writes them).
+template <bool PARTS>
+__global__ __launch_bounds__(256) void layernorm_kernel(const half_t* x, int ldx,
                                                         const half_t* __restrict__ w,
                                                         const half_t* __restrict__ b, int M,
-                                                        int N, float eps, half_t* __restrict__ out,
-                                                        int ldo) {
+                                                        int N, float eps, half_t* out, int ldo,
+                                                        const float* __restrict__ parts = nullptr,
+                                                        int nparts = 0,
+                                                        const half_t* __restrict__ pbias = nullptr,
+                                                        half_t* x_out = nullptr, int ldxo = 0) {
 #pragma clang fp contract(off)
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= M) return;
@@ -33,7 +43,30 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const half_t* __restrict
   for (int u = 0; u < LN_MAXCH; ++u) {
     const int c = lane + 64 * u;
     half8_t h = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
-    if (c < nc) h = *(const half8_t*)(xr + c * 8);
+    if (c < nc) {
+      h = *(const half8_t*)(xr + c * 8);
+      if (PARTS) {
+        const float* pp = parts + (int64_t)row * N + c * 8;
+        const int64_t ps = (int64_t)M * N;
+        float a[8];
+        const float4 lo = *(const float4*)pp, hi = *(const float4*)(pp + 4);
+        a[0] = lo.x; a[1] = lo.y; a[2] = lo.z; a[3] = lo.w;
+        a[4] = hi.x; a[5] = hi.y; a[6] = hi.z; a[7] = hi.w;
+        for (int p = 1; p < nparts; ++p) {
+          const float4 l2 = *(const float4*)(pp + p * ps), h2 = *(const float4*)(pp + p * ps + 4);
+          a[0] += l2.x; a[1] += l2.y; a[2] += l2.z; a[3] += l2.w;
+          a[4] += h2.x; a[5] += h2.y; a[6] += h2.z; a[7] += h2.w;
+        }
+        half8_t bb = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
+        if (pbias) bb = *(const half8_t*)(pbias + c * 8);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const half_t lin = pbias ? (half_t)(a[e] + (float)bb[e]) : (half_t)a[e];
+          h[e] = (half_t)((float)h[e] + (float)lin);
+        }
+        *(half8_t*)(x_out + (int64_t)row * ldxo + c * 8) = h;
+      }
+    }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       v[u][e] = (float)h[e];
@@ -67,6 +100,104 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const half_t* __restrict
   }
 }
 
+// Rows of N = 256 NC (the tower's 1280: NC = 5): lane l holds the 4-column chunks
+// l + 64 u, u < NC, so every lane has the same work and every load of the row - the
+// residual / input, NP fp32 partial slices, the linear's bias and the norm's gains - goes out
+// before any arithmetic (the kernel above waits chunk by chunk, and its 8-column chunks give
+// lanes 2 or 3 of them at N = 1280).  NP = 0: plain LayerNorm of x; NP > 0: x formed first
+// from the slices as in the kernel above.  Sums in this kernel's own order (chunks u, then
+// the 4 columns), so its outputs agree with the kernel above to fp32 rounding of the mean
+// and variance, and its two forms with each other bit for bit.
+template <int NC, int NP>
+__global__ __launch_bounds__(256) void layernorm4_kernel(const half_t* x, int ldx,
+                                                         const half_t* __restrict__ w,
+                                                         const half_t* __restrict__ b, int M,
+                                                         float eps, half_t* out, int ldo,
+                                                         const float* __restrict__ parts,
+                                                         const half_t* __restrict__ pbias,
+                                                         half_t* x_out, int ldxo) {
+#pragma clang fp contract(off)
+  constexpr int N = 256 * NC;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const int lane = threadIdx.x & 63;
+  const half_t* xr = x + (int64_t)row * ldx + 4 * lane;
+  half4_t xv[NC], wv[NC], bv[NC], pb[NP > 0 ? NC : 1];
+  float4 pv[NP > 0 ? NP : 1][NC];
+#pragma unroll
+  for (int u = 0; u < NC; ++u) {
+    xv[u] = *(const half4_t*)(xr + 256 * u);
+    if (NP > 0) {
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
+        pv[p][u] = *(const float4*)(parts + ((int64_t)p * M + row) * N + 4 * lane + 256 * u);
+      if (pbias) pb[u] = *(const half4_t*)(pbias + 4 * lane + 256 * u);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < NC; ++u) {
+    wv[u] = *(const half4_t*)(w + 4 * lane + 256 * u);
+    bv[u] = *(const half4_t*)(b + 4 * lane + 256 * u);
+  }
+  float v[NC][4];
+  float s = 0.f;
+#pragma unroll
+  for (int u = 0; u < NC; ++u) {
+    half4_t h = xv[u];
+    if (NP > 0) {
+      float a[4] = {pv[0][u].x, pv[0][u].y, pv[0][u].z, pv[0][u].w};
+#pragma unroll
+      for (int p = 1; p < NP; ++p) {
+        a[0] += pv[p][u].x; a[1] += pv[p][u].y; a[2] += pv[p][u].z; a[3] += pv[p][u].w;
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const half_t lin = pbias ? (half_t)(a[e] + (float)pb[u][e]) : (half_t)a[e];
+        h[e] = (half_t)((float)h[e] + (float)lin);
+      }
+      *(half4_t*)(x_out + (int64_t)row * ldxo + 4 * lane + 256 * u) = h;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[u][e] = (float)h[e];
+      s += v[u][e];
+    }
+  }
+  const float mean = wave_sum(s) / (float)N;
+  float q = 0.f;
+#pragma unroll
+  for (int u = 0; u < NC; ++u)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float d = v[u][e] - mean;
+      q += d * d;
+    }
+  const float var = wave_sum(q) / (float)N;
+  const float rstd = rsqrtf(var + eps);
+#pragma unroll
+  for (int u = 0; u < NC; ++u) {
+    half4_t y;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) y[e] = (half_t)((v[u][e] - mean) * rstd * (float)wv[u][e] + (float)bv[u][e]);
+    *(half4_t*)(out + (int64_t)row * ldo + 4 * lane + 256 * u) = y;
+  }
+}
+
+typedef void (*layernorm4_fn)(const half_t*, int, const half_t*, const half_t*, int, float,
+                              half_t*, int, const float*, const half_t*, half_t*, int);
+// The layernorm4_kernel instance for (N, nparts), or nullptr (the kernel above then).
+static layernorm4_fn layernorm4_for(int N, int nparts) {
+  if (N != 1280) return nullptr;
+  switch (nparts) {
+    case 0: return layernorm4_kernel<5, 0>;
+    case 1: return layernorm4_kernel<5, 1>;
+    case 2: return layernorm4_kernel<5, 2>;
+    case 3: return layernorm4_kernel<5, 3>;
+    case 4: return layernorm4_kernel<5, 4>;
+  }
+  return nullptr;
+}
+
 // LayerNorm of M rows of N (N % 8 == 0, N <= 2048); w, b fp16 [N]; out may alias x.
 extern "C" int omni_layernorm(const void* x, int ldx, const void* weight, const void* bias, int M,
                               int N, float eps, void* out, int ldo, void* stream) {
@@ -75,9 +206,48 @@ extern "C" int omni_layernorm(const void* x, int ldx, const void* weight, const 
   if ((N & 7) || N > 64 * 8 * LN_MAXCH) return OMNI_EUNSUPPORTED;
   if (!x || !weight || !bias || !out) return OMNI_EINVAL;
   if (ldx < N || ldo < N || (ldx & 7) || (ldo & 7)) return OMNI_EINVAL;
-  hipLaunchKernelGGL(layernorm_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0,
-                     (hipStream_t)stream, (const half_t*)x, ldx, (const half_t*)weight,
-                     (const half_t*)bias, M, N, eps, (half_t*)out, ldo);
+  if (layernorm4_fn kern = ((((uintptr_t)x | (uintptr_t)out | (uintptr_t)weight | (uintptr_t)bias) & 7) == 0 &&
+                             (ldx & 3) == 0 && (ldo & 3) == 0) ? layernorm4_for(N, 0) : nullptr)
+    hipLaunchKernelGGL(kern, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, (hipStream_t)stream,
+                       (const half_t*)x, ldx, (const half_t*)weight, (const half_t*)bias, M, eps,
+                       (half_t*)out, ldo, nullptr, nullptr, nullptr, 0);
+  else
+    hipLaunchKernelGGL(layernorm_kernel<false>, dim3((unsigned)((M + 3) / 4)), dim3(256), 0,
+                       (hipStream_t)stream, (const half_t*)x, ldx, (const half_t*)weight,
+                       (const half_t*)bias, M, N, eps, (half_t*)out, ldo, nullptr, 0, nullptr,
+                       nullptr, 0);
+  OMNI_CHECK_LAUNCH();
+  return OMNI_OK;
+}
+
+// The residual add of a split-K linear (fp32 slices [nparts][M][N], 1 <= nparts <= 16,
+// optional fp16 bias [N]) followed by a LayerNorm: residual_out = fp16(residual +
+// fp16(sum of the slices + bias)), as the linear's finish launch with the residual epilogue
+// writes it, then out = LayerNorm(residual_out) as omni_layernorm (model/qwen2_vit.py:66-69:
+// x = x + attn(...); norm2(x), and x = x + mlp(...) before the next block's norm1 or the
+// merger's ln_q).  residual_out may alias residual.
+extern "C" int omni_layernorm_partials(const float* partials, int nparts, const void* lin_bias,
+                                       const void* residual, int ldr, void* residual_out, int ldro,
+                                       const void* weight, const void* bias, int M, int N,
+                                       float eps, void* out, int ldo, void* stream) {
+  if (M < 0 || N <= 0 || nparts < 1 || nparts > 16) return OMNI_EINVAL;
+  if (M == 0) return OMNI_OK;
+  if ((N & 7) || N > 64 * 8 * LN_MAXCH) return OMNI_EUNSUPPORTED;
+  if (!partials || !residual || !residual_out || !weight || !bias || !out) return OMNI_EINVAL;
+  if (ldr < N || ldro < N || ldo < N || (ldr & 7) || (ldro & 7) || (ldo & 7)) return OMNI_EINVAL;
+  if (((uintptr_t)partials & 15) || ((uintptr_t)residual & 15) || ((uintptr_t)residual_out & 15) ||
+      ((uintptr_t)out & 15) || (lin_bias && ((uintptr_t)lin_bias & 15)))
+    return OMNI_EINVAL;
+  if (layernorm4_fn kern = (((uintptr_t)weight | (uintptr_t)bias) & 7) == 0 ? layernorm4_for(N, nparts) : nullptr)
+    hipLaunchKernelGGL(kern, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, (hipStream_t)stream,
+                       (const half_t*)residual, ldr, (const half_t*)weight, (const half_t*)bias, M,
+                       eps, (half_t*)out, ldo, partials, (const half_t*)lin_bias,
+                       (half_t*)residual_out, ldro);
+  else
+    hipLaunchKernelGGL(layernorm_kernel<true>, dim3((unsigned)((M + 3) / 4)), dim3(256), 0,
+                       (hipStream_t)stream, (const half_t*)residual, ldr, (const half_t*)weight,
+                       (const half_t*)bias, M, N, eps, (half_t*)out, ldo, partials, nparts,
+                       (const half_t*)lin_bias, (half_t*)residual_out, ldro);
   OMNI_CHECK_LAUNCH();
   return OMNI_OK;
 }

@@ -16,6 +16,7 @@ every kernel, the rotary frequencies in fp32 (inv_freq computed on the CPU in fp
 
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 from typing import Dict, List, Sequence, Tuple
 
@@ -25,6 +26,7 @@ from ._lib import call, lib, ptr, require_cuda, stream
 from .hostio import to_device
 
 EPI_STORE, EPI_QGELU, EPI_GELU, EPI_RESID = 0, 4, 5, 6
+EPI_PARTIAL = 2
 _QT = 64     # queries per attention workgroup (the kernel's tile)
 
 
@@ -120,6 +122,23 @@ def layer_norm_out(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor, eps: float
     return out
 
 
+def layer_norm_partials_out(parts: torch.Tensor, nparts: int, lin_bias: torch.Tensor | None,
+                            x: torch.Tensor, w: torch.Tensor, b: torch.Tensor, eps: float,
+                            out: torch.Tensor) -> torch.Tensor:
+    """x = fp16(x + fp16(sum of the nparts fp32 slices [S, M, N] + lin_bias)) in place (the
+    split-K linear's residual add, as its finish launch would write it), then out =
+    LayerNorm(x) as layer_norm_out."""
+    require_cuda(parts, dtype=torch.float32)
+    require_cuda(x, w, b, out, lin_bias, dtype=torch.float16)
+    M, N = x.shape
+    if parts.numel() < nparts * M * N:
+        raise ValueError("partial buffer smaller than nparts x M x N")
+    call("omni_layernorm_partials", ptr(parts), nparts, ptr(lin_bias), ptr(x), x.stride(0),
+         ptr(x), x.stride(0), ptr(w), ptr(b), M, N, float(eps), ptr(out), out.stride(0),
+         stream())
+    return out
+
+
 def vision_rope_(qkv: torch.Tensor, n_heads: int, head_dim: int, pos_hw: torch.Tensor,
                  inv_freq: torch.Tensor) -> torch.Tensor:
     """In-place 2-D rotary of the q and k heads of qkv rows (kernels/vision_rope.py:39-47)."""
@@ -142,11 +161,12 @@ def vit_attention_out(qkv: torch.Tensor, n_heads: int, head_dim: int, cu: torch.
 
 
 class VisionLinear:
-    """fp16 nn.Linear (weight [N, K], optional bias [N]) on one of two GEMMs:
-    ``pipe`` (omni_f16_gemm_pipe: weights in nn.Linear layout, a multi-stage LDS pipeline;
-    N % 128 == 0, K % 128 == 0, K >= 256 - every linear of the blocks and the merger) or
-    ``tiled`` (omni_f16_gemm_tiled: weights packed with K zero-padded to whole 128-column
-    groups - the patch embedding's K = 1176)."""
+    """fp16 nn.Linear (weight [N, K], optional bias [N]) on one of two GEMMs, its weight
+    packed once (omni_f16_pack) into the MFMA operand layout: ``pipe``
+    (omni_f16_gemm_pipe_packed: a multi-stage LDS pipeline, N % 128 == 0, K % 128 == 0,
+    K >= 256 - every linear of the blocks and the merger; it can also leave the K slices'
+    fp32 sums for the next kernel, ``out_partial``) or ``tiled`` (omni_f16_gemm_tiled, K
+    zero-padded to whole 128-column groups - the patch embedding's K = 1176)."""
 
     def __init__(self, weight: torch.Tensor, bias: torch.Tensor | None, device,
                  path: str | None = None):
@@ -157,18 +177,36 @@ class VisionLinear:
             raise ValueError(f"unknown GEMM path {path!r}")
         self.path = path
         self._ws = None
+        self._plans: Dict[tuple, int] = {}
         w = weight.to(device=device, dtype=torch.float16).contiguous()
         self.bias = None if bias is None else bias.to(device=device, dtype=torch.float16).contiguous()
         self.N, self.K = N, K
-        if path == "pipe":
-            self.w, self.Kp = w, K
-        else:
-            Kp = -(-K // 128) * 128
-            if Kp != K:
-                w = torch.nn.functional.pad(w, (0, Kp - K)).contiguous()
-            self.w = torch.empty_like(w)
-            call("omni_f16_pack", ptr(w), ptr(self.w), Kp, N, 0, stream())
-            self.Kp = Kp
+        Kp = -(-K // 128) * 128
+        if Kp != K:
+            w = torch.nn.functional.pad(w, (0, Kp - K)).contiguous()
+        self.w = torch.empty_like(w)
+        call("omni_f16_pack", ptr(w), ptr(self.w), Kp, N, 0, stream())
+        self.Kp = Kp
+
+    def slices(self, M: int, epilogue: int = EPI_STORE, tile_rows: int = 0,
+               ksplit: int = 0) -> int:
+        """K slices the pipe GEMM runs for M rows (the library's plan for ksplit 0, which the
+        call then makes itself; ksplit > 0 fixes them)."""
+        if ksplit:
+            return ksplit
+        key = (M, epilogue, tile_rows)
+        if key not in self._plans:
+            r, c, k = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+            call("omni_packed_gemm_pipe_plan", M, self.N, self.K, 1, epilogue,
+                 int(self.bias is not None and epilogue != EPI_PARTIAL), tile_rows, 0,
+                 ctypes.byref(r), ctypes.byref(c), ctypes.byref(k))
+            self._plans[key] = k.value
+        return self._plans[key]
+
+    def _workspace(self, need: int, device) -> torch.Tensor:
+        if self._ws is None or self._ws.numel() < need:
+            self._ws = torch.empty(need, device=device, dtype=torch.float32)
+        return self._ws
 
     def out(self, x: torch.Tensor, out: torch.Tensor, epilogue: int = EPI_STORE,
             res: torch.Tensor | None = None, tile_rows: int = 0,
@@ -178,24 +216,39 @@ class VisionLinear:
             raise ValueError(f"input has {x.shape[1]} columns, the linear takes {self.K}")
         if x.stride(1) != 1 or out.stride(1) != 1 or (res is not None and res.stride(1) != 1):
             raise ValueError("rows must be contiguous")
+        if epilogue == EPI_PARTIAL:
+            raise ValueError("the partial-sum form is out_partial")
         ldr = 0 if res is None else res.stride(0)
         if self.path == "pipe":
             M = x.shape[0]
-            ks = ksplit or lib().omni_f16_gemm_pipe_splits(M, self.N, self.K, tile_rows)
-            ws = None
-            if ks > 1:      # fp32 partial sums of the K slices
-                need = ks * M * self.N
-                if self._ws is None or self._ws.numel() < need:
-                    self._ws = torch.empty(need, device=x.device, dtype=torch.float32)
-                ws = self._ws
-            call("omni_f16_gemm_pipe", ptr(x), x.stride(0), ptr(self.w), ptr(self.bias), ptr(res),
-                 ldr, ptr(out), out.stride(0), M, self.N, self.K, epilogue, tile_rows, ks,
-                 ptr(ws), stream())
+            ks = self.slices(M, epilogue, tile_rows, ksplit)
+            ws = self._workspace(ks * M * self.N, x.device) if ks > 1 else None
+            call("omni_f16_gemm_pipe_packed", ptr(x), x.stride(0), ptr(self.w), ptr(self.bias),
+                 ptr(res), ldr, ptr(out), out.stride(0), M, self.N, self.K, epilogue, tile_rows,
+                 ksplit, ptr(ws), stream())
         else:
             call("omni_f16_gemm_tiled", ptr(x), x.stride(0), self.K, ptr(self.w), ptr(self.bias),
                  ptr(res), ldr, ptr(out), out.stride(0), x.shape[0], self.N, self.Kp, epilogue,
                  stream())
         return out
+
+    def out_partial(self, x: torch.Tensor, parts: torch.Tensor | None = None) -> Tuple[torch.Tensor, int]:
+        """The K slices' fp32 sums x . W^T (no bias) into parts [S, M, N] (the linear's own
+        workspace when None), for layer_norm_partials_out to finish; returns (parts, S)."""
+        if self.path != "pipe":
+            raise ValueError("the partial-sum form runs on the pipe GEMM")
+        require_cuda(x, dtype=torch.float16, contiguous=False)
+        if x.shape[1] != self.K or x.stride(1) != 1:
+            raise ValueError(f"input must be rows of {self.K} contiguous columns")
+        M = x.shape[0]
+        S = self.slices(M, EPI_PARTIAL)
+        if parts is None:
+            parts = self._workspace(S * M * self.N, x.device)
+        elif parts.numel() < S * M * self.N or parts.dtype != torch.float32:
+            raise ValueError("partial buffer too small or not fp32")
+        call("omni_f16_gemm_pipe_packed", ptr(x), x.stride(0), ptr(self.w), None, None, 0, None, 0,
+             M, self.N, self.K, EPI_PARTIAL, 0, 0, ptr(parts), stream())
+        return parts, S
 
 
 class _Block:
@@ -250,16 +303,30 @@ class Qwen2VIT:
         qkv, f = mk(S, 3 * D), mk(S, cfg.mlp_dim)
         self.patch_embed.out(pv, x)
         scale = hd ** -0.5
+        # proj and fc2 leave their K slices' fp32 sums; the LayerNorm that follows each adds
+        # them, the bias and the residual first (one launch where a finish launch and the
+        # norm were two), with the same roundings
+        np_ = max(max(b.proj.slices(S, EPI_PARTIAL), b.fc2.slices(S, EPI_PARTIAL))
+                  for b in self.blocks)
+        parts = torch.empty(np_ * S * D, device=dev, dtype=torch.float32)
+        pend = None                      # the previous block's fc2 slices
         for blk in self.blocks:
-            layer_norm_out(x, blk.n1w, blk.n1b, cfg.eps, h)
+            if pend is None:
+                layer_norm_out(x, blk.n1w, blk.n1b, cfg.eps, h)
+            else:
+                layer_norm_partials_out(parts, pend[0], pend[1], x, blk.n1w, blk.n1b, cfg.eps, h)
             blk.qkv.out(h, qkv)
             vision_rope_(qkv, nh, hd, pos, self.inv_freq)
             vit_attention_out(qkv, nh, hd, cu, tiles, scale, att)
-            blk.proj.out(att, x, EPI_RESID, res=x)
-            layer_norm_out(x, blk.n2w, blk.n2b, cfg.eps, h)
+            _, sp = blk.proj.out_partial(att, parts)
+            layer_norm_partials_out(parts, sp, blk.proj.bias, x, blk.n2w, blk.n2b, cfg.eps, h)
             blk.fc1.out(h, f, EPI_QGELU)
-            blk.fc2.out(f, x, EPI_RESID, res=x)
-        layer_norm_out(x, self.lnq_w, self.lnq_b, cfg.eps, h)
+            _, sf = blk.fc2.out_partial(f, parts)
+            pend = (sf, blk.fc2.bias)
+        if pend is None:
+            layer_norm_out(x, self.lnq_w, self.lnq_b, cfg.eps, h)
+        else:
+            layer_norm_partials_out(parts, pend[0], pend[1], x, self.lnq_w, self.lnq_b, cfg.eps, h)
         hm = h.view(S // m2, cfg.merged_dim)
         m1 = mk(S // m2, cfg.merged_dim)
         self.merger_fc1.out(hm, m1, EPI_GELU)

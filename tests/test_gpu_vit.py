@@ -237,3 +237,62 @@ def test_runner_pixel_inputs_match_oracle(gpu):
     err, cos = compare_logits(logits, exp)
     check_ids(torch.tensor([t[0] for t in pix]), exp, err)
     say(f"  prefill logits vs oracle: max-abs {err:.2e} cos {cos:.6f}")
+
+
+@pytest.mark.parametrize("M,N,K,epi,bias", [(300, 3840, 1280, 0, True), (257, 5120, 1280, 4, True),
+                                            (75, 5120, 5120, 5, True), (1024, 1280, 5120, 6, True),
+                                            (64, 1280, 1280, 6, False)])
+def test_packed_equals_rows_layout(gpu, M, N, K, epi, bias):
+    """omni_f16_gemm_pipe_packed (the tower's linears, packed weights) equals
+    omni_f16_gemm_pipe on the nn.Linear-layout weight bit for bit, at the same tile height
+    and K slices (the same k order per output), every epilogue."""
+    from omniserver_amd import vit
+    from omniserver_amd._lib import call, ptr, stream
+    say(f"packed vs row-layout pipe GEMM M={M} N={N} K={K} epi={epi}")
+    x, w = f16((M, K), 31).to(gpu), f16((N, K), 32, 0.02).to(gpu)
+    b = f16((N,), 33, 0.02).to(gpu) if bias else None
+    res = f16((M, N), 34).to(gpu)
+    lin = vit.VisionLinear(w, b, gpu)
+    for tile_rows, ks in ((128, 1), (256, 2), (128, 3)):
+        if K // 128 // ks < 2:
+            continue
+        ws = torch.empty(ks * M * N, device=gpu, dtype=torch.float32)
+        outs = []
+        for packed in (True, False):
+            o = res.clone() if epi == vit.EPI_RESID else torch.empty(M, N, device=gpu, dtype=torch.float16)
+            name = "omni_f16_gemm_pipe_packed" if packed else "omni_f16_gemm_pipe"
+            call(name, ptr(x), K, ptr(lin.w if packed else w), ptr(b), ptr(o) if epi == vit.EPI_RESID else None,
+                 N, ptr(o), N, M, N, K, epi, tile_rows, ks, ptr(ws), stream())
+            outs.append(o.cpu())
+        torch.cuda.synchronize()
+        assert torch.equal(outs[0], outs[1]), (tile_rows, ks)
+
+
+@pytest.mark.parametrize("M,N,K,bias", [(1024, 1280, 5120, True), (1024, 1280, 1280, True),
+                                        (300, 1280, 1280, False), (7, 1280, 5120, True)])
+def test_layernorm_partials(gpu, M, N, K, bias):
+    """proj / fc2 leaving their K slices (out_partial, the library's plan) and the next
+    LayerNorm adding them (layer_norm_partials_out: slices in order, the bias before the fp16
+    rounding, the residual after) equal the same GEMM finished with the residual epilogue at
+    the same slice count followed by the plain LayerNorm, bit for bit: the new residual rows
+    and the normalised rows."""
+    from omniserver_amd import vit
+    say(f"layernorm over partials M={M} N={N} K={K} bias={bias}")
+    x, w = f16((M, K), 41).to(gpu), f16((N, K), 42, 0.02).to(gpu)
+    b = f16((N,), 43, 0.02).to(gpu) if bias else None
+    res = f16((M, N), 44).to(gpu)
+    g, gb = (1.0 + 0.1 * f16((N,), 45)).to(gpu), f16((N,), 46, 0.1).to(gpu)
+    lin = vit.VisionLinear(w, b, gpu)
+    parts, S = lin.out_partial(x, torch.empty(16 * M * N, device=gpu, dtype=torch.float32))
+    r2, h2 = res.clone(), torch.empty(M, N, device=gpu, dtype=torch.float16)
+    vit.layer_norm_partials_out(parts, S, lin.bias, r2, g, gb, 1e-6, h2)
+    r1, h1 = res.clone(), torch.empty(M, N, device=gpu, dtype=torch.float16)
+    lin.out(x, r1, vit.EPI_RESID, res=r1, ksplit=S)
+    vit.layer_norm_out(r1, g, gb, 1e-6, h1)
+    torch.cuda.synchronize()
+    say(f"  {S} slices")
+    assert torch.equal(r1.cpu(), r2.cpu()) and torch.equal(h1.cpu(), h2.cpu())
+    # and against the oracle's x + linear, then LayerNorm
+    want_r = vref.r16(res.cpu().float() + vref.linear(x.cpu().float(), w.cpu().float(),
+                                                       None if b is None else b.cpu().float()))
+    assert (r2.cpu().float() - want_r).abs().max().item() <= 2e-3 * max(1.0, want_r.abs().max().item())

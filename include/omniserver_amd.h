@@ -336,10 +336,11 @@ int omni_f16_gemm_pipe_splits(int M, int N, int K, int tile_rows);
  * that sums them in order (omni_add_rmsnorm_partials, omni_mrope_kv_write_partials).
  * With tile_rows and ksplit both 0 and fp16 weights, shapes whose 128 x 192 tiles (STORE /
  * PARTIAL, N % 192 == 0) or persistent 256 x 256 tiles (STORE without a bias / SILU, M and
- * N % 256 == 0) take fewer grid rounds x tile work run those, and the SILU epilogue at
- * 129-256 rows runs 128 x 160 tiles (five gate|up pairs) where they fill the CUs in one
- * round (omni_packed_gemm_pipe_plan; same k order per output: results equal the 128 x 128
- * tiles' bit for bit). */
+ * N % 256 == 0) take fewer grid rounds x tile work run those, and 128 x 160 tiles (N % 160
+ * == 0: the SILU epilogue at 129-256 rows as five gate|up pairs, STORE with a bias where one
+ * round of them covers more CUs than one round of 128-column tiles) where they fill the CUs
+ * in one round (omni_packed_gemm_pipe_plan; same k order per output: results equal the
+ * 128 x 128 tiles' bit for bit). */
 int omni_packed_gemm_pipe(const void* x, int ldx, const void* w_packed, const void* scales_packed,
                           int fmt, const void* bias, int bias_after_round, void* out, int ldo,
                           int M, int N, int K, int epilogue, int tile_rows, int ksplit,

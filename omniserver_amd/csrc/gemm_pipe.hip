@@ -816,30 +816,36 @@ __global__ __launch_bounds__(512, 1) void gemm_bigp_f16_kernel(GemmPipeArgs a) {
   gp_wait_vmcnt<0>();                   // drain the clamped tail loads before exit
 }
 
-// 128 x 160 tiles (five gate|up column pairs) for the SiLU-fused gate_up projection on the
-// packed fp16 weights at 129-256 rows, one tile per workgroup: config 1's 256-token prompt
-// (N = 17920) has 224 of them, one round on 256 CUs, where 256 x 128 tiles fill 140 CUs and
-// 128 x 128 tiles take two rounds.  A step stages 16 KB of x and 20 KB of w (36 KB per CU
-// against 48 KB for a 256 x 128 tile; at these sizes a step's time follows the bytes it
-// stages).  8 waves, two per SIMD: 4 along m (32 rows each) x 2 along n, the first n group
-// holding pairs 0-2 (column tiles 0-5) and the second pairs 3-4 (column tiles 6-9), so that
-// every SIMD holds one wave of each.  Per 64-k step a wave reads 4 x fragments and 12 or 8 w
-// fragments and issues 24 or 16 MFMAs; the K order of every output is the 256 x 128 tiles'
-// (steps ascending, each step's two 32-k halves in order), so the outputs equal theirs bit
-// for bit.  w blocks: 20 per step, three loads each for waves 0-3 and two for waves 4-7.
-template <int NS>
-__global__ __launch_bounds__(512, 1) void gemm_silu160_kernel(GemmPipeArgs a) {
+// 128 x 160 tiles on the packed fp16 weights, one tile per workgroup, where they fill the
+// CUs in one round and the 128- / 256-row x 128 tiles would not: the SiLU-fused gate_up at
+// 129-256 rows (five gate|up column pairs; config 1's 256-token prompt, N = 17920: 224 tiles
+// where 256 x 128 tiles fill 140 CUs and 128 x 128 ones take two rounds) and the STORE /
+// QGELU / GELU / RESID epilogues with a bias (the vision tower's fc1, 1024 x 1280 -> 5120:
+// 256 tiles where 256 x 128 ones fill 160 CUs).  A step stages 16 KB of x and 20 KB of w (36
+// KB per CU against 48 KB for a 256 x 128 tile; at these sizes a step's time follows the
+// bytes it stages).  8 waves, two per SIMD: 4 along m (32 rows each) x 2 along n - for SILU
+// the first n group holds pairs 0-2 (column tiles 0-5) and the second pairs 3-4 (tiles 6-9),
+// otherwise five column tiles each - so that every SIMD holds one wave of each group.  Per
+// 64-k step a wave reads 4 x fragments and 8-12 w fragments and issues 16-24 MFMAs; the K
+// order of every output is the 128-column tiles' (steps ascending, each step's two 32-k
+// halves in order) and the epilogues are theirs, so the outputs equal theirs bit for bit.  w
+// blocks: 20 per step, three loads each for waves 0-3 and two for waves 4-7.
+template <int NS, int EPI>
+__global__ __launch_bounds__(512, 1) void gemm_n160_kernel(GemmPipeArgs a) {
 #pragma clang fp contract(off)
   constexpr int BM = 128, BN = 160;
-  constexpr int NCT = BN / 16;          // column tiles (gate and up of 5 pairs)
+  constexpr int NCT = BN / 16;          // column tiles
   constexpr int XLD = 2;                // x loads per wave and step (128 rows / 8 / 8)
+  constexpr bool SILU = EPI == GP_SILU;
   __shared__ __attribute__((aligned(1024))) uint8_t xl[NS][BM * GP_ROWB];
   __shared__ __attribute__((aligned(1024))) uint8_t wl[NS][2 * NCT * 1024];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave & 3;
-  const int wn = wave >> 2;             // 0: pairs 0-2, 1: pairs 3-4
+  const int wn = wave >> 2;
+  const int ct0 = SILU ? 6 * wn : 5 * wn;       // the wave's first column tile
+  const int ncw = SILU ? (wn ? 4 : 6) : 5;      // and its column tiles
   const int l16 = lane & 15;
   const int g4 = lane >> 4;
   const int tiles_m = (a.M + BM - 1) / BM;
@@ -883,8 +889,8 @@ __global__ __launch_bounds__(512, 1) void gemm_silu160_kernel(GemmPipeArgs a) {
     const uint32_t row = (uint32_t)(uintptr_t)(lds_u8*)&xl[st][r * GP_ROWB];
     const uint32_t bx0 = row + ((g4 ^ (l16 & 7)) << 4);
     const uint32_t bx1 = row + (((4 + g4) ^ (l16 & 7)) << 4);
-    const uint32_t bw = (uint32_t)(uintptr_t)(lds_u8*)&wl[st][wn ? 12 * 1024 : 0] + (uint32_t)lane * 16u;
-    if (wn == 0)
+    const uint32_t bw = (uint32_t)(uintptr_t)(lds_u8*)&wl[st][2 * ct0 * 1024] + (uint32_t)lane * 16u;
+    if (ncw == 6)
       asm volatile(
           "ds_read_b128 %0, %16\n\tds_read_b128 %1, %16 offset:1024\n\t"
           "ds_read_b128 %2, %16 offset:2048\n\tds_read_b128 %3, %16 offset:3072\n\t"
@@ -898,6 +904,21 @@ __global__ __launch_bounds__(512, 1) void gemm_silu160_kernel(GemmPipeArgs a) {
           : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
             "=&v"(v[6]), "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11]),
             "=&v"(v[12]), "=&v"(v[13]), "=&v"(v[14]), "=&v"(v[15])
+          : "v"(bw), "v"(bx0), "v"(bx1)
+          : "memory");
+    else if (ncw == 5)
+      asm volatile(
+          "ds_read_b128 %0, %14\n\tds_read_b128 %1, %14 offset:1024\n\t"
+          "ds_read_b128 %2, %14 offset:2048\n\tds_read_b128 %3, %14 offset:3072\n\t"
+          "ds_read_b128 %4, %14 offset:4096\n\tds_read_b128 %5, %14 offset:5120\n\t"
+          "ds_read_b128 %6, %14 offset:6144\n\tds_read_b128 %7, %14 offset:7168\n\t"
+          "ds_read_b128 %8, %14 offset:8192\n\tds_read_b128 %9, %14 offset:9216\n\t"
+          "ds_read_b128 %10, %15\n\tds_read_b128 %11, %16\n\t"
+          "ds_read_b128 %12, %15 offset:2048\n\tds_read_b128 %13, %16 offset:2048\n\t"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
+            "=&v"(v[6]), "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[12]), "=&v"(v[13]),
+            "=&v"(v[14]), "=&v"(v[15])
           : "v"(bw), "v"(bx0), "v"(bx1)
           : "memory");
     else
@@ -914,7 +935,6 @@ __global__ __launch_bounds__(512, 1) void gemm_silu160_kernel(GemmPipeArgs a) {
           : "v"(bw), "v"(bx0), "v"(bx1)
           : "memory");
   };
-  const int ncw = wn ? 4 : 6;           // the wave's column tiles
   f32x4 acc[6][2];
 #pragma unroll
   for (int c = 0; c < 6; ++c)
@@ -948,21 +968,42 @@ __global__ __launch_bounds__(512, 1) void gemm_silu160_kernel(GemmPipeArgs a) {
       }
   }
   gp_wait_vmcnt<0>();                   // drain the clamped tail loads
-  // lane holds columns 16 c + 4 g4 + q of the wave's tiles, rows m0 + 32 wm + 16 j + l16;
-  // pair p of the wave (column tiles 2 p, 2 p + 1) is intermediate pair n0 / 32 + 3 wn + p
+  // lane holds columns 16 (ct0 + c) + 4 g4 + q of the tile, rows m0 + 32 wm + 16 j + l16
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int m = m0 + 32 * wm + 16 * j + l16;
     if (m >= a.M) continue;
-    half_t* const ob = a.out + (int64_t)m * a.ldo + n0 / 2 + 48 * wn + 4 * g4;
+    if constexpr (SILU) {
+      // pair p of the wave (column tiles 2 p, 2 p + 1) is intermediate pair n0 / 32 + 3 wn + p
+      half_t* const ob = a.out + (int64_t)m * a.ldo + n0 / 2 + 48 * wn + 4 * g4;
 #pragma unroll
-    for (int p = 0; p < 3; ++p) {
-      if (2 * p >= ncw) break;
-      half4_t o;
+      for (int p = 0; p < 3; ++p) {
+        if (2 * p >= ncw) break;
+        half4_t o;
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        o[q] = (half_t)silu_mul_f32((float)(half_t)acc[2 * p][j][q], (float)(half_t)acc[2 * p + 1][j][q]);
-      *(half4_t*)(ob + 16 * p) = o;
+        for (int q = 0; q < 4; ++q)
+          o[q] = (half_t)silu_mul_f32((float)(half_t)acc[2 * p][j][q], (float)(half_t)acc[2 * p + 1][j][q]);
+        *(half4_t*)(ob + 16 * p) = o;
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < 5; ++c) {
+        const int n = n0 + 16 * (ct0 + c) + 4 * g4;
+        half4_t bb = (half4_t){0, 0, 0, 0};
+        if (a.bias) bb = *(const half4_t*)(a.bias + n);
+        half4_t rr = (half4_t){0, 0, 0, 0};
+        if constexpr (EPI == GP_RESID) rr = *(const half4_t*)(a.res + (int64_t)m * a.ldr + n);
+        half4_t o;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          half_t hv = gp_bias(acc[c][j][q], bb[q], a.bias != nullptr, a.bias_after_round);
+          if constexpr (EPI == GP_QGELU) hv = gp_quick_gelu(hv);
+          if constexpr (EPI == GP_GELU) hv = gp_gelu(hv);
+          if constexpr (EPI == GP_RESID) hv = (half_t)((float)rr[q] + (float)hv);
+          o[q] = hv;
+        }
+        *(half4_t*)(a.out + (int64_t)m * a.ldo + n) = o;
+      }
     }
   }
 }
@@ -1197,11 +1238,24 @@ static void gp_packed_plan(int M, int N, int K, int fmt, int epilogue, bool has_
   if (fmt != 1 || tile_rows != 0 || ks != 1) return;
   if (epilogue == GP_SILU && M > 128 && M <= 256 && N % 160 == 0 &&
       2 * (int64_t)(N / 160) <= gp_num_cus()) {
-    // gemm_silu160_kernel: one round of 128 x 160 tiles where the 256 x 128 tiles (also one
+    // gemm_n160_kernel: one round of 128 x 160 tiles where the 256 x 128 tiles (also one
     // round) stage a third more bytes per step per CU
     rows = 128;
     cols = 160;
     return;
+  }
+  if ((epilogue == GP_STORE || epilogue == GP_QGELU || epilogue == GP_GELU || epilogue == GP_RESID) &&
+      N % 160 == 0) {
+    // one round of 128 x 160 tiles where the 128-column tiles of the chosen height take one
+    // round too but on fewer CUs (the vision tower's fc1: 256 against 160 tiles)
+    const int64_t cus = gp_num_cus();
+    const int64_t t160 = (int64_t)ceil_div(M, 128) * (N / 160);
+    const int64_t tcur = (int64_t)ceil_div(M, rows) * (N / GP_BN);
+    if (t160 <= cus && tcur <= cus && t160 > tcur && !(cols == 192)) {
+      rows = 128;
+      cols = 160;
+      return;
+    }
   }
   if ((epilogue == GP_STORE || epilogue == GP_PARTIAL) && gp_wide_tiles(M, N, rows)) {
     rows = 128;
@@ -1356,10 +1410,17 @@ static int gp_packed_f16_launch(GemmPipeArgs& a, int epilogue, int tile_rows, in
     OMNI_CHECK_LAUNCH();
     return OMNI_OK;
   }
-  if (cols == 160) {                         // five gate|up pairs per tile, one tile per CU
-    if (epilogue != GP_SILU || M > 256 || N % 160) return OMNI_EINVAL;
+  if (cols == 160) {                         // 128 x 160 tiles, one per workgroup
+    if (N % 160 || ksplit != 1 || (epilogue == GP_SILU && M > 256)) return OMNI_EINVAL;
     const int grid = ceil_div(M, 128) * (N / 160);
-    hipLaunchKernelGGL((gemm_silu160_kernel<4>), dim3(grid), dim3(512), 0, st, a);
+    switch (epilogue) {
+      case GP_SILU: hipLaunchKernelGGL((gemm_n160_kernel<4, GP_SILU>), dim3(grid), dim3(512), 0, st, a); break;
+      case GP_STORE: hipLaunchKernelGGL((gemm_n160_kernel<4, GP_STORE>), dim3(grid), dim3(512), 0, st, a); break;
+      case GP_QGELU: hipLaunchKernelGGL((gemm_n160_kernel<4, GP_QGELU>), dim3(grid), dim3(512), 0, st, a); break;
+      case GP_GELU: hipLaunchKernelGGL((gemm_n160_kernel<4, GP_GELU>), dim3(grid), dim3(512), 0, st, a); break;
+      case GP_RESID: hipLaunchKernelGGL((gemm_n160_kernel<4, GP_RESID>), dim3(grid), dim3(512), 0, st, a); break;
+      default: return OMNI_EINVAL;
+    }
     OMNI_CHECK_LAUNCH();
     return OMNI_OK;
   }

@@ -207,8 +207,7 @@ def test_packed_silu160_plan(so):
     """The SiLU-fused gate_up at 129-256 rows on packed fp16 weights takes 128 x 160 tiles
     (five gate|up pairs) where they fill the 256 CUs in one round (config 1's 256-token
     prompt: 224 tiles); 128 rows or fewer, more than 256, int4 weights, N not a multiple of
-    160, too many tiles for one round, a forced tile height or the STORE epilogue keep the
-    other tiles."""
+    160, too many tiles for one round or a forced tile height keep the other tiles."""
     import ctypes
     from omniserver_amd._lib import lib
     L = lib()
@@ -228,4 +227,12 @@ def test_packed_silu160_plan(so):
     assert plan(256, 17920 + 128, 1536, 1, 1)[1] != 160
     assert plan(256, 25600 + 640, 1536, 1, 1)[1] != 160     # 2 x 164 tiles > 256 CUs
     assert plan(256, 17920, 1536, 1, 1, tile_rows=256) == (256, 128, 1)
-    assert plan(256, 17920, 1536, 1, 0)[1] != 160
+    # the biased STORE / QGELU / GELU / RESID epilogues take them too where one round of
+    # them covers more CUs than one round of 128-column tiles (the vision tower's fc1)
+    assert plan(1024, 5120, 1280, 1, 4) == (128, 160, 1)
+    assert plan(1024, 5120, 1280, 1, 0) == (128, 160, 1)
+    assert plan(256, 17920, 1536, 1, 0) == (128, 160, 1)
+    assert plan(1024, 1280, 5120, 1, 6)[1] != 160          # 64 tiles against 80
+    assert plan(1024, 3840, 1280, 1, 0)[1] != 160          # 192 against 240
+    assert plan(1024, 5120, 1280, 1, 2)[1] != 160          # partial sums keep their plan
+    assert plan(4096, 5120, 1280, 1, 4)[1] != 160          # more than one round

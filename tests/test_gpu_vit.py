@@ -298,30 +298,36 @@ def test_layernorm_partials(gpu, M, N, K, bias):
     assert (r2.cpu().float() - want_r).abs().max().item() <= 2e-3 * max(1.0, want_r.abs().max().item())
 
 
-@pytest.mark.parametrize("epi,bias", [(4, True), (0, True), (5, True), (6, True), (0, False)])
-def test_n160_tiles_equal_128_column_tiles(gpu, epi, bias):
-    """The vision tower's fc1 shape (1024 x 1280 -> 5120) on the library's own plan (128 x 160
-    tiles, one per CU) equals the forced 256 x 128 tiles bit for bit, every biased epilogue
-    (the same K order per output and the same epilogue arithmetic)."""
+@pytest.mark.parametrize("M,epi,bias", [(1024, 4, True), (1024, 0, True), (1024, 5, True),
+                                         (1024, 6, True), (1024, 0, False), (1000, 4, True),
+                                         (1000, 6, True)])
+def test_n160_tiles_equal_128_column_tiles(gpu, M, epi, bias):
+    """The vision tower's fc1 shape (1024 x 1280 -> 5120, and a ragged 1000 rows) on the
+    library's own plan (128 x 160 tiles, one per CU) equals the forced 256 x 128 tiles bit for
+    bit, every biased epilogue (the same K order per output and the same epilogue
+    arithmetic); rows past M untouched."""
     from omniserver_amd._lib import call, ptr, stream
     from omniserver_amd import vit
     import ctypes
     from omniserver_amd._lib import lib
-    M, K, N = 1024, 1280, 5120
+    K, N = 1280, 5120
     r, c, k = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
     lib().omni_packed_gemm_pipe_plan(M, N, K, 1, epi, int(bias), 0, 0, ctypes.byref(r), ctypes.byref(c), ctypes.byref(k))
     assert (r.value, c.value, k.value) == (128, 160, 1)
-    say(f"n160 tiles epi={epi} bias={bias}")
+    say(f"n160 tiles M={M} epi={epi} bias={bias}")
     x, w = f16((M, K), 51).to(gpu), f16((N, K), 52, 0.02).to(gpu)
     b = f16((N,), 53, 0.02).to(gpu) if bias else None
     res = f16((M, N), 54).to(gpu)
     lin = vit.VisionLinear(w, b, gpu)
     outs = []
     for tile_rows in (0, 256):
-        o = res.clone() if epi == vit.EPI_RESID else torch.full((M, N), float("nan"), device=gpu, dtype=torch.float16)
+        # one spare row past M: the tiles' ragged last rows must not store there
+        o = torch.full((M + 1, N), float("nan"), device=gpu, dtype=torch.float16)
+        if epi == vit.EPI_RESID:
+            o[:M] = res
         call("omni_f16_gemm_pipe_packed", ptr(x), K, ptr(lin.w), ptr(b), ptr(o) if epi == vit.EPI_RESID else None,
              N, ptr(o), N, M, N, K, epi, tile_rows, 1, None, stream())
         outs.append(o.cpu())
     torch.cuda.synchronize()
-    assert not torch.isnan(outs[0]).any()
-    assert torch.equal(outs[0], outs[1])
+    assert not torch.isnan(outs[0][:M]).any() and torch.isnan(outs[0][M]).all()
+    assert torch.equal(outs[0][:M], outs[1][:M])

@@ -263,32 +263,45 @@ def fp8_layer_gemms(device, M: int = 8192, reps: int = 10) -> dict:
     down 8960->1536.  Weights N(0, 0.02) quantised per output channel, activations N(0, 1)
     quantised per token; the timed region is the fp8 MFMA GEMM (fp32 accumulate, bf16 ->
     fp16 epilogue) with inputs resident in HBM, the median of five timed repetitions of
-    ``reps`` launches.  Achieved dense TFLOP/s against the MI355X fp8 peak (5.0 PFLOP/s)."""
+    ``reps`` launches after 0.1 s of untimed passes over the layer.  Achieved dense TFLOP/s
+    against the MI355X fp8 peak (5.0 PFLOP/s)."""
     from omniserver_amd.linear import FP8Linear
     shapes = [("qkv", 1536, 2048), ("o", 1536, 1536), ("gate_up", 1536, 17920),
               ("down", 8960, 1536)]
     g = torch.Generator(device=device)
     g.manual_seed(4)
-    per, tot_s, tot_f = {}, 0.0, 0.0
+    ops = []
     for name, K, N in shapes:
         lin = FP8Linear((torch.randn(N, K, device=device, generator=g) * 0.02).half(),
                         rowwise=True)
         x = torch.randn(M, K, device=device, generator=g).half()
         xq, sa = lin.quantize_input(x)
         out = torch.empty(M, N, device=device, dtype=torch.float16)
-        # the median of five timed repetitions after an untimed one: a shape's first launches
-        # run on freshly allocated buffers and ramping clocks (5-10 % slower on MI355X)
-        f = lambda: lin.gemm_out(xq, sa, out, FP8Linear.OUT_F16_VIA_BF16)
-        time_kernel(f, reps)
+        ops.append((name, 2.0 * M * N * K,
+                    lambda lin=lin, xq=xq, sa=sa, out=out:
+                        lin.gemm_out(xq, sa, out, FP8Linear.OUT_F16_VIA_BF16)))
+        del x
+    # Untimed passes over the whole layer for 0.1 s, then each shape's median of five timed
+    # repetitions: the first pass runs on freshly allocated buffers and ramping clocks (its
+    # layer time, reported as first_pass_us, is 2-4 % above the steady state on MI355X, and
+    # ~10 ms of passes do not close the gap), as a prefill's first layer would; the timed
+    # repetitions are the steady state of a running prefill.
+    first = sum(time_kernel(f, reps) for _, _, f in ops)
+    t_end = time.perf_counter() + 0.1
+    while time.perf_counter() < t_end:
+        for _, _, f in ops:
+            time_kernel(f, reps)
+    per, tot_s, tot_f = {}, 0.0, 0.0
+    for name, fl, f in ops:
         t = statistics.median(time_kernel(f, reps) for _ in range(5))
-        fl = 2.0 * M * N * K
         per[name] = {"us": round(t * 1e6, 1), "tflops": round(fl / t / 1e12, 1)}
         tot_s += t
         tot_f += fl
-        del lin, x, xq, sa, out
+    del ops
     return {"workload": f"one layer's W8A8 linears at M={M}", "gflop": round(tot_f / 1e9, 1),
             "us": round(tot_s * 1e6, 1), "achieved": round(tot_f / tot_s / 1e12, 1),
             "peak": PEAK_FP8 / 1e12, "unit": "TFLOP/s", "frac": round(tot_f / tot_s / PEAK_FP8, 4),
+            "first_pass_us": round(first * 1e6, 1),
             "per_shape": per,
             "mfma_busy_pct_counters": mfma_from_profiles("fp8 W8A8 M=8192")}
 
@@ -601,6 +614,11 @@ def vit_tower(device, grid=(1, 32, 32), reps: int = 5) -> dict:
     cfg = VisionConfig()
     tower = load_vit_from_state_dict(Qwen2VIT(device=device), synth.vision_tower(cfg, seed=5))
     pv = synth.pixel_patches([grid], cfg.patch_dim, 6).to(device)
+    # untimed forwards for 0.1 s first, so the timed ones run at the clocks of a busy GPU
+    t_end = time.perf_counter() + 0.1
+    while time.perf_counter() < t_end:
+        tower(pv, [grid])
+        torch.cuda.synchronize()
     t = time_kernel(lambda: tower(pv, [grid]), reps)
     fl = vit_flops([grid], cfg)
     return {"workload": f"vision tower, 32 blocks + merger, one image grid {list(grid)} "

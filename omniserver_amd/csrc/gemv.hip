@@ -940,9 +940,10 @@ static int gemv_common(int wf, const void* x, int ldx, const void* w, const void
   hipStream_t st = (hipStream_t)stream;
   if (M > 64) {   // many rows (prefill): STORE / SILU epilogues
     // the pipelined GEMM where its shape and alignment rules hold (every K slice at least
-    // 3 groups: its deepest pipeline is 6 steps of 64), else the tiled kernel
+    // 3 groups on int4 weights, whose deepest pipeline is 6 steps of 64, 2 on fp16 weights:
+    // 4 steps), else the tiled kernel
     const int slices = tile_split ? omni_gemm_slices(K, ksplit) : 1;
-    const bool pipe = (N % 128) == 0 && K >= 256 && KG / slices >= 3 &&
+    const bool pipe = (N % 128) == 0 && K >= 256 && KG / slices >= (wf == W_INT4 ? 3 : 2) &&
                       ((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0 &&
                       ((uintptr_t)out & 7) == 0 && (ldo & 3) == 0 &&
                       (!bias || ((uintptr_t)bias & 15) == 0) &&

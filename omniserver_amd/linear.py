@@ -104,6 +104,7 @@ class _Skinny(nn.Module):
     """Shared launch logic of the packed-weight linears."""
 
     fmt = "fp16"
+    FILL_SLICES = False     # tile_ksplit's slice rule for the fp16 linears
 
     def _init_plan(self):
         self.store_preset, self.partial_preset, self.partial_ksplit = _plan(self.fmt, self.K, self.N)
@@ -121,14 +122,22 @@ class _Skinny(nn.Module):
     def tile_ksplit(self, M: int) -> int:
         """K split of the tiled GEMM (more than MAX_SKINNY_M rows, STORE epilogue): when its
         128 x 128 tiles would leave over half of the 256 CUs idle (e.g. a 256-token prompt's
-        down projection: 24 tiles over K = 8960), the K groups are dealt to up to 8 slices of
-        at least 4 groups each, summed by a finish launch."""
+        down projection: 24 tiles over K = 8960), the K groups are dealt to slices summed by
+        a finish launch (or by the next kernel, forward_partial).  fp16 linears (FILL_SLICES)
+        take as many slices as keep the tiles in one round of the CUs, each at least 2 groups
+        (the pipeline's 4 stages of 64): graph-timed at M = 256, qkv 11.3 -> 9.9 us (6 slices
+        against 3), o 11.4 -> 9.7 (6), down 19.2 -> 17.5 (10 against 8).  GPTQ linears keep
+        up to 8 slices of at least 4 groups (their finished prefill form on the fp16
+        expansion plans its own slices, omni_f16_gemm_pipe_splits, and the partial form must
+        sum the same ones)."""
         if self.fuse_silu or M <= MAX_SKINNY_M:
             return 1
         tiles = -(-M // 128) * -(-self.N // 128)
         KG = self.K // 128
         if tiles >= 128 or KG < 8:
             return 1
+        if self.FILL_SLICES:
+            return max(1, min(KG // 2, 256 // tiles))
         return max(1, min(8, KG // 4, 256 // tiles))
 
     def forward_out(self, x2d: torch.Tensor, out: torch.Tensor, preset: int | None = None,
@@ -432,6 +441,7 @@ class F16Linear(_Skinny):
     """fp16 linear over the packed MFMA layout: y = fp16(x . W^T + b)."""
 
     fmt = "fp16"
+    FILL_SLICES = True
 
     def __init__(self, weight: torch.Tensor, bias=None, fuse_silu: bool = False):
         super().__init__()

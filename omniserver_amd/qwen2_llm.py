@@ -286,9 +286,10 @@ class Qwen2LLM(nn.Module):
             dparts = max(layer.down_proj.partial_plan(T) for layer in self.layers)
             qpart = opart = None
         else:
-            dparts = 8
-            qpart = f32(8 * T * l0.qkv_proj.N)
-            opart = f32(8 * T * l0.o_proj.N)
+            slices = lambda name: max(getattr(layer, name).tile_ksplit(T) for layer in self.layers)
+            dparts = slices("down_proj")
+            qpart = f32(slices("qkv_proj") * T * l0.qkv_proj.N)
+            opart = f32(slices("o_proj") * T * l0.o_proj.N)
         dpart = f32(dparts * T * l0.down_proj.N)
         residual = x.clone()
         h = torch.empty(T, H, device=dev, dtype=torch.float16)

@@ -385,3 +385,30 @@ def test_decode_addnorm_eligibility():
     assert ok(1) and not ok(2)
     m.cfg.hidden_size, m.decode_addnorm_rows = 1536, 0
     assert not ok(1)
+
+
+def test_prefill_k_slices():
+    """Prefill K slices of the tiled GEMM (tile_ksplit): fp16 linears fill one round of the
+    256 CUs with slices of at least two 128-groups (the 2B decoder at 256 rows: qkv / o 6,
+    down 10); GPTQ linears keep at most 8 slices of four groups; no split for the SiLU-fused
+    projection, at most 64 rows, or where the tiles already fill half the CUs."""
+    from types import SimpleNamespace
+    from omniserver_amd.linear import F16Linear, GPTQLinear
+    from omniserver_amd._lib import lib
+
+    def ks(cls, N, K, M, silu=False):
+        lin = SimpleNamespace(N=N, K=K, fuse_silu=silu, FILL_SLICES=cls.FILL_SLICES)
+        return cls.tile_ksplit(lin, M)
+
+    shapes = {"qkv": (2048, 1536), "o": (1536, 1536), "down": (1536, 8960)}
+    assert [ks(F16Linear, N, K, 256) for N, K in shapes.values()] == [6, 6, 10]
+    assert [ks(GPTQLinear, N, K, 256) for N, K in shapes.values()] == [3, 3, 8]
+    assert ks(F16Linear, 17920, 1536, 256, silu=True) == 1
+    assert ks(F16Linear, 2048, 1536, 64) == 1
+    for M in range(65, 1281, 37):
+        for N, K in shapes.values():
+            s = ks(F16Linear, N, K, M)
+            tiles = -(-M // 128) * (N // 128)
+            slices = lib().omni_gemm_slices(K, s)
+            assert tiles * slices <= 256 or s == 1, (M, N, K, s)
+            assert K // 128 // slices >= 2, (M, N, K, s)
